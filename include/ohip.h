@@ -1,0 +1,235 @@
+/*
+ * ohip.h -- C ABI of the MI355X (gfx950) execution provider for OxiONNX's
+ * dense-contraction hot path: Conv (implicit GEMM), Gemm / MatMul, and the
+ * INT8 family MatMulInteger / QLinearMatMul / ConvInteger / QLinearConv.
+ *
+ * Everything here is plain C: pointers, sizes and POD structs.  No exception
+ * crosses the boundary.  Every entry point returns an int status:
+ *     OHIP_OK (0)         success
+ *     OHIP_DECLINED (1)   configuration not handled; the caller runs its CPU
+ *                         kernel (the reference's Ok(None) contract,
+ *                         oxionnx-cuda/src/lib.rs:336-352)
+ *     < 0                 failure; ohip_last_error() holds the message
+ *                         (the reference's Err -> CPU fallback,
+ *                         src/session/run/sequential.rs:1019-1031)
+ *
+ * Device pointers passed to the ohip_gemm / ohip_conv2d family must live on
+ * the context's device; work is ordered on the context's single stream.
+ * All citations are into cool-japan/oxionnx v0.1.7.
+ */
+#ifndef OXIONNX_OHIP_H
+#define OXIONNX_OHIP_H
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define OHIP_OK 0
+#define OHIP_DECLINED 1
+#define OHIP_E_INVALID (-1)
+#define OHIP_E_HIP (-2)
+#define OHIP_E_SHAPE (-3)
+#define OHIP_E_NOMEM (-4)
+#define OHIP_E_NODEVICE (-5)
+
+/* Element types use ONNX TensorProto codes (oxionnx-core/src/dtype.rs:8). */
+enum ohip_dtype { OHIP_F32 = 1, OHIP_U8 = 2, OHIP_I8 = 3, OHIP_I32 = 6, OHIP_F16 = 10, OHIP_BF16 = 16 };
+
+/* Fused activation, the optimizer's attribute contract `activation` /
+ * `activation_min` / `activation_max` (oxionnx-ops/src/registry/conv_ops/conv.rs:124-156).
+ * LEAKY_RELU takes its slope in act_lo (oxionnx-gpu/src/shaders/conv2d.rs:134-232). */
+enum ohip_act { OHIP_ACT_NONE = 0, OHIP_ACT_RELU = 1, OHIP_ACT_CLIP = 2, OHIP_ACT_LEAKY_RELU = 3 };
+
+/* Gemm C operand shapes (oxionnx-ops/src/math_typed.rs:444-455, 718-727). */
+enum ohip_bias_kind { OHIP_C_NONE = 0, OHIP_C_SCALAR = 1, OHIP_C_ROW = 2, OHIP_C_FULL = 3 };
+
+enum ohip_layout { OHIP_NCHW = 0, OHIP_NHWC = 1 };
+
+/* Output kinds of the integer family. */
+enum ohip_qout { OHIP_QOUT_U8 = 0, OHIP_QOUT_I8 = 1, OHIP_QOUT_I32 = 2 };
+
+/* Performance classes for the dispatch gate (oxionnx-gpu/src/context/tuning.rs:271-611). */
+enum ohip_perf_class { OHIP_CLASS_MI355X = 0, OHIP_CLASS_PARITY = 1, OHIP_CLASS_NEVER = 2, OHIP_CLASS_LEGACY = 3 };
+
+typedef struct ohip_ctx ohip_ctx;
+typedef struct ohip_weight ohip_weight;
+
+/* ------------------------------------------------------------------ context */
+/* Replaces CudaContext::try_new (oxionnx-cuda/src/context.rs:467-481).  The
+ * context is Send + Sync: every entry point re-activates its device on the
+ * calling thread (activate_context, oxionnx-cuda/src/lib.rs:277-332). */
+int ohip_ctx_create(int device, ohip_ctx** out);
+void ohip_ctx_destroy(ohip_ctx* ctx);
+/* Adopt a caller stream (e.g. torch.cuda.current_stream()); NULL restores the
+ * context's own stream. */
+int ohip_ctx_set_stream(ohip_ctx* ctx, void* hip_stream);
+void* ohip_ctx_stream(ohip_ctx* ctx);
+int ohip_sync(ohip_ctx* ctx);
+int ohip_device_count(int* count);
+const char* ohip_last_error(void);
+const char* ohip_version(void);
+/* Env truthiness used by OXIONNX_HIP / OXIONNX_HIP_VERIFY / OXIONNX_HIP_STRICT /
+ * OXIONNX_HIP_RESIDENCY (same rule as oxionnx-cuda/src/context.rs:179-200). */
+int ohip_env_flag(const char* name);
+
+/* ------------------------------------------------------------------ memory */
+int ohip_malloc(ohip_ctx* ctx, size_t bytes, void** dptr);
+int ohip_free(ohip_ctx* ctx, void* dptr);
+int ohip_memcpy_h2d(ohip_ctx* ctx, void* dst, const void* src, size_t bytes);  /* stream-ordered */
+int ohip_memcpy_d2h(ohip_ctx* ctx, void* dst, const void* src, size_t bytes);  /* synchronous */
+int ohip_memcpy_d2d(ohip_ctx* ctx, void* dst, const void* src, size_t bytes);  /* stream-ordered */
+
+/* ------------------------------------------------------------------ gate */
+/* GpuTuning (oxionnx-gpu/src/context/tuning.rs:271-611) recalibrated for
+ * MI355X.  All of these are device-free. */
+typedef struct {
+    int perf_class;
+    uint64_t gemm_min_mac;          /* B uploaded per dispatch */
+    uint64_t gemm_min_mac_cached;   /* B resident in the weight cache */
+    uint64_t gemm_min_intensity;    /* FLOP per transferred element, per-dispatch B only */
+    uint64_t conv_min_mac;          /* implied GEMM of a Conv */
+} ohip_tuning;
+int ohip_tuning_for_class(int perf_class, ohip_tuning* out);
+int ohip_set_tuning(ohip_ctx* ctx, const ohip_tuning* t);
+int ohip_get_tuning(ohip_ctx* ctx, ohip_tuning* out);
+/* gemm_mac / gemm_intensity / gemm_admits / conv_admits (tuning.rs:500-611). */
+uint64_t ohip_gemm_mac(int64_t m, int64_t k, int64_t n);
+uint64_t ohip_gemm_intensity(int64_t m, int64_t k, int64_t n);
+int ohip_gemm_admits(const ohip_tuning* t, int64_t m, int64_t k, int64_t n, int b_cached);
+int ohip_conv_admits(const ohip_tuning* t, int64_t m, int64_t k, int64_t n);
+
+/* ------------------------------------------------------------------ weights */
+/* Session-lifetime weight residency keyed like ResidentWeights / WeightId
+ * (oxionnx-cuda/src/residency.rs:677-723) and initializer_key
+ * (src/session/gpu_dispatch.rs:614-624): (name, label, packed form, dtype,
+ * byte length).  key == NULL (or name == NULL) uploads transiently: the
+ * weight is freed by ohip_weight_release.  A cached weight is owned by the
+ * context; releasing it is a no-op.  Weights are packed on upload into the
+ * kernels' K-contiguous row layout, so no per-call transpose ever runs. */
+typedef struct {
+    const char* name;   /* initializer name */
+    const char* label;  /* operator slot, e.g. "Gemm.B" */
+} ohip_weight_key;
+
+/* Float GEMM operand B: host [K,N] (trans_b = 0) or [N,K] (trans_b = 1) of
+ * src_dtype (F32/F16/BF16), converted to dtype (F32/F16/BF16, RNE). */
+int ohip_weight_gemm(ohip_ctx* ctx, const ohip_weight_key* key, int src_dtype, const void* host,
+                     int64_t k, int64_t n, int trans_b, int dtype, ohip_weight** out);
+/* Float Conv filter: host [Cout, Cin/group, KH, KW] (group 1). */
+int ohip_weight_conv(ohip_ctx* ctx, const ohip_weight_key* key, int src_dtype, const void* host,
+                     int64_t cout, int64_t cin, int64_t kh, int64_t kw, int dtype, ohip_weight** out);
+/* Integer GEMM operand B of MatMulInteger / QLinearMatMul
+ * (oxionnx-ops/src/registry/quant_ops/qlinear_matmul.rs:106-133): host u8/i8
+ * [K,N] (or [N,K] with trans_b), per-tensor or per-column zero point, and the
+ * weight scale(s) (1 or N entries; NULL for MatMulInteger). */
+int ohip_weight_qgemm(ohip_ctx* ctx, const ohip_weight_key* key, int src_dtype, const void* host,
+                      int64_t k, int64_t n, int trans_b, const int32_t* zp, int n_zp,
+                      const float* scale, int n_scale, ohip_weight** out);
+/* Integer Conv filter of ConvInteger / QLinearConv
+ * (oxionnx-ops/src/registry/quant_ops/conv_kernel.rs:134-254): host u8/i8
+ * [Cout, Cin, KH, KW], per-tensor or per-output-channel zero point and scale. */
+int ohip_weight_qconv(ohip_ctx* ctx, const ohip_weight_key* key, int src_dtype, const void* host,
+                      int64_t cout, int64_t cin, int64_t kh, int64_t kw, const int32_t* zp, int n_zp,
+                      const float* scale, int n_scale, ohip_weight** out);
+void ohip_weight_release(ohip_weight* w);
+size_t ohip_weight_bytes(const ohip_weight* w);
+
+/* ------------------------------------------------------------------ float ops */
+/* Gemm / MatMul (oxionnx-ops/src/registry/math_ops/matmul_gemm.rs:9-355,
+ * math_typed.rs:589-788): Y[M,N] = act(alpha * A' B + beta * C).  A is a
+ * device [M,K] row-major matrix (or [K,M] with trans_a) of `dtype`; B is a
+ * packed weight of the same dtype; C / Y are `dtype`.  A batched MatMul whose
+ * B is shared collapses to M = batch * rows (oxionnx-cuda/src/matmul.rs:189-252). */
+typedef struct {
+    int64_t m, k, n;
+    int dtype;
+    int trans_a;
+    float alpha, beta;
+    int c_kind;            /* ohip_bias_kind */
+    int act;               /* ohip_act (OHIP_ACT_NONE for ONNX Gemm) */
+    float act_lo, act_hi;
+    int64_t lda, ldy;      /* row strides in elements; 0 = packed */
+} ohip_gemm_desc;
+int ohip_gemm(ohip_ctx* ctx, const ohip_gemm_desc* d, const void* a, const ohip_weight* b,
+              const void* c, void* y);
+
+/* Conv, rank 2, group 1 (oxionnx-ops/src/registry/conv_ops/conv.rs:163-323
+ * and conv_typed.rs:54-153): Y = act(conv(X, W) + bias).  Pads are
+ * [top, left, bottom, right], already resolved from auto_pad
+ * (conv/spatial.rs:228-257); asymmetric pads are supported.  NCHW inputs are
+ * transposed on the device into a channel-padded NHWC staging buffer; NHWC
+ * inputs must already carry channels padded to a multiple of 16 bytes. */
+typedef struct {
+    int64_t n, c, h, w;
+    int64_t cout, kh, kw, group;
+    int64_t stride_h, stride_w, dil_h, dil_w;
+    int64_t pad_t, pad_l, pad_b, pad_r;
+    int dtype;                     /* F32 / F16 / BF16 */
+    int in_layout, out_layout;     /* ohip_layout */
+    int act;
+    float act_lo, act_hi;
+} ohip_conv_desc;
+int ohip_conv2d(ohip_ctx* ctx, const ohip_conv_desc* d, const void* x, const ohip_weight* w,
+                const void* bias, void* y);
+/* Output extent per conv_out_dim (conv/spatial.rs:272-330); -1 if invalid. */
+int64_t ohip_conv_out_dim(int64_t in, int64_t pad_begin, int64_t pad_end, int64_t k, int64_t dil,
+                          int64_t stride);
+
+/* ------------------------------------------------------------------ integer ops */
+/* MatMulInteger / QLinearMatMul (qlinear_matmul.rs:174-254).  A is a device
+ * u8/i8 [M,K] matrix; a_zp holds 1 or M host entries.  For QOUT_U8/QOUT_I8
+ * the accumulator is requantised exactly like SatRange::requantize
+ * (quant_ops/mod.rs:229-233): combined = a_scale * w_scale / y_scale in f32,
+ * f64 product, + y_zp, round half to even, clamp to [lo, hi].  QOUT_I32 emits
+ * the raw accumulator (MatMulInteger).  The caller resolves [lo, hi]
+ * (SatRange::infer / for_dtype, mod.rs:188-221). */
+typedef struct {
+    int64_t m, k, n;
+    int a_dtype;                   /* U8 or I8 */
+    const int32_t* a_zp; int n_azp;
+    int out_kind;                  /* ohip_qout */
+    float a_scale, y_scale;
+    int32_t y_zp, lo, hi;
+    int64_t lda, ldy;              /* 0 = packed */
+} ohip_qgemm_desc;
+int ohip_qgemm(ohip_ctx* ctx, const ohip_qgemm_desc* d, const void* a, const ohip_weight* b, void* y);
+
+/* ConvInteger / QLinearConv (qlinear_conv.rs:34-203): padding taps contribute
+ * exactly zero, bias is int32 added into the accumulator, the weight scale
+ * may be per output channel. */
+typedef struct {
+    int64_t n, c, h, w;
+    int64_t cout, kh, kw, group;
+    int64_t stride_h, stride_w, dil_h, dil_w;
+    int64_t pad_t, pad_l, pad_b, pad_r;
+    int x_dtype;                   /* U8 or I8 */
+    int32_t x_zp;
+    int out_kind;
+    float x_scale, y_scale;
+    int32_t y_zp, lo, hi;
+    int in_layout, out_layout;
+} ohip_qconv_desc;
+int ohip_qconv2d(ohip_ctx* ctx, const ohip_qconv_desc* d, const void* x, const ohip_weight* w,
+                 const int32_t* bias_dev, void* y);
+
+/* ------------------------------------------------------------------ counters */
+/* CacheCounters (oxionnx-cuda/src/residency.rs:141-238) plus dispatch counts. */
+typedef struct {
+    uint64_t weight_hits, weight_misses, weight_transient;
+    uint64_t weight_uploaded_bytes, weight_resident_bytes;
+    uint64_t h2d_bytes, d2h_bytes;
+    uint64_t dispatches, declined;
+} ohip_counters;
+int ohip_get_counters(ohip_ctx* ctx, ohip_counters* out);
+int ohip_reset_counters(ohip_ctx* ctx);
+
+/* Testing / tuning knob: force a tile size (64, 128, 256) for the MFMA
+ * kernels, 0 = automatic. */
+int ohip_set_tile_override(ohip_ctx* ctx, int tile);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,89 @@
+// Internal contract between the host policy (ops.cpp, runtime.cpp) and the
+// device launchers (kernels.hip).  Plain structs, no HIP types beyond the
+// stream and error code.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace ohip {
+
+// ONNX TensorProto element type codes (the public header uses the same).
+enum { DT_F32 = 1, DT_U8 = 2, DT_I8 = 3, DT_I32 = 6, DT_F16 = 10, DT_BF16 = 16 };
+enum { ACT_NONE = 0, ACT_RELU = 1, ACT_CLIP = 2, ACT_LEAKY_RELU = 3 };
+enum { BIAS_NONE = 0, BIAS_SCALAR = 1, BIAS_I = 2, BIAS_J = 3, BIAS_FULL_JI = 4 };
+enum { QOUT_U8 = 0, QOUT_I8 = 1, QOUT_I32 = 2 };
+
+// Rows of K-contiguous 16-byte chunks.
+struct DenseOperand {
+  const void* base;
+  int64_t ld_bytes;
+  int rows;
+  int kc;             // 16-byte chunks per row that hold data
+  uint32_t xor_mask;  // 0x80808080 turns u8 into (u8 - 128) as int8
+  uint32_t pad;       // replicated into every dword of an out-of-range chunk
+};
+
+// Implicit im2col rows over an NHWC activation with channels padded to cpc
+// 16-byte chunks.
+struct Im2colOperand {
+  const void* base;
+  int H, W, OH, OW, KW, cpc;
+  int sh, sw, dh, dw, pt, pl;
+  int rows, kc;
+  uint32_t xor_mask, pad;
+};
+
+// Output mapping shared by both epilogues: element (i, j) lives at
+// (i / ohw) * bstride + (i % ohw) * si + j * sj.
+struct OutMap {
+  void* y;
+  int64_t si, sj, bstride;
+  int ohw, P, Q;
+  int vec;
+};
+
+struct FloatOut : OutMap {
+  float alpha, beta;
+  const void* bias;  // same element type as the output
+  int bias_mode;
+  int act;
+  float lo, hi;
+};
+
+struct QuantOut : OutMap {
+  int w_on_i;
+  const int32_t* colsum;
+  const int32_t* bias;
+  int32_t ca;
+  const int32_t* ca_rows;
+  const float* comb;
+  int n_comb;
+  int out_kind;
+  int32_t y_zp, lo, hi;
+};
+
+struct GemvArgs {
+  const void* a;   // [M][lda] activations
+  int64_t lda;     // elements
+  const void* w;   // [N][ldw] packed weight rows
+  int64_t ldw;     // elements
+  int M, N, kc;
+  int splits, chunks_per_split;
+  float* partial;  // [splits][M][N]
+};
+
+hipError_t run_dense_float(int dtype, const DenseOperand& x, const DenseOperand& y, const FloatOut& o, int tile,
+                           hipStream_t st);
+hipError_t run_conv_float(int dtype, const Im2colOperand& col, const DenseOperand& w, bool col_on_x,
+                          const FloatOut& o, int tile, hipStream_t st);
+hipError_t run_dense_quant(const DenseOperand& x, const DenseOperand& y, const QuantOut& o, int tile,
+                           hipStream_t st);
+hipError_t run_conv_quant(const Im2colOperand& col, const DenseOperand& w, bool col_on_x, const QuantOut& o,
+                          int tile, hipStream_t st);
+hipError_t run_gemv(int dtype, const GemvArgs& g, const FloatOut& o, hipStream_t st);
+hipError_t run_nchw_to_nhwc(int elem_bytes, const void* src, void* dst, int N, int C, int HW, int cp,
+                            hipStream_t st);
+hipError_t run_gather2d(int elem_bytes, const void* src, int64_t rs, int64_t cs, void* dst, int R, int K, int ld,
+                        hipStream_t st);
+
+}  // namespace ohip

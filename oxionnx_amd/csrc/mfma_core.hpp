@@ -1,0 +1,283 @@
+// Shared MFMA tile engine for every dense contraction in the provider.
+//
+// One kernel skeleton computes D[i][j] = sum_k X[i][k] * Y[j][k] for the
+// f32, f16, bf16 and int8 paths.  Both operands are staged in LDS as rows of
+// K-contiguous 16-byte chunks, so the same skeleton serves
+//   * Gemm / MatMul  (X = packed weight rows [N][K], Y = activation rows [M][K]),
+//   * Conv NCHW out  (X = implicit im2col rows of an NHWC input, Y = weights),
+//   * Conv NHWC out  (X = weights, Y = implicit im2col rows).
+// Nothing is materialised for im2col: the loader gathers 16-byte channel
+// chunks straight from the NHWC activation.
+//
+// Per 64-lane wave and per 16-byte fragment pair the engine issues
+//   f16/bf16: one v_mfma_f32_16x16x32_{f16,bf16}
+//   int8    : one v_mfma_i32_16x16x64_i8
+//   f32     : four v_mfma_f32_16x16x4_f32 (lane group g supplies k = 4g+e for
+//             the e-th instruction in both operands, so the sums agree)
+// and the 16x16 result lands with lane l holding rows 4*(l/16)..+3 of column
+// l%16: each lane owns four P-consecutive outputs, which is why the side whose
+// output index is memory-contiguous is always put on X.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace ohip {
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+
+enum class Op { F32, F16, BF16, I8 };
+
+template <Op O> struct OpT;
+template <> struct OpT<Op::F16> {
+  using Acc = f32x4;
+  static constexpr int kElemBytes = 2;
+  static __device__ __forceinline__ Acc mma(u32x4 a, u32x4 b, Acc c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
+                                                  __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+  }
+};
+template <> struct OpT<Op::BF16> {
+  using Acc = f32x4;
+  static constexpr int kElemBytes = 2;
+  static __device__ __forceinline__ Acc mma(u32x4 a, u32x4 b, Acc c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+  }
+};
+template <> struct OpT<Op::I8> {
+  using Acc = i32x4;
+  static constexpr int kElemBytes = 1;
+  static __device__ __forceinline__ Acc mma(u32x4 a, u32x4 b, Acc c) {
+    return __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(i32x4, a),
+                                                 __builtin_bit_cast(i32x4, b), c, 0, 0, 0);
+  }
+};
+template <> struct OpT<Op::F32> {
+  using Acc = f32x4;
+  static constexpr int kElemBytes = 4;
+  static __device__ __forceinline__ Acc mma(u32x4 a, u32x4 b, Acc c) {
+    c = __builtin_amdgcn_mfma_f32_16x16x4f32(__builtin_bit_cast(float, a.x),
+                                             __builtin_bit_cast(float, b.x), c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f32_16x16x4f32(__builtin_bit_cast(float, a.y),
+                                             __builtin_bit_cast(float, b.y), c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f32_16x16x4f32(__builtin_bit_cast(float, a.z),
+                                             __builtin_bit_cast(float, b.z), c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f32_16x16x4f32(__builtin_bit_cast(float, a.w),
+                                             __builtin_bit_cast(float, b.w), c, 0, 0, 0);
+    return c;
+  }
+};
+
+// Block tile: BP x BQ outputs, WP x WQ waves, one 128-byte K slab per stage.
+template <int BP_, int BQ_, int WP_, int WQ_> struct Tile {
+  static constexpr int BP = BP_, BQ = BQ_, WP = WP_, WQ = WQ_;
+  static constexpr int kThreads = 64 * WP * WQ;
+  static constexpr int TP = BP / (WP * 16), TQ = BQ / (WQ * 16);
+  static constexpr int kChunks = 8;          // 16-byte chunks per row per stage
+  static constexpr int kRowStride = 9;       // +1 chunk of padding: rows start 16 B apart mod 128
+  static constexpr int NX = BP * kChunks / kThreads;
+  static constexpr int NY = BQ * kChunks / kThreads;
+  static constexpr int kStage = (BP + BQ) * kRowStride;  // in u32x4 units
+  static_assert(TP >= 1 && TQ >= 1, "wave tile must hold at least one 16x16 MFMA tile");
+  static_assert(NX >= 1 && NY >= 1 && NX * kThreads == BP * kChunks && NY * kThreads == BQ * kChunks,
+                "loader split must be exact");
+};
+
+// ---------------------------------------------------------------- loaders
+// A loader owns NR rows of one operand for the lifetime of the block.  Thread
+// t loads chunk (t & 7) of rows (t >> 3) + i * (threads / 8), i < NR.
+struct DenseRows {
+  const char* base;   // row 0
+  int64_t ld;         // bytes between rows (multiple of 16)
+  int rows;           // valid rows
+  int kc;             // valid 16-byte chunks per row
+  uint32_t xor_mask;  // applied to every loaded dword (u8 -> int8 shift uses 0x80808080)
+  u32x4 pad;          // value used outside the matrix
+
+  template <int NR, int kThreads>
+  struct State { const char* ptr[NR]; bool ok[NR]; };
+
+  template <int NR, int kThreads>
+  __device__ __forceinline__ void init(State<NR, kThreads>& s, int row0, int t) const {
+#pragma unroll
+    for (int i = 0; i < NR; ++i) {
+      int r = row0 + (t >> 3) + i * (kThreads / 8);
+      s.ok[i] = r < rows;
+      s.ptr[i] = base + (int64_t)(s.ok[i] ? r : 0) * ld;
+    }
+  }
+  template <int NR, int kThreads>
+  __device__ __forceinline__ void load(const State<NR, kThreads>& s, int kt, int t, u32x4 (&v)[NR]) const {
+    const int gk = kt * 8 + (t & 7);
+    const bool kin = gk < kc;
+#pragma unroll
+    for (int i = 0; i < NR; ++i) {
+      if (s.ok[i] && kin) {
+        u32x4 x = *reinterpret_cast<const u32x4*>(s.ptr[i] + (int64_t)gk * 16);
+        v[i] = x ^ xor_mask;
+      } else {
+        v[i] = gk < kc ? pad : u32x4{0, 0, 0, 0};
+      }
+    }
+  }
+};
+
+// Implicit im2col over an NHWC activation whose channel count is padded to a
+// whole number of 16-byte chunks (cpc chunks per pixel).  Row r is output
+// pixel (n, oy, ox); K runs over (ky, kx, channel chunk).
+struct Im2colNHWC {
+  const char* base;    // x[0][0][0][0]
+  int H, W, OH, OW;
+  int KW;
+  int cpc;             // 16-byte channel chunks per pixel
+  int sh, sw, dh, dw, pt, pl;
+  int rows;            // N * OH * OW
+  int kc;              // KH * KW * cpc
+  uint32_t xor_mask;
+  u32x4 pad;           // value of a padding tap (already in the shifted domain)
+
+  template <int NR, int kThreads>
+  struct State { const char* img[NR]; int iy0[NR], ix0[NR]; bool ok[NR]; };
+
+  template <int NR, int kThreads>
+  __device__ __forceinline__ void init(State<NR, kThreads>& s, int row0, int t) const {
+    const int ohw = OH * OW;
+#pragma unroll
+    for (int i = 0; i < NR; ++i) {
+      int r = row0 + (t >> 3) + i * (kThreads / 8);
+      s.ok[i] = r < rows;
+      int rr = s.ok[i] ? r : 0;
+      int n = rr / ohw, rem = rr - n * ohw;
+      int oy = rem / OW, ox = rem - oy * OW;
+      s.img[i] = base + (int64_t)n * H * W * cpc * 16;
+      s.iy0[i] = oy * sh - pt;
+      s.ix0[i] = ox * sw - pl;
+    }
+  }
+  template <int NR, int kThreads>
+  __device__ __forceinline__ void load(const State<NR, kThreads>& s, int kt, int t, u32x4 (&v)[NR]) const {
+    const int gk = kt * 8 + (t & 7);
+    const bool kin = gk < kc;
+    const int tap = gk / cpc;
+    const int cc = gk - tap * cpc;
+    const int ky = tap / KW;
+    const int kx = tap - ky * KW;
+    const int dy = ky * dh, dx = kx * dw;
+#pragma unroll
+    for (int i = 0; i < NR; ++i) {
+      const int iy = s.iy0[i] + dy, ix = s.ix0[i] + dx;
+      const bool inside = s.ok[i] && kin && (unsigned)iy < (unsigned)H && (unsigned)ix < (unsigned)W;
+      if (inside) {
+        u32x4 x = *reinterpret_cast<const u32x4*>(s.img[i] + ((int64_t)(iy * W + ix) * cpc + cc) * 16);
+        v[i] = x ^ xor_mask;
+      } else {
+        v[i] = kin ? pad : u32x4{0, 0, 0, 0};
+      }
+    }
+  }
+};
+
+// XCD-aware tile order.  The dispatcher hands consecutive workgroup ids to
+// the 8 XCDs in turn; remapping makes each XCD own a contiguous run of
+// logical tiles, and the grouped order inside a run keeps GP P-tiles sharing
+// the same Q-tile panel resident in that XCD's L2.
+__device__ __forceinline__ void map_tile(int bid, int nb, int nP, int nQ, int& tp, int& tq) {
+  int id = bid;
+  if ((nb & 7) == 0) id = (bid & 7) * (nb >> 3) + (bid >> 3);
+  constexpr int GP = 8;
+  const int per_group = GP * nQ;
+  const int g = id / per_group;
+  const int first = g * GP;
+  const int gsz = min(nP - first, GP);
+  const int within = id - g * per_group;
+  tp = first + within % gsz;
+  tq = within / gsz;
+}
+
+template <Op O, class Tl, class LX, class LY, class Epi>
+__global__ void __launch_bounds__(Tl::kThreads)
+mfma_gemm_kernel(const LX lx, const LY ly, const Epi epi, int nP, int nQ, int kc) {
+  using A = typename OpT<O>::Acc;
+  __shared__ u32x4 smem[2 * Tl::kStage];
+  const int t = threadIdx.x;
+  const int lane = t & 63;
+  const int wave = t >> 6;
+  const int wp = wave % Tl::WP, wq = wave / Tl::WP;
+  int tp, tq;
+  map_tile(blockIdx.x, gridDim.x, nP, nQ, tp, tq);
+  const int p0 = tp * Tl::BP, q0 = tq * Tl::BQ;
+
+  typename LX::template State<Tl::NX, Tl::kThreads> sx;
+  typename LY::template State<Tl::NY, Tl::kThreads> sy;
+  lx.init(sx, p0, t);
+  ly.init(sy, q0, t);
+
+  u32x4 rx[Tl::NX], ry[Tl::NY];
+  A acc[Tl::TP][Tl::TQ];
+#pragma unroll
+  for (int a = 0; a < Tl::TP; ++a)
+#pragma unroll
+    for (int b = 0; b < Tl::TQ; ++b) acc[a][b] = A{0, 0, 0, 0};
+
+  const int nk = (kc + 7) >> 3;
+  const int srow = t >> 3, schunk = t & 7;
+
+  auto stash = [&](int stage) {
+    u32x4* s = smem + stage * Tl::kStage;
+#pragma unroll
+    for (int i = 0; i < Tl::NX; ++i)
+      s[(srow + i * (Tl::kThreads / 8)) * Tl::kRowStride + schunk] = rx[i];
+#pragma unroll
+    for (int i = 0; i < Tl::NY; ++i)
+      s[(Tl::BP + srow + i * (Tl::kThreads / 8)) * Tl::kRowStride + schunk] = ry[i];
+  };
+
+  if (nk > 0) {
+    lx.load(sx, 0, t, rx);
+    ly.load(sy, 0, t, ry);
+    stash(0);
+  }
+  __syncthreads();
+
+  const int xrow = (wp * Tl::TP * 16 + (lane & 15)) * Tl::kRowStride + (lane >> 4);
+  const int yrow = (Tl::BP + wq * Tl::TQ * 16 + (lane & 15)) * Tl::kRowStride + (lane >> 4);
+
+  for (int kt = 0; kt < nk; ++kt) {
+    const int cur = kt & 1;
+    const bool more = kt + 1 < nk;
+    if (more) {
+      lx.load(sx, kt + 1, t, rx);
+      ly.load(sy, kt + 1, t, ry);
+    }
+    const u32x4* s = smem + cur * Tl::kStage;
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk) {
+      u32x4 fx[Tl::TP], fy[Tl::TQ];
+#pragma unroll
+      for (int a = 0; a < Tl::TP; ++a) fx[a] = s[xrow + a * 16 * Tl::kRowStride + kk * 4];
+#pragma unroll
+      for (int b = 0; b < Tl::TQ; ++b) fy[b] = s[yrow + b * 16 * Tl::kRowStride + kk * 4];
+#pragma unroll
+      for (int a = 0; a < Tl::TP; ++a)
+#pragma unroll
+        for (int b = 0; b < Tl::TQ; ++b) acc[a][b] = OpT<O>::mma(fx[a], fy[b], acc[a][b]);
+    }
+    if (more) stash(cur ^ 1);
+    __syncthreads();
+  }
+
+#pragma unroll
+  for (int a = 0; a < Tl::TP; ++a)
+#pragma unroll
+    for (int b = 0; b < Tl::TQ; ++b) {
+      const int i0 = p0 + wp * Tl::TP * 16 + a * 16 + (lane >> 4) * 4;
+      const int j = q0 + wq * Tl::TQ * 16 + b * 16 + (lane & 15);
+      epi.store(i0, j, acc[a][b]);
+    }
+}
+
+}  // namespace ohip

@@ -1,0 +1,982 @@
+// Host side of the provider behind include/ohip.h: context, memory, weight
+// residency, the dispatch gate and the op entry points that choose and launch
+// the device kernels in kernels.hip.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cctype>
+#include <climits>
+#include <cmath>
+#include <cstdlib>
+#include <cstring>
+#include <map>
+#include <mutex>
+#include <new>
+#include <string>
+#include <vector>
+
+#include "../../include/ohip.h"
+#include "internal.hpp"
+
+using namespace ohip;
+
+// ------------------------------------------------------------------ errors
+static thread_local std::string g_last_error;
+
+static int fail(int code, const std::string& msg) {
+  g_last_error = msg;
+  return code;
+}
+static int hip_fail(hipError_t e, const char* what) {
+  return fail(OHIP_E_HIP, std::string(what) + ": " + hipGetErrorString(e));
+}
+#define HIP_TRY(expr, what)                 \
+  do {                                      \
+    hipError_t _e = (expr);                 \
+    if (_e != hipSuccess) return hip_fail(_e, what); \
+  } while (0)
+
+extern "C" const char* ohip_last_error(void) { return g_last_error.c_str(); }
+extern "C" const char* ohip_version(void) { return "oxionnx-hip 0.1.0 (gfx950)"; }
+
+// oxionnx-cuda/src/context.rs:165-193: unset -> false; "", 0, false, no, off
+// (trimmed, case-insensitive) -> false; anything else -> true.
+extern "C" int ohip_env_flag(const char* name) {
+  const char* v = name ? std::getenv(name) : nullptr;
+  if (!v) return 0;
+  std::string s(v);
+  size_t b = s.find_first_not_of(" \t\r\n"), e = s.find_last_not_of(" \t\r\n");
+  s = b == std::string::npos ? std::string() : s.substr(b, e - b + 1);
+  for (auto& ch : s) ch = (char)std::tolower((unsigned char)ch);
+  return !(s.empty() || s == "0" || s == "false" || s == "no" || s == "off");
+}
+
+// ------------------------------------------------------------------ types
+enum WeightKind { WK_GEMM = 1, WK_CONV = 2, WK_QGEMM = 3, WK_QCONV = 4 };
+
+struct ohip_weight {
+  ohip_ctx* ctx = nullptr;
+  bool cached = false;
+  int kind = 0;
+  int dtype = 0;           // F32/F16/BF16 for float, I8 for integer
+  int64_t rows = 0;        // N (gemm) or Cout (conv)
+  int64_t k = 0;           // logical K (gemm) or Cin (conv)
+  int64_t kh = 1, kw = 1;  // conv only
+  int cpc = 0;             // conv: 16-byte channel chunks per tap
+  int kc = 0;              // 16-byte chunks per packed row
+  int64_t ld_bytes = 0;
+  void* data = nullptr;
+  int32_t* colsum = nullptr;      // integer only
+  std::vector<float> scale;       // integer only (1 or rows entries)
+  float* comb = nullptr;          // device, rows entries (integer only)
+  float comb_a = NAN, comb_y = NAN;
+  size_t bytes = 0;
+};
+
+struct ohip_ctx {
+  int device = 0;
+  hipStream_t own = nullptr;
+  hipStream_t stream = nullptr;
+  ohip_tuning tuning{};
+  int tile_override = 0;
+  void* scratch = nullptr;
+  size_t scratch_bytes = 0;
+  std::map<std::string, ohip_weight*> weights;
+  ohip_counters counters{};
+  std::mutex mu;
+};
+
+static int activate(ohip_ctx* ctx) {
+  if (!ctx) return fail(OHIP_E_INVALID, "null context");
+  HIP_TRY(hipSetDevice(ctx->device), "hipSetDevice");
+  return OHIP_OK;
+}
+
+// One bump-allocated scratch region per call.  The region only grows; growth
+// synchronises the stream first so no in-flight kernel still reads the old one.
+struct ScratchPlan {
+  std::vector<size_t> sizes;
+  size_t add(size_t b) {
+    sizes.push_back((b + 255) & ~size_t(255));
+    return sizes.size() - 1;
+  }
+  size_t total() const {
+    size_t t = 0;
+    for (auto s : sizes) t += s;
+    return t;
+  }
+};
+
+static int scratch_reserve(ohip_ctx* ctx, size_t bytes) {
+  if (bytes <= ctx->scratch_bytes) return OHIP_OK;
+  HIP_TRY(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
+  if (ctx->scratch) HIP_TRY(hipFree(ctx->scratch), "hipFree(scratch)");
+  ctx->scratch = nullptr;
+  ctx->scratch_bytes = 0;
+  size_t want = std::max<size_t>(bytes, size_t(1) << 20);
+  hipError_t e = hipMalloc(&ctx->scratch, want);
+  if (e != hipSuccess) return fail(OHIP_E_NOMEM, std::string("scratch hipMalloc: ") + hipGetErrorString(e));
+  ctx->scratch_bytes = want;
+  return OHIP_OK;
+}
+
+static void* scratch_at(ohip_ctx* ctx, const ScratchPlan& p, size_t idx) {
+  size_t off = 0;
+  for (size_t i = 0; i < idx; ++i) off += p.sizes[i];
+  return static_cast<char*>(ctx->scratch) + off;
+}
+
+// ------------------------------------------------------------------ context
+extern "C" int ohip_device_count(int* count) {
+  if (!count) return fail(OHIP_E_INVALID, "null count");
+  int n = 0;
+  hipError_t e = hipGetDeviceCount(&n);
+  if (e != hipSuccess) n = 0;
+  *count = n;
+  return OHIP_OK;
+}
+
+extern "C" int ohip_ctx_create(int device, ohip_ctx** out) {
+  if (!out) return fail(OHIP_E_INVALID, "null out");
+  *out = nullptr;
+  int n = 0;
+  if (hipGetDeviceCount(&n) != hipSuccess || n <= 0) return fail(OHIP_E_NODEVICE, "no HIP device");
+  if (device < 0 || device >= n) return fail(OHIP_E_INVALID, "device index out of range");
+  HIP_TRY(hipSetDevice(device), "hipSetDevice");
+  hipDeviceProp_t prop;
+  HIP_TRY(hipGetDeviceProperties(&prop, device), "hipGetDeviceProperties");
+  if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+    return fail(OHIP_E_NODEVICE, std::string("kernels are built for gfx950, device is ") + prop.gcnArchName);
+  auto* ctx = new (std::nothrow) ohip_ctx();
+  if (!ctx) return fail(OHIP_E_NOMEM, "context allocation");
+  ctx->device = device;
+  hipError_t e = hipStreamCreateWithFlags(&ctx->own, hipStreamNonBlocking);
+  if (e != hipSuccess) {
+    delete ctx;
+    return hip_fail(e, "hipStreamCreate");
+  }
+  ctx->stream = ctx->own;
+  ohip_tuning_for_class(OHIP_CLASS_MI355X, &ctx->tuning);
+  *out = ctx;
+  return OHIP_OK;
+}
+
+static void weight_free(ohip_weight* w) {
+  if (!w) return;
+  if (w->data) (void)hipFree(w->data);
+  if (w->colsum) (void)hipFree(w->colsum);
+  if (w->comb) (void)hipFree(w->comb);
+  delete w;
+}
+
+extern "C" void ohip_ctx_destroy(ohip_ctx* ctx) {
+  if (!ctx) return;
+  (void)hipSetDevice(ctx->device);
+  (void)hipStreamSynchronize(ctx->stream);
+  for (auto& kv : ctx->weights) weight_free(kv.second);
+  if (ctx->scratch) (void)hipFree(ctx->scratch);
+  if (ctx->own) (void)hipStreamDestroy(ctx->own);
+  delete ctx;
+}
+
+extern "C" int ohip_ctx_set_stream(ohip_ctx* ctx, void* s) {
+  if (!ctx) return fail(OHIP_E_INVALID, "null context");
+  ctx->stream = s ? static_cast<hipStream_t>(s) : ctx->own;
+  return OHIP_OK;
+}
+extern "C" void* ohip_ctx_stream(ohip_ctx* ctx) { return ctx ? (void*)ctx->stream : nullptr; }
+
+extern "C" int ohip_sync(ohip_ctx* ctx) {
+  int rc = activate(ctx);
+  if (rc) return rc;
+  HIP_TRY(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
+  return OHIP_OK;
+}
+
+extern "C" int ohip_set_tile_override(ohip_ctx* ctx, int tile) {
+  if (!ctx) return fail(OHIP_E_INVALID, "null context");
+  if (tile != 0 && tile != 64 && tile != 128 && tile != 256) return fail(OHIP_E_INVALID, "tile must be 0/64/128/256");
+  ctx->tile_override = tile;
+  return OHIP_OK;
+}
+
+// ------------------------------------------------------------------ memory
+extern "C" int ohip_malloc(ohip_ctx* ctx, size_t bytes, void** p) {
+  int rc = activate(ctx);
+  if (rc) return rc;
+  if (!p) return fail(OHIP_E_INVALID, "null out");
+  hipError_t e = hipMalloc(p, bytes ? bytes : 1);
+  if (e != hipSuccess) return fail(OHIP_E_NOMEM, std::string("hipMalloc: ") + hipGetErrorString(e));
+  return OHIP_OK;
+}
+extern "C" int ohip_free(ohip_ctx* ctx, void* p) {
+  int rc = activate(ctx);
+  if (rc) return rc;
+  HIP_TRY(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
+  HIP_TRY(hipFree(p), "hipFree");
+  return OHIP_OK;
+}
+extern "C" int ohip_memcpy_h2d(ohip_ctx* ctx, void* dst, const void* src, size_t bytes) {
+  int rc = activate(ctx);
+  if (rc) return rc;
+  HIP_TRY(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, ctx->stream), "hipMemcpyAsync H2D");
+  ctx->counters.h2d_bytes += bytes;
+  return OHIP_OK;
+}
+extern "C" int ohip_memcpy_d2h(ohip_ctx* ctx, void* dst, const void* src, size_t bytes) {
+  int rc = activate(ctx);
+  if (rc) return rc;
+  HIP_TRY(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, ctx->stream), "hipMemcpyAsync D2H");
+  HIP_TRY(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
+  ctx->counters.d2h_bytes += bytes;
+  return OHIP_OK;
+}
+extern "C" int ohip_memcpy_d2d(ohip_ctx* ctx, void* dst, const void* src, size_t bytes) {
+  int rc = activate(ctx);
+  if (rc) return rc;
+  HIP_TRY(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, ctx->stream), "hipMemcpyAsync D2D");
+  return OHIP_OK;
+}
+
+// ------------------------------------------------------------------ gate
+// Thresholds for MI355X.  The reference's discrete-class numbers
+// (tuning.rs:487-545) were measured for an RTX A4000 behind PCIe with a
+// 24-thread host.  An MI355X finishes even the per-dispatch-upload cases far
+// sooner, so the floors are derived from its own cost model (PCIe Gen5 x16
+// ~50 GB/s effective, ~20 us fixed round trip, the reference's single-thread
+// 2-D sgemm at ~50 GFLOP/s): a per-dispatch GEMM wins once 2mkn / 50e9 exceeds
+// 20 us + 4 (mk + kn + mn) / 50e9, i.e. mkn >= ~1e6 and intensity >= ~8; a
+// cached B removes the k·n upload, leaving the fixed cost (mkn >= ~5e5).
+// Conv's implied GEMM uses the same fixed-cost floor.  bench.py and
+// tests/test_gate.py record the measured crossovers these are checked by.
+extern "C" int ohip_tuning_for_class(int cls, ohip_tuning* t) {
+  if (!t) return fail(OHIP_E_INVALID, "null tuning");
+  switch (cls) {
+    case OHIP_CLASS_MI355X:
+      *t = ohip_tuning{OHIP_CLASS_MI355X, 1000000ull, 500000ull, 8ull, 500000ull};
+      return OHIP_OK;
+    case OHIP_CLASS_PARITY:  // GpuTuning::PARITY (tuning.rs:409-425)
+      *t = ohip_tuning{OHIP_CLASS_PARITY, 0, 0, 0, 0};
+      return OHIP_OK;
+    case OHIP_CLASS_NEVER:  // GpuTuning::NEVER (tuning.rs:441-456)
+      *t = ohip_tuning{OHIP_CLASS_NEVER, UINT64_MAX, UINT64_MAX, UINT64_MAX, UINT64_MAX};
+      return OHIP_OK;
+    case OHIP_CLASS_LEGACY:  // GpuTuning::for_class(Discrete) (tuning.rs:487-545)
+      *t = ohip_tuning{OHIP_CLASS_LEGACY, 25000000ull, 5000000ull, 56ull, 10000000ull};
+      return OHIP_OK;
+    default: return fail(OHIP_E_INVALID, "unknown perf class");
+  }
+}
+extern "C" int ohip_set_tuning(ohip_ctx* ctx, const ohip_tuning* t) {
+  if (!ctx || !t) return fail(OHIP_E_INVALID, "null argument");
+  ctx->tuning = *t;
+  return OHIP_OK;
+}
+extern "C" int ohip_get_tuning(ohip_ctx* ctx, ohip_tuning* t) {
+  if (!ctx || !t) return fail(OHIP_E_INVALID, "null argument");
+  *t = ctx->tuning;
+  return OHIP_OK;
+}
+
+static bool mul_ok(uint64_t a, uint64_t b, uint64_t* r) { return !__builtin_mul_overflow(a, b, r); }
+
+// gemm_mac (tuning.rs:500-503); false on u64 overflow.
+static bool gemm_mac_checked(int64_t m, int64_t k, int64_t n, uint64_t* mac) {
+  if (m < 0 || k < 0 || n < 0) return false;
+  uint64_t mk;
+  return mul_ok((uint64_t)m, (uint64_t)k, &mk) && mul_ok(mk, (uint64_t)n, mac);
+}
+extern "C" uint64_t ohip_gemm_mac(int64_t m, int64_t k, int64_t n) {
+  uint64_t mac = 0;
+  return gemm_mac_checked(m, k, n, &mac) ? mac : UINT64_MAX;
+}
+// gemm_intensity (tuning.rs:516-529): floor(2mkn / (mk + kn + mn)); 0 if
+// degenerate or overflowing (the reference's None).
+extern "C" uint64_t ohip_gemm_intensity(int64_t m, int64_t k, int64_t n) {
+  if (m < 0 || k < 0 || n < 0) return 0;
+  uint64_t mk, kn, mn, mkn, f;
+  if (!mul_ok(m, k, &mk) || !mul_ok(k, n, &kn) || !mul_ok(m, n, &mn)) return 0;
+  uint64_t moved;
+  if (__builtin_add_overflow(mk, kn, &moved) || __builtin_add_overflow(moved, mn, &moved) || moved == 0) return 0;
+  if (!mul_ok(mk, n, &mkn) || !mul_ok(mkn, 2, &f)) return 0;
+  return f / moved;
+}
+// gemm_admits (tuning.rs:575-594): zero extents and overflow decline.
+extern "C" int ohip_gemm_admits(const ohip_tuning* t, int64_t m, int64_t k, int64_t n, int cached) {
+  if (!t || m <= 0 || k <= 0 || n <= 0) return 0;
+  uint64_t mac;
+  if (!gemm_mac_checked(m, k, n, &mac)) return 0;
+  if (cached) return mac >= t->gemm_min_mac_cached;
+  if (mac < t->gemm_min_mac) return 0;
+  if (t->gemm_min_intensity == 0) return 1;
+  uint64_t i = ohip_gemm_intensity(m, k, n);
+  return i != 0 && i >= t->gemm_min_intensity;
+}
+// conv_admits (tuning.rs:606-610): only overflow declines outright.
+extern "C" int ohip_conv_admits(const ohip_tuning* t, int64_t m, int64_t k, int64_t n) {
+  uint64_t mac;
+  if (!t || !gemm_mac_checked(m, k, n, &mac)) return 0;
+  return mac >= t->conv_min_mac;
+}
+
+// ------------------------------------------------------------------ host conversions
+static inline uint16_t f32_to_f16_rne(float f) {
+  uint32_t x;
+  std::memcpy(&x, &f, 4);
+  uint32_t sign = (x >> 16) & 0x8000u, exp = (x >> 23) & 0xffu, man = x & 0x7fffffu;
+  if (exp == 0xff) return (uint16_t)(man ? (sign | 0x7e00u | (man >> 13)) : (sign | 0x7c00u));
+  int e = (int)exp - 112;
+  if (e >= 31) return (uint16_t)(sign | 0x7c00u);
+  if (e <= 0) {
+    if (e < -10) return (uint16_t)sign;
+    uint32_t mm = man | 0x800000u;
+    int sh = 14 - e;
+    uint32_t h = mm >> sh, rem = mm & ((1u << sh) - 1), half = 1u << (sh - 1);
+    if (rem > half || (rem == half && (h & 1u))) ++h;
+    return (uint16_t)(sign | h);
+  }
+  uint32_t h = sign | ((uint32_t)e << 10) | (man >> 13), rem = man & 0x1fffu;
+  if (rem > 0x1000u || (rem == 0x1000u && (h & 1u))) ++h;
+  return (uint16_t)h;
+}
+static inline float f16_to_f32(uint16_t h) {
+  uint32_t sign = ((uint32_t)h & 0x8000u) << 16, exp = (h >> 10) & 0x1fu, man = h & 0x3ffu, x;
+  if (exp == 0) {
+    if (!man) x = sign;
+    else {
+      int e = -1;
+      do { man <<= 1; ++e; } while (!(man & 0x400u));
+      x = sign | ((uint32_t)(112 - e) << 23) | ((man & 0x3ffu) << 13);
+    }
+  } else if (exp == 31) x = sign | 0x7f800000u | (man << 13);
+  else x = sign | ((exp + 112) << 23) | (man << 13);
+  float f;
+  std::memcpy(&f, &x, 4);
+  return f;
+}
+static inline uint16_t f32_to_bf16_rne(float f) {
+  uint32_t x;
+  std::memcpy(&x, &f, 4);
+  if ((x & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((x >> 16) | 0x40u);
+  return (uint16_t)((x + 0x7fffu + ((x >> 16) & 1u)) >> 16);
+}
+static inline float bf16_to_f32(uint16_t h) {
+  uint32_t x = (uint32_t)h << 16;
+  float f;
+  std::memcpy(&f, &x, 4);
+  return f;
+}
+
+static int elem_bytes(int dt) {
+  switch (dt) {
+    case OHIP_F32: case OHIP_I32: return 4;
+    case OHIP_F16: case OHIP_BF16: return 2;
+    case OHIP_U8: case OHIP_I8: return 1;
+    default: return 0;
+  }
+}
+static bool is_float(int dt) { return dt == OHIP_F32 || dt == OHIP_F16 || dt == OHIP_BF16; }
+static int64_t round_up(int64_t v, int64_t m) { return (v + m - 1) / m * m; }
+
+static float read_float(int dt, const void* p, int64_t i) {
+  switch (dt) {
+    case OHIP_F32: return static_cast<const float*>(p)[i];
+    case OHIP_F16: return f16_to_f32(static_cast<const uint16_t*>(p)[i]);
+    case OHIP_BF16: return bf16_to_f32(static_cast<const uint16_t*>(p)[i]);
+    default: return 0.0f;
+  }
+}
+// Write v (given as the source element's value) into a dtype slot.  A
+// same-dtype copy keeps the exact bits.
+static void write_elem(int dst_dt, void* dst, int64_t i, int src_dt, const void* src, int64_t si) {
+  if (dst_dt == src_dt) {
+    int b = elem_bytes(dst_dt);
+    std::memcpy(static_cast<char*>(dst) + i * b, static_cast<const char*>(src) + si * b, b);
+    return;
+  }
+  float v = read_float(src_dt, src, si);
+  switch (dst_dt) {
+    case OHIP_F32: static_cast<float*>(dst)[i] = v; break;
+    case OHIP_F16: static_cast<uint16_t*>(dst)[i] = f32_to_f16_rne(v); break;
+    case OHIP_BF16: static_cast<uint16_t*>(dst)[i] = f32_to_bf16_rne(v); break;
+    default: break;
+  }
+}
+
+// ------------------------------------------------------------------ weights
+static std::string cache_key(const ohip_weight_key* key, int kind, int dtype, size_t src_bytes,
+                             const std::vector<int64_t>& shape) {
+  std::string k(key->name);
+  k += '\x1f';
+  k += key->label ? key->label : "";
+  k += '\x1f' + std::to_string(kind) + '\x1f' + std::to_string(dtype) + '\x1f' + std::to_string(src_bytes);
+  for (auto s : shape) k += '\x1f' + std::to_string(s);
+  return k;
+}
+
+// Returns the cached weight for key or null; sets *key_str for the insert.
+static ohip_weight* cache_lookup(ohip_ctx* ctx, const ohip_weight_key* key, const std::string& ks) {
+  if (!key || !key->name) return nullptr;
+  auto it = ctx->weights.find(ks);
+  if (it == ctx->weights.end()) return nullptr;
+  ctx->counters.weight_hits++;
+  return it->second;
+}
+
+static int weight_upload(ohip_ctx* ctx, ohip_weight* w, const void* packed, size_t bytes) {
+  hipError_t e = hipMalloc(&w->data, bytes ? bytes : 16);
+  if (e != hipSuccess) return fail(OHIP_E_NOMEM, std::string("weight hipMalloc: ") + hipGetErrorString(e));
+  HIP_TRY(hipMemcpyAsync(w->data, packed, bytes, hipMemcpyHostToDevice, ctx->stream), "weight upload");
+  HIP_TRY(hipStreamSynchronize(ctx->stream), "weight upload sync");
+  w->bytes = bytes;
+  ctx->counters.weight_uploaded_bytes += bytes;
+  ctx->counters.h2d_bytes += bytes;
+  return OHIP_OK;
+}
+
+static int weight_finish(ohip_ctx* ctx, const ohip_weight_key* key, const std::string& ks, ohip_weight* w,
+                         ohip_weight** out) {
+  w->ctx = ctx;
+  if (key && key->name) {
+    w->cached = true;
+    ctx->weights[ks] = w;
+    ctx->counters.weight_misses++;
+    ctx->counters.weight_resident_bytes += w->bytes;
+  } else {
+    ctx->counters.weight_transient++;
+  }
+  *out = w;
+  return OHIP_OK;
+}
+
+extern "C" void ohip_weight_release(ohip_weight* w) {
+  if (!w || w->cached) return;
+  (void)hipSetDevice(w->ctx->device);
+  (void)hipStreamSynchronize(w->ctx->stream);
+  weight_free(w);
+}
+extern "C" size_t ohip_weight_bytes(const ohip_weight* w) { return w ? w->bytes : 0; }
+
+static int chunk_elems(int dt) { return 16 / elem_bytes(dt); }
+
+extern "C" int ohip_weight_gemm(ohip_ctx* ctx, const ohip_weight_key* key, int src_dt, const void* host,
+                                int64_t k, int64_t n, int trans_b, int dt, ohip_weight** out) {
+  int rc = activate(ctx);
+  if (rc) return rc;
+  if (!host || !out || !is_float(src_dt) || !is_float(dt) || k <= 0 || n <= 0 || k > INT_MAX || n > INT_MAX)
+    return fail(OHIP_E_INVALID, "ohip_weight_gemm: bad arguments");
+  std::lock_guard<std::mutex> lock(ctx->mu);
+  const size_t src_bytes = (size_t)(k * n) * elem_bytes(src_dt);
+  std::string ks = key && key->name ? cache_key(key, WK_GEMM, dt, src_bytes, {k, n, trans_b}) : std::string();
+  if (ohip_weight* hit = cache_lookup(ctx, key, ks)) {
+    *out = hit;
+    return OHIP_OK;
+  }
+  const int64_t ce = chunk_elems(dt), kp = round_up(k, ce);
+  std::vector<char> packed((size_t)(n * kp) * elem_bytes(dt), 0);
+  for (int64_t j = 0; j < n; ++j)
+    for (int64_t p = 0; p < k; ++p)
+      write_elem(dt, packed.data(), j * kp + p, src_dt, host, trans_b ? j * k + p : p * n + j);
+  auto* w = new ohip_weight();
+  w->kind = WK_GEMM; w->dtype = dt; w->rows = n; w->k = k;
+  w->kc = (int)(kp / ce); w->ld_bytes = kp * elem_bytes(dt);
+  rc = weight_upload(ctx, w, packed.data(), packed.size());
+  if (rc) { weight_free(w); return rc; }
+  return weight_finish(ctx, key, ks, w, out);
+}
+
+extern "C" int ohip_weight_conv(ohip_ctx* ctx, const ohip_weight_key* key, int src_dt, const void* host,
+                                int64_t cout, int64_t cin, int64_t kh, int64_t kw, int dt, ohip_weight** out) {
+  int rc = activate(ctx);
+  if (rc) return rc;
+  if (!host || !out || !is_float(src_dt) || !is_float(dt) || cout <= 0 || cin <= 0 || kh <= 0 || kw <= 0)
+    return fail(OHIP_E_INVALID, "ohip_weight_conv: bad arguments");
+  std::lock_guard<std::mutex> lock(ctx->mu);
+  const size_t src_bytes = (size_t)(cout * cin * kh * kw) * elem_bytes(src_dt);
+  std::string ks = key && key->name ? cache_key(key, WK_CONV, dt, src_bytes, {cout, cin, kh, kw}) : std::string();
+  if (ohip_weight* hit = cache_lookup(ctx, key, ks)) {
+    *out = hit;
+    return OHIP_OK;
+  }
+  const int64_t ce = chunk_elems(dt), cp = round_up(cin, ce), kp = kh * kw * cp;
+  if (kp > INT_MAX / 2) return fail(OHIP_E_INVALID, "ohip_weight_conv: filter too large");
+  // [Cout][Cin][KH][KW] -> [Cout][KH][KW][Cp], channels innermost.
+  std::vector<char> packed((size_t)(cout * kp) * elem_bytes(dt), 0);
+  for (int64_t o = 0; o < cout; ++o)
+    for (int64_t c = 0; c < cin; ++c)
+      for (int64_t y = 0; y < kh; ++y)
+        for (int64_t x = 0; x < kw; ++x)
+          write_elem(dt, packed.data(), o * kp + (y * kw + x) * cp + c, src_dt, host, ((o * cin + c) * kh + y) * kw + x);
+  auto* w = new ohip_weight();
+  w->kind = WK_CONV; w->dtype = dt; w->rows = cout; w->k = cin; w->kh = kh; w->kw = kw;
+  w->cpc = (int)(cp / ce); w->kc = (int)(kp / ce); w->ld_bytes = kp * elem_bytes(dt);
+  rc = weight_upload(ctx, w, packed.data(), packed.size());
+  if (rc) { weight_free(w); return rc; }
+  return weight_finish(ctx, key, ks, w, out);
+}
+
+// Integer packing: B'' = w - w_zp[channel] as int8 (declines when a value
+// leaves [-128, 127]), rows K-contiguous, plus the per-channel sum of B''
+// that the epilogue's zero-point correction needs.
+static int qpack_common(ohip_ctx* ctx, ohip_weight* w, std::vector<int8_t>& packed, const std::vector<int32_t>& colsum,
+                        const float* scale, int n_scale) {
+  int rc = weight_upload(ctx, w, packed.data(), packed.size());
+  if (rc) return rc;
+  hipError_t e = hipMalloc(&w->colsum, colsum.size() * 4);
+  if (e != hipSuccess) return fail(OHIP_E_NOMEM, "colsum hipMalloc");
+  HIP_TRY(hipMemcpy(w->colsum, colsum.data(), colsum.size() * 4, hipMemcpyHostToDevice), "colsum upload");
+  e = hipMalloc(&w->comb, (size_t)w->rows * 4);
+  if (e != hipSuccess) return fail(OHIP_E_NOMEM, "comb hipMalloc");
+  if (scale && n_scale > 0) w->scale.assign(scale, scale + n_scale);
+  w->bytes += colsum.size() * 4 + (size_t)w->rows * 4;
+  return OHIP_OK;
+}
+
+static int32_t int_at(int dt, const void* p, int64_t i) {
+  return dt == OHIP_U8 ? (int32_t) static_cast<const uint8_t*>(p)[i] : (int32_t) static_cast<const int8_t*>(p)[i];
+}
+
+extern "C" int ohip_weight_qgemm(ohip_ctx* ctx, const ohip_weight_key* key, int src_dt, const void* host,
+                                 int64_t k, int64_t n, int trans_b, const int32_t* zp, int n_zp,
+                                 const float* scale, int n_scale, ohip_weight** out) {
+  int rc = activate(ctx);
+  if (rc) return rc;
+  if (!host || !out || (src_dt != OHIP_U8 && src_dt != OHIP_I8) || k <= 0 || n <= 0 || k > INT_MAX || n > INT_MAX)
+    return fail(OHIP_E_INVALID, "ohip_weight_qgemm: bad arguments");
+  if (zp && n_zp != 1 && n_zp != n) return fail(OHIP_E_SHAPE, "b_zero_point has the wrong length");
+  if (scale && n_scale != 1 && n_scale != n) return fail(OHIP_E_SHAPE, "b_scale has the wrong length");
+  std::lock_guard<std::mutex> lock(ctx->mu);
+  std::string ks;
+  if (key && key->name) {
+    std::vector<int64_t> shape{k, n, trans_b, n_zp};
+    for (int i = 0; zp && i < n_zp; ++i) shape.push_back(zp[i]);
+    ks = cache_key(key, WK_QGEMM, src_dt, (size_t)(k * n), shape);
+    if (ohip_weight* hit = cache_lookup(ctx, key, ks)) {
+      if (scale && n_scale > 0) hit->scale.assign(scale, scale + n_scale), hit->comb_a = NAN;
+      *out = hit;
+      return OHIP_OK;
+    }
+  }
+  const int64_t kp = round_up(k, 16);
+  std::vector<int8_t> packed((size_t)(n * kp), 0);
+  std::vector<int32_t> colsum((size_t)n, 0);
+  for (int64_t j = 0; j < n; ++j) {
+    const int32_t z = zp ? (n_zp == 1 ? zp[0] : zp[j]) : 0;
+    int32_t s = 0;
+    for (int64_t p = 0; p < k; ++p) {
+      int32_t v = int_at(src_dt, host, trans_b ? j * k + p : p * n + j) - z;
+      if (v < -128 || v > 127) return fail(OHIP_DECLINED, "weight minus zero point leaves int8 range");
+      packed[(size_t)(j * kp + p)] = (int8_t)v;
+      s += v;
+    }
+    colsum[(size_t)j] = s;
+  }
+  auto* w = new ohip_weight();
+  w->kind = WK_QGEMM; w->dtype = OHIP_I8; w->rows = n; w->k = k; w->kc = (int)(kp / 16); w->ld_bytes = kp;
+  rc = qpack_common(ctx, w, packed, colsum, scale, n_scale);
+  if (rc) { weight_free(w); return rc; }
+  return weight_finish(ctx, key, ks, w, out);
+}
+
+extern "C" int ohip_weight_qconv(ohip_ctx* ctx, const ohip_weight_key* key, int src_dt, const void* host,
+                                 int64_t cout, int64_t cin, int64_t kh, int64_t kw, const int32_t* zp, int n_zp,
+                                 const float* scale, int n_scale, ohip_weight** out) {
+  int rc = activate(ctx);
+  if (rc) return rc;
+  if (!host || !out || (src_dt != OHIP_U8 && src_dt != OHIP_I8) || cout <= 0 || cin <= 0 || kh <= 0 || kw <= 0)
+    return fail(OHIP_E_INVALID, "ohip_weight_qconv: bad arguments");
+  if (zp && n_zp != 1 && n_zp != cout) return fail(OHIP_E_SHAPE, "w_zero_point has the wrong length");
+  if (scale && n_scale != 1 && n_scale != cout) return fail(OHIP_E_SHAPE, "w_scale has the wrong length");
+  std::lock_guard<std::mutex> lock(ctx->mu);
+  std::string ks;
+  if (key && key->name) {
+    std::vector<int64_t> shape{cout, cin, kh, kw, n_zp};
+    for (int i = 0; zp && i < n_zp; ++i) shape.push_back(zp[i]);
+    ks = cache_key(key, WK_QCONV, src_dt, (size_t)(cout * cin * kh * kw), shape);
+    if (ohip_weight* hit = cache_lookup(ctx, key, ks)) {
+      if (scale && n_scale > 0) hit->scale.assign(scale, scale + n_scale), hit->comb_a = NAN;
+      *out = hit;
+      return OHIP_OK;
+    }
+  }
+  const int64_t cp = round_up(cin, 16), kp = kh * kw * cp;
+  std::vector<int8_t> packed((size_t)(cout * kp), 0);
+  std::vector<int32_t> colsum((size_t)cout, 0);
+  for (int64_t o = 0; o < cout; ++o) {
+    const int32_t z = zp ? (n_zp == 1 ? zp[0] : zp[o]) : 0;
+    int32_t s = 0;
+    for (int64_t c = 0; c < cin; ++c)
+      for (int64_t y = 0; y < kh; ++y)
+        for (int64_t x = 0; x < kw; ++x) {
+          int32_t v = int_at(src_dt, host, ((o * cin + c) * kh + y) * kw + x) - z;
+          if (v < -128 || v > 127) return fail(OHIP_DECLINED, "weight minus zero point leaves int8 range");
+          packed[(size_t)(o * kp + (y * kw + x) * cp + c)] = (int8_t)v;
+          s += v;
+        }
+    colsum[(size_t)o] = s;
+  }
+  auto* w = new ohip_weight();
+  w->kind = WK_QCONV; w->dtype = OHIP_I8; w->rows = cout; w->k = cin; w->kh = kh; w->kw = kw;
+  w->cpc = (int)(cp / 16); w->kc = (int)(kp / 16); w->ld_bytes = kp;
+  rc = qpack_common(ctx, w, packed, colsum, scale, n_scale);
+  if (rc) { weight_free(w); return rc; }
+  return weight_finish(ctx, key, ks, w, out);
+}
+
+// combined = a_scale * w_scale / y_scale, formed in f32 in that order
+// (qlinear_matmul.rs:248, qlinear_conv.rs:99), cached on the weight.
+static int ensure_comb(ohip_ctx* ctx, ohip_weight* w, float a_s, float y_s, int* n_comb) {
+  if (w->scale.empty()) return fail(OHIP_E_INVALID, "weight has no scale");
+  *n_comb = (int)w->scale.size();
+  if (w->comb_a == a_s && w->comb_y == y_s) return OHIP_OK;
+  std::vector<float> c(w->scale.size());
+  for (size_t i = 0; i < c.size(); ++i) {
+    volatile float prod = a_s * w->scale[i];
+    c[i] = prod / y_s;
+  }
+  HIP_TRY(hipMemcpyAsync(w->comb, c.data(), c.size() * 4, hipMemcpyHostToDevice, ctx->stream), "comb upload");
+  HIP_TRY(hipStreamSynchronize(ctx->stream), "comb upload sync");
+  w->comb_a = a_s;
+  w->comb_y = y_s;
+  return OHIP_OK;
+}
+
+// ------------------------------------------------------------------ helpers
+static bool aligned(const void* p, size_t a) { return ((uintptr_t)p % a) == 0; }
+
+extern "C" int64_t ohip_conv_out_dim(int64_t in, int64_t pb, int64_t pe, int64_t k, int64_t d, int64_t s) {
+  if (s <= 0 || k <= 0 || d <= 0 || in < 0 || pb < 0 || pe < 0) return -1;
+  int64_t eff = (k - 1) * d + 1, padded = in + pb + pe;
+  if (padded < eff) return -1;
+  return (padded - eff) / s + 1;
+}
+
+// Bring an activation matrix [R][K] (row stride ld elements, or transposed
+// [K][R]) into K-contiguous rows of whole 16-byte chunks.  Returns either the
+// original pointer or a scratch copy.
+struct RowsView {
+  const void* p;
+  int64_t ld_bytes;
+  int kc;
+};
+
+static bool rows_direct(const void* a, int64_t k, int64_t ld, int eb, int trans) {
+  const int ce = 16 / eb;
+  return !trans && k % ce == 0 && (ld * eb) % 16 == 0 && aligned(a, 16);
+}
+
+// ------------------------------------------------------------------ float GEMM
+static const int kMaxGemvM = 8;
+
+extern "C" int ohip_gemm(ohip_ctx* ctx, const ohip_gemm_desc* d, const void* a, const ohip_weight* b,
+                         const void* c, void* y) {
+  int rc = activate(ctx);
+  if (rc) return rc;
+  if (!d || !a || !b || !y) return fail(OHIP_E_INVALID, "ohip_gemm: null argument");
+  if (!is_float(d->dtype) || b->kind != WK_GEMM || b->dtype != d->dtype)
+    return fail(OHIP_E_INVALID, "ohip_gemm: weight kind / dtype mismatch");
+  if (d->k != b->k || d->n != b->rows || d->m < 0)
+    return fail(OHIP_E_SHAPE, "ohip_gemm: shape disagrees with the packed weight");
+  if (d->m > INT_MAX / 2 || d->n > INT_MAX / 2) return fail(OHIP_DECLINED, "ohip_gemm: extent too large");
+  if (d->m == 0) return OHIP_OK;
+  if (d->c_kind != OHIP_C_NONE && !c) return fail(OHIP_E_INVALID, "ohip_gemm: c_kind set but C is null");
+  std::lock_guard<std::mutex> lock(ctx->mu);
+  ctx->counters.dispatches++;
+  const int eb = elem_bytes(d->dtype), ce = 16 / eb;
+  const int64_t M = d->m, N = d->n, K = d->k;
+  const int64_t lda = d->lda ? d->lda : (d->trans_a ? M : K);
+  const int64_t ldy = d->ldy ? d->ldy : N;
+  const int64_t kp = round_up(K, ce);
+  const bool direct = rows_direct(a, K, lda, eb, d->trans_a);
+  const bool gemv = M <= kMaxGemvM;
+
+  int splits = 1, cps = b->kc;
+  if (gemv) {
+    // enough (slice, row) waves to cover the chip several times over
+    const int64_t want_waves = 8192;
+    int64_t s = std::max<int64_t>(1, want_waves / std::max<int64_t>(1, N));
+    s = std::min<int64_t>(s, std::max<int64_t>(1, b->kc / 64));
+    cps = (int)((b->kc + s - 1) / s);
+    splits = (int)((b->kc + cps - 1) / cps);
+  }
+  ScratchPlan plan;
+  size_t ia = direct ? SIZE_MAX : plan.add((size_t)(M * kp) * eb);
+  size_t ip = gemv ? plan.add((size_t)splits * M * N * 4) : SIZE_MAX;
+  rc = scratch_reserve(ctx, plan.total());
+  if (rc) return rc;
+
+  RowsView av{a, lda * eb, (int)(kp / ce)};
+  if (!direct) {
+    void* pa = scratch_at(ctx, plan, ia);
+    int64_t rs = d->trans_a ? 1 : lda, cs = d->trans_a ? lda : 1;
+    HIP_TRY(run_gather2d(eb, a, rs, cs, pa, (int)M, (int)K, (int)kp, ctx->stream), "pack A");
+    av = RowsView{pa, kp * eb, (int)(kp / ce)};
+  }
+
+  FloatOut o{};
+  o.y = y; o.si = 1; o.sj = ldy; o.bstride = 0; o.ohw = INT_MAX; o.P = (int)N; o.Q = (int)M;
+  o.vec = (ldy % 4 == 0) && aligned(y, 4 * eb);
+  o.alpha = d->alpha; o.beta = d->beta; o.bias = c;
+  o.bias_mode = d->c_kind == OHIP_C_SCALAR ? BIAS_SCALAR
+              : d->c_kind == OHIP_C_ROW    ? BIAS_I
+              : d->c_kind == OHIP_C_FULL   ? BIAS_FULL_JI
+                                           : BIAS_NONE;
+  o.act = d->act; o.lo = d->act_lo; o.hi = d->act_hi;
+  if (o.act == ACT_CLIP) {
+    if (std::isnan(o.lo)) o.lo = -INFINITY;
+    if (std::isnan(o.hi)) o.hi = INFINITY;
+    if (!(o.lo <= o.hi)) o.act = ACT_NONE;
+  }
+
+  hipError_t e;
+  if (gemv) {
+    GemvArgs g{av.p, av.ld_bytes / eb, b->data, b->ld_bytes / eb, (int)M, (int)N, b->kc, splits, cps,
+               static_cast<float*>(scratch_at(ctx, plan, ip))};
+    e = run_gemv(d->dtype, g, o, ctx->stream);
+  } else {
+    DenseOperand x{b->data, b->ld_bytes, (int)N, b->kc, 0u, 0u};
+    DenseOperand yv{av.p, av.ld_bytes, (int)M, av.kc, 0u, 0u};
+    e = run_dense_float(d->dtype, x, yv, o, ctx->tile_override, ctx->stream);
+  }
+  if (e != hipSuccess) return hip_fail(e, "ohip_gemm launch");
+  return OHIP_OK;
+}
+
+// ------------------------------------------------------------------ float Conv
+struct ConvGeo {
+  int64_t oh, ow;
+};
+
+static int conv_geo(int64_t h, int64_t w, int64_t kh, int64_t kw, int64_t sh, int64_t sw, int64_t dh, int64_t dw,
+                    int64_t pt, int64_t pl, int64_t pb, int64_t pr, ConvGeo* g) {
+  g->oh = ohip_conv_out_dim(h, pt, pb, kh, dh, sh);
+  g->ow = ohip_conv_out_dim(w, pl, pr, kw, dw, sw);
+  if (g->oh < 0 || g->ow < 0) return fail(OHIP_E_SHAPE, "conv: padded input smaller than the dilated kernel");
+  return OHIP_OK;
+}
+
+extern "C" int ohip_conv2d(ohip_ctx* ctx, const ohip_conv_desc* d, const void* x, const ohip_weight* w,
+                           const void* bias, void* y) {
+  int rc = activate(ctx);
+  if (rc) return rc;
+  if (!d || !x || !w || !y) return fail(OHIP_E_INVALID, "ohip_conv2d: null argument");
+  if (d->group != 1) return fail(OHIP_DECLINED, "ohip_conv2d: group != 1 is not handled");
+  if (!is_float(d->dtype) || w->kind != WK_CONV || w->dtype != d->dtype)
+    return fail(OHIP_E_INVALID, "ohip_conv2d: weight kind / dtype mismatch");
+  if (w->rows != d->cout || w->k != d->c || w->kh != d->kh || w->kw != d->kw)
+    return fail(OHIP_E_SHAPE, "ohip_conv2d: shape disagrees with the packed filter");
+  ConvGeo g;
+  rc = conv_geo(d->h, d->w, d->kh, d->kw, d->stride_h, d->stride_w, d->dil_h, d->dil_w, d->pad_t, d->pad_l,
+                d->pad_b, d->pad_r, &g);
+  if (rc) return rc;
+  const int eb = elem_bytes(d->dtype), ce = 16 / eb;
+  const int64_t cp = round_up(d->c, ce);
+  const int64_t rows = d->n * g.oh * g.ow;
+  if (rows > INT_MAX / 2 || d->n * d->h * d->w * cp > (int64_t)INT_MAX * 4)
+    return fail(OHIP_DECLINED, "ohip_conv2d: extent too large");
+  if (rows == 0) return OHIP_OK;
+  std::lock_guard<std::mutex> lock(ctx->mu);
+  ctx->counters.dispatches++;
+
+  ScratchPlan plan;
+  const bool stage = d->in_layout == OHIP_NCHW;
+  size_t ix = stage ? plan.add((size_t)(d->n * d->h * d->w * cp) * eb) : SIZE_MAX;
+  rc = scratch_reserve(ctx, plan.total());
+  if (rc) return rc;
+  const void* xin = x;
+  if (stage) {
+    void* px = scratch_at(ctx, plan, ix);
+    HIP_TRY(run_nchw_to_nhwc(eb, x, px, (int)d->n, (int)d->c, (int)(d->h * d->w), (int)cp, ctx->stream),
+            "NCHW -> NHWC");
+    xin = px;
+  } else if (!aligned(x, 16)) {
+    return fail(OHIP_E_INVALID, "ohip_conv2d: NHWC input must be 16-byte aligned");
+  }
+
+  Im2colOperand col{};
+  col.base = xin; col.H = (int)d->h; col.W = (int)d->w; col.OH = (int)g.oh; col.OW = (int)g.ow;
+  col.KW = (int)d->kw; col.cpc = (int)(cp / ce);
+  col.sh = (int)d->stride_h; col.sw = (int)d->stride_w; col.dh = (int)d->dil_h; col.dw = (int)d->dil_w;
+  col.pt = (int)d->pad_t; col.pl = (int)d->pad_l; col.rows = (int)rows; col.kc = w->kc;
+  col.xor_mask = 0; col.pad = 0;
+  DenseOperand wt{w->data, w->ld_bytes, (int)d->cout, w->kc, 0u, 0u};
+
+  FloatOut o{};
+  o.y = y; o.alpha = 1.0f; o.beta = 1.0f; o.bias = bias;
+  o.act = d->act; o.lo = d->act_lo; o.hi = d->act_hi;
+  if (o.act == ACT_CLIP) {
+    if (std::isnan(o.lo)) o.lo = -INFINITY;
+    if (std::isnan(o.hi)) o.hi = INFINITY;
+    if (!(o.lo <= o.hi)) o.act = ACT_NONE;
+  }
+  const int64_t ohw = g.oh * g.ow;
+  bool col_on_x;
+  if (d->out_layout == OHIP_NCHW) {
+    col_on_x = true;
+    o.si = 1; o.sj = ohw; o.bstride = d->cout * ohw; o.ohw = (int)ohw; o.P = (int)rows; o.Q = (int)d->cout;
+    o.vec = ohw % 4 == 0 && aligned(y, 4 * eb);
+    o.bias_mode = BIAS_J;
+  } else {
+    col_on_x = false;
+    const int64_t ldo = round_up(d->cout, ce);
+    o.si = 1; o.sj = ldo; o.bstride = 0; o.ohw = INT_MAX; o.P = (int)d->cout; o.Q = (int)rows;
+    o.vec = ldo % 4 == 0 && aligned(y, 4 * eb);
+    o.bias_mode = BIAS_I;
+  }
+  hipError_t e = run_conv_float(d->dtype, col, wt, col_on_x, o, ctx->tile_override, ctx->stream);
+  if (e != hipSuccess) return hip_fail(e, "ohip_conv2d launch");
+  return OHIP_OK;
+}
+
+// ------------------------------------------------------------------ integer GEMM
+// |sum (a - a_zp)(w - w_zp)| <= K * 255 * 128 once w - w_zp fits int8; below
+// this K the int32 accumulator can never overflow.
+static const int64_t kMaxExactK = ((int64_t)INT32_MAX) / (255 * 128);
+
+extern "C" int ohip_qgemm(ohip_ctx* ctx, const ohip_qgemm_desc* d, const void* a, const ohip_weight* b, void* y) {
+  int rc = activate(ctx);
+  if (rc) return rc;
+  if (!d || !a || !b || !y) return fail(OHIP_E_INVALID, "ohip_qgemm: null argument");
+  if (b->kind != WK_QGEMM) return fail(OHIP_E_INVALID, "ohip_qgemm: weight kind mismatch");
+  if (d->a_dtype != OHIP_U8 && d->a_dtype != OHIP_I8) return fail(OHIP_E_INVALID, "ohip_qgemm: A must be u8/i8");
+  if (d->k != b->k || d->n != b->rows || d->m < 0) return fail(OHIP_E_SHAPE, "ohip_qgemm: shape mismatch");
+  if (d->n_azp != 1 && d->n_azp != d->m) return fail(OHIP_E_SHAPE, "a_zero_point has the wrong length");
+  if (d->k > kMaxExactK) return fail(OHIP_DECLINED, "ohip_qgemm: K too large for an exact int32 accumulator");
+  if (d->m > INT_MAX / 2) return fail(OHIP_DECLINED, "ohip_qgemm: extent too large");
+  if (d->m == 0) return OHIP_OK;
+  std::lock_guard<std::mutex> lock(ctx->mu);
+  ctx->counters.dispatches++;
+  const int64_t M = d->m, N = d->n, K = d->k, kp = round_up(K, 16);
+  const int64_t lda = d->lda ? d->lda : K, ldy = d->ldy ? d->ldy : N;
+  const bool direct = rows_direct(a, K, lda, 1, 0);
+  const bool u8 = d->a_dtype == OHIP_U8;
+  const int32_t shift = u8 ? 128 : 0;
+  int n_comb = 1;
+  if (d->out_kind != OHIP_QOUT_I32) {
+    rc = ensure_comb(ctx, const_cast<ohip_weight*>(b), d->a_scale, d->y_scale, &n_comb);
+    if (rc) return rc;
+  }
+  ScratchPlan plan;
+  size_t ia = direct ? SIZE_MAX : plan.add((size_t)(M * kp));
+  size_t ir = d->n_azp > 1 ? plan.add((size_t)M * 4) : SIZE_MAX;
+  rc = scratch_reserve(ctx, plan.total());
+  if (rc) return rc;
+  const void* pa = a;
+  int64_t lda_b = lda;
+  if (!direct) {
+    void* s = scratch_at(ctx, plan, ia);
+    HIP_TRY(run_gather2d(1, a, lda, 1, s, (int)M, (int)K, (int)kp, ctx->stream), "pack A");
+    pa = s;
+    lda_b = kp;
+  }
+  int32_t* ca_rows = nullptr;
+  if (d->n_azp > 1) {
+    std::vector<int32_t> rows((size_t)M);
+    for (int64_t i = 0; i < M; ++i) rows[(size_t)i] = shift - d->a_zp[i];
+    ca_rows = static_cast<int32_t*>(scratch_at(ctx, plan, ir));
+    HIP_TRY(hipMemcpyAsync(ca_rows, rows.data(), rows.size() * 4, hipMemcpyHostToDevice, ctx->stream), "a_zp upload");
+    HIP_TRY(hipStreamSynchronize(ctx->stream), "a_zp upload sync");
+  }
+  QuantOut o{};
+  o.y = y; o.si = 1; o.sj = ldy; o.bstride = 0; o.ohw = INT_MAX; o.P = (int)N; o.Q = (int)M;
+  const int ob = d->out_kind == OHIP_QOUT_I32 ? 4 : 1;
+  o.vec = ldy % 4 == 0 && aligned(y, 4 * ob);
+  o.w_on_i = 1; o.colsum = b->colsum; o.bias = nullptr;
+  o.ca = shift - (d->a_zp ? d->a_zp[0] : 0); o.ca_rows = ca_rows;
+  o.comb = b->comb; o.n_comb = n_comb; o.out_kind = d->out_kind; o.y_zp = d->y_zp; o.lo = d->lo; o.hi = d->hi;
+  DenseOperand x{b->data, b->ld_bytes, (int)N, b->kc, 0u, 0u};
+  DenseOperand yv{pa, lda_b, (int)M, (int)(kp / 16), u8 ? 0x80808080u : 0u, 0u};
+  hipError_t e = run_dense_quant(x, yv, o, ctx->tile_override, ctx->stream);
+  if (e != hipSuccess) return hip_fail(e, "ohip_qgemm launch");
+  return OHIP_OK;
+}
+
+extern "C" int ohip_qconv2d(ohip_ctx* ctx, const ohip_qconv_desc* d, const void* x, const ohip_weight* w,
+                            const int32_t* bias, void* y) {
+  int rc = activate(ctx);
+  if (rc) return rc;
+  if (!d || !x || !w || !y) return fail(OHIP_E_INVALID, "ohip_qconv2d: null argument");
+  if (d->group != 1) return fail(OHIP_DECLINED, "ohip_qconv2d: group != 1 is not handled");
+  if (w->kind != WK_QCONV) return fail(OHIP_E_INVALID, "ohip_qconv2d: weight kind mismatch");
+  if (d->x_dtype != OHIP_U8 && d->x_dtype != OHIP_I8) return fail(OHIP_E_INVALID, "ohip_qconv2d: X must be u8/i8");
+  if (w->rows != d->cout || w->k != d->c || w->kh != d->kh || w->kw != d->kw)
+    return fail(OHIP_E_SHAPE, "ohip_qconv2d: shape disagrees with the packed filter");
+  if (d->c * d->kh * d->kw > kMaxExactK) return fail(OHIP_DECLINED, "ohip_qconv2d: K too large for exact int32");
+  ConvGeo g;
+  rc = conv_geo(d->h, d->w, d->kh, d->kw, d->stride_h, d->stride_w, d->dil_h, d->dil_w, d->pad_t, d->pad_l,
+                d->pad_b, d->pad_r, &g);
+  if (rc) return rc;
+  const int64_t cp = round_up(d->c, 16);
+  const int64_t rows = d->n * g.oh * g.ow;
+  if (rows > INT_MAX / 2) return fail(OHIP_DECLINED, "ohip_qconv2d: extent too large");
+  if (rows == 0) return OHIP_OK;
+  std::lock_guard<std::mutex> lock(ctx->mu);
+  ctx->counters.dispatches++;
+  const bool u8 = d->x_dtype == OHIP_U8;
+  const int32_t shift = u8 ? 128 : 0;
+  int n_comb = 1;
+  if (d->out_kind != OHIP_QOUT_I32) {
+    rc = ensure_comb(ctx, const_cast<ohip_weight*>(w), d->x_scale, d->y_scale, &n_comb);
+    if (rc) return rc;
+  }
+  ScratchPlan plan;
+  const bool stage = d->in_layout == OHIP_NCHW;
+  size_t ix = stage ? plan.add((size_t)(d->n * d->h * d->w * cp)) : SIZE_MAX;
+  rc = scratch_reserve(ctx, plan.total());
+  if (rc) return rc;
+  const void* xin = x;
+  if (stage) {
+    void* px = scratch_at(ctx, plan, ix);
+    HIP_TRY(run_nchw_to_nhwc(1, x, px, (int)d->n, (int)d->c, (int)(d->h * d->w), (int)cp, ctx->stream),
+            "NCHW -> NHWC");
+    xin = px;
+  } else if (!aligned(x, 16)) {
+    return fail(OHIP_E_INVALID, "ohip_qconv2d: NHWC input must be 16-byte aligned");
+  }
+  // A padding tap stands for x == x_zp, i.e. (x_zp - shift) in the shifted
+  // int8 domain, so it contributes exactly zero after the ca correction.
+  const uint8_t padb = (uint8_t)(int8_t)(d->x_zp - shift);
+  Im2colOperand col{};
+  col.base = xin; col.H = (int)d->h; col.W = (int)d->w; col.OH = (int)g.oh; col.OW = (int)g.ow;
+  col.KW = (int)d->kw; col.cpc = (int)(cp / 16);
+  col.sh = (int)d->stride_h; col.sw = (int)d->stride_w; col.dh = (int)d->dil_h; col.dw = (int)d->dil_w;
+  col.pt = (int)d->pad_t; col.pl = (int)d->pad_l; col.rows = (int)rows; col.kc = w->kc;
+  col.xor_mask = u8 ? 0x80808080u : 0u;
+  col.pad = padb * 0x01010101u;
+  DenseOperand wt{w->data, w->ld_bytes, (int)d->cout, w->kc, 0u, 0u};
+  QuantOut o{};
+  o.y = y; o.colsum = w->colsum; o.bias = bias; o.ca = shift - d->x_zp; o.ca_rows = nullptr;
+  o.comb = w->comb; o.n_comb = n_comb; o.out_kind = d->out_kind; o.y_zp = d->y_zp; o.lo = d->lo; o.hi = d->hi;
+  const int ob = d->out_kind == OHIP_QOUT_I32 ? 4 : 1;
+  const int64_t ohw = g.oh * g.ow;
+  bool col_on_x;
+  if (d->out_layout == OHIP_NCHW) {
+    col_on_x = true;
+    o.si = 1; o.sj = ohw; o.bstride = d->cout * ohw; o.ohw = (int)ohw; o.P = (int)rows; o.Q = (int)d->cout;
+    o.vec = ohw % 4 == 0 && aligned(y, 4 * ob);
+    o.w_on_i = 0;
+  } else {
+    col_on_x = false;
+    const int64_t ldo = ob == 1 ? round_up(d->cout, 16) : round_up(d->cout, 4);
+    o.si = 1; o.sj = ldo; o.bstride = 0; o.ohw = INT_MAX; o.P = (int)d->cout; o.Q = (int)rows;
+    o.vec = ldo % 4 == 0 && aligned(y, 4 * ob);
+    o.w_on_i = 1;
+  }
+  hipError_t e = run_conv_quant(col, wt, col_on_x, o, ctx->tile_override, ctx->stream);
+  if (e != hipSuccess) return hip_fail(e, "ohip_qconv2d launch");
+  return OHIP_OK;
+}
+
+// ------------------------------------------------------------------ counters
+extern "C" int ohip_get_counters(ohip_ctx* ctx, ohip_counters* out) {
+  if (!ctx || !out) return fail(OHIP_E_INVALID, "null argument");
+  *out = ctx->counters;
+  return OHIP_OK;
+}
+extern "C" int ohip_reset_counters(ohip_ctx* ctx) {
+  if (!ctx) return fail(OHIP_E_INVALID, "null context");
+  uint64_t resident = ctx->counters.weight_resident_bytes;
+  ctx->counters = ohip_counters{};
+  ctx->counters.weight_resident_bytes = resident;
+  return OHIP_OK;
+}
