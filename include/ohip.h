@@ -47,8 +47,12 @@ enum ohip_bias_kind { OHIP_C_NONE = 0, OHIP_C_SCALAR = 1, OHIP_C_ROW = 2, OHIP_C
 
 enum ohip_layout { OHIP_NCHW = 0, OHIP_NHWC = 1 };
 
-/* Output kinds of the integer family. */
-enum ohip_qout { OHIP_QOUT_U8 = 0, OHIP_QOUT_I8 = 1, OHIP_QOUT_I32 = 2 };
+/* Output kinds of the integer family: requantised u8 / i8 bytes, the raw int32
+ * accumulator (MatMulInteger / ConvInteger), or requantised values stored as
+ * f32 lanes -- the reference Tensor's own representation, which also carries
+ * the union saturation range [-128, 255] that no 8-bit type holds
+ * (quant_ops/mod.rs:188-200). */
+enum ohip_qout { OHIP_QOUT_U8 = 0, OHIP_QOUT_I8 = 1, OHIP_QOUT_I32 = 2, OHIP_QOUT_F32 = 3 };
 
 /* Performance classes for the dispatch gate (oxionnx-gpu/src/context/tuning.rs:271-611). */
 enum ohip_perf_class { OHIP_CLASS_MI355X = 0, OHIP_CLASS_PARITY = 1, OHIP_CLASS_NEVER = 2, OHIP_CLASS_LEGACY = 3 };
@@ -71,7 +75,7 @@ int ohip_device_count(int* count);
 const char* ohip_last_error(void);
 const char* ohip_version(void);
 /* Env truthiness used by OXIONNX_HIP / OXIONNX_HIP_VERIFY / OXIONNX_HIP_STRICT /
- * OXIONNX_HIP_RESIDENCY (same rule as oxionnx-cuda/src/context.rs:179-200). */
+ * OXIONNX_HIP_RESIDENCY (same rule as oxionnx-cuda/src/context.rs:165-193). */
 int ohip_env_flag(const char* name);
 
 /* ------------------------------------------------------------------ memory */

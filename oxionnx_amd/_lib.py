@@ -16,7 +16,7 @@ F32, U8, I8, I32, F16, BF16 = 1, 2, 3, 6, 10, 16
 ACT_NONE, ACT_RELU, ACT_CLIP, ACT_LEAKY_RELU = 0, 1, 2, 3
 C_NONE, C_SCALAR, C_ROW, C_FULL = 0, 1, 2, 3
 NCHW, NHWC = 0, 1
-QOUT_U8, QOUT_I8, QOUT_I32 = 0, 1, 2
+QOUT_U8, QOUT_I8, QOUT_I32, QOUT_F32 = 0, 1, 2, 3
 CLASS_MI355X, CLASS_PARITY, CLASS_NEVER, CLASS_LEGACY = 0, 1, 2, 3
 
 ELEM_BYTES = {F32: 4, U8: 1, I8: 1, I32: 4, F16: 2, BF16: 2}

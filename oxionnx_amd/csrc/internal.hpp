@@ -11,7 +11,7 @@ namespace ohip {
 enum { DT_F32 = 1, DT_U8 = 2, DT_I8 = 3, DT_I32 = 6, DT_F16 = 10, DT_BF16 = 16 };
 enum { ACT_NONE = 0, ACT_RELU = 1, ACT_CLIP = 2, ACT_LEAKY_RELU = 3 };
 enum { BIAS_NONE = 0, BIAS_SCALAR = 1, BIAS_I = 2, BIAS_J = 3, BIAS_FULL_JI = 4 };
-enum { QOUT_U8 = 0, QOUT_I8 = 1, QOUT_I32 = 2 };
+enum { QOUT_U8 = 0, QOUT_I8 = 1, QOUT_I32 = 2, QOUT_F32 = 3 };
 
 // Rows of K-contiguous 16-byte chunks.
 struct DenseOperand {
@@ -19,6 +19,7 @@ struct DenseOperand {
   int64_t ld_bytes;
   int rows;
   int kc;             // 16-byte chunks per row that hold data
+  int kwrap;          // > 0: loop chunk g >= kwrap reads chunk g - kwrap
   uint32_t xor_mask;  // 0x80808080 turns u8 into (u8 - 128) as int8
   uint32_t pad;       // replicated into every dword of an out-of-range chunk
 };
@@ -29,7 +30,7 @@ struct Im2colOperand {
   const void* base;
   int H, W, OH, OW, KW, cpc;
   int sh, sw, dh, dw, pt, pl;
-  int rows, kc;
+  int rows, kc, kwrap;
   uint32_t xor_mask, pad;
 };
 
@@ -53,6 +54,7 @@ struct FloatOut : OutMap {
 struct QuantOut : OutMap {
   int w_on_i;
   const int32_t* colsum;
+  const int8_t* flip;
   const int32_t* bias;
   int32_t ca;
   const int32_t* ca_rows;

@@ -93,12 +93,13 @@ struct QuantEpi {
   int vec;
   int w_on_i;               // weight channel index is i (else j)
   const int32_t* colsum;    // per weight channel
+  const int8_t* flip;       // per weight channel: 1 = the packed channel holds -(w - w_zp)
   const int32_t* bias;      // per weight channel, may be null
   int32_t ca;               // per-tensor correction factor
   const int32_t* ca_rows;   // per activation row, may be null
   const float* comb;        // combined scale per channel (n_comb == 1 -> per tensor)
   int n_comb;
-  int out_kind;             // QOUT_U8, QOUT_I8, QOUT_I32
+  int out_kind;             // QOUT_U8, QOUT_I8, QOUT_I32 (raw), QOUT_F32 (requantised, as f32)
   int32_t y_zp, lo, hi;
 
   __device__ __forceinline__ int64_t index(int i, int j) const {
@@ -110,6 +111,7 @@ struct QuantEpi {
     const int row = w_on_i ? j : i;
     const uint32_t c = (uint32_t)(ca_rows ? ca_rows[row] : ca);
     uint32_t v = (uint32_t)acc + c * (uint32_t)colsum[ch];
+    if (flip && flip[ch]) v = 0u - v;
     if (bias) v += (uint32_t)bias[ch];
     return (int32_t)v;
   }
@@ -132,7 +134,17 @@ struct QuantEpi {
       v[r] = exact(acc[r], i0 + r, j);
       if (out_kind != QOUT_I32) v[r] = requant(v[r], i0 + r, j);
     }
-    if (out_kind == QOUT_I32) {
+    if (out_kind == QOUT_F32) {
+      // requantised lanes stored as f32, the reference Tensor's representation
+      float* yy = reinterpret_cast<float*>(y);
+      if (vec && i0 + 3 < P) {
+        *reinterpret_cast<f32x4*>(yy + index(i0, j)) = f32x4{(float)v[0], (float)v[1], (float)v[2], (float)v[3]};
+      } else {
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          if (i0 + r < P) yy[index(i0 + r, j)] = (float)v[r];
+      }
+    } else if (out_kind == QOUT_I32) {
       int32_t* yy = reinterpret_cast<int32_t*>(y);
       if (vec && i0 + 3 < P) {
         *reinterpret_cast<i32x4*>(yy + index(i0, j)) = i32x4{v[0], v[1], v[2], v[3]};
@@ -205,7 +217,7 @@ static FloatEpi<OutT> make_float_epi(const FloatOut& o) {
 static QuantEpi make_quant_epi(const QuantOut& o) {
   QuantEpi e;
   e.y = o.y; e.si = o.si; e.sj = o.sj; e.bstride = o.bstride; e.ohw = o.ohw; e.P = o.P; e.Q = o.Q;
-  e.vec = o.vec; e.w_on_i = o.w_on_i; e.colsum = o.colsum; e.bias = o.bias; e.ca = o.ca;
+  e.vec = o.vec; e.w_on_i = o.w_on_i; e.colsum = o.colsum; e.flip = o.flip; e.bias = o.bias; e.ca = o.ca;
   e.ca_rows = o.ca_rows; e.comb = o.comb; e.n_comb = o.n_comb; e.out_kind = o.out_kind;
   e.y_zp = o.y_zp; e.lo = o.lo; e.hi = o.hi;
   return e;
@@ -214,7 +226,7 @@ static QuantEpi make_quant_epi(const QuantOut& o) {
 static DenseRows make_dense(const DenseOperand& d) {
   DenseRows r;
   r.base = reinterpret_cast<const char*>(d.base);
-  r.ld = d.ld_bytes; r.rows = d.rows; r.kc = d.kc; r.xor_mask = d.xor_mask;
+  r.ld = d.ld_bytes; r.rows = d.rows; r.kc = d.kc; r.kwrap = d.kwrap; r.xor_mask = d.xor_mask;
   r.pad = u32x4{d.pad, d.pad, d.pad, d.pad};
   return r;
 }
@@ -224,7 +236,7 @@ static Im2colNHWC make_im2col(const Im2colOperand& c) {
   r.base = reinterpret_cast<const char*>(c.base);
   r.H = c.H; r.W = c.W; r.OH = c.OH; r.OW = c.OW; r.KW = c.KW; r.cpc = c.cpc;
   r.sh = c.sh; r.sw = c.sw; r.dh = c.dh; r.dw = c.dw; r.pt = c.pt; r.pl = c.pl;
-  r.rows = c.rows; r.kc = c.kc; r.xor_mask = c.xor_mask;
+  r.rows = c.rows; r.kc = c.kc; r.kwrap = c.kwrap; r.xor_mask = c.xor_mask;
   r.pad = u32x4{c.pad, c.pad, c.pad, c.pad};
   return r;
 }
@@ -259,12 +271,14 @@ hipError_t run_conv_float(int dtype, const Im2colOperand& col, const DenseOperan
 hipError_t run_dense_quant(const DenseOperand& x, const DenseOperand& y, const QuantOut& o, int tile, hipStream_t st) {
   return launch_any<Op::I8>(make_dense(x), make_dense(y), make_quant_epi(o), o.P, o.Q, x.kc, tile, st);
 }
+// (x is always the packed weight for the integer GEMM, so x.kc is the full
+// loop length, including the second half of a split weight.)
 
 hipError_t run_conv_quant(const Im2colOperand& col, const DenseOperand& w, bool col_on_x, const QuantOut& o,
                           int tile, hipStream_t st) {
   if (col_on_x)
-    return launch_any<Op::I8>(make_im2col(col), make_dense(w), make_quant_epi(o), o.P, o.Q, col.kc, tile, st);
-  return launch_any<Op::I8>(make_dense(w), make_im2col(col), make_quant_epi(o), o.P, o.Q, col.kc, tile, st);
+    return launch_any<Op::I8>(make_im2col(col), make_dense(w), make_quant_epi(o), o.P, o.Q, w.kc, tile, st);
+  return launch_any<Op::I8>(make_dense(w), make_im2col(col), make_quant_epi(o), o.P, o.Q, w.kc, tile, st);
 }
 
 // ---------------------------------------------------------------- skinny GEMV
@@ -275,8 +289,7 @@ hipError_t run_conv_quant(const Im2colOperand& col, const DenseOperand& w, bool 
 template <class T> struct Vec16;
 template <> struct Vec16<float> {
   static __device__ __forceinline__ void unpack(u32x4 v, float (&f)[4]) {
-    f[0] = __builtin_bit_cast(float, v.x); f[1] = __builtin_bit_cast(float, v.y);
-    f[2] = __builtin_bit_cast(float, v.z); f[3] = __builtin_bit_cast(float, v.w);
+    f[0] = lane_f32(v.x); f[1] = lane_f32(v.y); f[2] = lane_f32(v.z); f[3] = lane_f32(v.w);
   }
   static constexpr int N = 4;
 };

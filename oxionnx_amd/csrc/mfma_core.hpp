@@ -31,6 +31,11 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
 enum class Op { F32, F16, BF16, I8 };
 
+// Bit-cast one 32-bit lane to float.  Taking the lane by value matters:
+// __builtin_bit_cast applied directly to a vector-element expression (v.y)
+// reads from the start of the vector on this compiler.
+__device__ __forceinline__ float lane_f32(uint32_t u) { return __builtin_bit_cast(float, u); }
+
 template <Op O> struct OpT;
 template <> struct OpT<Op::F16> {
   using Acc = f32x4;
@@ -60,14 +65,10 @@ template <> struct OpT<Op::F32> {
   using Acc = f32x4;
   static constexpr int kElemBytes = 4;
   static __device__ __forceinline__ Acc mma(u32x4 a, u32x4 b, Acc c) {
-    c = __builtin_amdgcn_mfma_f32_16x16x4f32(__builtin_bit_cast(float, a.x),
-                                             __builtin_bit_cast(float, b.x), c, 0, 0, 0);
-    c = __builtin_amdgcn_mfma_f32_16x16x4f32(__builtin_bit_cast(float, a.y),
-                                             __builtin_bit_cast(float, b.y), c, 0, 0, 0);
-    c = __builtin_amdgcn_mfma_f32_16x16x4f32(__builtin_bit_cast(float, a.z),
-                                             __builtin_bit_cast(float, b.z), c, 0, 0, 0);
-    c = __builtin_amdgcn_mfma_f32_16x16x4f32(__builtin_bit_cast(float, a.w),
-                                             __builtin_bit_cast(float, b.w), c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f32_16x16x4f32(lane_f32(a.x), lane_f32(b.x), c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f32_16x16x4f32(lane_f32(a.y), lane_f32(b.y), c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f32_16x16x4f32(lane_f32(a.z), lane_f32(b.z), c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f32_16x16x4f32(lane_f32(a.w), lane_f32(b.w), c, 0, 0, 0);
     return c;
   }
 };
@@ -95,6 +96,8 @@ struct DenseRows {
   int64_t ld;         // bytes between rows (multiple of 16)
   int rows;           // valid rows
   int kc;             // valid 16-byte chunks per row
+  int kwrap;          // > 0: chunk g >= kwrap reads chunk g - kwrap (the operand is
+                      // re-read against the second half of a split int8 weight)
   uint32_t xor_mask;  // applied to every loaded dword (u8 -> int8 shift uses 0x80808080)
   u32x4 pad;          // value used outside the matrix
 
@@ -112,7 +115,8 @@ struct DenseRows {
   }
   template <int NR, int kThreads>
   __device__ __forceinline__ void load(const State<NR, kThreads>& s, int kt, int t, u32x4 (&v)[NR]) const {
-    const int gk = kt * 8 + (t & 7);
+    int gk = kt * 8 + (t & 7);
+    if (kwrap > 0 && gk >= kwrap) gk -= kwrap;
     const bool kin = gk < kc;
 #pragma unroll
     for (int i = 0; i < NR; ++i) {
@@ -137,6 +141,7 @@ struct Im2colNHWC {
   int sh, sw, dh, dw, pt, pl;
   int rows;            // N * OH * OW
   int kc;              // KH * KW * cpc
+  int kwrap;           // as DenseRows::kwrap
   uint32_t xor_mask;
   u32x4 pad;           // value of a padding tap (already in the shifted domain)
 
@@ -160,7 +165,8 @@ struct Im2colNHWC {
   }
   template <int NR, int kThreads>
   __device__ __forceinline__ void load(const State<NR, kThreads>& s, int kt, int t, u32x4 (&v)[NR]) const {
-    const int gk = kt * 8 + (t & 7);
+    int gk = kt * 8 + (t & 7);
+    if (kwrap > 0 && gk >= kwrap) gk -= kwrap;
     const bool kin = gk < kc;
     const int tap = gk / cpc;
     const int cc = gk - tap * cpc;

@@ -67,6 +67,8 @@ struct ohip_weight {
   int64_t ld_bytes = 0;
   void* data = nullptr;
   int32_t* colsum = nullptr;      // integer only
+  int8_t* flip = nullptr;         // integer only, null when no channel is negated
+  int kwrap = 0;                  // integer only: > 0 when each row holds two int8 halves
   std::vector<float> scale;       // integer only (1 or rows entries)
   float* comb = nullptr;          // device, rows entries (integer only)
   float comb_a = NAN, comb_y = NAN;
@@ -82,6 +84,7 @@ struct ohip_ctx {
   void* scratch = nullptr;
   size_t scratch_bytes = 0;
   std::map<std::string, ohip_weight*> weights;
+  std::vector<ohip_weight*> transients;  // freed with the context if never released
   ohip_counters counters{};
   std::mutex mu;
 };
@@ -150,7 +153,7 @@ extern "C" int ohip_ctx_create(int device, ohip_ctx** out) {
   auto* ctx = new (std::nothrow) ohip_ctx();
   if (!ctx) return fail(OHIP_E_NOMEM, "context allocation");
   ctx->device = device;
-  hipError_t e = hipStreamCreateWithFlags(&ctx->own, hipStreamNonBlocking);
+  hipError_t e = hipStreamCreateWithFlags(&ctx->own, hipStreamDefault);
   if (e != hipSuccess) {
     delete ctx;
     return hip_fail(e, "hipStreamCreate");
@@ -165,6 +168,7 @@ static void weight_free(ohip_weight* w) {
   if (!w) return;
   if (w->data) (void)hipFree(w->data);
   if (w->colsum) (void)hipFree(w->colsum);
+  if (w->flip) (void)hipFree(w->flip);
   if (w->comb) (void)hipFree(w->comb);
   delete w;
 }
@@ -174,6 +178,7 @@ extern "C" void ohip_ctx_destroy(ohip_ctx* ctx) {
   (void)hipSetDevice(ctx->device);
   (void)hipStreamSynchronize(ctx->stream);
   for (auto& kv : ctx->weights) weight_free(kv.second);
+  for (auto* w : ctx->transients) weight_free(w);
   if (ctx->scratch) (void)hipFree(ctx->scratch);
   if (ctx->own) (void)hipStreamDestroy(ctx->own);
   delete ctx;
@@ -444,6 +449,7 @@ static int weight_finish(ohip_ctx* ctx, const ohip_weight_key* key, const std::s
     ctx->counters.weight_resident_bytes += w->bytes;
   } else {
     ctx->counters.weight_transient++;
+    ctx->transients.push_back(w);
   }
   *out = w;
   return OHIP_OK;
@@ -451,8 +457,13 @@ static int weight_finish(ohip_ctx* ctx, const ohip_weight_key* key, const std::s
 
 extern "C" void ohip_weight_release(ohip_weight* w) {
   if (!w || w->cached) return;
-  (void)hipSetDevice(w->ctx->device);
-  (void)hipStreamSynchronize(w->ctx->stream);
+  ohip_ctx* ctx = w->ctx;
+  std::lock_guard<std::mutex> lock(ctx->mu);
+  auto it = std::find(ctx->transients.begin(), ctx->transients.end(), w);
+  if (it == ctx->transients.end()) return;
+  ctx->transients.erase(it);
+  (void)hipSetDevice(ctx->device);
+  (void)hipStreamSynchronize(ctx->stream);
   weight_free(w);
 }
 extern "C" size_t ohip_weight_bytes(const ohip_weight* w) { return w ? w->bytes : 0; }
@@ -515,20 +526,85 @@ extern "C" int ohip_weight_conv(ohip_ctx* ctx, const ohip_weight_key* key, int s
   return weight_finish(ctx, key, ks, w, out);
 }
 
-// Integer packing: B'' = w - w_zp[channel] as int8 (declines when a value
-// leaves [-128, 127]), rows K-contiguous, plus the per-channel sum of B''
-// that the epilogue's zero-point correction needs.
-static int qpack_common(ohip_ctx* ctx, ohip_weight* w, std::vector<int8_t>& packed, const std::vector<int32_t>& colsum,
-                        const float* scale, int n_scale) {
-  int rc = weight_upload(ctx, w, packed.data(), packed.size());
+// Integer packing.  Each weight channel becomes v = w - w_zp[channel] in
+// K-contiguous int8 rows, plus sum(v) for the epilogue's zero-point
+// correction.  v spans at most 255 consecutive values inside [-255, 255]:
+//   * a channel whose maximum exceeds 254 is stored negated (its range then
+//     lies in [-255, 0]) and flagged, and the epilogue negates it back;
+//   * when any stored value leaves [-128, 127], every row holds two int8
+//     halves v1 = clamp(v, -128, 127) and v2 = v - v1 (both in range), laid
+//     out as [v1 row | v2 row]; the activation is re-read for the second half
+//     (kwrap), which doubles K but keeps the int8 MFMA path exact.
+struct QPacked {
+  std::vector<int8_t> data;
+  std::vector<int32_t> colsum;
+  std::vector<int8_t> flip;
+  bool any_flip = false;
+  int64_t kp = 0;
+  bool split = false;
+};
+
+template <class ValueAt>
+static void qpack_rows(int64_t rows, int64_t kp, int64_t klen, ValueAt value_at, QPacked& q) {
+  // value_at(row, j) gives v for j < klen, where j indexes the packed K axis
+  // (positions the caller never fills are zero)
+  std::vector<int32_t> v((size_t)(rows * kp), 0);
+  q.colsum.assign((size_t)rows, 0);
+  q.flip.assign((size_t)rows, 0);
+  int32_t lo = 0, hi = 0;
+  for (int64_t r = 0; r < rows; ++r) {
+    int32_t mx = INT32_MIN;
+    for (int64_t j = 0; j < klen; ++j) {
+      int32_t x;
+      if (!value_at(r, j, &x)) continue;
+      v[(size_t)(r * kp + j)] = x;
+      mx = std::max(mx, x);
+    }
+    const bool flip = mx > 254;
+    int32_t s = 0;
+    for (int64_t j = 0; j < kp; ++j) {
+      int32_t& x = v[(size_t)(r * kp + j)];
+      if (flip) x = -x;
+      s += x;
+      lo = std::min(lo, x);
+      hi = std::max(hi, x);
+    }
+    q.colsum[(size_t)r] = s;
+    q.flip[(size_t)r] = flip ? 1 : 0;
+    q.any_flip |= flip;
+  }
+  q.kp = kp;
+  q.split = lo < -128 || hi > 127;
+  const int64_t width = q.split ? 2 * kp : kp;
+  q.data.assign((size_t)(rows * width), 0);
+  for (int64_t r = 0; r < rows; ++r)
+    for (int64_t j = 0; j < kp; ++j) {
+      const int32_t x = v[(size_t)(r * kp + j)];
+      const int32_t a = std::min(127, std::max(-128, x));
+      q.data[(size_t)(r * width + j)] = (int8_t)a;
+      if (q.split) q.data[(size_t)(r * width + kp + j)] = (int8_t)(x - a);
+    }
+}
+
+static int qpack_upload(ohip_ctx* ctx, ohip_weight* w, const QPacked& q, const float* scale, int n_scale) {
+  w->kwrap = q.split ? (int)(q.kp / 16) : 0;
+  w->kc = (int)((q.split ? 2 * q.kp : q.kp) / 16);
+  w->ld_bytes = q.split ? 2 * q.kp : q.kp;
+  int rc = weight_upload(ctx, w, q.data.data(), q.data.size());
   if (rc) return rc;
-  hipError_t e = hipMalloc(&w->colsum, colsum.size() * 4);
+  hipError_t e = hipMalloc(&w->colsum, q.colsum.size() * 4);
   if (e != hipSuccess) return fail(OHIP_E_NOMEM, "colsum hipMalloc");
-  HIP_TRY(hipMemcpy(w->colsum, colsum.data(), colsum.size() * 4, hipMemcpyHostToDevice), "colsum upload");
+  HIP_TRY(hipMemcpy(w->colsum, q.colsum.data(), q.colsum.size() * 4, hipMemcpyHostToDevice), "colsum upload");
+  if (q.any_flip) {
+    e = hipMalloc(&w->flip, q.flip.size());
+    if (e != hipSuccess) return fail(OHIP_E_NOMEM, "flip hipMalloc");
+    HIP_TRY(hipMemcpy(w->flip, q.flip.data(), q.flip.size(), hipMemcpyHostToDevice), "flip upload");
+    w->bytes += q.flip.size();
+  }
   e = hipMalloc(&w->comb, (size_t)w->rows * 4);
   if (e != hipSuccess) return fail(OHIP_E_NOMEM, "comb hipMalloc");
   if (scale && n_scale > 0) w->scale.assign(scale, scale + n_scale);
-  w->bytes += colsum.size() * 4 + (size_t)w->rows * 4;
+  w->bytes += q.colsum.size() * 4 + (size_t)w->rows * 4;
   return OHIP_OK;
 }
 
@@ -541,7 +617,8 @@ extern "C" int ohip_weight_qgemm(ohip_ctx* ctx, const ohip_weight_key* key, int 
                                  const float* scale, int n_scale, ohip_weight** out) {
   int rc = activate(ctx);
   if (rc) return rc;
-  if (!host || !out || (src_dt != OHIP_U8 && src_dt != OHIP_I8) || k <= 0 || n <= 0 || k > INT_MAX || n > INT_MAX)
+  if (!host || !out || (src_dt != OHIP_U8 && src_dt != OHIP_I8) || k <= 0 || n <= 0 || k > INT_MAX / 4 ||
+      n > INT_MAX)
     return fail(OHIP_E_INVALID, "ohip_weight_qgemm: bad arguments");
   if (zp && n_zp != 1 && n_zp != n) return fail(OHIP_E_SHAPE, "b_zero_point has the wrong length");
   if (scale && n_scale != 1 && n_scale != n) return fail(OHIP_E_SHAPE, "b_scale has the wrong length");
@@ -557,23 +634,15 @@ extern "C" int ohip_weight_qgemm(ohip_ctx* ctx, const ohip_weight_key* key, int 
       return OHIP_OK;
     }
   }
-  const int64_t kp = round_up(k, 16);
-  std::vector<int8_t> packed((size_t)(n * kp), 0);
-  std::vector<int32_t> colsum((size_t)n, 0);
-  for (int64_t j = 0; j < n; ++j) {
+  QPacked q;
+  qpack_rows(n, round_up(k, 16), k, [&](int64_t j, int64_t p, int32_t* v) {
     const int32_t z = zp ? (n_zp == 1 ? zp[0] : zp[j]) : 0;
-    int32_t s = 0;
-    for (int64_t p = 0; p < k; ++p) {
-      int32_t v = int_at(src_dt, host, trans_b ? j * k + p : p * n + j) - z;
-      if (v < -128 || v > 127) return fail(OHIP_DECLINED, "weight minus zero point leaves int8 range");
-      packed[(size_t)(j * kp + p)] = (int8_t)v;
-      s += v;
-    }
-    colsum[(size_t)j] = s;
-  }
+    *v = int_at(src_dt, host, trans_b ? j * k + p : p * n + j) - z;
+    return true;
+  }, q);
   auto* w = new ohip_weight();
-  w->kind = WK_QGEMM; w->dtype = OHIP_I8; w->rows = n; w->k = k; w->kc = (int)(kp / 16); w->ld_bytes = kp;
-  rc = qpack_common(ctx, w, packed, colsum, scale, n_scale);
+  w->kind = WK_QGEMM; w->dtype = OHIP_I8; w->rows = n; w->k = k;
+  rc = qpack_upload(ctx, w, q, scale, n_scale);
   if (rc) { weight_free(w); return rc; }
   return weight_finish(ctx, key, ks, w, out);
 }
@@ -600,25 +669,21 @@ extern "C" int ohip_weight_qconv(ohip_ctx* ctx, const ohip_weight_key* key, int 
     }
   }
   const int64_t cp = round_up(cin, 16), kp = kh * kw * cp;
-  std::vector<int8_t> packed((size_t)(cout * kp), 0);
-  std::vector<int32_t> colsum((size_t)cout, 0);
-  for (int64_t o = 0; o < cout; ++o) {
+  if (kp > INT_MAX / 4) return fail(OHIP_E_INVALID, "ohip_weight_qconv: filter too large");
+  // packed K axis is (ky, kx, channel padded to cp)
+  QPacked q;
+  qpack_rows(cout, kp, kp, [&](int64_t o, int64_t j, int32_t* v) {
+    const int64_t tap = j / cp, c = j - tap * cp;
+    if (c >= cin) return false;
+    const int64_t y = tap / kw, x = tap - y * kw;
     const int32_t z = zp ? (n_zp == 1 ? zp[0] : zp[o]) : 0;
-    int32_t s = 0;
-    for (int64_t c = 0; c < cin; ++c)
-      for (int64_t y = 0; y < kh; ++y)
-        for (int64_t x = 0; x < kw; ++x) {
-          int32_t v = int_at(src_dt, host, ((o * cin + c) * kh + y) * kw + x) - z;
-          if (v < -128 || v > 127) return fail(OHIP_DECLINED, "weight minus zero point leaves int8 range");
-          packed[(size_t)(o * kp + (y * kw + x) * cp + c)] = (int8_t)v;
-          s += v;
-        }
-    colsum[(size_t)o] = s;
-  }
+    *v = int_at(src_dt, host, ((o * cin + c) * kh + y) * kw + x) - z;
+    return true;
+  }, q);
   auto* w = new ohip_weight();
   w->kind = WK_QCONV; w->dtype = OHIP_I8; w->rows = cout; w->k = cin; w->kh = kh; w->kw = kw;
-  w->cpc = (int)(cp / 16); w->kc = (int)(kp / 16); w->ld_bytes = kp;
-  rc = qpack_common(ctx, w, packed, colsum, scale, n_scale);
+  w->cpc = (int)(cp / 16);
+  rc = qpack_upload(ctx, w, q, scale, n_scale);
   if (rc) { weight_free(w); return rc; }
   return weight_finish(ctx, key, ks, w, out);
 }
@@ -734,8 +799,8 @@ extern "C" int ohip_gemm(ohip_ctx* ctx, const ohip_gemm_desc* d, const void* a, 
                static_cast<float*>(scratch_at(ctx, plan, ip))};
     e = run_gemv(d->dtype, g, o, ctx->stream);
   } else {
-    DenseOperand x{b->data, b->ld_bytes, (int)N, b->kc, 0u, 0u};
-    DenseOperand yv{av.p, av.ld_bytes, (int)M, av.kc, 0u, 0u};
+    DenseOperand x{b->data, b->ld_bytes, (int)N, b->kc, 0, 0u, 0u};
+    DenseOperand yv{av.p, av.ld_bytes, (int)M, av.kc, 0, 0u, 0u};
     e = run_dense_float(d->dtype, x, yv, o, ctx->tile_override, ctx->stream);
   }
   if (e != hipSuccess) return hip_fail(e, "ohip_gemm launch");
@@ -799,7 +864,7 @@ extern "C" int ohip_conv2d(ohip_ctx* ctx, const ohip_conv_desc* d, const void* x
   col.sh = (int)d->stride_h; col.sw = (int)d->stride_w; col.dh = (int)d->dil_h; col.dw = (int)d->dil_w;
   col.pt = (int)d->pad_t; col.pl = (int)d->pad_l; col.rows = (int)rows; col.kc = w->kc;
   col.xor_mask = 0; col.pad = 0;
-  DenseOperand wt{w->data, w->ld_bytes, (int)d->cout, w->kc, 0u, 0u};
+  DenseOperand wt{w->data, w->ld_bytes, (int)d->cout, w->kc, 0, 0u, 0u};
 
   FloatOut o{};
   o.y = y; o.alpha = 1.0f; o.beta = 1.0f; o.bias = bias;
@@ -829,9 +894,9 @@ extern "C" int ohip_conv2d(ohip_ctx* ctx, const ohip_conv_desc* d, const void* x
 }
 
 // ------------------------------------------------------------------ integer GEMM
-// |sum (a - a_zp)(w - w_zp)| <= K * 255 * 128 once w - w_zp fits int8; below
-// this K the int32 accumulator can never overflow.
-static const int64_t kMaxExactK = ((int64_t)INT32_MAX) / (255 * 128);
+// |sum (a - a_zp)(w - w_zp)| <= K * 255 * 255; below this K neither the
+// int32 MFMA accumulator nor the epilogue can overflow.
+static const int64_t kMaxExactK = ((int64_t)INT32_MAX) / (255 * 255);
 
 extern "C" int ohip_qgemm(ohip_ctx* ctx, const ohip_qgemm_desc* d, const void* a, const ohip_weight* b, void* y) {
   int rc = activate(ctx);
@@ -879,13 +944,13 @@ extern "C" int ohip_qgemm(ohip_ctx* ctx, const ohip_qgemm_desc* d, const void* a
   }
   QuantOut o{};
   o.y = y; o.si = 1; o.sj = ldy; o.bstride = 0; o.ohw = INT_MAX; o.P = (int)N; o.Q = (int)M;
-  const int ob = d->out_kind == OHIP_QOUT_I32 ? 4 : 1;
+  const int ob = (d->out_kind == OHIP_QOUT_I32 || d->out_kind == OHIP_QOUT_F32) ? 4 : 1;
   o.vec = ldy % 4 == 0 && aligned(y, 4 * ob);
-  o.w_on_i = 1; o.colsum = b->colsum; o.bias = nullptr;
+  o.w_on_i = 1; o.colsum = b->colsum; o.flip = b->flip; o.bias = nullptr;
   o.ca = shift - (d->a_zp ? d->a_zp[0] : 0); o.ca_rows = ca_rows;
   o.comb = b->comb; o.n_comb = n_comb; o.out_kind = d->out_kind; o.y_zp = d->y_zp; o.lo = d->lo; o.hi = d->hi;
-  DenseOperand x{b->data, b->ld_bytes, (int)N, b->kc, 0u, 0u};
-  DenseOperand yv{pa, lda_b, (int)M, (int)(kp / 16), u8 ? 0x80808080u : 0u, 0u};
+  DenseOperand x{b->data, b->ld_bytes, (int)N, b->kc, 0, 0u, 0u};
+  DenseOperand yv{pa, lda_b, (int)M, (int)(kp / 16), b->kwrap, u8 ? 0x80808080u : 0u, 0u};
   hipError_t e = run_dense_quant(x, yv, o, ctx->tile_override, ctx->stream);
   if (e != hipSuccess) return hip_fail(e, "ohip_qgemm launch");
   return OHIP_OK;
@@ -940,14 +1005,15 @@ extern "C" int ohip_qconv2d(ohip_ctx* ctx, const ohip_qconv_desc* d, const void*
   col.base = xin; col.H = (int)d->h; col.W = (int)d->w; col.OH = (int)g.oh; col.OW = (int)g.ow;
   col.KW = (int)d->kw; col.cpc = (int)(cp / 16);
   col.sh = (int)d->stride_h; col.sw = (int)d->stride_w; col.dh = (int)d->dil_h; col.dw = (int)d->dil_w;
-  col.pt = (int)d->pad_t; col.pl = (int)d->pad_l; col.rows = (int)rows; col.kc = w->kc;
+  col.pt = (int)d->pad_t; col.pl = (int)d->pad_l; col.rows = (int)rows;
+  col.kc = w->kwrap > 0 ? w->kwrap : w->kc; col.kwrap = w->kwrap;
   col.xor_mask = u8 ? 0x80808080u : 0u;
   col.pad = padb * 0x01010101u;
-  DenseOperand wt{w->data, w->ld_bytes, (int)d->cout, w->kc, 0u, 0u};
+  DenseOperand wt{w->data, w->ld_bytes, (int)d->cout, w->kc, 0, 0u, 0u};
   QuantOut o{};
-  o.y = y; o.colsum = w->colsum; o.bias = bias; o.ca = shift - d->x_zp; o.ca_rows = nullptr;
+  o.y = y; o.colsum = w->colsum; o.flip = w->flip; o.bias = bias; o.ca = shift - d->x_zp; o.ca_rows = nullptr;
   o.comb = w->comb; o.n_comb = n_comb; o.out_kind = d->out_kind; o.y_zp = d->y_zp; o.lo = d->lo; o.hi = d->hi;
-  const int ob = d->out_kind == OHIP_QOUT_I32 ? 4 : 1;
+  const int ob = (d->out_kind == OHIP_QOUT_I32 || d->out_kind == OHIP_QOUT_F32) ? 4 : 1;
   const int64_t ohw = g.oh * g.ow;
   bool col_on_x;
   if (d->out_layout == OHIP_NCHW) {

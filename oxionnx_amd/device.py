@@ -50,6 +50,7 @@ class Weight:
 
     def __init__(self, ctx, handle, kind, dtype, shape, cached):
         self.ctx, self.handle, self.kind, self.dtype, self.shape, self.cached = ctx, handle, kind, dtype, shape, cached
+        ctx._weights.add(self)
 
     @property
     def nbytes(self):
@@ -71,18 +72,27 @@ class HipContext:
     """Owns one ohip_ctx on one GPU (oxionnx-cuda's CudaContext counterpart)."""
 
     def __init__(self, device=0, adopt_torch_stream=True):
+        import weakref
         torch = _torch()
         self.device = device
+        self._weights = weakref.WeakSet()
         h = ctypes.c_void_p()
         L.check(L.lib().ohip_ctx_create(device, ctypes.byref(h)))
         self.h = h
         if adopt_torch_stream:
+            # torch's default stream is the legacy null stream (handle 0); the
+            # context's own stream is a blocking stream, which the null stream
+            # already orders against, so only a non-default torch stream is
+            # adopted explicitly.
             with torch.cuda.device(device):
                 s = torch.cuda.current_stream(device).cuda_stream
-            L.check(L.lib().ohip_ctx_set_stream(self.h, ctypes.c_void_p(s)))
+            if s:
+                L.check(L.lib().ohip_ctx_set_stream(self.h, ctypes.c_void_p(s)))
 
     def close(self):
         if self.h:
+            for w in list(self._weights):
+                w.handle = None       # the context frees every weight it owns
             L.lib().ohip_ctx_destroy(self.h)
             self.h = None
 
@@ -213,7 +223,8 @@ class HipContext:
         n = w.shape[1]
         azp = np.ascontiguousarray(np.atleast_1d(np.asarray(a_zp, np.int32)))
         if out is None:
-            odt = {L.QOUT_U8: torch.uint8, L.QOUT_I8: torch.int8, L.QOUT_I32: torch.int32}[out_kind]
+            odt = {L.QOUT_U8: torch.uint8, L.QOUT_I8: torch.int8, L.QOUT_I32: torch.int32,
+                   L.QOUT_F32: torch.float32}[out_kind]
             out = torch.empty((m, n), dtype=odt, device=a.device)
         d = L.QGemmDesc(m, k, n, ohip_dtype(a.dtype), azp.ctypes.data_as(ctypes.POINTER(ctypes.c_int32)),
                         azp.size, out_kind, a_scale, y_scale, y_zp, lo, hi, a.stride(0), out.stride(0))
@@ -234,12 +245,13 @@ class HipContext:
         ow = L.lib().ohip_conv_out_dim(wd, pads[1], pads[3], kw, dilations[1], strides[1])
         if oh < 0 or ow < 0:
             raise L.OhipError(L.E_SHAPE, "bad conv geometry")
-        odt = {L.QOUT_U8: torch.uint8, L.QOUT_I8: torch.int8, L.QOUT_I32: torch.int32}[out_kind]
+        odt = {L.QOUT_U8: torch.uint8, L.QOUT_I8: torch.int8, L.QOUT_I32: torch.int32,
+                   L.QOUT_F32: torch.float32}[out_kind]
         if out is None:
             if out_layout == L.NCHW:
                 out = torch.empty((n, cout, oh, ow), dtype=odt, device=x.device)
             else:
-                ld = (cout + 15) // 16 * 16 if out_kind != L.QOUT_I32 else (cout + 3) // 4 * 4
+                ld = (cout + 15) // 16 * 16 if out_kind in (L.QOUT_U8, L.QOUT_I8) else (cout + 3) // 4 * 4
                 out = torch.zeros((n, oh, ow, ld), dtype=odt, device=x.device)
         d = L.QConvDesc(n, c, h, wd, cout, kh, kw, 1, strides[0], strides[1], dilations[0], dilations[1],
                         pads[0], pads[1], pads[2], pads[3], ohip_dtype(x.dtype), int(x_zp), out_kind, x_scale,
