@@ -1,0 +1,234 @@
+"""Benchmark of the MI355X dense-contraction provider (one GPU).
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-sweep]
+
+A step is one Gemm launch of the headline workload, config 2's largest shape
+(M, K, N) = (4096, 4096, 11008) in f16 with a row bias, operands resident in
+HBM.  The JSON line reports whole-job TFLOP/s for that step, the roofline of
+the kernel (its average duration measured with HIP events on the stream it is
+launched on), the reference-algorithm CPU baseline on a bounded row sample,
+and a sweep over every configured workload (configs 1-3 of BASELINE.json).
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "conv/GEMM TFLOP/s & int8 TOPS (% MFMA peak); end-to-end ms/forward"
+PEAK_TFLOPS = {"f16": 2500.0, "bf16": 2500.0, "f32": 157.3, "int8": 5000.0}
+HBM_GBPS = 8000.0
+HEADLINE = (4096, 4096, 11008)
+GEMM_SWEEP = [(1, 25088, 512), (128, 768, 3072), (2048, 4096, 4096), (4096, 4096, 11008)]
+
+
+def parse():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=50)
+    p.add_argument("--warmup", type=int, default=5)
+    p.add_argument("--no-cpu", action="store_true")
+    p.add_argument("--no-sweep", action="store_true")
+    p.add_argument("--cpu-seconds", type=float, default=10.0)
+    p.add_argument("--only", default="", help="run one sweep item (for profiling)")
+    return p.parse_args()
+
+
+def time_launches(torch, stream, fn, iters, warmup):
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for _ in range(iters):
+        fn()
+    end.record(stream)
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / iters  # ms per launch
+
+
+def gemm_setup(torch, ctx, L, m, k, n, dtype, rng):
+    a = rng.uniform(-1, 1, (m, k)).astype(np.float32)
+    b = rng.normal(0, 1 / np.sqrt(k), (k, n)).astype(np.float32)
+    c = rng.normal(0, 0.01, n).astype(np.float32)
+    tdt = {L.F32: torch.float32, L.F16: torch.float16, L.BF16: torch.bfloat16}[dtype]
+    w = ctx.weight_gemm(b, dtype=dtype, name=f"B_{m}_{k}_{n}_{dtype}", label="Gemm.B")
+    at = torch.from_numpy(a).cuda().to(tdt)
+    ct = torch.from_numpy(c).cuda().to(tdt)
+    y = torch.empty((m, n), dtype=tdt, device="cuda")
+    return a, b, c, w, at, ct, y
+
+
+def load_traffic(name):
+    """HBM bytes per launch from a committed rocprofv3 --pmc summary, if any."""
+    path = os.path.join(ROOT, "profiles", f"{name}_pmc.txt")
+    if not os.path.exists(path):
+        return None
+    for line in open(path):
+        if line.startswith("traffic_bytes_per_launch:"):
+            return float(line.split(":", 1)[1])
+    return None
+
+
+def cpu_baseline_f16(seconds):
+    """The reference's f16 Gemm algorithm (math_typed.rs:589-634, restated in C
+    with the same per-element order) on a bounded row sample of the headline
+    shape, single-threaded like the reference."""
+    from oracle import oracle as O
+    m, k, n = HEADLINE
+    rng = np.random.default_rng(7)
+    a = O.f32_to_half_bits(rng.uniform(-1, 1, (8, k)).astype(np.float32))
+    b = O.f32_to_half_bits(rng.normal(0, 1 / np.sqrt(k), (k, n)).astype(np.float32))
+    c = O.f32_to_half_bits(rng.normal(0, 0.01, n).astype(np.float32))
+    t0 = time.perf_counter()
+    O.gemm_half(a, b, c, rows=(0, 1))
+    per_row = time.perf_counter() - t0
+    rows = int(max(1, min(8, seconds / max(per_row, 1e-6))))
+    t0 = time.perf_counter()
+    O.gemm_half(a, b, c, rows=(0, rows))
+    dt = time.perf_counter() - t0
+    flops = 2.0 * rows * k * n
+    return {"value": flops / dt / 1e12, "unit": "TFLOP/s", "cores": 1, "kind": "port",
+            "sample": f"{rows} of {m} output rows of the f16 Gemm ({rows}x{k}x{n}), {dt:.2f} s; "
+                      f"full forward extrapolates to {dt * m / rows:.0f} s"}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU only; multi-GPU sharding is a design "
+                                   "note (DESIGN.md), not a measured path", "n_gpus": args.gpus}))
+        sys.exit(2)
+    import torch
+    from oxionnx_amd import _lib as L
+    from oxionnx_amd.device import HipContext
+
+    torch.cuda.set_device(0)
+    stream = torch.cuda.Stream()
+    with torch.cuda.stream(stream):
+        ctx = HipContext(0)   # adopts `stream`: events below are recorded on it
+    rng = np.random.default_rng(2024)
+    extras = {}
+
+    with torch.cuda.stream(stream):
+        m, k, n = HEADLINE
+        _, _, _, w, at, ct, y = gemm_setup(torch, ctx, L, m, k, n, L.F16, rng)
+        step = lambda: ctx.gemm(at, w, ct, out=y)
+        for _ in range(args.warmup):
+            step()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        ev0.record(stream)
+        for _ in range(args.steps):
+            step()
+        ev1.record(stream)
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+        ms = ev0.elapsed_time(ev1) / args.steps
+        flops = 2.0 * m * k * n
+        tflops = flops / (ms * 1e-3) / 1e12
+        alg_bytes = 2 * (m * k + k * n + m * n) + 2 * n
+        traffic = load_traffic("gemm_f16_4096x4096x11008")
+
+        if not args.no_sweep:
+            sweep = []
+            for (mm, kk, nn) in GEMM_SWEEP:
+                for dt, name in ((L.F32, "f32"), (L.F16, "f16")):
+                    if args.only and args.only != f"gemm_{name}_{mm}x{kk}x{nn}":
+                        continue
+                    _, _, _, ww, aa, cc, yy = gemm_setup(torch, ctx, L, mm, kk, nn, dt, rng)
+                    iters = 200 if mm * kk * nn < 1e9 else 30
+                    t = time_launches(torch, stream, lambda: ctx.gemm(aa, ww, cc, out=yy), iters, 3)
+                    eb = 4 if dt == L.F32 else 2
+                    fl = 2.0 * mm * kk * nn
+                    by = eb * (mm * kk + kk * nn + mm * nn + nn)
+                    sweep.append({"shape": [mm, kk, nn], "dtype": name, "ms": round(t, 5),
+                                  "tflops": round(fl / t / 1e9, 2),
+                                  "frac_mfma": round(fl / t / 1e9 / PEAK_TFLOPS[name], 4),
+                                  "gbps": round(by / t / 1e6, 1),
+                                  "frac_hbm": round(by / t / 1e6 / HBM_GBPS, 4)})
+                    del ww, aa, cc, yy
+            extras["gemm_sweep"] = sweep
+            extras.update(bench_conv(torch, ctx, L, stream, rng, args.only))
+            extras.update(bench_int8(torch, ctx, L, stream, rng, args.only))
+
+    line = {
+        "metric": METRIC, "value": round(tflops, 2), "unit": "TFLOP/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 5),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f16",
+        "data": "synthetic (seeded numpy; A~U(-1,1), B~N(0,1/sqrt(K)) initializer, bias~N(0,0.01))",
+        "config": {"workload": "config 2: Gemm f16 (M,K,N)=(4096,4096,11008) + row bias, B resident",
+                   "M": m, "K": k, "N": n, "parallelism": "single GPU"},
+        "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK_TFLOPS["f16"],
+                     "unit": "TFLOP/s", "frac": round(tflops / PEAK_TFLOPS["f16"], 4),
+                     "traffic": traffic, "algorithmic_bytes": alg_bytes,
+                     "kernel": "mfma_gemm_kernel<Op::F16, Tile<256,256,2,4>, DenseRows, DenseRows, FloatEpi<_Float16>>"},
+        "wall_s_timed_region": round(wall, 3),
+    }
+    if not args.no_cpu:
+        line["cpu_baseline"] = cpu_baseline_f16(args.cpu_seconds)
+    line.update(extras)
+    print(json.dumps(line))
+    ctx.close()
+
+
+def bench_conv(torch, ctx, L, stream, rng, only):
+    """Config 1: single Conv f32 NCHW [1,64,128,128] * [64,64,3,3] + bias + fused Relu."""
+    if only and only != "conv_f32_cfg1":
+        return {}
+    x = rng.uniform(-1, 1, (1, 64, 128, 128)).astype(np.float32)
+    wgt = rng.normal(0, 0.05, (64, 64, 3, 3)).astype(np.float32)
+    b = rng.normal(0, 0.01, 64).astype(np.float32)
+    w = ctx.weight_conv(wgt, name="conv1.W", label="Conv.W")
+    xt = torch.from_numpy(x).cuda()
+    bt = torch.from_numpy(b).cuda()
+    y = torch.empty((1, 64, 128, 128), dtype=torch.float32, device="cuda")
+    t = time_launches(torch, stream, lambda: ctx.conv2d(xt, w, bt, pads=(1, 1, 1, 1), act=L.ACT_RELU, out=y),
+                      100, 5)
+    fl = 2.0 * 64 * 128 * 128 * 64 * 9
+    return {"conv_cfg1_f32": {"ms": round(t, 5), "tflops": round(fl / t / 1e9, 2),
+                              "frac_mfma": round(fl / t / 1e9 / PEAK_TFLOPS["f32"], 4),
+                              "note": "includes the NCHW->NHWC staging transpose"}}
+
+
+def bench_int8(torch, ctx, L, stream, rng, only):
+    """Config 3: QLinearMatMul BERT-base FFN pair + MatMulInteger."""
+    if only and only not in ("int8_ffn",):
+        return {}
+    out = {}
+    a = rng.integers(0, 256, (4096, 768)).astype(np.uint8)
+    b1 = rng.integers(-127, 128, (768, 3072)).astype(np.int8)
+    b2 = rng.integers(-127, 128, (3072, 768)).astype(np.int8)
+    s1 = rng.uniform(0.001, 0.01, 3072).astype(np.float32)
+    s2 = rng.uniform(0.001, 0.01, 768).astype(np.float32)
+    w1 = ctx.weight_qgemm(b1, zp=0, scale=s1, name="ffn1.B")
+    w2 = ctx.weight_qgemm(b2, zp=0, scale=s2, name="ffn2.B")
+    at = torch.from_numpy(a).cuda()
+    h = torch.empty((4096, 3072), dtype=torch.uint8, device="cuda")
+    y = torch.empty((4096, 768), dtype=torch.uint8, device="cuda")
+    yi = torch.empty((4096, 3072), dtype=torch.int32, device="cuda")
+
+    def pair():
+        ctx.qgemm(at, w1, a_zp=128, a_scale=0.02, y_scale=0.05, y_zp=128, out=h)
+        ctx.qgemm(h, w2, a_zp=128, a_scale=0.05, y_scale=0.05, y_zp=128, out=y)
+
+    t = time_launches(torch, stream, pair, 100, 5)
+    ops = 2 * 2.0 * 4096 * 768 * 3072
+    out["int8_ffn_pair"] = {"ms": round(t, 5), "tops": round(ops / t / 1e9, 2),
+                            "frac_mfma": round(ops / t / 1e9 / PEAK_TFLOPS["int8"], 4)}
+    t = time_launches(torch, stream, lambda: ctx.qgemm(at, w1, a_zp=128, out_kind=L.QOUT_I32, out=yi), 100, 5)
+    by = 4096 * 768 + 768 * 3072 + 4 * 4096 * 3072
+    out["matmul_integer_i32"] = {"ms": round(t, 5), "tops": round(ops / 2 / t / 1e9, 2),
+                                 "gbps": round(by / t / 1e6, 1), "frac_hbm": round(by / t / 1e6 / HBM_GBPS, 4)}
+    return out
+
+
+if __name__ == "__main__":
+    main()

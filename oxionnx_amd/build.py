@@ -20,7 +20,7 @@ LIB = os.path.join(HERE, "libohip.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 
-SOURCES = ["kernels.hip", "ops.cpp"]
+SOURCES = ["contract_f32.hip", "contract_f16.hip", "contract_bf16.hip", "contract_i8.hip", "aux_kernels.hip", "ops.cpp"]
 
 FLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-ffp-contract=off",

@@ -1,0 +1,254 @@
+// Dispatch by element type to the per-dtype contraction units, plus the
+// skinny-M GEMV path and the layout kernels that feed the MFMA kernels.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "launch.hpp"
+
+namespace ohip {
+
+hipError_t run_dense_f32(const DenseOperand&, const DenseOperand&, const FloatOut&, int, hipStream_t);
+hipError_t run_dense_f16(const DenseOperand&, const DenseOperand&, const FloatOut&, int, hipStream_t);
+hipError_t run_dense_bf16(const DenseOperand&, const DenseOperand&, const FloatOut&, int, hipStream_t);
+hipError_t run_dense_i8(const DenseOperand&, const DenseOperand&, const QuantOut&, int, hipStream_t);
+hipError_t run_conv_f32(const Im2colOperand&, const DenseOperand&, bool, const FloatOut&, int, hipStream_t);
+hipError_t run_conv_f16(const Im2colOperand&, const DenseOperand&, bool, const FloatOut&, int, hipStream_t);
+hipError_t run_conv_bf16(const Im2colOperand&, const DenseOperand&, bool, const FloatOut&, int, hipStream_t);
+hipError_t run_conv_i8(const Im2colOperand&, const DenseOperand&, bool, const QuantOut&, int, hipStream_t);
+
+hipError_t run_dense_float(int dtype, const DenseOperand& x, const DenseOperand& y, const FloatOut& o, int tile,
+                           hipStream_t st) {
+  switch (dtype) {
+    case DT_F32: return run_dense_f32(x, y, o, tile, st);
+    case DT_F16: return run_dense_f16(x, y, o, tile, st);
+    case DT_BF16: return run_dense_bf16(x, y, o, tile, st);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+hipError_t run_conv_float(int dtype, const Im2colOperand& col, const DenseOperand& w, bool col_on_x,
+                          const FloatOut& o, int tile, hipStream_t st) {
+  switch (dtype) {
+    case DT_F32: return run_conv_f32(col, w, col_on_x, o, tile, st);
+    case DT_F16: return run_conv_f16(col, w, col_on_x, o, tile, st);
+    case DT_BF16: return run_conv_bf16(col, w, col_on_x, o, tile, st);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+hipError_t run_dense_quant(const DenseOperand& x, const DenseOperand& y, const QuantOut& o, int tile, hipStream_t st) {
+  return run_dense_i8(x, y, o, tile, st);
+}
+
+hipError_t run_conv_quant(const Im2colOperand& col, const DenseOperand& w, bool col_on_x, const QuantOut& o,
+                          int tile, hipStream_t st) {
+  return run_conv_i8(col, w, col_on_x, o, tile, st);
+}
+
+// ---------------------------------------------------------------- skinny GEMV
+// y[m][n] = sum_k A[m][k] * W[n][k] for M <= kMaxGemvM.  Each wave owns one
+// weight row and one K slice, streams the row with 16-byte loads, and writes
+// one f32 partial per (slice, m, n); gemv_finish sums the slices in a fixed
+// order (deterministic) and applies the epilogue.
+template <class T> struct Vec16;
+template <> struct Vec16<float> {
+  static __device__ __forceinline__ void unpack(u32x4 v, float (&f)[4]) {
+    f[0] = lane_f32(v.x); f[1] = lane_f32(v.y); f[2] = lane_f32(v.z); f[3] = lane_f32(v.w);
+  }
+  static constexpr int N = 4;
+};
+template <> struct Vec16<_Float16> {
+  static constexpr int N = 8;
+  static __device__ __forceinline__ void unpack(u32x4 v, float (&f)[8]) {
+    f16x8 h = __builtin_bit_cast(f16x8, v);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) f[e] = (float)h[e];
+  }
+};
+template <> struct Vec16<__bf16> {
+  static constexpr int N = 8;
+  static __device__ __forceinline__ void unpack(u32x4 v, float (&f)[8]) {
+    uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      f[2 * e] = __builtin_bit_cast(float, w[e] << 16);
+      f[2 * e + 1] = __builtin_bit_cast(float, w[e] & 0xffff0000u);
+    }
+  }
+};
+
+template <class T, int M>
+__global__ void __launch_bounds__(256)
+gemv_partial_kernel(const T* __restrict__ a, int64_t lda, const T* __restrict__ w, int64_t ldw, int N, int kc,
+                    int chunks_per_split, float* __restrict__ part) {
+  const int lane = threadIdx.x & 63;
+  const int n = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int s = blockIdx.y;
+  if (n >= N) return;
+  const int c0 = s * chunks_per_split;
+  const int c1 = min(kc, c0 + chunks_per_split);
+  constexpr int E = Vec16<T>::N;
+  const u32x4* wr = reinterpret_cast<const u32x4*>(w + (int64_t)n * ldw);
+  float acc[M];
+#pragma unroll
+  for (int m = 0; m < M; ++m) acc[m] = 0.0f;
+  int c = c0 + lane;
+  for (; c + 64 < c1; c += 128) {
+    u32x4 w0 = __builtin_nontemporal_load(wr + c);
+    u32x4 w1 = __builtin_nontemporal_load(wr + c + 64);
+    float f0[E], f1[E];
+    Vec16<T>::unpack(w0, f0);
+    Vec16<T>::unpack(w1, f1);
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+      const u32x4* ar = reinterpret_cast<const u32x4*>(a + (int64_t)m * lda);
+      float g0[E], g1[E];
+      Vec16<T>::unpack(ar[c], g0);
+      Vec16<T>::unpack(ar[c + 64], g1);
+#pragma unroll
+      for (int e = 0; e < E; ++e) acc[m] += f0[e] * g0[e];
+#pragma unroll
+      for (int e = 0; e < E; ++e) acc[m] += f1[e] * g1[e];
+    }
+  }
+  for (; c < c1; c += 64) {
+    u32x4 w0 = __builtin_nontemporal_load(wr + c);
+    float f0[E];
+    Vec16<T>::unpack(w0, f0);
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+      const u32x4* ar = reinterpret_cast<const u32x4*>(a + (int64_t)m * lda);
+      float g0[E];
+      Vec16<T>::unpack(ar[c], g0);
+#pragma unroll
+      for (int e = 0; e < E; ++e) acc[m] += f0[e] * g0[e];
+    }
+  }
+#pragma unroll
+  for (int m = 0; m < M; ++m) {
+    float v = acc[m];
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+    if (lane == 0) part[((int64_t)s * M + m) * N + n] = v;
+  }
+}
+
+template <class OutT>
+__global__ void gemv_finish_kernel(const float* __restrict__ part, int splits, int M, int N, FloatEpi<OutT> epi) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= (int64_t)M * N) return;
+  const int m = (int)(idx / N), n = (int)(idx - (int64_t)m * N);
+  float v = 0.0f;
+  for (int s = 0; s < splits; ++s) v += part[((int64_t)s * M + m) * N + n];
+  // GEMM orientation: i = n (weight row), j = m (activation row)
+  epi.y[epi.index(n, m)] = from_f32<OutT>(epi.finish(v, n, m));
+}
+
+template <class T, class OutT>
+static hipError_t gemv_t(const GemvArgs& g, const FloatOut& o, hipStream_t st) {
+  constexpr int E = Vec16<T>::N;
+  (void)E;
+  const T* a = reinterpret_cast<const T*>(g.a);
+  const T* w = reinterpret_cast<const T*>(g.w);
+  dim3 grid((g.N + 3) / 4, g.splits);
+  switch (g.M) {
+#define OHIP_GEMV_CASE(MM)                                                                                   \
+  case MM:                                                                                                   \
+    hipLaunchKernelGGL((gemv_partial_kernel<T, MM>), grid, dim3(256), 0, st, a, g.lda, w, g.ldw, g.N, g.kc, \
+                       g.chunks_per_split, g.partial);                                                       \
+    break;
+    OHIP_GEMV_CASE(1) OHIP_GEMV_CASE(2) OHIP_GEMV_CASE(3) OHIP_GEMV_CASE(4)
+    OHIP_GEMV_CASE(5) OHIP_GEMV_CASE(6) OHIP_GEMV_CASE(7) OHIP_GEMV_CASE(8)
+#undef OHIP_GEMV_CASE
+    default: return hipErrorInvalidValue;
+  }
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  const int64_t total = (int64_t)g.M * g.N;
+  hipLaunchKernelGGL((gemv_finish_kernel<OutT>), dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st,
+                     g.partial, g.splits, g.M, g.N, make_float_epi<OutT>(o));
+  return hipGetLastError();
+}
+
+hipError_t run_gemv(int dtype, const GemvArgs& g, const FloatOut& o, hipStream_t st) {
+  switch (dtype) {
+    case DT_F32: return gemv_t<float, float>(g, o, st);
+    case DT_F16: return gemv_t<_Float16, _Float16>(g, o, st);
+    case DT_BF16: return gemv_t<__bf16, __bf16>(g, o, st);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+// ---------------------------------------------------------------- layout
+// NCHW -> NHWC with the channel axis zero-padded to cp: per image a [C][HW]
+// -> [HW][cp] transpose through a 32x33 LDS tile (coalesced on both sides).
+template <class T>
+__global__ void nchw_to_nhwc_kernel(const T* __restrict__ src, T* __restrict__ dst, int C, int HW, int cp) {
+  __shared__ T tile[32][33];
+  const int n = blockIdx.z;
+  const int c0 = blockIdx.y * 32, s0 = blockIdx.x * 32;
+  const T* s = src + (int64_t)n * C * HW;
+  T* d = dst + (int64_t)n * HW * cp;
+  for (int r = threadIdx.y; r < 32; r += blockDim.y) {
+    const int c = c0 + r, sp = s0 + threadIdx.x;
+    tile[r][threadIdx.x] = (c < C && sp < HW) ? s[(int64_t)c * HW + sp] : T(0);
+  }
+  __syncthreads();
+  for (int r = threadIdx.y; r < 32; r += blockDim.y) {
+    const int sp = s0 + r, c = c0 + threadIdx.x;
+    if (sp < HW && c < cp) d[(int64_t)sp * cp + c] = tile[threadIdx.x][r];
+  }
+}
+
+template <class T>
+static hipError_t nchw_to_nhwc_t(const void* src, void* dst, int N, int C, int HW, int cp, hipStream_t st) {
+  dim3 grid((HW + 31) / 32, (cp + 31) / 32, N), block(32, 8);
+  hipLaunchKernelGGL(nchw_to_nhwc_kernel<T>, grid, block, 0, st, reinterpret_cast<const T*>(src),
+                     reinterpret_cast<T*>(dst), C, HW, cp);
+  return hipGetLastError();
+}
+
+hipError_t run_nchw_to_nhwc(int elem_bytes, const void* src, void* dst, int N, int C, int HW, int cp,
+                            hipStream_t st) {
+  switch (elem_bytes) {
+    case 1: return nchw_to_nhwc_t<uint8_t>(src, dst, N, C, HW, cp, st);
+    case 2: return nchw_to_nhwc_t<uint16_t>(src, dst, N, C, HW, cp, st);
+    case 4: return nchw_to_nhwc_t<uint32_t>(src, dst, N, C, HW, cp, st);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+// dst[r][c] = c < K ? src[r * rs + c * cs] : 0 for a [R][ld] destination: pads a
+// row-major operand to whole 16-byte chunks, or materialises a transpose.
+template <class T>
+__global__ void gather2d_kernel(const T* __restrict__ src, int64_t rs, int64_t cs, T* __restrict__ dst, int R,
+                                int K, int ld) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= (int64_t)R * ld) return;
+  const int r = (int)(idx / ld), c = (int)(idx - (int64_t)r * ld);
+  dst[idx] = c < K ? src[r * rs + c * cs] : T(0);
+}
+
+hipError_t run_gather2d(int elem_bytes, const void* src, int64_t rs, int64_t cs, void* dst, int R, int K, int ld,
+                        hipStream_t st) {
+  const int64_t total = (int64_t)R * ld;
+  dim3 grid((unsigned)((total + 255) / 256)), block(256);
+  switch (elem_bytes) {
+    case 1:
+      hipLaunchKernelGGL(gather2d_kernel<uint8_t>, grid, block, 0, st, reinterpret_cast<const uint8_t*>(src), rs,
+                         cs, reinterpret_cast<uint8_t*>(dst), R, K, ld);
+      break;
+    case 2:
+      hipLaunchKernelGGL(gather2d_kernel<uint16_t>, grid, block, 0, st, reinterpret_cast<const uint16_t*>(src),
+                         rs, cs, reinterpret_cast<uint16_t*>(dst), R, K, ld);
+      break;
+    case 4:
+      hipLaunchKernelGGL(gather2d_kernel<uint32_t>, grid, block, 0, st, reinterpret_cast<const uint32_t*>(src),
+                         rs, cs, reinterpret_cast<uint32_t*>(dst), R, K, ld);
+      break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+}  // namespace ohip

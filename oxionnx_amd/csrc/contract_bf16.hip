@@ -1,0 +1,5 @@
+// MFMA contraction kernels, bf16.
+#define OHIP_OP Op::BF16
+#define OHIP_OUT __bf16
+#define OHIP_SUFFIX bf16
+#include "contract.inc"

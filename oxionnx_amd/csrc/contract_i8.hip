@@ -1,0 +1,6 @@
+// MFMA contraction kernels, i8.
+#define OHIP_OP Op::I8
+#define OHIP_OUT void
+#define OHIP_SUFFIX i8
+#define OHIP_QUANT 1
+#include "contract.inc"

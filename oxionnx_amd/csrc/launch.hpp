@@ -1,0 +1,261 @@
+// Epilogues, tile table and launch helpers shared by the per-dtype
+// contraction translation units (contract_*.hip) and the GEMV path.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "internal.hpp"
+#include "mfma_core.hpp"
+
+namespace ohip {
+
+// ---------------------------------------------------------------- epilogues
+template <class T> __device__ __forceinline__ float to_f32(T v) { return (float)v; }
+template <class T> __device__ __forceinline__ T from_f32(float v) { return (T)v; }
+
+__device__ __forceinline__ float activate(float v, int act, float lo, float hi) {
+  switch (act) {
+    case ACT_RELU: return v > 0.0f ? v : 0.0f;  // f32::max(NaN, 0) == 0
+    case ACT_CLIP: return v < lo ? lo : (v > hi ? hi : v);
+    case ACT_LEAKY_RELU: return v >= 0.0f ? v : v * lo;
+    default: return v;
+  }
+}
+
+// Float output: v = acc; v *= alpha (when alpha != 1); v += beta * bias; act;
+// round to OutT.  Output element (i, j) sits at
+//   (i / ohw) * bstride + (i % ohw) * si + j * sj.
+template <class OutT> struct FloatEpi {
+  OutT* y;
+  int64_t si, sj, bstride;
+  int ohw, P, Q;
+  int vec;            // si == 1 and every 4-run of i is contiguous and aligned
+  int has_alpha;
+  float alpha, beta;
+  const OutT* bias;
+  int bias_mode;      // BIAS_*
+  int act;
+  float lo, hi;
+
+  __device__ __forceinline__ float bias_at(int i, int j) const {
+    switch (bias_mode) {
+      case BIAS_SCALAR: return to_f32(bias[0]);
+      case BIAS_I: return to_f32(bias[i]);
+      case BIAS_J: return to_f32(bias[j]);
+      case BIAS_FULL_JI: return to_f32(bias[(int64_t)j * P + i]);
+      default: return 0.0f;
+    }
+  }
+  __device__ __forceinline__ float finish(float v, int i, int j) const {
+    if (has_alpha) v = v * alpha;
+    if (bias_mode != BIAS_NONE) v = v + beta * bias_at(i, j);
+    return activate(v, act, lo, hi);
+  }
+  __device__ __forceinline__ int64_t index(int i, int j) const {
+    if (bstride == 0) return (int64_t)i * si + (int64_t)j * sj;
+    const int n = i / ohw;
+    return (int64_t)n * bstride + (int64_t)(i - n * ohw) * si + (int64_t)j * sj;
+  }
+  __device__ __forceinline__ void store(int i0, int j, f32x4 acc) const {
+    if (j >= Q) return;
+    if (vec && i0 + 3 < P) {
+      OutT o[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) o[r] = from_f32<OutT>(finish(acc[r], i0 + r, j));
+      OutT* dst = y + index(i0, j);
+      if constexpr (sizeof(OutT) == 4) {
+        *reinterpret_cast<f32x4*>(dst) = f32x4{__builtin_bit_cast(float, o[0]), __builtin_bit_cast(float, o[1]),
+                                               __builtin_bit_cast(float, o[2]), __builtin_bit_cast(float, o[3])};
+      } else {
+        typedef uint16_t u16x4 __attribute__((ext_vector_type(4)));
+        *reinterpret_cast<u16x4*>(dst) =
+            u16x4{__builtin_bit_cast(uint16_t, o[0]), __builtin_bit_cast(uint16_t, o[1]),
+                  __builtin_bit_cast(uint16_t, o[2]), __builtin_bit_cast(uint16_t, o[3])};
+      }
+      return;
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      if (i0 + r < P) y[index(i0 + r, j)] = from_f32<OutT>(finish(acc[r], i0 + r, j));
+  }
+};
+
+// Integer output.  The MFMA sums A' * B'' where A' is the activation shifted
+// into int8 (u8 ^ 0x80 == u8 - 128) and B'' = w - w_zp.  The true accumulator
+// sum (a - a_zp)(w - w_zp) = sum A' B'' + ca * colsum(B'') with ca = shift -
+// a_zp, plus the int32 bias.  Arithmetic is modulo 2^32, exact whenever the
+// true value fits int32 (the host gate guarantees it).  Requantisation then
+// follows SatRange::requantize: f64 product with the f32 combined scale, + zp,
+// round half to even, clamp.
+struct QuantEpi {
+  void* y;
+  int64_t si, sj, bstride;
+  int ohw, P, Q;
+  int vec;
+  int w_on_i;               // weight channel index is i (else j)
+  const int32_t* colsum;    // per weight channel
+  const int8_t* flip;       // per weight channel: 1 = the packed channel holds -(w - w_zp)
+  const int32_t* bias;      // per weight channel, may be null
+  int32_t ca;               // per-tensor correction factor
+  const int32_t* ca_rows;   // per activation row, may be null
+  const float* comb;        // combined scale per channel (n_comb == 1 -> per tensor)
+  int n_comb;
+  int out_kind;             // QOUT_U8, QOUT_I8, QOUT_I32 (raw), QOUT_F32 (requantised, as f32)
+  int32_t y_zp, lo, hi;
+
+  __device__ __forceinline__ int64_t index(int i, int j) const {
+    if (bstride == 0) return (int64_t)i * si + (int64_t)j * sj;
+    const int n = i / ohw;
+    return (int64_t)n * bstride + (int64_t)(i - n * ohw) * si + (int64_t)j * sj;
+  }
+  __device__ __forceinline__ int32_t exact(int32_t acc, int i, int j) const {
+    const int ch = w_on_i ? i : j;
+    const int row = w_on_i ? j : i;
+    const uint32_t c = (uint32_t)(ca_rows ? ca_rows[row] : ca);
+    uint32_t v = (uint32_t)acc + c * (uint32_t)colsum[ch];
+    if (flip && flip[ch]) v = 0u - v;
+    if (bias) v += (uint32_t)bias[ch];
+    return (int32_t)v;
+  }
+  __device__ __forceinline__ int32_t requant(int32_t v, int i, int j) const {
+#pragma clang fp contract(off)
+    const int ch = w_on_i ? i : j;
+    const float cs = comb[n_comb > 1 ? ch : 0];
+    double d = (double)v * (double)cs;
+    d = d + (double)y_zp;
+    d = __builtin_rint(d);
+    d = d < (double)lo ? (double)lo : d;
+    d = d > (double)hi ? (double)hi : d;
+    return (int32_t)d;
+  }
+  __device__ __forceinline__ void store(int i0, int j, i32x4 acc) const {
+    if (j >= Q) return;
+    int32_t v[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      v[r] = exact(acc[r], i0 + r, j);
+      if (out_kind != QOUT_I32) v[r] = requant(v[r], i0 + r, j);
+    }
+    if (out_kind == QOUT_F32) {
+      // requantised lanes stored as f32, the reference Tensor's representation
+      float* yy = reinterpret_cast<float*>(y);
+      if (vec && i0 + 3 < P) {
+        *reinterpret_cast<f32x4*>(yy + index(i0, j)) = f32x4{(float)v[0], (float)v[1], (float)v[2], (float)v[3]};
+      } else {
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          if (i0 + r < P) yy[index(i0 + r, j)] = (float)v[r];
+      }
+    } else if (out_kind == QOUT_I32) {
+      int32_t* yy = reinterpret_cast<int32_t*>(y);
+      if (vec && i0 + 3 < P) {
+        *reinterpret_cast<i32x4*>(yy + index(i0, j)) = i32x4{v[0], v[1], v[2], v[3]};
+      } else {
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          if (i0 + r < P) yy[index(i0 + r, j)] = v[r];
+      }
+    } else {
+      uint8_t* yy = reinterpret_cast<uint8_t*>(y);
+      if (vec && i0 + 3 < P) {
+        uint32_t packed = (uint32_t)(v[0] & 0xff) | ((uint32_t)(v[1] & 0xff) << 8) |
+                          ((uint32_t)(v[2] & 0xff) << 16) | ((uint32_t)(v[3] & 0xff) << 24);
+        *reinterpret_cast<uint32_t*>(yy + index(i0, j)) = packed;
+      } else {
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          if (i0 + r < P) yy[index(i0 + r, j)] = (uint8_t)(v[r] & 0xff);
+      }
+    }
+  }
+};
+
+// ---------------------------------------------------------------- tiles
+// Tile ids (ohip_set_tile_override): block tile BP x BQ, WP x WQ waves.
+using T64 = Tile<64, 64, 2, 2>;           // 1
+using T128 = Tile<128, 128, 2, 2>;        // 2
+using T256x128 = Tile<256, 128, 2, 2>;    // 3
+using T128x256 = Tile<128, 256, 2, 2>;    // 4
+using T256 = Tile<256, 256, 2, 2>;        // 5
+using T256w8 = Tile<256, 256, 2, 4>;      // 6: 8 waves, 128x64 per wave
+using T256x128w8 = Tile<256, 128, 4, 2>;  // 7: 8 waves, 64x64 per wave
+using T128x256w8 = Tile<128, 256, 2, 4>;  // 8: 8 waves, 64x64 per wave
+constexpr int kTileCount = 8;
+
+template <Op O, class Tl, class LX, class LY, class Epi>
+inline hipError_t launch_tile(const LX& lx, const LY& ly, const Epi& epi, int P, int Q, int kc,
+                              hipStream_t st) {
+  const int nP = (P + Tl::BP - 1) / Tl::BP, nQ = (Q + Tl::BQ - 1) / Tl::BQ;
+  const int64_t nb = (int64_t)nP * nQ;
+  if (nb <= 0) return hipSuccess;
+  if (nb > 0x7fffffff) return hipErrorInvalidValue;
+  hipLaunchKernelGGL((mfma_gemm_kernel<O, Tl, LX, LY, Epi>), dim3((unsigned)nb), dim3(Tl::kThreads),
+                     0, st, lx, ly, epi, nP, nQ, kc);
+  return hipGetLastError();
+}
+
+// Automatic choice: the largest tile that still gives at least one block
+// per CU (256 CUs), else the smallest.
+inline int pick_tile(int P, int Q, int forced) {
+  if (forced >= 1 && forced <= kTileCount) return forced;
+  auto blocks = [&](int bp, int bq) { return (int64_t)((P + bp - 1) / bp) * ((Q + bq - 1) / bq); };
+  if (blocks(256, 256) >= 256) return 6;
+  if (blocks(256, 128) >= 256) return P >= Q ? 7 : 8;
+  if (blocks(128, 128) >= 200) return 2;
+  return 1;
+}
+
+template <Op O, class LX, class LY, class Epi>
+inline hipError_t launch_any(const LX& lx, const LY& ly, const Epi& epi, int P, int Q, int kc, int tile,
+                             hipStream_t st) {
+  switch (pick_tile(P, Q, tile)) {
+    case 2: return launch_tile<O, T128>(lx, ly, epi, P, Q, kc, st);
+    case 3: return launch_tile<O, T256x128>(lx, ly, epi, P, Q, kc, st);
+    case 4: return launch_tile<O, T128x256>(lx, ly, epi, P, Q, kc, st);
+    case 5: return launch_tile<O, T256>(lx, ly, epi, P, Q, kc, st);
+    case 6: return launch_tile<O, T256w8>(lx, ly, epi, P, Q, kc, st);
+    case 7: return launch_tile<O, T256x128w8>(lx, ly, epi, P, Q, kc, st);
+    case 8: return launch_tile<O, T128x256w8>(lx, ly, epi, P, Q, kc, st);
+    default: return launch_tile<O, T64>(lx, ly, epi, P, Q, kc, st);
+  }
+}
+
+template <class OutT>
+inline FloatEpi<OutT> make_float_epi(const FloatOut& o) {
+  FloatEpi<OutT> e;
+  e.y = reinterpret_cast<OutT*>(o.y);
+  e.si = o.si; e.sj = o.sj; e.bstride = o.bstride; e.ohw = o.ohw; e.P = o.P; e.Q = o.Q;
+  e.vec = o.vec; e.has_alpha = o.alpha != 1.0f; e.alpha = o.alpha; e.beta = o.beta;
+  e.bias = reinterpret_cast<const OutT*>(o.bias); e.bias_mode = o.bias ? o.bias_mode : BIAS_NONE;
+  e.act = o.act; e.lo = o.lo; e.hi = o.hi;
+  return e;
+}
+
+inline QuantEpi make_quant_epi(const QuantOut& o) {
+  QuantEpi e;
+  e.y = o.y; e.si = o.si; e.sj = o.sj; e.bstride = o.bstride; e.ohw = o.ohw; e.P = o.P; e.Q = o.Q;
+  e.vec = o.vec; e.w_on_i = o.w_on_i; e.colsum = o.colsum; e.flip = o.flip; e.bias = o.bias; e.ca = o.ca;
+  e.ca_rows = o.ca_rows; e.comb = o.comb; e.n_comb = o.n_comb; e.out_kind = o.out_kind;
+  e.y_zp = o.y_zp; e.lo = o.lo; e.hi = o.hi;
+  return e;
+}
+
+inline DenseRows make_dense(const DenseOperand& d) {
+  DenseRows r;
+  r.base = reinterpret_cast<const char*>(d.base);
+  r.ld = d.ld_bytes; r.rows = d.rows; r.kc = d.kc; r.kwrap = d.kwrap; r.xor_mask = d.xor_mask;
+  r.pad = u32x4{d.pad, d.pad, d.pad, d.pad};
+  return r;
+}
+
+inline Im2colNHWC make_im2col(const Im2colOperand& c) {
+  Im2colNHWC r;
+  r.base = reinterpret_cast<const char*>(c.base);
+  r.H = c.H; r.W = c.W; r.OH = c.OH; r.OW = c.OW; r.KW = c.KW; r.cpc = c.cpc;
+  r.sh = c.sh; r.sw = c.sw; r.dh = c.dh; r.dw = c.dw; r.pt = c.pt; r.pl = c.pl;
+  r.rows = c.rows; r.kc = c.kc; r.kwrap = c.kwrap; r.xor_mask = c.xor_mask;
+  r.pad = u32x4{c.pad, c.pad, c.pad, c.pad};
+  return r;
+}
+
+}  // namespace ohip

@@ -79,7 +79,7 @@ template <int BP_, int BQ_, int WP_, int WQ_> struct Tile {
   static constexpr int kThreads = 64 * WP * WQ;
   static constexpr int TP = BP / (WP * 16), TQ = BQ / (WQ * 16);
   static constexpr int kChunks = 8;          // 16-byte chunks per row per stage
-  static constexpr int kRowStride = 9;       // +1 chunk of padding: rows start 16 B apart mod 128
+  static constexpr int kRowStride = 8;       // rows are 128 B; chunks are XOR-swizzled (lds_slot)
   static constexpr int NX = BP * kChunks / kThreads;
   static constexpr int NY = BQ * kChunks / kThreads;
   static constexpr int kStage = (BP + BQ) * kRowStride;  // in u32x4 units
@@ -91,6 +91,12 @@ template <int BP_, int BQ_, int WP_, int WQ_> struct Tile {
 // ---------------------------------------------------------------- loaders
 // A loader owns NR rows of one operand for the lifetime of the block.  Thread
 // t loads chunk (t & 7) of rows (t >> 3) + i * (threads / 8), i < NR.
+//
+// load() only issues the 16-byte global loads -- every address is clamped
+// into the operand, so no branch and no wait sits between them -- and returns
+// a bit mask of which rows hold real data.  fix() runs after the MFMAs of the
+// current stage, when the loads have landed: it applies the u8 -> int8 shift
+// and substitutes the pad value for out-of-range rows, chunks and taps.
 struct DenseRows {
   const char* base;   // row 0
   int64_t ld;         // bytes between rows (multiple of 16)
@@ -102,30 +108,38 @@ struct DenseRows {
   u32x4 pad;          // value used outside the matrix
 
   template <int NR, int kThreads>
-  struct State { const char* ptr[NR]; bool ok[NR]; };
+  struct State { const char* ptr[NR]; uint32_t okmask; };
 
   template <int NR, int kThreads>
   __device__ __forceinline__ void init(State<NR, kThreads>& s, int row0, int t) const {
+    s.okmask = 0;
 #pragma unroll
     for (int i = 0; i < NR; ++i) {
       int r = row0 + (t >> 3) + i * (kThreads / 8);
-      s.ok[i] = r < rows;
-      s.ptr[i] = base + (int64_t)(s.ok[i] ? r : 0) * ld;
+      const bool ok = r < rows;
+      s.okmask |= (ok ? 1u : 0u) << i;
+      s.ptr[i] = base + (int64_t)(ok ? r : 0) * ld;
     }
   }
   template <int NR, int kThreads>
-  __device__ __forceinline__ void load(const State<NR, kThreads>& s, int kt, int t, u32x4 (&v)[NR]) const {
+  __device__ __forceinline__ uint32_t load(const State<NR, kThreads>& s, int kt, int t, u32x4 (&v)[NR]) const {
     int gk = kt * 8 + (t & 7);
     if (kwrap > 0 && gk >= kwrap) gk -= kwrap;
     const bool kin = gk < kc;
+    const int64_t off = (int64_t)(kin ? gk : 0) * 16;
 #pragma unroll
-    for (int i = 0; i < NR; ++i) {
-      if (s.ok[i] && kin) {
-        u32x4 x = *reinterpret_cast<const u32x4*>(s.ptr[i] + (int64_t)gk * 16);
-        v[i] = x ^ xor_mask;
-      } else {
-        v[i] = gk < kc ? pad : u32x4{0, 0, 0, 0};
-      }
+    for (int i = 0; i < NR; ++i) v[i] = *reinterpret_cast<const u32x4*>(s.ptr[i] + off);
+    return kin ? s.okmask : 0u;
+  }
+  template <int NR>
+  __device__ __forceinline__ void fix(u32x4 (&v)[NR], uint32_t valid) const {
+    if (xor_mask) {
+#pragma unroll
+      for (int i = 0; i < NR; ++i) v[i] ^= xor_mask;
+    }
+    if (valid != (1u << NR) - 1u) {  // only edge tiles, K tails and padding taps
+#pragma unroll
+      for (int i = 0; i < NR; ++i) v[i] = ((valid >> i) & 1u) ? v[i] : pad;
     }
   }
 };
@@ -146,16 +160,18 @@ struct Im2colNHWC {
   u32x4 pad;           // value of a padding tap (already in the shifted domain)
 
   template <int NR, int kThreads>
-  struct State { const char* img[NR]; int iy0[NR], ix0[NR]; bool ok[NR]; };
+  struct State { const char* img[NR]; int iy0[NR], ix0[NR]; uint32_t okmask; };
 
   template <int NR, int kThreads>
   __device__ __forceinline__ void init(State<NR, kThreads>& s, int row0, int t) const {
     const int ohw = OH * OW;
+    s.okmask = 0;
 #pragma unroll
     for (int i = 0; i < NR; ++i) {
       int r = row0 + (t >> 3) + i * (kThreads / 8);
-      s.ok[i] = r < rows;
-      int rr = s.ok[i] ? r : 0;
+      const bool ok = r < rows;
+      s.okmask |= (ok ? 1u : 0u) << i;
+      int rr = ok ? r : 0;
       int n = rr / ohw, rem = rr - n * ohw;
       int oy = rem / OW, ox = rem - oy * OW;
       s.img[i] = base + (int64_t)n * H * W * cpc * 16;
@@ -164,28 +180,58 @@ struct Im2colNHWC {
     }
   }
   template <int NR, int kThreads>
-  __device__ __forceinline__ void load(const State<NR, kThreads>& s, int kt, int t, u32x4 (&v)[NR]) const {
+  __device__ __forceinline__ uint32_t load(const State<NR, kThreads>& s, int kt, int t, u32x4 (&v)[NR]) const {
     int gk = kt * 8 + (t & 7);
     if (kwrap > 0 && gk >= kwrap) gk -= kwrap;
     const bool kin = gk < kc;
-    const int tap = gk / cpc;
-    const int cc = gk - tap * cpc;
+    const int g = kin ? gk : 0;
+    const int tap = g / cpc;
+    const int cc = g - tap * cpc;
     const int ky = tap / KW;
     const int kx = tap - ky * KW;
     const int dy = ky * dh, dx = kx * dw;
+    uint32_t valid = 0;
 #pragma unroll
     for (int i = 0; i < NR; ++i) {
       const int iy = s.iy0[i] + dy, ix = s.ix0[i] + dx;
-      const bool inside = s.ok[i] && kin && (unsigned)iy < (unsigned)H && (unsigned)ix < (unsigned)W;
-      if (inside) {
-        u32x4 x = *reinterpret_cast<const u32x4*>(s.img[i] + ((int64_t)(iy * W + ix) * cpc + cc) * 16);
-        v[i] = x ^ xor_mask;
-      } else {
-        v[i] = kin ? pad : u32x4{0, 0, 0, 0};
-      }
+      const bool inside = (unsigned)iy < (unsigned)H && (unsigned)ix < (unsigned)W;
+      valid |= (inside ? 1u : 0u) << i;
+      const int64_t off = inside ? ((int64_t)(iy * W + ix) * cpc + cc) * 16 : 0;
+      v[i] = *reinterpret_cast<const u32x4*>(s.img[i] + off);
+    }
+    return kin ? (valid & s.okmask) : 0u;
+  }
+  template <int NR>
+  __device__ __forceinline__ void fix(u32x4 (&v)[NR], uint32_t valid) const {
+    if (xor_mask) {
+#pragma unroll
+      for (int i = 0; i < NR; ++i) v[i] ^= xor_mask;
+    }
+    if (valid != (1u << NR) - 1u) {  // only edge tiles, K tails and padding taps
+#pragma unroll
+      for (int i = 0; i < NR; ++i) v[i] = ((valid >> i) & 1u) ? v[i] : pad;
     }
   }
 };
+
+// Compile-time loop: f(I) for I in [0, N), always fully unrolled.
+template <int I, int N> struct Unroll {
+  template <class F> static __device__ __forceinline__ void run(F& f) {
+    f(I);
+    Unroll<I + 1, N>::run(f);
+  }
+};
+template <int N> struct Unroll<N, N> {
+  template <class F> static __device__ __forceinline__ void run(F&) {}
+};
+
+// LDS slot of 16-byte chunk c (0..7) of staged row r.  Rows are 128 bytes
+// with no padding; the slot is c ^ (r & 7) ^ ((r >> 3) & 1), which keeps
+// every group of 8 consecutive rows on 8 distinct 16-byte bank groups (a
+// 32-bank LDS serving 8 lanes of a b128 access per cycle) and every group of
+// 16 rows on 16 distinct groups (64 banks serving 16 lanes), for both the
+// row-major stores and the MFMA fragment reads (16 rows at one chunk).
+__device__ __forceinline__ int lds_slot(int r, int c) { return c ^ (r & 7) ^ ((r >> 3) & 1); }
 
 // XCD-aware tile order.  The dispatcher hands consecutive workgroup ids to
 // the 8 XCDs in turn; remapping makes each XCD own a contiguous run of
@@ -232,58 +278,72 @@ mfma_gemm_kernel(const LX lx, const LY ly, const Epi epi, int nP, int nQ, int kc
   const int nk = (kc + 7) >> 3;
   const int srow = t >> 3, schunk = t & 7;
 
-  auto stash = [&](int stage) {
+  auto stash = [&](int stage, uint32_t vx, uint32_t vy) {
+    lx.fix(rx, vx);
+    ly.fix(ry, vy);
     u32x4* s = smem + stage * Tl::kStage;
 #pragma unroll
-    for (int i = 0; i < Tl::NX; ++i)
-      s[(srow + i * (Tl::kThreads / 8)) * Tl::kRowStride + schunk] = rx[i];
+    for (int i = 0; i < Tl::NX; ++i) {
+      const int r = srow + i * (Tl::kThreads / 8);
+      s[r * Tl::kRowStride + lds_slot(r, schunk)] = rx[i];
+    }
 #pragma unroll
-    for (int i = 0; i < Tl::NY; ++i)
-      s[(Tl::BP + srow + i * (Tl::kThreads / 8)) * Tl::kRowStride + schunk] = ry[i];
+    for (int i = 0; i < Tl::NY; ++i) {
+      const int r = Tl::BP + srow + i * (Tl::kThreads / 8);
+      s[r * Tl::kRowStride + lds_slot(r, schunk)] = ry[i];
+    }
   };
 
   if (nk > 0) {
-    lx.load(sx, 0, t, rx);
-    ly.load(sy, 0, t, ry);
-    stash(0);
+    const uint32_t vx = lx.load(sx, 0, t, rx);
+    const uint32_t vy = ly.load(sy, 0, t, ry);
+    stash(0, vx, vy);
   }
   __syncthreads();
 
-  const int xrow = (wp * Tl::TP * 16 + (lane & 15)) * Tl::kRowStride + (lane >> 4);
-  const int yrow = (Tl::BP + wq * Tl::TQ * 16 + (lane & 15)) * Tl::kRowStride + (lane >> 4);
+  // Fragment rows of this lane; every 16-row tile starts at a multiple of 16,
+  // so the slot pattern of (lane & 15) is the same for every tile.
+  const int xr = wp * Tl::TP * 16 + (lane & 15);
+  const int yr = Tl::BP + wq * Tl::TQ * 16 + (lane & 15);
+  int xslot[2], yslot[2];
+#pragma unroll
+  for (int kk = 0; kk < 2; ++kk) {
+    xslot[kk] = xr * Tl::kRowStride + lds_slot(xr, kk * 4 + (lane >> 4));
+    yslot[kk] = yr * Tl::kRowStride + lds_slot(yr, kk * 4 + (lane >> 4));
+  }
 
   for (int kt = 0; kt < nk; ++kt) {
     const int cur = kt & 1;
     const bool more = kt + 1 < nk;
+    uint32_t vx = 0, vy = 0;
     if (more) {
-      lx.load(sx, kt + 1, t, rx);
-      ly.load(sy, kt + 1, t, ry);
+      vx = lx.load(sx, kt + 1, t, rx);
+      vy = ly.load(sy, kt + 1, t, ry);
     }
     const u32x4* s = smem + cur * Tl::kStage;
 #pragma unroll
     for (int kk = 0; kk < 2; ++kk) {
       u32x4 fx[Tl::TP], fy[Tl::TQ];
 #pragma unroll
-      for (int a = 0; a < Tl::TP; ++a) fx[a] = s[xrow + a * 16 * Tl::kRowStride + kk * 4];
+      for (int a = 0; a < Tl::TP; ++a) fx[a] = s[xslot[kk] + a * 16 * Tl::kRowStride];
 #pragma unroll
-      for (int b = 0; b < Tl::TQ; ++b) fy[b] = s[yrow + b * 16 * Tl::kRowStride + kk * 4];
+      for (int b = 0; b < Tl::TQ; ++b) fy[b] = s[yslot[kk] + b * 16 * Tl::kRowStride];
 #pragma unroll
       for (int a = 0; a < Tl::TP; ++a)
 #pragma unroll
         for (int b = 0; b < Tl::TQ; ++b) acc[a][b] = OpT<O>::mma(fx[a], fy[b], acc[a][b]);
     }
-    if (more) stash(cur ^ 1);
+    if (more) stash(cur ^ 1, vx, vy);
     __syncthreads();
   }
 
-#pragma unroll
-  for (int a = 0; a < Tl::TP; ++a)
-#pragma unroll
-    for (int b = 0; b < Tl::TQ; ++b) {
-      const int i0 = p0 + wp * Tl::TP * 16 + a * 16 + (lane >> 4) * 4;
-      const int j = q0 + wq * Tl::TQ * 16 + b * 16 + (lane & 15);
-      epi.store(i0, j, acc[a][b]);
-    }
+  const int ibase = p0 + wp * Tl::TP * 16 + (lane >> 4) * 4;
+  const int jbase = q0 + wq * Tl::TQ * 16 + (lane & 15);
+  auto out = [&](int ab) {
+    const int a = ab / Tl::TQ, b = ab % Tl::TQ;
+    epi.store(ibase + a * 16, jbase + b * 16, acc[a][b]);
+  };
+  Unroll<0, Tl::TP * Tl::TQ>::run(out);
 }
 
 }  // namespace ohip

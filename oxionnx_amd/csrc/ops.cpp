@@ -198,10 +198,10 @@ extern "C" int ohip_sync(ohip_ctx* ctx) {
   return OHIP_OK;
 }
 
-extern "C" int ohip_set_tile_override(ohip_ctx* ctx, int tile) {
+extern "C" int ohip_set_tile_override(ohip_ctx* ctx, int tile_id) {
   if (!ctx) return fail(OHIP_E_INVALID, "null context");
-  if (tile != 0 && tile != 64 && tile != 128 && tile != 256) return fail(OHIP_E_INVALID, "tile must be 0/64/128/256");
-  ctx->tile_override = tile;
+  if (tile_id < 0 || tile_id > 8) return fail(OHIP_E_INVALID, "tile id must be 0..8");
+  ctx->tile_override = tile_id;
   return OHIP_OK;
 }
 

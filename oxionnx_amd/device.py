@@ -106,8 +106,9 @@ class HipContext:
     def sync(self):
         L.check(L.lib().ohip_sync(self.h))
 
-    def set_tile(self, tile):
-        L.check(L.lib().ohip_set_tile_override(self.h, tile))
+    def set_tile(self, tile_id):
+        """Force the MFMA block tile by id (include/ohip.h); 0 = automatic."""
+        L.check(L.lib().ohip_set_tile_override(self.h, tile_id))
 
     def tuning(self):
         t = L.Tuning()
