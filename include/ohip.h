@@ -218,6 +218,88 @@ typedef struct {
 int ohip_qconv2d(ohip_ctx* ctx, const ohip_qconv_desc* d, const void* x, const ohip_weight* w,
                  const int32_t* bias_dev, void* y);
 
+/* ------------------------------------------------------------------ device tensors */
+/* A run-scoped device activation (HipDeviceTensor; the DeviceActivation
+ * contract of src/session/gpu_activations.rs:117-189 and
+ * oxionnx-cuda/src/activation.rs).  Layout NCHW means plain row-major in the
+ * ONNX shape; NHWC means channels-last with the channel axis padded to a
+ * multiple of 16 bytes (the conv kernels' native layout). */
+typedef struct ohip_dtensor ohip_dtensor;
+int ohip_dtensor_alloc(ohip_ctx* ctx, int dtype, int rank, const int64_t* shape, int layout, ohip_dtensor** out);
+/* Take ownership of a device buffer of the context (NCHW layout). */
+int ohip_dtensor_wrap(ohip_ctx* ctx, void* dptr, int dtype, int rank, const int64_t* shape, ohip_dtensor** out);
+int ohip_dtensor_upload(ohip_ctx* ctx, ohip_dtensor* t, const void* host);      /* NCHW only */
+int ohip_dtensor_download(ohip_ctx* ctx, const ohip_dtensor* t, void* host);    /* NCHW only, synchronous */
+void* ohip_dtensor_ptr(const ohip_dtensor* t);
+int ohip_dtensor_layout(const ohip_dtensor* t);
+int ohip_dtensor_info(const ohip_dtensor* t, int* dtype, int* rank, int64_t* shape8, size_t* bytes);
+void ohip_dtensor_free(ohip_dtensor* t);
+
+/* ------------------------------------------------------------------ node dispatch */
+/* The drop-in boundary for the session's per-node provider chain
+ * (src/session/run/sequential.rs:614-665 -> dispatch_to_cuda :940-1034):
+ * is_supported_op / accepts_resident_slot / try_cuda_dispatch[_resident]
+ * (oxionnx-cuda/src/lib.rs:217, 419, 354, 561). */
+enum ohip_attr_kind { OHIP_ATTR_INT = 0, OHIP_ATTR_FLOAT = 1, OHIP_ATTR_INTS = 2, OHIP_ATTR_STRING = 3 };
+typedef struct {
+    const char* name;
+    int kind;
+    int64_t i;
+    float f;
+    const int64_t* ints;
+    int n_ints;
+    const char* s;
+} ohip_attr;
+
+/* One node operand: a host tensor (data) or a resident device tensor
+ * (device); both NULL marks an absent optional input.  dtype is the element
+ * type of data -- F32 lanes for the engine's untyped Tensor -- and
+ * declared_dtype the ONNX type a typed run knows (0 = unknown), which pins
+ * the QLinear* saturation range like SatRange::for_dtype. */
+typedef struct {
+    const char* name;
+    int dtype;
+    int declared_dtype;
+    int rank;
+    const int64_t* shape;
+    const void* data;
+    const ohip_dtensor* device;
+    int is_initializer;
+} ohip_tensor;
+
+typedef struct {
+    const char* op_type;
+    const char* name;
+    int n_inputs;
+    const ohip_tensor* inputs;
+    int n_attrs;
+    const ohip_attr* attrs;
+} ohip_node;
+
+enum ohip_placement { OHIP_PLACE_HOST = 0, OHIP_PLACE_DEVICE = 1 };
+
+/* A node result: host data (malloc'd by the library) or a device tensor. */
+typedef struct {
+    int dtype;
+    int rank;
+    int64_t shape[8];
+    void* data;
+    ohip_dtensor* device;
+} ohip_output;
+
+int ohip_is_supported_op(const char* op_type);
+int ohip_accepts_resident_slot(const char* op_type, int index);
+/* OHIP_OK: claimed, *out filled.  OHIP_DECLINED: run the CPU operator.
+ * < 0: failure (the caller logs it and falls back to the CPU). */
+int ohip_try_dispatch(ohip_ctx* ctx, const ohip_node* node, int placement, ohip_output* out);
+void ohip_output_free(ohip_output* out);
+/* Context creation gated by OXIONNX_HIP like CudaContext::try_new
+ * (oxionnx-cuda/src/context.rs:467-481): OHIP_DECLINED when not opted in. */
+int ohip_ctx_try_new(ohip_ctx** out);
+/* Record a decline reason in the counters (used by the dispatcher). */
+void ohip_note_declined(ohip_ctx* ctx, const char* why);
+const char* ohip_last_decline(ohip_ctx* ctx);
+
 /* ------------------------------------------------------------------ counters */
 /* CacheCounters (oxionnx-cuda/src/residency.rs:141-238) plus dispatch counts. */
 typedef struct {

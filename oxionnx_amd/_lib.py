@@ -79,6 +79,30 @@ class QConvDesc(ctypes.Structure):
                 ("out_layout", ctypes.c_int)]
 
 
+class Attr(ctypes.Structure):
+    _fields_ = [("name", ctypes.c_char_p), ("kind", ctypes.c_int), ("i", I64), ("f", ctypes.c_float),
+                ("ints", ctypes.POINTER(I64)), ("n_ints", ctypes.c_int), ("s", ctypes.c_char_p)]
+
+
+class TensorRef(ctypes.Structure):
+    _fields_ = [("name", ctypes.c_char_p), ("dtype", ctypes.c_int), ("declared_dtype", ctypes.c_int),
+                ("rank", ctypes.c_int), ("shape", ctypes.POINTER(I64)), ("data", VP), ("device", VP),
+                ("is_initializer", ctypes.c_int)]
+
+
+class Node(ctypes.Structure):
+    _fields_ = [("op_type", ctypes.c_char_p), ("name", ctypes.c_char_p), ("n_inputs", ctypes.c_int),
+                ("inputs", ctypes.POINTER(TensorRef)), ("n_attrs", ctypes.c_int), ("attrs", ctypes.POINTER(Attr))]
+
+
+class Output(ctypes.Structure):
+    _fields_ = [("dtype", ctypes.c_int), ("rank", ctypes.c_int), ("shape", I64 * 8), ("data", VP), ("device", VP)]
+
+
+ATTR_INT, ATTR_FLOAT, ATTR_INTS, ATTR_STRING = 0, 1, 2, 3
+PLACE_HOST, PLACE_DEVICE = 0, 1
+
+
 class Counters(ctypes.Structure):
     _fields_ = [(f, ctypes.c_uint64) for f in (
         "weight_hits", "weight_misses", "weight_transient", "weight_uploaded_bytes", "weight_resident_bytes",
@@ -126,6 +150,23 @@ SIGNATURES = {
     "ohip_get_counters": (ctypes.c_int, [VP, ctypes.POINTER(Counters)]),
     "ohip_reset_counters": (ctypes.c_int, [VP]),
     "ohip_set_tile_override": (ctypes.c_int, [VP, ctypes.c_int]),
+    "ohip_dtensor_alloc": (ctypes.c_int, [VP, ctypes.c_int, ctypes.c_int, ctypes.POINTER(I64), ctypes.c_int,
+                                          ctypes.POINTER(VP)]),
+    "ohip_dtensor_wrap": (ctypes.c_int, [VP, VP, ctypes.c_int, ctypes.c_int, ctypes.POINTER(I64), ctypes.POINTER(VP)]),
+    "ohip_dtensor_upload": (ctypes.c_int, [VP, VP, VP]),
+    "ohip_dtensor_download": (ctypes.c_int, [VP, VP, VP]),
+    "ohip_dtensor_ptr": (VP, [VP]),
+    "ohip_dtensor_layout": (ctypes.c_int, [VP]),
+    "ohip_dtensor_info": (ctypes.c_int, [VP, ctypes.POINTER(ctypes.c_int), ctypes.POINTER(ctypes.c_int),
+                                         ctypes.POINTER(I64), ctypes.POINTER(ctypes.c_size_t)]),
+    "ohip_dtensor_free": (None, [VP]),
+    "ohip_is_supported_op": (ctypes.c_int, [ctypes.c_char_p]),
+    "ohip_accepts_resident_slot": (ctypes.c_int, [ctypes.c_char_p, ctypes.c_int]),
+    "ohip_try_dispatch": (ctypes.c_int, [VP, ctypes.POINTER(Node), ctypes.c_int, ctypes.POINTER(Output)]),
+    "ohip_output_free": (None, [ctypes.POINTER(Output)]),
+    "ohip_ctx_try_new": (ctypes.c_int, [ctypes.POINTER(VP)]),
+    "ohip_note_declined": (None, [VP, ctypes.c_char_p]),
+    "ohip_last_decline": (ctypes.c_char_p, [VP]),
 }
 
 _lib = None

@@ -20,7 +20,7 @@ LIB = os.path.join(HERE, "libohip.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 
-SOURCES = ["contract_f32.hip", "contract_f16.hip", "contract_bf16.hip", "contract_i8.hip", "aux_kernels.hip", "ops.cpp"]
+SOURCES = ["contract_f32.hip", "contract_f16.hip", "contract_bf16.hip", "contract_i8.hip", "aux_kernels.hip", "ops.cpp", "dispatch.cpp"]
 
 FLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-ffp-contract=off",
@@ -30,8 +30,17 @@ FLAGS = [
 ]
 
 
-def _compile(src):
+def _compile(src, incremental=False):
     obj = os.path.join(OUT_DIR, os.path.splitext(src)[0] + ".o")
+    if incremental and os.path.exists(obj):
+        kern = ["mfma_core.hpp", "launch.hpp", "internal.hpp"]
+        local = {"ops.cpp": ["internal.hpp"], "dispatch.cpp": ["internal.hpp"],
+                 "aux_kernels.hip": kern}.get(src, kern + ["contract.inc"])
+        deps = [os.path.join(CSRC, f) for f in [src] + local]
+        if src.endswith(".cpp"):
+            deps.append(os.path.join(ROOT, "include", "ohip.h"))
+        if all(os.path.getmtime(d) <= os.path.getmtime(obj) for d in deps):
+            return obj
     lang = [] if src.endswith(".hip") else ["-x", "hip"]
     cmd = [HIPCC] + FLAGS + lang + ["-c", os.path.join(CSRC, src), "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
@@ -40,10 +49,13 @@ def _compile(src):
     return obj
 
 
-def build(verbose=True):
+def build(verbose=True, incremental=False):
+    """Compile every source (incremental=True skips objects newer than every
+    source and header -- a development shortcut; the driver's build() always
+    compiles everything)."""
     os.makedirs(OUT_DIR, exist_ok=True)
     with cf.ThreadPoolExecutor(max_workers=min(8, len(SOURCES))) as ex:
-        objs = list(ex.map(_compile, SOURCES))
+        objs = list(ex.map(lambda s: _compile(s, incremental), SOURCES))
     cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", LIB] + objs
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
@@ -54,5 +66,5 @@ def build(verbose=True):
 
 
 if __name__ == "__main__":
-    build()
+    build(incremental="--incremental" in sys.argv)
     sys.exit(0)

@@ -1,0 +1,657 @@
+// Node-level dispatch: the provider's counterpart of oxionnx-cuda's
+// try_cuda_dispatch / try_cuda_dispatch_resident (oxionnx-cuda/src/lib.rs:354-960).
+// A node arrives with its ONNX op type, attributes and operands (host tensors
+// or resident device tensors); the provider either claims it (OHIP_OK, outputs
+// returned on the host or kept on the device), declines it (OHIP_DECLINED: the
+// caller runs its CPU operator, which also reports malformed-model errors), or
+// fails (< 0).
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdlib>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "../../include/ohip.h"
+#include "internal.hpp"
+
+namespace {
+
+thread_local std::string t_err;
+
+int decline(const std::string& why) {
+  t_err = why;
+  return OHIP_DECLINED;
+}
+
+// ------------------------------------------------------------------ attributes
+const ohip_attr* find_attr(const ohip_node* n, const char* name) {
+  for (int i = 0; i < n->n_attrs; ++i)
+    if (n->attrs[i].name && std::strcmp(n->attrs[i].name, name) == 0) return &n->attrs[i];
+  return nullptr;
+}
+int64_t attr_i(const ohip_node* n, const char* name, int64_t dflt) {
+  const ohip_attr* a = find_attr(n, name);
+  return a && a->kind == OHIP_ATTR_INT ? a->i : dflt;
+}
+float attr_f(const ohip_node* n, const char* name, float dflt) {
+  const ohip_attr* a = find_attr(n, name);
+  if (!a) return dflt;
+  if (a->kind == OHIP_ATTR_FLOAT) return a->f;
+  if (a->kind == OHIP_ATTR_INT) return (float)a->i;
+  return dflt;
+}
+std::vector<int64_t> attr_ints(const ohip_node* n, const char* name) {
+  const ohip_attr* a = find_attr(n, name);
+  if (!a || a->kind != OHIP_ATTR_INTS || !a->ints) return {};
+  return std::vector<int64_t>(a->ints, a->ints + a->n_ints);
+}
+std::string attr_s(const ohip_node* n, const char* name) {
+  const ohip_attr* a = find_attr(n, name);
+  return a && a->kind == OHIP_ATTR_STRING && a->s ? std::string(a->s) : std::string();
+}
+
+// ------------------------------------------------------------------ operands
+const ohip_tensor* input(const ohip_node* n, int i) {
+  if (i >= n->n_inputs) return nullptr;
+  const ohip_tensor* t = &n->inputs[i];
+  if (!t->data && !t->device) return nullptr;  // an absent optional input
+  return t;
+}
+int64_t numel(const ohip_tensor* t) {
+  int64_t e = 1;
+  for (int i = 0; i < t->rank; ++i) e *= t->shape[i];
+  return e;
+}
+int ebytes(int dt) {
+  switch (dt) {
+    case OHIP_F32: case OHIP_I32: return 4;
+    case OHIP_F16: case OHIP_BF16: return 2;
+    case OHIP_U8: case OHIP_I8: return 1;
+    default: return 0;
+  }
+}
+bool host_only(const ohip_tensor* t) { return t && t->data; }
+
+// Element i of a host tensor as double (integers exact).
+double host_at(const ohip_tensor* t, int64_t i) {
+  switch (t->dtype) {
+    case OHIP_F32: return static_cast<const float*>(t->data)[i];
+    case OHIP_I32: return static_cast<const int32_t*>(t->data)[i];
+    case OHIP_U8: return static_cast<const uint8_t*>(t->data)[i];
+    case OHIP_I8: return static_cast<const int8_t*>(t->data)[i];
+    case OHIP_F16: {
+      uint16_t h = static_cast<const uint16_t*>(t->data)[i];
+      // exact f16 -> f32 widening
+      uint32_t s = (uint32_t)(h & 0x8000u) << 16, e = (h >> 10) & 0x1f, m = h & 0x3ff, x;
+      if (e == 0) {
+        if (!m) x = s;
+        else {
+          int k = -1;
+          do { m <<= 1; ++k; } while (!(m & 0x400u));
+          x = s | ((uint32_t)(112 - k) << 23) | ((m & 0x3ffu) << 13);
+        }
+      } else if (e == 31) x = s | 0x7f800000u | (m << 13);
+      else x = s | ((e + 112) << 23) | (m << 13);
+      float f;
+      std::memcpy(&f, &x, 4);
+      return f;
+    }
+    case OHIP_BF16: {
+      uint32_t x = (uint32_t) static_cast<const uint16_t*>(t->data)[i] << 16;
+      float f;
+      std::memcpy(&f, &x, 4);
+      return f;
+    }
+    default: return NAN;
+  }
+}
+
+// Store v as element idx of a dtype buffer (f16 / bf16 round to nearest even).
+void put_elem(int dt, void* buf, int64_t idx, double v) {
+  const float f = (float)v;
+  if (dt == OHIP_F32) {
+    std::memcpy(static_cast<char*>(buf) + idx * 4, &f, 4);
+  } else if (dt == OHIP_F16) {
+    const _Float16 h = (_Float16)f;
+    std::memcpy(static_cast<char*>(buf) + idx * 2, &h, 2);
+  } else if (dt == OHIP_BF16) {
+    uint32_t u;
+    std::memcpy(&u, &f, 4);
+    const uint16_t h = (uint16_t)(((u & 0x7fffffffu) > 0x7f800000u) ? ((u >> 16) | 0x40u)
+                                                                     : ((u + 0x7fffu + ((u >> 16) & 1u)) >> 16));
+    std::memcpy(static_cast<char*>(buf) + idx * 2, &h, 2);
+  }
+}
+
+// round half to even, the lane_to_i32 rule (quant_ops/mod.rs:74-92)
+bool lane_int(double v, int32_t* out) {
+  if (!std::isfinite(v)) return false;
+  double r = std::nearbyint(v);
+  if (r < INT32_MIN || r > INT32_MAX) return false;
+  *out = (int32_t)r;
+  return true;
+}
+
+// Quantised lanes -> bytes.  Picks u8 when every lane is in 0..255, else i8
+// when every lane is in -128..127; anything else is declined.
+bool to_bytes(const ohip_tensor* t, std::vector<uint8_t>& out, int* dt) {
+  const int64_t n = numel(t);
+  out.resize((size_t)n);
+  if (t->dtype == OHIP_U8 || t->dtype == OHIP_I8) {
+    std::memcpy(out.data(), t->data, (size_t)n);
+    *dt = t->dtype;
+    return true;
+  }
+  int32_t lo = INT32_MAX, hi = INT32_MIN;
+  std::vector<int32_t> v((size_t)n);
+  for (int64_t i = 0; i < n; ++i) {
+    if (!lane_int(host_at(t, i), &v[(size_t)i])) return false;
+    lo = std::min(lo, v[(size_t)i]);
+    hi = std::max(hi, v[(size_t)i]);
+  }
+  if (n == 0) lo = hi = 0;
+  if (lo >= 0 && hi <= 255) *dt = OHIP_U8;
+  else if (lo >= -128 && hi <= 127) *dt = OHIP_I8;
+  else return false;
+  for (int64_t i = 0; i < n; ++i) out[(size_t)i] = (uint8_t)(v[(size_t)i] & 0xff);
+  return true;
+}
+
+// zero_point_lanes (quant_ops/mod.rs:121-127): absent or empty -> [0].
+bool zp_lanes(const ohip_tensor* t, std::vector<int32_t>& out) {
+  out.clear();
+  if (!t || numel(t) == 0) {
+    out.push_back(0);
+    return true;
+  }
+  if (!host_only(t)) return false;
+  for (int64_t i = 0; i < numel(t); ++i) {
+    int32_t v;
+    if (!lane_int(host_at(t, i), &v)) return false;
+    out.push_back(v);
+  }
+  return true;
+}
+
+// scale_input (quant_ops/mod.rs:100-118): first element, finite, non-zero.
+bool scale_first(const ohip_tensor* t, float* s) {
+  if (!host_only(t) || numel(t) == 0) return false;
+  double v = host_at(t, 0);
+  if (!std::isfinite(v) || v == 0.0) return false;
+  *s = (float)v;
+  return true;
+}
+
+// SatRange::infer / for_dtype (quant_ops/mod.rs:188-221).
+void sat_range(const ohip_tensor* yzp_t, const std::vector<int32_t>& yzp, const std::vector<int32_t>& xzp,
+               int32_t* lo, int32_t* hi) {
+  if (yzp_t && yzp_t->declared_dtype == OHIP_U8) { *lo = 0; *hi = 255; return; }
+  if (yzp_t && yzp_t->declared_dtype == OHIP_I8) { *lo = -128; *hi = 127; return; }
+  for (const auto* lanes : {&yzp, &xzp}) {
+    for (int32_t v : *lanes) if (v > 127) { *lo = 0; *hi = 255; return; }
+    for (int32_t v : *lanes) if (v < 0) { *lo = -128; *hi = 127; return; }
+  }
+  *lo = -128;
+  *hi = 255;
+}
+
+// ------------------------------------------------------------------ staging
+struct Stage {
+  ohip_ctx* ctx;
+  std::vector<void*> bufs;
+  explicit Stage(ohip_ctx* c) : ctx(c) {}
+  ~Stage() {
+    for (void* p : bufs) ohip_free(ctx, p);
+  }
+  void* alloc(size_t bytes) {
+    void* p = nullptr;
+    if (ohip_malloc(ctx, bytes ? bytes : 16, &p) != OHIP_OK) return nullptr;
+    bufs.push_back(p);
+    return p;
+  }
+  // A device copy of a host tensor (or the resident pointer itself).
+  const void* operand(const ohip_tensor* t, const void* host_override = nullptr, size_t bytes = 0) {
+    if (t->device && !host_override) return ohip_dtensor_ptr(t->device);
+    const void* src = host_override ? host_override : t->data;
+    size_t nb = host_override ? bytes : (size_t)numel(t) * ebytes(t->dtype);
+    void* d = alloc(nb);
+    if (!d || ohip_memcpy_h2d(ctx, d, src, nb) != OHIP_OK) return nullptr;
+    return d;
+  }
+};
+
+void set_out(ohip_output* o, int dtype, const std::vector<int64_t>& shape) {
+  std::memset(o, 0, sizeof(*o));
+  o->dtype = dtype;
+  o->rank = (int)shape.size();
+  for (size_t i = 0; i < shape.size() && i < 8; ++i) o->shape[i] = shape[i];
+}
+
+int finish_output(ohip_ctx* ctx, Stage& st, int placement, ohip_output* o, void* dev, size_t bytes, int dev_dtype) {
+  if (placement == OHIP_PLACE_DEVICE) {
+    ohip_dtensor* t = nullptr;
+    int rc = ohip_dtensor_wrap(ctx, dev, dev_dtype, o->rank, o->shape, &t);
+    if (rc) return rc;
+    st.bufs.erase(std::remove(st.bufs.begin(), st.bufs.end(), dev), st.bufs.end());  // now owned by t
+    o->device = t;
+    return OHIP_OK;
+  }
+  o->data = std::malloc(bytes ? bytes : 1);
+  if (!o->data) return OHIP_E_NOMEM;
+  return ohip_memcpy_d2h(ctx, o->data, dev, bytes);
+}
+
+// ------------------------------------------------------------------ Conv geometry
+struct Geo {
+  int64_t n, c, h, w, cout, kh, kw, group;
+  int64_t sh, sw, dh, dw, pt, pl, pb, pr, oh, ow;
+  bool rank1;
+};
+
+// ConvGeometry::from_attrs (registry/conv_ops/conv.rs:38-121) and
+// resolve_pads / same_pad_split (conv/spatial.rs:204-257), rank 1 and 2.
+bool conv_geometry(const ohip_node* nd, const ohip_tensor* x, const ohip_tensor* w, Geo* g, std::string* why) {
+  if (x->rank != w->rank || (x->rank != 3 && x->rank != 4)) { *why = "Conv: only rank 1 and 2 spatial"; return false; }
+  g->rank1 = x->rank == 3;
+  g->n = x->shape[0];
+  g->c = x->shape[1];
+  g->h = g->rank1 ? 1 : x->shape[2];
+  g->w = x->shape[x->rank - 1];
+  g->cout = w->shape[0];
+  g->kh = g->rank1 ? 1 : w->shape[2];
+  g->kw = w->shape[w->rank - 1];
+  g->group = attr_i(nd, "group", 1);
+  if (g->group <= 0 || w->shape[1] * g->group != g->c || g->cout % g->group) { *why = "Conv: bad group"; return false; }
+  const int sr = g->rank1 ? 1 : 2;
+  auto strides = attr_ints(nd, "strides"), dil = attr_ints(nd, "dilations"), pads = attr_ints(nd, "pads");
+  auto ks = attr_ints(nd, "kernel_shape");
+  if (!ks.empty()) {
+    if ((int)ks.size() != sr || ks.back() != g->kw || (sr == 2 && ks[0] != g->kh)) {
+      *why = "Conv: kernel_shape disagrees with W";
+      return false;
+    }
+  }
+  if (strides.empty()) strides.assign(sr, 1);
+  if (dil.empty()) dil.assign(sr, 1);
+  if (pads.empty()) pads.assign(2 * sr, 0);
+  if ((int)strides.size() != sr || (int)dil.size() != sr || (int)pads.size() != 2 * sr) {
+    *why = "Conv: attribute rank mismatch";
+    return false;
+  }
+  for (auto v : strides) if (v <= 0) { *why = "Conv: stride"; return false; }
+  for (auto v : dil) if (v <= 0) { *why = "Conv: dilation"; return false; }
+  for (auto v : pads) if (v < 0) { *why = "Conv: negative pad"; return false; }
+  g->sh = sr == 2 ? strides[0] : 1;
+  g->sw = strides.back();
+  g->dh = sr == 2 ? dil[0] : 1;
+  g->dw = dil.back();
+  int64_t pt = sr == 2 ? pads[0] : 0, pl = sr == 2 ? pads[1] : pads[0];
+  int64_t pb = sr == 2 ? pads[2] : 0, pr = sr == 2 ? pads[3] : pads[1];
+  std::string ap = attr_s(nd, "auto_pad");
+  if (ap == "VALID") pt = pl = pb = pr = 0;
+  else if (ap == "SAME_UPPER" || ap == "SAME_LOWER") {
+    auto split = [&](int64_t in, int64_t k, int64_t s, int64_t d, int64_t* b, int64_t* e) {
+      int64_t out = (in + s - 1) / s, eff = (k - 1) * d + 1;
+      int64_t need = std::max<int64_t>(0, (out - 1) * s + eff - in), half = need / 2;
+      if (ap == "SAME_LOWER") { *b = need - half; *e = half; } else { *b = half; *e = need - half; }
+    };
+    if (sr == 2) split(g->h, g->kh, g->sh, g->dh, &pt, &pb);
+    split(g->w, g->kw, g->sw, g->dw, &pl, &pr);
+  } else if (!(ap.empty() || ap == "NOTSET")) {
+    *why = "Conv: unknown auto_pad";
+    return false;
+  }
+  g->pt = pt; g->pl = pl; g->pb = pb; g->pr = pr;
+  g->oh = ohip_conv_out_dim(g->h, pt, pb, g->kh, g->dh, g->sh);
+  g->ow = ohip_conv_out_dim(g->w, pl, pr, g->kw, g->dw, g->sw);
+  if (g->oh < 0 || g->ow < 0) { *why = "Conv: output extent"; return false; }
+  return true;
+}
+
+std::vector<int64_t> conv_out_shape(const Geo& g) {
+  if (g.rank1) return {g.n, g.cout, g.ow};
+  return {g.n, g.cout, g.oh, g.ow};
+}
+
+// apply_fused_activation's attribute contract (registry/conv_ops/conv.rs:124-156).
+void fused_act(const ohip_node* nd, int* act, float* lo, float* hi) {
+  std::string a = attr_s(nd, "activation");
+  *act = OHIP_ACT_NONE;
+  *lo = 0.0f;
+  *hi = 0.0f;
+  if (a == "relu") *act = OHIP_ACT_RELU;
+  else if (a == "clip") {
+    *act = OHIP_ACT_CLIP;
+    *lo = attr_f(nd, "activation_min", -INFINITY);
+    *hi = attr_f(nd, "activation_max", INFINITY);
+  }
+}
+
+std::string wkey_name(const ohip_tensor* t) { return t->name ? std::string(t->name) : std::string(); }
+
+// ------------------------------------------------------------------ float Conv
+int do_conv(ohip_ctx* ctx, const ohip_node* nd, int placement, ohip_output* out) {
+  const ohip_tensor *x = input(nd, 0), *w = input(nd, 1), *b = input(nd, 2);
+  if (!x || !w) return decline("Conv: missing input");
+  if (!host_only(w) || (b && !host_only(b))) return decline("Conv: filter / bias must be host tensors");
+  const int dt = x->dtype;
+  if (dt != OHIP_F32 && dt != OHIP_F16 && dt != OHIP_BF16) return decline("Conv: dtype");
+  Geo g;
+  std::string why;
+  if (!conv_geometry(nd, x, w, &g, &why)) return decline(why);
+  if (g.group != 1) return decline("Conv: group != 1");
+  ohip_tuning tun;
+  ohip_get_tuning(ctx, &tun);
+  if (!ohip_conv_admits(&tun, g.cout, g.c * g.kh * g.kw, g.n * g.oh * g.ow)) return decline("Conv: below conv_min_mac");
+  if (x->device && ohip_dtensor_layout(x->device) != OHIP_NCHW) return decline("Conv: resident input layout");
+
+  std::string name = wkey_name(w), label = "Conv.W";
+  ohip_weight_key key{name.c_str(), label.c_str()};
+  const bool cache = w->is_initializer && !name.empty();
+  ohip_weight* wt = nullptr;
+  int rc = ohip_weight_conv(ctx, cache ? &key : nullptr, w->dtype, w->data, g.cout, g.c, g.kh, g.kw, dt, &wt);
+  if (rc) return rc;
+  Stage st(ctx);
+  const void* xd = st.operand(x);
+  const void* bd = nullptr;
+  std::vector<char> bconv;
+  if (b) {
+    if (numel(b) != g.cout) {
+      if (!cache) ohip_weight_release(wt);
+      return decline("Conv: bias length");
+    }
+    if (b->dtype != dt) {  // e.g. f32 bias lanes on a typed conv: round once (RNE)
+      bconv.resize((size_t)g.cout * ebytes(dt));
+      for (int64_t i = 0; i < g.cout; ++i) put_elem(dt, bconv.data(), i, host_at(b, i));
+      bd = st.operand(b, bconv.data(), bconv.size());
+    } else {
+      bd = st.operand(b);
+    }
+  }
+  const auto oshape = conv_out_shape(g);
+  const size_t obytes = (size_t)(g.n * g.cout * g.oh * g.ow) * ebytes(dt);
+  void* yd = st.alloc(obytes);
+  if (!xd || !yd || (b && !bd)) { if (!cache) ohip_weight_release(wt); return OHIP_E_NOMEM; }
+  ohip_conv_desc d{g.n, g.c, g.h, g.w, g.cout, g.kh, g.kw, 1, g.sh, g.sw, g.dh, g.dw, g.pt, g.pl, g.pb, g.pr,
+                   dt, OHIP_NCHW, OHIP_NCHW, 0, 0.0f, 0.0f};
+  fused_act(nd, &d.act, &d.act_lo, &d.act_hi);
+  rc = ohip_conv2d(ctx, &d, xd, wt, bd, yd);
+  if (!cache) ohip_weight_release(wt);
+  if (rc) return rc;
+  set_out(out, dt, oshape);
+  return finish_output(ctx, st, placement, out, yd, obytes, dt);
+}
+
+// ------------------------------------------------------------------ Gemm / MatMul
+int do_gemm(ohip_ctx* ctx, const ohip_node* nd, bool is_matmul, int placement, ohip_output* out) {
+  const ohip_tensor *a = input(nd, 0), *b = input(nd, 1), *c = is_matmul ? nullptr : input(nd, 2);
+  if (!a || !b) return decline("Gemm: missing input");
+  if (!host_only(b) || (c && !host_only(c))) return decline("Gemm: B / C must be host tensors");
+  const int dt = a->dtype;
+  if (dt != OHIP_F32 && dt != OHIP_F16 && dt != OHIP_BF16) return decline("Gemm: dtype");
+  float alpha = 1.0f, beta = 1.0f;
+  int ta = 0, tb = 0;
+  int64_t m, k, n;
+  std::vector<int64_t> oshape;
+  if (is_matmul) {
+    // matmul_f32_into (math_typed.rs:334-423) with a shared 2-D (or 1-D) B
+    // collapses the batch into M (oxionnx-cuda/src/matmul.rs:189-252).
+    if (b->rank == 1) { k = b->shape[0]; n = 1; }
+    else if (b->rank == 2) { k = b->shape[0]; n = b->shape[1]; }
+    else return decline("MatMul: batched B");
+    if (a->rank == 1) { m = 1; if (a->shape[0] != k) return decline("MatMul: K"); }
+    else {
+      if (a->shape[a->rank - 1] != k) return decline("MatMul: K");
+      m = 1;
+      for (int i = 0; i < a->rank - 1; ++i) m *= a->shape[i];
+    }
+    for (int i = 0; i + 1 < a->rank; ++i) oshape.push_back(a->shape[i]);
+    if (b->rank == 2) oshape.push_back(n);
+  } else {
+    // GemmOp (registry/math_ops/matmul_gemm.rs:130-170)
+    if (a->rank != 2 || b->rank != 2) return decline("Gemm: rank");
+    alpha = attr_f(nd, "alpha", 1.0f);
+    beta = attr_f(nd, "beta", 1.0f);
+    ta = (int)attr_i(nd, "transA", 0);
+    tb = (int)attr_i(nd, "transB", 0);
+    m = ta ? a->shape[1] : a->shape[0];
+    k = ta ? a->shape[0] : a->shape[1];
+    int64_t kb = tb ? b->shape[1] : b->shape[0];
+    n = tb ? b->shape[0] : b->shape[1];
+    if (k != kb) return decline("Gemm: K");
+    oshape = {m, n};
+  }
+  if (m == 0 || n == 0 || k == 0) return decline("Gemm: empty");
+  ohip_tuning tun;
+  ohip_get_tuning(ctx, &tun);
+  const bool cache = b->is_initializer && b->name && *b->name;
+  if (!ohip_gemm_admits(&tun, m, k, n, cache)) return decline("Gemm: gate");
+  std::string name = wkey_name(b), label = std::string(is_matmul ? "MatMul.B" : "Gemm.B");
+  ohip_weight_key key{name.c_str(), label.c_str()};
+  ohip_weight* wt = nullptr;
+  int rc = ohip_weight_gemm(ctx, cache ? &key : nullptr, b->dtype, b->data, k, n, tb, dt, &wt);
+  if (rc) return rc;
+  Stage st(ctx);
+  const void* ad = st.operand(a);
+  // C: scalar, [n] / [1,n] row, [m,n] full; any other broadcast is expanded on the host
+  int c_kind = OHIP_C_NONE;
+  const void* cd = nullptr;
+  std::vector<char> cbuf;
+  if (c) {
+    const int64_t ce = numel(c);
+    const int64_t eb = ebytes(dt);
+    int64_t cr = 1, cc = 1;
+    if (c->rank >= 1) cc = c->shape[c->rank - 1];
+    if (c->rank >= 2) cr = c->shape[c->rank - 2];
+    if ((cr != 1 && cr != m) || (cc != 1 && cc != n) || ce != cr * cc) { ohip_weight_release(wt); return decline("Gemm: C shape"); }
+    if (ce == 1) c_kind = OHIP_C_SCALAR;
+    else if (cr == 1 && cc == n) c_kind = OHIP_C_ROW;
+    else c_kind = OHIP_C_FULL;
+    const int64_t len = c_kind == OHIP_C_SCALAR ? 1 : c_kind == OHIP_C_ROW ? n : m * n;
+    cbuf.resize((size_t)(len * eb));
+    for (int64_t i = 0; i < len; ++i) {
+      int64_t r = c_kind == OHIP_C_FULL ? i / n : 0, col = c_kind == OHIP_C_SCALAR ? 0 : i % n;
+      put_elem(dt, cbuf.data(), i, host_at(c, (cr == 1 ? 0 : r) * cc + (cc == 1 ? 0 : col)));
+    }
+    cd = st.operand(c, cbuf.data(), cbuf.size());
+  }
+  const size_t obytes = (size_t)(m * n) * ebytes(dt);
+  void* yd = st.alloc(obytes);
+  if (!ad || !yd || (c && !cd)) { if (!cache) ohip_weight_release(wt); return OHIP_E_NOMEM; }
+  ohip_gemm_desc d{m, k, n, dt, ta, alpha, beta, c_kind, OHIP_ACT_NONE, 0.0f, 0.0f, 0, 0};
+  rc = ohip_gemm(ctx, &d, ad, wt, cd, yd);
+  if (!cache) ohip_weight_release(wt);
+  if (rc) return rc;
+  set_out(out, dt, oshape);
+  return finish_output(ctx, st, placement, out, yd, obytes, dt);
+}
+
+// ------------------------------------------------------------------ integer MatMul
+int do_qmatmul(ohip_ctx* ctx, const ohip_node* nd, bool qlinear, int placement, ohip_output* out) {
+  // QLinearMatMul: a, a_scale, a_zp, b, b_scale, b_zp, y_scale, y_zp
+  // MatMulInteger: a, b, a_zp, b_zp
+  const ohip_tensor* a = input(nd, 0);
+  const ohip_tensor* b = input(nd, qlinear ? 3 : 1);
+  const ohip_tensor* azp_t = input(nd, qlinear ? 2 : 2);
+  const ohip_tensor* bzp_t = input(nd, qlinear ? 5 : 3);
+  if (!a || !b || !host_only(a) || !host_only(b)) return decline("integer MatMul: operands must be host tensors");
+  if (b->rank != 2 || a->rank < 1) return decline("integer MatMul: B must be 2-D");
+  const int64_t k = b->shape[0], n = b->shape[1];
+  if (a->shape[a->rank - 1] != k) return decline("integer MatMul: K");
+  int64_t m = 1;
+  for (int i = 0; i + 1 < a->rank; ++i) m *= a->shape[i];
+  if (m == 0 || n == 0 || k == 0) return decline("integer MatMul: empty");
+  std::vector<int32_t> azp, bzp, yzp;
+  if (!zp_lanes(azp_t, azp) || !zp_lanes(bzp_t, bzp)) return decline("integer MatMul: zero point");
+  if (azp.size() != 1 && (int64_t)azp.size() != m) return decline("integer MatMul: a_zero_point length");
+  if (bzp.size() != 1 && (int64_t)bzp.size() != n) return decline("integer MatMul: b_zero_point length");
+  float as = 1.0f, bs = 1.0f, ys = 1.0f;
+  int32_t lo = 0, hi = 0;
+  const ohip_tensor* yzp_t = nullptr;
+  if (qlinear) {
+    yzp_t = input(nd, 7);
+    if (!scale_first(input(nd, 1), &as) || !scale_first(input(nd, 4), &bs) || !scale_first(input(nd, 6), &ys))
+      return decline("QLinearMatMul: scale");
+    if (!zp_lanes(yzp_t, yzp)) return decline("QLinearMatMul: y_zero_point");
+    sat_range(yzp_t, yzp, azp, &lo, &hi);
+  }
+  ohip_tuning tun;
+  ohip_get_tuning(ctx, &tun);
+  const bool cache = b->is_initializer && b->name && *b->name;
+  if (!ohip_gemm_admits(&tun, m, k, n, cache)) return decline("integer MatMul: gate");
+  std::vector<uint8_t> abytes, bbytes;
+  int adt, bdt;
+  if (!to_bytes(a, abytes, &adt) || !to_bytes(b, bbytes, &bdt)) return decline("integer MatMul: lanes outside 8 bits");
+  std::string name = wkey_name(b), label = std::string(qlinear ? "QLinearMatMul.B" : "MatMulInteger.B");
+  ohip_weight_key key{name.c_str(), label.c_str()};
+  ohip_weight* wt = nullptr;
+  // only b_scale[0] is read, exactly like the reference's scale_input
+  int rc = ohip_weight_qgemm(ctx, cache ? &key : nullptr, bdt, bbytes.data(), k, n, 0, bzp.data(), (int)bzp.size(),
+                             qlinear ? &bs : nullptr, qlinear ? 1 : 0, &wt);
+  if (rc) return rc;
+  Stage st(ctx);
+  const void* ad = st.operand(a, abytes.data(), abytes.size());
+  const size_t obytes = (size_t)(m * n) * 4;
+  void* yd = st.alloc(obytes);
+  if (!ad || !yd) { if (!cache) ohip_weight_release(wt); return OHIP_E_NOMEM; }
+  ohip_qgemm_desc d{m, k, n, adt, azp.data(), (int)azp.size(), qlinear ? OHIP_QOUT_F32 : OHIP_QOUT_I32,
+                    as, ys, qlinear ? yzp[0] : 0, lo, hi, 0, 0};
+  rc = ohip_qgemm(ctx, &d, ad, wt, yd);
+  if (!cache) ohip_weight_release(wt);
+  if (rc) return rc;
+  std::vector<int64_t> oshape;
+  for (int i = 0; i + 1 < a->rank; ++i) oshape.push_back(a->shape[i]);
+  oshape.push_back(n);
+  set_out(out, qlinear ? OHIP_F32 : OHIP_I32, oshape);
+  return finish_output(ctx, st, placement, out, yd, obytes, qlinear ? OHIP_F32 : OHIP_I32);
+}
+
+// ------------------------------------------------------------------ integer Conv
+int do_qconv(ohip_ctx* ctx, const ohip_node* nd, bool qlinear, int placement, ohip_output* out) {
+  // QLinearConv: x, x_scale, x_zp, w, w_scale, w_zp, y_scale, y_zp, B
+  // ConvInteger: x, w, x_zp, w_zp
+  const ohip_tensor* x = input(nd, 0);
+  const ohip_tensor* w = input(nd, qlinear ? 3 : 1);
+  const ohip_tensor* xzp_t = input(nd, 2);
+  const ohip_tensor* wzp_t = input(nd, qlinear ? 5 : 3);
+  const ohip_tensor* bias = qlinear ? input(nd, 8) : nullptr;
+  if (!x || !w || !host_only(x) || !host_only(w)) return decline("integer Conv: operands must be host tensors");
+  Geo g;
+  std::string why;
+  if (!conv_geometry(nd, x, w, &g, &why)) return decline(why);
+  if (g.group != 1) return decline("integer Conv: group != 1");
+  std::vector<int32_t> xzp, wzp, yzp;
+  if (!zp_lanes(xzp_t, xzp) || !zp_lanes(wzp_t, wzp)) return decline("integer Conv: zero point");
+  if (wzp.size() != 1 && (int64_t)wzp.size() != g.cout) return decline("integer Conv: w_zero_point length");
+  float xs = 1.0f, ys = 1.0f;
+  std::vector<float> ws;
+  int32_t lo = 0, hi = 0;
+  const ohip_tensor* yzp_t = nullptr;
+  if (qlinear) {
+    yzp_t = input(nd, 7);
+    const ohip_tensor* ws_t = input(nd, 4);
+    if (!scale_first(input(nd, 1), &xs) || !scale_first(input(nd, 6), &ys) || !host_only(ws_t) || numel(ws_t) == 0)
+      return decline("QLinearConv: scale");
+    if (numel(ws_t) != 1 && numel(ws_t) != g.cout) return decline("QLinearConv: w_scale length");
+    for (int64_t i = 0; i < numel(ws_t); ++i) {
+      double v = host_at(ws_t, i);
+      if (!std::isfinite(v)) return decline("QLinearConv: w_scale");
+      ws.push_back((float)v);
+    }
+    if (!zp_lanes(yzp_t, yzp)) return decline("QLinearConv: y_zero_point");
+    std::vector<int32_t> x0{xzp[0]};
+    sat_range(yzp_t, yzp, x0, &lo, &hi);
+  }
+  std::vector<int32_t> bias_i;
+  if (bias) {
+    if (!host_only(bias) || numel(bias) != g.cout) return decline("QLinearConv: bias length");
+    for (int64_t i = 0; i < g.cout; ++i) {
+      int32_t v;
+      if (!lane_int(host_at(bias, i), &v)) return decline("QLinearConv: bias");
+      bias_i.push_back(v);
+    }
+  }
+  ohip_tuning tun;
+  ohip_get_tuning(ctx, &tun);
+  if (!ohip_conv_admits(&tun, g.cout, g.c * g.kh * g.kw, g.n * g.oh * g.ow)) return decline("integer Conv: gate");
+  std::vector<uint8_t> xb, wb;
+  int xdt, wdt;
+  if (!to_bytes(x, xb, &xdt) || !to_bytes(w, wb, &wdt)) return decline("integer Conv: lanes outside 8 bits");
+  const bool cache = w->is_initializer && w->name && *w->name;
+  std::string name = wkey_name(w), label = std::string(qlinear ? "QLinearConv.W" : "ConvInteger.W");
+  ohip_weight_key key{name.c_str(), label.c_str()};
+  ohip_weight* wt = nullptr;
+  int rc = ohip_weight_qconv(ctx, cache ? &key : nullptr, wdt, wb.data(), g.cout, g.c, g.kh, g.kw, wzp.data(),
+                             (int)wzp.size(), qlinear ? ws.data() : nullptr, qlinear ? (int)ws.size() : 0, &wt);
+  if (rc) return rc;
+  Stage st(ctx);
+  const void* xd = st.operand(x, xb.data(), xb.size());
+  const void* bd = bias ? st.operand(bias, bias_i.data(), bias_i.size() * 4) : nullptr;
+  const size_t obytes = (size_t)(g.n * g.cout * g.oh * g.ow) * 4;
+  void* yd = st.alloc(obytes);
+  if (!xd || !yd || (bias && !bd)) { if (!cache) ohip_weight_release(wt); return OHIP_E_NOMEM; }
+  ohip_qconv_desc d{g.n, g.c, g.h, g.w, g.cout, g.kh, g.kw, 1, g.sh, g.sw, g.dh, g.dw, g.pt, g.pl, g.pb, g.pr,
+                    xdt, xzp[0], qlinear ? OHIP_QOUT_F32 : OHIP_QOUT_I32, xs, ys, qlinear ? yzp[0] : 0, lo, hi,
+                    OHIP_NCHW, OHIP_NCHW};
+  rc = ohip_qconv2d(ctx, &d, xd, wt, static_cast<const int32_t*>(bd), yd);
+  if (!cache) ohip_weight_release(wt);
+  if (rc) return rc;
+  set_out(out, qlinear ? OHIP_F32 : OHIP_I32, conv_out_shape(g));
+  return finish_output(ctx, st, placement, out, yd, obytes, qlinear ? OHIP_F32 : OHIP_I32);
+}
+
+}  // namespace
+
+// ------------------------------------------------------------------ public
+// is_supported_op (oxionnx-cuda/src/lib.rs:217-275), restricted to this
+// provider's dense-contraction arms.
+extern "C" int ohip_is_supported_op(const char* op) {
+  if (!op) return 0;
+  static const char* kOps[] = {"Conv", "Gemm", "MatMul", "QLinearMatMul", "MatMulInteger", "QLinearConv",
+                               "ConvInteger"};
+  for (const char* o : kOps)
+    if (std::strcmp(op, o) == 0) return 1;
+  return 0;
+}
+
+// accepts_resident_slot (oxionnx-cuda/src/lib.rs:419-480): only the
+// activation slot of the float ops may be bound from a resident tensor; a
+// filter, a Gemm B/C and every quantisation parameter are read on the host.
+extern "C" int ohip_accepts_resident_slot(const char* op, int index) {
+  if (!op) return 0;
+  if (!std::strcmp(op, "Conv") || !std::strcmp(op, "Gemm") || !std::strcmp(op, "MatMul")) return index == 0;
+  return 0;
+}
+
+extern "C" int ohip_try_dispatch(ohip_ctx* ctx, const ohip_node* node, int placement, ohip_output* out) {
+  if (!ctx || !node || !node->op_type || !out) return OHIP_E_INVALID;
+  std::memset(out, 0, sizeof(*out));
+  const std::string op(node->op_type);
+  for (int i = 0; i < node->n_inputs; ++i) {
+    const ohip_tensor& t = node->inputs[i];
+    if (t.device && !ohip_accepts_resident_slot(node->op_type, i))
+      return decline("resident operand in a host-read slot");
+  }
+  int rc;
+  if (op == "Conv") rc = do_conv(ctx, node, placement, out);
+  else if (op == "Gemm") rc = do_gemm(ctx, node, false, placement, out);
+  else if (op == "MatMul") rc = do_gemm(ctx, node, true, placement, out);
+  else if (op == "QLinearMatMul") rc = do_qmatmul(ctx, node, true, placement, out);
+  else if (op == "MatMulInteger") rc = do_qmatmul(ctx, node, false, placement, out);
+  else if (op == "QLinearConv") rc = do_qconv(ctx, node, true, placement, out);
+  else if (op == "ConvInteger") rc = do_qconv(ctx, node, false, placement, out);
+  else rc = decline("unsupported op " + op);
+  if (rc == OHIP_DECLINED) ohip_note_declined(ctx, t_err.c_str());
+  return rc;
+}
+
+extern "C" void ohip_output_free(ohip_output* o) {
+  if (!o) return;
+  std::free(o->data);
+  o->data = nullptr;
+  if (o->device) ohip_dtensor_free(o->device);
+  o->device = nullptr;
+}

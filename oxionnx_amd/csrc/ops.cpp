@@ -86,7 +86,18 @@ struct ohip_ctx {
   std::map<std::string, ohip_weight*> weights;
   std::vector<ohip_weight*> transients;  // freed with the context if never released
   ohip_counters counters{};
+  std::string last_decline;
   std::mutex mu;
+};
+
+struct ohip_dtensor {
+  ohip_ctx* ctx = nullptr;
+  void* ptr = nullptr;
+  int dtype = 0;
+  int rank = 0;
+  int64_t shape[8] = {0};
+  int layout = OHIP_NCHW;
+  size_t bytes = 0;
 };
 
 static int activate(ohip_ctx* ctx) {
@@ -1032,6 +1043,105 @@ extern "C" int ohip_qconv2d(ohip_ctx* ctx, const ohip_qconv_desc* d, const void*
   if (e != hipSuccess) return hip_fail(e, "ohip_qconv2d launch");
   return OHIP_OK;
 }
+
+// ------------------------------------------------------------------ device tensors
+static int dt_bytes(int dtype, int rank, const int64_t* shape, int layout, size_t* out) {
+  const int eb = elem_bytes(dtype);
+  if (!eb || rank < 0 || rank > 8) return fail(OHIP_E_INVALID, "dtensor: bad dtype / rank");
+  int64_t e = 1;
+  for (int i = 0; i < rank; ++i) {
+    if (shape[i] < 0) return fail(OHIP_E_INVALID, "dtensor: negative extent");
+    e *= (layout == OHIP_NHWC && i == 1) ? round_up(shape[i], 16 / eb) : shape[i];
+  }
+  *out = (size_t)e * eb;
+  return OHIP_OK;
+}
+
+extern "C" int ohip_dtensor_alloc(ohip_ctx* ctx, int dtype, int rank, const int64_t* shape, int layout,
+                                  ohip_dtensor** out) {
+  int rc = activate(ctx);
+  if (rc) return rc;
+  if (!out || (rank && !shape)) return fail(OHIP_E_INVALID, "dtensor: null argument");
+  if (layout == OHIP_NHWC && rank != 4) return fail(OHIP_E_INVALID, "dtensor: NHWC needs rank 4");
+  size_t bytes;
+  rc = dt_bytes(dtype, rank, shape, layout, &bytes);
+  if (rc) return rc;
+  auto* t = new ohip_dtensor();
+  t->ctx = ctx; t->dtype = dtype; t->rank = rank; t->layout = layout; t->bytes = bytes;
+  for (int i = 0; i < rank; ++i) t->shape[i] = shape[i];
+  hipError_t e = hipMalloc(&t->ptr, bytes ? bytes : 16);
+  if (e != hipSuccess) {
+    delete t;
+    return fail(OHIP_E_NOMEM, std::string("dtensor hipMalloc: ") + hipGetErrorString(e));
+  }
+  if (layout == OHIP_NHWC) {  // channel padding must read as zero
+    e = hipMemsetAsync(t->ptr, 0, bytes, ctx->stream);
+    if (e != hipSuccess) { (void)hipFree(t->ptr); delete t; return hip_fail(e, "dtensor memset"); }
+  }
+  *out = t;
+  return OHIP_OK;
+}
+
+extern "C" int ohip_dtensor_wrap(ohip_ctx* ctx, void* p, int dtype, int rank, const int64_t* shape,
+                                 ohip_dtensor** out) {
+  if (!ctx || !p || !out) return fail(OHIP_E_INVALID, "dtensor_wrap: null argument");
+  size_t bytes;
+  int rc = dt_bytes(dtype, rank, shape, OHIP_NCHW, &bytes);
+  if (rc) return rc;
+  auto* t = new ohip_dtensor();
+  t->ctx = ctx; t->ptr = p; t->dtype = dtype; t->rank = rank; t->layout = OHIP_NCHW; t->bytes = bytes;
+  for (int i = 0; i < rank; ++i) t->shape[i] = shape[i];
+  *out = t;
+  return OHIP_OK;
+}
+
+extern "C" int ohip_dtensor_upload(ohip_ctx* ctx, ohip_dtensor* t, const void* host) {
+  if (!t || !host) return fail(OHIP_E_INVALID, "dtensor_upload: null argument");
+  if (t->layout != OHIP_NCHW) return fail(OHIP_E_INVALID, "dtensor_upload: NCHW tensors only");
+  return ohip_memcpy_h2d(ctx, t->ptr, host, t->bytes);
+}
+extern "C" int ohip_dtensor_download(ohip_ctx* ctx, const ohip_dtensor* t, void* host) {
+  if (!t || !host) return fail(OHIP_E_INVALID, "dtensor_download: null argument");
+  if (t->layout != OHIP_NCHW) return fail(OHIP_E_INVALID, "dtensor_download: NCHW tensors only");
+  return ohip_memcpy_d2h(ctx, host, t->ptr, t->bytes);
+}
+extern "C" void* ohip_dtensor_ptr(const ohip_dtensor* t) { return t ? t->ptr : nullptr; }
+extern "C" int ohip_dtensor_layout(const ohip_dtensor* t) { return t ? t->layout : -1; }
+extern "C" int ohip_dtensor_info(const ohip_dtensor* t, int* dtype, int* rank, int64_t* shape8, size_t* bytes) {
+  if (!t) return fail(OHIP_E_INVALID, "null dtensor");
+  if (dtype) *dtype = t->dtype;
+  if (rank) *rank = t->rank;
+  if (shape8) for (int i = 0; i < 8; ++i) shape8[i] = i < t->rank ? t->shape[i] : 0;
+  if (bytes) *bytes = t->bytes;
+  return OHIP_OK;
+}
+extern "C" void ohip_dtensor_free(ohip_dtensor* t) {
+  if (!t) return;
+  if (t->ptr) {
+    (void)hipSetDevice(t->ctx->device);
+    (void)hipStreamSynchronize(t->ctx->stream);
+    (void)hipFree(t->ptr);
+  }
+  delete t;
+}
+
+// ------------------------------------------------------------------ gating / declines
+extern "C" int ohip_ctx_try_new(ohip_ctx** out) {
+  if (!out) return fail(OHIP_E_INVALID, "null out");
+  *out = nullptr;
+  if (!ohip_env_flag("OXIONNX_HIP")) return fail(OHIP_DECLINED, "OXIONNX_HIP is not set");
+  int dev = 0;
+  if (const char* d = std::getenv("OXIONNX_HIP_DEVICE")) dev = std::atoi(d);
+  int rc = ohip_ctx_create(dev, out);
+  return rc == OHIP_E_NODEVICE ? fail(OHIP_DECLINED, "no gfx950 device") : rc;
+}
+extern "C" void ohip_note_declined(ohip_ctx* ctx, const char* why) {
+  if (!ctx) return;
+  std::lock_guard<std::mutex> lock(ctx->mu);
+  ctx->counters.declined++;
+  ctx->last_decline = why ? why : "";
+}
+extern "C" const char* ohip_last_decline(ohip_ctx* ctx) { return ctx ? ctx->last_decline.c_str() : ""; }
 
 // ------------------------------------------------------------------ counters
 extern "C" int ohip_get_counters(ohip_ctx* ctx, ohip_counters* out) {

@@ -1,0 +1,111 @@
+"""Device-free tests of the dispatch gate (GpuTuning, oxionnx-gpu/src/context/tuning.rs:271-611)
+and of the op-support predicates, the pattern of tuning.rs:622-868."""
+import ctypes
+
+import pytest
+
+from oxionnx_amd import _lib as L
+from oxionnx_amd import ep
+
+
+def tuning(cls):
+    t = L.Tuning()
+    assert L.lib().ohip_tuning_for_class(cls, ctypes.byref(t)) == 0
+    return t
+
+
+def admits(t, m, k, n, cached):
+    return bool(L.lib().ohip_gemm_admits(ctypes.byref(t), m, k, n, int(cached)))
+
+
+def conv_admits(t, m, k, n):
+    return bool(L.lib().ohip_conv_admits(ctypes.byref(t), m, k, n))
+
+
+def test_legacy_class_reproduces_the_reference_measured_table():
+    """tuning.rs:698-748: with the reference's discrete-class numbers the gate
+    must reach exactly the reference's measured admit/decline decisions."""
+    t = tuning(L.CLASS_LEGACY)
+    losses = [(1, 25088, 512), (2, 25088, 512), (8, 25088, 512), (16, 25088, 512), (24, 25088, 512),
+              (12, 1024, 1024), (16, 1024, 1024), (24, 1024, 1024), (2, 4096, 4096), (4, 4096, 4096),
+              (8, 4096, 4096), (48, 512, 512), (64, 512, 512), (32, 512, 1024), (32, 1024, 512)]
+    wins = [(32, 1024, 1024), (32, 2048, 2048), (32, 4096, 4096), (32, 25088, 512), (48, 512, 1024),
+            (96, 512, 512), (256, 1024, 1024), (384, 256, 256)]
+    for s in losses:
+        assert not admits(t, *s, cached=False), s
+    for s in wins:
+        assert admits(t, *s, cached=False), s
+
+
+def test_cached_weight_skips_the_intensity_gate():
+    """tuning.rs:757-766: ArcFace's head declines uploading, dispatches cached."""
+    t = tuning(L.CLASS_LEGACY)
+    assert not admits(t, 1, 25088, 512, False)
+    assert admits(t, 1, 25088, 512, True)
+    assert not admits(t, 1, 512, 2048, True)
+
+
+def test_intensity_closed_forms():
+    """tuning.rs:676-693."""
+    gi = L.lib().ohip_gemm_intensity
+    assert gi(1, 1 << 20, 1 << 20) == 1
+    assert gi(16, 1 << 20, 1 << 20) == 31
+    assert gi(1 << 20, 1 << 20, 1) == gi(1, 1 << 20, 1 << 20)
+    assert gi(1 << 20, 1, 1 << 20) == gi(1, 1 << 20, 1 << 20)
+    assert gi(0, 0, 0) == 0
+
+
+def test_conv_threshold_and_overflow():
+    t = tuning(L.CLASS_LEGACY)
+    assert conv_admits(t, 10_000_000, 1, 1)
+    assert not conv_admits(t, 9_999_999, 1, 1)
+    huge = 1 << 40
+    assert not admits(t, huge, huge, huge, True)
+    assert not admits(t, huge, huge, huge, False)
+    assert not conv_admits(t, huge, huge, huge)
+    assert not admits(t, 0, 4096, 4096, False)
+    assert not admits(t, 4096, 0, 4096, True)
+
+
+def test_parity_and_never_presets():
+    p = tuning(L.CLASS_PARITY)
+    assert admits(p, 1, 1, 1, False) and admits(p, 1, 1, 1, True) and conv_admits(p, 1, 1, 1)
+    assert not admits(p, 0, 8, 8, False)
+    nv = tuning(L.CLASS_NEVER)
+    assert not admits(nv, 4096, 4096, 4096, True)
+    assert not admits(nv, 4096, 4096, 4096, False)
+    assert not conv_admits(nv, 4096, 4096, 4096)
+
+
+def test_mi355x_class_admits_every_configured_workload():
+    """The recalibrated MI355X floors claim every configured dense
+    contraction and still decline toy shapes."""
+    t = tuning(L.CLASS_MI355X)
+    assert admits(t, 1, 25088, 512, True)            # config 2a, resident B
+    for m, k, n in [(128, 768, 3072), (2048, 4096, 4096), (4096, 4096, 11008)]:
+        assert admits(t, m, k, n, True) and admits(t, m, k, n, False)
+    assert admits(t, 4096, 768, 3072, True)         # config 3
+    assert conv_admits(t, 64, 64 * 9, 128 * 128)    # config 1
+    assert conv_admits(t, 16, 3 * 9, 320 * 320)     # config 5 stem
+    assert not admits(t, 4, 8, 8, False)
+    assert not admits(t, 1, 512, 512, True)
+    assert not conv_admits(t, 1, 9, 16)
+
+
+def test_op_support_predicates():
+    for op in ["Conv", "Gemm", "MatMul", "QLinearMatMul", "MatMulInteger", "QLinearConv", "ConvInteger"]:
+        assert ep.is_supported_op(op)
+    for op in ["Relu", "Transpose", "Add", "ConvTranspose", ""]:
+        assert not ep.is_supported_op(op)
+    assert ep.accepts_resident_slot("Conv", 0) and not ep.accepts_resident_slot("Conv", 1)
+    assert ep.accepts_resident_slot("Gemm", 0) and not ep.accepts_resident_slot("Gemm", 1)
+    assert not ep.accepts_resident_slot("QLinearConv", 0)
+
+
+def test_try_new_is_gated_by_the_env_flag(monkeypatch):
+    monkeypatch.delenv("OXIONNX_HIP", raising=False)
+    assert ep.HipContext.try_new() is None
+    monkeypatch.setenv("OXIONNX_HIP", "off")
+    assert ep.HipContext.try_new() is None
+    h = ctypes.c_void_p()
+    assert L.lib().ohip_ctx_try_new(ctypes.byref(h)) == L.DECLINED
