@@ -35,7 +35,8 @@ def parse():
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--no-sweep", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=10.0)
-    p.add_argument("--only", default="", help="run one sweep item (for profiling)")
+    p.add_argument("--only", default="", help="run one item (for profiling): 'headline', 'copy', "
+                   "'conv_f32_cfg1', 'int8_ffn', or a sweep item such as 'gemm_f16_2048x4096x4096'")
     return p.parse_args()
 
 
@@ -110,6 +111,16 @@ def main():
     from oxionnx_amd.device import HipContext
 
     torch.cuda.set_device(0)
+    if args.only == "copy":
+        # calibration for the FETCH_SIZE / WRITE_SIZE counters: a plain device
+        # copy of 256 MiB (reads 256 MiB, writes 256 MiB), five times
+        src = torch.empty(64 * 1024 * 1024, dtype=torch.float32, device="cuda").fill_(1.0)
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_bytes": src.numel() * 4, "launches": 5}))
+        return
     stream = torch.cuda.Stream()
     with torch.cuda.stream(stream):
         ctx = HipContext(0)   # adopts `stream`: events below are recorded on it
@@ -120,24 +131,25 @@ def main():
         m, k, n = HEADLINE
         _, _, _, w, at, ct, y = gemm_setup(torch, ctx, L, m, k, n, L.F16, rng)
         step = lambda: ctx.gemm(at, w, ct, out=y)
-        for _ in range(args.warmup):
+        steps = args.steps if args.only in ("", "headline") else 0   # profiling another item
+        for _ in range(args.warmup if steps else 0):
             step()
         torch.cuda.synchronize()
         t0 = time.perf_counter()
         ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         ev0.record(stream)
-        for _ in range(args.steps):
+        for _ in range(steps):
             step()
         ev1.record(stream)
         torch.cuda.synchronize()
         wall = time.perf_counter() - t0
-        ms = ev0.elapsed_time(ev1) / args.steps
+        ms = ev0.elapsed_time(ev1) / max(steps, 1) if steps else float("nan")
         flops = 2.0 * m * k * n
         tflops = flops / (ms * 1e-3) / 1e12
         alg_bytes = 2 * (m * k + k * n + m * n) + 2 * n
         traffic = load_traffic("gemm_f16_4096x4096x11008")
 
-        if not args.no_sweep:
+        if not args.no_sweep and args.only != "headline":
             sweep = []
             for (mm, kk, nn) in GEMM_SWEEP:
                 for dt, name in ((L.F32, "f32"), (L.F16, "f16")):
@@ -172,7 +184,7 @@ def main():
                      "kernel": "mfma_gemm_kernel<Op::F16, Tile<256,256,2,4>, DenseRows, DenseRows, FloatEpi<_Float16>>"},
         "wall_s_timed_region": round(wall, 3),
     }
-    if not args.no_cpu:
+    if not args.no_cpu and not args.only:
         line["cpu_baseline"] = cpu_baseline_f16(args.cpu_seconds)
     line.update(extras)
     print(json.dumps(line))
