@@ -312,8 +312,8 @@ int ohip_get_counters(ohip_ctx* ctx, ohip_counters* out);
 int ohip_reset_counters(ohip_ctx* ctx);
 
 /* Testing / tuning knob: force the MFMA block tile, 0 = automatic.
- * 1: 64x64 (4 waves)   2: 128x128 (4)   3: 256x128 (4)   4: 128x256 (4)
- * 5: 256x256 (4)       6: 256x256 (8)   7: 256x128 (8)   8: 128x256 (8) */
+ * 1: 64x64 (4 waves)   2: 128x128 (4)   3: 256x128 (8)   4: 128x256 (8)
+ * 5: 256x256 (4)       6: 256x256 (8) */
 int ohip_set_tile_override(ohip_ctx* ctx, int tile_id);
 
 #ifdef __cplusplus

@@ -46,10 +46,8 @@ hipError_t run_conv_quant(const Im2colOperand& col, const DenseOperand& w, bool 
 }
 
 // ---------------------------------------------------------------- skinny GEMV
-// y[m][n] = sum_k A[m][k] * W[n][k] for M <= kMaxGemvM.  Each wave owns one
-// weight row and one K slice, streams the row with 16-byte loads, and writes
-// one f32 partial per (slice, m, n); gemv_finish sums the slices in a fixed
-// order (deterministic) and applies the epilogue.
+// y[m][n] = sum_k A[m][k] * W[n][k] for M <= 8: the HBM-bound skinny path,
+// which streams every weight byte exactly once with 16-byte loads.
 template <class T> struct Vec16;
 template <> struct Vec16<float> {
   static __device__ __forceinline__ void unpack(u32x4 v, float (&f)[4]) {
@@ -77,104 +75,88 @@ template <> struct Vec16<__bf16> {
   }
 };
 
+// One block per weight row n: its 8 waves stride the row's 16-byte chunks
+// together (coalesced, four loads in flight per lane), reduce through
+// registers and LDS in a fixed order (deterministic), and thread 0 runs the
+// epilogue for the M outputs of that row.
 template <class T, int M>
-__global__ void __launch_bounds__(256)
-gemv_partial_kernel(const T* __restrict__ a, int64_t lda, const T* __restrict__ w, int64_t ldw, int N, int kc,
-                    int chunks_per_split, float* __restrict__ part) {
-  const int lane = threadIdx.x & 63;
-  const int n = blockIdx.x * 4 + (threadIdx.x >> 6);
-  const int s = blockIdx.y;
-  if (n >= N) return;
-  const int c0 = s * chunks_per_split;
-  const int c1 = min(kc, c0 + chunks_per_split);
+__global__ void __launch_bounds__(512)
+gemv_row_kernel(const T* __restrict__ a, int64_t lda, const T* __restrict__ w, int64_t ldw, int kc,
+                FloatEpi<T> epi) {
   constexpr int E = Vec16<T>::N;
+  constexpr int kWaves = 8;
+  __shared__ float red[kWaves][M];
+  const int n = blockIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const u32x4* wr = reinterpret_cast<const u32x4*>(w + (int64_t)n * ldw);
   float acc[M];
 #pragma unroll
   for (int m = 0; m < M; ++m) acc[m] = 0.0f;
-  int c = c0 + lane;
-  for (; c + 64 < c1; c += 128) {
-    u32x4 w0 = __builtin_nontemporal_load(wr + c);
-    u32x4 w1 = __builtin_nontemporal_load(wr + c + 64);
-    float f0[E], f1[E];
-    Vec16<T>::unpack(w0, f0);
-    Vec16<T>::unpack(w1, f1);
+  auto fma_chunk = [&](u32x4 wv, int c) {
+    float f[E];
+    Vec16<T>::unpack(wv, f);
 #pragma unroll
     for (int m = 0; m < M; ++m) {
       const u32x4* ar = reinterpret_cast<const u32x4*>(a + (int64_t)m * lda);
-      float g0[E], g1[E];
-      Vec16<T>::unpack(ar[c], g0);
-      Vec16<T>::unpack(ar[c + 64], g1);
+      float g[E];
+      Vec16<T>::unpack(ar[c], g);
 #pragma unroll
-      for (int e = 0; e < E; ++e) acc[m] += f0[e] * g0[e];
-#pragma unroll
-      for (int e = 0; e < E; ++e) acc[m] += f1[e] * g1[e];
+      for (int e = 0; e < E; ++e) acc[m] += f[e] * g[e];
     }
+  };
+  constexpr int S = kWaves * 64;
+  int c = tid;
+  for (; c + 3 * S < kc; c += 4 * S) {
+    const u32x4 w0 = __builtin_nontemporal_load(wr + c);
+    const u32x4 w1 = __builtin_nontemporal_load(wr + c + S);
+    const u32x4 w2 = __builtin_nontemporal_load(wr + c + 2 * S);
+    const u32x4 w3 = __builtin_nontemporal_load(wr + c + 3 * S);
+    fma_chunk(w0, c);
+    fma_chunk(w1, c + S);
+    fma_chunk(w2, c + 2 * S);
+    fma_chunk(w3, c + 3 * S);
   }
-  for (; c < c1; c += 64) {
-    u32x4 w0 = __builtin_nontemporal_load(wr + c);
-    float f0[E];
-    Vec16<T>::unpack(w0, f0);
-#pragma unroll
-    for (int m = 0; m < M; ++m) {
-      const u32x4* ar = reinterpret_cast<const u32x4*>(a + (int64_t)m * lda);
-      float g0[E];
-      Vec16<T>::unpack(ar[c], g0);
-#pragma unroll
-      for (int e = 0; e < E; ++e) acc[m] += f0[e] * g0[e];
-    }
-  }
+  for (; c < kc; c += S) fma_chunk(__builtin_nontemporal_load(wr + c), c);
 #pragma unroll
   for (int m = 0; m < M; ++m) {
     float v = acc[m];
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
-    if (lane == 0) part[((int64_t)s * M + m) * N + n] = v;
+    if (lane == 0) red[wave][m] = v;
+  }
+  __syncthreads();
+  if (tid < M) {
+    float v = 0.0f;
+#pragma unroll
+    for (int q = 0; q < kWaves; ++q) v += red[q][tid];
+    // GEMM orientation: i = n (weight row), j = m (activation row)
+    epi.y[epi.index(n, tid)] = from_f32<T>(epi.finish(v, n, tid));
   }
 }
 
-template <class OutT>
-__global__ void gemv_finish_kernel(const float* __restrict__ part, int splits, int M, int N, FloatEpi<OutT> epi) {
-  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (idx >= (int64_t)M * N) return;
-  const int m = (int)(idx / N), n = (int)(idx - (int64_t)m * N);
-  float v = 0.0f;
-  for (int s = 0; s < splits; ++s) v += part[((int64_t)s * M + m) * N + n];
-  // GEMM orientation: i = n (weight row), j = m (activation row)
-  epi.y[epi.index(n, m)] = from_f32<OutT>(epi.finish(v, n, m));
-}
-
-template <class T, class OutT>
+template <class T>
 static hipError_t gemv_t(const GemvArgs& g, const FloatOut& o, hipStream_t st) {
-  constexpr int E = Vec16<T>::N;
-  (void)E;
   const T* a = reinterpret_cast<const T*>(g.a);
   const T* w = reinterpret_cast<const T*>(g.w);
-  dim3 grid((g.N + 3) / 4, g.splits);
+  const FloatEpi<T> epi = make_float_epi<T>(o);
   switch (g.M) {
-#define OHIP_GEMV_CASE(MM)                                                                                   \
-  case MM:                                                                                                   \
-    hipLaunchKernelGGL((gemv_partial_kernel<T, MM>), grid, dim3(256), 0, st, a, g.lda, w, g.ldw, g.N, g.kc, \
-                       g.chunks_per_split, g.partial);                                                       \
+#define OHIP_GEMV_CASE(MM)                                                                                    \
+  case MM:                                                                                                    \
+    hipLaunchKernelGGL((gemv_row_kernel<T, MM>), dim3(g.N), dim3(512), 0, st, a, g.lda, w, g.ldw, g.kc, epi); \
     break;
     OHIP_GEMV_CASE(1) OHIP_GEMV_CASE(2) OHIP_GEMV_CASE(3) OHIP_GEMV_CASE(4)
     OHIP_GEMV_CASE(5) OHIP_GEMV_CASE(6) OHIP_GEMV_CASE(7) OHIP_GEMV_CASE(8)
 #undef OHIP_GEMV_CASE
     default: return hipErrorInvalidValue;
   }
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
-  const int64_t total = (int64_t)g.M * g.N;
-  hipLaunchKernelGGL((gemv_finish_kernel<OutT>), dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st,
-                     g.partial, g.splits, g.M, g.N, make_float_epi<OutT>(o));
   return hipGetLastError();
 }
 
 hipError_t run_gemv(int dtype, const GemvArgs& g, const FloatOut& o, hipStream_t st) {
   switch (dtype) {
-    case DT_F32: return gemv_t<float, float>(g, o, st);
-    case DT_F16: return gemv_t<_Float16, _Float16>(g, o, st);
-    case DT_BF16: return gemv_t<__bf16, __bf16>(g, o, st);
+    case DT_F32: return gemv_t<float>(g, o, st);
+    case DT_F16: return gemv_t<_Float16>(g, o, st);
+    case DT_BF16: return gemv_t<__bf16>(g, o, st);
     default: return hipErrorInvalidValue;
   }
 }

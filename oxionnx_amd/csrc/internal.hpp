@@ -20,8 +20,8 @@ struct DenseOperand {
   int rows;
   int kc;             // 16-byte chunks per row that hold data
   int kwrap;          // > 0: loop chunk g >= kwrap reads chunk g - kwrap
-  uint32_t xor_mask;  // 0x80808080 turns u8 into (u8 - 128) as int8
-  uint32_t pad;       // replicated into every dword of an out-of-range chunk
+  uint32_t xor_mask;  // applied after the LDS read: 0x80808080 turns u8 into (u8 - 128) as int8
+  const void* pad16;  // device address of 16 bytes read for any chunk outside the matrix
 };
 
 // Implicit im2col rows over an NHWC activation with channels padded to cpc
@@ -31,7 +31,8 @@ struct Im2colOperand {
   int H, W, OH, OW, KW, cpc;
   int sh, sw, dh, dw, pt, pl;
   int rows, kc, kwrap;
-  uint32_t xor_mask, pad;
+  uint32_t xor_mask;  // as DenseOperand::xor_mask
+  const void* pad16;  // 16 bytes standing for a padding tap (stored before the XOR)
 };
 
 // Output mapping shared by both epilogues: element (i, j) lives at
@@ -70,8 +71,6 @@ struct GemvArgs {
   const void* w;   // [N][ldw] packed weight rows
   int64_t ldw;     // elements
   int M, N, kc;
-  int splits, chunks_per_split;
-  float* partial;  // [splits][M][N]
 };
 
 hipError_t run_dense_float(int dtype, const DenseOperand& x, const DenseOperand& y, const FloatOut& o, int tile,

@@ -171,52 +171,49 @@ struct QuantEpi {
 };
 
 // ---------------------------------------------------------------- tiles
-// Tile ids (ohip_set_tile_override): block tile BP x BQ, WP x WQ waves.
-using T64 = Tile<64, 64, 2, 2>;           // 1
-using T128 = Tile<128, 128, 2, 2>;        // 2
-using T256x128 = Tile<256, 128, 2, 2>;    // 3
-using T128x256 = Tile<128, 256, 2, 2>;    // 4
-using T256 = Tile<256, 256, 2, 2>;        // 5
-using T256w8 = Tile<256, 256, 2, 4>;      // 6: 8 waves, 128x64 per wave
-using T256x128w8 = Tile<256, 128, 4, 2>;  // 7: 8 waves, 64x64 per wave
-using T128x256w8 = Tile<128, 256, 2, 4>;  // 8: 8 waves, 64x64 per wave
-constexpr int kTileCount = 8;
+// Tile ids (ohip_set_tile_override): block tile BP x BQ, WP x WQ waves,
+// LDS stages.
+using T64 = Tile<64, 64, 2, 2, 2>;          // 1: 4 waves, 32x32 per wave
+using T128 = Tile<128, 128, 2, 2, 3>;       // 2: 4 waves, 64x64 per wave
+using T256x128 = Tile<256, 128, 4, 2, 3>;   // 3: 8 waves, 64x64 per wave
+using T128x256 = Tile<128, 256, 2, 4, 3>;   // 4: 8 waves, 64x64 per wave
+using T256w4 = Tile<256, 256, 2, 2, 2>;     // 5: 4 waves, 128x128 per wave
+using T256 = Tile<256, 256, 2, 4, 2>;       // 6: 8 waves, 128x64 per wave
+constexpr int kTileCount = 6;
 
 template <Op O, class Tl, class LX, class LY, class Epi>
-inline hipError_t launch_tile(const LX& lx, const LY& ly, const Epi& epi, int P, int Q, int kc,
-                              hipStream_t st) {
+inline hipError_t launch_tile(const LX& lx, const LY& ly, const Epi& epi, int P, int Q, int kc, uint32_t xxor,
+                              uint32_t yxor, hipStream_t st) {
   const int nP = (P + Tl::BP - 1) / Tl::BP, nQ = (Q + Tl::BQ - 1) / Tl::BQ;
   const int64_t nb = (int64_t)nP * nQ;
   if (nb <= 0) return hipSuccess;
   if (nb > 0x7fffffff) return hipErrorInvalidValue;
   hipLaunchKernelGGL((mfma_gemm_kernel<O, Tl, LX, LY, Epi>), dim3((unsigned)nb), dim3(Tl::kThreads),
-                     0, st, lx, ly, epi, nP, nQ, kc);
+                     0, st, lx, ly, epi, nP, nQ, kc, xxor, yxor);
   return hipGetLastError();
 }
 
 // Automatic choice: the largest tile that still gives at least one block
-// per CU (256 CUs), else the smallest.
+// per CU (256 CUs), else the smaller ones.
 inline int pick_tile(int P, int Q, int forced) {
   if (forced >= 1 && forced <= kTileCount) return forced;
   auto blocks = [&](int bp, int bq) { return (int64_t)((P + bp - 1) / bp) * ((Q + bq - 1) / bq); };
   if (blocks(256, 256) >= 256) return 6;
-  if (blocks(256, 128) >= 256) return P >= Q ? 7 : 8;
-  if (blocks(128, 128) >= 200) return 2;
+  if (blocks(256, 128) >= 256) return P >= Q ? 3 : 4;
+  if (blocks(128, 128) >= 128) return 2;
   return 1;
 }
 
 template <Op O, class LX, class LY, class Epi>
 inline hipError_t launch_any(const LX& lx, const LY& ly, const Epi& epi, int P, int Q, int kc, int tile,
-                             hipStream_t st) {
+                             uint32_t xxor, uint32_t yxor, hipStream_t st) {
   switch (pick_tile(P, Q, tile)) {
-    case 2: return launch_tile<O, T128>(lx, ly, epi, P, Q, kc, st);
-    case 3: return launch_tile<O, T256x128>(lx, ly, epi, P, Q, kc, st);
-    case 4: return launch_tile<O, T128x256>(lx, ly, epi, P, Q, kc, st);
-    case 5: return launch_tile<O, T256>(lx, ly, epi, P, Q, kc, st);
-    case 6: return launch_tile<O, T256w8>(lx, ly, epi, P, Q, kc, st);
-    case 7: return launch_tile<O, T256x128w8>(lx, ly, epi, P, Q, kc, st);
-    case 8: return launch_tile<O, T128x256w8>(lx, ly, epi, P, Q, kc, st);
-    default: return launch_tile<O, T64>(lx, ly, epi, P, Q, kc, st);
+    case 2: return launch_tile<O, T128>(lx, ly, epi, P, Q, kc, xxor, yxor, st);
+    case 3: return launch_tile<O, T256x128>(lx, ly, epi, P, Q, kc, xxor, yxor, st);
+    case 4: return launch_tile<O, T128x256>(lx, ly, epi, P, Q, kc, xxor, yxor, st);
+    case 5: return launch_tile<O, T256w4>(lx, ly, epi, P, Q, kc, xxor, yxor, st);
+    case 6: return launch_tile<O, T256>(lx, ly, epi, P, Q, kc, xxor, yxor, st);
+    default: return launch_tile<O, T64>(lx, ly, epi, P, Q, kc, xxor, yxor, st);
   }
 }
 
@@ -243,8 +240,8 @@ inline QuantEpi make_quant_epi(const QuantOut& o) {
 inline DenseRows make_dense(const DenseOperand& d) {
   DenseRows r;
   r.base = reinterpret_cast<const char*>(d.base);
-  r.ld = d.ld_bytes; r.rows = d.rows; r.kc = d.kc; r.kwrap = d.kwrap; r.xor_mask = d.xor_mask;
-  r.pad = u32x4{d.pad, d.pad, d.pad, d.pad};
+  r.ld = d.ld_bytes; r.rows = d.rows; r.kc = d.kc; r.kwrap = d.kwrap;
+  r.pad = reinterpret_cast<const char*>(d.pad16);
   return r;
 }
 
@@ -253,8 +250,8 @@ inline Im2colNHWC make_im2col(const Im2colOperand& c) {
   r.base = reinterpret_cast<const char*>(c.base);
   r.H = c.H; r.W = c.W; r.OH = c.OH; r.OW = c.OW; r.KW = c.KW; r.cpc = c.cpc;
   r.sh = c.sh; r.sw = c.sw; r.dh = c.dh; r.dw = c.dw; r.pt = c.pt; r.pl = c.pl;
-  r.rows = c.rows; r.kc = c.kc; r.kwrap = c.kwrap; r.xor_mask = c.xor_mask;
-  r.pad = u32x4{c.pad, c.pad, c.pad, c.pad};
+  r.rows = c.rows; r.kc = c.kc; r.kwrap = c.kwrap;
+  r.pad = reinterpret_cast<const char*>(c.pad16);
   return r;
 }
 

@@ -9,14 +9,22 @@
 // Nothing is materialised for im2col: the loader gathers 16-byte channel
 // chunks straight from the NHWC activation.
 //
-// Per 64-lane wave and per 16-byte fragment pair the engine issues
-//   f16/bf16: one v_mfma_f32_16x16x32_{f16,bf16}
-//   int8    : one v_mfma_i32_16x16x64_i8
-//   f32     : four v_mfma_f32_16x16x4_f32 (lane group g supplies k = 4g+e for
-//             the e-th instruction in both operands, so the sums agree)
-// and the 16x16 result lands with lane l holding rows 4*(l/16)..+3 of column
-// l%16: each lane owns four P-consecutive outputs, which is why the side whose
-// output index is memory-contiguous is always put on X.
+// Global -> LDS traffic uses the LDS DMA path (global_load_lds_dwordx4): each
+// wave writes 1 KiB of contiguous LDS per load, with no VGPR staging, and the
+// operands run STAGES deep.  Out-of-range chunks (matrix edges, the K tail,
+// padding taps) are redirected to a 16-byte pad source in global memory.
+//
+// The MFMAs are the 32x32 shapes, which gfx950 runs at about twice the rate
+// of the 16x16 ones for f16 / bf16 and 1.4x for int8:
+//   f16/bf16: v_mfma_f32_32x32x16_{f16,bf16}  (lane l: row l%32, k 8*(l/32)..+7)
+//   int8    : v_mfma_i32_32x32x32_i8          (lane l: row l%32, k 16*(l/32)..+15)
+//   f32     : four v_mfma_f32_32x32x2_f32     (element e of lane l's 16-byte
+//             fragment is k = 4*(l/32)+e in both operands, so the sums agree)
+// so a 16-byte fragment of a row is chunk 2*ks + (l/32) of the 128-byte
+// stage, ks = 0..3.  The 32x32 result holds, in lane l, rows
+// 8*g + 4*(l/32) .. +3 (g = 0..3) of column l%32: four runs of four
+// P-consecutive outputs, which is why the side whose output index is
+// memory-contiguous is always put on X.
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -25,7 +33,9 @@ namespace ohip {
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+typedef int32_t i32x16 __attribute__((ext_vector_type(16)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
@@ -38,65 +48,78 @@ __device__ __forceinline__ float lane_f32(uint32_t u) { return __builtin_bit_cas
 
 template <Op O> struct OpT;
 template <> struct OpT<Op::F16> {
-  using Acc = f32x4;
-  static constexpr int kElemBytes = 2;
+  using Acc = f32x16;
+  using Out4 = f32x4;
   static __device__ __forceinline__ Acc mma(u32x4 a, u32x4 b, Acc c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
-                                                  __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c,
+                                                  0, 0, 0);
   }
 };
 template <> struct OpT<Op::BF16> {
-  using Acc = f32x4;
-  static constexpr int kElemBytes = 2;
+  using Acc = f32x16;
+  using Out4 = f32x4;
   static __device__ __forceinline__ Acc mma(u32x4 a, u32x4 b, Acc c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
-                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b),
+                                                   c, 0, 0, 0);
   }
 };
 template <> struct OpT<Op::I8> {
-  using Acc = i32x4;
-  static constexpr int kElemBytes = 1;
+  using Acc = i32x16;
+  using Out4 = i32x4;
   static __device__ __forceinline__ Acc mma(u32x4 a, u32x4 b, Acc c) {
-    return __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(i32x4, a),
-                                                 __builtin_bit_cast(i32x4, b), c, 0, 0, 0);
+    return __builtin_amdgcn_mfma_i32_32x32x32_i8(__builtin_bit_cast(i32x4, a), __builtin_bit_cast(i32x4, b), c, 0,
+                                                 0, 0);
   }
 };
 template <> struct OpT<Op::F32> {
-  using Acc = f32x4;
-  static constexpr int kElemBytes = 4;
+  using Acc = f32x16;
+  using Out4 = f32x4;
   static __device__ __forceinline__ Acc mma(u32x4 a, u32x4 b, Acc c) {
-    c = __builtin_amdgcn_mfma_f32_16x16x4f32(lane_f32(a.x), lane_f32(b.x), c, 0, 0, 0);
-    c = __builtin_amdgcn_mfma_f32_16x16x4f32(lane_f32(a.y), lane_f32(b.y), c, 0, 0, 0);
-    c = __builtin_amdgcn_mfma_f32_16x16x4f32(lane_f32(a.z), lane_f32(b.z), c, 0, 0, 0);
-    c = __builtin_amdgcn_mfma_f32_16x16x4f32(lane_f32(a.w), lane_f32(b.w), c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f32_32x32x2f32(lane_f32(a.x), lane_f32(b.x), c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f32_32x32x2f32(lane_f32(a.y), lane_f32(b.y), c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f32_32x32x2f32(lane_f32(a.z), lane_f32(b.z), c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f32_32x32x2f32(lane_f32(a.w), lane_f32(b.w), c, 0, 0, 0);
     return c;
   }
 };
 
-// Block tile: BP x BQ outputs, WP x WQ waves, one 128-byte K slab per stage.
-template <int BP_, int BQ_, int WP_, int WQ_> struct Tile {
-  static constexpr int BP = BP_, BQ = BQ_, WP = WP_, WQ = WQ_;
-  static constexpr int kThreads = 64 * WP * WQ;
-  static constexpr int TP = BP / (WP * 16), TQ = BQ / (WQ * 16);
-  static constexpr int kChunks = 8;          // 16-byte chunks per row per stage
-  static constexpr int kRowStride = 8;       // rows are 128 B; chunks are XOR-swizzled (lds_slot)
-  static constexpr int NX = BP * kChunks / kThreads;
-  static constexpr int NY = BQ * kChunks / kThreads;
-  static constexpr int kStage = (BP + BQ) * kRowStride;  // in u32x4 units
-  static_assert(TP >= 1 && TQ >= 1, "wave tile must hold at least one 16x16 MFMA tile");
-  static_assert(NX >= 1 && NY >= 1 && NX * kThreads == BP * kChunks && NY * kThreads == BQ * kChunks,
-                "loader split must be exact");
+// Block tile: BP x BQ outputs, WP x WQ waves, STAGES LDS buffers of one
+// 128-byte K slab each.
+template <int BP_, int BQ_, int WP_, int WQ_, int STAGES_> struct Tile {
+  static constexpr int BP = BP_, BQ = BQ_, WP = WP_, WQ = WQ_, STAGES = STAGES_;
+  static constexpr int kWaves = WP * WQ;
+  static constexpr int kThreads = 64 * kWaves;
+  static constexpr int TP = BP / (WP * 32), TQ = BQ / (WQ * 32);  // 32x32 MFMA tiles per wave
+  static constexpr int kRowStride = 8;                            // rows are 128 B (8 chunks)
+  static constexpr int NX = BP * 8 / kThreads;                    // DMA loads per thread per stage
+  static constexpr int NY = BQ * 8 / kThreads;
+  static constexpr int kStage = (BP + BQ) * kRowStride;           // in u32x4 units
+  static_assert(TP >= 1 && TQ >= 1, "wave tile must hold at least one 32x32 MFMA tile");
+  static_assert(NX * kThreads == BP * 8 && NY * kThreads == BQ * 8, "loader split must be exact");
+  static_assert(kWaves % 2 == 0, "the DMA swizzle phase relies on an even wave count");
+  static_assert(STAGES >= 2 && STAGES * kStage * 16 <= 160 * 1024, "LDS budget");
 };
 
+// LDS slot of 16-byte chunk c (0..7) of staged row r.  Rows are 128 bytes
+// with no padding; the slot is c ^ (r & 7) ^ ((r >> 3) & 1), which keeps
+// every group of 8 consecutive rows on 8 distinct 16-byte bank groups (a
+// 32-bank LDS serving 8 lanes of a b128 access per cycle) and every group of
+// 16 rows on 16 distinct groups (64 banks serving 16 lanes), for both the
+// row-major DMA writes and the MFMA fragment reads (rows at one chunk).
+__device__ __forceinline__ int lds_slot(int r, int c) { return c ^ (r & 7) ^ ((r >> 3) & 1); }
+
 // ---------------------------------------------------------------- loaders
-// A loader owns NR rows of one operand for the lifetime of the block.  Thread
-// t loads chunk (t & 7) of rows (t >> 3) + i * (threads / 8), i < NR.
-//
-// load() only issues the 16-byte global loads -- every address is clamped
-// into the operand, so no branch and no wait sits between them -- and returns
-// a bit mask of which rows hold real data.  fix() runs after the MFMAs of the
-// current stage, when the loads have landed: it applies the u8 -> int8 shift
-// and substitutes the pad value for out-of-range rows, chunks and taps.
+// DMA load i of a thread (i < NR) writes LDS row r = (i * W + w) * 8 + L / 8
+// (W waves, w = wave, L = lane) at slot L % 8, so it fetches the global chunk
+// lds_slot(r, L % 8) (the swizzle is its own inverse).  With W even,
+// r & 7 = L / 8 and (r >> 3) & 1 = w & 1 for every i: the chunk is a
+// per-thread constant.
+__device__ __forceinline__ int dma_chunk(int lane, int wave) { return (lane & 7) ^ (lane >> 3) ^ (wave & 1); }
+
+__device__ __forceinline__ void dma16(const void* g, u32x4* lds) {
+  __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void*)(lds), 16, 0, 0);
+}
+
 struct DenseRows {
   const char* base;   // row 0
   int64_t ld;         // bytes between rows (multiple of 16)
@@ -104,42 +127,33 @@ struct DenseRows {
   int kc;             // valid 16-byte chunks per row
   int kwrap;          // > 0: chunk g >= kwrap reads chunk g - kwrap (the operand is
                       // re-read against the second half of a split int8 weight)
-  uint32_t xor_mask;  // applied to every loaded dword (u8 -> int8 shift uses 0x80808080)
-  u32x4 pad;          // value used outside the matrix
+  const char* pad;    // 16 bytes that stand for any chunk outside the matrix
 
-  template <int NR, int kThreads>
-  struct State { const char* ptr[NR]; uint32_t okmask; };
+  template <int NR>
+  struct State { const char* ptr[NR]; uint32_t okmask; int c; };
 
-  template <int NR, int kThreads>
-  __device__ __forceinline__ void init(State<NR, kThreads>& s, int row0, int t) const {
+  template <int NR, int NW>
+  __device__ __forceinline__ void init(State<NR>& s, int row0, int lane, int wave) const {
+    s.c = dma_chunk(lane, wave);
     s.okmask = 0;
 #pragma unroll
     for (int i = 0; i < NR; ++i) {
-      int r = row0 + (t >> 3) + i * (kThreads / 8);
+      const int r = row0 + (i * NW + wave) * 8 + (lane >> 3);
       const bool ok = r < rows;
       s.okmask |= (ok ? 1u : 0u) << i;
       s.ptr[i] = base + (int64_t)(ok ? r : 0) * ld;
     }
   }
-  template <int NR, int kThreads>
-  __device__ __forceinline__ uint32_t load(const State<NR, kThreads>& s, int kt, int t, u32x4 (&v)[NR]) const {
-    int gk = kt * 8 + (t & 7);
+  template <int NR, int NW>
+  __device__ __forceinline__ void issue(const State<NR>& s, int kt, int wave, u32x4* lds_rows) const {
+    int gk = kt * 8 + s.c;
     if (kwrap > 0 && gk >= kwrap) gk -= kwrap;
     const bool kin = gk < kc;
-    const int64_t off = (int64_t)(kin ? gk : 0) * 16;
+    const int64_t off = (int64_t)gk * 16;
 #pragma unroll
-    for (int i = 0; i < NR; ++i) v[i] = *reinterpret_cast<const u32x4*>(s.ptr[i] + off);
-    return kin ? s.okmask : 0u;
-  }
-  template <int NR>
-  __device__ __forceinline__ void fix(u32x4 (&v)[NR], uint32_t valid) const {
-    if (xor_mask) {
-#pragma unroll
-      for (int i = 0; i < NR; ++i) v[i] ^= xor_mask;
-    }
-    if (valid != (1u << NR) - 1u) {  // only edge tiles, K tails and padding taps
-#pragma unroll
-      for (int i = 0; i < NR; ++i) v[i] = ((valid >> i) & 1u) ? v[i] : pad;
+    for (int i = 0; i < NR; ++i) {
+      const bool ok = kin && ((s.okmask >> i) & 1u);
+      dma16(ok ? s.ptr[i] + off : pad, lds_rows + (i * NW + wave) * 64);
     }
   }
 };
@@ -156,32 +170,32 @@ struct Im2colNHWC {
   int rows;            // N * OH * OW
   int kc;              // KH * KW * cpc
   int kwrap;           // as DenseRows::kwrap
-  uint32_t xor_mask;
-  u32x4 pad;           // value of a padding tap (already in the shifted domain)
+  const char* pad;     // 16 bytes that stand for a padding tap (and the K tail)
 
-  template <int NR, int kThreads>
-  struct State { const char* img[NR]; int iy0[NR], ix0[NR]; uint32_t okmask; };
+  template <int NR>
+  struct State { const char* img[NR]; int iy0[NR], ix0[NR]; uint32_t okmask; int c; };
 
-  template <int NR, int kThreads>
-  __device__ __forceinline__ void init(State<NR, kThreads>& s, int row0, int t) const {
+  template <int NR, int NW>
+  __device__ __forceinline__ void init(State<NR>& s, int row0, int lane, int wave) const {
+    s.c = dma_chunk(lane, wave);
     const int ohw = OH * OW;
     s.okmask = 0;
 #pragma unroll
     for (int i = 0; i < NR; ++i) {
-      int r = row0 + (t >> 3) + i * (kThreads / 8);
+      const int r = row0 + (i * NW + wave) * 8 + (lane >> 3);
       const bool ok = r < rows;
       s.okmask |= (ok ? 1u : 0u) << i;
-      int rr = ok ? r : 0;
-      int n = rr / ohw, rem = rr - n * ohw;
-      int oy = rem / OW, ox = rem - oy * OW;
+      const int rr = ok ? r : 0;
+      const int n = rr / ohw, rem = rr - n * ohw;
+      const int oy = rem / OW, ox = rem - oy * OW;
       s.img[i] = base + (int64_t)n * H * W * cpc * 16;
       s.iy0[i] = oy * sh - pt;
       s.ix0[i] = ox * sw - pl;
     }
   }
-  template <int NR, int kThreads>
-  __device__ __forceinline__ uint32_t load(const State<NR, kThreads>& s, int kt, int t, u32x4 (&v)[NR]) const {
-    int gk = kt * 8 + (t & 7);
+  template <int NR, int NW>
+  __device__ __forceinline__ void issue(const State<NR>& s, int kt, int wave, u32x4* lds_rows) const {
+    int gk = kt * 8 + s.c;
     if (kwrap > 0 && gk >= kwrap) gk -= kwrap;
     const bool kin = gk < kc;
     const int g = kin ? gk : 0;
@@ -190,26 +204,12 @@ struct Im2colNHWC {
     const int ky = tap / KW;
     const int kx = tap - ky * KW;
     const int dy = ky * dh, dx = kx * dw;
-    uint32_t valid = 0;
 #pragma unroll
     for (int i = 0; i < NR; ++i) {
       const int iy = s.iy0[i] + dy, ix = s.ix0[i] + dx;
-      const bool inside = (unsigned)iy < (unsigned)H && (unsigned)ix < (unsigned)W;
-      valid |= (inside ? 1u : 0u) << i;
-      const int64_t off = inside ? ((int64_t)(iy * W + ix) * cpc + cc) * 16 : 0;
-      v[i] = *reinterpret_cast<const u32x4*>(s.img[i] + off);
-    }
-    return kin ? (valid & s.okmask) : 0u;
-  }
-  template <int NR>
-  __device__ __forceinline__ void fix(u32x4 (&v)[NR], uint32_t valid) const {
-    if (xor_mask) {
-#pragma unroll
-      for (int i = 0; i < NR; ++i) v[i] ^= xor_mask;
-    }
-    if (valid != (1u << NR) - 1u) {  // only edge tiles, K tails and padding taps
-#pragma unroll
-      for (int i = 0; i < NR; ++i) v[i] = ((valid >> i) & 1u) ? v[i] : pad;
+      const bool inside =
+          kin && ((s.okmask >> i) & 1u) && (unsigned)iy < (unsigned)H && (unsigned)ix < (unsigned)W;
+      dma16(inside ? s.img[i] + ((int64_t)(iy * W + ix) * cpc + cc) * 16 : pad, lds_rows + (i * NW + wave) * 64);
     }
   }
 };
@@ -224,14 +224,6 @@ template <int I, int N> struct Unroll {
 template <int N> struct Unroll<N, N> {
   template <class F> static __device__ __forceinline__ void run(F&) {}
 };
-
-// LDS slot of 16-byte chunk c (0..7) of staged row r.  Rows are 128 bytes
-// with no padding; the slot is c ^ (r & 7) ^ ((r >> 3) & 1), which keeps
-// every group of 8 consecutive rows on 8 distinct 16-byte bank groups (a
-// 32-bank LDS serving 8 lanes of a b128 access per cycle) and every group of
-// 16 rows on 16 distinct groups (64 banks serving 16 lanes), for both the
-// row-major stores and the MFMA fragment reads (16 rows at one chunk).
-__device__ __forceinline__ int lds_slot(int r, int c) { return c ^ (r & 7) ^ ((r >> 3) & 1); }
 
 // XCD-aware tile order.  The dispatcher hands consecutive workgroup ids to
 // the 8 XCDs in turn; remapping makes each XCD own a contiguous run of
@@ -250,11 +242,22 @@ __device__ __forceinline__ void map_tile(int bid, int nb, int nP, int nQ, int& t
   tq = within / gsz;
 }
 
+// s_waitcnt vmcnt(N) with the other counters left at their maximum (gfx9
+// encoding: vmcnt in bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8).
+template <int N> __device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// xxor / yxor: XOR applied to every X / Y fragment after its LDS read
+// (0x80808080 turns u8 activations into u8 - 128 as int8; the pad source of
+// such an operand holds its pad bytes pre-XORed).
 template <Op O, class Tl, class LX, class LY, class Epi>
 __global__ void __launch_bounds__(Tl::kThreads)
-mfma_gemm_kernel(const LX lx, const LY ly, const Epi epi, int nP, int nQ, int kc) {
+mfma_gemm_kernel(const LX lx, const LY ly, const Epi epi, int nP, int nQ, int kc, uint32_t xxor, uint32_t yxor) {
   using A = typename OpT<O>::Acc;
-  __shared__ u32x4 smem[2 * Tl::kStage];
+  using O4 = typename OpT<O>::Out4;
+  __shared__ u32x4 smem[Tl::STAGES * Tl::kStage];
   const int t = threadIdx.x;
   const int lane = t & 63;
   const int wave = t >> 6;
@@ -263,87 +266,89 @@ mfma_gemm_kernel(const LX lx, const LY ly, const Epi epi, int nP, int nQ, int kc
   map_tile(blockIdx.x, gridDim.x, nP, nQ, tp, tq);
   const int p0 = tp * Tl::BP, q0 = tq * Tl::BQ;
 
-  typename LX::template State<Tl::NX, Tl::kThreads> sx;
-  typename LY::template State<Tl::NY, Tl::kThreads> sy;
-  lx.init(sx, p0, t);
-  ly.init(sy, q0, t);
+  typename LX::template State<Tl::NX> sx;
+  typename LY::template State<Tl::NY> sy;
+  lx.template init<Tl::NX, Tl::kWaves>(sx, p0, lane, wave);
+  ly.template init<Tl::NY, Tl::kWaves>(sy, q0, lane, wave);
 
-  u32x4 rx[Tl::NX], ry[Tl::NY];
   A acc[Tl::TP][Tl::TQ];
 #pragma unroll
   for (int a = 0; a < Tl::TP; ++a)
 #pragma unroll
-    for (int b = 0; b < Tl::TQ; ++b) acc[a][b] = A{0, 0, 0, 0};
+    for (int b = 0; b < Tl::TQ; ++b)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[a][b][e] = 0;
 
   const int nk = (kc + 7) >> 3;
-  const int srow = t >> 3, schunk = t & 7;
-
-  auto stash = [&](int stage, uint32_t vx, uint32_t vy) {
-    lx.fix(rx, vx);
-    ly.fix(ry, vy);
-    u32x4* s = smem + stage * Tl::kStage;
-#pragma unroll
-    for (int i = 0; i < Tl::NX; ++i) {
-      const int r = srow + i * (Tl::kThreads / 8);
-      s[r * Tl::kRowStride + lds_slot(r, schunk)] = rx[i];
-    }
-#pragma unroll
-    for (int i = 0; i < Tl::NY; ++i) {
-      const int r = Tl::BP + srow + i * (Tl::kThreads / 8);
-      s[r * Tl::kRowStride + lds_slot(r, schunk)] = ry[i];
-    }
+  // Every load is issued unconditionally (past the last stage it reads the
+  // pad source), so the wait below is a fixed count of outstanding loads.
+  auto issue = [&](int kt) {
+    u32x4* s = smem + (kt % Tl::STAGES) * Tl::kStage;
+    lx.template issue<Tl::NX, Tl::kWaves>(sx, kt, wave, s);
+    ly.template issue<Tl::NY, Tl::kWaves>(sy, kt, wave, s + Tl::BP * Tl::kRowStride);
   };
 
-  if (nk > 0) {
-    const uint32_t vx = lx.load(sx, 0, t, rx);
-    const uint32_t vy = ly.load(sy, 0, t, ry);
-    stash(0, vx, vy);
-  }
-  __syncthreads();
-
-  // Fragment rows of this lane; every 16-row tile starts at a multiple of 16,
-  // so the slot pattern of (lane & 15) is the same for every tile.
-  const int xr = wp * Tl::TP * 16 + (lane & 15);
-  const int yr = Tl::BP + wq * Tl::TQ * 16 + (lane & 15);
-  int xslot[2], yslot[2];
+  // Fragment slots of this lane: rows are tile bases (multiples of 32) plus
+  // lane % 32, chunk 2 * ks + lane / 32.
+  const int xr = wp * Tl::TP * 32 + (lane & 31);
+  const int yr = Tl::BP + wq * Tl::TQ * 32 + (lane & 31);
+  int xslot[4], yslot[4];
 #pragma unroll
-  for (int kk = 0; kk < 2; ++kk) {
-    xslot[kk] = xr * Tl::kRowStride + lds_slot(xr, kk * 4 + (lane >> 4));
-    yslot[kk] = yr * Tl::kRowStride + lds_slot(yr, kk * 4 + (lane >> 4));
+  for (int ks = 0; ks < 4; ++ks) {
+    xslot[ks] = xr * Tl::kRowStride + lds_slot(xr, 2 * ks + (lane >> 5));
+    yslot[ks] = yr * Tl::kRowStride + lds_slot(yr, 2 * ks + (lane >> 5));
   }
+
+#pragma unroll
+  for (int s = 0; s < Tl::STAGES - 1; ++s) issue(s);
 
   for (int kt = 0; kt < nk; ++kt) {
-    const int cur = kt & 1;
-    const bool more = kt + 1 < nk;
-    uint32_t vx = 0, vy = 0;
-    if (more) {
-      vx = lx.load(sx, kt + 1, t, rx);
-      vy = ly.load(sy, kt + 1, t, ry);
-    }
-    const u32x4* s = smem + cur * Tl::kStage;
+    // This thread's loads of stage kt have landed once only the younger
+    // stages' loads are outstanding; the barrier extends that to every wave
+    // and retires all reads of the buffer that the next issue overwrites.
+    wait_vmcnt<(Tl::STAGES - 2) * (Tl::NX + Tl::NY)>();
+    __syncthreads();
+    issue(kt + Tl::STAGES - 1);
+    const u32x4* s = smem + (kt % Tl::STAGES) * Tl::kStage;
+    // fragments double-buffered across the four k-steps of the stage
+    u32x4 fx[2][Tl::TP], fy[2][Tl::TQ];
 #pragma unroll
-    for (int kk = 0; kk < 2; ++kk) {
-      u32x4 fx[Tl::TP], fy[Tl::TQ];
+    for (int a = 0; a < Tl::TP; ++a) fx[0][a] = s[xslot[0] + a * 32 * Tl::kRowStride] ^ xxor;
 #pragma unroll
-      for (int a = 0; a < Tl::TP; ++a) fx[a] = s[xslot[kk] + a * 16 * Tl::kRowStride];
+    for (int b = 0; b < Tl::TQ; ++b) fy[0][b] = s[yslot[0] + b * 32 * Tl::kRowStride] ^ yxor;
 #pragma unroll
-      for (int b = 0; b < Tl::TQ; ++b) fy[b] = s[yslot[kk] + b * 16 * Tl::kRowStride];
+    for (int ks = 0; ks < 4; ++ks) {
+      const int cur = ks & 1;
+      if (ks < 3) {
+#pragma unroll
+        for (int a = 0; a < Tl::TP; ++a) fx[cur ^ 1][a] = s[xslot[ks + 1] + a * 32 * Tl::kRowStride] ^ xxor;
+#pragma unroll
+        for (int b = 0; b < Tl::TQ; ++b) fy[cur ^ 1][b] = s[yslot[ks + 1] + b * 32 * Tl::kRowStride] ^ yxor;
+      }
 #pragma unroll
       for (int a = 0; a < Tl::TP; ++a)
 #pragma unroll
-        for (int b = 0; b < Tl::TQ; ++b) acc[a][b] = OpT<O>::mma(fx[a], fy[b], acc[a][b]);
+        for (int b = 0; b < Tl::TQ; ++b) {
+          acc[a][b] = OpT<O>::mma(fx[cur][a], fy[cur][b], acc[a][b]);
+          // one MFMA, then one LDS read: keeps the next k-step's fragment
+          // reads interleaved with this one's MFMAs
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        }
     }
-    if (more) stash(cur ^ 1, vx, vy);
-    __syncthreads();
   }
 
-  const int ibase = p0 + wp * Tl::TP * 16 + (lane >> 4) * 4;
-  const int jbase = q0 + wq * Tl::TQ * 16 + (lane & 15);
-  auto out = [&](int ab) {
+  const int ibase = p0 + wp * Tl::TP * 32 + (lane >> 5) * 4;
+  const int jbase = q0 + wq * Tl::TQ * 32 + (lane & 31);
+  auto out = [&](int abg) {
+    const int g = abg & 3, ab = abg >> 2;
     const int a = ab / Tl::TQ, b = ab % Tl::TQ;
-    epi.store(ibase + a * 16, jbase + b * 16, acc[a][b]);
+    O4 v;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[e] = acc[a][b][4 * g + e];
+    epi.store(ibase + a * 32 + 8 * g, jbase + b * 32, v);
   };
-  Unroll<0, Tl::TP * Tl::TQ>::run(out);
+  Unroll<0, Tl::TP * Tl::TQ * 4>::run(out);
 }
 
 }  // namespace ohip

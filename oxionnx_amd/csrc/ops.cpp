@@ -83,6 +83,7 @@ struct ohip_ctx {
   int tile_override = 0;
   void* scratch = nullptr;
   size_t scratch_bytes = 0;
+  uint8_t* padtab = nullptr;  // 256 entries of 16 bytes: entry b is sixteen copies of byte b
   std::map<std::string, ohip_weight*> weights;
   std::vector<ohip_weight*> transients;  // freed with the context if never released
   ohip_counters counters{};
@@ -170,6 +171,18 @@ extern "C" int ohip_ctx_create(int device, ohip_ctx** out) {
     return hip_fail(e, "hipStreamCreate");
   }
   ctx->stream = ctx->own;
+  {
+    std::vector<uint8_t> tab(256 * 16);
+    for (int b = 0; b < 256; ++b) std::memset(tab.data() + b * 16, b, 16);
+    e = hipMalloc(&ctx->padtab, tab.size());
+    if (e == hipSuccess) e = hipMemcpy(ctx->padtab, tab.data(), tab.size(), hipMemcpyHostToDevice);
+    if (e != hipSuccess) {
+      if (ctx->padtab) (void)hipFree(ctx->padtab);
+      (void)hipStreamDestroy(ctx->own);
+      delete ctx;
+      return hip_fail(e, "pad table");
+    }
+  }
   ohip_tuning_for_class(OHIP_CLASS_MI355X, &ctx->tuning);
   *out = ctx;
   return OHIP_OK;
@@ -191,6 +204,7 @@ extern "C" void ohip_ctx_destroy(ohip_ctx* ctx) {
   for (auto& kv : ctx->weights) weight_free(kv.second);
   for (auto* w : ctx->transients) weight_free(w);
   if (ctx->scratch) (void)hipFree(ctx->scratch);
+  if (ctx->padtab) (void)hipFree(ctx->padtab);
   if (ctx->own) (void)hipStreamDestroy(ctx->own);
   delete ctx;
 }
@@ -211,7 +225,7 @@ extern "C" int ohip_sync(ohip_ctx* ctx) {
 
 extern "C" int ohip_set_tile_override(ohip_ctx* ctx, int tile_id) {
   if (!ctx) return fail(OHIP_E_INVALID, "null context");
-  if (tile_id < 0 || tile_id > 8) return fail(OHIP_E_INVALID, "tile id must be 0..8");
+  if (tile_id < 0 || tile_id > 6) return fail(OHIP_E_INVALID, "tile id must be 0..6");
   ctx->tile_override = tile_id;
   return OHIP_OK;
 }
@@ -720,6 +734,9 @@ static int ensure_comb(ohip_ctx* ctx, ohip_weight* w, float a_s, float y_s, int*
 // ------------------------------------------------------------------ helpers
 static bool aligned(const void* p, size_t a) { return ((uintptr_t)p % a) == 0; }
 
+// Device address of sixteen copies of byte b (the MFMA loaders' pad source).
+static const void* pad16(ohip_ctx* ctx, uint8_t b) { return ctx->padtab + (size_t)b * 16; }
+
 extern "C" int64_t ohip_conv_out_dim(int64_t in, int64_t pb, int64_t pe, int64_t k, int64_t d, int64_t s) {
   if (s <= 0 || k <= 0 || d <= 0 || in < 0 || pb < 0 || pe < 0) return -1;
   int64_t eff = (k - 1) * d + 1, padded = in + pb + pe;
@@ -766,18 +783,8 @@ extern "C" int ohip_gemm(ohip_ctx* ctx, const ohip_gemm_desc* d, const void* a, 
   const bool direct = rows_direct(a, K, lda, eb, d->trans_a);
   const bool gemv = M <= kMaxGemvM;
 
-  int splits = 1, cps = b->kc;
-  if (gemv) {
-    // enough (slice, row) waves to cover the chip several times over
-    const int64_t want_waves = 8192;
-    int64_t s = std::max<int64_t>(1, want_waves / std::max<int64_t>(1, N));
-    s = std::min<int64_t>(s, std::max<int64_t>(1, b->kc / 64));
-    cps = (int)((b->kc + s - 1) / s);
-    splits = (int)((b->kc + cps - 1) / cps);
-  }
   ScratchPlan plan;
   size_t ia = direct ? SIZE_MAX : plan.add((size_t)(M * kp) * eb);
-  size_t ip = gemv ? plan.add((size_t)splits * M * N * 4) : SIZE_MAX;
   rc = scratch_reserve(ctx, plan.total());
   if (rc) return rc;
 
@@ -806,12 +813,11 @@ extern "C" int ohip_gemm(ohip_ctx* ctx, const ohip_gemm_desc* d, const void* a, 
 
   hipError_t e;
   if (gemv) {
-    GemvArgs g{av.p, av.ld_bytes / eb, b->data, b->ld_bytes / eb, (int)M, (int)N, b->kc, splits, cps,
-               static_cast<float*>(scratch_at(ctx, plan, ip))};
+    GemvArgs g{av.p, av.ld_bytes / eb, b->data, b->ld_bytes / eb, (int)M, (int)N, b->kc};
     e = run_gemv(d->dtype, g, o, ctx->stream);
   } else {
-    DenseOperand x{b->data, b->ld_bytes, (int)N, b->kc, 0, 0u, 0u};
-    DenseOperand yv{av.p, av.ld_bytes, (int)M, av.kc, 0, 0u, 0u};
+    DenseOperand x{b->data, b->ld_bytes, (int)N, b->kc, 0, 0u, pad16(ctx, 0)};
+    DenseOperand yv{av.p, av.ld_bytes, (int)M, av.kc, 0, 0u, pad16(ctx, 0)};
     e = run_dense_float(d->dtype, x, yv, o, ctx->tile_override, ctx->stream);
   }
   if (e != hipSuccess) return hip_fail(e, "ohip_gemm launch");
@@ -874,8 +880,8 @@ extern "C" int ohip_conv2d(ohip_ctx* ctx, const ohip_conv_desc* d, const void* x
   col.KW = (int)d->kw; col.cpc = (int)(cp / ce);
   col.sh = (int)d->stride_h; col.sw = (int)d->stride_w; col.dh = (int)d->dil_h; col.dw = (int)d->dil_w;
   col.pt = (int)d->pad_t; col.pl = (int)d->pad_l; col.rows = (int)rows; col.kc = w->kc;
-  col.xor_mask = 0; col.pad = 0;
-  DenseOperand wt{w->data, w->ld_bytes, (int)d->cout, w->kc, 0, 0u, 0u};
+  col.xor_mask = 0; col.pad16 = pad16(ctx, 0);
+  DenseOperand wt{w->data, w->ld_bytes, (int)d->cout, w->kc, 0, 0u, pad16(ctx, 0)};
 
   FloatOut o{};
   o.y = y; o.alpha = 1.0f; o.beta = 1.0f; o.bias = bias;
@@ -960,8 +966,8 @@ extern "C" int ohip_qgemm(ohip_ctx* ctx, const ohip_qgemm_desc* d, const void* a
   o.w_on_i = 1; o.colsum = b->colsum; o.flip = b->flip; o.bias = nullptr;
   o.ca = shift - (d->a_zp ? d->a_zp[0] : 0); o.ca_rows = ca_rows;
   o.comb = b->comb; o.n_comb = n_comb; o.out_kind = d->out_kind; o.y_zp = d->y_zp; o.lo = d->lo; o.hi = d->hi;
-  DenseOperand x{b->data, b->ld_bytes, (int)N, b->kc, 0, 0u, 0u};
-  DenseOperand yv{pa, lda_b, (int)M, (int)(kp / 16), b->kwrap, u8 ? 0x80808080u : 0u, 0u};
+  DenseOperand x{b->data, b->ld_bytes, (int)N, b->kc, 0, 0u, pad16(ctx, 0)};
+  DenseOperand yv{pa, lda_b, (int)M, (int)(kp / 16), b->kwrap, u8 ? 0x80808080u : 0u, pad16(ctx, 0)};
   hipError_t e = run_dense_quant(x, yv, o, ctx->tile_override, ctx->stream);
   if (e != hipSuccess) return hip_fail(e, "ohip_qgemm launch");
   return OHIP_OK;
@@ -1010,8 +1016,9 @@ extern "C" int ohip_qconv2d(ohip_ctx* ctx, const ohip_qconv_desc* d, const void*
     return fail(OHIP_E_INVALID, "ohip_qconv2d: NHWC input must be 16-byte aligned");
   }
   // A padding tap stands for x == x_zp, i.e. (x_zp - shift) in the shifted
-  // int8 domain, so it contributes exactly zero after the ca correction.
-  const uint8_t padb = (uint8_t)(int8_t)(d->x_zp - shift);
+  // int8 domain, so it contributes exactly zero after the ca correction.  The
+  // pad source is read before the XOR, so it holds the raw byte x_zp.
+  const uint8_t padb = (uint8_t)(d->x_zp & 0xff);
   Im2colOperand col{};
   col.base = xin; col.H = (int)d->h; col.W = (int)d->w; col.OH = (int)g.oh; col.OW = (int)g.ow;
   col.KW = (int)d->kw; col.cpc = (int)(cp / 16);
@@ -1019,8 +1026,8 @@ extern "C" int ohip_qconv2d(ohip_ctx* ctx, const ohip_qconv_desc* d, const void*
   col.pt = (int)d->pad_t; col.pl = (int)d->pad_l; col.rows = (int)rows;
   col.kc = w->kwrap > 0 ? w->kwrap : w->kc; col.kwrap = w->kwrap;
   col.xor_mask = u8 ? 0x80808080u : 0u;
-  col.pad = padb * 0x01010101u;
-  DenseOperand wt{w->data, w->ld_bytes, (int)d->cout, w->kc, 0, 0u, 0u};
+  col.pad16 = pad16(ctx, padb);
+  DenseOperand wt{w->data, w->ld_bytes, (int)d->cout, w->kc, 0, 0u, pad16(ctx, 0)};
   QuantOut o{};
   o.y = y; o.colsum = w->colsum; o.flip = w->flip; o.bias = bias; o.ca = shift - d->x_zp; o.ca_rows = nullptr;
   o.comb = w->comb; o.n_comb = n_comb; o.out_kind = d->out_kind; o.y_zp = d->y_zp; o.lo = d->lo; o.hi = d->hi;
