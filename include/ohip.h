@@ -214,6 +214,12 @@ typedef struct {
     float x_scale, y_scale;
     int32_t y_zp, lo, hi;
     int in_layout, out_layout;
+    /* Optional host table of 256 bytes applied to every requantised byte
+     * (QOUT_U8 / QOUT_I8 only), indexed by the byte's bit pattern; NULL for
+     * none.  It carries a fused elementwise tail that maps quantised bytes
+     * to quantised bytes, e.g. DequantizeLinear -> Silu -> QuantizeLinear
+     * (indexing/quantize.rs:96-190, registry/nn_ops/activations.rs:477). */
+    const uint8_t* out_table;
 } ohip_qconv_desc;
 int ohip_qconv2d(ohip_ctx* ctx, const ohip_qconv_desc* d, const void* x, const ohip_weight* w,
                  const int32_t* bias_dev, void* y);

@@ -76,7 +76,7 @@ class QConvDesc(ctypes.Structure):
                [("x_dtype", ctypes.c_int), ("x_zp", ctypes.c_int32), ("out_kind", ctypes.c_int),
                 ("x_scale", ctypes.c_float), ("y_scale", ctypes.c_float), ("y_zp", ctypes.c_int32),
                 ("lo", ctypes.c_int32), ("hi", ctypes.c_int32), ("in_layout", ctypes.c_int),
-                ("out_layout", ctypes.c_int)]
+                ("out_layout", ctypes.c_int), ("out_table", VP)]
 
 
 class Attr(ctypes.Structure):

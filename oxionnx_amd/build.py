@@ -20,7 +20,7 @@ LIB = os.path.join(HERE, "libohip.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 
-SOURCES = ["contract_f32.hip", "contract_f16.hip", "contract_bf16.hip", "contract_i8.hip", "aux_kernels.hip", "ops.cpp", "dispatch.cpp"]
+SOURCES = ["contract_f32.hip", "contract_f16.hip", "contract_bf16.hip", "contract_i8.hip", "aux_kernels.hip", "nodes.hip", "ops.cpp", "dispatch.cpp"]
 
 FLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-ffp-contract=off",
@@ -35,7 +35,7 @@ def _compile(src, incremental=False):
     if incremental and os.path.exists(obj):
         kern = ["mfma_core.hpp", "launch.hpp", "internal.hpp"]
         local = {"ops.cpp": ["internal.hpp"], "dispatch.cpp": ["internal.hpp"],
-                 "aux_kernels.hip": kern}.get(src, kern + ["contract.inc"])
+                 "aux_kernels.hip": kern, "nodes.hip": ["internal.hpp"]}.get(src, kern + ["contract.inc"])
         deps = [os.path.join(CSRC, f) for f in [src] + local]
         if src.endswith(".cpp"):
             deps.append(os.path.join(ROOT, "include", "ohip.h"))

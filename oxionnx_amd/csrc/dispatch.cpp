@@ -17,6 +17,8 @@
 #include "../../include/ohip.h"
 #include "internal.hpp"
 
+int ohip_dtensor_alias_internal(const ohip_dtensor* src, int rank, const int64_t* shape, ohip_dtensor** out);
+
 namespace {
 
 thread_local std::string t_err;
@@ -323,7 +325,10 @@ void fused_act(const ohip_node* nd, int* act, float* lo, float* hi) {
   *lo = 0.0f;
   *hi = 0.0f;
   if (a == "relu") *act = OHIP_ACT_RELU;
-  else if (a == "clip") {
+  else if (a == "leaky_relu") {  // this provider's Conv + LeakyRelu fusion
+    *act = OHIP_ACT_LEAKY_RELU;
+    *lo = attr_f(nd, "activation_alpha", 0.01f);
+  } else if (a == "clip") {
     *act = OHIP_ACT_CLIP;
     *lo = attr_f(nd, "activation_min", -INFINITY);
     *hi = attr_f(nd, "activation_max", INFINITY);
@@ -530,6 +535,37 @@ int do_qmatmul(ohip_ctx* ctx, const ohip_node* nd, bool qlinear, int placement, 
 }
 
 // ------------------------------------------------------------------ integer Conv
+// The fused quantised tail DequantizeLinear -> Silu -> QuantizeLinear of a
+// QLinearConv output as a byte -> byte table.  Each entry is computed exactly
+// as the three reference nodes compute it, in f32 on the host:
+//   dequantize_linear_axis  (indexing/quantize.rs:162-190): (q - zp) * scale
+//   SiLUOp                  (registry/nn_ops/activations.rs:477-479): x / (1 + exp(-x))
+//   quantize_linear_axis    (indexing/quantize.rs:114-150): round_ties_even(x / s) + zp, clamped
+// so the table reproduces the unfused chain bit for bit.
+bool silu_table(const ohip_node* nd, bool in_signed, int32_t in_zp, float in_scale, uint8_t* table, int* out_dt) {
+  if (attr_s(nd, "activation") != "silu") return false;
+  const float ys = attr_f(nd, "activation_y_scale", NAN);
+  const int64_t yz = attr_i(nd, "activation_y_zero_point", 0);
+  if (!std::isfinite(ys) || ys == 0.0f) return false;
+  std::string ydt = attr_s(nd, "activation_y_dtype");
+  bool u8 = yz > 127;
+  if (ydt == "uint8") u8 = true;
+  else if (ydt == "int8") u8 = false;
+  const float lo = u8 ? 0.0f : -128.0f, hi = u8 ? 255.0f : 127.0f;
+  for (int b = 0; b < 256; ++b) {
+    const int32_t q = in_signed ? (int32_t)(int8_t)b : b;
+    const float x = ((float)q - (float)in_zp) * in_scale;
+    const float s = x / (1.0f + std::exp(-x));
+    float v = s / ys;
+    float r = std::isfinite(v) ? std::nearbyint(v) : v;
+    float o = r + (float)yz;
+    o = o < lo ? lo : (o > hi ? hi : o);
+    table[b] = (uint8_t)((int32_t)o & 0xff);
+  }
+  *out_dt = u8 ? OHIP_U8 : OHIP_I8;
+  return true;
+}
+
 int do_qconv(ohip_ctx* ctx, const ohip_node* nd, bool qlinear, int placement, ohip_output* out) {
   // QLinearConv: x, x_scale, x_zp, w, w_scale, w_zp, y_scale, y_zp, B
   // ConvInteger: x, w, x_zp, w_zp
@@ -538,7 +574,9 @@ int do_qconv(ohip_ctx* ctx, const ohip_node* nd, bool qlinear, int placement, oh
   const ohip_tensor* xzp_t = input(nd, 2);
   const ohip_tensor* wzp_t = input(nd, qlinear ? 5 : 3);
   const ohip_tensor* bias = qlinear ? input(nd, 8) : nullptr;
-  if (!x || !w || !host_only(x) || !host_only(w)) return decline("integer Conv: operands must be host tensors");
+  if (!x || !w || !host_only(w)) return decline("integer Conv: the filter must be a host tensor");
+  if (x->device && (x->dtype != OHIP_U8 && x->dtype != OHIP_I8)) return decline("integer Conv: resident X must be bytes");
+  if (x->device && ohip_dtensor_layout(x->device) != OHIP_NCHW) return decline("integer Conv: resident input layout");
   Geo g;
   std::string why;
   if (!conv_geometry(nd, x, w, &g, &why)) return decline(why);
@@ -574,12 +612,32 @@ int do_qconv(ohip_ctx* ctx, const ohip_node* nd, bool qlinear, int placement, oh
       bias_i.push_back(v);
     }
   }
+  // Output form: the requantised bytes when the caller keeps the result on
+  // the device and the range is one byte type, else the reference's f32 lanes.
+  int out_kind = qlinear ? OHIP_QOUT_F32 : OHIP_QOUT_I32;
+  int out_dt = qlinear ? OHIP_F32 : OHIP_I32;
+  if (qlinear && placement == OHIP_PLACE_DEVICE) {
+    if (lo == 0 && hi == 255) { out_kind = OHIP_QOUT_U8; out_dt = OHIP_U8; }
+    else if (lo == -128 && hi == 127) { out_kind = OHIP_QOUT_I8; out_dt = OHIP_I8; }
+  }
+  uint8_t table[256];
+  bool fused = false;
+  if (!attr_s(nd, "activation").empty()) {
+    if (!qlinear || (out_kind != OHIP_QOUT_U8 && out_kind != OHIP_QOUT_I8))
+      return decline("integer Conv: a fused tail needs a resident byte output");
+    int tdt;
+    if (!silu_table(nd, out_kind == OHIP_QOUT_I8, yzp[0], ys, table, &tdt)) return decline("integer Conv: fused tail");
+    fused = true;
+    out_dt = tdt;
+  }
   ohip_tuning tun;
   ohip_get_tuning(ctx, &tun);
   if (!ohip_conv_admits(&tun, g.cout, g.c * g.kh * g.kw, g.n * g.oh * g.ow)) return decline("integer Conv: gate");
   std::vector<uint8_t> xb, wb;
   int xdt, wdt;
-  if (!to_bytes(x, xb, &xdt) || !to_bytes(w, wb, &wdt)) return decline("integer Conv: lanes outside 8 bits");
+  if (x->device) xdt = x->dtype;
+  else if (!to_bytes(x, xb, &xdt)) return decline("integer Conv: lanes outside 8 bits");
+  if (!to_bytes(w, wb, &wdt)) return decline("integer Conv: lanes outside 8 bits");
   const bool cache = w->is_initializer && w->name && *w->name;
   std::string name = wkey_name(w), label = std::string(qlinear ? "QLinearConv.W" : "ConvInteger.W");
   ohip_weight_key key{name.c_str(), label.c_str()};
@@ -588,19 +646,583 @@ int do_qconv(ohip_ctx* ctx, const ohip_node* nd, bool qlinear, int placement, oh
                              (int)wzp.size(), qlinear ? ws.data() : nullptr, qlinear ? (int)ws.size() : 0, &wt);
   if (rc) return rc;
   Stage st(ctx);
-  const void* xd = st.operand(x, xb.data(), xb.size());
+  const void* xd = x->device ? ohip_dtensor_ptr(x->device) : st.operand(x, xb.data(), xb.size());
   const void* bd = bias ? st.operand(bias, bias_i.data(), bias_i.size() * 4) : nullptr;
-  const size_t obytes = (size_t)(g.n * g.cout * g.oh * g.ow) * 4;
+  const size_t ob = (out_kind == OHIP_QOUT_U8 || out_kind == OHIP_QOUT_I8) ? 1 : 4;
+  const size_t obytes = (size_t)(g.n * g.cout * g.oh * g.ow) * ob;
   void* yd = st.alloc(obytes);
   if (!xd || !yd || (bias && !bd)) { if (!cache) ohip_weight_release(wt); return OHIP_E_NOMEM; }
   ohip_qconv_desc d{g.n, g.c, g.h, g.w, g.cout, g.kh, g.kw, 1, g.sh, g.sw, g.dh, g.dw, g.pt, g.pl, g.pb, g.pr,
-                    xdt, xzp[0], qlinear ? OHIP_QOUT_F32 : OHIP_QOUT_I32, xs, ys, qlinear ? yzp[0] : 0, lo, hi,
-                    OHIP_NCHW, OHIP_NCHW};
+                    xdt, xzp[0], out_kind, xs, ys, qlinear ? yzp[0] : 0, lo, hi,
+                    OHIP_NCHW, OHIP_NCHW, fused ? table : nullptr};
   rc = ohip_qconv2d(ctx, &d, xd, wt, static_cast<const int32_t*>(bd), yd);
   if (!cache) ohip_weight_release(wt);
   if (rc) return rc;
-  set_out(out, qlinear ? OHIP_F32 : OHIP_I32, conv_out_shape(g));
-  return finish_output(ctx, st, placement, out, yd, obytes, qlinear ? OHIP_F32 : OHIP_I32);
+  set_out(out, out_dt, conv_out_shape(g));
+  return finish_output(ctx, st, placement, out, yd, obytes, out_dt);
+}
+
+// ================================================================== memory-bound nodes
+// Counterparts of the reference CUDA provider's elementwise / broadcast /
+// norm / pool / resize / pad / slice / concat / alias arms
+// (oxionnx-cuda/src/lib.rs:101-119), plus the quantise / dequantise pair of a
+// QDQ graph.  Float nodes run in the input's storage type (f32 or f16, f32
+// arithmetic); quantised activations stay bytes on the device.
+
+bool is_float_dt(int dt) { return dt == OHIP_F32 || dt == OHIP_F16; }
+
+// The storage type a node computes in: the first resident float input's
+// dtype, else f32 (host tensors are f32 lanes).
+int node_float_dtype(const ohip_node* nd) {
+  for (int i = 0; i < nd->n_inputs; ++i) {
+    const ohip_tensor* t = input(nd, i);
+    if (t && t->device) return t->dtype;
+  }
+  for (int i = 0; i < nd->n_inputs; ++i) {
+    const ohip_tensor* t = input(nd, i);
+    if (t && t->dtype == OHIP_F16) return OHIP_F16;
+  }
+  return OHIP_F32;
+}
+
+// Device pointer of a float operand in storage type dt: the resident buffer
+// (which must already be dt), or a converted upload of a host tensor.
+const void* float_operand(Stage& st, const ohip_tensor* t, int dt) {
+  if (t->device) return t->dtype == dt ? ohip_dtensor_ptr(t->device) : nullptr;
+  if (t->dtype == dt) return st.operand(t);
+  const int64_t n = numel(t);
+  std::vector<char> buf((size_t)n * ebytes(dt));
+  for (int64_t i = 0; i < n; ++i) put_elem(dt, buf.data(), i, host_at(t, i));
+  return st.operand(t, buf.data(), buf.size());
+}
+
+std::vector<int64_t> shape_of(const ohip_tensor* t) { return std::vector<int64_t>(t->shape, t->shape + t->rank); }
+
+// Host int64 lanes of a small shape-like input (pads, starts, axes, ...).
+bool host_ints(const ohip_tensor* t, std::vector<int64_t>& out) {
+  out.clear();
+  if (!t) return true;
+  if (!host_only(t)) return false;
+  for (int64_t i = 0; i < numel(t); ++i) {
+    const double v = host_at(t, i);
+    if (!std::isfinite(v)) return false;
+    out.push_back((int64_t)v);
+  }
+  return true;
+}
+
+int output_device(ohip_ctx* ctx, Stage& st, int placement, ohip_output* out, int dt, const std::vector<int64_t>& shape,
+                  void* yd, size_t bytes) {
+  // Host placement returns the reference Tensor's f32 lanes.
+  set_out(out, dt, shape);
+  if (placement == OHIP_PLACE_DEVICE || dt == OHIP_F32) return finish_output(ctx, st, placement, out, yd, bytes, dt);
+  std::vector<uint8_t> raw(bytes);
+  int rc = ohip_memcpy_d2h(ctx, raw.data(), yd, bytes);
+  if (rc) return rc;
+  const int64_t n = bytes / std::max(1, ebytes(dt));
+  float* f = static_cast<float*>(std::malloc((size_t)std::max<int64_t>(n, 1) * 4));
+  if (!f) return OHIP_E_NOMEM;
+  ohip_tensor view{};
+  view.dtype = dt;
+  view.data = raw.data();
+  for (int64_t i = 0; i < n; ++i) f[i] = (float)host_at(&view, i);
+  out->dtype = OHIP_F32;
+  out->data = f;
+  return OHIP_OK;
+}
+
+// ---------------------------------------------------------------- unary
+int do_unary(ohip_ctx* ctx, const ohip_node* nd, int op, int placement, ohip_output* out) {
+  const ohip_tensor* x = input(nd, 0);
+  if (!x) return decline("unary: missing input");
+  const int dt = node_float_dtype(nd);
+  if (!is_float_dt(dt)) return decline("unary: dtype");
+  float alpha = 0.0f;
+  if (op == ohip::UN_LEAKY_RELU) alpha = attr_f(nd, "alpha", 0.01f);
+  Stage st(ctx);
+  const void* xd = float_operand(st, x, dt);
+  const int64_t n = numel(x);
+  const size_t bytes = (size_t)n * ebytes(dt);
+  void* yd = st.alloc(bytes);
+  if (!xd || !yd) return OHIP_E_NOMEM;
+  hipError_t e = ohip::run_unary(dt, xd, yd, n, op, alpha, (hipStream_t)ohip_ctx_stream(ctx));
+  if (e != hipSuccess) return OHIP_E_HIP;
+  return output_device(ctx, st, placement, out, dt, shape_of(x), yd, bytes);
+}
+
+// ---------------------------------------------------------------- binary (numpy broadcasting)
+int do_binary(ohip_ctx* ctx, const ohip_node* nd, int op, int placement, ohip_output* out) {
+  const ohip_tensor *a = input(nd, 0), *b = input(nd, 1);
+  if (!a || !b) return decline("binary: missing input");
+  const int dt = node_float_dtype(nd);
+  if (!is_float_dt(dt)) return decline("binary: dtype");
+  const int rank = std::max(a->rank, b->rank);
+  if (rank > ohip::kMaxRank) return decline("binary: rank");
+  ohip::BcastPlan p{};
+  p.rank = rank;
+  int64_t sa = 1, sb = 1, n = 1;
+  std::vector<int64_t> oshape((size_t)rank);
+  for (int d = 0; d < rank; ++d) {
+    const int slot = ohip::kMaxRank - 1 - d;
+    const int ia = a->rank - 1 - d, ib = b->rank - 1 - d;
+    const int64_t ea = ia >= 0 ? a->shape[ia] : 1, eb = ib >= 0 ? b->shape[ib] : 1;
+    if (ea != eb && ea != 1 && eb != 1) return decline("binary: shapes do not broadcast");
+    const int64_t e = ea == 1 ? eb : ea;
+    p.shape[slot] = e;
+    p.sa[slot] = ea == 1 ? 0 : sa;
+    p.sb[slot] = eb == 1 ? 0 : sb;
+    sa *= ea;
+    sb *= eb;
+    n *= e;
+    oshape[(size_t)(rank - 1 - d)] = e;
+  }
+  const bool same = numel(a) == n && numel(b) == n;
+  Stage st(ctx);
+  const void* ad = float_operand(st, a, dt);
+  const void* bd = float_operand(st, b, dt);
+  const size_t bytes = (size_t)n * ebytes(dt);
+  void* yd = st.alloc(bytes);
+  if (!ad || !bd || !yd) return ad && bd ? OHIP_E_NOMEM : decline("binary: resident operand dtype");
+  hipError_t e = ohip::run_binary(dt, ad, bd, yd, n, p, same, op, (hipStream_t)ohip_ctx_stream(ctx));
+  if (e != hipSuccess) return OHIP_E_HIP;
+  return output_device(ctx, st, placement, out, dt, oshape, yd, bytes);
+}
+
+// ---------------------------------------------------------------- instance normalisation
+// OxiInstanceNorm (registry/oxi_instance_norm.rs:135-146): no affine term.
+// InstanceNormalization (nn/normalization.rs:251-280): per-channel scale, B.
+int do_instnorm(ohip_ctx* ctx, const ohip_node* nd, bool affine, int placement, ohip_output* out) {
+  const ohip_tensor* x = input(nd, 0);
+  if (!x || x->rank < 3) return decline("InstanceNorm: rank < 3");
+  const int dt = node_float_dtype(nd);
+  if (!is_float_dt(dt)) return decline("InstanceNorm: dtype");
+  const int64_t N = x->shape[0], C = x->shape[1];
+  int64_t spatial = 1;
+  for (int i = 2; i < x->rank; ++i) spatial *= x->shape[i];
+  if (spatial == 0 || N * C == 0) return decline("InstanceNorm: empty");
+  const float eps = attr_f(nd, "epsilon", 1e-5f);
+  Stage st(ctx);
+  ohip::NormAffine aff{nullptr, nullptr, 0, ohip::UN_IDENTITY, 0.0f};
+  std::vector<float> sc, bi;
+  if (affine) {
+    const ohip_tensor *s = input(nd, 1), *b = input(nd, 2);
+    if (!s || !b || !host_only(s) || !host_only(b) || numel(s) != C || numel(b) != C)
+      return decline("InstanceNormalization: scale / B");
+    for (int64_t i = 0; i < C; ++i) { sc.push_back((float)host_at(s, i)); bi.push_back((float)host_at(b, i)); }
+    aff.scale = static_cast<const float*>(st.operand(s, sc.data(), sc.size() * 4));
+    aff.bias = static_cast<const float*>(st.operand(b, bi.data(), bi.size() * 4));
+    if (!aff.scale || !aff.bias) return OHIP_E_NOMEM;
+  }
+  const void* xd = float_operand(st, x, dt);
+  const size_t bytes = (size_t)numel(x) * ebytes(dt);
+  void* yd = st.alloc(bytes);
+  if (!xd || !yd) return OHIP_E_NOMEM;
+  hipError_t e = ohip::run_instnorm(dt, xd, yd, N * C, spatial, (int)C, eps, aff, (hipStream_t)ohip_ctx_stream(ctx));
+  if (e != hipSuccess) return OHIP_E_HIP;
+  return output_device(ctx, st, placement, out, dt, shape_of(x), yd, bytes);
+}
+
+// ---------------------------------------------------------------- Resize (nearest, rank 4)
+// resolve_plan's scales branch (resize.rs:372-420): out = floor(in * scale)
+// in f32; only H and W may change.
+int do_resize(ohip_ctx* ctx, const ohip_node* nd, int placement, ohip_output* out) {
+  const ohip_tensor* x = input(nd, 0);
+  if (!x || x->rank != 4) return decline("Resize: rank 4 only");
+  if (attr_s(nd, "mode") != "nearest") return decline("Resize: nearest only");
+  if (find_attr(nd, "axes")) return decline("Resize: axes");
+  const ohip_tensor* scales = nd->n_inputs >= 3 ? input(nd, 2) : input(nd, 1);
+  if (nd->n_inputs >= 4 && input(nd, 3)) return decline("Resize: sizes");
+  if (!scales || !host_only(scales) || numel(scales) != 4) return decline("Resize: scales");
+  float s[4];
+  for (int i = 0; i < 4; ++i) s[i] = (float)host_at(scales, i);
+  if (s[0] != 1.0f || s[1] != 1.0f || !(s[2] > 0.0f) || !(s[3] > 0.0f) || !std::isfinite(s[2]) || !std::isfinite(s[3]))
+    return decline("Resize: N / C scales");
+  std::string cm = attr_s(nd, "coordinate_transformation_mode"), nm = attr_s(nd, "nearest_mode");
+  ohip::ResizePlan p{};
+  if (cm.empty() || cm == "half_pixel") p.coord = ohip::RZ_HALF_PIXEL;
+  else if (cm == "asymmetric") p.coord = ohip::RZ_ASYMMETRIC;
+  else if (cm == "align_corners") p.coord = ohip::RZ_ALIGN_CORNERS;
+  else if (cm == "pytorch_half_pixel") p.coord = ohip::RZ_PYTORCH_HALF_PIXEL;
+  else if (cm == "tf_half_pixel_for_nn") p.coord = ohip::RZ_TF_HALF_PIXEL_FOR_NN;
+  else return decline("Resize: coordinate_transformation_mode");
+  if (nm.empty() || nm == "round_prefer_floor") p.rule = ohip::RZ_ROUND_PREFER_FLOOR;
+  else if (nm == "round_prefer_ceil") p.rule = ohip::RZ_ROUND_PREFER_CEIL;
+  else if (nm == "floor") p.rule = ohip::RZ_FLOOR;
+  else if (nm == "ceil") p.rule = ohip::RZ_CEIL;
+  else return decline("Resize: nearest_mode");
+  p.ih = (int)x->shape[2]; p.iw = (int)x->shape[3];
+  p.oh = (int)std::floor((float)x->shape[2] * s[2]);
+  p.ow = (int)std::floor((float)x->shape[3] * s[3]);
+  p.sh = s[2]; p.sw = s[3];
+  if (p.ih <= 0 || p.iw <= 0 || p.oh <= 0 || p.ow <= 0) return decline("Resize: empty");
+  const int dt = x->device ? x->dtype : OHIP_F32;
+  const int eb = ebytes(dt);
+  Stage st(ctx);
+  const void* xd = st.operand(x);
+  const int64_t planes = x->shape[0] * x->shape[1];
+  const size_t bytes = (size_t)(planes * p.oh * p.ow) * eb;
+  void* yd = st.alloc(bytes);
+  if (!xd || !yd) return OHIP_E_NOMEM;
+  hipError_t e = ohip::run_resize_nearest(eb, xd, yd, planes, p, (hipStream_t)ohip_ctx_stream(ctx));
+  if (e != hipSuccess) return OHIP_E_HIP;
+  return output_device(ctx, st, placement, out, dt, {x->shape[0], x->shape[1], p.oh, p.ow}, yd, bytes);
+}
+
+// ---------------------------------------------------------------- Pad
+int do_pad(ohip_ctx* ctx, const ohip_node* nd, int placement, ohip_output* out) {
+  const ohip_tensor* x = input(nd, 0);
+  if (!x || x->rank < 1 || x->rank > ohip::kMaxRank) return decline("Pad: rank");
+  std::vector<int64_t> pads;
+  if (nd->n_inputs >= 2 && input(nd, 1)) {
+    if (!host_ints(input(nd, 1), pads)) return decline("Pad: pads must be a host tensor");
+  } else {
+    pads = attr_ints(nd, "pads");
+  }
+  if (nd->n_inputs >= 4 && input(nd, 3)) return decline("Pad: axes");
+  if ((int)pads.size() != 2 * x->rank) return decline("Pad: pads length");
+  for (auto v : pads) if (v < 0) return decline("Pad: negative pads");
+  std::string mode = attr_s(nd, "mode");
+  ohip::PadPlan p{};
+  p.rank = x->rank;
+  if (mode.empty() || mode == "constant") p.mode = ohip::PAD_CONSTANT;
+  else if (mode == "reflect") p.mode = ohip::PAD_REFLECT;
+  else if (mode == "edge") p.mode = ohip::PAD_EDGE;
+  else if (mode == "wrap") p.mode = ohip::PAD_WRAP;
+  else return decline("Pad: mode");
+  const int dt = x->device ? x->dtype : OHIP_F32;
+  const int eb = ebytes(dt);
+  double value = 0.0;
+  if (nd->n_inputs >= 3 && input(nd, 2)) {
+    const ohip_tensor* cv = input(nd, 2);
+    if (!host_only(cv) || numel(cv) < 1) return decline("Pad: constant_value");
+    value = host_at(cv, 0);
+  } else if (find_attr(nd, "value")) {
+    value = attr_f(nd, "value", 0.0f);
+  }
+  {
+    uint32_t bits = 0;
+    if (dt == OHIP_U8 || dt == OHIP_I8) bits = (uint32_t)((int32_t)std::nearbyint(value) & 0xff);
+    else { char tmp[4] = {0}; put_elem(dt, tmp, 0, value); std::memcpy(&bits, tmp, (size_t)eb); }
+    p.value_bits = bits;
+  }
+  std::vector<int64_t> oshape((size_t)x->rank);
+  int64_t n = 1;
+  for (int d = 0; d < x->rank; ++d) {
+    p.in[d] = x->shape[d];
+    p.begin[d] = pads[(size_t)d];
+    p.out[d] = x->shape[d] + pads[(size_t)d] + pads[(size_t)(d + x->rank)];
+    if (p.mode != ohip::PAD_CONSTANT && p.in[d] == 0 && p.out[d] > 0) return decline("Pad: empty axis");
+    if (p.mode == ohip::PAD_REFLECT && (pads[(size_t)d] >= p.in[d] || pads[(size_t)(d + x->rank)] >= p.in[d]) &&
+        p.in[d] > 1)
+      return decline("Pad: reflect pad wider than the axis");
+    oshape[(size_t)d] = p.out[d];
+    n *= p.out[d];
+  }
+  Stage st(ctx);
+  const void* xd = st.operand(x);
+  const size_t bytes = (size_t)n * eb;
+  void* yd = st.alloc(bytes);
+  if (!xd || !yd) return OHIP_E_NOMEM;
+  hipError_t e = ohip::run_pad(eb, xd, yd, n, p, (hipStream_t)ohip_ctx_stream(ctx));
+  if (e != hipSuccess) return OHIP_E_HIP;
+  return output_device(ctx, st, placement, out, dt, oshape, yd, bytes);
+}
+
+// ---------------------------------------------------------------- MaxPool (2-D)
+// PoolGeometry::resolve + pool_out_dim (conv/pooling.rs:44-90,
+// conv/spatial.rs:272-322); dilations, ceil_mode and auto_pad honoured.
+int do_maxpool(ohip_ctx* ctx, const ohip_node* nd, int placement, ohip_output* out) {
+  const ohip_tensor* x = input(nd, 0);
+  if (!x || x->rank != 4) return decline("MaxPool: 2-D only");
+  if (attr_i(nd, "storage_order", 0) != 0) return decline("MaxPool: storage_order");
+  auto ks = attr_ints(nd, "kernel_shape"), strides = attr_ints(nd, "strides"), pads = attr_ints(nd, "pads"),
+       dil = attr_ints(nd, "dilations");
+  if (ks.size() != 2) return decline("MaxPool: kernel_shape");
+  if (strides.empty()) strides = {1, 1};
+  if (dil.empty()) dil = {1, 1};
+  if (pads.empty()) pads = {0, 0, 0, 0};
+  if (strides.size() != 2 || dil.size() != 2 || pads.size() != 4) return decline("MaxPool: attribute rank");
+  for (auto v : ks) if (v <= 0) return decline("MaxPool: kernel");
+  for (auto v : strides) if (v <= 0) return decline("MaxPool: stride");
+  for (auto v : dil) if (v <= 0) return decline("MaxPool: dilation");
+  for (auto v : pads) if (v < 0) return decline("MaxPool: pads");
+  const bool ceil_mode = attr_i(nd, "ceil_mode", 0) != 0;
+  const int64_t ih = x->shape[2], iw = x->shape[3];
+  std::string ap = attr_s(nd, "auto_pad");
+  if (ap == "VALID") pads = {0, 0, 0, 0};
+  else if (ap == "SAME_UPPER" || ap == "SAME_LOWER") {
+    for (int a = 0; a < 2; ++a) {
+      const int64_t in = a ? iw : ih;
+      const int64_t o = (in + strides[(size_t)a] - 1) / strides[(size_t)a];
+      const int64_t eff = (ks[(size_t)a] - 1) * dil[(size_t)a] + 1;
+      const int64_t need = std::max<int64_t>(0, (o - 1) * strides[(size_t)a] + eff - in), half = need / 2;
+      pads[(size_t)a] = ap == "SAME_LOWER" ? need - half : half;
+      pads[(size_t)(a + 2)] = need - pads[(size_t)a];
+    }
+  } else if (!(ap.empty() || ap == "NOTSET")) {
+    return decline("MaxPool: auto_pad");
+  }
+  auto out_dim = [&](int64_t in, int64_t pb, int64_t pe, int64_t k, int64_t d, int64_t s) -> int64_t {
+    const int64_t eff = (k - 1) * d + 1, padded = in + pb + pe;
+    if (padded < eff) return -1;
+    const int64_t span = padded - eff;
+    int64_t o = ceil_mode ? (span + s - 1) / s + 1 : span / s + 1;
+    if (ceil_mode && o > 1 && (o - 1) * s >= in + pb) o -= 1;
+    return o;
+  };
+  const int64_t oh = out_dim(ih, pads[0], pads[2], ks[0], dil[0], strides[0]);
+  const int64_t ow = out_dim(iw, pads[1], pads[3], ks[1], dil[1], strides[1]);
+  if (oh <= 0 || ow <= 0) return decline("MaxPool: output extent");
+  const int dt = x->device ? x->dtype : OHIP_F32;
+  ohip::PoolPlan p{(int)ih, (int)iw, (int)oh, (int)ow, (int)ks[0], (int)ks[1], (int)strides[0], (int)strides[1],
+                   (int)pads[0], (int)pads[1], (int)dil[0], (int)dil[1]};
+  Stage st(ctx);
+  const void* xd = st.operand(x);
+  const int64_t planes = x->shape[0] * x->shape[1];
+  const size_t bytes = (size_t)(planes * oh * ow) * ebytes(dt);
+  void* yd = st.alloc(bytes);
+  if (!xd || !yd) return OHIP_E_NOMEM;
+  hipError_t e = ohip::run_maxpool(dt, xd, yd, planes, p, (hipStream_t)ohip_ctx_stream(ctx));
+  if (e != hipSuccess) return e == hipErrorInvalidValue ? decline("MaxPool: dtype") : OHIP_E_HIP;
+  return output_device(ctx, st, placement, out, dt, {x->shape[0], x->shape[1], oh, ow}, yd, bytes);
+}
+
+// ---------------------------------------------------------------- Concat (device copies)
+int do_concat(ohip_ctx* ctx, const ohip_node* nd, int placement, ohip_output* out) {
+  if (nd->n_inputs < 1) return decline("Concat: no inputs");
+  const ohip_tensor* t0 = input(nd, 0);
+  if (!t0) return decline("Concat: missing input");
+  const int rank = t0->rank;
+  int64_t axis = attr_i(nd, "axis", 0);
+  if (axis < 0) axis += rank;
+  if (axis < 0 || axis >= rank) return decline("Concat: axis");
+  int dt = -1;
+  for (int i = 0; i < nd->n_inputs; ++i) {
+    const ohip_tensor* t = input(nd, i);
+    if (t && t->device) { dt = t->dtype; break; }
+  }
+  if (dt < 0) dt = OHIP_F32;
+  const int eb = ebytes(dt);
+  std::vector<int64_t> oshape = shape_of(t0);
+  oshape[(size_t)axis] = 0;
+  int64_t outer = 1, inner = 1;
+  for (int d = 0; d < axis; ++d) outer *= t0->shape[d];
+  for (int d = axis + 1; d < rank; ++d) inner *= t0->shape[d];
+  for (int i = 0; i < nd->n_inputs; ++i) {
+    const ohip_tensor* t = input(nd, i);
+    if (!t || t->rank != rank) return decline("Concat: rank");
+    for (int d = 0; d < rank; ++d)
+      if (d != axis && t->shape[d] != t0->shape[d]) return decline("Concat: shapes");
+    if (t->device && t->dtype != dt) return decline("Concat: mixed dtypes");
+    if (!t->device && dt != OHIP_F32) return decline("Concat: host operand beside byte tensors");
+    oshape[(size_t)axis] += t->shape[axis];
+  }
+  Stage st(ctx);
+  const size_t row = (size_t)(oshape[(size_t)axis] * inner * eb);
+  const size_t bytes = (size_t)outer * row;
+  void* yd = st.alloc(bytes);
+  if (!yd) return OHIP_E_NOMEM;
+  hipStream_t s = (hipStream_t)ohip_ctx_stream(ctx);
+  size_t off = 0;
+  for (int i = 0; i < nd->n_inputs; ++i) {
+    const ohip_tensor* t = input(nd, i);
+    const void* td = st.operand(t);
+    if (!td) return OHIP_E_NOMEM;
+    const size_t w = (size_t)(t->shape[axis] * inner * eb);
+    if (w && outer)
+      if (hipMemcpy2DAsync(static_cast<char*>(yd) + off, row, td, w, w, (size_t)outer, hipMemcpyDeviceToDevice, s) !=
+          hipSuccess)
+        return OHIP_E_HIP;
+    off += w;
+  }
+  return output_device(ctx, st, placement, out, dt, oshape, yd, bytes);
+}
+
+// ---------------------------------------------------------------- Slice (positive steps)
+int do_slice(ohip_ctx* ctx, const ohip_node* nd, int placement, ohip_output* out) {
+  const ohip_tensor* x = input(nd, 0);
+  if (!x || x->rank < 1 || x->rank > ohip::kMaxRank) return decline("Slice: rank");
+  std::vector<int64_t> starts, ends, axes, steps;
+  if (nd->n_inputs >= 3) {
+    if (!host_ints(input(nd, 1), starts) || !host_ints(input(nd, 2), ends) ||
+        !host_ints(nd->n_inputs >= 4 ? input(nd, 3) : nullptr, axes) ||
+        !host_ints(nd->n_inputs >= 5 ? input(nd, 4) : nullptr, steps))
+      return decline("Slice: parameters must be host tensors");
+  } else {
+    starts = attr_ints(nd, "starts");
+    ends = attr_ints(nd, "ends");
+    axes = attr_ints(nd, "axes");
+  }
+  if (starts.size() != ends.size()) return decline("Slice: starts / ends");
+  if (axes.empty()) for (size_t i = 0; i < starts.size(); ++i) axes.push_back((int64_t)i);
+  if (steps.empty()) steps.assign(starts.size(), 1);
+  if (axes.size() != starts.size() || steps.size() != starts.size()) return decline("Slice: lengths");
+  ohip::SlicePlan p{};
+  p.rank = x->rank;
+  int64_t stride = 1;
+  for (int d = x->rank - 1; d >= 0; --d) {
+    p.in_stride[d] = stride;
+    stride *= x->shape[d];
+    p.start[d] = 0;
+    p.step[d] = 1;
+    p.out[d] = x->shape[d];
+  }
+  for (size_t i = 0; i < starts.size(); ++i) {
+    int64_t a = axes[i] < 0 ? axes[i] + x->rank : axes[i];
+    if (a < 0 || a >= x->rank) return decline("Slice: axis");
+    if (steps[i] <= 0) return decline("Slice: non-positive step");
+    const int64_t dim = x->shape[a];
+    int64_t s = starts[i], e = ends[i];
+    if (s < 0) s += dim;
+    if (e < 0) e += dim;
+    s = std::min(std::max<int64_t>(s, 0), dim);
+    e = std::min(std::max<int64_t>(e, 0), dim);
+    p.start[a] = s;
+    p.step[a] = steps[i];
+    p.out[a] = e > s ? (e - s + steps[i] - 1) / steps[i] : 0;
+  }
+  std::vector<int64_t> oshape(p.out, p.out + x->rank);
+  int64_t n = 1;
+  for (auto v : oshape) n *= v;
+  const int dt = x->device ? x->dtype : OHIP_F32;
+  const int eb = ebytes(dt);
+  Stage st(ctx);
+  const void* xd = st.operand(x);
+  const size_t bytes = (size_t)n * eb;
+  void* yd = st.alloc(bytes);
+  if (!xd || !yd) return OHIP_E_NOMEM;
+  hipError_t e = ohip::run_slice(eb, xd, yd, n, p, (hipStream_t)ohip_ctx_stream(ctx));
+  if (e != hipSuccess) return OHIP_E_HIP;
+  return output_device(ctx, st, placement, out, dt, oshape, yd, bytes);
+}
+
+// ---------------------------------------------------------------- shape aliases
+// Reshape / Flatten / Squeeze / Unsqueeze of a resident tensor: the output
+// shares the input's buffer (oxionnx-cuda's CudaDeviceTensor::alias); a host
+// input is declined (the CPU op is a free relabel).
+int do_alias(ohip_ctx* ctx, const ohip_node* nd, const std::string& op, int placement, ohip_output* out) {
+  const ohip_tensor* x = input(nd, 0);
+  if (!x || !x->device || placement != OHIP_PLACE_DEVICE) return decline(op + ": host operand");
+  std::vector<int64_t> in = shape_of(x), o;
+  int64_t total = 1;
+  for (auto v : in) total *= v;
+  if (op == "Reshape") {
+    std::vector<int64_t> sh;
+    if (!host_ints(input(nd, 1), sh)) return decline("Reshape: shape must be a host tensor");
+    const bool allowzero = attr_i(nd, "allowzero", 0) != 0;
+    int64_t known = 1;
+    int infer = -1;
+    for (size_t i = 0; i < sh.size(); ++i) {
+      int64_t v = sh[i];
+      if (v == 0 && !allowzero) { if (i >= in.size()) return decline("Reshape: 0 past rank"); v = in[i]; }
+      if (v == -1) { if (infer >= 0) return decline("Reshape: two -1"); infer = (int)i; o.push_back(1); continue; }
+      if (v < 0) return decline("Reshape: negative extent");
+      o.push_back(v);
+      known *= v;
+    }
+    if (infer >= 0) { if (known == 0 || total % known) return decline("Reshape: -1"); o[(size_t)infer] = total / known; }
+  } else if (op == "Flatten") {
+    int64_t axis = attr_i(nd, "axis", 1);
+    if (axis < 0) axis += (int64_t)in.size();
+    if (axis < 0 || axis > (int64_t)in.size()) return decline("Flatten: axis");
+    int64_t a = 1;
+    for (int64_t i = 0; i < axis; ++i) a *= in[(size_t)i];
+    o = {a, a ? total / a : 0};
+  } else {
+    std::vector<int64_t> axes;
+    if (nd->n_inputs >= 2 && input(nd, 1)) {
+      if (!host_ints(input(nd, 1), axes)) return decline(op + ": axes must be a host tensor");
+    } else {
+      axes = attr_ints(nd, "axes");
+    }
+    if (op == "Squeeze") {
+      const int r = (int)in.size();
+      std::vector<bool> drop((size_t)r, false);
+      if (axes.empty()) for (int i = 0; i < r; ++i) drop[(size_t)i] = in[(size_t)i] == 1;
+      for (auto a : axes) {
+        if (a < 0) a += r;
+        if (a < 0 || a >= r || in[(size_t)a] != 1) return decline("Squeeze: axis");
+        drop[(size_t)a] = true;
+      }
+      for (int i = 0; i < r; ++i) if (!drop[(size_t)i]) o.push_back(in[(size_t)i]);
+    } else {
+      const int r = (int)(in.size() + axes.size());
+      std::vector<bool> ins((size_t)r, false);
+      for (auto a : axes) {
+        if (a < 0) a += r;
+        if (a < 0 || a >= r || ins[(size_t)a]) return decline("Unsqueeze: axis");
+        ins[(size_t)a] = true;
+      }
+      size_t k = 0;
+      for (int i = 0; i < r; ++i) o.push_back(ins[(size_t)i] ? 1 : in[k++]);
+    }
+  }
+  int64_t check = 1;
+  for (auto v : o) check *= v;
+  if (check != total || o.size() > 8) return decline(op + ": element count");
+  ohip_dtensor* t = nullptr;
+  int rc = ohip_dtensor_alias_internal(x->device, (int)o.size(), o.data(), &t);
+  if (rc) return rc;
+  set_out(out, x->dtype, o);
+  out->device = t;
+  return OHIP_OK;
+}
+
+// ---------------------------------------------------------------- QuantizeLinear / DequantizeLinear
+// Per-tensor parameters only (quantize.rs:96-190).  The output integer
+// type follows saturation_range (:58-66), or y_zero_point's declared dtype.
+int do_quantize(ohip_ctx* ctx, const ohip_node* nd, int placement, ohip_output* out) {
+  const ohip_tensor *x = input(nd, 0), *s = input(nd, 1), *z = input(nd, 2);
+  if (!x) return decline("QuantizeLinear: missing input");
+  if (x->device && x->dtype != OHIP_F32) return decline("QuantizeLinear: resident input must be f32");
+  float scale;
+  if (!s || !host_only(s) || numel(s) != 1) return decline("QuantizeLinear: per-tensor scale only");
+  scale = (float)host_at(s, 0);
+  float zp = 0.0f;
+  if (z && numel(z) > 1) return decline("QuantizeLinear: per-tensor zero point only");
+  if (z && !host_only(z)) return decline("QuantizeLinear: zero point");
+  if (z && numel(z) == 0) return decline("QuantizeLinear: empty zero point");
+  if (z) zp = (float)host_at(z, 0);
+  bool u8 = !z || zp > 127.0f;
+  if (z && z->declared_dtype == OHIP_U8) u8 = true;
+  if (z && z->declared_dtype == OHIP_I8) u8 = false;
+  const float lo = u8 ? 0.0f : -128.0f, hi = u8 ? 255.0f : 127.0f;
+  Stage st(ctx);
+  const void* xd = float_operand(st, x, OHIP_F32);
+  const int64_t n = numel(x);
+  void* yd = st.alloc((size_t)n);
+  if (!xd || !yd) return OHIP_E_NOMEM;
+  hipError_t e = ohip::run_quantize(static_cast<const float*>(xd), static_cast<uint8_t*>(yd), n, scale, zp, lo, hi,
+                                    (hipStream_t)ohip_ctx_stream(ctx));
+  if (e != hipSuccess) return OHIP_E_HIP;
+  return output_device(ctx, st, placement, out, u8 ? OHIP_U8 : OHIP_I8, shape_of(x), yd, (size_t)n);
+}
+
+int do_dequantize(ohip_ctx* ctx, const ohip_node* nd, int placement, ohip_output* out) {
+  const ohip_tensor *x = input(nd, 0), *s = input(nd, 1), *z = input(nd, 2);
+  if (!x) return decline("DequantizeLinear: missing input");
+  if (!s || !host_only(s) || numel(s) != 1) return decline("DequantizeLinear: per-tensor scale only");
+  if (z && (!host_only(z) || numel(z) != 1)) return decline("DequantizeLinear: per-tensor zero point only");
+  const float scale = (float)host_at(s, 0), zp = z ? (float)host_at(z, 0) : 0.0f;
+  Stage st(ctx);
+  const void* xd;
+  int xdt;
+  std::vector<uint8_t> xb;
+  if (x->device) {
+    xdt = x->dtype;
+    if (xdt != OHIP_U8 && xdt != OHIP_I8) return decline("DequantizeLinear: resident input must be bytes");
+    xd = ohip_dtensor_ptr(x->device);
+  } else {
+    if (!to_bytes(x, xb, &xdt)) return decline("DequantizeLinear: lanes outside 8 bits");
+    xd = st.operand(x, xb.data(), xb.size());
+  }
+  const int64_t n = numel(x);
+  void* yd = st.alloc((size_t)n * 4);
+  if (!xd || !yd) return OHIP_E_NOMEM;
+  hipError_t e = ohip::run_dequantize(static_cast<const uint8_t*>(xd), xdt == OHIP_I8, static_cast<float*>(yd), n,
+                                      scale, zp, (hipStream_t)ohip_ctx_stream(ctx));
+  if (e != hipSuccess) return OHIP_E_HIP;
+  return output_device(ctx, st, placement, out, OHIP_F32, shape_of(x), yd, (size_t)n * 4);
 }
 
 }  // namespace
@@ -611,18 +1233,29 @@ int do_qconv(ohip_ctx* ctx, const ohip_node* nd, bool qlinear, int placement, oh
 extern "C" int ohip_is_supported_op(const char* op) {
   if (!op) return 0;
   static const char* kOps[] = {"Conv", "Gemm", "MatMul", "QLinearMatMul", "MatMulInteger", "QLinearConv",
-                               "ConvInteger"};
+                               "ConvInteger", "Relu", "LeakyRelu", "Tanh", "Sigmoid", "Silu", "Identity",
+                               "Add", "Sub", "Mul", "Div", "OxiInstanceNorm", "InstanceNormalization", "Resize",
+                               "Pad", "MaxPool", "Concat", "Slice", "Reshape", "Flatten", "Squeeze", "Unsqueeze",
+                               "QuantizeLinear", "DequantizeLinear"};
   for (const char* o : kOps)
     if (std::strcmp(op, o) == 0) return 1;
   return 0;
 }
 
-// accepts_resident_slot (oxionnx-cuda/src/lib.rs:419-480): only the
-// activation slot of the float ops may be bound from a resident tensor; a
-// filter, a Gemm B/C and every quantisation parameter are read on the host.
+// accepts_resident_slot (oxionnx-cuda/src/lib.rs:419-480): the activation
+// slots may be bound from resident tensors; filters, Gemm B / C, quantisation
+// parameters and shape-like inputs are read on the host.
 extern "C" int ohip_accepts_resident_slot(const char* op, int index) {
   if (!op) return 0;
-  if (!std::strcmp(op, "Conv") || !std::strcmp(op, "Gemm") || !std::strcmp(op, "MatMul")) return index == 0;
+  static const char* kSlot0[] = {"Conv", "Gemm", "MatMul", "QLinearConv", "Relu", "LeakyRelu", "Tanh", "Sigmoid",
+                                 "Silu", "Identity", "OxiInstanceNorm", "InstanceNormalization", "Resize", "Pad",
+                                 "MaxPool", "Slice", "Reshape", "Flatten", "Squeeze", "Unsqueeze",
+                                 "QuantizeLinear", "DequantizeLinear"};
+  for (const char* o : kSlot0)
+    if (std::strcmp(op, o) == 0) return index == 0;
+  if (!std::strcmp(op, "Add") || !std::strcmp(op, "Sub") || !std::strcmp(op, "Mul") || !std::strcmp(op, "Div"))
+    return index == 0 || index == 1;
+  if (!std::strcmp(op, "Concat")) return index >= 0;
   return 0;
 }
 
@@ -643,6 +1276,27 @@ extern "C" int ohip_try_dispatch(ohip_ctx* ctx, const ohip_node* node, int place
   else if (op == "MatMulInteger") rc = do_qmatmul(ctx, node, false, placement, out);
   else if (op == "QLinearConv") rc = do_qconv(ctx, node, true, placement, out);
   else if (op == "ConvInteger") rc = do_qconv(ctx, node, false, placement, out);
+  else if (op == "Relu") rc = do_unary(ctx, node, ohip::UN_RELU, placement, out);
+  else if (op == "LeakyRelu") rc = do_unary(ctx, node, ohip::UN_LEAKY_RELU, placement, out);
+  else if (op == "Tanh") rc = do_unary(ctx, node, ohip::UN_TANH, placement, out);
+  else if (op == "Sigmoid") rc = do_unary(ctx, node, ohip::UN_SIGMOID, placement, out);
+  else if (op == "Silu") rc = do_unary(ctx, node, ohip::UN_SILU, placement, out);
+  else if (op == "Identity") rc = do_unary(ctx, node, ohip::UN_IDENTITY, placement, out);
+  else if (op == "Add") rc = do_binary(ctx, node, ohip::BIN_ADD, placement, out);
+  else if (op == "Sub") rc = do_binary(ctx, node, ohip::BIN_SUB, placement, out);
+  else if (op == "Mul") rc = do_binary(ctx, node, ohip::BIN_MUL, placement, out);
+  else if (op == "Div") rc = do_binary(ctx, node, ohip::BIN_DIV, placement, out);
+  else if (op == "OxiInstanceNorm") rc = do_instnorm(ctx, node, false, placement, out);
+  else if (op == "InstanceNormalization") rc = do_instnorm(ctx, node, true, placement, out);
+  else if (op == "Resize") rc = do_resize(ctx, node, placement, out);
+  else if (op == "Pad") rc = do_pad(ctx, node, placement, out);
+  else if (op == "MaxPool") rc = do_maxpool(ctx, node, placement, out);
+  else if (op == "Concat") rc = do_concat(ctx, node, placement, out);
+  else if (op == "Slice") rc = do_slice(ctx, node, placement, out);
+  else if (op == "Reshape" || op == "Flatten" || op == "Squeeze" || op == "Unsqueeze")
+    rc = do_alias(ctx, node, op, placement, out);
+  else if (op == "QuantizeLinear") rc = do_quantize(ctx, node, placement, out);
+  else if (op == "DequantizeLinear") rc = do_dequantize(ctx, node, placement, out);
   else rc = decline("unsupported op " + op);
   if (rc == OHIP_DECLINED) ohip_note_declined(ctx, t_err.c_str());
   return rc;

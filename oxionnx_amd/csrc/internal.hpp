@@ -63,6 +63,7 @@ struct QuantOut : OutMap {
   int n_comb;
   int out_kind;
   int32_t y_zp, lo, hi;
+  const uint8_t* table;  // device, 256 entries: applied to requantised bytes (may be null)
 };
 
 struct GemvArgs {
@@ -86,5 +87,67 @@ hipError_t run_nchw_to_nhwc(int elem_bytes, const void* src, void* dst, int N, i
                             hipStream_t st);
 hipError_t run_gather2d(int elem_bytes, const void* src, int64_t rs, int64_t cs, void* dst, int R, int K, int ld,
                         hipStream_t st);
+
+// ---------------------------------------------------------------- memory-bound nodes
+enum { UN_IDENTITY = 0, UN_RELU = 1, UN_LEAKY_RELU = 2, UN_TANH = 3, UN_SIGMOID = 4, UN_SILU = 5 };
+enum { BIN_ADD = 0, BIN_SUB = 1, BIN_MUL = 2, BIN_DIV = 3 };
+enum { RZ_HALF_PIXEL = 0, RZ_ASYMMETRIC = 1, RZ_ALIGN_CORNERS = 2, RZ_PYTORCH_HALF_PIXEL = 3,
+       RZ_TF_HALF_PIXEL_FOR_NN = 4 };
+enum { RZ_ROUND_PREFER_FLOOR = 0, RZ_ROUND_PREFER_CEIL = 1, RZ_FLOOR = 2, RZ_CEIL = 3 };
+enum { PAD_CONSTANT = 0, PAD_REFLECT = 1, PAD_EDGE = 2, PAD_WRAP = 3 };
+constexpr int kMaxRank = 6;
+
+// Output extents (right-aligned in kMaxRank slots) and the element strides of
+// each operand along them (0 on a broadcast axis).
+struct BcastPlan {
+  int rank;
+  int64_t shape[kMaxRank], sa[kMaxRank], sb[kMaxRank];
+};
+
+// Optional affine term and activation applied after the normalisation.
+struct NormAffine {
+  const float* scale;  // per channel, or per (n, c) when per_sample
+  const float* bias;
+  int per_sample;
+  int act;             // UN_NONE / UN_RELU / UN_LEAKY_RELU
+  float alpha;
+};
+
+struct ResizePlan {
+  int ih, iw, oh, ow;
+  float sh, sw;        // scales of the H and W axes
+  int coord, rule;
+};
+
+struct PadPlan {
+  int rank, mode;
+  int64_t in[kMaxRank], out[kMaxRank], begin[kMaxRank];
+  uint32_t value_bits;  // the constant fill as the element's bit pattern
+};
+
+struct PoolPlan {
+  int ih, iw, oh, ow, kh, kw, sh, sw, pt, pl, dh, dw;
+};
+
+struct SlicePlan {
+  int rank;
+  int64_t out[kMaxRank], start[kMaxRank], step[kMaxRank], in_stride[kMaxRank];
+};
+
+hipError_t run_unary(int dt, const void* x, void* y, int64_t n, int op, float alpha, hipStream_t st);
+hipError_t run_binary(int dt, const void* a, const void* b, void* y, int64_t n, const BcastPlan& p, bool same, int op,
+                      hipStream_t st);
+hipError_t run_instnorm(int dt, const void* x, void* y, int64_t planes, int64_t spatial, int C, float eps,
+                        const NormAffine& aff, hipStream_t st);
+hipError_t run_resize_nearest(int elem_bytes, const void* x, void* y, int64_t planes, const ResizePlan& p,
+                              hipStream_t st);
+hipError_t run_pad(int elem_bytes, const void* x, void* y, int64_t n, const PadPlan& p, hipStream_t st);
+hipError_t run_slice(int elem_bytes, const void* x, void* y, int64_t n, const SlicePlan& p, hipStream_t st);
+hipError_t run_maxpool(int dt, const void* x, void* y, int64_t planes, const PoolPlan& p, hipStream_t st);
+hipError_t run_quantize(const float* x, uint8_t* y, int64_t n, float scale, float zp, float lo, float hi,
+                        hipStream_t st);
+hipError_t run_dequantize(const uint8_t* x, bool is_signed, float* y, int64_t n, float scale, float zp,
+                          hipStream_t st);
+hipError_t run_byte_table(const uint8_t* x, uint8_t* y, int64_t n, const uint8_t* table, hipStream_t st);
 
 }  // namespace ohip

@@ -102,6 +102,7 @@ struct QuantEpi {
   int n_comb;
   int out_kind;             // QOUT_U8, QOUT_I8, QOUT_I32 (raw), QOUT_F32 (requantised, as f32)
   int32_t y_zp, lo, hi;
+  const uint8_t* table;     // byte -> byte map applied after requantisation (may be null)
 
   __device__ __forceinline__ int64_t index(int i, int j) const {
     if (bstride == 0) return (int64_t)i * si + (int64_t)j * sj;
@@ -157,6 +158,10 @@ struct QuantEpi {
       }
     } else {
       uint8_t* yy = reinterpret_cast<uint8_t*>(y);
+      if (table) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) v[r] = table[v[r] & 0xff];
+      }
       if (vec && i0 + 3 < P) {
         uint32_t packed = (uint32_t)(v[0] & 0xff) | ((uint32_t)(v[1] & 0xff) << 8) |
                           ((uint32_t)(v[2] & 0xff) << 16) | ((uint32_t)(v[3] & 0xff) << 24);
@@ -181,39 +186,44 @@ using T256w4 = Tile<256, 256, 2, 2, 2>;     // 5: 4 waves, 128x128 per wave
 using T256 = Tile<256, 256, 2, 4, 2>;       // 6: 8 waves, 128x64 per wave
 constexpr int kTileCount = 6;
 
-template <Op O, class Tl, class LX, class LY, class Epi>
-inline hipError_t launch_tile(const LX& lx, const LY& ly, const Epi& epi, int P, int Q, int kc, uint32_t xxor,
-                              uint32_t yxor, hipStream_t st) {
+template <Op O, bool XX, bool XY, class Tl, class LX, class LY, class Epi>
+inline hipError_t launch_tile(const LX& lx, const LY& ly, const Epi& epi, int P, int Q, int kc, hipStream_t st) {
   const int nP = (P + Tl::BP - 1) / Tl::BP, nQ = (Q + Tl::BQ - 1) / Tl::BQ;
   const int64_t nb = (int64_t)nP * nQ;
   if (nb <= 0) return hipSuccess;
   if (nb > 0x7fffffff) return hipErrorInvalidValue;
-  hipLaunchKernelGGL((mfma_gemm_kernel<O, Tl, LX, LY, Epi>), dim3((unsigned)nb), dim3(Tl::kThreads),
-                     0, st, lx, ly, epi, nP, nQ, kc, xxor, yxor);
+  hipLaunchKernelGGL((mfma_gemm_kernel<O, Tl, LX, LY, Epi, XX, XY>), dim3((unsigned)nb), dim3(Tl::kThreads),
+                     0, st, lx, ly, epi, nP, nQ, kc);
   return hipGetLastError();
 }
 
-// Automatic choice: the largest tile that still gives at least one block
-// per CU (256 CUs), else the smaller ones.
-inline int pick_tile(int P, int Q, int forced) {
+// Automatic choice.  A short K loop (few 128-byte stages) is dominated by the
+// prologue and the epilogue, which many small resident blocks overlap best;
+// otherwise the largest tile that still gives at least one block per CU
+// (256 CUs), else the smaller ones.
+inline int pick_tile(int P, int Q, int kc, int forced) {
   if (forced >= 1 && forced <= kTileCount) return forced;
   auto blocks = [&](int bp, int bq) { return (int64_t)((P + bp - 1) / bp) * ((Q + bq - 1) / bq); };
+  const int nk = (kc + 7) / 8;
+  if (nk <= 16) return 1;
   if (blocks(256, 256) >= 256) return 6;
   if (blocks(256, 128) >= 256) return P >= Q ? 3 : 4;
   if (blocks(128, 128) >= 128) return 2;
   return 1;
 }
 
-template <Op O, class LX, class LY, class Epi>
+// XX / XY: the X / Y operand holds u8 activations that the MFMA reads as
+// int8 after XOR 0x80.
+template <Op O, bool XX, bool XY, class LX, class LY, class Epi>
 inline hipError_t launch_any(const LX& lx, const LY& ly, const Epi& epi, int P, int Q, int kc, int tile,
-                             uint32_t xxor, uint32_t yxor, hipStream_t st) {
-  switch (pick_tile(P, Q, tile)) {
-    case 2: return launch_tile<O, T128>(lx, ly, epi, P, Q, kc, xxor, yxor, st);
-    case 3: return launch_tile<O, T256x128>(lx, ly, epi, P, Q, kc, xxor, yxor, st);
-    case 4: return launch_tile<O, T128x256>(lx, ly, epi, P, Q, kc, xxor, yxor, st);
-    case 5: return launch_tile<O, T256w4>(lx, ly, epi, P, Q, kc, xxor, yxor, st);
-    case 6: return launch_tile<O, T256>(lx, ly, epi, P, Q, kc, xxor, yxor, st);
-    default: return launch_tile<O, T64>(lx, ly, epi, P, Q, kc, xxor, yxor, st);
+                             hipStream_t st) {
+  switch (pick_tile(P, Q, kc, tile)) {
+    case 2: return launch_tile<O, XX, XY, T128>(lx, ly, epi, P, Q, kc, st);
+    case 3: return launch_tile<O, XX, XY, T256x128>(lx, ly, epi, P, Q, kc, st);
+    case 4: return launch_tile<O, XX, XY, T128x256>(lx, ly, epi, P, Q, kc, st);
+    case 5: return launch_tile<O, XX, XY, T256w4>(lx, ly, epi, P, Q, kc, st);
+    case 6: return launch_tile<O, XX, XY, T256>(lx, ly, epi, P, Q, kc, st);
+    default: return launch_tile<O, XX, XY, T64>(lx, ly, epi, P, Q, kc, st);
   }
 }
 
@@ -233,7 +243,7 @@ inline QuantEpi make_quant_epi(const QuantOut& o) {
   e.y = o.y; e.si = o.si; e.sj = o.sj; e.bstride = o.bstride; e.ohw = o.ohw; e.P = o.P; e.Q = o.Q;
   e.vec = o.vec; e.w_on_i = o.w_on_i; e.colsum = o.colsum; e.flip = o.flip; e.bias = o.bias; e.ca = o.ca;
   e.ca_rows = o.ca_rows; e.comb = o.comb; e.n_comb = o.n_comb; e.out_kind = o.out_kind;
-  e.y_zp = o.y_zp; e.lo = o.lo; e.hi = o.hi;
+  e.y_zp = o.y_zp; e.lo = o.lo; e.hi = o.hi; e.table = o.table;
   return e;
 }
 
@@ -241,7 +251,6 @@ inline DenseRows make_dense(const DenseOperand& d) {
   DenseRows r;
   r.base = reinterpret_cast<const char*>(d.base);
   r.ld = d.ld_bytes; r.rows = d.rows; r.kc = d.kc; r.kwrap = d.kwrap;
-  r.pad = reinterpret_cast<const char*>(d.pad16);
   return r;
 }
 

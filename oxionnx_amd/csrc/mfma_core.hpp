@@ -9,10 +9,15 @@
 // Nothing is materialised for im2col: the loader gathers 16-byte channel
 // chunks straight from the NHWC activation.
 //
-// Global -> LDS traffic uses the LDS DMA path (global_load_lds_dwordx4): each
-// wave writes 1 KiB of contiguous LDS per load, with no VGPR staging, and the
-// operands run STAGES deep.  Out-of-range chunks (matrix edges, the K tail,
-// padding taps) are redirected to a 16-byte pad source in global memory.
+// Global -> LDS traffic uses the LDS DMA path (buffer_load / global_load
+// dwordx4 ... lds): each wave writes 1 KiB of contiguous LDS per load, with no
+// VGPR staging, and the operands run STAGES deep.  Dense operands go through
+// a buffer resource: the per-lane row offset is fixed for the whole loop and
+// the K position is a scalar offset, so a stage costs no vector address
+// arithmetic, and rows past the matrix edge, the K tail and prefetches past
+// the end read as zero through the resource's range check.  The implicit
+// im2col operand redirects padding taps to a 16-byte pad source in global
+// memory instead (its pad value is not always zero).
 //
 // The MFMAs are the 32x32 shapes, which gfx950 runs at about twice the rate
 // of the 16x16 ones for f16 / bf16 and 1.4x for int8:
@@ -120,40 +125,49 @@ __device__ __forceinline__ void dma16(const void* g, u32x4* lds) {
   __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void*)(lds), 16, 0, 0);
 }
 
+// Offset that fails the range check of every dense operand's buffer
+// resource (valid offsets stay below 2^31 - 1; the host checks the extent).
+constexpr int kOobOffset = (int)0x80000000u;
+
+__device__ __forceinline__ void buf16(__amdgpu_buffer_rsrc_t rs, int voff, int soff, u32x4* lds) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void*)(lds), 16, voff, soff, 0, 0);
+}
+
 struct DenseRows {
   const char* base;   // row 0
   int64_t ld;         // bytes between rows (multiple of 16)
   int rows;           // valid rows
   int kc;             // valid 16-byte chunks per row
   int kwrap;          // > 0: chunk g >= kwrap reads chunk g - kwrap (the operand is
-                      // re-read against the second half of a split int8 weight)
-  const char* pad;    // 16 bytes that stand for any chunk outside the matrix
+                      // re-read against the second half of a split int8 weight);
+                      // a multiple of 8, so a stage never straddles the wrap
 
   template <int NR>
-  struct State { const char* ptr[NR]; uint32_t okmask; int c; };
+  struct State { __amdgpu_buffer_rsrc_t rs; int voff[NR]; int c; };
 
   template <int NR, int NW>
   __device__ __forceinline__ void init(State<NR>& s, int row0, int lane, int wave) const {
     s.c = dma_chunk(lane, wave);
-    s.okmask = 0;
+    s.rs = __builtin_amdgcn_make_buffer_rsrc((void*)(base + (int64_t)row0 * ld), (short)0, 0x7fffffff, 0x00020000);
 #pragma unroll
     for (int i = 0; i < NR; ++i) {
-      const int r = row0 + (i * NW + wave) * 8 + (lane >> 3);
-      const bool ok = r < rows;
-      s.okmask |= (ok ? 1u : 0u) << i;
-      s.ptr[i] = base + (int64_t)(ok ? r : 0) * ld;
+      const int r = (i * NW + wave) * 8 + (lane >> 3);
+      s.voff[i] = row0 + r < rows ? (int)(r * ld) + s.c * 16 : kOobOffset;
     }
   }
   template <int NR, int NW>
   __device__ __forceinline__ void issue(const State<NR>& s, int kt, int wave, u32x4* lds_rows) const {
-    int gk = kt * 8 + s.c;
-    if (kwrap > 0 && gk >= kwrap) gk -= kwrap;
-    const bool kin = gk < kc;
-    const int64_t off = (int64_t)gk * 16;
+    int g0 = kt * 8;                       // first chunk of the stage (uniform)
+    if (kwrap > 0 && g0 >= kwrap) g0 -= kwrap;
+    const int soff = g0 * 16;
+    if (g0 + 8 <= kc) {
 #pragma unroll
-    for (int i = 0; i < NR; ++i) {
-      const bool ok = kin && ((s.okmask >> i) & 1u);
-      dma16(ok ? s.ptr[i] + off : pad, lds_rows + (i * NW + wave) * 64);
+      for (int i = 0; i < NR; ++i) buf16(s.rs, s.voff[i], soff, lds_rows + (i * NW + wave) * 64);
+    } else {
+      // K tail or past the end: chunks at or beyond kc read as zero
+      const bool kin = g0 + s.c < kc;
+#pragma unroll
+      for (int i = 0; i < NR; ++i) buf16(s.rs, kin ? s.voff[i] : kOobOffset, soff, lds_rows + (i * NW + wave) * 64);
     }
   }
 };
@@ -249,18 +263,47 @@ template <int N> __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
-// xxor / yxor: XOR applied to every X / Y fragment after its LDS read
-// (0x80808080 turns u8 activations into u8 - 128 as int8; the pad source of
-// such an operand holds its pad bytes pre-XORed).
-template <Op O, class Tl, class LX, class LY, class Epi>
+// s_waitcnt lgkmcnt(0) with the other counters at their maximum.
+__device__ __forceinline__ void wait_lgkm0() { __builtin_amdgcn_s_waitcnt(0xc07f); }
+
+// Workgroup barrier without the memory fences of __syncthreads (which would
+// also wait for every outstanding LDS DMA load, draining the prefetch
+// pipeline).  Callers order memory themselves: each wave waits (vmcnt) for
+// its own DMA loads of the stage that the barrier publishes, and (lgkmcnt)
+// for its LDS reads of the buffer that the next DMA overwrites.
+__device__ __forceinline__ void barrier_only() {
+  __builtin_amdgcn_sched_barrier(0);
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_sched_barrier(0);
+}
+
+// XX / XY: XOR 0x80 into every byte of an X / Y fragment before the MFMA
+// (turns u8 activations into u8 - 128 as int8; the pad source of such an
+// operand holds its pad bytes un-XORed).
+template <bool XOR> __device__ __forceinline__ u32x4 frag(u32x4 v) {
+  if (XOR) v ^= 0x80808080u;
+  return v;
+}
+
+// Main loop, per stage kt (STAGES LDS buffers, four MFMA k-steps a stage):
+//   k-step 0 issues the DMA loads of stage kt + STAGES - 1 (into the buffer
+//   of stage kt - 1, released by the previous stage's barrier), interleaved
+//   with the MFMAs;
+//   k-steps 0..2 read the next k-step's fragments under the MFMAs;
+//   k-step 3 waits until stage kt + 1 has landed, passes the barrier and
+//   reads stage kt + 1's first fragments under its MFMAs,
+// so the MFMA pipe is never left waiting on a barrier with no work queued.
+template <Op O, class Tl, class LX, class LY, class Epi, bool XX, bool XY>
 __global__ void __launch_bounds__(Tl::kThreads)
-mfma_gemm_kernel(const LX lx, const LY ly, const Epi epi, int nP, int nQ, int kc, uint32_t xxor, uint32_t yxor) {
+mfma_gemm_kernel(const LX lx, const LY ly, const Epi epi, int nP, int nQ, int kc) {
   using A = typename OpT<O>::Acc;
   using O4 = typename OpT<O>::Out4;
   __shared__ u32x4 smem[Tl::STAGES * Tl::kStage];
   const int t = threadIdx.x;
   const int lane = t & 63;
-  const int wave = t >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
   const int wp = wave % Tl::WP, wq = wave / Tl::WP;
   int tp, tq;
   map_tile(blockIdx.x, gridDim.x, nP, nQ, tp, tq);
@@ -280,8 +323,9 @@ mfma_gemm_kernel(const LX lx, const LY ly, const Epi epi, int nP, int nQ, int kc
       for (int e = 0; e < 16; ++e) acc[a][b][e] = 0;
 
   const int nk = (kc + 7) >> 3;
-  // Every load is issued unconditionally (past the last stage it reads the
-  // pad source), so the wait below is a fixed count of outstanding loads.
+  constexpr int NL = Tl::NX + Tl::NY;     // DMA loads per thread per stage
+  // Every stage issues all its loads (past the last stage they read zero or
+  // the pad source), so the waits below are fixed counts of outstanding loads.
   auto issue = [&](int kt) {
     u32x4* s = smem + (kt % Tl::STAGES) * Tl::kStage;
     lx.template issue<Tl::NX, Tl::kWaves>(sx, kt, wave, s);
@@ -301,39 +345,46 @@ mfma_gemm_kernel(const LX lx, const LY ly, const Epi epi, int nP, int nQ, int kc
 
 #pragma unroll
   for (int s = 0; s < Tl::STAGES - 1; ++s) issue(s);
+  wait_vmcnt<(Tl::STAGES - 2) * NL>();
+  barrier_only();
+
+  u32x4 fx[2][Tl::TP], fy[2][Tl::TQ];
+#pragma unroll
+  for (int a = 0; a < Tl::TP; ++a) fx[0][a] = smem[xslot[0] + a * 32 * Tl::kRowStride];
+#pragma unroll
+  for (int b = 0; b < Tl::TQ; ++b) fy[0][b] = smem[yslot[0] + b * 32 * Tl::kRowStride];
 
   for (int kt = 0; kt < nk; ++kt) {
-    // This thread's loads of stage kt have landed once only the younger
-    // stages' loads are outstanding; the barrier extends that to every wave
-    // and retires all reads of the buffer that the next issue overwrites.
-    wait_vmcnt<(Tl::STAGES - 2) * (Tl::NX + Tl::NY)>();
-    __syncthreads();
-    issue(kt + Tl::STAGES - 1);
     const u32x4* s = smem + (kt % Tl::STAGES) * Tl::kStage;
-    // fragments double-buffered across the four k-steps of the stage
-    u32x4 fx[2][Tl::TP], fy[2][Tl::TQ];
-#pragma unroll
-    for (int a = 0; a < Tl::TP; ++a) fx[0][a] = s[xslot[0] + a * 32 * Tl::kRowStride] ^ xxor;
-#pragma unroll
-    for (int b = 0; b < Tl::TQ; ++b) fy[0][b] = s[yslot[0] + b * 32 * Tl::kRowStride] ^ yxor;
+    const u32x4* sn = smem + ((kt + 1) % Tl::STAGES) * Tl::kStage;
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
       const int cur = ks & 1;
       if (ks < 3) {
 #pragma unroll
-        for (int a = 0; a < Tl::TP; ++a) fx[cur ^ 1][a] = s[xslot[ks + 1] + a * 32 * Tl::kRowStride] ^ xxor;
+        for (int a = 0; a < Tl::TP; ++a) fx[cur ^ 1][a] = s[xslot[ks + 1] + a * 32 * Tl::kRowStride];
 #pragma unroll
-        for (int b = 0; b < Tl::TQ; ++b) fy[cur ^ 1][b] = s[yslot[ks + 1] + b * 32 * Tl::kRowStride] ^ yxor;
+        for (int b = 0; b < Tl::TQ; ++b) fy[cur ^ 1][b] = s[yslot[ks + 1] + b * 32 * Tl::kRowStride];
+      } else {
+        wait_vmcnt<(Tl::STAGES - 2) * NL>();
+        wait_lgkm0();
+        barrier_only();
+#pragma unroll
+        for (int a = 0; a < Tl::TP; ++a) fx[cur ^ 1][a] = sn[xslot[0] + a * 32 * Tl::kRowStride];
+#pragma unroll
+        for (int b = 0; b < Tl::TQ; ++b) fy[cur ^ 1][b] = sn[yslot[0] + b * 32 * Tl::kRowStride];
       }
+      if (ks == 0) issue(kt + Tl::STAGES - 1);
 #pragma unroll
       for (int a = 0; a < Tl::TP; ++a)
 #pragma unroll
         for (int b = 0; b < Tl::TQ; ++b) {
-          acc[a][b] = OpT<O>::mma(fx[cur][a], fy[cur][b], acc[a][b]);
-          // one MFMA, then one LDS read: keeps the next k-step's fragment
-          // reads interleaved with this one's MFMAs
+          acc[a][b] = OpT<O>::mma(frag<XX>(fx[cur][a]), frag<XY>(fy[cur][b]), acc[a][b]);
+          // one MFMA, then one LDS read (and on k-step 0 one DMA load):
+          // keeps the fragment reads and the loads spread under the MFMAs
           __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
           __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+          if (ks == 0 && a * Tl::TQ + b < NL) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
         }
     }
   }

@@ -1,0 +1,411 @@
+// Device kernels for the memory-bound nodes that sit between the
+// contractions of a conv network (activations, broadcast arithmetic,
+// instance normalisation, nearest resize, pad, max pool, slice, quantise /
+// dequantise, byte tables).  They keep activations resident between the
+// contraction nodes; each is one pass over its tensor, bound by HBM.
+//
+// Float tensors are f32 or f16 storage with f32 arithmetic; quantised
+// tensors are u8 / i8 bytes.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "internal.hpp"
+
+namespace ohip {
+
+namespace {
+
+template <class T> __device__ __forceinline__ float ldf(const T* p, int64_t i) { return (float)p[i]; }
+template <class T> __device__ __forceinline__ void stf(T* p, int64_t i, float v) { p[i] = (T)v; }
+
+constexpr int kThreads = 256;
+
+inline unsigned grid_for(int64_t n, int per_thread = 1) {
+  int64_t b = (n + (int64_t)kThreads * per_thread - 1) / ((int64_t)kThreads * per_thread);
+  if (b < 1) b = 1;
+  if (b > 65535 * 16) b = 65535 * 16;  // grid-stride loops cover the rest
+  return (unsigned)b;
+}
+
+// ---------------------------------------------------------------- unary
+__device__ __forceinline__ float unary_op(float v, int op, float alpha) {
+  switch (op) {
+    case UN_RELU: return v > 0.0f ? v : 0.0f;
+    case UN_LEAKY_RELU: return v >= 0.0f ? v : v * alpha;
+    case UN_TANH: return tanhf(v);
+    case UN_SIGMOID: return 1.0f / (1.0f + expf(-v));
+    case UN_SILU: return v / (1.0f + expf(-v));
+    default: return v;
+  }
+}
+
+template <class T>
+__global__ void __launch_bounds__(kThreads) unary_kernel(const T* __restrict__ x, T* __restrict__ y, int64_t n, int op,
+                                                         float alpha) {
+  for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n; i += (int64_t)gridDim.x * kThreads)
+    stf(y, i, unary_op(ldf(x, i), op, alpha));
+}
+
+// ---------------------------------------------------------------- binary with broadcasting
+__device__ __forceinline__ float binary_op(float a, float b, int op) {
+  switch (op) {
+    case BIN_ADD: return a + b;
+    case BIN_SUB: return a - b;
+    case BIN_MUL: return a * b;
+    default: return a / b;
+  }
+}
+
+template <class T>
+__global__ void __launch_bounds__(kThreads) binary_kernel(const T* __restrict__ a, const T* __restrict__ b,
+                                                          T* __restrict__ y, int64_t n, BcastPlan p, int op) {
+  for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n; i += (int64_t)gridDim.x * kThreads) {
+    int64_t ia = 0, ib = 0, r = i;
+#pragma unroll
+    for (int d = kMaxRank - 1; d >= 0; --d) {
+      if (d < kMaxRank - p.rank) break;
+      const int64_t e = p.shape[d];
+      const int64_t c = r % e;
+      r /= e;
+      ia += c * p.sa[d];
+      ib += c * p.sb[d];
+    }
+    stf(y, i, binary_op(ldf(a, ia), ldf(b, ib), op));
+  }
+}
+
+// Same-shape operands: no index arithmetic.
+template <class T>
+__global__ void __launch_bounds__(kThreads) binary_same_kernel(const T* __restrict__ a, const T* __restrict__ b,
+                                                               T* __restrict__ y, int64_t n, int op) {
+  for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n; i += (int64_t)gridDim.x * kThreads)
+    stf(y, i, binary_op(ldf(a, i), ldf(b, i), op));
+}
+
+// ---------------------------------------------------------------- instance normalisation
+// One block per (n, c) plane: mean, then variance about the mean (two
+// passes, as the reference's normalize_plane), then the rescale with the
+// optional per-channel (or per-(n, c)) affine term and activation.
+__device__ __forceinline__ float block_sum(float v, float* red) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  __syncthreads();
+  if (lane == 0) red[wave] = v;
+  __syncthreads();
+  float s = 0.0f;
+#pragma unroll
+  for (int w = 0; w < kThreads / 64; ++w) s += red[w];
+  return s;
+}
+
+template <class T>
+__global__ void __launch_bounds__(kThreads) instnorm_kernel(const T* __restrict__ x, T* __restrict__ y, int64_t spatial,
+                                                            int C, float eps, NormAffine aff) {
+  __shared__ float red[kThreads / 64];
+  const int64_t plane = blockIdx.x;
+  const T* xp = x + plane * spatial;
+  T* yp = y + plane * spatial;
+  float s = 0.0f;
+  for (int64_t i = threadIdx.x; i < spatial; i += kThreads) s += ldf(xp, i);
+  const float mean = block_sum(s, red) / (float)spatial;
+  float q = 0.0f;
+  for (int64_t i = threadIdx.x; i < spatial; i += kThreads) {
+    const float d = ldf(xp, i) - mean;
+    q += d * d;
+  }
+  const float var = block_sum(q, red) / (float)spatial;
+  const float inv = 1.0f / sqrtf(var + eps);
+  const int c = (int)(plane % C);
+  const int64_t n = plane / C;
+  float sc = 1.0f, bi = 0.0f;
+  bool affine = false;
+  if (aff.scale) { sc = aff.scale[aff.per_sample ? plane : c]; affine = true; }
+  if (aff.bias) { bi = aff.bias[aff.per_sample ? n * C + c : c]; affine = true; }
+  for (int64_t i = threadIdx.x; i < spatial; i += kThreads) {
+    float v = (ldf(xp, i) - mean) * inv;
+    if (affine) {
+      if (aff.scale) v = v * sc;
+      if (aff.bias) v = v + bi;
+    }
+    if (aff.act == UN_RELU) v = v > 0.0f ? v : 0.0f;
+    else if (aff.act == UN_LEAKY_RELU) v = v >= 0.0f ? v : v * aff.alpha;
+    stf(yp, i, v);
+  }
+}
+
+// ---------------------------------------------------------------- nearest resize (rank 4, H and W)
+// Source index of output position j on one axis: transform_coord plus the
+// nearest rule and the clamp of the reference's build_axis
+// (oxionnx-ops/src/resize.rs:578-620, 712-722), evaluated in f32.
+__device__ __forceinline__ int nearest_src(int j, int in_len, int out_len, float scale, int coord, int rule) {
+  const float x = (float)j;
+  float src;
+  switch (coord) {
+    case RZ_ASYMMETRIC: src = x / scale; break;
+    case RZ_ALIGN_CORNERS: src = out_len <= 1 ? 0.0f : x * ((float)in_len - 1.0f) / ((float)out_len - 1.0f); break;
+    case RZ_PYTORCH_HALF_PIXEL: src = out_len > 1 ? (x + 0.5f) / scale - 0.5f : 0.0f; break;
+    case RZ_TF_HALF_PIXEL_FOR_NN: src = (x + 0.5f) / scale; break;
+    default: src = (x + 0.5f) / scale - 0.5f; break;
+  }
+  const float guard = 6.0f;  // 2 * taps + 4 with one tap
+  const float hi = (float)(in_len - 1);
+  src = src < -guard ? -guard : (src > hi + guard ? hi + guard : src);
+  float picked;
+  switch (rule) {
+    case RZ_ROUND_PREFER_CEIL: picked = floorf(src + 0.5f); break;
+    case RZ_FLOOR: picked = floorf(src); break;
+    case RZ_CEIL: picked = ceilf(src); break;
+    default: picked = ceilf(src - 0.5f); break;
+  }
+  int64_t k = (int64_t)picked;
+  k = k < 0 ? 0 : (k > in_len - 1 ? in_len - 1 : k);
+  return (int)k;
+}
+
+template <class T>
+__global__ void __launch_bounds__(kThreads) resize_nearest_kernel(const T* __restrict__ x, T* __restrict__ y,
+                                                                  int64_t planes, ResizePlan p) {
+  const int64_t n = planes * p.oh * p.ow;
+  for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n; i += (int64_t)gridDim.x * kThreads) {
+    const int ox = (int)(i % p.ow);
+    const int64_t t = i / p.ow;
+    const int oy = (int)(t % p.oh);
+    const int64_t pl = t / p.oh;
+    const int iy = nearest_src(oy, p.ih, p.oh, p.sh, p.coord, p.rule);
+    const int ix = nearest_src(ox, p.iw, p.ow, p.sw, p.coord, p.rule);
+    y[i] = x[(pl * p.ih + iy) * p.iw + ix];
+  }
+}
+
+// ---------------------------------------------------------------- pad (rank <= 6)
+__device__ __forceinline__ int64_t pad_src(int64_t o, int64_t begin, int64_t len, int mode, bool* inside) {
+  int64_t s = o - begin;
+  if (s >= 0 && s < len) return s;
+  if (mode == PAD_CONSTANT) { *inside = false; return 0; }
+  if (mode == PAD_EDGE) return s < 0 ? 0 : len - 1;
+  if (mode == PAD_WRAP) { s %= len; return s < 0 ? s + len : s; }
+  // reflect (len >= 2 is checked on the host, len == 1 maps everything to 0)
+  if (len == 1) return 0;
+  const int64_t period = 2 * (len - 1);
+  s %= period;
+  if (s < 0) s += period;
+  return s < len ? s : period - s;
+}
+
+template <class T>
+__global__ void __launch_bounds__(kThreads) pad_kernel(const T* __restrict__ x, T* __restrict__ y, int64_t n, PadPlan p) {
+  for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n; i += (int64_t)gridDim.x * kThreads) {
+    int64_t r = i, src = 0, mul = 1;
+    bool inside = true;
+    for (int d = p.rank - 1; d >= 0; --d) {
+      const int64_t o = r % p.out[d];
+      r /= p.out[d];
+      src += pad_src(o, p.begin[d], p.in[d], p.mode, &inside) * mul;
+      mul *= p.in[d];
+    }
+    y[i] = inside ? x[src] : (T)p.value_bits;
+  }
+}
+
+// ---------------------------------------------------------------- max pool (2-D)
+template <class T>
+__global__ void __launch_bounds__(kThreads) maxpool_kernel(const T* __restrict__ x, T* __restrict__ y, int64_t planes,
+                                                           PoolPlan p) {
+  const int64_t n = planes * p.oh * p.ow;
+  for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n; i += (int64_t)gridDim.x * kThreads) {
+    const int ox = (int)(i % p.ow);
+    const int64_t t = i / p.ow;
+    const int oy = (int)(t % p.oh);
+    const int64_t pl = t / p.oh;
+    const T* xp = x + pl * p.ih * p.iw;
+    // max_pool_into (conv/pooling.rs:166-240): strictly-greater update from
+    // -inf, so a NaN sample never wins
+    float best = -INFINITY;
+    for (int ky = 0; ky < p.kh; ++ky) {
+      const int iy = oy * p.sh - p.pt + ky * p.dh;
+      if (iy < 0 || iy >= p.ih) continue;
+      for (int kx = 0; kx < p.kw; ++kx) {
+        const int ix = ox * p.sw - p.pl + kx * p.dw;
+        if (ix < 0 || ix >= p.iw) continue;
+        const float v = (float)xp[iy * p.iw + ix];
+        if (v > best) best = v;
+      }
+    }
+    y[i] = (T)best;
+  }
+}
+
+// ---------------------------------------------------------------- strided slice (rank <= 6)
+template <class T>
+__global__ void __launch_bounds__(kThreads) slice_kernel(const T* __restrict__ x, T* __restrict__ y, int64_t n, SlicePlan p) {
+  for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n; i += (int64_t)gridDim.x * kThreads) {
+    int64_t r = i, src = 0;
+    for (int d = p.rank - 1; d >= 0; --d) {
+      const int64_t o = r % p.out[d];
+      r /= p.out[d];
+      src += (p.start[d] + o * p.step[d]) * p.in_stride[d];
+    }
+    y[i] = x[src];
+  }
+}
+
+// ---------------------------------------------------------------- quantise / dequantise / byte table
+// QuantizeLinear (indexing/quantize.rs:96-150): round_ties_even(x / scale) + zp,
+// clamped into [lo, hi]; the division is IEEE (correctly rounded), as on the host.
+__global__ void __launch_bounds__(kThreads) quantize_kernel(const float* __restrict__ x, uint8_t* __restrict__ y, int64_t n,
+                                                            float scale, float zp, float lo, float hi) {
+  for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n; i += (int64_t)gridDim.x * kThreads) {
+    const float v = x[i] / scale;
+    float r = __builtin_rintf(v);  // ties to even, the reference's round_ties_even
+    if (!__builtin_isfinite(v)) r = v;
+    float q = r + zp;
+    q = q < lo ? lo : (q > hi ? hi : q);
+    y[i] = (uint8_t)((int32_t)q & 0xff);
+  }
+}
+
+// DequantizeLinear (indexing/quantize.rs:152-190): (x - zp) * scale in f32.
+template <bool SIGNED>
+__global__ void __launch_bounds__(kThreads) dequantize_kernel(const uint8_t* __restrict__ x, float* __restrict__ y,
+                                                              int64_t n, float scale, float zp) {
+  for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n; i += (int64_t)gridDim.x * kThreads) {
+    const float v = SIGNED ? (float)(int8_t)x[i] : (float)x[i];
+    y[i] = (v - zp) * scale;
+  }
+}
+
+struct Table256 { uint8_t v[256]; };
+
+__global__ void __launch_bounds__(kThreads) byte_table_kernel(const uint8_t* __restrict__ x, uint8_t* __restrict__ y,
+                                                              int64_t n, Table256 t) {
+  __shared__ uint8_t tab[256];
+  tab[threadIdx.x] = t.v[threadIdx.x];
+  __syncthreads();
+  for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n; i += (int64_t)gridDim.x * kThreads)
+    y[i] = tab[x[i]];
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------- launchers
+hipError_t run_unary(int dt, const void* x, void* y, int64_t n, int op, float alpha, hipStream_t st) {
+  if (n <= 0) return hipSuccess;
+  if (dt == DT_F32)
+    hipLaunchKernelGGL(unary_kernel<float>, dim3(grid_for(n)), dim3(kThreads), 0, st, (const float*)x, (float*)y, n,
+                       op, alpha);
+  else if (dt == DT_F16)
+    hipLaunchKernelGGL(unary_kernel<_Float16>, dim3(grid_for(n)), dim3(kThreads), 0, st, (const _Float16*)x,
+                       (_Float16*)y, n, op, alpha);
+  else
+    return hipErrorInvalidValue;
+  return hipGetLastError();
+}
+
+hipError_t run_binary(int dt, const void* a, const void* b, void* y, int64_t n, const BcastPlan& p, bool same, int op,
+                      hipStream_t st) {
+  if (n <= 0) return hipSuccess;
+  if (dt == DT_F32) {
+    if (same)
+      hipLaunchKernelGGL(binary_same_kernel<float>, dim3(grid_for(n)), dim3(kThreads), 0, st, (const float*)a,
+                         (const float*)b, (float*)y, n, op);
+    else
+      hipLaunchKernelGGL(binary_kernel<float>, dim3(grid_for(n)), dim3(kThreads), 0, st, (const float*)a,
+                         (const float*)b, (float*)y, n, p, op);
+  } else if (dt == DT_F16) {
+    if (same)
+      hipLaunchKernelGGL(binary_same_kernel<_Float16>, dim3(grid_for(n)), dim3(kThreads), 0, st, (const _Float16*)a,
+                         (const _Float16*)b, (_Float16*)y, n, op);
+    else
+      hipLaunchKernelGGL(binary_kernel<_Float16>, dim3(grid_for(n)), dim3(kThreads), 0, st, (const _Float16*)a,
+                         (const _Float16*)b, (_Float16*)y, n, p, op);
+  } else {
+    return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+hipError_t run_instnorm(int dt, const void* x, void* y, int64_t planes, int64_t spatial, int C, float eps,
+                        const NormAffine& aff, hipStream_t st) {
+  if (planes <= 0 || spatial <= 0) return hipSuccess;
+  if (planes > 0x7fffffff) return hipErrorInvalidValue;
+  if (dt == DT_F32)
+    hipLaunchKernelGGL(instnorm_kernel<float>, dim3((unsigned)planes), dim3(kThreads), 0, st, (const float*)x,
+                       (float*)y, spatial, C, eps, aff);
+  else if (dt == DT_F16)
+    hipLaunchKernelGGL(instnorm_kernel<_Float16>, dim3((unsigned)planes), dim3(kThreads), 0, st, (const _Float16*)x,
+                       (_Float16*)y, spatial, C, eps, aff);
+  else
+    return hipErrorInvalidValue;
+  return hipGetLastError();
+}
+
+#define OHIP_BY_ELEM_SIZE(eb, KERNEL, grid, ...)                                                                  \
+  do {                                                                                                             \
+    switch (eb) {                                                                                                  \
+      case 1: hipLaunchKernelGGL(KERNEL<uint8_t>, grid, dim3(kThreads), 0, st, (const uint8_t*)x, (uint8_t*)y, __VA_ARGS__); break;     \
+      case 2: hipLaunchKernelGGL(KERNEL<uint16_t>, grid, dim3(kThreads), 0, st, (const uint16_t*)x, (uint16_t*)y, __VA_ARGS__); break;  \
+      case 4: hipLaunchKernelGGL(KERNEL<uint32_t>, grid, dim3(kThreads), 0, st, (const uint32_t*)x, (uint32_t*)y, __VA_ARGS__); break;  \
+      default: return hipErrorInvalidValue;                                                                        \
+    }                                                                                                              \
+    return hipGetLastError();                                                                                      \
+  } while (0)
+
+hipError_t run_resize_nearest(int elem_bytes, const void* x, void* y, int64_t planes, const ResizePlan& p,
+                              hipStream_t st) {
+  const int64_t n = planes * p.oh * p.ow;
+  if (n <= 0) return hipSuccess;
+  OHIP_BY_ELEM_SIZE(elem_bytes, resize_nearest_kernel, dim3(grid_for(n)), planes, p);
+}
+
+hipError_t run_pad(int elem_bytes, const void* x, void* y, int64_t n, const PadPlan& p, hipStream_t st) {
+  if (n <= 0) return hipSuccess;
+  // the fill value travels as the element's bit pattern
+  OHIP_BY_ELEM_SIZE(elem_bytes, pad_kernel, dim3(grid_for(n)), n, p);
+}
+
+hipError_t run_slice(int elem_bytes, const void* x, void* y, int64_t n, const SlicePlan& p, hipStream_t st) {
+  if (n <= 0) return hipSuccess;
+  OHIP_BY_ELEM_SIZE(elem_bytes, slice_kernel, dim3(grid_for(n)), n, p);
+}
+
+hipError_t run_maxpool(int dt, const void* x, void* y, int64_t planes, const PoolPlan& p, hipStream_t st) {
+  const int64_t n = planes * p.oh * p.ow;
+  if (n <= 0) return hipSuccess;
+  const dim3 g(grid_for(n));
+  switch (dt) {
+    case DT_F32: hipLaunchKernelGGL(maxpool_kernel<float>, g, dim3(kThreads), 0, st, (const float*)x, (float*)y, planes, p); break;
+    case DT_F16: hipLaunchKernelGGL(maxpool_kernel<_Float16>, g, dim3(kThreads), 0, st, (const _Float16*)x, (_Float16*)y, planes, p); break;
+    case DT_U8: hipLaunchKernelGGL(maxpool_kernel<uint8_t>, g, dim3(kThreads), 0, st, (const uint8_t*)x, (uint8_t*)y, planes, p); break;
+    case DT_I8: hipLaunchKernelGGL(maxpool_kernel<int8_t>, g, dim3(kThreads), 0, st, (const int8_t*)x, (int8_t*)y, planes, p); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+hipError_t run_quantize(const float* x, uint8_t* y, int64_t n, float scale, float zp, float lo, float hi,
+                        hipStream_t st) {
+  if (n <= 0) return hipSuccess;
+  hipLaunchKernelGGL(quantize_kernel, dim3(grid_for(n)), dim3(kThreads), 0, st, x, y, n, scale, zp, lo, hi);
+  return hipGetLastError();
+}
+
+hipError_t run_dequantize(const uint8_t* x, bool is_signed, float* y, int64_t n, float scale, float zp,
+                          hipStream_t st) {
+  if (n <= 0) return hipSuccess;
+  if (is_signed)
+    hipLaunchKernelGGL(dequantize_kernel<true>, dim3(grid_for(n)), dim3(kThreads), 0, st, x, y, n, scale, zp);
+  else
+    hipLaunchKernelGGL(dequantize_kernel<false>, dim3(grid_for(n)), dim3(kThreads), 0, st, x, y, n, scale, zp);
+  return hipGetLastError();
+}
+
+hipError_t run_byte_table(const uint8_t* x, uint8_t* y, int64_t n, const uint8_t* table, hipStream_t st) {
+  if (n <= 0) return hipSuccess;
+  Table256 t;
+  for (int i = 0; i < 256; ++i) t.v[i] = table[i];
+  hipLaunchKernelGGL(byte_table_kernel, dim3(grid_for(n)), dim3(kThreads), 0, st, x, y, n, t);
+  return hipGetLastError();
+}
+
+}  // namespace ohip

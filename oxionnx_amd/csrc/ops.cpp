@@ -10,6 +10,8 @@
 #include <cstdlib>
 #include <cstring>
 #include <map>
+#include <memory>
+#include <unordered_map>
 #include <mutex>
 #include <new>
 #include <string>
@@ -69,10 +71,23 @@ struct ohip_weight {
   int32_t* colsum = nullptr;      // integer only
   int8_t* flip = nullptr;         // integer only, null when no channel is negated
   int kwrap = 0;                  // integer only: > 0 when each row holds two int8 halves
+                                  // (chunks per half, a multiple of 8)
+  int kreal = 0;                  // integer only: chunks of one half that hold K
   std::vector<float> scale;       // integer only (1 or rows entries)
   float* comb = nullptr;          // device, rows entries (integer only)
   float comb_a = NAN, comb_y = NAN;
   size_t bytes = 0;
+};
+
+// Stream-ordered caching pool for device buffers (activations, staging).
+// Every user of a pooled buffer runs on the context's stream, so a buffer
+// returned to the pool may be handed out again at once: the next user's work
+// is queued behind the last reads of the previous one.  Nothing is freed to
+// HIP before the context is destroyed.
+struct DevPool {
+  std::multimap<size_t, void*> free_blocks;  // capacity -> buffer
+  std::unordered_map<void*, size_t> live;    // buffer -> capacity
+  size_t held = 0;                           // bytes held from HIP
 };
 
 struct ohip_ctx {
@@ -89,10 +104,22 @@ struct ohip_ctx {
   ohip_counters counters{};
   std::string last_decline;
   std::mutex mu;
+  std::mutex pool_mu;
+  DevPool pool;
+  std::map<std::string, uint8_t*> tables;  // device copies of 256-byte output tables, by content
+};
+
+// A device buffer shared by a tensor and its aliases (Reshape and friends);
+// the last owner returns it to the pool.
+struct DevBuf {
+  ohip_ctx* ctx;
+  void* ptr;
+  ~DevBuf();
 };
 
 struct ohip_dtensor {
   ohip_ctx* ctx = nullptr;
+  std::shared_ptr<DevBuf> buf;
   void* ptr = nullptr;
   int dtype = 0;
   int rank = 0;
@@ -205,6 +232,9 @@ extern "C" void ohip_ctx_destroy(ohip_ctx* ctx) {
   for (auto* w : ctx->transients) weight_free(w);
   if (ctx->scratch) (void)hipFree(ctx->scratch);
   if (ctx->padtab) (void)hipFree(ctx->padtab);
+  for (auto& kv : ctx->tables) (void)hipFree(kv.second);
+  for (auto& kv : ctx->pool.free_blocks) (void)hipFree(kv.second);
+  for (auto& kv : ctx->pool.live) (void)hipFree(kv.first);
   if (ctx->own) (void)hipStreamDestroy(ctx->own);
   delete ctx;
 }
@@ -231,20 +261,64 @@ extern "C" int ohip_set_tile_override(ohip_ctx* ctx, int tile_id) {
 }
 
 // ------------------------------------------------------------------ memory
+static size_t pool_class(size_t bytes) {
+  if (bytes == 0) bytes = 1;
+  if (bytes <= (64u << 10)) return (bytes + 255) & ~(size_t)255;
+  if (bytes <= (16u << 20)) return (bytes + 4095) & ~(size_t)4095;
+  return (bytes + (2u << 20) - 1) & ~(((size_t)2 << 20) - 1);
+}
+
+static int pool_alloc(ohip_ctx* ctx, size_t bytes, void** p) {
+  const size_t cap = pool_class(bytes);
+  std::lock_guard<std::mutex> lock(ctx->pool_mu);
+  auto it = ctx->pool.free_blocks.lower_bound(cap);
+  if (it != ctx->pool.free_blocks.end() && it->first <= 2 * cap) {
+    *p = it->second;
+    ctx->pool.live[*p] = it->first;
+    ctx->pool.free_blocks.erase(it);
+    return OHIP_OK;
+  }
+  hipError_t e = hipMalloc(p, cap);
+  if (e != hipSuccess) {
+    // give the cached blocks back to HIP once and retry
+    (void)hipStreamSynchronize(ctx->stream);
+    for (auto& kv : ctx->pool.free_blocks) { (void)hipFree(kv.second); ctx->pool.held -= kv.first; }
+    ctx->pool.free_blocks.clear();
+    e = hipMalloc(p, cap);
+    if (e != hipSuccess) return fail(OHIP_E_NOMEM, std::string("hipMalloc: ") + hipGetErrorString(e));
+  }
+  ctx->pool.live[*p] = cap;
+  ctx->pool.held += cap;
+  return OHIP_OK;
+}
+
+static int pool_free(ohip_ctx* ctx, void* p) {
+  if (!p) return OHIP_OK;
+  std::lock_guard<std::mutex> lock(ctx->pool_mu);
+  auto it = ctx->pool.live.find(p);
+  if (it == ctx->pool.live.end()) return fail(OHIP_E_INVALID, "ohip_free: not a buffer of this context");
+  ctx->pool.free_blocks.emplace(it->second, p);
+  ctx->pool.live.erase(it);
+  return OHIP_OK;
+}
+
+DevBuf::~DevBuf() {
+  if (ptr && ctx) (void)pool_free(ctx, ptr);
+}
+
+// Device buffers come from the context's stream-ordered pool: ohip_free
+// returns a buffer for reuse by later work on the same stream without a
+// device synchronisation.
 extern "C" int ohip_malloc(ohip_ctx* ctx, size_t bytes, void** p) {
   int rc = activate(ctx);
   if (rc) return rc;
   if (!p) return fail(OHIP_E_INVALID, "null out");
-  hipError_t e = hipMalloc(p, bytes ? bytes : 1);
-  if (e != hipSuccess) return fail(OHIP_E_NOMEM, std::string("hipMalloc: ") + hipGetErrorString(e));
-  return OHIP_OK;
+  return pool_alloc(ctx, bytes, p);
 }
 extern "C" int ohip_free(ohip_ctx* ctx, void* p) {
   int rc = activate(ctx);
   if (rc) return rc;
-  HIP_TRY(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
-  HIP_TRY(hipFree(p), "hipFree");
-  return OHIP_OK;
+  return pool_free(ctx, p);
 }
 extern "C" int ohip_memcpy_h2d(ohip_ctx* ctx, void* dst, const void* src, size_t bytes) {
   int rc = activate(ctx);
@@ -558,14 +632,16 @@ extern "C" int ohip_weight_conv(ohip_ctx* ctx, const ohip_weight_key* key, int s
 //     lies in [-255, 0]) and flagged, and the epilogue negates it back;
 //   * when any stored value leaves [-128, 127], every row holds two int8
 //     halves v1 = clamp(v, -128, 127) and v2 = v - v1 (both in range), laid
-//     out as [v1 row | v2 row]; the activation is re-read for the second half
-//     (kwrap), which doubles K but keeps the int8 MFMA path exact.
+//     out as [v1 row | v2 row], each half padded with zeros to a multiple of
+//     128 bytes (one MFMA stage); the activation is re-read for the second
+//     half (kwrap), which doubles K but keeps the int8 MFMA path exact.
 struct QPacked {
   std::vector<int8_t> data;
   std::vector<int32_t> colsum;
   std::vector<int8_t> flip;
   bool any_flip = false;
   int64_t kp = 0;
+  int64_t half = 0;  // bytes per half of a split row (kp rounded up to 128)
   bool split = false;
 };
 
@@ -600,21 +676,23 @@ static void qpack_rows(int64_t rows, int64_t kp, int64_t klen, ValueAt value_at,
   }
   q.kp = kp;
   q.split = lo < -128 || hi > 127;
-  const int64_t width = q.split ? 2 * kp : kp;
+  q.half = q.split ? (kp + 127) / 128 * 128 : kp;
+  const int64_t width = q.split ? 2 * q.half : kp;
   q.data.assign((size_t)(rows * width), 0);
   for (int64_t r = 0; r < rows; ++r)
     for (int64_t j = 0; j < kp; ++j) {
       const int32_t x = v[(size_t)(r * kp + j)];
       const int32_t a = std::min(127, std::max(-128, x));
       q.data[(size_t)(r * width + j)] = (int8_t)a;
-      if (q.split) q.data[(size_t)(r * width + kp + j)] = (int8_t)(x - a);
+      if (q.split) q.data[(size_t)(r * width + q.half + j)] = (int8_t)(x - a);
     }
 }
 
 static int qpack_upload(ohip_ctx* ctx, ohip_weight* w, const QPacked& q, const float* scale, int n_scale) {
-  w->kwrap = q.split ? (int)(q.kp / 16) : 0;
-  w->kc = (int)((q.split ? 2 * q.kp : q.kp) / 16);
-  w->ld_bytes = q.split ? 2 * q.kp : q.kp;
+  w->kwrap = q.split ? (int)(q.half / 16) : 0;
+  w->kreal = (int)(q.kp / 16);
+  w->kc = (int)((q.split ? 2 * q.half : q.kp) / 16);
+  w->ld_bytes = q.split ? 2 * q.half : q.kp;
   int rc = weight_upload(ctx, w, q.data.data(), q.data.size());
   if (rc) return rc;
   hipError_t e = hipMalloc(&w->colsum, q.colsum.size() * 4);
@@ -734,6 +812,16 @@ static int ensure_comb(ohip_ctx* ctx, ohip_weight* w, float a_s, float y_s, int*
 // ------------------------------------------------------------------ helpers
 static bool aligned(const void* p, size_t a) { return ((uintptr_t)p % a) == 0; }
 
+// Dense MFMA operands are addressed through a buffer resource with 32-bit
+// offsets: the whole operand must lie below 2^31 bytes.
+static bool dense_fits(const DenseOperand& d) {
+  return (int64_t)d.rows * d.ld_bytes <= (int64_t)INT32_MAX - 4096;
+}
+#define DENSE_FITS_OR_DECLINE(op, where)                                          \
+  do {                                                                          \
+    if (!dense_fits(op)) return fail(OHIP_DECLINED, where ": operand exceeds 2 GiB"); \
+  } while (0)
+
 // Device address of sixteen copies of byte b (the MFMA loaders' pad source).
 static const void* pad16(ohip_ctx* ctx, uint8_t b) { return ctx->padtab + (size_t)b * 16; }
 
@@ -818,6 +906,8 @@ extern "C" int ohip_gemm(ohip_ctx* ctx, const ohip_gemm_desc* d, const void* a, 
   } else {
     DenseOperand x{b->data, b->ld_bytes, (int)N, b->kc, 0, 0u, pad16(ctx, 0)};
     DenseOperand yv{av.p, av.ld_bytes, (int)M, av.kc, 0, 0u, pad16(ctx, 0)};
+    DENSE_FITS_OR_DECLINE(x, "ohip_gemm");
+    DENSE_FITS_OR_DECLINE(yv, "ohip_gemm");
     e = run_dense_float(d->dtype, x, yv, o, ctx->tile_override, ctx->stream);
   }
   if (e != hipSuccess) return hip_fail(e, "ohip_gemm launch");
@@ -905,6 +995,7 @@ extern "C" int ohip_conv2d(ohip_ctx* ctx, const ohip_conv_desc* d, const void* x
     o.vec = ldo % 4 == 0 && aligned(y, 4 * eb);
     o.bias_mode = BIAS_I;
   }
+  DENSE_FITS_OR_DECLINE(wt, "ohip_conv2d");
   hipError_t e = run_conv_float(d->dtype, col, wt, col_on_x, o, ctx->tile_override, ctx->stream);
   if (e != hipSuccess) return hip_fail(e, "ohip_conv2d launch");
   return OHIP_OK;
@@ -968,8 +1059,25 @@ extern "C" int ohip_qgemm(ohip_ctx* ctx, const ohip_qgemm_desc* d, const void* a
   o.comb = b->comb; o.n_comb = n_comb; o.out_kind = d->out_kind; o.y_zp = d->y_zp; o.lo = d->lo; o.hi = d->hi;
   DenseOperand x{b->data, b->ld_bytes, (int)N, b->kc, 0, 0u, pad16(ctx, 0)};
   DenseOperand yv{pa, lda_b, (int)M, (int)(kp / 16), b->kwrap, u8 ? 0x80808080u : 0u, pad16(ctx, 0)};
+  DENSE_FITS_OR_DECLINE(x, "ohip_qgemm");
+  DENSE_FITS_OR_DECLINE(yv, "ohip_qgemm");
   hipError_t e = run_dense_quant(x, yv, o, ctx->tile_override, ctx->stream);
   if (e != hipSuccess) return hip_fail(e, "ohip_qgemm launch");
+  return OHIP_OK;
+}
+
+// Device copy of a 256-byte output table, uploaded once per distinct content
+// (called with ctx->mu held).
+static int device_table(ohip_ctx* ctx, const uint8_t* host, const uint8_t** out) {
+  std::string key(reinterpret_cast<const char*>(host), 256);
+  auto it = ctx->tables.find(key);
+  if (it != ctx->tables.end()) { *out = it->second; return OHIP_OK; }
+  uint8_t* d = nullptr;
+  hipError_t e = hipMalloc(&d, 256);
+  if (e != hipSuccess) return fail(OHIP_E_NOMEM, "table hipMalloc");
+  HIP_TRY(hipMemcpy(d, host, 256, hipMemcpyHostToDevice), "table upload");
+  ctx->tables.emplace(key, d);
+  *out = d;
   return OHIP_OK;
 }
 
@@ -1024,13 +1132,20 @@ extern "C" int ohip_qconv2d(ohip_ctx* ctx, const ohip_qconv_desc* d, const void*
   col.KW = (int)d->kw; col.cpc = (int)(cp / 16);
   col.sh = (int)d->stride_h; col.sw = (int)d->stride_w; col.dh = (int)d->dil_h; col.dw = (int)d->dil_w;
   col.pt = (int)d->pad_t; col.pl = (int)d->pad_l; col.rows = (int)rows;
-  col.kc = w->kwrap > 0 ? w->kwrap : w->kc; col.kwrap = w->kwrap;
+  col.kc = w->kwrap > 0 ? w->kreal : w->kc; col.kwrap = w->kwrap;
   col.xor_mask = u8 ? 0x80808080u : 0u;
   col.pad16 = pad16(ctx, padb);
   DenseOperand wt{w->data, w->ld_bytes, (int)d->cout, w->kc, 0, 0u, pad16(ctx, 0)};
   QuantOut o{};
   o.y = y; o.colsum = w->colsum; o.flip = w->flip; o.bias = bias; o.ca = shift - d->x_zp; o.ca_rows = nullptr;
   o.comb = w->comb; o.n_comb = n_comb; o.out_kind = d->out_kind; o.y_zp = d->y_zp; o.lo = d->lo; o.hi = d->hi;
+  o.table = nullptr;
+  if (d->out_table) {
+    if (d->out_kind != OHIP_QOUT_U8 && d->out_kind != OHIP_QOUT_I8)
+      return fail(OHIP_E_INVALID, "ohip_qconv2d: an output table needs a byte output");
+    rc = device_table(ctx, d->out_table, &o.table);
+    if (rc) return rc;
+  }
   const int ob = (d->out_kind == OHIP_QOUT_I32 || d->out_kind == OHIP_QOUT_F32) ? 4 : 1;
   const int64_t ohw = g.oh * g.ow;
   bool col_on_x;
@@ -1046,6 +1161,7 @@ extern "C" int ohip_qconv2d(ohip_ctx* ctx, const ohip_qconv_desc* d, const void*
     o.vec = ldo % 4 == 0 && aligned(y, 4 * ob);
     o.w_on_i = 1;
   }
+  DENSE_FITS_OR_DECLINE(wt, "ohip_qconv2d");
   hipError_t e = run_conv_quant(col, wt, col_on_x, o, ctx->tile_override, ctx->stream);
   if (e != hipSuccess) return hip_fail(e, "ohip_qconv2d launch");
   return OHIP_OK;
@@ -1076,14 +1192,12 @@ extern "C" int ohip_dtensor_alloc(ohip_ctx* ctx, int dtype, int rank, const int6
   auto* t = new ohip_dtensor();
   t->ctx = ctx; t->dtype = dtype; t->rank = rank; t->layout = layout; t->bytes = bytes;
   for (int i = 0; i < rank; ++i) t->shape[i] = shape[i];
-  hipError_t e = hipMalloc(&t->ptr, bytes ? bytes : 16);
-  if (e != hipSuccess) {
-    delete t;
-    return fail(OHIP_E_NOMEM, std::string("dtensor hipMalloc: ") + hipGetErrorString(e));
-  }
+  rc = pool_alloc(ctx, bytes ? bytes : 16, &t->ptr);
+  if (rc) { delete t; return rc; }
+  t->buf = std::shared_ptr<DevBuf>(new DevBuf{ctx, t->ptr});
   if (layout == OHIP_NHWC) {  // channel padding must read as zero
-    e = hipMemsetAsync(t->ptr, 0, bytes, ctx->stream);
-    if (e != hipSuccess) { (void)hipFree(t->ptr); delete t; return hip_fail(e, "dtensor memset"); }
+    hipError_t e = hipMemsetAsync(t->ptr, 0, bytes, ctx->stream);
+    if (e != hipSuccess) { delete t; return hip_fail(e, "dtensor memset"); }
   }
   *out = t;
   return OHIP_OK;
@@ -1097,6 +1211,23 @@ extern "C" int ohip_dtensor_wrap(ohip_ctx* ctx, void* p, int dtype, int rank, co
   if (rc) return rc;
   auto* t = new ohip_dtensor();
   t->ctx = ctx; t->ptr = p; t->dtype = dtype; t->rank = rank; t->layout = OHIP_NCHW; t->bytes = bytes;
+  t->buf = std::shared_ptr<DevBuf>(new DevBuf{ctx, p});
+  for (int i = 0; i < rank; ++i) t->shape[i] = shape[i];
+  *out = t;
+  return OHIP_OK;
+}
+
+// A second tensor over the same buffer (a Reshape / Flatten / Squeeze /
+// Unsqueeze result): same bytes, new shape, shared ownership.
+int ohip_dtensor_alias_internal(const ohip_dtensor* src, int rank, const int64_t* shape, ohip_dtensor** out) {
+  if (!src || !out || rank < 0 || rank > 8) return fail(OHIP_E_INVALID, "dtensor_alias: bad argument");
+  size_t bytes;
+  int rc = dt_bytes(src->dtype, rank, shape, OHIP_NCHW, &bytes);
+  if (rc) return rc;
+  if (bytes != src->bytes || src->layout != OHIP_NCHW) return fail(OHIP_E_INVALID, "dtensor_alias: size mismatch");
+  auto* t = new ohip_dtensor();
+  t->ctx = src->ctx; t->buf = src->buf; t->ptr = src->ptr; t->dtype = src->dtype; t->rank = rank;
+  t->layout = OHIP_NCHW; t->bytes = bytes;
   for (int i = 0; i < rank; ++i) t->shape[i] = shape[i];
   *out = t;
   return OHIP_OK;
@@ -1124,12 +1255,7 @@ extern "C" int ohip_dtensor_info(const ohip_dtensor* t, int* dtype, int* rank, i
 }
 extern "C" void ohip_dtensor_free(ohip_dtensor* t) {
   if (!t) return;
-  if (t->ptr) {
-    (void)hipSetDevice(t->ctx->device);
-    (void)hipStreamSynchronize(t->ctx->stream);
-    (void)hipFree(t->ptr);
-  }
-  delete t;
+  delete t;  // the last owner of the buffer returns it to the pool
 }
 
 // ------------------------------------------------------------------ gating / declines

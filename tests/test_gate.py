@@ -93,13 +93,23 @@ def test_mi355x_class_admits_every_configured_workload():
 
 
 def test_op_support_predicates():
-    for op in ["Conv", "Gemm", "MatMul", "QLinearMatMul", "MatMulInteger", "QLinearConv", "ConvInteger"]:
-        assert ep.is_supported_op(op)
-    for op in ["Relu", "Transpose", "Add", "ConvTranspose", ""]:
+    # the contraction arms plus the memory-bound arms of the reference CUDA
+    # provider's claim list (oxionnx-cuda/src/lib.rs:101-119) that conv
+    # networks need between their contractions
+    for op in ["Conv", "Gemm", "MatMul", "QLinearMatMul", "MatMulInteger", "QLinearConv", "ConvInteger",
+               "Relu", "LeakyRelu", "Tanh", "Sigmoid", "Silu", "Add", "Sub", "Mul", "Div", "OxiInstanceNorm",
+               "InstanceNormalization", "Resize", "Pad", "MaxPool", "Concat", "Slice", "Reshape", "Flatten",
+               "Squeeze", "Unsqueeze", "QuantizeLinear", "DequantizeLinear"]:
+        assert ep.is_supported_op(op), op
+    for op in ["Transpose", "ConvTranspose", "Softmax", "LSTM", ""]:
         assert not ep.is_supported_op(op)
     assert ep.accepts_resident_slot("Conv", 0) and not ep.accepts_resident_slot("Conv", 1)
     assert ep.accepts_resident_slot("Gemm", 0) and not ep.accepts_resident_slot("Gemm", 1)
-    assert not ep.accepts_resident_slot("QLinearConv", 0)
+    assert ep.accepts_resident_slot("QLinearConv", 0) and not ep.accepts_resident_slot("QLinearConv", 3)
+    assert ep.accepts_resident_slot("Add", 1) and not ep.accepts_resident_slot("Add", 2)
+    assert ep.accepts_resident_slot("Concat", 3)
+    assert not ep.accepts_resident_slot("QLinearMatMul", 0)
+    assert not ep.accepts_resident_slot("Reshape", 1)
 
 
 def test_try_new_is_gated_by_the_env_flag(monkeypatch):
