@@ -100,6 +100,10 @@ void orc_apply_activation(float* data, int64_t count, int act, float lo, float h
 
 int orc_hardware_threads(void);
 
+/* elementwise nodes (oracle_float.c) */
+void orc_unary_f32(float* data, int64_t count, int op, float alpha);
+void orc_instance_norm_f32(float* data, int64_t planes, int64_t spatial, float eps);
+
 #ifdef __cplusplus
 }
 #endif

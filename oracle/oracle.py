@@ -92,6 +92,8 @@ def lib():
         L.orc_satrange_infer.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p,
                                          ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
         L.orc_resolve_pads2d.argtypes = [ctypes.c_int] + [ctypes.c_void_p] * 6
+        L.orc_unary_f32.argtypes = [ctypes.c_void_p, I64, ctypes.c_int, ctypes.c_float]
+        L.orc_instance_norm_f32.argtypes = [ctypes.c_void_p, I64, I64, ctypes.c_float]
     return _lib
 
 

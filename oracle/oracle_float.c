@@ -202,3 +202,43 @@ void orc_apply_activation(float* data, int64_t count, int act, float lo, float h
             }
     }
 }
+
+/* ---------------------------------------------------------------- elementwise nodes
+ * Unary activations, element by element in f32 with the C library's
+ * functions (the reference's f32::exp / f32::tanh lower to the same libm
+ * expf / tanhf on this platform):
+ *   op 0 LeakyRelu  nn/activations.rs:87-95      v >= 0 ? v : alpha * v
+ *   op 1 Tanh       nn/activations.rs:52-56      tanhf(v)
+ *   op 2 Sigmoid    nn/activations.rs:35-40      1 / (1 + expf(-v))
+ *   op 3 Silu       registry/nn_ops/activations.rs:477-479   v / (1 + expf(-v))
+ *   op 4 Relu       nn/activations.rs:16-21      v.max(0) (NaN -> 0) */
+void orc_unary_f32(float* data, int64_t count, int op, float alpha) {
+    for (int64_t i = 0; i < count; ++i) {
+        const float v = data[i];
+        switch (op) {
+            case 0: data[i] = v >= 0.0f ? v : alpha * v; break;
+            case 1: data[i] = tanhf(v); break;
+            case 2: data[i] = 1.0f / (1.0f + expf(-v)); break;
+            case 3: data[i] = v / (1.0f + expf(-v)); break;
+            default: data[i] = v > 0.0f ? v : 0.0f; break;
+        }
+    }
+}
+
+/* OxiInstanceNorm normalize_plane (registry/oxi_instance_norm.rs:56-65): per
+ * (n, c) plane, mean as an ascending f32 sum / count, variance about it the
+ * same way, then (v - mean) * (1 / sqrt(var + eps)). */
+void orc_instance_norm_f32(float* data, int64_t planes, int64_t spatial, float eps) {
+    for (int64_t p = 0; p < planes; ++p) {
+        float* x = data + p * spatial;
+        const float count = (float)spatial;
+        float s = 0.0f;
+        for (int64_t i = 0; i < spatial; ++i) s += x[i];
+        const float mean = s / count;
+        float q = 0.0f;
+        for (int64_t i = 0; i < spatial; ++i) q += (x[i] - mean) * (x[i] - mean);
+        const float var = q / count;
+        const float inv = 1.0f / sqrtf(var + eps);
+        for (int64_t i = 0; i < spatial; ++i) x[i] = (x[i] - mean) * inv;
+    }
+}

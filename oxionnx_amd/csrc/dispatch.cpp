@@ -545,12 +545,12 @@ int do_qmatmul(ohip_ctx* ctx, const ohip_node* nd, bool qlinear, int placement, 
 bool silu_table(const ohip_node* nd, bool in_signed, int32_t in_zp, float in_scale, uint8_t* table, int* out_dt) {
   if (attr_s(nd, "activation") != "silu") return false;
   const float ys = attr_f(nd, "activation_y_scale", NAN);
-  const int64_t yz = attr_i(nd, "activation_y_zero_point", 0);
   if (!std::isfinite(ys) || ys == 0.0f) return false;
-  std::string ydt = attr_s(nd, "activation_y_dtype");
-  bool u8 = yz > 127;
-  if (ydt == "uint8") u8 = true;
-  else if (ydt == "int8") u8 = false;
+  // saturation_range (quantize.rs:58-66): no zero point -> u8; a zero point
+  // above 127 -> u8; any other zero point -> i8
+  const bool has_zp = find_attr(nd, "activation_y_zero_point") != nullptr;
+  const int64_t yz = attr_i(nd, "activation_y_zero_point", 0);
+  const bool u8 = !has_zp || yz > 127;
   const float lo = u8 ? 0.0f : -128.0f, hi = u8 ? 255.0f : 127.0f;
   for (int b = 0; b < 256; ++b) {
     const int32_t q = in_signed ? (int32_t)(int8_t)b : b;
@@ -1169,8 +1169,7 @@ int do_alias(ohip_ctx* ctx, const ohip_node* nd, const std::string& op, int plac
 }
 
 // ---------------------------------------------------------------- QuantizeLinear / DequantizeLinear
-// Per-tensor parameters only (quantize.rs:96-190).  The output integer
-// type follows saturation_range (:58-66), or y_zero_point's declared dtype.
+// Per-tensor parameters only (quantize.rs:96-190).
 int do_quantize(ohip_ctx* ctx, const ohip_node* nd, int placement, ohip_output* out) {
   const ohip_tensor *x = input(nd, 0), *s = input(nd, 1), *z = input(nd, 2);
   if (!x) return decline("QuantizeLinear: missing input");
@@ -1183,9 +1182,9 @@ int do_quantize(ohip_ctx* ctx, const ohip_node* nd, int placement, ohip_output* 
   if (z && !host_only(z)) return decline("QuantizeLinear: zero point");
   if (z && numel(z) == 0) return decline("QuantizeLinear: empty zero point");
   if (z) zp = (float)host_at(z, 0);
-  bool u8 = !z || zp > 127.0f;
-  if (z && z->declared_dtype == OHIP_U8) u8 = true;
-  if (z && z->declared_dtype == OHIP_I8) u8 = false;
+  // saturation_range (quantize.rs:58-66): the output type follows the zero
+  // point's value, as in the reference (its Tensor carries no dtype tag)
+  const bool u8 = !z || zp > 127.0f;
   const float lo = u8 ? 0.0f : -128.0f, hi = u8 ? 255.0f : 127.0f;
   Stage st(ctx);
   const void* xd = float_operand(st, x, OHIP_F32);

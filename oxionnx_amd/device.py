@@ -76,6 +76,7 @@ class HipContext:
         torch = _torch()
         self.device = device
         self._weights = weakref.WeakSet()
+        self._dtensors = weakref.WeakSet()
         h = ctypes.c_void_p()
         L.check(L.lib().ohip_ctx_create(device, ctypes.byref(h)))
         self.h = h
@@ -93,6 +94,8 @@ class HipContext:
         if self.h:
             for w in list(self._weights):
                 w.handle = None       # the context frees every weight it owns
+            for t in list(self._dtensors):
+                t.free()              # device tensors return their buffers to the context's pool
             L.lib().ohip_ctx_destroy(self.h)
             self.h = None
 

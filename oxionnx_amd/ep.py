@@ -134,8 +134,10 @@ class DeviceTensor:
     """HipDeviceTensor: a run-scoped device activation (implements the
     DeviceActivation contract of src/session/gpu_activations.rs:117-189)."""
 
-    def __init__(self, handle):
+    def __init__(self, handle, ctx=None):
         self.h = handle
+        if ctx is not None:
+            ctx._dtensors.add(self)   # freed by the context's close() if still alive
         dt, rank = ctypes.c_int(), ctypes.c_int()
         shape = (L.I64 * 8)()
         nbytes = ctypes.c_size_t()
@@ -149,7 +151,7 @@ class DeviceTensor:
         h = ctypes.c_void_p()
         L.check(L.lib().ohip_dtensor_alloc(ctx.h, _NP2OHIP[arr.dtype], arr.ndim, shape, L.NCHW, ctypes.byref(h)))
         L.check(L.lib().ohip_dtensor_upload(ctx.h, h, arr.ctypes.data_as(ctypes.c_void_p)))
-        return cls(h)
+        return cls(h, ctx)
 
     def to_host(self, ctx):
         out = np.empty(self.shape, _OHIP2NP[self.dtype])
@@ -191,7 +193,7 @@ def _dispatch(node, weights, intermediates, ctx, placement):
     L.check(rc)
     shape = tuple(out.shape[:out.rank])
     if placement == L.PLACE_DEVICE:
-        return [DeviceTensor(out.device)]
+        return [DeviceTensor(out.device, ctx)]
     dt = _OHIP2NP[out.dtype]
     n = int(np.prod(shape)) if shape else 1
     buf = (ctypes.c_char * (n * np.dtype(dt).itemsize)).from_address(out.data)
