@@ -170,6 +170,7 @@ def main():
             extras["gemm_sweep"] = sweep
             extras.update(bench_conv(torch, ctx, L, stream, rng, args.only))
             extras.update(bench_int8(torch, ctx, L, stream, rng, args.only))
+            extras.update(bench_e2e(torch, ctx, stream, args.only, args.no_cpu))
 
     line = {
         "metric": METRIC, "value": round(tflops, 2), "unit": "TFLOP/s", "n_gpus": 1,
@@ -239,6 +240,57 @@ def bench_int8(torch, ctx, L, stream, rng, only):
     by = 4096 * 768 + 768 * 3072 + 4 * 4096 * 3072
     out["matmul_integer_i32"] = {"ms": round(t, 5), "tops": round(ops / 2 / t / 1e9, 2),
                                  "gbps": round(by / t / 1e6, 1), "frac_hbm": round(by / t / 1e6 / HBM_GBPS, 4)}
+    return out
+
+
+def bench_e2e(torch, ctx, stream, only, no_cpu):
+    """Configs 4 and 5 end to end: ms per forward through the session run loop
+    (graph inputs uploaded, every node dispatched through ohip_try_dispatch,
+    outputs downloaded), median of 10 forwards after 2 warm-up forwards; the
+    device-side time of the same forwards from events on the context's
+    stream; and the CPU graph oracle's time for one forward (the reference's
+    algorithms restated: multi-threaded im2col + sgemm convolution like its
+    rayon path, single-threaded integer convolution like its integer_conv)."""
+    from oxionnx_amd import workloads
+    from oxionnx_amd.session import Session
+    names = {"e2e_face_swap_f32": lambda: workloads.face_swap_generator(dtype="f32"),
+             "e2e_face_swap_f16": lambda: workloads.face_swap_generator(dtype="f16"),
+             "e2e_yolo_backbone_int8": lambda: workloads.yolo_backbone_int8(size=640)}
+    threads = max(1, min(16, int(os.environ.get("OMP_NUM_THREADS", "16"))))
+    out = {}
+    for key, make in names.items():
+        if only and only != key:
+            continue
+        g, feeds = make()
+        sess = Session(g, ctx)
+        for _ in range(2):
+            sess.run(feeds)
+        walls, gpus = [], []
+        for _ in range(10):
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            t0 = time.perf_counter()
+            e0.record(stream)
+            sess.run(feeds)
+            e1.record(stream)
+            walls.append((time.perf_counter() - t0) * 1e3)
+            torch.cuda.synchronize()
+            gpus.append(e0.elapsed_time(e1))
+        rec = {"ms_per_forward": round(float(np.median(walls)), 3),
+               "stream_ms": round(float(np.median(gpus)), 3),
+               "nodes": len(g.nodes), "nodes_after_fusion": len(sess.graph.nodes),
+               "conv_gmac": round(g.notes["conv_gmac"], 3),
+               "note": "wall clock per forward incl. input upload, Python run loop and output download"}
+        if not no_cpu and not only:
+            from oracle import graph_ref
+            t0 = time.perf_counter()
+            graph_ref.run_graph(g, feeds, half=key.endswith("f16"), nthreads=threads)
+            cpu = (time.perf_counter() - t0) * 1e3
+            rec["cpu_baseline"] = {"ms_per_forward": round(cpu, 1), "kind": "port",
+                                   "cores": 1 if "int8" in key else threads,
+                                   "sample": "one full forward of the same graph and inputs"}
+            rec["speedup_vs_cpu"] = round(cpu / rec["ms_per_forward"], 1)
+        out[key] = rec
     return out
 
 

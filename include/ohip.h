@@ -319,7 +319,11 @@ int ohip_reset_counters(ohip_ctx* ctx);
 
 /* Testing / tuning knob: force the MFMA block tile, 0 = automatic.
  * 1: 64x64 (4 waves)   2: 128x128 (4)   3: 256x128 (8)   4: 128x256 (8)
- * 5: 256x256 (4)       6: 256x256 (8) */
+ * 5: 256x256 (4)       6: 256x256 (8)   7: 128x128 (4, two LDS stages)
+ * 8: 128x128 (8, two LDS stages)           9: 64x64 (4, four LDS stages)
+ * 10: split-K over 64x64 (4, four LDS stages) tiles with an ordered reduction.
+ * The automatic choice splits K when the 64x64 tiling gives fewer than 256
+ * blocks and K is at least 16 stages of 128 bytes. */
 int ohip_set_tile_override(ohip_ctx* ctx, int tile_id);
 
 #ifdef __cplusplus

@@ -116,7 +116,7 @@ def run_graph(graph, feeds, half=False, nthreads=None):
                       dilations=a.int_lists.get("dilations"), group=a.ints.get("group", 1))
             if half:
                 yb = O.conv_half(O.f32_to_half_bits(x), O.f32_to_half_bits(w),
-                                 None if b is None else O.f32_to_half_bits(b), **kw)
+                                 None if b is None else O.f32_to_half_bits(b), nthreads=nthreads, **kw)
                 y = O.half_bits_to_f32(yb)
             else:
                 y = O.conv(x, w, b, nthreads=nthreads, **kw)

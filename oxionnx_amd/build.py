@@ -20,7 +20,7 @@ LIB = os.path.join(HERE, "libohip.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 
-SOURCES = ["contract_f32.hip", "contract_f16.hip", "contract_bf16.hip", "contract_i8.hip", "aux_kernels.hip", "nodes.hip", "ops.cpp", "dispatch.cpp"]
+SOURCES = [f"contract_{dt}_{part}.hip" for dt in ("i8", "f16", "f32", "bf16") for part in ("dense", "conv")] + [ "aux_kernels.hip", "nodes.hip", "ops.cpp", "dispatch.cpp"]
 
 FLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-ffp-contract=off",

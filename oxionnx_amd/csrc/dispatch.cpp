@@ -18,6 +18,8 @@
 #include "internal.hpp"
 
 int ohip_dtensor_alias_internal(const ohip_dtensor* src, int rank, const int64_t* shape, ohip_dtensor** out);
+int ohip_const_operand_internal(ohip_ctx* ctx, const char* name, const char* label, int dtype, const void* host,
+                                size_t bytes, const void** dev);
 
 namespace {
 
@@ -214,6 +216,18 @@ struct Stage {
     bufs.push_back(p);
     return p;
   }
+  // A host initializer operand (already converted to `host` / `bytes`, in
+  // dtype `dt`): the context's session-lifetime device copy.  Any other host
+  // tensor is copied for this call.
+  const void* cached(const ohip_tensor* t, const char* label, int dt, const void* host, size_t bytes) {
+    if (t->device) return ohip_dtensor_ptr(t->device);
+    if (t->is_initializer && t->name && *t->name) {
+      const void* d = nullptr;
+      if (ohip_const_operand_internal(ctx, t->name, label, dt, host, bytes, &d) != OHIP_OK) return nullptr;
+      return d;
+    }
+    return operand(t, host, bytes);
+  }
   // A device copy of a host tensor (or the resident pointer itself).
   const void* operand(const ohip_tensor* t, const void* host_override = nullptr, size_t bytes = 0) {
     if (t->device && !host_override) return ohip_dtensor_ptr(t->device);
@@ -371,9 +385,9 @@ int do_conv(ohip_ctx* ctx, const ohip_node* nd, int placement, ohip_output* out)
     if (b->dtype != dt) {  // e.g. f32 bias lanes on a typed conv: round once (RNE)
       bconv.resize((size_t)g.cout * ebytes(dt));
       for (int64_t i = 0; i < g.cout; ++i) put_elem(dt, bconv.data(), i, host_at(b, i));
-      bd = st.operand(b, bconv.data(), bconv.size());
+      bd = st.cached(b, "Conv.B", dt, bconv.data(), bconv.size());
     } else {
-      bd = st.operand(b);
+      bd = st.cached(b, "Conv.B", dt, b->data, (size_t)numel(b) * ebytes(dt));
     }
   }
   const auto oshape = conv_out_shape(g);
@@ -461,7 +475,7 @@ int do_gemm(ohip_ctx* ctx, const ohip_node* nd, bool is_matmul, int placement, o
       int64_t r = c_kind == OHIP_C_FULL ? i / n : 0, col = c_kind == OHIP_C_SCALAR ? 0 : i % n;
       put_elem(dt, cbuf.data(), i, host_at(c, (cr == 1 ? 0 : r) * cc + (cc == 1 ? 0 : col)));
     }
-    cd = st.operand(c, cbuf.data(), cbuf.size());
+    cd = st.cached(c, is_matmul ? "MatMul.C" : "Gemm.C", dt, cbuf.data(), cbuf.size());
   }
   const size_t obytes = (size_t)(m * n) * ebytes(dt);
   void* yd = st.alloc(obytes);
@@ -647,7 +661,7 @@ int do_qconv(ohip_ctx* ctx, const ohip_node* nd, bool qlinear, int placement, oh
   if (rc) return rc;
   Stage st(ctx);
   const void* xd = x->device ? ohip_dtensor_ptr(x->device) : st.operand(x, xb.data(), xb.size());
-  const void* bd = bias ? st.operand(bias, bias_i.data(), bias_i.size() * 4) : nullptr;
+  const void* bd = bias ? st.cached(bias, "QLinearConv.B", OHIP_I32, bias_i.data(), bias_i.size() * 4) : nullptr;
   const size_t ob = (out_kind == OHIP_QOUT_U8 || out_kind == OHIP_QOUT_I8) ? 1 : 4;
   const size_t obytes = (size_t)(g.n * g.cout * g.oh * g.ow) * ob;
   void* yd = st.alloc(obytes);
@@ -689,11 +703,11 @@ int node_float_dtype(const ohip_node* nd) {
 // (which must already be dt), or a converted upload of a host tensor.
 const void* float_operand(Stage& st, const ohip_tensor* t, int dt) {
   if (t->device) return t->dtype == dt ? ohip_dtensor_ptr(t->device) : nullptr;
-  if (t->dtype == dt) return st.operand(t);
+  if (t->dtype == dt) return st.cached(t, "float operand", dt, t->data, (size_t)numel(t) * ebytes(dt));
   const int64_t n = numel(t);
   std::vector<char> buf((size_t)n * ebytes(dt));
   for (int64_t i = 0; i < n; ++i) put_elem(dt, buf.data(), i, host_at(t, i));
-  return st.operand(t, buf.data(), buf.size());
+  return st.cached(t, "float operand", dt, buf.data(), buf.size());
 }
 
 std::vector<int64_t> shape_of(const ohip_tensor* t) { return std::vector<int64_t>(t->shape, t->shape + t->rank); }
@@ -809,8 +823,8 @@ int do_instnorm(ohip_ctx* ctx, const ohip_node* nd, bool affine, int placement, 
     if (!s || !b || !host_only(s) || !host_only(b) || numel(s) != C || numel(b) != C)
       return decline("InstanceNormalization: scale / B");
     for (int64_t i = 0; i < C; ++i) { sc.push_back((float)host_at(s, i)); bi.push_back((float)host_at(b, i)); }
-    aff.scale = static_cast<const float*>(st.operand(s, sc.data(), sc.size() * 4));
-    aff.bias = static_cast<const float*>(st.operand(b, bi.data(), bi.size() * 4));
+    aff.scale = static_cast<const float*>(st.cached(s, "InstanceNormalization.scale", OHIP_F32, sc.data(), sc.size() * 4));
+    aff.bias = static_cast<const float*>(st.cached(b, "InstanceNormalization.B", OHIP_F32, bi.data(), bi.size() * 4));
     if (!aff.scale || !aff.bias) return OHIP_E_NOMEM;
   }
   const void* xd = float_operand(st, x, dt);

@@ -5,6 +5,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <algorithm>
+
 namespace ohip {
 
 // ONNX TensorProto element type codes (the public header uses the same).
@@ -42,7 +44,28 @@ struct OutMap {
   int64_t si, sj, bstride;
   int ohw, P, Q;
   int vec;
+  int splits;      // > 1: split-K over `splits` slices, partial sums in split_ws
+  void* split_ws;  // splits * Q * round_up(P, 4) accumulators (4 bytes each)
 };
+
+// Split-K plan: a contraction whose 64x64 tiling leaves the 256 CUs short
+// of blocks and whose K loop is long is cut into K slices (each at least 8
+// stages of 128 bytes), aiming at two blocks per CU.  forced_tile 10 forces
+// the split path; any other forced tile disables it.
+inline int plan_splits(int P, int Q, int kc, int forced_tile) {
+  if (forced_tile != 0 && forced_tile != 10) return 1;
+  const int64_t nk = (kc + 7) / 8;
+  const int64_t nb = (int64_t)((P + 63) / 64) * ((Q + 63) / 64);
+  if (forced_tile == 10) return (int)std::max<int64_t>(2, std::min<int64_t>(16, nk / 2 > 0 ? nk / 2 : 1));
+  if (nb >= 256 || nk < 16) return 1;
+  int64_t s = (512 + nb - 1) / nb;
+  s = std::min<int64_t>(s, nk / 8);
+  s = std::min<int64_t>(s, 16);
+  return (int)std::max<int64_t>(s, 1);
+}
+inline size_t split_ws_bytes(int P, int Q, int splits) {
+  return splits > 1 ? (size_t)splits * (size_t)Q * (size_t)((P + 3) / 4 * 4) * 4 : 0;
+}
 
 struct FloatOut : OutMap {
   float alpha, beta;

@@ -7,6 +7,8 @@
 #include "internal.hpp"
 #include "mfma_core.hpp"
 
+#include <type_traits>
+
 namespace ohip {
 
 // ---------------------------------------------------------------- epilogues
@@ -55,6 +57,29 @@ template <class OutT> struct FloatEpi {
     if (bstride == 0) return (int64_t)i * si + (int64_t)j * sj;
     const int n = i / ohw;
     return (int64_t)n * bstride + (int64_t)(i - n * ohw) * si + (int64_t)j * sj;
+  }
+  // LDS-staged epilogue (mfma_core.hpp): 1- and 2-byte outputs are written as
+  // whole 16-byte row chunks when rows of i are contiguous and aligned.
+  static constexpr int kStageBytes = sizeof(OutT) <= 2 ? (int)sizeof(OutT) : 0;
+  __device__ __forceinline__ bool staged_ok(int bp) const {
+    return vec && ((uintptr_t)y % 16 == 0) && ((sj * (int64_t)sizeof(OutT)) % 16 == 0) &&
+           (bstride == 0 || ohw % bp == 0);
+  }
+  __device__ __forceinline__ char* out_ptr(int i, int j) const { return reinterpret_cast<char*>(y + index(i, j)); }
+  // The four outputs (i0..i0+3, j) as packed bits; positions outside the
+  // matrix give 0 and read nothing.
+  __device__ __forceinline__ uint64_t pack4(int i0, int j, f32x4 acc) const {
+    uint64_t bits = 0;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const bool in = j < Q && i0 + r < P;
+      const OutT o = from_f32<OutT>(in ? finish(acc[r], i0 + r, j) : 0.0f);
+      uint64_t b;
+      if constexpr (sizeof(OutT) == 2) b = __builtin_bit_cast(uint16_t, o);
+      else b = __builtin_bit_cast(uint32_t, o);
+      bits |= b << (r * 8 * sizeof(OutT));
+    }
+    return bits;
   }
   __device__ __forceinline__ void store(int i0, int j, f32x4 acc) const {
     if (j >= Q) return;
@@ -129,6 +154,25 @@ struct QuantEpi {
     d = d > (double)hi ? (double)hi : d;
     return (int32_t)d;
   }
+  static constexpr int kStageBytes = 1;
+  __device__ __forceinline__ bool staged_ok(int bp) const {
+    return (out_kind == QOUT_U8 || out_kind == QOUT_I8) && vec && ((uintptr_t)y % 16 == 0) && (sj % 16 == 0) &&
+           (bstride == 0 || ohw % bp == 0);
+  }
+  __device__ __forceinline__ char* out_ptr(int i, int j) const { return reinterpret_cast<char*>(y) + index(i, j); }
+  __device__ __forceinline__ uint64_t pack4(int i0, int j, i32x4 acc) const {
+    uint64_t bits = 0;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      int32_t v = 0;
+      if (j < Q && i0 + r < P) {
+        v = requant(exact(acc[r], i0 + r, j), i0 + r, j);
+        if (table) v = table[v & 0xff];
+      }
+      bits |= (uint64_t)(uint32_t)(v & 0xff) << (r * 8);
+    }
+    return bits;
+  }
   __device__ __forceinline__ void store(int i0, int j, i32x4 acc) const {
     if (j >= Q) return;
     int32_t v[4];
@@ -184,7 +228,10 @@ using T256x128 = Tile<256, 128, 4, 2, 3>;   // 3: 8 waves, 64x64 per wave
 using T128x256 = Tile<128, 256, 2, 4, 3>;   // 4: 8 waves, 64x64 per wave
 using T256w4 = Tile<256, 256, 2, 2, 2>;     // 5: 4 waves, 128x128 per wave
 using T256 = Tile<256, 256, 2, 4, 2>;       // 6: 8 waves, 128x64 per wave
-constexpr int kTileCount = 6;
+using T128s2 = Tile<128, 128, 2, 2, 2>;     // 7: 4 waves, 64x64 per wave, two blocks per CU
+using T128w8 = Tile<128, 128, 2, 4, 2>;     // 8: 8 waves, 64x32 per wave, two blocks per CU
+using T64s4 = Tile<64, 64, 2, 2, 4>;        // 9: 4 waves, 32x32 per wave, four stages
+constexpr int kTileCount = 9;
 
 template <Op O, bool XX, bool XY, class Tl, class LX, class LY, class Epi>
 inline hipError_t launch_tile(const LX& lx, const LY& ly, const Epi& epi, int P, int Q, int kc, hipStream_t st) {
@@ -193,36 +240,67 @@ inline hipError_t launch_tile(const LX& lx, const LY& ly, const Epi& epi, int P,
   if (nb <= 0) return hipSuccess;
   if (nb > 0x7fffffff) return hipErrorInvalidValue;
   hipLaunchKernelGGL((mfma_gemm_kernel<O, Tl, LX, LY, Epi, XX, XY>), dim3((unsigned)nb), dim3(Tl::kThreads),
-                     0, st, lx, ly, epi, nP, nQ, kc);
+                     0, st, lx, ly, epi, nP, nQ, kc, 1);
   return hipGetLastError();
 }
 
-// Automatic choice.  A short K loop (few 128-byte stages) is dominated by the
-// prologue and the epilogue, which many small resident blocks overlap best;
-// otherwise the largest tile that still gives at least one block per CU
-// (256 CUs), else the smaller ones.
+// Split-K launch on the 64x64 four-stage tile: partial sums into the
+// workspace, then the ordered reduction applies the real epilogue.
+template <Op O, bool XX, bool XY, class LX, class LY, class Epi>
+inline hipError_t launch_split(const LX& lx, const LY& ly, const Epi& epi, int P, int Q, int kc, int splits,
+                               void* ws, hipStream_t st) {
+  using Tl = Tile<64, 64, 2, 2, 4>;
+  using T = typename std::conditional<O == Op::I8, int32_t, float>::type;
+  using V = typename OpT<O>::Out4;
+  const int nP = (P + Tl::BP - 1) / Tl::BP, nQ = (Q + Tl::BQ - 1) / Tl::BQ;
+  const int64_t nb = (int64_t)nP * nQ;
+  if (nb <= 0) return hipSuccess;
+  if (nb > 0x7fffffff || splits > 65535 || !ws) return hipErrorInvalidValue;
+  const int Pp = (P + 3) / 4 * 4;
+  PartialEpi<T> pe{reinterpret_cast<T*>(ws), P, Pp, Q};
+  hipLaunchKernelGGL((mfma_gemm_kernel<O, Tl, LX, LY, PartialEpi<T>, XX, XY>), dim3((unsigned)nb, (unsigned)splits),
+                     dim3(Tl::kThreads), 0, st, lx, ly, pe, nP, nQ, kc, splits);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  const int64_t groups = (int64_t)(Pp / 4) * Q;
+  const unsigned grid = (unsigned)std::min<int64_t>((groups + 255) / 256, 65535 * 4);
+  hipLaunchKernelGGL((split_reduce_kernel<T, V, Epi>), dim3(grid), dim3(256), 0, st, reinterpret_cast<const T*>(ws),
+                     splits, P, Pp, Q, epi);
+  return hipGetLastError();
+}
+
+// Automatic choice (split-K is decided beforehand, plan_splits).  The
+// largest tile that still gives at least one block per CU (256 CUs); among
+// the smaller tiles, the two-stage 128x128 tile keeps two blocks resident
+// per CU and the four-stage 64x64 tile hides the load latency of the
+// narrowest problems.  A short K loop (few 128-byte stages) is dominated by
+// the prologue and the epilogue, which the resident 128x128 blocks overlap.
 inline int pick_tile(int P, int Q, int kc, int forced) {
   if (forced >= 1 && forced <= kTileCount) return forced;
   auto blocks = [&](int bp, int bq) { return (int64_t)((P + bp - 1) / bp) * ((Q + bq - 1) / bq); };
   const int nk = (kc + 7) / 8;
-  if (nk <= 16) return 1;
+  if (nk <= 16) return blocks(128, 128) >= 256 ? 8 : 9;
   if (blocks(256, 256) >= 256) return 6;
   if (blocks(256, 128) >= 256) return P >= Q ? 3 : 4;
-  if (blocks(128, 128) >= 128) return 2;
-  return 1;
+  if (blocks(128, 128) >= 128) return 8;
+  return 9;
 }
 
 // XX / XY: the X / Y operand holds u8 activations that the MFMA reads as
 // int8 after XOR 0x80.
 template <Op O, bool XX, bool XY, class LX, class LY, class Epi>
 inline hipError_t launch_any(const LX& lx, const LY& ly, const Epi& epi, int P, int Q, int kc, int tile,
-                             hipStream_t st) {
+                             int splits, void* split_ws, hipStream_t st) {
+  if (splits > 1) return launch_split<O, XX, XY>(lx, ly, epi, P, Q, kc, splits, split_ws, st);
   switch (pick_tile(P, Q, kc, tile)) {
     case 2: return launch_tile<O, XX, XY, T128>(lx, ly, epi, P, Q, kc, st);
     case 3: return launch_tile<O, XX, XY, T256x128>(lx, ly, epi, P, Q, kc, st);
     case 4: return launch_tile<O, XX, XY, T128x256>(lx, ly, epi, P, Q, kc, st);
     case 5: return launch_tile<O, XX, XY, T256w4>(lx, ly, epi, P, Q, kc, st);
     case 6: return launch_tile<O, XX, XY, T256>(lx, ly, epi, P, Q, kc, st);
+    case 7: return launch_tile<O, XX, XY, T128s2>(lx, ly, epi, P, Q, kc, st);
+    case 8: return launch_tile<O, XX, XY, T128w8>(lx, ly, epi, P, Q, kc, st);
+    case 9: return launch_tile<O, XX, XY, T64s4>(lx, ly, epi, P, Q, kc, st);
     default: return launch_tile<O, XX, XY, T64>(lx, ly, epi, P, Q, kc, st);
   }
 }

@@ -297,7 +297,7 @@ template <bool XOR> __device__ __forceinline__ u32x4 frag(u32x4 v) {
 // so the MFMA pipe is never left waiting on a barrier with no work queued.
 template <Op O, class Tl, class LX, class LY, class Epi, bool XX, bool XY>
 __global__ void __launch_bounds__(Tl::kThreads)
-mfma_gemm_kernel(const LX lx, const LY ly, const Epi epi, int nP, int nQ, int kc) {
+mfma_gemm_kernel(const LX lx, const LY ly, const Epi epi, int nP, int nQ, int kc, int splits) {
   using A = typename OpT<O>::Acc;
   using O4 = typename OpT<O>::Out4;
   __shared__ u32x4 smem[Tl::STAGES * Tl::kStage];
@@ -322,7 +322,11 @@ mfma_gemm_kernel(const LX lx, const LY ly, const Epi epi, int nP, int nQ, int kc
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[a][b][e] = 0;
 
-  const int nk = (kc + 7) >> 3;
+  // K stages of this block: all of them, or slice blockIdx.y of `splits`
+  const int nk_all = (kc + 7) >> 3;
+  const int per = (nk_all + splits - 1) / splits;
+  const int kbeg = (int)blockIdx.y * per;
+  const int kend = min(kbeg + per, nk_all);
   constexpr int NL = Tl::NX + Tl::NY;     // DMA loads per thread per stage
   // Every stage issues all its loads (past the last stage they read zero or
   // the pad source), so the waits below are fixed counts of outstanding loads.
@@ -344,17 +348,20 @@ mfma_gemm_kernel(const LX lx, const LY ly, const Epi epi, int nP, int nQ, int kc
   }
 
 #pragma unroll
-  for (int s = 0; s < Tl::STAGES - 1; ++s) issue(s);
+  for (int s = 0; s < Tl::STAGES - 1; ++s) issue(kbeg + s);
   wait_vmcnt<(Tl::STAGES - 2) * NL>();
   barrier_only();
 
   u32x4 fx[2][Tl::TP], fy[2][Tl::TQ];
+  {
+    const u32x4* s0 = smem + (kbeg % Tl::STAGES) * Tl::kStage;
 #pragma unroll
-  for (int a = 0; a < Tl::TP; ++a) fx[0][a] = smem[xslot[0] + a * 32 * Tl::kRowStride];
+    for (int a = 0; a < Tl::TP; ++a) fx[0][a] = s0[xslot[0] + a * 32 * Tl::kRowStride];
 #pragma unroll
-  for (int b = 0; b < Tl::TQ; ++b) fy[0][b] = smem[yslot[0] + b * 32 * Tl::kRowStride];
+    for (int b = 0; b < Tl::TQ; ++b) fy[0][b] = s0[yslot[0] + b * 32 * Tl::kRowStride];
+  }
 
-  for (int kt = 0; kt < nk; ++kt) {
+  for (int kt = kbeg; kt < kend; ++kt) {
     const u32x4* s = smem + (kt % Tl::STAGES) * Tl::kStage;
     const u32x4* sn = smem + ((kt + 1) % Tl::STAGES) * Tl::kStage;
 #pragma unroll
@@ -391,6 +398,56 @@ mfma_gemm_kernel(const LX lx, const LY ly, const Epi epi, int nP, int nQ, int kc
 
   const int ibase = p0 + wp * Tl::TP * 32 + (lane >> 5) * 4;
   const int jbase = q0 + wq * Tl::TQ * 32 + (lane & 31);
+
+  // Staged epilogue: the block's outputs go through LDS (the stage buffers
+  // are free once the last loads have landed) and leave as whole 16-byte
+  // chunks of output rows, instead of 4-element pieces of 32 rows per store.
+  // Staged row `lj` holds outputs (p0.., q0 + lj); its 16-byte chunk c sits
+  // at slot c ^ (lj % CPR) so the fragment writes spread over the banks.
+  if constexpr (Epi::kStageBytes > 0) {
+    constexpr int EB = Epi::kStageBytes;
+    constexpr int CPR = Tl::BP * EB / 16;   // 16-byte chunks per staged row
+    constexpr int EPC = 16 / EB;            // outputs per chunk
+    static_assert(Tl::BQ * Tl::BP * EB <= Tl::STAGES * Tl::kStage * 16, "staging must fit the stage buffers");
+    if (epi.staged_ok(Tl::BP)) {
+      wait_vmcnt<0>();
+      wait_lgkm0();
+      barrier_only();
+      char* stg = reinterpret_cast<char*>(smem);
+      auto put = [&](int abg) {
+        const int g = abg & 3, ab = abg >> 2;
+        const int a = ab / Tl::TQ, b = ab % Tl::TQ;
+        const int i0 = ibase + a * 32 + 8 * g, j = jbase + b * 32;
+        O4 v;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = acc[a][b][4 * g + e];
+        const uint64_t bits = epi.pack4(i0, j, v);
+        const int li = i0 - p0, lj = j - q0;
+        const int byte = li * EB;
+        char* dst = stg + lj * (Tl::BP * EB) + (((byte >> 4) ^ (lj & (CPR - 1))) << 4) + (byte & 15);
+        if constexpr (EB == 2) *reinterpret_cast<uint64_t*>(dst) = bits;
+        else *reinterpret_cast<uint32_t*>(dst) = (uint32_t)bits;
+      };
+      Unroll<0, Tl::TP * Tl::TQ * 4>::run(put);
+      wait_lgkm0();
+      barrier_only();
+      for (int c = t; c < Tl::BQ * CPR; c += Tl::kThreads) {
+        const int row = c / CPR, cc = c - row * CPR;
+        const int j = q0 + row, i = p0 + cc * EPC;
+        if (j >= epi.Q || i >= epi.P) continue;
+        const u32x4 v = *reinterpret_cast<const u32x4*>(stg + row * (Tl::BP * EB) + ((cc ^ (row & (CPR - 1))) << 4));
+        if (i + EPC <= epi.P) {
+          *reinterpret_cast<u32x4*>(epi.out_ptr(i, j)) = v;
+        } else {
+          const uint8_t* bytes = reinterpret_cast<const uint8_t*>(&v);
+          for (int e = 0; e < EPC && i + e < epi.P; ++e)
+            for (int k = 0; k < EB; ++k) epi.out_ptr(i + e, j)[k] = (char)bytes[e * EB + k];
+        }
+      }
+      return;
+    }
+  }
+
   auto out = [&](int abg) {
     const int g = abg & 3, ab = abg >> 2;
     const int a = ab / Tl::TQ, b = ab % Tl::TQ;
@@ -400,6 +457,33 @@ mfma_gemm_kernel(const LX lx, const LY ly, const Epi epi, int nP, int nQ, int kc
     epi.store(ibase + a * 32 + 8 * g, jbase + b * 32, v);
   };
   Unroll<0, Tl::TP * Tl::TQ * 4>::run(out);
+}
+
+// Split-K: slice s of the K loop stores its raw accumulators (f32, or i32
+// modulo 2^32) at ws[(s * Q + j) * Pp + i]; the reduction adds the slices in
+// slice order and hands each run of four sums to the real epilogue.
+template <class T> struct PartialEpi {
+  T* ws;
+  int P, Pp, Q;
+  static constexpr int kStageBytes = 0;
+  template <class V> __device__ __forceinline__ void store(int i0, int j, V v) const {
+    if (j >= Q || i0 >= P) return;
+    T* dst = ws + ((int64_t)blockIdx.y * Q + j) * Pp + i0;
+    *reinterpret_cast<V*>(dst) = v;
+  }
+};
+
+template <class T, class V, class Epi>
+__global__ void __launch_bounds__(256) split_reduce_kernel(const T* __restrict__ ws, int splits, int P, int Pp, int Q,
+                                                           const Epi epi) {
+  const int groups = Pp / 4;
+  const int64_t n = (int64_t)groups * Q;
+  for (int64_t g = (int64_t)blockIdx.x * 256 + threadIdx.x; g < n; g += (int64_t)gridDim.x * 256) {
+    const int j = (int)(g / groups), i0 = (int)(g - (int64_t)j * groups) * 4;
+    V acc = *reinterpret_cast<const V*>(ws + (int64_t)j * Pp + i0);
+    for (int s = 1; s < splits; ++s) acc += *reinterpret_cast<const V*>(ws + ((int64_t)s * Q + j) * Pp + i0);
+    epi.store(i0, j, acc);
+  }
 }
 
 }  // namespace ohip

@@ -107,6 +107,7 @@ struct ohip_ctx {
   std::mutex pool_mu;
   DevPool pool;
   std::map<std::string, uint8_t*> tables;  // device copies of 256-byte output tables, by content
+  std::map<std::string, void*> consts;     // device copies of small initializer operands
 };
 
 // A device buffer shared by a tensor and its aliases (Reshape and friends);
@@ -233,6 +234,7 @@ extern "C" void ohip_ctx_destroy(ohip_ctx* ctx) {
   if (ctx->scratch) (void)hipFree(ctx->scratch);
   if (ctx->padtab) (void)hipFree(ctx->padtab);
   for (auto& kv : ctx->tables) (void)hipFree(kv.second);
+  for (auto& kv : ctx->consts) (void)hipFree(kv.second);
   for (auto& kv : ctx->pool.free_blocks) (void)hipFree(kv.second);
   for (auto& kv : ctx->pool.live) (void)hipFree(kv.first);
   if (ctx->own) (void)hipStreamDestroy(ctx->own);
@@ -255,7 +257,7 @@ extern "C" int ohip_sync(ohip_ctx* ctx) {
 
 extern "C" int ohip_set_tile_override(ohip_ctx* ctx, int tile_id) {
   if (!ctx) return fail(OHIP_E_INVALID, "null context");
-  if (tile_id < 0 || tile_id > 6) return fail(OHIP_E_INVALID, "tile id must be 0..6");
+  if (tile_id < 0 || tile_id > 10) return fail(OHIP_E_INVALID, "tile id must be 0..10");
   ctx->tile_override = tile_id;
   return OHIP_OK;
 }
@@ -873,6 +875,8 @@ extern "C" int ohip_gemm(ohip_ctx* ctx, const ohip_gemm_desc* d, const void* a, 
 
   ScratchPlan plan;
   size_t ia = direct ? SIZE_MAX : plan.add((size_t)(M * kp) * eb);
+  const int splits = gemv ? 1 : plan_splits((int)N, (int)M, b->kc, ctx->tile_override);
+  size_t iw = splits > 1 ? plan.add(split_ws_bytes((int)N, (int)M, splits)) : SIZE_MAX;
   rc = scratch_reserve(ctx, plan.total());
   if (rc) return rc;
 
@@ -908,6 +912,8 @@ extern "C" int ohip_gemm(ohip_ctx* ctx, const ohip_gemm_desc* d, const void* a, 
     DenseOperand yv{av.p, av.ld_bytes, (int)M, av.kc, 0, 0u, pad16(ctx, 0)};
     DENSE_FITS_OR_DECLINE(x, "ohip_gemm");
     DENSE_FITS_OR_DECLINE(yv, "ohip_gemm");
+    o.splits = splits;
+    o.split_ws = splits > 1 ? scratch_at(ctx, plan, iw) : nullptr;
     e = run_dense_float(d->dtype, x, yv, o, ctx->tile_override, ctx->stream);
   }
   if (e != hipSuccess) return hip_fail(e, "ohip_gemm launch");
@@ -953,6 +959,10 @@ extern "C" int ohip_conv2d(ohip_ctx* ctx, const ohip_conv_desc* d, const void* x
   ScratchPlan plan;
   const bool stage = d->in_layout == OHIP_NCHW;
   size_t ix = stage ? plan.add((size_t)(d->n * d->h * d->w * cp) * eb) : SIZE_MAX;
+  const bool nchw_out = d->out_layout == OHIP_NCHW;
+  const int sP = nchw_out ? (int)rows : (int)d->cout, sQ = nchw_out ? (int)d->cout : (int)rows;
+  const int splits = plan_splits(sP, sQ, (int)(d->kh * d->kw * (cp / ce)), ctx->tile_override);
+  size_t iw = splits > 1 ? plan.add(split_ws_bytes(sP, sQ, splits)) : SIZE_MAX;
   rc = scratch_reserve(ctx, plan.total());
   if (rc) return rc;
   const void* xin = x;
@@ -996,6 +1006,8 @@ extern "C" int ohip_conv2d(ohip_ctx* ctx, const ohip_conv_desc* d, const void* x
     o.bias_mode = BIAS_I;
   }
   DENSE_FITS_OR_DECLINE(wt, "ohip_conv2d");
+  o.splits = splits;
+  o.split_ws = splits > 1 ? scratch_at(ctx, plan, iw) : nullptr;
   hipError_t e = run_conv_float(d->dtype, col, wt, col_on_x, o, ctx->tile_override, ctx->stream);
   if (e != hipSuccess) return hip_fail(e, "ohip_conv2d launch");
   return OHIP_OK;
@@ -1032,6 +1044,8 @@ extern "C" int ohip_qgemm(ohip_ctx* ctx, const ohip_qgemm_desc* d, const void* a
   ScratchPlan plan;
   size_t ia = direct ? SIZE_MAX : plan.add((size_t)(M * kp));
   size_t ir = d->n_azp > 1 ? plan.add((size_t)M * 4) : SIZE_MAX;
+  const int splits = plan_splits((int)N, (int)M, b->kc, ctx->tile_override);
+  size_t iw = splits > 1 ? plan.add(split_ws_bytes((int)N, (int)M, splits)) : SIZE_MAX;
   rc = scratch_reserve(ctx, plan.total());
   if (rc) return rc;
   const void* pa = a;
@@ -1061,6 +1075,8 @@ extern "C" int ohip_qgemm(ohip_ctx* ctx, const ohip_qgemm_desc* d, const void* a
   DenseOperand yv{pa, lda_b, (int)M, (int)(kp / 16), b->kwrap, u8 ? 0x80808080u : 0u, pad16(ctx, 0)};
   DENSE_FITS_OR_DECLINE(x, "ohip_qgemm");
   DENSE_FITS_OR_DECLINE(yv, "ohip_qgemm");
+  o.splits = splits;
+  o.split_ws = splits > 1 ? scratch_at(ctx, plan, iw) : nullptr;
   hipError_t e = run_dense_quant(x, yv, o, ctx->tile_override, ctx->stream);
   if (e != hipSuccess) return hip_fail(e, "ohip_qgemm launch");
   return OHIP_OK;
@@ -1112,6 +1128,10 @@ extern "C" int ohip_qconv2d(ohip_ctx* ctx, const ohip_qconv_desc* d, const void*
   ScratchPlan plan;
   const bool stage = d->in_layout == OHIP_NCHW;
   size_t ix = stage ? plan.add((size_t)(d->n * d->h * d->w * cp)) : SIZE_MAX;
+  const bool nchw_out = d->out_layout == OHIP_NCHW;
+  const int sP = nchw_out ? (int)rows : (int)d->cout, sQ = nchw_out ? (int)d->cout : (int)rows;
+  const int splits = plan_splits(sP, sQ, w->kc, ctx->tile_override);
+  size_t iw = splits > 1 ? plan.add(split_ws_bytes(sP, sQ, splits)) : SIZE_MAX;
   rc = scratch_reserve(ctx, plan.total());
   if (rc) return rc;
   const void* xin = x;
@@ -1162,6 +1182,8 @@ extern "C" int ohip_qconv2d(ohip_ctx* ctx, const ohip_qconv_desc* d, const void*
     o.w_on_i = 1;
   }
   DENSE_FITS_OR_DECLINE(wt, "ohip_qconv2d");
+  o.splits = splits;
+  o.split_ws = splits > 1 ? scratch_at(ctx, plan, iw) : nullptr;
   hipError_t e = run_conv_quant(col, wt, col_on_x, o, ctx->tile_override, ctx->stream);
   if (e != hipSuccess) return hip_fail(e, "ohip_qconv2d launch");
   return OHIP_OK;
@@ -1214,6 +1236,32 @@ extern "C" int ohip_dtensor_wrap(ohip_ctx* ctx, void* p, int dtype, int rank, co
   t->buf = std::shared_ptr<DevBuf>(new DevBuf{ctx, p});
   for (int i = 0; i < rank; ++i) t->shape[i] = shape[i];
   *out = t;
+  return OHIP_OK;
+}
+
+// Session-lifetime device copy of a small initializer operand (a bias, a Gemm
+// C, a normalisation scale, a broadcast constant), in the form the caller
+// converted it to: initializers are invariant for the context's life, as
+// for the weight cache (oxionnx-cuda/src/lib.rs:519-541), so each is
+// uploaded once instead of on every dispatch.
+int ohip_const_operand_internal(ohip_ctx* ctx, const char* name, const char* label, int dtype, const void* host,
+                                size_t bytes, const void** dev) {
+  if (!ctx || !name || !*name || !host || !dev) return fail(OHIP_E_INVALID, "const operand: bad argument");
+  std::string k(name);
+  k += '\x1f';
+  k += label ? label : "";
+  k += '\x1f' + std::to_string(dtype) + '\x1f' + std::to_string(bytes);
+  std::lock_guard<std::mutex> lock(ctx->mu);
+  auto it = ctx->consts.find(k);
+  if (it != ctx->consts.end()) { *dev = it->second; return OHIP_OK; }
+  void* d = nullptr;
+  hipError_t e = hipMalloc(&d, bytes ? bytes : 16);
+  if (e != hipSuccess) return fail(OHIP_E_NOMEM, "const operand hipMalloc");
+  HIP_TRY(hipMemcpyAsync(d, host, bytes, hipMemcpyHostToDevice, ctx->stream), "const operand upload");
+  HIP_TRY(hipStreamSynchronize(ctx->stream), "const operand upload sync");
+  ctx->counters.h2d_bytes += bytes;
+  ctx->consts.emplace(k, d);
+  *dev = d;
   return OHIP_OK;
 }
 

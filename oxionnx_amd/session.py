@@ -133,19 +133,24 @@ class Session:
                     self.last_use[t] = i
         for o in outs:
             self.last_use[o] = len(self.graph.nodes)
+        self.prepared = [ep.PreparedNode(n, self.graph.initializers) for n in self.graph.nodes]
+        # per node: the activations whose last consumer it is
+        self.release = [[t for t in dict.fromkeys(n.inputs) if t and self.last_use.get(t) == i]
+                        for i, n in enumerate(self.graph.nodes)]
 
     def run(self, feeds: Dict[str, np.ndarray], keep_device: bool = False):
         acts = {}
         try:
             for name in self.graph.inputs:
                 acts[name] = ep.DeviceTensor.from_host(self.ctx, np.ascontiguousarray(feeds[name]))
-            for i, n in enumerate(self.graph.nodes):
-                res = ep.try_hip_dispatch_resident(n, self.graph.initializers, acts, self.ctx)
+            for i, pn in enumerate(self.prepared):
+                res = pn.dispatch_resident(acts, self.ctx)
                 if res is None:
+                    n = pn.node
                     raise NodeDeclined(f"{n.op} node '{n.name}': {self.ctx.last_decline()}")
-                acts[n.outputs[0]] = res[0]
-                for t in n.inputs:
-                    if t and self.last_use.get(t) == i and t in acts:
+                acts[pn.node.outputs[0]] = res
+                for t in self.release[i]:
+                    if t in acts:
                         acts.pop(t).free()
             if keep_device:
                 out = {o: acts.pop(o) for o in self.graph.outputs}

@@ -28,8 +28,21 @@ def ctx():
     c.close()
 
 
+_SERIAL = [0]
+
+
+def unique_graph(nodes, inits, inputs, outputs):
+    """Initializer names made unique per test case: the provider keeps
+    session-lifetime device copies of initializers keyed by name (they are
+    invariant for a context's life, as in the reference's weight cache)."""
+    _SERIAL[0] += 1
+    ren = {k: f"{k}#{_SERIAL[0]}" for k in inits}
+    nodes = [ep.Node(n.op, [ren.get(t, t) for t in n.inputs], list(n.outputs), n.attrs, n.name) for n in nodes]
+    return Graph(nodes, {ren[k]: v for k, v in inits.items()}, inputs, outputs)
+
+
 def run_one(ctx, node, inits, feeds, optimize=False):
-    g = Graph([node], inits, list(feeds), node.outputs)
+    g = unique_graph([node], inits, list(feeds), node.outputs)
     out = Session(g, ctx, optimize=optimize).run(feeds)
     ref = G.run_graph(g, feeds, half=any(np.asarray(v).dtype == np.float16 for v in feeds.values()))
     return out, ref
@@ -131,7 +144,7 @@ def test_concat_slice_reshape(ctx):
              ep.Node("Reshape", ["s", "sh"], ["y"])]
     inits = {"st": np.asarray([1, 1], np.float32), "en": np.asarray([4, 5], np.float32),
              "ax": np.asarray([1, 3], np.float32), "sh": np.asarray([1, -1], np.float32)}
-    g = Graph(nodes, inits, ["a", "b"], ["y"])
+    g = unique_graph(nodes, inits, ["a", "b"], ["y"])
     out = Session(g, ctx).run({"a": a, "b": b})
     ref = G.run_graph(g, {"a": a, "b": b})
     np.testing.assert_array_equal(out["y"], ref["y"])
@@ -147,7 +160,7 @@ def test_quantize_dequantize(ctx, zp):
         inits["z"] = np.asarray([zp], np.uint8 if zp > 127 else np.int8)
         ins.append("z")
     nodes = [ep.Node("QuantizeLinear", ins, ["q"]), ep.Node("DequantizeLinear", ["q"] + ins[1:], ["y"])]
-    g = Graph(nodes, inits, ["x"], ["q", "y"])
+    g = unique_graph(nodes, inits, ["x"], ["q", "y"])
     out = Session(g, ctx).run({"x": x})
     ref = G.run_graph(g, {"x": x})
     np.testing.assert_array_equal(out["q"].astype(np.float32), ref["q"])
@@ -177,7 +190,7 @@ def _qconv_chain(rng, cin=8, cout=16, k=3, x_dtype=np.uint8, x_zp=0, post_zp=-10
 def test_qconv_silu_fused_is_bit_exact(ctx, post_zp, x_dtype, x_zp):
     rng = np.random.default_rng(7)
     nodes, inits = _qconv_chain(rng, x_dtype=x_dtype, x_zp=x_zp, post_zp=post_zp)
-    g = Graph(nodes, inits, ["x"], ["y"])
+    g = unique_graph(nodes, inits, ["x"], ["y"])
     assert len(fuse(g).nodes) == 1
     lo, hi = (0, 256) if x_dtype == np.uint8 else (-128, 128)
     x = rng.integers(lo, hi, (1, 8, 23, 19)).astype(x_dtype)

@@ -50,7 +50,7 @@ GEMM_SHAPES = [(1, 64, 32), (3, 100, 17), (8, 256, 64), (9, 64, 40), (33, 70, 45
 
 
 @pytest.mark.parametrize("mkn", GEMM_SHAPES, ids=str)
-@pytest.mark.parametrize("tile", list(range(7)))
+@pytest.mark.parametrize("tile", list(range(11)))
 def test_gemm_f32_matches_oracle(torch, ctx, mkn, tile):
     from oxionnx_amd import _lib as L
     m, k, n = mkn
