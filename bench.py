@@ -244,13 +244,15 @@ def bench_int8(torch, ctx, L, stream, rng, only):
 
 
 def bench_e2e(torch, ctx, stream, only, no_cpu):
-    """Configs 4 and 5 end to end: ms per forward through the session run loop
-    (graph inputs uploaded, every node dispatched through ohip_try_dispatch,
-    outputs downloaded), median of 10 forwards after 2 warm-up forwards; the
-    device-side time of the same forwards from events on the context's
-    stream; and the CPU graph oracle's time for one forward (the reference's
-    algorithms restated: multi-threaded im2col + sgemm convolution like its
-    rayon path, single-threaded integer convolution like its integer_conv)."""
+    """Configs 4 and 5 end to end, median of 10 forwards each:
+    * the session run loop (graph inputs uploaded, every node dispatched
+      through ohip_try_dispatch, outputs downloaded);
+    * the same forward captured once into a HIP graph and replayed (inputs
+      uploaded, graph launched, outputs downloaded) -- ms_per_forward;
+    * events on the context's stream around both;
+    * the CPU graph oracle's time for one forward (the reference's algorithms
+      restated: multi-threaded im2col + sgemm convolution like its rayon
+      path, single-threaded integer convolution like its integer_conv)."""
     from oxionnx_amd import workloads
     from oxionnx_amd.session import Session
     names = {"e2e_face_swap_f32": lambda: workloads.face_swap_generator(dtype="f32"),
@@ -276,11 +278,28 @@ def bench_e2e(torch, ctx, stream, only, no_cpu):
             walls.append((time.perf_counter() - t0) * 1e3)
             torch.cuda.synchronize()
             gpus.append(e0.elapsed_time(e1))
-        rec = {"ms_per_forward": round(float(np.median(walls)), 3),
-               "stream_ms": round(float(np.median(gpus)), 3),
+        cap = sess.capture(feeds)
+        gwalls, ggpus = [], []
+        for _ in range(10):
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            t0 = time.perf_counter()
+            e0.record(stream)
+            cap.replay(feeds)
+            e1.record(stream)
+            gwalls.append((time.perf_counter() - t0) * 1e3)
+            torch.cuda.synchronize()
+            ggpus.append(e0.elapsed_time(e1))
+        cap.close()
+        rec = {"ms_per_forward": round(float(np.median(gwalls)), 3),
+               "ms_per_forward_run_loop": round(float(np.median(walls)), 3),
+               "stream_ms_graph": round(float(np.median(ggpus)), 3),
+               "stream_ms_run_loop": round(float(np.median(gpus)), 3),
                "nodes": len(g.nodes), "nodes_after_fusion": len(sess.graph.nodes),
                "conv_gmac": round(g.notes["conv_gmac"], 3),
-               "note": "wall clock per forward incl. input upload, Python run loop and output download"}
+               "note": "ms_per_forward: wall clock of one forward replayed from its captured HIP graph, incl. "
+                       "input upload and output download; ms_per_forward_run_loop: the same forward "
+                       "dispatched node by node through the Python run loop"}
         if not no_cpu and not only:
             from oracle import graph_ref
             t0 = time.perf_counter()
@@ -290,6 +309,7 @@ def bench_e2e(torch, ctx, stream, only, no_cpu):
                                    "cores": 1 if "int8" in key else threads,
                                    "sample": "one full forward of the same graph and inputs"}
             rec["speedup_vs_cpu"] = round(cpu / rec["ms_per_forward"], 1)
+            rec["speedup_vs_cpu_run_loop"] = round(cpu / rec["ms_per_forward_run_loop"], 1)
         out[key] = rec
     return out
 

@@ -71,6 +71,25 @@ void ohip_ctx_destroy(ohip_ctx* ctx);
 int ohip_ctx_set_stream(ohip_ctx* ctx, void* hip_stream);
 void* ohip_ctx_stream(ohip_ctx* ctx);
 int ohip_sync(ohip_ctx* ctx);
+
+/* ------------------------------------------------------------------ graphs
+ * Capture of a whole forward into one HIP graph (the reference's CUDA-graph
+ * cache, oxionnx-cuda/src/graph_cache.rs): ohip_graph_begin opens a capture
+ * on the context's stream; every dispatch until ohip_graph_end is recorded,
+ * not run.  Dispatches must already be warm (weights, constants and output
+ * tables cached), because uploads and synchronisations cannot be captured.
+ * While a capture is open, freed device buffers are parked for the graph,
+ * which keeps them until ohip_graph_destroy; a replay writes the same
+ * buffers, so the caller keeps the captured inputs and outputs alive and
+ * refills / reads them around ohip_graph_launch.  ohip_pool_parking(ctx, 1)
+ * parks buffers without a capture (a dry run that leaves every buffer the
+ * forward needs in the pool); ohip_pool_parking(ctx, 0) releases them. */
+typedef struct ohip_graph ohip_graph;
+int ohip_pool_parking(ohip_ctx* ctx, int on);
+int ohip_graph_begin(ohip_ctx* ctx);
+int ohip_graph_end(ohip_ctx* ctx, ohip_graph** out);
+int ohip_graph_launch(ohip_graph* g);
+void ohip_graph_destroy(ohip_graph* g);
 int ohip_device_count(int* count);
 const char* ohip_last_error(void);
 const char* ohip_version(void);

@@ -116,6 +116,11 @@ SIGNATURES = {
     "ohip_ctx_set_stream": (ctypes.c_int, [VP, VP]),
     "ohip_ctx_stream": (VP, [VP]),
     "ohip_sync": (ctypes.c_int, [VP]),
+    "ohip_pool_parking": (ctypes.c_int, [VP, ctypes.c_int]),
+    "ohip_graph_begin": (ctypes.c_int, [VP]),
+    "ohip_graph_end": (ctypes.c_int, [VP, ctypes.POINTER(VP)]),
+    "ohip_graph_launch": (ctypes.c_int, [VP]),
+    "ohip_graph_destroy": (None, [VP]),
     "ohip_device_count": (ctypes.c_int, [ctypes.POINTER(ctypes.c_int)]),
     "ohip_last_error": (ctypes.c_char_p, []),
     "ohip_version": (ctypes.c_char_p, []),

@@ -20,6 +20,7 @@
 int ohip_dtensor_alias_internal(const ohip_dtensor* src, int rank, const int64_t* shape, ohip_dtensor** out);
 int ohip_const_operand_internal(ohip_ctx* ctx, const char* name, const char* label, int dtype, const void* host,
                                 size_t bytes, const void** dev);
+int ohip_hip_error_internal(hipError_t e, const char* what);
 
 namespace {
 
@@ -760,7 +761,7 @@ int do_unary(ohip_ctx* ctx, const ohip_node* nd, int op, int placement, ohip_out
   void* yd = st.alloc(bytes);
   if (!xd || !yd) return OHIP_E_NOMEM;
   hipError_t e = ohip::run_unary(dt, xd, yd, n, op, alpha, (hipStream_t)ohip_ctx_stream(ctx));
-  if (e != hipSuccess) return OHIP_E_HIP;
+  if (e != hipSuccess) return ohip_hip_error_internal(e, "node kernel launch");
   return output_device(ctx, st, placement, out, dt, shape_of(x), yd, bytes);
 }
 
@@ -798,7 +799,7 @@ int do_binary(ohip_ctx* ctx, const ohip_node* nd, int op, int placement, ohip_ou
   void* yd = st.alloc(bytes);
   if (!ad || !bd || !yd) return ad && bd ? OHIP_E_NOMEM : decline("binary: resident operand dtype");
   hipError_t e = ohip::run_binary(dt, ad, bd, yd, n, p, same, op, (hipStream_t)ohip_ctx_stream(ctx));
-  if (e != hipSuccess) return OHIP_E_HIP;
+  if (e != hipSuccess) return ohip_hip_error_internal(e, "node kernel launch");
   return output_device(ctx, st, placement, out, dt, oshape, yd, bytes);
 }
 
@@ -832,7 +833,7 @@ int do_instnorm(ohip_ctx* ctx, const ohip_node* nd, bool affine, int placement, 
   void* yd = st.alloc(bytes);
   if (!xd || !yd) return OHIP_E_NOMEM;
   hipError_t e = ohip::run_instnorm(dt, xd, yd, N * C, spatial, (int)C, eps, aff, (hipStream_t)ohip_ctx_stream(ctx));
-  if (e != hipSuccess) return OHIP_E_HIP;
+  if (e != hipSuccess) return ohip_hip_error_internal(e, "node kernel launch");
   return output_device(ctx, st, placement, out, dt, shape_of(x), yd, bytes);
 }
 
@@ -878,7 +879,7 @@ int do_resize(ohip_ctx* ctx, const ohip_node* nd, int placement, ohip_output* ou
   void* yd = st.alloc(bytes);
   if (!xd || !yd) return OHIP_E_NOMEM;
   hipError_t e = ohip::run_resize_nearest(eb, xd, yd, planes, p, (hipStream_t)ohip_ctx_stream(ctx));
-  if (e != hipSuccess) return OHIP_E_HIP;
+  if (e != hipSuccess) return ohip_hip_error_internal(e, "node kernel launch");
   return output_device(ctx, st, placement, out, dt, {x->shape[0], x->shape[1], p.oh, p.ow}, yd, bytes);
 }
 
@@ -938,7 +939,7 @@ int do_pad(ohip_ctx* ctx, const ohip_node* nd, int placement, ohip_output* out) 
   void* yd = st.alloc(bytes);
   if (!xd || !yd) return OHIP_E_NOMEM;
   hipError_t e = ohip::run_pad(eb, xd, yd, n, p, (hipStream_t)ohip_ctx_stream(ctx));
-  if (e != hipSuccess) return OHIP_E_HIP;
+  if (e != hipSuccess) return ohip_hip_error_internal(e, "node kernel launch");
   return output_device(ctx, st, placement, out, dt, oshape, yd, bytes);
 }
 
@@ -997,11 +998,11 @@ int do_maxpool(ohip_ctx* ctx, const ohip_node* nd, int placement, ohip_output* o
   void* yd = st.alloc(bytes);
   if (!xd || !yd) return OHIP_E_NOMEM;
   hipError_t e = ohip::run_maxpool(dt, xd, yd, planes, p, (hipStream_t)ohip_ctx_stream(ctx));
-  if (e != hipSuccess) return e == hipErrorInvalidValue ? decline("MaxPool: dtype") : OHIP_E_HIP;
+  if (e != hipSuccess) return e == hipErrorInvalidValue ? decline("MaxPool: dtype") : ohip_hip_error_internal(e, "MaxPool launch");
   return output_device(ctx, st, placement, out, dt, {x->shape[0], x->shape[1], oh, ow}, yd, bytes);
 }
 
-// ---------------------------------------------------------------- Concat (device copies)
+// ---------------------------------------------------------------- Concat (device copy kernels)
 int do_concat(ohip_ctx* ctx, const ohip_node* nd, int placement, ohip_output* out) {
   if (nd->n_inputs < 1) return decline("Concat: no inputs");
   const ohip_tensor* t0 = input(nd, 0);
@@ -1044,9 +1045,9 @@ int do_concat(ohip_ctx* ctx, const ohip_node* nd, int placement, ohip_output* ou
     if (!td) return OHIP_E_NOMEM;
     const size_t w = (size_t)(t->shape[axis] * inner * eb);
     if (w && outer)
-      if (hipMemcpy2DAsync(static_cast<char*>(yd) + off, row, td, w, w, (size_t)outer, hipMemcpyDeviceToDevice, s) !=
+      if (ohip::run_copy2d(td, (int64_t)w, static_cast<char*>(yd) + off, (int64_t)row, (int64_t)w, outer, s) !=
           hipSuccess)
-        return OHIP_E_HIP;
+        return ohip_hip_error_internal(hipGetLastError(), "Concat copy");
     off += w;
   }
   return output_device(ctx, st, placement, out, dt, oshape, yd, bytes);
@@ -1106,7 +1107,7 @@ int do_slice(ohip_ctx* ctx, const ohip_node* nd, int placement, ohip_output* out
   void* yd = st.alloc(bytes);
   if (!xd || !yd) return OHIP_E_NOMEM;
   hipError_t e = ohip::run_slice(eb, xd, yd, n, p, (hipStream_t)ohip_ctx_stream(ctx));
-  if (e != hipSuccess) return OHIP_E_HIP;
+  if (e != hipSuccess) return ohip_hip_error_internal(e, "node kernel launch");
   return output_device(ctx, st, placement, out, dt, oshape, yd, bytes);
 }
 
@@ -1207,7 +1208,7 @@ int do_quantize(ohip_ctx* ctx, const ohip_node* nd, int placement, ohip_output* 
   if (!xd || !yd) return OHIP_E_NOMEM;
   hipError_t e = ohip::run_quantize(static_cast<const float*>(xd), static_cast<uint8_t*>(yd), n, scale, zp, lo, hi,
                                     (hipStream_t)ohip_ctx_stream(ctx));
-  if (e != hipSuccess) return OHIP_E_HIP;
+  if (e != hipSuccess) return ohip_hip_error_internal(e, "node kernel launch");
   return output_device(ctx, st, placement, out, u8 ? OHIP_U8 : OHIP_I8, shape_of(x), yd, (size_t)n);
 }
 
@@ -1234,7 +1235,7 @@ int do_dequantize(ohip_ctx* ctx, const ohip_node* nd, int placement, ohip_output
   if (!xd || !yd) return OHIP_E_NOMEM;
   hipError_t e = ohip::run_dequantize(static_cast<const uint8_t*>(xd), xdt == OHIP_I8, static_cast<float*>(yd), n,
                                       scale, zp, (hipStream_t)ohip_ctx_stream(ctx));
-  if (e != hipSuccess) return OHIP_E_HIP;
+  if (e != hipSuccess) return ohip_hip_error_internal(e, "node kernel launch");
   return output_device(ctx, st, placement, out, OHIP_F32, shape_of(x), yd, (size_t)n * 4);
 }
 

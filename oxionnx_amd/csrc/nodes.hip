@@ -275,6 +275,17 @@ __global__ void __launch_bounds__(kThreads) dequantize_kernel(const uint8_t* __r
   }
 }
 
+// ---------------------------------------------------------------- 2-D copy (Concat)
+template <class T>
+__global__ void __launch_bounds__(kThreads) copy2d_kernel(const T* __restrict__ src, int64_t sp, T* __restrict__ dst,
+                                                          int64_t dp, int64_t width, int64_t rows) {
+  const int64_t n = width * rows;
+  for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n; i += (int64_t)gridDim.x * kThreads) {
+    const int64_t r = i / width, c = i - r * width;
+    dst[r * dp + c] = src[r * sp + c];
+  }
+}
+
 struct Table256 { uint8_t v[256]; };
 
 __global__ void __launch_bounds__(kThreads) byte_table_kernel(const uint8_t* __restrict__ x, uint8_t* __restrict__ y,
@@ -397,6 +408,31 @@ hipError_t run_dequantize(const uint8_t* x, bool is_signed, float* y, int64_t n,
     hipLaunchKernelGGL(dequantize_kernel<true>, dim3(grid_for(n)), dim3(kThreads), 0, st, x, y, n, scale, zp);
   else
     hipLaunchKernelGGL(dequantize_kernel<false>, dim3(grid_for(n)), dim3(kThreads), 0, st, x, y, n, scale, zp);
+  return hipGetLastError();
+}
+
+// Copies `rows` rows of `width` bytes (pitches in bytes), in 16-, 4- or
+// 1-byte units as the alignment of every operand allows.
+hipError_t run_copy2d(const void* src, int64_t src_pitch, void* dst, int64_t dst_pitch, int64_t width, int64_t rows,
+                      hipStream_t st) {
+  if (width <= 0 || rows <= 0) return hipSuccess;
+  auto fits = [&](int u) {
+    return (uintptr_t)src % u == 0 && (uintptr_t)dst % u == 0 && src_pitch % u == 0 && dst_pitch % u == 0 &&
+           width % u == 0;
+  };
+  if (fits(16)) {
+    const int64_t w = width / 16, n = w * rows;
+    hipLaunchKernelGGL(copy2d_kernel<uint4>, dim3(grid_for(n)), dim3(kThreads), 0, st, (const uint4*)src,
+                       src_pitch / 16, (uint4*)dst, dst_pitch / 16, w, rows);
+  } else if (fits(4)) {
+    const int64_t w = width / 4, n = w * rows;
+    hipLaunchKernelGGL(copy2d_kernel<uint32_t>, dim3(grid_for(n)), dim3(kThreads), 0, st, (const uint32_t*)src,
+                       src_pitch / 4, (uint32_t*)dst, dst_pitch / 4, w, rows);
+  } else {
+    const int64_t n = width * rows;
+    hipLaunchKernelGGL(copy2d_kernel<uint8_t>, dim3(grid_for(n)), dim3(kThreads), 0, st, (const uint8_t*)src,
+                       src_pitch, (uint8_t*)dst, dst_pitch, width, rows);
+  }
   return hipGetLastError();
 }
 

@@ -39,6 +39,9 @@ static int hip_fail(hipError_t e, const char* what) {
   } while (0)
 
 extern "C" const char* ohip_last_error(void) { return g_last_error.c_str(); }
+
+// Records a HIP failure of the node-level dispatcher as the last error.
+int ohip_hip_error_internal(hipError_t e, const char* what) { return hip_fail(e, what); }
 extern "C" const char* ohip_version(void) { return "oxionnx-hip 0.1.0 (gfx950)"; }
 
 // oxionnx-cuda/src/context.rs:165-193: unset -> false; "", 0, false, no, off
@@ -88,6 +91,8 @@ struct DevPool {
   std::multimap<size_t, void*> free_blocks;  // capacity -> buffer
   std::unordered_map<void*, size_t> live;    // buffer -> capacity
   size_t held = 0;                           // bytes held from HIP
+  bool parking = false;                      // freed buffers are parked, not reused
+  std::vector<std::pair<void*, size_t>> parked;
 };
 
 struct ohip_ctx {
@@ -299,9 +304,97 @@ static int pool_free(ohip_ctx* ctx, void* p) {
   std::lock_guard<std::mutex> lock(ctx->pool_mu);
   auto it = ctx->pool.live.find(p);
   if (it == ctx->pool.live.end()) return fail(OHIP_E_INVALID, "ohip_free: not a buffer of this context");
-  ctx->pool.free_blocks.emplace(it->second, p);
+  if (ctx->pool.parking) ctx->pool.parked.emplace_back(p, it->second);
+  else ctx->pool.free_blocks.emplace(it->second, p);
   ctx->pool.live.erase(it);
   return OHIP_OK;
+}
+
+// ------------------------------------------------------------------ graphs
+// A captured forward.  While a capture (or a parking dry run) is open, freed
+// pool buffers are parked instead of reused, so every buffer the captured
+// kernels touch stays reserved for the graph; the graph returns them to the
+// pool when destroyed.
+struct ohip_graph {
+  ohip_ctx* ctx = nullptr;
+  hipGraph_t graph = nullptr;
+  hipGraphExec_t exec = nullptr;
+  std::vector<std::pair<void*, size_t>> held;
+};
+
+static void unpark_all(ohip_ctx* ctx, std::vector<std::pair<void*, size_t>>& v) {
+  for (auto& pb : v) ctx->pool.free_blocks.emplace(pb.second, pb.first);
+  v.clear();
+}
+
+extern "C" int ohip_pool_parking(ohip_ctx* ctx, int on) {
+  if (!ctx) return fail(OHIP_E_INVALID, "null context");
+  std::lock_guard<std::mutex> lock(ctx->pool_mu);
+  ctx->pool.parking = on != 0;
+  if (!on) unpark_all(ctx, ctx->pool.parked);
+  return OHIP_OK;
+}
+
+extern "C" int ohip_graph_begin(ohip_ctx* ctx) {
+  int rc = activate(ctx);
+  if (rc) return rc;
+  {
+    std::lock_guard<std::mutex> lock(ctx->pool_mu);
+    unpark_all(ctx, ctx->pool.parked);
+    ctx->pool.parking = true;
+  }
+  hipError_t e = hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeRelaxed);
+  if (e != hipSuccess) {
+    std::lock_guard<std::mutex> lock(ctx->pool_mu);
+    ctx->pool.parking = false;
+    return hip_fail(e, "hipStreamBeginCapture");
+  }
+  return OHIP_OK;
+}
+
+extern "C" int ohip_graph_end(ohip_ctx* ctx, ohip_graph** out) {
+  int rc = activate(ctx);
+  if (rc) return rc;
+  if (!out) return fail(OHIP_E_INVALID, "null out");
+  auto* g = new ohip_graph();
+  g->ctx = ctx;
+  hipError_t e = hipStreamEndCapture(ctx->stream, &g->graph);
+  {
+    std::lock_guard<std::mutex> lock(ctx->pool_mu);
+    ctx->pool.parking = false;
+    g->held.swap(ctx->pool.parked);
+  }
+  if (e == hipSuccess) e = hipGraphInstantiate(&g->exec, g->graph, nullptr, nullptr, 0);
+  if (e != hipSuccess) {
+    if (g->graph) (void)hipGraphDestroy(g->graph);
+    std::lock_guard<std::mutex> lock(ctx->pool_mu);
+    unpark_all(ctx, g->held);
+    delete g;
+    return hip_fail(e, "graph capture");
+  }
+  *out = g;
+  return OHIP_OK;
+}
+
+extern "C" int ohip_graph_launch(ohip_graph* g) {
+  if (!g) return fail(OHIP_E_INVALID, "null graph");
+  int rc = activate(g->ctx);
+  if (rc) return rc;
+  HIP_TRY(hipGraphLaunch(g->exec, g->ctx->stream), "hipGraphLaunch");
+  return OHIP_OK;
+}
+
+extern "C" void ohip_graph_destroy(ohip_graph* g) {
+  if (!g) return;
+  (void)hipSetDevice(g->ctx->device);
+  (void)hipStreamSynchronize(g->ctx->stream);
+  if (g->exec) (void)hipGraphExecDestroy(g->exec);
+  if (g->graph) (void)hipGraphDestroy(g->graph);
+  {
+    std::lock_guard<std::mutex> lock(g->ctx->pool_mu);
+    unpark_all(g->ctx, g->held);
+  }
+  delete g;
 }
 
 DevBuf::~DevBuf() {
@@ -713,6 +806,16 @@ static int qpack_upload(ohip_ctx* ctx, ohip_weight* w, const QPacked& q, const f
   return OHIP_OK;
 }
 
+// The weight scales of a cached integer weight are re-read on every dispatch
+// (they are separate initializers); the combined scales are only recomputed
+// when they changed.
+static bool same_scales(const std::vector<float>& have, const float* s, int n) {
+  if ((int)have.size() != n) return false;
+  for (int i = 0; i < n; ++i)
+    if (!(have[(size_t)i] == s[i])) return false;
+  return true;
+}
+
 static int32_t int_at(int dt, const void* p, int64_t i) {
   return dt == OHIP_U8 ? (int32_t) static_cast<const uint8_t*>(p)[i] : (int32_t) static_cast<const int8_t*>(p)[i];
 }
@@ -734,7 +837,8 @@ extern "C" int ohip_weight_qgemm(ohip_ctx* ctx, const ohip_weight_key* key, int 
     for (int i = 0; zp && i < n_zp; ++i) shape.push_back(zp[i]);
     ks = cache_key(key, WK_QGEMM, src_dt, (size_t)(k * n), shape);
     if (ohip_weight* hit = cache_lookup(ctx, key, ks)) {
-      if (scale && n_scale > 0) hit->scale.assign(scale, scale + n_scale), hit->comb_a = NAN;
+      if (scale && n_scale > 0 && !same_scales(hit->scale, scale, n_scale))
+        hit->scale.assign(scale, scale + n_scale), hit->comb_a = NAN;
       *out = hit;
       return OHIP_OK;
     }
@@ -768,7 +872,8 @@ extern "C" int ohip_weight_qconv(ohip_ctx* ctx, const ohip_weight_key* key, int 
     for (int i = 0; zp && i < n_zp; ++i) shape.push_back(zp[i]);
     ks = cache_key(key, WK_QCONV, src_dt, (size_t)(cout * cin * kh * kw), shape);
     if (ohip_weight* hit = cache_lookup(ctx, key, ks)) {
-      if (scale && n_scale > 0) hit->scale.assign(scale, scale + n_scale), hit->comb_a = NAN;
+      if (scale && n_scale > 0 && !same_scales(hit->scale, scale, n_scale))
+        hit->scale.assign(scale, scale + n_scale), hit->comb_a = NAN;
       *out = hit;
       return OHIP_OK;
     }

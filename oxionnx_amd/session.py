@@ -17,11 +17,13 @@ reference's optimizer passes (src/optimizer/fusion/mod.rs):
     consumer of the previous, becomes one QLinearConv whose requantised bytes
     pass through a 256-entry table that reproduces the three nodes exactly.
 """
+import ctypes
 from dataclasses import dataclass, field, replace
 from typing import Dict, List
 
 import numpy as np
 
+from . import _lib as L
 from . import ep
 
 
@@ -138,20 +140,25 @@ class Session:
         self.release = [[t for t in dict.fromkeys(n.inputs) if t and self.last_use.get(t) == i]
                         for i, n in enumerate(self.graph.nodes)]
 
+    def _forward(self, acts, keep):
+        """Dispatches every node; frees each activation after its last
+        consumer unless it is in `keep`."""
+        for i, pn in enumerate(self.prepared):
+            res = pn.dispatch_resident(acts, self.ctx)
+            if res is None:
+                n = pn.node
+                raise NodeDeclined(f"{n.op} node '{n.name}': {self.ctx.last_decline()}")
+            acts[pn.node.outputs[0]] = res
+            for t in self.release[i]:
+                if t in acts and t not in keep:
+                    acts.pop(t).free()
+
     def run(self, feeds: Dict[str, np.ndarray], keep_device: bool = False):
         acts = {}
         try:
             for name in self.graph.inputs:
                 acts[name] = ep.DeviceTensor.from_host(self.ctx, np.ascontiguousarray(feeds[name]))
-            for i, pn in enumerate(self.prepared):
-                res = pn.dispatch_resident(acts, self.ctx)
-                if res is None:
-                    n = pn.node
-                    raise NodeDeclined(f"{n.op} node '{n.name}': {self.ctx.last_decline()}")
-                acts[pn.node.outputs[0]] = res
-                for t in self.release[i]:
-                    if t in acts:
-                        acts.pop(t).free()
+            self._forward(acts, ())
             if keep_device:
                 out = {o: acts.pop(o) for o in self.graph.outputs}
             else:
@@ -160,3 +167,66 @@ class Session:
         finally:
             for t in acts.values():
                 t.free()
+
+    def capture(self, feeds: Dict[str, np.ndarray]) -> "CapturedForward":
+        """Records one forward into a HIP graph (the reference's CUDA-graph
+        cache, oxionnx-cuda/src/graph_cache.rs).  Two eager forwards warm the
+        caches; a dry run with parked buffers leaves every buffer the forward
+        needs in the pool; the captured forward then owns its buffers."""
+        lib = L.lib()
+        self.run(feeds)
+        self.run(feeds)
+        L.check(lib.ohip_pool_parking(self.ctx.h, 1))
+        try:
+            self.run(feeds)
+        finally:
+            L.check(lib.ohip_pool_parking(self.ctx.h, 0))
+        inputs = {n: ep.DeviceTensor.from_host(self.ctx, np.ascontiguousarray(feeds[n])) for n in self.graph.inputs}
+        L.check(lib.ohip_sync(self.ctx.h))
+        acts = dict(inputs)
+        L.check(lib.ohip_graph_begin(self.ctx.h))
+        try:
+            self._forward(acts, set(inputs))
+        except BaseException:
+            g = ctypes.c_void_p()
+            if lib.ohip_graph_end(self.ctx.h, ctypes.byref(g)) == L.OK:
+                lib.ohip_graph_destroy(g)
+            raise
+        g = ctypes.c_void_p()
+        L.check(lib.ohip_graph_end(self.ctx.h, ctypes.byref(g)))
+        outputs = {o: acts.pop(o) for o in self.graph.outputs}
+        for t in acts.values():
+            if t not in inputs.values():
+                t.free()
+        return CapturedForward(self.ctx, g, inputs, outputs)
+
+
+class CapturedForward:
+    """A replayable forward: refill the captured inputs, launch, read the
+    captured outputs."""
+
+    def __init__(self, ctx, graph, inputs, outputs):
+        self.ctx, self.g, self.inputs, self.outputs = ctx, graph, inputs, outputs
+
+    def replay(self, feeds: Dict[str, np.ndarray], download: bool = True):
+        lib = L.lib()
+        for name, t in self.inputs.items():
+            arr = np.ascontiguousarray(feeds[name])
+            L.check(lib.ohip_dtensor_upload(self.ctx.h, t.h, arr.ctypes.data_as(ctypes.c_void_p)))
+        L.check(lib.ohip_graph_launch(self.g))
+        if not download:
+            return None
+        return {o: t.to_host(self.ctx) for o, t in self.outputs.items()}
+
+    def close(self):
+        if self.g:
+            L.lib().ohip_graph_destroy(self.g)
+            self.g = None
+        for t in list(self.inputs.values()) + list(self.outputs.values()):
+            t.free()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

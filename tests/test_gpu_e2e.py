@@ -229,3 +229,27 @@ def test_face_swap_generator_f16_end_to_end(ctx):
     assert out["y"].dtype == np.float16
     close(out["logits"], ref["logits"], 3e-2)
     close(out["y"], ref["y"], 3e-2)
+
+
+@pytest.mark.parametrize("which", ["yolo", "face_f16"])
+def test_captured_forward_replays_match_eager(ctx, which):
+    """A HIP-graph replay of a whole forward, several times, with eager work
+    and new inputs between the replays; every replay equals the eager run."""
+    if which == "yolo":
+        g, feeds = workloads.yolo_backbone_int8(size=320)
+        other = {"x": np.random.default_rng(9).integers(0, 256, feeds["x"].shape).astype(np.uint8)}
+    else:
+        g, feeds = workloads.face_swap_generator(dtype="f16")
+        other = {k: (v.astype(np.float32) * 0.5).astype(np.float16) for k, v in feeds.items()}
+    sess = Session(g, ctx)
+    eager = sess.run(feeds)
+    eager_other = sess.run(other)
+    cap = sess.capture(feeds)
+    try:
+        for feed, ref in ((feeds, eager), (other, eager_other), (feeds, eager)):
+            got = cap.replay(feed)
+            sess.run(other)  # eager work between replays
+            for k in ref:
+                np.testing.assert_array_equal(got[k], ref[k], err_msg=k)
+    finally:
+        cap.close()
