@@ -46,6 +46,7 @@ enum ohip_act { OHIP_ACT_NONE = 0, OHIP_ACT_RELU = 1, OHIP_ACT_CLIP = 2, OHIP_AC
 enum ohip_bias_kind { OHIP_C_NONE = 0, OHIP_C_SCALAR = 1, OHIP_C_ROW = 2, OHIP_C_FULL = 3 };
 
 enum ohip_layout { OHIP_NCHW = 0, OHIP_NHWC = 1 };
+enum ohip_pad_mode { OHIP_PAD_ZEROS = 0, OHIP_PAD_REFLECT = 1, OHIP_PAD_EDGE = 2 };
 
 /* Output kinds of the integer family: requantised u8 / i8 bytes, the raw int32
  * accumulator (MatMulInteger / ConvInteger), or requantised values stored as
@@ -193,6 +194,11 @@ typedef struct {
     int in_layout, out_layout;     /* ohip_layout */
     int act;
     float act_lo, act_hi;
+    /* OHIP_PAD_ZEROS: the pads are ONNX Conv zero padding.  OHIP_PAD_REFLECT /
+     * OHIP_PAD_EDGE: they are a reflect / edge Pad node fused in front of the
+     * convolution (ONNX Pad semantics), applied while the NCHW input is
+     * staged (in_layout must be NCHW). */
+    int pad_mode;
 } ohip_conv_desc;
 int ohip_conv2d(ohip_ctx* ctx, const ohip_conv_desc* d, const void* x, const ohip_weight* w,
                 const void* bias, void* y);

@@ -16,6 +16,7 @@ F32, U8, I8, I32, F16, BF16 = 1, 2, 3, 6, 10, 16
 ACT_NONE, ACT_RELU, ACT_CLIP, ACT_LEAKY_RELU = 0, 1, 2, 3
 C_NONE, C_SCALAR, C_ROW, C_FULL = 0, 1, 2, 3
 NCHW, NHWC = 0, 1
+PAD_ZEROS, PAD_REFLECT, PAD_EDGE = 0, 1, 2
 QOUT_U8, QOUT_I8, QOUT_I32, QOUT_F32 = 0, 1, 2, 3
 CLASS_MI355X, CLASS_PARITY, CLASS_NEVER, CLASS_LEGACY = 0, 1, 2, 3
 
@@ -60,7 +61,8 @@ class ConvDesc(ctypes.Structure):
     _fields_ = [(f, I64) for f in ("n", "c", "h", "w", "cout", "kh", "kw", "group", "stride_h", "stride_w",
                                     "dil_h", "dil_w", "pad_t", "pad_l", "pad_b", "pad_r")] + \
                [("dtype", ctypes.c_int), ("in_layout", ctypes.c_int), ("out_layout", ctypes.c_int),
-                ("act", ctypes.c_int), ("act_lo", ctypes.c_float), ("act_hi", ctypes.c_float)]
+                ("act", ctypes.c_int), ("act_lo", ctypes.c_float), ("act_hi", ctypes.c_float),
+                ("pad_mode", ctypes.c_int)]
 
 
 class QGemmDesc(ctypes.Structure):

@@ -200,6 +200,65 @@ hipError_t run_nchw_to_nhwc(int elem_bytes, const void* src, void* dst, int N, i
   }
 }
 
+// NCHW [C][H][W] -> NHWC [Hp][Wp][cp] with the spatial border filled by
+// reflection (mode 1) or edge replication (mode 2): the Pad node in front of
+// a convolution, fused into its staging transpose.  Padded pixel (y, x)
+// reads source pixel (src_y, src_x) of the ONNX Pad mapping.
+__device__ __forceinline__ int pad_map(int o, int begin, int len, int mode) {
+  int s = o - begin;
+  if (s >= 0 && s < len) return s;
+  if (mode == 2 || len == 1) return s < 0 ? 0 : len - 1;
+  const int period = 2 * (len - 1);
+  s %= period;
+  if (s < 0) s += period;
+  return s < len ? s : period - s;
+}
+
+template <class T>
+__global__ void nchw_to_nhwc_pad_kernel(const T* __restrict__ src, T* __restrict__ dst, int C, int H, int W, int cp,
+                                        int Hp, int Wp, int pt, int pl, int mode) {
+  __shared__ T tile[32][33];
+  const int n = blockIdx.z;
+  const int c0 = blockIdx.y * 32, s0 = blockIdx.x * 32;
+  const int HWp = Hp * Wp;
+  const T* s = src + (int64_t)n * C * H * W;
+  T* d = dst + (int64_t)n * HWp * cp;
+  for (int r = threadIdx.y; r < 32; r += blockDim.y) {
+    const int c = c0 + r, sp = s0 + threadIdx.x;
+    T v = T(0);
+    if (c < C && sp < HWp) {
+      const int y = sp / Wp, x = sp - y * Wp;
+      v = s[(int64_t)c * H * W + pad_map(y, pt, H, mode) * W + pad_map(x, pl, W, mode)];
+    }
+    tile[r][threadIdx.x] = v;
+  }
+  __syncthreads();
+  for (int r = threadIdx.y; r < 32; r += blockDim.y) {
+    const int sp = s0 + r, c = c0 + threadIdx.x;
+    if (sp < HWp && c < cp) d[(int64_t)sp * cp + c] = tile[threadIdx.x][r];
+  }
+}
+
+template <class T>
+static hipError_t nchw_to_nhwc_pad_t(const void* src, void* dst, int N, int C, int H, int W, int cp, int pt, int pl,
+                                     int pb, int pr, int mode, hipStream_t st) {
+  const int Hp = H + pt + pb, Wp = W + pl + pr;
+  dim3 grid((Hp * Wp + 31) / 32, (cp + 31) / 32, N), block(32, 8);
+  hipLaunchKernelGGL(nchw_to_nhwc_pad_kernel<T>, grid, block, 0, st, reinterpret_cast<const T*>(src),
+                     reinterpret_cast<T*>(dst), C, H, W, cp, Hp, Wp, pt, pl, mode);
+  return hipGetLastError();
+}
+
+hipError_t run_nchw_to_nhwc_pad(int elem_bytes, const void* src, void* dst, int N, int C, int H, int W, int cp,
+                                int pt, int pl, int pb, int pr, int mode, hipStream_t st) {
+  switch (elem_bytes) {
+    case 1: return nchw_to_nhwc_pad_t<uint8_t>(src, dst, N, C, H, W, cp, pt, pl, pb, pr, mode, st);
+    case 2: return nchw_to_nhwc_pad_t<uint16_t>(src, dst, N, C, H, W, cp, pt, pl, pb, pr, mode, st);
+    case 4: return nchw_to_nhwc_pad_t<uint32_t>(src, dst, N, C, H, W, cp, pt, pl, pb, pr, mode, st);
+    default: return hipErrorInvalidValue;
+  }
+}
+
 // dst[r][c] = c < K ? src[r * rs + c * cs] : 0 for a [R][ld] destination: pads a
 // row-major operand to whole 16-byte chunks, or materialises a transpose.
 template <class T>

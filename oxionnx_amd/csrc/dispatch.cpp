@@ -396,8 +396,18 @@ int do_conv(ohip_ctx* ctx, const ohip_node* nd, int placement, ohip_output* out)
   void* yd = st.alloc(obytes);
   if (!xd || !yd || (b && !bd)) { if (!cache) ohip_weight_release(wt); return OHIP_E_NOMEM; }
   ohip_conv_desc d{g.n, g.c, g.h, g.w, g.cout, g.kh, g.kw, 1, g.sh, g.sw, g.dh, g.dw, g.pt, g.pl, g.pb, g.pr,
-                   dt, OHIP_NCHW, OHIP_NCHW, 0, 0.0f, 0.0f};
+                   dt, OHIP_NCHW, OHIP_NCHW, 0, 0.0f, 0.0f, OHIP_PAD_ZEROS};
   fused_act(nd, &d.act, &d.act_lo, &d.act_hi);
+  // this provider's Pad -> Conv fusion: the pads are a reflect / edge Pad's
+  {
+    const std::string pm = attr_s(nd, "pad_mode");
+    if (pm == "reflect") d.pad_mode = OHIP_PAD_REFLECT;
+    else if (pm == "edge") d.pad_mode = OHIP_PAD_EDGE;
+    else if (!pm.empty() && pm != "constant") {
+      if (!cache) ohip_weight_release(wt);
+      return decline("Conv: pad_mode");
+    }
+  }
   rc = ohip_conv2d(ctx, &d, xd, wt, bd, yd);
   if (!cache) ohip_weight_release(wt);
   if (rc) return rc;
@@ -806,6 +816,13 @@ int do_binary(ohip_ctx* ctx, const ohip_node* nd, int op, int placement, ohip_ou
 // ---------------------------------------------------------------- instance normalisation
 // OxiInstanceNorm (registry/oxi_instance_norm.rs:135-146): no affine term.
 // InstanceNormalization (nn/normalization.rs:251-280): per-channel scale, B.
+// This provider's fused AdaIN form of OxiInstanceNorm (the optimizer-side
+// fusion of OxiInstanceNorm -> Mul(gamma) -> Add(beta) [-> Relu], the
+// modulation of style-based generators): inputs 1 / 2 are resident [N, S]
+// style rows; gamma of sample n, channel c is element n * S + scale_offset + c
+// of input 1 and beta the same of input 2 at bias_offset; "activation" may be
+// "relu".  The arithmetic is the unfused chain's: norm, then * gamma, then
+// + beta, then the activation, each in f32.
 int do_instnorm(ohip_ctx* ctx, const ohip_node* nd, bool affine, int placement, ohip_output* out) {
   const ohip_tensor* x = input(nd, 0);
   if (!x || x->rank < 3) return decline("InstanceNorm: rank < 3");
@@ -817,16 +834,34 @@ int do_instnorm(ohip_ctx* ctx, const ohip_node* nd, bool affine, int placement, 
   if (spatial == 0 || N * C == 0) return decline("InstanceNorm: empty");
   const float eps = attr_f(nd, "epsilon", 1e-5f);
   Stage st(ctx);
-  ohip::NormAffine aff{nullptr, nullptr, 0, ohip::UN_IDENTITY, 0.0f};
+  ohip::NormAffine aff{nullptr, nullptr, 0, 0, 0, ohip::UN_IDENTITY, 0.0f};
   std::vector<float> sc, bi;
   if (affine) {
     const ohip_tensor *s = input(nd, 1), *b = input(nd, 2);
     if (!s || !b || !host_only(s) || !host_only(b) || numel(s) != C || numel(b) != C)
       return decline("InstanceNormalization: scale / B");
     for (int64_t i = 0; i < C; ++i) { sc.push_back((float)host_at(s, i)); bi.push_back((float)host_at(b, i)); }
-    aff.scale = static_cast<const float*>(st.cached(s, "InstanceNormalization.scale", OHIP_F32, sc.data(), sc.size() * 4));
-    aff.bias = static_cast<const float*>(st.cached(b, "InstanceNormalization.B", OHIP_F32, bi.data(), bi.size() * 4));
+    aff.scale = st.cached(s, "InstanceNormalization.scale", OHIP_F32, sc.data(), sc.size() * 4);
+    aff.bias = st.cached(b, "InstanceNormalization.B", OHIP_F32, bi.data(), bi.size() * 4);
     if (!aff.scale || !aff.bias) return OHIP_E_NOMEM;
+  } else if (nd->n_inputs >= 3 && input(nd, 1) && input(nd, 2)) {
+    const ohip_tensor *g = input(nd, 1), *b = input(nd, 2);
+    if (!g->device || !b->device || g->dtype != dt || b->dtype != dt || g->rank != 2 || b->rank != 2 ||
+        g->shape[0] != N || b->shape[0] != N || g->shape[1] != b->shape[1])
+      return decline("OxiInstanceNorm: modulation operands must be resident [N, S] rows of the input's dtype");
+    const int64_t so = attr_i(nd, "scale_offset", 0), bo = attr_i(nd, "bias_offset", 0), S = g->shape[1];
+    if (so < 0 || bo < 0 || so + C > S || bo + C > S) return decline("OxiInstanceNorm: modulation offsets");
+    const int eb = ebytes(dt);
+    aff.scale = static_cast<const char*>(ohip_dtensor_ptr(g->device)) + so * eb;
+    aff.bias = static_cast<const char*>(ohip_dtensor_ptr(b->device)) + bo * eb;
+    aff.per_sample = 1;
+    aff.stride = S;
+    aff.same_type = 1;
+    std::string act = attr_s(nd, "activation");
+    if (act == "relu") aff.act = ohip::UN_RELU;
+    else if (!act.empty()) return decline("OxiInstanceNorm: activation");
+  } else if (nd->n_inputs > 1 && (input(nd, 1) || (nd->n_inputs > 2 && input(nd, 2)))) {
+    return decline("OxiInstanceNorm: one input or three");
   }
   const void* xd = float_operand(st, x, dt);
   const size_t bytes = (size_t)numel(x) * ebytes(dt);
@@ -1262,13 +1297,14 @@ extern "C" int ohip_is_supported_op(const char* op) {
 extern "C" int ohip_accepts_resident_slot(const char* op, int index) {
   if (!op) return 0;
   static const char* kSlot0[] = {"Conv", "Gemm", "MatMul", "QLinearConv", "Relu", "LeakyRelu", "Tanh", "Sigmoid",
-                                 "Silu", "Identity", "OxiInstanceNorm", "InstanceNormalization", "Resize", "Pad",
+                                 "Silu", "Identity", "InstanceNormalization", "Resize", "Pad",
                                  "MaxPool", "Slice", "Reshape", "Flatten", "Squeeze", "Unsqueeze",
                                  "QuantizeLinear", "DequantizeLinear"};
   for (const char* o : kSlot0)
     if (std::strcmp(op, o) == 0) return index == 0;
   if (!std::strcmp(op, "Add") || !std::strcmp(op, "Sub") || !std::strcmp(op, "Mul") || !std::strcmp(op, "Div"))
     return index == 0 || index == 1;
+  if (!std::strcmp(op, "OxiInstanceNorm")) return index >= 0 && index <= 2;
   if (!std::strcmp(op, "Concat")) return index >= 0;
   return 0;
 }

@@ -49,15 +49,16 @@ struct OutMap {
 };
 
 // Split-K plan: a contraction whose 64x64 tiling leaves the 256 CUs short
-// of blocks and whose K loop is long is cut into K slices (each at least 8
-// stages of 128 bytes), aiming at two blocks per CU.  forced_tile 10 forces
+// of blocks (under one block per CU with at least 16 stages of 128 bytes of
+// K, or under two with at least 32) is cut into K slices (each at least 8
+// stages), aiming at two blocks per CU.  forced_tile 10 forces
 // the split path; any other forced tile disables it.
 inline int plan_splits(int P, int Q, int kc, int forced_tile) {
   if (forced_tile != 0 && forced_tile != 10) return 1;
   const int64_t nk = (kc + 7) / 8;
   const int64_t nb = (int64_t)((P + 63) / 64) * ((Q + 63) / 64);
   if (forced_tile == 10) return (int)std::max<int64_t>(2, std::min<int64_t>(16, nk / 2 > 0 ? nk / 2 : 1));
-  if (nb >= 256 || nk < 16) return 1;
+  if (nb >= 512 || nk < 16 || (nb >= 256 && nk < 32)) return 1;
   int64_t s = (512 + nb - 1) / nb;
   s = std::min<int64_t>(s, nk / 8);
   s = std::min<int64_t>(s, 16);
@@ -108,6 +109,8 @@ hipError_t run_conv_quant(const Im2colOperand& col, const DenseOperand& w, bool 
 hipError_t run_gemv(int dtype, const GemvArgs& g, const FloatOut& o, hipStream_t st);
 hipError_t run_nchw_to_nhwc(int elem_bytes, const void* src, void* dst, int N, int C, int HW, int cp,
                             hipStream_t st);
+hipError_t run_nchw_to_nhwc_pad(int elem_bytes, const void* src, void* dst, int N, int C, int H, int W, int cp,
+                                int pt, int pl, int pb, int pr, int mode, hipStream_t st);
 hipError_t run_gather2d(int elem_bytes, const void* src, int64_t rs, int64_t cs, void* dst, int R, int K, int ld,
                         hipStream_t st);
 
@@ -129,9 +132,11 @@ struct BcastPlan {
 
 // Optional affine term and activation applied after the normalisation.
 struct NormAffine {
-  const float* scale;  // per channel, or per (n, c) when per_sample
-  const float* bias;
-  int per_sample;
+  const void* scale;   // per channel, or per (n, c) when per_sample; f32 or the tensor's dtype
+  const void* bias;
+  int per_sample;      // scale / bias index n * stride + c
+  int64_t stride;      // per-sample row stride (elements) of scale / bias
+  int same_type;       // scale / bias are in the normalised tensor's dtype (else f32)
   int act;             // UN_NONE / UN_RELU / UN_LEAKY_RELU
   float alpha;
 };

@@ -282,7 +282,7 @@ inline int pick_tile(int P, int Q, int kc, int forced) {
   if (nk <= 16) return blocks(128, 128) >= 256 ? 8 : 9;
   if (blocks(256, 256) >= 256) return 6;
   if (blocks(256, 128) >= 256) return P >= Q ? 3 : 4;
-  if (blocks(128, 128) >= 128) return 8;
+  if (blocks(128, 128) >= 192) return 8;
   return 9;
 }
 

@@ -120,8 +120,15 @@ __global__ void __launch_bounds__(kThreads) instnorm_kernel(const T* __restrict_
   const int64_t n = plane / C;
   float sc = 1.0f, bi = 0.0f;
   bool affine = false;
-  if (aff.scale) { sc = aff.scale[aff.per_sample ? plane : c]; affine = true; }
-  if (aff.bias) { bi = aff.bias[aff.per_sample ? n * C + c : c]; affine = true; }
+  const int64_t ai = aff.per_sample ? n * aff.stride + c : c;
+  if (aff.scale) {
+    sc = aff.same_type ? ldf(static_cast<const T*>(aff.scale), ai) : static_cast<const float*>(aff.scale)[ai];
+    affine = true;
+  }
+  if (aff.bias) {
+    bi = aff.same_type ? ldf(static_cast<const T*>(aff.bias), ai) : static_cast<const float*>(aff.bias)[ai];
+    affine = true;
+  }
   for (int64_t i = threadIdx.x; i < spatial; i += kThreads) {
     float v = (ldf(xp, i) - mean) * inv;
     if (affine) {

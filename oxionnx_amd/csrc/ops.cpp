@@ -1061,9 +1061,19 @@ extern "C" int ohip_conv2d(ohip_ctx* ctx, const ohip_conv_desc* d, const void* x
   std::lock_guard<std::mutex> lock(ctx->mu);
   ctx->counters.dispatches++;
 
+  // A fused reflect / edge Pad is applied by the staging transpose, which
+  // then writes the padded image; the convolution itself runs unpadded.
+  const bool fused_pad = d->pad_mode == OHIP_PAD_REFLECT || d->pad_mode == OHIP_PAD_EDGE;
+  if (d->pad_mode != OHIP_PAD_ZEROS && !fused_pad) return fail(OHIP_E_INVALID, "ohip_conv2d: pad_mode");
+  if (fused_pad && d->in_layout != OHIP_NCHW) return fail(OHIP_E_INVALID, "ohip_conv2d: a fused Pad needs an NCHW input");
+  if (d->pad_mode == OHIP_PAD_REFLECT &&
+      ((d->h > 1 && (d->pad_t >= d->h || d->pad_b >= d->h)) || (d->w > 1 && (d->pad_l >= d->w || d->pad_r >= d->w))))
+    return fail(OHIP_DECLINED, "ohip_conv2d: reflect pad wider than the image");
+  const int64_t sh_ = fused_pad ? d->h + d->pad_t + d->pad_b : d->h;
+  const int64_t sw_ = fused_pad ? d->w + d->pad_l + d->pad_r : d->w;
   ScratchPlan plan;
   const bool stage = d->in_layout == OHIP_NCHW;
-  size_t ix = stage ? plan.add((size_t)(d->n * d->h * d->w * cp) * eb) : SIZE_MAX;
+  size_t ix = stage ? plan.add((size_t)(d->n * sh_ * sw_ * cp) * eb) : SIZE_MAX;
   const bool nchw_out = d->out_layout == OHIP_NCHW;
   const int sP = nchw_out ? (int)rows : (int)d->cout, sQ = nchw_out ? (int)d->cout : (int)rows;
   const int splits = plan_splits(sP, sQ, (int)(d->kh * d->kw * (cp / ce)), ctx->tile_override);
@@ -1073,18 +1083,24 @@ extern "C" int ohip_conv2d(ohip_ctx* ctx, const ohip_conv_desc* d, const void* x
   const void* xin = x;
   if (stage) {
     void* px = scratch_at(ctx, plan, ix);
-    HIP_TRY(run_nchw_to_nhwc(eb, x, px, (int)d->n, (int)d->c, (int)(d->h * d->w), (int)cp, ctx->stream),
-            "NCHW -> NHWC");
+    if (fused_pad)
+      HIP_TRY(run_nchw_to_nhwc_pad(eb, x, px, (int)d->n, (int)d->c, (int)d->h, (int)d->w, (int)cp, (int)d->pad_t,
+                                   (int)d->pad_l, (int)d->pad_b, (int)d->pad_r, (int)d->pad_mode, ctx->stream),
+              "NCHW -> padded NHWC");
+    else
+      HIP_TRY(run_nchw_to_nhwc(eb, x, px, (int)d->n, (int)d->c, (int)(d->h * d->w), (int)cp, ctx->stream),
+              "NCHW -> NHWC");
     xin = px;
   } else if (!aligned(x, 16)) {
     return fail(OHIP_E_INVALID, "ohip_conv2d: NHWC input must be 16-byte aligned");
   }
 
   Im2colOperand col{};
-  col.base = xin; col.H = (int)d->h; col.W = (int)d->w; col.OH = (int)g.oh; col.OW = (int)g.ow;
+  col.base = xin; col.H = (int)sh_; col.W = (int)sw_; col.OH = (int)g.oh; col.OW = (int)g.ow;
   col.KW = (int)d->kw; col.cpc = (int)(cp / ce);
   col.sh = (int)d->stride_h; col.sw = (int)d->stride_w; col.dh = (int)d->dil_h; col.dw = (int)d->dil_w;
-  col.pt = (int)d->pad_t; col.pl = (int)d->pad_l; col.rows = (int)rows; col.kc = w->kc;
+  col.pt = fused_pad ? 0 : (int)d->pad_t; col.pl = fused_pad ? 0 : (int)d->pad_l;
+  col.rows = (int)rows; col.kc = w->kc;
   col.xor_mask = 0; col.pad16 = pad16(ctx, 0);
   DenseOperand wt{w->data, w->ld_bytes, (int)d->cout, w->kc, 0, 0u, pad16(ctx, 0)};
 

@@ -8,14 +8,20 @@ The reference session runs a declined node on its CPU operator; this package
 has no CPU operators, so a decline here raises ``NodeDeclined`` naming the
 node and the provider's reason.
 
-``optimize`` applies two node fusions before the run, in the manner of the
+``optimize`` applies node fusions before the run, in the manner of the
 reference's optimizer passes (src/optimizer/fusion/mod.rs):
   * Conv followed by its only consumer Relu / LeakyRelu becomes one Conv with
     the ``activation`` attribute (the reference's Conv+Relu fusion contract,
     registry/conv_ops/conv.rs:124-156; LeakyRelu is this provider's addition);
   * QLinearConv -> DequantizeLinear -> Silu -> QuantizeLinear, each the only
     consumer of the previous, becomes one QLinearConv whose requantised bytes
-    pass through a 256-entry table that reproduces the three nodes exactly.
+    pass through a 256-entry table that reproduces the three nodes exactly;
+  * a reflect / edge Pad consumed only by an unpadded Conv becomes the Conv's
+    pads with ``pad_mode`` (applied while the input is staged);
+  * OxiInstanceNorm -> Mul(gamma) -> Add(beta) [-> Relu], where gamma and beta
+    are Reshape(Slice(style)) column ranges of one style tensor (AdaIN),
+    becomes one OxiInstanceNorm that reads the modulation from the style rows.
+Nodes left without consumers are dropped.
 """
 import ctypes
 from dataclasses import dataclass, field, replace
@@ -117,8 +123,109 @@ def fuse(graph: Graph) -> Graph:
                 nodes[j] = nodes[k] = nodes[q] = None
                 changed = True
                 break
+            if n.op == "Pad" and n.attrs.strings.get("mode", "constant") in ("reflect", "edge"):
+                if _fuse_pad_into_conv(nodes, i, sole, inits):
+                    changed = True
+                    break
+            if n.op == "OxiInstanceNorm" and len([t for t in n.inputs if t]) == 1:
+                if _fuse_adain(nodes, i, sole, inits):
+                    changed = True
+                    break
         nodes = [n for n in nodes if n is not None] if changed else nodes
-    return replace(graph, nodes=nodes)
+    return replace(graph, nodes=_drop_dead(nodes, keep_out))
+
+
+def _drop_dead(nodes, keep):
+    """Removes nodes none of whose outputs is consumed or a graph output."""
+    while True:
+        used = {t for n in nodes for t in n.inputs if t}
+        live = [n for n in nodes if any(o in used or o in keep for o in n.outputs)]
+        if len(live) == len(nodes):
+            return nodes
+        nodes = live
+
+
+def _ints(inits, name):
+    v = inits.get(name)
+    if v is None:
+        return None
+    return [int(x) for x in np.asarray(v.data if isinstance(v, ep.Typed) else v).reshape(-1)]
+
+
+def _fuse_pad_into_conv(nodes, i, sole, inits):
+    """Pad(reflect | edge) on H / W only, consumed only by an unpadded Conv:
+    the Conv takes the pads with pad_mode, and its input staging applies them."""
+    pad = nodes[i]
+    j = sole(pad.outputs[0])
+    if j is None or nodes[j].op != "Conv" or nodes[j].inputs[0] != pad.outputs[0]:
+        return False
+    conv = nodes[j]
+    p = _ints(inits, pad.inputs[1]) if len(pad.inputs) > 1 and pad.inputs[1] else pad.attrs.int_lists.get("pads")
+    if p is None or len(p) != 8 or p[0] or p[1] or p[4] or p[5] or min(p) < 0:
+        return False
+    if any(conv.attrs.int_lists.get("pads", [0, 0, 0, 0])) or conv.attrs.strings.get("auto_pad", "NOTSET") not in ("NOTSET", ""):
+        return False
+    if conv.attrs.ints.get("group", 1) != 1 or "pad_mode" in conv.attrs.strings:
+        return False
+    a = replace(conv.attrs, strings=dict(conv.attrs.strings), int_lists=dict(conv.attrs.int_lists))
+    a.int_lists["pads"] = [p[2], p[3], p[6], p[7]]
+    a.strings["pad_mode"] = pad.attrs.strings.get("mode")
+    nodes[j] = replace(conv, inputs=[pad.inputs[0]] + list(conv.inputs[1:]), attrs=a)
+    nodes[i] = None
+    return True
+
+
+def _modulation(nodes, producer, inits, tensor):
+    """tensor = Reshape(Slice(S, [a], [b], [1]), [N, b - a, 1, 1]) -> (S, a), else None."""
+    r = producer.get(tensor)
+    if r is None or nodes[r] is None or nodes[r].op != "Reshape":
+        return None
+    sl = producer.get(nodes[r].inputs[0])
+    if sl is None or nodes[sl] is None or nodes[sl].op != "Slice" or len(nodes[sl].inputs) < 4:
+        return None
+    s = nodes[sl]
+    st, en, ax = _ints(inits, s.inputs[1]), _ints(inits, s.inputs[2]), _ints(inits, s.inputs[3])
+    shp = _ints(inits, nodes[r].inputs[1])
+    if not st or not en or ax != [1] or len(st) != 1 or len(en) != 1 or st[0] < 0 or en[0] <= st[0]:
+        return None
+    if s.inputs[4:] and s.inputs[4] and _ints(inits, s.inputs[4]) != [1]:
+        return None
+    if shp is None or len(shp) != 4 or shp[1] != en[0] - st[0] or shp[2] != 1 or shp[3] != 1:
+        return None
+    return s.inputs[0], st[0]
+
+
+def _fuse_adain(nodes, i, sole, inits):
+    """OxiInstanceNorm -> Mul(gamma) -> Add(beta) [-> Relu], gamma / beta being
+    Reshape(Slice(style)) column ranges of one style tensor: one
+    OxiInstanceNorm reading the modulation straight from the style rows."""
+    producer = {o: k for k, nd in enumerate(nodes) if nd is not None for o in nd.outputs}
+    norm = nodes[i]
+    j = sole(norm.outputs[0])
+    if j is None or nodes[j].op != "Mul":
+        return False
+    mul = nodes[j]
+    g = mul.inputs[1] if mul.inputs[0] == norm.outputs[0] else mul.inputs[0]
+    k = sole(mul.outputs[0])
+    if k is None or nodes[k].op != "Add":
+        return False
+    add = nodes[k]
+    b = add.inputs[1] if add.inputs[0] == mul.outputs[0] else add.inputs[0]
+    gm, bm = _modulation(nodes, producer, inits, g), _modulation(nodes, producer, inits, b)
+    if gm is None or bm is None or gm[0] != bm[0]:
+        return False
+    last, act = k, None
+    r = sole(add.outputs[0])
+    if r is not None and nodes[r].op == "Relu":
+        last, act = r, "relu"
+    a = replace(norm.attrs, strings=dict(norm.attrs.strings), ints=dict(norm.attrs.ints))
+    a.ints["scale_offset"], a.ints["bias_offset"] = gm[1], bm[1]
+    if act:
+        a.strings["activation"] = act
+    nodes[i] = replace(norm, inputs=[norm.inputs[0], gm[0], bm[0]], outputs=list(nodes[last].outputs), attrs=a)
+    for idx in {j, k, last}:
+        nodes[idx] = None
+    return True
 
 
 class Session:
