@@ -130,7 +130,7 @@ gemv_row_kernel(const T* __restrict__ a, int64_t lda, const T* __restrict__ w, i
 #pragma unroll
     for (int q = 0; q < kWaves; ++q) v += red[q][tid];
     // GEMM orientation: i = n (weight row), j = m (activation row)
-    epi.y[epi.index(n, tid)] = from_f32<T>(epi.finish(v, n, tid));
+    epi.store_one(v, n, tid);
   }
 }
 

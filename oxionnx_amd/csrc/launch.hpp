@@ -7,6 +7,7 @@
 #include "internal.hpp"
 #include "mfma_core.hpp"
 
+#include <cstdlib>
 #include <type_traits>
 
 namespace ohip {
@@ -24,84 +25,147 @@ __device__ __forceinline__ float activate(float v, int act, float lo, float hi) 
   }
 }
 
-// Float output: v = acc; v *= alpha (when alpha != 1); v += beta * bias; act;
-// round to OutT.  Output element (i, j) sits at
-//   (i / ohw) * bstride + (i % ohw) * si + j * sj.
+// Both epilogues read their per-position parameters (biases, column sums,
+// scales) in two batches before any output is formed: PreI for the sixteen
+// i positions i0 + 8g + r (g, r < 4) of a 32-row MFMA tile, PreJ for one j.
+// Each batch is a run of independent loads with a single wait.  finish()
+// then turns the tile's sixteen accumulators into output bit patterns with
+// its mode switches outside the element loops: the epilogue runs once per
+// block, and a per-element branch tree there costs more instruction fetch
+// than a short K loop costs MFMA time.
+
+// an index clamped into [0, n): positions past the edge read a valid element
+// whose value is then discarded
+__device__ __forceinline__ int clamp_index(int i, int n) { return i < n ? i : n - 1; }
+
+// o[r] = p[i + r] for r < 4: one vector load when i is a multiple of 4, the
+// run lies inside [0, n) and p is 16-byte aligned (vec), else clamped scalars
+template <class T> __device__ __forceinline__ void load4(const T* p, int i, int n, bool vec, T (&o)[4]) {
+  if (vec && (i & 3) == 0 && i + 3 < n) {
+    if constexpr (sizeof(T) == 4) {
+      const u32x4 v = *reinterpret_cast<const u32x4*>(p + i);
+      const uint32_t w0 = v.x, w1 = v.y, w2 = v.z, w3 = v.w;   // lanes by value before the bit casts
+      o[0] = __builtin_bit_cast(T, w0); o[1] = __builtin_bit_cast(T, w1);
+      o[2] = __builtin_bit_cast(T, w2); o[3] = __builtin_bit_cast(T, w3);
+    } else if constexpr (sizeof(T) == 2) {
+      typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+      const u32x2 v = *reinterpret_cast<const u32x2*>(p + i);
+      const uint32_t lo = v.x, hi = v.y;
+      o[0] = __builtin_bit_cast(T, (uint16_t)lo); o[1] = __builtin_bit_cast(T, (uint16_t)(lo >> 16));
+      o[2] = __builtin_bit_cast(T, (uint16_t)hi); o[3] = __builtin_bit_cast(T, (uint16_t)(hi >> 16));
+    } else {
+      const uint32_t v = *reinterpret_cast<const uint32_t*>(p + i);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) o[r] = __builtin_bit_cast(T, (uint8_t)(v >> (8 * r)));
+    }
+  } else {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) o[r] = p[clamp_index(i + r, n)];
+  }
+}
+
+template <class T> __device__ __forceinline__ uint32_t out_bits(T v) {
+  if constexpr (sizeof(T) == 2) return __builtin_bit_cast(uint16_t, v);
+  else return __builtin_bit_cast(uint32_t, v);
+}
+
+// Float output: v = acc * alpha; v = v + beta * bias; act; round to OutT.
+// alpha == 1 multiplies exactly, and a missing bias adds -0.0, the exact
+// additive identity, so neither needs a branch.
 template <class OutT> struct FloatEpi {
-  OutT* y;
-  int64_t si, sj, bstride;
-  int ohw, P, Q;
-  int vec;            // si == 1 and every 4-run of i is contiguous and aligned
-  int has_alpha;
+  OutAddr out;
   float alpha, beta;
   const OutT* bias;
   int bias_mode;      // BIAS_*
+  int bias_vec;       // bias is 16-byte aligned: runs of four load as one vector
   int act;
   float lo, hi;
 
-  __device__ __forceinline__ float bias_at(int i, int j) const {
-    switch (bias_mode) {
-      case BIAS_SCALAR: return to_f32(bias[0]);
-      case BIAS_I: return to_f32(bias[i]);
-      case BIAS_J: return to_f32(bias[j]);
-      case BIAS_FULL_JI: return to_f32(bias[(int64_t)j * P + i]);
-      default: return 0.0f;
-    }
-  }
-  __device__ __forceinline__ float finish(float v, int i, int j) const {
-    if (has_alpha) v = v * alpha;
-    if (bias_mode != BIAS_NONE) v = v + beta * bias_at(i, j);
-    return activate(v, act, lo, hi);
-  }
-  __device__ __forceinline__ int64_t index(int i, int j) const {
-    if (bstride == 0) return (int64_t)i * si + (int64_t)j * sj;
-    const int n = i / ohw;
-    return (int64_t)n * bstride + (int64_t)(i - n * ohw) * si + (int64_t)j * sj;
-  }
-  // LDS-staged epilogue (mfma_core.hpp): 1- and 2-byte outputs are written as
-  // whole 16-byte row chunks when rows of i are contiguous and aligned.
   static constexpr int kStageBytes = sizeof(OutT) <= 2 ? (int)sizeof(OutT) : 0;
+  __device__ __forceinline__ int out_bytes() const { return (int)sizeof(OutT); }
+  __device__ __forceinline__ OutAddr addr() const { return out; }
   __device__ __forceinline__ bool staged_ok(int bp) const {
-    return vec && ((uintptr_t)y % 16 == 0) && ((sj * (int64_t)sizeof(OutT)) % 16 == 0) &&
-           (bstride == 0 || ohw % bp == 0);
+    return out.stage && out.vec && ((uintptr_t)out.y % 16 == 0) && ((out.sj * (int64_t)sizeof(OutT)) % 16 == 0) &&
+           (out.bstride == 0 || out.ohw % bp == 0);
   }
-  __device__ __forceinline__ char* out_ptr(int i, int j) const { return reinterpret_cast<char*>(y + index(i, j)); }
-  // The four outputs (i0..i0+3, j) as packed bits; positions outside the
-  // matrix give 0 and read nothing.
-  __device__ __forceinline__ uint64_t pack4(int i0, int j, f32x4 acc) const {
-    uint64_t bits = 0;
+
+  struct PreI { float b[16]; };   // beta * bias per row (BIAS_I, BIAS_SCALAR), else -0
+  struct PreJ { float b; };       // beta * bias per column (BIAS_J), else -0
+  __device__ __forceinline__ void load_i(PreI& p, int i0, int ng) const {
+#pragma clang fp contract(off)
+    if (bias_mode == BIAS_I) {
+      // unconditional loads at clamped (in-range) positions, selected
+      // afterwards: the sixteen loads issue back to back under one wait
+      OutT raw[16];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const bool in = j < Q && i0 + r < P;
-      const OutT o = from_f32<OutT>(in ? finish(acc[r], i0 + r, j) : 0.0f);
-      uint64_t b;
-      if constexpr (sizeof(OutT) == 2) b = __builtin_bit_cast(uint16_t, o);
-      else b = __builtin_bit_cast(uint32_t, o);
-      bits |= b << (r * 8 * sizeof(OutT));
-    }
-    return bits;
-  }
-  __device__ __forceinline__ void store(int i0, int j, f32x4 acc) const {
-    if (j >= Q) return;
-    if (vec && i0 + 3 < P) {
-      OutT o[4];
+      for (int g = 0; g < 4; ++g) {
+        OutT q[4];
+        load4(bias, i0 + 8 * g, out.P, bias_vec, q);
 #pragma unroll
-      for (int r = 0; r < 4; ++r) o[r] = from_f32<OutT>(finish(acc[r], i0 + r, j));
-      OutT* dst = y + index(i0, j);
-      if constexpr (sizeof(OutT) == 4) {
-        *reinterpret_cast<f32x4*>(dst) = f32x4{__builtin_bit_cast(float, o[0]), __builtin_bit_cast(float, o[1]),
-                                               __builtin_bit_cast(float, o[2]), __builtin_bit_cast(float, o[3])};
-      } else {
-        typedef uint16_t u16x4 __attribute__((ext_vector_type(4)));
-        *reinterpret_cast<u16x4*>(dst) =
-            u16x4{__builtin_bit_cast(uint16_t, o[0]), __builtin_bit_cast(uint16_t, o[1]),
-                  __builtin_bit_cast(uint16_t, o[2]), __builtin_bit_cast(uint16_t, o[3])};
+        for (int r = 0; r < 4; ++r) raw[4 * g + r] = q[r];
       }
-      return;
+#pragma unroll
+      for (int k = 0; k < 16; ++k) {
+        const int i = i0 + 8 * (k >> 2) + (k & 3);
+        p.b[k] = ((k >> 2) < ng && i < out.P) ? beta * to_f32(raw[k]) : 0.0f;
+      }
+    } else {
+      const float s = bias_mode == BIAS_SCALAR ? beta * to_f32(bias[0]) : -0.0f;
+#pragma unroll
+      for (int k = 0; k < 16; ++k) p.b[k] = s;
+    }
+  }
+  __device__ __forceinline__ void load_j(PreJ& p, int j) const {
+#pragma clang fp contract(off)
+    if (bias_mode == BIAS_J) {
+      const float x = to_f32(bias[clamp_index(j, out.Q)]);
+      p.b = j < out.Q ? beta * x : 0.0f;
+    } else {
+      p.b = -0.0f;
+    }
+  }
+  template <class A>
+  __device__ __forceinline__ void finish(const PreI& pi, const PreJ& pj, int i0, int j, A acc,
+                                         uint32_t (&bits)[16]) const {
+#pragma clang fp contract(off)
+    float v[16];
+#pragma unroll
+    for (int k = 0; k < 16; ++k) v[k] = acc[k] * alpha;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) v[k] = v[k] + (pi.b[k] + pj.b);
+    if (bias_mode == BIAS_FULL_JI) {
+      OutT c[16];
+      const int64_t cj = (int64_t)clamp_index(j, out.Q) * out.P;
+#pragma unroll
+      for (int k = 0; k < 16; ++k) c[k] = bias[cj + clamp_index(i0 + 8 * (k >> 2) + (k & 3), out.P)];
+#pragma unroll
+      for (int k = 0; k < 16; ++k) v[k] = v[k] + beta * to_f32(c[k]);
+    }
+    if (act == ACT_RELU) {
+#pragma unroll
+      for (int k = 0; k < 16; ++k) v[k] = v[k] > 0.0f ? v[k] : 0.0f;   // f32::max(NaN, 0) == 0
+    } else if (act == ACT_CLIP) {
+#pragma unroll
+      for (int k = 0; k < 16; ++k) v[k] = v[k] < lo ? lo : (v[k] > hi ? hi : v[k]);
+    } else if (act == ACT_LEAKY_RELU) {
+#pragma unroll
+      for (int k = 0; k < 16; ++k) v[k] = v[k] >= 0.0f ? v[k] : v[k] * lo;
     }
 #pragma unroll
-    for (int r = 0; r < 4; ++r)
-      if (i0 + r < P) y[index(i0 + r, j)] = from_f32<OutT>(finish(acc[r], i0 + r, j));
+    for (int k = 0; k < 16; ++k) bits[k] = out_bits(from_f32<OutT>(v[k]));
+  }
+  // one output of a reduction that has no MFMA tile (the GEMV path)
+  __device__ __forceinline__ void store_one(float acc, int i, int j) const {
+    PreI pi;
+    PreJ pj;
+    load_i(pi, i, 1);
+    load_j(pj, j);
+    f32x16 a = {};
+    a[0] = acc;
+    uint32_t bits[16];
+    finish(pi, pj, i, j, a, bits);
+    OutT* dst = reinterpret_cast<OutT*>(out.y) + out.row(i) + (int64_t)j * out.sj;
+    *dst = __builtin_bit_cast(OutT, (typename std::conditional<sizeof(OutT) == 2, uint16_t, uint32_t>::type)bits[0]);
   }
 };
 
@@ -113,10 +177,7 @@ template <class OutT> struct FloatEpi {
 // follows SatRange::requantize: f64 product with the f32 combined scale, + zp,
 // round half to even, clamp.
 struct QuantEpi {
-  void* y;
-  int64_t si, sj, bstride;
-  int ohw, P, Q;
-  int vec;
+  OutAddr out;
   int w_on_i;               // weight channel index is i (else j)
   const int32_t* colsum;    // per weight channel
   const int8_t* flip;       // per weight channel: 1 = the packed channel holds -(w - w_zp)
@@ -128,25 +189,77 @@ struct QuantEpi {
   int out_kind;             // QOUT_U8, QOUT_I8, QOUT_I32 (raw), QOUT_F32 (requantised, as f32)
   int32_t y_zp, lo, hi;
   const uint8_t* table;     // byte -> byte map applied after requantisation (may be null)
+  int vec_ok;               // every per-channel / per-row array is 16-byte aligned
 
-  __device__ __forceinline__ int64_t index(int i, int j) const {
-    if (bstride == 0) return (int64_t)i * si + (int64_t)j * sj;
-    const int n = i / ohw;
-    return (int64_t)n * bstride + (int64_t)(i - n * ohw) * si + (int64_t)j * sj;
+  static constexpr int kStageBytes = 1;
+  __device__ __forceinline__ int out_bytes() const { return (out_kind == QOUT_U8 || out_kind == QOUT_I8) ? 1 : 4; }
+  __device__ __forceinline__ OutAddr addr() const { return out; }
+  __device__ __forceinline__ bool staged_ok(int bp) const {
+    return out.stage && (out_kind == QOUT_U8 || out_kind == QOUT_I8) && out.vec && ((uintptr_t)out.y % 16 == 0) &&
+           (out.sj % 16 == 0) && (out.bstride == 0 || out.ohw % bp == 0);
   }
-  __device__ __forceinline__ int32_t exact(int32_t acc, int i, int j) const {
-    const int ch = w_on_i ? i : j;
-    const int row = w_on_i ? j : i;
-    const uint32_t c = (uint32_t)(ca_rows ? ca_rows[row] : ca);
-    uint32_t v = (uint32_t)acc + c * (uint32_t)colsum[ch];
-    if (flip && flip[ch]) v = 0u - v;
-    if (bias) v += (uint32_t)bias[ch];
+
+  // per-channel terms of a weight channel, and the correction factor of an
+  // activation row
+  struct Chan { int32_t cs, bi, fl; float cb; };
+  struct PreI { Chan c[16]; int32_t ca[16]; };
+  struct PreJ { Chan c; int32_t ca; };
+  // ch must be in range (callers clamp); the loads carry no branch
+  __device__ __forceinline__ Chan chan(int ch) const {
+    Chan c;
+    c.cs = colsum[ch];
+    c.bi = bias ? bias[ch] : 0;
+    c.fl = flip ? flip[ch] : 0;
+    c.cb = comb[n_comb > 1 ? ch : 0];
+    return c;
+  }
+  __device__ __forceinline__ void load_i(PreI& p, int i0, int ng) const {
+    if (w_on_i) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int i = i0 + 8 * g;
+        int32_t cs[4], bi[4] = {0, 0, 0, 0};
+        int8_t fl[4] = {0, 0, 0, 0};
+        float cb[4];
+        load4(colsum, i, out.P, vec_ok, cs);
+        if (bias) load4(bias, i, out.P, vec_ok, bi);
+        if (flip) load4(flip, i, out.P, vec_ok, fl);
+        if (n_comb > 1) {
+          load4(comb, i, out.P, vec_ok, cb);
+        } else {
+          const float c0 = comb[0];
+          cb[0] = cb[1] = cb[2] = cb[3] = c0;
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) p.c[4 * g + r] = Chan{cs[r], bi[r], (int32_t)fl[r], cb[r]};
+      }
+    } else if (ca_rows) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        int32_t q[4];
+        load4(ca_rows, i0 + 8 * g, out.P, vec_ok, q);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) p.ca[4 * g + r] = q[r];
+      }
+    } else {
+#pragma unroll
+      for (int k = 0; k < 16; ++k) p.ca[k] = ca;
+    }
+    (void)ng;
+  }
+  __device__ __forceinline__ void load_j(PreJ& p, int j) const {
+    const int jj = clamp_index(j, out.Q);
+    if (w_on_i) p.ca = ca_rows ? ca_rows[jj] : ca;
+    else p.c = chan(jj);
+  }
+  static __device__ __forceinline__ int32_t exact(int32_t acc, const Chan& c, int32_t ca_v) {
+    uint32_t v = (uint32_t)acc + (uint32_t)ca_v * (uint32_t)c.cs;
+    if (c.fl) v = 0u - v;
+    v += (uint32_t)c.bi;
     return (int32_t)v;
   }
-  __device__ __forceinline__ int32_t requant(int32_t v, int i, int j) const {
+  __device__ __forceinline__ int32_t requant(int32_t v, float cs) const {
 #pragma clang fp contract(off)
-    const int ch = w_on_i ? i : j;
-    const float cs = comb[n_comb > 1 ? ch : 0];
     double d = (double)v * (double)cs;
     d = d + (double)y_zp;
     d = __builtin_rint(d);
@@ -154,67 +267,37 @@ struct QuantEpi {
     d = d > (double)hi ? (double)hi : d;
     return (int32_t)d;
   }
-  static constexpr int kStageBytes = 1;
-  __device__ __forceinline__ bool staged_ok(int bp) const {
-    return (out_kind == QOUT_U8 || out_kind == QOUT_I8) && vec && ((uintptr_t)y % 16 == 0) && (sj % 16 == 0) &&
-           (bstride == 0 || ohw % bp == 0);
-  }
-  __device__ __forceinline__ char* out_ptr(int i, int j) const { return reinterpret_cast<char*>(y) + index(i, j); }
-  __device__ __forceinline__ uint64_t pack4(int i0, int j, i32x4 acc) const {
-    uint64_t bits = 0;
+  template <class A>
+  __device__ __forceinline__ void finish(const PreI& pi, const PreJ& pj, int, int, A acc,
+                                         uint32_t (&bits)[16]) const {
+    int32_t v[16];
+    float cb[16];
+    if (w_on_i) {
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      int32_t v = 0;
-      if (j < Q && i0 + r < P) {
-        v = requant(exact(acc[r], i0 + r, j), i0 + r, j);
-        if (table) v = table[v & 0xff];
-      }
-      bits |= (uint64_t)(uint32_t)(v & 0xff) << (r * 8);
-    }
-    return bits;
-  }
-  __device__ __forceinline__ void store(int i0, int j, i32x4 acc) const {
-    if (j >= Q) return;
-    int32_t v[4];
+      for (int k = 0; k < 16; ++k) { v[k] = exact(acc[k], pi.c[k], pj.ca); cb[k] = pi.c[k].cb; }
+    } else {
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      v[r] = exact(acc[r], i0 + r, j);
-      if (out_kind != QOUT_I32) v[r] = requant(v[r], i0 + r, j);
+      for (int k = 0; k < 16; ++k) { v[k] = exact(acc[k], pj.c, pi.ca[k]); cb[k] = pj.c.cb; }
     }
+    if (out_kind == QOUT_I32) {
+#pragma unroll
+      for (int k = 0; k < 16; ++k) bits[k] = (uint32_t)v[k];
+      return;
+    }
+#pragma unroll
+    for (int k = 0; k < 16; ++k) v[k] = requant(v[k], cb[k]);
     if (out_kind == QOUT_F32) {
       // requantised lanes stored as f32, the reference Tensor's representation
-      float* yy = reinterpret_cast<float*>(y);
-      if (vec && i0 + 3 < P) {
-        *reinterpret_cast<f32x4*>(yy + index(i0, j)) = f32x4{(float)v[0], (float)v[1], (float)v[2], (float)v[3]};
-      } else {
 #pragma unroll
-        for (int r = 0; r < 4; ++r)
-          if (i0 + r < P) yy[index(i0 + r, j)] = (float)v[r];
-      }
-    } else if (out_kind == QOUT_I32) {
-      int32_t* yy = reinterpret_cast<int32_t*>(y);
-      if (vec && i0 + 3 < P) {
-        *reinterpret_cast<i32x4*>(yy + index(i0, j)) = i32x4{v[0], v[1], v[2], v[3]};
-      } else {
+      for (int k = 0; k < 16; ++k) bits[k] = __builtin_bit_cast(uint32_t, (float)v[k]);
+      return;
+    }
+    if (table) {
 #pragma unroll
-        for (int r = 0; r < 4; ++r)
-          if (i0 + r < P) yy[index(i0 + r, j)] = v[r];
-      }
+      for (int k = 0; k < 16; ++k) bits[k] = table[v[k] & 0xff];
     } else {
-      uint8_t* yy = reinterpret_cast<uint8_t*>(y);
-      if (table) {
 #pragma unroll
-        for (int r = 0; r < 4; ++r) v[r] = table[v[r] & 0xff];
-      }
-      if (vec && i0 + 3 < P) {
-        uint32_t packed = (uint32_t)(v[0] & 0xff) | ((uint32_t)(v[1] & 0xff) << 8) |
-                          ((uint32_t)(v[2] & 0xff) << 16) | ((uint32_t)(v[3] & 0xff) << 24);
-        *reinterpret_cast<uint32_t*>(yy + index(i0, j)) = packed;
-      } else {
-#pragma unroll
-        for (int r = 0; r < 4; ++r)
-          if (i0 + r < P) yy[index(i0 + r, j)] = (uint8_t)(v[r] & 0xff);
-      }
+      for (int k = 0; k < 16; ++k) bits[k] = (uint32_t)v[k] & 0xff;
     }
   }
 };
@@ -264,7 +347,7 @@ inline hipError_t launch_split(const LX& lx, const LY& ly, const Epi& epi, int P
   if (e != hipSuccess) return e;
   const int64_t groups = (int64_t)(Pp / 4) * Q;
   const unsigned grid = (unsigned)std::min<int64_t>((groups + 255) / 256, 65535 * 4);
-  hipLaunchKernelGGL((split_reduce_kernel<T, V, Epi>), dim3(grid), dim3(256), 0, st, reinterpret_cast<const T*>(ws),
+  hipLaunchKernelGGL((split_reduce_kernel<T, typename OpT<O>::Acc, Epi>), dim3(grid), dim3(256), 0, st, reinterpret_cast<const T*>(ws),
                      splits, P, Pp, Q, epi);
   return hipGetLastError();
 }
@@ -305,23 +388,44 @@ inline hipError_t launch_any(const LX& lx, const LY& ly, const Epi& epi, int P, 
   }
 }
 
+// OHIP_STAGE=0 turns the LDS-staged epilogue off (a measurement switch)
+inline int stage_allowed() {
+  static const int v = [] {
+    const char* e = std::getenv("OHIP_STAGE");
+    return (e && e[0] == '0') ? 0 : 1;
+  }();
+  return v;
+}
+
+inline OutAddr make_out_addr(const OutMap& o) {
+  OutAddr a;
+  a.stage = stage_allowed();
+  a.y = reinterpret_cast<char*>(o.y);
+  a.si = o.si; a.sj = o.sj; a.bstride = o.bstride; a.ohw = o.ohw > 0 ? o.ohw : 1;
+  magic_div(a.ohw, &a.ohw_mul, &a.ohw_shift);
+  a.P = o.P; a.Q = o.Q; a.vec = o.vec;
+  return a;
+}
+
 template <class OutT>
 inline FloatEpi<OutT> make_float_epi(const FloatOut& o) {
   FloatEpi<OutT> e;
-  e.y = reinterpret_cast<OutT*>(o.y);
-  e.si = o.si; e.sj = o.sj; e.bstride = o.bstride; e.ohw = o.ohw; e.P = o.P; e.Q = o.Q;
-  e.vec = o.vec; e.has_alpha = o.alpha != 1.0f; e.alpha = o.alpha; e.beta = o.beta;
+  e.out = make_out_addr(o);
+  e.alpha = o.alpha; e.beta = o.beta;
   e.bias = reinterpret_cast<const OutT*>(o.bias); e.bias_mode = o.bias ? o.bias_mode : BIAS_NONE;
+  e.bias_vec = ((uintptr_t)o.bias % 16) == 0;
   e.act = o.act; e.lo = o.lo; e.hi = o.hi;
   return e;
 }
 
 inline QuantEpi make_quant_epi(const QuantOut& o) {
   QuantEpi e;
-  e.y = o.y; e.si = o.si; e.sj = o.sj; e.bstride = o.bstride; e.ohw = o.ohw; e.P = o.P; e.Q = o.Q;
-  e.vec = o.vec; e.w_on_i = o.w_on_i; e.colsum = o.colsum; e.flip = o.flip; e.bias = o.bias; e.ca = o.ca;
+  e.out = make_out_addr(o);
+  e.w_on_i = o.w_on_i; e.colsum = o.colsum; e.flip = o.flip; e.bias = o.bias; e.ca = o.ca;
   e.ca_rows = o.ca_rows; e.comb = o.comb; e.n_comb = o.n_comb; e.out_kind = o.out_kind;
   e.y_zp = o.y_zp; e.lo = o.lo; e.hi = o.hi; e.table = o.table;
+  auto al = [](const void* p) { return ((uintptr_t)p % 16) == 0; };
+  e.vec_ok = al(o.colsum) && al(o.flip) && al(o.bias) && al(o.ca_rows) && al(o.comb);
   return e;
 }
 

@@ -295,6 +295,72 @@ template <bool XOR> __device__ __forceinline__ u32x4 frag(u32x4 v) {
 //   k-step 3 waits until stage kt + 1 has landed, passes the barrier and
 //   reads stage kt + 1's first fragments under its MFMAs,
 // so the MFMA pipe is never left waiting on a barrier with no work queued.
+// Where the outputs go: element (i, j) sits at
+//   (i / ohw) * bstride + (i % ohw) * si + j * sj      (elements of `eb` bytes)
+// with i / ohw computed as (i * ohw_mul) >> ohw_shift (exact for 0 <= i < 2^31,
+// magic_div below).  vec: si == 1 and every aligned run of four i is
+// contiguous and 4-element aligned in memory.
+struct OutAddr {
+  char* y;
+  int64_t si, sj, bstride;
+  int ohw;
+  uint32_t ohw_mul;
+  int ohw_shift;
+  int P, Q;
+  int vec;
+  int stage;   // the staged epilogue may be used
+  __device__ __forceinline__ int64_t row(int i) const {
+    if (bstride == 0) return (int64_t)i * si;
+    const int n = (int)(((uint64_t)(uint32_t)i * ohw_mul) >> ohw_shift);
+    return (int64_t)n * bstride + (int64_t)(i - n * ohw) * si;
+  }
+};
+
+// Division by an invariant d >= 1 for dividends below 2^31: with
+// s = ceil(log2 d) and m = ceil(2^(31+s) / d) (which fits 32 bits),
+// floor(i * m / 2^(31+s)) == floor(i / d), because the rounding excess of m
+// contributes less than i / 2^(31+s) * d / d < 2^-s <= 1/d.
+inline void magic_div(int d, uint32_t* mul, int* shift) {
+  int s = 0;
+  while ((1ll << s) < d) ++s;
+  const unsigned __int128 num = (unsigned __int128)1 << (31 + s);
+  *mul = (uint32_t)((num + (unsigned)d - 1) / (unsigned)d);
+  *shift = 31 + s;
+}
+
+// Stores `ng` groups of four outputs (rows i0 + 8g .. +3, column j) whose bit
+// patterns are bits[4g + r]; rows[g] = out.row(i0 + 8g).
+__device__ __forceinline__ void store_tile(const OutAddr& out, int eb, const int64_t* rows, int i0, int j,
+                                           const uint32_t (&bits)[16], int ng) {
+  if (j >= out.Q) return;
+  const int64_t cj = (int64_t)j * out.sj;
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    if (g >= ng) break;
+    const int ig = i0 + 8 * g;
+    const uint32_t* v = bits + 4 * g;
+    if (out.vec && ig + 3 < out.P) {
+      char* dst = out.y + (rows[g] + cj) * eb;
+      if (eb == 4) *reinterpret_cast<u32x4*>(dst) = u32x4{v[0], v[1], v[2], v[3]};
+      else if (eb == 2) {
+        typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+        *reinterpret_cast<u32x2*>(dst) = u32x2{v[0] | (v[1] << 16), v[2] | (v[3] << 16)};
+      } else {
+        *reinterpret_cast<uint32_t*>(dst) = v[0] | (v[1] << 8) | (v[2] << 16) | (v[3] << 24);
+      }
+    } else {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        if (ig + r >= out.P) break;
+        char* dst = out.y + (out.row(ig + r) + cj) * eb;
+        if (eb == 4) *reinterpret_cast<uint32_t*>(dst) = v[r];
+        else if (eb == 2) *reinterpret_cast<uint16_t*>(dst) = (uint16_t)v[r];
+        else *reinterpret_cast<uint8_t*>(dst) = (uint8_t)v[r];
+      }
+    }
+  }
+}
+
 template <Op O, class Tl, class LX, class LY, class Epi, bool XX, bool XY>
 __global__ void __launch_bounds__(Tl::kThreads)
 mfma_gemm_kernel(const LX lx, const LY ly, const Epi epi, int nP, int nQ, int kc, int splits) {
@@ -398,65 +464,99 @@ mfma_gemm_kernel(const LX lx, const LY ly, const Epi epi, int nP, int nQ, int kc
 
   const int ibase = p0 + wp * Tl::TP * 32 + (lane >> 5) * 4;
   const int jbase = q0 + wq * Tl::TQ * 32 + (lane & 31);
+  const OutAddr out = epi.addr();
+
+  // the per-column epilogue terms, loaded once for all of this lane's rows
+  typename Epi::PreJ pj[Tl::TQ];
+#pragma unroll
+  for (int b = 0; b < Tl::TQ; ++b) epi.load_j(pj[b], jbase + b * 32);
 
   // Staged epilogue: the block's outputs go through LDS (the stage buffers
   // are free once the last loads have landed) and leave as whole 16-byte
   // chunks of output rows, instead of 4-element pieces of 32 rows per store.
   // Staged row `lj` holds outputs (p0.., q0 + lj); its 16-byte chunk c sits
   // at slot c ^ (lj % CPR) so the fragment writes spread over the banks.
-  if constexpr (Epi::kStageBytes > 0) {
-    constexpr int EB = Epi::kStageBytes;
-    constexpr int CPR = Tl::BP * EB / 16;   // 16-byte chunks per staged row
-    constexpr int EPC = 16 / EB;            // outputs per chunk
-    static_assert(Tl::BQ * Tl::BP * EB <= Tl::STAGES * Tl::kStage * 16, "staging must fit the stage buffers");
-    if (epi.staged_ok(Tl::BP)) {
-      wait_vmcnt<0>();
-      wait_lgkm0();
-      barrier_only();
-      char* stg = reinterpret_cast<char*>(smem);
-      auto put = [&](int abg) {
-        const int g = abg & 3, ab = abg >> 2;
-        const int a = ab / Tl::TQ, b = ab % Tl::TQ;
-        const int i0 = ibase + a * 32 + 8 * g, j = jbase + b * 32;
-        O4 v;
+  constexpr int EB = Epi::kStageBytes > 0 ? Epi::kStageBytes : 1;
+  constexpr int CPR = Tl::BP * EB / 16;   // 16-byte chunks per staged row
+  constexpr int EPC = 16 / EB;            // outputs per chunk
+  static_assert(Epi::kStageBytes == 0 || Tl::BQ * Tl::BP * EB <= Tl::STAGES * Tl::kStage * 16,
+                "staging must fit the stage buffers");
+  char* stg = reinterpret_cast<char*>(smem);
+  bool staged = false;
+  if constexpr (Epi::kStageBytes > 0) staged = epi.staged_ok(Tl::BP);
+  if (staged) {
+    wait_vmcnt<0>();
+    wait_lgkm0();
+    barrier_only();
+  }
+
+  // Every 32x32 tile of the lane is finished once (16 output bit patterns)
+  // and then either staged or stored; the finishing code holds its branches
+  // outside the element loops, so the epilogue stays short.
 #pragma unroll
-        for (int e = 0; e < 4; ++e) v[e] = acc[a][b][4 * g + e];
-        const uint64_t bits = epi.pack4(i0, j, v);
-        const int li = i0 - p0, lj = j - q0;
-        const int byte = li * EB;
-        char* dst = stg + lj * (Tl::BP * EB) + (((byte >> 4) ^ (lj & (CPR - 1))) << 4) + (byte & 15);
-        if constexpr (EB == 2) *reinterpret_cast<uint64_t*>(dst) = bits;
-        else *reinterpret_cast<uint32_t*>(dst) = (uint32_t)bits;
-      };
-      Unroll<0, Tl::TP * Tl::TQ * 4>::run(put);
+  for (int a = 0; a < Tl::TP; ++a) {
+    const int i0 = ibase + a * 32;
+    typename Epi::PreI pi;
+    epi.load_i(pi, i0, 4);
+    int64_t rows[4];
+    if (!staged) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) rows[g] = out.row(i0 + 8 * g);
+    }
+#pragma unroll
+    for (int b = 0; b < Tl::TQ; ++b) {
+      const int j = jbase + b * 32;
+      uint32_t bits[16];
+      epi.finish(pi, pj[b], i0, j, acc[a][b], bits);
+      if constexpr (Epi::kStageBytes > 0) {
+        if (staged) {
+          const int lj = j - q0;
+#pragma unroll
+          for (int g = 0; g < 4; ++g) {
+            const int byte = (i0 + 8 * g - p0) * EB;
+            char* dst = stg + lj * (Tl::BP * EB) + (((byte >> 4) ^ (lj & (CPR - 1))) << 4) + (byte & 15);
+            if constexpr (EB == 2) {
+              *reinterpret_cast<uint32_t*>(dst) = bits[4 * g] | (bits[4 * g + 1] << 16);
+              *reinterpret_cast<uint32_t*>(dst + 4) = bits[4 * g + 2] | (bits[4 * g + 3] << 16);
+            } else {
+              *reinterpret_cast<uint32_t*>(dst) =
+                  bits[4 * g] | (bits[4 * g + 1] << 8) | (bits[4 * g + 2] << 16) | (bits[4 * g + 3] << 24);
+            }
+          }
+          continue;
+        }
+      }
+      store_tile(out, epi.out_bytes(), rows, i0, j, bits, 4);
+    }
+  }
+
+  if constexpr (Epi::kStageBytes > 0) {
+    if (staged) {
       wait_lgkm0();
       barrier_only();
       for (int c = t; c < Tl::BQ * CPR; c += Tl::kThreads) {
         const int row = c / CPR, cc = c - row * CPR;
         const int j = q0 + row, i = p0 + cc * EPC;
-        if (j >= epi.Q || i >= epi.P) continue;
+        if (j >= out.Q || i >= out.P) continue;
         const u32x4 v = *reinterpret_cast<const u32x4*>(stg + row * (Tl::BP * EB) + ((cc ^ (row & (CPR - 1))) << 4));
-        if (i + EPC <= epi.P) {
-          *reinterpret_cast<u32x4*>(epi.out_ptr(i, j)) = v;
+        char* dst = out.y + (out.row(i) + (int64_t)j * out.sj) * EB;
+        if (i + EPC <= out.P) {
+          *reinterpret_cast<u32x4*>(dst) = v;
         } else {
-          const uint8_t* bytes = reinterpret_cast<const uint8_t*>(&v);
-          for (int e = 0; e < EPC && i + e < epi.P; ++e)
-            for (int k = 0; k < EB; ++k) epi.out_ptr(i + e, j)[k] = (char)bytes[e * EB + k];
+          // the row's last, partial chunk: its bytes one at a time (shifts,
+          // not a dynamically indexed copy of v, which would live in memory)
+          const int nbytes = (out.P - i) * EB;
+#pragma unroll
+          for (int w = 0; w < 4; ++w) {
+            const uint32_t word = v[w];
+#pragma unroll
+            for (int b = 0; b < 4; ++b)
+              if (4 * w + b < nbytes) dst[4 * w + b] = (char)(word >> (8 * b));
+          }
         }
       }
-      return;
     }
   }
-
-  auto out = [&](int abg) {
-    const int g = abg & 3, ab = abg >> 2;
-    const int a = ab / Tl::TQ, b = ab % Tl::TQ;
-    O4 v;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) v[e] = acc[a][b][4 * g + e];
-    epi.store(ibase + a * 32 + 8 * g, jbase + b * 32, v);
-  };
-  Unroll<0, Tl::TP * Tl::TQ * 4>::run(out);
 }
 
 // Split-K: slice s of the K loop stores its raw accumulators (f32, or i32
@@ -466,23 +566,48 @@ template <class T> struct PartialEpi {
   T* ws;
   int P, Pp, Q;
   static constexpr int kStageBytes = 0;
-  template <class V> __device__ __forceinline__ void store(int i0, int j, V v) const {
-    if (j >= Q || i0 >= P) return;
-    T* dst = ws + ((int64_t)blockIdx.y * Q + j) * Pp + i0;
-    *reinterpret_cast<V*>(dst) = v;
+  struct PreI {};
+  struct PreJ {};
+  __device__ __forceinline__ void load_i(PreI&, int, int) const {}
+  __device__ __forceinline__ void load_j(PreJ&, int) const {}
+  __device__ __forceinline__ int out_bytes() const { return 4; }
+  __device__ __forceinline__ OutAddr addr() const {
+    OutAddr o{};
+    o.y = reinterpret_cast<char*>(ws + (int64_t)blockIdx.y * Q * Pp);
+    o.si = 1; o.sj = Pp; o.bstride = 0; o.ohw = 1; o.P = P; o.Q = Q; o.vec = 1;
+    return o;
+  }
+  template <class A>
+  __device__ __forceinline__ void finish(const PreI&, const PreJ&, int, int, A acc, uint32_t (&bits)[16]) const {
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+      const auto e = acc[k];   // by value: a bit_cast of the element expression itself reads lane 0
+      bits[k] = __builtin_bit_cast(uint32_t, e);
+    }
   }
 };
 
-template <class T, class V, class Epi>
+template <class T, class A, class Epi>
 __global__ void __launch_bounds__(256) split_reduce_kernel(const T* __restrict__ ws, int splits, int P, int Pp, int Q,
                                                            const Epi epi) {
+  typedef T T4 __attribute__((ext_vector_type(4)));
   const int groups = Pp / 4;
   const int64_t n = (int64_t)groups * Q;
+  const OutAddr out = epi.addr();
   for (int64_t g = (int64_t)blockIdx.x * 256 + threadIdx.x; g < n; g += (int64_t)gridDim.x * 256) {
     const int j = (int)(g / groups), i0 = (int)(g - (int64_t)j * groups) * 4;
-    V acc = *reinterpret_cast<const V*>(ws + (int64_t)j * Pp + i0);
-    for (int s = 1; s < splits; ++s) acc += *reinterpret_cast<const V*>(ws + ((int64_t)s * Q + j) * Pp + i0);
-    epi.store(i0, j, acc);
+    typename Epi::PreI pi;
+    typename Epi::PreJ pj;
+    epi.load_i(pi, i0, 1);
+    epi.load_j(pj, j);
+    T4 sum = *reinterpret_cast<const T4*>(ws + (int64_t)j * Pp + i0);
+    for (int s = 1; s < splits; ++s) sum += *reinterpret_cast<const T4*>(ws + ((int64_t)s * Q + j) * Pp + i0);
+    A acc = {};
+    acc[0] = sum[0]; acc[1] = sum[1]; acc[2] = sum[2]; acc[3] = sum[3];
+    uint32_t bits[16];
+    epi.finish(pi, pj, i0, j, acc, bits);
+    int64_t rows[4] = {out.row(i0), 0, 0, 0};
+    store_tile(out, epi.out_bytes(), rows, i0, j, bits, 1);
   }
 }
 
