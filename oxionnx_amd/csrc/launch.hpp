@@ -26,13 +26,12 @@ __device__ __forceinline__ float activate(float v, int act, float lo, float hi) 
 }
 
 // Both epilogues read their per-position parameters (biases, column sums,
-// scales) in two batches before any output is formed: PreI for the sixteen
-// i positions i0 + 8g + r (g, r < 4) of a 32-row MFMA tile, PreJ for one j.
-// Each batch is a run of independent loads with a single wait.  finish()
-// then turns the tile's sixteen accumulators into output bit patterns with
-// its mode switches outside the element loops: the epilogue runs once per
-// block, and a per-element branch tree there costs more instruction fetch
-// than a short K loop costs MFMA time.
+// scales) in batches before any output is formed: PreI for a group of four
+// consecutive i positions (one vector load per array where aligned), PreJ
+// for one j.  finish() then turns the group's four accumulators into output
+// bit patterns with its mode switches outside the element loops: the
+// epilogue runs once per block, and a per-element branch tree there costs
+// more than a short K loop costs MFMA time.
 
 // an index clamped into [0, n): positions past the edge read a valid element
 // whose value is then discarded
@@ -89,30 +88,19 @@ template <class OutT> struct FloatEpi {
            (out.bstride == 0 || out.ohw % bp == 0);
   }
 
-  struct PreI { float b[16]; };   // beta * bias per row (BIAS_I, BIAS_SCALAR), else -0
+  struct PreI { float b[4]; };    // beta * bias per row (BIAS_I, BIAS_SCALAR), else -0
   struct PreJ { float b; };       // beta * bias per column (BIAS_J), else -0
-  __device__ __forceinline__ void load_i(PreI& p, int i0, int ng) const {
+  __device__ __forceinline__ void load_i(PreI& p, int i) const {
 #pragma clang fp contract(off)
     if (bias_mode == BIAS_I) {
-      // unconditional loads at clamped (in-range) positions, selected
-      // afterwards: the sixteen loads issue back to back under one wait
-      OutT raw[16];
+      OutT raw[4];
+      load4(bias, i, out.P, bias_vec, raw);
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        OutT q[4];
-        load4(bias, i0 + 8 * g, out.P, bias_vec, q);
-#pragma unroll
-        for (int r = 0; r < 4; ++r) raw[4 * g + r] = q[r];
-      }
-#pragma unroll
-      for (int k = 0; k < 16; ++k) {
-        const int i = i0 + 8 * (k >> 2) + (k & 3);
-        p.b[k] = ((k >> 2) < ng && i < out.P) ? beta * to_f32(raw[k]) : 0.0f;
-      }
+      for (int r = 0; r < 4; ++r) p.b[r] = i + r < out.P ? beta * to_f32(raw[r]) : 0.0f;
     } else {
       const float s = bias_mode == BIAS_SCALAR ? beta * to_f32(bias[0]) : -0.0f;
 #pragma unroll
-      for (int k = 0; k < 16; ++k) p.b[k] = s;
+      for (int r = 0; r < 4; ++r) p.b[r] = s;
     }
   }
   __device__ __forceinline__ void load_j(PreJ& p, int j) const {
@@ -125,44 +113,43 @@ template <class OutT> struct FloatEpi {
     }
   }
   template <class A>
-  __device__ __forceinline__ void finish(const PreI& pi, const PreJ& pj, int i0, int j, A acc,
-                                         uint32_t (&bits)[16]) const {
+  __device__ __forceinline__ void finish(const PreI& pi, const PreJ& pj, int i, int j, A acc,
+                                         uint32_t (&bits)[4]) const {
 #pragma clang fp contract(off)
-    float v[16];
+    float v[4];
 #pragma unroll
-    for (int k = 0; k < 16; ++k) v[k] = acc[k] * alpha;
+    for (int r = 0; r < 4; ++r) v[r] = acc[r] * alpha;
 #pragma unroll
-    for (int k = 0; k < 16; ++k) v[k] = v[k] + (pi.b[k] + pj.b);
+    for (int r = 0; r < 4; ++r) v[r] = v[r] + (pi.b[r] + pj.b);
     if (bias_mode == BIAS_FULL_JI) {
-      OutT c[16];
+      OutT c[4];
       const int64_t cj = (int64_t)clamp_index(j, out.Q) * out.P;
 #pragma unroll
-      for (int k = 0; k < 16; ++k) c[k] = bias[cj + clamp_index(i0 + 8 * (k >> 2) + (k & 3), out.P)];
+      for (int r = 0; r < 4; ++r) c[r] = bias[cj + clamp_index(i + r, out.P)];
 #pragma unroll
-      for (int k = 0; k < 16; ++k) v[k] = v[k] + beta * to_f32(c[k]);
+      for (int r = 0; r < 4; ++r) v[r] = v[r] + beta * to_f32(c[r]);
     }
     if (act == ACT_RELU) {
 #pragma unroll
-      for (int k = 0; k < 16; ++k) v[k] = v[k] > 0.0f ? v[k] : 0.0f;   // f32::max(NaN, 0) == 0
+      for (int r = 0; r < 4; ++r) v[r] = v[r] > 0.0f ? v[r] : 0.0f;   // f32::max(NaN, 0) == 0
     } else if (act == ACT_CLIP) {
 #pragma unroll
-      for (int k = 0; k < 16; ++k) v[k] = v[k] < lo ? lo : (v[k] > hi ? hi : v[k]);
+      for (int r = 0; r < 4; ++r) v[r] = v[r] < lo ? lo : (v[r] > hi ? hi : v[r]);
     } else if (act == ACT_LEAKY_RELU) {
 #pragma unroll
-      for (int k = 0; k < 16; ++k) v[k] = v[k] >= 0.0f ? v[k] : v[k] * lo;
+      for (int r = 0; r < 4; ++r) v[r] = v[r] >= 0.0f ? v[r] : v[r] * lo;
     }
 #pragma unroll
-    for (int k = 0; k < 16; ++k) bits[k] = out_bits(from_f32<OutT>(v[k]));
+    for (int r = 0; r < 4; ++r) bits[r] = out_bits(from_f32<OutT>(v[r]));
   }
   // one output of a reduction that has no MFMA tile (the GEMV path)
   __device__ __forceinline__ void store_one(float acc, int i, int j) const {
     PreI pi;
     PreJ pj;
-    load_i(pi, i, 1);
+    load_i(pi, i);
     load_j(pj, j);
-    f32x16 a = {};
-    a[0] = acc;
-    uint32_t bits[16];
+    f32x4 a = {acc, 0.0f, 0.0f, 0.0f};
+    uint32_t bits[4];
     finish(pi, pj, i, j, a, bits);
     OutT* dst = reinterpret_cast<OutT*>(out.y) + out.row(i) + (int64_t)j * out.sj;
     *dst = __builtin_bit_cast(OutT, (typename std::conditional<sizeof(OutT) == 2, uint16_t, uint32_t>::type)bits[0]);
@@ -202,8 +189,6 @@ struct QuantEpi {
   // per-channel terms of a weight channel, and the correction factor of an
   // activation row
   struct Chan { int32_t cs, bi, fl; float cb; };
-  struct PreI { Chan c[16]; int32_t ca[16]; };
-  struct PreJ { Chan c; int32_t ca; };
   // ch must be in range (callers clamp); the loads carry no branch
   __device__ __forceinline__ Chan chan(int ch) const {
     Chan c;
@@ -213,39 +198,30 @@ struct QuantEpi {
     c.cb = comb[n_comb > 1 ? ch : 0];
     return c;
   }
-  __device__ __forceinline__ void load_i(PreI& p, int i0, int ng) const {
+  struct PreI { Chan c[4]; int32_t ca[4]; };   // c when w_on_i, else ca
+  struct PreJ { Chan c; int32_t ca; };         // ca when w_on_i, else c
+  __device__ __forceinline__ void load_i(PreI& p, int i) const {
     if (w_on_i) {
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const int i = i0 + 8 * g;
-        int32_t cs[4], bi[4] = {0, 0, 0, 0};
-        int8_t fl[4] = {0, 0, 0, 0};
-        float cb[4];
-        load4(colsum, i, out.P, vec_ok, cs);
-        if (bias) load4(bias, i, out.P, vec_ok, bi);
-        if (flip) load4(flip, i, out.P, vec_ok, fl);
-        if (n_comb > 1) {
-          load4(comb, i, out.P, vec_ok, cb);
-        } else {
-          const float c0 = comb[0];
-          cb[0] = cb[1] = cb[2] = cb[3] = c0;
-        }
-#pragma unroll
-        for (int r = 0; r < 4; ++r) p.c[4 * g + r] = Chan{cs[r], bi[r], (int32_t)fl[r], cb[r]};
+      int32_t cs[4], bi[4] = {0, 0, 0, 0};
+      int8_t fl[4] = {0, 0, 0, 0};
+      float cb[4];
+      load4(colsum, i, out.P, vec_ok, cs);
+      if (bias) load4(bias, i, out.P, vec_ok, bi);
+      if (flip) load4(flip, i, out.P, vec_ok, fl);
+      if (n_comb > 1) {
+        load4(comb, i, out.P, vec_ok, cb);
+      } else {
+        const float c0 = comb[0];
+        cb[0] = cb[1] = cb[2] = cb[3] = c0;
       }
+#pragma unroll
+      for (int r = 0; r < 4; ++r) p.c[r] = Chan{cs[r], bi[r], (int32_t)fl[r], cb[r]};
     } else if (ca_rows) {
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        int32_t q[4];
-        load4(ca_rows, i0 + 8 * g, out.P, vec_ok, q);
-#pragma unroll
-        for (int r = 0; r < 4; ++r) p.ca[4 * g + r] = q[r];
-      }
+      load4(ca_rows, i, out.P, vec_ok, p.ca);
     } else {
 #pragma unroll
-      for (int k = 0; k < 16; ++k) p.ca[k] = ca;
+      for (int r = 0; r < 4; ++r) p.ca[r] = ca;
     }
-    (void)ng;
   }
   __device__ __forceinline__ void load_j(PreJ& p, int j) const {
     const int jj = clamp_index(j, out.Q);
@@ -269,35 +245,35 @@ struct QuantEpi {
   }
   template <class A>
   __device__ __forceinline__ void finish(const PreI& pi, const PreJ& pj, int, int, A acc,
-                                         uint32_t (&bits)[16]) const {
-    int32_t v[16];
-    float cb[16];
+                                         uint32_t (&bits)[4]) const {
+    int32_t v[4];
+    float cb[4];
     if (w_on_i) {
 #pragma unroll
-      for (int k = 0; k < 16; ++k) { v[k] = exact(acc[k], pi.c[k], pj.ca); cb[k] = pi.c[k].cb; }
+      for (int r = 0; r < 4; ++r) { v[r] = exact(acc[r], pi.c[r], pj.ca); cb[r] = pi.c[r].cb; }
     } else {
 #pragma unroll
-      for (int k = 0; k < 16; ++k) { v[k] = exact(acc[k], pj.c, pi.ca[k]); cb[k] = pj.c.cb; }
+      for (int r = 0; r < 4; ++r) { v[r] = exact(acc[r], pj.c, pi.ca[r]); cb[r] = pj.c.cb; }
     }
     if (out_kind == QOUT_I32) {
 #pragma unroll
-      for (int k = 0; k < 16; ++k) bits[k] = (uint32_t)v[k];
+      for (int r = 0; r < 4; ++r) bits[r] = (uint32_t)v[r];
       return;
     }
 #pragma unroll
-    for (int k = 0; k < 16; ++k) v[k] = requant(v[k], cb[k]);
+    for (int r = 0; r < 4; ++r) v[r] = requant(v[r], cb[r]);
     if (out_kind == QOUT_F32) {
       // requantised lanes stored as f32, the reference Tensor's representation
 #pragma unroll
-      for (int k = 0; k < 16; ++k) bits[k] = __builtin_bit_cast(uint32_t, (float)v[k]);
+      for (int r = 0; r < 4; ++r) bits[r] = __builtin_bit_cast(uint32_t, (float)v[r]);
       return;
     }
     if (table) {
 #pragma unroll
-      for (int k = 0; k < 16; ++k) bits[k] = table[v[k] & 0xff];
+      for (int r = 0; r < 4; ++r) bits[r] = table[v[r] & 0xff];
     } else {
 #pragma unroll
-      for (int k = 0; k < 16; ++k) bits[k] = (uint32_t)v[k] & 0xff;
+      for (int r = 0; r < 4; ++r) bits[r] = (uint32_t)v[r] & 0xff;
     }
   }
 };
@@ -347,7 +323,7 @@ inline hipError_t launch_split(const LX& lx, const LY& ly, const Epi& epi, int P
   if (e != hipSuccess) return e;
   const int64_t groups = (int64_t)(Pp / 4) * Q;
   const unsigned grid = (unsigned)std::min<int64_t>((groups + 255) / 256, 65535 * 4);
-  hipLaunchKernelGGL((split_reduce_kernel<T, typename OpT<O>::Acc, Epi>), dim3(grid), dim3(256), 0, st, reinterpret_cast<const T*>(ws),
+  hipLaunchKernelGGL((split_reduce_kernel<T, V, Epi>), dim3(grid), dim3(256), 0, st, reinterpret_cast<const T*>(ws),
                      splits, P, Pp, Q, epi);
   return hipGetLastError();
 }

@@ -328,36 +328,31 @@ inline void magic_div(int d, uint32_t* mul, int* shift) {
   *shift = 31 + s;
 }
 
-// Stores `ng` groups of four outputs (rows i0 + 8g .. +3, column j) whose bit
-// patterns are bits[4g + r]; rows[g] = out.row(i0 + 8g).
-__device__ __forceinline__ void store_tile(const OutAddr& out, int eb, const int64_t* rows, int i0, int j,
-                                           const uint32_t (&bits)[16], int ng) {
+// Stores the four outputs (rows i .. i+3, column j) whose bit patterns are
+// bits[r]; row = out.row(i).
+__device__ __forceinline__ void store_group(const OutAddr& out, int eb, int64_t row, int i, int j,
+                                            const uint32_t (&v)[4]) {
   if (j >= out.Q) return;
   const int64_t cj = (int64_t)j * out.sj;
-#pragma unroll
-  for (int g = 0; g < 4; ++g) {
-    if (g >= ng) break;
-    const int ig = i0 + 8 * g;
-    const uint32_t* v = bits + 4 * g;
-    if (out.vec && ig + 3 < out.P) {
-      char* dst = out.y + (rows[g] + cj) * eb;
-      if (eb == 4) *reinterpret_cast<u32x4*>(dst) = u32x4{v[0], v[1], v[2], v[3]};
-      else if (eb == 2) {
-        typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-        *reinterpret_cast<u32x2*>(dst) = u32x2{v[0] | (v[1] << 16), v[2] | (v[3] << 16)};
-      } else {
-        *reinterpret_cast<uint32_t*>(dst) = v[0] | (v[1] << 8) | (v[2] << 16) | (v[3] << 24);
-      }
+  if (out.vec && i + 3 < out.P) {
+    char* dst = out.y + (row + cj) * eb;
+    if (eb == 4) {
+      *reinterpret_cast<u32x4*>(dst) = u32x4{v[0], v[1], v[2], v[3]};
+    } else if (eb == 2) {
+      typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+      *reinterpret_cast<u32x2*>(dst) = u32x2{v[0] | (v[1] << 16), v[2] | (v[3] << 16)};
     } else {
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        if (ig + r >= out.P) break;
-        char* dst = out.y + (out.row(ig + r) + cj) * eb;
-        if (eb == 4) *reinterpret_cast<uint32_t*>(dst) = v[r];
-        else if (eb == 2) *reinterpret_cast<uint16_t*>(dst) = (uint16_t)v[r];
-        else *reinterpret_cast<uint8_t*>(dst) = (uint8_t)v[r];
-      }
+      *reinterpret_cast<uint32_t*>(dst) = v[0] | (v[1] << 8) | (v[2] << 16) | (v[3] << 24);
     }
+    return;
+  }
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    if (i + r >= out.P) break;
+    char* dst = out.y + (out.row(i + r) + cj) * eb;
+    if (eb == 4) *reinterpret_cast<uint32_t*>(dst) = v[r];
+    else if (eb == 2) *reinterpret_cast<uint16_t*>(dst) = (uint16_t)v[r];
+    else *reinterpret_cast<uint8_t*>(dst) = (uint8_t)v[r];
   }
 }
 
@@ -365,7 +360,7 @@ template <Op O, class Tl, class LX, class LY, class Epi, bool XX, bool XY>
 __global__ void __launch_bounds__(Tl::kThreads)
 mfma_gemm_kernel(const LX lx, const LY ly, const Epi epi, int nP, int nQ, int kc, int splits) {
   using A = typename OpT<O>::Acc;
-  using O4 = typename OpT<O>::Out4;
+  using A4 = typename OpT<O>::Out4;
   __shared__ u32x4 smem[Tl::STAGES * Tl::kStage];
   const int t = threadIdx.x;
   const int lane = t & 63;
@@ -490,43 +485,44 @@ mfma_gemm_kernel(const LX lx, const LY ly, const Epi epi, int nP, int nQ, int kc
     barrier_only();
   }
 
-  // Every 32x32 tile of the lane is finished once (16 output bit patterns)
-  // and then either staged or stored; the finishing code holds its branches
-  // outside the element loops, so the epilogue stays short.
+  // The lane's outputs are finished one group at a time (rows i0 + 8g .. +3
+  // of every column b): the group's row terms are loaded, its four outputs per
+  // column turned into bit patterns and staged or stored.  Working a group at
+  // a time keeps the epilogue's live registers to a few per column, so the
+  // epilogue does not set the kernel's register count (and occupancy).
 #pragma unroll
   for (int a = 0; a < Tl::TP; ++a) {
-    const int i0 = ibase + a * 32;
-    typename Epi::PreI pi;
-    epi.load_i(pi, i0, 4);
-    int64_t rows[4];
-    if (!staged) {
 #pragma unroll
-      for (int g = 0; g < 4; ++g) rows[g] = out.row(i0 + 8 * g);
-    }
+    for (int g = 0; g < 4; ++g) {
+      const int ig = ibase + a * 32 + 8 * g;
+      typename Epi::PreI pi;
+      epi.load_i(pi, ig);
+      int64_t row = 0;
+      if (!staged) row = out.row(ig);
 #pragma unroll
-    for (int b = 0; b < Tl::TQ; ++b) {
-      const int j = jbase + b * 32;
-      uint32_t bits[16];
-      epi.finish(pi, pj[b], i0, j, acc[a][b], bits);
-      if constexpr (Epi::kStageBytes > 0) {
-        if (staged) {
-          const int lj = j - q0;
+      for (int b = 0; b < Tl::TQ; ++b) {
+        const int j = jbase + b * 32;
+        A4 v;
 #pragma unroll
-          for (int g = 0; g < 4; ++g) {
-            const int byte = (i0 + 8 * g - p0) * EB;
+        for (int e = 0; e < 4; ++e) v[e] = acc[a][b][4 * g + e];
+        uint32_t bits[4];
+        epi.finish(pi, pj[b], ig, j, v, bits);
+        if constexpr (Epi::kStageBytes > 0) {
+          if (staged) {
+            const int lj = j - q0;
+            const int byte = (ig - p0) * EB;
             char* dst = stg + lj * (Tl::BP * EB) + (((byte >> 4) ^ (lj & (CPR - 1))) << 4) + (byte & 15);
             if constexpr (EB == 2) {
-              *reinterpret_cast<uint32_t*>(dst) = bits[4 * g] | (bits[4 * g + 1] << 16);
-              *reinterpret_cast<uint32_t*>(dst + 4) = bits[4 * g + 2] | (bits[4 * g + 3] << 16);
+              typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+              *reinterpret_cast<u32x2*>(dst) = u32x2{bits[0] | (bits[1] << 16), bits[2] | (bits[3] << 16)};
             } else {
-              *reinterpret_cast<uint32_t*>(dst) =
-                  bits[4 * g] | (bits[4 * g + 1] << 8) | (bits[4 * g + 2] << 16) | (bits[4 * g + 3] << 24);
+              *reinterpret_cast<uint32_t*>(dst) = bits[0] | (bits[1] << 8) | (bits[2] << 16) | (bits[3] << 24);
             }
+            continue;
           }
-          continue;
         }
+        store_group(out, epi.out_bytes(), row, ig, j, bits);
       }
-      store_tile(out, epi.out_bytes(), rows, i0, j, bits, 4);
     }
   }
 
@@ -568,7 +564,7 @@ template <class T> struct PartialEpi {
   static constexpr int kStageBytes = 0;
   struct PreI {};
   struct PreJ {};
-  __device__ __forceinline__ void load_i(PreI&, int, int) const {}
+  __device__ __forceinline__ void load_i(PreI&, int) const {}
   __device__ __forceinline__ void load_j(PreJ&, int) const {}
   __device__ __forceinline__ int out_bytes() const { return 4; }
   __device__ __forceinline__ OutAddr addr() const {
@@ -578,9 +574,9 @@ template <class T> struct PartialEpi {
     return o;
   }
   template <class A>
-  __device__ __forceinline__ void finish(const PreI&, const PreJ&, int, int, A acc, uint32_t (&bits)[16]) const {
+  __device__ __forceinline__ void finish(const PreI&, const PreJ&, int, int, A acc, uint32_t (&bits)[4]) const {
 #pragma unroll
-    for (int k = 0; k < 16; ++k) {
+    for (int k = 0; k < 4; ++k) {
       const auto e = acc[k];   // by value: a bit_cast of the element expression itself reads lane 0
       bits[k] = __builtin_bit_cast(uint32_t, e);
     }
@@ -590,7 +586,6 @@ template <class T> struct PartialEpi {
 template <class T, class A, class Epi>
 __global__ void __launch_bounds__(256) split_reduce_kernel(const T* __restrict__ ws, int splits, int P, int Pp, int Q,
                                                            const Epi epi) {
-  typedef T T4 __attribute__((ext_vector_type(4)));
   const int groups = Pp / 4;
   const int64_t n = (int64_t)groups * Q;
   const OutAddr out = epi.addr();
@@ -598,16 +593,13 @@ __global__ void __launch_bounds__(256) split_reduce_kernel(const T* __restrict__
     const int j = (int)(g / groups), i0 = (int)(g - (int64_t)j * groups) * 4;
     typename Epi::PreI pi;
     typename Epi::PreJ pj;
-    epi.load_i(pi, i0, 1);
+    epi.load_i(pi, i0);
     epi.load_j(pj, j);
-    T4 sum = *reinterpret_cast<const T4*>(ws + (int64_t)j * Pp + i0);
-    for (int s = 1; s < splits; ++s) sum += *reinterpret_cast<const T4*>(ws + ((int64_t)s * Q + j) * Pp + i0);
-    A acc = {};
-    acc[0] = sum[0]; acc[1] = sum[1]; acc[2] = sum[2]; acc[3] = sum[3];
-    uint32_t bits[16];
+    A acc = *reinterpret_cast<const A*>(ws + (int64_t)j * Pp + i0);
+    for (int s = 1; s < splits; ++s) acc += *reinterpret_cast<const A*>(ws + ((int64_t)s * Q + j) * Pp + i0);
+    uint32_t bits[4];
     epi.finish(pi, pj, i0, j, acc, bits);
-    int64_t rows[4] = {out.row(i0), 0, 0, 0};
-    store_tile(out, epi.out_bytes(), rows, i0, j, bits, 1);
+    store_group(out, epi.out_bytes(), out.row(i0), i0, j, bits);
   }
 }
 
