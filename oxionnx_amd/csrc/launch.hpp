@@ -290,7 +290,7 @@ using T256 = Tile<256, 256, 2, 4, 2>;       // 6: 8 waves, 128x64 per wave
 using T128s2 = Tile<128, 128, 2, 2, 2>;     // 7: 4 waves, 64x64 per wave, two blocks per CU
 using T128w8 = Tile<128, 128, 2, 4, 2>;     // 8: 8 waves, 64x32 per wave, two blocks per CU
 using T64s4 = Tile<64, 64, 2, 2, 4>;        // 9: 4 waves, 32x32 per wave, four stages
-constexpr int kTileCount = 9;
+constexpr int kTileCount = 9;               // 10 is the split-K path (launch_split)
 
 template <Op O, bool XX, bool XY, class Tl, class LX, class LY, class Epi>
 inline hipError_t launch_tile(const LX& lx, const LY& ly, const Epi& epi, int P, int Q, int kc, hipStream_t st) {

@@ -88,19 +88,23 @@ template <> struct OpT<Op::F32> {
   }
 };
 
-// Block tile: BP x BQ outputs, WP x WQ waves, STAGES LDS buffers of one
-// 128-byte K slab each.
-template <int BP_, int BQ_, int WP_, int WQ_, int STAGES_> struct Tile {
-  static constexpr int BP = BP_, BQ = BQ_, WP = WP_, WQ = WQ_, STAGES = STAGES_;
+// Block tile: BP x BQ outputs, WP x WQ waves, STAGES LDS buffers of one K
+// slab each; a slab holds CH 16-byte chunks per row (CH = 8: 128-byte slabs,
+// four MFMA k-steps; CH = 4: 64-byte slabs, two k-steps, so the same LDS
+// holds twice the stages and the loads run further ahead of their use).
+template <int BP_, int BQ_, int WP_, int WQ_, int STAGES_, int CH_ = 8> struct Tile {
+  static constexpr int BP = BP_, BQ = BQ_, WP = WP_, WQ = WQ_, STAGES = STAGES_, CH = CH_;
+  static constexpr int KS = CH / 2;                               // MFMA k-steps per slab
   static constexpr int kWaves = WP * WQ;
   static constexpr int kThreads = 64 * kWaves;
   static constexpr int TP = BP / (WP * 32), TQ = BQ / (WQ * 32);  // 32x32 MFMA tiles per wave
-  static constexpr int kRowStride = 8;                            // rows are 128 B (8 chunks)
-  static constexpr int NX = BP * 8 / kThreads;                    // DMA loads per thread per stage
-  static constexpr int NY = BQ * 8 / kThreads;
+  static constexpr int kRowStride = CH;                           // rows are CH * 16 bytes
+  static constexpr int NX = BP * CH / kThreads;                   // DMA loads per thread per stage
+  static constexpr int NY = BQ * CH / kThreads;
   static constexpr int kStage = (BP + BQ) * kRowStride;           // in u32x4 units
+  static_assert(CH == 8 || CH == 4, "slabs are 128 or 64 bytes");
   static_assert(TP >= 1 && TQ >= 1, "wave tile must hold at least one 32x32 MFMA tile");
-  static_assert(NX * kThreads == BP * 8 && NY * kThreads == BQ * 8, "loader split must be exact");
+  static_assert(NX * kThreads == BP * CH && NY * kThreads == BQ * CH, "loader split must be exact");
   static_assert(kWaves % 2 == 0, "the DMA swizzle phase relies on an even wave count");
   static_assert(STAGES >= 2 && STAGES * kStage * 16 <= 160 * 1024, "LDS budget");
 };
@@ -111,15 +115,27 @@ template <int BP_, int BQ_, int WP_, int WQ_, int STAGES_> struct Tile {
 // 32-bank LDS serving 8 lanes of a b128 access per cycle) and every group of
 // 16 rows on 16 distinct groups (64 banks serving 16 lanes), for both the
 // row-major DMA writes and the MFMA fragment reads (rows at one chunk).
-__device__ __forceinline__ int lds_slot(int r, int c) { return c ^ (r & 7) ^ ((r >> 3) & 1); }
+//
+// For 64-byte rows (CH = 4) the slot is c ^ ((r >> 1) & 3) ^ ((r >> 3) & 1):
+// the 16-byte bank group of (r, slot) is 4 * (r % 4) + slot modulo 16 (or
+// 4 * (r % 2) + slot modulo 8), and this XOR makes both distinct over every
+// aligned group of 16 (8) rows for each chunk c.
+template <int CH> __device__ __forceinline__ int lds_slot(int r, int c) {
+  if constexpr (CH == 8) return c ^ (r & 7) ^ ((r >> 3) & 1);
+  else return c ^ ((r >> 1) & 3) ^ ((r >> 3) & 1);
+}
 
 // ---------------------------------------------------------------- loaders
-// DMA load i of a thread (i < NR) writes LDS row r = (i * W + w) * 8 + L / 8
-// (W waves, w = wave, L = lane) at slot L % 8, so it fetches the global chunk
-// lds_slot(r, L % 8) (the swizzle is its own inverse).  With W even,
-// r & 7 = L / 8 and (r >> 3) & 1 = w & 1 for every i: the chunk is a
+// DMA load i of a thread (i < NR) writes 1 KiB of LDS: rows
+// (i * W + w) * (64 / CH) + L / CH (W waves, w = wave, L = lane) at slot
+// L % CH, so it fetches the global chunk lds_slot(r, L % CH) (the swizzle is
+// its own inverse).  CH = 8: with W even, r & 7 = L / 8 and (r >> 3) & 1 =
+// w & 1 for every i; CH = 4: r & 15 = L / 4.  Either way the chunk is a
 // per-thread constant.
-__device__ __forceinline__ int dma_chunk(int lane, int wave) { return (lane & 7) ^ (lane >> 3) ^ (wave & 1); }
+template <int CH> __device__ __forceinline__ int dma_chunk(int lane, int wave) {
+  if constexpr (CH == 8) return (lane & 7) ^ (lane >> 3) ^ (wave & 1);
+  else return (lane & 3) ^ ((lane >> 3) & 3) ^ ((lane >> 5) & 1);
+}
 
 __device__ __forceinline__ void dma16(const void* g, u32x4* lds) {
   __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void*)(lds), 16, 0, 0);
@@ -145,22 +161,22 @@ struct DenseRows {
   template <int NR>
   struct State { __amdgpu_buffer_rsrc_t rs; int voff[NR]; int c; };
 
-  template <int NR, int NW>
+  template <int NR, int NW, int CH>
   __device__ __forceinline__ void init(State<NR>& s, int row0, int lane, int wave) const {
-    s.c = dma_chunk(lane, wave);
+    s.c = dma_chunk<CH>(lane, wave);
     s.rs = __builtin_amdgcn_make_buffer_rsrc((void*)(base + (int64_t)row0 * ld), (short)0, 0x7fffffff, 0x00020000);
 #pragma unroll
     for (int i = 0; i < NR; ++i) {
-      const int r = (i * NW + wave) * 8 + (lane >> 3);
+      const int r = (i * NW + wave) * (64 / CH) + lane / CH;
       s.voff[i] = row0 + r < rows ? (int)(r * ld) + s.c * 16 : kOobOffset;
     }
   }
-  template <int NR, int NW>
+  template <int NR, int NW, int CH>
   __device__ __forceinline__ void issue(const State<NR>& s, int kt, int wave, u32x4* lds_rows) const {
-    int g0 = kt * 8;                       // first chunk of the stage (uniform)
+    int g0 = kt * CH;                      // first chunk of the stage (uniform)
     if (kwrap > 0 && g0 >= kwrap) g0 -= kwrap;
     const int soff = g0 * 16;
-    if (g0 + 8 <= kc) {
+    if (g0 + CH <= kc) {
 #pragma unroll
       for (int i = 0; i < NR; ++i) buf16(s.rs, s.voff[i], soff, lds_rows + (i * NW + wave) * 64);
     } else {
@@ -189,14 +205,14 @@ struct Im2colNHWC {
   template <int NR>
   struct State { const char* img[NR]; int iy0[NR], ix0[NR]; uint32_t okmask; int c; };
 
-  template <int NR, int NW>
+  template <int NR, int NW, int CH>
   __device__ __forceinline__ void init(State<NR>& s, int row0, int lane, int wave) const {
-    s.c = dma_chunk(lane, wave);
+    s.c = dma_chunk<CH>(lane, wave);
     const int ohw = OH * OW;
     s.okmask = 0;
 #pragma unroll
     for (int i = 0; i < NR; ++i) {
-      const int r = row0 + (i * NW + wave) * 8 + (lane >> 3);
+      const int r = row0 + (i * NW + wave) * (64 / CH) + lane / CH;
       const bool ok = r < rows;
       s.okmask |= (ok ? 1u : 0u) << i;
       const int rr = ok ? r : 0;
@@ -207,9 +223,9 @@ struct Im2colNHWC {
       s.ix0[i] = ox * sw - pl;
     }
   }
-  template <int NR, int NW>
+  template <int NR, int NW, int CH>
   __device__ __forceinline__ void issue(const State<NR>& s, int kt, int wave, u32x4* lds_rows) const {
-    int gk = kt * 8 + s.c;
+    int gk = kt * CH + s.c;
     if (kwrap > 0 && gk >= kwrap) gk -= kwrap;
     const bool kin = gk < kc;
     const int g = kin ? gk : 0;
@@ -287,12 +303,13 @@ template <bool XOR> __device__ __forceinline__ u32x4 frag(u32x4 v) {
   return v;
 }
 
-// Main loop, per stage kt (STAGES LDS buffers, four MFMA k-steps a stage):
+// Main loop, per stage kt (STAGES LDS buffers, KS = CH / 2 MFMA k-steps a
+// stage):
 //   k-step 0 issues the DMA loads of stage kt + STAGES - 1 (into the buffer
 //   of stage kt - 1, released by the previous stage's barrier), interleaved
 //   with the MFMAs;
-//   k-steps 0..2 read the next k-step's fragments under the MFMAs;
-//   k-step 3 waits until stage kt + 1 has landed, passes the barrier and
+//   k-steps 0..KS-2 read the next k-step's fragments under the MFMAs;
+//   k-step KS-1 waits until stage kt + 1 has landed, passes the barrier and
 //   reads stage kt + 1's first fragments under its MFMAs,
 // so the MFMA pipe is never left waiting on a barrier with no work queued.
 // Where the outputs go: element (i, j) sits at
@@ -372,8 +389,8 @@ mfma_gemm_kernel(const LX lx, const LY ly, const Epi epi, int nP, int nQ, int kc
 
   typename LX::template State<Tl::NX> sx;
   typename LY::template State<Tl::NY> sy;
-  lx.template init<Tl::NX, Tl::kWaves>(sx, p0, lane, wave);
-  ly.template init<Tl::NY, Tl::kWaves>(sy, q0, lane, wave);
+  lx.template init<Tl::NX, Tl::kWaves, Tl::CH>(sx, p0, lane, wave);
+  ly.template init<Tl::NY, Tl::kWaves, Tl::CH>(sy, q0, lane, wave);
 
   A acc[Tl::TP][Tl::TQ];
 #pragma unroll
@@ -384,7 +401,7 @@ mfma_gemm_kernel(const LX lx, const LY ly, const Epi epi, int nP, int nQ, int kc
       for (int e = 0; e < 16; ++e) acc[a][b][e] = 0;
 
   // K stages of this block: all of them, or slice blockIdx.y of `splits`
-  const int nk_all = (kc + 7) >> 3;
+  const int nk_all = (kc + Tl::CH - 1) / Tl::CH;
   const int per = (nk_all + splits - 1) / splits;
   const int kbeg = (int)blockIdx.y * per;
   const int kend = min(kbeg + per, nk_all);
@@ -393,19 +410,19 @@ mfma_gemm_kernel(const LX lx, const LY ly, const Epi epi, int nP, int nQ, int kc
   // the pad source), so the waits below are fixed counts of outstanding loads.
   auto issue = [&](int kt) {
     u32x4* s = smem + (kt % Tl::STAGES) * Tl::kStage;
-    lx.template issue<Tl::NX, Tl::kWaves>(sx, kt, wave, s);
-    ly.template issue<Tl::NY, Tl::kWaves>(sy, kt, wave, s + Tl::BP * Tl::kRowStride);
+    lx.template issue<Tl::NX, Tl::kWaves, Tl::CH>(sx, kt, wave, s);
+    ly.template issue<Tl::NY, Tl::kWaves, Tl::CH>(sy, kt, wave, s + Tl::BP * Tl::kRowStride);
   };
 
   // Fragment slots of this lane: rows are tile bases (multiples of 32) plus
   // lane % 32, chunk 2 * ks + lane / 32.
   const int xr = wp * Tl::TP * 32 + (lane & 31);
   const int yr = Tl::BP + wq * Tl::TQ * 32 + (lane & 31);
-  int xslot[4], yslot[4];
+  int xslot[Tl::KS], yslot[Tl::KS];
 #pragma unroll
-  for (int ks = 0; ks < 4; ++ks) {
-    xslot[ks] = xr * Tl::kRowStride + lds_slot(xr, 2 * ks + (lane >> 5));
-    yslot[ks] = yr * Tl::kRowStride + lds_slot(yr, 2 * ks + (lane >> 5));
+  for (int ks = 0; ks < Tl::KS; ++ks) {
+    xslot[ks] = xr * Tl::kRowStride + lds_slot<Tl::CH>(xr, 2 * ks + (lane >> 5));
+    yslot[ks] = yr * Tl::kRowStride + lds_slot<Tl::CH>(yr, 2 * ks + (lane >> 5));
   }
 
 #pragma unroll
@@ -426,9 +443,9 @@ mfma_gemm_kernel(const LX lx, const LY ly, const Epi epi, int nP, int nQ, int kc
     const u32x4* s = smem + (kt % Tl::STAGES) * Tl::kStage;
     const u32x4* sn = smem + ((kt + 1) % Tl::STAGES) * Tl::kStage;
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
+    for (int ks = 0; ks < Tl::KS; ++ks) {
       const int cur = ks & 1;
-      if (ks < 3) {
+      if (ks < Tl::KS - 1) {
 #pragma unroll
         for (int a = 0; a < Tl::TP; ++a) fx[cur ^ 1][a] = s[xslot[ks + 1] + a * 32 * Tl::kRowStride];
 #pragma unroll
@@ -454,6 +471,7 @@ mfma_gemm_kernel(const LX lx, const LY ly, const Epi epi, int nP, int nQ, int kc
           __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
           if (ks == 0 && a * Tl::TQ + b < NL) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
         }
+
     }
   }
 
