@@ -347,8 +347,9 @@ int ohip_reset_counters(ohip_ctx* ctx);
  * 5: 256x256 (4)       6: 256x256 (8)   7: 128x128 (4, two LDS stages)
  * 8: 128x128 (8, two LDS stages)           9: 64x64 (4, four LDS stages)
  * 10: split-K over 64x64 (4, four LDS stages) tiles with an ordered reduction.
- * The automatic choice splits K when the 64x64 tiling gives fewer than 256
- * blocks and K is at least 16 stages of 128 bytes. */
+ * 11: split-K over 128x128 (8, two LDS stages) tiles with an ordered reduction.
+ * The automatic choice splits K (on 64x64 tiles) when the 64x64 tiling gives
+ * fewer than 256 blocks and K is at least 16 stages of 128 bytes. */
 int ohip_set_tile_override(ohip_ctx* ctx, int tile_id);
 
 #ifdef __cplusplus

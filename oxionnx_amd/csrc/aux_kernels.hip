@@ -134,15 +134,62 @@ gemv_row_kernel(const T* __restrict__ a, int64_t lda, const T* __restrict__ w, i
   }
 }
 
+// Rows of at most kWaveRowChunks 16-byte chunks: one wave per weight row
+// (four rows per block), each lane striding the row's chunks, the partial
+// sums reduced across the wave by a fixed butterfly (deterministic); lane 0
+// runs the epilogue for the M outputs of the row.  A block per row would
+// leave most of its waves without a chunk.
+constexpr int kWaveRowChunks = 256;
+
+template <class T, int M>
+__global__ void __launch_bounds__(256)
+gemv_wave_kernel(const T* __restrict__ a, int64_t lda, const T* __restrict__ w, int64_t ldw, int kc, int N,
+                 FloatEpi<T> epi) {
+  constexpr int E = Vec16<T>::N;
+  const int lane = threadIdx.x & 63;
+  const int n = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (n >= N) return;
+  const u32x4* wr = reinterpret_cast<const u32x4*>(w + (int64_t)n * ldw);
+  float acc[M];
+#pragma unroll
+  for (int m = 0; m < M; ++m) acc[m] = 0.0f;
+  for (int c = lane; c < kc; c += 64) {
+    float f[E];
+    Vec16<T>::unpack(__builtin_nontemporal_load(wr + c), f);
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+      float g[E];
+      Vec16<T>::unpack(reinterpret_cast<const u32x4*>(a + (int64_t)m * lda)[c], g);
+#pragma unroll
+      for (int e = 0; e < E; ++e) acc[m] += f[e] * g[e];
+    }
+  }
+#pragma unroll
+  for (int m = 0; m < M; ++m) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) acc[m] += __shfl_xor(acc[m], off, 64);
+  }
+  if (lane == 0) {
+#pragma unroll
+    for (int m = 0; m < M; ++m) epi.store_one(acc[m], n, m);
+  }
+}
+
 template <class T>
 static hipError_t gemv_t(const GemvArgs& g, const FloatOut& o, hipStream_t st) {
   const T* a = reinterpret_cast<const T*>(g.a);
   const T* w = reinterpret_cast<const T*>(g.w);
   const FloatEpi<T> epi = make_float_epi<T>(o);
+  const bool by_wave = g.kc <= kWaveRowChunks;
+  const unsigned wave_blocks = (unsigned)((g.N + 3) / 4);
   switch (g.M) {
-#define OHIP_GEMV_CASE(MM)                                                                                    \
-  case MM:                                                                                                    \
-    hipLaunchKernelGGL((gemv_row_kernel<T, MM>), dim3(g.N), dim3(512), 0, st, a, g.lda, w, g.ldw, g.kc, epi); \
+#define OHIP_GEMV_CASE(MM)                                                                                      \
+  case MM:                                                                                                      \
+    if (by_wave)                                                                                                \
+      hipLaunchKernelGGL((gemv_wave_kernel<T, MM>), dim3(wave_blocks), dim3(256), 0, st, a, g.lda, w, g.ldw, \
+                         g.kc, g.N, epi);                                                                       \
+    else                                                                                                        \
+      hipLaunchKernelGGL((gemv_row_kernel<T, MM>), dim3(g.N), dim3(512), 0, st, a, g.lda, w, g.ldw, g.kc, epi); \
     break;
     OHIP_GEMV_CASE(1) OHIP_GEMV_CASE(2) OHIP_GEMV_CASE(3) OHIP_GEMV_CASE(4)
     OHIP_GEMV_CASE(5) OHIP_GEMV_CASE(6) OHIP_GEMV_CASE(7) OHIP_GEMV_CASE(8)
@@ -257,6 +304,154 @@ hipError_t run_nchw_to_nhwc_pad(int elem_bytes, const void* src, void* dst, int 
     case 4: return nchw_to_nhwc_pad_t<uint32_t>(src, dst, N, C, H, W, cp, pt, pl, pb, pr, mode, st);
     default: return hipErrorInvalidValue;
   }
+}
+
+// NCHW [C][H][W] -> NHWC [Hp][Wp][cpt] staging of a grouped convolution's
+// input for the implicit-im2col loader.  The channel axis is laid out per group: slot g * cpg + ci holds
+// channel g * cg + ci for ci < cg, and zero for the padding slots up to cpg
+// (cpg a whole number of 16-byte chunks, cpt = groups * cpg).  The spatial
+// border, if any, is filled by pad_map (a fused reflect / edge Pad).
+struct StageGeo {
+  int C, H, W, Hp, Wp, pt, pl, mode, cg, cpg, cpt;
+  __device__ __forceinline__ int64_t src_off(int64_t px) const {   // -1 past the image
+    const int y = (int)(px / Wp), x = (int)(px - (int64_t)y * Wp);
+    return (int64_t)pad_map(y, pt, H, mode) * W + pad_map(x, pl, W, mode);
+  }
+  __device__ __forceinline__ int channel(int slot) const {         // -1 for a padding slot
+    const int g = slot / cpg, ci = slot - g * cpg, c = g * cg + ci;
+    return (ci < cg && c < C) ? c : -1;
+  }
+};
+
+// A block moves 32 pixels x 64 slots through LDS, reading source rows along
+// the pixels and writing whole 16-byte slot vectors.
+template <class T>
+__global__ void __launch_bounds__(256)
+stage_nhwc_tile_kernel(const T* __restrict__ src, T* __restrict__ dst, StageGeo g) {
+  constexpr int VE = 16 / (int)sizeof(T), PX = 32, SL = 64;
+  __shared__ T tile[SL][PX + 1];
+  const int n = blockIdx.z;
+  const int s0 = blockIdx.y * SL;
+  const int64_t p0 = (int64_t)blockIdx.x * PX;
+  const int64_t HWp = (int64_t)g.Hp * g.Wp;
+  const T* s = src + (int64_t)n * g.C * g.H * g.W;
+  const int64_t plane = (int64_t)g.H * g.W;
+  const int tx = threadIdx.x & (PX - 1), ty = threadIdx.x / PX;
+  const int64_t px = p0 + tx;
+  const int64_t off = px < HWp ? g.src_off(px) : -1;
+  for (int r = ty; r < SL; r += 256 / PX) {
+    const int slot = s0 + r;
+    const int c = (off >= 0 && slot < g.cpt) ? g.channel(slot) : -1;
+    tile[r][tx] = c >= 0 ? s[c * plane + off] : T(0);
+  }
+  __syncthreads();
+  T* d = dst + (int64_t)n * HWp * g.cpt;
+  for (int v = threadIdx.x; v < PX * (SL / VE); v += 256) {
+    const int p = v / (SL / VE), q = v - p * (SL / VE);
+    const int64_t pix = p0 + p;
+    const int slot = s0 + q * VE;
+    if (pix >= HWp || slot >= g.cpt) continue;
+    T e[VE];
+#pragma unroll
+    for (int k = 0; k < VE; ++k) e[k] = tile[q * VE + k][p];
+    *reinterpret_cast<u32x4*>(d + pix * g.cpt + slot) = __builtin_bit_cast(u32x4, e);
+  }
+}
+
+template <class T>
+static hipError_t stage_nhwc_t(const void* src, void* dst, int N, int C, int H, int W, int pt, int pl, int pb,
+                               int pr, int mode, int cg, int cpg, int groups, hipStream_t st) {
+  StageGeo g{C, H, W, H + pt + pb, W + pl + pr, pt, pl, mode, cg, cpg, groups * cpg};
+  const int64_t HWp = (int64_t)g.Hp * g.Wp;
+  if (g.cpt % (16 / (int)sizeof(T)) != 0 || (uintptr_t)dst % 16 != 0) return hipErrorInvalidValue;
+  const T* s = reinterpret_cast<const T*>(src);
+  T* d = reinterpret_cast<T*>(dst);
+  hipLaunchKernelGGL(stage_nhwc_tile_kernel<T>,
+                     dim3((unsigned)((HWp + 31) / 32), (unsigned)((g.cpt + 63) / 64), (unsigned)N), dim3(256), 0, st,
+                     s, d, g);
+  return hipGetLastError();
+}
+
+hipError_t run_stage_nhwc(int elem_bytes, const void* src, void* dst, int N, int C, int H, int W, int pt, int pl,
+                          int pb, int pr, int mode, int cg, int cpg, int groups, hipStream_t st) {
+  switch (elem_bytes) {
+    case 1: return stage_nhwc_t<uint8_t>(src, dst, N, C, H, W, pt, pl, pb, pr, mode, cg, cpg, groups, st);
+    case 2: return stage_nhwc_t<uint16_t>(src, dst, N, C, H, W, pt, pl, pb, pr, mode, cg, cpg, groups, st);
+    case 4: return stage_nhwc_t<uint32_t>(src, dst, N, C, H, W, pt, pl, pb, pr, mode, cg, cpg, groups, st);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+
+// ---------------------------------------------------------------- direct conv
+// Convolution for channel groups too narrow for the MFMA engine (depthwise
+// and other small groups): one thread per output element, f32 accumulation
+// over the (ci, ky, kx) taps of its group in that order; NCHW input, NCHW or
+// NHWC output.  The filter is the packed [Cout][KH][KW][cpg] form.  Zero
+// padding skips the taps outside the image; a fused reflect / edge Pad maps
+// them into it (pad_map), as the staging transpose does for the MFMA path.
+template <class T>
+__global__ void __launch_bounds__(256)
+conv_direct_kernel(const T* __restrict__ x, const T* __restrict__ w, const T* __restrict__ bias, T* __restrict__ y,
+                   DirectConvArgs a) {
+  const int64_t total = (int64_t)a.N * a.cout * a.OH * a.OW;
+  for (int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x; idx < total; idx += (int64_t)gridDim.x * 256) {
+    int64_t r = idx;
+    const int ox = (int)(r % a.OW); r /= a.OW;
+    const int oy = (int)(r % a.OH); r /= a.OH;
+    const int co = (int)(r % a.cout);
+    const int n = (int)(r / a.cout);
+    const int g = co / a.coutg;
+    const T* xg = x + ((int64_t)n * a.C + (int64_t)g * a.cg) * a.H * a.W;
+    const T* wr = w + (int64_t)co * a.ldw;
+    float acc = 0.0f;
+    for (int ci = 0; ci < a.cg; ++ci) {
+      const T* xc = xg + (int64_t)ci * a.H * a.W;
+      for (int ky = 0; ky < a.KH; ++ky) {
+        int iy = oy * a.sh + ky * a.dh;
+        if (a.pad_mode == 0) {
+          iy -= a.pt;
+          if ((unsigned)iy >= (unsigned)a.H) continue;
+        } else {
+          iy = pad_map(iy, a.pt, a.H, a.pad_mode);
+        }
+        for (int kx = 0; kx < a.KW; ++kx) {
+          int ix = ox * a.sw + kx * a.dw;
+          if (a.pad_mode == 0) {
+            ix -= a.pl;
+            if ((unsigned)ix >= (unsigned)a.W) continue;
+          } else {
+            ix = pad_map(ix, a.pl, a.W, a.pad_mode);
+          }
+          acc += to_f32(xc[(int64_t)iy * a.W + ix]) * to_f32(wr[(ky * a.KW + kx) * a.cpg + ci]);
+        }
+      }
+    }
+    float v = acc;
+    if (bias) v = v + to_f32(bias[co]);
+    v = activate(v, a.act, a.lo, a.hi);
+    const int64_t o = a.nhwc_out ? (((int64_t)n * a.OH + oy) * a.OW + ox) * a.ldo + co
+                                 : (((int64_t)n * a.cout + co) * a.OH + oy) * a.OW + ox;
+    y[o] = from_f32<T>(v);
+  }
+}
+
+hipError_t run_conv_direct(int dtype, const void* x, const void* w, const void* bias, void* y,
+                           const DirectConvArgs& a, hipStream_t st) {
+  const int64_t total = (int64_t)a.N * a.cout * a.OH * a.OW;
+  if (total <= 0) return hipSuccess;
+  const unsigned grid = (unsigned)std::min<int64_t>((total + 255) / 256, 65535 * 16);
+#define OHIP_DIRECT(T)                                                                                      \
+  hipLaunchKernelGGL(conv_direct_kernel<T>, dim3(grid), dim3(256), 0, st, reinterpret_cast<const T*>(x), \
+                     reinterpret_cast<const T*>(w), reinterpret_cast<const T*>(bias), reinterpret_cast<T*>(y), a)
+  switch (dtype) {
+    case DT_F32: OHIP_DIRECT(float); break;
+    case DT_F16: OHIP_DIRECT(_Float16); break;
+    case DT_BF16: OHIP_DIRECT(__bf16); break;
+    default: return hipErrorInvalidValue;
+  }
+#undef OHIP_DIRECT
+  return hipGetLastError();
 }
 
 // dst[r][c] = c < K ? src[r * rs + c * cs] : 0 for a [R][ld] destination: pads a

@@ -362,17 +362,17 @@ int do_conv(ohip_ctx* ctx, const ohip_node* nd, int placement, ohip_output* out)
   Geo g;
   std::string why;
   if (!conv_geometry(nd, x, w, &g, &why)) return decline(why);
-  if (g.group != 1) return decline("Conv: group != 1");
+  const int64_t cg = g.c / g.group;
   ohip_tuning tun;
   ohip_get_tuning(ctx, &tun);
-  if (!ohip_conv_admits(&tun, g.cout, g.c * g.kh * g.kw, g.n * g.oh * g.ow)) return decline("Conv: below conv_min_mac");
+  if (!ohip_conv_admits(&tun, g.cout, cg * g.kh * g.kw, g.n * g.oh * g.ow)) return decline("Conv: below conv_min_mac");
   if (x->device && ohip_dtensor_layout(x->device) != OHIP_NCHW) return decline("Conv: resident input layout");
 
   std::string name = wkey_name(w), label = "Conv.W";
   ohip_weight_key key{name.c_str(), label.c_str()};
   const bool cache = w->is_initializer && !name.empty();
   ohip_weight* wt = nullptr;
-  int rc = ohip_weight_conv(ctx, cache ? &key : nullptr, w->dtype, w->data, g.cout, g.c, g.kh, g.kw, dt, &wt);
+  int rc = ohip_weight_conv(ctx, cache ? &key : nullptr, w->dtype, w->data, g.cout, cg, g.kh, g.kw, dt, &wt);
   if (rc) return rc;
   Stage st(ctx);
   const void* xd = st.operand(x);
@@ -395,7 +395,7 @@ int do_conv(ohip_ctx* ctx, const ohip_node* nd, int placement, ohip_output* out)
   const size_t obytes = (size_t)(g.n * g.cout * g.oh * g.ow) * ebytes(dt);
   void* yd = st.alloc(obytes);
   if (!xd || !yd || (b && !bd)) { if (!cache) ohip_weight_release(wt); return OHIP_E_NOMEM; }
-  ohip_conv_desc d{g.n, g.c, g.h, g.w, g.cout, g.kh, g.kw, 1, g.sh, g.sw, g.dh, g.dw, g.pt, g.pl, g.pb, g.pr,
+  ohip_conv_desc d{g.n, g.c, g.h, g.w, g.cout, g.kh, g.kw, g.group, g.sh, g.sw, g.dh, g.dw, g.pt, g.pl, g.pb, g.pr,
                    dt, OHIP_NCHW, OHIP_NCHW, 0, 0.0f, 0.0f, OHIP_PAD_ZEROS};
   fused_act(nd, &d.act, &d.act_lo, &d.act_hi);
   // this provider's Pad -> Conv fusion: the pads are a reflect / edge Pad's

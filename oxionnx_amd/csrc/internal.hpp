@@ -29,8 +29,9 @@ struct DenseOperand {
 // Implicit im2col rows over an NHWC activation with channels padded to cpc
 // 16-byte chunks.
 struct Im2colOperand {
-  const void* base;
+  const void* base;   // channel chunk 0 of this operand's channel group at pixel (0, 0)
   int H, W, OH, OW, KW, cpc;
+  int pstride;        // 16-byte chunks between pixels (0: cpc)
   int sh, sw, dh, dw, pt, pl;
   int rows, kc, kwrap;
   uint32_t xor_mask;  // as DenseOperand::xor_mask
@@ -48,16 +49,20 @@ struct OutMap {
   void* split_ws;  // splits * Q * round_up(P, 4) accumulators (4 bytes each)
 };
 
-// Split-K plan: a contraction whose 64x64 tiling leaves the 256 CUs short
-// of blocks (under one block per CU with at least 16 stages of 128 bytes of
-// K, or under two with at least 32) is cut into K slices (each at least 8
-// stages), aiming at two blocks per CU.  forced_tile 10 forces
-// the split path; any other forced tile disables it.
+// Split-K plan.  The slices run on the 64x64 four-stage tile when its
+// tiling leaves the 256 CUs short of blocks (under one block per CU with at
+// least 16 stages of 128 bytes of K, or under two with at least 32); slices
+// keep at least 8 stages each and aim at two blocks per CU.  forced_tile
+// 10 / 11 force the split path on the 64x64 / 128x128 (eight-wave) tile; any
+// other forced tile disables it.  (The 128x128 slices measured slower on the
+// generator's resident NHWC convolutions, so the automatic plan keeps 64x64.)
+inline int split_tile_size(int, int, int forced_tile) { return forced_tile == 11 ? 128 : 64; }
 inline int plan_splits(int P, int Q, int kc, int forced_tile) {
-  if (forced_tile != 0 && forced_tile != 10) return 1;
+  if (forced_tile != 0 && forced_tile != 10 && forced_tile != 11) return 1;
   const int64_t nk = (kc + 7) / 8;
-  const int64_t nb = (int64_t)((P + 63) / 64) * ((Q + 63) / 64);
-  if (forced_tile == 10) return (int)std::max<int64_t>(2, std::min<int64_t>(16, nk / 2 > 0 ? nk / 2 : 1));
+  const int bs = split_tile_size(P, Q, forced_tile);
+  const int64_t nb = (int64_t)((P + bs - 1) / bs) * ((Q + bs - 1) / bs);
+  if (forced_tile != 0) return (int)std::max<int64_t>(2, std::min<int64_t>(16, nk / 2 > 0 ? nk / 2 : 1));
   if (nb >= 512 || nk < 16 || (nb >= 256 && nk < 32)) return 1;
   int64_t s = (512 + nb - 1) / nb;
   s = std::min<int64_t>(s, nk / 8);
@@ -107,6 +112,25 @@ hipError_t run_dense_quant(const DenseOperand& x, const DenseOperand& y, const Q
 hipError_t run_conv_quant(const Im2colOperand& col, const DenseOperand& w, bool col_on_x, const QuantOut& o,
                           int tile, hipStream_t st);
 hipError_t run_gemv(int dtype, const GemvArgs& g, const FloatOut& o, hipStream_t st);
+// Direct (non-MFMA) grouped convolution; see conv_direct_kernel.
+struct DirectConvArgs {
+  int N, C, H, W, cout, cg, coutg, KH, KW;
+  int sh, sw, dh, dw, pt, pl, pad_mode;  // pad_mode 0: zeros (pt, pl are the conv's pads); 1/2: reflect / edge
+  int OH, OW;
+  int64_t ldw;    // elements between filter rows
+  int cpg;        // channel slots per tap in the packed filter
+  int nhwc_out;
+  int64_t ldo;    // NHWC output: elements between pixels
+  int act;
+  float lo, hi;
+};
+hipError_t run_conv_direct(int dtype, const void* x, const void* w, const void* bias, void* y,
+                           const DirectConvArgs& a, hipStream_t st);
+
+// NCHW -> NHWC staging with per-group channel slots and an optional
+// reflect (1) / edge (2) spatial border; see stage_nhwc_kernel.
+hipError_t run_stage_nhwc(int elem_bytes, const void* src, void* dst, int N, int C, int H, int W, int pt, int pl,
+                          int pb, int pr, int mode, int cg, int cpg, int groups, hipStream_t st);
 hipError_t run_nchw_to_nhwc(int elem_bytes, const void* src, void* dst, int N, int C, int HW, int cp,
                             hipStream_t st);
 hipError_t run_nchw_to_nhwc_pad(int elem_bytes, const void* src, void* dst, int N, int C, int H, int W, int cp,

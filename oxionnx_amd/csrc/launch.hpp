@@ -290,7 +290,7 @@ using T256 = Tile<256, 256, 2, 4, 2>;       // 6: 8 waves, 128x64 per wave
 using T128s2 = Tile<128, 128, 2, 2, 2>;     // 7: 4 waves, 64x64 per wave, two blocks per CU
 using T128w8 = Tile<128, 128, 2, 4, 2>;     // 8: 8 waves, 64x32 per wave, two blocks per CU
 using T64s4 = Tile<64, 64, 2, 2, 4>;        // 9: 4 waves, 32x32 per wave, four stages
-constexpr int kTileCount = 9;               // 10 is the split-K path (launch_split)
+constexpr int kTileCount = 9;               // 10, 11: the split-K paths (launch_split_on)
 
 template <Op O, bool XX, bool XY, class Tl, class LX, class LY, class Epi>
 inline hipError_t launch_tile(const LX& lx, const LY& ly, const Epi& epi, int P, int Q, int kc, hipStream_t st) {
@@ -303,12 +303,11 @@ inline hipError_t launch_tile(const LX& lx, const LY& ly, const Epi& epi, int P,
   return hipGetLastError();
 }
 
-// Split-K launch on the 64x64 four-stage tile: partial sums into the
-// workspace, then the ordered reduction applies the real epilogue.
-template <Op O, bool XX, bool XY, class LX, class LY, class Epi>
-inline hipError_t launch_split(const LX& lx, const LY& ly, const Epi& epi, int P, int Q, int kc, int splits,
-                               void* ws, hipStream_t st) {
-  using Tl = Tile<64, 64, 2, 2, 4>;
+// Split-K launch: partial sums of every K slice into the workspace, then the
+// ordered reduction applies the real epilogue.
+template <Op O, bool XX, bool XY, class Tl, class LX, class LY, class Epi>
+inline hipError_t launch_split_on(const LX& lx, const LY& ly, const Epi& epi, int P, int Q, int kc, int splits,
+                                  void* ws, hipStream_t st) {
   using T = typename std::conditional<O == Op::I8, int32_t, float>::type;
   using V = typename OpT<O>::Out4;
   const int nP = (P + Tl::BP - 1) / Tl::BP, nQ = (Q + Tl::BQ - 1) / Tl::BQ;
@@ -350,7 +349,11 @@ inline int pick_tile(int P, int Q, int kc, int forced) {
 template <Op O, bool XX, bool XY, class LX, class LY, class Epi>
 inline hipError_t launch_any(const LX& lx, const LY& ly, const Epi& epi, int P, int Q, int kc, int tile,
                              int splits, void* split_ws, hipStream_t st) {
-  if (splits > 1) return launch_split<O, XX, XY>(lx, ly, epi, P, Q, kc, splits, split_ws, st);
+  if (splits > 1) {
+    if (split_tile_size(P, Q, tile) == 128)
+      return launch_split_on<O, XX, XY, T128w8>(lx, ly, epi, P, Q, kc, splits, split_ws, st);
+    return launch_split_on<O, XX, XY, T64s4>(lx, ly, epi, P, Q, kc, splits, split_ws, st);
+  }
   switch (pick_tile(P, Q, kc, tile)) {
     case 2: return launch_tile<O, XX, XY, T128>(lx, ly, epi, P, Q, kc, st);
     case 3: return launch_tile<O, XX, XY, T256x128>(lx, ly, epi, P, Q, kc, st);
@@ -416,6 +419,7 @@ inline Im2colNHWC make_im2col(const Im2colOperand& c) {
   Im2colNHWC r;
   r.base = reinterpret_cast<const char*>(c.base);
   r.H = c.H; r.W = c.W; r.OH = c.OH; r.OW = c.OW; r.KW = c.KW; r.cpc = c.cpc;
+  r.pstride = c.pstride > 0 ? c.pstride : c.cpc;
   r.sh = c.sh; r.sw = c.sw; r.dh = c.dh; r.dw = c.dw; r.pt = c.pt; r.pl = c.pl;
   r.rows = c.rows; r.kc = c.kc; r.kwrap = c.kwrap;
   r.pad = reinterpret_cast<const char*>(c.pad16);

@@ -195,7 +195,8 @@ struct Im2colNHWC {
   const char* base;    // x[0][0][0][0]
   int H, W, OH, OW;
   int KW;
-  int cpc;             // 16-byte channel chunks per pixel
+  int cpc;             // 16-byte channel chunks per tap (the K extent of one pixel)
+  int pstride;         // 16-byte chunks between pixels (>= cpc: grouped channels)
   int sh, sw, dh, dw, pt, pl;
   int rows;            // N * OH * OW
   int kc;              // KH * KW * cpc
@@ -218,7 +219,7 @@ struct Im2colNHWC {
       const int rr = ok ? r : 0;
       const int n = rr / ohw, rem = rr - n * ohw;
       const int oy = rem / OW, ox = rem - oy * OW;
-      s.img[i] = base + (int64_t)n * H * W * cpc * 16;
+      s.img[i] = base + (int64_t)n * H * W * pstride * 16;
       s.iy0[i] = oy * sh - pt;
       s.ix0[i] = ox * sw - pl;
     }
@@ -239,7 +240,7 @@ struct Im2colNHWC {
       const int iy = s.iy0[i] + dy, ix = s.ix0[i] + dx;
       const bool inside =
           kin && ((s.okmask >> i) & 1u) && (unsigned)iy < (unsigned)H && (unsigned)ix < (unsigned)W;
-      dma16(inside ? s.img[i] + ((int64_t)(iy * W + ix) * cpc + cc) * 16 : pad, lds_rows + (i * NW + wave) * 64);
+      dma16(inside ? s.img[i] + ((int64_t)(iy * W + ix) * pstride + cc) * 16 : pad, lds_rows + (i * NW + wave) * 64);
     }
   }
 };

@@ -262,7 +262,7 @@ extern "C" int ohip_sync(ohip_ctx* ctx) {
 
 extern "C" int ohip_set_tile_override(ohip_ctx* ctx, int tile_id) {
   if (!ctx) return fail(OHIP_E_INVALID, "null context");
-  if (tile_id < 0 || tile_id > 10) return fail(OHIP_E_INVALID, "tile id must be 0..10");
+  if (tile_id < 0 || tile_id > 11) return fail(OHIP_E_INVALID, "tile id must be 0..11");
   ctx->tile_override = tile_id;
   return OHIP_OK;
 }
@@ -1043,23 +1043,23 @@ extern "C" int ohip_conv2d(ohip_ctx* ctx, const ohip_conv_desc* d, const void* x
   int rc = activate(ctx);
   if (rc) return rc;
   if (!d || !x || !w || !y) return fail(OHIP_E_INVALID, "ohip_conv2d: null argument");
-  if (d->group != 1) return fail(OHIP_DECLINED, "ohip_conv2d: group != 1 is not handled");
+  if (d->group < 1 || d->c % d->group || d->cout % d->group) return fail(OHIP_E_SHAPE, "ohip_conv2d: bad group");
   if (!is_float(d->dtype) || w->kind != WK_CONV || w->dtype != d->dtype)
     return fail(OHIP_E_INVALID, "ohip_conv2d: weight kind / dtype mismatch");
-  if (w->rows != d->cout || w->k != d->c || w->kh != d->kh || w->kw != d->kw)
+  const int64_t G = d->group, cg = d->c / G, coutg = d->cout / G;
+  if (w->rows != d->cout || w->k != cg || w->kh != d->kh || w->kw != d->kw)
     return fail(OHIP_E_SHAPE, "ohip_conv2d: shape disagrees with the packed filter");
   ConvGeo g;
   rc = conv_geo(d->h, d->w, d->kh, d->kw, d->stride_h, d->stride_w, d->dil_h, d->dil_w, d->pad_t, d->pad_l,
                 d->pad_b, d->pad_r, &g);
   if (rc) return rc;
   const int eb = elem_bytes(d->dtype), ce = 16 / eb;
-  const int64_t cp = round_up(d->c, ce);
+  const int64_t cp = round_up(cg, ce);   // channel slots per group and tap
+  const int64_t cpt = G * cp;            // channel slots per staged pixel
   const int64_t rows = d->n * g.oh * g.ow;
-  if (rows > INT_MAX / 2 || d->n * d->h * d->w * cp > (int64_t)INT_MAX * 4)
+  if (rows > INT_MAX / 2 || d->n * d->h * d->w * cpt > (int64_t)INT_MAX * 4)
     return fail(OHIP_DECLINED, "ohip_conv2d: extent too large");
   if (rows == 0) return OHIP_OK;
-  std::lock_guard<std::mutex> lock(ctx->mu);
-  ctx->counters.dispatches++;
 
   // A fused reflect / edge Pad is applied by the staging transpose, which
   // then writes the padded image; the convolution itself runs unpadded.
@@ -1069,13 +1069,44 @@ extern "C" int ohip_conv2d(ohip_ctx* ctx, const ohip_conv_desc* d, const void* x
   if (d->pad_mode == OHIP_PAD_REFLECT &&
       ((d->h > 1 && (d->pad_t >= d->h || d->pad_b >= d->h)) || (d->w > 1 && (d->pad_l >= d->w || d->pad_r >= d->w))))
     return fail(OHIP_DECLINED, "ohip_conv2d: reflect pad wider than the image");
+  int act = d->act;
+  float lo = d->act_lo, hi = d->act_hi;
+  if (act == ACT_CLIP) {
+    if (std::isnan(lo)) lo = -INFINITY;
+    if (std::isnan(hi)) hi = INFINITY;
+    if (!(lo <= hi)) act = ACT_NONE;
+  }
+  const int64_t ohw = g.oh * g.ow;
+  const int64_t ldo = round_up(d->cout, ce);
+
+  // Groups whose output or input channel span is too narrow to fill an MFMA
+  // tile (depthwise, and small groups) run the direct kernel on the NCHW
+  // input; wider groups run one MFMA launch per group.
+  const bool direct = G > 1 && (coutg < 16 || cg * d->kh * d->kw < 32 || G > 64);
+  if (G > 1 && d->in_layout != OHIP_NCHW && (direct || cg % ce != 0))
+    return fail(OHIP_DECLINED, "ohip_conv2d: this grouped convolution needs an NCHW input");
+  std::lock_guard<std::mutex> lock(ctx->mu);
+  ctx->counters.dispatches++;
+  if (direct) {
+    DirectConvArgs a{};
+    a.N = (int)d->n; a.C = (int)d->c; a.H = (int)d->h; a.W = (int)d->w; a.cout = (int)d->cout;
+    a.cg = (int)cg; a.coutg = (int)coutg; a.KH = (int)d->kh; a.KW = (int)d->kw;
+    a.sh = (int)d->stride_h; a.sw = (int)d->stride_w; a.dh = (int)d->dil_h; a.dw = (int)d->dil_w;
+    a.pt = (int)d->pad_t; a.pl = (int)d->pad_l; a.pad_mode = fused_pad ? d->pad_mode : 0;
+    a.OH = (int)g.oh; a.OW = (int)g.ow; a.ldw = w->ld_bytes / eb; a.cpg = (int)cp;
+    a.nhwc_out = d->out_layout != OHIP_NCHW; a.ldo = ldo; a.act = act; a.lo = lo; a.hi = hi;
+    hipError_t e = run_conv_direct(d->dtype, x, w->data, bias, y, a, ctx->stream);
+    if (e != hipSuccess) return hip_fail(e, "ohip_conv2d direct launch");
+    return OHIP_OK;
+  }
+
   const int64_t sh_ = fused_pad ? d->h + d->pad_t + d->pad_b : d->h;
   const int64_t sw_ = fused_pad ? d->w + d->pad_l + d->pad_r : d->w;
   ScratchPlan plan;
   const bool stage = d->in_layout == OHIP_NCHW;
-  size_t ix = stage ? plan.add((size_t)(d->n * sh_ * sw_ * cp) * eb) : SIZE_MAX;
+  size_t ix = stage ? plan.add((size_t)(d->n * sh_ * sw_ * cpt) * eb) : SIZE_MAX;
   const bool nchw_out = d->out_layout == OHIP_NCHW;
-  const int sP = nchw_out ? (int)rows : (int)d->cout, sQ = nchw_out ? (int)d->cout : (int)rows;
+  const int sP = nchw_out ? (int)rows : (int)coutg, sQ = nchw_out ? (int)coutg : (int)rows;
   const int splits = plan_splits(sP, sQ, (int)(d->kh * d->kw * (cp / ce)), ctx->tile_override);
   size_t iw = splits > 1 ? plan.add(split_ws_bytes(sP, sQ, splits)) : SIZE_MAX;
   rc = scratch_reserve(ctx, plan.total());
@@ -1083,7 +1114,13 @@ extern "C" int ohip_conv2d(ohip_ctx* ctx, const ohip_conv_desc* d, const void* x
   const void* xin = x;
   if (stage) {
     void* px = scratch_at(ctx, plan, ix);
-    if (fused_pad)
+    if (G > 1)
+      HIP_TRY(run_stage_nhwc(eb, x, px, (int)d->n, (int)d->c, (int)d->h, (int)d->w, fused_pad ? (int)d->pad_t : 0,
+                             fused_pad ? (int)d->pad_l : 0, fused_pad ? (int)d->pad_b : 0,
+                             fused_pad ? (int)d->pad_r : 0, fused_pad ? d->pad_mode : 0, (int)cg, (int)cp, (int)G,
+                             ctx->stream),
+              "NCHW -> grouped NHWC");
+    else if (fused_pad)
       HIP_TRY(run_nchw_to_nhwc_pad(eb, x, px, (int)d->n, (int)d->c, (int)d->h, (int)d->w, (int)cp, (int)d->pad_t,
                                    (int)d->pad_l, (int)d->pad_b, (int)d->pad_r, (int)d->pad_mode, ctx->stream),
               "NCHW -> padded NHWC");
@@ -1095,42 +1132,42 @@ extern "C" int ohip_conv2d(ohip_ctx* ctx, const ohip_conv_desc* d, const void* x
     return fail(OHIP_E_INVALID, "ohip_conv2d: NHWC input must be 16-byte aligned");
   }
 
-  Im2colOperand col{};
-  col.base = xin; col.H = (int)sh_; col.W = (int)sw_; col.OH = (int)g.oh; col.OW = (int)g.ow;
-  col.KW = (int)d->kw; col.cpc = (int)(cp / ce);
-  col.sh = (int)d->stride_h; col.sw = (int)d->stride_w; col.dh = (int)d->dil_h; col.dw = (int)d->dil_w;
-  col.pt = fused_pad ? 0 : (int)d->pad_t; col.pl = fused_pad ? 0 : (int)d->pad_l;
-  col.rows = (int)rows; col.kc = w->kc;
-  col.xor_mask = 0; col.pad16 = pad16(ctx, 0);
-  DenseOperand wt{w->data, w->ld_bytes, (int)d->cout, w->kc, 0, 0u, pad16(ctx, 0)};
+  for (int64_t gi = 0; gi < G; ++gi) {
+    Im2colOperand col{};
+    col.base = static_cast<const char*>(xin) + gi * cp * eb;
+    col.H = (int)sh_; col.W = (int)sw_; col.OH = (int)g.oh; col.OW = (int)g.ow;
+    col.KW = (int)d->kw; col.cpc = (int)(cp / ce); col.pstride = (int)(cpt / ce);
+    col.sh = (int)d->stride_h; col.sw = (int)d->stride_w; col.dh = (int)d->dil_h; col.dw = (int)d->dil_w;
+    col.pt = fused_pad ? 0 : (int)d->pad_t; col.pl = fused_pad ? 0 : (int)d->pad_l;
+    col.rows = (int)rows; col.kc = w->kc;
+    col.xor_mask = 0; col.pad16 = pad16(ctx, 0);
+    DenseOperand wt{static_cast<const char*>(w->data) + gi * coutg * w->ld_bytes, w->ld_bytes, (int)coutg, w->kc,
+                    0, 0u, pad16(ctx, 0)};
 
-  FloatOut o{};
-  o.y = y; o.alpha = 1.0f; o.beta = 1.0f; o.bias = bias;
-  o.act = d->act; o.lo = d->act_lo; o.hi = d->act_hi;
-  if (o.act == ACT_CLIP) {
-    if (std::isnan(o.lo)) o.lo = -INFINITY;
-    if (std::isnan(o.hi)) o.hi = INFINITY;
-    if (!(o.lo <= o.hi)) o.act = ACT_NONE;
+    FloatOut o{};
+    o.alpha = 1.0f; o.beta = 1.0f;
+    o.bias = bias ? static_cast<const char*>(bias) + gi * coutg * eb : nullptr;
+    o.act = act; o.lo = lo; o.hi = hi;
+    bool col_on_x;
+    if (nchw_out) {
+      col_on_x = true;
+      o.y = static_cast<char*>(y) + gi * coutg * ohw * eb;
+      o.si = 1; o.sj = ohw; o.bstride = d->cout * ohw; o.ohw = (int)ohw; o.P = (int)rows; o.Q = (int)coutg;
+      o.vec = ohw % 4 == 0 && aligned(o.y, 4 * eb);
+      o.bias_mode = BIAS_J;
+    } else {
+      col_on_x = false;
+      o.y = static_cast<char*>(y) + gi * coutg * eb;
+      o.si = 1; o.sj = ldo; o.bstride = 0; o.ohw = INT_MAX; o.P = (int)coutg; o.Q = (int)rows;
+      o.vec = ldo % 4 == 0 && aligned(o.y, 4 * eb);
+      o.bias_mode = BIAS_I;
+    }
+    DENSE_FITS_OR_DECLINE(wt, "ohip_conv2d");
+    o.splits = splits;
+    o.split_ws = splits > 1 ? scratch_at(ctx, plan, iw) : nullptr;
+    hipError_t e = run_conv_float(d->dtype, col, wt, col_on_x, o, ctx->tile_override, ctx->stream);
+    if (e != hipSuccess) return hip_fail(e, "ohip_conv2d launch");
   }
-  const int64_t ohw = g.oh * g.ow;
-  bool col_on_x;
-  if (d->out_layout == OHIP_NCHW) {
-    col_on_x = true;
-    o.si = 1; o.sj = ohw; o.bstride = d->cout * ohw; o.ohw = (int)ohw; o.P = (int)rows; o.Q = (int)d->cout;
-    o.vec = ohw % 4 == 0 && aligned(y, 4 * eb);
-    o.bias_mode = BIAS_J;
-  } else {
-    col_on_x = false;
-    const int64_t ldo = round_up(d->cout, ce);
-    o.si = 1; o.sj = ldo; o.bstride = 0; o.ohw = INT_MAX; o.P = (int)d->cout; o.Q = (int)rows;
-    o.vec = ldo % 4 == 0 && aligned(y, 4 * eb);
-    o.bias_mode = BIAS_I;
-  }
-  DENSE_FITS_OR_DECLINE(wt, "ohip_conv2d");
-  o.splits = splits;
-  o.split_ws = splits > 1 ? scratch_at(ctx, plan, iw) : nullptr;
-  hipError_t e = run_conv_float(d->dtype, col, wt, col_on_x, o, ctx->tile_override, ctx->stream);
-  if (e != hipSuccess) return hip_fail(e, "ohip_conv2d launch");
   return OHIP_OK;
 }
 

@@ -196,8 +196,9 @@ class HipContext:
         return out
 
     def conv2d(self, x, w, bias=None, strides=(1, 1), pads=(0, 0, 0, 0), dilations=(1, 1), act=L.ACT_NONE,
-               act_lo=0.0, act_hi=0.0, in_layout=L.NCHW, out_layout=L.NCHW, out=None):
-        """pads = [top, left, bottom, right]; x NCHW (or NHWC channel-padded)."""
+               act_lo=0.0, act_hi=0.0, in_layout=L.NCHW, out_layout=L.NCHW, out=None, group=1):
+        """pads = [top, left, bottom, right]; x NCHW (or NHWC channel-padded);
+        w holds Cin / group input channels per filter (ONNX Conv's group)."""
         torch = _torch()
         dt = ohip_dtype(x.dtype)
         cout, cin, kh, kw = w.shape
@@ -205,7 +206,7 @@ class HipContext:
             n, c, h, wd = x.shape
         else:
             n, h, wd = x.shape[:3]
-            c = cin
+            c = cin * group
         oh = L.lib().ohip_conv_out_dim(h, pads[0], pads[2], kh, dilations[0], strides[0])
         ow = L.lib().ohip_conv_out_dim(wd, pads[1], pads[3], kw, dilations[1], strides[1])
         if oh < 0 or ow < 0:
@@ -216,7 +217,7 @@ class HipContext:
             else:
                 ce = 16 // L.ELEM_BYTES[dt]
                 out = torch.zeros((n, oh, ow, (cout + ce - 1) // ce * ce), dtype=x.dtype, device=x.device)
-        d = L.ConvDesc(n, c, h, wd, cout, kh, kw, 1, strides[0], strides[1], dilations[0], dilations[1],
+        d = L.ConvDesc(n, c, h, wd, cout, kh, kw, group, strides[0], strides[1], dilations[0], dilations[1],
                        pads[0], pads[1], pads[2], pads[3], dt, in_layout, out_layout, act, act_lo, act_hi)
         L.check(L.lib().ohip_conv2d(self.h, ctypes.byref(d), _ptr(x), w.handle, _ptr(bias), _ptr(out)))
         return out

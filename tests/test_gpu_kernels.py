@@ -45,12 +45,12 @@ def _dev(torch, a):
 
 
 # ------------------------------------------------------------------ float GEMM
-GEMM_SHAPES = [(1, 64, 32), (3, 100, 17), (8, 256, 64), (9, 64, 40), (33, 70, 45), (64, 64, 64),
+GEMM_SHAPES = [(1, 64, 32), (3, 100, 17), (8, 256, 64), (2, 5000, 40), (9, 64, 40), (33, 70, 45), (64, 64, 64),
                (128, 256, 384), (200, 136, 72), (256, 512, 520), (300, 1000, 129)]
 
 
 @pytest.mark.parametrize("mkn", GEMM_SHAPES, ids=str)
-@pytest.mark.parametrize("tile", list(range(11)))
+@pytest.mark.parametrize("tile", list(range(12)))
 def test_gemm_f32_matches_oracle(torch, ctx, mkn, tile):
     from oxionnx_amd import _lib as L
     m, k, n = mkn
@@ -162,6 +162,46 @@ def test_conv_f32_matches_oracle(torch, ctx, case, act):
     # activation's magnitude, not the accumulation's, so scale by the unclipped output
     scale = np.max(np.abs(O.conv(x, w, b, strides=s, pads=p, dilations=d)))
     assert np.max(np.abs(y.astype(np.float64) - want)) <= F32_TOL * scale
+
+
+# Grouped convolutions: (x shape, w shape, group, strides, pads, dilations).
+# Depthwise and narrow groups take the direct kernel, wide groups one MFMA
+# launch per group (channel slots per group padded to 16 bytes).
+GROUP_CASES = [
+    ((2, 8, 11, 13), (8, 1, 3, 3), 8, (1, 1), (1, 1, 1, 1), (1, 1)),        # depthwise
+    ((1, 6, 9, 9), (12, 1, 5, 5), 6, (2, 2), (2, 1, 2, 1), (1, 1)),         # depthwise, multiplier 2
+    ((1, 6, 10, 10), (4, 3, 3, 3), 2, (1, 1), (1, 1, 1, 1), (2, 2)),        # narrow groups, dilated
+    ((2, 64, 12, 12), (64, 16, 3, 3), 4, (1, 1), (1, 1, 1, 1), (1, 1)),     # MFMA per group, aligned
+    ((1, 40, 9, 9), (48, 20, 3, 3), 2, (2, 2), (0, 1, 1, 0), (1, 1)),       # MFMA per group, padded slots
+]
+
+
+@pytest.mark.parametrize("case", GROUP_CASES, ids=lambda c: f"{c[0]}x{c[1]}g{c[2]}")
+@pytest.mark.parametrize("dt", ["f32", "f16"])
+def test_grouped_conv_matches_oracle(torch, ctx, case, dt):
+    from oxionnx_amd import _lib as L
+    xs, ws, grp, s, p, d = case
+    rng = np.random.default_rng(sum(xs) + sum(ws) + grp)
+    x = rng.uniform(-1, 1, xs).astype(np.float32)
+    w = rng.normal(0, 0.2, ws).astype(np.float32)
+    b = rng.normal(0, 0.1, ws[0]).astype(np.float32)
+    if dt == "f32":
+        wt = ctx.weight_conv(w)
+        y = ctx.conv2d(_dev(torch, x), wt, _dev(torch, b), strides=s, pads=p, dilations=d, group=grp,
+                       act=L.ACT_RELU).cpu().numpy()
+        want = O.conv(x, w, b, activation="relu", strides=s, pads=p, dilations=d, group=grp)
+        scale = max(1.0, float(np.max(np.abs(want))))
+        assert y.shape == want.shape
+        assert np.max(np.abs(y.astype(np.float64) - want)) <= F32_TOL * scale
+    else:
+        xh, wh, bh = (O.f32_to_half_bits(v) for v in (x, w, b))
+        wt = ctx.weight_conv(O.half_bits_to_f32(wh), dtype=L.F16)
+        xt = torch.from_numpy(xh.view(np.int16)).cuda().view(torch.float16)
+        bt = torch.from_numpy(bh.view(np.int16)).cuda().view(torch.float16)
+        y = ctx.conv2d(xt, wt, bt, strides=s, pads=p, dilations=d, group=grp)
+        got = O.half_bits_to_f32(y.view(torch.int16).cpu().numpy().view(np.uint16))
+        want = O.half_bits_to_f32(O.conv_half(xh, wh, bh, strides=s, pads=p, dilations=d, group=grp))
+        assert _rel_err(got, want) <= HALF_TOL
 
 
 @pytest.mark.parametrize("c", [c for c in G.cases("Conv") + G.cases("Conv1D")
