@@ -454,6 +454,76 @@ hipError_t run_conv_direct(int dtype, const void* x, const void* w, const void* 
   return hipGetLastError();
 }
 
+// Integer counterpart for narrow groups: exact int32 sum of
+// (x - x_zp) * (w - w_zp) over the group's taps (padding taps skipped, as in
+// integer_conv), the packed filter decoded as stored (two int8 halves when
+// the rows are split, negated for a flipped channel), + bias, then the
+// output kind's epilogue: raw int32, or requantisation (f64 product with the
+// f32 combined scale, + y_zp, round half to even, clamp), optionally mapped
+// through the 256-entry byte table, stored as a byte or as an f32 lane.
+__global__ void __launch_bounds__(256)
+qconv_direct_kernel(const uint8_t* __restrict__ x, const int8_t* __restrict__ w, void* __restrict__ y,
+                    DirectQConvArgs a) {
+#pragma clang fp contract(off)
+  const int64_t total = (int64_t)a.N * a.cout * a.OH * a.OW;
+  for (int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x; idx < total; idx += (int64_t)gridDim.x * 256) {
+    int64_t r = idx;
+    const int ox = (int)(r % a.OW); r /= a.OW;
+    const int oy = (int)(r % a.OH); r /= a.OH;
+    const int co = (int)(r % a.cout);
+    const int n = (int)(r / a.cout);
+    const int g = co / a.coutg;
+    const uint8_t* xg = x + ((int64_t)n * a.C + (int64_t)g * a.cg) * a.H * a.W;
+    const int8_t* wr = w + (int64_t)co * a.ldw;
+    int32_t acc = 0;
+    for (int ci = 0; ci < a.cg; ++ci) {
+      const uint8_t* xc = xg + (int64_t)ci * a.H * a.W;
+      for (int ky = 0; ky < a.KH; ++ky) {
+        const int iy = oy * a.sh - a.pt + ky * a.dh;
+        if ((unsigned)iy >= (unsigned)a.H) continue;
+        for (int kx = 0; kx < a.KW; ++kx) {
+          const int ix = ox * a.sw - a.pl + kx * a.dw;
+          if ((unsigned)ix >= (unsigned)a.W) continue;
+          const uint8_t raw = xc[(int64_t)iy * a.W + ix];
+          const int32_t xv = (a.x_signed ? (int32_t)(int8_t)raw : (int32_t)raw) - a.x_zp;
+          const int64_t k = (int64_t)(ky * a.KW + kx) * a.cpg + ci;
+          int32_t v = wr[k];
+          if (a.half) v += wr[a.half + k];
+          acc += xv * v;
+        }
+      }
+    }
+    if (a.flip && a.flip[co]) acc = -acc;
+    if (a.bias) acc += a.bias[co];
+    const int64_t o = a.nhwc_out ? (((int64_t)n * a.OH + oy) * a.OW + ox) * a.ldo + co
+                                 : (((int64_t)n * a.cout + co) * a.OH + oy) * a.OW + ox;
+    if (a.out_kind == QOUT_I32) {
+      reinterpret_cast<int32_t*>(y)[o] = acc;
+      continue;
+    }
+    double d = (double)acc * (double)a.comb[a.n_comb > 1 ? co : 0];
+    d = d + (double)a.y_zp;
+    d = __builtin_rint(d);
+    d = d < (double)a.lo ? (double)a.lo : d;
+    d = d > (double)a.hi ? (double)a.hi : d;
+    const int32_t q = (int32_t)d;
+    if (a.out_kind == QOUT_F32) {
+      reinterpret_cast<float*>(y)[o] = (float)q;
+    } else {
+      reinterpret_cast<uint8_t*>(y)[o] = a.table ? a.table[q & 0xff] : (uint8_t)(q & 0xff);
+    }
+  }
+}
+
+hipError_t run_qconv_direct(const void* x, const void* w, void* y, const DirectQConvArgs& a, hipStream_t st) {
+  const int64_t total = (int64_t)a.N * a.cout * a.OH * a.OW;
+  if (total <= 0) return hipSuccess;
+  const unsigned grid = (unsigned)std::min<int64_t>((total + 255) / 256, 65535 * 16);
+  hipLaunchKernelGGL(qconv_direct_kernel, dim3(grid), dim3(256), 0, st, reinterpret_cast<const uint8_t*>(x),
+                     reinterpret_cast<const int8_t*>(w), y, a);
+  return hipGetLastError();
+}
+
 // dst[r][c] = c < K ? src[r * rs + c * cs] : 0 for a [R][ld] destination: pads a
 // row-major operand to whole 16-byte chunks, or materialises a transpose.
 template <class T>

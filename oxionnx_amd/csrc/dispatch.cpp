@@ -605,7 +605,7 @@ int do_qconv(ohip_ctx* ctx, const ohip_node* nd, bool qlinear, int placement, oh
   Geo g;
   std::string why;
   if (!conv_geometry(nd, x, w, &g, &why)) return decline(why);
-  if (g.group != 1) return decline("integer Conv: group != 1");
+  const int64_t cg = g.c / g.group;
   std::vector<int32_t> xzp, wzp, yzp;
   if (!zp_lanes(xzp_t, xzp) || !zp_lanes(wzp_t, wzp)) return decline("integer Conv: zero point");
   if (wzp.size() != 1 && (int64_t)wzp.size() != g.cout) return decline("integer Conv: w_zero_point length");
@@ -657,7 +657,7 @@ int do_qconv(ohip_ctx* ctx, const ohip_node* nd, bool qlinear, int placement, oh
   }
   ohip_tuning tun;
   ohip_get_tuning(ctx, &tun);
-  if (!ohip_conv_admits(&tun, g.cout, g.c * g.kh * g.kw, g.n * g.oh * g.ow)) return decline("integer Conv: gate");
+  if (!ohip_conv_admits(&tun, g.cout, cg * g.kh * g.kw, g.n * g.oh * g.ow)) return decline("integer Conv: gate");
   std::vector<uint8_t> xb, wb;
   int xdt, wdt;
   if (x->device) xdt = x->dtype;
@@ -667,7 +667,7 @@ int do_qconv(ohip_ctx* ctx, const ohip_node* nd, bool qlinear, int placement, oh
   std::string name = wkey_name(w), label = std::string(qlinear ? "QLinearConv.W" : "ConvInteger.W");
   ohip_weight_key key{name.c_str(), label.c_str()};
   ohip_weight* wt = nullptr;
-  int rc = ohip_weight_qconv(ctx, cache ? &key : nullptr, wdt, wb.data(), g.cout, g.c, g.kh, g.kw, wzp.data(),
+  int rc = ohip_weight_qconv(ctx, cache ? &key : nullptr, wdt, wb.data(), g.cout, cg, g.kh, g.kw, wzp.data(),
                              (int)wzp.size(), qlinear ? ws.data() : nullptr, qlinear ? (int)ws.size() : 0, &wt);
   if (rc) return rc;
   Stage st(ctx);
@@ -677,7 +677,7 @@ int do_qconv(ohip_ctx* ctx, const ohip_node* nd, bool qlinear, int placement, oh
   const size_t obytes = (size_t)(g.n * g.cout * g.oh * g.ow) * ob;
   void* yd = st.alloc(obytes);
   if (!xd || !yd || (bias && !bd)) { if (!cache) ohip_weight_release(wt); return OHIP_E_NOMEM; }
-  ohip_qconv_desc d{g.n, g.c, g.h, g.w, g.cout, g.kh, g.kw, 1, g.sh, g.sw, g.dh, g.dw, g.pt, g.pl, g.pb, g.pr,
+  ohip_qconv_desc d{g.n, g.c, g.h, g.w, g.cout, g.kh, g.kw, g.group, g.sh, g.sw, g.dh, g.dw, g.pt, g.pl, g.pb, g.pr,
                     xdt, xzp[0], out_kind, xs, ys, qlinear ? yzp[0] : 0, lo, hi,
                     OHIP_NCHW, OHIP_NCHW, fused ? table : nullptr};
   rc = ohip_qconv2d(ctx, &d, xd, wt, static_cast<const int32_t*>(bd), yd);

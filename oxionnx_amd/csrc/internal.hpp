@@ -127,6 +127,28 @@ struct DirectConvArgs {
 hipError_t run_conv_direct(int dtype, const void* x, const void* w, const void* bias, void* y,
                            const DirectConvArgs& a, hipStream_t st);
 
+// Direct (non-MFMA) grouped integer convolution; see qconv_direct_kernel.
+struct DirectQConvArgs {
+  int N, C, H, W, cout, cg, coutg, KH, KW;
+  int sh, sw, dh, dw, pt, pl;
+  int OH, OW;
+  int64_t ldw;       // bytes between packed filter rows
+  int cpg;           // channel slots per tap in the packed filter
+  int64_t half;      // bytes to a split row's second half (0: rows are not split)
+  int x_signed;      // X is int8 (else uint8)
+  int32_t x_zp;
+  const int8_t* flip;    // per output channel, may be null
+  const int32_t* bias;   // per output channel, may be null
+  const float* comb;     // combined scales (n_comb == 1: per tensor)
+  int n_comb;
+  int out_kind;          // QOUT_*
+  int32_t y_zp, lo, hi;
+  const uint8_t* table;  // may be null
+  int nhwc_out;
+  int64_t ldo;
+};
+hipError_t run_qconv_direct(const void* x, const void* w, void* y, const DirectQConvArgs& a, hipStream_t st);
+
 // NCHW -> NHWC staging with per-group channel slots and an optional
 // reflect (1) / edge (2) spatial border; see stage_nhwc_kernel.
 hipError_t run_stage_nhwc(int elem_bytes, const void* src, void* dst, int N, int C, int H, int W, int pt, int pl,

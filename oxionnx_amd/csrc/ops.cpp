@@ -1260,20 +1260,29 @@ extern "C" int ohip_qconv2d(ohip_ctx* ctx, const ohip_qconv_desc* d, const void*
   int rc = activate(ctx);
   if (rc) return rc;
   if (!d || !x || !w || !y) return fail(OHIP_E_INVALID, "ohip_qconv2d: null argument");
-  if (d->group != 1) return fail(OHIP_DECLINED, "ohip_qconv2d: group != 1 is not handled");
+  if (d->group < 1 || d->c % d->group || d->cout % d->group) return fail(OHIP_E_SHAPE, "ohip_qconv2d: bad group");
   if (w->kind != WK_QCONV) return fail(OHIP_E_INVALID, "ohip_qconv2d: weight kind mismatch");
   if (d->x_dtype != OHIP_U8 && d->x_dtype != OHIP_I8) return fail(OHIP_E_INVALID, "ohip_qconv2d: X must be u8/i8");
-  if (w->rows != d->cout || w->k != d->c || w->kh != d->kh || w->kw != d->kw)
+  const int64_t G = d->group, cg = d->c / G, coutg = d->cout / G;
+  if (w->rows != d->cout || w->k != cg || w->kh != d->kh || w->kw != d->kw)
     return fail(OHIP_E_SHAPE, "ohip_qconv2d: shape disagrees with the packed filter");
-  if (d->c * d->kh * d->kw > kMaxExactK) return fail(OHIP_DECLINED, "ohip_qconv2d: K too large for exact int32");
+  if (cg * d->kh * d->kw > kMaxExactK) return fail(OHIP_DECLINED, "ohip_qconv2d: K too large for exact int32");
   ConvGeo g;
   rc = conv_geo(d->h, d->w, d->kh, d->kw, d->stride_h, d->stride_w, d->dil_h, d->dil_w, d->pad_t, d->pad_l,
                 d->pad_b, d->pad_r, &g);
   if (rc) return rc;
-  const int64_t cp = round_up(d->c, 16);
+  const int64_t cp = round_up(cg, 16);   // channel slots per group and tap
+  const int64_t cpt = G * cp;            // channel slots per staged pixel
   const int64_t rows = d->n * g.oh * g.ow;
   if (rows > INT_MAX / 2) return fail(OHIP_DECLINED, "ohip_qconv2d: extent too large");
   if (rows == 0) return OHIP_OK;
+  // narrow groups (depthwise and the like) run the exact direct kernel on the
+  // NCHW input; wider groups run one MFMA launch per group
+  const bool direct = G > 1 && (coutg < 16 || cg * d->kh * d->kw < 32 || G > 64);
+  if (G > 1 && d->in_layout != OHIP_NCHW && (direct || cg % 16 != 0))
+    return fail(OHIP_DECLINED, "ohip_qconv2d: this grouped convolution needs an NCHW input");
+  if (d->out_table && d->out_kind != OHIP_QOUT_U8 && d->out_kind != OHIP_QOUT_I8)
+    return fail(OHIP_E_INVALID, "ohip_qconv2d: an output table needs a byte output");
   std::lock_guard<std::mutex> lock(ctx->mu);
   ctx->counters.dispatches++;
   const bool u8 = d->x_dtype == OHIP_U8;
@@ -1283,11 +1292,35 @@ extern "C" int ohip_qconv2d(ohip_ctx* ctx, const ohip_qconv_desc* d, const void*
     rc = ensure_comb(ctx, const_cast<ohip_weight*>(w), d->x_scale, d->y_scale, &n_comb);
     if (rc) return rc;
   }
+  const uint8_t* table = nullptr;
+  if (d->out_table) {
+    rc = device_table(ctx, d->out_table, &table);
+    if (rc) return rc;
+  }
+  const int ob = (d->out_kind == OHIP_QOUT_I32 || d->out_kind == OHIP_QOUT_F32) ? 4 : 1;
+  const int64_t ohw = g.oh * g.ow;
+  const int64_t ldo = ob == 1 ? round_up(d->cout, 16) : round_up(d->cout, 4);
+  const bool nchw_out = d->out_layout == OHIP_NCHW;
+
+  if (direct) {
+    DirectQConvArgs a{};
+    a.N = (int)d->n; a.C = (int)d->c; a.H = (int)d->h; a.W = (int)d->w; a.cout = (int)d->cout;
+    a.cg = (int)cg; a.coutg = (int)coutg; a.KH = (int)d->kh; a.KW = (int)d->kw;
+    a.sh = (int)d->stride_h; a.sw = (int)d->stride_w; a.dh = (int)d->dil_h; a.dw = (int)d->dil_w;
+    a.pt = (int)d->pad_t; a.pl = (int)d->pad_l; a.OH = (int)g.oh; a.OW = (int)g.ow;
+    a.ldw = w->ld_bytes; a.cpg = (int)cp; a.half = w->kwrap > 0 ? (int64_t)w->kwrap * 16 : 0;
+    a.x_signed = !u8; a.x_zp = d->x_zp; a.flip = w->flip; a.bias = bias; a.comb = w->comb; a.n_comb = n_comb;
+    a.out_kind = d->out_kind; a.y_zp = d->y_zp; a.lo = d->lo; a.hi = d->hi; a.table = table;
+    a.nhwc_out = !nchw_out; a.ldo = ldo;
+    hipError_t e = run_qconv_direct(x, w->data, y, a, ctx->stream);
+    if (e != hipSuccess) return hip_fail(e, "ohip_qconv2d direct launch");
+    return OHIP_OK;
+  }
+
   ScratchPlan plan;
   const bool stage = d->in_layout == OHIP_NCHW;
-  size_t ix = stage ? plan.add((size_t)(d->n * d->h * d->w * cp)) : SIZE_MAX;
-  const bool nchw_out = d->out_layout == OHIP_NCHW;
-  const int sP = nchw_out ? (int)rows : (int)d->cout, sQ = nchw_out ? (int)d->cout : (int)rows;
+  size_t ix = stage ? plan.add((size_t)(d->n * d->h * d->w * cpt)) : SIZE_MAX;
+  const int sP = nchw_out ? (int)rows : (int)coutg, sQ = nchw_out ? (int)coutg : (int)rows;
   const int splits = plan_splits(sP, sQ, w->kc, ctx->tile_override);
   size_t iw = splits > 1 ? plan.add(split_ws_bytes(sP, sQ, splits)) : SIZE_MAX;
   rc = scratch_reserve(ctx, plan.total());
@@ -1295,55 +1328,62 @@ extern "C" int ohip_qconv2d(ohip_ctx* ctx, const ohip_qconv_desc* d, const void*
   const void* xin = x;
   if (stage) {
     void* px = scratch_at(ctx, plan, ix);
-    HIP_TRY(run_nchw_to_nhwc(1, x, px, (int)d->n, (int)d->c, (int)(d->h * d->w), (int)cp, ctx->stream),
-            "NCHW -> NHWC");
+    if (G > 1)
+      HIP_TRY(run_stage_nhwc(1, x, px, (int)d->n, (int)d->c, (int)d->h, (int)d->w, 0, 0, 0, 0, 0, (int)cg, (int)cp,
+                             (int)G, ctx->stream),
+              "NCHW -> grouped NHWC");
+    else
+      HIP_TRY(run_nchw_to_nhwc(1, x, px, (int)d->n, (int)d->c, (int)(d->h * d->w), (int)cp, ctx->stream),
+              "NCHW -> NHWC");
     xin = px;
   } else if (!aligned(x, 16)) {
     return fail(OHIP_E_INVALID, "ohip_qconv2d: NHWC input must be 16-byte aligned");
   }
   // A padding tap stands for x == x_zp, i.e. (x_zp - shift) in the shifted
   // int8 domain, so it contributes exactly zero after the ca correction.  The
-  // pad source is read before the XOR, so it holds the raw byte x_zp.
+  // pad source is read before the XOR, so it holds the raw byte x_zp.  The
+  // channel-padding slots of the staged input meet zero filter entries.
   const uint8_t padb = (uint8_t)(d->x_zp & 0xff);
-  Im2colOperand col{};
-  col.base = xin; col.H = (int)d->h; col.W = (int)d->w; col.OH = (int)g.oh; col.OW = (int)g.ow;
-  col.KW = (int)d->kw; col.cpc = (int)(cp / 16);
-  col.sh = (int)d->stride_h; col.sw = (int)d->stride_w; col.dh = (int)d->dil_h; col.dw = (int)d->dil_w;
-  col.pt = (int)d->pad_t; col.pl = (int)d->pad_l; col.rows = (int)rows;
-  col.kc = w->kwrap > 0 ? w->kreal : w->kc; col.kwrap = w->kwrap;
-  col.xor_mask = u8 ? 0x80808080u : 0u;
-  col.pad16 = pad16(ctx, padb);
-  DenseOperand wt{w->data, w->ld_bytes, (int)d->cout, w->kc, 0, 0u, pad16(ctx, 0)};
-  QuantOut o{};
-  o.y = y; o.colsum = w->colsum; o.flip = w->flip; o.bias = bias; o.ca = shift - d->x_zp; o.ca_rows = nullptr;
-  o.comb = w->comb; o.n_comb = n_comb; o.out_kind = d->out_kind; o.y_zp = d->y_zp; o.lo = d->lo; o.hi = d->hi;
-  o.table = nullptr;
-  if (d->out_table) {
-    if (d->out_kind != OHIP_QOUT_U8 && d->out_kind != OHIP_QOUT_I8)
-      return fail(OHIP_E_INVALID, "ohip_qconv2d: an output table needs a byte output");
-    rc = device_table(ctx, d->out_table, &o.table);
-    if (rc) return rc;
+  for (int64_t gi = 0; gi < G; ++gi) {
+    Im2colOperand col{};
+    col.base = static_cast<const char*>(xin) + gi * cp;
+    col.H = (int)d->h; col.W = (int)d->w; col.OH = (int)g.oh; col.OW = (int)g.ow;
+    col.KW = (int)d->kw; col.cpc = (int)(cp / 16); col.pstride = (int)(cpt / 16);
+    col.sh = (int)d->stride_h; col.sw = (int)d->stride_w; col.dh = (int)d->dil_h; col.dw = (int)d->dil_w;
+    col.pt = (int)d->pad_t; col.pl = (int)d->pad_l; col.rows = (int)rows;
+    col.kc = w->kwrap > 0 ? w->kreal : w->kc; col.kwrap = w->kwrap;
+    col.xor_mask = u8 ? 0x80808080u : 0u;
+    col.pad16 = pad16(ctx, padb);
+    DenseOperand wt{static_cast<const char*>(w->data) + gi * coutg * w->ld_bytes, w->ld_bytes, (int)coutg, w->kc,
+                    0, 0u, pad16(ctx, 0)};
+    QuantOut o{};
+    o.colsum = w->colsum + gi * coutg;
+    o.flip = w->flip ? w->flip + gi * coutg : nullptr;
+    o.bias = bias ? bias + gi * coutg : nullptr;
+    o.ca = shift - d->x_zp; o.ca_rows = nullptr;
+    o.comb = (n_comb > 1 && w->comb) ? w->comb + gi * coutg : w->comb;
+    o.n_comb = n_comb; o.out_kind = d->out_kind; o.y_zp = d->y_zp; o.lo = d->lo; o.hi = d->hi;
+    o.table = table;
+    bool col_on_x;
+    if (nchw_out) {
+      col_on_x = true;
+      o.y = static_cast<char*>(y) + gi * coutg * ohw * ob;
+      o.si = 1; o.sj = ohw; o.bstride = d->cout * ohw; o.ohw = (int)ohw; o.P = (int)rows; o.Q = (int)coutg;
+      o.vec = ohw % 4 == 0 && aligned(o.y, 4 * ob);
+      o.w_on_i = 0;
+    } else {
+      col_on_x = false;
+      o.y = static_cast<char*>(y) + gi * coutg * ob;
+      o.si = 1; o.sj = ldo; o.bstride = 0; o.ohw = INT_MAX; o.P = (int)coutg; o.Q = (int)rows;
+      o.vec = ldo % 4 == 0 && aligned(o.y, 4 * ob);
+      o.w_on_i = 1;
+    }
+    DENSE_FITS_OR_DECLINE(wt, "ohip_qconv2d");
+    o.splits = splits;
+    o.split_ws = splits > 1 ? scratch_at(ctx, plan, iw) : nullptr;
+    hipError_t e = run_conv_quant(col, wt, col_on_x, o, ctx->tile_override, ctx->stream);
+    if (e != hipSuccess) return hip_fail(e, "ohip_qconv2d launch");
   }
-  const int ob = (d->out_kind == OHIP_QOUT_I32 || d->out_kind == OHIP_QOUT_F32) ? 4 : 1;
-  const int64_t ohw = g.oh * g.ow;
-  bool col_on_x;
-  if (d->out_layout == OHIP_NCHW) {
-    col_on_x = true;
-    o.si = 1; o.sj = ohw; o.bstride = d->cout * ohw; o.ohw = (int)ohw; o.P = (int)rows; o.Q = (int)d->cout;
-    o.vec = ohw % 4 == 0 && aligned(y, 4 * ob);
-    o.w_on_i = 0;
-  } else {
-    col_on_x = false;
-    const int64_t ldo = ob == 1 ? round_up(d->cout, 16) : round_up(d->cout, 4);
-    o.si = 1; o.sj = ldo; o.bstride = 0; o.ohw = INT_MAX; o.P = (int)d->cout; o.Q = (int)rows;
-    o.vec = ldo % 4 == 0 && aligned(y, 4 * ob);
-    o.w_on_i = 1;
-  }
-  DENSE_FITS_OR_DECLINE(wt, "ohip_qconv2d");
-  o.splits = splits;
-  o.split_ws = splits > 1 ? scratch_at(ctx, plan, iw) : nullptr;
-  hipError_t e = run_conv_quant(col, wt, col_on_x, o, ctx->tile_override, ctx->stream);
-  if (e != hipSuccess) return hip_fail(e, "ohip_qconv2d launch");
   return OHIP_OK;
 }
 

@@ -238,14 +238,14 @@ class HipContext:
 
     def qconv2d(self, x, w, bias=None, x_zp=0, out_kind=L.QOUT_U8, x_scale=1.0, y_scale=1.0, y_zp=0, lo=0,
                 hi=255, strides=(1, 1), pads=(0, 0, 0, 0), dilations=(1, 1), in_layout=L.NCHW,
-                out_layout=L.NCHW, out=None):
+                out_layout=L.NCHW, out=None, group=1):
         torch = _torch()
         cout, cin, kh, kw = w.shape
         if in_layout == L.NCHW:
             n, c, h, wd = x.shape
         else:
             n, h, wd = x.shape[:3]
-            c = cin
+            c = cin * group
         oh = L.lib().ohip_conv_out_dim(h, pads[0], pads[2], kh, dilations[0], strides[0])
         ow = L.lib().ohip_conv_out_dim(wd, pads[1], pads[3], kw, dilations[1], strides[1])
         if oh < 0 or ow < 0:
@@ -258,7 +258,7 @@ class HipContext:
             else:
                 ld = (cout + 15) // 16 * 16 if out_kind in (L.QOUT_U8, L.QOUT_I8) else (cout + 3) // 4 * 4
                 out = torch.zeros((n, oh, ow, ld), dtype=odt, device=x.device)
-        d = L.QConvDesc(n, c, h, wd, cout, kh, kw, 1, strides[0], strides[1], dilations[0], dilations[1],
+        d = L.QConvDesc(n, c, h, wd, cout, kh, kw, group, strides[0], strides[1], dilations[0], dilations[1],
                         pads[0], pads[1], pads[2], pads[3], ohip_dtype(x.dtype), int(x_zp), out_kind, x_scale,
                         y_scale, y_zp, lo, hi, in_layout, out_layout)
         L.check(L.lib().ohip_qconv2d(self.h, ctypes.byref(d), _ptr(x), w.handle, _ptr(bias), _ptr(out)))

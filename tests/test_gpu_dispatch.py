@@ -77,10 +77,7 @@ QUANT = G.cases("MatMulInteger") + G.cases("QLinearMatMul") + G.cases("ConvInteg
 
 @pytest.mark.parametrize("c", QUANT, ids=lambda c: c["name"])
 def test_quantized_golden_through_the_boundary(ctx, c):
-    out = _run(ctx, c)
-    if c["attrs"].get("group", 1) != 1:
-        assert out is None, "grouped convolutions are declined to the CPU operator"
-        return
+    out = _run(ctx, c)   # grouped (depthwise) convolutions included
     assert out is not None, ctx.last_decline()
     assert list(out[0].shape) == c["shape"]
     assert out[0].dtype == np.float32

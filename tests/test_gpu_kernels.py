@@ -204,16 +204,16 @@ def test_grouped_conv_matches_oracle(torch, ctx, case, dt):
         assert _rel_err(got, want) <= HALF_TOL
 
 
-@pytest.mark.parametrize("c", [c for c in G.cases("Conv") + G.cases("Conv1D")
-                               if c["attrs"].get("group", 1) == 1], ids=lambda c: c["name"])
+@pytest.mark.parametrize("c", G.cases("Conv") + G.cases("Conv1D"), ids=lambda c: c["name"])
 def test_conv_golden_vectors(torch, ctx, c):
     x, w, b = G.conv_inputs(c)
     attrs = G.conv_attrs(c)
+    grp = c["attrs"].get("group", 1)
     s, p, d, out_shape = O.conv_geometry(x.shape, w.shape, attrs.get("strides"), attrs.get("pads"),
-                                         attrs.get("dilations"), 1, attrs.get("auto_pad", "NOTSET"))
+                                         attrs.get("dilations"), grp, attrs.get("auto_pad", "NOTSET"))
     wt = ctx.weight_conv(w)
     y = ctx.conv2d(_dev(torch, x), wt, None if b is None else _dev(torch, b), strides=s, pads=p,
-                   dilations=d).cpu().numpy()
+                   dilations=d, group=grp).cpu().numpy()
     np.testing.assert_allclose(y.ravel(), np.asarray(c["expected"], np.float32), atol=c["tol"])
 
 
@@ -383,8 +383,34 @@ def test_conv_integer_bit_exact(torch, ctx, case):
     np.testing.assert_array_equal(y.cpu().numpy(), want)
 
 
-@pytest.mark.parametrize("c", [c for c in G.cases("ConvInteger") + G.cases("QLinearConv")
-                               if c["attrs"].get("group", 1) == 1], ids=lambda c: c["name"])
+@pytest.mark.parametrize("case", GROUP_CASES, ids=lambda c: f"{c[0]}x{c[1]}g{c[2]}")
+@pytest.mark.parametrize("wzp", [3, -128], ids=["split_rows", "flipped_channels"])
+def test_grouped_integer_conv_bit_exact(torch, ctx, case, wzp):
+    """Grouped / depthwise ConvInteger and QLinearConv against integer_conv.
+    w_zp 3 pushes w - w_zp past int8 (the packed rows split in two halves);
+    w_zp -128 pushes it past 254 (the channel is stored negated)."""
+    from oxionnx_amd import _lib as L
+    xs, ws, grp, s, p, d = case
+    rng = np.random.default_rng(sum(xs) + sum(ws) + grp + abs(wzp))
+    x = rng.integers(0, 256, xs).astype(np.uint8)
+    w = rng.integers(-127, 128, ws).astype(np.int8)
+    w.flat[0] = 127
+    wt = ctx.weight_qconv(w, zp=wzp, scale=rng.uniform(0.001, 0.01, ws[0]).astype(np.float32))
+    y = ctx.qconv2d(_dev(torch, x), wt, x_zp=100, out_kind=L.QOUT_I32, strides=s, pads=p, dilations=d,
+                    group=grp)
+    want = O.conv_integer(x, w, 100, wzp, strides=s, pads=p, dilations=d, group=grp)
+    np.testing.assert_array_equal(y.cpu().numpy(), want)
+    bias = rng.integers(-5000, 5000, ws[0]).astype(np.int32)
+    ws_ = rng.uniform(0.001, 0.01, ws[0]).astype(np.float32)
+    wt = ctx.weight_qconv(w, zp=wzp, scale=ws_)
+    y = ctx.qconv2d(_dev(torch, x), wt, _dev(torch, bias), x_zp=100, out_kind=L.QOUT_U8, x_scale=0.02,
+                    y_scale=0.05, y_zp=128, lo=0, hi=255, strides=s, pads=p, dilations=d, group=grp)
+    want = O.qlinear_conv(x, 0.02, 100, w, ws_, wzp, 0.05, 128, bias, strides=s, pads=p, dilations=d,
+                          group=grp)
+    np.testing.assert_array_equal(y.cpu().numpy().astype(np.float32), want)
+
+
+@pytest.mark.parametrize("c", G.cases("ConvInteger") + G.cases("QLinearConv"), ids=lambda c: c["name"])
 def test_integer_conv_golden_vectors(torch, ctx, c):
     from oxionnx_amd import _lib as L
     dts = c["dtypes"]
@@ -392,14 +418,16 @@ def test_integer_conv_golden_vectors(torch, ctx, c):
     x = G.arr(c, "x").astype(npdt[dts["x"]])
     w = G.arr(c, "w").astype(npdt[dts["w"]])
     attrs = G.conv_attrs(c)
+    grp = c["attrs"].get("group", 1)
     s, p, d, _ = O.conv_geometry(x.shape, w.shape, attrs.get("strides"), attrs.get("pads"),
-                                 attrs.get("dilations"), 1, attrs.get("auto_pad", "NOTSET"))
+                                 attrs.get("dilations"), grp, attrs.get("auto_pad", "NOTSET"))
     g = lambda nm: G.arr(c, nm)
     xzp = int(g("x_zp")[0]) if g("x_zp") is not None else 0
     wzp = g("w_zp").astype(np.int32) if g("w_zp") is not None else np.array([0], np.int32)
     if c["op"] == "ConvInteger":
         wt = ctx.weight_qconv(w, zp=wzp)
-        y = ctx.qconv2d(_dev(torch, x), wt, x_zp=xzp, out_kind=L.QOUT_I32, strides=s, pads=p, dilations=d)
+        y = ctx.qconv2d(_dev(torch, x), wt, x_zp=xzp, out_kind=L.QOUT_I32, strides=s, pads=p, dilations=d,
+                        group=grp)
         assert y.cpu().numpy().ravel().tolist() == c["expected"]
         return
     lo, hi = O.satrange_infer(g("y_zp"), [xzp])
@@ -408,7 +436,7 @@ def test_integer_conv_golden_vectors(torch, ctx, c):
     bias = None if g("b") is None else _dev(torch, g("b").astype(np.int32))
     y = ctx.qconv2d(_dev(torch, x), wt, bias, x_zp=xzp, out_kind=kind,
                     x_scale=float(g("x_scale")[0]), y_scale=float(g("y_scale")[0]), y_zp=int(g("y_zp")[0]),
-                    lo=lo, hi=hi, strides=s, pads=p, dilations=d)
+                    lo=lo, hi=hi, strides=s, pads=p, dilations=d, group=grp)
     assert y.cpu().numpy().astype(np.float32).ravel().tolist() == c["expected"]
 
 
