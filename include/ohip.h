@@ -141,7 +141,7 @@ typedef struct {
  * src_dtype (F32/F16/BF16), converted to dtype (F32/F16/BF16, RNE). */
 int ohip_weight_gemm(ohip_ctx* ctx, const ohip_weight_key* key, int src_dtype, const void* host,
                      int64_t k, int64_t n, int trans_b, int dtype, ohip_weight** out);
-/* Float Conv filter: host [Cout, Cin/group, KH, KW] (group 1). */
+/* Float Conv filter: host [Cout, Cin/group, KH, KW]. */
 int ohip_weight_conv(ohip_ctx* ctx, const ohip_weight_key* key, int src_dtype, const void* host,
                      int64_t cout, int64_t cin, int64_t kh, int64_t kw, int dtype, ohip_weight** out);
 /* Integer GEMM operand B of MatMulInteger / QLinearMatMul
@@ -157,6 +157,11 @@ int ohip_weight_qgemm(ohip_ctx* ctx, const ohip_weight_key* key, int src_dtype, 
 int ohip_weight_qconv(ohip_ctx* ctx, const ohip_weight_key* key, int src_dtype, const void* host,
                       int64_t cout, int64_t cin, int64_t kh, int64_t kw, const int32_t* zp, int n_zp,
                       const float* scale, int n_scale, ohip_weight** out);
+/* Float ConvTranspose filter: host [Cin, Cout/group, KH, KW] of src_dtype,
+ * converted to dtype and kept in that layout (conv/transpose.rs:78-214). */
+int ohip_weight_conv_transpose(ohip_ctx* ctx, const ohip_weight_key* key, int src_dtype, const void* host,
+                               int64_t cin, int64_t cout_per_group, int64_t kh, int64_t kw, int dtype,
+                               ohip_weight** out);
 void ohip_weight_release(ohip_weight* w);
 size_t ohip_weight_bytes(const ohip_weight* w);
 
@@ -179,8 +184,10 @@ typedef struct {
 int ohip_gemm(ohip_ctx* ctx, const ohip_gemm_desc* d, const void* a, const ohip_weight* b,
               const void* c, void* y);
 
-/* Conv, rank 2, group 1 (oxionnx-ops/src/registry/conv_ops/conv.rs:163-323
- * and conv_typed.rs:54-153): Y = act(conv(X, W) + bias).  Pads are
+/* Conv, rank 2, any group (oxionnx-ops/src/registry/conv_ops/conv.rs:163-323
+ * and conv_typed.rs:54-153): Y = act(conv(X, W) + bias).  Groups run one
+ * MFMA launch each, or a direct kernel when a group is too narrow for an
+ * MFMA tile (depthwise).  Pads are
  * [top, left, bottom, right], already resolved from auto_pad
  * (conv/spatial.rs:228-257); asymmetric pads are supported.  NCHW inputs are
  * transposed on the device into a channel-padded NHWC staging buffer; NHWC
@@ -205,6 +212,27 @@ int ohip_conv2d(ohip_ctx* ctx, const ohip_conv_desc* d, const void* x, const ohi
 /* Output extent per conv_out_dim (conv/spatial.rs:272-330); -1 if invalid. */
 int64_t ohip_conv_out_dim(int64_t in, int64_t pad_begin, int64_t pad_end, int64_t k, int64_t dil,
                           int64_t stride);
+
+/* ConvTranspose, rank 2 (ConvTransposeOp, oxionnx-ops/src/registry/conv_ops/conv.rs:556-710,
+ * conv/transpose.rs:78-309, conv_typed.rs:159-222): Y = scatter(X, W) + bias with
+ * W [Cin, Cout/group, KH, KW]; the caller resolves output_shape / auto_pad into
+ * pads (conv.rs:412-470).  X and Y are NCHW of `dtype`; each output is
+ * accumulated in f32 in the reference's scatter order, so the result equals
+ * the reference's (f16 / bf16 rounded once, RNE). */
+typedef struct {
+    int64_t n, c, h, w;
+    int64_t cout, kh, kw, group;
+    int64_t stride_h, stride_w, dil_h, dil_w;
+    int64_t pad_t, pad_l, pad_b, pad_r;
+    int64_t out_pad_h, out_pad_w;
+    int dtype;                     /* F32 / F16 / BF16 */
+} ohip_convt_desc;
+int ohip_conv_transpose2d(ohip_ctx* ctx, const ohip_convt_desc* d, const void* x, const ohip_weight* w,
+                          const void* bias, void* y);
+/* Output extent stride * (in - 1) + out_pad + (k - 1) * dil + 1 - pads
+ * (conv/spatial.rs:346-407); -1 if invalid. */
+int64_t ohip_conv_transpose_out_dim(int64_t in, int64_t stride, int64_t out_pad, int64_t k, int64_t dil,
+                                    int64_t pad_begin, int64_t pad_end);
 
 /* ------------------------------------------------------------------ integer ops */
 /* MatMulInteger / QLinearMatMul (qlinear_matmul.rs:174-254).  A is a device

@@ -98,6 +98,10 @@ int orc_conv2d_f32(const float* x, int64_t n, int64_t c, int64_t h, int64_t w,
  * 1 relu, 2 clip(lo,hi) with NaN bound = unbounded and inverted = no-op. */
 void orc_apply_activation(float* data, int64_t count, int act, float lo, float hi);
 
+int orc_conv_transpose2d_f32(const float* x, int64_t n, int64_t c, int64_t h, int64_t w,
+                             const float* wt, int64_t coutpg, int64_t kh, int64_t kw, const float* bias,
+                             const int64_t strides[2], const int64_t pads[4], const int64_t dils[2],
+                             int64_t group, int64_t oh, int64_t ow, float* out);
 int orc_hardware_threads(void);
 
 /* elementwise nodes (oracle_float.c) */

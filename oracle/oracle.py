@@ -61,6 +61,9 @@ def lib():
         L.orc_bf16_to_f32.restype = ctypes.c_float
         L.orc_bf16_to_f32.argtypes = [ctypes.c_uint16]
         L.orc_hardware_threads.restype = ctypes.c_int
+        L.orc_conv_transpose2d_f32.argtypes = [ctypes.c_void_p, I64, I64, I64, I64, ctypes.c_void_p, I64, I64, I64,
+                                               ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+                                               ctypes.c_void_p, I64, I64, I64, ctypes.c_void_p]
         L.orc_gemm_half.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, I64, I64, I64,
                                     ctypes.c_int, ctypes.c_int, ctypes.c_float, ctypes.c_float,
                                     ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p, I64, I64]
@@ -229,6 +232,79 @@ def conv_geometry(x_shape, w_shape, strides=None, pads=None, dilations=None, gro
     if oh < 0 or ow < 0:
         raise ValueError("padded input extent is smaller than the dilated kernel extent")
     return strides, pads, dilations, [x_shape[0], w_shape[0], oh, ow]
+
+
+def _convt_natural(in_dim, stride, out_pad, k, d):
+    """conv_transpose_natural_dim (conv/spatial.rs:370-407)."""
+    return stride * (in_dim - 1) + out_pad + (k - 1) * d + 1
+
+
+def conv_transpose_geometry(x_shape, w_shape, strides=None, pads=None, dilations=None, group=1,
+                            output_padding=None, output_shape=None, auto_pad="NOTSET"):
+    """ConvTransposeGeometry::from_attrs (registry/conv_ops/conv.rs:349-470) with
+    derive_transpose_pads (:519-554) and read_output_shape_attr (:490-515),
+    rank 2.  W is [C_in, C_out/group, kH, kW]."""
+    strides = list(strides) if strides else [1, 1]
+    dilations = list(dilations) if dilations else [1, 1]
+    out_pad = list(output_padding) if output_padding else [0, 0]
+    if x_shape[1] != w_shape[0]:
+        raise ValueError("ConvTranspose: input channels != weight input channels")
+    if x_shape[1] % group:
+        raise ValueError("ConvTranspose: input channels not divisible by group")
+    target = None
+    if output_shape:
+        target = list(output_shape[-2:]) if len(output_shape) in (2, 4) else None
+        if target is None or min(target) < 1:
+            raise ValueError("ConvTranspose: output_shape")
+    elif auto_pad in ("SAME_UPPER", "SAME_LOWER"):
+        target = [x_shape[2 + a] * strides[a] for a in range(2)]
+    if target is None:
+        pads = [0, 0, 0, 0] if auto_pad == "VALID" else (list(pads) if pads else [0, 0, 0, 0])
+    else:
+        pads = [0, 0, 0, 0]
+        for a in range(2):
+            nat = _convt_natural(x_shape[2 + a], strides[a], out_pad[a], w_shape[2 + a], dilations[a])
+            total = nat - target[a]
+            if total < 0:
+                raise ValueError("ConvTranspose: output_shape exceeds the un-cropped extent")
+            half = total // 2
+            begin, end = (half, total - half) if auto_pad == "SAME_UPPER" else (total - half, half)
+            pads[a], pads[a + 2] = begin, end
+    out = [x_shape[0], w_shape[1] * group]
+    for a in range(2):
+        nat = _convt_natural(x_shape[2 + a], strides[a], out_pad[a], w_shape[2 + a], dilations[a])
+        if nat - pads[a] - pads[a + 2] < 0:
+            raise ValueError("ConvTranspose: pads exceed the un-cropped output extent")
+        out.append(nat - pads[a] - pads[a + 2])
+    return strides, pads, dilations, out
+
+
+def conv_transpose(x, w, b=None, **attrs):
+    """ConvTransposeOp::execute for rank 2, f32 (registry/conv_ops/conv.rs:561-582,
+    conv/transpose.rs:78-309)."""
+    x = np.ascontiguousarray(x, np.float32)
+    w = np.ascontiguousarray(w, np.float32)
+    group = attrs.get("group", 1)
+    s, p, d, out_shape = conv_transpose_geometry(x.shape, w.shape, attrs.get("strides"), attrs.get("pads"),
+                                                 attrs.get("dilations"), group, attrs.get("output_padding"),
+                                                 attrs.get("output_shape"), attrs.get("auto_pad", "NOTSET"))
+    out = np.zeros(out_shape, np.float32)
+    bb = None if b is None else np.ascontiguousarray(b, np.float32)
+    rc = lib().orc_conv_transpose2d_f32(_p(x), *x.shape, _p(w), w.shape[1], w.shape[2], w.shape[3],
+                                        None if bb is None else _p(bb), _p(_i64(s)), _p(_i64(p)),
+                                        _p(_i64(d)), group, out_shape[2], out_shape[3], _p(out))
+    if rc:
+        raise ValueError("ConvTranspose: bad arguments")
+    return out
+
+
+def conv_transpose_half(x_bits, w_bits, b_bits=None, bf16=False, **attrs):
+    """conv_transpose_f16 / _bf16 (conv_typed.rs:159-222): promote, f32 scatter,
+    round the result back (RNE)."""
+    xf = half_bits_to_f32(x_bits, bf16)
+    wf = half_bits_to_f32(w_bits, bf16)
+    bf = None if b_bits is None else half_bits_to_f32(b_bits, bf16)
+    return f32_to_half_bits(conv_transpose(xf, wf, bf, **attrs), bf16)
 
 
 def integer_conv(x, w, x_zp=0, w_zp=None, bias=None, **attrs):

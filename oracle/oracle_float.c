@@ -242,3 +242,48 @@ void orc_instance_norm_f32(float* data, int64_t planes, int64_t spatial, float e
         for (int64_t i = 0; i < spatial; ++i) x[i] = (x[i] - mean) * inv;
     }
 }
+
+/* ConvTranspose, rank 2, f32: conv_transpose_into + scatter_rank2
+ * (oxionnx-ops/src/conv/transpose.rs:78-214, 233-309).  The output is zeroed,
+ * every input element scatters in_val * w[ci][oc][ky][kx] to
+ * (iy * s + ky * d - pad_begin, ...) when that lands inside the cropped
+ * output, visiting batch, group, input channel, input position, output
+ * channel, kernel offset in that order; the bias is added afterwards. */
+int orc_conv_transpose2d_f32(const float* x, int64_t n, int64_t c, int64_t h, int64_t w,
+                             const float* wt, int64_t coutpg, int64_t kh, int64_t kw, const float* bias,
+                             const int64_t strides[2], const int64_t pads[4], const int64_t dils[2],
+                             int64_t group, int64_t oh, int64_t ow, float* out) {
+    if (group <= 0 || c % group) return -1;
+    const int64_t cpg = c / group, cout = coutpg * group;
+    memset(out, 0, (size_t)(n * cout * oh * ow) * sizeof(float));
+    for (int64_t ni = 0; ni < n; ++ni)
+        for (int64_t g = 0; g < group; ++g)
+            for (int64_t ic = 0; ic < cpg; ++ic) {
+                const int64_t ci = g * cpg + ic;
+                for (int64_t iy = 0; iy < h; ++iy)
+                    for (int64_t ix = 0; ix < w; ++ix) {
+                        const float v = x[((ni * c + ci) * h + iy) * w + ix];
+                        for (int64_t oc = 0; oc < coutpg; ++oc) {
+                            const int64_t co = g * coutpg + oc;
+                            const float* wb = wt + (ci * coutpg + oc) * kh * kw;
+                            float* ob = out + (ni * cout + co) * oh * ow;
+                            for (int64_t ky = 0; ky < kh; ++ky) {
+                                const int64_t oyr = iy * strides[0] + ky * dils[0];
+                                if (oyr < pads[0] || oyr - pads[0] >= oh) continue;
+                                for (int64_t kx = 0; kx < kw; ++kx) {
+                                    const int64_t oxr = ix * strides[1] + kx * dils[1];
+                                    if (oxr < pads[1] || oxr - pads[1] >= ow) continue;
+                                    ob[(oyr - pads[0]) * ow + (oxr - pads[1])] += v * wb[ky * kw + kx];
+                                }
+                            }
+                        }
+                    }
+            }
+    if (bias)
+        for (int64_t ni = 0; ni < n; ++ni)
+            for (int64_t co = 0; co < cout; ++co) {
+                float* ob = out + (ni * cout + co) * oh * ow;
+                for (int64_t i = 0; i < oh * ow; ++i) ob[i] += bias[co];
+            }
+    return 0;
+}

@@ -65,6 +65,12 @@ class ConvDesc(ctypes.Structure):
                 ("pad_mode", ctypes.c_int)]
 
 
+class ConvTDesc(ctypes.Structure):
+    _fields_ = [(f, I64) for f in ("n", "c", "h", "w", "cout", "kh", "kw", "group", "stride_h", "stride_w",
+                                    "dil_h", "dil_w", "pad_t", "pad_l", "pad_b", "pad_r", "out_pad_h",
+                                    "out_pad_w")] + [("dtype", ctypes.c_int)]
+
+
 class QGemmDesc(ctypes.Structure):
     _fields_ = [("m", I64), ("k", I64), ("n", I64), ("a_dtype", ctypes.c_int),
                 ("a_zp", ctypes.POINTER(ctypes.c_int32)), ("n_azp", ctypes.c_int), ("out_kind", ctypes.c_int),
@@ -152,6 +158,10 @@ SIGNATURES = {
     "ohip_gemm": (ctypes.c_int, [VP, ctypes.POINTER(GemmDesc), VP, VP, VP, VP]),
     "ohip_conv2d": (ctypes.c_int, [VP, ctypes.POINTER(ConvDesc), VP, VP, VP, VP]),
     "ohip_conv_out_dim": (I64, [I64, I64, I64, I64, I64, I64]),
+    "ohip_weight_conv_transpose": (ctypes.c_int, [VP, ctypes.POINTER(WeightKey), ctypes.c_int, VP, I64, I64, I64,
+                                                  I64, ctypes.c_int, ctypes.POINTER(VP)]),
+    "ohip_conv_transpose2d": (ctypes.c_int, [VP, ctypes.POINTER(ConvTDesc), VP, VP, VP, VP]),
+    "ohip_conv_transpose_out_dim": (I64, [I64, I64, I64, I64, I64, I64, I64]),
     "ohip_qgemm": (ctypes.c_int, [VP, ctypes.POINTER(QGemmDesc), VP, VP, VP]),
     "ohip_qconv2d": (ctypes.c_int, [VP, ctypes.POINTER(QConvDesc), VP, VP, VP, VP]),
     "ohip_get_counters": (ctypes.c_int, [VP, ctypes.POINTER(Counters)]),

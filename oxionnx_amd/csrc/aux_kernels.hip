@@ -524,6 +524,69 @@ hipError_t run_qconv_direct(const void* x, const void* w, void* y, const DirectQ
   return hipGetLastError();
 }
 
+// ---------------------------------------------------------------- ConvTranspose
+// Output-stationary form of the reference's scatter: output (n, co, oy, ox)
+// gathers x[ci][iy][ix] * w[ci][oc][ky][kx] over the taps with
+// iy * sh + ky * dh - pt == oy (and likewise for x).  Walking ci, then ky and
+// kx downwards (iy and ix upwards) adds the contributions in the order the
+// scatter delivers them to this output, from an f32 zero, and the bias comes
+// last, so the f32 result is the reference's to the bit.
+template <class T>
+__global__ void __launch_bounds__(256)
+convt_kernel(const T* __restrict__ x, const T* __restrict__ w, const T* __restrict__ bias, T* __restrict__ y,
+             ConvTArgs a) {
+#pragma clang fp contract(off)
+  const int64_t total = (int64_t)a.N * a.cout * a.OH * a.OW;
+  for (int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x; idx < total; idx += (int64_t)gridDim.x * 256) {
+    int64_t r = idx;
+    const int ox = (int)(r % a.OW); r /= a.OW;
+    const int oy = (int)(r % a.OH); r /= a.OH;
+    const int co = (int)(r % a.cout);
+    const int n = (int)(r / a.cout);
+    const int g = co / a.coutg, oc = co - g * a.coutg;
+    const int ty = oy + a.pt, tx = ox + a.pl;
+    float acc = 0.0f;
+    for (int ic = 0; ic < a.cg; ++ic) {
+      const int ci = g * a.cg + ic;
+      const T* xc = x + ((int64_t)n * a.C + ci) * a.H * a.W;
+      const T* wc = w + ((int64_t)ci * a.coutg + oc) * a.KH * a.KW;
+      for (int ky = a.KH - 1; ky >= 0; --ky) {
+        const int sy = ty - ky * a.dh;
+        if (sy < 0 || sy % a.sh) continue;
+        const int iy = sy / a.sh;
+        if (iy >= a.H) continue;
+        for (int kx = a.KW - 1; kx >= 0; --kx) {
+          const int sx = tx - kx * a.dw;
+          if (sx < 0 || sx % a.sw) continue;
+          const int ix = sx / a.sw;
+          if (ix >= a.W) continue;
+          acc += to_f32(xc[(int64_t)iy * a.W + ix]) * to_f32(wc[ky * a.KW + kx]);
+        }
+      }
+    }
+    if (bias) acc += to_f32(bias[co]);
+    y[(((int64_t)n * a.cout + co) * a.OH + oy) * a.OW + ox] = from_f32<T>(acc);
+  }
+}
+
+hipError_t run_conv_transpose(int dtype, const void* x, const void* w, const void* bias, void* y,
+                              const ConvTArgs& a, hipStream_t st) {
+  const int64_t total = (int64_t)a.N * a.cout * a.OH * a.OW;
+  if (total <= 0) return hipSuccess;
+  const unsigned grid = (unsigned)std::min<int64_t>((total + 255) / 256, 65535 * 16);
+#define OHIP_CONVT(T)                                                                                \
+  hipLaunchKernelGGL(convt_kernel<T>, dim3(grid), dim3(256), 0, st, reinterpret_cast<const T*>(x), \
+                     reinterpret_cast<const T*>(w), reinterpret_cast<const T*>(bias), reinterpret_cast<T*>(y), a)
+  switch (dtype) {
+    case DT_F32: OHIP_CONVT(float); break;
+    case DT_F16: OHIP_CONVT(_Float16); break;
+    case DT_BF16: OHIP_CONVT(__bf16); break;
+    default: return hipErrorInvalidValue;
+  }
+#undef OHIP_CONVT
+  return hipGetLastError();
+}
+
 // dst[r][c] = c < K ? src[r * rs + c * cs] : 0 for a [R][ld] destination: pads a
 // row-major operand to whole 16-byte chunks, or materialises a transpose.
 template <class T>

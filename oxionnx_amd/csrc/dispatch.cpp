@@ -415,6 +415,103 @@ int do_conv(ohip_ctx* ctx, const ohip_node* nd, int placement, ohip_output* out)
   return finish_output(ctx, st, placement, out, yd, obytes, dt);
 }
 
+// ------------------------------------------------------------------ ConvTranspose
+// ConvTransposeGeometry::from_attrs (registry/conv_ops/conv.rs:349-470) with
+// derive_transpose_pads (:519-554) and read_output_shape_attr (:490-515),
+// rank 2: output_shape (2 or 4 entries) or SAME_* auto_pad fix the target
+// extent and the pads are derived from it; otherwise the explicit pads (or
+// none for VALID) crop the natural extent.
+int do_conv_transpose(ohip_ctx* ctx, const ohip_node* nd, int placement, ohip_output* out) {
+  const ohip_tensor *x = input(nd, 0), *w = input(nd, 1), *b = input(nd, 2);
+  if (!x || !w) return decline("ConvTranspose: missing input");
+  if (!host_only(w) || (b && !host_only(b))) return decline("ConvTranspose: filter / bias must be host tensors");
+  const int dt = x->dtype;
+  if (dt != OHIP_F32 && dt != OHIP_F16 && dt != OHIP_BF16) return decline("ConvTranspose: dtype");
+  if (x->rank != 4 || w->rank != 4) return decline("ConvTranspose: only rank 2 spatial");
+  if (x->device && ohip_dtensor_layout(x->device) != OHIP_NCHW) return decline("ConvTranspose: resident input layout");
+  const int64_t n = x->shape[0], c = x->shape[1], h = x->shape[2], wd = x->shape[3];
+  const int64_t coutg = w->shape[1], kh = w->shape[2], kw = w->shape[3];
+  const int64_t group = attr_i(nd, "group", 1);
+  if (group <= 0 || w->shape[0] != c || c % group) return decline("ConvTranspose: bad group / channels");
+  auto strides = attr_ints(nd, "strides"), dil = attr_ints(nd, "dilations"), pads = attr_ints(nd, "pads");
+  auto opad = attr_ints(nd, "output_padding"), oshape = attr_ints(nd, "output_shape"), ks = attr_ints(nd, "kernel_shape");
+  if (!ks.empty() && (ks.size() != 2 || ks[0] != kh || ks[1] != kw)) return decline("ConvTranspose: kernel_shape");
+  if (strides.empty()) strides.assign(2, 1);
+  if (dil.empty()) dil.assign(2, 1);
+  if (pads.empty()) pads.assign(4, 0);
+  if (opad.empty()) opad.assign(2, 0);
+  if (strides.size() != 2 || dil.size() != 2 || pads.size() != 4 || opad.size() != 2)
+    return decline("ConvTranspose: attribute rank mismatch");
+  for (int a = 0; a < 2; ++a)
+    if (strides[a] <= 0 || dil[a] <= 0 || opad[a] < 0) return decline("ConvTranspose: stride / dilation / output_padding");
+  for (auto v : pads) if (v < 0) return decline("ConvTranspose: negative pad");
+  const std::string ap = attr_s(nd, "auto_pad");
+  if (!(ap.empty() || ap == "NOTSET" || ap == "VALID" || ap == "SAME_UPPER" || ap == "SAME_LOWER"))
+    return decline("ConvTranspose: unknown auto_pad");
+  const int64_t in[2] = {h, wd}, kk[2] = {kh, kw};
+  bool has_target = false;
+  int64_t target[2] = {0, 0};
+  if (!oshape.empty()) {
+    if (oshape.size() != 2 && oshape.size() != 4) return decline("ConvTranspose: output_shape length");
+    target[0] = oshape[oshape.size() - 2];
+    target[1] = oshape[oshape.size() - 1];
+    if (target[0] < 1 || target[1] < 1) return decline("ConvTranspose: output_shape");
+    has_target = true;
+  } else if (ap == "SAME_UPPER" || ap == "SAME_LOWER") {
+    target[0] = h * strides[0];
+    target[1] = wd * strides[1];
+    has_target = true;
+  }
+  if (has_target) {
+    for (int a = 0; a < 2; ++a) {
+      const int64_t natural = strides[a] * (in[a] - 1) + opad[a] + (kk[a] - 1) * dil[a] + 1;
+      const int64_t total = natural - target[a];
+      if (total < 0) return decline("ConvTranspose: output_shape exceeds the un-cropped extent");
+      const int64_t half = total / 2;
+      pads[a] = ap == "SAME_UPPER" ? half : total - half;
+      pads[a + 2] = ap == "SAME_UPPER" ? total - half : half;
+    }
+  } else if (ap == "VALID") {
+    pads.assign(4, 0);
+  }
+  ohip_convt_desc d{n, c, h, wd, coutg * group, kh, kw, group, strides[0], strides[1], dil[0], dil[1],
+                    pads[0], pads[1], pads[2], pads[3], opad[0], opad[1], dt};
+  const int64_t oh = ohip_conv_transpose_out_dim(h, strides[0], opad[0], kh, dil[0], pads[0], pads[2]);
+  const int64_t ow = ohip_conv_transpose_out_dim(wd, strides[1], opad[1], kw, dil[1], pads[1], pads[3]);
+  if (oh < 0 || ow < 0) return decline("ConvTranspose: pads exceed the un-cropped extent");
+  ohip_tuning tun;
+  ohip_get_tuning(ctx, &tun);
+  if (!ohip_conv_admits(&tun, d.cout, (c / group) * kh * kw, n * h * wd)) return decline("ConvTranspose: gate");
+
+  std::string name = wkey_name(w), label = "ConvTranspose.W";
+  ohip_weight_key key{name.c_str(), label.c_str()};
+  const bool cache = w->is_initializer && !name.empty();
+  ohip_weight* wt = nullptr;
+  int rc = ohip_weight_conv_transpose(ctx, cache ? &key : nullptr, w->dtype, w->data, c, coutg, kh, kw, dt, &wt);
+  if (rc) return rc;
+  Stage st(ctx);
+  const void* xd = st.operand(x);
+  const void* bd = nullptr;
+  std::vector<char> bconv;
+  if (b) {
+    if (numel(b) != d.cout) {
+      if (!cache) ohip_weight_release(wt);
+      return decline("ConvTranspose: bias length");
+    }
+    bconv.resize((size_t)d.cout * ebytes(dt));
+    for (int64_t i = 0; i < d.cout; ++i) put_elem(dt, bconv.data(), i, host_at(b, i));
+    bd = st.cached(b, "ConvTranspose.B", dt, bconv.data(), bconv.size());
+  }
+  const size_t obytes = (size_t)(n * d.cout * oh * ow) * ebytes(dt);
+  void* yd = st.alloc(obytes);
+  if (!xd || !yd || (b && !bd)) { if (!cache) ohip_weight_release(wt); return OHIP_E_NOMEM; }
+  rc = ohip_conv_transpose2d(ctx, &d, xd, wt, bd, yd);
+  if (!cache) ohip_weight_release(wt);
+  if (rc) return rc;
+  set_out(out, dt, {n, d.cout, oh, ow});
+  return finish_output(ctx, st, placement, out, yd, obytes, dt);
+}
+
 // ------------------------------------------------------------------ Gemm / MatMul
 int do_gemm(ohip_ctx* ctx, const ohip_node* nd, bool is_matmul, int placement, ohip_output* out) {
   const ohip_tensor *a = input(nd, 0), *b = input(nd, 1), *c = is_matmul ? nullptr : input(nd, 2);
@@ -1281,7 +1378,7 @@ int do_dequantize(ohip_ctx* ctx, const ohip_node* nd, int placement, ohip_output
 // provider's dense-contraction arms.
 extern "C" int ohip_is_supported_op(const char* op) {
   if (!op) return 0;
-  static const char* kOps[] = {"Conv", "Gemm", "MatMul", "QLinearMatMul", "MatMulInteger", "QLinearConv",
+  static const char* kOps[] = {"Conv", "ConvTranspose", "Gemm", "MatMul", "QLinearMatMul", "MatMulInteger", "QLinearConv",
                                "ConvInteger", "Relu", "LeakyRelu", "Tanh", "Sigmoid", "Silu", "Identity",
                                "Add", "Sub", "Mul", "Div", "OxiInstanceNorm", "InstanceNormalization", "Resize",
                                "Pad", "MaxPool", "Concat", "Slice", "Reshape", "Flatten", "Squeeze", "Unsqueeze",
@@ -1296,7 +1393,7 @@ extern "C" int ohip_is_supported_op(const char* op) {
 // parameters and shape-like inputs are read on the host.
 extern "C" int ohip_accepts_resident_slot(const char* op, int index) {
   if (!op) return 0;
-  static const char* kSlot0[] = {"Conv", "Gemm", "MatMul", "QLinearConv", "Relu", "LeakyRelu", "Tanh", "Sigmoid",
+  static const char* kSlot0[] = {"Conv", "ConvTranspose", "Gemm", "MatMul", "QLinearConv", "Relu", "LeakyRelu", "Tanh", "Sigmoid",
                                  "Silu", "Identity", "InstanceNormalization", "Resize", "Pad",
                                  "MaxPool", "Slice", "Reshape", "Flatten", "Squeeze", "Unsqueeze",
                                  "QuantizeLinear", "DequantizeLinear"};
@@ -1320,6 +1417,7 @@ extern "C" int ohip_try_dispatch(ohip_ctx* ctx, const ohip_node* node, int place
   }
   int rc;
   if (op == "Conv") rc = do_conv(ctx, node, placement, out);
+  else if (op == "ConvTranspose") rc = do_conv_transpose(ctx, node, placement, out);
   else if (op == "Gemm") rc = do_gemm(ctx, node, false, placement, out);
   else if (op == "MatMul") rc = do_gemm(ctx, node, true, placement, out);
   else if (op == "QLinearMatMul") rc = do_qmatmul(ctx, node, true, placement, out);

@@ -149,6 +149,15 @@ struct DirectQConvArgs {
 };
 hipError_t run_qconv_direct(const void* x, const void* w, void* y, const DirectQConvArgs& a, hipStream_t st);
 
+// ConvTranspose as an output-stationary gather; see convt_kernel.
+struct ConvTArgs {
+  int N, C, H, W, cout, cg, coutg, KH, KW;
+  int sh, sw, dh, dw, pt, pl;
+  int OH, OW;
+};
+hipError_t run_conv_transpose(int dtype, const void* x, const void* w, const void* bias, void* y,
+                              const ConvTArgs& a, hipStream_t st);
+
 // NCHW -> NHWC staging with per-group channel slots and an optional
 // reflect (1) / edge (2) spatial border; see stage_nhwc_kernel.
 hipError_t run_stage_nhwc(int elem_bytes, const void* src, void* dst, int N, int C, int H, int W, int pt, int pl,

@@ -57,7 +57,7 @@ extern "C" int ohip_env_flag(const char* name) {
 }
 
 // ------------------------------------------------------------------ types
-enum WeightKind { WK_GEMM = 1, WK_CONV = 2, WK_QGEMM = 3, WK_QCONV = 4 };
+enum WeightKind { WK_GEMM = 1, WK_CONV = 2, WK_QGEMM = 3, WK_QCONV = 4, WK_CONVT = 5 };
 
 struct ohip_weight {
   ohip_ctx* ctx = nullptr;
@@ -720,6 +720,33 @@ extern "C" int ohip_weight_conv(ohip_ctx* ctx, const ohip_weight_key* key, int s
   return weight_finish(ctx, key, ks, w, out);
 }
 
+// ConvTranspose filter: [Cin][Cout/group][KH][KW] kept as is (converted to
+// the compute dtype); the gather kernel reads it in that layout.
+extern "C" int ohip_weight_conv_transpose(ohip_ctx* ctx, const ohip_weight_key* key, int src_dt, const void* host,
+                                          int64_t cin, int64_t coutg, int64_t kh, int64_t kw, int dt,
+                                          ohip_weight** out) {
+  int rc = activate(ctx);
+  if (rc) return rc;
+  if (!host || !out || !is_float(src_dt) || !is_float(dt) || cin <= 0 || coutg <= 0 || kh <= 0 || kw <= 0)
+    return fail(OHIP_E_INVALID, "ohip_weight_conv_transpose: bad arguments");
+  std::lock_guard<std::mutex> lock(ctx->mu);
+  const int64_t count = cin * coutg * kh * kw;
+  const size_t src_bytes = (size_t)count * elem_bytes(src_dt);
+  std::string ks = key && key->name ? cache_key(key, WK_CONVT, dt, src_bytes, {cin, coutg, kh, kw}) : std::string();
+  if (ohip_weight* hit = cache_lookup(ctx, key, ks)) {
+    *out = hit;
+    return OHIP_OK;
+  }
+  std::vector<char> conv((size_t)count * elem_bytes(dt));
+  for (int64_t i = 0; i < count; ++i) write_elem(dt, conv.data(), i, src_dt, host, i);
+  auto* w = new ohip_weight();
+  w->kind = WK_CONVT; w->dtype = dt; w->rows = cin; w->k = coutg; w->kh = kh; w->kw = kw;
+  w->ld_bytes = coutg * kh * kw * elem_bytes(dt);
+  rc = weight_upload(ctx, w, conv.data(), conv.size());
+  if (rc) { weight_free(w); return rc; }
+  return weight_finish(ctx, key, ks, w, out);
+}
+
 // Integer packing.  Each weight channel becomes v = w - w_zp[channel] in
 // K-contiguous int8 rows, plus sum(v) for the epilogue's zero-point
 // correction.  v spans at most 255 consecutive values inside [-255, 255]:
@@ -937,6 +964,13 @@ extern "C" int64_t ohip_conv_out_dim(int64_t in, int64_t pb, int64_t pe, int64_t
   int64_t eff = (k - 1) * d + 1, padded = in + pb + pe;
   if (padded < eff) return -1;
   return (padded - eff) / s + 1;
+}
+
+extern "C" int64_t ohip_conv_transpose_out_dim(int64_t in, int64_t s, int64_t op, int64_t k, int64_t d,
+                                               int64_t pb, int64_t pe) {
+  if (s <= 0 || k <= 0 || d <= 0 || in <= 0 || op < 0 || pb < 0 || pe < 0) return -1;
+  const int64_t natural = s * (in - 1) + op + (k - 1) * d + 1;
+  return natural - pb - pe >= 0 ? natural - pb - pe : -1;
 }
 
 // Bring an activation matrix [R][K] (row stride ld elements, or transposed
@@ -1168,6 +1202,35 @@ extern "C" int ohip_conv2d(ohip_ctx* ctx, const ohip_conv_desc* d, const void* x
     hipError_t e = run_conv_float(d->dtype, col, wt, col_on_x, o, ctx->tile_override, ctx->stream);
     if (e != hipSuccess) return hip_fail(e, "ohip_conv2d launch");
   }
+  return OHIP_OK;
+}
+
+// ------------------------------------------------------------------ ConvTranspose
+extern "C" int ohip_conv_transpose2d(ohip_ctx* ctx, const ohip_convt_desc* d, const void* x, const ohip_weight* w,
+                                     const void* bias, void* y) {
+  int rc = activate(ctx);
+  if (rc) return rc;
+  if (!d || !x || !w || !y) return fail(OHIP_E_INVALID, "ohip_conv_transpose2d: null argument");
+  if (!is_float(d->dtype) || w->kind != WK_CONVT || w->dtype != d->dtype)
+    return fail(OHIP_E_INVALID, "ohip_conv_transpose2d: weight kind / dtype mismatch");
+  if (d->group < 1 || d->c % d->group || d->cout % d->group)
+    return fail(OHIP_E_SHAPE, "ohip_conv_transpose2d: bad group");
+  if (w->rows != d->c || w->k * d->group != d->cout || w->kh != d->kh || w->kw != d->kw)
+    return fail(OHIP_E_SHAPE, "ohip_conv_transpose2d: shape disagrees with the filter");
+  const int64_t oh = ohip_conv_transpose_out_dim(d->h, d->stride_h, d->out_pad_h, d->kh, d->dil_h, d->pad_t, d->pad_b);
+  const int64_t ow = ohip_conv_transpose_out_dim(d->w, d->stride_w, d->out_pad_w, d->kw, d->dil_w, d->pad_l, d->pad_r);
+  if (oh < 0 || ow < 0) return fail(OHIP_E_SHAPE, "ohip_conv_transpose2d: pads exceed the un-cropped extent");
+  if (d->n * d->cout * oh * ow > (int64_t)INT_MAX * 8 || d->h * d->w > INT_MAX / 2)
+    return fail(OHIP_DECLINED, "ohip_conv_transpose2d: extent too large");
+  std::lock_guard<std::mutex> lock(ctx->mu);
+  ctx->counters.dispatches++;
+  ConvTArgs a{};
+  a.N = (int)d->n; a.C = (int)d->c; a.H = (int)d->h; a.W = (int)d->w; a.cout = (int)d->cout;
+  a.cg = (int)(d->c / d->group); a.coutg = (int)(d->cout / d->group); a.KH = (int)d->kh; a.KW = (int)d->kw;
+  a.sh = (int)d->stride_h; a.sw = (int)d->stride_w; a.dh = (int)d->dil_h; a.dw = (int)d->dil_w;
+  a.pt = (int)d->pad_t; a.pl = (int)d->pad_l; a.OH = (int)oh; a.OW = (int)ow;
+  hipError_t e = run_conv_transpose(d->dtype, x, w->data, bias, y, a, ctx->stream);
+  if (e != hipSuccess) return hip_fail(e, "ohip_conv_transpose2d launch");
   return OHIP_OK;
 }
 

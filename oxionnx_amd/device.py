@@ -153,6 +153,17 @@ class HipContext:
                                          w.ctypes.data_as(ctypes.c_void_p), *w.shape, dtype, ctypes.byref(h)))
         return Weight(self, h, "conv", dtype, w.shape, name is not None)
 
+    def weight_conv_transpose(self, w, dtype=L.F32, name=None, label="ConvTranspose.W"):
+        """ConvTranspose filter [Cin, Cout/group, KH, KW]."""
+        w = np.ascontiguousarray(w)
+        if w.dtype == np.float64:
+            w = w.astype(np.float32)
+        h = ctypes.c_void_p()
+        L.check(L.lib().ohip_weight_conv_transpose(self.h, _key(name, label), _np_ohip_dtype(w),
+                                                   w.ctypes.data_as(ctypes.c_void_p), *w.shape, dtype,
+                                                   ctypes.byref(h)))
+        return Weight(self, h, "convt", dtype, w.shape, name is not None)
+
     def weight_qgemm(self, b, zp=None, scale=None, trans_b=False, name=None, label="QLinearMatMul.B"):
         b = np.ascontiguousarray(b)
         k, n = (b.shape[1], b.shape[0]) if trans_b else b.shape
@@ -220,6 +231,24 @@ class HipContext:
         d = L.ConvDesc(n, c, h, wd, cout, kh, kw, group, strides[0], strides[1], dilations[0], dilations[1],
                        pads[0], pads[1], pads[2], pads[3], dt, in_layout, out_layout, act, act_lo, act_hi)
         L.check(L.lib().ohip_conv2d(self.h, ctypes.byref(d), _ptr(x), w.handle, _ptr(bias), _ptr(out)))
+        return out
+
+    def conv_transpose2d(self, x, w, bias=None, strides=(1, 1), pads=(0, 0, 0, 0), dilations=(1, 1),
+                         output_padding=(0, 0), group=1, out=None):
+        """ConvTranspose, NCHW; pads = [top, left, bottom, right] (already resolved)."""
+        torch = _torch()
+        dt = ohip_dtype(x.dtype)
+        cin, coutg, kh, kw = w.shape
+        n, c, h, wd = x.shape
+        oh = L.lib().ohip_conv_transpose_out_dim(h, strides[0], output_padding[0], kh, dilations[0], pads[0], pads[2])
+        ow = L.lib().ohip_conv_transpose_out_dim(wd, strides[1], output_padding[1], kw, dilations[1], pads[1], pads[3])
+        if oh < 0 or ow < 0:
+            raise L.OhipError(L.E_SHAPE, "bad ConvTranspose geometry")
+        if out is None:
+            out = torch.empty((n, coutg * group, oh, ow), dtype=x.dtype, device=x.device)
+        d = L.ConvTDesc(n, c, h, wd, coutg * group, kh, kw, group, strides[0], strides[1], dilations[0],
+                        dilations[1], pads[0], pads[1], pads[2], pads[3], output_padding[0], output_padding[1], dt)
+        L.check(L.lib().ohip_conv_transpose2d(self.h, ctypes.byref(d), _ptr(x), w.handle, _ptr(bias), _ptr(out)))
         return out
 
     def qgemm(self, a, w, a_zp=0, out_kind=L.QOUT_U8, a_scale=1.0, y_scale=1.0, y_zp=0, lo=0, hi=255, out=None):

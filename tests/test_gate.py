@@ -6,6 +6,7 @@ import pytest
 
 from oxionnx_amd import _lib as L
 from oxionnx_amd import ep
+from oracle import oracle as O
 
 
 def tuning(cls):
@@ -96,14 +97,15 @@ def test_op_support_predicates():
     # the contraction arms plus the memory-bound arms of the reference CUDA
     # provider's claim list (oxionnx-cuda/src/lib.rs:101-119) that conv
     # networks need between their contractions
-    for op in ["Conv", "Gemm", "MatMul", "QLinearMatMul", "MatMulInteger", "QLinearConv", "ConvInteger",
-               "Relu", "LeakyRelu", "Tanh", "Sigmoid", "Silu", "Add", "Sub", "Mul", "Div", "OxiInstanceNorm",
+    for op in ["Conv", "ConvTranspose", "Gemm", "MatMul", "QLinearMatMul", "MatMulInteger", "QLinearConv",
+               "ConvInteger", "Relu", "LeakyRelu", "Tanh", "Sigmoid", "Silu", "Add", "Sub", "Mul", "Div", "OxiInstanceNorm",
                "InstanceNormalization", "Resize", "Pad", "MaxPool", "Concat", "Slice", "Reshape", "Flatten",
                "Squeeze", "Unsqueeze", "QuantizeLinear", "DequantizeLinear"]:
         assert ep.is_supported_op(op), op
-    for op in ["Transpose", "ConvTranspose", "Softmax", "LSTM", ""]:
+    for op in ["Transpose", "Softmax", "LSTM", ""]:
         assert not ep.is_supported_op(op)
     assert ep.accepts_resident_slot("Conv", 0) and not ep.accepts_resident_slot("Conv", 1)
+    assert ep.accepts_resident_slot("ConvTranspose", 0) and not ep.accepts_resident_slot("ConvTranspose", 1)
     assert ep.accepts_resident_slot("Gemm", 0) and not ep.accepts_resident_slot("Gemm", 1)
     assert ep.accepts_resident_slot("QLinearConv", 0) and not ep.accepts_resident_slot("QLinearConv", 3)
     assert ep.accepts_resident_slot("Add", 1) and not ep.accepts_resident_slot("Add", 2)
@@ -119,3 +121,18 @@ def test_try_new_is_gated_by_the_env_flag(monkeypatch):
     assert ep.HipContext.try_new() is None
     h = ctypes.c_void_p()
     assert L.lib().ohip_ctx_try_new(ctypes.byref(h)) == L.DECLINED
+
+
+def test_conv_transpose_extent_matches_the_oracle_geometry():
+    """ohip_conv_transpose_out_dim (device-free) against the oracle's
+    conv_transpose_geometry, including invalid crops."""
+    from oxionnx_amd import _lib as L
+    for (i, s, op, k, d, pb, pe) in [(5, 2, 1, 3, 1, 1, 1), (7, 3, 0, 4, 2, 0, 2), (1, 1, 0, 1, 1, 0, 0),
+                                     (3, 2, 0, 3, 1, 4, 4)]:
+        got = L.lib().ohip_conv_transpose_out_dim(i, s, op, k, d, pb, pe)
+        try:
+            want = O.conv_transpose_geometry((1, 1, i, i), (1, 1, k, k), [s, s], [pb, pb, pe, pe], [d, d], 1,
+                                             [op, op])[3][2]
+        except ValueError:
+            want = -1
+        assert got == want, (i, s, op, k, d, pb, pe)

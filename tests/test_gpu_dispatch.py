@@ -160,3 +160,37 @@ def test_resident_chain_keeps_activations_on_the_device(ctx):
     np.testing.assert_array_equal(dy.to_host(ctx), host_y)
     want = O.conv(O.conv(x, w1, activation="relu", pads=[1, 1, 1, 1]), w2, pads=[1, 1, 1, 1])
     assert np.max(np.abs(host_y - want)) <= 1e-4 * np.max(np.abs(want))
+
+
+@pytest.mark.parametrize("attrs", [
+    dict(strides=[2, 2]),
+    dict(strides=[2, 2], output_shape=[1, 3, 10, 10]),
+    dict(strides=[2, 2], auto_pad="SAME_UPPER"),
+    dict(strides=[2, 2], auto_pad="SAME_LOWER", output_padding=[1, 0]),
+    dict(strides=[1, 2], pads=[1, 0, 0, 1], dilations=[2, 1], group=2, kernel_shape=[3, 3]),
+], ids=["natural", "output_shape", "same_upper", "same_lower_outpad", "group_dilated"])
+def test_conv_transpose_node_through_the_boundary(ctx, attrs):
+    """ConvTranspose (registry/conv_ops/conv.rs:556-710): the node's output_shape /
+    auto_pad / output_padding resolve to the extent and pads the reference
+    derives (conv.rs:412-470), and the values equal the scatter's."""
+    from oxionnx_amd import ep
+    from oxionnx_amd.ep import Attributes
+    rng = np.random.default_rng(23)
+    g = attrs.get("group", 1)
+    x = rng.uniform(-1, 1, (1, 4, 5, 5)).astype(np.float32)
+    w = rng.normal(0, 0.3, (4, 6 // g if g > 1 else 3, 3, 3)).astype(np.float32)
+    b = rng.normal(0, 0.1, w.shape[1] * g).astype(np.float32)
+    a = Attributes()
+    for k, v in attrs.items():
+        if isinstance(v, list):
+            a.int_lists[k] = v
+        elif isinstance(v, str):
+            a.strings[k] = v
+        else:
+            a.ints[k] = v
+    node = ep.Node("ConvTranspose", ["x", "w", "b"], attrs=a)
+    out = ep.try_hip_dispatch(node, {"w": w, "b": b}, {"x": x}, ctx)
+    assert out is not None, ctx.last_decline()
+    want = O.conv_transpose(x, w, b, **attrs)
+    assert out[0].shape == want.shape
+    np.testing.assert_array_equal(out[0].view(np.uint32), want.view(np.uint32))

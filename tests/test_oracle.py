@@ -277,3 +277,83 @@ def test_conv_geometry_same_pads():
     assert p == [1, 1, 0, 0]
     with pytest.raises(ValueError):
         O.conv_geometry([1, 1, 2, 2], [1, 1, 5, 5])
+
+
+# ------------------------------------------------------------------ ConvTranspose
+def test_conv_transpose_known_answers():
+    """oxionnx-ops/src/conv/tests.rs:137-253 (test_conv_transpose_basic / _upsample /
+    _with_bias / _with_padding / _multi_channel)."""
+    x = np.array([1, 2, 3, 4], np.float32).reshape(1, 1, 2, 2)
+    assert O.conv_transpose(x, np.ones((1, 1, 1, 1), np.float32)).ravel().tolist() == [1, 2, 3, 4]
+    up = O.conv_transpose(np.ones((1, 1, 1, 1), np.float32), np.ones((1, 1, 2, 2), np.float32), strides=[2, 2])
+    assert up.shape == (1, 1, 2, 2) and up.ravel().tolist() == [1, 1, 1, 1]
+    yb = O.conv_transpose(np.ones((1, 1, 1, 1), np.float32), np.full((1, 1, 1, 1), 2, np.float32),
+                          np.array([3], np.float32))
+    assert yb.ravel().tolist() == [5.0]
+    yp = O.conv_transpose(x, np.ones((1, 1, 3, 3), np.float32), pads=[1, 1, 1, 1])
+    # pads 1 crop the 4x4 scatter of a 3x3 ones kernel to its centre: every
+    # output sums all four inputs
+    assert yp.shape == (1, 1, 2, 2) and yp.ravel().tolist() == [10, 10, 10, 10]
+    xm = np.array([1, 1, 1, 1, 2, 2, 2, 2], np.float32).reshape(1, 2, 2, 2)
+    assert O.conv_transpose(xm, np.ones((2, 1, 1, 1), np.float32)).ravel().tolist() == [3, 3, 3, 3]
+
+
+def test_conv_transpose_output_shape_rules():
+    """tests/s4_engine_stitch.rs:277-325: the 4-entry output_shape form, SAME_UPPER
+    (in * stride) and the natural extent stride * (in - 1) + k."""
+    g = lambda **a: O.conv_transpose_geometry((1, 1, 3, 3), (1, 2, 3, 3), strides=[2, 2], **a)[3]
+    assert g(output_shape=[1, 2, 6, 6]) == [1, 2, 6, 6]
+    assert g(auto_pad="SAME_UPPER") == [1, 2, 6, 6]
+    assert g() == [1, 2, 7, 7]
+    # SAME_UPPER crops the odd pixel from the end, SAME_LOWER from the start
+    assert O.conv_transpose_geometry((1, 1, 3, 3), (1, 1, 3, 3), [2, 2], auto_pad="SAME_UPPER")[1] == [0, 0, 1, 1]
+    assert O.conv_transpose_geometry((1, 1, 3, 3), (1, 1, 3, 3), [2, 2], auto_pad="SAME_LOWER")[1] == [1, 1, 0, 0]
+
+
+@pytest.mark.parametrize("case", [
+    ((1, 4, 5, 6), (4, 3, 3, 3), dict(strides=[2, 2], pads=[1, 0, 0, 1], output_padding=[1, 0])),
+    ((2, 6, 4, 4), (6, 2, 4, 4), dict(strides=[2, 2], pads=[1, 1, 1, 1], group=3)),
+    ((1, 3, 5, 5), (3, 5, 3, 2), dict(strides=[1, 3], dilations=[2, 1])),
+    ((1, 8, 3, 3), (8, 1, 3, 3), dict(strides=[2, 2], group=8, output_padding=[1, 1])),
+])
+def test_conv_transpose_matches_torch(case):
+    """Against torch's float64 conv_transpose2d as an independent library
+    routine (pads here are symmetric per axis where torch needs them)."""
+    import torch
+    xs, ws, attrs = case
+    rng = np.random.default_rng(sum(xs) + sum(ws))
+    x = rng.uniform(-1, 1, xs).astype(np.float32)
+    w = rng.normal(0, 0.3, ws).astype(np.float32)
+    b = rng.normal(0, 0.1, ws[1] * attrs.get("group", 1)).astype(np.float32)
+    got = O.conv_transpose(x, w, b, **attrs)
+    s, p, d, shape = O.conv_transpose_geometry(x.shape, w.shape, attrs.get("strides"), attrs.get("pads"),
+                                               attrs.get("dilations"), attrs.get("group", 1),
+                                               attrs.get("output_padding"))
+    # torch crops symmetrically: run it uncropped and without the bias, append
+    # the output_padding rows / columns (which no input reaches), add the bias,
+    # then crop [begin, end) per axis
+    full = torch.nn.functional.conv_transpose2d(
+        torch.from_numpy(x).double(), torch.from_numpy(w).double(), None,
+        stride=tuple(s), padding=0, output_padding=0, groups=attrs.get("group", 1), dilation=tuple(d)).numpy()
+    op = attrs.get("output_padding", [0, 0])
+    full = np.pad(full, [(0, 0), (0, 0), (0, op[0]), (0, op[1])]) + b.astype(np.float64).reshape(1, -1, 1, 1)
+    want = full[:, :, p[0]:full.shape[2] - p[2], p[1]:full.shape[3] - p[3]]
+    assert got.shape == want.shape == tuple(shape)
+    np.testing.assert_allclose(got, want, atol=1e-5 * max(1.0, np.abs(want).max()))
+
+
+def test_conv_transpose_is_the_adjoint_of_conv():
+    """<Conv(z, W), x> == <z, ConvTranspose(x, W)>: the scatter is the exact
+    adjoint of the gather with the same weights, strides, pads and dilations."""
+    rng = np.random.default_rng(5)
+    z = rng.normal(size=(1, 3, 9, 8)).astype(np.float32)
+    w = rng.normal(size=(4, 3, 3, 3)).astype(np.float32)          # Conv: [Cout, Cin, k, k]
+    attrs = dict(strides=[2, 2], pads=[1, 1, 1, 1], dilations=[1, 1])
+    y = O.conv(z, w, None, **attrs)                                 # [1, 4, 5, 4]
+    x = rng.normal(size=y.shape).astype(np.float32)
+    zt = O.conv_transpose(x, w, None, strides=[2, 2], pads=[1, 1, 1, 1],
+                          output_shape=list(z.shape[2:]))           # ConvTranspose W: [C_in=4, C_out=3]
+    assert zt.shape == z.shape
+    lhs = float(np.dot(y.astype(np.float64).ravel(), x.astype(np.float64).ravel()))
+    rhs = float(np.dot(z.astype(np.float64).ravel(), zt.astype(np.float64).ravel()))
+    assert abs(lhs - rhs) <= 1e-4 * max(1.0, abs(lhs))
