@@ -170,6 +170,7 @@ def main():
             extras["gemm_sweep"] = sweep
             extras.update(bench_conv(torch, ctx, L, stream, rng, args.only))
             extras.update(bench_int8(torch, ctx, L, stream, rng, args.only))
+            extras.update(bench_widened(torch, ctx, L, stream, rng, args.only))
             extras.update(bench_e2e(torch, ctx, stream, args.only, args.no_cpu))
 
     line = {
@@ -182,7 +183,7 @@ def main():
         "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK_TFLOPS["f16"],
                      "unit": "TFLOP/s", "frac": round(tflops / PEAK_TFLOPS["f16"], 4),
                      "traffic": traffic, "algorithmic_bytes": alg_bytes,
-                     "kernel": "mfma_gemm_kernel<Op::F16, Tile<256,256,2,4,2>, DenseRows, DenseRows, FloatEpi<_Float16>, false, false>"},
+                     "kernel": "mfma_gemm_kernel<Op::F16, Tile<256,256,2,4,2,8>, DenseRows, DenseRows, FloatEpi<_Float16>, false, false>"},
         "wall_s_timed_region": round(wall, 3),
     }
     if not args.no_cpu and not args.only:
@@ -240,6 +241,50 @@ def bench_int8(torch, ctx, L, stream, rng, only):
     by = 4096 * 768 + 768 * 3072 + 4 * 4096 * 3072
     out["matmul_integer_i32"] = {"ms": round(t, 5), "tops": round(ops / 2 / t / 1e9, 2),
                                  "gbps": round(by / t / 1e6, 1), "frac_hbm": round(by / t / 1e6 / HBM_GBPS, 4)}
+    return out
+
+
+def bench_widened(torch, ctx, L, stream, rng, only):
+    """The convolution forms beyond plain Conv, at decoder / mobile-net shapes,
+    f16 NCHW, operands resident:
+    * depthwise 3x3 [1,256,56,56] (the direct kernel; memory-bound: GB/s of
+      input + output + filter against HBM);
+    * grouped 3x3 [1,256,56,56], 8 groups of 32 channels (one MFMA launch
+      per group);
+    * ConvTranspose 4x4 stride 2 [1,512,32,32] -> [1,256,64,64] (four
+      sub-pixel phases on the MFMA engine)."""
+    keys = ("depthwise_conv_f16", "grouped_conv_f16", "conv_transpose_f16")
+    if only and only not in keys:
+        return {}
+    out = {}
+    x = torch.from_numpy(rng.uniform(-1, 1, (1, 256, 56, 56)).astype(np.float32)).cuda().half()
+    if not only or only == keys[0]:
+        wt = ctx.weight_conv(rng.normal(0, 0.2, (256, 1, 3, 3)).astype(np.float32), dtype=L.F16)
+        y = torch.empty((1, 256, 56, 56), dtype=torch.float16, device="cuda")
+        t = time_launches(torch, stream, lambda: ctx.conv2d(x, wt, None, pads=(1, 1, 1, 1), group=256, out=y),
+                          100, 5)
+        by = 2 * (2 * 256 * 56 * 56 + 256 * 9)
+        fl = 2.0 * 256 * 56 * 56 * 9
+        out[keys[0]] = {"ms": round(t, 5), "gbps": round(by / t / 1e6, 1),
+                        "frac_hbm": round(by / t / 1e6 / HBM_GBPS, 4), "tflops": round(fl / t / 1e9, 2)}
+    if not only or only == keys[1]:
+        wt = ctx.weight_conv(rng.normal(0, 0.05, (256, 32, 3, 3)).astype(np.float32), dtype=L.F16)
+        y = torch.empty((1, 256, 56, 56), dtype=torch.float16, device="cuda")
+        t = time_launches(torch, stream, lambda: ctx.conv2d(x, wt, None, pads=(1, 1, 1, 1), group=8, out=y),
+                          100, 5)
+        fl = 2.0 * 256 * 56 * 56 * 32 * 9
+        out[keys[1]] = {"ms": round(t, 5), "tflops": round(fl / t / 1e9, 2),
+                        "frac_mfma": round(fl / t / 1e9 / PEAK_TFLOPS["f16"], 4)}
+    if not only or only == keys[2]:
+        xt = torch.from_numpy(rng.uniform(-1, 1, (1, 512, 32, 32)).astype(np.float32)).cuda().half()
+        wt = ctx.weight_conv_transpose(rng.normal(0, 0.02, (512, 256, 4, 4)).astype(np.float32), dtype=L.F16,
+                                       strides=(2, 2), pads=(1, 1, 1, 1))
+        y = torch.empty((1, 256, 64, 64), dtype=torch.float16, device="cuda")
+        t = time_launches(torch, stream, lambda: ctx.conv_transpose2d(xt, wt, None, strides=(2, 2),
+                                                                    pads=(1, 1, 1, 1), out=y), 20, 2)
+        fl = 2.0 * 512 * 32 * 32 * 256 * 16   # every input scatters a 4x4 tap into the output
+        out[keys[2]] = {"ms": round(t, 5), "tflops": round(fl / t / 1e9, 2),
+                        "frac_mfma": round(fl / t / 1e9 / PEAK_TFLOPS["f16"], 4)}
     return out
 
 

@@ -158,10 +158,14 @@ int ohip_weight_qconv(ohip_ctx* ctx, const ohip_weight_key* key, int src_dtype, 
                       int64_t cout, int64_t cin, int64_t kh, int64_t kw, const int32_t* zp, int n_zp,
                       const float* scale, int n_scale, ohip_weight** out);
 /* Float ConvTranspose filter: host [Cin, Cout/group, KH, KW] of src_dtype,
- * converted to dtype and kept in that layout (conv/transpose.rs:78-214). */
+ * converted to dtype (conv/transpose.rs:78-214).  The node's strides, top /
+ * left pads, dilations and group select its form: for group 1, dilation 1
+ * and a kernel at least as wide as the stride, the sub-pixel phase filters
+ * of the MFMA path are packed as well. */
 int ohip_weight_conv_transpose(ohip_ctx* ctx, const ohip_weight_key* key, int src_dtype, const void* host,
-                               int64_t cin, int64_t cout_per_group, int64_t kh, int64_t kw, int dtype,
-                               ohip_weight** out);
+                               int64_t cin, int64_t cout_per_group, int64_t kh, int64_t kw, int64_t stride_h,
+                               int64_t stride_w, int64_t pad_t, int64_t pad_l, int64_t dil_h, int64_t dil_w,
+                               int64_t group, int dtype, ohip_weight** out);
 void ohip_weight_release(ohip_weight* w);
 size_t ohip_weight_bytes(const ohip_weight* w);
 
@@ -216,9 +220,12 @@ int64_t ohip_conv_out_dim(int64_t in, int64_t pad_begin, int64_t pad_end, int64_
 /* ConvTranspose, rank 2 (ConvTransposeOp, oxionnx-ops/src/registry/conv_ops/conv.rs:556-710,
  * conv/transpose.rs:78-309, conv_typed.rs:159-222): Y = scatter(X, W) + bias with
  * W [Cin, Cout/group, KH, KW]; the caller resolves output_shape / auto_pad into
- * pads (conv.rs:412-470).  X and Y are NCHW of `dtype`; each output is
- * accumulated in f32 in the reference's scatter order, so the result equals
- * the reference's (f16 / bf16 rounded once, RNE). */
+ * pads (conv.rs:412-470).  X and Y are NCHW of `dtype`.  With phase filters
+ * (see ohip_weight_conv_transpose) every output phase runs as a stride-1
+ * implicit-GEMM convolution on the MFMA engine (f32 accumulation, results
+ * within the reference's tolerance); otherwise an output-stationary gather
+ * accumulates each output in the reference's scatter order, equal to the
+ * reference's result (f16 / bf16 rounded once, RNE). */
 typedef struct {
     int64_t n, c, h, w;
     int64_t cout, kh, kw, group;

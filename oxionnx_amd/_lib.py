@@ -159,7 +159,8 @@ SIGNATURES = {
     "ohip_conv2d": (ctypes.c_int, [VP, ctypes.POINTER(ConvDesc), VP, VP, VP, VP]),
     "ohip_conv_out_dim": (I64, [I64, I64, I64, I64, I64, I64]),
     "ohip_weight_conv_transpose": (ctypes.c_int, [VP, ctypes.POINTER(WeightKey), ctypes.c_int, VP, I64, I64, I64,
-                                                  I64, ctypes.c_int, ctypes.POINTER(VP)]),
+                                                  I64, I64, I64, I64, I64, I64, I64, I64, ctypes.c_int,
+                                                  ctypes.POINTER(VP)]),
     "ohip_conv_transpose2d": (ctypes.c_int, [VP, ctypes.POINTER(ConvTDesc), VP, VP, VP, VP]),
     "ohip_conv_transpose_out_dim": (I64, [I64, I64, I64, I64, I64, I64, I64]),
     "ohip_qgemm": (ctypes.c_int, [VP, ctypes.POINTER(QGemmDesc), VP, VP, VP]),

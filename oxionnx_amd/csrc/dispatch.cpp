@@ -487,7 +487,8 @@ int do_conv_transpose(ohip_ctx* ctx, const ohip_node* nd, int placement, ohip_ou
   ohip_weight_key key{name.c_str(), label.c_str()};
   const bool cache = w->is_initializer && !name.empty();
   ohip_weight* wt = nullptr;
-  int rc = ohip_weight_conv_transpose(ctx, cache ? &key : nullptr, w->dtype, w->data, c, coutg, kh, kw, dt, &wt);
+  int rc = ohip_weight_conv_transpose(ctx, cache ? &key : nullptr, w->dtype, w->data, c, coutg, kh, kw, strides[0],
+                                      strides[1], pads[0], pads[1], dil[0], dil[1], group, dt, &wt);
   if (rc) return rc;
   Stage st(ctx);
   const void* xd = st.operand(x);

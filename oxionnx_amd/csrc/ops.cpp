@@ -80,6 +80,11 @@ struct ohip_weight {
   float* comb = nullptr;          // device, rows entries (integer only)
   float comb_a = NAN, comb_y = NAN;
   size_t bytes = 0;
+  // ConvTranspose only: the sub-pixel phase filters (packed like a Conv
+  // filter, phase ry * ph_sw + rx) for strides (ph_sh, ph_sw) and pad
+  // residues (ph_pt, ph_pl); empty when the gather kernel serves the node.
+  std::vector<ohip_weight*> phases;
+  int64_t ph_sh = 0, ph_sw = 0, ph_pt = 0, ph_pl = 0;
 };
 
 // Stream-ordered caching pool for device buffers (activations, staging).
@@ -223,6 +228,7 @@ extern "C" int ohip_ctx_create(int device, ohip_ctx** out) {
 
 static void weight_free(ohip_weight* w) {
   if (!w) return;
+  for (auto* p : w->phases) weight_free(p);
   if (w->data) (void)hipFree(w->data);
   if (w->colsum) (void)hipFree(w->colsum);
   if (w->flip) (void)hipFree(w->flip);
@@ -721,29 +727,70 @@ extern "C" int ohip_weight_conv(ohip_ctx* ctx, const ohip_weight_key* key, int s
 }
 
 // ConvTranspose filter: [Cin][Cout/group][KH][KW] kept as is (converted to
-// the compute dtype); the gather kernel reads it in that layout.
+// the compute dtype) for the gather kernel, plus, for group 1, dilation 1 and
+// a kernel at least as wide as the stride, the sub-pixel phase filters.
+// Output phase (ry, rx) = (oy mod sh, ox mod sw) receives exactly the taps
+// ky = ky0 + sh * m with ky0 = (ry + pt) mod sh (likewise kx), and reads input
+// row iy = (oy + pt - ky) / sh, so over the phase's output grid it is a
+// stride-1 convolution with Mky = ceil((KH - ky0) / sh) taps, taken in
+// reverse: phase tap m' holds ky0 + sh * (Mky - 1 - m').  Each phase filter is
+// packed like a Conv filter, [Cout][Mky][Mkx][Cp].
 extern "C" int ohip_weight_conv_transpose(ohip_ctx* ctx, const ohip_weight_key* key, int src_dt, const void* host,
-                                          int64_t cin, int64_t coutg, int64_t kh, int64_t kw, int dt,
-                                          ohip_weight** out) {
+                                          int64_t cin, int64_t coutg, int64_t kh, int64_t kw, int64_t stride_h,
+                                          int64_t stride_w, int64_t pad_t, int64_t pad_l, int64_t dil_h,
+                                          int64_t dil_w, int64_t group, int dt, ohip_weight** out) {
   int rc = activate(ctx);
   if (rc) return rc;
-  if (!host || !out || !is_float(src_dt) || !is_float(dt) || cin <= 0 || coutg <= 0 || kh <= 0 || kw <= 0)
+  if (!host || !out || !is_float(src_dt) || !is_float(dt) || cin <= 0 || coutg <= 0 || kh <= 0 || kw <= 0 ||
+      stride_h <= 0 || stride_w <= 0 || pad_t < 0 || pad_l < 0 || dil_h <= 0 || dil_w <= 0 || group <= 0)
     return fail(OHIP_E_INVALID, "ohip_weight_conv_transpose: bad arguments");
   std::lock_guard<std::mutex> lock(ctx->mu);
   const int64_t count = cin * coutg * kh * kw;
   const size_t src_bytes = (size_t)count * elem_bytes(src_dt);
-  std::string ks = key && key->name ? cache_key(key, WK_CONVT, dt, src_bytes, {cin, coutg, kh, kw}) : std::string();
+  const bool phased = group == 1 && dil_h == 1 && dil_w == 1 && kh >= stride_h && kw >= stride_w;
+  std::string ks;
+  if (key && key->name)
+    ks = cache_key(key, WK_CONVT, dt, src_bytes,
+                   {cin, coutg, kh, kw, group, phased ? stride_h : 0, phased ? stride_w : 0,
+                    phased ? pad_t % stride_h : 0, phased ? pad_l % stride_w : 0});
   if (ohip_weight* hit = cache_lookup(ctx, key, ks)) {
     *out = hit;
     return OHIP_OK;
   }
-  std::vector<char> conv((size_t)count * elem_bytes(dt));
+  const int eb = elem_bytes(dt);
+  std::vector<char> conv((size_t)count * eb);
   for (int64_t i = 0; i < count; ++i) write_elem(dt, conv.data(), i, src_dt, host, i);
   auto* w = new ohip_weight();
   w->kind = WK_CONVT; w->dtype = dt; w->rows = cin; w->k = coutg; w->kh = kh; w->kw = kw;
-  w->ld_bytes = coutg * kh * kw * elem_bytes(dt);
+  w->ld_bytes = coutg * kh * kw * eb;
   rc = weight_upload(ctx, w, conv.data(), conv.size());
   if (rc) { weight_free(w); return rc; }
+  if (phased) {
+    w->ph_sh = stride_h; w->ph_sw = stride_w; w->ph_pt = pad_t % stride_h; w->ph_pl = pad_l % stride_w;
+    const int64_t ce = chunk_elems(dt), cp = round_up(cin, ce);
+    for (int64_t ry = 0; ry < stride_h; ++ry)
+      for (int64_t rx = 0; rx < stride_w; ++rx) {
+        const int64_t ky0 = (ry + pad_t) % stride_h, kx0 = (rx + pad_l) % stride_w;
+        const int64_t mky = (kh - ky0 + stride_h - 1) / stride_h, mkx = (kw - kx0 + stride_w - 1) / stride_w;
+        const int64_t kp = mky * mkx * cp;
+        std::vector<char> packed((size_t)(coutg * kp) * eb, 0);
+        for (int64_t o = 0; o < coutg; ++o)
+          for (int64_t my = 0; my < mky; ++my)
+            for (int64_t mx = 0; mx < mkx; ++mx) {
+              const int64_t ky = ky0 + stride_h * (mky - 1 - my), kx = kx0 + stride_w * (mkx - 1 - mx);
+              for (int64_t c = 0; c < cin; ++c)
+                write_elem(dt, packed.data(), o * kp + (my * mkx + mx) * cp + c, src_dt, host,
+                           ((c * coutg + o) * kh + ky) * kw + kx);
+            }
+        auto* ph = new ohip_weight();
+        ph->ctx = ctx; ph->kind = WK_CONV; ph->dtype = dt; ph->rows = coutg; ph->k = cin; ph->kh = mky; ph->kw = mkx;
+        ph->cpc = (int)(cp / ce); ph->kc = (int)(kp / ce); ph->ld_bytes = kp * eb;
+        rc = weight_upload(ctx, ph, packed.data(), packed.size());
+        if (rc) { weight_free(ph); weight_free(w); return rc; }
+        w->bytes += ph->bytes;
+        w->phases.push_back(ph);
+      }
+  }
   return weight_finish(ctx, key, ks, w, out);
 }
 
@@ -1224,6 +1271,59 @@ extern "C" int ohip_conv_transpose2d(ohip_ctx* ctx, const ohip_convt_desc* d, co
     return fail(OHIP_DECLINED, "ohip_conv_transpose2d: extent too large");
   std::lock_guard<std::mutex> lock(ctx->mu);
   ctx->counters.dispatches++;
+  if (!w->phases.empty() && d->group == 1 && d->dil_h == 1 && d->dil_w == 1 && w->ph_sh == d->stride_h &&
+      w->ph_sw == d->stride_w && w->ph_pt == d->pad_t % d->stride_h && w->ph_pl == d->pad_l % d->stride_w) {
+    // sub-pixel phases on the MFMA engine: every phase is a stride-1
+    // implicit-im2col convolution of the staged input, written to the
+    // phase's strided output positions
+    const int eb = elem_bytes(d->dtype), ce = 16 / eb;
+    const int64_t cp = round_up(d->c, ce), sh = d->stride_h, sw = d->stride_w;
+    int64_t max_rows = 0;
+    for (int64_t ry = 0; ry < sh; ++ry)
+      for (int64_t rx = 0; rx < sw; ++rx)
+        max_rows = std::max<int64_t>(max_rows, ((oh - ry + sh - 1) / sh) * ((ow - rx + sw - 1) / sw));
+    int max_splits = 1;
+    for (auto* ph : w->phases)
+      max_splits = std::max(max_splits, plan_splits((int)max_rows, (int)d->cout, ph->kc, ctx->tile_override));
+    ScratchPlan plan;
+    size_t ix = plan.add((size_t)(d->n * d->h * d->w * cp) * eb);
+    size_t iw = max_splits > 1 ? plan.add(split_ws_bytes((int)max_rows, (int)d->cout, max_splits)) : SIZE_MAX;
+    rc = scratch_reserve(ctx, plan.total());
+    if (rc) return rc;
+    void* px = scratch_at(ctx, plan, ix);
+    HIP_TRY(run_nchw_to_nhwc(eb, x, px, (int)d->n, (int)d->c, (int)(d->h * d->w), (int)cp, ctx->stream),
+            "NCHW -> NHWC");
+    for (int64_t n = 0; n < d->n; ++n)
+      for (int64_t ry = 0; ry < sh; ++ry)
+        for (int64_t rx = 0; rx < sw; ++rx) {
+          const ohip_weight* ph = w->phases[(size_t)(ry * sw + rx)];
+          const int64_t ohp = (oh - ry + sh - 1) / sh, owp = (ow - rx + sw - 1) / sw;
+          if (ohp <= 0 || owp <= 0) continue;
+          const int64_t ky0 = (ry + d->pad_t) % sh, kx0 = (rx + d->pad_l) % sw;
+          const int64_t c0y = (ry + d->pad_t - ky0) / sh, c0x = (rx + d->pad_l - kx0) / sw;
+          Im2colOperand col{};
+          col.base = static_cast<const char*>(px) + n * d->h * d->w * cp * eb;
+          col.H = (int)d->h; col.W = (int)d->w; col.OH = (int)ohp; col.OW = (int)owp;
+          col.KW = (int)ph->kw; col.cpc = (int)(cp / ce);
+          col.sh = 1; col.sw = 1; col.dh = 1; col.dw = 1;
+          col.pt = (int)(ph->kh - 1 - c0y); col.pl = (int)(ph->kw - 1 - c0x);
+          col.rows = (int)(ohp * owp); col.kc = ph->kc;
+          col.xor_mask = 0; col.pad16 = pad16(ctx, 0);
+          DenseOperand wt{ph->data, ph->ld_bytes, (int)d->cout, ph->kc, 0, 0u, pad16(ctx, 0)};
+          FloatOut o{};
+          o.y = static_cast<char*>(y) + (n * d->cout * oh * ow + ry * ow + rx) * eb;
+          o.alpha = 1.0f; o.beta = 1.0f; o.bias = bias; o.bias_mode = BIAS_J; o.act = ACT_NONE;
+          o.si = sw; o.sj = oh * ow; o.bstride = sh * ow; o.ohw = (int)owp;
+          o.P = (int)(ohp * owp); o.Q = (int)d->cout; o.vec = 0;
+          const int splits = plan_splits(o.P, o.Q, ph->kc, ctx->tile_override);
+          o.splits = splits;
+          o.split_ws = splits > 1 ? scratch_at(ctx, plan, iw) : nullptr;
+          DENSE_FITS_OR_DECLINE(wt, "ohip_conv_transpose2d");
+          hipError_t e = run_conv_float(d->dtype, col, wt, true, o, ctx->tile_override, ctx->stream);
+          if (e != hipSuccess) return hip_fail(e, "ohip_conv_transpose2d phase launch");
+        }
+    return OHIP_OK;
+  }
   ConvTArgs a{};
   a.N = (int)d->n; a.C = (int)d->c; a.H = (int)d->h; a.W = (int)d->w; a.cout = (int)d->cout;
   a.cg = (int)(d->c / d->group); a.coutg = (int)(d->cout / d->group); a.KH = (int)d->kh; a.KW = (int)d->kw;

@@ -153,15 +153,18 @@ class HipContext:
                                          w.ctypes.data_as(ctypes.c_void_p), *w.shape, dtype, ctypes.byref(h)))
         return Weight(self, h, "conv", dtype, w.shape, name is not None)
 
-    def weight_conv_transpose(self, w, dtype=L.F32, name=None, label="ConvTranspose.W"):
-        """ConvTranspose filter [Cin, Cout/group, KH, KW]."""
+    def weight_conv_transpose(self, w, dtype=L.F32, strides=(1, 1), pads=(0, 0, 0, 0), dilations=(1, 1),
+                              group=1, name=None, label="ConvTranspose.W"):
+        """ConvTranspose filter [Cin, Cout/group, KH, KW], packed for the node's
+        strides / top-left pads / dilations / group."""
         w = np.ascontiguousarray(w)
         if w.dtype == np.float64:
             w = w.astype(np.float32)
         h = ctypes.c_void_p()
         L.check(L.lib().ohip_weight_conv_transpose(self.h, _key(name, label), _np_ohip_dtype(w),
-                                                   w.ctypes.data_as(ctypes.c_void_p), *w.shape, dtype,
-                                                   ctypes.byref(h)))
+                                                   w.ctypes.data_as(ctypes.c_void_p), *w.shape, strides[0],
+                                                   strides[1], pads[0], pads[1], dilations[0], dilations[1],
+                                                   group, dtype, ctypes.byref(h)))
         return Weight(self, h, "convt", dtype, w.shape, name is not None)
 
     def weight_qgemm(self, b, zp=None, scale=None, trans_b=False, name=None, label="QLinearMatMul.B"):

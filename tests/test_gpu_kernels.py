@@ -204,48 +204,63 @@ def test_grouped_conv_matches_oracle(torch, ctx, case, dt):
         assert _rel_err(got, want) <= HALF_TOL
 
 
-# ConvTranspose: (x shape, w shape [Cin, Cout/g, kh, kw], attrs with resolved pads)
+# ConvTranspose: (x shape, w shape [Cin, Cout/g, kh, kw], attrs with resolved pads).
+# Group 1 / dilation 1 / kernel >= stride runs the sub-pixel phases on the
+# MFMA engine (within the tolerances); the rest runs the gather kernel, which
+# adds every output's contributions in the reference's order (bit-exact).
 CONVT_CASES = [
     ((1, 8, 7, 9), (8, 6, 3, 3), dict(strides=[2, 2], pads=[1, 1, 1, 1], output_padding=[1, 1])),
     ((2, 6, 5, 5), (6, 4, 4, 4), dict(strides=[2, 2], pads=[1, 1, 1, 1], group=2)),
     ((1, 4, 6, 5), (4, 3, 3, 2), dict(strides=[1, 3], pads=[0, 1, 2, 0], dilations=[2, 1])),
     ((1, 16, 4, 4), (16, 1, 3, 3), dict(strides=[2, 2], group=16)),
     ((1, 64, 8, 8), (64, 32, 4, 4), dict(strides=[2, 2], pads=[1, 1, 1, 1])),
+    ((2, 24, 5, 7), (24, 40, 3, 3), dict(strides=[1, 1], pads=[1, 0, 0, 2])),
+    ((1, 32, 6, 5), (32, 16, 5, 3), dict(strides=[3, 2], pads=[2, 1, 1, 0], output_padding=[2, 1])),
 ]
+
+
+def _convt_uses_gather(ws, attrs):
+    s = attrs.get("strides", [1, 1])
+    return (attrs.get("group", 1) != 1 or attrs.get("dilations", [1, 1]) != [1, 1]
+            or ws[2] < s[0] or ws[3] < s[1])
 
 
 @pytest.mark.parametrize("case", CONVT_CASES, ids=lambda c: f"{c[0]}x{c[1]}")
 @pytest.mark.parametrize("dt", ["f32", "f16", "bf16"])
-def test_conv_transpose_bit_exact(torch, ctx, case, dt):
-    """Each output sums its scatter contributions in the reference's order,
-    from an f32 zero, bias last: the f32 result equals the oracle's bit for
-    bit, and the half results equal its once-rounded values."""
+def test_conv_transpose_matches_oracle(torch, ctx, case, dt):
     from oxionnx_amd import _lib as L
     xs, ws, attrs = case
     rng = np.random.default_rng(sum(xs) + sum(ws))
     x = rng.uniform(-1, 1, xs).astype(np.float32)
     w = rng.normal(0, 0.3, ws).astype(np.float32)
     b = rng.normal(0, 0.1, ws[1] * attrs.get("group", 1)).astype(np.float32)
-    kw_ = dict(strides=attrs.get("strides", [1, 1]), pads=attrs.get("pads", [0, 0, 0, 0]),
-               dilations=attrs.get("dilations", [1, 1]), output_padding=attrs.get("output_padding", [0, 0]),
-               group=attrs.get("group", 1))
+    geo = dict(strides=attrs.get("strides", [1, 1]), pads=attrs.get("pads", [0, 0, 0, 0]),
+               dilations=attrs.get("dilations", [1, 1]), group=attrs.get("group", 1))
+    exact = _convt_uses_gather(ws, attrs)
     if dt == "f32":
-        wt = ctx.weight_conv_transpose(w)
-        y = ctx.conv_transpose2d(_dev(torch, x), wt, _dev(torch, b), **kw_).cpu().numpy()
+        wt = ctx.weight_conv_transpose(w, **geo)
+        y = ctx.conv_transpose2d(_dev(torch, x), wt, _dev(torch, b),
+                                 output_padding=attrs.get("output_padding", [0, 0]), **geo).cpu().numpy()
         want = O.conv_transpose(x, w, b, **attrs)
         assert y.shape == want.shape
-        np.testing.assert_array_equal(y.view(np.uint32), want.view(np.uint32))
+        if exact:
+            np.testing.assert_array_equal(y.view(np.uint32), want.view(np.uint32))
+        else:
+            assert np.max(np.abs(y.astype(np.float64) - want)) <= F32_TOL * max(1.0, float(np.abs(want).max()))
     else:
         bf = dt == "bf16"
         tdt = torch.bfloat16 if bf else torch.float16
         xh, wh, bh = (O.f32_to_half_bits(v, bf) for v in (x, w, b))
-        wt = ctx.weight_conv_transpose(O.half_bits_to_f32(wh, bf), dtype=L.BF16 if bf else L.F16)
+        wt = ctx.weight_conv_transpose(O.half_bits_to_f32(wh, bf), dtype=L.BF16 if bf else L.F16, **geo)
         xt = torch.from_numpy(xh.view(np.int16)).cuda().view(tdt)
         bt = torch.from_numpy(bh.view(np.int16)).cuda().view(tdt)
-        y = ctx.conv_transpose2d(xt, wt, bt, **kw_)
+        y = ctx.conv_transpose2d(xt, wt, bt, output_padding=attrs.get("output_padding", [0, 0]), **geo)
         got = y.view(torch.int16).cpu().numpy().view(np.uint16)
         want = O.conv_transpose_half(xh, wh, bh, bf16=bf, **attrs)
-        np.testing.assert_array_equal(got, want)
+        if exact:
+            np.testing.assert_array_equal(got, want)
+        else:
+            assert _rel_err(O.half_bits_to_f32(got, bf), O.half_bits_to_f32(want, bf)) <= HALF_TOL
 
 
 @pytest.mark.parametrize("c", G.cases("Conv") + G.cases("Conv1D"), ids=lambda c: c["name"])
