@@ -188,6 +188,19 @@ typedef struct {
 int ohip_gemm(ohip_ctx* ctx, const ohip_gemm_desc* d, const void* a, const ohip_weight* b,
               const void* c, void* y);
 
+/* MatMul with both operands on the device (MatMulOp, matmul_gemm.rs:9-126;
+ * matmul_f32_into / typed_matmul_batch_info, math_typed.rs:85-115,334-423):
+ * A [a_batches][M][K] and B [b_batches][K][N] row-major of `dtype`, Y
+ * [batch][M][N]; slice s reads A slice s % a_batches and B slice
+ * s % b_batches, like the reference's strided batch (oxionnx-cuda/src/matmul.rs:189-252).
+ * B is brought into K-contiguous rows in scratch on every call. */
+typedef struct {
+    int64_t m, k, n;
+    int64_t batch, a_batches, b_batches;
+    int dtype;                     /* F32 / F16 / BF16 */
+} ohip_matmul_desc;
+int ohip_matmul(ohip_ctx* ctx, const ohip_matmul_desc* d, const void* a, const void* b, void* y);
+
 /* Conv, rank 2, any group (oxionnx-ops/src/registry/conv_ops/conv.rs:163-323
  * and conv_typed.rs:54-153): Y = act(conv(X, W) + bias).  Groups run one
  * MFMA launch each, or a direct kernel when a group is too narrow for an

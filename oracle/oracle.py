@@ -435,6 +435,45 @@ def gemm_half(a_bits, b_bits, c_bits=None, alpha=1.0, beta=1.0, trans_a=0, trans
     return out
 
 
+def typed_matmul_batch_info(a_shape, b_shape):
+    """typed_matmul_batch_info (math_typed.rs:85-115): the output batch is the
+    numpy broadcast of the batch prefixes; a_batches / b_batches are the
+    products of each operand's own prefix."""
+    if len(a_shape) < 2 or len(b_shape) < 2 or a_shape[-1] != b_shape[-2]:
+        raise ValueError("typed matmul: shapes")
+    out_batch = list(np.broadcast_shapes(tuple(a_shape[:-2]), tuple(b_shape[:-2])))
+    batch = int(np.prod(out_batch)) if out_batch else 1
+    a_batches = int(np.prod(a_shape[:-2])) if len(a_shape) > 2 else 1
+    b_batches = int(np.prod(b_shape[:-2])) if len(b_shape) > 2 else 1
+    return batch, a_batches, b_batches, out_batch + [a_shape[-2], b_shape[-1]]
+
+
+def matmul_batched(a, b):
+    """matmul_f32_into (math_typed.rs:334-423): slice s is A slice s % a_batches
+    times B slice s % b_batches; each slice in float64 (the reference's sgemm
+    is pinned at tolerance)."""
+    a = np.asarray(a, np.float32)
+    b = np.asarray(b, np.float32)
+    batch, na, nb, shape = typed_matmul_batch_info(a.shape, b.shape)
+    a3 = a.reshape(na, a.shape[-2], a.shape[-1]).astype(np.float64)
+    b3 = b.reshape(nb, b.shape[-2], b.shape[-1]).astype(np.float64)
+    out = np.stack([a3[s % na] @ b3[s % nb] for s in range(batch)])
+    return out.reshape(shape)
+
+
+def matmul_batched_half(a_bits, b_bits, bf16=False):
+    """matmul_f16 / matmul_bf16 (math_typed.rs:147-189, 258-317): the same slice
+    rule, each slice the per-element ascending-p f32 loop rounded once (RNE),
+    which is gemm_half with alpha 1 and no C."""
+    a = np.asarray(a_bits, np.uint16)
+    b = np.asarray(b_bits, np.uint16)
+    batch, na, nb, shape = typed_matmul_batch_info(a.shape, b.shape)
+    a3 = a.reshape(na, a.shape[-2], a.shape[-1])
+    b3 = b.reshape(nb, b.shape[-2], b.shape[-1])
+    out = np.stack([gemm_half(a3[s % na], b3[s % nb], None, bf16=bf16) for s in range(batch)])
+    return out.reshape(shape)
+
+
 def gemm(a, b, c=None, alpha=1.0, beta=1.0, trans_a=0, trans_b=0, nthreads=1):
     """gemm_f32 (math_typed.rs:759-788); single-threaded like the reference's
     2-D sgemm (matrixmultiply threading off, Cargo.toml:43)."""

@@ -71,6 +71,10 @@ class ConvTDesc(ctypes.Structure):
                                     "out_pad_w")] + [("dtype", ctypes.c_int)]
 
 
+class MatMulDesc(ctypes.Structure):
+    _fields_ = [(f, I64) for f in ("m", "k", "n", "batch", "a_batches", "b_batches")] + [("dtype", ctypes.c_int)]
+
+
 class QGemmDesc(ctypes.Structure):
     _fields_ = [("m", I64), ("k", I64), ("n", I64), ("a_dtype", ctypes.c_int),
                 ("a_zp", ctypes.POINTER(ctypes.c_int32)), ("n_azp", ctypes.c_int), ("out_kind", ctypes.c_int),
@@ -157,6 +161,7 @@ SIGNATURES = {
     "ohip_weight_bytes": (ctypes.c_size_t, [VP]),
     "ohip_gemm": (ctypes.c_int, [VP, ctypes.POINTER(GemmDesc), VP, VP, VP, VP]),
     "ohip_conv2d": (ctypes.c_int, [VP, ctypes.POINTER(ConvDesc), VP, VP, VP, VP]),
+    "ohip_matmul": (ctypes.c_int, [VP, ctypes.POINTER(MatMulDesc), VP, VP, VP]),
     "ohip_conv_out_dim": (I64, [I64, I64, I64, I64, I64, I64]),
     "ohip_weight_conv_transpose": (ctypes.c_int, [VP, ctypes.POINTER(WeightKey), ctypes.c_int, VP, I64, I64, I64,
                                                   I64, I64, I64, I64, I64, I64, I64, I64, ctypes.c_int,

@@ -587,6 +587,49 @@ hipError_t run_conv_transpose(int dtype, const void* x, const void* w, const voi
   return hipGetLastError();
 }
 
+// ---------------------------------------------------------------- batched transpose
+// dst[s][n][c] = c < K ? src[s][c][n] : 0 for the slices s of a batched [K][N]
+// matrix (row stride ld elements in dst): MatMul's B operand brought into
+// K-contiguous rows.  32 x 32 tiles through LDS, coalesced on both sides.
+template <class T>
+__global__ void __launch_bounds__(256)
+transpose_batched_kernel(const T* __restrict__ src, T* __restrict__ dst, int K, int N, int ld) {
+  __shared__ T tile[32][33];
+  const int s = blockIdx.z;
+  const int c0 = blockIdx.y * 32, n0 = blockIdx.x * 32;
+  const T* sp = src + (int64_t)s * K * N;
+  T* dp = dst + (int64_t)s * N * ld;
+  const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;
+  for (int r = ty; r < 32; r += 8) {
+    const int c = c0 + r, n = n0 + tx;
+    tile[r][tx] = (c < K && n < N) ? sp[(int64_t)c * N + n] : T(0);
+  }
+  __syncthreads();
+  for (int r = ty; r < 32; r += 8) {
+    const int n = n0 + r, c = c0 + tx;
+    if (n < N && c < ld) dp[(int64_t)n * ld + c] = tile[tx][r];
+  }
+}
+
+hipError_t run_transpose_batched(int elem_bytes, const void* src, void* dst, int slices, int K, int N, int ld,
+                                 hipStream_t st) {
+  if (slices <= 0 || K <= 0 || N <= 0) return hipSuccess;
+  if (slices > 65535) return hipErrorInvalidValue;
+  dim3 grid((unsigned)((N + 31) / 32), (unsigned)((ld + 31) / 32), (unsigned)slices), block(256);
+  switch (elem_bytes) {
+    case 2:
+      hipLaunchKernelGGL(transpose_batched_kernel<uint16_t>, grid, block, 0, st,
+                         reinterpret_cast<const uint16_t*>(src), reinterpret_cast<uint16_t*>(dst), K, N, ld);
+      break;
+    case 4:
+      hipLaunchKernelGGL(transpose_batched_kernel<uint32_t>, grid, block, 0, st,
+                         reinterpret_cast<const uint32_t*>(src), reinterpret_cast<uint32_t*>(dst), K, N, ld);
+      break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
 // dst[r][c] = c < K ? src[r * rs + c * cs] : 0 for a [R][ld] destination: pads a
 // row-major operand to whole 16-byte chunks, or materialises a transpose.
 template <class T>

@@ -514,9 +514,56 @@ int do_conv_transpose(ohip_ctx* ctx, const ohip_node* nd, int placement, ohip_ou
 }
 
 // ------------------------------------------------------------------ Gemm / MatMul
+// MatMul whose B is batched (or already on the device): both operands on the
+// device, the batch bookkeeping of typed_matmul_batch_info (math_typed.rs:85-115,
+// numpy broadcasting of the batch prefixes; slice s reads A slice s % a_batches
+// and B slice s % b_batches, math_typed.rs:352-369).
+int do_matmul_batched(ohip_ctx* ctx, const ohip_node* nd, int placement, ohip_output* out) {
+  const ohip_tensor *a = input(nd, 0), *b = input(nd, 1);
+  const int dt = a->dtype;
+  if (dt != OHIP_F32 && dt != OHIP_F16 && dt != OHIP_BF16) return decline("MatMul: dtype");
+  if (b->device && b->dtype != dt) return decline("MatMul: operand dtypes differ");
+  if (a->rank < 2 || b->rank < 2) return decline("MatMul: batched operands must be at least 2-D");
+  const int64_t m = a->shape[a->rank - 2], k = a->shape[a->rank - 1];
+  const int64_t k2 = b->shape[b->rank - 2], n = b->shape[b->rank - 1];
+  if (k != k2) return decline("MatMul: K");
+  std::vector<int64_t> ab(a->shape, a->shape + a->rank - 2), bb(b->shape, b->shape + b->rank - 2);
+  const size_t r = std::max(ab.size(), bb.size());
+  std::vector<int64_t> ob(r, 1);
+  for (size_t i = 0; i < r; ++i) {
+    const int64_t x = i + ab.size() >= r ? ab[i + ab.size() - r] : 1;
+    const int64_t y = i + bb.size() >= r ? bb[i + bb.size() - r] : 1;
+    if (x != y && x != 1 && y != 1) return decline("MatMul: batch dimensions do not broadcast");
+    ob[i] = std::max(x, y);
+  }
+  int64_t batch = 1, a_batches = 1, b_batches = 1;
+  for (auto v : ob) batch *= v;
+  for (auto v : ab) a_batches *= v;
+  for (auto v : bb) b_batches *= v;
+  if (m == 0 || n == 0 || k == 0 || batch == 0) return decline("MatMul: empty");
+  ohip_tuning tun;
+  ohip_get_tuning(ctx, &tun);
+  if (!ohip_gemm_admits(&tun, m * batch, k, n, false)) return decline("MatMul: gate");
+  Stage st(ctx);
+  const void* ad = st.operand(a);
+  const void* bd = st.operand(b);
+  std::vector<int64_t> oshape = ob;
+  oshape.push_back(m);
+  oshape.push_back(n);
+  const size_t obytes = (size_t)(batch * m * n) * ebytes(dt);
+  void* yd = st.alloc(obytes);
+  if (!ad || !bd || !yd) return OHIP_E_NOMEM;
+  ohip_matmul_desc d{m, k, n, batch, a_batches, b_batches, dt};
+  int rc = ohip_matmul(ctx, &d, ad, bd, yd);
+  if (rc) return rc;
+  set_out(out, dt, oshape);
+  return finish_output(ctx, st, placement, out, yd, obytes, dt);
+}
+
 int do_gemm(ohip_ctx* ctx, const ohip_node* nd, bool is_matmul, int placement, ohip_output* out) {
   const ohip_tensor *a = input(nd, 0), *b = input(nd, 1), *c = is_matmul ? nullptr : input(nd, 2);
   if (!a || !b) return decline("Gemm: missing input");
+  if (is_matmul && (b->rank > 2 || b->device)) return do_matmul_batched(ctx, nd, placement, out);
   if (!host_only(b) || (c && !host_only(c))) return decline("Gemm: B / C must be host tensors");
   const int dt = a->dtype;
   if (dt != OHIP_F32 && dt != OHIP_F16 && dt != OHIP_BF16) return decline("Gemm: dtype");

@@ -24,6 +24,8 @@ struct DenseOperand {
   int kwrap;          // > 0: loop chunk g >= kwrap reads chunk g - kwrap
   uint32_t xor_mask;  // applied after the LDS read: 0x80808080 turns u8 into (u8 - 128) as int8
   const void* pad16;  // device address of 16 bytes read for any chunk outside the matrix
+  int zmod;           // batched launch: slice z reads matrix z % zmod (0 / 1: one matrix for all)
+  int64_t zstride;    // bytes between those matrices
 };
 
 // Implicit im2col rows over an NHWC activation with channels padded to cpc
@@ -47,6 +49,8 @@ struct OutMap {
   int vec;
   int splits;      // > 1: split-K over `splits` slices, partial sums in split_ws
   void* split_ws;  // splits * Q * round_up(P, 4) accumulators (4 bytes each)
+  int batch;       // > 1: a batched launch of `batch` independent contractions (no split-K)
+  int64_t zstride; // bytes between the batch slices' outputs
 };
 
 // Split-K plan.  The slices run on the 64x64 four-stage tile when its
@@ -148,6 +152,10 @@ struct DirectQConvArgs {
   int64_t ldo;
 };
 hipError_t run_qconv_direct(const void* x, const void* w, void* y, const DirectQConvArgs& a, hipStream_t st);
+
+// dst[s][n][c] = c < K ? src[s][c][n] : 0, ld elements per dst row.
+hipError_t run_transpose_batched(int elem_bytes, const void* src, void* dst, int slices, int K, int N, int ld,
+                                 hipStream_t st);
 
 // ConvTranspose as an output-stationary gather; see convt_kernel.
 struct ConvTArgs {

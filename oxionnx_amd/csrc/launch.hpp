@@ -296,10 +296,11 @@ template <Op O, bool XX, bool XY, class Tl, class LX, class LY, class Epi>
 inline hipError_t launch_tile(const LX& lx, const LY& ly, const Epi& epi, int P, int Q, int kc, hipStream_t st) {
   const int nP = (P + Tl::BP - 1) / Tl::BP, nQ = (Q + Tl::BQ - 1) / Tl::BQ;
   const int64_t nb = (int64_t)nP * nQ;
+  const int batch = epi.out.batch > 1 ? epi.out.batch : 1;   // slices on blockIdx.z
   if (nb <= 0) return hipSuccess;
-  if (nb > 0x7fffffff) return hipErrorInvalidValue;
-  hipLaunchKernelGGL((mfma_gemm_kernel<O, Tl, LX, LY, Epi, XX, XY>), dim3((unsigned)nb), dim3(Tl::kThreads),
-                     0, st, lx, ly, epi, nP, nQ, kc, 1);
+  if (nb > 0x7fffffff || batch > 65535) return hipErrorInvalidValue;
+  hipLaunchKernelGGL((mfma_gemm_kernel<O, Tl, LX, LY, Epi, XX, XY>), dim3((unsigned)nb, 1, (unsigned)batch),
+                     dim3(Tl::kThreads), 0, st, lx, ly, epi, nP, nQ, kc, 1);
   return hipGetLastError();
 }
 
@@ -349,6 +350,7 @@ inline int pick_tile(int P, int Q, int kc, int forced) {
 template <Op O, bool XX, bool XY, class LX, class LY, class Epi>
 inline hipError_t launch_any(const LX& lx, const LY& ly, const Epi& epi, int P, int Q, int kc, int tile,
                              int splits, void* split_ws, hipStream_t st) {
+  if (splits > 1 && epi.out.batch > 1) return hipErrorInvalidValue;   // one workspace: no split-K per slice
   if (splits > 1) {
     if (split_tile_size(P, Q, tile) == 128)
       return launch_split_on<O, XX, XY, T128w8>(lx, ly, epi, P, Q, kc, splits, split_ws, st);
@@ -383,6 +385,7 @@ inline OutAddr make_out_addr(const OutMap& o) {
   a.si = o.si; a.sj = o.sj; a.bstride = o.bstride; a.ohw = o.ohw > 0 ? o.ohw : 1;
   magic_div(a.ohw, &a.ohw_mul, &a.ohw_shift);
   a.P = o.P; a.Q = o.Q; a.vec = o.vec;
+  a.batch = o.batch > 1 ? o.batch : 1; a.zstride = o.zstride;
   return a;
 }
 
@@ -412,6 +415,7 @@ inline DenseRows make_dense(const DenseOperand& d) {
   DenseRows r;
   r.base = reinterpret_cast<const char*>(d.base);
   r.ld = d.ld_bytes; r.rows = d.rows; r.kc = d.kc; r.kwrap = d.kwrap;
+  r.zmod = d.zmod; r.zstride = d.zstride;
   return r;
 }
 

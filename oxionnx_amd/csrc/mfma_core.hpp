@@ -157,6 +157,8 @@ struct DenseRows {
   int kwrap;          // > 0: chunk g >= kwrap reads chunk g - kwrap (the operand is
                       // re-read against the second half of a split int8 weight);
                       // a multiple of 8, so a stage never straddles the wrap
+  int zmod;           // batched launch: slice blockIdx.z reads matrix z % zmod
+  int64_t zstride;    // bytes between those matrices
 
   template <int NR>
   struct State { __amdgpu_buffer_rsrc_t rs; int voff[NR]; int c; };
@@ -164,7 +166,8 @@ struct DenseRows {
   template <int NR, int NW, int CH>
   __device__ __forceinline__ void init(State<NR>& s, int row0, int lane, int wave) const {
     s.c = dma_chunk<CH>(lane, wave);
-    s.rs = __builtin_amdgcn_make_buffer_rsrc((void*)(base + (int64_t)row0 * ld), (short)0, 0x7fffffff, 0x00020000);
+    const char* b0 = zmod > 1 ? base + (int64_t)(blockIdx.z % zmod) * zstride : base;
+    s.rs = __builtin_amdgcn_make_buffer_rsrc((void*)(b0 + (int64_t)row0 * ld), (short)0, 0x7fffffff, 0x00020000);
 #pragma unroll
     for (int i = 0; i < NR; ++i) {
       const int r = (i * NW + wave) * (64 / CH) + lane / CH;
@@ -326,7 +329,9 @@ struct OutAddr {
   int ohw_shift;
   int P, Q;
   int vec;
-  int stage;   // the staged epilogue may be used
+  int stage;         // the staged epilogue may be used
+  int batch;         // > 1: batched launch, slice blockIdx.z
+  int64_t zstride;   // bytes between the slices' outputs
   __device__ __forceinline__ int64_t row(int i) const {
     if (bstride == 0) return (int64_t)i * si;
     const int n = (int)(((uint64_t)(uint32_t)i * ohw_mul) >> ohw_shift);
@@ -478,7 +483,8 @@ mfma_gemm_kernel(const LX lx, const LY ly, const Epi epi, int nP, int nQ, int kc
 
   const int ibase = p0 + wp * Tl::TP * 32 + (lane >> 5) * 4;
   const int jbase = q0 + wq * Tl::TQ * 32 + (lane & 31);
-  const OutAddr out = epi.addr();
+  OutAddr out = epi.addr();
+  if (out.batch > 1) out.y += (int64_t)blockIdx.z * out.zstride;
 
   // the per-column epilogue terms, loaded once for all of this lane's rows
   typename Epi::PreJ pj[Tl::TQ];

@@ -1252,6 +1252,53 @@ extern "C" int ohip_conv2d(ohip_ctx* ctx, const ohip_conv_desc* d, const void* x
   return OHIP_OK;
 }
 
+// ------------------------------------------------------------------ batched MatMul
+extern "C" int ohip_matmul(ohip_ctx* ctx, const ohip_matmul_desc* d, const void* a, const void* b, void* y) {
+  int rc = activate(ctx);
+  if (rc) return rc;
+  if (!d || !a || !b || !y) return fail(OHIP_E_INVALID, "ohip_matmul: null argument");
+  if (!is_float(d->dtype)) return fail(OHIP_E_INVALID, "ohip_matmul: dtype");
+  if (d->m < 0 || d->k <= 0 || d->n < 0 || d->batch < 1 || d->a_batches < 1 || d->b_batches < 1)
+    return fail(OHIP_E_SHAPE, "ohip_matmul: bad extents");
+  if (d->batch > 65535) return fail(OHIP_DECLINED, "ohip_matmul: more than 65535 slices");
+  if (d->m == 0 || d->n == 0) return OHIP_OK;
+  const int eb = elem_bytes(d->dtype), ce = 16 / eb;
+  const int64_t M = d->m, K = d->k, N = d->n, kp = round_up(K, ce);
+  if (M * d->a_batches > INT_MAX / 2 || N > INT_MAX / 2 || kp * eb > INT_MAX / 4)
+    return fail(OHIP_DECLINED, "ohip_matmul: extent too large");
+  std::lock_guard<std::mutex> lock(ctx->mu);
+  ctx->counters.dispatches++;
+  const bool a_direct = (K * eb) % 16 == 0 && aligned(a, 16);
+  ScratchPlan plan;
+  size_t ib = plan.add((size_t)(d->b_batches * N * kp) * eb);
+  size_t ia = a_direct ? SIZE_MAX : plan.add((size_t)(d->a_batches * M * kp) * eb);
+  rc = scratch_reserve(ctx, plan.total());
+  if (rc) return rc;
+  void* pb = scratch_at(ctx, plan, ib);
+  HIP_TRY(run_transpose_batched(eb, b, pb, (int)d->b_batches, (int)K, (int)N, (int)kp, ctx->stream),
+          "MatMul B -> K-contiguous rows");
+  const void* pa = a;
+  if (!a_direct) {
+    void* t = scratch_at(ctx, plan, ia);
+    HIP_TRY(run_gather2d(eb, a, K, 1, t, (int)(d->a_batches * M), (int)K, (int)kp, ctx->stream), "MatMul A pack");
+    pa = t;
+  }
+  const int64_t lda = a_direct ? K * eb : kp * eb;
+  DenseOperand xo{pb, kp * eb, (int)N, (int)(kp / ce), 0, 0u, pad16(ctx, 0), (int)d->b_batches, N * kp * eb};
+  DenseOperand yo{pa, lda, (int)M, (int)(kp / ce), 0, 0u, pad16(ctx, 0), (int)d->a_batches, M * lda};
+  FloatOut o{};
+  o.y = y; o.si = 1; o.sj = N; o.bstride = 0; o.ohw = INT_MAX; o.P = (int)N; o.Q = (int)M;
+  o.vec = N % 4 == 0 && aligned(y, 4 * eb);
+  o.alpha = 1.0f; o.beta = 1.0f; o.bias = nullptr; o.bias_mode = BIAS_NONE; o.act = ACT_NONE;
+  o.splits = 1; o.split_ws = nullptr; o.batch = (int)d->batch; o.zstride = M * N * eb;
+  DENSE_FITS_OR_DECLINE(xo, "ohip_matmul");
+  DENSE_FITS_OR_DECLINE(yo, "ohip_matmul");
+  hipError_t e = run_dense_float(d->dtype, xo, yo, o, ctx->tile_override >= 1 && ctx->tile_override <= 9
+                                                          ? ctx->tile_override : 0, ctx->stream);
+  if (e != hipSuccess) return hip_fail(e, "ohip_matmul launch");
+  return OHIP_OK;
+}
+
 // ------------------------------------------------------------------ ConvTranspose
 extern "C" int ohip_conv_transpose2d(ohip_ctx* ctx, const ohip_convt_desc* d, const void* x, const ohip_weight* w,
                                      const void* bias, void* y) {

@@ -236,6 +236,22 @@ class HipContext:
         L.check(L.lib().ohip_conv2d(self.h, ctypes.byref(d), _ptr(x), w.handle, _ptr(bias), _ptr(out)))
         return out
 
+    def matmul(self, a, b, out=None):
+        """Batched MatMul of two device tensors, [..., M, K] x [..., K, N], with the
+        reference's slice rule (slice s: A slice s % a_batches, B slice s % b_batches)."""
+        torch = _torch()
+        dt = ohip_dtype(a.dtype)
+        batch_shape = list(np.broadcast_shapes(tuple(a.shape[:-2]), tuple(b.shape[:-2])))
+        batch = int(np.prod(batch_shape)) if batch_shape else 1
+        na = int(np.prod(a.shape[:-2])) if a.dim() > 2 else 1
+        nb = int(np.prod(b.shape[:-2])) if b.dim() > 2 else 1
+        m, k, n = a.shape[-2], a.shape[-1], b.shape[-1]
+        if out is None:
+            out = torch.empty(batch_shape + [m, n], dtype=a.dtype, device=a.device)
+        d = L.MatMulDesc(m, k, n, batch, na, nb, dt)
+        L.check(L.lib().ohip_matmul(self.h, ctypes.byref(d), _ptr(a.contiguous()), _ptr(b.contiguous()), _ptr(out)))
+        return out
+
     def conv_transpose2d(self, x, w, bias=None, strides=(1, 1), pads=(0, 0, 0, 0), dilations=(1, 1),
                          output_padding=(0, 0), group=1, out=None):
         """ConvTranspose, NCHW; pads = [top, left, bottom, right] (already resolved)."""

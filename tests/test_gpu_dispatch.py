@@ -194,3 +194,19 @@ def test_conv_transpose_node_through_the_boundary(ctx, attrs):
     want = O.conv_transpose(x, w, b, **attrs)
     assert out[0].shape == want.shape
     assert np.max(np.abs(out[0].astype(np.float64) - want)) <= 1e-4 * max(1.0, float(np.abs(want).max()))
+
+
+def test_batched_matmul_node_through_the_boundary(ctx):
+    """MatMulOp with a batched B (matmul_gemm.rs:9-126): the batch prefixes
+    broadcast and slice s pairs A slice s % a_batches with B slice s % b_batches
+    (math_typed.rs:352-369)."""
+    from oxionnx_amd import ep
+    rng = np.random.default_rng(31)
+    for ash, bsh in [((2, 3, 40, 24), (3, 24, 36)), ((5, 17, 64), (5, 64, 9))]:
+        a = rng.uniform(-1, 1, ash).astype(np.float32)
+        b = rng.normal(0, 0.2, bsh).astype(np.float32)
+        out = ep.try_hip_dispatch(ep.Node("MatMul", ["a", "b"]), {"b": b}, {"a": a}, ctx)
+        assert out is not None, ctx.last_decline()
+        want = O.matmul_batched(a, b)
+        assert out[0].shape == want.shape
+        assert np.max(np.abs(out[0] - want)) <= 1e-4 * max(1.0, float(np.abs(want).max()))

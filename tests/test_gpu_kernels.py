@@ -204,6 +204,42 @@ def test_grouped_conv_matches_oracle(torch, ctx, case, dt):
         assert _rel_err(got, want) <= HALF_TOL
 
 
+# Batched MatMul with both operands on the device: (A shape, B shape).  The
+# slice rule is the reference's (s % a_batches, s % b_batches), which is not
+# numpy's broadcast for every shape (the [4,1,..] x [3,..] case below).
+BMM_CASES = [
+    ((3, 37, 52), (3, 52, 29)),
+    ((2, 3, 64, 64), (3, 64, 48)),
+    ((4, 1, 5, 7), (3, 7, 4)),
+    ((8, 128, 96), (96, 160)),
+    ((1, 33, 21), (6, 21, 70)),
+]
+
+
+@pytest.mark.parametrize("case", BMM_CASES, ids=lambda c: f"{c[0]}x{c[1]}")
+@pytest.mark.parametrize("dt", ["f32", "f16", "bf16"])
+def test_batched_matmul_matches_oracle(torch, ctx, case, dt):
+    ash, bsh = case
+    rng = np.random.default_rng(sum(ash) + sum(bsh))
+    a = rng.uniform(-1, 1, ash).astype(np.float32)
+    b = rng.normal(0, 1 / np.sqrt(bsh[-2]), bsh).astype(np.float32)
+    if dt == "f32":
+        y = ctx.matmul(_dev(torch, a), _dev(torch, b)).cpu().numpy()
+        want = O.matmul_batched(a, b)
+        assert y.shape == want.shape
+        assert _rel_err(y, want) <= F32_TOL
+    else:
+        bf = dt == "bf16"
+        tdt = torch.bfloat16 if bf else torch.float16
+        ah, bh = O.f32_to_half_bits(a, bf), O.f32_to_half_bits(b, bf)
+        at = torch.from_numpy(ah.view(np.int16)).cuda().view(tdt)
+        bt = torch.from_numpy(bh.view(np.int16)).cuda().view(tdt)
+        got = O.half_bits_to_f32(ctx.matmul(at, bt).view(torch.int16).cpu().numpy().view(np.uint16), bf)
+        want = O.half_bits_to_f32(O.matmul_batched_half(ah, bh, bf), bf)
+        assert got.shape == want.shape
+        assert _rel_err(got, want) <= HALF_TOL
+
+
 # ConvTranspose: (x shape, w shape [Cin, Cout/g, kh, kw], attrs with resolved pads).
 # Group 1 / dilation 1 / kernel >= stride runs the sub-pixel phases on the
 # MFMA engine (within the tolerances); the rest runs the gather kernel, which

@@ -357,3 +357,25 @@ def test_conv_transpose_is_the_adjoint_of_conv():
     lhs = float(np.dot(y.astype(np.float64).ravel(), x.astype(np.float64).ravel()))
     rhs = float(np.dot(z.astype(np.float64).ravel(), zt.astype(np.float64).ravel()))
     assert abs(lhs - rhs) <= 1e-4 * max(1.0, abs(lhs))
+
+
+def test_batched_matmul_slice_rule():
+    """typed_matmul_batch_info + the s % batches slice pairing (math_typed.rs:85-115,
+    352-369): where the batch prefixes are whole, it agrees with numpy's
+    broadcast matmul; where one prefix is partial it follows the modulo rule."""
+    rng = np.random.default_rng(3)
+    a = rng.normal(size=(2, 3, 4, 5)).astype(np.float32)
+    b = rng.normal(size=(3, 5, 6)).astype(np.float32)
+    np.testing.assert_allclose(O.matmul_batched(a, b), np.matmul(a.astype(np.float64), b), atol=1e-12)
+    a = rng.normal(size=(4, 1, 2, 3)).astype(np.float32)
+    b = rng.normal(size=(3, 3, 2)).astype(np.float32)
+    got = O.matmul_batched(a, b)
+    assert got.shape == (4, 3, 2, 2)
+    a3, b3 = a.reshape(4, 2, 3).astype(np.float64), b.astype(np.float64)
+    for s in range(12):
+        np.testing.assert_allclose(got.reshape(12, 2, 2)[s], a3[s % 4] @ b3[s % 3], atol=1e-12)
+    # the half path: per slice the f16 Gemm loop, rounded once
+    ah, bh = O.f32_to_half_bits(a), O.f32_to_half_bits(b)
+    hb = O.matmul_batched_half(ah, bh)
+    assert hb.shape == (4, 3, 2, 2)
+    np.testing.assert_array_equal(hb.reshape(12, 2, 2)[5], O.gemm_half(ah.reshape(4, 2, 3)[1], bh[2], None))
