@@ -34,6 +34,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <utility>
+
 namespace ohip {
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
@@ -92,6 +94,16 @@ template <> struct OpT<Op::F32> {
 // slab each; a slab holds CH 16-byte chunks per row (CH = 8: 128-byte slabs,
 // four MFMA k-steps; CH = 4: 64-byte slabs, two k-steps, so the same LDS
 // holds twice the stages and the loads run further ahead of their use).
+// static_for<N>(f): f(std::integral_constant<int, 0>{}) .. f(..N - 1), expanded
+// at compile time.
+template <class F, int... I>
+__device__ __forceinline__ void static_for_impl(F& f, std::integer_sequence<int, I...>) {
+  (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, class F> __device__ __forceinline__ void static_for(F&& f) {
+  static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
+
 template <int BP_, int BQ_, int WP_, int WQ_, int STAGES_, int CH_ = 8> struct Tile {
   static constexpr int BP = BP_, BQ = BQ_, WP = WP_, WQ = WQ_, STAGES = STAGES_, CH = CH_;
   static constexpr int KS = CH / 2;                               // MFMA k-steps per slab
@@ -515,41 +527,40 @@ mfma_gemm_kernel(const LX lx, const LY ly, const Epi epi, int nP, int nQ, int kc
   // column turned into bit patterns and staged or stored.  Working a group at
   // a time keeps the epilogue's live registers to a few per column, so the
   // epilogue does not set the kernel's register count (and occupancy).
+  // (Compile-time loops: every accumulator index is a constant, so the
+  // accumulators stay in registers however large the unrolled body is.)
+  static_for<Tl::TP * 4>([&](auto ag) __attribute__((always_inline)) {
+    constexpr int a = decltype(ag)::value / 4, g = decltype(ag)::value % 4;
+    const int ig = ibase + a * 32 + 8 * g;
+    typename Epi::PreI pi;
+    epi.load_i(pi, ig);
+    int64_t row = 0;
+    if (!staged) row = out.row(ig);
+    static_for<Tl::TQ>([&](auto bc) __attribute__((always_inline)) {
+      constexpr int b = decltype(bc)::value;
+      const int j = jbase + b * 32;
+      A4 v;
 #pragma unroll
-  for (int a = 0; a < Tl::TP; ++a) {
-#pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      const int ig = ibase + a * 32 + 8 * g;
-      typename Epi::PreI pi;
-      epi.load_i(pi, ig);
-      int64_t row = 0;
-      if (!staged) row = out.row(ig);
-#pragma unroll
-      for (int b = 0; b < Tl::TQ; ++b) {
-        const int j = jbase + b * 32;
-        A4 v;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) v[e] = acc[a][b][4 * g + e];
-        uint32_t bits[4];
-        epi.finish(pi, pj[b], ig, j, v, bits);
-        if constexpr (Epi::kStageBytes > 0) {
-          if (staged) {
-            const int lj = j - q0;
-            const int byte = (ig - p0) * EB;
-            char* dst = stg + lj * (Tl::BP * EB) + (((byte >> 4) ^ (lj & (CPR - 1))) << 4) + (byte & 15);
-            if constexpr (EB == 2) {
-              typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-              *reinterpret_cast<u32x2*>(dst) = u32x2{bits[0] | (bits[1] << 16), bits[2] | (bits[3] << 16)};
-            } else {
-              *reinterpret_cast<uint32_t*>(dst) = bits[0] | (bits[1] << 8) | (bits[2] << 16) | (bits[3] << 24);
-            }
-            continue;
+      for (int e = 0; e < 4; ++e) v[e] = acc[a][b][4 * g + e];
+      uint32_t bits[4];
+      epi.finish(pi, pj[b], ig, j, v, bits);
+      if constexpr (Epi::kStageBytes > 0) {
+        if (staged) {
+          const int lj = j - q0;
+          const int byte = (ig - p0) * EB;
+          char* dst = stg + lj * (Tl::BP * EB) + (((byte >> 4) ^ (lj & (CPR - 1))) << 4) + (byte & 15);
+          if constexpr (EB == 2) {
+            typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+            *reinterpret_cast<u32x2*>(dst) = u32x2{bits[0] | (bits[1] << 16), bits[2] | (bits[3] << 16)};
+          } else {
+            *reinterpret_cast<uint32_t*>(dst) = bits[0] | (bits[1] << 8) | (bits[2] << 16) | (bits[3] << 24);
           }
+          return;
         }
-        store_group(out, epi.out_bytes(), row, ig, j, bits);
       }
-    }
-  }
+      store_group(out, epi.out_bytes(), row, ig, j, bits);
+    });
+  });
 
   if constexpr (Epi::kStageBytes > 0) {
     if (staged) {
