@@ -186,20 +186,27 @@ struct DenseRows {
       s.voff[i] = row0 + r < rows ? (int)(r * ld) + s.c * 16 : kOobOffset;
     }
   }
+  // Loads of stage kt: step() computes what the stage's loads share, load(i)
+  // issues this thread's i-th 16-byte load (the kernel spreads them under its
+  // MFMAs), issue() does all of them.
+  struct Step { int soff; bool kin; };
   template <int NR, int NW, int CH>
-  __device__ __forceinline__ void issue(const State<NR>& s, int kt, int wave, u32x4* lds_rows) const {
+  __device__ __forceinline__ Step step(const State<NR>& s, int kt) const {
     int g0 = kt * CH;                      // first chunk of the stage (uniform)
     if (kwrap > 0 && g0 >= kwrap) g0 -= kwrap;
-    const int soff = g0 * 16;
-    if (g0 + CH <= kc) {
+    // K tail or past the end: chunks at or beyond kc read as zero (a select
+    // per load, not a branch, so the K loop stays one basic block)
+    return Step{g0 * 16, g0 + s.c < kc};
+  }
+  template <int NR, int NW, int CH>
+  __device__ __forceinline__ void load(const State<NR>& s, const Step& st, int i, int wave, u32x4* lds_rows) const {
+    buf16(s.rs, st.kin ? s.voff[i] : kOobOffset, st.soff, lds_rows + (i * NW + wave) * 64);
+  }
+  template <int NR, int NW, int CH>
+  __device__ __forceinline__ void issue(const State<NR>& s, int kt, int wave, u32x4* lds_rows) const {
+    const Step st = step<NR, NW, CH>(s, kt);
 #pragma unroll
-      for (int i = 0; i < NR; ++i) buf16(s.rs, s.voff[i], soff, lds_rows + (i * NW + wave) * 64);
-    } else {
-      // K tail or past the end: chunks at or beyond kc read as zero
-      const bool kin = g0 + s.c < kc;
-#pragma unroll
-      for (int i = 0; i < NR; ++i) buf16(s.rs, kin ? s.voff[i] : kOobOffset, soff, lds_rows + (i * NW + wave) * 64);
-    }
+    for (int i = 0; i < NR; ++i) load<NR, NW, CH>(s, st, i, wave, lds_rows);
   }
 };
 
@@ -239,8 +246,9 @@ struct Im2colNHWC {
       s.ix0[i] = ox * sw - pl;
     }
   }
+  struct Step { int dy, dx, cc; bool kin; };
   template <int NR, int NW, int CH>
-  __device__ __forceinline__ void issue(const State<NR>& s, int kt, int wave, u32x4* lds_rows) const {
+  __device__ __forceinline__ Step step(const State<NR>& s, int kt) const {
     int gk = kt * CH + s.c;
     if (kwrap > 0 && gk >= kwrap) gk -= kwrap;
     const bool kin = gk < kc;
@@ -249,14 +257,20 @@ struct Im2colNHWC {
     const int cc = g - tap * cpc;
     const int ky = tap / KW;
     const int kx = tap - ky * KW;
-    const int dy = ky * dh, dx = kx * dw;
+    return Step{ky * dh, kx * dw, cc, kin};
+  }
+  template <int NR, int NW, int CH>
+  __device__ __forceinline__ void load(const State<NR>& s, const Step& st, int i, int wave, u32x4* lds_rows) const {
+    const int iy = s.iy0[i] + st.dy, ix = s.ix0[i] + st.dx;
+    const bool inside =
+        st.kin && ((s.okmask >> i) & 1u) && (unsigned)iy < (unsigned)H && (unsigned)ix < (unsigned)W;
+    dma16(inside ? s.img[i] + ((int64_t)(iy * W + ix) * pstride + st.cc) * 16 : pad, lds_rows + (i * NW + wave) * 64);
+  }
+  template <int NR, int NW, int CH>
+  __device__ __forceinline__ void issue(const State<NR>& s, int kt, int wave, u32x4* lds_rows) const {
+    const Step st = step<NR, NW, CH>(s, kt);
 #pragma unroll
-    for (int i = 0; i < NR; ++i) {
-      const int iy = s.iy0[i] + dy, ix = s.ix0[i] + dx;
-      const bool inside =
-          kin && ((s.okmask >> i) & 1u) && (unsigned)iy < (unsigned)H && (unsigned)ix < (unsigned)W;
-      dma16(inside ? s.img[i] + ((int64_t)(iy * W + ix) * pstride + cc) * 16 : pad, lds_rows + (i * NW + wave) * 64);
-    }
+    for (int i = 0; i < NR; ++i) load<NR, NW, CH>(s, st, i, wave, lds_rows);
   }
 };
 
@@ -457,40 +471,63 @@ mfma_gemm_kernel(const LX lx, const LY ly, const Epi epi, int nP, int nQ, int kc
     for (int b = 0; b < Tl::TQ; ++b) fy[0][b] = s0[yslot[0] + b * 32 * Tl::kRowStride];
   }
 
+  // One k-step in program order, fenced so the compiler keeps it: each MFMA
+  // is followed by at most one fragment read for the next k-step (in the
+  // order the next k-step consumes them, so the waits before its MFMAs are
+  // partial) and, on k-step 0, by one DMA load of the stage STAGES - 1 ahead.
+  // The last k-step reads the next stage: its first MFMAs go before the
+  // stage barrier, which then overlaps them.
+  constexpr int NM = Tl::TP * Tl::TQ;      // MFMAs per k-step
+  constexpr int NRD = Tl::TP + Tl::TQ;     // fragment reads per k-step
+  constexpr int PRE = NM >= 4 ? 2 : 0;     // MFMAs of the last k-step ahead of the barrier
   for (int kt = kbeg; kt < kend; ++kt) {
     const u32x4* s = smem + (kt % Tl::STAGES) * Tl::kStage;
     const u32x4* sn = smem + ((kt + 1) % Tl::STAGES) * Tl::kStage;
-#pragma unroll
-    for (int ks = 0; ks < Tl::KS; ++ks) {
-      const int cur = ks & 1;
-      if (ks < Tl::KS - 1) {
-#pragma unroll
-        for (int a = 0; a < Tl::TP; ++a) fx[cur ^ 1][a] = s[xslot[ks + 1] + a * 32 * Tl::kRowStride];
-#pragma unroll
-        for (int b = 0; b < Tl::TQ; ++b) fy[cur ^ 1][b] = s[yslot[ks + 1] + b * 32 * Tl::kRowStride];
-      } else {
-        wait_vmcnt<(Tl::STAGES - 2) * NL>();
-        wait_lgkm0();
-        barrier_only();
-#pragma unroll
-        for (int a = 0; a < Tl::TP; ++a) fx[cur ^ 1][a] = sn[xslot[0] + a * 32 * Tl::kRowStride];
-#pragma unroll
-        for (int b = 0; b < Tl::TQ; ++b) fy[cur ^ 1][b] = sn[yslot[0] + b * 32 * Tl::kRowStride];
-      }
-      if (ks == 0) issue(kt + Tl::STAGES - 1);
-#pragma unroll
-      for (int a = 0; a < Tl::TP; ++a)
-#pragma unroll
-        for (int b = 0; b < Tl::TQ; ++b) {
-          acc[a][b] = OpT<O>::mma(frag<XX>(fx[cur][a]), frag<XY>(fy[cur][b]), acc[a][b]);
-          // one MFMA, then one LDS read (and on k-step 0 one DMA load):
-          // keeps the fragment reads and the loads spread under the MFMAs
-          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-          if (ks == 0 && a * Tl::TQ + b < NL) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+    u32x4* sd = smem + ((kt + Tl::STAGES - 1) % Tl::STAGES) * Tl::kStage;
+    const typename LX::Step stx = lx.template step<Tl::NX, Tl::kWaves, Tl::CH>(sx, kt + Tl::STAGES - 1);
+    const typename LY::Step sty = ly.template step<Tl::NY, Tl::kWaves, Tl::CH>(sy, kt + Tl::STAGES - 1);
+    auto dma = [&](int i) __attribute__((always_inline)) {
+      if (i < Tl::NX) lx.template load<Tl::NX, Tl::kWaves, Tl::CH>(sx, stx, i, wave, sd);
+      else ly.template load<Tl::NY, Tl::kWaves, Tl::CH>(sy, sty, i - Tl::NX, wave, sd + Tl::BP * Tl::kRowStride);
+    };
+    static_for<Tl::KS>([&](auto ksc) __attribute__((always_inline)) {
+      constexpr int ks = decltype(ksc)::value;
+      constexpr bool last = ks == Tl::KS - 1;
+      constexpr int cur = ks & 1, nxt = cur ^ 1;
+      const u32x4* src = last ? sn : s;
+      const int kr = last ? 0 : ks + 1;
+      // read r of the next k-step: fx[0], fy[0 .. TQ-1], fx[1 .. TP-1]
+      auto read = [&](auto rc) __attribute__((always_inline)) {
+        constexpr int r = decltype(rc)::value;
+        if constexpr (r == 0) fx[nxt][0] = src[xslot[kr]];
+        else if constexpr (r <= Tl::TQ) fy[nxt][r - 1] = src[yslot[kr] + (r - 1) * 32 * Tl::kRowStride];
+        else fx[nxt][r - Tl::TQ] = src[xslot[kr] + (r - Tl::TQ) * 32 * Tl::kRowStride];
+      };
+      static_for<NM>([&](auto mc) __attribute__((always_inline)) {
+        constexpr int m = decltype(mc)::value;
+        constexpr int a = m / Tl::TQ, b = m % Tl::TQ;
+        if constexpr (last && m == PRE) {
+          wait_vmcnt<(Tl::STAGES - 2) * NL>();
+          wait_lgkm0();
+          barrier_only();
         }
-
-    }
+        acc[a][b] = OpT<O>::mma(frag<XX>(fx[cur][a]), frag<XY>(fy[cur][b]), acc[a][b]);
+        __builtin_amdgcn_sched_barrier(0);
+        constexpr int r = last ? m - PRE : m;
+        if constexpr (r >= 0 && r < NRD) read(std::integral_constant<int, r>{});
+        if constexpr (ks == 0 && m < NL) dma(m);
+        __builtin_amdgcn_sched_barrier(0);
+      });
+      // the reads and loads that outnumber the MFMAs (small tiles)
+      static_for<(NRD > NM - (last ? PRE : 0) ? NRD - (NM - (last ? PRE : 0)) : 0)>([&](auto rc) __attribute__((always_inline)) {
+        constexpr int r = NM - (last ? PRE : 0) + decltype(rc)::value;
+        read(std::integral_constant<int, r>{});
+      });
+      if constexpr (ks == 0) {
+        static_for<(NL > NM ? NL - NM : 0)>([&](auto ic) __attribute__((always_inline)) { dma(NM + decltype(ic)::value); });
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    });
   }
 
   const int ibase = p0 + wp * Tl::TP * 32 + (lane >> 5) * 4;
