@@ -229,6 +229,115 @@ __global__ void nchw_to_nhwc_kernel(const T* __restrict__ src, T* __restrict__ d
   }
 }
 
+__device__ __forceinline__ int pad_map(int o, int begin, int len, int mode) {
+  int s = o - begin;
+  if (s >= 0 && s < len) return s;
+  if (mode == 2 || len == 1) return s < 0 ? 0 : len - 1;
+  const int period = 2 * (len - 1);
+  s %= period;
+  if (s < 0) s += period;
+  return s < len ? s : period - s;
+}
+
+// Row-tiled staging, the fast form of both transposes above: a block takes
+// one span of source pixels (a run of the flattened H x W axis, or one whole
+// source row when a reflect / edge border is added) for up to 64 channels,
+// reads it with 16-byte loads along the pixels, transposes it through LDS and
+// writes whole 16-byte channel vectors of every output pixel it covers.
+// Output pixel x of the span takes LDS column map(x): x itself, or
+// pad_map(x) for a bordered row.  Channels from C up to cp are written as
+// zero.  Needs the span and the row to be whole 16-byte chunks.
+struct RowStage {
+  int C, H, W, HW, cp, tc;    // tc: channels per block (a multiple of 16 / sizeof(T), <= 64)
+  int span;                   // pixels per block (unbordered form)
+  int Hp, Wp, pt, pl, mode;   // bordered form
+};
+
+template <class T, bool BORDER>
+__global__ void __launch_bounds__(256) stage_rows_kernel(const T* __restrict__ src, T* __restrict__ dst, RowStage g) {
+  constexpr int V = 16 / (int)sizeof(T);
+  extern __shared__ u32x4 stage_lds[];
+  T* tile = reinterpret_cast<T*>(stage_lds);
+  const int RS = g.tc + V;   // LDS row stride in elements (keeps rows 16-byte aligned)
+  const int n = blockIdx.z, c0 = blockIdx.y * g.tc;
+  int64_t sbase, obase;
+  int L, O;
+  if (BORDER) {
+    const int y = blockIdx.x;
+    sbase = (int64_t)pad_map(y, g.pt, g.H, g.mode) * g.W;
+    L = g.W;
+    O = g.Wp;
+    obase = (int64_t)y * g.Wp;
+  } else {
+    const int64_t p0 = (int64_t)blockIdx.x * g.span;
+    L = O = (int)min((int64_t)g.span, (int64_t)g.HW - p0);
+    sbase = obase = p0;
+  }
+  const T* s = src + (int64_t)n * g.C * g.HW + sbase;
+  const int lc = L / V;
+  for (int v = threadIdx.x; v < g.tc * lc; v += 256) {
+    const int c = v / lc, q = v - c * lc;
+    u32x4 w = {0u, 0u, 0u, 0u};
+    if (c0 + c < g.C) w = *reinterpret_cast<const u32x4*>(s + (int64_t)(c0 + c) * g.HW + q * V);
+    T e[V];
+    __builtin_memcpy(e, &w, 16);
+#pragma unroll
+    for (int k = 0; k < V; ++k) tile[(q * V + k) * RS + c] = e[k];
+  }
+  __syncthreads();
+  const int oc = g.tc / V;
+  const int64_t HWo = BORDER ? (int64_t)g.Hp * g.Wp : (int64_t)g.HW;
+  T* d = dst + ((int64_t)n * HWo + obase) * g.cp + c0;
+  for (int v = threadIdx.x; v < O * oc; v += 256) {
+    const int x = v / oc, q = v - x * oc;
+    if (c0 + q * V >= g.cp) continue;
+    const int m = BORDER ? pad_map(x, g.pl, g.W, g.mode) : x;
+    *reinterpret_cast<u32x4*>(d + (int64_t)x * g.cp + q * V) = *reinterpret_cast<const u32x4*>(tile + m * RS + q * V);
+  }
+}
+
+// Launches the row-tiled form when its conditions hold; hipErrorNotSupported
+// otherwise (the caller then uses the element-tiled kernels).
+template <class T>
+static hipError_t stage_rows_t(const void* src, void* dst, int N, int C, int H, int W, int cp, int pt, int pl, int pb,
+                               int pr, int mode, hipStream_t st) {
+  constexpr int V = 16 / (int)sizeof(T);
+  const bool border = pt | pl | pb | pr;
+  const int HW = H * W;
+  if (cp % V != 0 || (uintptr_t)src % 16 != 0 || (uintptr_t)dst % 16 != 0) return hipErrorNotSupported;
+  if (border ? W % V != 0 : HW % V != 0) return hipErrorNotSupported;
+  RowStage g{};
+  g.C = C; g.H = H; g.W = W; g.HW = HW; g.cp = cp;
+  g.tc = cp < 64 ? cp : 64;
+  g.Hp = H + pt + pb; g.Wp = W + pl + pr; g.pt = pt; g.pl = pl; g.mode = mode;
+  const int ctiles = (cp + g.tc - 1) / g.tc;
+  const size_t px_bytes = (size_t)(g.tc + V) * sizeof(T);
+  dim3 grid;
+  size_t lds;
+  if (border) {
+    lds = (size_t)W * px_bytes;
+    if (lds > 48 * 1024) return hipErrorNotSupported;
+    grid = dim3((unsigned)g.Hp, (unsigned)ctiles, (unsigned)N);
+  } else {
+    // about 1024 blocks, each span a whole number of chunks within 32 KB of LDS
+    const int64_t lds_px = (int64_t)(32 * 1024 / px_bytes) / V * V;
+    int64_t span = ((int64_t)HW * ctiles * N + 1023) / 1024;
+    span = (span + V - 1) / V * V;
+    span = std::max<int64_t>(span, 4 * V);
+    span = std::min<int64_t>(span, std::min<int64_t>(lds_px, HW));
+    g.span = (int)span;
+    lds = (size_t)span * px_bytes;
+    grid = dim3((unsigned)((HW + span - 1) / span), (unsigned)ctiles, (unsigned)N);
+  }
+  if (border)
+    hipLaunchKernelGGL((stage_rows_kernel<T, true>), grid, dim3(256), lds, st, reinterpret_cast<const T*>(src),
+                       reinterpret_cast<T*>(dst), g);
+  else
+    hipLaunchKernelGGL((stage_rows_kernel<T, false>), grid, dim3(256), lds, st, reinterpret_cast<const T*>(src),
+                       reinterpret_cast<T*>(dst), g);
+  return hipGetLastError();
+}
+
 template <class T>
 static hipError_t nchw_to_nhwc_t(const void* src, void* dst, int N, int C, int HW, int cp, hipStream_t st) {
   dim3 grid((HW + 31) / 32, (cp + 31) / 32, N), block(32, 8);
@@ -239,6 +348,13 @@ static hipError_t nchw_to_nhwc_t(const void* src, void* dst, int N, int C, int H
 
 hipError_t run_nchw_to_nhwc(int elem_bytes, const void* src, void* dst, int N, int C, int HW, int cp,
                             hipStream_t st) {
+  hipError_t e = hipErrorNotSupported;
+  switch (elem_bytes) {
+    case 1: e = stage_rows_t<uint8_t>(src, dst, N, C, 1, HW, cp, 0, 0, 0, 0, 0, st); break;
+    case 2: e = stage_rows_t<uint16_t>(src, dst, N, C, 1, HW, cp, 0, 0, 0, 0, 0, st); break;
+    case 4: e = stage_rows_t<uint32_t>(src, dst, N, C, 1, HW, cp, 0, 0, 0, 0, 0, st); break;
+  }
+  if (e != hipErrorNotSupported) return e;
   switch (elem_bytes) {
     case 1: return nchw_to_nhwc_t<uint8_t>(src, dst, N, C, HW, cp, st);
     case 2: return nchw_to_nhwc_t<uint16_t>(src, dst, N, C, HW, cp, st);
@@ -251,15 +367,6 @@ hipError_t run_nchw_to_nhwc(int elem_bytes, const void* src, void* dst, int N, i
 // reflection (mode 1) or edge replication (mode 2): the Pad node in front of
 // a convolution, fused into its staging transpose.  Padded pixel (y, x)
 // reads source pixel (src_y, src_x) of the ONNX Pad mapping.
-__device__ __forceinline__ int pad_map(int o, int begin, int len, int mode) {
-  int s = o - begin;
-  if (s >= 0 && s < len) return s;
-  if (mode == 2 || len == 1) return s < 0 ? 0 : len - 1;
-  const int period = 2 * (len - 1);
-  s %= period;
-  if (s < 0) s += period;
-  return s < len ? s : period - s;
-}
 
 template <class T>
 __global__ void nchw_to_nhwc_pad_kernel(const T* __restrict__ src, T* __restrict__ dst, int C, int H, int W, int cp,
@@ -298,6 +405,13 @@ static hipError_t nchw_to_nhwc_pad_t(const void* src, void* dst, int N, int C, i
 
 hipError_t run_nchw_to_nhwc_pad(int elem_bytes, const void* src, void* dst, int N, int C, int H, int W, int cp,
                                 int pt, int pl, int pb, int pr, int mode, hipStream_t st) {
+  hipError_t e = hipErrorNotSupported;
+  switch (elem_bytes) {
+    case 1: e = stage_rows_t<uint8_t>(src, dst, N, C, H, W, cp, pt, pl, pb, pr, mode, st); break;
+    case 2: e = stage_rows_t<uint16_t>(src, dst, N, C, H, W, cp, pt, pl, pb, pr, mode, st); break;
+    case 4: e = stage_rows_t<uint32_t>(src, dst, N, C, H, W, cp, pt, pl, pb, pr, mode, st); break;
+  }
+  if (e != hipErrorNotSupported) return e;
   switch (elem_bytes) {
     case 1: return nchw_to_nhwc_pad_t<uint8_t>(src, dst, N, C, H, W, cp, pt, pl, pb, pr, mode, st);
     case 2: return nchw_to_nhwc_pad_t<uint16_t>(src, dst, N, C, H, W, cp, pt, pl, pb, pr, mode, st);

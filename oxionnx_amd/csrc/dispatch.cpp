@@ -18,6 +18,8 @@
 #include "internal.hpp"
 
 int ohip_dtensor_alias_internal(const ohip_dtensor* src, int rank, const int64_t* shape, ohip_dtensor** out);
+int ohip_dtensor_view_internal(const ohip_dtensor* src, int rank, const int64_t* shape, size_t byte_offset,
+                               ohip_dtensor** out);
 int ohip_const_operand_internal(ohip_ctx* ctx, const char* name, const char* label, int dtype, const void* host,
                                 size_t bytes, const void** dev);
 int ohip_hip_error_internal(hipError_t e, const char* what);
@@ -1218,17 +1220,48 @@ int do_concat(ohip_ctx* ctx, const ohip_node* nd, int placement, ohip_output* ou
   void* yd = st.alloc(bytes);
   if (!yd) return OHIP_E_NOMEM;
   hipStream_t s = (hipStream_t)ohip_ctx_stream(ctx);
+  // the inputs in groups of up to kConcatMax, one launch per group
   size_t off = 0;
+  ohip::ConcatPlan p{};
+  size_t group_off = 0;
+  auto flush = [&]() -> int {
+    if (p.n == 0) return OHIP_OK;
+    p.dst = static_cast<char*>(yd) + group_off;
+    const int64_t gw = (int64_t)(off - group_off);
+    // rows of the group's part: pitch `row` in the output; a one-group concat
+    // writes whole output rows
+    if (gw == (int64_t)row) {
+      if (ohip::run_concat_rows(p, gw, outer, s) != hipSuccess)
+        return ohip_hip_error_internal(hipGetLastError(), "Concat copy");
+    } else {
+      for (int k = 0; k < p.n; ++k)
+        if (p.w[k] && outer &&
+            ohip::run_copy2d(p.src[k], p.w[k], static_cast<char*>(p.dst) + p.off[k], (int64_t)row, p.w[k], outer, s) !=
+                hipSuccess)
+          return ohip_hip_error_internal(hipGetLastError(), "Concat copy");
+    }
+    p.n = 0;
+    group_off = off;
+    return OHIP_OK;
+  };
   for (int i = 0; i < nd->n_inputs; ++i) {
     const ohip_tensor* t = input(nd, i);
     const void* td = st.operand(t);
     if (!td) return OHIP_E_NOMEM;
     const size_t w = (size_t)(t->shape[axis] * inner * eb);
-    if (w && outer)
-      if (ohip::run_copy2d(td, (int64_t)w, static_cast<char*>(yd) + off, (int64_t)row, (int64_t)w, outer, s) !=
-          hipSuccess)
-        return ohip_hip_error_internal(hipGetLastError(), "Concat copy");
+    if (p.n == ohip::kConcatMax) {
+      int rc = flush();
+      if (rc) return rc;
+    }
+    p.src[p.n] = td;
+    p.w[p.n] = (int64_t)w;
+    p.off[p.n] = (int64_t)(off - group_off);
+    ++p.n;
     off += w;
+  }
+  {
+    int rc = flush();
+    if (rc) return rc;
   }
   return output_device(ctx, st, placement, out, dt, oshape, yd, bytes);
 }
@@ -1281,6 +1314,32 @@ int do_slice(ohip_ctx* ctx, const ohip_node* nd, int placement, ohip_output* out
   for (auto v : oshape) n *= v;
   const int dt = x->device ? x->dtype : OHIP_F32;
   const int eb = ebytes(dt);
+  // A resident input whose slice is one contiguous run (every axis before the
+  // first sliced one has extent 1 in the output, the axes after it are whole,
+  // unit step) becomes a view of the input's buffer: no copy, no launch.  The
+  // view starts on a 16-byte boundary, as every freshly allocated tensor does.
+  if (x->device && placement == OHIP_PLACE_DEVICE && ohip_dtensor_layout(x->device) == OHIP_NCHW && n > 0) {
+    int k = 0;
+    while (k < x->rank && p.out[k] == x->shape[k]) ++k;   // first sliced axis
+    bool contiguous = true;
+    int64_t off = 0;
+    for (int d = 0; d < x->rank; ++d) {
+      if (d < k) { if (p.out[d] != 1 && x->shape[d] != 1) contiguous = false; }
+      else if (d == k) { if (p.step[d] != 1 && p.out[d] > 1) contiguous = false; }
+      else if (p.out[d] != x->shape[d]) contiguous = false;
+      off += p.start[d] * p.in_stride[d];
+    }
+    // axes before k are whole; a whole axis of extent > 1 before k breaks it
+    for (int d = 0; d < k; ++d) if (x->shape[d] != 1) contiguous = false;
+    if (contiguous && (off * eb) % 16 == 0) {
+      ohip_dtensor* t = nullptr;
+      int rc = ohip_dtensor_view_internal(x->device, x->rank, oshape.data(), (size_t)(off * eb), &t);
+      if (rc) return rc;
+      set_out(out, dt, oshape);
+      out->device = t;
+      return OHIP_OK;
+    }
+  }
   Stage st(ctx);
   const void* xd = st.operand(x);
   const size_t bytes = (size_t)n * eb;

@@ -240,6 +240,15 @@ hipError_t run_quantize(const float* x, uint8_t* y, int64_t n, float scale, floa
 hipError_t run_dequantize(const uint8_t* x, bool is_signed, float* y, int64_t n, float scale, float zp,
                           hipStream_t st);
 hipError_t run_byte_table(const uint8_t* x, uint8_t* y, int64_t n, const uint8_t* table, hipStream_t st);
+constexpr int kConcatMax = 8;
+struct ConcatPlan {
+  const void* src[kConcatMax];
+  int64_t w[kConcatMax];     // row width of each input
+  int64_t off[kConcatMax];   // where that input's part of an output row starts
+  int n;
+  void* dst;
+};
+hipError_t run_concat_rows(ConcatPlan p, int64_t row, int64_t rows, hipStream_t st);
 hipError_t run_copy2d(const void* src, int64_t src_pitch, void* dst, int64_t dst_pitch, int64_t width, int64_t rows,
                       hipStream_t st);
 

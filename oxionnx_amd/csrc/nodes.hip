@@ -293,6 +293,21 @@ __global__ void __launch_bounds__(kThreads) copy2d_kernel(const T* __restrict__ 
   }
 }
 
+// Concat of up to kConcatMax inputs in one launch: output row r is the
+// inputs' rows r laid end to end; unit c of a row belongs to the input whose
+// [off, off + w) range holds it.
+template <class T>
+__global__ void __launch_bounds__(kThreads) concat_rows_kernel(ConcatPlan p, int64_t row, int64_t rows) {
+  const int64_t n = row * rows;
+  for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n; i += (int64_t)gridDim.x * kThreads) {
+    const int64_t r = i / row, c = i - r * row;
+    int k = 0;
+#pragma unroll
+    for (int j = 1; j < kConcatMax; ++j) k += (j < p.n && c >= p.off[j]) ? 1 : 0;
+    reinterpret_cast<T*>(p.dst)[i] = reinterpret_cast<const T*>(p.src[k])[r * p.w[k] + (c - p.off[k])];
+  }
+}
+
 struct Table256 { uint8_t v[256]; };
 
 __global__ void __launch_bounds__(kThreads) byte_table_kernel(const uint8_t* __restrict__ x, uint8_t* __restrict__ y,
@@ -440,6 +455,26 @@ hipError_t run_copy2d(const void* src, int64_t src_pitch, void* dst, int64_t dst
     hipLaunchKernelGGL(copy2d_kernel<uint8_t>, dim3(grid_for(n)), dim3(kThreads), 0, st, (const uint8_t*)src,
                        src_pitch, (uint8_t*)dst, dst_pitch, width, rows);
   }
+  return hipGetLastError();
+}
+
+// widths and offsets in bytes on entry; converted to units of the widest
+// element size that every pointer and width allows
+hipError_t run_concat_rows(ConcatPlan p, int64_t row, int64_t rows, hipStream_t st) {
+  if (row <= 0 || rows <= 0) return hipSuccess;
+  if (p.n < 1 || p.n > kConcatMax) return hipErrorInvalidValue;
+  auto fits = [&](int u) {
+    if ((uintptr_t)p.dst % u || row % u) return false;
+    for (int k = 0; k < p.n; ++k)
+      if ((uintptr_t)p.src[k] % u || p.w[k] % u) return false;
+    return true;
+  };
+  const int u = fits(16) ? 16 : fits(4) ? 4 : 1;
+  for (int k = 0; k < p.n; ++k) { p.w[k] /= u; p.off[k] /= u; }
+  const int64_t ru = row / u, n = ru * rows;
+  if (u == 16) hipLaunchKernelGGL(concat_rows_kernel<uint4>, dim3(grid_for(n)), dim3(kThreads), 0, st, p, ru, rows);
+  else if (u == 4) hipLaunchKernelGGL(concat_rows_kernel<uint32_t>, dim3(grid_for(n)), dim3(kThreads), 0, st, p, ru, rows);
+  else hipLaunchKernelGGL(concat_rows_kernel<uint8_t>, dim3(grid_for(n)), dim3(kThreads), 0, st, p, ru, rows);
   return hipGetLastError();
 }
 

@@ -1689,6 +1689,24 @@ int ohip_dtensor_alias_internal(const ohip_dtensor* src, int rank, const int64_t
   return OHIP_OK;
 }
 
+// A tensor over a contiguous sub-range of another's buffer (a Slice that
+// keeps one run of elements), starting byte_offset bytes in; shared ownership.
+int ohip_dtensor_view_internal(const ohip_dtensor* src, int rank, const int64_t* shape, size_t byte_offset,
+                               ohip_dtensor** out) {
+  if (!src || !out || rank < 0 || rank > 8) return fail(OHIP_E_INVALID, "dtensor_view: bad argument");
+  size_t bytes;
+  int rc = dt_bytes(src->dtype, rank, shape, OHIP_NCHW, &bytes);
+  if (rc) return rc;
+  if (src->layout != OHIP_NCHW || byte_offset > src->bytes || bytes > src->bytes - byte_offset)
+    return fail(OHIP_E_INVALID, "dtensor_view: range outside the source");
+  auto* t = new ohip_dtensor();
+  t->ctx = src->ctx; t->buf = src->buf; t->ptr = static_cast<char*>(src->ptr) + byte_offset; t->dtype = src->dtype;
+  t->rank = rank; t->layout = OHIP_NCHW; t->bytes = bytes;
+  for (int i = 0; i < rank; ++i) t->shape[i] = shape[i];
+  *out = t;
+  return OHIP_OK;
+}
+
 extern "C" int ohip_dtensor_upload(ohip_ctx* ctx, ohip_dtensor* t, const void* host) {
   if (!t || !host) return fail(OHIP_E_INVALID, "dtensor_upload: null argument");
   if (t->layout != OHIP_NCHW) return fail(OHIP_E_INVALID, "dtensor_upload: NCHW tensors only");

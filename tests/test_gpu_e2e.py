@@ -157,6 +157,48 @@ def test_concat_slice_reshape(ctx):
     np.testing.assert_array_equal(out["y"], ref["y"])
 
 
+@pytest.mark.parametrize("n_in", [3, 8, 10])
+def test_concat_inputs_and_channel_slice_views(ctx, n_in):
+    """Concat in one launch (up to 8 inputs; more fall back to a copy per
+    input), then channel Slices of the single-image result: on 16-byte
+    boundaries they are views of its buffer, elsewhere copies; both feed
+    further nodes, and the views outlive their source node."""
+    rng = np.random.default_rng(n_in)
+    xs = {f"a{i}": rng.normal(0, 1, (1, 2 + i % 3, 4, 4)).astype(np.float32) for i in range(n_in)}
+    total = sum(v.shape[1] for v in xs.values())
+    nodes = [ep.Node("Concat", list(xs), ["c"], A(ints={"axis": 1})),
+             ep.Node("Slice", ["c", "s0", "e0", "ax"], ["v0"]),     # channels 0..1: offset 0
+             ep.Node("Slice", ["c", "s1", "e1", "ax"], ["v1"]),     # channels 1..3: offset 64 bytes
+             ep.Node("Slice", ["c", "s2", "e2", "ax3"], ["v2"]),    # a column range: a copy
+             ep.Node("Add", ["v0", "v0"], ["y0"]), ep.Node("Relu", ["v1"], ["y1"])]
+    inits = {"s0": np.asarray([0], np.float32), "e0": np.asarray([2], np.float32),
+             "s1": np.asarray([1], np.float32), "e1": np.asarray([3], np.float32),
+             "s2": np.asarray([1], np.float32), "e2": np.asarray([3], np.float32),
+             "ax": np.asarray([1], np.float32), "ax3": np.asarray([3], np.float32)}
+    g = unique_graph(nodes, inits, list(xs), ["c", "y0", "y1", "v2"])
+    out = Session(g, ctx).run(xs)
+    ref = G.run_graph(g, xs)
+    assert out["c"].shape == (1, total, 4, 4)
+    for k in ("c", "y0", "y1", "v2"):
+        np.testing.assert_array_equal(out[k], ref[k], err_msg=k)
+
+
+@pytest.mark.parametrize("hw", [(5, 3), (4, 4), (8, 2)])
+def test_concat_u8_alignment_units(ctx, hw):
+    """Byte tensors concatenated in 1-, 4- or 16-byte units as their row
+    widths allow."""
+    rng = np.random.default_rng(7)
+    chans = [3, 16, 1, 4]
+    feeds = {f"f{i}": rng.normal(0, 2, (2, c) + hw).astype(np.float32) for i, c in enumerate(chans)}
+    nodes = [ep.Node("QuantizeLinear", [f"f{i}", "s", "z"], [f"q{i}"]) for i in range(len(chans))]
+    nodes.append(ep.Node("Concat", [f"q{i}" for i in range(len(chans))], ["y"], A(ints={"axis": 1})))
+    inits = {"s": np.asarray([0.05], np.float32), "z": np.asarray([128], np.uint8)}
+    g = unique_graph(nodes, inits, list(feeds), ["y"])
+    out = Session(g, ctx).run(feeds)
+    ref = G.run_graph(g, feeds)
+    np.testing.assert_array_equal(out["y"].astype(np.float32), ref["y"].astype(np.float32))
+
+
 @pytest.mark.parametrize("zp", [None, 0, 128, -100, 3])
 def test_quantize_dequantize(ctx, zp):
     x = (RNG.normal(0, 3, (1, 4, 6, 6)).astype(np.float32))
@@ -265,17 +307,24 @@ def test_captured_forward_replays_match_eager(ctx, which):
         cap.close()
 
 
+# (x shape): a row width that is not a whole 16-byte chunk takes the
+# element-tiled staging kernel; whole-chunk rows take the row-tiled one, here
+# with a partial last channel tile (70 channels) and a single-row image.
+@pytest.mark.parametrize("xshape", [(2, 5, 11, 9), (1, 70, 16, 32), (2, 3, 1, 64)], ids=str)
 @pytest.mark.parametrize("mode", ["reflect", "edge"])
 @pytest.mark.parametrize("dt", [np.float32, np.float16])
-def test_pad_conv_fusion(ctx, mode, dt):
+def test_pad_conv_fusion(ctx, mode, dt, xshape):
     rng = np.random.default_rng(3)
+    cin = xshape[1]
+    pads = [0, 0, 2, 1, 0, 0, 1, 3] if xshape[2] > 2 else [0, 0, 0, 1, 0, 0, 0, 3]
     nodes = [ep.Node("Pad", ["x", "p"], ["xp"], A(strings={"mode": mode})),
-             ep.Node("Conv", ["xp", "w", "b"], ["y"], A(int_lists={"kernel_shape": [3, 3]}))]
-    inits = {"p": np.asarray([0, 0, 2, 1, 0, 0, 1, 3], np.float32),
-             "w": rng.normal(0, 0.1, (16, 5, 3, 3)).astype(dt), "b": rng.normal(0, 0.1, 16).astype(dt)}
+             ep.Node("Conv", ["xp", "w", "b"], ["y"], A(int_lists={"kernel_shape": [3, 3] if xshape[2] > 2 else [1, 3]}))]
+    ks = (3, 3) if xshape[2] > 2 else (1, 3)
+    inits = {"p": np.asarray(pads, np.float32),
+             "w": rng.normal(0, 0.1, (16, cin) + ks).astype(dt), "b": rng.normal(0, 0.1, 16).astype(dt)}
     g = unique_graph(nodes, inits, ["x"], ["y"])
     assert [n.op for n in fuse(g).nodes] == ["Conv"]
-    x = rng.uniform(-1, 1, (2, 5, 11, 9)).astype(dt)
+    x = rng.uniform(-1, 1, xshape).astype(dt)
     out = Session(g, ctx).run({"x": x})
     ref = G.run_graph(g, {"x": x}, half=dt == np.float16)
     close(out["y"], ref["y"], 1e-4 if dt == np.float32 else 1e-2)

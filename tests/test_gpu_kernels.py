@@ -139,6 +139,8 @@ CONV_CASES = [
     ((1, 32, 12, 12), (16, 32, 1, 1), (1, 1), (0, 0, 0, 0), (1, 1)),
     ((1, 128, 16, 16), (3, 128, 7, 7), (1, 1), (3, 3, 3, 3), (1, 1)),
     ((3, 5, 9, 11), (7, 5, 3, 2), (1, 2), (0, 1, 1, 0), (1, 1)),
+    # row-tiled staging: a partial last channel tile, several images
+    ((2, 70, 8, 16), (8, 70, 3, 3), (1, 1), (1, 1, 1, 1), (1, 1)),
 ]
 
 
@@ -431,6 +433,9 @@ QCONV_CASES = [
     ((2, 32, 11, 9), (24, 32, 1, 1), (1, 1), (0, 0, 0, 0), (1, 1)),
     ((1, 20, 12, 12), (8, 20, 3, 3), (1, 1), (2, 1, 0, 2), (2, 2)),
     ((1, 64, 10, 10), (64, 64, 5, 5), (1, 1), (2, 2, 2, 2), (1, 1)),
+    # row-tiled staging: 3 channels padded to 16, a partial channel tile
+    ((1, 3, 32, 32), (16, 3, 3, 3), (2, 2), (1, 1, 1, 1), (1, 1)),
+    ((2, 80, 16, 16), (16, 80, 1, 1), (1, 1), (0, 0, 0, 0), (1, 1)),
 ]
 
 
