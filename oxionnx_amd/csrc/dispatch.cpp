@@ -1478,6 +1478,79 @@ int do_dequantize(ohip_ctx* ctx, const ohip_node* nd, int placement, ohip_output
   return output_device(ctx, st, placement, out, OHIP_F32, shape_of(x), yd, (size_t)n * 4);
 }
 
+// ---------------------------------------------------------------- QLinearAdd
+// This provider's fusion of DequantizeLinear(A), DequantizeLinear(B), Add and
+// QuantizeLinear (the dequantised residual sum of quantised networks), with
+// the ONNX contrib operator's inputs: A, A_scale, A_zero_point, B, B_scale,
+// B_zero_point, C_scale, C_zero_point (per-tensor).  Each step is computed as
+// the unfused node computes it (do_dequantize, do_binary, do_quantize); the
+// output type follows C's zero point as QuantizeLinear's does.
+int do_qadd(ohip_ctx* ctx, const ohip_node* nd, int placement, ohip_output* out) {
+  if (nd->n_inputs < 7) return decline("QLinearAdd: inputs");
+  const ohip_tensor* a = input(nd, 0);
+  const ohip_tensor* b = input(nd, 3);
+  if (!a || !b) return decline("QLinearAdd: missing operand");
+  auto scalar = [&](int i, bool need, float* v) {
+    const ohip_tensor* t = input(nd, i);
+    if (!t) { *v = 0.0f; return !need; }
+    if (!host_only(t) || numel(t) != 1) return false;
+    *v = (float)host_at(t, 0);
+    return true;
+  };
+  ohip::QAddArgs q{};
+  if (!scalar(1, true, &q.sa) || !scalar(2, false, &q.za) || !scalar(4, true, &q.sb) || !scalar(5, false, &q.zb) ||
+      !scalar(6, true, &q.sc) || !scalar(7, false, &q.zc))
+    return decline("QLinearAdd: per-tensor scales and zero points only");
+  const bool has_zc = input(nd, 7) != nullptr;
+  const bool u8 = !has_zc || q.zc > 127.0f;
+  q.lo = u8 ? 0.0f : -128.0f;
+  q.hi = u8 ? 255.0f : 127.0f;
+  const int rank = std::max(a->rank, b->rank);
+  if (rank > ohip::kMaxRank) return decline("QLinearAdd: rank");
+  ohip::BcastPlan p{};
+  p.rank = rank;
+  int64_t sa = 1, sb = 1, n = 1;
+  std::vector<int64_t> oshape((size_t)rank);
+  for (int d = 0; d < rank; ++d) {
+    const int slot = ohip::kMaxRank - 1 - d;
+    const int ia = a->rank - 1 - d, ib = b->rank - 1 - d;
+    const int64_t ea = ia >= 0 ? a->shape[ia] : 1, eb = ib >= 0 ? b->shape[ib] : 1;
+    if (ea != eb && ea != 1 && eb != 1) return decline("QLinearAdd: shapes do not broadcast");
+    const int64_t e = ea == 1 ? eb : ea;
+    p.shape[slot] = e;
+    p.sa[slot] = ea == 1 ? 0 : sa;
+    p.sb[slot] = eb == 1 ? 0 : sb;
+    sa *= ea;
+    sb *= eb;
+    n *= e;
+    oshape[(size_t)(rank - 1 - d)] = e;
+  }
+  const bool same = numel(a) == n && numel(b) == n;
+  Stage st(ctx);
+  std::vector<uint8_t> ab, bb;
+  auto bytes_of = [&](const ohip_tensor* t, std::vector<uint8_t>& hb, int* dt) -> const void* {
+    if (t->device) {
+      *dt = t->dtype;
+      if (*dt != OHIP_U8 && *dt != OHIP_I8) return nullptr;
+      return ohip_dtensor_ptr(t->device);
+    }
+    if (!to_bytes(t, hb, dt)) return nullptr;
+    return st.operand(t, hb.data(), hb.size());
+  };
+  int adt = -1, bdt = -1;
+  const void* ad = bytes_of(a, ab, &adt);
+  const void* bd = bytes_of(b, bb, &bdt);
+  if (!ad || !bd) return decline("QLinearAdd: operands must be 8-bit");
+  q.a_signed = adt == OHIP_I8;
+  q.b_signed = bdt == OHIP_I8;
+  void* yd = st.alloc((size_t)n);
+  if (!yd) return OHIP_E_NOMEM;
+  hipError_t e = ohip::run_qadd(static_cast<const uint8_t*>(ad), static_cast<const uint8_t*>(bd),
+                                static_cast<uint8_t*>(yd), n, p, same, q, (hipStream_t)ohip_ctx_stream(ctx));
+  if (e != hipSuccess) return ohip_hip_error_internal(e, "node kernel launch");
+  return output_device(ctx, st, placement, out, u8 ? OHIP_U8 : OHIP_I8, oshape, yd, (size_t)n);
+}
+
 }  // namespace
 
 // ------------------------------------------------------------------ public
@@ -1489,7 +1562,7 @@ extern "C" int ohip_is_supported_op(const char* op) {
                                "ConvInteger", "Relu", "LeakyRelu", "Tanh", "Sigmoid", "Silu", "Identity",
                                "Add", "Sub", "Mul", "Div", "OxiInstanceNorm", "InstanceNormalization", "Resize",
                                "Pad", "MaxPool", "Concat", "Slice", "Reshape", "Flatten", "Squeeze", "Unsqueeze",
-                               "QuantizeLinear", "DequantizeLinear"};
+                               "QuantizeLinear", "DequantizeLinear", "QLinearAdd"};
   for (const char* o : kOps)
     if (std::strcmp(op, o) == 0) return 1;
   return 0;
@@ -1510,6 +1583,7 @@ extern "C" int ohip_accepts_resident_slot(const char* op, int index) {
     return index == 0 || index == 1;
   if (!std::strcmp(op, "OxiInstanceNorm")) return index >= 0 && index <= 2;
   if (!std::strcmp(op, "Concat")) return index >= 0;
+  if (!std::strcmp(op, "QLinearAdd")) return index == 0 || index == 3;
   return 0;
 }
 
@@ -1552,6 +1626,7 @@ extern "C" int ohip_try_dispatch(ohip_ctx* ctx, const ohip_node* node, int place
     rc = do_alias(ctx, node, op, placement, out);
   else if (op == "QuantizeLinear") rc = do_quantize(ctx, node, placement, out);
   else if (op == "DequantizeLinear") rc = do_dequantize(ctx, node, placement, out);
+  else if (op == "QLinearAdd") rc = do_qadd(ctx, node, placement, out);
   else rc = decline("unsupported op " + op);
   if (rc == OHIP_DECLINED) ohip_note_declined(ctx, t_err.c_str());
   return rc;

@@ -240,6 +240,15 @@ hipError_t run_quantize(const float* x, uint8_t* y, int64_t n, float scale, floa
 hipError_t run_dequantize(const uint8_t* x, bool is_signed, float* y, int64_t n, float scale, float zp,
                           hipStream_t st);
 hipError_t run_byte_table(const uint8_t* x, uint8_t* y, int64_t n, const uint8_t* table, hipStream_t st);
+// QLinearAdd parameters: operand scales / zero points, the output's scale,
+// zero point and saturation range, and whether each operand is int8.
+struct QAddArgs {
+  float sa, za, sb, zb, sc, zc, lo, hi;
+  int a_signed, b_signed;
+};
+hipError_t run_qadd(const uint8_t* a, const uint8_t* b, uint8_t* y, int64_t n, const BcastPlan& p, bool same,
+                    const QAddArgs& q, hipStream_t st);
+
 constexpr int kConcatMax = 8;
 struct ConcatPlan {
   const void* src[kConcatMax];

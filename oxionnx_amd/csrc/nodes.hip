@@ -282,6 +282,42 @@ __global__ void __launch_bounds__(kThreads) dequantize_kernel(const uint8_t* __r
   }
 }
 
+// The dequantised residual sum in one pass: DequantizeLinear of both byte
+// operands, their f32 Add and QuantizeLinear of the sum, each step the
+// arithmetic of its own kernel above (no contraction across the steps).
+template <bool SAME>
+__global__ void __launch_bounds__(kThreads) qadd_kernel(const uint8_t* __restrict__ a, const uint8_t* __restrict__ b,
+                                                        uint8_t* __restrict__ y, int64_t n, BcastPlan p, QAddArgs q) {
+#pragma clang fp contract(off)
+  for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n; i += (int64_t)gridDim.x * kThreads) {
+    int64_t ia = i, ib = i;
+    if (!SAME) {
+      ia = ib = 0;
+      int64_t r = i;
+#pragma unroll
+      for (int d = kMaxRank - 1; d >= 0; --d) {
+        if (d < kMaxRank - p.rank) break;
+        const int64_t e = p.shape[d];
+        const int64_t c = r % e;
+        r /= e;
+        ia += c * p.sa[d];
+        ib += c * p.sb[d];
+      }
+    }
+    const float va = q.a_signed ? (float)(int8_t)a[ia] : (float)a[ia];
+    const float vb = q.b_signed ? (float)(int8_t)b[ib] : (float)b[ib];
+    const float da = (va - q.za) * q.sa;
+    const float db = (vb - q.zb) * q.sb;
+    const float sum = da + db;
+    const float v = sum / q.sc;
+    float r = __builtin_rintf(v);
+    if (!__builtin_isfinite(v)) r = v;
+    float o = r + q.zc;
+    o = o < q.lo ? q.lo : (o > q.hi ? q.hi : o);
+    y[i] = (uint8_t)((int32_t)o & 0xff);
+  }
+}
+
 // ---------------------------------------------------------------- 2-D copy (Concat)
 template <class T>
 __global__ void __launch_bounds__(kThreads) copy2d_kernel(const T* __restrict__ src, int64_t sp, T* __restrict__ dst,
@@ -420,6 +456,16 @@ hipError_t run_quantize(const float* x, uint8_t* y, int64_t n, float scale, floa
                         hipStream_t st) {
   if (n <= 0) return hipSuccess;
   hipLaunchKernelGGL(quantize_kernel, dim3(grid_for(n)), dim3(kThreads), 0, st, x, y, n, scale, zp, lo, hi);
+  return hipGetLastError();
+}
+
+hipError_t run_qadd(const uint8_t* a, const uint8_t* b, uint8_t* y, int64_t n, const BcastPlan& p, bool same,
+                    const QAddArgs& q, hipStream_t st) {
+  if (n <= 0) return hipSuccess;
+  if (same)
+    hipLaunchKernelGGL(qadd_kernel<true>, dim3(grid_for(n)), dim3(kThreads), 0, st, a, b, y, n, p, q);
+  else
+    hipLaunchKernelGGL(qadd_kernel<false>, dim3(grid_for(n)), dim3(kThreads), 0, st, a, b, y, n, p, q);
   return hipGetLastError();
 }
 

@@ -21,6 +21,10 @@ reference's optimizer passes (src/optimizer/fusion/mod.rs):
   * OxiInstanceNorm -> Mul(gamma) -> Add(beta) [-> Relu], where gamma and beta
     are Reshape(Slice(style)) column ranges of one style tensor (AdaIN),
     becomes one OxiInstanceNorm that reads the modulation from the style rows.
+  * DequantizeLinear(A), DequantizeLinear(B) -> Add -> QuantizeLinear, each
+    the only consumer of the previous (the dequantised residual sum of a
+    quantised network), becomes one QLinearAdd node (the ONNX contrib
+    operator's inputs) that the provider runs as the same steps in one pass.
 Nodes left without consumers are dropped.
 """
 import ctypes
@@ -127,12 +131,48 @@ def fuse(graph: Graph) -> Graph:
                 if _fuse_pad_into_conv(nodes, i, sole, inits):
                     changed = True
                     break
+            if n.op == "Add" and _fuse_qadd(nodes, i, sole, cons):
+                changed = True
+                break
             if n.op == "OxiInstanceNorm" and len([t for t in n.inputs if t]) == 1:
                 if _fuse_adain(nodes, i, sole, inits):
                     changed = True
                     break
         nodes = [n for n in nodes if n is not None] if changed else nodes
     return replace(graph, nodes=_drop_dead(nodes, keep_out))
+
+
+def _fuse_qadd(nodes, i, sole, cons):
+    """Add(DequantizeLinear(a), DequantizeLinear(b)) -> QuantizeLinear as one
+    QLinearAdd [a, a_scale, a_zp, b, b_scale, b_zp, y_scale, y_zp]."""
+    add = nodes[i]
+    if len(add.inputs) != 2:
+        return False
+    producers = {}
+    for j, m in enumerate(nodes):
+        if m is not None:
+            for o in m.outputs:
+                producers[o] = j
+    deqs = []
+    for t in add.inputs:
+        j = producers.get(t)
+        if j is None or nodes[j].op != "DequantizeLinear" or sole(t) != i or len(nodes[j].inputs) < 2:
+            return False
+        deqs.append(j)
+    if deqs[0] == deqs[1]:
+        return False
+    q = sole(add.outputs[0])
+    if q is None or nodes[q].op != "QuantizeLinear" or len(nodes[q].inputs) < 2:
+        return False
+
+    def three(m):
+        ins = list(m.inputs) + [""] * (3 - len(m.inputs))
+        return ins[:3]
+
+    inputs = three(nodes[deqs[0]]) + three(nodes[deqs[1]]) + three(nodes[q])[1:]
+    nodes[i] = ep.Node("QLinearAdd", inputs, list(nodes[q].outputs), name=add.name)
+    nodes[deqs[0]] = nodes[deqs[1]] = nodes[q] = None
+    return True
 
 
 def _drop_dead(nodes, keep):

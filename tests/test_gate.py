@@ -100,7 +100,7 @@ def test_op_support_predicates():
     for op in ["Conv", "ConvTranspose", "Gemm", "MatMul", "QLinearMatMul", "MatMulInteger", "QLinearConv",
                "ConvInteger", "Relu", "LeakyRelu", "Tanh", "Sigmoid", "Silu", "Add", "Sub", "Mul", "Div", "OxiInstanceNorm",
                "InstanceNormalization", "Resize", "Pad", "MaxPool", "Concat", "Slice", "Reshape", "Flatten",
-               "Squeeze", "Unsqueeze", "QuantizeLinear", "DequantizeLinear"]:
+               "Squeeze", "Unsqueeze", "QuantizeLinear", "DequantizeLinear", "QLinearAdd"]:
         assert ep.is_supported_op(op), op
     for op in ["Transpose", "Softmax", "LSTM", ""]:
         assert not ep.is_supported_op(op)
@@ -108,6 +108,8 @@ def test_op_support_predicates():
     assert ep.accepts_resident_slot("ConvTranspose", 0) and not ep.accepts_resident_slot("ConvTranspose", 1)
     assert ep.accepts_resident_slot("Gemm", 0) and not ep.accepts_resident_slot("Gemm", 1)
     assert ep.accepts_resident_slot("QLinearConv", 0) and not ep.accepts_resident_slot("QLinearConv", 3)
+    assert ep.accepts_resident_slot("QLinearAdd", 0) and ep.accepts_resident_slot("QLinearAdd", 3)
+    assert not ep.accepts_resident_slot("QLinearAdd", 1) and not ep.accepts_resident_slot("QLinearAdd", 6)
     assert ep.accepts_resident_slot("Add", 1) and not ep.accepts_resident_slot("Add", 2)
     assert ep.accepts_resident_slot("Concat", 3)
     assert not ep.accepts_resident_slot("QLinearMatMul", 0)

@@ -199,6 +199,44 @@ def test_concat_u8_alignment_units(ctx, hw):
     np.testing.assert_array_equal(out["y"].astype(np.float32), ref["y"].astype(np.float32))
 
 
+# (a shape, b shape, a zero point, b zero point, output zero point or None)
+QADD_CASES = [
+    ((1, 16, 20, 20), (1, 16, 20, 20), -100, -100, -100),
+    ((1, 8, 6, 6), (1, 8, 6, 6), 128, 3, 128),
+    ((2, 4, 5, 5), (1, 4, 1, 5), 0, 128, None),
+    ((1, 3, 7), (7,), -20, 5, 0),
+]
+
+
+@pytest.mark.parametrize("case", QADD_CASES, ids=str)
+def test_qlinear_add_fusion_bit_exact(ctx, case):
+    """DequantizeLinear x2 -> Add -> QuantizeLinear fuses into one QLinearAdd
+    whose bytes equal the unfused chain's (broadcasting, u8 / i8 operands,
+    output type from the zero point's value)."""
+    ash, bsh, za, zb, zc = case
+    rng = np.random.default_rng(len(ash) * 7 + abs(za))
+
+    def zp_arr(z):
+        return np.asarray([z], np.uint8 if z > 127 else np.int8)
+
+    feeds = {"fa": rng.normal(0, 3, ash).astype(np.float32), "fb": rng.normal(0, 3, bsh).astype(np.float32)}
+    inits = {"sa": np.asarray([0.07], np.float32), "za": zp_arr(za), "sb": np.asarray([0.045], np.float32),
+             "zb": zp_arr(zb), "sc": np.asarray([0.09], np.float32)}
+    nodes = [ep.Node("QuantizeLinear", ["fa", "sa", "za"], ["a"]), ep.Node("QuantizeLinear", ["fb", "sb", "zb"], ["b"]),
+             ep.Node("DequantizeLinear", ["a", "sa", "za"], ["da"]), ep.Node("DequantizeLinear", ["b", "sb", "zb"], ["db"]),
+             ep.Node("Add", ["da", "db"], ["s"])]
+    if zc is None:
+        nodes.append(ep.Node("QuantizeLinear", ["s", "sc"], ["y"]))
+    else:
+        inits["zc"] = zp_arr(zc)
+        nodes.append(ep.Node("QuantizeLinear", ["s", "sc", "zc"], ["y"]))
+    g = unique_graph(nodes, inits, ["fa", "fb"], ["y"])
+    assert [n.op for n in fuse(g).nodes] == ["QuantizeLinear", "QuantizeLinear", "QLinearAdd"]
+    out = Session(g, ctx).run(feeds)
+    ref = G.run_graph(g, feeds)
+    np.testing.assert_array_equal(out["y"].astype(np.float32), ref["y"].astype(np.float32))
+
+
 @pytest.mark.parametrize("zp", [None, 0, 128, -100, 3])
 def test_quantize_dequantize(ctx, zp):
     x = (RNG.normal(0, 3, (1, 4, 6, 6)).astype(np.float32))
