@@ -69,8 +69,7 @@ def _scalar(inits, name):
 
 
 def fuse(graph: Graph) -> Graph:
-    nodes = list(graph.nodes)
-    inits = graph.initializers
+    nodes, inits = _merge_sibling_gemms(list(graph.nodes), dict(graph.initializers), set(graph.outputs))
     keep_out = set(graph.outputs)
     changed = True
     while changed:
@@ -139,7 +138,93 @@ def fuse(graph: Graph) -> Graph:
                     changed = True
                     break
         nodes = [n for n in nodes if n is not None] if changed else nodes
-    return replace(graph, nodes=_drop_dead(nodes, keep_out))
+    return replace(graph, nodes=_drop_dead(nodes, keep_out), initializers=inits)
+
+
+def _init_array(inits, name):
+    v = inits.get(name) if name else None
+    if v is None or isinstance(v, ep.Typed):
+        return None
+    return np.asarray(v)
+
+
+def _merge_sibling_gemms(nodes, inits, keep_out):
+    """Gemm nodes that read the same A with initializer B / C (same transB,
+    alpha, beta, K and dtype, no fused attribute) become one Gemm over the
+    concatenated weights; each former output is a column range of the merged
+    one.  Column Slices of a former output are re-pointed at the merged
+    output with shifted bounds (on a single-row output the provider serves
+    them as views, so the merge costs no copy); any other use gets a Slice
+    node.  One launch replaces several skinny ones (the per-block style Gemms
+    of a style-modulated generator all read one latent row)."""
+    groups = {}
+    for i, n in enumerate(nodes):
+        if n.op != "Gemm" or len(n.inputs) != 3 or n.attrs.strings or n.attrs.ints.get("transA", 0):
+            continue
+        b, c = _init_array(inits, n.inputs[1]), _init_array(inits, n.inputs[2])
+        if b is None or c is None or b.ndim != 2 or c.ndim != 1 or b.dtype != c.dtype:
+            continue
+        tb = n.attrs.ints.get("transB", 0)
+        k, nn = (b.shape[1], b.shape[0]) if tb else b.shape
+        if c.shape[0] != nn:
+            continue
+        key = (n.inputs[0], tb, n.attrs.floats.get("alpha", 1.0), n.attrs.floats.get("beta", 1.0), str(b.dtype), k)
+        groups.setdefault(key, []).append(i)
+    cons = _consumers(nodes)
+    inserted = {}
+    for key, members in groups.items():
+        if len(members) < 2:
+            continue
+        tb = key[1]
+        first = nodes[members[0]]
+        bs = [_init_array(inits, nodes[m].inputs[1]) for m in members]
+        cs = [_init_array(inits, nodes[m].inputs[2]) for m in members]
+        wname, bname, out = first.name + "_mB", first.name + "_mC", first.outputs[0] + "_merged"
+        inits[wname] = np.concatenate(bs, axis=0 if tb else 1)
+        inits[bname] = np.concatenate(cs)
+        merged = ep.Node("Gemm", [first.inputs[0], wname, bname], [out], replace(first.attrs), name=first.name + "_merged")
+        extra = []
+        off = 0
+        for m, c in zip(members, cs):
+            o, width = nodes[m].outputs[0], c.shape[0]
+            users = cons.get(o, [])
+            movable = o not in keep_out and all(_column_slice(nodes[u], o, inits) is not None for u in users)
+            if movable:
+                for u in users:
+                    lo, hi = _column_slice(nodes[u], o, inits)
+                    lo, hi = max(0, min(lo, width)), max(0, min(hi, width))
+                    sn, en = nodes[u].name + "_ms", nodes[u].name + "_me"
+                    inits[sn], inits[en] = np.asarray([off + lo], np.float32), np.asarray([off + max(lo, hi)], np.float32)
+                    nodes[u] = replace(nodes[u], inputs=[out, sn, en] + list(nodes[u].inputs[3:]))
+            else:
+                sn, en, ax = o + "_ms", o + "_me", o + "_max"
+                inits[sn], inits[en], inits[ax] = (np.asarray([off], np.float32), np.asarray([off + width], np.float32),
+                                                   np.asarray([1], np.float32))
+                extra.append(ep.Node("Slice", [out, sn, en, ax], [o], name=o + "_view"))
+            off += width
+        nodes[members[0]] = merged
+        inserted[members[0]] = extra
+        for m in members[1:]:
+            nodes[m] = None
+    result = []
+    for i, n in enumerate(nodes):
+        if n is not None:
+            result.append(n)
+            result.extend(inserted.get(i, []))
+    return result, inits
+
+
+def _column_slice(node, tensor, inits):
+    """(start, end) of a unit-step Slice of `tensor` along axis 1 (or -1) of
+    a matrix, normalised against nothing yet (negative bounds excluded)."""
+    if node.op != "Slice" or len(node.inputs) < 4 or node.inputs[0] != tensor:
+        return None
+    st, en, ax = _ints(inits, node.inputs[1]), _ints(inits, node.inputs[2]), _ints(inits, node.inputs[3])
+    if not st or not en or ax not in ([1], [-1]) or len(st) != 1 or len(en) != 1 or st[0] < 0 or en[0] < 0:
+        return None
+    if node.inputs[4:] and node.inputs[4] and _ints(inits, node.inputs[4]) != [1]:
+        return None
+    return st[0], en[0]
 
 
 def _fuse_qadd(nodes, i, sole, cons):

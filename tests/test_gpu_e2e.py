@@ -113,6 +113,18 @@ def test_resize_nearest(ctx, coord, rule, scales):
     np.testing.assert_array_equal(out["y"], ref["y"])
 
 
+# output rows narrower than a block (several rows per block iteration) and
+# wider (a block loops over the row)
+@pytest.mark.parametrize("xshape,scales", [((2, 5, 9, 150), (1, 1, 2, 2)), ((1, 3, 40, 7), (1, 1, 0.5, 3)),
+                                           ((1, 2, 3, 1100), (1, 1, 1, 1.5))], ids=str)
+@pytest.mark.parametrize("dt", [np.float32, np.float16])
+def test_resize_nearest_row_shapes(ctx, xshape, scales, dt):
+    x = np.random.default_rng(11).normal(0, 1, xshape).astype(dt)
+    node = ep.Node("Resize", ["x", "", "sc"], ["y"], A(strings={"mode": "nearest"}))
+    out, ref = run_one(ctx, node, {"sc": np.asarray(scales, np.float32)}, {"x": x})
+    np.testing.assert_array_equal(out["y"].astype(np.float32), ref["y"].astype(np.float32))
+
+
 @pytest.mark.parametrize("mode", ["constant", "reflect", "edge"])
 @pytest.mark.parametrize("pads", [[0, 0, 3, 3, 0, 0, 3, 3], [0, 1, 1, 2, 1, 0, 2, 1]])
 def test_pad(ctx, mode, pads):

@@ -1,0 +1,59 @@
+"""Graph rewrites of the session's fusion pass, checked on the CPU: the
+rewritten graph, run through the oracle's graph runner, gives the original
+graph's outputs (merging sibling Gemms only regroups columns, so the f32
+results agree to the oracle's own summation differences)."""
+import numpy as np
+import pytest
+
+from oracle import graph_ref as G
+from oxionnx_amd import ep
+from oxionnx_amd.ep import Attributes as A
+from oxionnx_amd.session import Graph, fuse
+
+
+def _f32(v):
+    return np.asarray(v, np.float32)
+
+
+@pytest.mark.parametrize("trans_b", [0, 1])
+def test_sibling_gemms_merge_into_one(trans_b):
+    rng = np.random.default_rng(trans_b)
+    widths = [6, 10, 4]
+    inits, nodes = {}, []
+    for i, n in enumerate(widths):
+        w = rng.normal(0, 0.3, (n, 8) if trans_b else (8, n)).astype(np.float32)
+        inits[f"W{i}"], inits[f"C{i}"] = w, rng.normal(0, 0.1, n).astype(np.float32)
+        nodes.append(ep.Node("Gemm", ["lat", f"W{i}", f"C{i}"], [f"s{i}"], A(ints={"transB": trans_b}), name=f"g{i}"))
+    # s0: two column slices; s1: a graph output and a Relu; s2: a slice with an end past the width
+    inits.update({"a0": _f32([0]), "b0": _f32([3]), "a1": _f32([3]), "b1": _f32([6]), "ax": _f32([1]),
+                  "a2": _f32([1]), "b2": _f32([99])})
+    nodes += [ep.Node("Slice", ["s0", "a0", "b0", "ax"], ["p0"], name="sl0"),
+              ep.Node("Slice", ["s0", "a1", "b1", "ax"], ["p1"], name="sl1"),
+              ep.Node("Relu", ["s1"], ["r1"], name="relu"),
+              ep.Node("Slice", ["s2", "a2", "b2", "ax"], ["p2"], name="sl2")]
+    g = Graph(nodes, inits, ["lat"], ["p0", "p1", "s1", "r1", "p2"])
+    f = fuse(g)
+    assert [n.op for n in f.nodes].count("Gemm") == 1
+    feeds = {"lat": rng.normal(0, 1, (2, 8)).astype(np.float32)}
+    want, got = G.run_graph(g, feeds), G.run_graph(f, feeds)
+    for k in g.outputs:
+        assert got[k].shape == want[k].shape, k
+        np.testing.assert_allclose(got[k], want[k], rtol=1e-6, atol=1e-6, err_msg=k)
+
+
+def test_gemms_with_different_a_or_attributes_stay_apart():
+    rng = np.random.default_rng(2)
+    inits = {f"W{i}": rng.normal(0, 1, (4, 3)).astype(np.float32) for i in range(3)}
+    inits.update({f"C{i}": np.zeros(3, np.float32) for i in range(3)})
+    nodes = [ep.Node("Gemm", ["x", "W0", "C0"], ["y0"]),
+             ep.Node("Gemm", ["z", "W1", "C1"], ["y1"]),
+             ep.Node("Gemm", ["x", "W2", "C2"], ["y2"], A(floats={"alpha": 0.5}))]
+    g = Graph(nodes, inits, ["x", "z"], ["y0", "y1", "y2"])
+    assert [n.op for n in fuse(g).nodes] == ["Gemm", "Gemm", "Gemm"]
+
+
+def test_face_swap_style_gemms_merge():
+    from oxionnx_amd import workloads
+    g, _ = workloads.face_swap_generator(dtype="f32", n_blocks=2)
+    ops = [n.op for n in fuse(g).nodes]
+    assert ops.count("Gemm") == 1 and ops.count("OxiInstanceNorm") == 4
