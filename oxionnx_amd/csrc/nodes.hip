@@ -186,27 +186,41 @@ __global__ void __launch_bounds__(kThreads) resize_nearest_kernel(const T* __res
 }
 
 // Row form: the source row is found once per output row and the source
-// column of every output column once per block (an LDS table), so an output
-// element costs one load and one store.  A row of up to kThreads columns
-// shares the block with the next rows.
+// column of every output column once per block (an LDS table).  A thread
+// writes one 16-byte run of a row (or one element when the row is not whole
+// runs); the runs of one row share the block with the next rows.  32-bit
+// row indices (the launcher checks the count).
 constexpr int kResizeMaxCols = 4096;
 template <class T>
 __global__ void __launch_bounds__(kThreads) resize_nearest_rows_kernel(const T* __restrict__ x, T* __restrict__ y,
-                                                                       int64_t rows, ResizePlan p) {
+                                                                       int rows, ResizePlan p) {
+  constexpr int V = 16 / (int)sizeof(T);
   __shared__ int ixmap[kResizeMaxCols];
   for (int ox = threadIdx.x; ox < p.ow; ox += kThreads) ixmap[ox] = nearest_src(ox, p.iw, p.ow, p.sw, p.coord, p.rule);
   __syncthreads();
-  const int span = p.ow < kThreads ? p.ow : kThreads;
-  const int rpi = kThreads / span;   // rows per block iteration
-  const int lr = threadIdx.x / span, ox0 = threadIdx.x - lr * span;
+  const bool vec = p.ow % V == 0;
+  const int units = vec ? p.ow / V : p.ow;          // per row
+  const int span = units < kThreads ? units : kThreads;
+  const int rpi = kThreads / span;                  // rows per block iteration
+  const int lr = threadIdx.x / span, u0 = threadIdx.x - lr * span;
   if (lr >= rpi) return;
-  for (int64_t r = (int64_t)blockIdx.x * rpi + lr; r < rows; r += (int64_t)gridDim.x * rpi) {
-    const int oy = (int)(r % p.oh);
-    const int64_t pl = r / p.oh;
+  for (int r = blockIdx.x * rpi + lr; r < rows; r += gridDim.x * rpi) {
+    const int oy = r % p.oh, pl = r / p.oh;
     const int iy = nearest_src(oy, p.ih, p.oh, p.sh, p.coord, p.rule);
-    const T* xr = x + (pl * p.ih + iy) * p.iw;
-    T* yr = y + r * p.ow;
-    for (int ox = ox0; ox < p.ow; ox += span) yr[ox] = xr[ixmap[ox]];
+    const T* xr = x + ((int64_t)pl * p.ih + iy) * p.iw;
+    T* yr = y + (int64_t)r * p.ow;
+    if (vec) {
+      for (int u = u0; u < units; u += span) {
+        T e[V];
+#pragma unroll
+        for (int k = 0; k < V; ++k) e[k] = xr[ixmap[u * V + k]];
+        uint4 w;
+        __builtin_memcpy(&w, e, 16);
+        *reinterpret_cast<uint4*>(yr + u * V) = w;
+      }
+    } else {
+      for (int ox = u0; ox < p.ow; ox += span) yr[ox] = xr[ixmap[ox]];
+    }
   }
 }
 
@@ -449,11 +463,13 @@ hipError_t run_resize_nearest(int elem_bytes, const void* x, void* y, int64_t pl
                               hipStream_t st) {
   const int64_t n = planes * p.oh * p.ow;
   if (n <= 0) return hipSuccess;
-  if (p.ow <= kResizeMaxCols) {
-    const int64_t rows = planes * p.oh;
-    const int rpi = kThreads / (p.ow < kThreads ? p.ow : kThreads);
+  const int64_t rows = planes * p.oh;
+  if (p.ow <= kResizeMaxCols && rows < (int64_t)1 << 30 && (uintptr_t)y % 16 == 0) {
+    const int v = 16 / elem_bytes;
+    const int units = p.ow % v == 0 ? p.ow / v : p.ow;
+    const int rpi = kThreads / (units < kThreads ? units : kThreads);
     const int64_t blocks = std::min<int64_t>((rows + rpi - 1) / rpi, 65536);
-    OHIP_BY_ELEM_SIZE(elem_bytes, resize_nearest_rows_kernel, dim3((unsigned)blocks), rows, p);
+    OHIP_BY_ELEM_SIZE(elem_bytes, resize_nearest_rows_kernel, dim3((unsigned)blocks), (int)rows, p);
   }
   OHIP_BY_ELEM_SIZE(elem_bytes, resize_nearest_kernel, dim3(grid_for(n)), planes, p);
 }
