@@ -170,6 +170,7 @@ def main():
             extras["gemm_sweep"] = sweep
             extras.update(bench_conv(torch, ctx, L, stream, rng, args.only))
             extras.update(bench_int8(torch, ctx, L, stream, rng, args.only))
+            extras.update(bench_large(torch, ctx, L, stream, rng, args.only))
             extras.update(bench_widened(torch, ctx, L, stream, rng, args.only))
             extras.update(bench_e2e(torch, ctx, stream, args.only, args.no_cpu))
 
@@ -241,6 +242,34 @@ def bench_int8(torch, ctx, L, stream, rng, only):
     by = 4096 * 768 + 768 * 3072 + 4 * 4096 * 3072
     out["matmul_integer_i32"] = {"ms": round(t, 5), "tops": round(ops / 2 / t / 1e9, 2),
                                  "gbps": round(by / t / 1e6, 1), "frac_hbm": round(by / t / 1e6 / HBM_GBPS, 4)}
+    return out
+
+
+def bench_large(torch, ctx, L, stream, rng, only):
+    """The same kernels at a large square shape, (M,K,N) = 8192^3: f16 Gemm
+    (B resident, row bias) and int8 QLinearMatMul (u8 out), where the tile
+    count fills the chip several times and the fixed per-launch costs vanish."""
+    keys = ("large_gemm_f16", "large_qlinear_matmul_i8")
+    if only and only not in keys:
+        return {}
+    out = {}
+    m = k = n = 8192
+    fl = 2.0 * m * k * n
+    if not only or only == keys[0]:
+        _, _, _, w, at, ct, y = gemm_setup(torch, ctx, L, m, k, n, L.F16, rng)
+        t = time_launches(torch, stream, lambda: ctx.gemm(at, w, ct, out=y), 20, 3)
+        out[keys[0]] = {"shape": [m, k, n], "ms": round(t, 5), "tflops": round(fl / t / 1e9, 2),
+                        "frac_mfma": round(fl / t / 1e9 / PEAK_TFLOPS["f16"], 4)}
+        del w, at, ct, y
+    if not only or only == keys[1]:
+        a = torch.from_numpy(rng.integers(0, 256, (m, k)).astype(np.uint8)).cuda()
+        wq = ctx.weight_qgemm(rng.integers(-127, 128, (k, n)).astype(np.int8), zp=0,
+                              scale=rng.uniform(0.001, 0.01, n).astype(np.float32), name="large.B")
+        yq = torch.empty((m, n), dtype=torch.uint8, device="cuda")
+        t = time_launches(torch, stream, lambda: ctx.qgemm(a, wq, a_zp=128, a_scale=0.02, y_scale=0.05, y_zp=128,
+                                                           out=yq), 20, 3)
+        out[keys[1]] = {"shape": [m, k, n], "ms": round(t, 5), "tops": round(fl / t / 1e9, 2),
+                        "frac_mfma": round(fl / t / 1e9 / PEAK_TFLOPS["int8"], 4)}
     return out
 
 
