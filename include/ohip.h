@@ -293,6 +293,10 @@ typedef struct {
      * to quantised bytes, e.g. DequantizeLinear -> Silu -> QuantizeLinear
      * (indexing/quantize.rs:96-190, registry/nn_ops/activations.rs:477). */
     const uint8_t* out_table;
+    /* NHWC input only: channel slots between consecutive pixels (a multiple
+     * of 16, at least c rounded up to 16); 0 means c rounded up to 16.  A
+     * larger pitch reads a channel range of a wider NHWC tensor in place. */
+    int64_t in_pitch;
 } ohip_qconv_desc;
 int ohip_qconv2d(ohip_ctx* ctx, const ohip_qconv_desc* d, const void* x, const ohip_weight* w,
                  const int32_t* bias_dev, void* y);
@@ -301,18 +305,28 @@ int ohip_qconv2d(ohip_ctx* ctx, const ohip_qconv_desc* d, const void* x, const o
 /* A run-scoped device activation (HipDeviceTensor; the DeviceActivation
  * contract of src/session/gpu_activations.rs:117-189 and
  * oxionnx-cuda/src/activation.rs).  Layout NCHW means plain row-major in the
- * ONNX shape; NHWC means channels-last with the channel axis padded to a
- * multiple of 16 bytes (the conv kernels' native layout). */
+ * ONNX shape; NHWC means channels-last (the conv kernels' native layout)
+ * with a pixel pitch of at least the channel count: the channel count
+ * padded to 16 bytes for an allocated tensor, the source's pitch for a
+ * channel range of another NHWC tensor.  The shape is always the ONNX
+ * (N, C, H, W) shape. */
 typedef struct ohip_dtensor ohip_dtensor;
 int ohip_dtensor_alloc(ohip_ctx* ctx, int dtype, int rank, const int64_t* shape, int layout, ohip_dtensor** out);
 /* Take ownership of a device buffer of the context (NCHW layout). */
 int ohip_dtensor_wrap(ohip_ctx* ctx, void* dptr, int dtype, int rank, const int64_t* shape, ohip_dtensor** out);
 int ohip_dtensor_upload(ohip_ctx* ctx, ohip_dtensor* t, const void* host);      /* NCHW only */
-int ohip_dtensor_download(ohip_ctx* ctx, const ohip_dtensor* t, void* host);    /* NCHW only, synchronous */
+int ohip_dtensor_download(ohip_ctx* ctx, const ohip_dtensor* t, void* host);    /* NCHW bytes, synchronous */
 void* ohip_dtensor_ptr(const ohip_dtensor* t);
 int ohip_dtensor_layout(const ohip_dtensor* t);
 int ohip_dtensor_info(const ohip_dtensor* t, int* dtype, int* rank, int64_t* shape8, size_t* bytes);
 void ohip_dtensor_free(ohip_dtensor* t);
+/* The NCHW form of a resident tensor as a new tensor, enqueued on the
+ * context's stream (an NCHW tensor is shared, not copied).  No counterpart in
+ * the reference, whose device activations always hold the ONNX layout: this
+ * provider keeps convolution outputs NHWC between convolutions, and a
+ * session converts its graph outputs with this call inside the forward (so
+ * a captured forward includes the conversion). */
+int ohip_dtensor_to_nchw(ohip_ctx* ctx, const ohip_dtensor* t, ohip_dtensor** out);
 
 /* ------------------------------------------------------------------ node dispatch */
 /* The drop-in boundary for the session's per-node provider chain

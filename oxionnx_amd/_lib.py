@@ -88,7 +88,7 @@ class QConvDesc(ctypes.Structure):
                [("x_dtype", ctypes.c_int), ("x_zp", ctypes.c_int32), ("out_kind", ctypes.c_int),
                 ("x_scale", ctypes.c_float), ("y_scale", ctypes.c_float), ("y_zp", ctypes.c_int32),
                 ("lo", ctypes.c_int32), ("hi", ctypes.c_int32), ("in_layout", ctypes.c_int),
-                ("out_layout", ctypes.c_int), ("out_table", VP)]
+                ("out_layout", ctypes.c_int), ("out_table", VP), ("in_pitch", I64)]
 
 
 class Attr(ctypes.Structure):
@@ -180,6 +180,7 @@ SIGNATURES = {
     "ohip_dtensor_download": (ctypes.c_int, [VP, VP, VP]),
     "ohip_dtensor_ptr": (VP, [VP]),
     "ohip_dtensor_layout": (ctypes.c_int, [VP]),
+    "ohip_dtensor_to_nchw": (ctypes.c_int, [VP, VP, ctypes.POINTER(VP)]),
     "ohip_dtensor_info": (ctypes.c_int, [VP, ctypes.POINTER(ctypes.c_int), ctypes.POINTER(ctypes.c_int),
                                          ctypes.POINTER(I64), ctypes.POINTER(ctypes.c_size_t)]),
     "ohip_dtensor_free": (None, [VP]),

@@ -346,6 +346,47 @@ static hipError_t nchw_to_nhwc_t(const void* src, void* dst, int N, int C, int H
   return hipGetLastError();
 }
 
+// The inverse: NHWC with a pixel pitch back to NCHW, through a 32 x 32 LDS
+// tile (pixels x channels).
+template <class T>
+__global__ void nhwc_to_nchw_kernel(const T* __restrict__ src, T* __restrict__ dst, int C, int HW, int pitch) {
+  __shared__ T tile[32][33];
+  const int n = blockIdx.z;
+  const int c0 = blockIdx.y * 32, s0 = blockIdx.x * 32;
+  const T* s = src + (int64_t)n * HW * pitch;
+  T* d = dst + (int64_t)n * C * HW;
+  for (int r = threadIdx.y; r < 32; r += blockDim.y) {
+    const int sp = s0 + r, c = c0 + threadIdx.x;
+    tile[r][threadIdx.x] = (sp < HW && c < C) ? s[(int64_t)sp * pitch + c] : T(0);
+  }
+  __syncthreads();
+  for (int r = threadIdx.y; r < 32; r += blockDim.y) {
+    const int c = c0 + r, sp = s0 + threadIdx.x;
+    if (c < C && sp < HW) d[(int64_t)c * HW + sp] = tile[threadIdx.x][r];
+  }
+}
+
+hipError_t run_nhwc_to_nchw(int elem_bytes, const void* src, void* dst, int N, int C, int HW, int pitch,
+                            hipStream_t st) {
+  if (N <= 0 || C <= 0 || HW <= 0) return hipSuccess;
+  dim3 grid((HW + 31) / 32, (C + 31) / 32, N), block(32, 8);
+  switch (elem_bytes) {
+    case 1:
+      hipLaunchKernelGGL(nhwc_to_nchw_kernel<uint8_t>, grid, block, 0, st, (const uint8_t*)src, (uint8_t*)dst, C, HW, pitch);
+      break;
+    case 2:
+      hipLaunchKernelGGL(nhwc_to_nchw_kernel<uint16_t>, grid, block, 0, st, (const uint16_t*)src, (uint16_t*)dst, C, HW,
+                         pitch);
+      break;
+    case 4:
+      hipLaunchKernelGGL(nhwc_to_nchw_kernel<uint32_t>, grid, block, 0, st, (const uint32_t*)src, (uint32_t*)dst, C, HW,
+                         pitch);
+      break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
 hipError_t run_nchw_to_nhwc(int elem_bytes, const void* src, void* dst, int N, int C, int HW, int cp,
                             hipStream_t st) {
   hipError_t e = hipErrorNotSupported;

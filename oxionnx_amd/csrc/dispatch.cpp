@@ -22,6 +22,10 @@ int ohip_dtensor_view_internal(const ohip_dtensor* src, int rank, const int64_t*
                                ohip_dtensor** out);
 int ohip_const_operand_internal(ohip_ctx* ctx, const char* name, const char* label, int dtype, const void* host,
                                 size_t bytes, const void** dev);
+int ohip_dtensor_set_nhwc_internal(ohip_dtensor* t, int64_t pitch);
+int64_t ohip_dtensor_pitch_internal(const ohip_dtensor* t);
+int ohip_dtensor_view_nhwc_internal(const ohip_dtensor* src, int64_t c0, int64_t cn, ohip_dtensor** out);
+int ohip_dtensor_to_nchw_internal(ohip_ctx* ctx, const ohip_dtensor* t, void* dst);
 int ohip_hip_error_internal(hipError_t e, const char* what);
 
 namespace {
@@ -241,6 +245,16 @@ struct Stage {
     return d;
   }
 };
+
+// OHIP_NHWC=0 keeps every resident convolution output NCHW (a measurement
+// switch)
+bool nhwc_residency() {
+  static const bool v = [] {
+    const char* e = std::getenv("OHIP_NHWC");
+    return !(e && e[0] == '0');
+  }();
+  return v;
+}
 
 void set_out(ohip_output* o, int dtype, const std::vector<int64_t>& shape) {
   std::memset(o, 0, sizeof(*o));
@@ -748,7 +762,9 @@ int do_qconv(ohip_ctx* ctx, const ohip_node* nd, bool qlinear, int placement, oh
   const ohip_tensor* bias = qlinear ? input(nd, 8) : nullptr;
   if (!x || !w || !host_only(w)) return decline("integer Conv: the filter must be a host tensor");
   if (x->device && (x->dtype != OHIP_U8 && x->dtype != OHIP_I8)) return decline("integer Conv: resident X must be bytes");
-  if (x->device && ohip_dtensor_layout(x->device) != OHIP_NCHW) return decline("integer Conv: resident input layout");
+  const bool x_nhwc = x->device && ohip_dtensor_layout(x->device) == OHIP_NHWC;
+  if (x->device && !x_nhwc && ohip_dtensor_layout(x->device) != OHIP_NCHW)
+    return decline("integer Conv: resident input layout");
   Geo g;
   std::string why;
   if (!conv_geometry(nd, x, w, &g, &why)) return decline(why);
@@ -822,16 +838,24 @@ int do_qconv(ohip_ctx* ctx, const ohip_node* nd, bool qlinear, int placement, oh
   const void* bd = bias ? st.cached(bias, "QLinearConv.B", OHIP_I32, bias_i.data(), bias_i.size() * 4) : nullptr;
   const size_t ob = (out_kind == OHIP_QOUT_U8 || out_kind == OHIP_QOUT_I8) ? 1 : 4;
   const size_t obytes = (size_t)(g.n * g.cout * g.oh * g.ow) * ob;
+  // A resident byte output stays NHWC (the next convolution's staging
+  // layout) when its channels fill whole 16-byte chunks; the dispatcher
+  // converts it for consumers that need NCHW.
+  const bool y_nhwc = placement == OHIP_PLACE_DEVICE && ob == 1 && g.group == 1 && !g.rank1 && g.cout % 16 == 0 &&
+                      nhwc_residency();
   void* yd = st.alloc(obytes);
   if (!xd || !yd || (bias && !bd)) { if (!cache) ohip_weight_release(wt); return OHIP_E_NOMEM; }
   ohip_qconv_desc d{g.n, g.c, g.h, g.w, g.cout, g.kh, g.kw, g.group, g.sh, g.sw, g.dh, g.dw, g.pt, g.pl, g.pb, g.pr,
                     xdt, xzp[0], out_kind, xs, ys, qlinear ? yzp[0] : 0, lo, hi,
-                    OHIP_NCHW, OHIP_NCHW, fused ? table : nullptr};
+                    x_nhwc ? OHIP_NHWC : OHIP_NCHW, y_nhwc ? OHIP_NHWC : OHIP_NCHW, fused ? table : nullptr,
+                    x_nhwc ? ohip_dtensor_pitch_internal(x->device) : 0};
   rc = ohip_qconv2d(ctx, &d, xd, wt, static_cast<const int32_t*>(bd), yd);
   if (!cache) ohip_weight_release(wt);
   if (rc) return rc;
   set_out(out, out_dt, conv_out_shape(g));
-  return finish_output(ctx, st, placement, out, yd, obytes, out_dt);
+  rc = finish_output(ctx, st, placement, out, yd, obytes, out_dt);
+  if (rc == OHIP_OK && y_nhwc) rc = ohip_dtensor_set_nhwc_internal(out->device, g.cout);
+  return rc;
 }
 
 // ================================================================== memory-bound nodes
@@ -1173,6 +1197,12 @@ int do_maxpool(ohip_ctx* ctx, const ohip_node* nd, int placement, ohip_output* o
   const int dt = x->device ? x->dtype : OHIP_F32;
   ohip::PoolPlan p{(int)ih, (int)iw, (int)oh, (int)ow, (int)ks[0], (int)ks[1], (int)strides[0], (int)strides[1],
                    (int)pads[0], (int)pads[1], (int)dil[0], (int)dil[1]};
+  // a resident NHWC input is pooled in place; the output is compact NHWC
+  const bool nhwc = x->device && ohip_dtensor_layout(x->device) == OHIP_NHWC;
+  if (nhwc) {
+    p.nhwc_c = (int)x->shape[1];
+    p.pitch = ohip_dtensor_pitch_internal(x->device);
+  }
   Stage st(ctx);
   const void* xd = st.operand(x);
   const int64_t planes = x->shape[0] * x->shape[1];
@@ -1181,7 +1211,9 @@ int do_maxpool(ohip_ctx* ctx, const ohip_node* nd, int placement, ohip_output* o
   if (!xd || !yd) return OHIP_E_NOMEM;
   hipError_t e = ohip::run_maxpool(dt, xd, yd, planes, p, (hipStream_t)ohip_ctx_stream(ctx));
   if (e != hipSuccess) return e == hipErrorInvalidValue ? decline("MaxPool: dtype") : ohip_hip_error_internal(e, "MaxPool launch");
-  return output_device(ctx, st, placement, out, dt, {x->shape[0], x->shape[1], oh, ow}, yd, bytes);
+  int rc = output_device(ctx, st, placement, out, dt, {x->shape[0], x->shape[1], oh, ow}, yd, bytes);
+  if (rc == OHIP_OK && nhwc && out->device) rc = ohip_dtensor_set_nhwc_internal(out->device, x->shape[1]);
+  return rc;
 }
 
 // ---------------------------------------------------------------- Concat (device copy kernels)
@@ -1214,6 +1246,18 @@ int do_concat(ohip_ctx* ctx, const ohip_node* nd, int placement, ohip_output* ou
     if (!t->device && dt != OHIP_F32) return decline("Concat: host operand beside byte tensors");
     oshape[(size_t)axis] += t->shape[axis];
   }
+  // every input resident NHWC, channel axis (the dispatcher converts any
+  // other mix first): rows are pixels, each input adds its channels with its
+  // own pixel pitch, the output is compact NHWC
+  bool nhwc = rank == 4 && axis == 1;
+  for (int i = 0; i < nd->n_inputs && nhwc; ++i) {
+    const ohip_tensor* t = input(nd, i);
+    nhwc = t->device && ohip_dtensor_layout(t->device) == OHIP_NHWC;
+  }
+  if (nhwc) {
+    outer = t0->shape[0] * t0->shape[2] * t0->shape[3];
+    inner = 1;
+  }
   Stage st(ctx);
   const size_t row = (size_t)(oshape[(size_t)axis] * inner * eb);
   const size_t bytes = (size_t)outer * row;
@@ -1236,7 +1280,7 @@ int do_concat(ohip_ctx* ctx, const ohip_node* nd, int placement, ohip_output* ou
     } else {
       for (int k = 0; k < p.n; ++k)
         if (p.w[k] && outer &&
-            ohip::run_copy2d(p.src[k], p.w[k], static_cast<char*>(p.dst) + p.off[k], (int64_t)row, p.w[k], outer, s) !=
+            ohip::run_copy2d(p.src[k], p.sp[k], static_cast<char*>(p.dst) + p.off[k], (int64_t)row, p.w[k], outer, s) !=
                 hipSuccess)
           return ohip_hip_error_internal(hipGetLastError(), "Concat copy");
     }
@@ -1255,6 +1299,7 @@ int do_concat(ohip_ctx* ctx, const ohip_node* nd, int placement, ohip_output* ou
     }
     p.src[p.n] = td;
     p.w[p.n] = (int64_t)w;
+    p.sp[p.n] = nhwc ? ohip_dtensor_pitch_internal(t->device) * eb : (int64_t)w;
     p.off[p.n] = (int64_t)(off - group_off);
     ++p.n;
     off += w;
@@ -1263,7 +1308,9 @@ int do_concat(ohip_ctx* ctx, const ohip_node* nd, int placement, ohip_output* ou
     int rc = flush();
     if (rc) return rc;
   }
-  return output_device(ctx, st, placement, out, dt, oshape, yd, bytes);
+  int rc = output_device(ctx, st, placement, out, dt, oshape, yd, bytes);
+  if (rc == OHIP_OK && nhwc && out->device) rc = ohip_dtensor_set_nhwc_internal(out->device, oshape[1]);
+  return rc;
 }
 
 // ---------------------------------------------------------------- Slice (positive steps)
@@ -1314,11 +1361,35 @@ int do_slice(ohip_ctx* ctx, const ohip_node* nd, int placement, ohip_output* out
   for (auto v : oshape) n *= v;
   const int dt = x->device ? x->dtype : OHIP_F32;
   const int eb = ebytes(dt);
+  // A resident NHWC input: a whole-chunk channel range (unit step, every
+  // other axis whole) is a view with the input's pixel pitch; anything else
+  // reads the input's NCHW form.
+  Stage st(ctx);
+  const void* xnchw = nullptr;
+  if (x->device && ohip_dtensor_layout(x->device) == OHIP_NHWC) {
+    bool chan_only = x->rank == 4 && (p.step[1] == 1 || p.out[1] <= 1);
+    for (int d = 0; d < x->rank && chan_only; ++d)
+      if (d != 1 && p.out[d] != x->shape[d]) chan_only = false;
+    if (chan_only && placement == OHIP_PLACE_DEVICE && (p.start[1] * eb) % 16 == 0 && (p.out[1] * eb) % 16 == 0 &&
+        p.out[1] > 0) {
+      ohip_dtensor* t = nullptr;
+      int rc = ohip_dtensor_view_nhwc_internal(x->device, p.start[1], p.out[1], &t);
+      if (rc) return rc;
+      set_out(out, dt, oshape);
+      out->device = t;
+      return OHIP_OK;
+    }
+    void* c = st.alloc((size_t)std::max<int64_t>(numel(x) * eb, 16));
+    if (!c) return OHIP_E_NOMEM;
+    int rc = ohip_dtensor_to_nchw_internal(ctx, x->device, c);
+    if (rc) return rc;
+    xnchw = c;
+  }
   // A resident input whose slice is one contiguous run (every axis before the
   // first sliced one has extent 1 in the output, the axes after it are whole,
   // unit step) becomes a view of the input's buffer: no copy, no launch.  The
   // view starts on a 16-byte boundary, as every freshly allocated tensor does.
-  if (x->device && placement == OHIP_PLACE_DEVICE && ohip_dtensor_layout(x->device) == OHIP_NCHW && n > 0) {
+  if (!xnchw && x->device && placement == OHIP_PLACE_DEVICE && ohip_dtensor_layout(x->device) == OHIP_NCHW && n > 0) {
     int k = 0;
     while (k < x->rank && p.out[k] == x->shape[k]) ++k;   // first sliced axis
     bool contiguous = true;
@@ -1340,8 +1411,7 @@ int do_slice(ohip_ctx* ctx, const ohip_node* nd, int placement, ohip_output* out
       return OHIP_OK;
     }
   }
-  Stage st(ctx);
-  const void* xd = st.operand(x);
+  const void* xd = xnchw ? xnchw : st.operand(x);
   const size_t bytes = (size_t)n * eb;
   void* yd = st.alloc(bytes);
   if (!xd || !yd) return OHIP_E_NOMEM;
@@ -1525,7 +1595,22 @@ int do_qadd(ohip_ctx* ctx, const ohip_node* nd, int placement, ohip_output* out)
     n *= e;
     oshape[(size_t)(rank - 1 - d)] = e;
   }
-  const bool same = numel(a) == n && numel(b) == n;
+  bool same = numel(a) == n && numel(b) == n;
+  // both operands resident NHWC of one shape (the dispatcher converts any
+  // other NHWC operand first): pixels x channels with each operand's pitch,
+  // the output compact NHWC
+  const bool nhwc = a->device && b->device && ohip_dtensor_layout(a->device) == OHIP_NHWC &&
+                    ohip_dtensor_layout(b->device) == OHIP_NHWC;
+  if (nhwc) {
+    p = ohip::BcastPlan{};
+    p.rank = 2;
+    p.shape[ohip::kMaxRank - 2] = a->shape[0] * a->shape[2] * a->shape[3];
+    p.shape[ohip::kMaxRank - 1] = a->shape[1];
+    p.sa[ohip::kMaxRank - 2] = ohip_dtensor_pitch_internal(a->device);
+    p.sb[ohip::kMaxRank - 2] = ohip_dtensor_pitch_internal(b->device);
+    p.sa[ohip::kMaxRank - 1] = p.sb[ohip::kMaxRank - 1] = 1;
+    same = p.sa[ohip::kMaxRank - 2] == a->shape[1] && p.sb[ohip::kMaxRank - 2] == a->shape[1];
+  }
   Stage st(ctx);
   std::vector<uint8_t> ab, bb;
   auto bytes_of = [&](const ohip_tensor* t, std::vector<uint8_t>& hb, int* dt) -> const void* {
@@ -1548,7 +1633,9 @@ int do_qadd(ohip_ctx* ctx, const ohip_node* nd, int placement, ohip_output* out)
   hipError_t e = ohip::run_qadd(static_cast<const uint8_t*>(ad), static_cast<const uint8_t*>(bd),
                                 static_cast<uint8_t*>(yd), n, p, same, q, (hipStream_t)ohip_ctx_stream(ctx));
   if (e != hipSuccess) return ohip_hip_error_internal(e, "node kernel launch");
-  return output_device(ctx, st, placement, out, u8 ? OHIP_U8 : OHIP_I8, oshape, yd, (size_t)n);
+  int rc = output_device(ctx, st, placement, out, u8 ? OHIP_U8 : OHIP_I8, oshape, yd, (size_t)n);
+  if (rc == OHIP_OK && nhwc && out->device) rc = ohip_dtensor_set_nhwc_internal(out->device, a->shape[1]);
+  return rc;
 }
 
 }  // namespace
@@ -1587,15 +1674,84 @@ extern "C" int ohip_accepts_resident_slot(const char* op, int index) {
   return 0;
 }
 
+namespace {
+
+int dispatch_node(ohip_ctx* ctx, const ohip_node* node, int placement, ohip_output* out);
+
+// Whether a node reads resident NHWC operand i in place (device placement
+// only): QLinearConv's X (group 1), QLinearAdd's operands when both are NHWC
+// of one shape, Concat along channels when every input is NHWC, MaxPool, and
+// Slice (a channel range is a view; anything else converts inside do_slice).
+bool takes_nhwc(const ohip_node* nd, int i, int placement) {
+  if (placement != OHIP_PLACE_DEVICE) return false;   // host results are the NCHW lanes
+  auto nhwc = [&](int k) {
+    return k < nd->n_inputs && nd->inputs[k].device && ohip_dtensor_layout(nd->inputs[k].device) == OHIP_NHWC;
+  };
+  const std::string op(nd->op_type);
+  if (op == "QLinearConv") return i == 0 && attr_i(nd, "group", 1) == 1;
+  if (op == "Slice" || op == "MaxPool") return i == 0;
+  if (op == "QLinearAdd") {
+    if ((i != 0 && i != 3) || !nhwc(0) || !nhwc(3)) return false;
+    const ohip_tensor &a = nd->inputs[0], &b = nd->inputs[3];
+    if (a.rank != 4 || b.rank != 4) return false;
+    for (int d = 0; d < 4; ++d) if (a.shape[d] != b.shape[d]) return false;
+    return true;
+  }
+  if (op == "Concat") {
+    if (nd->n_inputs < 1 || nd->inputs[0].rank != 4) return false;
+    int64_t axis = attr_i(nd, "axis", 0);
+    if (axis < 0) axis += 4;
+    if (axis != 1) return false;
+    for (int k = 0; k < nd->n_inputs; ++k) if (!nhwc(k)) return false;
+    return true;
+  }
+  return false;
+}
+
+}  // namespace
+
+// Resident NHWC operands that the node does not read in place are converted
+// to NCHW first (into pool buffers released after the node is enqueued); the
+// node then sees the layout of the reference's tensors.
 extern "C" int ohip_try_dispatch(ohip_ctx* ctx, const ohip_node* node, int placement, ohip_output* out) {
   if (!ctx || !node || !node->op_type || !out) return OHIP_E_INVALID;
   std::memset(out, 0, sizeof(*out));
-  const std::string op(node->op_type);
   for (int i = 0; i < node->n_inputs; ++i) {
     const ohip_tensor& t = node->inputs[i];
     if (t.device && !ohip_accepts_resident_slot(node->op_type, i))
       return decline("resident operand in a host-read slot");
   }
+  std::vector<ohip_tensor> ins;
+  std::vector<ohip_dtensor*> temps;
+  for (int i = 0; i < node->n_inputs; ++i) {
+    const ohip_tensor& t = node->inputs[i];
+    if (!t.device || ohip_dtensor_layout(t.device) != OHIP_NHWC || takes_nhwc(node, i, placement)) continue;
+    if (ins.empty()) ins.assign(node->inputs, node->inputs + node->n_inputs);
+    const int64_t n = numel(&t);
+    void* p = nullptr;
+    int rc = ohip_malloc(ctx, (size_t)std::max<int64_t>(n * ebytes(t.dtype), 16), &p);
+    if (rc == OHIP_OK) rc = ohip_dtensor_to_nchw_internal(ctx, t.device, p);
+    ohip_dtensor* c = nullptr;
+    if (rc == OHIP_OK) rc = ohip_dtensor_wrap(ctx, p, t.dtype, t.rank, t.shape, &c);
+    if (rc) {
+      if (p && !c) ohip_free(ctx, p);
+      for (auto* x : temps) ohip_dtensor_free(x);
+      return rc;
+    }
+    temps.push_back(c);
+    ins[(size_t)i].device = c;
+  }
+  ohip_node local = *node;
+  if (!ins.empty()) local.inputs = ins.data();
+  const int rc = dispatch_node(ctx, &local, placement, out);
+  for (auto* x : temps) ohip_dtensor_free(x);
+  return rc;
+}
+
+namespace {
+
+int dispatch_node(ohip_ctx* ctx, const ohip_node* node, int placement, ohip_output* out) {
+  const std::string op(node->op_type);
   int rc;
   if (op == "Conv") rc = do_conv(ctx, node, placement, out);
   else if (op == "ConvTranspose") rc = do_conv_transpose(ctx, node, placement, out);
@@ -1631,6 +1787,8 @@ extern "C" int ohip_try_dispatch(ohip_ctx* ctx, const ohip_node* node, int place
   if (rc == OHIP_DECLINED) ohip_note_declined(ctx, t_err.c_str());
   return rc;
 }
+
+}  // namespace
 
 extern "C" void ohip_output_free(ohip_output* o) {
   if (!o) return;

@@ -170,6 +170,9 @@ hipError_t run_conv_transpose(int dtype, const void* x, const void* w, const voi
 // reflect (1) / edge (2) spatial border; see stage_nhwc_kernel.
 hipError_t run_stage_nhwc(int elem_bytes, const void* src, void* dst, int N, int C, int H, int W, int pt, int pl,
                           int pb, int pr, int mode, int cg, int cpg, int groups, hipStream_t st);
+// NHWC [N][HW][pitch] (first C slots meaningful) -> NCHW [N][C][HW]
+hipError_t run_nhwc_to_nchw(int elem_bytes, const void* src, void* dst, int N, int C, int HW, int pitch,
+                            hipStream_t st);
 hipError_t run_nchw_to_nhwc(int elem_bytes, const void* src, void* dst, int N, int C, int HW, int cp,
                             hipStream_t st);
 hipError_t run_nchw_to_nhwc_pad(int elem_bytes, const void* src, void* dst, int N, int C, int H, int W, int cp,
@@ -218,6 +221,8 @@ struct PadPlan {
 
 struct PoolPlan {
   int ih, iw, oh, ow, kh, kw, sh, sw, pt, pl, dh, dw;
+  int nhwc_c = 0;       // > 0: NHWC input of this many channels (output compact NHWC)
+  int64_t pitch = 0;    // NHWC input: element slots between pixels
 };
 
 struct SlicePlan {
@@ -254,6 +259,7 @@ struct ConcatPlan {
   const void* src[kConcatMax];
   int64_t w[kConcatMax];     // row width of each input
   int64_t off[kConcatMax];   // where that input's part of an output row starts
+  int64_t sp[kConcatMax];    // that input's row pitch (its width, or an NHWC pixel pitch)
   int n;
   void* dst;
 };

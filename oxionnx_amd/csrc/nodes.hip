@@ -282,6 +282,36 @@ __global__ void __launch_bounds__(kThreads) maxpool_kernel(const T* __restrict__
   }
 }
 
+// The same pool over an NHWC input with a pixel pitch: output element
+// (n, oy, ox, c), compact NHWC, with the NCHW kernel's comparisons.
+template <class T>
+__global__ void __launch_bounds__(kThreads) maxpool_nhwc_kernel(const T* __restrict__ x, T* __restrict__ y,
+                                                                int64_t images, PoolPlan p) {
+  const int C = p.nhwc_c;
+  const int64_t n = images * p.oh * p.ow * C;
+  for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n; i += (int64_t)gridDim.x * kThreads) {
+    const int c = (int)(i % C);
+    int64_t t = i / C;
+    const int ox = (int)(t % p.ow);
+    t /= p.ow;
+    const int oy = (int)(t % p.oh);
+    const int64_t img = t / p.oh;
+    const T* xp = x + img * p.ih * p.iw * p.pitch + c;
+    float best = -INFINITY;
+    for (int ky = 0; ky < p.kh; ++ky) {
+      const int iy = oy * p.sh - p.pt + ky * p.dh;
+      if (iy < 0 || iy >= p.ih) continue;
+      for (int kx = 0; kx < p.kw; ++kx) {
+        const int ix = ox * p.sw - p.pl + kx * p.dw;
+        if (ix < 0 || ix >= p.iw) continue;
+        const float v = (float)xp[((int64_t)iy * p.iw + ix) * p.pitch];
+        if (v > best) best = v;
+      }
+    }
+    y[i] = (T)best;
+  }
+}
+
 // ---------------------------------------------------------------- strided slice (rank <= 6)
 template <class T>
 __global__ void __launch_bounds__(kThreads) slice_kernel(const T* __restrict__ x, T* __restrict__ y, int64_t n, SlicePlan p) {
@@ -379,7 +409,7 @@ __global__ void __launch_bounds__(kThreads) concat_rows_kernel(ConcatPlan p, int
     int k = 0;
 #pragma unroll
     for (int j = 1; j < kConcatMax; ++j) k += (j < p.n && c >= p.off[j]) ? 1 : 0;
-    reinterpret_cast<T*>(p.dst)[i] = reinterpret_cast<const T*>(p.src[k])[r * p.w[k] + (c - p.off[k])];
+    reinterpret_cast<T*>(p.dst)[i] = reinterpret_cast<const T*>(p.src[k])[r * p.sp[k] + (c - p.off[k])];
   }
 }
 
@@ -489,6 +519,17 @@ hipError_t run_maxpool(int dt, const void* x, void* y, int64_t planes, const Poo
   const int64_t n = planes * p.oh * p.ow;
   if (n <= 0) return hipSuccess;
   const dim3 g(grid_for(n));
+  if (p.nhwc_c > 0) {
+    const int64_t images = planes / p.nhwc_c;
+    switch (dt) {
+      case DT_U8: hipLaunchKernelGGL(maxpool_nhwc_kernel<uint8_t>, g, dim3(kThreads), 0, st, (const uint8_t*)x, (uint8_t*)y, images, p); break;
+      case DT_I8: hipLaunchKernelGGL(maxpool_nhwc_kernel<int8_t>, g, dim3(kThreads), 0, st, (const int8_t*)x, (int8_t*)y, images, p); break;
+      case DT_F16: hipLaunchKernelGGL(maxpool_nhwc_kernel<_Float16>, g, dim3(kThreads), 0, st, (const _Float16*)x, (_Float16*)y, images, p); break;
+      case DT_F32: hipLaunchKernelGGL(maxpool_nhwc_kernel<float>, g, dim3(kThreads), 0, st, (const float*)x, (float*)y, images, p); break;
+      default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+  }
   switch (dt) {
     case DT_F32: hipLaunchKernelGGL(maxpool_kernel<float>, g, dim3(kThreads), 0, st, (const float*)x, (float*)y, planes, p); break;
     case DT_F16: hipLaunchKernelGGL(maxpool_kernel<_Float16>, g, dim3(kThreads), 0, st, (const _Float16*)x, (_Float16*)y, planes, p); break;
@@ -559,11 +600,11 @@ hipError_t run_concat_rows(ConcatPlan p, int64_t row, int64_t rows, hipStream_t 
   auto fits = [&](int u) {
     if ((uintptr_t)p.dst % u || row % u) return false;
     for (int k = 0; k < p.n; ++k)
-      if ((uintptr_t)p.src[k] % u || p.w[k] % u) return false;
+      if ((uintptr_t)p.src[k] % u || p.w[k] % u || p.sp[k] % u) return false;
     return true;
   };
   const int u = fits(16) ? 16 : fits(4) ? 4 : 1;
-  for (int k = 0; k < p.n; ++k) { p.w[k] /= u; p.off[k] /= u; }
+  for (int k = 0; k < p.n; ++k) { p.w[k] /= u; p.off[k] /= u; p.sp[k] /= u; }
   const int64_t ru = row / u, n = ru * rows;
   if (u == 16) hipLaunchKernelGGL(concat_rows_kernel<uint4>, dim3(grid_for(n)), dim3(kThreads), 0, st, p, ru, rows);
   else if (u == 4) hipLaunchKernelGGL(concat_rows_kernel<uint32_t>, dim3(grid_for(n)), dim3(kThreads), 0, st, p, ru, rows);

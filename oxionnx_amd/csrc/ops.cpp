@@ -137,6 +137,7 @@ struct ohip_dtensor {
   int64_t shape[8] = {0};
   int layout = OHIP_NCHW;
   size_t bytes = 0;
+  int64_t pitch = 0;   // NHWC: element slots between consecutive pixels (>= shape[1])
 };
 
 static int activate(ohip_ctx* ctx) {
@@ -1483,6 +1484,11 @@ extern "C" int ohip_qconv2d(ohip_ctx* ctx, const ohip_qconv_desc* d, const void*
   if (rc) return rc;
   const int64_t cp = round_up(cg, 16);   // channel slots per group and tap
   const int64_t cpt = G * cp;            // channel slots per staged pixel
+  // pixel stride of an NHWC input: its own pitch (a channel range of a wider
+  // tensor read in place), else the padded channel count
+  const int64_t in_pstride = d->in_layout == OHIP_NHWC && d->in_pitch > 0 ? d->in_pitch : cpt;
+  if (d->in_layout == OHIP_NHWC && d->in_pitch > 0 && (G > 1 || d->in_pitch % 16 || d->in_pitch < cp))
+    return fail(OHIP_E_INVALID, "ohip_qconv2d: in_pitch must be a multiple of 16 covering the channels, group 1");
   const int64_t rows = d->n * g.oh * g.ow;
   if (rows > INT_MAX / 2) return fail(OHIP_DECLINED, "ohip_qconv2d: extent too large");
   if (rows == 0) return OHIP_OK;
@@ -1558,7 +1564,7 @@ extern "C" int ohip_qconv2d(ohip_ctx* ctx, const ohip_qconv_desc* d, const void*
     Im2colOperand col{};
     col.base = static_cast<const char*>(xin) + gi * cp;
     col.H = (int)d->h; col.W = (int)d->w; col.OH = (int)g.oh; col.OW = (int)g.ow;
-    col.KW = (int)d->kw; col.cpc = (int)(cp / 16); col.pstride = (int)(cpt / 16);
+    col.KW = (int)d->kw; col.cpc = (int)(cp / 16); col.pstride = (int)((stage ? cpt : in_pstride) / 16);
     col.sh = (int)d->stride_h; col.sw = (int)d->stride_w; col.dh = (int)d->dil_h; col.dw = (int)d->dil_w;
     col.pt = (int)d->pad_t; col.pl = (int)d->pad_l; col.rows = (int)rows;
     col.kc = w->kwrap > 0 ? w->kreal : w->kc; col.kwrap = w->kwrap;
@@ -1707,6 +1713,52 @@ int ohip_dtensor_view_internal(const ohip_dtensor* src, int rank, const int64_t*
   return OHIP_OK;
 }
 
+// NHWC resident tensors: a produced one is marked with its pixel pitch; a
+// channel range of one is a view with the same pitch; the pitch is read by
+// the consumers that take NHWC in place, and the conversion to NCHW serves
+// the rest.
+int ohip_dtensor_set_nhwc_internal(ohip_dtensor* t, int64_t pitch) {
+  if (!t || t->rank != 4 || pitch < t->shape[1]) return fail(OHIP_E_INVALID, "dtensor: NHWC pitch");
+  t->layout = OHIP_NHWC;
+  t->pitch = pitch;
+  return OHIP_OK;
+}
+int64_t ohip_dtensor_pitch_internal(const ohip_dtensor* t) { return t && t->layout == OHIP_NHWC ? t->pitch : 0; }
+int ohip_dtensor_view_nhwc_internal(const ohip_dtensor* src, int64_t c0, int64_t cn, ohip_dtensor** out) {
+  if (!src || !out || src->layout != OHIP_NHWC || c0 < 0 || cn < 0 || c0 + cn > src->shape[1])
+    return fail(OHIP_E_INVALID, "dtensor_view: NHWC channel range");
+  auto* t = new ohip_dtensor(*src);
+  t->ptr = static_cast<char*>(src->ptr) + c0 * elem_bytes(src->dtype);
+  t->shape[1] = cn;
+  *out = t;
+  return OHIP_OK;
+}
+// Writes the NCHW form of an NHWC tensor into dst (shape-product elements).
+int ohip_dtensor_to_nchw_internal(ohip_ctx* ctx, const ohip_dtensor* t, void* dst) {
+  if (!t || t->layout != OHIP_NHWC || !dst) return fail(OHIP_E_INVALID, "dtensor_to_nchw: not NHWC");
+  HIP_TRY(run_nhwc_to_nchw(elem_bytes(t->dtype), t->ptr, dst, (int)t->shape[0], (int)t->shape[1],
+                           (int)(t->shape[2] * t->shape[3]), (int)t->pitch, ctx->stream),
+          "NHWC -> NCHW");
+  return OHIP_OK;
+}
+
+extern "C" int ohip_dtensor_to_nchw(ohip_ctx* ctx, const ohip_dtensor* t, ohip_dtensor** out) {
+  if (!t || !out) return fail(OHIP_E_INVALID, "dtensor_to_nchw: null argument");
+  if (t->layout == OHIP_NCHW) return ohip_dtensor_alias_internal(t, t->rank, t->shape, out);
+  int rc = activate(ctx);
+  if (rc) return rc;
+  size_t nb = 0;
+  rc = dt_bytes(t->dtype, t->rank, t->shape, OHIP_NCHW, &nb);
+  if (rc) return rc;
+  void* p = nullptr;
+  rc = ohip_malloc(ctx, nb ? nb : 16, &p);
+  if (rc) return rc;
+  rc = ohip_dtensor_to_nchw_internal(ctx, t, p);
+  if (!rc) rc = ohip_dtensor_wrap(ctx, p, t->dtype, t->rank, t->shape, out);
+  if (rc) ohip_free(ctx, p);
+  return rc;
+}
+
 extern "C" int ohip_dtensor_upload(ohip_ctx* ctx, ohip_dtensor* t, const void* host) {
   if (!t || !host) return fail(OHIP_E_INVALID, "dtensor_upload: null argument");
   if (t->layout != OHIP_NCHW) return fail(OHIP_E_INVALID, "dtensor_upload: NCHW tensors only");
@@ -1714,6 +1766,21 @@ extern "C" int ohip_dtensor_upload(ohip_ctx* ctx, ohip_dtensor* t, const void* h
 }
 extern "C" int ohip_dtensor_download(ohip_ctx* ctx, const ohip_dtensor* t, void* host) {
   if (!t || !host) return fail(OHIP_E_INVALID, "dtensor_download: null argument");
+  if (t->layout == OHIP_NHWC) {
+    // the NCHW form through a temporary buffer
+    int rc = activate(ctx);
+    if (rc) return rc;
+    size_t nb = 0;
+    rc = dt_bytes(t->dtype, t->rank, t->shape, OHIP_NCHW, &nb);
+    if (rc) return rc;
+    void* tmp = nullptr;
+    rc = ohip_malloc(ctx, nb ? nb : 16, &tmp);
+    if (rc) return rc;
+    rc = ohip_dtensor_to_nchw_internal(ctx, t, tmp);
+    if (!rc) rc = ohip_memcpy_d2h(ctx, host, tmp, nb);
+    ohip_free(ctx, tmp);
+    return rc;
+  }
   if (t->layout != OHIP_NCHW) return fail(OHIP_E_INVALID, "dtensor_download: NCHW tensors only");
   return ohip_memcpy_d2h(ctx, host, t->ptr, t->bytes);
 }

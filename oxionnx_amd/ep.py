@@ -154,6 +154,15 @@ class DeviceTensor:
         L.check(L.lib().ohip_dtensor_upload(ctx.h, h, arr.ctypes.data_as(ctypes.c_void_p)))
         return cls(h, ctx)
 
+    def to_nchw(self, ctx):
+        """This tensor in NCHW layout: itself, or a converted copy (the
+        conversion is enqueued on the context's stream)."""
+        if L.lib().ohip_dtensor_layout(self.h) == L.NCHW:
+            return self
+        h = ctypes.c_void_p()
+        L.check(L.lib().ohip_dtensor_to_nchw(ctx.h, self.h, ctypes.byref(h)))
+        return DeviceTensor(h, ctx)
+
     def to_host(self, ctx):
         out = np.empty(self.shape, _OHIP2NP[self.dtype])
         L.check(L.lib().ohip_dtensor_download(ctx.h, self.h, out.ctypes.data_as(ctypes.c_void_p)))

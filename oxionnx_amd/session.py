@@ -384,6 +384,15 @@ class Session:
             for t in self.release[i]:
                 if t in acts and t not in keep:
                     acts.pop(t).free()
+        # graph outputs leave in the ONNX layout (resident convolution
+        # outputs are NHWC inside the forward)
+        for o in self.graph.outputs:
+            t = acts.get(o)
+            if t is not None and t not in keep:
+                c = t.to_nchw(self.ctx)
+                if c is not t:
+                    t.free()
+                    acts[o] = c
 
     def run(self, feeds: Dict[str, np.ndarray], keep_device: bool = False):
         acts = {}

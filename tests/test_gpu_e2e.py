@@ -249,6 +249,48 @@ def test_qlinear_add_fusion_bit_exact(ctx, case):
     np.testing.assert_array_equal(out["y"].astype(np.float32), ref["y"].astype(np.float32))
 
 
+def test_nhwc_resident_int8_chain_bit_exact(ctx):
+    """Resident QLinearConv outputs stay NHWC: whole-chunk channel Slices are
+    views read in place by the next QLinearConv, the fused QLinearAdd, the
+    Concat and MaxPool; a misaligned Slice and DequantizeLinear read the NCHW
+    form; graph outputs leave the forward as NCHW.  Bytes equal the oracle's."""
+    rng = np.random.default_rng(17)
+    inits = {"xs": np.asarray([0.02], np.float32), "xz": np.asarray([128], np.uint8),
+             "ys": np.asarray([0.05], np.float32), "yz": np.asarray([128], np.uint8),
+             "ax": np.asarray([1], np.float32)}
+
+    def qconv(name, x, cin, cout, k, stride=1):
+        inits[name + "w"] = rng.integers(-127, 128, (cout, cin, k, k)).astype(np.int8)
+        inits[name + "s"] = rng.uniform(0.002, 0.01, cout).astype(np.float32)
+        inits[name + "z"] = np.zeros(cout, np.int8)
+        return ep.Node("QLinearConv", [x, "xs" if x == "x" else "ys", "xz" if x == "x" else "yz", name + "w",
+                                       name + "s", name + "z", "ys", "yz"], [name],
+                       A(int_lists={"kernel_shape": [k, k], "strides": [stride, stride], "pads": [k // 2] * 4}))
+
+    def sl(name, x, lo, hi):
+        inits[name + "a"], inits[name + "b"] = np.asarray([lo], np.float32), np.asarray([hi], np.float32)
+        return ep.Node("Slice", [x, name + "a", name + "b", "ax"], [name])
+
+    nodes = [qconv("c1", "x", 16, 32, 3), sl("s0", "c1", 0, 16), sl("s1", "c1", 16, 32), sl("s2", "c1", 4, 12),
+             qconv("c2", "s1", 16, 16, 1),
+             ep.Node("DequantizeLinear", ["s0", "ys", "yz"], ["da"]), ep.Node("DequantizeLinear", ["c2", "ys", "yz"], ["db"]),
+             ep.Node("Add", ["da", "db"], ["sum"]), ep.Node("QuantizeLinear", ["sum", "ys", "yz"], ["c3"]),
+             ep.Node("Concat", ["s0", "s1", "c3"], ["cat"], A(ints={"axis": 1})),
+             qconv("c4", "cat", 48, 16, 3, stride=2),
+             ep.Node("DequantizeLinear", ["c2", "ys", "yz"], ["deq"]),
+             ep.Node("MaxPool", ["c3"], ["pool"], A(int_lists={"kernel_shape": [3, 3], "strides": [1, 1],
+                                                            "pads": [1, 1, 1, 1]})),
+             ep.Node("MaxPool", ["s1"], ["pool2"], A(int_lists={"kernel_shape": [2, 2], "strides": [2, 2]}))]
+    g = unique_graph(nodes, inits, ["x"], ["c4", "deq", "pool", "s2", "cat", "pool2"])
+    assert "QLinearAdd" in [n.op for n in fuse(g).nodes]
+    feeds = {"x": rng.integers(0, 256, (1, 16, 12, 12)).astype(np.uint8)}
+    out = Session(g, ctx).run(feeds)
+    ref = G.run_graph(g, feeds)
+    for k in ("c4", "deq", "pool", "s2", "cat", "pool2"):
+        assert out[k].shape == ref[k].shape, k
+        np.testing.assert_array_equal(np.asarray(out[k], np.float32), np.asarray(ref[k], np.float32), err_msg=k)
+
+
 @pytest.mark.parametrize("zp", [None, 0, 128, -100, 3])
 def test_quantize_dequantize(ctx, zp):
     x = (RNG.normal(0, 3, (1, 4, 6, 6)).astype(np.float32))
