@@ -1163,8 +1163,14 @@ extern "C" int ohip_conv2d(ohip_ctx* ctx, const ohip_conv_desc* d, const void* x
 
   // Groups whose output or input channel span is too narrow to fill an MFMA
   // tile (depthwise, and small groups) run the direct kernel on the NCHW
-  // input; wider groups run one MFMA launch per group.
-  const bool direct = G > 1 && (coutg < 16 || cg * d->kh * d->kw < 32 || G > 64);
+  // input; wider groups run one MFMA launch per group.  So do ungrouped
+  // convolutions of an NCHW input with under 32 taps x channels (an RGB stem,
+  // whose 16-byte channel padding would multiply the staged bytes).  A long
+  // reduction stays on the engine even for a few output channels: one
+  // thread per output walking thousands of taps is latency-bound (an RGB
+  // head, 128 channels x 7x7 taps, ran 20x slower direct).
+  const bool narrow = G == 1 && d->in_layout == OHIP_NCHW && cg * d->kh * d->kw < 32;
+  const bool direct = (G > 1 && (coutg < 16 || cg * d->kh * d->kw < 32 || G > 64)) || narrow;
   if (G > 1 && d->in_layout != OHIP_NCHW && (direct || cg % ce != 0))
     return fail(OHIP_DECLINED, "ohip_conv2d: this grouped convolution needs an NCHW input");
   std::lock_guard<std::mutex> lock(ctx->mu);
@@ -1493,8 +1499,11 @@ extern "C" int ohip_qconv2d(ohip_ctx* ctx, const ohip_qconv_desc* d, const void*
   if (rows > INT_MAX / 2) return fail(OHIP_DECLINED, "ohip_qconv2d: extent too large");
   if (rows == 0) return OHIP_OK;
   // narrow groups (depthwise and the like) run the exact direct kernel on the
-  // NCHW input; wider groups run one MFMA launch per group
-  const bool direct = G > 1 && (coutg < 16 || cg * d->kh * d->kw < 32 || G > 64);
+  // NCHW input; wider groups run one MFMA launch per group.  So do ungrouped
+  // convolutions of an NCHW input with under 32 taps x channels (as
+  // ohip_conv2d).
+  const bool narrow = G == 1 && d->in_layout == OHIP_NCHW && cg * d->kh * d->kw < 32;
+  const bool direct = (G > 1 && (coutg < 16 || cg * d->kh * d->kw < 32 || G > 64)) || narrow;
   if (G > 1 && d->in_layout != OHIP_NCHW && (direct || cg % 16 != 0))
     return fail(OHIP_DECLINED, "ohip_qconv2d: this grouped convolution needs an NCHW input");
   if (d->out_table && d->out_kind != OHIP_QOUT_U8 && d->out_kind != OHIP_QOUT_I8)
