@@ -61,10 +61,10 @@ struct OutMap {
 // other forced tile disables it.  (The 128x128 slices measured slower on the
 // generator's resident NHWC convolutions, so the automatic plan keeps 64x64.)
 inline int split_tile_size(int, int, int forced_tile) { return forced_tile == 11 ? 128 : 64; }
-inline int plan_splits(int P, int Q, int kc, int forced_tile) {
+inline int plan_splits(int P, int Q, int kc, int forced_tile, int auto_bs = 64) {
   if (forced_tile != 0 && forced_tile != 10 && forced_tile != 11) return 1;
   const int64_t nk = (kc + 7) / 8;
-  const int bs = split_tile_size(P, Q, forced_tile);
+  const int bs = forced_tile == 0 ? auto_bs : split_tile_size(P, Q, forced_tile);
   const int64_t nb = (int64_t)((P + bs - 1) / bs) * ((Q + bs - 1) / bs);
   if (forced_tile != 0) return (int)std::max<int64_t>(2, std::min<int64_t>(16, nk / 2 > 0 ? nk / 2 : 1));
   if (nb >= 512 || nk < 16 || (nb >= 256 && nk < 32)) return 1;
@@ -72,6 +72,22 @@ inline int plan_splits(int P, int Q, int kc, int forced_tile) {
   s = std::min<int64_t>(s, nk / 8);
   s = std::min<int64_t>(s, 16);
   return (int)std::max<int64_t>(s, 1);
+}
+// The split plan and the tile id to launch it with.  f32 contractions are
+// bound by the f32 MFMA rate, which the eight-wave 128x128 tile sustains
+// better than the 64x64 one (two accumulator chains per wave instead of
+// one), so their slices run on it (as forced tile 11) when that still gives
+// the chip a block per CU.
+struct SplitChoice {
+  int splits, tile;
+};
+inline SplitChoice plan_split_tile(int P, int Q, int kc, int override_tile, bool mfma_f32) {
+  if (override_tile == 0 && mfma_f32) {
+    const int s = plan_splits(P, Q, kc, 0, 128);
+    const int64_t nb = (int64_t)((P + 127) / 128) * ((Q + 127) / 128);
+    if (s > 1 && nb * s >= 256) return {s, 11};
+  }
+  return {plan_splits(P, Q, kc, override_tile), override_tile};
 }
 inline size_t split_ws_bytes(int P, int Q, int splits) {
   return splits > 1 ? (size_t)splits * (size_t)Q * (size_t)((P + 3) / 4 * 4) * 4 : 0;

@@ -1062,7 +1062,9 @@ extern "C" int ohip_gemm(ohip_ctx* ctx, const ohip_gemm_desc* d, const void* a, 
 
   ScratchPlan plan;
   size_t ia = direct ? SIZE_MAX : plan.add((size_t)(M * kp) * eb);
-  const int splits = gemv ? 1 : plan_splits((int)N, (int)M, b->kc, ctx->tile_override);
+  const SplitChoice sc = gemv ? SplitChoice{1, ctx->tile_override}
+                              : plan_split_tile((int)N, (int)M, b->kc, ctx->tile_override, d->dtype == OHIP_F32);
+  const int splits = sc.splits;
   size_t iw = splits > 1 ? plan.add(split_ws_bytes((int)N, (int)M, splits)) : SIZE_MAX;
   rc = scratch_reserve(ctx, plan.total());
   if (rc) return rc;
@@ -1101,7 +1103,7 @@ extern "C" int ohip_gemm(ohip_ctx* ctx, const ohip_gemm_desc* d, const void* a, 
     DENSE_FITS_OR_DECLINE(yv, "ohip_gemm");
     o.splits = splits;
     o.split_ws = splits > 1 ? scratch_at(ctx, plan, iw) : nullptr;
-    e = run_dense_float(d->dtype, x, yv, o, ctx->tile_override, ctx->stream);
+    e = run_dense_float(d->dtype, x, yv, o, sc.tile, ctx->stream);
   }
   if (e != hipSuccess) return hip_fail(e, "ohip_gemm launch");
   return OHIP_OK;
@@ -1195,7 +1197,9 @@ extern "C" int ohip_conv2d(ohip_ctx* ctx, const ohip_conv_desc* d, const void* x
   size_t ix = stage ? plan.add((size_t)(d->n * sh_ * sw_ * cpt) * eb) : SIZE_MAX;
   const bool nchw_out = d->out_layout == OHIP_NCHW;
   const int sP = nchw_out ? (int)rows : (int)coutg, sQ = nchw_out ? (int)coutg : (int)rows;
-  const int splits = plan_splits(sP, sQ, (int)(d->kh * d->kw * (cp / ce)), ctx->tile_override);
+  const SplitChoice sc =
+      plan_split_tile(sP, sQ, (int)(d->kh * d->kw * (cp / ce)), ctx->tile_override, d->dtype == OHIP_F32);
+  const int splits = sc.splits;
   size_t iw = splits > 1 ? plan.add(split_ws_bytes(sP, sQ, splits)) : SIZE_MAX;
   rc = scratch_reserve(ctx, plan.total());
   if (rc) return rc;
@@ -1253,7 +1257,7 @@ extern "C" int ohip_conv2d(ohip_ctx* ctx, const ohip_conv_desc* d, const void* x
     DENSE_FITS_OR_DECLINE(wt, "ohip_conv2d");
     o.splits = splits;
     o.split_ws = splits > 1 ? scratch_at(ctx, plan, iw) : nullptr;
-    hipError_t e = run_conv_float(d->dtype, col, wt, col_on_x, o, ctx->tile_override, ctx->stream);
+    hipError_t e = run_conv_float(d->dtype, col, wt, col_on_x, o, sc.tile, ctx->stream);
     if (e != hipSuccess) return hip_fail(e, "ohip_conv2d launch");
   }
   return OHIP_OK;
