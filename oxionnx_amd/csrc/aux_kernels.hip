@@ -591,6 +591,171 @@ conv_direct_kernel(const T* __restrict__ x, const T* __restrict__ w, const T* __
   }
 }
 
+// ---------------------------------------------------------------- few output channels
+constexpr int kFewTile = 16;   // output tile edge; one thread per output pixel
+
+int fewout_slice(const DirectConvArgs& a) {
+  const int ih = (kFewTile - 1) * a.sh + (a.KH - 1) * a.dh + 1, iw = (kFewTile - 1) * a.sw + (a.KW - 1) * a.dw + 1;
+  const int per = ih * iw + (a.cout <= 4 ? 4 : kFewOutMax) * a.KH * a.KW;   // floats per input channel
+  const int cs = (48 * 1024 / 4) / per;
+  return std::max(1, std::min(cs, a.C));
+}
+
+template <class T, int CO, int KWC>   // KWC: the filter width when known at compile time (0: a.KW)
+__global__ void __launch_bounds__(256) conv_fewout_kernel(const T* __restrict__ x, const T* __restrict__ w,
+                                                          float* __restrict__ ws, DirectConvArgs a, int cslice) {
+  typedef float f32x4 __attribute__((ext_vector_type(4)));
+  extern __shared__ f32x4 fsm4[];
+  float* fsm = reinterpret_cast<float*>(fsm4);
+  const int IH = (kFewTile - 1) * a.sh + (a.KH - 1) * a.dh + 1, IW = (kFewTile - 1) * a.sw + (a.KW - 1) * a.dw + 1;
+  const int KK = a.KH * a.KW;
+  const int tiles_x = (a.OW + kFewTile - 1) / kFewTile;
+  const int ox0 = (int)(blockIdx.x % tiles_x) * kFewTile, oy0 = (int)(blockIdx.x / tiles_x) * kFewTile;
+  const int ci0 = blockIdx.y * cslice, n = blockIdx.z;
+  const int cs = min(cslice, a.C - ci0);
+  // weights first, [ci][tap][CO] (CO consecutive floats: one broadcast read
+  // per tap and 4 outputs), then the input patch [ci][IH][IW]
+  f32x4* wsm = fsm4;
+  float* xs = fsm + cslice * KK * CO;
+  const T* xn = x + ((int64_t)n * a.C + ci0) * a.H * a.W;
+  // Both staging loops issue their global loads in batches of 8 before any
+  // LDS store, so a thread's loads overlap instead of each waiting a round
+  // trip.
+  constexpr int B = 8;
+  const int nw = cs * KK * CO;
+  for (int base = threadIdx.x; base < nw; base += 256 * B) {
+    float v[B];
+#pragma unroll
+    for (int u = 0; u < B; ++u) {
+      const int idx = base + u * 256;
+      const int co = idx % CO, r = idx / CO;
+      const int t = r % KK, ci = r / KK;
+      v[u] = idx < nw && co < a.cout ? to_f32(w[(int64_t)co * a.ldw + t * a.cpg + ci0 + ci]) : 0.0f;
+    }
+#pragma unroll
+    for (int u = 0; u < B; ++u)
+      if (base + u * 256 < nw) fsm[base + u * 256] = v[u];
+  }
+  // the input patch of the tile (padded positions as the direct kernel reads them)
+  const int nx = cs * IH * IW;
+  for (int base = threadIdx.x; base < nx; base += 256 * B) {
+    float v[B];
+#pragma unroll
+    for (int u = 0; u < B; ++u) {
+      const int idx = base + u * 256;
+      const int ci = idx / (IH * IW), r = idx - ci * (IH * IW);
+      const int yy = r / IW, xx = r - yy * IW;
+      int iy = oy0 * a.sh + yy, ix = ox0 * a.sw + xx;
+      bool ok = idx < nx;
+      if (a.pad_mode == 0) {
+        iy -= a.pt;
+        ix -= a.pl;
+        ok = ok && (unsigned)iy < (unsigned)a.H && (unsigned)ix < (unsigned)a.W;
+      } else {
+        iy = pad_map(iy, a.pt, a.H, a.pad_mode);
+        ix = pad_map(ix, a.pl, a.W, a.pad_mode);
+      }
+      v[u] = ok ? to_f32(xn[((int64_t)ci * a.H + iy) * a.W + ix]) : 0.0f;
+    }
+#pragma unroll
+    for (int u = 0; u < B; ++u)
+      if (base + u * 256 < nx) xs[base + u * 256] = v[u];
+  }
+  __syncthreads();
+  const int tx = threadIdx.x % kFewTile, ty = threadIdx.x / kFewTile;
+  const int ox = ox0 + tx, oy = oy0 + ty;
+  f32x4 acc[CO / 4];
+#pragma unroll
+  for (int q = 0; q < CO / 4; ++q) acc[q] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  for (int ci = 0; ci < cs; ++ci) {
+    const float* xc = xs + ci * IH * IW + (ty * a.sh) * IW + tx * a.sw;
+    const f32x4* wc = wsm + ci * KK * (CO / 4);
+    for (int ky = 0; ky < a.KH; ++ky) {
+      const float* xr = xc + ky * a.dh * IW;
+      const f32x4* wr = wc + ky * a.KW * (CO / 4);
+      if constexpr (KWC > 0) {
+        // a whole filter row: independent LDS reads, then the FMAs
+        float v[KWC];
+#pragma unroll
+        for (int kx = 0; kx < KWC; ++kx) v[kx] = xr[kx * a.dw];
+#pragma unroll
+        for (int kx = 0; kx < KWC; ++kx)
+#pragma unroll
+          for (int q = 0; q < CO / 4; ++q) acc[q] += v[kx] * wr[kx * (CO / 4) + q];
+      } else {
+        for (int kx = 0; kx < a.KW; ++kx) {
+          const float v = xr[kx * a.dw];
+#pragma unroll
+          for (int q = 0; q < CO / 4; ++q) acc[q] += v * wr[kx * (CO / 4) + q];
+        }
+      }
+    }
+  }
+  if (ox < a.OW && oy < a.OH) {
+    const int64_t plane = (int64_t)a.OH * a.OW;
+    float* wp = ws + (((int64_t)blockIdx.y * a.N + n) * a.cout) * plane + (int64_t)oy * a.OW + ox;
+#pragma unroll
+    for (int co = 0; co < CO; ++co)
+      if (co < a.cout) wp[co * plane] = acc[co / 4][co % 4];
+  }
+}
+
+template <class T>
+__global__ void __launch_bounds__(256) fewout_reduce_kernel(const float* __restrict__ ws, const T* __restrict__ bias,
+                                                            T* __restrict__ y, DirectConvArgs a, int slices) {
+  const int64_t plane = (int64_t)a.OH * a.OW, total = (int64_t)a.N * a.cout * plane;
+  for (int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x; idx < total; idx += (int64_t)gridDim.x * 256) {
+    float v = ws[idx];
+    for (int s = 1; s < slices; ++s) v += ws[(int64_t)s * total + idx];
+    const int64_t p = idx % plane, nc = idx / plane;
+    const int co = (int)(nc % a.cout), n = (int)(nc / a.cout);
+    if (bias) v = v + to_f32(bias[co]);
+    v = activate(v, a.act, a.lo, a.hi);
+    const int64_t o = a.nhwc_out ? ((int64_t)n * plane + p) * a.ldo + co : idx;
+    y[o] = from_f32<T>(v);
+  }
+}
+
+hipError_t run_conv_fewout(int dtype, const void* x, const void* w, const void* bias, void* y, float* ws,
+                           const DirectConvArgs& a, int cslice, hipStream_t st) {
+  if (a.cout > kFewOutMax || cslice < 1) return hipErrorInvalidValue;
+  const int64_t total = (int64_t)a.N * a.cout * a.OH * a.OW;
+  if (total <= 0) return hipSuccess;
+  const int slices = (a.C + cslice - 1) / cslice;
+  const int IH = (kFewTile - 1) * a.sh + (a.KH - 1) * a.dh + 1, IW = (kFewTile - 1) * a.sw + (a.KW - 1) * a.dw + 1;
+  const int co = a.cout <= 4 ? 4 : kFewOutMax;
+  const size_t lds = (size_t)cslice * (IH * IW + co * a.KH * a.KW) * 4;
+  if (lds > 64 * 1024) return hipErrorInvalidValue;
+  const dim3 grid((unsigned)(((a.OW + kFewTile - 1) / kFewTile) * ((a.OH + kFewTile - 1) / kFewTile)), (unsigned)slices,
+                  (unsigned)a.N);
+  const unsigned rgrid = (unsigned)std::min<int64_t>((total + 255) / 256, 65535 * 16);
+#define OHIP_FEW_KW(T, CO)                                                                                             \
+  switch (a.KW) {                                                                                                       \
+    case 3: hipLaunchKernelGGL((conv_fewout_kernel<T, CO, 3>), grid, dim3(256), lds, st, reinterpret_cast<const T*>(x), \
+                               reinterpret_cast<const T*>(w), ws, a, cslice); break;                                  \
+    case 5: hipLaunchKernelGGL((conv_fewout_kernel<T, CO, 5>), grid, dim3(256), lds, st, reinterpret_cast<const T*>(x), \
+                               reinterpret_cast<const T*>(w), ws, a, cslice); break;                                  \
+    case 7: hipLaunchKernelGGL((conv_fewout_kernel<T, CO, 7>), grid, dim3(256), lds, st, reinterpret_cast<const T*>(x), \
+                               reinterpret_cast<const T*>(w), ws, a, cslice); break;                                  \
+    default: hipLaunchKernelGGL((conv_fewout_kernel<T, CO, 0>), grid, dim3(256), lds, st, reinterpret_cast<const T*>(x),\
+                                reinterpret_cast<const T*>(w), ws, a, cslice); break;                                 \
+  }
+#define OHIP_FEW(T)                                                                                                    \
+  if (co == 4) { OHIP_FEW_KW(T, 4) }                                                                                    \
+  else { OHIP_FEW_KW(T, 8) }                                                                                            \
+  hipLaunchKernelGGL(fewout_reduce_kernel<T>, dim3(rgrid), dim3(256), 0, st, ws, reinterpret_cast<const T*>(bias),   \
+                     reinterpret_cast<T*>(y), a, slices)
+  switch (dtype) {
+    case DT_F32: OHIP_FEW(float); break;
+    case DT_F16: OHIP_FEW(_Float16); break;
+    case DT_BF16: OHIP_FEW(__bf16); break;
+    default: return hipErrorInvalidValue;
+  }
+#undef OHIP_FEW
+#undef OHIP_FEW_KW
+  return hipGetLastError();
+}
+
 hipError_t run_conv_direct(int dtype, const void* x, const void* w, const void* bias, void* y,
                            const DirectConvArgs& a, hipStream_t st) {
   const int64_t total = (int64_t)a.N * a.cout * a.OH * a.OW;

@@ -147,6 +147,18 @@ struct DirectConvArgs {
 hipError_t run_conv_direct(int dtype, const void* x, const void* w, const void* bias, void* y,
                            const DirectConvArgs& a, hipStream_t st);
 
+// Ungrouped convolution with at most 8 output channels over a long
+// reduction (an RGB head): the input channels are cut into `cslice`-wide
+// slices; a block stages one slice's input patch of a 16x16 output tile in
+// LDS and writes its partial sums (f32) to ws[slice][n][co][oy][ox]; the
+// reduction adds the slices in order and applies bias, activation and the
+// output type as conv_direct_kernel does.  ws holds
+// ceil(C / cslice) * N * cout * OH * OW floats.
+constexpr int kFewOutMax = 8;
+int fewout_slice(const DirectConvArgs& a);   // channels per slice for the LDS budget
+hipError_t run_conv_fewout(int dtype, const void* x, const void* w, const void* bias, void* y, float* ws,
+                           const DirectConvArgs& a, int cslice, hipStream_t st);
+
 // Direct (non-MFMA) grouped integer convolution; see qconv_direct_kernel.
 struct DirectQConvArgs {
   int N, C, H, W, cout, cg, coutg, KH, KW;

@@ -1122,6 +1122,16 @@ static int conv_geo(int64_t h, int64_t w, int64_t kh, int64_t kw, int64_t sh, in
   return OHIP_OK;
 }
 
+// OHIP_FEWOUT=0 keeps few-output convolutions on the MFMA engine (a
+// measurement switch)
+static bool few_out_allowed() {
+  static const bool v = [] {
+    const char* e = std::getenv("OHIP_FEWOUT");
+    return !(e && e[0] == '0');
+  }();
+  return v;
+}
+
 extern "C" int ohip_conv2d(ohip_ctx* ctx, const ohip_conv_desc* d, const void* x, const ohip_weight* w,
                            const void* bias, void* y) {
   int rc = activate(ctx);
@@ -1175,9 +1185,16 @@ extern "C" int ohip_conv2d(ohip_ctx* ctx, const ohip_conv_desc* d, const void* x
   const bool direct = (G > 1 && (coutg < 16 || cg * d->kh * d->kw < 32 || G > 64)) || narrow;
   if (G > 1 && d->in_layout != OHIP_NCHW && (direct || cg % ce != 0))
     return fail(OHIP_DECLINED, "ohip_conv2d: this grouped convolution needs an NCHW input");
+  // A few output channels over a long reduction (an RGB head) would fill a
+  // sliver of an f32 MFMA tile (f32 MFMA runs at a sixteenth of the f16
+  // rate): the few-output kernel stages input patches in LDS and reduces over
+  // channel slices instead (128 -> 3 channels, 7x7, 128x128: 50 us against
+  // 232).  f16 / bf16 stay on the engine, which is faster there.
+  const bool fewout = !direct && d->dtype == OHIP_F32 && G == 1 && d->in_layout == OHIP_NCHW &&
+                      d->cout <= kFewOutMax && cg * d->kh * d->kw >= 32 && rows * d->cout >= 16384 && few_out_allowed();
   std::lock_guard<std::mutex> lock(ctx->mu);
   ctx->counters.dispatches++;
-  if (direct) {
+  if (direct || fewout) {
     DirectConvArgs a{};
     a.N = (int)d->n; a.C = (int)d->c; a.H = (int)d->h; a.W = (int)d->w; a.cout = (int)d->cout;
     a.cg = (int)cg; a.coutg = (int)coutg; a.KH = (int)d->kh; a.KW = (int)d->kw;
@@ -1185,6 +1202,18 @@ extern "C" int ohip_conv2d(ohip_ctx* ctx, const ohip_conv_desc* d, const void* x
     a.pt = (int)d->pad_t; a.pl = (int)d->pad_l; a.pad_mode = fused_pad ? d->pad_mode : 0;
     a.OH = (int)g.oh; a.OW = (int)g.ow; a.ldw = w->ld_bytes / eb; a.cpg = (int)cp;
     a.nhwc_out = d->out_layout != OHIP_NCHW; a.ldo = ldo; a.act = act; a.lo = lo; a.hi = hi;
+    if (fewout) {
+      const int cslice = fewout_slice(a);
+      const int64_t slices = (d->c + cslice - 1) / cslice;
+      ScratchPlan plan;
+      const size_t iw = plan.add((size_t)(slices * d->n * d->cout * ohw) * 4);
+      rc = scratch_reserve(ctx, plan.total());
+      if (rc) return rc;
+      hipError_t e = run_conv_fewout(d->dtype, x, w->data, bias, y, static_cast<float*>(scratch_at(ctx, plan, iw)), a,
+                                     cslice, ctx->stream);
+      if (e != hipSuccess) return hip_fail(e, "ohip_conv2d few-output launch");
+      return OHIP_OK;
+    }
     hipError_t e = run_conv_direct(d->dtype, x, w->data, bias, y, a, ctx->stream);
     if (e != hipSuccess) return hip_fail(e, "ohip_conv2d direct launch");
     return OHIP_OK;

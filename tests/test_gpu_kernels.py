@@ -141,10 +141,13 @@ CONV_CASES = [
     ((3, 5, 9, 11), (7, 5, 3, 2), (1, 2), (0, 1, 1, 0), (1, 1)),
     # row-tiled staging: a partial last channel tile, several images
     ((2, 70, 8, 16), (8, 70, 3, 3), (1, 1), (1, 1, 1, 1), (1, 1)),
-    # an RGB stem (27 taps x channels: the direct kernel) and an RGB head (3
-    # output channels over 27K outputs: the engine)
+    # an RGB stem (27 taps x channels: the direct kernel); few output
+    # channels over a long reduction (the few-output kernel): an RGB head,
+    # stride 2 with uneven pads over two images, dilation 2
     ((1, 3, 64, 64), (16, 3, 3, 3), (2, 2), (1, 1, 1, 1), (1, 1)),
     ((1, 64, 96, 96), (3, 64, 3, 3), (1, 1), (1, 1, 1, 1), (1, 1)),
+    ((2, 40, 90, 90), (8, 40, 5, 5), (2, 2), (2, 1, 2, 1), (1, 1)),
+    ((1, 32, 80, 80), (5, 32, 3, 3), (1, 1), (2, 2, 2, 2), (2, 2)),
 ]
 
 
