@@ -30,8 +30,8 @@ GEMM_SWEEP = [(1, 25088, 512), (128, 768, 3072), (2048, 4096, 4096), (4096, 4096
 def parse():
     p = argparse.ArgumentParser()
     p.add_argument("--gpus", type=int, default=1)
-    p.add_argument("--steps", type=int, default=50)
-    p.add_argument("--warmup", type=int, default=5)
+    p.add_argument("--steps", type=int, default=100)
+    p.add_argument("--warmup", type=int, default=30)
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--no-sweep", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=10.0)

@@ -6,6 +6,7 @@
 #include <stdint.h>
 
 #include <algorithm>
+#include <cstdlib>
 
 namespace ohip {
 
@@ -61,8 +62,19 @@ struct OutMap {
 // other forced tile disables it.  (The 128x128 slices measured slower on the
 // generator's resident NHWC convolutions, so the automatic plan keeps 64x64.)
 inline int split_tile_size(int, int, int forced_tile) { return forced_tile == 11 ? 128 : 64; }
+// OHIP_SPLITS=n (2..16) forces that many split-K slices wherever a split
+// plan is made (a measurement switch)
+inline int forced_splits() {
+  static const int v = [] {
+    const char* e = std::getenv("OHIP_SPLITS");
+    const int n = e ? std::atoi(e) : 0;
+    return n >= 2 && n <= 16 ? n : 0;
+  }();
+  return v;
+}
 inline int plan_splits(int P, int Q, int kc, int forced_tile, int auto_bs = 64) {
   if (forced_tile != 0 && forced_tile != 10 && forced_tile != 11) return 1;
+  if (forced_splits()) return forced_splits();
   const int64_t nk = (kc + 7) / 8;
   const int bs = forced_tile == 0 ? auto_bs : split_tile_size(P, Q, forced_tile);
   const int64_t nb = (int64_t)((P + bs - 1) / bs) * ((Q + bs - 1) / bs);
