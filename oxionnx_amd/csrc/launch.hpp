@@ -81,12 +81,14 @@ template <class OutT> struct FloatEpi {
   float lo, hi;
 
   static constexpr int kStageBytes = sizeof(OutT) <= 2 ? (int)sizeof(OutT) : 0;
+  static constexpr bool kStageWide = sizeof(OutT) == 4;   // f32 outputs stage as 4-byte elements
   __device__ __forceinline__ int out_bytes() const { return (int)sizeof(OutT); }
   __device__ __forceinline__ OutAddr addr() const { return out; }
   __device__ __forceinline__ bool staged_ok(int bp) const {
     return out.stage && out.vec && ((uintptr_t)out.y % 16 == 0) && ((out.sj * (int64_t)sizeof(OutT)) % 16 == 0) &&
            (out.bstride == 0 || out.ohw % bp == 0);
   }
+  __device__ __forceinline__ bool staged_wide_ok(int bp) const { return sizeof(OutT) == 4 && staged_ok(bp); }
 
   struct PreI { float b[4]; };    // beta * bias per row (BIAS_I, BIAS_SCALAR), else -0
   struct PreJ { float b; };       // beta * bias per column (BIAS_J), else -0
@@ -179,11 +181,16 @@ struct QuantEpi {
   int vec_ok;               // every per-channel / per-row array is 16-byte aligned
 
   static constexpr int kStageBytes = 1;
+  static constexpr bool kStageWide = true;   // int32 / f32 outputs stage as 4-byte elements
   __device__ __forceinline__ int out_bytes() const { return (out_kind == QOUT_U8 || out_kind == QOUT_I8) ? 1 : 4; }
   __device__ __forceinline__ OutAddr addr() const { return out; }
   __device__ __forceinline__ bool staged_ok(int bp) const {
     return out.stage && (out_kind == QOUT_U8 || out_kind == QOUT_I8) && out.vec && ((uintptr_t)out.y % 16 == 0) &&
            (out.sj % 16 == 0) && (out.bstride == 0 || out.ohw % bp == 0);
+  }
+  __device__ __forceinline__ bool staged_wide_ok(int bp) const {
+    return out.stage && (out_kind == QOUT_I32 || out_kind == QOUT_F32) && out.vec && ((uintptr_t)out.y % 16 == 0) &&
+           (out.sj % 4 == 0) && (out.bstride == 0 || out.ohw % bp == 0);
   }
 
   // per-channel terms of a weight channel, and the correction factor of an

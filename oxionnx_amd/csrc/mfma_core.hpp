@@ -545,19 +545,36 @@ mfma_gemm_kernel(const LX lx, const LY ly, const Epi epi, int nP, int nQ, int kc
   // chunks of output rows, instead of 4-element pieces of 32 rows per store.
   // Staged row `lj` holds outputs (p0.., q0 + lj); its 16-byte chunk c sits
   // at slot c ^ (lj % CPR) so the fragment writes spread over the banks.
-  constexpr int EB = Epi::kStageBytes > 0 ? Epi::kStageBytes : 1;
-  constexpr int CPR = Tl::BP * EB / 16;   // 16-byte chunks per staged row
-  constexpr int EPC = 16 / EB;            // outputs per chunk
-  static_assert(Epi::kStageBytes == 0 || Tl::BQ * Tl::BP * EB <= Tl::STAGES * Tl::kStage * 16,
+  // Mode 1 stages the epilogue's narrow output (1 or 2 bytes); mode 2 stages
+  // 4-byte outputs (int32, f32) when the tile's stage buffers hold them.
+  constexpr int EBN = Epi::kStageBytes > 0 ? Epi::kStageBytes : 1;
+  constexpr bool kWide = Epi::kStageWide && Tl::BQ * Tl::BP * 4 <= Tl::STAGES * Tl::kStage * 16;
+  static_assert(Epi::kStageBytes == 0 || Tl::BQ * Tl::BP * EBN <= Tl::STAGES * Tl::kStage * 16,
                 "staging must fit the stage buffers");
   char* stg = reinterpret_cast<char*>(smem);
-  bool staged = false;
-  if constexpr (Epi::kStageBytes > 0) staged = epi.staged_ok(Tl::BP);
+  int smode = 0;
+  if constexpr (Epi::kStageBytes > 0) smode = epi.staged_ok(Tl::BP) ? 1 : 0;
+  if constexpr (kWide) if (smode == 0 && epi.staged_wide_ok(Tl::BP)) smode = 2;
+  const bool staged = smode != 0;
   if (staged) {
     wait_vmcnt<0>();
     wait_lgkm0();
     barrier_only();
   }
+  auto stage_write = [&](auto ebc, int lj, int ig, const uint32_t (&bits)[4]) __attribute__((always_inline)) {
+    constexpr int EB = decltype(ebc)::value;
+    constexpr int CPR = Tl::BP * EB / 16;
+    const int byte = (ig - p0) * EB;
+    char* dst = stg + lj * (Tl::BP * EB) + (((byte >> 4) ^ (lj & (CPR - 1))) << 4) + (byte & 15);
+    if constexpr (EB == 4) {
+      *reinterpret_cast<u32x4*>(dst) = u32x4{bits[0], bits[1], bits[2], bits[3]};
+    } else if constexpr (EB == 2) {
+      typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+      *reinterpret_cast<u32x2*>(dst) = u32x2{bits[0] | (bits[1] << 16), bits[2] | (bits[3] << 16)};
+    } else {
+      *reinterpret_cast<uint32_t*>(dst) = bits[0] | (bits[1] << 8) | (bits[2] << 16) | (bits[3] << 24);
+    }
+  };
 
   // The lane's outputs are finished one group at a time (rows i0 + 8g .. +3
   // of every column b): the group's row terms are loaded, its four outputs per
@@ -582,16 +599,14 @@ mfma_gemm_kernel(const LX lx, const LY ly, const Epi epi, int nP, int nQ, int kc
       uint32_t bits[4];
       epi.finish(pi, pj[b], ig, j, v, bits);
       if constexpr (Epi::kStageBytes > 0) {
-        if (staged) {
-          const int lj = j - q0;
-          const int byte = (ig - p0) * EB;
-          char* dst = stg + lj * (Tl::BP * EB) + (((byte >> 4) ^ (lj & (CPR - 1))) << 4) + (byte & 15);
-          if constexpr (EB == 2) {
-            typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-            *reinterpret_cast<u32x2*>(dst) = u32x2{bits[0] | (bits[1] << 16), bits[2] | (bits[3] << 16)};
-          } else {
-            *reinterpret_cast<uint32_t*>(dst) = bits[0] | (bits[1] << 8) | (bits[2] << 16) | (bits[3] << 24);
-          }
+        if (smode == 1) {
+          stage_write(std::integral_constant<int, EBN>{}, j - q0, ig, bits);
+          return;
+        }
+      }
+      if constexpr (kWide) {
+        if (smode == 2) {
+          stage_write(std::integral_constant<int, 4>{}, j - q0, ig, bits);
           return;
         }
       }
@@ -599,32 +614,39 @@ mfma_gemm_kernel(const LX lx, const LY ly, const Epi epi, int nP, int nQ, int kc
     });
   });
 
-  if constexpr (Epi::kStageBytes > 0) {
-    if (staged) {
-      wait_lgkm0();
-      barrier_only();
-      for (int c = t; c < Tl::BQ * CPR; c += Tl::kThreads) {
-        const int row = c / CPR, cc = c - row * CPR;
-        const int j = q0 + row, i = p0 + cc * EPC;
-        if (j >= out.Q || i >= out.P) continue;
-        const u32x4 v = *reinterpret_cast<const u32x4*>(stg + row * (Tl::BP * EB) + ((cc ^ (row & (CPR - 1))) << 4));
-        char* dst = out.y + (out.row(i) + (int64_t)j * out.sj) * EB;
-        if (i + EPC <= out.P) {
-          *reinterpret_cast<u32x4*>(dst) = v;
-        } else {
-          // the row's last, partial chunk: its bytes one at a time (shifts,
-          // not a dynamically indexed copy of v, which would live in memory)
-          const int nbytes = (out.P - i) * EB;
+  auto flush = [&](auto ebc) __attribute__((always_inline)) {
+    constexpr int EB = decltype(ebc)::value;
+    constexpr int CPR = Tl::BP * EB / 16;   // 16-byte chunks per staged row
+    constexpr int EPC = 16 / EB;            // outputs per chunk
+    wait_lgkm0();
+    barrier_only();
+    for (int c = t; c < Tl::BQ * CPR; c += Tl::kThreads) {
+      const int row = c / CPR, cc = c - row * CPR;
+      const int j = q0 + row, i = p0 + cc * EPC;
+      if (j >= out.Q || i >= out.P) continue;
+      const u32x4 v = *reinterpret_cast<const u32x4*>(stg + row * (Tl::BP * EB) + ((cc ^ (row & (CPR - 1))) << 4));
+      char* dst = out.y + (out.row(i) + (int64_t)j * out.sj) * EB;
+      if (i + EPC <= out.P) {
+        *reinterpret_cast<u32x4*>(dst) = v;
+      } else {
+        // the row's last, partial chunk: its bytes one at a time (shifts,
+        // not a dynamically indexed copy of v, which would live in memory)
+        const int nbytes = (out.P - i) * EB;
 #pragma unroll
-          for (int w = 0; w < 4; ++w) {
-            const uint32_t word = v[w];
+        for (int w = 0; w < 4; ++w) {
+          const uint32_t word = v[w];
 #pragma unroll
-            for (int b = 0; b < 4; ++b)
-              if (4 * w + b < nbytes) dst[4 * w + b] = (char)(word >> (8 * b));
-          }
+          for (int bb = 0; bb < 4; ++bb)
+            if (4 * w + bb < nbytes) dst[4 * w + bb] = (char)(word >> (8 * bb));
         }
       }
     }
+  };
+  if constexpr (Epi::kStageBytes > 0) {
+    if (smode == 1) flush(std::integral_constant<int, EBN>{});
+  }
+  if constexpr (kWide) {
+    if (smode == 2) flush(std::integral_constant<int, 4>{});
   }
 }
 
@@ -635,6 +657,9 @@ template <class T> struct PartialEpi {
   T* ws;
   int P, Pp, Q;
   static constexpr int kStageBytes = 0;
+  static constexpr bool kStageWide = false;
+  __device__ __forceinline__ bool staged_ok(int) const { return false; }
+  __device__ __forceinline__ bool staged_wide_ok(int) const { return false; }
   struct PreI {};
   struct PreJ {};
   __device__ __forceinline__ void load_i(PreI&, int) const {}
