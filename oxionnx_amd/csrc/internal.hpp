@@ -94,12 +94,13 @@ struct SplitChoice {
   int splits, tile;
 };
 inline SplitChoice plan_split_tile(int P, int Q, int kc, int override_tile, bool mfma_f32) {
-  if (override_tile == 0 && mfma_f32) {
+  const int s64 = plan_splits(P, Q, kc, override_tile);
+  if (override_tile == 0 && mfma_f32 && s64 > 1) {   // only where the 64x64 plan splits too
     const int s = plan_splits(P, Q, kc, 0, 128);
     const int64_t nb = (int64_t)((P + 127) / 128) * ((Q + 127) / 128);
     if (s > 1 && nb * s >= 256) return {s, 11};
   }
-  return {plan_splits(P, Q, kc, override_tile), override_tile};
+  return {s64, override_tile};
 }
 inline size_t split_ws_bytes(int P, int Q, int splits) {
   return splits > 1 ? (size_t)splits * (size_t)Q * (size_t)((P + 3) / 4 * 4) * 4 : 0;
