@@ -103,8 +103,8 @@ def cpu_baseline_f16(seconds):
 def main():
     args = parse()
     if args.gpus != 1:
-        print(json.dumps({"error": "this build runs on one GPU only; multi-GPU sharding is a design "
-                                   "note (DESIGN.md), not a measured path", "n_gpus": args.gpus}))
+        print(json.dumps({"error": "this build runs on one GPU only; how the path would shard across GPUs "
+                                   "is a design note, not a measured path", "n_gpus": args.gpus}))
         sys.exit(2)
     import torch
     from oxionnx_amd import _lib as L
