@@ -1772,6 +1772,8 @@ int ohip_dtensor_view_nhwc_internal(const ohip_dtensor* src, int64_t c0, int64_t
   auto* t = new ohip_dtensor(*src);
   t->ptr = static_cast<char*>(src->ptr) + c0 * elem_bytes(src->dtype);
   t->shape[1] = cn;
+  size_t nb = 0;   // the view's own element bytes (its NCHW form's size)
+  if (dt_bytes(t->dtype, t->rank, t->shape, OHIP_NCHW, &nb) == OHIP_OK) t->bytes = nb;
   *out = t;
   return OHIP_OK;
 }
