@@ -93,7 +93,7 @@ def test_binary_two_resident_operands(ctx):
     close(out["y"], ref["y"], 1e-6)
 
 
-@pytest.mark.parametrize("shape", [(1, 512, 32, 32), (2, 3, 5, 7), (1, 4, 1, 1), (1, 2, 300)])
+@pytest.mark.parametrize("shape", [(1, 512, 32, 32), (2, 3, 5, 7), (1, 4, 1, 1), (1, 2, 300), (1, 3, 40, 50), (1, 2, 64, 64)])
 def test_oxi_instance_norm(ctx, shape):
     x = (RNG.normal(3, 2, shape)).astype(np.float32)
     node = ep.Node("OxiInstanceNorm", ["x"], ["y"], A(floats={"epsilon": 1e-5}))
