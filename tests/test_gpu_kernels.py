@@ -68,6 +68,27 @@ def test_gemm_f32_matches_oracle(torch, ctx, mkn, tile):
     assert _rel_err(y, want) <= F32_TOL
 
 
+@pytest.mark.parametrize("dt", ["f32", "f16", "bf16"])
+def test_gemm_many_tiles_matches_float64(torch, ctx, dt):
+    """A Gemm of 280 tiles of 256x256 (one whole round of the 256 CUs and a
+    part-filled one) with a row bias, against torch float64 on the device at
+    the dtype's tolerance (the CPU oracle would take minutes at this size)."""
+    from oxionnx_amd import _lib as L
+    m, k, n = 1024, 1152, 17920
+    g = torch.Generator(device="cuda").manual_seed(5)
+    a = torch.rand((m, k), generator=g, device="cuda", dtype=torch.float32) * 2 - 1
+    b = torch.randn((k, n), generator=g, device="cuda", dtype=torch.float32) / np.sqrt(k)
+    c = torch.randn((n,), generator=g, device="cuda", dtype=torch.float32) * 0.1
+    tdt = {"f32": torch.float32, "f16": torch.float16, "bf16": torch.bfloat16}[dt]
+    ldt = {"f32": L.F32, "f16": L.F16, "bf16": L.BF16}[dt]
+    a, b, c = a.to(tdt), b.to(tdt), c.to(tdt)
+    w = ctx.weight_gemm(b.float().cpu().numpy(), dtype=ldt)
+    y = ctx.gemm(a, w, c).double()
+    want = a.double() @ b.double() + c.double()
+    err = float((y - want).abs().max() / want.abs().max())
+    assert err <= (F32_TOL if dt == "f32" else HALF_TOL), err
+
+
 @pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
 @pytest.mark.parametrize("ckind", ["none", "scalar", "row", "full"])
 def test_gemm_f32_transposes_alpha_beta_bias(torch, ctx, ta, tb, ckind):
