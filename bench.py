@@ -34,7 +34,7 @@ def parse():
     p.add_argument("--warmup", type=int, default=30)
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--no-sweep", action="store_true")
-    p.add_argument("--cpu-seconds", type=float, default=10.0)
+    p.add_argument("--cpu-seconds", type=float, default=20.0)
     p.add_argument("--only", default="", help="run one item (for profiling): 'headline', 'copy', "
                    "'conv_f32_cfg1', 'int8_ffn', or a sweep item such as 'gemm_f16_2048x4096x4096'")
     return p.parse_args()
@@ -84,13 +84,23 @@ def cpu_baseline_f16(seconds):
     from oracle import oracle as O
     m, k, n = HEADLINE
     rng = np.random.default_rng(7)
-    a = O.f32_to_half_bits(rng.uniform(-1, 1, (8, k)).astype(np.float32))
     b = O.f32_to_half_bits(rng.normal(0, 1 / np.sqrt(k), (k, n)).astype(np.float32))
     c = O.f32_to_half_bits(rng.normal(0, 0.01, n).astype(np.float32))
+    # per-row and per-call costs from a 1-row and a 4-row call (each call
+    # also converts the operands: a fixed cost)
+    a4 = O.f32_to_half_bits(rng.uniform(-1, 1, (4, k)).astype(np.float32))
+    O.gemm_half(a4, b, c, rows=(0, 1))   # first call: library load, page faults
     t0 = time.perf_counter()
-    O.gemm_half(a, b, c, rows=(0, 1))
-    per_row = time.perf_counter() - t0
-    rows = int(max(1, min(8, seconds / max(per_row, 1e-6))))
+    O.gemm_half(a4, b, c, rows=(0, 1))
+    t1 = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    O.gemm_half(a4, b, c, rows=(0, 4))
+    t4 = time.perf_counter() - t0
+    per_row = max((t4 - t1) / 3, 1e-6)
+    seconds = max(seconds - (t1 - per_row), per_row)
+    # as many rows as fill the requested CPU time (the sample is a row band)
+    rows = int(max(1, min(m, seconds / max(per_row, 1e-6))))
+    a = O.f32_to_half_bits(rng.uniform(-1, 1, (rows, k)).astype(np.float32))
     t0 = time.perf_counter()
     O.gemm_half(a, b, c, rows=(0, rows))
     dt = time.perf_counter() - t0
