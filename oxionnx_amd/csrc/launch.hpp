@@ -329,6 +329,7 @@ inline hipError_t launch_split_on(const LX& lx, const LY& ly, const Epi& epi, in
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   const int64_t groups = (int64_t)(Pp / 4) * Q;
+  if (groups > 0x7fffffff) return hipErrorInvalidValue;   // the reduction indexes groups in 32 bits
   const unsigned grid = (unsigned)std::min<int64_t>((groups + 255) / 256, 65535 * 4);
   hipLaunchKernelGGL((split_reduce_kernel<T, V, Epi>), dim3(grid), dim3(256), 0, st, reinterpret_cast<const T*>(ws),
                      splits, P, Pp, Q, epi);

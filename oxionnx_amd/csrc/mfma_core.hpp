@@ -686,15 +686,28 @@ __global__ void __launch_bounds__(256) split_reduce_kernel(const T* __restrict__
                                                            const Epi epi) {
   const int groups = Pp / 4;
   const int64_t n = (int64_t)groups * Q;
+  const int64_t slice = (int64_t)Q * Pp;   // elements per K slice
   const OutAddr out = epi.addr();
   for (int64_t g = (int64_t)blockIdx.x * 256 + threadIdx.x; g < n; g += (int64_t)gridDim.x * 256) {
-    const int j = (int)(g / groups), i0 = (int)(g - (int64_t)j * groups) * 4;
+    // n < 2^31 for every workspace the host sizes, so the index split is 32-bit
+    const int gi = (int)g;
+    const int j = gi / groups, i0 = (gi - j * groups) * 4;
     typename Epi::PreI pi;
     typename Epi::PreJ pj;
     epi.load_i(pi, i0);
     epi.load_j(pj, j);
-    A acc = *reinterpret_cast<const A*>(ws + (int64_t)j * Pp + i0);
-    for (int s = 1; s < splits; ++s) acc += *reinterpret_cast<const A*>(ws + ((int64_t)s * Q + j) * Pp + i0);
+    const T* src = ws + (int64_t)j * Pp + i0;
+    A acc = *reinterpret_cast<const A*>(src);
+    int s = 1;
+    // four slices' loads in flight before their adds; the adds stay in slice order
+    for (; s + 4 <= splits; s += 4) {
+      const A v0 = *reinterpret_cast<const A*>(src + s * slice);
+      const A v1 = *reinterpret_cast<const A*>(src + (s + 1) * slice);
+      const A v2 = *reinterpret_cast<const A*>(src + (s + 2) * slice);
+      const A v3 = *reinterpret_cast<const A*>(src + (s + 3) * slice);
+      acc += v0; acc += v1; acc += v2; acc += v3;
+    }
+    for (; s < splits; ++s) acc += *reinterpret_cast<const A*>(src + s * slice);
     uint32_t bits[4];
     epi.finish(pi, pj, i0, j, acc, bits);
     store_group(out, epi.out_bytes(), out.row(i0), i0, j, bits);
