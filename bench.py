@@ -292,8 +292,10 @@ def bench_widened(torch, ctx, L, stream, rng, only):
     * grouped 3x3 [1,256,56,56], 8 groups of 32 channels (one MFMA launch
       per group);
     * ConvTranspose 4x4 stride 2 [1,512,32,32] -> [1,256,64,64] (four
-      sub-pixel phases on the MFMA engine)."""
-    keys = ("depthwise_conv_f16", "grouped_conv_f16", "conv_transpose_f16")
+      sub-pixel phases on the MFMA engine);
+    * config 4's residual conv, 3x3 512 -> 512 at 32x32 (input staging,
+      split-K slices and their reduction included)."""
+    keys = ("depthwise_conv_f16", "grouped_conv_f16", "conv_transpose_f16", "conv_res_f16")
     if only and only not in keys:
         return {}
     out = {}
@@ -324,6 +326,16 @@ def bench_widened(torch, ctx, L, stream, rng, only):
                                                                     pads=(1, 1, 1, 1), out=y), 20, 2)
         fl = 2.0 * 512 * 32 * 32 * 256 * 16   # every input scatters a 4x4 tap into the output
         out[keys[2]] = {"ms": round(t, 5), "tflops": round(fl / t / 1e9, 2),
+                        "frac_mfma": round(fl / t / 1e9 / PEAK_TFLOPS["f16"], 4)}
+    if not only or only == keys[3]:
+        xr = torch.from_numpy(rng.uniform(-1, 1, (1, 512, 32, 32)).astype(np.float32)).cuda().half()
+        wt = ctx.weight_conv(rng.normal(0, 0.02, (512, 512, 3, 3)).astype(np.float32), dtype=L.F16)
+        y = torch.empty((1, 512, 32, 32), dtype=torch.float16, device="cuda")
+        f = lambda: ctx.conv2d(xr, wt, None, pads=(1, 1, 1, 1), out=y)
+        time_launches(torch, stream, f, 20, 5)
+        t = time_launches(torch, stream, f, 100, 0)
+        fl = 2.0 * 1024 * 512 * 4608
+        out[keys[3]] = {"ms": round(t, 5), "tflops": round(fl / t / 1e9, 2),
                         "frac_mfma": round(fl / t / 1e9 / PEAK_TFLOPS["f16"], 4)}
     return out
 
