@@ -289,8 +289,8 @@ def bench_widened(torch, ctx, L, stream, rng, only):
     f16 NCHW, operands resident:
     * depthwise 3x3 [1,256,56,56] (the direct kernel; memory-bound: GB/s of
       input + output + filter against HBM);
-    * grouped 3x3 [1,256,56,56], 8 groups of 32 channels (one MFMA launch
-      per group);
+    * grouped 3x3 [1,256,56,56], 8 groups of 32 channels (one MFMA launch,
+      the group on the grid z);
     * ConvTranspose 4x4 stride 2 [1,512,32,32] -> [1,256,64,64] (four
       sub-pixel phases on the MFMA engine);
     * config 4's residual conv, 3x3 512 -> 512 at 32x32 (input staging,

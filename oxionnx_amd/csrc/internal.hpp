@@ -39,6 +39,7 @@ struct Im2colOperand {
   int rows, kc, kwrap;
   uint32_t xor_mask;  // as DenseOperand::xor_mask
   const void* pad16;  // 16 bytes standing for a padding tap (stored before the XOR)
+  int64_t zstride;    // batched launch: slice z starts z * zstride bytes past base (0: one operand)
 };
 
 // Output mapping shared by both epilogues: element (i, j) lives at
@@ -109,6 +110,7 @@ inline size_t split_ws_bytes(int P, int Q, int splits) {
 struct FloatOut : OutMap {
   float alpha, beta;
   const void* bias;  // same element type as the output
+  int64_t bias_z;    // batched launch: slice z reads bias + z * bias_z elements (BIAS_I / BIAS_J)
   int bias_mode;
   int act;
   float lo, hi;

@@ -75,6 +75,7 @@ template <class OutT> struct FloatEpi {
   OutAddr out;
   float alpha, beta;
   const OutT* bias;
+  int64_t bias_z;     // batched launch: slice blockIdx.z reads bias + z * bias_z (BIAS_I / BIAS_J)
   int bias_mode;      // BIAS_*
   int bias_vec;       // bias is 16-byte aligned: runs of four load as one vector
   int act;
@@ -96,7 +97,7 @@ template <class OutT> struct FloatEpi {
 #pragma clang fp contract(off)
     if (bias_mode == BIAS_I) {
       OutT raw[4];
-      load4(bias, i, out.P, bias_vec, raw);
+      load4(bias + (int64_t)blockIdx.z * bias_z, i, out.P, bias_vec, raw);
 #pragma unroll
       for (int r = 0; r < 4; ++r) p.b[r] = i + r < out.P ? beta * to_f32(raw[r]) : 0.0f;
     } else {
@@ -108,7 +109,7 @@ template <class OutT> struct FloatEpi {
   __device__ __forceinline__ void load_j(PreJ& p, int j) const {
 #pragma clang fp contract(off)
     if (bias_mode == BIAS_J) {
-      const float x = to_f32(bias[clamp_index(j, out.Q)]);
+      const float x = to_f32(bias[(int64_t)blockIdx.z * bias_z + clamp_index(j, out.Q)]);
       p.b = j < out.Q ? beta * x : 0.0f;
     } else {
       p.b = -0.0f;
@@ -403,7 +404,8 @@ inline FloatEpi<OutT> make_float_epi(const FloatOut& o) {
   e.out = make_out_addr(o);
   e.alpha = o.alpha; e.beta = o.beta;
   e.bias = reinterpret_cast<const OutT*>(o.bias); e.bias_mode = o.bias ? o.bias_mode : BIAS_NONE;
-  e.bias_vec = ((uintptr_t)o.bias % 16) == 0;
+  e.bias_z = o.bias_z;
+  e.bias_vec = ((uintptr_t)o.bias % 16) == 0 && (o.bias_z * (int64_t)sizeof(OutT)) % 16 == 0;
   e.act = o.act; e.lo = o.lo; e.hi = o.hi;
   return e;
 }
@@ -435,6 +437,7 @@ inline Im2colNHWC make_im2col(const Im2colOperand& c) {
   r.sh = c.sh; r.sw = c.sw; r.dh = c.dh; r.dw = c.dw; r.pt = c.pt; r.pl = c.pl;
   r.rows = c.rows; r.kc = c.kc; r.kwrap = c.kwrap;
   r.pad = reinterpret_cast<const char*>(c.pad16);
+  r.zstride = c.zstride;
   return r;
 }
 

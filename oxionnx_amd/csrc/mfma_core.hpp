@@ -224,6 +224,7 @@ struct Im2colNHWC {
   int kc;              // KH * KW * cpc
   int kwrap;           // as DenseRows::kwrap
   const char* pad;     // 16 bytes that stand for a padding tap (and the K tail)
+  int64_t zstride;     // batched launch: slice blockIdx.z reads base + z * zstride
 
   template <int NR>
   struct State { const char* img[NR]; int iy0[NR], ix0[NR]; uint32_t okmask; int c; };
@@ -241,7 +242,7 @@ struct Im2colNHWC {
       const int rr = ok ? r : 0;
       const int n = rr / ohw, rem = rr - n * ohw;
       const int oy = rem / OW, ox = rem - oy * OW;
-      s.img[i] = base + (int64_t)n * H * W * pstride * 16;
+      s.img[i] = base + (int64_t)blockIdx.z * zstride + (int64_t)n * H * W * pstride * 16;
       s.iy0[i] = oy * sh - pt;
       s.ix0[i] = ox * sw - pl;
     }
@@ -553,8 +554,10 @@ mfma_gemm_kernel(const LX lx, const LY ly, const Epi epi, int nP, int nQ, int kc
                 "staging must fit the stage buffers");
   char* stg = reinterpret_cast<char*>(smem);
   int smode = 0;
-  if constexpr (Epi::kStageBytes > 0) smode = epi.staged_ok(Tl::BP) ? 1 : 0;
-  if constexpr (kWide) if (smode == 0 && epi.staged_wide_ok(Tl::BP)) smode = 2;
+  // the batch slice's own output must be 16-byte aligned too (the Epi checks slice 0's)
+  const bool zaligned = ((uintptr_t)out.y % 16) == 0;
+  if constexpr (Epi::kStageBytes > 0) smode = zaligned && epi.staged_ok(Tl::BP) ? 1 : 0;
+  if constexpr (kWide) if (smode == 0 && zaligned && epi.staged_wide_ok(Tl::BP)) smode = 2;
   const bool staged = smode != 0;
   if (staged) {
     wait_vmcnt<0>();

@@ -1175,7 +1175,8 @@ extern "C" int ohip_conv2d(ohip_ctx* ctx, const ohip_conv_desc* d, const void* x
 
   // Groups whose output or input channel span is too narrow to fill an MFMA
   // tile (depthwise, and small groups) run the direct kernel on the NCHW
-  // input; wider groups run one MFMA launch per group.  So do ungrouped
+  // input; wider groups run on the MFMA engine (one launch with the group on
+  // the grid z, or a launch per group under split-K).  So do ungrouped
   // convolutions of an NCHW input with under 32 taps x channels (an RGB stem,
   // whose 16-byte channel padding would multiply the staged bytes).  A long
   // reduction stays on the engine even for a few output channels: one
@@ -1253,7 +1254,12 @@ extern "C" int ohip_conv2d(ohip_ctx* ctx, const ohip_conv_desc* d, const void* x
     return fail(OHIP_E_INVALID, "ohip_conv2d: NHWC input must be 16-byte aligned");
   }
 
-  for (int64_t gi = 0; gi < G; ++gi) {
+  // Groups without split-K run as one launch, group = blockIdx.z: the input
+  // channel chunks, the weight rows, the bias and the output channels of
+  // group z sit at fixed strides from group 0's.  Split plans share one
+  // workspace, so those run a launch per group.
+  const bool one_launch = G > 1 && G <= 65535 && splits == 1;
+  for (int64_t gi = 0; gi < (one_launch ? 1 : G); ++gi) {
     Im2colOperand col{};
     col.base = static_cast<const char*>(xin) + gi * cp * eb;
     col.H = (int)sh_; col.W = (int)sw_; col.OH = (int)g.oh; col.OW = (int)g.ow;
@@ -1286,6 +1292,14 @@ extern "C" int ohip_conv2d(ohip_ctx* ctx, const ohip_conv_desc* d, const void* x
     DENSE_FITS_OR_DECLINE(wt, "ohip_conv2d");
     o.splits = splits;
     o.split_ws = splits > 1 ? scratch_at(ctx, plan, iw) : nullptr;
+    if (one_launch) {
+      col.zstride = cp * eb;
+      wt.zmod = (int)G; wt.zstride = coutg * w->ld_bytes;
+      o.batch = (int)G; o.zstride = nchw_out ? coutg * ohw * eb : coutg * eb;
+      o.bias_z = coutg;
+      // vector stores need every group's first output aligned, not only group 0's
+      o.vec = o.vec && o.zstride % (4 * eb) == 0;
+    }
     hipError_t e = run_conv_float(d->dtype, col, wt, col_on_x, o, sc.tile, ctx->stream);
     if (e != hipSuccess) return hip_fail(e, "ohip_conv2d launch");
   }

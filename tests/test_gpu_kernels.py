@@ -196,8 +196,12 @@ def test_conv_f32_matches_oracle(torch, ctx, case, act):
 
 # Grouped convolutions: (x shape, w shape, group, strides, pads, dilations).
 # Depthwise and narrow groups take the direct kernel, wide groups one MFMA
-# launch per group (channel slots per group padded to 16 bytes).
+# launch with the group on the grid's z (channel slots per group padded to 16
+# bytes); groups whose bias or output starts off 16-byte alignment included.
 GROUP_CASES = [
+    ((1, 32, 4, 5), (34, 16, 3, 3), 2, (1, 1), (1, 1, 1, 1), (1, 1)),       # 17 outputs a group: odd offsets
+    ((1, 60, 7, 9), (60, 20, 3, 3), 3, (1, 1), (1, 1, 1, 1), (1, 1)),       # 20 a group, 63 pixels
+    ((2, 48, 6, 6), (48, 16, 1, 1), 3, (1, 1), (0, 0, 0, 0), (1, 1)),       # 1x1, aligned groups
     ((2, 8, 11, 13), (8, 1, 3, 3), 8, (1, 1), (1, 1, 1, 1), (1, 1)),        # depthwise
     ((1, 6, 9, 9), (12, 1, 5, 5), 6, (2, 2), (2, 1, 2, 1), (1, 1)),         # depthwise, multiplier 2
     ((1, 6, 10, 10), (4, 3, 3, 3), 2, (1, 1), (1, 1, 1, 1), (2, 2)),        # narrow groups, dilated
