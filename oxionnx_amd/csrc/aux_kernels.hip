@@ -537,6 +537,25 @@ hipError_t run_stage_nhwc(int elem_bytes, const void* src, void* dst, int N, int
   }
 }
 
+// (n, co, oy, ox) of flat output index idx; 32-bit divisions when the
+// whole output indexes in 32 bits (64-bit division is a long instruction
+// sequence, and these kernels do little else per output)
+__device__ __forceinline__ void split_out_index(int64_t idx, int64_t total, int OW, int OH, int cout, int& ox, int& oy,
+                                                int& co, int& n) {
+  if (total <= 0x7fffffff) {
+    int r = (int)idx;
+    ox = r % OW; r /= OW;
+    oy = r % OH; r /= OH;
+    co = r % cout;
+    n = r / cout;
+  } else {
+    int64_t r = idx;
+    ox = (int)(r % OW); r /= OW;
+    oy = (int)(r % OH); r /= OH;
+    co = (int)(r % cout);
+    n = (int)(r / cout);
+  }
+}
 
 // ---------------------------------------------------------------- direct conv
 // Convolution for channel groups too narrow for the MFMA engine (depthwise
@@ -551,11 +570,8 @@ conv_direct_kernel(const T* __restrict__ x, const T* __restrict__ w, const T* __
                    DirectConvArgs a) {
   const int64_t total = (int64_t)a.N * a.cout * a.OH * a.OW;
   for (int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x; idx < total; idx += (int64_t)gridDim.x * 256) {
-    int64_t r = idx;
-    const int ox = (int)(r % a.OW); r /= a.OW;
-    const int oy = (int)(r % a.OH); r /= a.OH;
-    const int co = (int)(r % a.cout);
-    const int n = (int)(r / a.cout);
+    int ox, oy, co, n;
+    split_out_index(idx, total, a.OW, a.OH, a.cout, ox, oy, co, n);
     const int g = co / a.coutg;
     const T* xg = x + ((int64_t)n * a.C + (int64_t)g * a.cg) * a.H * a.W;
     const T* wr = w + (int64_t)co * a.ldw;
@@ -787,11 +803,8 @@ qconv_direct_kernel(const uint8_t* __restrict__ x, const int8_t* __restrict__ w,
 #pragma clang fp contract(off)
   const int64_t total = (int64_t)a.N * a.cout * a.OH * a.OW;
   for (int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x; idx < total; idx += (int64_t)gridDim.x * 256) {
-    int64_t r = idx;
-    const int ox = (int)(r % a.OW); r /= a.OW;
-    const int oy = (int)(r % a.OH); r /= a.OH;
-    const int co = (int)(r % a.cout);
-    const int n = (int)(r / a.cout);
+    int ox, oy, co, n;
+    split_out_index(idx, total, a.OW, a.OH, a.cout, ox, oy, co, n);
     const int g = co / a.coutg;
     const uint8_t* xg = x + ((int64_t)n * a.C + (int64_t)g * a.cg) * a.H * a.W;
     const int8_t* wr = w + (int64_t)co * a.ldw;
@@ -858,11 +871,8 @@ convt_kernel(const T* __restrict__ x, const T* __restrict__ w, const T* __restri
 #pragma clang fp contract(off)
   const int64_t total = (int64_t)a.N * a.cout * a.OH * a.OW;
   for (int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x; idx < total; idx += (int64_t)gridDim.x * 256) {
-    int64_t r = idx;
-    const int ox = (int)(r % a.OW); r /= a.OW;
-    const int oy = (int)(r % a.OH); r /= a.OH;
-    const int co = (int)(r % a.cout);
-    const int n = (int)(r / a.cout);
+    int ox, oy, co, n;
+    split_out_index(idx, total, a.OW, a.OH, a.cout, ox, oy, co, n);
     const int g = co / a.coutg, oc = co - g * a.coutg;
     const int ty = oy + a.pt, tx = ox + a.pl;
     float acc = 0.0f;
