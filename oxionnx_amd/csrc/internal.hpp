@@ -40,6 +40,8 @@ struct Im2colOperand {
   uint32_t xor_mask;  // as DenseOperand::xor_mask
   const void* pad16;  // 16 bytes standing for a padding tap (stored before the XOR)
   int64_t zstride;    // batched launch: slice z starts z * zstride bytes past base (0: one operand)
+  int zpads;          // > 0: slice z (< zpads <= 4) uses pads zpt[z], zpl[z]
+  int zpt[4], zpl[4];
 };
 
 // Output mapping shared by both epilogues: element (i, j) lives at
@@ -53,6 +55,8 @@ struct OutMap {
   void* split_ws;  // splits * Q * round_up(P, 4) accumulators (4 bytes each)
   int batch;       // > 1: a batched launch of `batch` independent contractions (no split-K)
   int64_t zstride; // bytes between the batch slices' outputs
+  int zsw;         // > 0: slice z's output starts at (z / zsw) * zrow + (z % zsw) * zstride
+  int64_t zrow;
 };
 
 // Split-K plan.  The slices run on the 64x64 four-stage tile when its

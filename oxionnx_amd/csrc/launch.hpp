@@ -395,6 +395,7 @@ inline OutAddr make_out_addr(const OutMap& o) {
   magic_div(a.ohw, &a.ohw_mul, &a.ohw_shift);
   a.P = o.P; a.Q = o.Q; a.vec = o.vec;
   a.batch = o.batch > 1 ? o.batch : 1; a.zstride = o.zstride;
+  a.zsw = o.zsw; a.zrow = o.zrow;
   return a;
 }
 
@@ -438,6 +439,8 @@ inline Im2colNHWC make_im2col(const Im2colOperand& c) {
   r.rows = c.rows; r.kc = c.kc; r.kwrap = c.kwrap;
   r.pad = reinterpret_cast<const char*>(c.pad16);
   r.zstride = c.zstride;
+  r.zpads = c.zpads;
+  for (int i = 0; i < 4; ++i) { r.zpt[i] = c.zpt[i]; r.zpl[i] = c.zpl[i]; }
   return r;
 }
 

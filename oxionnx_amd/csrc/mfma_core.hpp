@@ -225,6 +225,8 @@ struct Im2colNHWC {
   int kwrap;           // as DenseRows::kwrap
   const char* pad;     // 16 bytes that stand for a padding tap (and the K tail)
   int64_t zstride;     // batched launch: slice blockIdx.z reads base + z * zstride
+  int zpads;           // > 0: slice z (< zpads <= 4) uses pads zpt[z], zpl[z] instead of pt, pl
+  int zpt[4], zpl[4];
 
   template <int NR>
   struct State { const char* img[NR]; int iy0[NR], ix0[NR]; uint32_t okmask; int c; };
@@ -233,6 +235,8 @@ struct Im2colNHWC {
   __device__ __forceinline__ void init(State<NR>& s, int row0, int lane, int wave) const {
     s.c = dma_chunk<CH>(lane, wave);
     const int ohw = OH * OW;
+    const int z = (int)blockIdx.z;
+    const int pt_ = zpads > 0 ? zpt[z & 3] : pt, pl_ = zpads > 0 ? zpl[z & 3] : pl;
     s.okmask = 0;
 #pragma unroll
     for (int i = 0; i < NR; ++i) {
@@ -243,8 +247,8 @@ struct Im2colNHWC {
       const int n = rr / ohw, rem = rr - n * ohw;
       const int oy = rem / OW, ox = rem - oy * OW;
       s.img[i] = base + (int64_t)blockIdx.z * zstride + (int64_t)n * H * W * pstride * 16;
-      s.iy0[i] = oy * sh - pt;
-      s.ix0[i] = ox * sw - pl;
+      s.iy0[i] = oy * sh - pt_;
+      s.ix0[i] = ox * sw - pl_;
     }
   }
   struct Step { int dy, dx, cc; bool kin; };
@@ -359,6 +363,8 @@ struct OutAddr {
   int stage;         // the staged epilogue may be used
   int batch;         // > 1: batched launch, slice blockIdx.z
   int64_t zstride;   // bytes between the slices' outputs
+  int zsw;           // > 0: slice z starts (z / zsw) * zrow + (z % zsw) * zstride bytes in
+  int64_t zrow;
   __device__ __forceinline__ int64_t row(int i) const {
     if (bstride == 0) return (int64_t)i * si;
     const int n = (int)(((uint64_t)(uint32_t)i * ohw_mul) >> ohw_shift);
@@ -534,7 +540,11 @@ mfma_gemm_kernel(const LX lx, const LY ly, const Epi epi, int nP, int nQ, int kc
   const int ibase = p0 + wp * Tl::TP * 32 + (lane >> 5) * 4;
   const int jbase = q0 + wq * Tl::TQ * 32 + (lane & 31);
   OutAddr out = epi.addr();
-  if (out.batch > 1) out.y += (int64_t)blockIdx.z * out.zstride;
+  if (out.batch > 1) {
+    const int z = (int)blockIdx.z;
+    out.y += out.zsw > 0 ? (int64_t)(z / out.zsw) * out.zrow + (int64_t)(z % out.zsw) * out.zstride
+                         : (int64_t)z * out.zstride;
+  }
 
   // the per-column epilogue terms, loaded once for all of this lane's rows
   typename Epi::PreJ pj[Tl::TQ];

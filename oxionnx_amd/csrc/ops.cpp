@@ -85,6 +85,10 @@ struct ohip_weight {
   // residues (ph_pt, ph_pl); empty when the gather kernel serves the node.
   std::vector<ohip_weight*> phases;
   int64_t ph_sh = 0, ph_sw = 0, ph_pt = 0, ph_pl = 0;
+  // all phase filters in one allocation, phase z at z * ph_zstride bytes
+  // (when every phase has the same tap count and there are at most four)
+  ohip_weight* ph_all = nullptr;
+  int64_t ph_zstride = 0;
 };
 
 // Stream-ordered caching pool for device buffers (activations, staging).
@@ -230,6 +234,7 @@ extern "C" int ohip_ctx_create(int device, ohip_ctx** out) {
 static void weight_free(ohip_weight* w) {
   if (!w) return;
   for (auto* p : w->phases) weight_free(p);
+  if (w->ph_all) weight_free(w->ph_all);
   if (w->data) (void)hipFree(w->data);
   if (w->colsum) (void)hipFree(w->colsum);
   if (w->flip) (void)hipFree(w->flip);
@@ -769,6 +774,8 @@ extern "C" int ohip_weight_conv_transpose(ohip_ctx* ctx, const ohip_weight_key* 
   if (phased) {
     w->ph_sh = stride_h; w->ph_sw = stride_w; w->ph_pt = pad_t % stride_h; w->ph_pl = pad_l % stride_w;
     const int64_t ce = chunk_elems(dt), cp = round_up(cin, ce);
+    std::vector<char> all;   // every phase's packed filter, in phase order
+    int64_t all_kp = 0;      // their common K extent (-1: they differ)
     for (int64_t ry = 0; ry < stride_h; ++ry)
       for (int64_t rx = 0; rx < stride_w; ++rx) {
         const int64_t ky0 = (ry + pad_t) % stride_h, kx0 = (rx + pad_l) % stride_w;
@@ -790,7 +797,22 @@ extern "C" int ohip_weight_conv_transpose(ohip_ctx* ctx, const ohip_weight_key* 
         if (rc) { weight_free(ph); weight_free(w); return rc; }
         w->bytes += ph->bytes;
         w->phases.push_back(ph);
+        all.insert(all.end(), packed.begin(), packed.end());
+        if (all_kp == 0) all_kp = kp;
+        if (kp != all_kp) all_kp = -1;
       }
+    const int64_t nph = stride_h * stride_w;
+    if (all_kp > 0 && nph <= 4) {
+      auto* pa = new ohip_weight();
+      pa->ctx = ctx; pa->kind = WK_CONV; pa->dtype = dt; pa->rows = coutg; pa->k = cin;
+      pa->kh = w->phases[0]->kh; pa->kw = w->phases[0]->kw; pa->cpc = w->phases[0]->cpc; pa->kc = w->phases[0]->kc;
+      pa->ld_bytes = all_kp * eb;
+      rc = weight_upload(ctx, pa, all.data(), all.size());
+      if (rc) { weight_free(pa); weight_free(w); return rc; }
+      w->bytes += pa->bytes;
+      w->ph_all = pa;
+      w->ph_zstride = coutg * all_kp * eb;
+    }
   }
   return weight_finish(ctx, key, ks, w, out);
 }
@@ -1132,6 +1154,15 @@ static bool few_out_allowed() {
   return v;
 }
 
+// OHIP_CONVT_ONE=0 runs ConvTranspose phases as a launch each (a measurement switch)
+static bool ph_one_launch() {
+  static const bool v = [] {
+    const char* e = std::getenv("OHIP_CONVT_ONE");
+    return !(e && e[0] == '0');
+  }();
+  return v;
+}
+
 extern "C" int ohip_conv2d(ohip_ctx* ctx, const ohip_conv_desc* d, const void* x, const ohip_weight* w,
                            const void* bias, void* y) {
   int rc = activate(ctx);
@@ -1394,6 +1425,47 @@ extern "C" int ohip_conv_transpose2d(ohip_ctx* ctx, const ohip_convt_desc* d, co
     void* px = scratch_at(ctx, plan, ix);
     HIP_TRY(run_nchw_to_nhwc(eb, x, px, (int)d->n, (int)d->c, (int)(d->h * d->w), (int)cp, ctx->stream),
             "NCHW -> NHWC");
+    // Every phase in one launch, phase z = ry * sw + rx on the grid's z, when
+    // the phases share one filter allocation and one output grid and none
+    // needs split-K: the phase's pads, filter and output offset follow z.
+    const int64_t ohp0 = oh / sh, owp0 = ow / sw;
+    const int64_t blocks64 = ((ohp0 * owp0 + 63) / 64) * ((d->cout + 63) / 64) * sh * sw;
+    if (w->ph_all && oh % sh == 0 && ow % sw == 0 && ohp0 > 0 && owp0 > 0 && ph_one_launch() &&
+        (blocks64 >= 256 ||
+         plan_splits((int)(ohp0 * owp0), (int)d->cout, w->ph_all->kc, ctx->tile_override) == 1)) {
+      const ohip_weight* pa = w->ph_all;
+      for (int64_t n = 0; n < d->n; ++n) {
+        Im2colOperand col{};
+        col.base = static_cast<const char*>(px) + n * d->h * d->w * cp * eb;
+        col.H = (int)d->h; col.W = (int)d->w; col.OH = (int)ohp0; col.OW = (int)owp0;
+        col.KW = (int)pa->kw; col.cpc = (int)(cp / ce);
+        col.sh = 1; col.sw = 1; col.dh = 1; col.dw = 1;
+        col.rows = (int)(ohp0 * owp0); col.kc = pa->kc;
+        col.xor_mask = 0; col.pad16 = pad16(ctx, 0);
+        col.zpads = (int)(sh * sw);
+        for (int64_t ry = 0; ry < sh; ++ry)
+          for (int64_t rx = 0; rx < sw; ++rx) {
+            const int64_t ky0 = (ry + d->pad_t) % sh, kx0 = (rx + d->pad_l) % sw;
+            const int64_t c0y = (ry + d->pad_t - ky0) / sh, c0x = (rx + d->pad_l - kx0) / sw;
+            col.zpt[ry * sw + rx] = (int)(pa->kh - 1 - c0y);
+            col.zpl[ry * sw + rx] = (int)(pa->kw - 1 - c0x);
+          }
+        col.pt = col.zpt[0]; col.pl = col.zpl[0];
+        DenseOperand wt{pa->data, pa->ld_bytes, (int)d->cout, pa->kc, 0, 0u, pad16(ctx, 0), (int)(sh * sw),
+                        w->ph_zstride};
+        FloatOut o{};
+        o.y = static_cast<char*>(y) + n * d->cout * oh * ow * eb;
+        o.alpha = 1.0f; o.beta = 1.0f; o.bias = bias; o.bias_mode = BIAS_J; o.act = ACT_NONE;
+        o.si = sw; o.sj = oh * ow; o.bstride = sh * ow; o.ohw = (int)owp0;
+        o.P = (int)(ohp0 * owp0); o.Q = (int)d->cout; o.vec = 0;
+        o.splits = 1; o.split_ws = nullptr;
+        o.batch = (int)(sh * sw); o.zsw = (int)sw; o.zrow = ow * eb; o.zstride = eb;   // phase (ry, rx) at ry * ow + rx
+        DENSE_FITS_OR_DECLINE(wt, "ohip_conv_transpose2d");
+        hipError_t e = run_conv_float(d->dtype, col, wt, true, o, ctx->tile_override, ctx->stream);
+        if (e != hipSuccess) return hip_fail(e, "ohip_conv_transpose2d phase launch");
+      }
+      return OHIP_OK;
+    }
     for (int64_t n = 0; n < d->n; ++n)
       for (int64_t ry = 0; ry < sh; ++ry)
         for (int64_t rx = 0; rx < sw; ++rx) {

@@ -284,6 +284,8 @@ CONVT_CASES = [
     ((1, 4, 6, 5), (4, 3, 3, 2), dict(strides=[1, 3], pads=[0, 1, 2, 0], dilations=[2, 1])),
     ((1, 16, 4, 4), (16, 1, 3, 3), dict(strides=[2, 2], group=16)),
     ((1, 64, 8, 8), (64, 32, 4, 4), dict(strides=[2, 2], pads=[1, 1, 1, 1])),
+    ((2, 32, 5, 6), (32, 24, 2, 2), dict(strides=[2, 2], pads=[0, 0, 0, 0])),          # phases in one launch
+    ((1, 128, 16, 16), (128, 64, 4, 4), dict(strides=[2, 2], pads=[1, 2, 1, 2])),      # one launch, uneven pads
     ((2, 24, 5, 7), (24, 40, 3, 3), dict(strides=[1, 1], pads=[1, 0, 0, 2])),
     ((1, 32, 6, 5), (32, 16, 5, 3), dict(strides=[3, 2], pads=[2, 1, 1, 0], output_padding=[2, 1])),
 ]
