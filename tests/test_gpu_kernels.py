@@ -247,6 +247,8 @@ BMM_CASES = [
     ((4, 1, 5, 7), (3, 7, 4)),
     ((8, 128, 96), (96, 160)),
     ((1, 33, 21), (6, 21, 70)),
+    ((4, 5, 64), (64, 36)),      # 2-byte slices start 8 bytes off a 16-byte boundary
+    ((2, 37, 96), (96, 12)),
 ]
 
 
