@@ -1718,8 +1718,11 @@ extern "C" int ohip_try_dispatch(ohip_ctx* ctx, const ohip_node* node, int place
   std::memset(out, 0, sizeof(*out));
   for (int i = 0; i < node->n_inputs; ++i) {
     const ohip_tensor& t = node->inputs[i];
-    if (t.device && !ohip_accepts_resident_slot(node->op_type, i))
-      return decline("resident operand in a host-read slot");
+    if (t.device && !ohip_accepts_resident_slot(node->op_type, i)) {
+      decline(std::string(node->op_type) + ": resident operand in host-read slot " + std::to_string(i));
+      ohip_note_declined(ctx, t_err.c_str());
+      return OHIP_DECLINED;
+    }
   }
   std::vector<ohip_tensor> ins;
   std::vector<ohip_dtensor*> temps;

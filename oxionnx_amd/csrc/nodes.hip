@@ -129,11 +129,15 @@ __global__ void __launch_bounds__(kThreads) instnorm_kernel(const T* __restrict_
     bi = aff.same_type ? ldf(static_cast<const T*>(aff.bias), ai) : static_cast<const float*>(aff.bias)[ai];
     affine = true;
   }
+  // A fused affine tail keeps the unfused chain's storage roundings: the
+  // normalised value, the product and the sum are each rounded to T, as the
+  // OxiInstanceNorm -> Mul -> Add nodes store them.
   for (int64_t i = threadIdx.x; i < spatial; i += kThreads) {
     float v = (ldf(xp, i) - mean) * inv;
     if (affine) {
-      if (aff.scale) v = v * sc;
-      if (aff.bias) v = v + bi;
+      v = (float)(T)v;
+      if (aff.scale) v = (float)(T)(v * sc);
+      if (aff.bias) v = (float)(T)(v + bi);
     }
     if (aff.act == UN_RELU) v = v > 0.0f ? v : 0.0f;
     else if (aff.act == UN_LEAKY_RELU) v = v >= 0.0f ? v : v * aff.alpha;

@@ -3,11 +3,13 @@ workloads (face-swap generator f32 / f16, int8 YOLOv8n-style backbone),
 through the node-level C ABI (ohip_try_dispatch via ep / session) against
 the CPU graph executor oracle.graph_ref.
 
-Bars: byte / integer paths bit-exact; f32 nodes within 1e-4 of the output
-magnitude, f16 within 1e-2.  End to end the float generator is checked on
-its pre-Tanh logits, f32 within 2e-4 of their magnitude over 27 contractions
-and 12 instance norms, f16 within 3e-2, and its Tanh output within the same
-absolute bound (Tanh is 1-Lipschitz).
+Bars: byte / integer paths bit-exact; f32 within 1e-4 and f16 within 1e-2
+of the output magnitude (max |reference|).  End to end the float generator's
+pre-Tanh logits are held to that bar; its Tanh output y is held to 1e-4 of
+max |y| in f32, and in f16 to the logits' absolute bound (Tanh is
+1-Lipschitz) plus an accuracy bar against the f32 forward: the reference's
+own f16 y differs from its f32 y by 2.9e-2 of max |y|, so a 1e-2 bar relative
+to max |y| would be finer than the reference's own f16 arithmetic.
 """
 import numpy as np
 import pytest
@@ -59,9 +61,9 @@ def close(got, ref, tol):
     got = np.asarray(got, np.float32)
     ref = np.asarray(ref, np.float32)
     assert got.shape == ref.shape
-    scale = max(1.0, float(np.abs(ref).max()))
+    scale = float(np.abs(ref).max())
     err = float(np.abs(got - ref).max())
-    assert err <= tol * scale, (err, scale)
+    assert err <= tol * scale or err == 0.0, (err, scale)
 
 
 RNG = np.random.default_rng(11)
@@ -359,9 +361,8 @@ def test_face_swap_generator_f32_end_to_end(ctx):
     assert len(sess.graph.nodes) < len(g.nodes)  # Conv + LeakyRelu fused
     out = sess.run(feeds)
     ref = G.run_graph(g, feeds)
-    close(out["logits"], ref["logits"], 2e-4)
-    bound = 2e-4 * max(1.0, float(np.abs(ref["logits"]).max()))
-    assert float(np.abs(out["y"] - ref["y"]).max()) <= bound
+    close(out["logits"], ref["logits"], 1e-4)
+    close(out["y"], ref["y"], 1e-4)
 
 
 def test_face_swap_generator_f16_end_to_end(ctx):
@@ -369,10 +370,19 @@ def test_face_swap_generator_f16_end_to_end(ctx):
     out = Session(g, ctx).run(feeds)
     ref = G.run_graph(g, feeds, half=True)
     assert out["y"].dtype == np.float16
-    close(out["logits"], ref["logits"], 3e-2)
+    close(out["logits"], ref["logits"], 1e-2)
     # tanh is 1-Lipschitz: y is held to the logits' absolute bound
-    bound = 3e-2 * max(1.0, float(np.abs(ref["logits"]).max()))
+    bound = 1e-2 * float(np.abs(ref["logits"]).max())
     assert float(np.abs(out["y"].astype(np.float32) - ref["y"]).max()) <= bound
+    # accuracy: against the f32 forward of the same weights (f16-rounded), the
+    # device f16 forward is as close as the reference's f16 forward is
+    g32, _ = workloads.face_swap_generator(dtype="f32")
+    g32.initializers.update({k: np.asarray(v, np.float32) for k, v in g.initializers.items()})
+    exact = G.run_graph(g32, {k: v.astype(np.float32) for k, v in feeds.items()})
+    for k in ("logits", "y"):
+        e_dev = float(np.abs(out[k].astype(np.float32) - exact[k]).max())
+        e_ref = float(np.abs(ref[k] - exact[k]).max())
+        assert e_dev <= 1.25 * e_ref, (k, e_dev, e_ref)
 
 
 @pytest.mark.parametrize("which", ["yolo", "face_f16"])
