@@ -233,6 +233,107 @@ case("test_gemm_f16_parity", "oxionnx-ops/tests/gemm_native_dtype_test.rs:320-38
      {"a": T(GA, [4, 4]), "b": T(GB, [4, 4]), "c": T(GC, [4])},
      {"alpha": 0.5, "beta": 0.5, "transA": 0, "transB": 0}, exp, [4, 4], tol=1e-2)
 
+
+# ---- graph nodes of the end-to-end workloads (oracle/graph_ref.py) --------
+# Nearest Resize: oxionnx-ops/tests/w1_resize.rs:144-151 (inputs d14 / d22 /
+# d45), :8-23 (expected rows), :200-263, :590-611, :613-637.
+D14 = T([1.0, 2.0, 3.0, 4.0], [1, 1, 1, 4])
+D22 = T([1.0, 2.0, 3.0, 4.0], [1, 1, 2, 2])
+rz = "oxionnx-ops/tests/w1_resize.rs"
+for mode, exp in [("round_prefer_floor", [1.0, 1.0, 2.0, 2.0, 3.0, 3.0, 4.0, 4.0]),
+                  ("round_prefer_ceil", [1.0, 1.0, 2.0, 2.0, 3.0, 3.0, 4.0, 4.0]),
+                  ("floor", [1.0, 1.0, 1.0, 2.0, 2.0, 3.0, 3.0, 4.0]),
+                  ("ceil", [1.0, 2.0, 2.0, 3.0, 3.0, 4.0, 4.0, 4.0])]:
+    case(f"resize_nearest_half_pixel_{mode}", rz + ":8-11,219-233", "Resize",
+         {"x": D14, "scales": T([1.0, 1.0, 1.0, 2.0], [4])},
+         {"mode": "nearest", "coordinate_transformation_mode": "half_pixel", "nearest_mode": mode},
+         exp, [1, 1, 1, 8])
+case("resize_nearest_asymmetric_prefer_floor", rz + ":14-17,236-248", "Resize",
+     {"x": D22, "scales": T([1.0, 1.0, 2.0, 2.0], [4])},
+     {"mode": "nearest", "coordinate_transformation_mode": "asymmetric", "nearest_mode": "round_prefer_floor"},
+     [1.0, 1.0, 2.0, 2.0, 1.0, 1.0, 2.0, 2.0, 3.0, 3.0, 4.0, 4.0, 3.0, 3.0, 4.0, 4.0], [1, 1, 4, 4])
+case("resize_nearest_asymmetric_prefer_ceil", rz + ":19-23,250-262", "Resize",
+     {"x": D22, "scales": T([1.0, 1.0, 2.0, 2.0], [4])},
+     {"mode": "nearest", "coordinate_transformation_mode": "asymmetric", "nearest_mode": "round_prefer_ceil"},
+     [1.0, 2.0, 2.0, 2.0, 3.0, 4.0, 4.0, 4.0, 3.0, 4.0, 4.0, 4.0, 3.0, 4.0, 4.0, 4.0], [1, 1, 4, 4])
+case("resize_nearest_tf_half_pixel_for_nn", rz + ":590-611", "Resize",
+     {"x": D14, "scales": T([1.0, 1.0, 1.0, 2.0], [4])},
+     {"mode": "nearest", "coordinate_transformation_mode": "tf_half_pixel_for_nn",
+      "nearest_mode": "round_prefer_floor"},
+     [1.0, 2.0, 2.0, 3.0, 3.0, 4.0, 4.0, 4.0], [1, 1, 1, 8])
+for sc, hw in [(0.5, [2, 2]), (0.6, [2, 3]), (1.3, [5, 6]), (2.7, [10, 13])]:
+    case(f"resize_output_shape_floor_{sc}", rz + ":613-637", "ResizeShape",
+         {"x": T(iota(20), [1, 1, 4, 5]), "scales": T([1.0, 1.0, sc, sc], [4])},
+         {"mode": "nearest", "coordinate_transformation_mode": "half_pixel"}, None, [1, 1] + hw)
+# Upsample-9 (scales input): the asymmetric mapping, tests/w2_vision_ops_e2e.rs:578-608
+case("upsample_nearest_scales_input_is_asymmetric", "tests/w2_vision_ops_e2e.rs:578-608", "Resize",
+     {"x": D22, "scales": T([1.0, 1.0, 2.0, 2.0], [4])},
+     {"mode": "nearest", "coordinate_transformation_mode": "asymmetric", "nearest_mode": "floor"},
+     [1., 1., 2., 2., 1., 1., 2., 2., 3., 3., 4., 4., 3., 3., 4., 4.], [1, 1, 4, 4])
+case("upsample_nearest_scales_attribute", "tests/w2_vision_ops_e2e.rs:610-640", "Resize",
+     {"x": D22, "scales": T([1.0, 1.0, 2.0, 3.0], [4])},
+     {"mode": "nearest", "coordinate_transformation_mode": "asymmetric", "nearest_mode": "floor"},
+     [1., 1., 1., 2., 2., 2., 1., 1., 1., 2., 2., 2., 3., 3., 3., 4., 4., 4., 3., 3., 3., 4., 4., 4.],
+     [1, 1, 4, 6])
+
+# MaxPool (floor mode): tests/conformance_conv.rs:94-126, tests/op_conv_tests.rs:111-141,
+# oxionnx-ops/tests/w1_conv_pool.rs:276-328
+case("conformance_maxpool_2x2", "tests/conformance_conv.rs:94-126", "MaxPool",
+     {"x": T([float(v) for v in range(1, 17)], [1, 1, 4, 4])},
+     {"kernel_shape": [2, 2], "strides": [2, 2], "pads": [0, 0, 0, 0]}, [6.0, 8.0, 14.0, 16.0], [1, 1, 2, 2])
+case("test_maxpool", "tests/op_conv_tests.rs:111-141", "MaxPool",
+     {"x": T([float(v) for v in range(1, 17)], [1, 1, 4, 4])},
+     {"kernel_shape": [2, 2], "strides": [2, 2], "pads": [0, 0, 0, 0]}, [6.0, 8.0, 14.0, 16.0], [1, 1, 2, 2])
+case("max_pool_floor_5x5_k2_s2", "oxionnx-ops/tests/w1_conv_pool.rs:294-303", "MaxPool",
+     {"x": T(iota(25), [1, 1, 5, 5])}, {"kernel_shape": [2, 2], "strides": [2, 2]},
+     [6.0, 8.0, 16.0, 18.0], [1, 1, 2, 2])
+case("max_pool_floor_4x4_k3_s2", "oxionnx-ops/tests/w1_conv_pool.rs:323-328", "MaxPool",
+     {"x": T(iota(16), [1, 1, 4, 4])}, {"kernel_shape": [3, 3], "strides": [2, 2]}, [10.0], [1, 1, 1, 1])
+
+# Pad: oxionnx-ops/src/shape/tests.rs:187-199 (reflect), oxionnx-ops/tests/stitch_s2_shape.rs:154-167
+# (an empty constant_value falls back to 0)
+case("test_pad_reflect", "oxionnx-ops/src/shape/tests.rs:187-199", "Pad",
+     {"x": T([1.0, 2.0, 3.0, 4.0, 5.0, 6.0], [2, 3]), "pads": T([0, 1, 0, 1], [4])},
+     {"mode": "reflect"}, [2.0, 1.0, 2.0, 3.0, 2.0, 5.0, 4.0, 5.0, 6.0, 5.0], [2, 5])
+case("pad_constant_default_zero", "oxionnx-ops/tests/stitch_s2_shape.rs:154-167", "Pad",
+     {"x": T([1.0, 2.0], [2]), "pads": T([1, 1], [2])}, {"mode": "constant"}, [0.0, 1.0, 2.0, 0.0], [4])
+
+# QuantizeLinear / DequantizeLinear (per tensor): tests/conformance_quant.rs:13-62,
+# oxionnx-ops/tests/w1_indexing_quant.rs:420-476 (each per-axis row there taken as a per-tensor case)
+qsrc = "oxionnx-ops/tests/w1_indexing_quant.rs"
+case("conformance_quantize", "tests/conformance_quant.rs:13-62", "QuantizeLinear",
+     {"x": T([0.0, 1.0, 2.0, 3.0, 4.0], [5]), "scale": T([0.1], [1]), "zp": T([0.0], [1])}, {},
+     [0.0, 10.0, 20.0, 30.0, 40.0], [5])
+case("conformance_dequantize", "tests/conformance_quant.rs:13-62", "DequantizeLinear",
+     {"x": T([0.0, 10.0, 20.0, 30.0, 40.0], [5]), "scale": T([0.1], [1]), "zp": T([0.0], [1])}, {},
+     [0.0, 1.0, 2.0, 3.0, 4.0], [5], tol=0.1)
+case("quantize_ties_to_even_row1", qsrc + ":421-439", "QuantizeLinear",
+     {"x": T([4.0, 5.0, 6.0], [3]), "scale": T([10.0], [1])}, {}, [0.0, 0.0, 1.0], [3])
+case("quantize_ties_to_even_columns", qsrc + ":441-453", "QuantizeLinear",
+     {"x": T([2.0, 5.0], [2]), "scale": T([2.0], [1])}, {}, [1.0, 2.0], [2])
+case("quantize_zero_point_row1", qsrc + ":455-465", "QuantizeLinear",
+     {"x": T([7.0, 3.0], [2]), "scale": T([1.0], [1]), "zp": T([100.0], [1])}, {}, [107.0, 103.0], [2])
+case("dequantize_row0", qsrc + ":467-476", "DequantizeLinear",
+     {"x": T([10.0, 20.0], [2]), "scale": T([2.0], [1]), "zp": T([1.0], [1])}, {}, [18.0, 38.0], [2], tol=0.0)
+case("dequantize_row1", qsrc + ":467-476", "DequantizeLinear",
+     {"x": T([30.0, 40.0], [2]), "scale": T([0.5], [1]), "zp": T([2.0], [1])}, {}, [14.0, 19.0], [2], tol=0.0)
+
+# Unary activations: tests/w3_simd_scalar_reference_equivalence.rs:61-63 (input A),
+# :156-173 (Sigmoid), :176-193 (Tanh), :227-244 (SiLU); tests/op_nn_tests.rs:404-421 (LeakyRelu)
+UA = [-3.0, -1.5, -0.5, -0.001, 0.0, 0.001, 0.25, 0.5, 1.0, 1.5, 2.0, 4.5]
+us = "tests/w3_simd_scalar_reference_equivalence.rs"
+case("sigmoid_matches_numpy_reference", us + ":156-173", "Sigmoid", {"x": T(UA, [12])}, {},
+     [0.047425873, 0.18242553, 0.37754068, 0.49975, 0.5, 0.50025, 0.5621765, 0.62245935, 0.7310586,
+      0.8175745, 0.8807971, 0.9890131], [12], tol=1e-6)
+case("tanh_matches_numpy_reference", us + ":176-193", "Tanh", {"x": T(UA, [12])}, {},
+     [-0.9950548, -0.90514827, -0.46211717, -0.0009999997, 0.0, 0.0009999997, 0.24491866, 0.46211717,
+      0.7615942, 0.90514827, 0.9640276, 0.99975324], [12], tol=1e-6)
+case("silu_matches_numpy_reference", us + ":227-244", "Silu", {"x": T(UA, [12])}, {},
+     [-0.14227762, -0.27363828, -0.18877034, -0.00049975, 0.0, 0.00050025, 0.14054413, 0.31122968,
+      0.7310586, 1.2263618, 1.7615942, 4.4505587], [12], tol=1e-6)
+case("test_leaky_relu", "tests/op_nn_tests.rs:404-421", "LeakyRelu", {"x": T([-10.0, -1.0, 0.0, 1.0, 10.0], [5])},
+     {"alpha": 0.1}, [-1.0, -0.1, 0.0, 1.0, 10.0], [5], tol=1e-5)
+
 if __name__ == "__main__":
     here = os.path.dirname(os.path.abspath(__file__))
     with open(os.path.join(here, "reference_vectors.json"), "w") as f:

@@ -455,3 +455,47 @@ def test_adain_fusion(ctx, relu, dt):
     out = Session(g, ctx).run(feeds)
     ref = G.run_graph(g, feeds, half=dt == np.float16)
     close(out["y"], ref["y"], 1e-4 if dt == np.float32 else 1e-2)
+
+
+def _golden_attrs(d):
+    a = A()
+    for k, v in d.items():
+        if isinstance(v, list):
+            a.int_lists[k] = v
+        elif isinstance(v, str):
+            a.strings[k] = v
+        elif isinstance(v, float):
+            a.floats[k] = v
+        else:
+            a.ints[k] = v
+    return a
+
+
+_NODE_GOLDEN = [c for op in ("Resize", "MaxPool", "Pad", "QuantizeLinear", "DequantizeLinear", "Sigmoid", "Tanh",
+                             "Silu", "LeakyRelu") for c in __import__("tests._golden", fromlist=["cases"]).cases(op)]
+
+
+@pytest.mark.parametrize("c", _NODE_GOLDEN, ids=lambda c: c["name"])
+def test_node_golden_vectors_on_the_device(ctx, c):
+    """The reference's known answers for the memory-bound nodes, through the
+    device kernels (resident input, one node)."""
+    from tests import _golden as GV
+    x = GV.arr(c, "x")
+    if c["op"] == "Resize":
+        names, inits = ["x", "", "sc"], {"sc": GV.arr(c, "scales")}
+    elif c["op"] == "Pad":
+        names, inits = ["x", "p"], {"p": GV.arr(c, "pads")}
+    elif c["op"] in ("QuantizeLinear", "DequantizeLinear"):
+        names, inits = ["x", "s"], {"s": GV.arr(c, "scale")}
+        if GV.arr(c, "zp") is not None:
+            names.append("z")
+            inits["z"] = GV.arr(c, "zp")
+        if c["op"] == "DequantizeLinear":
+            x = x.astype(np.uint8 if x.min() >= 0 else np.int8)
+    else:
+        names, inits = ["x"], {}
+    node = ep.Node(c["op"], names, ["y"], _golden_attrs(c["attrs"]))
+    g = unique_graph([node], inits, ["x"], ["y"])
+    y = Session(g, ctx).run({"x": x})["y"]
+    assert list(y.shape) == c["shape"]
+    np.testing.assert_allclose(np.asarray(y, np.float64).ravel(), c["expected"], atol=c.get("tol", 0.0), rtol=0)
