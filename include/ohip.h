@@ -226,6 +226,16 @@ typedef struct {
 } ohip_conv_desc;
 int ohip_conv2d(ohip_ctx* ctx, const ohip_conv_desc* d, const void* x, const ohip_weight* w,
                 const void* bias, void* y);
+/* ohip_conv2d without device allocation.  No counterpart in the reference:
+ * it is for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).  Same
+ * kernels and results as ohip_conv2d; the NCHW staging copy and the split-K
+ * partial sums live in a static 32 MiB device array per GPU instead of the
+ * context's growable scratch.  A call needing more scratch than that returns
+ * OHIP_E_NOMEM and launches nothing.  Every call on one GPU shares the array,
+ * so calls that overlap on one GPU (other streams or contexts) race. */
+int ohip_conv2d_noalloc(ohip_ctx* ctx, const ohip_conv_desc* d, const void* x, const ohip_weight* w,
+                        const void* bias, void* y);
 /* Output extent per conv_out_dim (conv/spatial.rs:272-330); -1 if invalid. */
 int64_t ohip_conv_out_dim(int64_t in, int64_t pad_begin, int64_t pad_end, int64_t k, int64_t dil,
                           int64_t stride);
@@ -394,12 +404,15 @@ void ohip_note_declined(ohip_ctx* ctx, const char* why);
 const char* ohip_last_decline(ohip_ctx* ctx);
 
 /* ------------------------------------------------------------------ counters */
-/* CacheCounters (oxionnx-cuda/src/residency.rs:141-238) plus dispatch counts. */
+/* CacheCounters (oxionnx-cuda/src/residency.rs:141-238) plus dispatch counts
+ * and device allocations (hipMalloc calls for the context's weights, pool,
+ * scratch and constants; a steady-state forward makes none). */
 typedef struct {
     uint64_t weight_hits, weight_misses, weight_transient;
     uint64_t weight_uploaded_bytes, weight_resident_bytes;
     uint64_t h2d_bytes, d2h_bytes;
     uint64_t dispatches, declined;
+    uint64_t device_allocs;
 } ohip_counters;
 int ohip_get_counters(ohip_ctx* ctx, ohip_counters* out);
 int ohip_reset_counters(ohip_ctx* ctx);

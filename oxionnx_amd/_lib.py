@@ -118,7 +118,7 @@ PLACE_HOST, PLACE_DEVICE = 0, 1
 class Counters(ctypes.Structure):
     _fields_ = [(f, ctypes.c_uint64) for f in (
         "weight_hits", "weight_misses", "weight_transient", "weight_uploaded_bytes", "weight_resident_bytes",
-        "h2d_bytes", "d2h_bytes", "dispatches", "declined")]
+        "h2d_bytes", "d2h_bytes", "dispatches", "declined", "device_allocs")]
 
 
 # name -> (restype, argtypes); the list is the C ABI of include/ohip.h.
@@ -161,6 +161,7 @@ SIGNATURES = {
     "ohip_weight_bytes": (ctypes.c_size_t, [VP]),
     "ohip_gemm": (ctypes.c_int, [VP, ctypes.POINTER(GemmDesc), VP, VP, VP, VP]),
     "ohip_conv2d": (ctypes.c_int, [VP, ctypes.POINTER(ConvDesc), VP, VP, VP, VP]),
+    "ohip_conv2d_noalloc": (ctypes.c_int, [VP, ctypes.POINTER(ConvDesc), VP, VP, VP, VP]),
     "ohip_matmul": (ctypes.c_int, [VP, ctypes.POINTER(MatMulDesc), VP, VP, VP]),
     "ohip_conv_out_dim": (I64, [I64, I64, I64, I64, I64, I64]),
     "ohip_weight_conv_transpose": (ctypes.c_int, [VP, ctypes.POINTER(WeightKey), ctypes.c_int, VP, I64, I64, I64,

@@ -4,6 +4,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <atomic>
 #include <cctype>
 #include <climits>
 #include <cmath>
@@ -122,7 +123,16 @@ struct ohip_ctx {
   DevPool pool;
   std::map<std::string, uint8_t*> tables;  // device copies of 256-byte output tables, by content
   std::map<std::string, void*> consts;     // device copies of small initializer operands
+  std::atomic<uint64_t> device_allocs{0};  // hipMalloc calls made for this context
 };
+
+// Every device allocation of a context goes through here, so the counters
+// can show that a steady-state forward allocates nothing.
+static hipError_t dev_malloc(ohip_ctx* ctx, void** p, size_t bytes) {
+  hipError_t e = hipMalloc(p, bytes);
+  if (e == hipSuccess) ctx->device_allocs.fetch_add(1, std::memory_order_relaxed);
+  return e;
+}
 
 // A device buffer shared by a tensor and its aliases (Reshape and friends);
 // the last owner returns it to the pool.
@@ -172,7 +182,7 @@ static int scratch_reserve(ohip_ctx* ctx, size_t bytes) {
   ctx->scratch = nullptr;
   ctx->scratch_bytes = 0;
   size_t want = std::max<size_t>(bytes, size_t(1) << 20);
-  hipError_t e = hipMalloc(&ctx->scratch, want);
+  hipError_t e = dev_malloc(ctx, &ctx->scratch, want);
   if (e != hipSuccess) return fail(OHIP_E_NOMEM, std::string("scratch hipMalloc: ") + hipGetErrorString(e));
   ctx->scratch_bytes = want;
   return OHIP_OK;
@@ -182,6 +192,63 @@ static void* scratch_at(ohip_ctx* ctx, const ScratchPlan& p, size_t idx) {
   size_t off = 0;
   for (size_t i = 0; i < idx; ++i) off += p.sizes[i];
   return static_cast<char*>(ctx->scratch) + off;
+}
+
+static void* plan_at(char* base, const ScratchPlan& p, size_t idx) {
+  size_t off = 0;
+  for (size_t i = 0; i < idx; ++i) off += p.sizes[i];
+  return base + off;
+}
+
+// ------------------------------------------------------------------ static scratch
+// The scratch of the allocation-free entry points (ohip_conv2d_noalloc): one
+// array per GPU, held from the library's load until the process ends.  In
+// host code `scratch` names a host-side stand-in, never the device memory:
+// its device address is looked up once per device (at context creation, with
+// that device current) and only that address is handed to kernels.  Every
+// call on a GPU shares its array and it keeps the last call's contents;
+// calls that overlap on one GPU (two streams, two contexts) race.
+static constexpr size_t kStaticScratchBytes = size_t(32) << 20;
+static __device__ __align__(256) unsigned char scratch[kStaticScratchBytes];
+
+static constexpr int kMaxScratchDevices = 64;
+static std::mutex g_scratch_mu;
+static void* g_scratch_ptr[kMaxScratchDevices];
+static bool g_scratch_looked_up[kMaxScratchDevices];
+
+// Called with `device` current.
+static int static_scratch_init(int device) {
+  if (device < 0 || device >= kMaxScratchDevices) return fail(OHIP_E_INVALID, "static scratch: device index");
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_looked_up[device]) return g_scratch_ptr[device] ? OHIP_OK : fail(OHIP_E_HIP, "static scratch unavailable");
+  g_scratch_looked_up[device] = true;
+  void* p = nullptr;
+  hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+  if (e != hipSuccess || !p) return hip_fail(e == hipSuccess ? hipErrorInvalidSymbol : e, "hipGetSymbolAddress(scratch)");
+  g_scratch_ptr[device] = p;
+  return OHIP_OK;
+}
+
+// The scratch of one call: the context's growable region, or (noalloc) this
+// device's static array, which is never grown.
+static int call_scratch(ohip_ctx* ctx, size_t bytes, bool noalloc, char** base) {
+  if (!noalloc) {
+    int rc = scratch_reserve(ctx, bytes);
+    if (rc) return rc;
+    *base = static_cast<char*>(ctx->scratch);
+    return OHIP_OK;
+  }
+  if (bytes > kStaticScratchBytes)
+    return fail(OHIP_E_NOMEM, "ohip_conv2d_noalloc: needs " + std::to_string(bytes) +
+                                  " bytes of scratch, more than the static " + std::to_string(kStaticScratchBytes));
+  void* p = nullptr;
+  {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (ctx->device >= 0 && ctx->device < kMaxScratchDevices) p = g_scratch_ptr[ctx->device];
+  }
+  if (!p) return fail(OHIP_E_HIP, "ohip_conv2d_noalloc: the static scratch of this device was not set up");
+  *base = static_cast<char*>(p);
+  return OHIP_OK;
 }
 
 // ------------------------------------------------------------------ context
@@ -217,7 +284,7 @@ extern "C" int ohip_ctx_create(int device, ohip_ctx** out) {
   {
     std::vector<uint8_t> tab(256 * 16);
     for (int b = 0; b < 256; ++b) std::memset(tab.data() + b * 16, b, 16);
-    e = hipMalloc(&ctx->padtab, tab.size());
+    e = dev_malloc(ctx, (void**)&ctx->padtab, tab.size());
     if (e == hipSuccess) e = hipMemcpy(ctx->padtab, tab.data(), tab.size(), hipMemcpyHostToDevice);
     if (e != hipSuccess) {
       if (ctx->padtab) (void)hipFree(ctx->padtab);
@@ -227,6 +294,8 @@ extern "C" int ohip_ctx_create(int device, ohip_ctx** out) {
     }
   }
   ohip_tuning_for_class(OHIP_CLASS_MI355X, &ctx->tuning);
+  // A failed lookup leaves only ohip_conv2d_noalloc unusable on this device.
+  if (static_scratch_init(device) != OHIP_OK) (void)hipGetLastError();
   *out = ctx;
   return OHIP_OK;
 }
@@ -297,13 +366,13 @@ static int pool_alloc(ohip_ctx* ctx, size_t bytes, void** p) {
     ctx->pool.free_blocks.erase(it);
     return OHIP_OK;
   }
-  hipError_t e = hipMalloc(p, cap);
+  hipError_t e = dev_malloc(ctx, p, cap);
   if (e != hipSuccess) {
     // give the cached blocks back to HIP once and retry
     (void)hipStreamSynchronize(ctx->stream);
     for (auto& kv : ctx->pool.free_blocks) { (void)hipFree(kv.second); ctx->pool.held -= kv.first; }
     ctx->pool.free_blocks.clear();
-    e = hipMalloc(p, cap);
+    e = dev_malloc(ctx, p, cap);
     if (e != hipSuccess) return fail(OHIP_E_NOMEM, std::string("hipMalloc: ") + hipGetErrorString(e));
   }
   ctx->pool.live[*p] = cap;
@@ -635,7 +704,7 @@ static ohip_weight* cache_lookup(ohip_ctx* ctx, const ohip_weight_key* key, cons
 }
 
 static int weight_upload(ohip_ctx* ctx, ohip_weight* w, const void* packed, size_t bytes) {
-  hipError_t e = hipMalloc(&w->data, bytes ? bytes : 16);
+  hipError_t e = dev_malloc(ctx, &w->data, bytes ? bytes : 16);
   if (e != hipSuccess) return fail(OHIP_E_NOMEM, std::string("weight hipMalloc: ") + hipGetErrorString(e));
   HIP_TRY(hipMemcpyAsync(w->data, packed, bytes, hipMemcpyHostToDevice, ctx->stream), "weight upload");
   HIP_TRY(hipStreamSynchronize(ctx->stream), "weight upload sync");
@@ -887,16 +956,16 @@ static int qpack_upload(ohip_ctx* ctx, ohip_weight* w, const QPacked& q, const f
   w->ld_bytes = q.split ? 2 * q.half : q.kp;
   int rc = weight_upload(ctx, w, q.data.data(), q.data.size());
   if (rc) return rc;
-  hipError_t e = hipMalloc(&w->colsum, q.colsum.size() * 4);
+  hipError_t e = dev_malloc(ctx, (void**)&w->colsum, q.colsum.size() * 4);
   if (e != hipSuccess) return fail(OHIP_E_NOMEM, "colsum hipMalloc");
   HIP_TRY(hipMemcpy(w->colsum, q.colsum.data(), q.colsum.size() * 4, hipMemcpyHostToDevice), "colsum upload");
   if (q.any_flip) {
-    e = hipMalloc(&w->flip, q.flip.size());
+    e = dev_malloc(ctx, (void**)&w->flip, q.flip.size());
     if (e != hipSuccess) return fail(OHIP_E_NOMEM, "flip hipMalloc");
     HIP_TRY(hipMemcpy(w->flip, q.flip.data(), q.flip.size(), hipMemcpyHostToDevice), "flip upload");
     w->bytes += q.flip.size();
   }
-  e = hipMalloc(&w->comb, (size_t)w->rows * 4);
+  e = dev_malloc(ctx, (void**)&w->comb, (size_t)w->rows * 4);
   if (e != hipSuccess) return fail(OHIP_E_NOMEM, "comb hipMalloc");
   if (scale && n_scale > 0) w->scale.assign(scale, scale + n_scale);
   w->bytes += q.colsum.size() * 4 + (size_t)w->rows * 4;
@@ -1163,8 +1232,8 @@ static bool ph_one_launch() {
   return v;
 }
 
-extern "C" int ohip_conv2d(ohip_ctx* ctx, const ohip_conv_desc* d, const void* x, const ohip_weight* w,
-                           const void* bias, void* y) {
+static int conv2d_impl(ohip_ctx* ctx, const ohip_conv_desc* d, const void* x, const ohip_weight* w, const void* bias,
+                       void* y, bool noalloc) {
   int rc = activate(ctx);
   if (rc) return rc;
   if (!d || !x || !w || !y) return fail(OHIP_E_INVALID, "ohip_conv2d: null argument");
@@ -1239,9 +1308,10 @@ extern "C" int ohip_conv2d(ohip_ctx* ctx, const ohip_conv_desc* d, const void* x
       const int64_t slices = (d->c + cslice - 1) / cslice;
       ScratchPlan plan;
       const size_t iw = plan.add((size_t)(slices * d->n * d->cout * ohw) * 4);
-      rc = scratch_reserve(ctx, plan.total());
+      char* sbase = nullptr;
+      rc = call_scratch(ctx, plan.total(), noalloc, &sbase);
       if (rc) return rc;
-      hipError_t e = run_conv_fewout(d->dtype, x, w->data, bias, y, static_cast<float*>(scratch_at(ctx, plan, iw)), a,
+      hipError_t e = run_conv_fewout(d->dtype, x, w->data, bias, y, static_cast<float*>(plan_at(sbase, plan, iw)), a,
                                      cslice, ctx->stream);
       if (e != hipSuccess) return hip_fail(e, "ohip_conv2d few-output launch");
       return OHIP_OK;
@@ -1262,11 +1332,12 @@ extern "C" int ohip_conv2d(ohip_ctx* ctx, const ohip_conv_desc* d, const void* x
       plan_split_tile(sP, sQ, (int)(d->kh * d->kw * (cp / ce)), ctx->tile_override, d->dtype == OHIP_F32);
   const int splits = sc.splits;
   size_t iw = splits > 1 ? plan.add(split_ws_bytes(sP, sQ, splits)) : SIZE_MAX;
-  rc = scratch_reserve(ctx, plan.total());
+  char* sbase = nullptr;
+  rc = call_scratch(ctx, plan.total(), noalloc, &sbase);
   if (rc) return rc;
   const void* xin = x;
   if (stage) {
-    void* px = scratch_at(ctx, plan, ix);
+    void* px = plan_at(sbase, plan, ix);
     if (G > 1)
       HIP_TRY(run_stage_nhwc(eb, x, px, (int)d->n, (int)d->c, (int)d->h, (int)d->w, fused_pad ? (int)d->pad_t : 0,
                              fused_pad ? (int)d->pad_l : 0, fused_pad ? (int)d->pad_b : 0,
@@ -1322,7 +1393,7 @@ extern "C" int ohip_conv2d(ohip_ctx* ctx, const ohip_conv_desc* d, const void* x
     }
     DENSE_FITS_OR_DECLINE(wt, "ohip_conv2d");
     o.splits = splits;
-    o.split_ws = splits > 1 ? scratch_at(ctx, plan, iw) : nullptr;
+    o.split_ws = splits > 1 ? plan_at(sbase, plan, iw) : nullptr;
     if (one_launch) {
       col.zstride = cp * eb;
       wt.zmod = (int)G; wt.zstride = coutg * w->ld_bytes;
@@ -1335,6 +1406,19 @@ extern "C" int ohip_conv2d(ohip_ctx* ctx, const ohip_conv_desc* d, const void* x
     if (e != hipSuccess) return hip_fail(e, "ohip_conv2d launch");
   }
   return OHIP_OK;
+}
+
+extern "C" int ohip_conv2d(ohip_ctx* ctx, const ohip_conv_desc* d, const void* x, const ohip_weight* w,
+                           const void* bias, void* y) {
+  return conv2d_impl(ctx, d, x, w, bias, y, false);
+}
+
+// Same kernels as ohip_conv2d; the staging copy and the split-K partial sums
+// live in this device's static scratch array instead of the context's
+// growable scratch, so the call makes no device allocation.
+extern "C" int ohip_conv2d_noalloc(ohip_ctx* ctx, const ohip_conv_desc* d, const void* x, const ohip_weight* w,
+                                   const void* bias, void* y) {
+  return conv2d_impl(ctx, d, x, w, bias, y, true);
 }
 
 // ------------------------------------------------------------------ batched MatMul
@@ -1583,7 +1667,7 @@ static int device_table(ohip_ctx* ctx, const uint8_t* host, const uint8_t** out)
   auto it = ctx->tables.find(key);
   if (it != ctx->tables.end()) { *out = it->second; return OHIP_OK; }
   uint8_t* d = nullptr;
-  hipError_t e = hipMalloc(&d, 256);
+  hipError_t e = dev_malloc(ctx, (void**)&d, 256);
   if (e != hipSuccess) return fail(OHIP_E_NOMEM, "table hipMalloc");
   HIP_TRY(hipMemcpy(d, host, 256, hipMemcpyHostToDevice), "table upload");
   ctx->tables.emplace(key, d);
@@ -1797,7 +1881,7 @@ int ohip_const_operand_internal(ohip_ctx* ctx, const char* name, const char* lab
   auto it = ctx->consts.find(k);
   if (it != ctx->consts.end()) { *dev = it->second; return OHIP_OK; }
   void* d = nullptr;
-  hipError_t e = hipMalloc(&d, bytes ? bytes : 16);
+  hipError_t e = dev_malloc(ctx, &d, bytes ? bytes : 16);
   if (e != hipSuccess) return fail(OHIP_E_NOMEM, "const operand hipMalloc");
   HIP_TRY(hipMemcpyAsync(d, host, bytes, hipMemcpyHostToDevice, ctx->stream), "const operand upload");
   HIP_TRY(hipStreamSynchronize(ctx->stream), "const operand upload sync");
@@ -1951,6 +2035,7 @@ extern "C" const char* ohip_last_decline(ohip_ctx* ctx) { return ctx ? ctx->last
 extern "C" int ohip_get_counters(ohip_ctx* ctx, ohip_counters* out) {
   if (!ctx || !out) return fail(OHIP_E_INVALID, "null argument");
   *out = ctx->counters;
+  out->device_allocs = ctx->device_allocs.load(std::memory_order_relaxed);
   return OHIP_OK;
 }
 extern "C" int ohip_reset_counters(ohip_ctx* ctx) {
@@ -1958,5 +2043,6 @@ extern "C" int ohip_reset_counters(ohip_ctx* ctx) {
   uint64_t resident = ctx->counters.weight_resident_bytes;
   ctx->counters = ohip_counters{};
   ctx->counters.weight_resident_bytes = resident;
+  ctx->device_allocs.store(0, std::memory_order_relaxed);
   return OHIP_OK;
 }

@@ -210,9 +210,11 @@ class HipContext:
         return out
 
     def conv2d(self, x, w, bias=None, strides=(1, 1), pads=(0, 0, 0, 0), dilations=(1, 1), act=L.ACT_NONE,
-               act_lo=0.0, act_hi=0.0, in_layout=L.NCHW, out_layout=L.NCHW, out=None, group=1):
+               act_lo=0.0, act_hi=0.0, in_layout=L.NCHW, out_layout=L.NCHW, out=None, group=1, noalloc=False):
         """pads = [top, left, bottom, right]; x NCHW (or NHWC channel-padded);
-        w holds Cin / group input channels per filter (ONNX Conv's group)."""
+        w holds Cin / group input channels per filter (ONNX Conv's group).
+        noalloc=True calls ohip_conv2d_noalloc (static scratch, no device
+        allocation; `out` should then be given)."""
         torch = _torch()
         dt = ohip_dtype(x.dtype)
         cout, cin, kh, kw = w.shape
@@ -233,7 +235,8 @@ class HipContext:
                 out = torch.zeros((n, oh, ow, (cout + ce - 1) // ce * ce), dtype=x.dtype, device=x.device)
         d = L.ConvDesc(n, c, h, wd, cout, kh, kw, group, strides[0], strides[1], dilations[0], dilations[1],
                        pads[0], pads[1], pads[2], pads[3], dt, in_layout, out_layout, act, act_lo, act_hi)
-        L.check(L.lib().ohip_conv2d(self.h, ctypes.byref(d), _ptr(x), w.handle, _ptr(bias), _ptr(out)))
+        fn = L.lib().ohip_conv2d_noalloc if noalloc else L.lib().ohip_conv2d
+        L.check(fn(self.h, ctypes.byref(d), _ptr(x), w.handle, _ptr(bias), _ptr(out)))
         return out
 
     def matmul(self, a, b, out=None):

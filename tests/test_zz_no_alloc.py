@@ -1,0 +1,72 @@
+"""ohip_conv2d_noalloc (no device allocation, static per-GPU scratch) against
+ohip_conv2d through the C ABI: identical results on two calls in a row, the
+second with a smaller input, and no device allocation by either noalloc
+call.  The cases use the scratch: an NCHW input (the staging copy) and a
+split-K contraction (partial sums)."""
+import ctypes
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def torch():
+    import torch as t
+    assert t.cuda.is_available(), "GPU tests need a GPU"
+    return t
+
+
+@pytest.fixture(scope="module")
+def ctx(torch):
+    from oxionnx_amd.device import HipContext
+    c = HipContext(0)
+    yield c
+    c.close()
+
+
+def _case(torch, ctx, dt, xs, ws, pads, seed):
+    from oxionnx_amd import _lib as L
+    rng = np.random.default_rng(seed)
+    tdt = {"f32": torch.float32, "f16": torch.float16}[dt]
+    x = torch.from_numpy(rng.uniform(-1, 1, xs).astype(np.float32)).cuda().to(tdt)
+    w = rng.normal(0, 0.05, ws).astype(np.float32)
+    b = torch.from_numpy(rng.normal(0, 0.01, ws[0]).astype(np.float32)).cuda().to(tdt)
+    wt = ctx.weight_conv(w, dtype=L.F32 if dt == "f32" else L.F16)
+    return x, wt, b
+
+
+# (dtype, x shape, w shape, pads): the first takes split-K (a 512 -> 512 3x3
+# conv at 32x32), the second is smaller and unsplit
+CALLS = [("f16", (1, 512, 32, 32), (512, 512, 3, 3), (1, 1, 1, 1)),
+         ("f16", (1, 64, 20, 24), (96, 64, 3, 3), (1, 1, 1, 1)),
+         ("f32", (1, 128, 64, 64), (256, 128, 3, 3), (1, 1, 1, 1)),
+         ("f32", (2, 16, 9, 11), (24, 16, 3, 3), (0, 1, 2, 1))]
+
+
+@pytest.mark.parametrize("pair", [(0, 1), (2, 3)], ids=["f16", "f32"])
+def test_noalloc_matches_conv2d_twice(torch, ctx, pair):
+    from oxionnx_amd import _lib as L
+    for i in pair:
+        dt, xs, ws, pads = CALLS[i]
+        x, wt, b = _case(torch, ctx, dt, xs, ws, pads, seed=i)
+        want = ctx.conv2d(x, wt, b, pads=pads, act=L.ACT_RELU)
+        got = torch.full_like(want, float("nan"))
+        torch.cuda.synchronize()
+        ctx.reset_counters()
+        ctx.conv2d(x, wt, b, pads=pads, act=L.ACT_RELU, out=got, noalloc=True)
+        torch.cuda.synchronize()
+        assert ctx.counters()["device_allocs"] == 0
+        assert torch.equal(got, want), (i, float((got.float() - want.float()).abs().max()))
+
+
+def test_noalloc_rejects_more_scratch_than_the_static_array(torch, ctx):
+    from oxionnx_amd import _lib as L
+    # an NCHW f32 input of 40 MiB needs a staging copy larger than 32 MiB
+    x = torch.zeros((1, 160, 256, 256), dtype=torch.float32, device="cuda")
+    wt = ctx.weight_conv(np.zeros((16, 160, 1, 1), np.float32))
+    out = torch.zeros((1, 16, 256, 256), dtype=torch.float32, device="cuda")
+    with pytest.raises(L.OhipError) as e:
+        ctx.conv2d(x, wt, None, out=out, noalloc=True)
+    assert e.value.code == L.E_NOMEM and "static" in str(e.value)
