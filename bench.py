@@ -4,7 +4,9 @@
 
 A step is one Gemm launch of the headline workload, config 2's largest shape
 (M, K, N) = (4096, 4096, 11008) in f16 with a row bias, operands resident in
-HBM.  The JSON line reports whole-job TFLOP/s for that step, the roofline of
+HBM.  Before the W warm-up steps the same launch runs back to back for
+--settle-ms (100 ms) of wall time: an idle GPU needs that long under load to
+leave its idle clock, and the timed steps are meant to see the settled one.  The JSON line reports whole-job TFLOP/s for that step, the roofline of
 the kernel (its average duration measured with HIP events on the stream it is
 launched on), the reference-algorithm CPU baseline on a bounded row sample,
 and a sweep over every configured workload (configs 1-3 of BASELINE.json).
@@ -24,6 +26,8 @@ METRIC = "conv/GEMM TFLOP/s & int8 TOPS (% MFMA peak); end-to-end ms/forward"
 PEAK_TFLOPS = {"f16": 2500.0, "bf16": 2500.0, "f32": 157.3, "int8": 5000.0}
 HBM_GBPS = 8000.0
 HEADLINE = (4096, 4096, 11008)
+# host threads this process may run on (the CPU baselines state how many they used)
+HOST_CORES = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
 GEMM_SWEEP = [(1, 25088, 512), (128, 768, 3072), (2048, 4096, 4096), (4096, 4096, 11008)]
 
 
@@ -35,9 +39,24 @@ def parse():
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--no-sweep", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=20.0)
+    p.add_argument("--settle-ms", type=float, default=100.0,
+                   help="GPU time of headline launches run before the warm-up steps, so that the timed "
+                        "steps see the clock the GPU settles at under this load, not its idle ramp")
     p.add_argument("--only", default="", help="run one item (for profiling): 'headline', 'copy', "
                    "'conv_f32_cfg1', 'int8_ffn', or a sweep item such as 'gemm_f16_2048x4096x4096'")
     return p.parse_args()
+
+
+def settle_clock(torch, fn, ms):
+    """Runs fn back to back until `ms` of wall time have passed (an idle
+    MI355X takes some 10-20 ms of load to leave its idle clock); returns the
+    wall ms spent.  Not part of the timed region."""
+    t0 = time.perf_counter()
+    while (time.perf_counter() - t0) * 1e3 < ms:
+        for _ in range(4):
+            fn()
+        torch.cuda.synchronize()
+    return (time.perf_counter() - t0) * 1e3
 
 
 def time_launches(torch, stream, fn, iters, warmup):
@@ -105,7 +124,7 @@ def cpu_baseline_f16(seconds):
     O.gemm_half(a, b, c, rows=(0, rows))
     dt = time.perf_counter() - t0
     flops = 2.0 * rows * k * n
-    return {"value": flops / dt / 1e12, "unit": "TFLOP/s", "cores": 1, "kind": "port",
+    return {"value": flops / dt / 1e12, "unit": "TFLOP/s", "cores": 1, "host_cores": HOST_CORES, "kind": "port",
             "sample": f"{rows} of {m} output rows of the f16 Gemm ({rows}x{k}x{n}), {dt:.2f} s; "
                       f"full forward extrapolates to {dt * m / rows:.0f} s"}
 
@@ -142,6 +161,7 @@ def main():
         _, _, _, w, at, ct, y = gemm_setup(torch, ctx, L, m, k, n, L.F16, rng)
         step = lambda: ctx.gemm(at, w, ct, out=y)
         steps = args.steps if args.only in ("", "headline") else 0   # profiling another item
+        settled = settle_clock(torch, step, args.settle_ms) if steps else 0.0
         for _ in range(args.warmup if steps else 0):
             step()
         torch.cuda.synchronize()
@@ -183,6 +203,7 @@ def main():
             extras.update(bench_large(torch, ctx, L, stream, rng, args.only))
             extras.update(bench_widened(torch, ctx, L, stream, rng, args.only))
             extras.update(bench_e2e(torch, ctx, stream, args.only, args.no_cpu))
+            extras.update(bench_gate(torch, ctx, L, args.only))
 
     line = {
         "metric": METRIC, "value": round(tflops, 2), "unit": "TFLOP/s", "n_gpus": 1,
@@ -196,6 +217,7 @@ def main():
                      "traffic": traffic, "algorithmic_bytes": alg_bytes,
                      "kernel": "mfma_gemm_kernel<Op::F16, Tile<256,256,2,4,2,8>, DenseRows, DenseRows, FloatEpi<_Float16>, false, false>"},
         "wall_s_timed_region": round(wall, 3),
+        "settle_ms_before_warmup": round(settled, 1),
     }
     if not args.no_cpu and not args.only:
         line["cpu_baseline"] = cpu_baseline_f16(args.cpu_seconds)
@@ -340,6 +362,87 @@ def bench_widened(torch, ctx, L, stream, rng, only):
     return out
 
 
+GATE_M = [1, 2, 4, 8, 12, 16, 24, 32, 48, 64, 96, 128, 256]
+GATE_KN = [(128, 128), (256, 256), (512, 512), (1024, 1024), (2048, 2048), (4096, 4096), (25088, 512)]
+GATE_CONV = [(c, hw) for c in (8, 16, 32, 64, 128) for hw in (8, 16, 32, 64)]
+
+
+def _best_ms(fn, reps):
+    fn()
+    best = float("inf")
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        fn()
+        best = min(best, (time.perf_counter() - t0) * 1e3)
+    return best
+
+
+def bench_gate(torch, ctx, L, only):
+    """--only gate: the GPU / CPU crossover table the MI355X dispatch gate is
+    set from, in the reference's method (tuning.rs:60-83): per shape, the
+    best wall time of the provider's Gemm node with host operands in and the
+    host result out (B uploaded every call, or B resident in the weight
+    cache after its first call), against the reference's CPU algorithm on
+    this host (2-D Gemm: single-threaded packed sgemm, math_typed.rs:45-79;
+    Conv: im2col + sgemm over every host thread, conv2d.rs:246-547).  Not
+    part of the default run."""
+    if only != "gate":
+        return {}
+    import ctypes
+    from oracle import oracle as O
+    from oxionnx_amd import ep
+    t = L.Tuning()
+    L.lib().ohip_tuning_for_class(L.CLASS_PARITY, ctypes.byref(t))
+    ctx.set_tuning(t)   # time every shape on the device, however small
+    rng = np.random.default_rng(77)
+    gemm = []
+    node = ep.Node("Gemm", ["a", "b"], ["y"])
+    for kk, nn in GATE_KN:
+        b = rng.normal(0, 1 / np.sqrt(kk), (kk, nn)).astype(np.float32)
+        for mm in GATE_M:
+            a = rng.uniform(-1, 1, (mm, kk)).astype(np.float32)
+            reps = 15 if mm * kk * nn < 2e8 else 5
+            cpu = _best_ms(lambda: O.gemm(a, b, nthreads=1), reps)
+            up = _best_ms(lambda: ep.try_hip_dispatch(node, {}, {"a": a, "b": b}, ctx), reps)
+            wname = f"gate.B.{kk}.{nn}"
+            cnode = ep.Node("Gemm", ["a", wname], ["y"])
+            cached = _best_ms(lambda: ep.try_hip_dispatch(cnode, {wname: b}, {"a": a}, ctx), reps)
+            gemm.append({"m": mm, "k": kk, "n": nn, "cpu_ms": round(cpu, 4), "gpu_upload_ms": round(up, 4),
+                         "gpu_cached_ms": round(cached, 4), "ratio_upload": round(up / cpu, 3),
+                         "ratio_cached": round(cached / cpu, 3)})
+    conv = []
+    for c, hw in GATE_CONV:
+        x = rng.uniform(-1, 1, (1, c, hw, hw)).astype(np.float32)
+        w = rng.normal(0, 0.05, (c, c, 3, 3)).astype(np.float32)
+        wname = f"gate.W.{c}.{hw}"
+        cn = ep.Node("Conv", ["x", wname], ["y"], ep.Attributes(int_lists={"pads": [1, 1, 1, 1]}))
+        reps = 15 if c * c * 9 * hw * hw < 2e8 else 5
+        cpu = _best_ms(lambda: O.conv(x, w, pads=[1, 1, 1, 1], nthreads=HOST_CORES), reps)
+        gpu = _best_ms(lambda: ep.try_hip_dispatch(cn, {wname: w}, {"x": x}, ctx), reps)
+        conv.append({"cout": c, "cin": c, "kernel": 3, "hw": hw, "implied_mac": c * c * 9 * hw * hw,
+                     "cpu_ms": round(cpu, 4), "gpu_ms": round(gpu, 4), "ratio": round(gpu / cpu, 3)})
+    return {"gate": {"host_cores": HOST_CORES, "gemm": gemm, "conv": conv,
+                     "note": "ratio = GPU / CPU wall time; > 1 means the GPU lost"}}
+
+
+def _time_forwards(torch, stream, fwd, n=10):
+    """(median wall ms, median stream ms) of n forwards after two untimed ones."""
+    for _ in range(2):
+        fwd()
+    walls, gpus = [], []
+    for _ in range(n):
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0 = time.perf_counter()
+        e0.record(stream)
+        fwd()
+        e1.record(stream)
+        walls.append((time.perf_counter() - t0) * 1e3)
+        torch.cuda.synchronize()
+        gpus.append(e0.elapsed_time(e1))
+    return round(float(np.median(walls)), 3), round(float(np.median(gpus)), 3)
+
+
 def bench_e2e(torch, ctx, stream, only, no_cpu):
     """Configs 4 and 5 end to end, median of 10 forwards each:
     * the session run loop (graph inputs uploaded, every node dispatched
@@ -362,51 +465,45 @@ def bench_e2e(torch, ctx, stream, only, no_cpu):
             continue
         g, feeds = make()
         sess = Session(g, ctx)
-        for _ in range(2):
-            sess.run(feeds)
-        walls, gpus = [], []
-        for _ in range(10):
-            torch.cuda.synchronize()
-            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            t0 = time.perf_counter()
-            e0.record(stream)
-            sess.run(feeds)
-            e1.record(stream)
-            walls.append((time.perf_counter() - t0) * 1e3)
-            torch.cuda.synchronize()
-            gpus.append(e0.elapsed_time(e1))
+        loop = _time_forwards(torch, stream, lambda: sess.run(feeds))
         cap = sess.capture(feeds)
-        gwalls, ggpus = [], []
-        for _ in range(10):
-            torch.cuda.synchronize()
-            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            t0 = time.perf_counter()
-            e0.record(stream)
-            cap.replay(feeds)
-            e1.record(stream)
-            gwalls.append((time.perf_counter() - t0) * 1e3)
-            torch.cuda.synchronize()
-            ggpus.append(e0.elapsed_time(e1))
+        graph = _time_forwards(torch, stream, lambda: cap.replay(feeds))
         cap.close()
-        rec = {"ms_per_forward": round(float(np.median(gwalls)), 3),
-               "ms_per_forward_run_loop": round(float(np.median(walls)), 3),
-               "stream_ms_graph": round(float(np.median(ggpus)), 3),
-               "stream_ms_run_loop": round(float(np.median(gpus)), 3),
+        # the same graph with only the fusion the reference's optimizer makes
+        # (Conv + Relu): every other node runs as its own device kernel
+        rsess = Session(g, ctx, optimize="reference")
+        rloop = _time_forwards(torch, stream, lambda: rsess.run(feeds))
+        rcap = rsess.capture(feeds)
+        rgraph = _time_forwards(torch, stream, lambda: rcap.replay(feeds))
+        rcap.close()
+        rec = {"ms_per_forward": graph[0], "ms_per_forward_run_loop": loop[0],
+               "stream_ms_graph": graph[1], "stream_ms_run_loop": loop[1],
+               "reference_fusions_only": {"ms_per_forward": rgraph[0], "ms_per_forward_run_loop": rloop[0],
+                                          "stream_ms_graph": rgraph[1], "nodes": len(rsess.graph.nodes)},
                "nodes": len(g.nodes), "nodes_after_fusion": len(sess.graph.nodes),
                "conv_gmac": round(g.notes["conv_gmac"], 3),
                "note": "ms_per_forward: wall clock of one forward replayed from its captured HIP graph, incl. "
                        "input upload and output download; ms_per_forward_run_loop: the same forward "
-                       "dispatched node by node through the Python run loop"}
+                       "dispatched node by node through the Python run loop; reference_fusions_only: the "
+                       "graph with only the reference optimizer's Conv+Relu fusion (no provider-side "
+                       "rewrites)"}
         if not no_cpu and not only:
             from oracle import graph_ref
             t0 = time.perf_counter()
             graph_ref.run_graph(g, feeds, half=key.endswith("f16"), nthreads=threads)
             cpu = (time.perf_counter() - t0) * 1e3
-            rec["cpu_baseline"] = {"ms_per_forward": round(cpu, 1), "kind": "port",
-                                   "cores": 1 if "int8" in key else threads,
-                                   "sample": "one full forward of the same graph and inputs"}
+            int8 = "int8" in key
+            rec["cpu_baseline"] = {
+                "ms_per_forward": round(cpu, 1), "kind": "port", "cores": 1 if int8 else threads,
+                "host_cores": HOST_CORES,
+                "sample": "one full forward of the same graph and inputs" + (
+                    "; integer convolution single-threaded like the reference's integer_conv" if int8 else
+                    "; float convolution as im2col + a blocked, FMA-vectorised i-k-j sgemm over row "
+                    "splits (oracle/oracle_sgemm.c: a stand-in for matrixmultiply's packed microkernel, "
+                    "not that kernel)")}
             rec["speedup_vs_cpu"] = round(cpu / rec["ms_per_forward"], 1)
             rec["speedup_vs_cpu_run_loop"] = round(cpu / rec["ms_per_forward_run_loop"], 1)
+            rec["speedup_vs_cpu_reference_fusions_only"] = round(cpu / rgraph[0], 1)
         out[key] = rec
     return out
 

@@ -404,15 +404,19 @@ void ohip_note_declined(ohip_ctx* ctx, const char* why);
 const char* ohip_last_decline(ohip_ctx* ctx);
 
 /* ------------------------------------------------------------------ counters */
-/* CacheCounters (oxionnx-cuda/src/residency.rs:141-238) plus dispatch counts
- * and device allocations (hipMalloc calls for the context's weights, pool,
- * scratch and constants; a steady-state forward makes none). */
+/* CacheCounters (oxionnx-cuda/src/residency.rs:141-238) plus dispatch counts,
+ * device allocations (hipMalloc calls for the context's weights, pool,
+ * scratch and constants; a steady-state forward makes none), host fences
+ * (stream synchronisations for a read-back or ohip_sync) and, as a gauge not
+ * reset by ohip_reset_counters, the pool buffers currently handed out. */
 typedef struct {
     uint64_t weight_hits, weight_misses, weight_transient;
     uint64_t weight_uploaded_bytes, weight_resident_bytes;
     uint64_t h2d_bytes, d2h_bytes;
     uint64_t dispatches, declined;
     uint64_t device_allocs;
+    uint64_t stream_syncs;
+    uint64_t pool_live;
 } ohip_counters;
 int ohip_get_counters(ohip_ctx* ctx, ohip_counters* out);
 int ohip_reset_counters(ohip_ctx* ctx);

@@ -993,4 +993,34 @@ hipError_t run_gather2d(int elem_bytes, const void* src, int64_t rs, int64_t cs,
   return hipGetLastError();
 }
 
+// ---------------------------------------------------------------- float conversion
+template <int S, int D>
+__global__ void __launch_bounds__(256) convert_float_kernel(const void* __restrict__ src, void* __restrict__ dst,
+                                                            int64_t n) {
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
+    float v;
+    if constexpr (S == DT_F32) v = static_cast<const float*>(src)[i];
+    else if constexpr (S == DT_F16) v = f16_bits_to_f32(static_cast<const uint16_t*>(src)[i]);
+    else v = bf16_bits_to_f32(static_cast<const uint16_t*>(src)[i]);
+    if constexpr (D == DT_F32) static_cast<float*>(dst)[i] = v;
+    else if constexpr (D == DT_F16) static_cast<uint16_t*>(dst)[i] = f32_to_f16_bits(v);
+    else static_cast<uint16_t*>(dst)[i] = f32_to_bf16_bits(v);
+  }
+}
+
+hipError_t run_convert_float(int src_dt, int dst_dt, const void* src, void* dst, int64_t n, hipStream_t st) {
+  if (n <= 0) return hipSuccess;
+  const int64_t blocks = std::min<int64_t>((n + 255) / 256, 8192);
+  dim3 grid((unsigned)blocks), block(256);
+#define OHIP_CONV_CASE(S, D)                                                                       \
+  if (src_dt == S && dst_dt == D) {                                                                \
+    hipLaunchKernelGGL((convert_float_kernel<S, D>), grid, block, 0, st, src, dst, n);             \
+    return hipGetLastError();                                                                      \
+  }
+  OHIP_CONV_CASE(DT_F32, DT_F16) OHIP_CONV_CASE(DT_F32, DT_BF16) OHIP_CONV_CASE(DT_F16, DT_F32)
+  OHIP_CONV_CASE(DT_F16, DT_BF16) OHIP_CONV_CASE(DT_BF16, DT_F32) OHIP_CONV_CASE(DT_BF16, DT_F16)
+#undef OHIP_CONV_CASE
+  return hipErrorInvalidValue;
+}
+
 }  // namespace ohip

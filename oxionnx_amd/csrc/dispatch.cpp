@@ -37,6 +37,16 @@ int decline(const std::string& why) {
   return OHIP_DECLINED;
 }
 
+// The size gate prices a transfer: an operand that is already a resident
+// device tensor skips it (skips_size_threshold,
+// oxionnx-gpu/src/context/activation.rs:248-250), since declining would read
+// it back for a CPU kernel instead.
+bool any_resident(const ohip_node* nd) {
+  for (int i = 0; i < nd->n_inputs; ++i)
+    if (nd->inputs[i].device) return true;
+  return false;
+}
+
 // ------------------------------------------------------------------ attributes
 const ohip_attr* find_attr(const ohip_node* n, const char* name) {
   for (int i = 0; i < n->n_attrs; ++i)
@@ -381,7 +391,8 @@ int do_conv(ohip_ctx* ctx, const ohip_node* nd, int placement, ohip_output* out)
   const int64_t cg = g.c / g.group;
   ohip_tuning tun;
   ohip_get_tuning(ctx, &tun);
-  if (!ohip_conv_admits(&tun, g.cout, cg * g.kh * g.kw, g.n * g.oh * g.ow)) return decline("Conv: below conv_min_mac");
+  if (!any_resident(nd) && !ohip_conv_admits(&tun, g.cout, cg * g.kh * g.kw, g.n * g.oh * g.ow))
+    return decline("Conv: below conv_min_mac");
   if (x->device && ohip_dtensor_layout(x->device) != OHIP_NCHW) return decline("Conv: resident input layout");
 
   std::string name = wkey_name(w), label = "Conv.W";
@@ -497,7 +508,8 @@ int do_conv_transpose(ohip_ctx* ctx, const ohip_node* nd, int placement, ohip_ou
   if (oh < 0 || ow < 0) return decline("ConvTranspose: pads exceed the un-cropped extent");
   ohip_tuning tun;
   ohip_get_tuning(ctx, &tun);
-  if (!ohip_conv_admits(&tun, d.cout, (c / group) * kh * kw, n * h * wd)) return decline("ConvTranspose: gate");
+  if (!any_resident(nd) && !ohip_conv_admits(&tun, d.cout, (c / group) * kh * kw, n * h * wd))
+    return decline("ConvTranspose: gate");
 
   std::string name = wkey_name(w), label = "ConvTranspose.W";
   ohip_weight_key key{name.c_str(), label.c_str()};
@@ -559,7 +571,7 @@ int do_matmul_batched(ohip_ctx* ctx, const ohip_node* nd, int placement, ohip_ou
   if (m == 0 || n == 0 || k == 0 || batch == 0) return decline("MatMul: empty");
   ohip_tuning tun;
   ohip_get_tuning(ctx, &tun);
-  if (!ohip_gemm_admits(&tun, m * batch, k, n, false)) return decline("MatMul: gate");
+  if (!any_resident(nd) && !ohip_gemm_admits(&tun, m * batch, k, n, false)) return decline("MatMul: gate");
   Stage st(ctx);
   const void* ad = st.operand(a);
   const void* bd = st.operand(b);
@@ -619,7 +631,7 @@ int do_gemm(ohip_ctx* ctx, const ohip_node* nd, bool is_matmul, int placement, o
   ohip_tuning tun;
   ohip_get_tuning(ctx, &tun);
   const bool cache = b->is_initializer && b->name && *b->name;
-  if (!ohip_gemm_admits(&tun, m, k, n, cache)) return decline("Gemm: gate");
+  if (!any_resident(nd) && !ohip_gemm_admits(&tun, m, k, n, cache)) return decline("Gemm: gate");
   std::string name = wkey_name(b), label = std::string(is_matmul ? "MatMul.B" : "Gemm.B");
   ohip_weight_key key{name.c_str(), label.c_str()};
   ohip_weight* wt = nullptr;
@@ -692,7 +704,7 @@ int do_qmatmul(ohip_ctx* ctx, const ohip_node* nd, bool qlinear, int placement, 
   ohip_tuning tun;
   ohip_get_tuning(ctx, &tun);
   const bool cache = b->is_initializer && b->name && *b->name;
-  if (!ohip_gemm_admits(&tun, m, k, n, cache)) return decline("integer MatMul: gate");
+  if (!any_resident(nd) && !ohip_gemm_admits(&tun, m, k, n, cache)) return decline("integer MatMul: gate");
   std::vector<uint8_t> abytes, bbytes;
   int adt, bdt;
   if (!to_bytes(a, abytes, &adt) || !to_bytes(b, bbytes, &bdt)) return decline("integer MatMul: lanes outside 8 bits");
@@ -820,7 +832,8 @@ int do_qconv(ohip_ctx* ctx, const ohip_node* nd, bool qlinear, int placement, oh
   }
   ohip_tuning tun;
   ohip_get_tuning(ctx, &tun);
-  if (!ohip_conv_admits(&tun, g.cout, cg * g.kh * g.kw, g.n * g.oh * g.ow)) return decline("integer Conv: gate");
+  if (!any_resident(nd) && !ohip_conv_admits(&tun, g.cout, cg * g.kh * g.kw, g.n * g.oh * g.ow))
+    return decline("integer Conv: gate");
   std::vector<uint8_t> xb, wb;
   int xdt, wdt;
   if (x->device) xdt = x->dtype;

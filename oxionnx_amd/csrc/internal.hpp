@@ -16,6 +16,60 @@ enum { ACT_NONE = 0, ACT_RELU = 1, ACT_CLIP = 2, ACT_LEAKY_RELU = 3 };
 enum { BIAS_NONE = 0, BIAS_SCALAR = 1, BIAS_I = 2, BIAS_J = 3, BIAS_FULL_JI = 4 };
 enum { QOUT_U8 = 0, QOUT_I8 = 1, QOUT_I32 = 2, QOUT_F32 = 3 };
 
+// ------------------------------------------------------------------ half conversions
+// Bit-exact on host and device: round to nearest even, NaN kept quiet with
+// its top payload bits, overflow to infinity, subnormals rounded.
+__host__ __device__ inline uint16_t f32_to_f16_bits(float f) {
+  uint32_t x;
+  __builtin_memcpy(&x, &f, 4);
+  uint32_t sign = (x >> 16) & 0x8000u, exp = (x >> 23) & 0xffu, man = x & 0x7fffffu;
+  if (exp == 0xff) return (uint16_t)(man ? (sign | 0x7e00u | (man >> 13)) : (sign | 0x7c00u));
+  int e = (int)exp - 112;
+  if (e >= 31) return (uint16_t)(sign | 0x7c00u);
+  if (e <= 0) {
+    if (e < -10) return (uint16_t)sign;
+    uint32_t mm = man | 0x800000u;
+    int sh = 14 - e;
+    uint32_t h = mm >> sh, rem = mm & ((1u << sh) - 1), half = 1u << (sh - 1);
+    if (rem > half || (rem == half && (h & 1u))) ++h;
+    return (uint16_t)(sign | h);
+  }
+  uint32_t h = sign | ((uint32_t)e << 10) | (man >> 13), rem = man & 0x1fffu;
+  if (rem > 0x1000u || (rem == 0x1000u && (h & 1u))) ++h;
+  return (uint16_t)h;
+}
+__host__ __device__ inline float f16_bits_to_f32(uint16_t h) {
+  uint32_t sign = ((uint32_t)h & 0x8000u) << 16, exp = (h >> 10) & 0x1fu, man = h & 0x3ffu, x;
+  if (exp == 0) {
+    if (!man) x = sign;
+    else {
+      int e = -1;
+      do { man <<= 1; ++e; } while (!(man & 0x400u));
+      x = sign | ((uint32_t)(112 - e) << 23) | ((man & 0x3ffu) << 13);
+    }
+  } else if (exp == 31) x = sign | 0x7f800000u | (man << 13);
+  else x = sign | ((exp + 112) << 23) | (man << 13);
+  float f;
+  __builtin_memcpy(&f, &x, 4);
+  return f;
+}
+__host__ __device__ inline uint16_t f32_to_bf16_bits(float f) {
+  uint32_t x;
+  __builtin_memcpy(&x, &f, 4);
+  if ((x & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((x >> 16) | 0x40u);
+  return (uint16_t)((x + 0x7fffu + ((x >> 16) & 1u)) >> 16);
+}
+__host__ __device__ inline float bf16_bits_to_f32(uint16_t h) {
+  uint32_t x = (uint32_t)h << 16;
+  float f;
+  __builtin_memcpy(&f, &x, 4);
+  return f;
+}
+
+// Element conversion of a float array between F32 / F16 / BF16 (ONNX codes),
+// with the rounding above.
+hipError_t run_convert_float(int src_dt, int dst_dt, const void* src, void* dst, int64_t n, hipStream_t st);
+
 // Rows of K-contiguous 16-byte chunks.
 struct DenseOperand {
   const void* base;

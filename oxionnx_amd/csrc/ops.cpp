@@ -72,6 +72,7 @@ struct ohip_weight {
   int kc = 0;              // 16-byte chunks per packed row
   int64_t ld_bytes = 0;
   void* data = nullptr;
+  bool pooled = false;            // data is a pool buffer (a transient weight)
   int32_t* colsum = nullptr;      // integer only
   int8_t* flip = nullptr;         // integer only, null when no channel is negated
   int kwrap = 0;                  // integer only: > 0 when each row holds two int8 halves
@@ -300,11 +301,14 @@ extern "C" int ohip_ctx_create(int device, ohip_ctx** out) {
   return OHIP_OK;
 }
 
+static int pool_free(ohip_ctx* ctx, void* p);
+
 static void weight_free(ohip_weight* w) {
   if (!w) return;
   for (auto* p : w->phases) weight_free(p);
   if (w->ph_all) weight_free(w->ph_all);
-  if (w->data) (void)hipFree(w->data);
+  if (w->data && w->pooled) (void)pool_free(w->ctx, w->data);
+  else if (w->data) (void)hipFree(w->data);
   if (w->colsum) (void)hipFree(w->colsum);
   if (w->flip) (void)hipFree(w->flip);
   if (w->comb) (void)hipFree(w->comb);
@@ -338,6 +342,7 @@ extern "C" int ohip_sync(ohip_ctx* ctx) {
   int rc = activate(ctx);
   if (rc) return rc;
   HIP_TRY(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
+  ctx->counters.stream_syncs++;
   return OHIP_OK;
 }
 
@@ -509,6 +514,7 @@ extern "C" int ohip_memcpy_d2h(ohip_ctx* ctx, void* dst, const void* src, size_t
   HIP_TRY(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, ctx->stream), "hipMemcpyAsync D2H");
   HIP_TRY(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
   ctx->counters.d2h_bytes += bytes;
+  ctx->counters.stream_syncs++;
   return OHIP_OK;
 }
 extern "C" int ohip_memcpy_d2d(ohip_ctx* ctx, void* dst, const void* src, size_t bytes) {
@@ -533,7 +539,11 @@ extern "C" int ohip_tuning_for_class(int cls, ohip_tuning* t) {
   if (!t) return fail(OHIP_E_INVALID, "null tuning");
   switch (cls) {
     case OHIP_CLASS_MI355X:
-      *t = ohip_tuning{OHIP_CLASS_MI355X, 1000000ull, 500000ull, 8ull, 500000ull};
+      // Measured crossovers against the reference's CPU algorithms on an
+      // MI355X box's host (bench.py --only gate): the smallest sizes at and
+      // above which every measured shape ran faster on the device.  No
+      // intensity gate: no shape above the size floor lost, down to intensity 2.
+      *t = ohip_tuning{OHIP_CLASS_MI355X, 4000000ull, 1500000ull, 0ull, 600000ull};
       return OHIP_OK;
     case OHIP_CLASS_PARITY:  // GpuTuning::PARITY (tuning.rs:409-425)
       *t = ohip_tuning{OHIP_CLASS_PARITY, 0, 0, 0, 0};
@@ -600,52 +610,10 @@ extern "C" int ohip_conv_admits(const ohip_tuning* t, int64_t m, int64_t k, int6
 }
 
 // ------------------------------------------------------------------ host conversions
-static inline uint16_t f32_to_f16_rne(float f) {
-  uint32_t x;
-  std::memcpy(&x, &f, 4);
-  uint32_t sign = (x >> 16) & 0x8000u, exp = (x >> 23) & 0xffu, man = x & 0x7fffffu;
-  if (exp == 0xff) return (uint16_t)(man ? (sign | 0x7e00u | (man >> 13)) : (sign | 0x7c00u));
-  int e = (int)exp - 112;
-  if (e >= 31) return (uint16_t)(sign | 0x7c00u);
-  if (e <= 0) {
-    if (e < -10) return (uint16_t)sign;
-    uint32_t mm = man | 0x800000u;
-    int sh = 14 - e;
-    uint32_t h = mm >> sh, rem = mm & ((1u << sh) - 1), half = 1u << (sh - 1);
-    if (rem > half || (rem == half && (h & 1u))) ++h;
-    return (uint16_t)(sign | h);
-  }
-  uint32_t h = sign | ((uint32_t)e << 10) | (man >> 13), rem = man & 0x1fffu;
-  if (rem > 0x1000u || (rem == 0x1000u && (h & 1u))) ++h;
-  return (uint16_t)h;
-}
-static inline float f16_to_f32(uint16_t h) {
-  uint32_t sign = ((uint32_t)h & 0x8000u) << 16, exp = (h >> 10) & 0x1fu, man = h & 0x3ffu, x;
-  if (exp == 0) {
-    if (!man) x = sign;
-    else {
-      int e = -1;
-      do { man <<= 1; ++e; } while (!(man & 0x400u));
-      x = sign | ((uint32_t)(112 - e) << 23) | ((man & 0x3ffu) << 13);
-    }
-  } else if (exp == 31) x = sign | 0x7f800000u | (man << 13);
-  else x = sign | ((exp + 112) << 23) | (man << 13);
-  float f;
-  std::memcpy(&f, &x, 4);
-  return f;
-}
-static inline uint16_t f32_to_bf16_rne(float f) {
-  uint32_t x;
-  std::memcpy(&x, &f, 4);
-  if ((x & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((x >> 16) | 0x40u);
-  return (uint16_t)((x + 0x7fffu + ((x >> 16) & 1u)) >> 16);
-}
-static inline float bf16_to_f32(uint16_t h) {
-  uint32_t x = (uint32_t)h << 16;
-  float f;
-  std::memcpy(&f, &x, 4);
-  return f;
-}
+static inline uint16_t f32_to_f16_rne(float f) { return f32_to_f16_bits(f); }
+static inline float f16_to_f32(uint16_t h) { return f16_bits_to_f32(h); }
+static inline uint16_t f32_to_bf16_rne(float f) { return f32_to_bf16_bits(f); }
+static inline float bf16_to_f32(uint16_t h) { return bf16_bits_to_f32(h); }
 
 static int elem_bytes(int dt) {
   switch (dt) {
@@ -738,12 +706,69 @@ extern "C" void ohip_weight_release(ohip_weight* w) {
   if (it == ctx->transients.end()) return;
   ctx->transients.erase(it);
   (void)hipSetDevice(ctx->device);
-  (void)hipStreamSynchronize(ctx->stream);
+  // a pooled weight goes back to the stream-ordered pool: work queued after
+  // this on the stream may reuse it, so no wait is needed
+  bool pool_only = w->pooled && !w->colsum && !w->flip && !w->comb && w->phases.empty() && !w->ph_all;
+  if (!pool_only) (void)hipStreamSynchronize(ctx->stream);
   weight_free(w);
 }
 extern "C" size_t ohip_weight_bytes(const ohip_weight* w) { return w ? w->bytes : 0; }
 
 static int chunk_elems(int dt) { return 16 / elem_bytes(dt); }
+
+// Packs a Gemm B operand on the device: the host matrix is copied as it is
+// into a pool buffer, converted to the compute dtype (the rounding of
+// f32_to_f16_bits / f32_to_bf16_bits) and brought into [N][Kp] K-contiguous
+// rows (zero padded) by the transpose or row-gather kernel.  A cached weight
+// gets a buffer of its own; a transient one (no key) lives in a pool buffer,
+// so a per-dispatch B costs one host copy and two small kernels, and no
+// device allocation once the pool holds its size.
+static int gemm_weight_pack_device(ohip_ctx* ctx, ohip_weight* w, const void* host, int src_dt, int64_t k, int64_t n,
+                                   int trans_b, int64_t kp, bool cached) {
+  w->ctx = ctx;
+  const int dt = w->dtype, eb = elem_bytes(dt);
+  const size_t raw = (size_t)(k * n) * elem_bytes(src_dt), packed = (size_t)(n * kp) * eb;
+  if (k * n > INT_MAX || n * kp > INT_MAX) return fail(OHIP_DECLINED, "ohip_weight_gemm: operand too large");
+  void* stage = nullptr;
+  void* conv = nullptr;
+  int rc = pool_alloc(ctx, raw, &stage);
+  if (rc) return rc;
+  auto cleanup = [&]() {
+    if (conv && conv != stage) (void)pool_free(ctx, conv);
+    (void)pool_free(ctx, stage);
+  };
+  hipError_t e = hipMemcpyAsync(stage, host, raw, hipMemcpyHostToDevice, ctx->stream);
+  // the caller's host buffer may go away when this returns
+  if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+  if (e != hipSuccess) { cleanup(); return hip_fail(e, "weight upload"); }
+  conv = stage;
+  if (src_dt != dt) {
+    rc = pool_alloc(ctx, (size_t)(k * n) * eb, &conv);
+    if (rc) { conv = nullptr; cleanup(); return rc; }
+    e = run_convert_float(src_dt, dt, stage, conv, k * n, ctx->stream);
+    if (e != hipSuccess) { cleanup(); return hip_fail(e, "weight conversion"); }
+  }
+  if (cached) {
+    e = dev_malloc(ctx, &w->data, packed ? packed : 16);
+    if (e != hipSuccess) { cleanup(); return fail(OHIP_E_NOMEM, std::string("weight hipMalloc: ") + hipGetErrorString(e)); }
+  } else {
+    rc = pool_alloc(ctx, packed ? packed : 16, &w->data);
+    if (rc) { cleanup(); return rc; }
+    w->pooled = true;
+  }
+  e = trans_b ? run_gather2d(eb, conv, k, 1, w->data, (int)n, (int)k, (int)kp, ctx->stream)
+              : run_transpose_batched(eb, conv, w->data, 1, (int)k, (int)n, (int)kp, ctx->stream);
+  cleanup();
+  if (e != hipSuccess) return hip_fail(e, "weight packing");
+  if (cached) {
+    // a cached weight is read by later calls on any stream the caller picks
+    HIP_TRY(hipStreamSynchronize(ctx->stream), "weight packing sync");
+  }
+  w->bytes = packed;
+  ctx->counters.weight_uploaded_bytes += raw;
+  ctx->counters.h2d_bytes += raw;
+  return OHIP_OK;
+}
 
 extern "C" int ohip_weight_gemm(ohip_ctx* ctx, const ohip_weight_key* key, int src_dt, const void* host,
                                 int64_t k, int64_t n, int trans_b, int dt, ohip_weight** out) {
@@ -759,14 +784,10 @@ extern "C" int ohip_weight_gemm(ohip_ctx* ctx, const ohip_weight_key* key, int s
     return OHIP_OK;
   }
   const int64_t ce = chunk_elems(dt), kp = round_up(k, ce);
-  std::vector<char> packed((size_t)(n * kp) * elem_bytes(dt), 0);
-  for (int64_t j = 0; j < n; ++j)
-    for (int64_t p = 0; p < k; ++p)
-      write_elem(dt, packed.data(), j * kp + p, src_dt, host, trans_b ? j * k + p : p * n + j);
   auto* w = new ohip_weight();
   w->kind = WK_GEMM; w->dtype = dt; w->rows = n; w->k = k;
   w->kc = (int)(kp / ce); w->ld_bytes = kp * elem_bytes(dt);
-  rc = weight_upload(ctx, w, packed.data(), packed.size());
+  rc = gemm_weight_pack_device(ctx, w, host, src_dt, k, n, trans_b, kp, key && key->name);
   if (rc) { weight_free(w); return rc; }
   return weight_finish(ctx, key, ks, w, out);
 }
@@ -2036,6 +2057,10 @@ extern "C" int ohip_get_counters(ohip_ctx* ctx, ohip_counters* out) {
   if (!ctx || !out) return fail(OHIP_E_INVALID, "null argument");
   *out = ctx->counters;
   out->device_allocs = ctx->device_allocs.load(std::memory_order_relaxed);
+  {
+    std::lock_guard<std::mutex> lock(ctx->pool_mu);
+    out->pool_live = ctx->pool.live.size();
+  }
   return OHIP_OK;
 }
 extern "C" int ohip_reset_counters(ohip_ctx* ctx) {

@@ -4,9 +4,15 @@ with every node offered to ``try_hip_dispatch_resident`` and activations kept
 resident between nodes (``RunActivations``, src/session/gpu_activations.rs:102-431:
 an activation is released after its last consumer).
 
-The reference session runs a declined node on its CPU operator; this package
-has no CPU operators, so a decline here raises ``NodeDeclined`` naming the
-node and the provider's reason.
+A node the provider cannot claim (no device arm, or a decline at dispatch
+time) runs on the caller's CPU operators, ``cpu_ops(node, inputs)``, the way
+the reference session falls back to its own operators
+(src/session/run/sequential.rs:886-932, ``materialize_resident_cuda_inputs``):
+a resident operand is read back once per run and the host copy memoized for
+every later CPU consumer, and a host value is uploaded once for its device
+consumers.  This package has no CPU operators of its own; with no
+``cpu_ops`` such a node raises ``NodeDeclined`` naming it and the provider's
+reason.
 
 ``optimize`` applies node fusions before the run, in the manner of the
 reference's optimizer passes (src/optimizer/fusion/mod.rs):
@@ -68,8 +74,15 @@ def _scalar(inits, name):
     return float(a[0]) if a.size == 1 else None
 
 
-def fuse(graph: Graph) -> Graph:
-    nodes, inits = _merge_sibling_gemms(list(graph.nodes), dict(graph.initializers), set(graph.outputs))
+def fuse(graph: Graph, level: str = "all") -> Graph:
+    """level "all": every fusion below; level "reference": only the fusion the
+    reference's own optimizer produces for these graphs, Conv followed by its
+    only consumer Relu (registry/conv_ops/conv.rs:124-156)."""
+    ref_only = level == "reference"
+    if ref_only:
+        nodes, inits = list(graph.nodes), dict(graph.initializers)
+    else:
+        nodes, inits = _merge_sibling_gemms(list(graph.nodes), dict(graph.initializers), set(graph.outputs))
     keep_out = set(graph.outputs)
     changed = True
     while changed:
@@ -85,7 +98,7 @@ def fuse(graph: Graph) -> Graph:
                 continue
             if n.op == "Conv" and "activation" not in n.attrs.strings:
                 j = sole(n.outputs[0])
-                if j is not None and nodes[j].op in ("Relu", "LeakyRelu"):
+                if j is not None and nodes[j].op in (("Relu",) if ref_only else ("Relu", "LeakyRelu")):
                     a = replace(n.attrs, strings=dict(n.attrs.strings), floats=dict(n.attrs.floats))
                     if nodes[j].op == "Relu":
                         a.strings["activation"] = "relu"
@@ -96,6 +109,8 @@ def fuse(graph: Graph) -> Graph:
                     nodes[j] = None
                     changed = True
                     break
+            if ref_only:
+                continue
             if n.op == "QLinearConv" and "activation" not in n.attrs.strings:
                 j = sole(n.outputs[0])
                 if j is None or nodes[j].op != "DequantizeLinear":
@@ -356,8 +371,17 @@ def _fuse_adain(nodes, i, sole, inits):
 class Session:
     """Runs a Graph on one HipContext with resident activations."""
 
-    def __init__(self, graph: Graph, ctx: ep.HipContext, optimize: bool = True):
-        self.graph = fuse(graph) if optimize else graph
+    def __init__(self, graph: Graph, ctx: ep.HipContext, optimize=True, cpu_ops=None):
+        """optimize: True (every fusion), "reference" (only the reference
+        optimizer's Conv + Relu) or False.  cpu_ops(node, inputs) -> list of
+        host arrays: the host's operators for nodes the provider does not
+        claim (inputs are host arrays, initializers included; '' slots are
+        None)."""
+        self.cpu_ops = cpu_ops
+        if optimize == "reference":
+            self.graph = fuse(graph, level="reference")
+        else:
+            self.graph = fuse(graph) if optimize else graph
         self.ctx = ctx
         outs = set(self.graph.outputs)
         self.last_use = {}
@@ -368,27 +392,75 @@ class Session:
         for o in outs:
             self.last_use[o] = len(self.graph.nodes)
         self.prepared = [ep.PreparedNode(n, self.graph.initializers) for n in self.graph.nodes]
+        # planned CPU islands: ops with no device arm (is_supported_op, lib.rs:217)
+        self.cpu_planned = [not ep.is_supported_op(n.op) for n in self.graph.nodes]
         # per node: the activations whose last consumer it is
         self.release = [[t for t in dict.fromkeys(n.inputs) if t and self.last_use.get(t) == i]
                         for i, n in enumerate(self.graph.nodes)]
 
-    def _forward(self, acts, keep):
+    def _host_value(self, acts, host, name):
+        """The host copy of a run value: read back once and memoized."""
+        if name in host:
+            return host[name]
+        v = acts[name]
+        if isinstance(v, ep.DeviceTensor):
+            v = v.to_host(self.ctx)
+        host[name] = v
+        return v
+
+    def _run_on_cpu(self, i, acts, host, reason):
+        n = self.graph.nodes[i]
+        if self.cpu_ops is None:
+            raise NodeDeclined(f"{n.op} node '{n.name}': {reason}")
+        inits = self.graph.initializers
+        ins = []
+        for t in n.inputs:
+            if not t:
+                ins.append(None)
+            elif t in inits:
+                v = inits[t]
+                ins.append(np.asarray(v.data if isinstance(v, ep.Typed) else v))
+            else:
+                ins.append(self._host_value(acts, host, t))
+        outs = self.cpu_ops(n, ins)
+        for name, v in zip(n.outputs, outs):
+            acts[name] = np.ascontiguousarray(v)
+            host[name] = acts[name]
+
+    def _forward(self, acts, keep, capturing=False):
         """Dispatches every node; frees each activation after its last
-        consumer unless it is in `keep`."""
+        consumer unless it is in `keep`.  Values produced on the host (CPU
+        islands) are uploaded once for their device consumers."""
+        host = {}
         for i, pn in enumerate(self.prepared):
-            res = pn.dispatch_resident(acts, self.ctx)
-            if res is None:
-                n = pn.node
-                raise NodeDeclined(f"{n.op} node '{n.name}': {self.ctx.last_decline()}")
-            acts[pn.node.outputs[0]] = res
+            n = pn.node
+            if self.cpu_planned[i]:
+                if capturing:
+                    raise NodeDeclined(f"{n.op} node '{n.name}': a CPU island cannot be captured")
+                self._run_on_cpu(i, acts, host, "no device arm for this op")
+            else:
+                for _, t in pn.dynamic:
+                    if not isinstance(acts[t], ep.DeviceTensor):
+                        acts[t] = ep.DeviceTensor.from_host(self.ctx, acts[t])
+                res = pn.dispatch_resident(acts, self.ctx)
+                if res is None:
+                    reason = self.ctx.last_decline()
+                    if capturing:
+                        raise NodeDeclined(f"{n.op} node '{n.name}': {reason}")
+                    self._run_on_cpu(i, acts, host, reason)
+                else:
+                    acts[n.outputs[0]] = res
             for t in self.release[i]:
                 if t in acts and t not in keep:
-                    acts.pop(t).free()
+                    v = acts.pop(t)
+                    host.pop(t, None)
+                    if isinstance(v, ep.DeviceTensor):
+                        v.free()
         # graph outputs leave in the ONNX layout (resident convolution
         # outputs are NHWC inside the forward)
         for o in self.graph.outputs:
             t = acts.get(o)
-            if t is not None and t not in keep:
+            if isinstance(t, ep.DeviceTensor) and t not in keep:
                 c = t.to_nchw(self.ctx)
                 if c is not t:
                     t.free()
@@ -397,17 +469,23 @@ class Session:
     def run(self, feeds: Dict[str, np.ndarray], keep_device: bool = False):
         acts = {}
         try:
+            # graph inputs stay host values until a device node consumes them
             for name in self.graph.inputs:
-                acts[name] = ep.DeviceTensor.from_host(self.ctx, np.ascontiguousarray(feeds[name]))
+                acts[name] = np.ascontiguousarray(feeds[name])
             self._forward(acts, ())
             if keep_device:
-                out = {o: acts.pop(o) for o in self.graph.outputs}
+                out = {}
+                for o in self.graph.outputs:
+                    v = acts.pop(o)
+                    out[o] = v if isinstance(v, ep.DeviceTensor) else ep.DeviceTensor.from_host(self.ctx, v)
             else:
-                out = {o: acts[o].to_host(self.ctx) for o in self.graph.outputs}
+                out = {o: (acts[o].to_host(self.ctx) if isinstance(acts[o], ep.DeviceTensor) else acts[o])
+                       for o in self.graph.outputs}
             return out
         finally:
             for t in acts.values():
-                t.free()
+                if isinstance(t, ep.DeviceTensor):
+                    t.free()
 
     def capture(self, feeds: Dict[str, np.ndarray]) -> "CapturedForward":
         """Records one forward into a HIP graph (the reference's CUDA-graph
@@ -427,7 +505,7 @@ class Session:
         acts = dict(inputs)
         L.check(lib.ohip_graph_begin(self.ctx.h))
         try:
-            self._forward(acts, set(inputs))
+            self._forward(acts, set(inputs), capturing=True)
         except BaseException:
             g = ctypes.c_void_p()
             if lib.ohip_graph_end(self.ctx.h, ctypes.byref(g)) == L.OK:

@@ -78,6 +78,48 @@ def test_parity_and_never_presets():
     assert not conv_admits(nv, 4096, 4096, 4096)
 
 
+# The MI355X crossover table (bench.py --only gate on an MI355X box; the
+# GPU / CPU ratios are recorded in the measured-table summary of profiles/).
+# (m, k, n, upload ratio, cached ratio): > 1 means the GPU lost.
+MI355X_GEMM = [
+    (1, 128, 128, 5.659, 4.006), (16, 128, 128, 3.987, 2.825), (64, 128, 128, 1.972, 1.269),
+    (96, 128, 128, 1.479, 0.966), (128, 128, 128, 1.159, 0.748), (256, 128, 128, 0.664, 0.459),
+    (1, 256, 256, 2.906, 1.817), (16, 256, 256, 1.625, 1.057), (24, 256, 256, 1.552, 0.920),
+    (32, 256, 256, 1.113, 0.663), (48, 256, 256, 0.883, 0.531), (64, 256, 256, 0.677, 0.411),
+    (1, 512, 512, 1.334, 0.488), (4, 512, 512, 1.318, 0.499), (8, 512, 512, 0.862, 0.354),
+    (12, 512, 512, 1.056, 0.436), (16, 512, 512, 0.783, 0.326), (64, 512, 512, 0.259, 0.128),
+    (1, 1024, 1024, 0.622, 0.123), (16, 1024, 1024, 0.325, 0.089), (1, 4096, 4096, 0.225, 0.004),
+    (256, 4096, 4096, 0.025, 0.005), (1, 25088, 512, 0.262, 0.007), (32, 25088, 512, 0.124, 0.012),
+]
+# (channels, H = W, ratio) of a 3x3 pad-1 conv, implied m*k*n = c*c*9*hw*hw
+MI355X_CONV = [(8, 8, 1.489), (8, 16, 1.233), (16, 8, 1.447), (16, 16, 1.012), (8, 32, 0.723),
+               (32, 8, 0.223), (16, 32, 0.416), (64, 8, 0.176), (128, 64, 0.069)]
+
+
+def test_mi355x_class_reproduces_the_measured_table():
+    """Every measured loss is declined; every admitted shape measured a win
+    (the floors err towards the CPU: some small wins are declined too)."""
+    t = tuning(L.CLASS_MI355X)
+    for m, k, n, up, cached in MI355X_GEMM:
+        if up >= 1:
+            assert not admits(t, m, k, n, False), (m, k, n, up)
+        if cached >= 1:
+            assert not admits(t, m, k, n, True), (m, k, n, cached)
+        if admits(t, m, k, n, False):
+            assert up < 1, (m, k, n, up)
+        if admits(t, m, k, n, True):
+            assert cached < 1, (m, k, n, cached)
+    for c, hw, r in MI355X_CONV:
+        mk = (c, c * 9, hw * hw)
+        if r >= 1:
+            assert not conv_admits(t, *mk), (c, hw, r)
+        if conv_admits(t, *mk):
+            assert r < 1, (c, hw, r)
+    # the skinny shapes the reference's discrete-GPU gate declines by
+    # intensity win on this box, uploading B or not
+    assert admits(t, 1, 4096, 4096, False) and admits(t, 1, 25088, 512, False)
+
+
 def test_mi355x_class_admits_every_configured_workload():
     """The recalibrated MI355X floors claim every configured dense
     contraction and still decline toy shapes."""
@@ -89,7 +131,7 @@ def test_mi355x_class_admits_every_configured_workload():
     assert conv_admits(t, 64, 64 * 9, 128 * 128)    # config 1
     assert conv_admits(t, 16, 3 * 9, 320 * 320)     # config 5 stem
     assert not admits(t, 4, 8, 8, False)
-    assert not admits(t, 1, 512, 512, True)
+    assert not admits(t, 1, 256, 256, True)
     assert not conv_admits(t, 1, 9, 16)
 
 
