@@ -468,6 +468,7 @@ def bench_e2e(torch, ctx, stream, only, no_cpu):
         loop = _time_forwards(torch, stream, lambda: sess.run(feeds))
         cap = sess.capture(feeds)
         graph = _time_forwards(torch, stream, lambda: cap.replay(feeds))
+        resident = _time_forwards(torch, stream, lambda: cap.replay(None, download=False))
         cap.close()
         # the same graph with only the fusion the reference's optimizer makes
         # (Conv + Relu): every other node runs as its own device kernel
@@ -478,12 +479,14 @@ def bench_e2e(torch, ctx, stream, only, no_cpu):
         rcap.close()
         rec = {"ms_per_forward": graph[0], "ms_per_forward_run_loop": loop[0],
                "stream_ms_graph": graph[1], "stream_ms_run_loop": loop[1],
+               "stream_ms_graph_io_resident": resident[1],
                "reference_fusions_only": {"ms_per_forward": rgraph[0], "ms_per_forward_run_loop": rloop[0],
                                           "stream_ms_graph": rgraph[1], "nodes": len(rsess.graph.nodes)},
                "nodes": len(g.nodes), "nodes_after_fusion": len(sess.graph.nodes),
                "conv_gmac": round(g.notes["conv_gmac"], 3),
                "note": "ms_per_forward: wall clock of one forward replayed from its captured HIP graph, incl. "
-                       "input upload and output download; ms_per_forward_run_loop: the same forward "
+                       "input upload and output download (PCIe); stream_ms_graph_io_resident: the replay alone, its input "
+                       "already on the device and its outputs left there; ms_per_forward_run_loop: the same forward "
                        "dispatched node by node through the Python run loop; reference_fusions_only: the "
                        "graph with only the reference optimizer's Conv+Relu fusion (no provider-side "
                        "rewrites)"}

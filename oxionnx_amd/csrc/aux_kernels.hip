@@ -848,9 +848,113 @@ qconv_direct_kernel(const uint8_t* __restrict__ x, const int8_t* __restrict__ w,
   }
 }
 
+// An ungrouped convolution with few taps x channels (an RGB stem: 3 channels
+// x 3x3) as one thread per output pixel computing every output channel: the
+// pixel's taps are read once into registers (zero-point shifted; padding taps
+// are zero, as "padding taps are skipped"), the filter sits in LDS as int16
+// (the two halves of a split row already summed, flipped rows negated), and
+// each output channel is a broadcast-read dot product plus the same epilogue
+// as qconv_direct_kernel.  An NHWC byte output leaves as 16-byte channel runs.
+constexpr int kStemTaps = 32, kStemCout = 64;
+
+__global__ void __launch_bounds__(256)
+qconv_stem_kernel(const uint8_t* __restrict__ x, const int8_t* __restrict__ w, void* __restrict__ y,
+                  DirectQConvArgs a) {
+#pragma clang fp contract(off)
+  __shared__ int16_t wl[kStemCout * kStemTaps];
+  __shared__ int tap_off[kStemTaps];   // ci * H * W + ky * dh * W + kx * dw
+  __shared__ int tap_dy[kStemTaps], tap_dx[kStemTaps];
+  const int ntaps = a.cg * a.KH * a.KW;
+  for (int i = threadIdx.x; i < kStemCout * kStemTaps; i += 256) {
+    const int co = i / kStemTaps, t = i - co * kStemTaps;
+    int v = 0;
+    if (co < a.cout && t < ntaps) {
+      const int ci = t / (a.KH * a.KW), r = t - ci * (a.KH * a.KW), ky = r / a.KW, kx = r - ky * a.KW;
+      const int8_t* wr = w + (int64_t)co * a.ldw;
+      const int64_t k = (int64_t)(ky * a.KW + kx) * a.cpg + ci;
+      v = wr[k];
+      if (a.half) v += wr[a.half + k];
+      if (a.flip && a.flip[co]) v = -v;
+    }
+    wl[i] = (int16_t)v;
+  }
+  for (int t = threadIdx.x; t < kStemTaps; t += 256) {
+    int off = 0, dy = 0, dx = 0;
+    if (t < ntaps) {
+      const int ci = t / (a.KH * a.KW), r = t - ci * (a.KH * a.KW), ky = r / a.KW, kx = r - ky * a.KW;
+      dy = ky * a.dh;
+      dx = kx * a.dw;
+      off = ci * a.H * a.W + dy * a.W + dx;
+    }
+    tap_off[t] = off; tap_dy[t] = dy; tap_dx[t] = dx;
+  }
+  __syncthreads();
+  const int64_t pixels = (int64_t)a.N * a.OH * a.OW;
+  for (int64_t p = (int64_t)blockIdx.x * 256 + threadIdx.x; p < pixels; p += (int64_t)gridDim.x * 256) {
+    const int ox = (int)(p % a.OW);
+    const int64_t r = p / a.OW;
+    const int oy = (int)(r % a.OH), n = (int)(r / a.OH);
+    const int iy0 = oy * a.sh - a.pt, ix0 = ox * a.sw - a.pl;
+    const uint8_t* xn = x + (int64_t)n * a.C * a.H * a.W + (int64_t)iy0 * a.W + ix0;
+    int32_t xv[kStemTaps];
+#pragma unroll
+    for (int t = 0; t < kStemTaps; ++t) {
+      int32_t v = 0;
+      if (t < ntaps) {
+        const int iy = iy0 + tap_dy[t], ix = ix0 + tap_dx[t];
+        if ((unsigned)iy < (unsigned)a.H && (unsigned)ix < (unsigned)a.W) {
+          const uint8_t raw = xn[tap_off[t]];
+          v = (a.x_signed ? (int32_t)(int8_t)raw : (int32_t)raw) - a.x_zp;
+        }
+      }
+      xv[t] = v;
+    }
+    uint32_t packed[4] = {0u, 0u, 0u, 0u};
+    for (int co = 0; co < a.cout; ++co) {
+      const int16_t* wr = wl + co * kStemTaps;
+      int32_t acc = 0;
+#pragma unroll
+      for (int t = 0; t < kStemTaps; ++t) acc += xv[t] * (int32_t)wr[t];
+      if (a.bias) acc += a.bias[co];
+      const int64_t o = a.nhwc_out ? p * a.ldo + co : (((int64_t)n * a.cout + co) * a.OH + oy) * a.OW + ox;
+      if (a.out_kind == QOUT_I32) {
+        reinterpret_cast<int32_t*>(y)[o] = acc;
+        continue;
+      }
+      double d = (double)acc * (double)a.comb[a.n_comb > 1 ? co : 0];
+      d = d + (double)a.y_zp;
+      d = __builtin_rint(d);
+      d = d < (double)a.lo ? (double)a.lo : d;
+      d = d > (double)a.hi ? (double)a.hi : d;
+      const int32_t q = (int32_t)d;
+      if (a.out_kind == QOUT_F32) {
+        reinterpret_cast<float*>(y)[o] = (float)q;
+        continue;
+      }
+      const uint8_t b = a.table ? a.table[q & 0xff] : (uint8_t)(q & 0xff);
+      if (a.nhwc_out && a.cout == 16 && a.ldo == 16) {
+        packed[co >> 2] |= (uint32_t)b << (8 * (co & 3));
+      } else {
+        reinterpret_cast<uint8_t*>(y)[o] = b;
+      }
+    }
+    if (a.nhwc_out && a.cout == 16 && a.ldo == 16 && a.out_kind != QOUT_I32 && a.out_kind != QOUT_F32) {
+      *reinterpret_cast<u32x4*>(reinterpret_cast<uint8_t*>(y) + p * 16) = u32x4{packed[0], packed[1], packed[2], packed[3]};
+    }
+  }
+}
+
 hipError_t run_qconv_direct(const void* x, const void* w, void* y, const DirectQConvArgs& a, hipStream_t st) {
   const int64_t total = (int64_t)a.N * a.cout * a.OH * a.OW;
   if (total <= 0) return hipSuccess;
+  if (a.cg == a.C && a.cg * a.KH * a.KW <= kStemTaps && a.cout <= kStemCout && (int64_t)a.C * a.H * a.W < INT_MAX &&
+      (!a.nhwc_out || a.cout != 16 || a.ldo != 16 || (uintptr_t)y % 16 == 0)) {
+    const int64_t pixels = (int64_t)a.N * a.OH * a.OW;
+    const unsigned grid = (unsigned)std::min<int64_t>((pixels + 255) / 256, 65535 * 16);
+    hipLaunchKernelGGL(qconv_stem_kernel, dim3(grid), dim3(256), 0, st, reinterpret_cast<const uint8_t*>(x),
+                       reinterpret_cast<const int8_t*>(w), y, a);
+    return hipGetLastError();
+  }
   const unsigned grid = (unsigned)std::min<int64_t>((total + 255) / 256, 65535 * 16);
   hipLaunchKernelGGL(qconv_direct_kernel, dim3(grid), dim3(256), 0, st, reinterpret_cast<const uint8_t*>(x),
                      reinterpret_cast<const int8_t*>(w), y, a);

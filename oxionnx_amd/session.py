@@ -527,9 +527,10 @@ class CapturedForward:
     def __init__(self, ctx, graph, inputs, outputs):
         self.ctx, self.g, self.inputs, self.outputs = ctx, graph, inputs, outputs
 
-    def replay(self, feeds: Dict[str, np.ndarray], download: bool = True):
+    def replay(self, feeds, download: bool = True):
+        """feeds None: the captured inputs keep their device contents."""
         lib = L.lib()
-        for name, t in self.inputs.items():
+        for name, t in (self.inputs.items() if feeds is not None else ()):
             arr = np.ascontiguousarray(feeds[name])
             L.check(lib.ohip_dtensor_upload(self.ctx.h, t.h, arr.ctypes.data_as(ctypes.c_void_p)))
         L.check(lib.ohip_graph_launch(self.g))

@@ -472,6 +472,11 @@ QCONV_CASES = [
     # row-tiled staging: 3 channels padded to 16, a partial channel tile
     ((1, 3, 32, 32), (16, 3, 3, 3), (2, 2), (1, 1, 1, 1), (1, 1)),
     ((2, 80, 16, 16), (16, 80, 1, 1), (1, 1), (0, 0, 0, 0), (1, 1)),
+    # few taps x channels (the pixel-per-thread stem kernel): 40 outputs,
+    # one channel with 25 taps over two images, dilation with asymmetric pads
+    ((1, 2, 17, 23), (40, 2, 3, 3), (1, 2), (1, 0, 2, 1), (1, 1)),
+    ((2, 1, 19, 15), (16, 1, 5, 5), (2, 1), (2, 2, 2, 2), (1, 1)),
+    ((1, 3, 30, 30), (24, 3, 3, 3), (1, 1), (2, 1, 2, 0), (2, 2)),
 ]
 
 
@@ -517,6 +522,31 @@ def test_conv_integer_bit_exact(torch, ctx, case):
     y = ctx.qconv2d(_dev(torch, x), wt, x_zp=100, out_kind=L.QOUT_I32, strides=s, pads=p, dilations=d)
     want = O.conv_integer(x, w, 100, 3, strides=s, pads=p, dilations=d)
     np.testing.assert_array_equal(y.cpu().numpy(), want)
+
+
+@pytest.mark.parametrize("wzp", [3, -128], ids=["split_rows", "flipped_channels"])
+@pytest.mark.parametrize("out_kind", ["i32", "u8"])
+def test_stem_integer_conv_split_and_flipped_rows(torch, ctx, wzp, out_kind):
+    """The stem kernel's filter staging: rows split in two int8 halves
+    (w_zp 3) and negated channels (w_zp -128)."""
+    from oxionnx_amd import _lib as L
+    rng = np.random.default_rng(41 + abs(wzp))
+    x = rng.integers(0, 256, (1, 3, 33, 35)).astype(np.uint8)
+    w = rng.integers(-127, 128, (16, 3, 3, 3)).astype(np.int8)
+    if out_kind == "i32":
+        wt = ctx.weight_qconv(w, zp=wzp)
+        y = ctx.qconv2d(_dev(torch, x), wt, x_zp=9, out_kind=L.QOUT_I32, strides=(2, 2), pads=(1, 1, 1, 1))
+        want = O.conv_integer(x, w, 9, wzp, strides=(2, 2), pads=[1, 1, 1, 1])
+        np.testing.assert_array_equal(y.cpu().numpy(), want)
+    else:
+        wsc = rng.uniform(0.0005, 0.002, 16).astype(np.float32)
+        wt = ctx.weight_qconv(w, zp=wzp, scale=wsc)
+        y = ctx.qconv2d(_dev(torch, x), wt, x_zp=9, out_kind=L.QOUT_U8, x_scale=1 / 255, y_scale=0.05, y_zp=128,
+                        lo=0, hi=255, strides=(2, 2), pads=(1, 1, 1, 1), out_layout=L.NHWC)
+        got = y[..., :16].permute(0, 3, 1, 2).cpu().numpy()
+        want = O.qlinear_conv(x, np.float32(1 / 255), 9, w, wsc, np.full(16, wzp), np.float32(0.05), 128,
+                              strides=(2, 2), pads=[1, 1, 1, 1])
+        np.testing.assert_array_equal(got.astype(np.float32), want)
 
 
 @pytest.mark.parametrize("case", GROUP_CASES, ids=lambda c: f"{c[0]}x{c[1]}g{c[2]}")
