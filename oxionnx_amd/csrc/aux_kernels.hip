@@ -849,111 +849,220 @@ qconv_direct_kernel(const uint8_t* __restrict__ x, const int8_t* __restrict__ w,
 }
 
 // An ungrouped convolution with few taps x channels (an RGB stem: 3 channels
-// x 3x3) as one thread per output pixel computing every output channel: the
-// pixel's taps are read once into registers (zero-point shifted; padding taps
-// are zero, as "padding taps are skipped"), the filter sits in LDS as int16
-// (the two halves of a split row already summed, flipped rows negated), and
-// each output channel is a broadcast-read dot product plus the same epilogue
-// as qconv_direct_kernel.  An NHWC byte output leaves as 16-byte channel runs.
-constexpr int kStemTaps = 32, kStemCout = 64;
+// x 3x3) on an NCHW byte image.  A block computes a kStemTH x kStemTW tile of
+// output pixels, a thread one pixel and every output channel:
+//   * the input patch the tile reads is staged in LDS with 4-byte loads (rows
+//     of the image are 4-byte aligned), a padding position holding the zero
+//     point byte, so that its (x - x_zp) term is exactly zero ("padding taps
+//     are skipped");
+//   * the filter sits in LDS as int16 in [tap][channel] order (the two halves
+//     of a split row already summed, flipped channels negated), read as
+//     16-byte broadcast vectors;
+//   * the byte table of a fused tail is copied into LDS;
+//   * the epilogue is qconv_direct_kernel's; sixteen byte channels of an NHWC
+//     output leave as one 16-byte store.
+constexpr int kStemTaps = 32, kStemCout = 64, kStemTH = 4, kStemTW = 64;
+constexpr int kStemPatchBytes = 16384;
+
+struct StemGeo {
+  int PR, RB, ND;   // patch rows, bytes per staged row (ND dwords)
+};
 
 __global__ void __launch_bounds__(256)
 qconv_stem_kernel(const uint8_t* __restrict__ x, const int8_t* __restrict__ w, void* __restrict__ y,
-                  DirectQConvArgs a) {
+                  DirectQConvArgs a, StemGeo sg) {
 #pragma clang fp contract(off)
-  __shared__ int16_t wl[kStemCout * kStemTaps];
-  __shared__ int tap_off[kStemTaps];   // ci * H * W + ky * dh * W + kx * dw
-  __shared__ int tap_dy[kStemTaps], tap_dx[kStemTaps];
+  // filter as int16 pairs of consecutive taps: wl[(t / 2) * kStemCout + co]
+  // holds taps t (low half) and t + 1 (high half) of channel co
+  __shared__ __attribute__((aligned(16))) uint32_t wl[kStemTaps / 2 * kStemCout];
+  __shared__ __attribute__((aligned(16))) uint32_t patch[kStemPatchBytes / 4];
+  __shared__ int tap_off[kStemTaps];
+  __shared__ uint8_t tab[256];
+  __shared__ int32_t sbias[kStemCout];
+  __shared__ float scomb[kStemCout];
   const int ntaps = a.cg * a.KH * a.KW;
-  for (int i = threadIdx.x; i < kStemCout * kStemTaps; i += 256) {
-    const int co = i / kStemTaps, t = i - co * kStemTaps;
-    int v = 0;
-    if (co < a.cout && t < ntaps) {
-      const int ci = t / (a.KH * a.KW), r = t - ci * (a.KH * a.KW), ky = r / a.KW, kx = r - ky * a.KW;
-      const int8_t* wr = w + (int64_t)co * a.ldw;
-      const int64_t k = (int64_t)(ky * a.KW + kx) * a.cpg + ci;
-      v = wr[k];
-      if (a.half) v += wr[a.half + k];
-      if (a.flip && a.flip[co]) v = -v;
-    }
-    wl[i] = (int16_t)v;
+  // per-channel epilogue terms in LDS: read from global memory inside the
+  // channel loop they would be one scalar-load round trip per channel
+  if (threadIdx.x < kStemCout) {
+    const int co = threadIdx.x < a.cout ? threadIdx.x : 0;
+    sbias[threadIdx.x] = a.bias ? a.bias[co] : 0;
+    scomb[threadIdx.x] = a.out_kind == QOUT_I32 ? 0.0f : a.comb[a.n_comb > 1 ? co : 0];
   }
-  for (int t = threadIdx.x; t < kStemTaps; t += 256) {
-    int off = 0, dy = 0, dx = 0;
-    if (t < ntaps) {
-      const int ci = t / (a.KH * a.KW), r = t - ci * (a.KH * a.KW), ky = r / a.KW, kx = r - ky * a.KW;
-      dy = ky * a.dh;
-      dx = kx * a.dw;
-      off = ci * a.H * a.W + dy * a.W + dx;
-    }
-    tap_off[t] = off; tap_dy[t] = dy; tap_dx[t] = dx;
-  }
-  __syncthreads();
-  const int64_t pixels = (int64_t)a.N * a.OH * a.OW;
-  for (int64_t p = (int64_t)blockIdx.x * 256 + threadIdx.x; p < pixels; p += (int64_t)gridDim.x * 256) {
-    const int ox = (int)(p % a.OW);
-    const int64_t r = p / a.OW;
-    const int oy = (int)(r % a.OH), n = (int)(r / a.OH);
-    const int iy0 = oy * a.sh - a.pt, ix0 = ox * a.sw - a.pl;
-    const uint8_t* xn = x + (int64_t)n * a.C * a.H * a.W + (int64_t)iy0 * a.W + ix0;
-    int32_t xv[kStemTaps];
+  const int kk = a.KH * a.KW;
+  // filter staging: every load of the thread's eight entries is issued
+  // before any is used (clamped addresses, masked afterwards), so the block
+  // waits for one round trip, not eight
+  {
+    constexpr int PER = kStemTaps * kStemCout / 256;
+    int8_t w0[PER], w1[PER], fl[PER];
+    bool ok[PER];
 #pragma unroll
-    for (int t = 0; t < kStemTaps; ++t) {
-      int32_t v = 0;
-      if (t < ntaps) {
-        const int iy = iy0 + tap_dy[t], ix = ix0 + tap_dx[t];
-        if ((unsigned)iy < (unsigned)a.H && (unsigned)ix < (unsigned)a.W) {
-          const uint8_t raw = xn[tap_off[t]];
-          v = (a.x_signed ? (int32_t)(int8_t)raw : (int32_t)raw) - a.x_zp;
+    for (int j = 0; j < PER; ++j) {
+      const int i = threadIdx.x + j * 256;
+      const int t = i / kStemCout, co = i - t * kStemCout;
+      ok[j] = co < a.cout && t < ntaps;
+      const int tt = ok[j] ? t : 0, cc = ok[j] ? co : 0;
+      const int ci = tt / kk, r = tt - ci * kk, ky = r / a.KW, kx = r - ky * a.KW;
+      const int8_t* wr = w + (int64_t)cc * a.ldw + (int64_t)(ky * a.KW + kx) * a.cpg + ci;
+      w0[j] = wr[0];
+      w1[j] = a.half ? wr[a.half] : (int8_t)0;
+      fl[j] = a.flip ? a.flip[cc] : (int8_t)0;
+    }
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+      int v = (int)w0[j] + (int)w1[j];
+      if (fl[j]) v = -v;
+      const int i = threadIdx.x + j * 256;
+      const int t = i / kStemCout, co = i - t * kStemCout;
+      reinterpret_cast<int16_t*>(wl)[2 * ((t >> 1) * kStemCout + co) + (t & 1)] = (int16_t)(ok[j] ? v : 0);
+    }
+  }
+  if (threadIdx.x < kStemTaps) {
+    const int t = threadIdx.x;
+    int off = 0;
+    if (t < ntaps) {
+      const int ci = t / kk, r = t - ci * kk, ky = r / a.KW, kx = r - ky * a.KW;
+      off = (ci * sg.PR + ky * a.dh) * sg.RB + kx * a.dw;
+    }
+    tap_off[t] = off;
+  }
+  if (a.table) tab[threadIdx.x] = a.table[threadIdx.x];
+
+  // stage the input patch: rows iy0 .. iy0 + PR - 1 of every channel, image
+  // columns A .. A + RB - 1 (A = the tile's first input column rounded down to
+  // a multiple of 4)
+  const int ox0 = blockIdx.x * kStemTW, oy0 = blockIdx.y * kStemTH, n = blockIdx.z;
+  const int iy0 = oy0 * a.sh - a.pt, ixl = ox0 * a.sw - a.pl;
+  const int A = ixl >= 0 ? (ixl & ~3) : -((-ixl + 3) & ~3);
+  const uint8_t padb = (uint8_t)(a.x_zp & 0xff);
+  const uint32_t pad4 = padb * 0x01010101u;
+  const uint8_t* xn = x + (int64_t)n * a.C * a.H * a.W;
+  const int total = a.C * sg.PR * sg.ND;
+  // four dwords per thread and round, their loads issued together; a dword
+  // that straddles the image's left or right edge is assembled bytewise
+  for (int i0 = 0; i0 < total; i0 += 4 * 256) {
+    uint32_t v[4];
+    int slot[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int i = i0 + j * 256 + threadIdx.x;
+      slot[j] = -1;
+      v[j] = pad4;
+      if (i < total) {
+        const int d = i % sg.ND, cr = i / sg.ND, r = cr % sg.PR, c = cr / sg.PR;
+        const int iy = iy0 + r, gx = A + 4 * d;
+        slot[j] = (c * sg.PR + r) * (sg.RB / 4) + d;
+        if ((unsigned)iy < (unsigned)a.H) {
+          const uint8_t* row = xn + ((int64_t)c * a.H + iy) * a.W;
+          if (gx >= 0 && gx + 3 < a.W) {
+            v[j] = *reinterpret_cast<const uint32_t*>(row + gx);
+          } else {
+            uint32_t u = 0;
+#pragma unroll
+            for (int b = 0; b < 4; ++b) {
+              const int gxb = gx + b;
+              const uint32_t byte = (gxb >= 0 && gxb < a.W) ? row[gxb] : padb;
+              u |= byte << (8 * b);
+            }
+            v[j] = u;
+          }
         }
       }
-      xv[t] = v;
     }
-    uint32_t packed[4] = {0u, 0u, 0u, 0u};
-    for (int co = 0; co < a.cout; ++co) {
-      const int16_t* wr = wl + co * kStemTaps;
-      int32_t acc = 0;
 #pragma unroll
-      for (int t = 0; t < kStemTaps; ++t) acc += xv[t] * (int32_t)wr[t];
-      if (a.bias) acc += a.bias[co];
+    for (int j = 0; j < 4; ++j)
+      if (slot[j] >= 0) patch[slot[j]] = v[j];
+  }
+  __syncthreads();
+
+  const int ty = threadIdx.x / kStemTW, tx = threadIdx.x - ty * kStemTW;
+  const int oy = oy0 + ty, ox = ox0 + tx;
+  if (oy >= a.OH || ox >= a.OW) return;
+  const uint8_t* pb = reinterpret_cast<const uint8_t*>(patch) + ty * a.sh * sg.RB + tx * a.sw + (ixl - A);
+  // the taps as int16 pairs (|x - x_zp| <= 255), dotted with the filter pairs
+  // by v_dot2 (two multiply-adds an instruction, exact in int32)
+  typedef short s16x2 __attribute__((ext_vector_type(2)));
+  s16x2 xp[kStemTaps / 2];
+#pragma unroll
+  for (int t = 0; t < kStemTaps; t += 2) {
+    const uint8_t r0 = t < ntaps ? pb[tap_off[t]] : padb;
+    const uint8_t r1 = t + 1 < ntaps ? pb[tap_off[t + 1]] : padb;
+    const int32_t x0 = (a.x_signed ? (int32_t)(int8_t)r0 : (int32_t)r0) - a.x_zp;
+    const int32_t x1 = (a.x_signed ? (int32_t)(int8_t)r1 : (int32_t)r1) - a.x_zp;
+    xp[t >> 1] = s16x2{(short)x0, (short)x1};
+  }
+  const int64_t p = ((int64_t)n * a.OH + oy) * a.OW + ox;
+  const bool bytes = a.out_kind != QOUT_I32 && a.out_kind != QOUT_F32;
+  for (int c0 = 0; c0 < a.cout; c0 += 16) {
+    int32_t acc[16];
+#pragma unroll
+    for (int e = 0; e < 16; ++e) acc[e] = 0;
+#pragma unroll
+    for (int tp = 0; tp < kStemTaps / 2; ++tp) {
+      if (2 * tp < ntaps) {
+        const uint32_t* wr = wl + tp * kStemCout + c0;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const u32x4 wv = *reinterpret_cast<const u32x4*>(wr + 4 * q);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const uint32_t we = wv[e];   // by value: a bit_cast of the element expression itself reads lane 0
+            acc[4 * q + e] = __builtin_amdgcn_sdot2(xp[tp], __builtin_bit_cast(s16x2, we), acc[4 * q + e], false);
+          }
+        }
+      }
+    }
+    uint32_t words[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const int co = c0 + e;
+      if (co >= a.cout) break;
+      const int32_t v = acc[e] + sbias[co];
       const int64_t o = a.nhwc_out ? p * a.ldo + co : (((int64_t)n * a.cout + co) * a.OH + oy) * a.OW + ox;
       if (a.out_kind == QOUT_I32) {
-        reinterpret_cast<int32_t*>(y)[o] = acc;
+        reinterpret_cast<int32_t*>(y)[o] = v;
         continue;
       }
-      double d = (double)acc * (double)a.comb[a.n_comb > 1 ? co : 0];
-      d = d + (double)a.y_zp;
-      d = __builtin_rint(d);
-      d = d < (double)a.lo ? (double)a.lo : d;
-      d = d > (double)a.hi ? (double)a.hi : d;
-      const int32_t q = (int32_t)d;
+      double dd = (double)v * (double)scomb[co];
+      dd = dd + (double)a.y_zp;
+      dd = __builtin_rint(dd);
+      dd = dd < (double)a.lo ? (double)a.lo : dd;
+      dd = dd > (double)a.hi ? (double)a.hi : dd;
+      const int32_t q = (int32_t)dd;
       if (a.out_kind == QOUT_F32) {
         reinterpret_cast<float*>(y)[o] = (float)q;
         continue;
       }
-      const uint8_t b = a.table ? a.table[q & 0xff] : (uint8_t)(q & 0xff);
-      if (a.nhwc_out && a.cout == 16 && a.ldo == 16) {
-        packed[co >> 2] |= (uint32_t)b << (8 * (co & 3));
-      } else {
-        reinterpret_cast<uint8_t*>(y)[o] = b;
-      }
+      const uint8_t b = a.table ? tab[q & 0xff] : (uint8_t)(q & 0xff);
+      words[e >> 2] |= (uint32_t)b << (8 * (e & 3));
+      if (!a.nhwc_out || c0 + 16 > a.cout) reinterpret_cast<uint8_t*>(y)[o] = b;
     }
-    if (a.nhwc_out && a.cout == 16 && a.ldo == 16 && a.out_kind != QOUT_I32 && a.out_kind != QOUT_F32) {
-      *reinterpret_cast<u32x4*>(reinterpret_cast<uint8_t*>(y) + p * 16) = u32x4{packed[0], packed[1], packed[2], packed[3]};
-    }
+    if (bytes && a.nhwc_out && c0 + 16 <= a.cout)
+      *reinterpret_cast<u32x4*>(reinterpret_cast<uint8_t*>(y) + p * a.ldo + c0) =
+          u32x4{words[0], words[1], words[2], words[3]};
   }
 }
 
 hipError_t run_qconv_direct(const void* x, const void* w, void* y, const DirectQConvArgs& a, hipStream_t st) {
   const int64_t total = (int64_t)a.N * a.cout * a.OH * a.OW;
   if (total <= 0) return hipSuccess;
-  if (a.cg == a.C && a.cg * a.KH * a.KW <= kStemTaps && a.cout <= kStemCout && (int64_t)a.C * a.H * a.W < INT_MAX &&
-      (!a.nhwc_out || a.cout != 16 || a.ldo != 16 || (uintptr_t)y % 16 == 0)) {
-    const int64_t pixels = (int64_t)a.N * a.OH * a.OW;
-    const unsigned grid = (unsigned)std::min<int64_t>((pixels + 255) / 256, 65535 * 16);
-    hipLaunchKernelGGL(qconv_stem_kernel, dim3(grid), dim3(256), 0, st, reinterpret_cast<const uint8_t*>(x),
-                       reinterpret_cast<const int8_t*>(w), y, a);
-    return hipGetLastError();
+  if (a.cg == a.C && a.cg * a.KH * a.KW <= kStemTaps && a.cout <= kStemCout && a.W % 4 == 0 &&
+      (int64_t)a.C * a.H * a.W < INT_MAX && (uintptr_t)x % 4 == 0 &&
+      (!a.nhwc_out || ((uintptr_t)y % 16 == 0 && a.ldo % 16 == 0)) && a.N <= 65535) {
+    StemGeo sg;
+    sg.PR = (kStemTH - 1) * a.sh + (a.KH - 1) * a.dh + 1;
+    const int pc = (kStemTW - 1) * a.sw + (a.KW - 1) * a.dw + 1;
+    sg.ND = (pc + 3) / 4 + 1;   // the tile's first column may sit up to 3 bytes into its dword
+    sg.RB = sg.ND * 4;
+    if ((int64_t)a.C * sg.PR * sg.RB <= kStemPatchBytes) {
+      dim3 grid((unsigned)((a.OW + kStemTW - 1) / kStemTW), (unsigned)((a.OH + kStemTH - 1) / kStemTH),
+                (unsigned)a.N);
+      if (grid.y <= 65535) {
+        hipLaunchKernelGGL(qconv_stem_kernel, grid, dim3(256), 0, st, reinterpret_cast<const uint8_t*>(x),
+                           reinterpret_cast<const int8_t*>(w), y, a, sg);
+        return hipGetLastError();
+      }
+    }
   }
   const unsigned grid = (unsigned)std::min<int64_t>((total + 255) / 256, 65535 * 16);
   hipLaunchKernelGGL(qconv_direct_kernel, dim3(grid), dim3(256), 0, st, reinterpret_cast<const uint8_t*>(x),

@@ -1726,7 +1726,8 @@ extern "C" int ohip_qconv2d(ohip_ctx* ctx, const ohip_qconv_desc* d, const void*
   // NCHW input; wider groups run one MFMA launch per group.  So do ungrouped
   // convolutions of an NCHW input with under 32 taps x channels (as
   // ohip_conv2d).
-  const bool narrow = G == 1 && d->in_layout == OHIP_NCHW && cg * d->kh * d->kw < 32;
+  static const int stem_mode = [] { const char* e = std::getenv("OHIP_QSTEM"); return e ? std::atoi(e) : 1; }();
+  const bool narrow = G == 1 && d->in_layout == OHIP_NCHW && cg * d->kh * d->kw < 32 && stem_mode == 1;
   const bool direct = (G > 1 && (coutg < 16 || cg * d->kh * d->kw < 32 || G > 64)) || narrow;
   if (G > 1 && d->in_layout != OHIP_NCHW && (direct || cg % 16 != 0))
     return fail(OHIP_DECLINED, "ohip_qconv2d: this grouped convolution needs an NCHW input");

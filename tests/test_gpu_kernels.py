@@ -472,11 +472,13 @@ QCONV_CASES = [
     # row-tiled staging: 3 channels padded to 16, a partial channel tile
     ((1, 3, 32, 32), (16, 3, 3, 3), (2, 2), (1, 1, 1, 1), (1, 1)),
     ((2, 80, 16, 16), (16, 80, 1, 1), (1, 1), (0, 0, 0, 0), (1, 1)),
-    # few taps x channels (the pixel-per-thread stem kernel): 40 outputs,
-    # one channel with 25 taps over two images, dilation with asymmetric pads
-    ((1, 2, 17, 23), (40, 2, 3, 3), (1, 2), (1, 0, 2, 1), (1, 1)),
+    # few taps x channels (the tiled stem kernel): 40 outputs, one channel
+    # with 25 taps over two images (odd rows: the thread-per-output kernel),
+    # dilation with asymmetric pads
+    ((1, 2, 17, 24), (40, 2, 3, 3), (1, 2), (1, 0, 2, 1), (1, 1)),
     ((2, 1, 19, 15), (16, 1, 5, 5), (2, 1), (2, 2, 2, 2), (1, 1)),
-    ((1, 3, 30, 30), (24, 3, 3, 3), (1, 1), (2, 1, 2, 0), (2, 2)),
+    ((1, 3, 30, 32), (24, 3, 3, 3), (1, 1), (2, 1, 2, 0), (2, 2)),
+    ((1, 3, 30, 30), (16, 3, 3, 3), (2, 2), (1, 1, 1, 1), (1, 1)),   # rows not 4-byte multiples
 ]
 
 
@@ -531,7 +533,7 @@ def test_stem_integer_conv_split_and_flipped_rows(torch, ctx, wzp, out_kind):
     (w_zp 3) and negated channels (w_zp -128)."""
     from oxionnx_amd import _lib as L
     rng = np.random.default_rng(41 + abs(wzp))
-    x = rng.integers(0, 256, (1, 3, 33, 35)).astype(np.uint8)
+    x = rng.integers(0, 256, (1, 3, 33, 36)).astype(np.uint8)
     w = rng.integers(-127, 128, (16, 3, 3, 3)).astype(np.int8)
     if out_kind == "i32":
         wt = ctx.weight_qconv(w, zp=wzp)
