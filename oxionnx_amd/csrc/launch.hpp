@@ -298,7 +298,11 @@ using T256 = Tile<256, 256, 2, 4, 2>;       // 6: 8 waves, 128x64 per wave
 using T128s2 = Tile<128, 128, 2, 2, 2>;     // 7: 4 waves, 64x64 per wave, two blocks per CU
 using T128w8 = Tile<128, 128, 2, 4, 2>;     // 8: 8 waves, 64x32 per wave, two blocks per CU
 using T64s4 = Tile<64, 64, 2, 2, 4>;        // 9: 4 waves, 32x32 per wave, four stages
-constexpr int kTileCount = 9;               // 10, 11: the split-K paths (launch_split_on)
+                                            // 10, 11: the split-K paths (launch_split_on)
+using T128d4 = Tile<128, 128, 2, 4, 4>;     // 12: 8 waves, 64x32 per wave, four stages (one block per CU)
+using T64d8 = Tile<64, 64, 2, 2, 8>;        // 13: 4 waves, 32x32 per wave, eight stages
+using T128x4w4 = Tile<128, 128, 2, 2, 4>;   // 14: 4 waves, 64x64 per wave, four stages
+
 
 template <Op O, bool XX, bool XY, class Tl, class LX, class LY, class Epi>
 inline hipError_t launch_tile(const LX& lx, const LY& ly, const Epi& epi, int P, int Q, int kc, hipStream_t st) {
@@ -344,7 +348,7 @@ inline hipError_t launch_split_on(const LX& lx, const LY& ly, const Epi& epi, in
 // narrowest problems.  A short K loop (few 128-byte stages) is dominated by
 // the prologue and the epilogue, which the resident 128x128 blocks overlap.
 inline int pick_tile(int P, int Q, int kc, int forced) {
-  if (forced >= 1 && forced <= kTileCount) return forced;
+  if (plain_tile_id(forced)) return forced;
   auto blocks = [&](int bp, int bq) { return (int64_t)((P + bp - 1) / bp) * ((Q + bq - 1) / bq); };
   const int nk = (kc + 7) / 8;
   if (nk <= 16) return blocks(128, 128) >= 256 ? 8 : 9;
@@ -374,6 +378,9 @@ inline hipError_t launch_any(const LX& lx, const LY& ly, const Epi& epi, int P, 
     case 7: return launch_tile<O, XX, XY, T128s2>(lx, ly, epi, P, Q, kc, st);
     case 8: return launch_tile<O, XX, XY, T128w8>(lx, ly, epi, P, Q, kc, st);
     case 9: return launch_tile<O, XX, XY, T64s4>(lx, ly, epi, P, Q, kc, st);
+    case 12: return launch_tile<O, XX, XY, T128d4>(lx, ly, epi, P, Q, kc, st);
+    case 13: return launch_tile<O, XX, XY, T64d8>(lx, ly, epi, P, Q, kc, st);
+    case 14: return launch_tile<O, XX, XY, T128x4w4>(lx, ly, epi, P, Q, kc, st);
     default: return launch_tile<O, XX, XY, T64>(lx, ly, epi, P, Q, kc, st);
   }
 }

@@ -412,12 +412,26 @@ __device__ __forceinline__ void store_group(const OutAddr& out, int eb, int64_t 
   }
 }
 
+#ifdef OHIP_KTIMING
+// Diagnostic build only (never in the shipped library): per-block stamps of
+// the 100 MHz real-time counter at kernel start, after the prologue, after
+// the K loop and at the end.
+extern __device__ uint64_t ohip_ktime[4 * 65536];
+#define OHIP_STAMP(i) do { if (threadIdx.x == 0 && blockIdx.y == 0 && blockIdx.z == 0 && blockIdx.x < 65536) \
+    ohip_ktime[(i) * 65536 + blockIdx.x] = __builtin_amdgcn_s_memrealtime(); } while (0)
+#else
+#define OHIP_STAMP(i) do {} while (0)
+#endif
+
 template <Op O, class Tl, class LX, class LY, class Epi, bool XX, bool XY>
 __global__ void __launch_bounds__(Tl::kThreads)
 mfma_gemm_kernel(const LX lx, const LY ly, const Epi epi, int nP, int nQ, int kc, int splits) {
+  OHIP_STAMP(0);
   using A = typename OpT<O>::Acc;
   using A4 = typename OpT<O>::Out4;
-  __shared__ u32x4 smem[Tl::STAGES * Tl::kStage];
+  // the stage buffers, then (after the K loop) the block's per-row epilogue terms
+  constexpr int kRowTerms = (int)((Tl::BP / 4 * sizeof(typename Epi::PreI) + 15) / 16);
+  __shared__ u32x4 smem[Tl::STAGES * Tl::kStage + kRowTerms];
   const int t = threadIdx.x;
   const int lane = t & 63;
   const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
@@ -468,6 +482,7 @@ mfma_gemm_kernel(const LX lx, const LY ly, const Epi epi, int nP, int nQ, int kc
   for (int s = 0; s < Tl::STAGES - 1; ++s) issue(kbeg + s);
   wait_vmcnt<(Tl::STAGES - 2) * NL>();
   barrier_only();
+  OHIP_STAMP(1);
 
   u32x4 fx[2][Tl::TP], fy[2][Tl::TQ];
   {
@@ -537,6 +552,7 @@ mfma_gemm_kernel(const LX lx, const LY ly, const Epi epi, int nP, int nQ, int kc
     });
   }
 
+  OHIP_STAMP(2);
   const int ibase = p0 + wp * Tl::TP * 32 + (lane >> 5) * 4;
   const int jbase = q0 + wq * Tl::TQ * 32 + (lane & 31);
   OutAddr out = epi.addr();
@@ -569,11 +585,18 @@ mfma_gemm_kernel(const LX lx, const LY ly, const Epi epi, int nP, int nQ, int kc
   if constexpr (Epi::kStageBytes > 0) smode = zaligned && epi.staged_ok(Tl::BP) ? 1 : 0;
   if constexpr (kWide) if (smode == 0 && zaligned && epi.staged_wide_ok(Tl::BP)) smode = 2;
   const bool staged = smode != 0;
-  if (staged) {
-    wait_vmcnt<0>();
-    wait_lgkm0();
-    barrier_only();
+  // The per-row epilogue terms of the block's BP rows, fetched once by the
+  // first BP / 4 threads into LDS (one global round trip for the block; read
+  // group by group from global memory they cost a round trip per group).
+  typename Epi::PreI* s_rows = reinterpret_cast<typename Epi::PreI*>(smem + Tl::STAGES * Tl::kStage);
+  if (t < Tl::BP / 4) {
+    typename Epi::PreI pr;
+    epi.load_i(pr, p0 + 4 * t);
+    s_rows[t] = pr;
   }
+  wait_vmcnt<0>();
+  wait_lgkm0();
+  barrier_only();
   auto stage_write = [&](auto ebc, int lj, int ig, const uint32_t (&bits)[4]) __attribute__((always_inline)) {
     constexpr int EB = decltype(ebc)::value;
     constexpr int CPR = Tl::BP * EB / 16;
@@ -599,8 +622,7 @@ mfma_gemm_kernel(const LX lx, const LY ly, const Epi epi, int nP, int nQ, int kc
   static_for<Tl::TP * 4>([&](auto ag) __attribute__((always_inline)) {
     constexpr int a = decltype(ag)::value / 4, g = decltype(ag)::value % 4;
     const int ig = ibase + a * 32 + 8 * g;
-    typename Epi::PreI pi;
-    epi.load_i(pi, ig);
+    const typename Epi::PreI pi = s_rows[(ig - p0) >> 2];
     int64_t row = 0;
     if (!staged) row = out.row(ig);
     static_for<Tl::TQ>([&](auto bc) __attribute__((always_inline)) {
@@ -661,6 +683,7 @@ mfma_gemm_kernel(const LX lx, const LY ly, const Epi epi, int nP, int nQ, int kc
   if constexpr (kWide) {
     if (smode == 2) flush(std::integral_constant<int, 4>{});
   }
+  OHIP_STAMP(3);
 }
 
 // Split-K: slice s of the K loop stores its raw accumulators (f32, or i32

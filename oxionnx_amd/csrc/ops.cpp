@@ -348,7 +348,7 @@ extern "C" int ohip_sync(ohip_ctx* ctx) {
 
 extern "C" int ohip_set_tile_override(ohip_ctx* ctx, int tile_id) {
   if (!ctx) return fail(OHIP_E_INVALID, "null context");
-  if (tile_id < 0 || tile_id > 11) return fail(OHIP_E_INVALID, "tile id must be 0..11");
+  if (tile_id < 0 || tile_id > 14) return fail(OHIP_E_INVALID, "tile id must be 0..14");
   ctx->tile_override = tile_id;
   return OHIP_OK;
 }
@@ -1483,7 +1483,7 @@ extern "C" int ohip_matmul(ohip_ctx* ctx, const ohip_matmul_desc* d, const void*
   o.splits = 1; o.split_ws = nullptr; o.batch = (int)d->batch; o.zstride = M * N * eb;
   DENSE_FITS_OR_DECLINE(xo, "ohip_matmul");
   DENSE_FITS_OR_DECLINE(yo, "ohip_matmul");
-  hipError_t e = run_dense_float(d->dtype, xo, yo, o, ctx->tile_override >= 1 && ctx->tile_override <= 9
+  hipError_t e = run_dense_float(d->dtype, xo, yo, o, plain_tile_id(ctx->tile_override)
                                                           ? ctx->tile_override : 0, ctx->stream);
   if (e != hipSuccess) return hip_fail(e, "ohip_matmul launch");
   return OHIP_OK;
