@@ -416,7 +416,7 @@ __device__ __forceinline__ void store_group(const OutAddr& out, int eb, int64_t 
 // Diagnostic build only (never in the shipped library): per-block stamps of
 // the 100 MHz real-time counter at kernel start, after the prologue, after
 // the K loop and at the end.
-extern __device__ uint64_t ohip_ktime[4 * 65536];
+extern __device__ uint64_t ohip_ktime[8 * 65536];
 #define OHIP_STAMP(i) do { if (threadIdx.x == 0 && blockIdx.y == 0 && blockIdx.z == 0 && blockIdx.x < 65536) \
     ohip_ktime[(i) * 65536 + blockIdx.x] = __builtin_amdgcn_s_memrealtime(); } while (0)
 #else
@@ -597,6 +597,7 @@ mfma_gemm_kernel(const LX lx, const LY ly, const Epi epi, int nP, int nQ, int kc
   wait_vmcnt<0>();
   wait_lgkm0();
   barrier_only();
+  OHIP_STAMP(4);
   auto stage_write = [&](auto ebc, int lj, int ig, const uint32_t (&bits)[4]) __attribute__((always_inline)) {
     constexpr int EB = decltype(ebc)::value;
     constexpr int CPR = Tl::BP * EB / 16;
@@ -649,6 +650,7 @@ mfma_gemm_kernel(const LX lx, const LY ly, const Epi epi, int nP, int nQ, int kc
     });
   });
 
+  OHIP_STAMP(5);
   auto flush = [&](auto ebc) __attribute__((always_inline)) {
     constexpr int EB = decltype(ebc)::value;
     constexpr int CPR = Tl::BP * EB / 16;   // 16-byte chunks per staged row
