@@ -15,6 +15,9 @@ hipError_t run_conv_f32(const Im2colOperand&, const DenseOperand&, bool, const F
 hipError_t run_conv_f16(const Im2colOperand&, const DenseOperand&, bool, const FloatOut&, int, hipStream_t);
 hipError_t run_conv_bf16(const Im2colOperand&, const DenseOperand&, bool, const FloatOut&, int, hipStream_t);
 hipError_t run_conv_i8(const Im2colOperand&, const DenseOperand&, bool, const QuantOut&, int, hipStream_t);
+hipError_t run_halo_f32(const HaloGeo&, bool, const FloatOut&, hipStream_t);
+hipError_t run_halo_f16(const HaloGeo&, bool, const FloatOut&, hipStream_t);
+hipError_t run_halo_bf16(const HaloGeo&, bool, const FloatOut&, hipStream_t);
 
 hipError_t run_dense_float(int dtype, const DenseOperand& x, const DenseOperand& y, const FloatOut& o, int tile,
                            hipStream_t st) {
@@ -32,6 +35,15 @@ hipError_t run_conv_float(int dtype, const Im2colOperand& col, const DenseOperan
     case DT_F32: return run_conv_f32(col, w, col_on_x, o, tile, st);
     case DT_F16: return run_conv_f16(col, w, col_on_x, o, tile, st);
     case DT_BF16: return run_conv_bf16(col, w, col_on_x, o, tile, st);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+hipError_t run_halo_float(int dtype, const HaloGeo& g, bool pix_on_x, const FloatOut& o, hipStream_t st) {
+  switch (dtype) {
+    case DT_F32: return run_halo_f32(g, pix_on_x, o, st);
+    case DT_F16: return run_halo_f16(g, pix_on_x, o, st);
+    case DT_BF16: return run_halo_bf16(g, pix_on_x, o, st);
     default: return hipErrorInvalidValue;
   }
 }

@@ -1,0 +1,217 @@
+// Halo-patch convolution: stride 1, dilation 1, KH x KW taps, one group,
+// NHWC input.  The engine's implicit-im2col loader fetches every tap's
+// channel chunk of every output pixel from global memory (KH * KW reads of
+// each input byte per output tile); here a block stages, per channel slab,
+// the input patch its output rows need (TH + KH - 1 rows of OW + KW - 1
+// pixels, padding read as zero) ONCE in LDS, and the KH * KW taps read their
+// MFMA fragments from that patch at a pixel offset of ky * PW + kx.  The
+// filter slab (the KH * KW taps of CC channel chunks for the block's output
+// channels) is staged next to it.  Per FLOP the block then fetches the
+// filter bytes plus about (TH + KH - 1)(OW + KW - 1) / (TH * OW * KH * KW)
+// of the activation bytes the im2col gather would: on the 512-channel 3x3
+// conv at 32x32 a stage is 29 KiB against the 72 KiB the engine's 64x64
+// tiles fetch for the same MFMA work.  That matters because a CU's vector
+// memory path delivers a fixed number of outstanding cache lines per L2
+// round trip (about 40-50 GB/s per CU here), which is what bounds these
+// mid-size convolutions, not the MFMA rate.
+//
+// A pixel tile is TH whole output rows of one image (TH * OW = the tile's
+// pixel extent), so its outputs are a contiguous run of the GEMM's pixel
+// index and the engine's epilogues (float, split-K partials) apply
+// unchanged.  PIX_ON_X puts the pixels on the X side (P = pixels, NCHW
+// output, contiguous along pixels), otherwise the filter rows are X
+// (P = output channels, NHWC output).
+//
+// LDS: a stage is [filter rows x (taps x CC chunks)] then [patch pixels x CC
+// chunks], 16-byte chunks XOR-swizzled within each row so that 16
+// consecutive rows (filter rows, or patch pixels at any starting offset)
+// read at one logical chunk fall on 16 distinct bank groups.  The DMA
+// loads write 1 KiB of contiguous LDS each; load m of a stage belongs to
+// wave m % waves, so the per-wave load count (and with it the vmcnt waits)
+// is one of two compile-time values.
+#pragma once
+#include "internal.hpp"
+#include "mfma_core.hpp"
+
+namespace ohip {
+
+template <int BP_, int BQ_, int WP_, int WQ_, int CC_, int STAGES_, int KH_, int KW_, int PIXMAX_, bool PIX_ON_X_>
+struct HaloTile {
+  static constexpr int BP = BP_, BQ = BQ_, WP = WP_, WQ = WQ_, CC = CC_, STAGES = STAGES_;
+  static constexpr int KH = KH_, KW = KW_, TAPS = KH * KW, PIXMAX = PIXMAX_;
+  static constexpr bool PIX_ON_X = PIX_ON_X_;
+  static constexpr int kWaves = WP * WQ, kThreads = 64 * kWaves;
+  static constexpr int TP = BP / (WP * 32), TQ = BQ / (WQ * 32);
+  static constexpr int BPIX = PIX_ON_X ? BP : BQ, BCO = PIX_ON_X ? BQ : BP;
+  static constexpr int RW = TAPS * CC;                    // chunks per staged filter row
+  static constexpr int WI = BCO * RW / 64;                // filter DMA loads per stage
+  static constexpr int PI = (PIXMAX * CC + 63) / 64;      // patch DMA loads per stage
+  static constexpr int TI = WI + PI;
+  static constexpr int kStage = TI * 64;                  // u32x4 slots per stage
+  static constexpr int NLO = TI / kWaves, NHI = (TI + kWaves - 1) / kWaves;
+  static_assert(CC == 2 || CC == 4, "slabs of 2 or 4 chunks");
+  static_assert(BCO * RW % 64 == 0, "filter slab must be whole DMA loads");
+  static_assert(TP >= 1 && TQ >= 1, "wave tile must hold a 32x32 MFMA tile");
+  static_assert(STAGES >= 2 && STAGES * kStage * 16 + 4096 <= 160 * 1024, "LDS budget");
+  static_assert(2 * NHI < 64, "vmcnt range");
+};
+
+// bank-group swizzle of a row's chunks (row stride a multiple of CC chunks)
+template <int CC> __device__ __forceinline__ int halo_swz(int r) {
+  if constexpr (CC == 2) return (r >> 3) & 1;
+  else return (r >> 2) & 3;
+}
+
+template <Op O, class Ht, class Epi>
+__global__ void __launch_bounds__(Ht::kThreads)
+halo_conv_kernel(const HaloGeo g, const Epi epi, int nP, int nQ, int splits, int gp) {
+  OHIP_STAMP(0);
+  using A = typename OpT<O>::Acc;
+  constexpr int CC = Ht::CC;
+  constexpr int kRowTerms = (int)((Ht::BP / 4 * sizeof(typename Epi::PreI) + 15) / 16);
+  __shared__ u32x4 smem[Ht::STAGES * Ht::kStage + kRowTerms];
+  const int t = threadIdx.x;
+  const int lane = t & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+  const int wp = wave % Ht::WP, wq = wave / Ht::WP;
+  int tp, tq;
+  map_tile(blockIdx.x, gridDim.x, nP, nQ, gp, tp, tq);
+  const int p0 = tp * Ht::BP, q0 = tq * Ht::BQ;
+  const int pix0 = Ht::PIX_ON_X ? p0 : q0;
+  const int co0 = Ht::PIX_ON_X ? q0 : p0;
+  const int ohw = g.OH * g.OW;
+  const int n = pix0 / ohw;
+  const int oy0 = (pix0 - n * ohw) >> g.ow_shift;
+  const int PW = g.OW + Ht::KW - 1;
+  const int npix = (g.th + Ht::KH - 1) * PW;
+
+  const __amdgpu_buffer_rsrc_t rw =
+      __builtin_amdgcn_make_buffer_rsrc((void*)(g.w + (int64_t)co0 * g.ldw), (short)0, 0x7fffffff, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rx =
+      __builtin_amdgcn_make_buffer_rsrc((void*)(g.x + (int64_t)n * g.img_bytes), (short)0, 0x7fffffff, 0x00020000);
+
+  // this thread's share of a stage's DMA loads: global offset at slab 0 and
+  // the channel chunk within the slab (for the channel tail)
+  int voff[Ht::NHI], sub[Ht::NHI];
+#pragma unroll
+  for (int i = 0; i < Ht::NHI; ++i) {
+    const int m = i * Ht::kWaves + wave;
+    voff[i] = kOobOffset;
+    sub[i] = 0;
+    if (m < Ht::WI) {
+      const int slot = m * 64 + lane;
+      const int row = slot / Ht::RW, phys = slot - row * Ht::RW;
+      const int c = phys ^ halo_swz<CC>(row);
+      const int tap = c / CC, s = c - tap * CC;
+      sub[i] = s;
+      if (co0 + row < g.cout) voff[i] = (int)(row * g.ldw) + (tap * g.cpc + s) * 16;
+    } else if (m < Ht::TI) {
+      const int slot = (m - Ht::WI) * 64 + lane;
+      const int pix = slot / CC, phys = slot - pix * CC;
+      const int c = phys ^ halo_swz<CC>(pix);
+      const int py = pix / PW, px = pix - py * PW;
+      const int iy = oy0 + py - g.pt, ix = px - g.pl;
+      sub[i] = c;
+      if (pix < npix && (unsigned)iy < (unsigned)g.H && (unsigned)ix < (unsigned)g.W)
+        voff[i] = ((iy * g.W + ix) * g.pstride + c) * 16;
+    }
+  }
+
+  const int nslab = (g.cpc + CC - 1) / CC;
+  const int per = (nslab + splits - 1) / splits;
+  const int sbeg = (int)blockIdx.y * per;
+  const int send = min(sbeg + per, nslab);
+  // Every stage issues the same loads (past the last slab, and in the
+  // channel tail, they read zero through the range check), so the waits are
+  // fixed counts.
+  auto issue = [&](int s) __attribute__((always_inline)) {
+    u32x4* base = smem + (s % Ht::STAGES) * Ht::kStage;
+    const bool live = s < send;
+    const int soff = s * CC * 16;
+#pragma unroll
+    for (int i = 0; i < Ht::NHI; ++i) {
+      const int m = i * Ht::kWaves + wave;
+      if (m < Ht::TI) {
+        const int off = live && s * CC + sub[i] < g.cpc ? voff[i] : kOobOffset;
+        buf16(m < Ht::WI ? rw : rx, off, soff, base + m * 64);
+      }
+    }
+  };
+  auto wait_stages = [&](auto kc) __attribute__((always_inline)) {
+    constexpr int K = decltype(kc)::value;
+    if (wave < Ht::TI % Ht::kWaves) wait_vmcnt<K * Ht::NHI>();
+    else wait_vmcnt<K * Ht::NLO>();
+  };
+
+  // fragment slots: filter rows (chunk t * CC + 2u + lane / 32, swizzled),
+  // patch pixels (tap offset added per tap)
+  constexpr int TCO = Ht::PIX_ON_X ? Ht::TQ : Ht::TP;
+  constexpr int TPX = Ht::PIX_ON_X ? Ht::TP : Ht::TQ;
+  const int wco = Ht::PIX_ON_X ? wq : wp, wpx = Ht::PIX_ON_X ? wp : wq;
+  const int hi = lane >> 5;
+  int wslot[TCO][CC / 2];
+#pragma unroll
+  for (int c = 0; c < TCO; ++c) {
+    const int row = wco * TCO * 32 + c * 32 + (lane & 31);
+#pragma unroll
+    for (int u = 0; u < CC / 2; ++u) wslot[c][u] = row * Ht::RW + ((2 * u + hi) ^ halo_swz<CC>(row));
+  }
+  int pbase[TPX];
+#pragma unroll
+  for (int b = 0; b < TPX; ++b) {
+    const int ql = wpx * TPX * 32 + b * 32 + (lane & 31);
+    const int qy = ql >> g.ow_shift, qx = ql & (g.OW - 1);
+    pbase[b] = qy * PW + qx;
+  }
+
+  A acc[Ht::TP][Ht::TQ];
+#pragma unroll
+  for (int a = 0; a < Ht::TP; ++a)
+#pragma unroll
+    for (int b = 0; b < Ht::TQ; ++b)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[a][b][e] = 0;
+
+#pragma unroll
+  for (int s = 0; s < Ht::STAGES - 1; ++s) issue(sbeg + s);
+  wait_stages(std::integral_constant<int, Ht::STAGES - 2>{});
+  barrier_only();
+  OHIP_STAMP(1);
+
+  for (int s = sbeg; s < send; ++s) {
+    issue(s + Ht::STAGES - 1);
+    const u32x4* S = smem + (s % Ht::STAGES) * Ht::kStage;
+    const u32x4* SP = S + Ht::WI * 64;
+    static_for<Ht::TAPS>([&](auto tc) __attribute__((always_inline)) {
+      constexpr int tap = decltype(tc)::value;
+      constexpr int ky = tap / Ht::KW, kx = tap % Ht::KW;
+      const int toff = ky * PW + kx;
+      static_for<CC / 2>([&](auto uc) __attribute__((always_inline)) {
+        constexpr int u = decltype(uc)::value;
+        u32x4 wf[TCO], pf[TPX];
+#pragma unroll
+        for (int c = 0; c < TCO; ++c) wf[c] = S[wslot[c][u] + tap * CC];
+#pragma unroll
+        for (int b = 0; b < TPX; ++b) {
+          const int pix = pbase[b] + toff;
+          pf[b] = SP[pix * CC + ((2 * u + hi) ^ halo_swz<CC>(pix))];
+        }
+#pragma unroll
+        for (int a = 0; a < Ht::TP; ++a)
+#pragma unroll
+          for (int b = 0; b < Ht::TQ; ++b) {
+            if constexpr (Ht::PIX_ON_X) acc[a][b] = OpT<O>::mma(pf[a], wf[b], acc[a][b]);
+            else acc[a][b] = OpT<O>::mma(wf[a], pf[b], acc[a][b]);
+          }
+      });
+    });
+    wait_stages(std::integral_constant<int, Ht::STAGES - 2>{});
+    wait_lgkm0();
+    barrier_only();
+  }
+  OHIP_STAMP(2);
+  tile_epilogue<O, Ht>(epi, acc, smem, p0, q0, wp, wq, lane, t);
+  OHIP_STAMP(3);
+}
+
+}  // namespace ohip

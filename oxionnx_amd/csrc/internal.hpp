@@ -199,6 +199,26 @@ struct GemvArgs {
   int M, N, kc;
 };
 
+// Halo-patch convolution geometry (stride 1, dilation 1, one group, NHWC
+// input, pixel tiles of whole output rows); see halo_conv_kernel.
+struct HaloGeo {
+  const char* x;      // NHWC input, image 0; pixels are `pstride` 16-byte chunks apart
+  int64_t img_bytes;  // bytes between images
+  int H, W, OH, OW;
+  int pt, pl;         // zero padding (top, left); the patch reads zeros outside the image
+  int pstride;
+  int cpc;            // channel chunks per tap (the input's valid chunks and the filter's)
+  int th;             // output rows per pixel tile
+  int ow_shift;       // log2(OW)
+  const char* w;      // filter rows [cout][KH * KW taps][cpc chunks]
+  int64_t ldw;        // bytes between filter rows
+  int cout;           // valid filter rows
+};
+hipError_t run_halo_float(int dtype, const HaloGeo& g, bool pix_on_x, const FloatOut& o, hipStream_t st);
+// pixel-tile extent and largest staged patch of the halo path
+constexpr int kHaloBPix = 256;
+constexpr int kHaloPixMax = 400;
+
 hipError_t run_dense_float(int dtype, const DenseOperand& x, const DenseOperand& y, const FloatOut& o, int tile,
                            hipStream_t st);
 hipError_t run_conv_float(int dtype, const Im2colOperand& col, const DenseOperand& w, bool col_on_x,

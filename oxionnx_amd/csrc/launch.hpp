@@ -6,6 +6,7 @@
 
 #include "internal.hpp"
 #include "mfma_core.hpp"
+#include "halo_conv.hpp"
 
 #include <cstdlib>
 #include <type_traits>
@@ -304,6 +305,13 @@ using T64d8 = Tile<64, 64, 2, 2, 8>;        // 13: 4 waves, 32x32 per wave, eigh
 using T128x4w4 = Tile<128, 128, 2, 2, 4>;   // 14: 4 waves, 64x64 per wave, four stages
 
 
+// Tiles per XCD group along P in the engine's tile order (map_tile);
+// OHIP_GP overrides the default of 8 (a measurement switch)
+inline int tile_group_width() {
+  static const int v = [] { const char* e = std::getenv("OHIP_GP"); return e ? std::max(1, std::atoi(e)) : 8; }();
+  return v;
+}
+
 template <Op O, bool XX, bool XY, class Tl, class LX, class LY, class Epi>
 inline hipError_t launch_tile(const LX& lx, const LY& ly, const Epi& epi, int P, int Q, int kc, hipStream_t st) {
   const int nP = (P + Tl::BP - 1) / Tl::BP, nQ = (Q + Tl::BQ - 1) / Tl::BQ;
@@ -312,7 +320,22 @@ inline hipError_t launch_tile(const LX& lx, const LY& ly, const Epi& epi, int P,
   if (nb <= 0) return hipSuccess;
   if (nb > 0x7fffffff || batch > 65535) return hipErrorInvalidValue;
   hipLaunchKernelGGL((mfma_gemm_kernel<O, Tl, LX, LY, Epi, XX, XY>), dim3((unsigned)nb, 1, (unsigned)batch),
-                     dim3(Tl::kThreads), 0, st, lx, ly, epi, nP, nQ, kc, 1);
+                     dim3(Tl::kThreads), 0, st, lx, ly, epi, nP, nQ, kc, 1, tile_group_width());
+  return hipGetLastError();
+}
+
+// The ordered reduction of `splits` partial-sum slices (PartialEpi layout),
+// which applies the real epilogue.
+template <Op O, class Epi>
+inline hipError_t launch_reduce(const void* ws, int splits, int P, int Q, const Epi& epi, hipStream_t st) {
+  using T = typename std::conditional<O == Op::I8, int32_t, float>::type;
+  using V = typename OpT<O>::Out4;
+  const int Pp = (P + 3) / 4 * 4;
+  const int64_t groups = (int64_t)(Pp / 4) * Q;
+  if (groups > 0x7fffffff) return hipErrorInvalidValue;   // the reduction indexes groups in 32 bits
+  const unsigned grid = (unsigned)std::min<int64_t>((groups + 255) / 256, 65535 * 4);
+  hipLaunchKernelGGL((split_reduce_kernel<T, V, Epi>), dim3(grid), dim3(256), 0, st, reinterpret_cast<const T*>(ws),
+                     splits, P, Pp, Q, epi);
   return hipGetLastError();
 }
 
@@ -322,7 +345,6 @@ template <Op O, bool XX, bool XY, class Tl, class LX, class LY, class Epi>
 inline hipError_t launch_split_on(const LX& lx, const LY& ly, const Epi& epi, int P, int Q, int kc, int splits,
                                   void* ws, hipStream_t st) {
   using T = typename std::conditional<O == Op::I8, int32_t, float>::type;
-  using V = typename OpT<O>::Out4;
   const int nP = (P + Tl::BP - 1) / Tl::BP, nQ = (Q + Tl::BQ - 1) / Tl::BQ;
   const int64_t nb = (int64_t)nP * nQ;
   if (nb <= 0) return hipSuccess;
@@ -330,15 +352,39 @@ inline hipError_t launch_split_on(const LX& lx, const LY& ly, const Epi& epi, in
   const int Pp = (P + 3) / 4 * 4;
   PartialEpi<T> pe{reinterpret_cast<T*>(ws), P, Pp, Q};
   hipLaunchKernelGGL((mfma_gemm_kernel<O, Tl, LX, LY, PartialEpi<T>, XX, XY>), dim3((unsigned)nb, (unsigned)splits),
-                     dim3(Tl::kThreads), 0, st, lx, ly, pe, nP, nQ, kc, splits);
+                     dim3(Tl::kThreads), 0, st, lx, ly, pe, nP, nQ, kc, splits, tile_group_width());
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  const int64_t groups = (int64_t)(Pp / 4) * Q;
-  if (groups > 0x7fffffff) return hipErrorInvalidValue;   // the reduction indexes groups in 32 bits
-  const unsigned grid = (unsigned)std::min<int64_t>((groups + 255) / 256, 65535 * 4);
-  hipLaunchKernelGGL((split_reduce_kernel<T, V, Epi>), dim3(grid), dim3(256), 0, st, reinterpret_cast<const T*>(ws),
-                     splits, P, Pp, Q, epi);
-  return hipGetLastError();
+  return launch_reduce<O>(ws, splits, P, Q, epi, st);
+}
+
+// Halo-patch convolution (halo_conv_kernel): 64 output channels x 256
+// pixels per block, eight waves, four stages of two-chunk slabs.  Each XCD
+// owns whole output-channel tiles (the filter is the operand that would be
+// re-read), with every pixel tile of them.
+template <Op O, bool PIXX, class Epi>
+inline hipError_t launch_halo(const HaloGeo& g, const Epi& epi, int P, int Q, int splits, void* ws, hipStream_t st) {
+  using Ht = HaloTile<PIXX ? kHaloBPix : 64, PIXX ? 64 : kHaloBPix, PIXX ? 4 : 2, PIXX ? 2 : 4, 2, 4, 3, 3,
+                      kHaloPixMax, PIXX>;
+  using T = typename std::conditional<O == Op::I8, int32_t, float>::type;
+  const int nP = (P + Ht::BP - 1) / Ht::BP, nQ = (Q + Ht::BQ - 1) / Ht::BQ;
+  const int64_t nb = (int64_t)nP * nQ;
+  if (nb <= 0) return hipSuccess;
+  if (nb > 0x7fffffff || splits < 1 || splits > 65535) return hipErrorInvalidValue;
+  const int gp = PIXX ? nP : 1;
+  if (splits == 1) {
+    hipLaunchKernelGGL((halo_conv_kernel<O, Ht, Epi>), dim3((unsigned)nb, 1), dim3(Ht::kThreads), 0, st, g, epi, nP,
+                       nQ, 1, gp);
+    return hipGetLastError();
+  }
+  if (!ws) return hipErrorInvalidValue;
+  const int Pp = (P + 3) / 4 * 4;
+  PartialEpi<T> pe{reinterpret_cast<T*>(ws), P, Pp, Q};
+  hipLaunchKernelGGL((halo_conv_kernel<O, Ht, PartialEpi<T>>), dim3((unsigned)nb, (unsigned)splits),
+                     dim3(Ht::kThreads), 0, st, g, pe, nP, nQ, splits, gp);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  return launch_reduce<O>(ws, splits, P, Q, epi, st);
 }
 
 // Automatic choice (split-K is decided beforehand, plan_splits).  The
@@ -365,6 +411,11 @@ inline hipError_t launch_any(const LX& lx, const LY& ly, const Epi& epi, int P, 
                              int splits, void* split_ws, hipStream_t st) {
   if (splits > 1 && epi.out.batch > 1) return hipErrorInvalidValue;   // one workspace: no split-K per slice
   if (splits > 1) {
+    // OHIP_SPLIT_TILE=12/13/14 runs the slices on that deeper-pipelined tile (a measurement switch)
+    static const int sv = [] { const char* e = std::getenv("OHIP_SPLIT_TILE"); return e ? std::atoi(e) : 0; }();
+    if (sv == 12) return launch_split_on<O, XX, XY, T128d4>(lx, ly, epi, P, Q, kc, splits, split_ws, st);
+    if (sv == 13) return launch_split_on<O, XX, XY, T64d8>(lx, ly, epi, P, Q, kc, splits, split_ws, st);
+    if (sv == 14) return launch_split_on<O, XX, XY, T128x4w4>(lx, ly, epi, P, Q, kc, splits, split_ws, st);
     if (split_tile_size(P, Q, tile) == 128)
       return launch_split_on<O, XX, XY, T128w8>(lx, ly, epi, P, Q, kc, splits, split_ws, st);
     return launch_split_on<O, XX, XY, T64s4>(lx, ly, epi, P, Q, kc, splits, split_ws, st);
@@ -395,7 +446,7 @@ inline int stage_allowed() {
 }
 
 inline OutAddr make_out_addr(const OutMap& o) {
-  OutAddr a;
+  OutAddr a{};
   a.stage = stage_allowed();
   a.y = reinterpret_cast<char*>(o.y);
   a.si = o.si; a.sj = o.sj; a.bstride = o.bstride; a.ohw = o.ohw > 0 ? o.ohw : 1;

@@ -294,14 +294,13 @@ template <int N> struct Unroll<N, N> {
 // the 8 XCDs in turn; remapping makes each XCD own a contiguous run of
 // logical tiles, and the grouped order inside a run keeps GP P-tiles sharing
 // the same Q-tile panel resident in that XCD's L2.
-__device__ __forceinline__ void map_tile(int bid, int nb, int nP, int nQ, int& tp, int& tq) {
+__device__ __forceinline__ void map_tile(int bid, int nb, int nP, int nQ, int gp, int& tp, int& tq) {
   int id = bid;
   if ((nb & 7) == 0) id = (bid & 7) * (nb >> 3) + (bid >> 3);
-  constexpr int GP = 8;
-  const int per_group = GP * nQ;
+  const int per_group = gp * nQ;
   const int g = id / per_group;
-  const int first = g * GP;
-  const int gsz = min(nP - first, GP);
+  const int first = g * gp;
+  const int gsz = min(nP - first, gp);
   const int within = id - g * per_group;
   tp = first + within % gsz;
   tq = within / gsz;
@@ -417,142 +416,21 @@ __device__ __forceinline__ void store_group(const OutAddr& out, int eb, int64_t 
 // the 100 MHz real-time counter at kernel start, after the prologue, after
 // the K loop and at the end.
 extern __device__ uint64_t ohip_ktime[8 * 65536];
-#define OHIP_STAMP(i) do { if (threadIdx.x == 0 && blockIdx.y == 0 && blockIdx.z == 0 && blockIdx.x < 65536) \
-    ohip_ktime[(i) * 65536 + blockIdx.x] = __builtin_amdgcn_s_memrealtime(); } while (0)
+#define OHIP_STAMP(i) do { const uint32_t kt_b = blockIdx.y * gridDim.x + blockIdx.x; \
+    if (threadIdx.x == 0 && blockIdx.z == 0 && kt_b < 65536) \
+    ohip_ktime[(i) * 65536 + kt_b] = __builtin_amdgcn_s_memrealtime(); } while (0)
 #else
 #define OHIP_STAMP(i) do {} while (0)
 #endif
 
-template <Op O, class Tl, class LX, class LY, class Epi, bool XX, bool XY>
-__global__ void __launch_bounds__(Tl::kThreads)
-mfma_gemm_kernel(const LX lx, const LY ly, const Epi epi, int nP, int nQ, int kc, int splits) {
-  OHIP_STAMP(0);
-  using A = typename OpT<O>::Acc;
+// The block's epilogue: finishes the accumulators of the tile at (p0, q0)
+// through `epi` (staged through `smem`, which holds at least
+// Tl::STAGES * Tl::kStage + the row-term tail u32x4 slots, free once the
+// K loop's loads have landed).  Shared by every contraction kernel.
+template <Op O, class Tl, class Epi, class A>
+__device__ __forceinline__ void tile_epilogue(const Epi& epi, A (&acc)[Tl::TP][Tl::TQ], u32x4* smem, int p0, int q0,
+                                              int wp, int wq, int lane, int t) {
   using A4 = typename OpT<O>::Out4;
-  // the stage buffers, then (after the K loop) the block's per-row epilogue terms
-  constexpr int kRowTerms = (int)((Tl::BP / 4 * sizeof(typename Epi::PreI) + 15) / 16);
-  __shared__ u32x4 smem[Tl::STAGES * Tl::kStage + kRowTerms];
-  const int t = threadIdx.x;
-  const int lane = t & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
-  const int wp = wave % Tl::WP, wq = wave / Tl::WP;
-  int tp, tq;
-  map_tile(blockIdx.x, gridDim.x, nP, nQ, tp, tq);
-  const int p0 = tp * Tl::BP, q0 = tq * Tl::BQ;
-
-  typename LX::template State<Tl::NX> sx;
-  typename LY::template State<Tl::NY> sy;
-  lx.template init<Tl::NX, Tl::kWaves, Tl::CH>(sx, p0, lane, wave);
-  ly.template init<Tl::NY, Tl::kWaves, Tl::CH>(sy, q0, lane, wave);
-
-  A acc[Tl::TP][Tl::TQ];
-#pragma unroll
-  for (int a = 0; a < Tl::TP; ++a)
-#pragma unroll
-    for (int b = 0; b < Tl::TQ; ++b)
-#pragma unroll
-      for (int e = 0; e < 16; ++e) acc[a][b][e] = 0;
-
-  // K stages of this block: all of them, or slice blockIdx.y of `splits`
-  const int nk_all = (kc + Tl::CH - 1) / Tl::CH;
-  const int per = (nk_all + splits - 1) / splits;
-  const int kbeg = (int)blockIdx.y * per;
-  const int kend = min(kbeg + per, nk_all);
-  constexpr int NL = Tl::NX + Tl::NY;     // DMA loads per thread per stage
-  // Every stage issues all its loads (past the last stage they read zero or
-  // the pad source), so the waits below are fixed counts of outstanding loads.
-  auto issue = [&](int kt) {
-    u32x4* s = smem + (kt % Tl::STAGES) * Tl::kStage;
-    lx.template issue<Tl::NX, Tl::kWaves, Tl::CH>(sx, kt, wave, s);
-    ly.template issue<Tl::NY, Tl::kWaves, Tl::CH>(sy, kt, wave, s + Tl::BP * Tl::kRowStride);
-  };
-
-  // Fragment slots of this lane: rows are tile bases (multiples of 32) plus
-  // lane % 32, chunk 2 * ks + lane / 32.
-  const int xr = wp * Tl::TP * 32 + (lane & 31);
-  const int yr = Tl::BP + wq * Tl::TQ * 32 + (lane & 31);
-  int xslot[Tl::KS], yslot[Tl::KS];
-#pragma unroll
-  for (int ks = 0; ks < Tl::KS; ++ks) {
-    xslot[ks] = xr * Tl::kRowStride + lds_slot<Tl::CH>(xr, 2 * ks + (lane >> 5));
-    yslot[ks] = yr * Tl::kRowStride + lds_slot<Tl::CH>(yr, 2 * ks + (lane >> 5));
-  }
-
-#pragma unroll
-  for (int s = 0; s < Tl::STAGES - 1; ++s) issue(kbeg + s);
-  wait_vmcnt<(Tl::STAGES - 2) * NL>();
-  barrier_only();
-  OHIP_STAMP(1);
-
-  u32x4 fx[2][Tl::TP], fy[2][Tl::TQ];
-  {
-    const u32x4* s0 = smem + (kbeg % Tl::STAGES) * Tl::kStage;
-#pragma unroll
-    for (int a = 0; a < Tl::TP; ++a) fx[0][a] = s0[xslot[0] + a * 32 * Tl::kRowStride];
-#pragma unroll
-    for (int b = 0; b < Tl::TQ; ++b) fy[0][b] = s0[yslot[0] + b * 32 * Tl::kRowStride];
-  }
-
-  // One k-step in program order, fenced so the compiler keeps it: each MFMA
-  // is followed by at most one fragment read for the next k-step (in the
-  // order the next k-step consumes them, so the waits before its MFMAs are
-  // partial) and, on k-step 0, by one DMA load of the stage STAGES - 1 ahead.
-  // The last k-step reads the next stage: its first MFMAs go before the
-  // stage barrier, which then overlaps them.
-  constexpr int NM = Tl::TP * Tl::TQ;      // MFMAs per k-step
-  constexpr int NRD = Tl::TP + Tl::TQ;     // fragment reads per k-step
-  constexpr int PRE = NM >= 4 ? 2 : 0;     // MFMAs of the last k-step ahead of the barrier
-  for (int kt = kbeg; kt < kend; ++kt) {
-    const u32x4* s = smem + (kt % Tl::STAGES) * Tl::kStage;
-    const u32x4* sn = smem + ((kt + 1) % Tl::STAGES) * Tl::kStage;
-    u32x4* sd = smem + ((kt + Tl::STAGES - 1) % Tl::STAGES) * Tl::kStage;
-    const typename LX::Step stx = lx.template step<Tl::NX, Tl::kWaves, Tl::CH>(sx, kt + Tl::STAGES - 1);
-    const typename LY::Step sty = ly.template step<Tl::NY, Tl::kWaves, Tl::CH>(sy, kt + Tl::STAGES - 1);
-    auto dma = [&](int i) __attribute__((always_inline)) {
-      if (i < Tl::NX) lx.template load<Tl::NX, Tl::kWaves, Tl::CH>(sx, stx, i, wave, sd);
-      else ly.template load<Tl::NY, Tl::kWaves, Tl::CH>(sy, sty, i - Tl::NX, wave, sd + Tl::BP * Tl::kRowStride);
-    };
-    static_for<Tl::KS>([&](auto ksc) __attribute__((always_inline)) {
-      constexpr int ks = decltype(ksc)::value;
-      constexpr bool last = ks == Tl::KS - 1;
-      constexpr int cur = ks & 1, nxt = cur ^ 1;
-      const u32x4* src = last ? sn : s;
-      const int kr = last ? 0 : ks + 1;
-      // read r of the next k-step: fx[0], fy[0 .. TQ-1], fx[1 .. TP-1]
-      auto read = [&](auto rc) __attribute__((always_inline)) {
-        constexpr int r = decltype(rc)::value;
-        if constexpr (r == 0) fx[nxt][0] = src[xslot[kr]];
-        else if constexpr (r <= Tl::TQ) fy[nxt][r - 1] = src[yslot[kr] + (r - 1) * 32 * Tl::kRowStride];
-        else fx[nxt][r - Tl::TQ] = src[xslot[kr] + (r - Tl::TQ) * 32 * Tl::kRowStride];
-      };
-      static_for<NM>([&](auto mc) __attribute__((always_inline)) {
-        constexpr int m = decltype(mc)::value;
-        constexpr int a = m / Tl::TQ, b = m % Tl::TQ;
-        if constexpr (last && m == PRE) {
-          wait_vmcnt<(Tl::STAGES - 2) * NL>();
-          wait_lgkm0();
-          barrier_only();
-        }
-        acc[a][b] = OpT<O>::mma(frag<XX>(fx[cur][a]), frag<XY>(fy[cur][b]), acc[a][b]);
-        __builtin_amdgcn_sched_barrier(0);
-        constexpr int r = last ? m - PRE : m;
-        if constexpr (r >= 0 && r < NRD) read(std::integral_constant<int, r>{});
-        if constexpr (ks == 0 && m < NL) dma(m);
-        __builtin_amdgcn_sched_barrier(0);
-      });
-      // the reads and loads that outnumber the MFMAs (small tiles)
-      static_for<(NRD > NM - (last ? PRE : 0) ? NRD - (NM - (last ? PRE : 0)) : 0)>([&](auto rc) __attribute__((always_inline)) {
-        constexpr int r = NM - (last ? PRE : 0) + decltype(rc)::value;
-        read(std::integral_constant<int, r>{});
-      });
-      if constexpr (ks == 0) {
-        static_for<(NL > NM ? NL - NM : 0)>([&](auto ic) __attribute__((always_inline)) { dma(NM + decltype(ic)::value); });
-      }
-      __builtin_amdgcn_sched_barrier(0);
-    });
-  }
-
-  OHIP_STAMP(2);
   const int ibase = p0 + wp * Tl::TP * 32 + (lane >> 5) * 4;
   const int jbase = q0 + wq * Tl::TQ * 32 + (lane & 31);
   OutAddr out = epi.addr();
@@ -685,6 +563,138 @@ mfma_gemm_kernel(const LX lx, const LY ly, const Epi epi, int nP, int nQ, int kc
   if constexpr (kWide) {
     if (smode == 2) flush(std::integral_constant<int, 4>{});
   }
+}
+
+template <Op O, class Tl, class LX, class LY, class Epi, bool XX, bool XY>
+__global__ void __launch_bounds__(Tl::kThreads)
+mfma_gemm_kernel(const LX lx, const LY ly, const Epi epi, int nP, int nQ, int kc, int splits, int gp) {
+  OHIP_STAMP(0);
+  using A = typename OpT<O>::Acc;
+  // the stage buffers, then (after the K loop) the block's per-row epilogue terms
+  constexpr int kRowTerms = (int)((Tl::BP / 4 * sizeof(typename Epi::PreI) + 15) / 16);
+  __shared__ u32x4 smem[Tl::STAGES * Tl::kStage + kRowTerms];
+  const int t = threadIdx.x;
+  const int lane = t & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+  const int wp = wave % Tl::WP, wq = wave / Tl::WP;
+  int tp, tq;
+  map_tile(blockIdx.x, gridDim.x, nP, nQ, gp, tp, tq);
+  const int p0 = tp * Tl::BP, q0 = tq * Tl::BQ;
+
+  typename LX::template State<Tl::NX> sx;
+  typename LY::template State<Tl::NY> sy;
+  lx.template init<Tl::NX, Tl::kWaves, Tl::CH>(sx, p0, lane, wave);
+  ly.template init<Tl::NY, Tl::kWaves, Tl::CH>(sy, q0, lane, wave);
+
+  A acc[Tl::TP][Tl::TQ];
+#pragma unroll
+  for (int a = 0; a < Tl::TP; ++a)
+#pragma unroll
+    for (int b = 0; b < Tl::TQ; ++b)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[a][b][e] = 0;
+
+  // K stages of this block: all of them, or slice blockIdx.y of `splits`
+  const int nk_all = (kc + Tl::CH - 1) / Tl::CH;
+  const int per = (nk_all + splits - 1) / splits;
+  const int kbeg = (int)blockIdx.y * per;
+  const int kend = min(kbeg + per, nk_all);
+  constexpr int NL = Tl::NX + Tl::NY;     // DMA loads per thread per stage
+  // Every stage issues all its loads (past the last stage they read zero or
+  // the pad source), so the waits below are fixed counts of outstanding loads.
+  auto issue = [&](int kt) {
+    u32x4* s = smem + (kt % Tl::STAGES) * Tl::kStage;
+    lx.template issue<Tl::NX, Tl::kWaves, Tl::CH>(sx, kt, wave, s);
+    ly.template issue<Tl::NY, Tl::kWaves, Tl::CH>(sy, kt, wave, s + Tl::BP * Tl::kRowStride);
+  };
+
+  // Fragment slots of this lane: rows are tile bases (multiples of 32) plus
+  // lane % 32, chunk 2 * ks + lane / 32.
+  const int xr = wp * Tl::TP * 32 + (lane & 31);
+  const int yr = Tl::BP + wq * Tl::TQ * 32 + (lane & 31);
+  int xslot[Tl::KS], yslot[Tl::KS];
+#pragma unroll
+  for (int ks = 0; ks < Tl::KS; ++ks) {
+    xslot[ks] = xr * Tl::kRowStride + lds_slot<Tl::CH>(xr, 2 * ks + (lane >> 5));
+    yslot[ks] = yr * Tl::kRowStride + lds_slot<Tl::CH>(yr, 2 * ks + (lane >> 5));
+  }
+
+#pragma unroll
+  for (int s = 0; s < Tl::STAGES - 1; ++s) issue(kbeg + s);
+  wait_vmcnt<(Tl::STAGES - 2) * NL>();
+  barrier_only();
+  OHIP_STAMP(1);
+
+  u32x4 fx[2][Tl::TP], fy[2][Tl::TQ];
+  {
+    const u32x4* s0 = smem + (kbeg % Tl::STAGES) * Tl::kStage;
+#pragma unroll
+    for (int a = 0; a < Tl::TP; ++a) fx[0][a] = s0[xslot[0] + a * 32 * Tl::kRowStride];
+#pragma unroll
+    for (int b = 0; b < Tl::TQ; ++b) fy[0][b] = s0[yslot[0] + b * 32 * Tl::kRowStride];
+  }
+
+  // One k-step in program order, fenced so the compiler keeps it: each MFMA
+  // is followed by at most one fragment read for the next k-step (in the
+  // order the next k-step consumes them, so the waits before its MFMAs are
+  // partial) and, on k-step 0, by one DMA load of the stage STAGES - 1 ahead.
+  // The last k-step reads the next stage: its first MFMAs go before the
+  // stage barrier, which then overlaps them.
+  constexpr int NM = Tl::TP * Tl::TQ;      // MFMAs per k-step
+  constexpr int NRD = Tl::TP + Tl::TQ;     // fragment reads per k-step
+  constexpr int PRE = NM >= 4 ? 2 : 0;     // MFMAs of the last k-step ahead of the barrier
+  for (int kt = kbeg; kt < kend; ++kt) {
+    const u32x4* s = smem + (kt % Tl::STAGES) * Tl::kStage;
+    const u32x4* sn = smem + ((kt + 1) % Tl::STAGES) * Tl::kStage;
+    u32x4* sd = smem + ((kt + Tl::STAGES - 1) % Tl::STAGES) * Tl::kStage;
+    const typename LX::Step stx = lx.template step<Tl::NX, Tl::kWaves, Tl::CH>(sx, kt + Tl::STAGES - 1);
+    const typename LY::Step sty = ly.template step<Tl::NY, Tl::kWaves, Tl::CH>(sy, kt + Tl::STAGES - 1);
+    auto dma = [&](int i) __attribute__((always_inline)) {
+      if (i < Tl::NX) lx.template load<Tl::NX, Tl::kWaves, Tl::CH>(sx, stx, i, wave, sd);
+      else ly.template load<Tl::NY, Tl::kWaves, Tl::CH>(sy, sty, i - Tl::NX, wave, sd + Tl::BP * Tl::kRowStride);
+    };
+    static_for<Tl::KS>([&](auto ksc) __attribute__((always_inline)) {
+      constexpr int ks = decltype(ksc)::value;
+      constexpr bool last = ks == Tl::KS - 1;
+      constexpr int cur = ks & 1, nxt = cur ^ 1;
+      const u32x4* src = last ? sn : s;
+      const int kr = last ? 0 : ks + 1;
+      // read r of the next k-step: fx[0], fy[0 .. TQ-1], fx[1 .. TP-1]
+      auto read = [&](auto rc) __attribute__((always_inline)) {
+        constexpr int r = decltype(rc)::value;
+        if constexpr (r == 0) fx[nxt][0] = src[xslot[kr]];
+        else if constexpr (r <= Tl::TQ) fy[nxt][r - 1] = src[yslot[kr] + (r - 1) * 32 * Tl::kRowStride];
+        else fx[nxt][r - Tl::TQ] = src[xslot[kr] + (r - Tl::TQ) * 32 * Tl::kRowStride];
+      };
+      static_for<NM>([&](auto mc) __attribute__((always_inline)) {
+        constexpr int m = decltype(mc)::value;
+        constexpr int a = m / Tl::TQ, b = m % Tl::TQ;
+        if constexpr (last && m == PRE) {
+          wait_vmcnt<(Tl::STAGES - 2) * NL>();
+          wait_lgkm0();
+          barrier_only();
+        }
+        acc[a][b] = OpT<O>::mma(frag<XX>(fx[cur][a]), frag<XY>(fy[cur][b]), acc[a][b]);
+        __builtin_amdgcn_sched_barrier(0);
+        constexpr int r = last ? m - PRE : m;
+        if constexpr (r >= 0 && r < NRD) read(std::integral_constant<int, r>{});
+        if constexpr (ks == 0 && m < NL) dma(m);
+        __builtin_amdgcn_sched_barrier(0);
+      });
+      // the reads and loads that outnumber the MFMAs (small tiles)
+      static_for<(NRD > NM - (last ? PRE : 0) ? NRD - (NM - (last ? PRE : 0)) : 0)>([&](auto rc) __attribute__((always_inline)) {
+        constexpr int r = NM - (last ? PRE : 0) + decltype(rc)::value;
+        read(std::integral_constant<int, r>{});
+      });
+      if constexpr (ks == 0) {
+        static_for<(NL > NM ? NL - NM : 0)>([&](auto ic) __attribute__((always_inline)) { dma(NM + decltype(ic)::value); });
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    });
+  }
+
+  OHIP_STAMP(2);
+  tile_epilogue<O, Tl>(epi, acc, smem, p0, q0, wp, wq, lane, t);
   OHIP_STAMP(3);
 }
 
@@ -735,17 +745,18 @@ __global__ void __launch_bounds__(256) split_reduce_kernel(const T* __restrict__
     epi.load_i(pi, i0);
     epi.load_j(pj, j);
     const T* src = ws + (int64_t)j * Pp + i0;
-    A acc = *reinterpret_cast<const A*>(src);
+    auto ld = [&](const T* p) __attribute__((always_inline)) { return *reinterpret_cast<const A*>(p); };
+    A acc = ld(src);
     int s = 1;
     // four slices' loads in flight before their adds; the adds stay in slice order
     for (; s + 4 <= splits; s += 4) {
-      const A v0 = *reinterpret_cast<const A*>(src + s * slice);
-      const A v1 = *reinterpret_cast<const A*>(src + (s + 1) * slice);
-      const A v2 = *reinterpret_cast<const A*>(src + (s + 2) * slice);
-      const A v3 = *reinterpret_cast<const A*>(src + (s + 3) * slice);
+      const A v0 = ld(src + s * slice);
+      const A v1 = ld(src + (s + 1) * slice);
+      const A v2 = ld(src + (s + 2) * slice);
+      const A v3 = ld(src + (s + 3) * slice);
       acc += v0; acc += v1; acc += v2; acc += v3;
     }
-    for (; s < splits; ++s) acc += *reinterpret_cast<const A*>(src + s * slice);
+    for (; s < splits; ++s) acc += ld(src + s * slice);
     uint32_t bits[4];
     epi.finish(pi, pj, i0, j, acc, bits);
     store_group(out, epi.out_bytes(), out.row(i0), i0, j, bits);

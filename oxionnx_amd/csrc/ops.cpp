@@ -348,7 +348,7 @@ extern "C" int ohip_sync(ohip_ctx* ctx) {
 
 extern "C" int ohip_set_tile_override(ohip_ctx* ctx, int tile_id) {
   if (!ctx) return fail(OHIP_E_INVALID, "null context");
-  if (tile_id < 0 || tile_id > 14) return fail(OHIP_E_INVALID, "tile id must be 0..14");
+  if (tile_id < 0 || tile_id > 15) return fail(OHIP_E_INVALID, "tile id must be 0..15");
   ctx->tile_override = tile_id;
   return OHIP_OK;
 }
@@ -1253,6 +1253,51 @@ static bool ph_one_launch() {
   return v;
 }
 
+// OHIP_HALO=0 keeps 3x3 convolutions on the engine's im2col path;
+// OHIP_HALO_SPLITS=n forces the halo path's split count (measurement switches)
+static bool halo_allowed() {
+  static const bool v = [] {
+    const char* e = std::getenv("OHIP_HALO");
+    return !(e && e[0] == '0');
+  }();
+  return v;
+}
+
+// Split-K slices for the halo-patch kernel, or 0 where it does not apply:
+// one group, 3x3, stride and dilation 1, an output width of 16, 32 or 64
+// (256-pixel tiles of whole rows whose padded patch fits the stage) and an
+// output height those tiles divide; automatically only for f16 / bf16 from
+// 3 GFLOP up (below that the engine's shorter launches win), always under
+// tile override 15.  Slices are added until the grid gives every CU a
+// block, keeping at least eight channel slabs per slice: every slice's
+// partial sums make a round trip through memory (written at the end of the
+// contraction, read by the reduction), which costs more than the extra
+// slices' parallelism returns below that.
+static int halo_plan(ohip_ctx* ctx, const ohip_conv_desc* d, int64_t G, int64_t w_in, const ConvGeo& g, int cpc,
+                     int64_t img_bytes) {
+  const bool forced = ctx->tile_override == 15;
+  if (!halo_allowed() || (ctx->tile_override != 0 && !forced) || G != 1) return 0;
+  if (d->kh != 3 || d->kw != 3 || d->stride_h != 1 || d->stride_w != 1 || d->dil_h != 1 || d->dil_w != 1) return 0;
+  if (g.ow != 16 && g.ow != 32 && g.ow != 64) return 0;
+  const int64_t th = kHaloBPix / g.ow;
+  if (g.oh % th != 0 || (th + 2) * (g.ow + 2) > kHaloPixMax || w_in > 65535) return 0;
+  if (img_bytes >= ((int64_t)1 << 31) - 65536) return 0;
+  const int64_t rows = d->n * g.oh * g.ow;
+  const double flops = 2.0 * (double)rows * (double)d->cout * (double)d->c * 9.0;
+  if (!forced && (d->dtype == OHIP_F32 || flops < 3e9)) return 0;
+  const int64_t nb = ((rows + kHaloBPix - 1) / kHaloBPix) * ((d->cout + 63) / 64);
+  const int nslab = (cpc + 1) / 2;
+  static const int forced_splits = [] {
+    const char* e = std::getenv("OHIP_HALO_SPLITS");
+    return e ? std::atoi(e) : 0;
+  }();
+  if (forced_splits >= 1 && forced_splits <= 64) return std::min(forced_splits, nslab);
+  int64_t s = nb >= 256 ? 1 : (256 + nb - 1) / nb;
+  s = std::min<int64_t>(s, std::max(1, nslab / 8));
+  s = std::min<int64_t>(s, 16);
+  return (int)std::max<int64_t>(s, 1);
+}
+
 static int conv2d_impl(ohip_ctx* ctx, const ohip_conv_desc* d, const void* x, const ohip_weight* w, const void* bias,
                        void* y, bool noalloc) {
   int rc = activate(ctx);
@@ -1349,8 +1394,13 @@ static int conv2d_impl(ohip_ctx* ctx, const ohip_conv_desc* d, const void* x, co
   size_t ix = stage ? plan.add((size_t)(d->n * sh_ * sw_ * cpt) * eb) : SIZE_MAX;
   const bool nchw_out = d->out_layout == OHIP_NCHW;
   const int sP = nchw_out ? (int)rows : (int)coutg, sQ = nchw_out ? (int)coutg : (int)rows;
-  const SplitChoice sc =
-      plan_split_tile(sP, sQ, (int)(d->kh * d->kw * (cp / ce)), ctx->tile_override, d->dtype == OHIP_F32);
+  // 3x3 stride-1 convolutions whose output rows tile 256-pixel blocks run
+  // the halo-patch kernel (the input patch staged once per channel slab for
+  // all nine taps) instead of the engine's im2col gather.
+  const int hsplits = halo_plan(ctx, d, G, sw_, g, (int)(cp / ce), (int64_t)(sh_ * sw_ * cpt * eb));
+  const SplitChoice sc = hsplits ? SplitChoice{hsplits, 0}
+                                 : plan_split_tile(sP, sQ, (int)(d->kh * d->kw * (cp / ce)), ctx->tile_override,
+                                                   d->dtype == OHIP_F32);
   const int splits = sc.splits;
   size_t iw = splits > 1 ? plan.add(split_ws_bytes(sP, sQ, splits)) : SIZE_MAX;
   char* sbase = nullptr;
@@ -1375,6 +1425,38 @@ static int conv2d_impl(ohip_ctx* ctx, const ohip_conv_desc* d, const void* x, co
     xin = px;
   } else if (!aligned(x, 16)) {
     return fail(OHIP_E_INVALID, "ohip_conv2d: NHWC input must be 16-byte aligned");
+  }
+
+  if (hsplits) {
+    HaloGeo hg{};
+    hg.x = static_cast<const char*>(xin);
+    hg.img_bytes = sh_ * sw_ * cpt * eb;
+    hg.H = (int)sh_; hg.W = (int)sw_; hg.OH = (int)g.oh; hg.OW = (int)g.ow;
+    hg.pt = fused_pad ? 0 : (int)d->pad_t; hg.pl = fused_pad ? 0 : (int)d->pad_l;
+    hg.pstride = (int)(cpt / ce); hg.cpc = (int)(cp / ce);
+    hg.th = kHaloBPix / (int)g.ow;
+    hg.ow_shift = 0;
+    while ((1 << hg.ow_shift) < g.ow) ++hg.ow_shift;
+    hg.w = static_cast<const char*>(w->data); hg.ldw = w->ld_bytes; hg.cout = (int)coutg;
+    FloatOut o{};
+    o.alpha = 1.0f; o.beta = 1.0f;
+    o.bias = bias;
+    o.act = act; o.lo = lo; o.hi = hi;
+    o.y = y;
+    if (nchw_out) {
+      o.si = 1; o.sj = ohw; o.bstride = d->cout * ohw; o.ohw = (int)ohw; o.P = (int)rows; o.Q = (int)coutg;
+      o.vec = ohw % 4 == 0 && aligned(o.y, 4 * eb);
+      o.bias_mode = BIAS_J;
+    } else {
+      o.si = 1; o.sj = ldo; o.bstride = 0; o.ohw = INT_MAX; o.P = (int)coutg; o.Q = (int)rows;
+      o.vec = ldo % 4 == 0 && aligned(o.y, 4 * eb);
+      o.bias_mode = BIAS_I;
+    }
+    o.splits = splits;
+    o.split_ws = splits > 1 ? plan_at(sbase, plan, iw) : nullptr;
+    hipError_t e = run_halo_float(d->dtype, hg, nchw_out, o, ctx->stream);
+    if (e != hipSuccess) return hip_fail(e, "ohip_conv2d halo launch");
+    return OHIP_OK;
   }
 
   // Groups without split-K run as one launch, group = blockIdx.z: the input

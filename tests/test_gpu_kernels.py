@@ -383,6 +383,59 @@ def test_conv_nhwc_output_matches_nchw(torch, ctx):
     np.testing.assert_array_equal(y1.cpu().numpy(), y2[..., :20].permute(0, 3, 1, 2).cpu().numpy())
 
 
+# Halo-patch path (3x3, stride 1, 256-pixel tiles of whole output rows):
+# (x shape, cout, pads).  A channel tail inside the last slab, partial
+# output-channel tiles, two images, an uneven top pad, a valid (unpadded)
+# conv, 64-wide rows, and the 512-channel residual conv (split-K).
+HALO_CASES = [
+    ((2, 24, 16, 16), 40, (1, 1, 1, 1)),
+    ((1, 8, 15, 16), 24, (2, 1, 1, 1)),
+    ((1, 16, 34, 34), 64, (0, 0, 0, 0)),
+    ((1, 128, 16, 64), 96, (1, 1, 1, 1)),
+    ((1, 512, 32, 32), 512, (1, 1, 1, 1)),
+]
+
+
+@pytest.mark.parametrize("case", HALO_CASES, ids=lambda c: f"{c[0]}x{c[1]}p{c[2]}")
+@pytest.mark.parametrize("dt", ["f32", "f16", "bf16"])
+@pytest.mark.parametrize("nhwc_out", [False, True], ids=["nchw", "nhwc"])
+def test_halo_conv_matches_oracle(torch, ctx, case, dt, nhwc_out):
+    from oxionnx_amd import _lib as L
+    xs, cout, p = case
+    rng = np.random.default_rng(11 + sum(xs) + cout)
+    x = rng.uniform(-1, 1, xs).astype(np.float32)
+    w = rng.normal(0, 0.05, (cout, xs[1], 3, 3)).astype(np.float32)
+    b = rng.normal(0, 0.01, cout).astype(np.float32)
+    lay = L.NHWC if nhwc_out else L.NCHW
+
+    def run(xd, wt, bd):
+        ctx.set_tile(15)   # the halo-patch kernel wherever the geometry allows
+        try:
+            y = ctx.conv2d(xd, wt, bd, pads=p, act=L.ACT_RELU, out_layout=lay)
+        finally:
+            ctx.set_tile(0)
+        if nhwc_out:
+            y = y[..., :cout].permute(0, 3, 1, 2)
+        return y
+
+    if dt == "f32":
+        y = run(_dev(torch, x), ctx.weight_conv(w), _dev(torch, b)).cpu().numpy()
+        want = O.conv(x, w, b, activation="relu", pads=p)
+        scale = np.max(np.abs(O.conv(x, w, b, pads=p)))
+        assert np.max(np.abs(y.astype(np.float64) - want)) <= F32_TOL * scale
+        return
+    bf16 = dt == "bf16"
+    xh, wh, bh = (O.f32_to_half_bits(v, bf16) for v in (x, w, b))
+    tdt = torch.bfloat16 if bf16 else torch.float16
+    wt = ctx.weight_conv(O.half_bits_to_f32(wh, bf16), dtype=L.BF16 if bf16 else L.F16)
+    xt = torch.from_numpy(xh.view(np.int16)).cuda().view(tdt)
+    bt = torch.from_numpy(bh.view(np.int16)).cuda().view(tdt)
+    y = run(xt, wt, bt).contiguous()
+    got = O.half_bits_to_f32(y.view(torch.int16).cpu().numpy().view(np.uint16), bf16)
+    want = O.half_bits_to_f32(O.conv_half(xh, wh, bh, bf16=bf16, activation="relu", pads=p), bf16)
+    assert _rel_err(got, want) <= HALF_TOL
+
+
 # ------------------------------------------------------------------ integer GEMM
 @pytest.mark.parametrize("mkn", [(1, 16, 16), (4, 768, 96), (37, 100, 53), (128, 768, 3072), (300, 256, 200)],
                          ids=str)
