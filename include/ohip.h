@@ -407,8 +407,10 @@ const char* ohip_last_decline(ohip_ctx* ctx);
 /* CacheCounters (oxionnx-cuda/src/residency.rs:141-238) plus dispatch counts,
  * device allocations (hipMalloc calls for the context's weights, pool,
  * scratch and constants; a steady-state forward makes none), host fences
- * (stream synchronisations for a read-back or ohip_sync) and, as a gauge not
- * reset by ohip_reset_counters, the pool buffers currently handed out. */
+ * (stream synchronisations for a read-back or ohip_sync), as a gauge not
+ * reset by ohip_reset_counters, the pool buffers currently handed out, and
+ * the contraction launches issued (one per MFMA-engine, halo, GEMV or
+ * integer contraction launch; a split-K reduction belongs to its launch). */
 typedef struct {
     uint64_t weight_hits, weight_misses, weight_transient;
     uint64_t weight_uploaded_bytes, weight_resident_bytes;
@@ -417,6 +419,7 @@ typedef struct {
     uint64_t device_allocs;
     uint64_t stream_syncs;
     uint64_t pool_live;
+    uint64_t contraction_launches;
 } ohip_counters;
 int ohip_get_counters(ohip_ctx* ctx, ohip_counters* out);
 int ohip_reset_counters(ohip_ctx* ctx);

@@ -119,7 +119,7 @@ class Counters(ctypes.Structure):
     _fields_ = [(f, ctypes.c_uint64) for f in (
         "weight_hits", "weight_misses", "weight_transient", "weight_uploaded_bytes", "weight_resident_bytes",
         "h2d_bytes", "d2h_bytes", "dispatches", "declined", "device_allocs", "stream_syncs",
-        "pool_live")]
+        "pool_live", "contraction_launches")]
 
 
 # name -> (restype, argtypes); the list is the C ABI of include/ohip.h.

@@ -388,6 +388,7 @@ struct ConcatPlan {
   void* dst;
 };
 hipError_t run_concat_rows(ConcatPlan p, int64_t row, int64_t rows, hipStream_t st);
+hipError_t run_zero_fill(void* p, size_t bytes, hipStream_t st);
 hipError_t run_copy2d(const void* src, int64_t src_pitch, void* dst, int64_t dst_pitch, int64_t width, int64_t rows,
                       hipStream_t st);
 

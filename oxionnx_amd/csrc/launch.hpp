@@ -436,6 +436,15 @@ inline hipError_t launch_any(const LX& lx, const LY& ly, const Epi& epi, int P, 
   }
 }
 
+// Per-slice pads (Im2colNHWC::zpt / zpl) hold four entries, indexed by the
+// batch slice: a launch that uses them must have at most four slices and no
+// more slices than entries.
+inline bool zpads_fit(const Im2colOperand& col, const OutMap& o) {
+  if (col.zpads <= 0) return true;
+  const int batch = o.batch > 1 ? o.batch : 1;
+  return col.zpads <= 4 && batch <= col.zpads;
+}
+
 // OHIP_STAGE=0 turns the LDS-staged epilogue off (a measurement switch)
 inline int stage_allowed() {
   static const int v = [] {

@@ -596,6 +596,25 @@ hipError_t run_copy2d(const void* src, int64_t src_pitch, void* dst, int64_t dst
   return hipGetLastError();
 }
 
+// Zero fill (a kernel, not hipMemsetAsync, so it is safe inside a captured
+// graph): 16-byte stores where the buffer allows, else bytes.
+template <class T>
+__global__ void __launch_bounds__(kThreads) zero_fill_kernel(T* __restrict__ p, int64_t n) {
+  for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n; i += (int64_t)gridDim.x * kThreads) p[i] = T{};
+}
+
+hipError_t run_zero_fill(void* p, size_t bytes, hipStream_t st) {
+  if (bytes == 0) return hipSuccess;
+  if ((uintptr_t)p % 16 == 0 && bytes % 16 == 0) {
+    const int64_t n = (int64_t)(bytes / 16);
+    hipLaunchKernelGGL(zero_fill_kernel<uint4>, dim3(grid_for(n)), dim3(kThreads), 0, st, (uint4*)p, n);
+  } else {
+    hipLaunchKernelGGL(zero_fill_kernel<uint8_t>, dim3(grid_for((int64_t)bytes)), dim3(kThreads), 0, st,
+                       (uint8_t*)p, (int64_t)bytes);
+  }
+  return hipGetLastError();
+}
+
 // widths and offsets in bytes on entry; converted to units of the widest
 // element size that every pointer and width allows
 hipError_t run_concat_rows(ConcatPlan p, int64_t row, int64_t rows, hipStream_t st) {

@@ -1207,6 +1207,7 @@ extern "C" int ohip_gemm(ohip_ctx* ctx, const ohip_gemm_desc* d, const void* a, 
   hipError_t e;
   if (gemv) {
     GemvArgs g{av.p, av.ld_bytes / eb, b->data, b->ld_bytes / eb, (int)M, (int)N, b->kc};
+    ctx->counters.contraction_launches++;
     e = run_gemv(d->dtype, g, o, ctx->stream);
   } else {
     DenseOperand x{b->data, b->ld_bytes, (int)N, b->kc, 0, 0u, pad16(ctx, 0)};
@@ -1215,6 +1216,7 @@ extern "C" int ohip_gemm(ohip_ctx* ctx, const ohip_gemm_desc* d, const void* a, 
     DENSE_FITS_OR_DECLINE(yv, "ohip_gemm");
     o.splits = splits;
     o.split_ws = splits > 1 ? scratch_at(ctx, plan, iw) : nullptr;
+    ctx->counters.contraction_launches++;
     e = run_dense_float(d->dtype, x, yv, o, sc.tile, ctx->stream);
   }
   if (e != hipSuccess) return hip_fail(e, "ohip_gemm launch");
@@ -1454,6 +1456,7 @@ static int conv2d_impl(ohip_ctx* ctx, const ohip_conv_desc* d, const void* x, co
     }
     o.splits = splits;
     o.split_ws = splits > 1 ? plan_at(sbase, plan, iw) : nullptr;
+    ctx->counters.contraction_launches++;
     hipError_t e = run_halo_float(d->dtype, hg, nchw_out, o, ctx->stream);
     if (e != hipSuccess) return hip_fail(e, "ohip_conv2d halo launch");
     return OHIP_OK;
@@ -1505,6 +1508,7 @@ static int conv2d_impl(ohip_ctx* ctx, const ohip_conv_desc* d, const void* x, co
       // vector stores need every group's first output aligned, not only group 0's
       o.vec = o.vec && o.zstride % (4 * eb) == 0;
     }
+    ctx->counters.contraction_launches++;
     hipError_t e = run_conv_float(d->dtype, col, wt, col_on_x, o, sc.tile, ctx->stream);
     if (e != hipSuccess) return hip_fail(e, "ohip_conv2d launch");
   }
@@ -1565,6 +1569,7 @@ extern "C" int ohip_matmul(ohip_ctx* ctx, const ohip_matmul_desc* d, const void*
   o.splits = 1; o.split_ws = nullptr; o.batch = (int)d->batch; o.zstride = M * N * eb;
   DENSE_FITS_OR_DECLINE(xo, "ohip_matmul");
   DENSE_FITS_OR_DECLINE(yo, "ohip_matmul");
+  ctx->counters.contraction_launches++;
   hipError_t e = run_dense_float(d->dtype, xo, yo, o, plain_tile_id(ctx->tile_override)
                                                           ? ctx->tile_override : 0, ctx->stream);
   if (e != hipSuccess) return hip_fail(e, "ohip_matmul launch");
@@ -1601,9 +1606,22 @@ extern "C" int ohip_conv_transpose2d(ohip_ctx* ctx, const ohip_convt_desc* d, co
     for (int64_t ry = 0; ry < sh; ++ry)
       for (int64_t rx = 0; rx < sw; ++rx)
         max_rows = std::max<int64_t>(max_rows, ((oh - ry + sh - 1) / sh) * ((ow - rx + sw - 1) / sw));
+    // Every phase in one launch, phase z = ry * sw + rx on the grid's z, when
+    // the phases share one filter allocation and one output grid and none
+    // runs split-K: the phase's pads, filter and output offset follow z.  A
+    // combined grid of 256+ blocks fills the chip without splitting; a
+    // forced split (tile 10 / 11, OHIP_SPLITS) keeps the per-phase launches.
+    const int64_t ohp0 = oh / sh, owp0 = ow / sw;
+    const int64_t blocks64 = ((ohp0 * owp0 + 63) / 64) * ((d->cout + 63) / 64) * sh * sw;
+    const bool split_forced = ctx->tile_override == 10 || ctx->tile_override == 11 || forced_splits() != 0;
+    const bool one = w->ph_all && oh % sh == 0 && ow % sw == 0 && ohp0 > 0 && owp0 > 0 && ph_one_launch() &&
+                     !split_forced &&
+                     (blocks64 >= 256 ||
+                      plan_splits((int)(ohp0 * owp0), (int)d->cout, w->ph_all->kc, ctx->tile_override) == 1);
     int max_splits = 1;
-    for (auto* ph : w->phases)
-      max_splits = std::max(max_splits, plan_splits((int)max_rows, (int)d->cout, ph->kc, ctx->tile_override));
+    if (!one)
+      for (auto* ph : w->phases)
+        max_splits = std::max(max_splits, plan_splits((int)max_rows, (int)d->cout, ph->kc, ctx->tile_override));
     ScratchPlan plan;
     size_t ix = plan.add((size_t)(d->n * d->h * d->w * cp) * eb);
     size_t iw = max_splits > 1 ? plan.add(split_ws_bytes((int)max_rows, (int)d->cout, max_splits)) : SIZE_MAX;
@@ -1612,14 +1630,7 @@ extern "C" int ohip_conv_transpose2d(ohip_ctx* ctx, const ohip_convt_desc* d, co
     void* px = scratch_at(ctx, plan, ix);
     HIP_TRY(run_nchw_to_nhwc(eb, x, px, (int)d->n, (int)d->c, (int)(d->h * d->w), (int)cp, ctx->stream),
             "NCHW -> NHWC");
-    // Every phase in one launch, phase z = ry * sw + rx on the grid's z, when
-    // the phases share one filter allocation and one output grid and none
-    // needs split-K: the phase's pads, filter and output offset follow z.
-    const int64_t ohp0 = oh / sh, owp0 = ow / sw;
-    const int64_t blocks64 = ((ohp0 * owp0 + 63) / 64) * ((d->cout + 63) / 64) * sh * sw;
-    if (w->ph_all && oh % sh == 0 && ow % sw == 0 && ohp0 > 0 && owp0 > 0 && ph_one_launch() &&
-        (blocks64 >= 256 ||
-         plan_splits((int)(ohp0 * owp0), (int)d->cout, w->ph_all->kc, ctx->tile_override) == 1)) {
+    if (one) {
       const ohip_weight* pa = w->ph_all;
       for (int64_t n = 0; n < d->n; ++n) {
         Im2colOperand col{};
@@ -1648,6 +1659,7 @@ extern "C" int ohip_conv_transpose2d(ohip_ctx* ctx, const ohip_convt_desc* d, co
         o.splits = 1; o.split_ws = nullptr;
         o.batch = (int)(sh * sw); o.zsw = (int)sw; o.zrow = ow * eb; o.zstride = eb;   // phase (ry, rx) at ry * ow + rx
         DENSE_FITS_OR_DECLINE(wt, "ohip_conv_transpose2d");
+        ctx->counters.contraction_launches++;
         hipError_t e = run_conv_float(d->dtype, col, wt, true, o, ctx->tile_override, ctx->stream);
         if (e != hipSuccess) return hip_fail(e, "ohip_conv_transpose2d phase launch");
       }
@@ -1679,6 +1691,7 @@ extern "C" int ohip_conv_transpose2d(ohip_ctx* ctx, const ohip_convt_desc* d, co
           o.splits = splits;
           o.split_ws = splits > 1 ? scratch_at(ctx, plan, iw) : nullptr;
           DENSE_FITS_OR_DECLINE(wt, "ohip_conv_transpose2d");
+          ctx->counters.contraction_launches++;
           hipError_t e = run_conv_float(d->dtype, col, wt, true, o, ctx->tile_override, ctx->stream);
           if (e != hipSuccess) return hip_fail(e, "ohip_conv_transpose2d phase launch");
         }
@@ -1758,6 +1771,7 @@ extern "C" int ohip_qgemm(ohip_ctx* ctx, const ohip_qgemm_desc* d, const void* a
   DENSE_FITS_OR_DECLINE(yv, "ohip_qgemm");
   o.splits = splits;
   o.split_ws = splits > 1 ? scratch_at(ctx, plan, iw) : nullptr;
+  ctx->counters.contraction_launches++;
   hipError_t e = run_dense_quant(x, yv, o, ctx->tile_override, ctx->stream);
   if (e != hipSuccess) return hip_fail(e, "ohip_qgemm launch");
   return OHIP_OK;
@@ -1913,6 +1927,7 @@ extern "C" int ohip_qconv2d(ohip_ctx* ctx, const ohip_qconv_desc* d, const void*
     DENSE_FITS_OR_DECLINE(wt, "ohip_qconv2d");
     o.splits = splits;
     o.split_ws = splits > 1 ? scratch_at(ctx, plan, iw) : nullptr;
+    ctx->counters.contraction_launches++;
     hipError_t e = run_conv_quant(col, wt, col_on_x, o, ctx->tile_override, ctx->stream);
     if (e != hipSuccess) return hip_fail(e, "ohip_qconv2d launch");
   }
@@ -1947,9 +1962,9 @@ extern "C" int ohip_dtensor_alloc(ohip_ctx* ctx, int dtype, int rank, const int6
   rc = pool_alloc(ctx, bytes ? bytes : 16, &t->ptr);
   if (rc) { delete t; return rc; }
   t->buf = std::shared_ptr<DevBuf>(new DevBuf{ctx, t->ptr});
-  if (layout == OHIP_NHWC) {  // channel padding must read as zero
-    hipError_t e = hipMemsetAsync(t->ptr, 0, bytes, ctx->stream);
-    if (e != hipSuccess) { delete t; return hip_fail(e, "dtensor memset"); }
+  if (layout == OHIP_NHWC) {  // channel padding must read as zero (a fill kernel: capture-safe)
+    hipError_t e = run_zero_fill(t->ptr, bytes, ctx->stream);
+    if (e != hipSuccess) { delete t; return hip_fail(e, "dtensor zero fill"); }
   }
   *out = t;
   return OHIP_OK;

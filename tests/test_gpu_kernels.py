@@ -290,6 +290,19 @@ CONVT_CASES = [
     ((1, 128, 16, 16), (128, 64, 4, 4), dict(strides=[2, 2], pads=[1, 2, 1, 2])),      # one launch, uneven pads
     ((2, 24, 5, 7), (24, 40, 3, 3), dict(strides=[1, 1], pads=[1, 0, 0, 2])),
     ((1, 32, 6, 5), (32, 16, 5, 3), dict(strides=[3, 2], pads=[2, 1, 1, 0], output_padding=[2, 1])),
+    # two phases in one launch: (2, 1) and (1, 2) strides (the z / zsw output offsets)
+    ((1, 32, 8, 8), (32, 16, 4, 3), dict(strides=[2, 1], pads=[1, 1, 1, 1])),
+    ((2, 16, 6, 8), (16, 24, 3, 4), dict(strides=[1, 2], pads=[1, 1, 1, 1])),
+]
+
+# (case, contraction launches one forward must take): one launch per image
+# when every phase fits one grid, a launch per phase and image otherwise
+# (an odd output extent: the phases' grids differ).
+CONVT_LAUNCHES = [
+    (((1, 32, 8, 8), (32, 16, 4, 3), dict(strides=[2, 1], pads=[1, 1, 1, 1])), 1),
+    (((2, 16, 6, 8), (16, 24, 3, 4), dict(strides=[1, 2], pads=[1, 1, 1, 1])), 2),
+    (((2, 32, 5, 6), (32, 24, 2, 2), dict(strides=[2, 2], pads=[0, 0, 0, 0])), 2),
+    (((1, 8, 7, 9), (8, 6, 3, 3), dict(strides=[2, 2], pads=[1, 1, 1, 1])), 4),
 ]
 
 
@@ -335,6 +348,24 @@ def test_conv_transpose_matches_oracle(torch, ctx, case, dt):
             np.testing.assert_array_equal(got, want)
         else:
             assert _rel_err(O.half_bits_to_f32(got, bf), O.half_bits_to_f32(want, bf)) <= HALF_TOL
+
+
+@pytest.mark.parametrize("case,launches", CONVT_LAUNCHES, ids=lambda c: str(c))
+def test_conv_transpose_launch_count(torch, ctx, case, launches):
+    xs, ws, attrs = case
+    rng = np.random.default_rng(7 + sum(xs))
+    x = rng.uniform(-1, 1, xs).astype(np.float32)
+    w = rng.normal(0, 0.3, ws).astype(np.float32)
+    geo = dict(strides=attrs["strides"], pads=attrs["pads"], dilations=[1, 1], group=1)
+    wt = ctx.weight_conv_transpose(w, **geo)
+    xd = _dev(torch, x)
+    ctx.conv_transpose2d(xd, wt, None, **geo)
+    ctx.sync()
+    ctx.reset_counters()
+    y = ctx.conv_transpose2d(xd, wt, None, **geo).cpu().numpy()
+    assert ctx.counters()["contraction_launches"] == launches
+    want = O.conv_transpose(x, w, None, **attrs)
+    assert np.max(np.abs(y.astype(np.float64) - want)) <= F32_TOL * max(1.0, float(np.abs(want).max()))
 
 
 @pytest.mark.parametrize("c", G.cases("Conv") + G.cases("Conv1D"), ids=lambda c: c["name"])
