@@ -195,16 +195,20 @@ struct QuantEpi {
            (out.sj % 4 == 0) && (out.bstride == 0 || out.ohw % bp == 0);
   }
 
-  // per-channel terms of a weight channel, and the correction factor of an
-  // activation row
-  struct Chan { int32_t cs, bi, fl; float cb; };
+  // Per-channel terms of a weight channel, prepared once per block: cs the
+  // column sum, k = ca * cs when the correction factor is per tensor (so an
+  // output adds it instead of multiplying), bi the int32 bias, fl the flip
+  // mask (-1: the packed channel holds -(w - w_zp)), cb the combined scale
+  // widened to f64.  Per activation row: the correction factor ca.
+  struct Chan { int32_t cs, k, bi, fl; double cb; };
   // ch must be in range (callers clamp); the loads carry no branch
   __device__ __forceinline__ Chan chan(int ch) const {
     Chan c;
     c.cs = colsum[ch];
+    c.k = (int32_t)((uint32_t)ca * (uint32_t)c.cs);
     c.bi = bias ? bias[ch] : 0;
-    c.fl = flip ? flip[ch] : 0;
-    c.cb = comb[n_comb > 1 ? ch : 0];
+    c.fl = (flip && flip[ch]) ? -1 : 0;
+    c.cb = (double)comb[n_comb > 1 ? ch : 0];
     return c;
   }
   struct PreI { Chan c[4]; int32_t ca[4]; };   // c when w_on_i, else ca
@@ -224,7 +228,8 @@ struct QuantEpi {
         cb[0] = cb[1] = cb[2] = cb[3] = c0;
       }
 #pragma unroll
-      for (int r = 0; r < 4; ++r) p.c[r] = Chan{cs[r], bi[r], (int32_t)fl[r], cb[r]};
+      for (int r = 0; r < 4; ++r)
+        p.c[r] = Chan{cs[r], (int32_t)((uint32_t)ca * (uint32_t)cs[r]), bi[r], fl[r] ? -1 : 0, (double)cb[r]};
     } else if (ca_rows) {
       load4(ca_rows, i, out.P, vec_ok, p.ca);
     } else {
@@ -237,32 +242,55 @@ struct QuantEpi {
     if (w_on_i) p.ca = ca_rows ? ca_rows[jj] : ca;
     else p.c = chan(jj);
   }
-  static __device__ __forceinline__ int32_t exact(int32_t acc, const Chan& c, int32_t ca_v) {
-    uint32_t v = (uint32_t)acc + (uint32_t)ca_v * (uint32_t)c.cs;
-    if (c.fl) v = 0u - v;
+  // the exact int32 accumulator (modulo 2^32): acc + ca * cs, negated for a
+  // flipped channel, + bias; `k` is ca * cs when ca is per tensor
+  static __device__ __forceinline__ int32_t exact(int32_t acc, const Chan& c, int32_t k) {
+    uint32_t v = (uint32_t)acc + (uint32_t)k;
+    v = (v ^ (uint32_t)c.fl) - (uint32_t)c.fl;   // fl = -1: two's complement negation
     v += (uint32_t)c.bi;
     return (int32_t)v;
   }
-  __device__ __forceinline__ int32_t requant(int32_t v, float cs) const {
+  // SatRange::requantize: f64 product with the combined scale, + zp, round
+  // half to even, clamp (d is never NaN, so max / min clamp exactly)
+  __device__ __forceinline__ int32_t requant(int32_t v, double cs) const {
 #pragma clang fp contract(off)
-    double d = (double)v * (double)cs;
+    double d = (double)v * cs;
     d = d + (double)y_zp;
     d = __builtin_rint(d);
-    d = d < (double)lo ? (double)lo : d;
-    d = d > (double)hi ? (double)hi : d;
+    d = __builtin_fmax(d, (double)lo);
+    d = __builtin_fmin(d, (double)hi);
     return (int32_t)d;
   }
   template <class A>
   __device__ __forceinline__ void finish(const PreI& pi, const PreJ& pj, int, int, A acc,
                                          uint32_t (&bits)[4]) const {
-    int32_t v[4];
-    float cb[4];
-    if (w_on_i) {
+    int32_t v[4], k[4];
+    double cb[4];
+    // a per-row correction factor multiplies per output; a per-tensor one
+    // was folded into k (a uniform branch: the common path has no multiply)
+    if (__builtin_expect(ca_rows != nullptr, 0)) {
 #pragma unroll
-      for (int r = 0; r < 4; ++r) { v[r] = exact(acc[r], pi.c[r], pj.ca); cb[r] = pi.c[r].cb; }
+      for (int r = 0; r < 4; ++r)
+        k[r] = w_on_i ? (int32_t)((uint32_t)pj.ca * (uint32_t)pi.c[r].cs)
+                      : (int32_t)((uint32_t)pi.ca[r] * (uint32_t)pj.c.cs);
     } else {
 #pragma unroll
-      for (int r = 0; r < 4; ++r) { v[r] = exact(acc[r], pj.c, pi.ca[r]); cb[r] = pj.c.cb; }
+      for (int r = 0; r < 4; ++r) k[r] = w_on_i ? pi.c[r].k : pj.c.k;
+    }
+    if (w_on_i) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int32_t a = acc[r];   // by value
+        v[r] = exact(a, pi.c[r], k[r]);
+        cb[r] = pi.c[r].cb;
+      }
+    } else {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int32_t a = acc[r];
+        v[r] = exact(a, pj.c, k[r]);
+        cb[r] = pj.c.cb;
+      }
     }
     if (out_kind == QOUT_I32) {
 #pragma unroll
@@ -393,11 +421,16 @@ inline hipError_t launch_halo(const HaloGeo& g, const Epi& epi, int P, int Q, in
 // per CU and the four-stage 64x64 tile hides the load latency of the
 // narrowest problems.  A short K loop (few 128-byte stages) is dominated by
 // the prologue and the epilogue, which the resident 128x128 blocks overlap.
-inline int pick_tile(int P, int Q, int kc, int forced) {
+inline int pick_tile(int P, int Q, int kc, int forced, bool int8 = false) {
   if (plain_tile_id(forced)) return forced;
   auto blocks = [&](int bp, int bq) { return (int64_t)((P + bp - 1) / bp) * ((Q + bq - 1) / bq); };
   const int nk = (kc + 7) / 8;
   if (nk <= 16) return blocks(128, 128) >= 256 ? 8 : 9;
+  // int8 with a long K and about one round of 128x128 tiles (config 3's
+  // second FFN GEMM, 4096x3072x768: 192 tiles): the four-stage eight-wave
+  // tile, one block per CU with deeper prefetch (21.1 against 22.1 us for
+  // the two-stage tile; at a short K, 4096x768x3072, it loses: 30.7 / 25.4)
+  if (int8 && nk >= 16 && blocks(128, 128) >= 192 && blocks(128, 128) < 320 && blocks(256, 256) < 256) return 12;
   if (blocks(256, 256) >= 256) return 6;
   if (blocks(256, 128) >= 256) return P >= Q ? 3 : 4;
   if (blocks(128, 128) >= 192) return 8;
@@ -420,7 +453,7 @@ inline hipError_t launch_any(const LX& lx, const LY& ly, const Epi& epi, int P, 
       return launch_split_on<O, XX, XY, T128w8>(lx, ly, epi, P, Q, kc, splits, split_ws, st);
     return launch_split_on<O, XX, XY, T64s4>(lx, ly, epi, P, Q, kc, splits, split_ws, st);
   }
-  switch (pick_tile(P, Q, kc, tile)) {
+  switch (pick_tile(P, Q, kc, tile, O == Op::I8)) {
     case 2: return launch_tile<O, XX, XY, T128>(lx, ly, epi, P, Q, kc, st);
     case 3: return launch_tile<O, XX, XY, T256x128>(lx, ly, epi, P, Q, kc, st);
     case 4: return launch_tile<O, XX, XY, T128x256>(lx, ly, epi, P, Q, kc, st);
