@@ -236,6 +236,26 @@ int ohip_conv2d(ohip_ctx* ctx, const ohip_conv_desc* d, const void* x, const ohi
  * so calls that overlap on one GPU (other streams or contexts) race. */
 int ohip_conv2d_noalloc(ohip_ctx* ctx, const ohip_conv_desc* d, const void* x, const ohip_weight* w,
                         const void* bias, void* y);
+
+/* Conv followed by instance normalisation, one node of this provider's graph
+ * fusion (Conv -> OxiInstanceNorm [-> Mul(gamma) -> Add(beta)] [-> Relu]).
+ * No counterpart in the reference, whose session runs the two nodes:
+ * y = InstanceNorm(conv(x)) with the conv output rounded to its dtype first,
+ * exactly as the unfused pair computes it.  When the convolution splits K,
+ * the normalisation reads the partial sums directly (no reduction launch).
+ * The conv must be ungrouped, NCHW in / out and without activation. */
+typedef struct {
+    float epsilon;
+    const void* scale;     /* gamma per channel (or per (n, c) when per_sample); may be null */
+    const void* bias;      /* beta, same indexing; may be null */
+    int per_sample;        /* scale / bias element n * stride + c */
+    int64_t stride;
+    int same_type;         /* scale / bias in the tensor's dtype (else f32) */
+    int act;               /* OHIP_ACT_NONE, OHIP_ACT_RELU or OHIP_ACT_LEAKY_RELU */
+    float alpha;           /* leaky slope */
+} ohip_norm_desc;
+int ohip_conv2d_instnorm(ohip_ctx* ctx, const ohip_conv_desc* d, const void* x, const ohip_weight* w,
+                         const void* bias, const ohip_norm_desc* norm, void* y);
 /* Output extent per conv_out_dim (conv/spatial.rs:272-330); -1 if invalid. */
 int64_t ohip_conv_out_dim(int64_t in, int64_t pad_begin, int64_t pad_end, int64_t k, int64_t dil,
                           int64_t stride);

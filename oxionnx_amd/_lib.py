@@ -65,6 +65,12 @@ class ConvDesc(ctypes.Structure):
                 ("pad_mode", ctypes.c_int)]
 
 
+class NormDesc(ctypes.Structure):
+    _fields_ = [("epsilon", ctypes.c_float), ("scale", ctypes.c_void_p), ("bias", ctypes.c_void_p),
+                ("per_sample", ctypes.c_int), ("stride", I64), ("same_type", ctypes.c_int), ("act", ctypes.c_int),
+                ("alpha", ctypes.c_float)]
+
+
 class ConvTDesc(ctypes.Structure):
     _fields_ = [(f, I64) for f in ("n", "c", "h", "w", "cout", "kh", "kw", "group", "stride_h", "stride_w",
                                     "dil_h", "dil_w", "pad_t", "pad_l", "pad_b", "pad_r", "out_pad_h",
@@ -163,6 +169,7 @@ SIGNATURES = {
     "ohip_gemm": (ctypes.c_int, [VP, ctypes.POINTER(GemmDesc), VP, VP, VP, VP]),
     "ohip_conv2d": (ctypes.c_int, [VP, ctypes.POINTER(ConvDesc), VP, VP, VP, VP]),
     "ohip_conv2d_noalloc": (ctypes.c_int, [VP, ctypes.POINTER(ConvDesc), VP, VP, VP, VP]),
+    "ohip_conv2d_instnorm": (ctypes.c_int, [VP, ctypes.POINTER(ConvDesc), VP, VP, VP, ctypes.POINTER(NormDesc), VP]),
     "ohip_matmul": (ctypes.c_int, [VP, ctypes.POINTER(MatMulDesc), VP, VP, VP]),
     "ohip_conv_out_dim": (I64, [I64, I64, I64, I64, I64, I64]),
     "ohip_weight_conv_transpose": (ctypes.c_int, [VP, ctypes.POINTER(WeightKey), ctypes.c_int, VP, I64, I64, I64,

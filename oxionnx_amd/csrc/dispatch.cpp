@@ -379,7 +379,12 @@ void fused_act(const ohip_node* nd, int* act, float* lo, float* hi) {
 std::string wkey_name(const ohip_tensor* t) { return t->name ? std::string(t->name) : std::string(); }
 
 // ------------------------------------------------------------------ float Conv
-int do_conv(ohip_ctx* ctx, const ohip_node* nd, int placement, ohip_output* out) {
+// with_norm: this provider's fused Conv -> OxiInstanceNorm node
+// (OhipConvInstanceNorm): inputs 0-2 are the Conv's, inputs 3 / 4 the
+// optional AdaIN modulation rows (resident [N, S], as the fused
+// OxiInstanceNorm takes them), attributes the Conv's plus "epsilon",
+// "scale_offset", "bias_offset" and "norm_activation" ("relu" or empty).
+int do_conv(ohip_ctx* ctx, const ohip_node* nd, int placement, ohip_output* out, bool with_norm = false) {
   const ohip_tensor *x = input(nd, 0), *w = input(nd, 1), *b = input(nd, 2);
   if (!x || !w) return decline("Conv: missing input");
   if (!host_only(w) || (b && !host_only(b))) return decline("Conv: filter / bias must be host tensors");
@@ -391,7 +396,8 @@ int do_conv(ohip_ctx* ctx, const ohip_node* nd, int placement, ohip_output* out)
   const int64_t cg = g.c / g.group;
   ohip_tuning tun;
   ohip_get_tuning(ctx, &tun);
-  if (!any_resident(nd) && !ohip_conv_admits(&tun, g.cout, cg * g.kh * g.kw, g.n * g.oh * g.ow))
+  // the fused node has no host counterpart to fall back to: it always runs here
+  if (!with_norm && !any_resident(nd) && !ohip_conv_admits(&tun, g.cout, cg * g.kh * g.kw, g.n * g.oh * g.ow))
     return decline("Conv: below conv_min_mac");
   if (x->device && ohip_dtensor_layout(x->device) != OHIP_NCHW) return decline("Conv: resident input layout");
 
@@ -435,7 +441,37 @@ int do_conv(ohip_ctx* ctx, const ohip_node* nd, int placement, ohip_output* out)
       return decline("Conv: pad_mode");
     }
   }
-  rc = ohip_conv2d(ctx, &d, xd, wt, bd, yd);
+  if (with_norm) {
+    ohip_norm_desc nm{};
+    nm.epsilon = attr_f(nd, "epsilon", 1e-5f);
+    const ohip_tensor *gm = nd->n_inputs > 3 ? input(nd, 3) : nullptr, *bt = nd->n_inputs > 4 ? input(nd, 4) : nullptr;
+    if (gm || bt) {
+      if (!gm || !bt || !gm->device || !bt->device || gm->dtype != dt || bt->dtype != dt || gm->rank != 2 ||
+          bt->rank != 2 || gm->shape[0] != g.n || bt->shape[0] != g.n || gm->shape[1] != bt->shape[1]) {
+        if (!cache) ohip_weight_release(wt);
+        return decline("ConvInstanceNorm: modulation operands must be resident [N, S] rows of the input's dtype");
+      }
+      const int64_t so = attr_i(nd, "scale_offset", 0), bo = attr_i(nd, "bias_offset", 0), S = gm->shape[1];
+      if (so < 0 || bo < 0 || so + g.cout > S || bo + g.cout > S) {
+        if (!cache) ohip_weight_release(wt);
+        return decline("ConvInstanceNorm: modulation offsets");
+      }
+      nm.scale = static_cast<const char*>(ohip_dtensor_ptr(gm->device)) + so * ebytes(dt);
+      nm.bias = static_cast<const char*>(ohip_dtensor_ptr(bt->device)) + bo * ebytes(dt);
+      nm.per_sample = 1;
+      nm.stride = S;
+      nm.same_type = 1;
+    }
+    const std::string na = attr_s(nd, "norm_activation");
+    if (na == "relu") nm.act = OHIP_ACT_RELU;
+    else if (!na.empty()) {
+      if (!cache) ohip_weight_release(wt);
+      return decline("ConvInstanceNorm: activation");
+    }
+    rc = ohip_conv2d_instnorm(ctx, &d, xd, wt, bd, &nm, yd);
+  } else {
+    rc = ohip_conv2d(ctx, &d, xd, wt, bd, yd);
+  }
   if (!cache) ohip_weight_release(wt);
   if (rc) return rc;
   set_out(out, dt, oshape);
@@ -1662,7 +1698,7 @@ extern "C" int ohip_is_supported_op(const char* op) {
                                "ConvInteger", "Relu", "LeakyRelu", "Tanh", "Sigmoid", "Silu", "Identity",
                                "Add", "Sub", "Mul", "Div", "OxiInstanceNorm", "InstanceNormalization", "Resize",
                                "Pad", "MaxPool", "Concat", "Slice", "Reshape", "Flatten", "Squeeze", "Unsqueeze",
-                               "QuantizeLinear", "DequantizeLinear", "QLinearAdd"};
+                               "QuantizeLinear", "DequantizeLinear", "QLinearAdd", "OhipConvInstanceNorm"};
   for (const char* o : kOps)
     if (std::strcmp(op, o) == 0) return 1;
   return 0;
@@ -1682,6 +1718,7 @@ extern "C" int ohip_accepts_resident_slot(const char* op, int index) {
   if (!std::strcmp(op, "Add") || !std::strcmp(op, "Sub") || !std::strcmp(op, "Mul") || !std::strcmp(op, "Div"))
     return index == 0 || index == 1;
   if (!std::strcmp(op, "OxiInstanceNorm")) return index >= 0 && index <= 2;
+  if (!std::strcmp(op, "OhipConvInstanceNorm")) return index == 0 || index == 3 || index == 4;
   if (!std::strcmp(op, "Concat")) return index >= 0;
   if (!std::strcmp(op, "QLinearAdd")) return index == 0 || index == 3;
   return 0;
@@ -1788,6 +1825,7 @@ int dispatch_node(ohip_ctx* ctx, const ohip_node* node, int placement, ohip_outp
   else if (op == "Mul") rc = do_binary(ctx, node, ohip::BIN_MUL, placement, out);
   else if (op == "Div") rc = do_binary(ctx, node, ohip::BIN_DIV, placement, out);
   else if (op == "OxiInstanceNorm") rc = do_instnorm(ctx, node, false, placement, out);
+  else if (op == "OhipConvInstanceNorm") rc = do_conv(ctx, node, placement, out, true);
   else if (op == "InstanceNormalization") rc = do_instnorm(ctx, node, true, placement, out);
   else if (op == "Resize") rc = do_resize(ctx, node, placement, out);
   else if (op == "Pad") rc = do_pad(ctx, node, placement, out);

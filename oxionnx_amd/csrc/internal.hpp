@@ -111,6 +111,7 @@ struct OutMap {
   int64_t zstride; // bytes between the batch slices' outputs
   int zsw;         // > 0: slice z's output starts at (z / zsw) * zrow + (z % zsw) * zstride
   int64_t zrow;
+  int defer_reduce; // split-K: leave the partial sums in split_ws (the caller consumes them)
 };
 
 // Split-K plan.  The slices run on the 64x64 four-stage tile when its
@@ -359,6 +360,14 @@ hipError_t run_binary(int dt, const void* a, const void* b, void* y, int64_t n, 
                       hipStream_t st);
 hipError_t run_instnorm(int dt, const void* x, void* y, int64_t planes, int64_t spatial, int C, float eps,
                         const NormAffine& aff, hipStream_t st);
+// Instance normalisation of a split-K convolution's NCHW output straight from
+// its partial sums (PartialEpi layout: slice s, channel c, pixel i at
+// ws[(s * C + c) * Pp + i], images one after another along i): each output
+// is the ordered slice sum + the conv bias rounded to the tensor's dtype, as
+// the split reduction stores it, then normalised as run_instnorm does.
+constexpr int64_t kNormPartialsMaxSpatial = 16384;
+hipError_t run_instnorm_partials(int dt, const float* ws, int splits, int64_t Pp, const void* conv_bias, void* y,
+                                 int64_t N, int64_t spatial, int C, float eps, const NormAffine& aff, hipStream_t st);
 hipError_t run_resize_nearest(int elem_bytes, const void* x, void* y, int64_t planes, const ResizePlan& p,
                               hipStream_t st);
 hipError_t run_pad(int elem_bytes, const void* x, void* y, int64_t n, const PadPlan& p, hipStream_t st);

@@ -382,7 +382,7 @@ inline hipError_t launch_split_on(const LX& lx, const LY& ly, const Epi& epi, in
   hipLaunchKernelGGL((mfma_gemm_kernel<O, Tl, LX, LY, PartialEpi<T>, XX, XY>), dim3((unsigned)nb, (unsigned)splits),
                      dim3(Tl::kThreads), 0, st, lx, ly, pe, nP, nQ, kc, splits, tile_group_width());
   hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
+  if (e != hipSuccess || epi.out.defer) return e;
   return launch_reduce<O>(ws, splits, P, Q, epi, st);
 }
 
@@ -411,7 +411,7 @@ inline hipError_t launch_halo(const HaloGeo& g, const Epi& epi, int P, int Q, in
   hipLaunchKernelGGL((halo_conv_kernel<O, Ht, PartialEpi<T>>), dim3((unsigned)nb, (unsigned)splits),
                      dim3(Ht::kThreads), 0, st, g, pe, nP, nQ, splits, gp);
   hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
+  if (e != hipSuccess || epi.out.defer) return e;
   return launch_reduce<O>(ws, splits, P, Q, epi, st);
 }
 
@@ -496,6 +496,7 @@ inline OutAddr make_out_addr(const OutMap& o) {
   a.P = o.P; a.Q = o.Q; a.vec = o.vec;
   a.batch = o.batch > 1 ? o.batch : 1; a.zstride = o.zstride;
   a.zsw = o.zsw; a.zrow = o.zrow;
+  a.defer = o.defer_reduce;
   return a;
 }
 

@@ -364,6 +364,7 @@ struct OutAddr {
   int64_t zstride;   // bytes between the slices' outputs
   int zsw;           // > 0: slice z starts (z / zsw) * zrow + (z % zsw) * zstride bytes in
   int64_t zrow;
+  int defer;         // host side: a split-K launch leaves its partial sums for the caller
   __device__ __forceinline__ int64_t row(int i) const {
     if (bstride == 0) return (int64_t)i * si;
     const int n = (int)(((uint64_t)(uint32_t)i * ohw_mul) >> ohw_shift);

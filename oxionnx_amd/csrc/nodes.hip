@@ -145,6 +145,87 @@ __global__ void __launch_bounds__(kThreads) instnorm_kernel(const T* __restrict_
   }
 }
 
+// The same normalisation over a plane rebuilt from split-K partial sums in
+// LDS: x_i = T(sum over slices in slice order + bias), the value the split
+// reduction would have stored; the three passes then read LDS instead of
+// global memory, in the same order, so the result is the unfused pair's.
+template <class T>
+__global__ void __launch_bounds__(kThreads) instnorm_partials_kernel(const float* __restrict__ ws, int splits,
+                                                                     int64_t slice, int64_t Pp,
+                                                                     const T* __restrict__ cbias, T* __restrict__ y,
+                                                                     int spatial, int C, float eps, NormAffine aff) {
+#pragma clang fp contract(off)
+  extern __shared__ float xs[];
+  __shared__ float red[kThreads / 64];
+  const int64_t plane = blockIdx.x;
+  const int c = (int)(plane % C);
+  const int64_t n = plane / C;
+  const float* src = ws + (int64_t)c * Pp + n * spatial;
+  const float b = cbias ? (float)cbias[c] : -0.0f;
+  if ((spatial & 3) == 0 && ((uintptr_t)src & 15) == 0 && (slice & 3) == 0) {
+    // four pixels a thread, 16-byte loads, up to four slices in flight; the
+    // adds stay in slice order
+    typedef float f4 __attribute__((ext_vector_type(4)));
+    for (int i = 4 * threadIdx.x; i < spatial; i += 4 * kThreads) {
+      f4 acc = *reinterpret_cast<const f4*>(src + i);
+      int s = 1;
+      for (; s + 4 <= splits; s += 4) {
+        const f4 v0 = *reinterpret_cast<const f4*>(src + s * slice + i);
+        const f4 v1 = *reinterpret_cast<const f4*>(src + (s + 1) * slice + i);
+        const f4 v2 = *reinterpret_cast<const f4*>(src + (s + 2) * slice + i);
+        const f4 v3 = *reinterpret_cast<const f4*>(src + (s + 3) * slice + i);
+        acc += v0; acc += v1; acc += v2; acc += v3;
+      }
+      for (; s < splits; ++s) acc += *reinterpret_cast<const f4*>(src + s * slice + i);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float a = acc[e];
+        xs[i + e] = (float)(T)(a + b);
+      }
+    }
+  } else {
+    for (int i = threadIdx.x; i < spatial; i += kThreads) {
+      float acc = src[i];
+      for (int s = 1; s < splits; ++s) acc += src[s * slice + i];
+      xs[i] = (float)(T)(acc + b);
+    }
+  }
+  __syncthreads();
+  T* yp = y + plane * spatial;
+  float s = 0.0f;
+  for (int i = threadIdx.x; i < spatial; i += kThreads) s += xs[i];
+  const float mean = block_sum(s, red) / (float)spatial;
+  float q = 0.0f;
+  for (int i = threadIdx.x; i < spatial; i += kThreads) {
+    const float d = xs[i] - mean;
+    q += d * d;
+  }
+  const float var = block_sum(q, red) / (float)spatial;
+  const float inv = 1.0f / sqrtf(var + eps);
+  float sc = 1.0f, bi = 0.0f;
+  bool affine = false;
+  const int64_t ai = aff.per_sample ? n * aff.stride + c : c;
+  if (aff.scale) {
+    sc = aff.same_type ? (float)static_cast<const T*>(aff.scale)[ai] : static_cast<const float*>(aff.scale)[ai];
+    affine = true;
+  }
+  if (aff.bias) {
+    bi = aff.same_type ? (float)static_cast<const T*>(aff.bias)[ai] : static_cast<const float*>(aff.bias)[ai];
+    affine = true;
+  }
+  for (int i = threadIdx.x; i < spatial; i += kThreads) {
+    float v = (xs[i] - mean) * inv;
+    if (affine) {
+      v = (float)(T)v;
+      if (aff.scale) v = (float)(T)(v * sc);
+      if (aff.bias) v = (float)(T)(v + bi);
+    }
+    if (aff.act == UN_RELU) v = v > 0.0f ? v : 0.0f;
+    else if (aff.act == UN_LEAKY_RELU) v = v >= 0.0f ? v : v * aff.alpha;
+    yp[i] = (T)v;
+  }
+}
+
 // ---------------------------------------------------------------- nearest resize (rank 4, H and W)
 // Source index of output position j on one axis: transform_coord plus the
 // nearest rule and the clamp of the reference's build_axis
@@ -477,6 +558,24 @@ hipError_t run_instnorm(int dt, const void* x, void* y, int64_t planes, int64_t 
   else if (dt == DT_F16)
     hipLaunchKernelGGL(instnorm_kernel<_Float16>, dim3((unsigned)planes), dim3(kThreads), 0, st, (const _Float16*)x,
                        (_Float16*)y, spatial, C, eps, aff);
+  else
+    return hipErrorInvalidValue;
+  return hipGetLastError();
+}
+
+hipError_t run_instnorm_partials(int dt, const float* ws, int splits, int64_t Pp, const void* conv_bias, void* y,
+                                 int64_t N, int64_t spatial, int C, float eps, const NormAffine& aff, hipStream_t st) {
+  const int64_t planes = N * C;
+  if (planes <= 0 || spatial <= 0) return hipSuccess;
+  if (planes > 0x7fffffff || spatial > kNormPartialsMaxSpatial || splits < 1) return hipErrorInvalidValue;
+  const int64_t slice = (int64_t)C * Pp;
+  const size_t shm = (size_t)spatial * sizeof(float);
+  if (dt == DT_F32)
+    hipLaunchKernelGGL(instnorm_partials_kernel<float>, dim3((unsigned)planes), dim3(kThreads), shm, st, ws, splits,
+                       slice, Pp, (const float*)conv_bias, (float*)y, (int)spatial, C, eps, aff);
+  else if (dt == DT_F16)
+    hipLaunchKernelGGL(instnorm_partials_kernel<_Float16>, dim3((unsigned)planes), dim3(kThreads), shm, st, ws,
+                       splits, slice, Pp, (const _Float16*)conv_bias, (_Float16*)y, (int)spatial, C, eps, aff);
   else
     return hipErrorInvalidValue;
   return hipGetLastError();

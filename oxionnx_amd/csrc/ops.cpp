@@ -1300,8 +1300,18 @@ static int halo_plan(ohip_ctx* ctx, const ohip_conv_desc* d, int64_t G, int64_t 
   return (int)std::max<int64_t>(s, 1);
 }
 
+// A fused instance normalisation for conv2d_impl (ohip_conv2d_instnorm).
+struct ConvNorm {
+  float eps;
+  NormAffine aff;
+};
+// conv2d_impl's answer when a ConvNorm cannot read the split-K partial sums
+// (no split, a grouped or direct convolution, an NHWC output, a large
+// plane): nothing has been launched, and the caller runs the two steps.
+constexpr int kNormTwoStep = 1 << 20;
+
 static int conv2d_impl(ohip_ctx* ctx, const ohip_conv_desc* d, const void* x, const ohip_weight* w, const void* bias,
-                       void* y, bool noalloc) {
+                       void* y, bool noalloc, const ConvNorm* norm = nullptr) {
   int rc = activate(ctx);
   if (rc) return rc;
   if (!d || !x || !w || !y) return fail(OHIP_E_INVALID, "ohip_conv2d: null argument");
@@ -1361,6 +1371,9 @@ static int conv2d_impl(ohip_ctx* ctx, const ohip_conv_desc* d, const void* x, co
   // 232).  f16 / bf16 stay on the engine, which is faster there.
   const bool fewout = !direct && d->dtype == OHIP_F32 && G == 1 && d->in_layout == OHIP_NCHW &&
                       d->cout <= kFewOutMax && cg * d->kh * d->kw >= 32 && rows * d->cout >= 16384 && few_out_allowed();
+  if (norm && (direct || fewout || G != 1 || d->out_layout != OHIP_NCHW || g.oh * g.ow > kNormPartialsMaxSpatial ||
+               d->dtype == OHIP_BF16))
+    return kNormTwoStep;
   std::lock_guard<std::mutex> lock(ctx->mu);
   ctx->counters.dispatches++;
   if (direct || fewout) {
@@ -1404,6 +1417,10 @@ static int conv2d_impl(ohip_ctx* ctx, const ohip_conv_desc* d, const void* x, co
                                  : plan_split_tile(sP, sQ, (int)(d->kh * d->kw * (cp / ce)), ctx->tile_override,
                                                    d->dtype == OHIP_F32);
   const int splits = sc.splits;
+  if (norm && splits == 1) {   // counted again by the two-step path's plain call
+    ctx->counters.dispatches--;
+    return kNormTwoStep;
+  }
   size_t iw = splits > 1 ? plan.add(split_ws_bytes(sP, sQ, splits)) : SIZE_MAX;
   char* sbase = nullptr;
   rc = call_scratch(ctx, plan.total(), noalloc, &sbase);
@@ -1456,9 +1473,15 @@ static int conv2d_impl(ohip_ctx* ctx, const ohip_conv_desc* d, const void* x, co
     }
     o.splits = splits;
     o.split_ws = splits > 1 ? plan_at(sbase, plan, iw) : nullptr;
+    o.defer_reduce = norm ? 1 : 0;
     ctx->counters.contraction_launches++;
     hipError_t e = run_halo_float(d->dtype, hg, nchw_out, o, ctx->stream);
     if (e != hipSuccess) return hip_fail(e, "ohip_conv2d halo launch");
+    if (norm) {
+      e = run_instnorm_partials(d->dtype, static_cast<const float*>(o.split_ws), splits, (rows + 3) / 4 * 4, bias, y,
+                                d->n, ohw, (int)d->cout, norm->eps, norm->aff, ctx->stream);
+      if (e != hipSuccess) return hip_fail(e, "ohip_conv2d_instnorm launch");
+    }
     return OHIP_OK;
   }
 
@@ -1508,9 +1531,15 @@ static int conv2d_impl(ohip_ctx* ctx, const ohip_conv_desc* d, const void* x, co
       // vector stores need every group's first output aligned, not only group 0's
       o.vec = o.vec && o.zstride % (4 * eb) == 0;
     }
+    o.defer_reduce = norm ? 1 : 0;
     ctx->counters.contraction_launches++;
     hipError_t e = run_conv_float(d->dtype, col, wt, col_on_x, o, sc.tile, ctx->stream);
     if (e != hipSuccess) return hip_fail(e, "ohip_conv2d launch");
+    if (norm) {
+      e = run_instnorm_partials(d->dtype, static_cast<const float*>(o.split_ws), splits, (rows + 3) / 4 * 4, bias, y,
+                                d->n, ohw, (int)d->cout, norm->eps, norm->aff, ctx->stream);
+      if (e != hipSuccess) return hip_fail(e, "ohip_conv2d_instnorm launch");
+    }
   }
   return OHIP_OK;
 }
@@ -1518,6 +1547,44 @@ static int conv2d_impl(ohip_ctx* ctx, const ohip_conv_desc* d, const void* x, co
 extern "C" int ohip_conv2d(ohip_ctx* ctx, const ohip_conv_desc* d, const void* x, const ohip_weight* w,
                            const void* bias, void* y) {
   return conv2d_impl(ctx, d, x, w, bias, y, false);
+}
+
+// Conv -> instance normalisation.  With a split-K plan the normalisation
+// reads the partial sums (one launch fewer, no conv output round trip);
+// otherwise the conv writes a pooled temporary that the normalisation reads.
+extern "C" int ohip_conv2d_instnorm(ohip_ctx* ctx, const ohip_conv_desc* d, const void* x, const ohip_weight* w,
+                                    const void* bias, const ohip_norm_desc* nd, void* y) {
+  int rc = activate(ctx);
+  if (rc) return rc;
+  if (!d || !nd || !y) return fail(OHIP_E_INVALID, "ohip_conv2d_instnorm: null argument");
+  if (d->act != OHIP_ACT_NONE) return fail(OHIP_E_INVALID, "ohip_conv2d_instnorm: the conv must have no activation");
+  if (d->out_layout != OHIP_NCHW) return fail(OHIP_E_INVALID, "ohip_conv2d_instnorm: NCHW output only");
+  if (d->dtype != OHIP_F32 && d->dtype != OHIP_F16) return fail(OHIP_DECLINED, "ohip_conv2d_instnorm: f32 / f16 only");
+  if (nd->act != OHIP_ACT_NONE && nd->act != OHIP_ACT_RELU && nd->act != OHIP_ACT_LEAKY_RELU)
+    return fail(OHIP_E_INVALID, "ohip_conv2d_instnorm: activation");
+  ConvNorm cn{};
+  cn.eps = nd->epsilon;
+  cn.aff.scale = nd->scale; cn.aff.bias = nd->bias; cn.aff.per_sample = nd->per_sample; cn.aff.stride = nd->stride;
+  cn.aff.same_type = nd->same_type;
+  cn.aff.act = nd->act == OHIP_ACT_RELU ? UN_RELU : nd->act == OHIP_ACT_LEAKY_RELU ? UN_LEAKY_RELU : UN_IDENTITY;
+  cn.aff.alpha = nd->alpha;
+  rc = conv2d_impl(ctx, d, x, w, bias, y, false, &cn);
+  if (rc != kNormTwoStep) return rc;
+  ConvGeo g;
+  rc = conv_geo(d->h, d->w, d->kh, d->kw, d->stride_h, d->stride_w, d->dil_h, d->dil_w, d->pad_t, d->pad_l, d->pad_b,
+                d->pad_r, &g);
+  if (rc) return rc;
+  const int64_t spatial = g.oh * g.ow;
+  void* tmp = nullptr;
+  rc = pool_alloc(ctx, (size_t)(d->n * d->cout * spatial) * elem_bytes(d->dtype), &tmp);
+  if (rc) return rc;
+  rc = conv2d_impl(ctx, d, x, w, bias, tmp, false, nullptr);
+  if (rc == OHIP_OK) {
+    hipError_t e = run_instnorm(d->dtype, tmp, y, d->n * d->cout, spatial, (int)d->cout, cn.eps, cn.aff, ctx->stream);
+    if (e != hipSuccess) rc = hip_fail(e, "ohip_conv2d_instnorm: normalisation launch");
+  }
+  const int rf = pool_free(ctx, tmp);
+  return rc ? rc : rf;
 }
 
 // Same kernels as ohip_conv2d; the staging copy and the split-K partial sums

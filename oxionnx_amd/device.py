@@ -239,6 +239,32 @@ class HipContext:
         L.check(fn(self.h, ctypes.byref(d), _ptr(x), w.handle, _ptr(bias), _ptr(out)))
         return out
 
+    def conv2d_instnorm(self, x, w, bias=None, pads=(0, 0, 0, 0), strides=(1, 1), dilations=(1, 1), eps=1e-5,
+                        gamma=None, beta=None, scale_offset=0, bias_offset=0, relu=False, out=None):
+        """Conv (NCHW, ungrouped, no activation) followed by instance
+        normalisation in one call (ohip_conv2d_instnorm); gamma / beta are
+        optional [N, S] device rows of the tensor's dtype (the AdaIN form:
+        channel c of sample n reads element n * S + offset + c)."""
+        torch = _torch()
+        dt = ohip_dtype(x.dtype)
+        cout, cin, kh, kw = w.shape
+        n, c, h, wd = x.shape
+        oh = L.lib().ohip_conv_out_dim(h, pads[0], pads[2], kh, dilations[0], strides[0])
+        ow = L.lib().ohip_conv_out_dim(wd, pads[1], pads[3], kw, dilations[1], strides[1])
+        if out is None:
+            out = torch.empty((n, cout, oh, ow), dtype=x.dtype, device=x.device)
+        d = L.ConvDesc(n, c, h, wd, cout, kh, kw, 1, strides[0], strides[1], dilations[0], dilations[1],
+                       pads[0], pads[1], pads[2], pads[3], dt, L.NCHW, L.NCHW, L.ACT_NONE, 0.0, 0.0, 0)
+        nd = L.NormDesc(eps, None, None, 0, 0, 0, L.ACT_RELU if relu else L.ACT_NONE, 0.0)
+        if gamma is not None:
+            eb = L.ELEM_BYTES[dt]
+            nd.scale = gamma.data_ptr() + scale_offset * eb
+            nd.bias = beta.data_ptr() + bias_offset * eb
+            nd.per_sample, nd.stride, nd.same_type = 1, gamma.shape[1], 1
+        L.check(L.lib().ohip_conv2d_instnorm(self.h, ctypes.byref(d), _ptr(x), w.handle, _ptr(bias),
+                                             ctypes.byref(nd), _ptr(out)))
+        return out
+
     def matmul(self, a, b, out=None):
         """Batched MatMul of two device tensors, [..., M, K] x [..., K, N], with the
         reference's slice rule (slice s: A slice s % a_batches, B slice s % b_batches)."""

@@ -153,7 +153,47 @@ def fuse(graph: Graph, level: str = "all") -> Graph:
                     changed = True
                     break
         nodes = [n for n in nodes if n is not None] if changed else nodes
+    if not ref_only:
+        nodes = _fuse_conv_instnorm(nodes, keep_out, inits)
     return replace(graph, nodes=_drop_dead(nodes, keep_out), initializers=inits)
+
+
+def _fuse_conv_instnorm(nodes, keep_out, inits):
+    """Conv (ungrouped, no activation) whose only consumer is an
+    OxiInstanceNorm (plain, or the fused AdaIN form above): one
+    OhipConvInstanceNorm node, inputs [x, W, B or '', gamma rows, beta rows],
+    the Conv's attributes plus the norm's epsilon, modulation offsets and
+    activation (as "norm_activation").  Runs after the other fusions so the
+    AdaIN tail is already folded into the norm."""
+    cons = _consumers(nodes)
+    out = list(nodes)
+    for i, n in enumerate(out):
+        if n is None or n.op != "Conv" or "activation" in n.attrs.strings or n.attrs.ints.get("group", 1) != 1:
+            continue
+        c = cons.get(n.outputs[0], [])
+        if len(c) != 1 or n.outputs[0] in keep_out:
+            continue
+        norm = out[c[0]]
+        if norm is None or norm.op != "OxiInstanceNorm":
+            continue
+        w = inits.get(n.inputs[1]) if len(n.inputs) > 1 else None
+        if w is None or np.asarray(w.data if isinstance(w, ep.Typed) else w).dtype not in (np.float32, np.float16):
+            continue   # the fused kernels cover f32 / f16
+        extra = [t for t in norm.inputs[1:] if t]
+        if extra and len(extra) != 2:
+            continue
+        a = replace(n.attrs, strings=dict(n.attrs.strings), floats=dict(n.attrs.floats), ints=dict(n.attrs.ints))
+        a.floats["epsilon"] = norm.attrs.floats.get("epsilon", 1e-5)
+        for key in ("scale_offset", "bias_offset"):
+            if key in norm.attrs.ints:
+                a.ints[key] = norm.attrs.ints[key]
+        if "activation" in norm.attrs.strings:
+            a.strings["norm_activation"] = norm.attrs.strings["activation"]
+        ins = list(n.inputs) + [""] * (3 - len(n.inputs))
+        # at the norm's position: the modulation rows may be produced after the conv
+        out[c[0]] = replace(n, op="OhipConvInstanceNorm", inputs=ins + extra, outputs=list(norm.outputs), attrs=a)
+        out[i] = None
+    return [n for n in out if n is not None]
 
 
 def _init_array(inits, name):

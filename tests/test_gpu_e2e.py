@@ -499,3 +499,68 @@ def test_node_golden_vectors_on_the_device(ctx, c):
     y = Session(g, ctx).run({"x": x})["y"]
     assert list(y.shape) == c["shape"]
     np.testing.assert_allclose(np.asarray(y, np.float64).ravel(), c["expected"], atol=c.get("tol", 0.0), rtol=0)
+
+
+def _conv_adain_graph(n, c, hw, dtype, adain=True, relu=True, seed=3):
+    """x -> Pad(reflect 1) -> Conv 3x3 c->c -> OxiInstanceNorm [-> Mul(gamma)
+    -> Add(beta)] [-> Relu], gamma / beta column ranges of a style input."""
+    A = ep.Attributes
+    rng = np.random.default_rng(seed)
+    f = lambda v: np.asarray(v, np.float32)
+    inits = {"pads": f([0, 0, 1, 1, 0, 0, 1, 1]), "W": rng.normal(0, 0.02, (c, c, 3, 3)).astype(np.float32),
+             "B": rng.normal(0, 0.02, c).astype(np.float32)}
+    nodes = [ep.Node("Pad", ["x", "pads"], ["xp"], A(strings={"mode": "reflect"}), name="pad"),
+             ep.Node("Conv", ["xp", "W", "B"], ["h"], A(int_lists={"kernel_shape": [3, 3]}), name="conv"),
+             ep.Node("OxiInstanceNorm", ["h"], ["nrm"], A(floats={"epsilon": 1e-5}), name="norm")]
+    last = "nrm"
+    if adain:
+        for part, (lo, hi) in (("g", (0, c)), ("b", (c, 2 * c))):
+            inits[part + "st"], inits[part + "en"], inits[part + "ax"] = f([lo]), f([hi]), f([1])
+            inits[part + "sh"] = f([n, c, 1, 1])
+            nodes.append(ep.Node("Slice", ["style", part + "st", part + "en", part + "ax"], [part + "sl"], name=part + "sl"))
+            nodes.append(ep.Node("Reshape", [part + "sl", part + "sh"], [part + "4d"], name=part + "4d"))
+        nodes.append(ep.Node("Mul", ["nrm", "g4d"], ["mul"], name="mul"))
+        nodes.append(ep.Node("Add", ["mul", "b4d"], ["add"], name="add"))
+        last = "add"
+    if relu:
+        nodes.append(ep.Node("Relu", [last], ["y"], name="y"))
+    else:
+        nodes[-1].outputs = ["y"]
+    feeds = {"x": rng.uniform(-1, 1, (n, c, hw, hw)).astype(np.float32),
+             "style": (rng.normal(0, 0.3, (n, 2 * c)) + np.r_[np.ones(c), np.zeros(c)]).astype(np.float32)}
+    if dtype == "f16":
+        for k in ("W", "B"):
+            inits[k] = inits[k].astype(np.float16)
+        feeds = {k: v.astype(np.float16) for k, v in feeds.items()}
+    inputs = ["x", "style"] if adain else ["x"]
+    if not adain:
+        feeds.pop("style")
+    return Graph(nodes, inits, inputs, ["y"], name="conv_adain"), feeds
+
+
+# (n, channels, extent, dtype, AdaIN, Relu): the 512-channel residual conv
+# (split K on the halo-patch kernel: the norm reads the partial sums), a
+# 128-channel one (split on the engine), two images, and small convs whose
+# single-slice plan takes the two-step path
+CONV_NORM_CASES = [
+    (1, 512, 32, "f16", True, True),
+    (1, 512, 32, "f32", True, False),
+    (1, 128, 32, "f16", False, True),
+    (2, 64, 16, "f16", True, True),
+    (2, 16, 8, "f32", False, False),
+]
+
+
+@pytest.mark.parametrize("case", CONV_NORM_CASES, ids=str)
+def test_conv_instnorm_fusion_matches_unfused(ctx, case):
+    """The fused Conv -> norm node equals the unfused node chain bit for bit
+    (the same conv sums and roundings; only launches and round trips go)."""
+    n, c, hw, dt, adain, relu = case
+    g, feeds = _conv_adain_graph(n, c, hw, dt, adain, relu)
+    fused = Session(g, ctx)
+    assert [nd.op for nd in fused.graph.nodes].count("OhipConvInstanceNorm") == 1
+    got = fused.run(feeds)["y"]
+    want = Session(g, ctx, optimize="reference").run(feeds)["y"]
+    np.testing.assert_array_equal(got, want)
+    ref = G.run_graph(g, feeds, half=(dt == "f16"))["y"]
+    close(got, ref, 1e-2 if dt == "f16" else 1e-4)

@@ -56,4 +56,24 @@ def test_face_swap_style_gemms_merge():
     from oxionnx_amd import workloads
     g, _ = workloads.face_swap_generator(dtype="f32", n_blocks=2)
     ops = [n.op for n in fuse(g).nodes]
-    assert ops.count("Gemm") == 1 and ops.count("OxiInstanceNorm") == 4
+    # each residual conv and its AdaIN norm become one fused node
+    assert ops.count("Gemm") == 1 and ops.count("OhipConvInstanceNorm") == 4
+    assert ops.count("OxiInstanceNorm") == 0 and ops.count("Conv") == 6
+
+
+def test_conv_instnorm_fusion_attributes():
+    """Conv (reflect Pad folded in) -> AdaIN norm -> Relu becomes one node
+    carrying both halves' attributes; a grouped conv, or a conv with a second
+    consumer, is left alone."""
+    from oxionnx_amd import workloads
+    g, _ = workloads.face_swap_generator(dtype="f32", n_blocks=1)
+    nodes = fuse(g).nodes
+    fused = [n for n in nodes if n.op == "OhipConvInstanceNorm"]
+    assert len(fused) == 2
+    first, second = fused
+    assert first.attrs.strings.get("pad_mode") == "reflect"
+    assert first.attrs.strings.get("norm_activation") == "relu" and "norm_activation" not in second.attrs.strings
+    assert len(first.inputs) == 5 and first.inputs[3] == first.inputs[4]
+    assert first.attrs.floats["epsilon"] == 1e-5
+    assert first.attrs.ints["bias_offset"] - first.attrs.ints["scale_offset"] == 512
+    assert "activation" not in first.attrs.strings
