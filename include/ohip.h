@@ -253,6 +253,8 @@ typedef struct {
     int same_type;         /* scale / bias in the tensor's dtype (else f32) */
     int act;               /* OHIP_ACT_NONE, OHIP_ACT_RELU or OHIP_ACT_LEAKY_RELU */
     float alpha;           /* leaky slope */
+    const void* residual;  /* added after the activation: an NCHW tensor of the output's shape and
+                              dtype (a fused residual Add), may be null */
 } ohip_norm_desc;
 int ohip_conv2d_instnorm(ohip_ctx* ctx, const ohip_conv_desc* d, const void* x, const ohip_weight* w,
                          const void* bias, const ohip_norm_desc* norm, void* y);

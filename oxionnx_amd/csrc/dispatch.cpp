@@ -379,6 +379,10 @@ void fused_act(const ohip_node* nd, int* act, float* lo, float* hi) {
 std::string wkey_name(const ohip_tensor* t) { return t->name ? std::string(t->name) : std::string(); }
 
 // ------------------------------------------------------------------ float Conv
+bool bcast_plan(const int64_t* as, int ra, const int64_t* bs, int rb, ohip::BcastPlan* p, std::vector<int64_t>* oshape,
+                int64_t* n_out);
+const void* float_operand(Stage& st, const ohip_tensor* t, int dt);
+
 // with_norm: this provider's fused Conv -> OxiInstanceNorm node
 // (OhipConvInstanceNorm): inputs 0-2 are the Conv's, inputs 3 / 4 the
 // optional AdaIN modulation rows (resident [N, S], as the fused
@@ -468,7 +472,45 @@ int do_conv(ohip_ctx* ctx, const ohip_node* nd, int placement, ohip_output* out,
       if (!cache) ohip_weight_release(wt);
       return decline("ConvInstanceNorm: activation");
     }
-    rc = ohip_conv2d_instnorm(ctx, &d, xd, wt, bd, &nm, yd);
+    // input 5: a fused residual Add (the other operand of an Add that was the
+    // norm's only consumer); added in the kernel when it has the output's
+    // shape, else broadcast by the binary kernel after the fused pair
+    const ohip_tensor* res = nd->n_inputs > 5 ? input(nd, 5) : nullptr;
+    if (res) {
+      const void* rd = float_operand(st, res, dt);
+      if (!rd) {
+        if (!cache) ohip_weight_release(wt);
+        return decline("ConvInstanceNorm: residual dtype");
+      }
+      const bool same = res->rank == (int)oshape.size() &&
+                        std::equal(oshape.begin(), oshape.end(), res->shape);
+      if (same) {
+        nm.residual = rd;
+        rc = ohip_conv2d_instnorm(ctx, &d, xd, wt, bd, &nm, yd);
+      } else {
+        ohip::BcastPlan p{};
+        std::vector<int64_t> bshape;
+        int64_t n = 0;
+        if (!bcast_plan(oshape.data(), (int)oshape.size(), res->shape, res->rank, &p, &bshape, &n)) {
+          if (!cache) ohip_weight_release(wt);
+          return decline("ConvInstanceNorm: residual shape");
+        }
+        void* bd2 = st.alloc((size_t)n * ebytes(dt));
+        if (!bd2) { if (!cache) ohip_weight_release(wt); return OHIP_E_NOMEM; }
+        rc = ohip_conv2d_instnorm(ctx, &d, xd, wt, bd, &nm, yd);
+        if (rc == OHIP_OK) {
+          hipError_t e = ohip::run_binary(dt, yd, rd, bd2, n, p, false, ohip::BIN_ADD,
+                                          (hipStream_t)ohip_ctx_stream(ctx));
+          if (e != hipSuccess) rc = ohip_hip_error_internal(e, "node kernel launch");
+        }
+        if (!cache) ohip_weight_release(wt);
+        if (rc) return rc;
+        set_out(out, dt, bshape);
+        return finish_output(ctx, st, placement, out, bd2, (size_t)n * ebytes(dt), dt);
+      }
+    } else {
+      rc = ohip_conv2d_instnorm(ctx, &d, xd, wt, bd, &nm, yd);
+    }
   } else {
     rc = ohip_conv2d(ctx, &d, xd, wt, bd, yd);
   }
@@ -996,31 +1038,45 @@ int do_unary(ohip_ctx* ctx, const ohip_node* nd, int op, int placement, ohip_out
 }
 
 // ---------------------------------------------------------------- binary (numpy broadcasting)
+// The broadcast plan of a (rank ra) against b (rank rb): false when the
+// shapes do not broadcast or the rank exceeds the kernel's.
+bool bcast_plan(const int64_t* as, int ra, const int64_t* bs, int rb, ohip::BcastPlan* p, std::vector<int64_t>* oshape,
+                int64_t* n_out) {
+  const int rank = std::max(ra, rb);
+  if (rank > ohip::kMaxRank) return false;
+  *p = ohip::BcastPlan{};
+  p->rank = rank;
+  int64_t sa = 1, sb = 1, n = 1;
+  oshape->assign((size_t)rank, 0);
+  for (int d = 0; d < rank; ++d) {
+    const int slot = ohip::kMaxRank - 1 - d;
+    const int ia = ra - 1 - d, ib = rb - 1 - d;
+    const int64_t ea = ia >= 0 ? as[ia] : 1, eb = ib >= 0 ? bs[ib] : 1;
+    if (ea != eb && ea != 1 && eb != 1) return false;
+    const int64_t e = ea == 1 ? eb : ea;
+    p->shape[slot] = e;
+    p->sa[slot] = ea == 1 ? 0 : sa;
+    p->sb[slot] = eb == 1 ? 0 : sb;
+    sa *= ea;
+    sb *= eb;
+    n *= e;
+    (*oshape)[(size_t)(rank - 1 - d)] = e;
+  }
+  *n_out = n;
+  return true;
+}
+
 int do_binary(ohip_ctx* ctx, const ohip_node* nd, int op, int placement, ohip_output* out) {
   const ohip_tensor *a = input(nd, 0), *b = input(nd, 1);
   if (!a || !b) return decline("binary: missing input");
   const int dt = node_float_dtype(nd);
   if (!is_float_dt(dt)) return decline("binary: dtype");
-  const int rank = std::max(a->rank, b->rank);
-  if (rank > ohip::kMaxRank) return decline("binary: rank");
+  if (std::max(a->rank, b->rank) > ohip::kMaxRank) return decline("binary: rank");
   ohip::BcastPlan p{};
-  p.rank = rank;
-  int64_t sa = 1, sb = 1, n = 1;
-  std::vector<int64_t> oshape((size_t)rank);
-  for (int d = 0; d < rank; ++d) {
-    const int slot = ohip::kMaxRank - 1 - d;
-    const int ia = a->rank - 1 - d, ib = b->rank - 1 - d;
-    const int64_t ea = ia >= 0 ? a->shape[ia] : 1, eb = ib >= 0 ? b->shape[ib] : 1;
-    if (ea != eb && ea != 1 && eb != 1) return decline("binary: shapes do not broadcast");
-    const int64_t e = ea == 1 ? eb : ea;
-    p.shape[slot] = e;
-    p.sa[slot] = ea == 1 ? 0 : sa;
-    p.sb[slot] = eb == 1 ? 0 : sb;
-    sa *= ea;
-    sb *= eb;
-    n *= e;
-    oshape[(size_t)(rank - 1 - d)] = e;
-  }
+  std::vector<int64_t> oshape;
+  int64_t n = 0;
+  if (!bcast_plan(a->shape, a->rank, b->shape, b->rank, &p, &oshape, &n))
+    return decline("binary: shapes do not broadcast");
   const bool same = numel(a) == n && numel(b) == n;
   Stage st(ctx);
   const void* ad = float_operand(st, a, dt);
@@ -1718,7 +1774,7 @@ extern "C" int ohip_accepts_resident_slot(const char* op, int index) {
   if (!std::strcmp(op, "Add") || !std::strcmp(op, "Sub") || !std::strcmp(op, "Mul") || !std::strcmp(op, "Div"))
     return index == 0 || index == 1;
   if (!std::strcmp(op, "OxiInstanceNorm")) return index >= 0 && index <= 2;
-  if (!std::strcmp(op, "OhipConvInstanceNorm")) return index == 0 || index == 3 || index == 4;
+  if (!std::strcmp(op, "OhipConvInstanceNorm")) return index == 0 || index == 3 || index == 4 || index == 5;
   if (!std::strcmp(op, "Concat")) return index >= 0;
   if (!std::strcmp(op, "QLinearAdd")) return index == 0 || index == 3;
   return 0;

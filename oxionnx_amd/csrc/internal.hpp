@@ -330,6 +330,7 @@ struct NormAffine {
   int same_type;       // scale / bias are in the normalised tensor's dtype (else f32)
   int act;             // UN_NONE / UN_RELU / UN_LEAKY_RELU
   float alpha;
+  const void* residual;   // added last (an Add of a same-shape tensor of the dtype), may be null
 };
 
 struct ResizePlan {

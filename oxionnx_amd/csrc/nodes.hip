@@ -141,6 +141,7 @@ __global__ void __launch_bounds__(kThreads) instnorm_kernel(const T* __restrict_
     }
     if (aff.act == UN_RELU) v = v > 0.0f ? v : 0.0f;
     else if (aff.act == UN_LEAKY_RELU) v = v >= 0.0f ? v : v * aff.alpha;
+    if (aff.residual) v = (float)(T)v + ldf(static_cast<const T*>(aff.residual) + plane * spatial, i);
     stf(yp, i, v);
   }
 }
@@ -222,6 +223,7 @@ __global__ void __launch_bounds__(kThreads) instnorm_partials_kernel(const float
     }
     if (aff.act == UN_RELU) v = v > 0.0f ? v : 0.0f;
     else if (aff.act == UN_LEAKY_RELU) v = v >= 0.0f ? v : v * aff.alpha;
+    if (aff.residual) v = (float)(T)v + (float)static_cast<const T*>(aff.residual)[plane * spatial + i];
     yp[i] = (T)v;
   }
 }

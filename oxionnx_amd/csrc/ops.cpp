@@ -1568,6 +1568,7 @@ extern "C" int ohip_conv2d_instnorm(ohip_ctx* ctx, const ohip_conv_desc* d, cons
   cn.aff.same_type = nd->same_type;
   cn.aff.act = nd->act == OHIP_ACT_RELU ? UN_RELU : nd->act == OHIP_ACT_LEAKY_RELU ? UN_LEAKY_RELU : UN_IDENTITY;
   cn.aff.alpha = nd->alpha;
+  cn.aff.residual = nd->residual;
   rc = conv2d_impl(ctx, d, x, w, bias, y, false, &cn);
   if (rc != kNormTwoStep) return rc;
   ConvGeo g;

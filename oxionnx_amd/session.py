@@ -161,10 +161,11 @@ def fuse(graph: Graph, level: str = "all") -> Graph:
 def _fuse_conv_instnorm(nodes, keep_out, inits):
     """Conv (ungrouped, no activation) whose only consumer is an
     OxiInstanceNorm (plain, or the fused AdaIN form above): one
-    OhipConvInstanceNorm node, inputs [x, W, B or '', gamma rows, beta rows],
-    the Conv's attributes plus the norm's epsilon, modulation offsets and
-    activation (as "norm_activation").  Runs after the other fusions so the
-    AdaIN tail is already folded into the norm."""
+    OhipConvInstanceNorm node, inputs [x, W, B or '', gamma rows, beta rows
+    (or '', ''), residual], the Conv's attributes plus the norm's epsilon,
+    modulation offsets and activation (as "norm_activation"); a two-input
+    Add that is the norm's only consumer becomes the residual.  Runs after
+    the other fusions so the AdaIN tail is already folded into the norm."""
     cons = _consumers(nodes)
     out = list(nodes)
     for i, n in enumerate(out):
@@ -190,8 +191,23 @@ def _fuse_conv_instnorm(nodes, keep_out, inits):
         if "activation" in norm.attrs.strings:
             a.strings["norm_activation"] = norm.attrs.strings["activation"]
         ins = list(n.inputs) + [""] * (3 - len(n.inputs))
-        # at the norm's position: the modulation rows may be produced after the conv
-        out[c[0]] = replace(n, op="OhipConvInstanceNorm", inputs=ins + extra, outputs=list(norm.outputs), attrs=a)
+        ins += extra if extra else ["", ""]
+        outs, pos = list(norm.outputs), c[0]
+        # a residual Add as the norm's only consumer folds in as input 5
+        r = cons.get(norm.outputs[0], [])
+        if len(r) == 1 and norm.outputs[0] not in keep_out and out[r[0]] is not None and out[r[0]].op == "Add":
+            add = out[r[0]]
+            if len(add.inputs) == 2 and add.inputs.count(norm.outputs[0]) == 1:
+                ins.append(add.inputs[1] if add.inputs[0] == norm.outputs[0] else add.inputs[0])
+                outs, pos = list(add.outputs), r[0]
+                out[r[0]] = None
+        if len(ins) == 5 and not extra:
+            ins = ins[:3]
+        # at the last folded node's position: the modulation rows and the
+        # residual may be produced after the conv
+        out[pos] = replace(n, op="OhipConvInstanceNorm", inputs=ins, outputs=outs, attrs=a)
+        if pos != c[0]:
+            out[c[0]] = None
         out[i] = None
     return [n for n in out if n is not None]
 

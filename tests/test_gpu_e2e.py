@@ -501,9 +501,11 @@ def test_node_golden_vectors_on_the_device(ctx, c):
     np.testing.assert_allclose(np.asarray(y, np.float64).ravel(), c["expected"], atol=c.get("tol", 0.0), rtol=0)
 
 
-def _conv_adain_graph(n, c, hw, dtype, adain=True, relu=True, seed=3):
+def _conv_adain_graph(n, c, hw, dtype, adain=True, relu=True, seed=3, residual=None):
     """x -> Pad(reflect 1) -> Conv 3x3 c->c -> OxiInstanceNorm [-> Mul(gamma)
-    -> Add(beta)] [-> Relu], gamma / beta column ranges of a style input."""
+    -> Add(beta)] [-> Relu] [-> Add(residual)], gamma / beta column ranges
+    of a style input; residual "skip" adds x, "bcast" a [1, c, 1, 1]
+    initializer."""
     A = ep.Attributes
     rng = np.random.default_rng(seed)
     f = lambda v: np.asarray(v, np.float32)
@@ -523,14 +525,21 @@ def _conv_adain_graph(n, c, hw, dtype, adain=True, relu=True, seed=3):
         nodes.append(ep.Node("Add", ["mul", "b4d"], ["add"], name="add"))
         last = "add"
     if relu:
-        nodes.append(ep.Node("Relu", [last], ["y"], name="y"))
-    else:
-        nodes[-1].outputs = ["y"]
+        nodes.append(ep.Node("Relu", [last], ["act"], name="act"))
+        last = "act"
+    if residual:
+        other = "x"
+        if residual == "bcast":
+            inits["rb"] = rng.normal(0, 0.5, (1, c, 1, 1)).astype(np.float32)
+            other = "rb"
+        nodes.append(ep.Node("Add", [last, other], ["res"], name="res"))
+    nodes[-1].outputs = ["y"]
     feeds = {"x": rng.uniform(-1, 1, (n, c, hw, hw)).astype(np.float32),
              "style": (rng.normal(0, 0.3, (n, 2 * c)) + np.r_[np.ones(c), np.zeros(c)]).astype(np.float32)}
     if dtype == "f16":
-        for k in ("W", "B"):
-            inits[k] = inits[k].astype(np.float16)
+        for k in ("W", "B", "rb"):
+            if k in inits:
+                inits[k] = inits[k].astype(np.float16)
         feeds = {k: v.astype(np.float16) for k, v in feeds.items()}
     inputs = ["x", "style"] if adain else ["x"]
     if not adain:
@@ -543,11 +552,12 @@ def _conv_adain_graph(n, c, hw, dtype, adain=True, relu=True, seed=3):
 # 128-channel one (split on the engine), two images, and small convs whose
 # single-slice plan takes the two-step path
 CONV_NORM_CASES = [
-    (1, 512, 32, "f16", True, True),
-    (1, 512, 32, "f32", True, False),
-    (1, 128, 32, "f16", False, True),
-    (2, 64, 16, "f16", True, True),
-    (2, 16, 8, "f32", False, False),
+    (1, 512, 32, "f16", True, True, None),
+    (1, 512, 32, "f16", True, False, "skip"),
+    (1, 512, 32, "f32", True, False, None),
+    (1, 128, 32, "f16", False, True, "bcast"),
+    (2, 64, 16, "f16", True, True, "skip"),
+    (2, 16, 8, "f32", False, False, None),
 ]
 
 
@@ -555,8 +565,8 @@ CONV_NORM_CASES = [
 def test_conv_instnorm_fusion_matches_unfused(ctx, case):
     """The fused Conv -> norm node equals the unfused node chain bit for bit
     (the same conv sums and roundings; only launches and round trips go)."""
-    n, c, hw, dt, adain, relu = case
-    g, feeds = _conv_adain_graph(n, c, hw, dt, adain, relu)
+    n, c, hw, dt, adain, relu, residual = case
+    g, feeds = _conv_adain_graph(n, c, hw, dt, adain, relu, residual=residual)
     fused = Session(g, ctx)
     assert [nd.op for nd in fused.graph.nodes].count("OhipConvInstanceNorm") == 1
     got = fused.run(feeds)["y"]

@@ -77,3 +77,6 @@ def test_conv_instnorm_fusion_attributes():
     assert first.attrs.floats["epsilon"] == 1e-5
     assert first.attrs.ints["bias_offset"] - first.attrs.ints["scale_offset"] == 512
     assert "activation" not in first.attrs.strings
+    # the block's skip Add folds into the second node as its residual (input 5)
+    assert len(second.inputs) == 6 and second.outputs[0].startswith("skip")
+    assert not any(n.op == "Add" for n in nodes)
