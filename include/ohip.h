@@ -243,7 +243,8 @@ int ohip_conv2d_noalloc(ohip_ctx* ctx, const ohip_conv_desc* d, const void* x, c
  * y = InstanceNorm(conv(x)) with the conv output rounded to its dtype first,
  * exactly as the unfused pair computes it.  When the convolution splits K,
  * the normalisation reads the partial sums directly (no reduction launch).
- * The conv must be ungrouped, NCHW in / out and without activation. */
+ * The conv must be ungrouped and without activation; out_layout may be
+ * OHIP_NHWC (cout elements per pixel, whole 16-byte pixels). */
 typedef struct {
     float epsilon;
     const void* scale;     /* gamma per channel (or per (n, c) when per_sample); may be null */
@@ -253,8 +254,9 @@ typedef struct {
     int same_type;         /* scale / bias in the tensor's dtype (else f32) */
     int act;               /* OHIP_ACT_NONE, OHIP_ACT_RELU or OHIP_ACT_LEAKY_RELU */
     float alpha;           /* leaky slope */
-    const void* residual;  /* added after the activation: an NCHW tensor of the output's shape and
-                              dtype (a fused residual Add), may be null */
+    const void* residual;  /* added after the activation: a tensor of the output's shape and dtype
+                              (a fused residual Add), may be null */
+    int residual_layout;   /* OHIP_NCHW, or OHIP_NHWC with cout elements per pixel */
 } ohip_norm_desc;
 int ohip_conv2d_instnorm(ohip_ctx* ctx, const ohip_conv_desc* d, const void* x, const ohip_weight* w,
                          const void* bias, const ohip_norm_desc* norm, void* y);

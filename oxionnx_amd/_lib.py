@@ -68,7 +68,7 @@ class ConvDesc(ctypes.Structure):
 class NormDesc(ctypes.Structure):
     _fields_ = [("epsilon", ctypes.c_float), ("scale", ctypes.c_void_p), ("bias", ctypes.c_void_p),
                 ("per_sample", ctypes.c_int), ("stride", I64), ("same_type", ctypes.c_int), ("act", ctypes.c_int),
-                ("alpha", ctypes.c_float), ("residual", ctypes.c_void_p)]
+                ("alpha", ctypes.c_float), ("residual", ctypes.c_void_p), ("residual_layout", ctypes.c_int)]
 
 
 class ConvTDesc(ctypes.Structure):

@@ -27,6 +27,7 @@ int64_t ohip_dtensor_pitch_internal(const ohip_dtensor* t);
 int ohip_dtensor_view_nhwc_internal(const ohip_dtensor* src, int64_t c0, int64_t cn, ohip_dtensor** out);
 int ohip_dtensor_to_nchw_internal(ohip_ctx* ctx, const ohip_dtensor* t, void* dst);
 int ohip_hip_error_internal(hipError_t e, const char* what);
+int ohip_conv_halo_splits_internal(ohip_ctx* ctx, const ohip_conv_desc* d);
 
 namespace {
 
@@ -403,7 +404,10 @@ int do_conv(ohip_ctx* ctx, const ohip_node* nd, int placement, ohip_output* out,
   // the fused node has no host counterpart to fall back to: it always runs here
   if (!with_norm && !any_resident(nd) && !ohip_conv_admits(&tun, g.cout, cg * g.kh * g.kw, g.n * g.oh * g.ow))
     return decline("Conv: below conv_min_mac");
-  if (x->device && ohip_dtensor_layout(x->device) != OHIP_NCHW) return decline("Conv: resident input layout");
+  // a resident NHWC input reaches here only where the halo-patch path reads
+  // it in place (takes_nhwc)
+  const bool x_nhwc = x->device && ohip_dtensor_layout(x->device) == OHIP_NHWC;
+  if (x_nhwc && ohip_dtensor_pitch_internal(x->device) != g.c) return decline("Conv: NHWC pixel pitch");
 
   std::string name = wkey_name(w), label = "Conv.W";
   ohip_weight_key key{name.c_str(), label.c_str()};
@@ -432,8 +436,12 @@ int do_conv(ohip_ctx* ctx, const ohip_node* nd, int placement, ohip_output* out,
   const size_t obytes = (size_t)(g.n * g.cout * g.oh * g.ow) * ebytes(dt);
   void* yd = st.alloc(obytes);
   if (!xd || !yd || (b && !bd)) { if (!cache) ohip_weight_release(wt); return OHIP_E_NOMEM; }
+  // a session layout hint: every consumer of this output reads NHWC in place
+  const bool y_nhwc = placement == OHIP_PLACE_DEVICE && attr_i(nd, "out_nhwc", 0) == 1 && g.group == 1 &&
+                      !g.rank1 && g.cout % (16 / ebytes(dt)) == 0 && (!with_norm || g.cout % 8 == 0);
   ohip_conv_desc d{g.n, g.c, g.h, g.w, g.cout, g.kh, g.kw, g.group, g.sh, g.sw, g.dh, g.dw, g.pt, g.pl, g.pb, g.pr,
-                   dt, OHIP_NCHW, OHIP_NCHW, 0, 0.0f, 0.0f, OHIP_PAD_ZEROS};
+                   dt, x_nhwc ? OHIP_NHWC : OHIP_NCHW, y_nhwc ? OHIP_NHWC : OHIP_NCHW, 0, 0.0f, 0.0f,
+                   OHIP_PAD_ZEROS};
   fused_act(nd, &d.act, &d.act_lo, &d.act_hi);
   // this provider's Pad -> Conv fusion: the pads are a reflect / edge Pad's
   {
@@ -486,6 +494,7 @@ int do_conv(ohip_ctx* ctx, const ohip_node* nd, int placement, ohip_output* out,
                         std::equal(oshape.begin(), oshape.end(), res->shape);
       if (same) {
         nm.residual = rd;
+        nm.residual_layout = res->device ? ohip_dtensor_layout(res->device) : OHIP_NCHW;
         rc = ohip_conv2d_instnorm(ctx, &d, xd, wt, bd, &nm, yd);
       } else {
         ohip::BcastPlan p{};
@@ -517,7 +526,27 @@ int do_conv(ohip_ctx* ctx, const ohip_node* nd, int placement, ohip_output* out,
   if (!cache) ohip_weight_release(wt);
   if (rc) return rc;
   set_out(out, dt, oshape);
-  return finish_output(ctx, st, placement, out, yd, obytes, dt);
+  rc = finish_output(ctx, st, placement, out, yd, obytes, dt);
+  if (rc == OHIP_OK && y_nhwc) rc = ohip_dtensor_set_nhwc_internal(out->device, g.cout);
+  return rc;
+}
+
+// Whether a float conv (or the conv of the fused conv + norm node) reads a
+// resident NHWC input in place: ungrouped, on the halo-patch path at this
+// geometry.
+bool conv_takes_nhwc(ohip_ctx* ctx, const ohip_node* nd) {
+  const ohip_tensor *x = input(nd, 0), *w = input(nd, 1);
+  if (!x || !w || !x->device || x->rank != 4) return false;
+  Geo g;
+  std::string why;
+  if (!conv_geometry(nd, x, w, &g, &why) || g.group != 1) return false;
+  if (ohip_dtensor_pitch_internal(x->device) != g.c) return false;
+  ohip_conv_desc d{g.n, g.c, g.h, g.w, g.cout, g.kh, g.kw, g.group, g.sh, g.sw, g.dh, g.dw, g.pt, g.pl, g.pb, g.pr,
+                   x->dtype, OHIP_NHWC, OHIP_NCHW, 0, 0.0f, 0.0f, OHIP_PAD_ZEROS};
+  const std::string pm = attr_s(nd, "pad_mode");
+  if (pm == "reflect") d.pad_mode = OHIP_PAD_REFLECT;
+  else if (pm == "edge") d.pad_mode = OHIP_PAD_EDGE;
+  return ohip_conv_halo_splits_internal(ctx, &d) > 0;
 }
 
 // ------------------------------------------------------------------ ConvTranspose
@@ -1788,13 +1817,25 @@ int dispatch_node(ohip_ctx* ctx, const ohip_node* node, int placement, ohip_outp
 // only): QLinearConv's X (group 1), QLinearAdd's operands when both are NHWC
 // of one shape, Concat along channels when every input is NHWC, MaxPool, and
 // Slice (a channel range is a view; anything else converts inside do_slice).
-bool takes_nhwc(const ohip_node* nd, int i, int placement) {
+bool takes_nhwc(ohip_ctx* ctx, const ohip_node* nd, int i, int placement) {
   if (placement != OHIP_PLACE_DEVICE) return false;   // host results are the NCHW lanes
   auto nhwc = [&](int k) {
     return k < nd->n_inputs && nd->inputs[k].device && ohip_dtensor_layout(nd->inputs[k].device) == OHIP_NHWC;
   };
   const std::string op(nd->op_type);
   if (op == "QLinearConv") return i == 0 && attr_i(nd, "group", 1) == 1;
+  if (op == "Conv") return i == 0 && conv_takes_nhwc(ctx, nd);
+  if (op == "OhipConvInstanceNorm") {
+    if (i == 0) return conv_takes_nhwc(ctx, nd);
+    if (i != 5 || !nhwc(5)) return false;
+    // the residual is read in place when it has the output's shape (whole 16-byte pixels)
+    const ohip_tensor *x = input(nd, 0), *w = input(nd, 1), &r = nd->inputs[5];
+    Geo g;
+    std::string why;
+    if (!x || !w || r.rank != 4 || !conv_geometry(nd, x, w, &g, &why)) return false;
+    return r.shape[0] == g.n && r.shape[1] == g.cout && r.shape[2] == g.oh && r.shape[3] == g.ow &&
+           ohip_dtensor_pitch_internal(r.device) == g.cout && g.cout % (16 / ebytes(r.dtype)) == 0;
+  }
   if (op == "Slice" || op == "MaxPool") return i == 0;
   if (op == "QLinearAdd") {
     if ((i != 0 && i != 3) || !nhwc(0) || !nhwc(3)) return false;
@@ -1834,7 +1875,7 @@ extern "C" int ohip_try_dispatch(ohip_ctx* ctx, const ohip_node* node, int place
   std::vector<ohip_dtensor*> temps;
   for (int i = 0; i < node->n_inputs; ++i) {
     const ohip_tensor& t = node->inputs[i];
-    if (!t.device || ohip_dtensor_layout(t.device) != OHIP_NHWC || takes_nhwc(node, i, placement)) continue;
+    if (!t.device || ohip_dtensor_layout(t.device) != OHIP_NHWC || takes_nhwc(ctx, node, i, placement)) continue;
     if (ins.empty()) ins.assign(node->inputs, node->inputs + node->n_inputs);
     const int64_t n = numel(&t);
     void* p = nullptr;

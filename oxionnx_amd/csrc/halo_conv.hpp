@@ -110,7 +110,14 @@ halo_conv_kernel(const HaloGeo g, const Epi epi, int nP, int nQ, int splits, int
       const int pix = slot / CC, phys = slot - pix * CC;
       const int c = phys ^ halo_swz<CC>(pix);
       const int py = pix / PW, px = pix - py * PW;
-      const int iy = oy0 + py - g.pt, ix = px - g.pl;
+      int iy = oy0 + py - g.pt, ix = px - g.pl;
+      if (g.pad_mode == 1) {          // reflect (pads below the extent; the host checks)
+        iy = iy < 0 ? -iy : (iy >= g.H ? 2 * g.H - 2 - iy : iy);
+        ix = ix < 0 ? -ix : (ix >= g.W ? 2 * g.W - 2 - ix : ix);
+      } else if (g.pad_mode == 2) {   // edge
+        iy = iy < 0 ? 0 : (iy >= g.H ? g.H - 1 : iy);
+        ix = ix < 0 ? 0 : (ix >= g.W ? g.W - 1 : ix);
+      }
       sub[i] = c;
       if (pix < npix && (unsigned)iy < (unsigned)g.H && (unsigned)ix < (unsigned)g.W)
         voff[i] = ((iy * g.W + ix) * g.pstride + c) * 16;

@@ -206,7 +206,8 @@ struct HaloGeo {
   const char* x;      // NHWC input, image 0; pixels are `pstride` 16-byte chunks apart
   int64_t img_bytes;  // bytes between images
   int H, W, OH, OW;
-  int pt, pl;         // zero padding (top, left); the patch reads zeros outside the image
+  int pt, pl;         // padding (top, left) of the patch
+  int pad_mode;       // 0: zeros outside the image; 1 / 2: reflect / edge (indices mapped into it)
   int pstride;
   int cpc;            // channel chunks per tap (the input's valid chunks and the filter's)
   int th;             // output rows per pixel tile
@@ -331,6 +332,7 @@ struct NormAffine {
   int act;             // UN_NONE / UN_RELU / UN_LEAKY_RELU
   float alpha;
   const void* residual;   // added last (an Add of a same-shape tensor of the dtype), may be null
+  int res_nhwc;           // the residual is NHWC with C elements per pixel (else NCHW)
 };
 
 struct ResizePlan {
@@ -361,14 +363,16 @@ hipError_t run_binary(int dt, const void* a, const void* b, void* y, int64_t n, 
                       hipStream_t st);
 hipError_t run_instnorm(int dt, const void* x, void* y, int64_t planes, int64_t spatial, int C, float eps,
                         const NormAffine& aff, hipStream_t st);
-// Instance normalisation of a split-K convolution's NCHW output straight from
+// Instance normalisation of a split-K convolution's output straight from
 // its partial sums (PartialEpi layout: slice s, channel c, pixel i at
 // ws[(s * C + c) * Pp + i], images one after another along i): each output
 // is the ordered slice sum + the conv bias rounded to the tensor's dtype, as
-// the split reduction stores it, then normalised as run_instnorm does.
+// the split reduction stores it, then normalised as run_instnorm does.  The
+// output is NCHW, or NHWC with C elements per pixel (out_nhwc).
 constexpr int64_t kNormPartialsMaxSpatial = 16384;
 hipError_t run_instnorm_partials(int dt, const float* ws, int splits, int64_t Pp, const void* conv_bias, void* y,
-                                 int64_t N, int64_t spatial, int C, float eps, const NormAffine& aff, hipStream_t st);
+                                 int64_t N, int64_t spatial, int C, float eps, const NormAffine& aff, bool out_nhwc,
+                                 hipStream_t st);
 hipError_t run_resize_nearest(int elem_bytes, const void* x, void* y, int64_t planes, const ResizePlan& p,
                               hipStream_t st);
 hipError_t run_pad(int elem_bytes, const void* x, void* y, int64_t n, const PadPlan& p, hipStream_t st);

@@ -141,7 +141,10 @@ __global__ void __launch_bounds__(kThreads) instnorm_kernel(const T* __restrict_
     }
     if (aff.act == UN_RELU) v = v > 0.0f ? v : 0.0f;
     else if (aff.act == UN_LEAKY_RELU) v = v >= 0.0f ? v : v * aff.alpha;
-    if (aff.residual) v = (float)(T)v + ldf(static_cast<const T*>(aff.residual) + plane * spatial, i);
+    if (aff.residual) {
+      const T* r = static_cast<const T*>(aff.residual);
+      v = (float)(T)v + (aff.res_nhwc ? ldf(r, (n * spatial + i) * C + c) : ldf(r + plane * spatial, i));
+    }
     stf(yp, i, v);
   }
 }
@@ -154,7 +157,8 @@ template <class T>
 __global__ void __launch_bounds__(kThreads) instnorm_partials_kernel(const float* __restrict__ ws, int splits,
                                                                      int64_t slice, int64_t Pp,
                                                                      const T* __restrict__ cbias, T* __restrict__ y,
-                                                                     int spatial, int C, float eps, NormAffine aff) {
+                                                                     int spatial, int C, float eps, NormAffine aff,
+                                                                     int out_nhwc) {
 #pragma clang fp contract(off)
   extern __shared__ float xs[];
   __shared__ float red[kThreads / 64];
@@ -223,8 +227,12 @@ __global__ void __launch_bounds__(kThreads) instnorm_partials_kernel(const float
     }
     if (aff.act == UN_RELU) v = v > 0.0f ? v : 0.0f;
     else if (aff.act == UN_LEAKY_RELU) v = v >= 0.0f ? v : v * aff.alpha;
-    if (aff.residual) v = (float)(T)v + (float)static_cast<const T*>(aff.residual)[plane * spatial + i];
-    yp[i] = (T)v;
+    if (aff.residual) {
+      const T* r = static_cast<const T*>(aff.residual);
+      v = (float)(T)v + (float)(aff.res_nhwc ? r[(n * spatial + i) * C + c] : r[plane * spatial + i]);
+    }
+    if (out_nhwc) y[(n * spatial + i) * C + c] = (T)v;   // channel c of each pixel (C per pixel)
+    else yp[i] = (T)v;
   }
 }
 
@@ -566,7 +574,8 @@ hipError_t run_instnorm(int dt, const void* x, void* y, int64_t planes, int64_t 
 }
 
 hipError_t run_instnorm_partials(int dt, const float* ws, int splits, int64_t Pp, const void* conv_bias, void* y,
-                                 int64_t N, int64_t spatial, int C, float eps, const NormAffine& aff, hipStream_t st) {
+                                 int64_t N, int64_t spatial, int C, float eps, const NormAffine& aff, bool out_nhwc,
+                                 hipStream_t st) {
   const int64_t planes = N * C;
   if (planes <= 0 || spatial <= 0) return hipSuccess;
   if (planes > 0x7fffffff || spatial > kNormPartialsMaxSpatial || splits < 1) return hipErrorInvalidValue;
@@ -574,10 +583,11 @@ hipError_t run_instnorm_partials(int dt, const float* ws, int splits, int64_t Pp
   const size_t shm = (size_t)spatial * sizeof(float);
   if (dt == DT_F32)
     hipLaunchKernelGGL(instnorm_partials_kernel<float>, dim3((unsigned)planes), dim3(kThreads), shm, st, ws, splits,
-                       slice, Pp, (const float*)conv_bias, (float*)y, (int)spatial, C, eps, aff);
+                       slice, Pp, (const float*)conv_bias, (float*)y, (int)spatial, C, eps, aff, (int)out_nhwc);
   else if (dt == DT_F16)
     hipLaunchKernelGGL(instnorm_partials_kernel<_Float16>, dim3((unsigned)planes), dim3(kThreads), shm, st, ws,
-                       splits, slice, Pp, (const _Float16*)conv_bias, (_Float16*)y, (int)spatial, C, eps, aff);
+                       splits, slice, Pp, (const _Float16*)conv_bias, (_Float16*)y, (int)spatial, C, eps, aff,
+                       (int)out_nhwc);
   else
     return hipErrorInvalidValue;
   return hipGetLastError();

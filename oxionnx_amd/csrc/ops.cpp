@@ -1337,7 +1337,8 @@ static int conv2d_impl(ohip_ctx* ctx, const ohip_conv_desc* d, const void* x, co
   // then writes the padded image; the convolution itself runs unpadded.
   const bool fused_pad = d->pad_mode == OHIP_PAD_REFLECT || d->pad_mode == OHIP_PAD_EDGE;
   if (d->pad_mode != OHIP_PAD_ZEROS && !fused_pad) return fail(OHIP_E_INVALID, "ohip_conv2d: pad_mode");
-  if (fused_pad && d->in_layout != OHIP_NCHW) return fail(OHIP_E_INVALID, "ohip_conv2d: a fused Pad needs an NCHW input");
+  // a fused Pad on an NHWC input is applied by the halo-patch loader (checked below)
+  const bool nhwc_pad = fused_pad && d->in_layout == OHIP_NHWC;
   if (d->pad_mode == OHIP_PAD_REFLECT &&
       ((d->h > 1 && (d->pad_t >= d->h || d->pad_b >= d->h)) || (d->w > 1 && (d->pad_l >= d->w || d->pad_r >= d->w))))
     return fail(OHIP_DECLINED, "ohip_conv2d: reflect pad wider than the image");
@@ -1371,8 +1372,11 @@ static int conv2d_impl(ohip_ctx* ctx, const ohip_conv_desc* d, const void* x, co
   // 232).  f16 / bf16 stay on the engine, which is faster there.
   const bool fewout = !direct && d->dtype == OHIP_F32 && G == 1 && d->in_layout == OHIP_NCHW &&
                       d->cout <= kFewOutMax && cg * d->kh * d->kw >= 32 && rows * d->cout >= 16384 && few_out_allowed();
-  if (norm && (direct || fewout || G != 1 || d->out_layout != OHIP_NCHW || g.oh * g.ow > kNormPartialsMaxSpatial ||
-               d->dtype == OHIP_BF16))
+  // with a norm, out_layout is the normalised output's; the contraction
+  // itself runs in the NCHW orientation (channel planes contiguous in the
+  // partial sums)
+  const bool norm_nhwc = norm && d->out_layout == OHIP_NHWC;
+  if (norm && (direct || fewout || G != 1 || g.oh * g.ow > kNormPartialsMaxSpatial || d->dtype == OHIP_BF16))
     return kNormTwoStep;
   std::lock_guard<std::mutex> lock(ctx->mu);
   ctx->counters.dispatches++;
@@ -1402,17 +1406,22 @@ static int conv2d_impl(ohip_ctx* ctx, const ohip_conv_desc* d, const void* x, co
     return OHIP_OK;
   }
 
-  const int64_t sh_ = fused_pad ? d->h + d->pad_t + d->pad_b : d->h;
-  const int64_t sw_ = fused_pad ? d->w + d->pad_l + d->pad_r : d->w;
+  // extents of the buffer the contraction reads: an NCHW input is staged
+  // with a fused Pad applied, an NHWC input is read as it is
+  const bool pad_staged = fused_pad && !nhwc_pad;
+  const int64_t sh_ = pad_staged ? d->h + d->pad_t + d->pad_b : d->h;
+  const int64_t sw_ = pad_staged ? d->w + d->pad_l + d->pad_r : d->w;
   ScratchPlan plan;
   const bool stage = d->in_layout == OHIP_NCHW;
   size_t ix = stage ? plan.add((size_t)(d->n * sh_ * sw_ * cpt) * eb) : SIZE_MAX;
-  const bool nchw_out = d->out_layout == OHIP_NCHW;
+  const bool nchw_out = norm || d->out_layout == OHIP_NCHW;
   const int sP = nchw_out ? (int)rows : (int)coutg, sQ = nchw_out ? (int)coutg : (int)rows;
   // 3x3 stride-1 convolutions whose output rows tile 256-pixel blocks run
   // the halo-patch kernel (the input patch staged once per channel slab for
   // all nine taps) instead of the engine's im2col gather.
   const int hsplits = halo_plan(ctx, d, G, sw_, g, (int)(cp / ce), (int64_t)(sh_ * sw_ * cpt * eb));
+  if (nhwc_pad && !hsplits)
+    return fail(OHIP_DECLINED, "ohip_conv2d: a reflect / edge Pad on an NHWC input needs the halo-patch path");
   const SplitChoice sc = hsplits ? SplitChoice{hsplits, 0}
                                  : plan_split_tile(sP, sQ, (int)(d->kh * d->kw * (cp / ce)), ctx->tile_override,
                                                    d->dtype == OHIP_F32);
@@ -1451,7 +1460,8 @@ static int conv2d_impl(ohip_ctx* ctx, const ohip_conv_desc* d, const void* x, co
     hg.x = static_cast<const char*>(xin);
     hg.img_bytes = sh_ * sw_ * cpt * eb;
     hg.H = (int)sh_; hg.W = (int)sw_; hg.OH = (int)g.oh; hg.OW = (int)g.ow;
-    hg.pt = fused_pad ? 0 : (int)d->pad_t; hg.pl = fused_pad ? 0 : (int)d->pad_l;
+    hg.pt = pad_staged ? 0 : (int)d->pad_t; hg.pl = pad_staged ? 0 : (int)d->pad_l;
+    hg.pad_mode = nhwc_pad ? d->pad_mode : 0;
     hg.pstride = (int)(cpt / ce); hg.cpc = (int)(cp / ce);
     hg.th = kHaloBPix / (int)g.ow;
     hg.ow_shift = 0;
@@ -1478,8 +1488,8 @@ static int conv2d_impl(ohip_ctx* ctx, const ohip_conv_desc* d, const void* x, co
     hipError_t e = run_halo_float(d->dtype, hg, nchw_out, o, ctx->stream);
     if (e != hipSuccess) return hip_fail(e, "ohip_conv2d halo launch");
     if (norm) {
-      e = run_instnorm_partials(d->dtype, static_cast<const float*>(o.split_ws), splits, (rows + 3) / 4 * 4, bias, y,
-                                d->n, ohw, (int)d->cout, norm->eps, norm->aff, ctx->stream);
+      e = run_instnorm_partials(d->dtype, static_cast<const float*>(o.split_ws), splits, (rows + 3) / 4 * 4, bias,
+                                y, d->n, ohw, (int)d->cout, norm->eps, norm->aff, norm_nhwc, ctx->stream);
       if (e != hipSuccess) return hip_fail(e, "ohip_conv2d_instnorm launch");
     }
     return OHIP_OK;
@@ -1536,8 +1546,8 @@ static int conv2d_impl(ohip_ctx* ctx, const ohip_conv_desc* d, const void* x, co
     hipError_t e = run_conv_float(d->dtype, col, wt, col_on_x, o, sc.tile, ctx->stream);
     if (e != hipSuccess) return hip_fail(e, "ohip_conv2d launch");
     if (norm) {
-      e = run_instnorm_partials(d->dtype, static_cast<const float*>(o.split_ws), splits, (rows + 3) / 4 * 4, bias, y,
-                                d->n, ohw, (int)d->cout, norm->eps, norm->aff, ctx->stream);
+      e = run_instnorm_partials(d->dtype, static_cast<const float*>(o.split_ws), splits, (rows + 3) / 4 * 4, bias,
+                                y, d->n, ohw, (int)d->cout, norm->eps, norm->aff, norm_nhwc, ctx->stream);
       if (e != hipSuccess) return hip_fail(e, "ohip_conv2d_instnorm launch");
     }
   }
@@ -1549,6 +1559,20 @@ extern "C" int ohip_conv2d(ohip_ctx* ctx, const ohip_conv_desc* d, const void* x
   return conv2d_impl(ctx, d, x, w, bias, y, false);
 }
 
+// The halo-patch split count an ungrouped convolution of a resident NHWC
+// input would run with (0: not on the halo path), for the dispatcher's
+// layout choices.
+int ohip_conv_halo_splits_internal(ohip_ctx* ctx, const ohip_conv_desc* d) {
+  if (!ctx || !d || d->group != 1 || !is_float(d->dtype)) return 0;
+  ConvGeo g;
+  if (conv_geo(d->h, d->w, d->kh, d->kw, d->stride_h, d->stride_w, d->dil_h, d->dil_w, d->pad_t, d->pad_l, d->pad_b,
+               d->pad_r, &g) != OHIP_OK)
+    return 0;
+  const int eb = elem_bytes(d->dtype), ce = 16 / eb;
+  const int64_t cp = round_up(d->c, ce);
+  return halo_plan(ctx, d, 1, d->w, g, (int)(cp / ce), d->h * d->w * cp * eb);
+}
+
 // Conv -> instance normalisation.  With a split-K plan the normalisation
 // reads the partial sums (one launch fewer, no conv output round trip);
 // otherwise the conv writes a pooled temporary that the normalisation reads.
@@ -1558,7 +1582,8 @@ extern "C" int ohip_conv2d_instnorm(ohip_ctx* ctx, const ohip_conv_desc* d, cons
   if (rc) return rc;
   if (!d || !nd || !y) return fail(OHIP_E_INVALID, "ohip_conv2d_instnorm: null argument");
   if (d->act != OHIP_ACT_NONE) return fail(OHIP_E_INVALID, "ohip_conv2d_instnorm: the conv must have no activation");
-  if (d->out_layout != OHIP_NCHW) return fail(OHIP_E_INVALID, "ohip_conv2d_instnorm: NCHW output only");
+  if (d->out_layout == OHIP_NHWC && d->cout % (16 / elem_bytes(d->dtype)))
+    return fail(OHIP_E_INVALID, "ohip_conv2d_instnorm: an NHWC output needs whole 16-byte pixels");
   if (d->dtype != OHIP_F32 && d->dtype != OHIP_F16) return fail(OHIP_DECLINED, "ohip_conv2d_instnorm: f32 / f16 only");
   if (nd->act != OHIP_ACT_NONE && nd->act != OHIP_ACT_RELU && nd->act != OHIP_ACT_LEAKY_RELU)
     return fail(OHIP_E_INVALID, "ohip_conv2d_instnorm: activation");
@@ -1569,23 +1594,40 @@ extern "C" int ohip_conv2d_instnorm(ohip_ctx* ctx, const ohip_conv_desc* d, cons
   cn.aff.act = nd->act == OHIP_ACT_RELU ? UN_RELU : nd->act == OHIP_ACT_LEAKY_RELU ? UN_LEAKY_RELU : UN_IDENTITY;
   cn.aff.alpha = nd->alpha;
   cn.aff.residual = nd->residual;
+  cn.aff.res_nhwc = nd->residual && nd->residual_layout == OHIP_NHWC;
+  if (cn.aff.res_nhwc && d->cout % (16 / elem_bytes(d->dtype)))
+    return fail(OHIP_E_INVALID, "ohip_conv2d_instnorm: an NHWC residual needs whole 16-byte pixels");
   rc = conv2d_impl(ctx, d, x, w, bias, y, false, &cn);
   if (rc != kNormTwoStep) return rc;
+  // two steps: the conv (NCHW) into a pooled temporary, the normalisation
+  // from it (NCHW), and for an NHWC output a transpose of that
   ConvGeo g;
   rc = conv_geo(d->h, d->w, d->kh, d->kw, d->stride_h, d->stride_w, d->dil_h, d->dil_w, d->pad_t, d->pad_l, d->pad_b,
                 d->pad_r, &g);
   if (rc) return rc;
   const int64_t spatial = g.oh * g.ow;
+  const size_t bytes = (size_t)(d->n * d->cout * spatial) * elem_bytes(d->dtype);
+  const bool to_nhwc = d->out_layout == OHIP_NHWC;
   void* tmp = nullptr;
-  rc = pool_alloc(ctx, (size_t)(d->n * d->cout * spatial) * elem_bytes(d->dtype), &tmp);
-  if (rc) return rc;
-  rc = conv2d_impl(ctx, d, x, w, bias, tmp, false, nullptr);
-  if (rc == OHIP_OK) {
-    hipError_t e = run_instnorm(d->dtype, tmp, y, d->n * d->cout, spatial, (int)d->cout, cn.eps, cn.aff, ctx->stream);
+  void* tmp2 = nullptr;
+  rc = pool_alloc(ctx, bytes, &tmp);
+  if (!rc && to_nhwc) rc = pool_alloc(ctx, bytes, &tmp2);
+  if (!rc) {
+    ohip_conv_desc dc = *d;
+    dc.out_layout = OHIP_NCHW;
+    rc = conv2d_impl(ctx, &dc, x, w, bias, tmp, false, nullptr);
+  }
+  if (!rc) {
+    hipError_t e = run_instnorm(d->dtype, tmp, to_nhwc ? tmp2 : y, d->n * d->cout, spatial, (int)d->cout, cn.eps,
+                                cn.aff, ctx->stream);
+    if (e == hipSuccess && to_nhwc)
+      e = run_nchw_to_nhwc(elem_bytes(d->dtype), tmp2, y, (int)d->n, (int)d->cout, (int)spatial, (int)d->cout,
+                           ctx->stream);
     if (e != hipSuccess) rc = hip_fail(e, "ohip_conv2d_instnorm: normalisation launch");
   }
   const int rf = pool_free(ctx, tmp);
-  return rc ? rc : rf;
+  const int rf2 = pool_free(ctx, tmp2);
+  return rc ? rc : (rf ? rf : rf2);
 }
 
 // Same kernels as ohip_conv2d; the staging copy and the split-K partial sums

@@ -74,7 +74,7 @@ def _scalar(inits, name):
     return float(a[0]) if a.size == 1 else None
 
 
-def fuse(graph: Graph, level: str = "all") -> Graph:
+def fuse(graph: Graph, level: str = "all", nhwc: bool = True) -> Graph:
     """level "all": every fusion below; level "reference": only the fusion the
     reference's own optimizer produces for these graphs, Conv followed by its
     only consumer Relu (registry/conv_ops/conv.rs:124-156)."""
@@ -155,7 +155,59 @@ def fuse(graph: Graph, level: str = "all") -> Graph:
         nodes = [n for n in nodes if n is not None] if changed else nodes
     if not ref_only:
         nodes = _fuse_conv_instnorm(nodes, keep_out, inits)
+        if nhwc:
+            nodes = _plan_nhwc(_drop_dead(nodes, keep_out), keep_out, inits)
     return replace(graph, nodes=_drop_dead(nodes, keep_out), initializers=inits)
+
+
+def _halo_candidate(node, inits):
+    """A conv the device can run on its halo-patch path with a resident NHWC
+    input: 3x3, stride and dilation 1, ungrouped, an f16 / bf16 filter (the
+    output extent is checked by the dispatcher, which converts otherwise)."""
+    if node.op not in ("Conv", "OhipConvInstanceNorm"):
+        return False
+    a = node.attrs
+    if a.ints.get("group", 1) != 1 or list(a.int_lists.get("kernel_shape", [3, 3])) != [3, 3]:
+        return False
+    if any(v != 1 for v in a.int_lists.get("strides", [1, 1])) or any(v != 1 for v in a.int_lists.get("dilations", [1, 1])):
+        return False
+    w = inits.get(node.inputs[1]) if len(node.inputs) > 1 else None
+    if w is None:
+        return False
+    wd = np.asarray(w.data if isinstance(w, ep.Typed) else w)
+    return wd.ndim == 4 and wd.shape[2:] == (3, 3) and wd.dtype == np.float16
+
+
+def _plan_nhwc(nodes, keep_out, inits):
+    """Layout hints for float activations: a Conv / OhipConvInstanceNorm
+    output whose every consumer reads it in place as NHWC (the input of a
+    halo-path conv, or the residual of a fused node that has the same
+    shape) is produced NHWC ("out_nhwc"), which removes the consumers' NCHW
+    -> NHWC staging.  The dispatcher treats the hint as a preference and
+    converts for any consumer that cannot take the layout."""
+    cons = _consumers(nodes)
+    out = list(nodes)
+    for i, n in enumerate(out):
+        if n.op not in ("Conv", "OhipConvInstanceNorm") or n.attrs.ints.get("group", 1) != 1:
+            continue
+        t = n.outputs[0]
+        users = cons.get(t, [])
+        if t in keep_out or not users:
+            continue
+        ok = True
+        for u in users:
+            un = out[u]
+            if un.inputs and un.inputs[0] == t and _halo_candidate(un, inits) and t not in un.inputs[1:5]:
+                continue
+            if un.op == "OhipConvInstanceNorm" and len(un.inputs) > 5 and un.inputs[5] == t and un.inputs[0] != t:
+                continue
+            ok = False
+            break
+        if ok:
+            a = replace(n.attrs, ints=dict(n.attrs.ints))
+            a.ints["out_nhwc"] = 1
+            out[i] = replace(n, attrs=a)
+    return out
 
 
 def _fuse_conv_instnorm(nodes, keep_out, inits):
@@ -427,9 +479,10 @@ def _fuse_adain(nodes, i, sole, inits):
 class Session:
     """Runs a Graph on one HipContext with resident activations."""
 
-    def __init__(self, graph: Graph, ctx: ep.HipContext, optimize=True, cpu_ops=None):
+    def __init__(self, graph: Graph, ctx: ep.HipContext, optimize=True, cpu_ops=None, nhwc=True):
         """optimize: True (every fusion), "reference" (only the reference
-        optimizer's Conv + Relu) or False.  cpu_ops(node, inputs) -> list of
+        optimizer's Conv + Relu) or False; nhwc: with every fusion, the NHWC
+        layout hints for float activations (False keeps them NCHW).  cpu_ops(node, inputs) -> list of
         host arrays: the host's operators for nodes the provider does not
         claim (inputs are host arrays, initializers included; '' slots are
         None)."""
@@ -437,7 +490,7 @@ class Session:
         if optimize == "reference":
             self.graph = fuse(graph, level="reference")
         else:
-            self.graph = fuse(graph) if optimize else graph
+            self.graph = fuse(graph, nhwc=nhwc) if optimize else graph
         self.ctx = ctx
         outs = set(self.graph.outputs)
         self.last_use = {}

@@ -574,3 +574,16 @@ def test_conv_instnorm_fusion_matches_unfused(ctx, case):
     np.testing.assert_array_equal(got, want)
     ref = G.run_graph(g, feeds, half=(dt == "f16"))["y"]
     close(got, ref, 1e-2 if dt == "f16" else 1e-4)
+
+
+def test_face_swap_nhwc_trunk_matches_nchw(ctx):
+    """The residual trunk kept NHWC between its convolutions (halo-patch convs
+    reading the reflect pad in place, norms writing NHWC) gives the same bits
+    as the NCHW forward with its staging transposes."""
+    g, feeds = workloads.face_swap_generator(dtype="f16", n_blocks=2)
+    nhwc = Session(g, ctx)
+    assert sum(1 for n in nhwc.graph.nodes if n.attrs.ints.get("out_nhwc")) >= 3
+    got = nhwc.run(feeds)
+    want = Session(g, ctx, nhwc=False).run(feeds)
+    for k in ("logits", "y"):
+        np.testing.assert_array_equal(got[k], want[k], err_msg=k)
