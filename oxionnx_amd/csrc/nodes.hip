@@ -7,6 +7,7 @@
 // Float tensors are f32 or f16 storage with f32 arithmetic; quantised
 // tensors are u8 / i8 bytes.
 #include <hip/hip_runtime.h>
+#include <type_traits>
 #include <stdint.h>
 
 #include "internal.hpp"
@@ -153,25 +154,47 @@ __global__ void __launch_bounds__(kThreads) instnorm_kernel(const T* __restrict_
 // LDS: x_i = T(sum over slices in slice order + bias), the value the split
 // reduction would have stored; the three passes then read LDS instead of
 // global memory, in the same order, so the result is the unfused pair's.
-template <class T>
-__global__ void __launch_bounds__(kThreads) instnorm_partials_kernel(const float* __restrict__ ws, int splits,
-                                                                     int64_t slice, int64_t Pp,
-                                                                     const T* __restrict__ cbias, T* __restrict__ y,
-                                                                     int spatial, int C, float eps, NormAffine aff,
-                                                                     int out_nhwc) {
+// PPB planes (channels of one image) per block, 256 threads each with its
+// own reduction slots, so every plane's statistics are the 256-thread
+// block's above; with PPB > 1 (an NHWC output) each pixel's PPB channels
+// are written (and a residual read) as one run.
+template <int PPB>
+__device__ __forceinline__ float group_sum(float v, float* red, int g) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
+  const int lane = threadIdx.x & 63, wave = (threadIdx.x >> 6) & 3;
+  __syncthreads();
+  if (lane == 0) red[4 * g + wave] = v;
+  __syncthreads();
+  float s = 0.0f;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) s += red[4 * g + w];
+  return s;
+}
+
+template <class T, int PPB>
+__global__ void __launch_bounds__(kThreads * PPB) instnorm_partials_kernel(const float* __restrict__ ws, int splits,
+                                                                           int64_t slice, int64_t Pp,
+                                                                           const T* __restrict__ cbias,
+                                                                           T* __restrict__ y, int spatial, int C,
+                                                                           float eps, NormAffine aff, int out_nhwc) {
 #pragma clang fp contract(off)
-  extern __shared__ float xs[];
-  __shared__ float red[kThreads / 64];
-  const int64_t plane = blockIdx.x;
-  const int c = (int)(plane % C);
-  const int64_t n = plane / C;
+  static_assert(kThreads == 256, "256 threads a plane");
+  extern __shared__ float xs_all[];        // PPB planes of `spatial` values
+  __shared__ float red[4 * PPB];
+  const int g = threadIdx.x >> 8, lt = threadIdx.x & 255;
+  const int groups = C / PPB;
+  const int64_t n = blockIdx.x / groups;
+  const int c0 = (int)(blockIdx.x % groups) * PPB, c = c0 + g;
+  const int64_t plane = n * C + c;
+  float* xs = xs_all + g * spatial;
   const float* src = ws + (int64_t)c * Pp + n * spatial;
   const float b = cbias ? (float)cbias[c] : -0.0f;
   if ((spatial & 3) == 0 && ((uintptr_t)src & 15) == 0 && (slice & 3) == 0) {
     // four pixels a thread, 16-byte loads, up to four slices in flight; the
     // adds stay in slice order
     typedef float f4 __attribute__((ext_vector_type(4)));
-    for (int i = 4 * threadIdx.x; i < spatial; i += 4 * kThreads) {
+    for (int i = 4 * lt; i < spatial; i += 4 * kThreads) {
       f4 acc = *reinterpret_cast<const f4*>(src + i);
       int s = 1;
       for (; s + 4 <= splits; s += 4) {
@@ -189,23 +212,22 @@ __global__ void __launch_bounds__(kThreads) instnorm_partials_kernel(const float
       }
     }
   } else {
-    for (int i = threadIdx.x; i < spatial; i += kThreads) {
+    for (int i = lt; i < spatial; i += kThreads) {
       float acc = src[i];
       for (int s = 1; s < splits; ++s) acc += src[s * slice + i];
       xs[i] = (float)(T)(acc + b);
     }
   }
   __syncthreads();
-  T* yp = y + plane * spatial;
   float s = 0.0f;
-  for (int i = threadIdx.x; i < spatial; i += kThreads) s += xs[i];
-  const float mean = block_sum(s, red) / (float)spatial;
+  for (int i = lt; i < spatial; i += kThreads) s += xs[i];
+  const float mean = group_sum<PPB>(s, red, g) / (float)spatial;
   float q = 0.0f;
-  for (int i = threadIdx.x; i < spatial; i += kThreads) {
+  for (int i = lt; i < spatial; i += kThreads) {
     const float d = xs[i] - mean;
     q += d * d;
   }
-  const float var = block_sum(q, red) / (float)spatial;
+  const float var = group_sum<PPB>(q, red, g) / (float)spatial;
   const float inv = 1.0f / sqrtf(var + eps);
   float sc = 1.0f, bi = 0.0f;
   bool affine = false;
@@ -218,7 +240,9 @@ __global__ void __launch_bounds__(kThreads) instnorm_partials_kernel(const float
     bi = aff.same_type ? (float)static_cast<const T*>(aff.bias)[ai] : static_cast<const float*>(aff.bias)[ai];
     affine = true;
   }
-  for (int i = threadIdx.x; i < spatial; i += kThreads) {
+  const T* res = static_cast<const T*>(aff.residual);
+  T* yp = y + plane * spatial;
+  for (int i = lt; i < spatial; i += kThreads) {
     float v = (xs[i] - mean) * inv;
     if (affine) {
       v = (float)(T)v;
@@ -227,12 +251,52 @@ __global__ void __launch_bounds__(kThreads) instnorm_partials_kernel(const float
     }
     if (aff.act == UN_RELU) v = v > 0.0f ? v : 0.0f;
     else if (aff.act == UN_LEAKY_RELU) v = v >= 0.0f ? v : v * aff.alpha;
-    if (aff.residual) {
-      const T* r = static_cast<const T*>(aff.residual);
-      v = (float)(T)v + (float)(aff.res_nhwc ? r[(n * spatial + i) * C + c] : r[plane * spatial + i]);
+    if constexpr (PPB == 1) {
+      if (res) v = (float)(T)v + (float)(aff.res_nhwc ? res[(n * spatial + i) * C + c] : res[plane * spatial + i]);
+      if (out_nhwc) y[(n * spatial + i) * C + c] = (T)v;   // channel c of each pixel (C per pixel)
+      else yp[i] = (T)v;
+    } else {
+      xs[i] = (float)(T)v;   // the stored value; the residual is added below, per run
     }
-    if (out_nhwc) y[(n * spatial + i) * C + c] = (T)v;   // channel c of each pixel (C per pixel)
-    else yp[i] = (T)v;
+  }
+  if constexpr (PPB > 1) {
+    __syncthreads();
+    // each pixel's PPB channels as one run (NHWC output, C per pixel)
+    constexpr int kBytes = PPB * (int)sizeof(T);
+    using Run = typename std::conditional<kBytes % 16 == 0, uint4,
+                typename std::conditional<kBytes % 8 == 0, uint2, uint32_t>::type>::type;
+    constexpr int kRuns = kBytes / (int)sizeof(Run);
+    for (int i = threadIdx.x; i < spatial; i += kThreads * PPB) {
+      const int64_t pix = n * spatial + i;
+      T r[PPB];
+      if (res) {
+        if (aff.res_nhwc) {
+          const Run* rp = reinterpret_cast<const Run*>(res + pix * C + c0);
+#pragma unroll
+          for (int k = 0; k < kRuns; ++k) {
+            const Run w = rp[k];
+            __builtin_memcpy(reinterpret_cast<char*>(r) + sizeof(Run) * k, &w, sizeof(Run));
+          }
+        } else {
+#pragma unroll
+          for (int k = 0; k < PPB; ++k) r[k] = res[(n * C + c0 + k) * (int64_t)spatial + i];
+        }
+      }
+      T o[PPB];
+#pragma unroll
+      for (int k = 0; k < PPB; ++k) {
+        float v = xs_all[k * spatial + i];
+        if (res) v = v + (float)r[k];
+        o[k] = (T)v;
+      }
+      Run* dp = reinterpret_cast<Run*>(y + pix * C + c0);
+#pragma unroll
+      for (int k = 0; k < kRuns; ++k) {
+        Run w;
+        __builtin_memcpy(&w, reinterpret_cast<const char*>(o) + sizeof(Run) * k, sizeof(Run));
+        dp[k] = w;
+      }
+    }
   }
 }
 
@@ -580,12 +644,31 @@ hipError_t run_instnorm_partials(int dt, const float* ws, int splits, int64_t Pp
   if (planes <= 0 || spatial <= 0) return hipSuccess;
   if (planes > 0x7fffffff || spatial > kNormPartialsMaxSpatial || splits < 1) return hipErrorInvalidValue;
   const int64_t slice = (int64_t)C * Pp;
+  // an NHWC output takes four channels a block (8- / 16-byte runs per pixel)
+  constexpr int PPB = 4;
+  const bool wide = out_nhwc && C % PPB == 0 && (size_t)PPB * spatial * sizeof(float) <= 64 * 1024 &&
+                    (uintptr_t)y % (PPB * (dt == DT_F32 ? 4 : 2)) == 0 &&
+                    (!aff.residual || !aff.res_nhwc || (uintptr_t)aff.residual % (PPB * (dt == DT_F32 ? 4 : 2)) == 0);
+  if (wide) {
+    const size_t shm = (size_t)PPB * spatial * sizeof(float);
+    const unsigned blocks = (unsigned)(planes / PPB);
+    if (dt == DT_F32)
+      hipLaunchKernelGGL((instnorm_partials_kernel<float, PPB>), dim3(blocks), dim3(kThreads * PPB), shm, st, ws,
+                         splits, slice, Pp, (const float*)conv_bias, (float*)y, (int)spatial, C, eps, aff, 1);
+    else if (dt == DT_F16)
+      hipLaunchKernelGGL((instnorm_partials_kernel<_Float16, PPB>), dim3(blocks), dim3(kThreads * PPB), shm, st, ws,
+                         splits, slice, Pp, (const _Float16*)conv_bias, (_Float16*)y, (int)spatial, C, eps, aff, 1);
+    else
+      return hipErrorInvalidValue;
+    return hipGetLastError();
+  }
   const size_t shm = (size_t)spatial * sizeof(float);
   if (dt == DT_F32)
-    hipLaunchKernelGGL(instnorm_partials_kernel<float>, dim3((unsigned)planes), dim3(kThreads), shm, st, ws, splits,
-                       slice, Pp, (const float*)conv_bias, (float*)y, (int)spatial, C, eps, aff, (int)out_nhwc);
+    hipLaunchKernelGGL((instnorm_partials_kernel<float, 1>), dim3((unsigned)planes), dim3(kThreads), shm, st, ws,
+                       splits, slice, Pp, (const float*)conv_bias, (float*)y, (int)spatial, C, eps, aff,
+                       (int)out_nhwc);
   else if (dt == DT_F16)
-    hipLaunchKernelGGL(instnorm_partials_kernel<_Float16>, dim3((unsigned)planes), dim3(kThreads), shm, st, ws,
+    hipLaunchKernelGGL((instnorm_partials_kernel<_Float16, 1>), dim3((unsigned)planes), dim3(kThreads), shm, st, ws,
                        splits, slice, Pp, (const _Float16*)conv_bias, (_Float16*)y, (int)spatial, C, eps, aff,
                        (int)out_nhwc);
   else
