@@ -42,6 +42,9 @@ def parse():
     p.add_argument("--settle-ms", type=float, default=100.0,
                    help="GPU time of headline launches run before the warm-up steps, so that the timed "
                         "steps see the clock the GPU settles at under this load, not its idle ramp")
+    p.add_argument("--e2e-fused-only", action="store_true",
+                   help="end-to-end items: skip the reference-fusions-only forwards (a kernel trace then holds "
+                        "only the provider's fused graph)")
     p.add_argument("--only", default="", help="run one item (for profiling): 'headline', 'copy', "
                    "'conv_f32_cfg1', 'int8_ffn', or a sweep item such as 'gemm_f16_2048x4096x4096'")
     return p.parse_args()
@@ -202,7 +205,7 @@ def main():
             extras.update(bench_int8(torch, ctx, L, stream, rng, args.only))
             extras.update(bench_large(torch, ctx, L, stream, rng, args.only))
             extras.update(bench_widened(torch, ctx, L, stream, rng, args.only))
-            extras.update(bench_e2e(torch, ctx, stream, args.only, args.no_cpu))
+            extras.update(bench_e2e(torch, ctx, stream, args.only, args.no_cpu, args.e2e_fused_only))
             extras.update(bench_gate(torch, ctx, L, args.only))
 
     line = {
@@ -443,7 +446,7 @@ def _time_forwards(torch, stream, fwd, n=10):
     return round(float(np.median(walls)), 3), round(float(np.median(gpus)), 3)
 
 
-def bench_e2e(torch, ctx, stream, only, no_cpu):
+def bench_e2e(torch, ctx, stream, only, no_cpu, fused_only=False):
     """Configs 4 and 5 end to end, median of 10 forwards each:
     * the session run loop (graph inputs uploaded, every node dispatched
       through ohip_try_dispatch, outputs downloaded);
@@ -472,16 +475,18 @@ def bench_e2e(torch, ctx, stream, only, no_cpu):
         cap.close()
         # the same graph with only the fusion the reference's optimizer makes
         # (Conv + Relu): every other node runs as its own device kernel
-        rsess = Session(g, ctx, optimize="reference")
-        rloop = _time_forwards(torch, stream, lambda: rsess.run(feeds))
-        rcap = rsess.capture(feeds)
-        rgraph = _time_forwards(torch, stream, lambda: rcap.replay(feeds))
-        rcap.close()
         rec = {"ms_per_forward": graph[0], "ms_per_forward_run_loop": loop[0],
                "stream_ms_graph": graph[1], "stream_ms_run_loop": loop[1],
-               "stream_ms_graph_io_resident": resident[1],
-               "reference_fusions_only": {"ms_per_forward": rgraph[0], "ms_per_forward_run_loop": rloop[0],
-                                          "stream_ms_graph": rgraph[1], "nodes": len(rsess.graph.nodes)},
+               "stream_ms_graph_io_resident": resident[1]}
+        if not fused_only:
+            rsess = Session(g, ctx, optimize="reference")
+            rloop = _time_forwards(torch, stream, lambda: rsess.run(feeds))
+            rcap = rsess.capture(feeds)
+            rgraph = _time_forwards(torch, stream, lambda: rcap.replay(feeds))
+            rcap.close()
+            rec["reference_fusions_only"] = {"ms_per_forward": rgraph[0], "ms_per_forward_run_loop": rloop[0],
+                                             "stream_ms_graph": rgraph[1], "nodes": len(rsess.graph.nodes)}
+        rec.update({
                "nodes": len(g.nodes), "nodes_after_fusion": len(sess.graph.nodes),
                "conv_gmac": round(g.notes["conv_gmac"], 3),
                "note": "ms_per_forward: wall clock of one forward replayed from its captured HIP graph, incl. "
@@ -489,7 +494,7 @@ def bench_e2e(torch, ctx, stream, only, no_cpu):
                        "already on the device and its outputs left there; ms_per_forward_run_loop: the same forward "
                        "dispatched node by node through the Python run loop; reference_fusions_only: the "
                        "graph with only the reference optimizer's Conv+Relu fusion (no provider-side "
-                       "rewrites)"}
+                       "rewrites)"})
         if not no_cpu and not only:
             from oracle import graph_ref
             t0 = time.perf_counter()
@@ -506,7 +511,8 @@ def bench_e2e(torch, ctx, stream, only, no_cpu):
                     "not that kernel)")}
             rec["speedup_vs_cpu"] = round(cpu / rec["ms_per_forward"], 1)
             rec["speedup_vs_cpu_run_loop"] = round(cpu / rec["ms_per_forward_run_loop"], 1)
-            rec["speedup_vs_cpu_reference_fusions_only"] = round(cpu / rgraph[0], 1)
+            if not fused_only:
+                rec["speedup_vs_cpu_reference_fusions_only"] = round(cpu / rgraph[0], 1)
         out[key] = rec
     return out
 
