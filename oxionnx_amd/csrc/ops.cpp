@@ -1369,7 +1369,8 @@ static int conv2d_impl(ohip_ctx* ctx, const ohip_conv_desc* d, const void* x, co
   // sliver of an f32 MFMA tile (f32 MFMA runs at a sixteenth of the f16
   // rate): the few-output kernel stages input patches in LDS and reduces over
   // channel slices instead (128 -> 3 channels, 7x7, 128x128: 50 us against
-  // 232).  f16 / bf16 stay on the engine, which is faster there.
+  // 232).  f16 / bf16 stay on the engine, which is faster there (the same
+  // head in f16: 42.7 us on the engine, 55.5 us few-output).
   const bool fewout = !direct && d->dtype == OHIP_F32 && G == 1 && d->in_layout == OHIP_NCHW &&
                       d->cout <= kFewOutMax && cg * d->kh * d->kw >= 32 && rows * d->cout >= 16384 && few_out_allowed();
   // with a norm, out_layout is the normalised output's; the contraction
