@@ -190,6 +190,29 @@ __global__ void __launch_bounds__(kThreads * PPB) instnorm_partials_kernel(const
   float* xs = xs_all + g * spatial;
   const float* src = ws + (int64_t)c * Pp + n * spatial;
   const float b = cbias ? (float)cbias[c] : -0.0f;
+  // Loads the epilogue needs are issued here, so their round trip overlaps
+  // the partial-sum reads instead of following the statistics: the affine
+  // terms and, for an NHWC output, this thread's first residual run.
+  const int64_t ai = aff.per_sample ? n * aff.stride + c : c;
+  float sc = 1.0f, bi = 0.0f;
+  if (aff.scale)
+    sc = aff.same_type ? (float)static_cast<const T*>(aff.scale)[ai] : static_cast<const float*>(aff.scale)[ai];
+  if (aff.bias)
+    bi = aff.same_type ? (float)static_cast<const T*>(aff.bias)[ai] : static_cast<const float*>(aff.bias)[ai];
+  const T* res = static_cast<const T*>(aff.residual);
+  constexpr int kRunBytes = PPB * (int)sizeof(T);
+  using Run = typename std::conditional<kRunBytes % 16 == 0, uint4,
+              typename std::conditional<kRunBytes % 8 == 0, uint2, uint32_t>::type>::type;
+  constexpr int kRuns = kRunBytes / (int)sizeof(Run) > 0 ? kRunBytes / (int)sizeof(Run) : 1;
+  Run r0[kRuns];
+  const bool pre = PPB > 1 && res && aff.res_nhwc && (int)threadIdx.x < spatial;
+  if constexpr (PPB > 1) {
+    if (pre) {
+      const Run* rp = reinterpret_cast<const Run*>(res + (n * spatial + threadIdx.x) * C + c0);
+#pragma unroll
+      for (int k = 0; k < kRuns; ++k) r0[k] = rp[k];
+    }
+  }
   if ((spatial & 3) == 0 && ((uintptr_t)src & 15) == 0 && (slice & 3) == 0) {
     // four pixels a thread, 16-byte loads, up to four slices in flight; the
     // adds stay in slice order
@@ -229,18 +252,7 @@ __global__ void __launch_bounds__(kThreads * PPB) instnorm_partials_kernel(const
   }
   const float var = group_sum<PPB>(q, red, g) / (float)spatial;
   const float inv = 1.0f / sqrtf(var + eps);
-  float sc = 1.0f, bi = 0.0f;
-  bool affine = false;
-  const int64_t ai = aff.per_sample ? n * aff.stride + c : c;
-  if (aff.scale) {
-    sc = aff.same_type ? (float)static_cast<const T*>(aff.scale)[ai] : static_cast<const float*>(aff.scale)[ai];
-    affine = true;
-  }
-  if (aff.bias) {
-    bi = aff.same_type ? (float)static_cast<const T*>(aff.bias)[ai] : static_cast<const float*>(aff.bias)[ai];
-    affine = true;
-  }
-  const T* res = static_cast<const T*>(aff.residual);
+  const bool affine = aff.scale || aff.bias;
   T* yp = y + plane * spatial;
   for (int i = lt; i < spatial; i += kThreads) {
     float v = (xs[i] - mean) * inv;
@@ -262,21 +274,21 @@ __global__ void __launch_bounds__(kThreads * PPB) instnorm_partials_kernel(const
   if constexpr (PPB > 1) {
     __syncthreads();
     // each pixel's PPB channels as one run (NHWC output, C per pixel)
-    constexpr int kBytes = PPB * (int)sizeof(T);
-    using Run = typename std::conditional<kBytes % 16 == 0, uint4,
-                typename std::conditional<kBytes % 8 == 0, uint2, uint32_t>::type>::type;
-    constexpr int kRuns = kBytes / (int)sizeof(Run);
     for (int i = threadIdx.x; i < spatial; i += kThreads * PPB) {
       const int64_t pix = n * spatial + i;
       T r[PPB];
       if (res) {
         if (aff.res_nhwc) {
           const Run* rp = reinterpret_cast<const Run*>(res + pix * C + c0);
+          Run w[kRuns];
+          if (i == (int)threadIdx.x) {   // the run loaded up front
 #pragma unroll
-          for (int k = 0; k < kRuns; ++k) {
-            const Run w = rp[k];
-            __builtin_memcpy(reinterpret_cast<char*>(r) + sizeof(Run) * k, &w, sizeof(Run));
+            for (int k = 0; k < kRuns; ++k) w[k] = r0[k];
+          } else {
+#pragma unroll
+            for (int k = 0; k < kRuns; ++k) w[k] = rp[k];
           }
+          __builtin_memcpy(r, w, sizeof(w));
         } else {
 #pragma unroll
           for (int k = 0; k < PPB; ++k) r[k] = res[(n * C + c0 + k) * (int64_t)spatial + i];
