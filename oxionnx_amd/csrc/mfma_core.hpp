@@ -430,7 +430,7 @@ extern __device__ uint64_t ohip_ktime[8 * 65536];
 // K loop's loads have landed).  Shared by every contraction kernel.
 template <Op O, class Tl, class Epi, class A>
 __device__ __forceinline__ void tile_epilogue(const Epi& epi, A (&acc)[Tl::TP][Tl::TQ], u32x4* smem, int p0, int q0,
-                                              int wp, int wq, int lane, int t) {
+                                              int wp, int wq, int lane, int t, bool rows_ready = false) {
   using A4 = typename OpT<O>::Out4;
   const int ibase = p0 + wp * Tl::TP * 32 + (lane >> 5) * 4;
   const int jbase = q0 + wq * Tl::TQ * 32 + (lane & 31);
@@ -467,8 +467,9 @@ __device__ __forceinline__ void tile_epilogue(const Epi& epi, A (&acc)[Tl::TP][T
   // The per-row epilogue terms of the block's BP rows, fetched once by the
   // first BP / 4 threads into LDS (one global round trip for the block; read
   // group by group from global memory they cost a round trip per group).
+  // (rows_ready: the kernel stored them before its K loop)
   typename Epi::PreI* s_rows = reinterpret_cast<typename Epi::PreI*>(smem + Tl::STAGES * Tl::kStage);
-  if (t < Tl::BP / 4) {
+  if (!rows_ready && t < Tl::BP / 4) {
     typename Epi::PreI pr;
     epi.load_i(pr, p0 + 4 * t);
     s_rows[t] = pr;
@@ -620,8 +621,16 @@ mfma_gemm_kernel(const LX lx, const LY ly, const Epi epi, int nP, int nQ, int kc
     yslot[ks] = yr * Tl::kRowStride + lds_slot<Tl::CH>(yr, 2 * ks + (lane >> 5));
   }
 
+  // The epilogue's per-row terms are loaded ahead of the first stages (their
+  // round trip then overlaps the stages' instead of following the K loop)
+  // and parked in LDS past the stage buffers.
+  {
+    typename Epi::PreI pr;
+    if (t < Tl::BP / 4) epi.load_i(pr, p0 + 4 * t);
 #pragma unroll
-  for (int s = 0; s < Tl::STAGES - 1; ++s) issue(kbeg + s);
+    for (int s = 0; s < Tl::STAGES - 1; ++s) issue(kbeg + s);
+    if (t < Tl::BP / 4) reinterpret_cast<typename Epi::PreI*>(smem + Tl::STAGES * Tl::kStage)[t] = pr;
+  }
   wait_vmcnt<(Tl::STAGES - 2) * NL>();
   barrier_only();
   OHIP_STAMP(1);
@@ -695,7 +704,7 @@ mfma_gemm_kernel(const LX lx, const LY ly, const Epi epi, int nP, int nQ, int kc
   }
 
   OHIP_STAMP(2);
-  tile_epilogue<O, Tl>(epi, acc, smem, p0, q0, wp, wq, lane, t);
+  tile_epilogue<O, Tl>(epi, acc, smem, p0, q0, wp, wq, lane, t, true);
   OHIP_STAMP(3);
 }
 
