@@ -162,8 +162,9 @@ def fuse(graph: Graph, level: str = "all", nhwc: bool = True) -> Graph:
 
 def _halo_candidate(node, inits):
     """A conv the device can run on its halo-patch path with a resident NHWC
-    input: 3x3, stride and dilation 1, ungrouped, an f16 / bf16 filter (the
-    output extent is checked by the dispatcher, which converts otherwise)."""
+    input: 3x3, stride and dilation 1, ungrouped, an f32 / f16 filter (the
+    output extent and size are checked by the dispatcher, which converts
+    otherwise)."""
     if node.op not in ("Conv", "OhipConvInstanceNorm"):
         return False
     a = node.attrs
@@ -175,7 +176,7 @@ def _halo_candidate(node, inits):
     if w is None:
         return False
     wd = np.asarray(w.data if isinstance(w, ep.Typed) else w)
-    return wd.ndim == 4 and wd.shape[2:] == (3, 3) and wd.dtype == np.float16
+    return wd.ndim == 4 and wd.shape[2:] == (3, 3) and wd.dtype in (np.float16, np.float32)
 
 
 def _plan_nhwc(nodes, keep_out, inits):
