@@ -576,11 +576,12 @@ def test_conv_instnorm_fusion_matches_unfused(ctx, case):
     close(got, ref, 1e-2 if dt == "f16" else 1e-4)
 
 
-def test_face_swap_nhwc_trunk_matches_nchw(ctx):
+@pytest.mark.parametrize("dt", ["f16", "f32"])
+def test_face_swap_nhwc_trunk_matches_nchw(ctx, dt):
     """The residual trunk kept NHWC between its convolutions (halo-patch convs
     reading the reflect pad in place, norms writing NHWC) gives the same bits
     as the NCHW forward with its staging transposes."""
-    g, feeds = workloads.face_swap_generator(dtype="f16", n_blocks=2)
+    g, feeds = workloads.face_swap_generator(dtype=dt, n_blocks=2)
     nhwc = Session(g, ctx)
     assert sum(1 for n in nhwc.graph.nodes if n.attrs.ints.get("out_nhwc")) >= 3
     got = nhwc.run(feeds)
