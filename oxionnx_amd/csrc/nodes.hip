@@ -483,6 +483,70 @@ __global__ void __launch_bounds__(kThreads) maxpool_nhwc_kernel(const T* __restr
   }
 }
 
+// Byte pools over an NHWC input whose channels come in 4-byte groups (C, the
+// pitch and both pointers multiples of 4): a thread takes four channels of
+// one output pixel, one 32-bit load per tap, and keeps a byte maximum per
+// lane (the float kernel's comparison on the same integers).  With the
+// window size a template argument (K x K, dilation 1) every tap's load is
+// issued before the maxima, from a clamped address, and a tap outside the
+// image is masked; K = 0 walks a general window.
+template <bool SIGNED, int K>
+__global__ void __launch_bounds__(kThreads) maxpool_nhwc_b4_kernel(const uint32_t* __restrict__ x,
+                                                                   uint32_t* __restrict__ y, int64_t images,
+                                                                   PoolPlan p) {
+  const int G = p.nhwc_c / 4;
+  const int64_t pitch = p.pitch / 4;
+  const int64_t n = images * p.oh * p.ow * G;
+  auto merge = [](int (&best)[4], uint32_t w) __attribute__((always_inline)) {
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      const int v = SIGNED ? (int)(int8_t)(w >> (8 * b)) : (int)((w >> (8 * b)) & 0xff);
+      best[b] = v > best[b] ? v : best[b];
+    }
+  };
+  for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n; i += (int64_t)gridDim.x * kThreads) {
+    const int g = (int)(i % G);
+    int64_t t = i / G;
+    const int ox = (int)(t % p.ow);
+    t /= p.ow;
+    const int oy = (int)(t % p.oh);
+    const int64_t img = t / p.oh;
+    const uint32_t* xp = x + img * p.ih * p.iw * pitch + g;
+    int best[4];
+#pragma unroll
+    for (int b = 0; b < 4; ++b) best[b] = SIGNED ? -128 : 0;
+    const int iy0 = oy * p.sh - p.pt, ix0 = ox * p.sw - p.pl;
+    if constexpr (K > 0) {
+      uint32_t w[K][K];
+#pragma unroll
+      for (int ky = 0; ky < K; ++ky) {
+        const int iy = min(max(iy0 + ky, 0), p.ih - 1);
+#pragma unroll
+        for (int kx = 0; kx < K; ++kx) {
+          const int ix = min(max(ix0 + kx, 0), p.iw - 1);
+          w[ky][kx] = xp[((int64_t)iy * p.iw + ix) * pitch];
+        }
+      }
+#pragma unroll
+      for (int ky = 0; ky < K; ++ky)
+#pragma unroll
+        for (int kx = 0; kx < K; ++kx)
+          if ((unsigned)(iy0 + ky) < (unsigned)p.ih && (unsigned)(ix0 + kx) < (unsigned)p.iw) merge(best, w[ky][kx]);
+    } else {
+      for (int ky = 0; ky < p.kh; ++ky) {
+        const int iy = iy0 + ky * p.dh;
+        if (iy < 0 || iy >= p.ih) continue;
+        for (int kx = 0; kx < p.kw; ++kx) {
+          const int ix = ix0 + kx * p.dw;
+          if (ix < 0 || ix >= p.iw) continue;
+          merge(best, xp[((int64_t)iy * p.iw + ix) * pitch]);
+        }
+      }
+    }
+    y[i] = (best[0] & 0xff) | ((best[1] & 0xff) << 8) | ((best[2] & 0xff) << 16) | ((uint32_t)(best[3] & 0xff) << 24);
+  }
+}
+
 // ---------------------------------------------------------------- strided slice (rank <= 6)
 template <class T>
 __global__ void __launch_bounds__(kThreads) slice_kernel(const T* __restrict__ x, T* __restrict__ y, int64_t n, SlicePlan p) {
@@ -731,6 +795,17 @@ hipError_t run_maxpool(int dt, const void* x, void* y, int64_t planes, const Poo
   const dim3 g(grid_for(n));
   if (p.nhwc_c > 0) {
     const int64_t images = planes / p.nhwc_c;
+    if ((dt == DT_U8 || dt == DT_I8) && p.nhwc_c % 4 == 0 && p.pitch % 4 == 0 && (uintptr_t)x % 4 == 0 &&
+        (uintptr_t)y % 4 == 0) {
+      const int k = p.kh == p.kw && p.dh == 1 && p.dw == 1 && (p.kh == 3 || p.kh == 5) ? p.kh : 0;
+      const dim3 g4(grid_for(n / 4));
+      const uint32_t* xs = static_cast<const uint32_t*>(x);
+      uint32_t* ys = static_cast<uint32_t*>(y);
+#define OHIP_POOL_B4(S)                                                                                          switch (k) {                                                                                                     case 3: hipLaunchKernelGGL((maxpool_nhwc_b4_kernel<S, 3>), g4, dim3(kThreads), 0, st, xs, ys, images, p); break;     case 5: hipLaunchKernelGGL((maxpool_nhwc_b4_kernel<S, 5>), g4, dim3(kThreads), 0, st, xs, ys, images, p); break;     default: hipLaunchKernelGGL((maxpool_nhwc_b4_kernel<S, 0>), g4, dim3(kThreads), 0, st, xs, ys, images, p); break;   }
+      if (dt == DT_I8) { OHIP_POOL_B4(true) } else { OHIP_POOL_B4(false) }
+#undef OHIP_POOL_B4
+      return hipGetLastError();
+    }
     switch (dt) {
       case DT_U8: hipLaunchKernelGGL(maxpool_nhwc_kernel<uint8_t>, g, dim3(kThreads), 0, st, (const uint8_t*)x, (uint8_t*)y, images, p); break;
       case DT_I8: hipLaunchKernelGGL(maxpool_nhwc_kernel<int8_t>, g, dim3(kThreads), 0, st, (const int8_t*)x, (int8_t*)y, images, p); break;

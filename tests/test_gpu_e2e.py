@@ -293,6 +293,32 @@ def test_nhwc_resident_int8_chain_bit_exact(ctx):
         np.testing.assert_array_equal(np.asarray(out[k], np.float32), np.asarray(ref[k], np.float32), err_msg=k)
 
 
+@pytest.mark.parametrize("cout", [16, 12, 6])
+@pytest.mark.parametrize("signed", [False, True], ids=["u8", "i8"])
+@pytest.mark.parametrize("pool", [([5, 5], [1, 1], [2, 2, 2, 2]), ([3, 3], [2, 2], [1, 1, 1, 1]),
+                                  ([2, 3], [2, 1], [0, 1, 0, 1])], ids=["k5", "k3s2", "k2x3"])
+def test_maxpool_resident_nhwc_bytes(ctx, cout, signed, pool):
+    """MaxPool over a resident NHWC QLinearConv output (channel pitch 16):
+    four channels a thread where the channel count allows, the per-byte
+    kernel otherwise; bytes equal the oracle's."""
+    rng = np.random.default_rng(cout * 7 + signed)
+    yt = np.int8 if signed else np.uint8
+    ks, st, pads = pool
+    inits = {"xs": np.asarray([0.02], np.float32), "xz": np.asarray([128], np.uint8),
+             "w": rng.integers(-127, 128, (cout, 8, 3, 3)).astype(np.int8),
+             "ws": rng.uniform(0.002, 0.01, cout).astype(np.float32), "wz": np.zeros(cout, np.int8),
+             "ys": np.asarray([0.05], np.float32), "yz": np.asarray([0], yt)}
+    nodes = [ep.Node("QLinearConv", ["x", "xs", "xz", "w", "ws", "wz", "ys", "yz"], ["c"],
+                     A(int_lists={"kernel_shape": [3, 3], "pads": [1, 1, 1, 1]})),
+             ep.Node("MaxPool", ["c"], ["y"], A(int_lists={"kernel_shape": ks, "strides": st, "pads": pads}))]
+    g = unique_graph(nodes, inits, ["x"], ["y"])
+    feeds = {"x": rng.integers(0, 256, (2, 8, 13, 11)).astype(np.uint8)}
+    out = Session(g, ctx).run(feeds)
+    ref = G.run_graph(g, feeds)
+    assert out["y"].shape == ref["y"].shape
+    np.testing.assert_array_equal(np.asarray(out["y"], np.float32), np.asarray(ref["y"], np.float32))
+
+
 @pytest.mark.parametrize("zp", [None, 0, 128, -100, 3])
 def test_quantize_dequantize(ctx, zp):
     x = (RNG.normal(0, 3, (1, 4, 6, 6)).astype(np.float32))
