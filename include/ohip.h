@@ -243,8 +243,9 @@ int ohip_conv2d_noalloc(ohip_ctx* ctx, const ohip_conv_desc* d, const void* x, c
  * y = InstanceNorm(conv(x)) with the conv output rounded to its dtype first,
  * exactly as the unfused pair computes it.  When the convolution splits K,
  * the normalisation reads the partial sums directly (no reduction launch).
- * The conv must be ungrouped and without activation; out_layout may be
- * OHIP_NHWC (cout elements per pixel, whole 16-byte pixels). */
+ * The conv must be ungrouped and without activation, of dtype F32 or F16
+ * (BF16 declines); out_layout may be OHIP_NHWC (cout elements per pixel,
+ * whole 16-byte pixels). */
 typedef struct {
     float epsilon;
     const void* scale;     /* gamma per channel (or per (n, c) when per_sample); may be null */

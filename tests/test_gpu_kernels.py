@@ -467,6 +467,67 @@ def test_halo_conv_matches_oracle(torch, ctx, case, dt, nhwc_out):
     assert _rel_err(got, want) <= HALF_TOL
 
 
+# ------------------------------------------------------------------ fused conv + instance norm
+CONV_NORM_KERNEL_CASES = [
+    ((1, 64, 32, 32), 128, "f32", True, True),
+    ((1, 16, 20, 20), 16, "f32", False, False),
+    ((2, 32, 16, 16), 64, "f16", False, True),
+    ((1, 512, 32, 32), 512, "f16", True, True),     # split K: the norm reads the partial sums
+    ((1, 32, 24, 24), 48, "bf16", True, True),      # declined: the norm kernels are f32 / f16
+]
+
+
+@pytest.mark.parametrize("case", CONV_NORM_KERNEL_CASES, ids=str)
+def test_conv2d_instnorm_entry_point(torch, ctx, case):
+    """ohip_conv2d_instnorm against the oracle's conv (rounded to the dtype,
+    as the node chain stores it) followed by a float64 instance norm with
+    the chain's roundings: normalised value, gamma product, beta sum."""
+    from oxionnx_amd import _lib as L
+    xs, cout, dt, adain, relu = case
+    n = xs[0]
+    rng = np.random.default_rng(xs[1] + cout + n)
+    x = rng.uniform(-1, 1, xs).astype(np.float32)
+    w = rng.normal(0, 0.05, (cout, xs[1], 3, 3)).astype(np.float32)
+    b = rng.normal(0, 0.01, cout).astype(np.float32)
+    ab = rng.normal(1, 0.3, (n, 2 * cout)).astype(np.float32)   # AdaIN rows: gamma then beta
+    half = dt != "f32"
+    bf16 = dt == "bf16"
+    if half:
+        xh, wh, bh, abh = (O.f32_to_half_bits(v, bf16) for v in (x, w, b, ab))
+        tdt = torch.bfloat16 if bf16 else torch.float16
+        dev = lambda v: torch.from_numpy(v.view(np.int16)).cuda().view(tdt)   # noqa: E731
+        wt = ctx.weight_conv(O.half_bits_to_f32(wh, bf16), dtype=L.BF16 if bf16 else L.F16)
+        xt, bt, abt = dev(xh), dev(bh), dev(abh)
+        conv = O.half_bits_to_f32(O.conv_half(xh, wh, bh, bf16=bf16, pads=(1, 1, 1, 1)), bf16).astype(np.float64)
+        g64 = O.half_bits_to_f32(abh, bf16).astype(np.float64)
+        rnd = lambda v: O.half_bits_to_f32(O.f32_to_half_bits(v.astype(np.float32), bf16), bf16).astype(np.float64)  # noqa: E731
+    else:
+        wt = ctx.weight_conv(w)
+        xt, bt, abt = _dev(torch, x), _dev(torch, b), _dev(torch, ab)
+        conv = O.conv(x, w, b, pads=(1, 1, 1, 1)).astype(np.float32).astype(np.float64)
+        g64 = ab.astype(np.float64)
+        rnd = lambda v: v.astype(np.float32).astype(np.float64)  # noqa: E731
+    call = lambda: ctx.conv2d_instnorm(xt, wt, bt, pads=(1, 1, 1, 1), eps=1e-5,  # noqa: E731
+                                       gamma=abt if adain else None, beta=abt if adain else None,
+                                       scale_offset=0, bias_offset=cout, relu=relu)
+    if bf16:
+        with pytest.raises(L.OhipDeclined):
+            call()
+        return
+    y = call()
+    got = (O.half_bits_to_f32(y.contiguous().view(torch.int16).cpu().numpy().view(np.uint16), bf16)
+           if half else y.cpu().numpy()).astype(np.float64)
+    mean = conv.mean(axis=(2, 3), keepdims=True)
+    var = ((conv - mean) ** 2).mean(axis=(2, 3), keepdims=True)
+    want = (conv - mean) / np.sqrt(var + 1e-5)
+    if adain:
+        want = rnd(rnd(rnd(want) * g64[:, :cout, None, None]) + g64[:, cout:, None, None])
+    if relu:
+        want = np.maximum(want, 0.0)
+    assert got.shape == want.shape
+    assert _rel_err(got, want) <= (HALF_TOL if half else F32_TOL)
+
+
 # ------------------------------------------------------------------ integer GEMM
 @pytest.mark.parametrize("mkn", [(1, 16, 16), (4, 768, 96), (37, 100, 53), (128, 768, 3072), (300, 256, 200)],
                          ids=str)
