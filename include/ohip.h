@@ -458,6 +458,8 @@ int ohip_reset_counters(ohip_ctx* ctx);
  * 12: 128x128 (8, four stages)   13: 64x64 (4, eight stages)   14: 128x128 (4, four stages)
  * 15: 3x3 stride-1 convolutions take the halo-patch kernel wherever its
  *     geometry allows (automatically only from 3 GFLOP up).
+ * 16: 256x256 (8) with a third LDS buffer for the X operand, whose loads run
+ *     two stages ahead (the automatic f16 / bf16 choice where 6 would be).
  * The automatic choice splits K (on 64x64 tiles) when the 64x64 tiling gives
  * fewer than 256 blocks and K is at least 16 stages of 128 bytes. */
 int ohip_set_tile_override(ohip_ctx* ctx, int tile_id);

@@ -48,6 +48,7 @@ struct HaloTile {
   static constexpr int PI = (PIXMAX * CC + 63) / 64;      // patch DMA loads per stage
   static constexpr int TI = WI + PI;
   static constexpr int kStage = TI * 64;                  // u32x4 slots per stage
+  static constexpr int kStageArea = STAGES * kStage;
   static constexpr int NLO = TI / kWaves, NHI = (TI + kWaves - 1) / kWaves;
   static_assert(CC == 2 || CC == 4, "slabs of 2 or 4 chunks");
   static_assert(BCO * RW % 64 == 0, "filter slab must be whole DMA loads");

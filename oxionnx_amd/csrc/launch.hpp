@@ -331,6 +331,7 @@ using T64s4 = Tile<64, 64, 2, 2, 4>;        // 9: 4 waves, 32x32 per wave, four 
 using T128d4 = Tile<128, 128, 2, 4, 4>;     // 12: 8 waves, 64x32 per wave, four stages (one block per CU)
 using T64d8 = Tile<64, 64, 2, 2, 8>;        // 13: 4 waves, 32x32 per wave, eight stages
 using T128x4w4 = Tile<128, 128, 2, 2, 4>;   // 14: 4 waves, 64x64 per wave, four stages
+using T256x3 = Tile<256, 256, 2, 4, 2, 8, 3>;  // 16: as 6 with a third X buffer, X loads two stages ahead
 
 
 // Tiles per XCD group along P in the engine's tile order (map_tile);
@@ -421,7 +422,7 @@ inline hipError_t launch_halo(const HaloGeo& g, const Epi& epi, int P, int Q, in
 // per CU and the four-stage 64x64 tile hides the load latency of the
 // narrowest problems.  A short K loop (few 128-byte stages) is dominated by
 // the prologue and the epilogue, which the resident 128x128 blocks overlap.
-inline int pick_tile(int P, int Q, int kc, int forced, bool int8 = false) {
+inline int pick_tile(int P, int Q, int kc, int forced, bool int8 = false, bool half = false) {
   if (plain_tile_id(forced)) return forced;
   auto blocks = [&](int bp, int bq) { return (int64_t)((P + bp - 1) / bp) * ((Q + bq - 1) / bq); };
   const int nk = (kc + 7) / 8;
@@ -431,7 +432,10 @@ inline int pick_tile(int P, int Q, int kc, int forced, bool int8 = false) {
   // tile, one block per CU with deeper prefetch (21.1 against 22.1 us for
   // the two-stage tile; at a short K, 4096x768x3072, it loses: 30.7 / 25.4)
   if (int8 && nk >= 16 && blocks(128, 128) >= 192 && blocks(128, 128) < 320 && blocks(256, 256) < 256) return 12;
-  if (blocks(256, 256) >= 256) return 6;
+  // f16 / bf16 take the 256x256 tile with the X operand's loads two stages
+  // ahead (bit-identical; headline 312.0 -> 308.7 us, f16 8192^3 889.7 ->
+  // 868.6, bf16 863.6 -> 844.9; int8 and f32 lose 1-3 % on it)
+  if (blocks(256, 256) >= 256) return half ? 16 : 6;
   if (blocks(256, 128) >= 256) return P >= Q ? 3 : 4;
   if (blocks(128, 128) >= 192) return 8;
   return 9;
@@ -453,7 +457,7 @@ inline hipError_t launch_any(const LX& lx, const LY& ly, const Epi& epi, int P, 
       return launch_split_on<O, XX, XY, T128w8>(lx, ly, epi, P, Q, kc, splits, split_ws, st);
     return launch_split_on<O, XX, XY, T64s4>(lx, ly, epi, P, Q, kc, splits, split_ws, st);
   }
-  switch (pick_tile(P, Q, kc, tile, O == Op::I8)) {
+  switch (pick_tile(P, Q, kc, tile, O == Op::I8, O == Op::F16 || O == Op::BF16)) {
     case 2: return launch_tile<O, XX, XY, T128>(lx, ly, epi, P, Q, kc, st);
     case 3: return launch_tile<O, XX, XY, T256x128>(lx, ly, epi, P, Q, kc, st);
     case 4: return launch_tile<O, XX, XY, T128x256>(lx, ly, epi, P, Q, kc, st);
@@ -465,6 +469,7 @@ inline hipError_t launch_any(const LX& lx, const LY& ly, const Epi& epi, int P, 
     case 12: return launch_tile<O, XX, XY, T128d4>(lx, ly, epi, P, Q, kc, st);
     case 13: return launch_tile<O, XX, XY, T64d8>(lx, ly, epi, P, Q, kc, st);
     case 14: return launch_tile<O, XX, XY, T128x4w4>(lx, ly, epi, P, Q, kc, st);
+    case 16: return launch_tile<O, XX, XY, T256x3>(lx, ly, epi, P, Q, kc, st);
     default: return launch_tile<O, XX, XY, T64>(lx, ly, epi, P, Q, kc, st);
   }
 }

@@ -104,8 +104,11 @@ template <int N, class F> __device__ __forceinline__ void static_for(F&& f) {
   static_for_impl(f, std::make_integer_sequence<int, N>{});
 }
 
-template <int BP_, int BQ_, int WP_, int WQ_, int STAGES_, int CH_ = 8> struct Tile {
-  static constexpr int BP = BP_, BQ = BQ_, WP = WP_, WQ = WQ_, STAGES = STAGES_, CH = CH_;
+// XST > STAGES (only STAGES = 2, XST = 3): the X operand keeps a third
+// buffer and its loads run two stages ahead, the Y operand's one, so a CU
+// has half as many bytes again in flight within the same LDS.
+template <int BP_, int BQ_, int WP_, int WQ_, int STAGES_, int CH_ = 8, int XST_ = STAGES_> struct Tile {
+  static constexpr int BP = BP_, BQ = BQ_, WP = WP_, WQ = WQ_, STAGES = STAGES_, CH = CH_, XST = XST_;
   static constexpr int KS = CH / 2;                               // MFMA k-steps per slab
   static constexpr int kWaves = WP * WQ;
   static constexpr int kThreads = 64 * kWaves;
@@ -114,11 +117,15 @@ template <int BP_, int BQ_, int WP_, int WQ_, int STAGES_, int CH_ = 8> struct T
   static constexpr int NX = BP * CH / kThreads;                   // DMA loads per thread per stage
   static constexpr int NY = BQ * CH / kThreads;
   static constexpr int kStage = (BP + BQ) * kRowStride;           // in u32x4 units
+  // X buffers first (XST of BP rows), then the Y buffers (STAGES of BQ rows)
+  static constexpr int kYBase = XST * BP * kRowStride;
+  static constexpr int kStageArea = kYBase + STAGES * BQ * kRowStride;
   static_assert(CH == 8 || CH == 4, "slabs are 128 or 64 bytes");
   static_assert(TP >= 1 && TQ >= 1, "wave tile must hold at least one 32x32 MFMA tile");
   static_assert(NX * kThreads == BP * CH && NY * kThreads == BQ * CH, "loader split must be exact");
   static_assert(kWaves % 2 == 0, "the DMA swizzle phase relies on an even wave count");
-  static_assert(STAGES >= 2 && STAGES * kStage * 16 <= 160 * 1024, "LDS budget");
+  static_assert(STAGES >= 2 && kStageArea * 16 <= 160 * 1024, "LDS budget");
+  static_assert(XST == STAGES || (STAGES == 2 && XST == 3), "X runs at most one stage deeper, over two");
 };
 
 // LDS slot of 16-byte chunk c (0..7) of staged row r.  Rows are 128 bytes
@@ -454,9 +461,13 @@ __device__ __forceinline__ void tile_epilogue(const Epi& epi, A (&acc)[Tl::TP][T
   // Mode 1 stages the epilogue's narrow output (1 or 2 bytes); mode 2 stages
   // 4-byte outputs (int32, f32) when the tile's stage buffers hold them.
   constexpr int EBN = Epi::kStageBytes > 0 ? Epi::kStageBytes : 1;
-  constexpr bool kWide = Epi::kStageWide && Tl::BQ * Tl::BP * 4 <= Tl::STAGES * Tl::kStage * 16;
-  static_assert(Epi::kStageBytes == 0 || Tl::BQ * Tl::BP * EBN <= Tl::STAGES * Tl::kStage * 16,
-                "staging must fit the stage buffers");
+  // the row terms sit past the stage buffers, or (when both do not fit the
+  // LDS) at the end of them, written once every load has landed
+  constexpr int kRowTerms = (int)((Tl::BP / 4 * sizeof(typename Epi::PreI) + 15) / 16);
+  constexpr bool kRowsInside = (Tl::kStageArea + kRowTerms) * 16 > 160 * 1024;
+  constexpr int kStageCap = (kRowsInside ? Tl::kStageArea - kRowTerms : Tl::kStageArea) * 16;
+  constexpr bool kWide = Epi::kStageWide && Tl::BQ * Tl::BP * 4 <= kStageCap;
+  static_assert(Epi::kStageBytes == 0 || Tl::BQ * Tl::BP * EBN <= kStageCap, "staging must fit the stage buffers");
   char* stg = reinterpret_cast<char*>(smem);
   int smode = 0;
   // the batch slice's own output must be 16-byte aligned too (the Epi checks slice 0's)
@@ -468,7 +479,13 @@ __device__ __forceinline__ void tile_epilogue(const Epi& epi, A (&acc)[Tl::TP][T
   // first BP / 4 threads into LDS (one global round trip for the block; read
   // group by group from global memory they cost a round trip per group).
   // (rows_ready: the kernel stored them before its K loop)
-  typename Epi::PreI* s_rows = reinterpret_cast<typename Epi::PreI*>(smem + Tl::STAGES * Tl::kStage);
+  typename Epi::PreI* s_rows =
+      reinterpret_cast<typename Epi::PreI*>(smem + (kRowsInside ? Tl::kStageArea - kRowTerms : Tl::kStageArea));
+  if constexpr (kRowsInside) {
+    wait_vmcnt<0>();
+    wait_lgkm0();
+    barrier_only();
+  }
   if (!rows_ready && t < Tl::BP / 4) {
     typename Epi::PreI pr;
     epi.load_i(pr, p0 + 4 * t);
@@ -574,7 +591,8 @@ mfma_gemm_kernel(const LX lx, const LY ly, const Epi epi, int nP, int nQ, int kc
   using A = typename OpT<O>::Acc;
   // the stage buffers, then (after the K loop) the block's per-row epilogue terms
   constexpr int kRowTerms = (int)((Tl::BP / 4 * sizeof(typename Epi::PreI) + 15) / 16);
-  __shared__ u32x4 smem[Tl::STAGES * Tl::kStage + kRowTerms];
+  constexpr bool kRowsInside = (Tl::kStageArea + kRowTerms) * 16 > 160 * 1024;
+  __shared__ u32x4 smem[kRowsInside ? Tl::kStageArea : Tl::kStageArea + kRowTerms];
   const int t = threadIdx.x;
   const int lane = t & 63;
   const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
@@ -604,16 +622,17 @@ mfma_gemm_kernel(const LX lx, const LY ly, const Epi epi, int nP, int nQ, int kc
   constexpr int NL = Tl::NX + Tl::NY;     // DMA loads per thread per stage
   // Every stage issues all its loads (past the last stage they read zero or
   // the pad source), so the waits below are fixed counts of outstanding loads.
-  auto issue = [&](int kt) {
-    u32x4* s = smem + (kt % Tl::STAGES) * Tl::kStage;
-    lx.template issue<Tl::NX, Tl::kWaves, Tl::CH>(sx, kt, wave, s);
-    ly.template issue<Tl::NY, Tl::kWaves, Tl::CH>(sy, kt, wave, s + Tl::BP * Tl::kRowStride);
+  auto xbuf = [&](int kt) __attribute__((always_inline)) { return smem + (kt % Tl::XST) * (Tl::BP * Tl::kRowStride); };
+  auto ybuf = [&](int kt) __attribute__((always_inline)) {
+    return smem + Tl::kYBase + (kt % Tl::STAGES) * (Tl::BQ * Tl::kRowStride);
   };
+  auto issue_x = [&](int kt) { lx.template issue<Tl::NX, Tl::kWaves, Tl::CH>(sx, kt, wave, xbuf(kt)); };
+  auto issue_y = [&](int kt) { ly.template issue<Tl::NY, Tl::kWaves, Tl::CH>(sy, kt, wave, ybuf(kt)); };
 
   // Fragment slots of this lane: rows are tile bases (multiples of 32) plus
   // lane % 32, chunk 2 * ks + lane / 32.
   const int xr = wp * Tl::TP * 32 + (lane & 31);
-  const int yr = Tl::BP + wq * Tl::TQ * 32 + (lane & 31);
+  const int yr = wq * Tl::TQ * 32 + (lane & 31);
   int xslot[Tl::KS], yslot[Tl::KS];
 #pragma unroll
   for (int ks = 0; ks < Tl::KS; ++ks) {
@@ -624,24 +643,35 @@ mfma_gemm_kernel(const LX lx, const LY ly, const Epi epi, int nP, int nQ, int kc
   // The epilogue's per-row terms are loaded ahead of the first stages (their
   // round trip then overlaps the stages' instead of following the K loop)
   // and parked in LDS past the stage buffers.
+  // Load order (the waits count outstanding loads): the prologue issues
+  // X(kbeg), Y(kbeg), X(kbeg + 1), Y(kbeg + 1), ... up to each operand's
+  // depth; stage kt issues Y(kt + STAGES - 1), then X(kt + XST - 1).  At the
+  // end of stage kt, X and Y of stage kt + 1 have landed once at most
+  // kAhead loads remain outstanding.
+  constexpr int kAhead = (Tl::STAGES - 2) * Tl::NY + (Tl::XST - 2) * Tl::NX;
   {
     typename Epi::PreI pr;
-    if (t < Tl::BP / 4) epi.load_i(pr, p0 + 4 * t);
+    if constexpr (!kRowsInside) if (t < Tl::BP / 4) epi.load_i(pr, p0 + 4 * t);
 #pragma unroll
-    for (int s = 0; s < Tl::STAGES - 1; ++s) issue(kbeg + s);
-    if (t < Tl::BP / 4) reinterpret_cast<typename Epi::PreI*>(smem + Tl::STAGES * Tl::kStage)[t] = pr;
+    for (int s = 0; s < Tl::XST - 1; ++s) {
+      issue_x(kbeg + s);
+      if (s < Tl::STAGES - 1) issue_y(kbeg + s);
+    }
+    if constexpr (!kRowsInside)
+      if (t < Tl::BP / 4) reinterpret_cast<typename Epi::PreI*>(smem + Tl::kStageArea)[t] = pr;
   }
-  wait_vmcnt<(Tl::STAGES - 2) * NL>();
+  wait_vmcnt<kAhead>();
   barrier_only();
   OHIP_STAMP(1);
 
   u32x4 fx[2][Tl::TP], fy[2][Tl::TQ];
   {
-    const u32x4* s0 = smem + (kbeg % Tl::STAGES) * Tl::kStage;
+    const u32x4* x0 = xbuf(kbeg);
+    const u32x4* y0 = ybuf(kbeg);
 #pragma unroll
-    for (int a = 0; a < Tl::TP; ++a) fx[0][a] = s0[xslot[0] + a * 32 * Tl::kRowStride];
+    for (int a = 0; a < Tl::TP; ++a) fx[0][a] = x0[xslot[0] + a * 32 * Tl::kRowStride];
 #pragma unroll
-    for (int b = 0; b < Tl::TQ; ++b) fy[0][b] = s0[yslot[0] + b * 32 * Tl::kRowStride];
+    for (int b = 0; b < Tl::TQ; ++b) fy[0][b] = y0[yslot[0] + b * 32 * Tl::kRowStride];
   }
 
   // One k-step in program order, fenced so the compiler keeps it: each MFMA
@@ -654,33 +684,38 @@ mfma_gemm_kernel(const LX lx, const LY ly, const Epi epi, int nP, int nQ, int kc
   constexpr int NRD = Tl::TP + Tl::TQ;     // fragment reads per k-step
   constexpr int PRE = NM >= 4 ? 2 : 0;     // MFMAs of the last k-step ahead of the barrier
   for (int kt = kbeg; kt < kend; ++kt) {
-    const u32x4* s = smem + (kt % Tl::STAGES) * Tl::kStage;
-    const u32x4* sn = smem + ((kt + 1) % Tl::STAGES) * Tl::kStage;
-    u32x4* sd = smem + ((kt + Tl::STAGES - 1) % Tl::STAGES) * Tl::kStage;
-    const typename LX::Step stx = lx.template step<Tl::NX, Tl::kWaves, Tl::CH>(sx, kt + Tl::STAGES - 1);
+    const u32x4* sX = xbuf(kt);
+    const u32x4* sY = ybuf(kt);
+    const u32x4* snX = xbuf(kt + 1);
+    const u32x4* snY = ybuf(kt + 1);
+    u32x4* sdX = xbuf(kt + Tl::XST - 1);
+    u32x4* sdY = ybuf(kt + Tl::STAGES - 1);
+    const typename LX::Step stx = lx.template step<Tl::NX, Tl::kWaves, Tl::CH>(sx, kt + Tl::XST - 1);
     const typename LY::Step sty = ly.template step<Tl::NY, Tl::kWaves, Tl::CH>(sy, kt + Tl::STAGES - 1);
+    // Y's loads first, then X's (the order the waits count on)
     auto dma = [&](int i) __attribute__((always_inline)) {
-      if (i < Tl::NX) lx.template load<Tl::NX, Tl::kWaves, Tl::CH>(sx, stx, i, wave, sd);
-      else ly.template load<Tl::NY, Tl::kWaves, Tl::CH>(sy, sty, i - Tl::NX, wave, sd + Tl::BP * Tl::kRowStride);
+      if (i < Tl::NY) ly.template load<Tl::NY, Tl::kWaves, Tl::CH>(sy, sty, i, wave, sdY);
+      else lx.template load<Tl::NX, Tl::kWaves, Tl::CH>(sx, stx, i - Tl::NY, wave, sdX);
     };
     static_for<Tl::KS>([&](auto ksc) __attribute__((always_inline)) {
       constexpr int ks = decltype(ksc)::value;
       constexpr bool last = ks == Tl::KS - 1;
       constexpr int cur = ks & 1, nxt = cur ^ 1;
-      const u32x4* src = last ? sn : s;
+      const u32x4* srcX = last ? snX : sX;
+      const u32x4* srcY = last ? snY : sY;
       const int kr = last ? 0 : ks + 1;
       // read r of the next k-step: fx[0], fy[0 .. TQ-1], fx[1 .. TP-1]
       auto read = [&](auto rc) __attribute__((always_inline)) {
         constexpr int r = decltype(rc)::value;
-        if constexpr (r == 0) fx[nxt][0] = src[xslot[kr]];
-        else if constexpr (r <= Tl::TQ) fy[nxt][r - 1] = src[yslot[kr] + (r - 1) * 32 * Tl::kRowStride];
-        else fx[nxt][r - Tl::TQ] = src[xslot[kr] + (r - Tl::TQ) * 32 * Tl::kRowStride];
+        if constexpr (r == 0) fx[nxt][0] = srcX[xslot[kr]];
+        else if constexpr (r <= Tl::TQ) fy[nxt][r - 1] = srcY[yslot[kr] + (r - 1) * 32 * Tl::kRowStride];
+        else fx[nxt][r - Tl::TQ] = srcX[xslot[kr] + (r - Tl::TQ) * 32 * Tl::kRowStride];
       };
       static_for<NM>([&](auto mc) __attribute__((always_inline)) {
         constexpr int m = decltype(mc)::value;
         constexpr int a = m / Tl::TQ, b = m % Tl::TQ;
         if constexpr (last && m == PRE) {
-          wait_vmcnt<(Tl::STAGES - 2) * NL>();
+          wait_vmcnt<kAhead>();
           wait_lgkm0();
           barrier_only();
         }
@@ -704,7 +739,7 @@ mfma_gemm_kernel(const LX lx, const LY ly, const Epi epi, int nP, int nQ, int kc
   }
 
   OHIP_STAMP(2);
-  tile_epilogue<O, Tl>(epi, acc, smem, p0, q0, wp, wq, lane, t, true);
+  tile_epilogue<O, Tl>(epi, acc, smem, p0, q0, wp, wq, lane, t, !kRowsInside);
   OHIP_STAMP(3);
 }
 

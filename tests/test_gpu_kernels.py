@@ -50,7 +50,7 @@ GEMM_SHAPES = [(1, 64, 32), (3, 100, 17), (8, 256, 64), (2, 5000, 40), (9, 64, 4
 
 
 @pytest.mark.parametrize("mkn", GEMM_SHAPES, ids=str)
-@pytest.mark.parametrize("tile", list(range(12)))
+@pytest.mark.parametrize("tile", list(range(12)) + [16])
 def test_gemm_f32_matches_oracle(torch, ctx, mkn, tile):
     from oxionnx_amd import _lib as L
     m, k, n = mkn
@@ -120,7 +120,8 @@ def test_gemm_golden_vectors(torch, ctx, c):
 @pytest.mark.parametrize("bf16", [False, True], ids=["f16", "bf16"])
 @pytest.mark.parametrize("mkn", [(1, 128, 64), (5, 96, 40), (64, 64, 64), (130, 264, 200), (512, 768, 384)],
                          ids=str)
-def test_gemm_half_matches_oracle(torch, ctx, bf16, mkn):
+@pytest.mark.parametrize("tile", [0, 6, 16])
+def test_gemm_half_matches_oracle(torch, ctx, bf16, mkn, tile):
     from oxionnx_amd import _lib as L
     m, k, n = mkn
     rng = np.random.default_rng(m + k + n)
@@ -133,7 +134,11 @@ def test_gemm_half_matches_oracle(torch, ctx, bf16, mkn):
     w = ctx.weight_gemm(O.half_bits_to_f32(bh, bf16), dtype=dt)
     at = torch.from_numpy(ah.view(np.int16)).cuda().view(tdt)
     ct = torch.from_numpy(ch.view(np.int16)).cuda().view(tdt)
-    y = ctx.gemm(at, w, ct, alpha=1.0, beta=1.0)
+    ctx.set_tile(tile)
+    try:
+        y = ctx.gemm(at, w, ct, alpha=1.0, beta=1.0)
+    finally:
+        ctx.set_tile(0)
     got = O.half_bits_to_f32(y.view(torch.int16).cpu().numpy().view(np.uint16), bf16)
     want = O.half_bits_to_f32(O.gemm_half(ah, bh, ch, 1.0, 1.0, bf16=bf16), bf16)
     assert _rel_err(got, want) <= HALF_TOL
