@@ -422,16 +422,17 @@ inline hipError_t launch_halo(const HaloGeo& g, const Epi& epi, int P, int Q, in
 // per CU and the four-stage 64x64 tile hides the load latency of the
 // narrowest problems.  A short K loop (few 128-byte stages) is dominated by
 // the prologue and the epilogue, which the resident 128x128 blocks overlap.
-inline int pick_tile(int P, int Q, int kc, int forced, bool int8 = false, bool half = false) {
+inline int pick_tile(int P, int Q, int kc, int forced, bool half = false) {
   if (plain_tile_id(forced)) return forced;
   auto blocks = [&](int bp, int bq) { return (int64_t)((P + bp - 1) / bp) * ((Q + bq - 1) / bq); };
   const int nk = (kc + 7) / 8;
   if (nk <= 16) return blocks(128, 128) >= 256 ? 8 : 9;
-  // int8 with a long K and about one round of 128x128 tiles (config 3's
-  // second FFN GEMM, 4096x3072x768: 192 tiles): the four-stage eight-wave
-  // tile, one block per CU with deeper prefetch (21.1 against 22.1 us for
-  // the two-stage tile; at a short K, 4096x768x3072, it loses: 30.7 / 25.4)
-  if (int8 && nk >= 16 && blocks(128, 128) >= 192 && blocks(128, 128) < 320 && blocks(256, 256) < 256) return 12;
+  // a long K and about one round of 128x128 tiles (config 3's second FFN
+  // GEMM, 4096x3072x768: 192 tiles): the four-stage eight-wave tile, one
+  // block per CU with deeper prefetch (int8 21.1 against 22.1 us for the
+  // two-stage tile; f16 1024x4096x4096 43.8 against 55.5, 768x4096x4096
+  // 38.5 against 52.0; f32 within 3 %)
+  if (blocks(128, 128) >= 192 && blocks(128, 128) < 320 && blocks(256, 256) < 256) return 12;
   // f16 / bf16 take the 256x256 tile with the X operand's loads two stages
   // ahead (bit-identical; headline 312.0 -> 308.7 us, f16 8192^3 889.7 ->
   // 868.6, bf16 863.6 -> 844.9; int8 and f32 lose 1-3 % on it)
@@ -457,7 +458,7 @@ inline hipError_t launch_any(const LX& lx, const LY& ly, const Epi& epi, int P, 
       return launch_split_on<O, XX, XY, T128w8>(lx, ly, epi, P, Q, kc, splits, split_ws, st);
     return launch_split_on<O, XX, XY, T64s4>(lx, ly, epi, P, Q, kc, splits, split_ws, st);
   }
-  switch (pick_tile(P, Q, kc, tile, O == Op::I8, O == Op::F16 || O == Op::BF16)) {
+  switch (pick_tile(P, Q, kc, tile, O == Op::F16 || O == Op::BF16)) {
     case 2: return launch_tile<O, XX, XY, T128>(lx, ly, epi, P, Q, kc, st);
     case 3: return launch_tile<O, XX, XY, T256x128>(lx, ly, epi, P, Q, kc, st);
     case 4: return launch_tile<O, XX, XY, T128x256>(lx, ly, epi, P, Q, kc, st);
