@@ -104,9 +104,9 @@ template <int N, class F> __device__ __forceinline__ void static_for(F&& f) {
   static_for_impl(f, std::make_integer_sequence<int, N>{});
 }
 
-// XST > STAGES (only STAGES = 2, XST = 3): the X operand keeps a third
-// buffer and its loads run two stages ahead, the Y operand's one, so a CU
-// has half as many bytes again in flight within the same LDS.
+// XST > STAGES: the X operand keeps more buffers than Y and its loads run
+// further ahead (XST = 3 over STAGES = 2: X two stages ahead, Y one), so a
+// CU has more bytes in flight within the same LDS.
 template <int BP_, int BQ_, int WP_, int WQ_, int STAGES_, int CH_ = 8, int XST_ = STAGES_> struct Tile {
   static constexpr int BP = BP_, BQ = BQ_, WP = WP_, WQ = WQ_, STAGES = STAGES_, CH = CH_, XST = XST_;
   static constexpr int KS = CH / 2;                               // MFMA k-steps per slab
@@ -125,7 +125,7 @@ template <int BP_, int BQ_, int WP_, int WQ_, int STAGES_, int CH_ = 8, int XST_
   static_assert(NX * kThreads == BP * CH && NY * kThreads == BQ * CH, "loader split must be exact");
   static_assert(kWaves % 2 == 0, "the DMA swizzle phase relies on an even wave count");
   static_assert(STAGES >= 2 && kStageArea * 16 <= 160 * 1024, "LDS budget");
-  static_assert(XST == STAGES || (STAGES == 2 && XST == 3), "X runs at most one stage deeper, over two");
+  static_assert(XST >= STAGES, "X runs at least as deep as Y");
 };
 
 // LDS slot of 16-byte chunk c (0..7) of staged row r.  Rows are 128 bytes
@@ -647,8 +647,12 @@ mfma_gemm_kernel(const LX lx, const LY ly, const Epi epi, int nP, int nQ, int kc
   // X(kbeg), Y(kbeg), X(kbeg + 1), Y(kbeg + 1), ... up to each operand's
   // depth; stage kt issues Y(kt + STAGES - 1), then X(kt + XST - 1).  At the
   // end of stage kt, X and Y of stage kt + 1 have landed once at most
-  // kAhead loads remain outstanding.
-  constexpr int kAhead = (Tl::STAGES - 2) * Tl::NY + (Tl::XST - 2) * Tl::NX;
+  // kAhead loads remain outstanding (the loads issued after Y(kt + 1) in the
+  // steady state: that stage's X and every later stage's; earlier in the
+  // loop more were, so the wait is stricter than needed, never looser);
+  // after the prologue, once at most kAheadPro remain.
+  constexpr int kAhead = (Tl::XST > Tl::STAGES ? Tl::NX : 0) + (Tl::STAGES - 2) * NL;
+  constexpr int kAheadPro = (Tl::XST - 2) * Tl::NX + (Tl::STAGES - 2) * Tl::NY;
   {
     typename Epi::PreI pr;
     if constexpr (!kRowsInside) if (t < Tl::BP / 4) epi.load_i(pr, p0 + 4 * t);
@@ -660,7 +664,7 @@ mfma_gemm_kernel(const LX lx, const LY ly, const Epi epi, int nP, int nQ, int kc
     if constexpr (!kRowsInside)
       if (t < Tl::BP / 4) reinterpret_cast<typename Epi::PreI*>(smem + Tl::kStageArea)[t] = pr;
   }
-  wait_vmcnt<kAhead>();
+  wait_vmcnt<kAheadPro>();
   barrier_only();
   OHIP_STAMP(1);
 
