@@ -546,6 +546,9 @@ bool conv_takes_nhwc(ohip_ctx* ctx, const ohip_node* nd) {
   const std::string pm = attr_s(nd, "pad_mode");
   if (pm == "reflect") d.pad_mode = OHIP_PAD_REFLECT;
   else if (pm == "edge") d.pad_mode = OHIP_PAD_EDGE;
+  // zero padding: the engine's implicit im2col reads the NHWC tensor as it
+  // is; a reflect / edge pad is applied in place only by the halo path
+  if (d.pad_mode == OHIP_PAD_ZEROS) return true;
   return ohip_conv_halo_splits_internal(ctx, &d) > 0;
 }
 

@@ -160,30 +160,34 @@ def fuse(graph: Graph, level: str = "all", nhwc: bool = True) -> Graph:
     return replace(graph, nodes=_drop_dead(nodes, keep_out), initializers=inits)
 
 
-def _halo_candidate(node, inits):
-    """A conv the device can run on its halo-patch path with a resident NHWC
-    input: 3x3, stride and dilation 1, ungrouped, an f32 / f16 filter (the
-    output extent and size are checked by the dispatcher, which converts
-    otherwise)."""
+def _nhwc_reader(node, inits):
+    """A conv the device runs on a resident NHWC input in place: ungrouped,
+    an f32 / f16 filter, and either zero padding (the engine's implicit
+    im2col reads NHWC as it is) or the halo-patch geometry (3x3, stride and
+    dilation 1), whose loader applies a fused reflect / edge Pad.  The
+    dispatcher checks extents and sizes and converts otherwise."""
     if node.op not in ("Conv", "OhipConvInstanceNorm"):
         return False
     a = node.attrs
-    if a.ints.get("group", 1) != 1 or list(a.int_lists.get("kernel_shape", [3, 3])) != [3, 3]:
-        return False
-    if any(v != 1 for v in a.int_lists.get("strides", [1, 1])) or any(v != 1 for v in a.int_lists.get("dilations", [1, 1])):
+    if a.ints.get("group", 1) != 1:
         return False
     w = inits.get(node.inputs[1]) if len(node.inputs) > 1 else None
     if w is None:
         return False
     wd = np.asarray(w.data if isinstance(w, ep.Typed) else w)
-    return wd.ndim == 4 and wd.shape[2:] == (3, 3) and wd.dtype in (np.float16, np.float32)
+    if wd.ndim != 4 or wd.dtype not in (np.float16, np.float32):
+        return False
+    if a.strings.get("pad_mode", "constant") in ("constant", ""):
+        return True
+    return (wd.shape[2:] == (3, 3) and all(v == 1 for v in a.int_lists.get("strides", [1, 1]))
+            and all(v == 1 for v in a.int_lists.get("dilations", [1, 1])))
 
 
 def _plan_nhwc(nodes, keep_out, inits):
     """Layout hints for float activations: a Conv / OhipConvInstanceNorm
-    output whose every consumer reads it in place as NHWC (the input of a
-    halo-path conv, or the residual of a fused node that has the same
-    shape) is produced NHWC ("out_nhwc"), which removes the consumers' NCHW
+    output whose every consumer reads it in place as NHWC (the input of an
+    ungrouped conv with zero padding or on the halo path, or the residual of
+    a fused node that has the same shape) is produced NHWC ("out_nhwc"), which removes the consumers' NCHW
     -> NHWC staging.  The dispatcher treats the hint as a preference and
     converts for any consumer that cannot take the layout."""
     cons = _consumers(nodes)
@@ -198,7 +202,7 @@ def _plan_nhwc(nodes, keep_out, inits):
         ok = True
         for u in users:
             un = out[u]
-            if un.inputs and un.inputs[0] == t and _halo_candidate(un, inits) and t not in un.inputs[1:5]:
+            if un.inputs and un.inputs[0] == t and _nhwc_reader(un, inits) and t not in un.inputs[1:5]:
                 continue
             if un.op == "OhipConvInstanceNorm" and len(un.inputs) > 5 and un.inputs[5] == t and un.inputs[0] != t:
                 continue
