@@ -1215,15 +1215,22 @@ int do_resize(ohip_ctx* ctx, const ohip_node* nd, int placement, ohip_output* ou
   if (p.ih <= 0 || p.iw <= 0 || p.oh <= 0 || p.ow <= 0) return decline("Resize: empty");
   const int dt = x->device ? x->dtype : OHIP_F32;
   const int eb = ebytes(dt);
+  // a resident NHWC input (passed only under an "out_nhwc" hint, see
+  // takes_nhwc) resizes NHWC -> NHWC
+  const bool nhwc = x->device && ohip_dtensor_layout(x->device) == OHIP_NHWC;
   Stage st(ctx);
   const void* xd = st.operand(x);
   const int64_t planes = x->shape[0] * x->shape[1];
   const size_t bytes = (size_t)(planes * p.oh * p.ow) * eb;
   void* yd = st.alloc(bytes);
   if (!xd || !yd) return OHIP_E_NOMEM;
-  hipError_t e = ohip::run_resize_nearest(eb, xd, yd, planes, p, (hipStream_t)ohip_ctx_stream(ctx));
+  hipError_t e = nhwc ? ohip::run_resize_nearest_nhwc(eb, xd, yd, x->shape[0], x->shape[1], p,
+                                                      (hipStream_t)ohip_ctx_stream(ctx))
+                      : ohip::run_resize_nearest(eb, xd, yd, planes, p, (hipStream_t)ohip_ctx_stream(ctx));
   if (e != hipSuccess) return ohip_hip_error_internal(e, "node kernel launch");
-  return output_device(ctx, st, placement, out, dt, {x->shape[0], x->shape[1], p.oh, p.ow}, yd, bytes);
+  int rc = output_device(ctx, st, placement, out, dt, {x->shape[0], x->shape[1], p.oh, p.ow}, yd, bytes);
+  if (rc == OHIP_OK && nhwc && out->device) rc = ohip_dtensor_set_nhwc_internal(out->device, x->shape[1]);
+  return rc;
 }
 
 // ---------------------------------------------------------------- Pad
@@ -1840,6 +1847,14 @@ bool takes_nhwc(ohip_ctx* ctx, const ohip_node* nd, int i, int placement) {
            ohip_dtensor_pitch_internal(r.device) == g.cout && g.cout % (16 / ebytes(r.dtype)) == 0;
   }
   if (op == "Slice" || op == "MaxPool") return i == 0;
+  if (op == "Resize") {
+    // NHWC in, NHWC out, when the session asks for an NHWC output (whole
+    // 16-byte pixels, C per pixel)
+    if (i != 0 || !nhwc(0) || attr_i(nd, "out_nhwc", 0) == 0) return false;
+    const ohip_tensor& x = nd->inputs[0];
+    return x.rank == 4 && ohip_dtensor_pitch_internal(x.device) == x.shape[1] &&
+           (x.shape[1] * ebytes(x.dtype)) % 16 == 0;
+  }
   if (op == "QLinearAdd") {
     if ((i != 0 && i != 3) || !nhwc(0) || !nhwc(3)) return false;
     const ohip_tensor &a = nd->inputs[0], &b = nd->inputs[3];

@@ -375,6 +375,9 @@ hipError_t run_instnorm_partials(int dt, const float* ws, int splits, int64_t Pp
                                  hipStream_t st);
 hipError_t run_resize_nearest(int elem_bytes, const void* x, void* y, int64_t planes, const ResizePlan& p,
                               hipStream_t st);
+// NHWC (C elements a pixel, C * elem_bytes a multiple of 16, 16-byte aligned)
+hipError_t run_resize_nearest_nhwc(int elem_bytes, const void* x, void* y, int64_t images, int64_t C,
+                                   const ResizePlan& p, hipStream_t st);
 hipError_t run_pad(int elem_bytes, const void* x, void* y, int64_t n, const PadPlan& p, hipStream_t st);
 hipError_t run_slice(int elem_bytes, const void* x, void* y, int64_t n, const SlicePlan& p, hipStream_t st);
 hipError_t run_maxpool(int dt, const void* x, void* y, int64_t planes, const PoolPlan& p, hipStream_t st);

@@ -763,6 +763,36 @@ hipError_t run_instnorm_partials(int dt, const float* ws, int splits, int64_t Pp
     return hipGetLastError();                                                                                      \
   } while (0)
 
+// Nearest resize of an NHWC tensor (C elements a pixel, whole 16-byte
+// pixels): every 16-byte chunk of an output pixel is the same chunk of its
+// source pixel, the source row and column from the NCHW kernel's rule.
+__global__ void __launch_bounds__(kThreads) resize_nearest_nhwc_kernel(const uint4* __restrict__ x,
+                                                                       uint4* __restrict__ y, int64_t n, int cpp,
+                                                                       ResizePlan p) {
+  for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n; i += (int64_t)gridDim.x * kThreads) {
+    const int c = (int)(i % cpp);
+    int64_t t = i / cpp;
+    const int ox = (int)(t % p.ow);
+    t /= p.ow;
+    const int oy = (int)(t % p.oh);
+    const int64_t img = t / p.oh;
+    const int iy = nearest_src(oy, p.ih, p.oh, p.sh, p.coord, p.rule);
+    const int ix = nearest_src(ox, p.iw, p.ow, p.sw, p.coord, p.rule);
+    y[i] = x[((img * p.ih + iy) * p.iw + ix) * cpp + c];
+  }
+}
+
+hipError_t run_resize_nearest_nhwc(int elem_bytes, const void* x, void* y, int64_t images, int64_t C,
+                                   const ResizePlan& p, hipStream_t st) {
+  if ((C * elem_bytes) % 16 != 0 || (uintptr_t)x % 16 != 0 || (uintptr_t)y % 16 != 0) return hipErrorInvalidValue;
+  const int cpp = (int)(C * elem_bytes / 16);
+  const int64_t n = images * p.oh * p.ow * cpp;
+  if (n <= 0) return hipSuccess;
+  hipLaunchKernelGGL(resize_nearest_nhwc_kernel, dim3(grid_for(n)), dim3(kThreads), 0, st,
+                     static_cast<const uint4*>(x), static_cast<uint4*>(y), n, cpp, p);
+  return hipGetLastError();
+}
+
 hipError_t run_resize_nearest(int elem_bytes, const void* x, void* y, int64_t planes, const ResizePlan& p,
                               hipStream_t st) {
   const int64_t n = planes * p.oh * p.ow;
@@ -801,7 +831,12 @@ hipError_t run_maxpool(int dt, const void* x, void* y, int64_t planes, const Poo
       const dim3 g4(grid_for(n / 4));
       const uint32_t* xs = static_cast<const uint32_t*>(x);
       uint32_t* ys = static_cast<uint32_t*>(y);
-#define OHIP_POOL_B4(S)                                                                                          switch (k) {                                                                                                     case 3: hipLaunchKernelGGL((maxpool_nhwc_b4_kernel<S, 3>), g4, dim3(kThreads), 0, st, xs, ys, images, p); break;     case 5: hipLaunchKernelGGL((maxpool_nhwc_b4_kernel<S, 5>), g4, dim3(kThreads), 0, st, xs, ys, images, p); break;     default: hipLaunchKernelGGL((maxpool_nhwc_b4_kernel<S, 0>), g4, dim3(kThreads), 0, st, xs, ys, images, p); break;   }
+#define OHIP_POOL_B4(S)                                                                                  \
+  switch (k) {                                                                                           \
+    case 3: hipLaunchKernelGGL((maxpool_nhwc_b4_kernel<S, 3>), g4, dim3(kThreads), 0, st, xs, ys, images, p); break; \
+    case 5: hipLaunchKernelGGL((maxpool_nhwc_b4_kernel<S, 5>), g4, dim3(kThreads), 0, st, xs, ys, images, p); break; \
+    default: hipLaunchKernelGGL((maxpool_nhwc_b4_kernel<S, 0>), g4, dim3(kThreads), 0, st, xs, ys, images, p); break; \
+  }
       if (dt == DT_I8) { OHIP_POOL_B4(true) } else { OHIP_POOL_B4(false) }
 #undef OHIP_POOL_B4
       return hipGetLastError();

@@ -186,29 +186,36 @@ def _nhwc_reader(node, inits):
 def _plan_nhwc(nodes, keep_out, inits):
     """Layout hints for float activations: a Conv / OhipConvInstanceNorm
     output whose every consumer reads it in place as NHWC (the input of an
-    ungrouped conv with zero padding or on the halo path, or the residual of
-    a fused node that has the same shape) is produced NHWC ("out_nhwc"), which removes the consumers' NCHW
-    -> NHWC staging.  The dispatcher treats the hint as a preference and
-    converts for any consumer that cannot take the layout."""
+    ungrouped conv with zero padding or on the halo path, the residual of a
+    fused node that has the same shape, or a nearest Resize that is itself
+    hinted) is produced NHWC ("out_nhwc"), which removes the consumers' NCHW
+    -> NHWC staging; a nearest Resize (4-D, scales on H and W only) is
+    hinted when every consumer of its output reads NHWC, and then resizes
+    NHWC -> NHWC.  Nodes are visited from the end, so a consumer's hint is
+    known when its producer is decided.  The dispatcher treats the hints as
+    preferences and converts for any consumer that cannot take the layout."""
     cons = _consumers(nodes)
     out = list(nodes)
-    for i, n in enumerate(out):
-        if n.op not in ("Conv", "OhipConvInstanceNorm") or n.attrs.ints.get("group", 1) != 1:
+
+    def reads_nhwc(un, t):
+        if un.inputs and un.inputs[0] == t and _nhwc_reader(un, inits) and t not in un.inputs[1:5]:
+            return True
+        if un.op == "OhipConvInstanceNorm" and len(un.inputs) > 5 and un.inputs[5] == t and un.inputs[0] != t:
+            return True
+        return un.op == "Resize" and un.inputs and un.inputs[0] == t and un.attrs.ints.get("out_nhwc") == 1
+
+    for i in range(len(out) - 1, -1, -1):
+        n = out[i]
+        if n.op == "Resize":
+            if n.attrs.strings.get("mode") != "nearest" or "axes" in n.attrs.int_lists:
+                continue
+        elif n.op not in ("Conv", "OhipConvInstanceNorm") or n.attrs.ints.get("group", 1) != 1:
             continue
         t = n.outputs[0]
         users = cons.get(t, [])
         if t in keep_out or not users:
             continue
-        ok = True
-        for u in users:
-            un = out[u]
-            if un.inputs and un.inputs[0] == t and _nhwc_reader(un, inits) and t not in un.inputs[1:5]:
-                continue
-            if un.op == "OhipConvInstanceNorm" and len(un.inputs) > 5 and un.inputs[5] == t and un.inputs[0] != t:
-                continue
-            ok = False
-            break
-        if ok:
+        if all(reads_nhwc(out[u], t) for u in users):
             a = replace(n.attrs, ints=dict(n.attrs.ints))
             a.ints["out_nhwc"] = 1
             out[i] = replace(n, attrs=a)

@@ -610,6 +610,7 @@ def test_face_swap_nhwc_trunk_matches_nchw(ctx, dt):
     g, feeds = workloads.face_swap_generator(dtype=dt, n_blocks=2)
     nhwc = Session(g, ctx)
     assert sum(1 for n in nhwc.graph.nodes if n.attrs.ints.get("out_nhwc")) >= 3
+    assert any(n.op == "Resize" and n.attrs.ints.get("out_nhwc") for n in nhwc.graph.nodes)
     got = nhwc.run(feeds)
     want = Session(g, ctx, nhwc=False).run(feeds)
     for k in ("logits", "y"):
