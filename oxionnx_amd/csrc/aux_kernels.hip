@@ -785,6 +785,143 @@ hipError_t run_conv_fewout(int dtype, const void* x, const void* w, const void* 
   return hipGetLastError();
 }
 
+// Few output channels on the MFMA: an ungrouped stride-1 KH x KW
+// convolution of an NHWC f16 / bf16 input (an RGB head) whose 1-4 output
+// channels would fill a sliver of the engine's 64-column tiles, each tap
+// re-gathering its pixels from global memory.  A block takes one output row
+// (up to 128 pixels, a wave per 32) and a slice of input channels: per slab
+// of 16 channels it stages the row's input patch once, KH rows of OW + KW -
+// 1 pixels, with the zero / reflect / edge border applied by the loader, and
+// every tap reads its A fragments (32 pixels x 16 channels) from the patch
+// at pixel offset kx.  The slice's filter sits in LDS for the valid output
+// channels only; the other B columns are zero registers.  The slice's sums
+// go to the same partial-sum layout as the few-output kernel, whose
+// reduction adds the slices in order and applies bias and activation.
+constexpr int kFewCoMax = 4;        // output channels (B columns) kept
+constexpr int kFewCoSlab = 16;      // channels per slab (one k-step of a tap)
+
+template <Op O, class T, int KH, int KW>
+__global__ void __launch_bounds__(256) fewco_mfma_kernel(const T* __restrict__ x, const T* __restrict__ w,
+                                                         float* __restrict__ ws, DirectConvArgs a, int pitch,
+                                                         int cslice) {
+  constexpr int TAPS = KH * KW;
+  extern __shared__ u32x4 fsm[];
+  const int PW = a.OW + KW - 1;
+  const int slabs = cslice / kFewCoSlab;
+  u32x4* pat = fsm;                                 // [KH][PW][2] chunks
+  u32x4* wl = fsm + KH * PW * 2;                    // [slab][tap][2][kFewCoMax]
+  const int n = (int)blockIdx.x / a.OH, oy = (int)blockIdx.x % a.OH;
+  const int c0 = (int)blockIdx.y * cslice;
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int m = lane & 31, hh = lane >> 5;
+  const int nw = slabs * TAPS * 2 * kFewCoMax;
+  for (int i = t; i < nw; i += 256) {
+    const int co = i % kFewCoMax;
+    int r = i / kFewCoMax;
+    const int h = r & 1;
+    r >>= 1;
+    const int tap = r % TAPS, sl = r / TAPS;
+    u32x4 v = u32x4{0u, 0u, 0u, 0u};
+    if (co < a.cout) v = *reinterpret_cast<const u32x4*>(w + co * a.ldw + (int64_t)tap * a.cpg + c0 + sl * kFewCoSlab + h * 8);
+    wl[i] = v;
+  }
+  typename OpT<O>::Acc acc;
+#pragma unroll
+  for (int e = 0; e < 16; ++e) acc[e] = 0.0f;
+  const int px0 = wave * 32;
+  const T* xn = x + (int64_t)n * a.H * a.W * pitch;
+  const int np = KH * PW * 2;
+  for (int sl = 0; sl < slabs; ++sl) {
+    __syncthreads();   // the previous slab's patch has been read (the filter written, for slab 0)
+    const int cc = c0 + sl * kFewCoSlab;
+    for (int i = t; i < np; i += 256) {
+      const int h = i & 1, r = i >> 1;
+      const int px = r % PW, ky = r / PW;
+      int iy = oy + ky, ix = px;   // padded coordinates
+      bool ok = px < a.OW + KW - 1;
+      if (a.pad_mode == 0) {
+        iy -= a.pt;
+        ix -= a.pl;
+        ok = ok && (unsigned)iy < (unsigned)a.H && (unsigned)ix < (unsigned)a.W;
+      } else {
+        iy = pad_map(iy, a.pt, a.H, a.pad_mode);
+        ix = pad_map(ix, a.pl, a.W, a.pad_mode);
+      }
+      u32x4 v = u32x4{0u, 0u, 0u, 0u};
+      if (ok) v = *reinterpret_cast<const u32x4*>(xn + ((int64_t)iy * a.W + ix) * pitch + cc + h * 8);
+      pat[i] = v;
+    }
+    __syncthreads();
+    if (px0 < a.OW) {
+      const u32x4* wsl = wl + sl * TAPS * 2 * kFewCoMax;
+#pragma unroll
+      for (int ky = 0; ky < KH; ++ky)
+#pragma unroll
+        for (int kx = 0; kx < KW; ++kx) {
+          const u32x4 av = pat[((ky * PW) + px0 + m + kx) * 2 + hh];
+          const u32x4 bv = m < a.cout ? wsl[((ky * KW + kx) * 2 + hh) * kFewCoMax + m] : u32x4{0u, 0u, 0u, 0u};
+          acc = OpT<O>::mma(av, bv, acc);
+        }
+    }
+  }
+  // lane: pixels px0 + 8g + 4hh + e (rows of A), output channel m (column of B)
+  if (px0 < a.OW && m < a.cout) {
+    const int64_t plane = (int64_t)a.OH * a.OW;
+    float* dst = ws + (((int64_t)blockIdx.y * a.N + n) * a.cout + m) * plane + (int64_t)oy * a.OW;
+#pragma unroll
+    for (int g = 0; g < 4; ++g)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int px = px0 + 8 * g + 4 * hh + e;
+        if (px < a.OW) dst[px] = acc[4 * g + e];
+      }
+  }
+}
+
+int fewco_slice(const DirectConvArgs& a) {
+  // enough slices to give every CU about two blocks, at least one slab each
+  const int64_t rows = (int64_t)a.N * a.OH;
+  int slabs = a.C / kFewCoSlab, s = 1;
+  while (s < slabs && rows * s < 512 && slabs % (2 * s) == 0) s *= 2;
+  return a.C / s;
+}
+
+bool fewco_supported(int dtype, const DirectConvArgs& a, int pitch) {
+  if (dtype != DT_F16 && dtype != DT_BF16) return false;
+  if (a.cout > kFewCoMax || a.cout < 1 || a.OW > 128 || a.sh != 1 || a.sw != 1 || a.dh != 1 || a.dw != 1) return false;
+  if (a.KH != a.KW || (a.KH != 3 && a.KH != 5 && a.KH != 7)) return false;
+  if (a.C % kFewCoSlab != 0 || pitch % 8 != 0 || a.cpg % 8 != 0 || a.ldw % 8 != 0) return false;
+  const size_t lds = ((size_t)a.KH * (a.OW + a.KW - 1) * 2 + (size_t)(fewco_slice(a) / kFewCoSlab) * a.KH * a.KW * 2 * kFewCoMax) * 16;
+  return lds <= 64 * 1024;
+}
+
+hipError_t run_conv_fewco(int dtype, const void* x, int pitch, const void* w, const void* bias, void* y, float* ws,
+                          const DirectConvArgs& a, hipStream_t st) {
+  if (!fewco_supported(dtype, a, pitch)) return hipErrorInvalidValue;
+  const int cslice = fewco_slice(a);
+  const int slices = a.C / cslice;
+  const int64_t total = (int64_t)a.N * a.cout * a.OH * a.OW;
+  if (total <= 0) return hipSuccess;
+  const size_t lds = ((size_t)a.KH * (a.OW + a.KW - 1) * 2 + (size_t)(cslice / kFewCoSlab) * a.KH * a.KW * 2 * kFewCoMax) * 16;
+  const dim3 grid((unsigned)(a.N * a.OH), (unsigned)slices);
+  const unsigned rgrid = (unsigned)std::min<int64_t>((total + 255) / 256, 65535 * 16);
+#define OHIP_FEWCO(OP, T)                                                                                         \
+  switch (a.KH) {                                                                                                 \
+    case 3: hipLaunchKernelGGL((fewco_mfma_kernel<OP, T, 3, 3>), grid, dim3(256), lds, st, reinterpret_cast<const T*>(x), \
+                               reinterpret_cast<const T*>(w), ws, a, pitch, cslice); break;                         \
+    case 5: hipLaunchKernelGGL((fewco_mfma_kernel<OP, T, 5, 5>), grid, dim3(256), lds, st, reinterpret_cast<const T*>(x), \
+                               reinterpret_cast<const T*>(w), ws, a, pitch, cslice); break;                         \
+    default: hipLaunchKernelGGL((fewco_mfma_kernel<OP, T, 7, 7>), grid, dim3(256), lds, st, reinterpret_cast<const T*>(x), \
+                                reinterpret_cast<const T*>(w), ws, a, pitch, cslice); break;                        \
+  }                                                                                                               \
+  hipLaunchKernelGGL(fewout_reduce_kernel<T>, dim3(rgrid), dim3(256), 0, st, ws, reinterpret_cast<const T*>(bias), \
+                     reinterpret_cast<T*>(y), a, slices)
+  if (dtype == DT_F16) { OHIP_FEWCO(Op::F16, _Float16); }
+  else { OHIP_FEWCO(Op::BF16, __bf16); }
+#undef OHIP_FEWCO
+  return hipGetLastError();
+}
+
 hipError_t run_conv_direct(int dtype, const void* x, const void* w, const void* bias, void* y,
                            const DirectConvArgs& a, hipStream_t st) {
   const int64_t total = (int64_t)a.N * a.cout * a.OH * a.OW;

@@ -28,6 +28,7 @@ int ohip_dtensor_view_nhwc_internal(const ohip_dtensor* src, int64_t c0, int64_t
 int ohip_dtensor_to_nchw_internal(ohip_ctx* ctx, const ohip_dtensor* t, void* dst);
 int ohip_hip_error_internal(hipError_t e, const char* what);
 int ohip_conv_halo_splits_internal(ohip_ctx* ctx, const ohip_conv_desc* d);
+int ohip_conv_fewco_internal(const ohip_conv_desc* d);
 
 namespace {
 
@@ -549,7 +550,7 @@ bool conv_takes_nhwc(ohip_ctx* ctx, const ohip_node* nd) {
   // zero padding: the engine's implicit im2col reads the NHWC tensor as it
   // is; a reflect / edge pad is applied in place only by the halo path
   if (d.pad_mode == OHIP_PAD_ZEROS) return true;
-  return ohip_conv_halo_splits_internal(ctx, &d) > 0;
+  return ohip_conv_halo_splits_internal(ctx, &d) > 0 || ohip_conv_fewco_internal(&d) != 0;
 }
 
 // ------------------------------------------------------------------ ConvTranspose

@@ -254,6 +254,13 @@ hipError_t run_conv_direct(int dtype, const void* x, const void* w, const void* 
 // ceil(C / cslice) * N * cout * OH * OW floats.
 constexpr int kFewOutMax = 8;
 int fewout_slice(const DirectConvArgs& a);   // channels per slice for the LDS budget
+// The same few-output convolution on the MFMA for an NHWC f16 / bf16 input
+// (pitch: channel slots per pixel), stride and dilation 1, square 3 / 5 / 7
+// filters, at most 4 output channels, output rows up to 128 pixels.
+bool fewco_supported(int dtype, const DirectConvArgs& a, int pitch);
+int fewco_slice(const DirectConvArgs& a);
+hipError_t run_conv_fewco(int dtype, const void* x, int pitch, const void* w, const void* bias, void* y, float* ws,
+                          const DirectConvArgs& a, hipStream_t st);
 hipError_t run_conv_fewout(int dtype, const void* x, const void* w, const void* bias, void* y, float* ws,
                            const DirectConvArgs& a, int cslice, hipStream_t st);
 

@@ -1377,18 +1377,38 @@ static int conv2d_impl(ohip_ctx* ctx, const ohip_conv_desc* d, const void* x, co
   // itself runs in the NCHW orientation (channel planes contiguous in the
   // partial sums)
   const bool norm_nhwc = norm && d->out_layout == OHIP_NHWC;
-  if (norm && (direct || fewout || G != 1 || g.oh * g.ow > kNormPartialsMaxSpatial || d->dtype == OHIP_BF16))
+  DirectConvArgs a{};
+  a.N = (int)d->n; a.C = (int)d->c; a.H = (int)d->h; a.W = (int)d->w; a.cout = (int)d->cout;
+  a.cg = (int)cg; a.coutg = (int)coutg; a.KH = (int)d->kh; a.KW = (int)d->kw;
+  a.sh = (int)d->stride_h; a.sw = (int)d->stride_w; a.dh = (int)d->dil_h; a.dw = (int)d->dil_w;
+  a.pt = (int)d->pad_t; a.pl = (int)d->pad_l; a.pad_mode = fused_pad ? d->pad_mode : 0;
+  a.OH = (int)g.oh; a.OW = (int)g.ow; a.ldw = w->ld_bytes / eb; a.cpg = (int)cp;
+  a.nhwc_out = d->out_layout != OHIP_NCHW; a.ldo = ldo; a.act = act; a.lo = lo; a.hi = hi;
+  // An NHWC f16 / bf16 input with at most 4 output channels (an RGB head)
+  // runs the few-output MFMA kernel: a row's input patch staged once per
+  // channel slab instead of the engine's per-tap gather, whose 64-column
+  // tiles would be 1-4 columns full (128 -> 3 channels, 7x7, 128x128 with a
+  // reflect pad: 45.9 us staged on the engine).
+  const bool fewco = !direct && G == 1 && d->in_layout == OHIP_NHWC && few_out_allowed() &&
+                     fewco_supported(d->dtype, a, (int)cpt);
+  if (norm && (direct || fewout || fewco || G != 1 || g.oh * g.ow > kNormPartialsMaxSpatial || d->dtype == OHIP_BF16))
     return kNormTwoStep;
   std::lock_guard<std::mutex> lock(ctx->mu);
   ctx->counters.dispatches++;
+  if (fewco) {
+    const int64_t slices = d->c / fewco_slice(a);
+    ScratchPlan plan;
+    const size_t iw = plan.add((size_t)(slices * d->n * d->cout * ohw) * 4);
+    char* sbase = nullptr;
+    rc = call_scratch(ctx, plan.total(), noalloc, &sbase);
+    if (rc) return rc;
+    if (!aligned(x, 16)) return fail(OHIP_E_INVALID, "ohip_conv2d: NHWC input must be 16-byte aligned");
+    hipError_t e = run_conv_fewco(d->dtype, x, (int)cpt, w->data, bias, y, static_cast<float*>(plan_at(sbase, plan, iw)),
+                                  a, ctx->stream);
+    if (e != hipSuccess) return hip_fail(e, "ohip_conv2d few-output MFMA launch");
+    return OHIP_OK;
+  }
   if (direct || fewout) {
-    DirectConvArgs a{};
-    a.N = (int)d->n; a.C = (int)d->c; a.H = (int)d->h; a.W = (int)d->w; a.cout = (int)d->cout;
-    a.cg = (int)cg; a.coutg = (int)coutg; a.KH = (int)d->kh; a.KW = (int)d->kw;
-    a.sh = (int)d->stride_h; a.sw = (int)d->stride_w; a.dh = (int)d->dil_h; a.dw = (int)d->dil_w;
-    a.pt = (int)d->pad_t; a.pl = (int)d->pad_l; a.pad_mode = fused_pad ? d->pad_mode : 0;
-    a.OH = (int)g.oh; a.OW = (int)g.ow; a.ldw = w->ld_bytes / eb; a.cpg = (int)cp;
-    a.nhwc_out = d->out_layout != OHIP_NCHW; a.ldo = ldo; a.act = act; a.lo = lo; a.hi = hi;
     if (fewout) {
       const int cslice = fewout_slice(a);
       const int64_t slices = (d->c + cslice - 1) / cslice;
@@ -1572,6 +1592,25 @@ int ohip_conv_halo_splits_internal(ohip_ctx* ctx, const ohip_conv_desc* d) {
   const int eb = elem_bytes(d->dtype), ce = 16 / eb;
   const int64_t cp = round_up(d->c, ce);
   return halo_plan(ctx, d, 1, d->w, g, (int)(cp / ce), d->h * d->w * cp * eb);
+}
+
+// Whether ohip_conv2d would run this convolution of a resident NHWC input
+// (channel pitch = the channels padded to 16 bytes) on the few-output MFMA
+// kernel, which applies a fused reflect / edge pad in its loader.
+int ohip_conv_fewco_internal(const ohip_conv_desc* d) {
+  if (!d || d->group != 1 || !is_float(d->dtype) || !few_out_allowed()) return 0;
+  ConvGeo g;
+  if (conv_geo(d->h, d->w, d->kh, d->kw, d->stride_h, d->stride_w, d->dil_h, d->dil_w, d->pad_t, d->pad_l, d->pad_b,
+               d->pad_r, &g) != OHIP_OK)
+    return 0;
+  const int ce = 16 / elem_bytes(d->dtype);
+  const int64_t cp = round_up(d->c, ce);
+  DirectConvArgs a{};
+  a.N = (int)d->n; a.C = (int)d->c; a.H = (int)d->h; a.W = (int)d->w; a.cout = (int)d->cout;
+  a.KH = (int)d->kh; a.KW = (int)d->kw; a.sh = (int)d->stride_h; a.sw = (int)d->stride_w;
+  a.dh = (int)d->dil_h; a.dw = (int)d->dil_w; a.OH = (int)g.oh; a.OW = (int)g.ow;
+  a.cpg = (int)cp; a.ldw = d->kh * d->kw * cp;
+  return fewco_supported(d->dtype, a, (int)cp) ? 1 : 0;
 }
 
 // Conv -> instance normalisation.  With a split-K plan the normalisation

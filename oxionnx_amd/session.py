@@ -163,9 +163,11 @@ def fuse(graph: Graph, level: str = "all", nhwc: bool = True) -> Graph:
 def _nhwc_reader(node, inits):
     """A conv the device runs on a resident NHWC input in place: ungrouped,
     an f32 / f16 filter, and either zero padding (the engine's implicit
-    im2col reads NHWC as it is) or the halo-patch geometry (3x3, stride and
-    dilation 1), whose loader applies a fused reflect / edge Pad.  The
-    dispatcher checks extents and sizes and converts otherwise."""
+    im2col reads NHWC as it is) or a fused reflect / edge Pad that a loader
+    applies: the halo-patch geometry (3x3, stride and dilation 1) or the
+    few-output MFMA kernel (f16, at most 4 output channels, square 5x5 /
+    7x7).  The dispatcher checks dtypes, extents and sizes and converts
+    otherwise."""
     if node.op not in ("Conv", "OhipConvInstanceNorm"):
         return False
     a = node.attrs
@@ -179,8 +181,11 @@ def _nhwc_reader(node, inits):
         return False
     if a.strings.get("pad_mode", "constant") in ("constant", ""):
         return True
-    return (wd.shape[2:] == (3, 3) and all(v == 1 for v in a.int_lists.get("strides", [1, 1]))
+    unit = (all(v == 1 for v in a.int_lists.get("strides", [1, 1]))
             and all(v == 1 for v in a.int_lists.get("dilations", [1, 1])))
+    # the halo-patch path (3x3), or the few-output kernel (an RGB head)
+    return unit and (wd.shape[2:] == (3, 3) or (wd.dtype == np.float16 and wd.shape[0] <= 4
+                                                and wd.shape[2] == wd.shape[3] and wd.shape[2] in (5, 7)))
 
 
 def _plan_nhwc(nodes, keep_out, inits):

@@ -604,14 +604,24 @@ def test_conv_instnorm_fusion_matches_unfused(ctx, case):
 
 @pytest.mark.parametrize("dt", ["f16", "f32"])
 def test_face_swap_nhwc_trunk_matches_nchw(ctx, dt):
-    """The residual trunk kept NHWC between its convolutions (halo-patch convs
-    reading the reflect pad in place, norms writing NHWC) gives the same bits
-    as the NCHW forward with its staging transposes."""
+    """Everything from the stem's output to the last upsampling conv kept
+    NHWC (convs reading it in place, halo-patch convs applying the reflect
+    pad, norms and Resize writing NHWC) gives the same bits as the NCHW
+    forward with its staging transposes.  The RGB head after it is compared
+    within tolerance: on an NHWC f16 input it runs the few-output MFMA
+    kernel, on an NCHW one the engine, which sum in different orders."""
     g, feeds = workloads.face_swap_generator(dtype=dt, n_blocks=2)
-    nhwc = Session(g, ctx)
+    head_pad = max(i for i, n in enumerate(g.nodes) if n.op == "Pad")
+    trunk_out = g.nodes[head_pad].inputs[0]
+    trunk = Graph(g.nodes[:head_pad], g.initializers, g.inputs, [trunk_out])
+    nhwc = Session(trunk, ctx)
     assert sum(1 for n in nhwc.graph.nodes if n.attrs.ints.get("out_nhwc")) >= 3
     assert any(n.op == "Resize" and n.attrs.ints.get("out_nhwc") for n in nhwc.graph.nodes)
-    got = nhwc.run(feeds)
+    np.testing.assert_array_equal(nhwc.run(feeds)[trunk_out], Session(trunk, ctx, nhwc=False).run(feeds)[trunk_out])
+    got = Session(g, ctx).run(feeds)
     want = Session(g, ctx, nhwc=False).run(feeds)
     for k in ("logits", "y"):
-        np.testing.assert_array_equal(got[k], want[k], err_msg=k)
+        if dt == "f32":
+            np.testing.assert_array_equal(got[k], want[k], err_msg=k)
+        else:
+            close(got[k], want[k], 2e-3)

@@ -472,6 +472,51 @@ def test_halo_conv_matches_oracle(torch, ctx, case, dt, nhwc_out):
     assert _rel_err(got, want) <= HALF_TOL
 
 
+# ------------------------------------------------------------------ few output channels on the MFMA
+FEWCO_CASES = [
+    # (N, C, H, W, cout, k, pad mode)
+    (1, 128, 20, 24, 3, 7, "reflect"),
+    (2, 32, 9, 16, 4, 5, "edge"),
+    (1, 16, 7, 128, 1, 3, "zeros"),
+    (1, 64, 12, 100, 3, 7, "zeros"),
+]
+
+
+@pytest.mark.parametrize("case", FEWCO_CASES, ids=str)
+@pytest.mark.parametrize("bf16", [False, True], ids=["f16", "bf16"])
+def test_fewout_mfma_conv_matches_oracle(torch, ctx, case, bf16):
+    """An NHWC f16 / bf16 conv with at most 4 output channels (the few-output
+    MFMA kernel: a row's input patch staged per 16-channel slab, the border
+    applied by its loader) against the oracle conv of the padded image."""
+    import ctypes
+
+    from oxionnx_amd import _lib as L
+    n, c, h, wd, cout, k, mode = case
+    p = k // 2
+    rng = np.random.default_rng(c + cout + k + h)
+    x = rng.uniform(-1, 1, (n, c, h, wd)).astype(np.float32)
+    w = rng.normal(0, 0.05, (cout, c, k, k)).astype(np.float32)
+    b = rng.normal(0, 0.01, cout).astype(np.float32)
+    xh, wh, bh = (O.f32_to_half_bits(v, bf16) for v in (x, w, b))
+    tdt = torch.bfloat16 if bf16 else torch.float16
+    ldt = L.BF16 if bf16 else L.F16
+    wt = ctx.weight_conv(O.half_bits_to_f32(wh, bf16), dtype=ldt)
+    xn = torch.from_numpy(xh.view(np.int16)).cuda().view(tdt).permute(0, 2, 3, 1).contiguous()
+    bt = torch.from_numpy(bh.view(np.int16)).cuda().view(tdt)
+    y = torch.empty((n, cout, h, wd), dtype=tdt, device="cuda")
+    pm = {"zeros": L.PAD_ZEROS, "reflect": L.PAD_REFLECT, "edge": L.PAD_EDGE}[mode]
+    d = L.ConvDesc(n, c, h, wd, cout, k, k, 1, 1, 1, 1, 1, p, p, p, p, ldt, L.NHWC, L.NCHW, L.ACT_NONE, 0.0, 0.0, pm)
+    L.check(L.lib().ohip_conv2d(ctx.h, ctypes.byref(d), ctypes.c_void_p(xn.data_ptr()), wt.handle,
+                                ctypes.c_void_p(bt.data_ptr()), ctypes.c_void_p(y.data_ptr())))
+    got = O.half_bits_to_f32(y.view(torch.int16).cpu().numpy().view(np.uint16), bf16)
+    if mode == "zeros":
+        want = O.conv_half(xh, wh, bh, bf16=bf16, pads=(p, p, p, p))
+    else:
+        xp = np.pad(xh, ((0, 0), (0, 0), (p, p), (p, p)), mode="reflect" if mode == "reflect" else "edge")
+        want = O.conv_half(xp, wh, bh, bf16=bf16, pads=(0, 0, 0, 0))
+    assert _rel_err(got, O.half_bits_to_f32(want, bf16)) <= HALF_TOL
+
+
 # ------------------------------------------------------------------ fused conv + instance norm
 CONV_NORM_KERNEL_CASES = [
     ((1, 64, 32, 32), 128, "f32", True, True),

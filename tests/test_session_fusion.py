@@ -82,20 +82,23 @@ def test_conv_instnorm_fusion_attributes():
     assert not any(n.op == "Add" for n in nodes)
 
 
-def test_nhwc_plan_hints_conv_and_resize_chains():
+@pytest.mark.parametrize("dt", ["f16", "f32"])
+def test_nhwc_plan_hints_conv_and_resize_chains(dt):
     """The layout plan marks a conv output NHWC when every consumer reads it
-    in place (a zero-padded ungrouped conv, a hinted nearest Resize), and
-    leaves graph outputs and reflect-padded non-3x3 readers alone."""
+    in place (a zero-padded ungrouped conv, a hinted nearest Resize, the
+    reflect-padded RGB head in f16, whose few-output MFMA kernel pads in its
+    loader), never a graph output, and not the f32 head's input (its
+    few-output kernel reads NCHW)."""
     from oxionnx_amd import workloads
-    g, _ = workloads.face_swap_generator(dtype="f16", n_blocks=1)
+    g, _ = workloads.face_swap_generator(dtype=dt, n_blocks=1)
     nodes = fuse(g).nodes
     hinted = {n.outputs[0] for n in nodes if n.attrs.ints.get("out_nhwc")}
     by_out = {n.outputs[0]: n for n in nodes}
     assert not hinted & set(g.outputs)
     resizes = [n for n in nodes if n.op == "Resize"]
     assert resizes and all(n.attrs.ints.get("out_nhwc") for n in resizes)
-    # the head conv (7x7, reflect pad) reads NCHW: its input is not hinted
     head = [n for n in nodes if n.op == "Conv" and n.attrs.strings.get("pad_mode") == "reflect"
-            and n.attrs.int_lists.get("kernel_shape") == [7, 7]]
-    assert head and all(h.inputs[0] not in hinted for h in head if h.inputs[0] != "x")
+            and n.attrs.int_lists.get("kernel_shape") == [7, 7] and n.inputs[0] != "x"]
+    assert len(head) == 1
+    assert (head[0].inputs[0] in hinted) == (dt == "f16")
     assert any(by_out[t].op in ("Conv", "OhipConvInstanceNorm") for t in hinted)
