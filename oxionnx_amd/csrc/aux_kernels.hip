@@ -815,41 +815,64 @@ __global__ void __launch_bounds__(256) fewco_mfma_kernel(const T* __restrict__ x
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const int m = lane & 31, hh = lane >> 5;
   const int nw = slabs * TAPS * 2 * kFewCoMax;
-  for (int i = t; i < nw; i += 256) {
-    const int co = i % kFewCoMax;
-    int r = i / kFewCoMax;
-    const int h = r & 1;
-    r >>= 1;
-    const int tap = r % TAPS, sl = r / TAPS;
-    u32x4 v = u32x4{0u, 0u, 0u, 0u};
-    if (co < a.cout) v = *reinterpret_cast<const u32x4*>(w + co * a.ldw + (int64_t)tap * a.cpg + c0 + sl * kFewCoSlab + h * 8);
-    wl[i] = v;
-  }
-  typename OpT<O>::Acc acc;
+  for (int base = t; base < nw; base += 256 * 4) {   // four loads in flight a thread
+    u32x4 v[4];
 #pragma unroll
-  for (int e = 0; e < 16; ++e) acc[e] = 0.0f;
+    for (int u = 0; u < 4; ++u) {
+      const int i = base + u * 256;
+      const int co = i % kFewCoMax;
+      int r = i / kFewCoMax;
+      const int h = r & 1;
+      r >>= 1;
+      const int tap = r % TAPS, sl = r / TAPS;
+      v[u] = i < nw && co < a.cout
+                 ? *reinterpret_cast<const u32x4*>(w + co * a.ldw + (int64_t)tap * a.cpg + c0 + sl * kFewCoSlab + h * 8)
+                 : u32x4{0u, 0u, 0u, 0u};
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+      if (base + u * 256 < nw) wl[base + u * 256] = v[u];
+  }
+  // taps alternate over kChains independent accumulators (one chain of
+  // dependent MFMAs would wait out each one's latency)
+  constexpr int kChains = 4;
+  typename OpT<O>::Acc acc[kChains];
+#pragma unroll
+  for (int j = 0; j < kChains; ++j)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) acc[j][e] = 0.0f;
   const int px0 = wave * 32;
   const T* xn = x + (int64_t)n * a.H * a.W * pitch;
   const int np = KH * PW * 2;
   for (int sl = 0; sl < slabs; ++sl) {
     __syncthreads();   // the previous slab's patch has been read (the filter written, for slab 0)
     const int cc = c0 + sl * kFewCoSlab;
-    for (int i = t; i < np; i += 256) {
-      const int h = i & 1, r = i >> 1;
-      const int px = r % PW, ky = r / PW;
-      int iy = oy + ky, ix = px;   // padded coordinates
-      bool ok = px < a.OW + KW - 1;
-      if (a.pad_mode == 0) {
-        iy -= a.pt;
-        ix -= a.pl;
-        ok = ok && (unsigned)iy < (unsigned)a.H && (unsigned)ix < (unsigned)a.W;
-      } else {
-        iy = pad_map(iy, a.pt, a.H, a.pad_mode);
-        ix = pad_map(ix, a.pl, a.W, a.pad_mode);
+    // the patch's loads are issued in batches of 8 before any LDS store, so
+    // a thread's loads overlap instead of each waiting a round trip
+    constexpr int B = 8;
+    for (int base = t; base < np; base += 256 * B) {
+      u32x4 v[B];
+#pragma unroll
+      for (int u = 0; u < B; ++u) {
+        const int i = base + u * 256;
+        const int h = i & 1, r = i >> 1;
+        const int px = r % PW, ky = r / PW;
+        int iy = oy + ky, ix = px;   // padded coordinates
+        bool ok = i < np;
+        if (a.pad_mode == 0) {
+          iy -= a.pt;
+          ix -= a.pl;
+          ok = ok && (unsigned)iy < (unsigned)a.H && (unsigned)ix < (unsigned)a.W;
+        } else {
+          iy = pad_map(iy, a.pt, a.H, a.pad_mode);
+          ix = pad_map(ix, a.pl, a.W, a.pad_mode);
+        }
+        v[u] = ok ? *reinterpret_cast<const u32x4*>(xn + ((int64_t)iy * a.W + ix) * pitch + cc + h * 8)
+                  : u32x4{0u, 0u, 0u, 0u};
       }
-      u32x4 v = u32x4{0u, 0u, 0u, 0u};
-      if (ok) v = *reinterpret_cast<const u32x4*>(xn + ((int64_t)iy * a.W + ix) * pitch + cc + h * 8);
-      pat[i] = v;
+#pragma unroll
+      for (int u = 0; u < B; ++u)
+        if (base + u * 256 < np) pat[base + u * 256] = v[u];
     }
     __syncthreads();
     if (px0 < a.OW) {
@@ -860,10 +883,12 @@ __global__ void __launch_bounds__(256) fewco_mfma_kernel(const T* __restrict__ x
         for (int kx = 0; kx < KW; ++kx) {
           const u32x4 av = pat[((ky * PW) + px0 + m + kx) * 2 + hh];
           const u32x4 bv = m < a.cout ? wsl[((ky * KW + kx) * 2 + hh) * kFewCoMax + m] : u32x4{0u, 0u, 0u, 0u};
-          acc = OpT<O>::mma(av, bv, acc);
+          acc[(ky * KW + kx) % kChains] = OpT<O>::mma(av, bv, acc[(ky * KW + kx) % kChains]);
         }
     }
   }
+#pragma unroll
+  for (int j = 1; j < kChains; ++j) acc[0] += acc[j];
   // lane: pixels px0 + 8g + 4hh + e (rows of A), output channel m (column of B)
   if (px0 < a.OW && m < a.cout) {
     const int64_t plane = (int64_t)a.OH * a.OW;
@@ -873,7 +898,7 @@ __global__ void __launch_bounds__(256) fewco_mfma_kernel(const T* __restrict__ x
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const int px = px0 + 8 * g + 4 * hh + e;
-        if (px < a.OW) dst[px] = acc[4 * g + e];
+        if (px < a.OW) dst[px] = acc[0][4 * g + e];
       }
   }
 }
