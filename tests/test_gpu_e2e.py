@@ -602,6 +602,33 @@ def test_conv_instnorm_fusion_matches_unfused(ctx, case):
     close(got, ref, 1e-2 if dt == "f16" else 1e-4)
 
 
+@pytest.mark.parametrize("coord", ["half_pixel", "asymmetric", "align_corners"])
+@pytest.mark.parametrize("scales", [(1, 1, 2, 2), (1, 1, 1.5, 0.75), (1, 1, 3, 2.5)], ids=str)
+@pytest.mark.parametrize("dt", [np.float16, np.float32], ids=["f16", "f32"])
+def test_nhwc_resize_between_convs(ctx, coord, scales, dt):
+    """Conv -> nearest Resize -> Conv with the layout plan keeping both
+    intermediates NHWC (the Resize runs NHWC -> NHWC) equals the NCHW forward
+    bit for bit (16 output channels: both forwards run the second conv on
+    the engine), and the oracle within the dtype's bar."""
+    rng = np.random.default_rng(int(scales[2] * 10 + scales[3] * 100))
+    inits = {"wa": rng.normal(0, 0.1, (16, 8, 3, 3)).astype(dt), "ba": rng.normal(0, 0.1, 16).astype(dt),
+             "wb": rng.normal(0, 0.1, (16, 16, 3, 3)).astype(dt), "bb": rng.normal(0, 0.1, 16).astype(dt),
+             "sc": np.asarray(scales, np.float32)}
+    conv = {"kernel_shape": [3, 3], "pads": [1, 1, 1, 1]}
+    nodes = [ep.Node("Conv", ["x", "wa", "ba"], ["a"], A(int_lists=conv)),
+             ep.Node("Resize", ["a", "", "sc"], ["r"], A(strings={"mode": "nearest",
+                                                                 "coordinate_transformation_mode": coord})),
+             ep.Node("Conv", ["r", "wb", "bb"], ["y"], A(int_lists=conv))]
+    g = unique_graph(nodes, inits, ["x"], ["y"])
+    feeds = {"x": rng.uniform(-1, 1, (2, 8, 10, 14)).astype(dt)}
+    s = Session(g, ctx)
+    assert [n.attrs.ints.get("out_nhwc", 0) for n in s.graph.nodes] == [1, 1, 0]
+    got = s.run(feeds)["y"]
+    np.testing.assert_array_equal(got, Session(g, ctx, nhwc=False).run(feeds)["y"])
+    ref = G.run_graph(g, feeds, half=(dt == np.float16))["y"]
+    close(got, ref, 1e-2 if dt == np.float16 else 1e-4)
+
+
 @pytest.mark.parametrize("dt", ["f16", "f32"])
 def test_face_swap_nhwc_trunk_matches_nchw(ctx, dt):
     """Everything from the stem's output to the last upsampling conv kept
