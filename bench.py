@@ -245,7 +245,7 @@ def bench_conv(torch, ctx, L, stream, rng, only):
     fl = 2.0 * 64 * 128 * 128 * 64 * 9
     return {"conv_cfg1_f32": {"ms": round(t, 5), "tflops": round(fl / t / 1e9, 2),
                               "frac_mfma": round(fl / t / 1e9 / PEAK_TFLOPS["f32"], 4),
-                              "note": "includes the NCHW->NHWC staging transpose"}}
+                              "note": "NCHW input and output as the ONNX node has them (no layout staging is needed on this path)"}}
 
 
 def bench_int8(torch, ctx, L, stream, rng, only):

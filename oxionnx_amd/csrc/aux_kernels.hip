@@ -947,6 +947,153 @@ hipError_t run_conv_fewco(int dtype, const void* x, int pitch, const void* w, co
   return hipGetLastError();
 }
 
+// f32 stride-1 convolution straight from an NCHW input (config 1's shape):
+// the f32 MFMA takes one element of each operand per lane, so a block can
+// stage, per slab of 8 input channels, the channel-major input patch of its
+// output row segment (KH rows of 64 + KW - 1 pixels, zero border) and the
+// slab's filter ([64 output channels][taps x 8 channels]) in LDS and run every
+// tap from the patch at pixel offset kx: no NHWC staging transpose, and the
+// input is fetched once per slab instead of once per tap.  A block is one
+// 64-pixel segment of an output row x 64 output channels, four waves of
+// 32 x 32; the next slab's loads are issued into registers before the
+// current slab's MFMAs and stored after them (two LDS buffers).  k runs
+// (tap, channel): MFMA step j covers k = 2j, 2j + 1, one tap and channels
+// 2j % 8 + {0, 1}, so both operands' addresses are a per-lane base plus a
+// compile-time offset.
+constexpr int kF32Seg = 64, kF32Co = 64, kF32Cs = 8;
+
+template <int KH, int KW, bool MAPPED>
+__global__ void __launch_bounds__(256) conv_nchw_f32_kernel(const float* __restrict__ x, const float* __restrict__ w,
+                                                            const float* __restrict__ bias, float* __restrict__ y,
+                                                            DirectConvArgs a) {
+  constexpr int TAPS = KH * KW, KS = TAPS * kF32Cs;           // k per slab
+  constexpr int PWP = kF32Seg + KW - 1;                       // patch row
+  constexpr int PATCH = kF32Cs * KH * PWP;                    // floats
+  constexpr int FST = KS + 1;                                 // filter row stride (odd: no bank conflicts)
+  constexpr int FILT = kF32Co * FST;
+  constexpr int NP = (PATCH + 255) / 256, NF = (kF32Co * TAPS * 2 + 255) / 256;
+  __shared__ float lds[2][PATCH + FILT];
+  const int segs = (a.OW + kF32Seg - 1) / kF32Seg;
+  const int seg = (int)blockIdx.x % segs;
+  const int oy = ((int)blockIdx.x / segs) % a.OH, n = (int)blockIdx.x / segs / a.OH;
+  const int co0 = (int)blockIdx.y * kF32Co, ox0 = seg * kF32Seg;
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int wp = wave & 1, wq = wave >> 1, m = lane & 31, kk = lane >> 5;
+  const float* xn = x + (int64_t)n * a.C * a.H * a.W;
+  const int slabs = (a.C + kF32Cs - 1) / kF32Cs;
+
+  float pv[NP];
+  f32x4 fv[NF];
+  auto load = [&](int sl) __attribute__((always_inline)) {
+    const int c0 = sl * kF32Cs;
+#pragma unroll
+    for (int u = 0; u < NP; ++u) {
+      const int i = t + u * 256;
+      const int px = i % PWP, r = i / PWP, ky = r % KH, c = r / KH;
+      int iy = oy + ky, ix = ox0 + px;   // padded coordinates
+      bool ok = i < PATCH && c0 + c < a.C;
+      if constexpr (!MAPPED) {
+        iy -= a.pt;
+        ix -= a.pl;
+        ok = ok && (unsigned)iy < (unsigned)a.H && (unsigned)ix < (unsigned)a.W;
+      } else {
+        iy = pad_map(iy, a.pt, a.H, a.pad_mode);
+        ix = pad_map(ix, a.pl, a.W, a.pad_mode);
+      }
+      pv[u] = ok ? xn[((int64_t)(c0 + c) * a.H + iy) * a.W + ix] : 0.0f;
+    }
+#pragma unroll
+    for (int u = 0; u < NF; ++u) {
+      const int i = t + u * 256;        // (co, tap, half)
+      const int h = i & 1, r = i >> 1, tap = r % TAPS, co = r / TAPS;
+      const bool ok = i < kF32Co * TAPS * 2 && co0 + co < a.cout && c0 + 4 * h < a.cpg;
+      fv[u] = ok ? *reinterpret_cast<const f32x4*>(w + (int64_t)(co0 + co) * a.ldw + (int64_t)tap * a.cpg + c0 + 4 * h)
+                 : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+  };
+  auto store = [&](int b) __attribute__((always_inline)) {
+    float* pd = lds[b];
+    float* fd = lds[b] + PATCH;
+#pragma unroll
+    for (int u = 0; u < NP; ++u)
+      if (t + u * 256 < PATCH) pd[t + u * 256] = pv[u];
+#pragma unroll
+    for (int u = 0; u < NF; ++u) {
+      const int i = t + u * 256;
+      if (i < kF32Co * TAPS * 2) {
+        const int h = i & 1, r = i >> 1, tap = r % TAPS, co = r / TAPS;
+        float* d = fd + co * FST + tap * kF32Cs + 4 * h;
+        d[0] = fv[u][0]; d[1] = fv[u][1]; d[2] = fv[u][2]; d[3] = fv[u][3];
+      }
+    }
+  };
+
+  f32x16 acc;
+#pragma unroll
+  for (int e = 0; e < 16; ++e) acc[e] = 0.0f;
+  const int abase = kk * KH * PWP + wp * 32 + m;   // channel kk of the pair, this lane's pixel
+  const int bbase = (wq * 32 + m) * FST + kk;
+  load(0);
+  store(0);
+  __syncthreads();
+  for (int sl = 0; sl < slabs; ++sl) {
+    const int b = sl & 1;
+    if (sl + 1 < slabs) load(sl + 1);
+    const float* pa = lds[b] + abase;
+    const float* pb = lds[b] + PATCH + bbase;
+#pragma unroll
+    for (int j = 0; j < KS / 2; ++j) {
+      const int tap = (2 * j) / kF32Cs, cp2 = (2 * j) % kF32Cs;
+      const int ky = tap / KW, kx = tap % KW;
+      const float av = pa[(cp2 * KH + ky) * PWP + kx];
+      const float bv = pb[2 * j];
+      acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av, bv, acc, 0, 0, 0);
+    }
+    if (sl + 1 < slabs) store(b ^ 1);
+    __syncthreads();
+  }
+  // lane: pixels wp * 32 + 8g + 4kk + e, output channel wq * 32 + m
+  const int co = co0 + wq * 32 + m;
+  if (co >= a.cout) return;
+  const float bi = bias ? bias[co] : -0.0f;
+  float* yr = y + (((int64_t)n * a.cout + co) * a.OH + oy) * a.OW;
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    const int px = ox0 + wp * 32 + 8 * g + 4 * kk;
+    float v[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[e] = activate(acc[4 * g + e] + bi, a.act, a.lo, a.hi);
+    if (px + 3 < a.OW && (a.OW & 3) == 0) {
+      *reinterpret_cast<f32x4*>(yr + px) = f32x4{v[0], v[1], v[2], v[3]};
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if (px + e < a.OW) yr[px + e] = v[e];
+    }
+  }
+}
+
+bool conv_nchw_f32_supported(const DirectConvArgs& a) {
+  return a.KH == a.KW && (a.KH == 3 || (a.KH == 1 && a.pad_mode == 0)) && a.sh == 1 && a.sw == 1 && a.dh == 1 && a.dw == 1 &&
+         !a.nhwc_out && a.cpg % 4 == 0 && a.ldw % 4 == 0;
+}
+
+hipError_t run_conv_nchw_f32(const float* x, const float* w, const float* bias, float* y, const DirectConvArgs& a,
+                             hipStream_t st) {
+  if (!conv_nchw_f32_supported(a)) return hipErrorInvalidValue;
+  const int64_t blocks = (int64_t)a.N * a.OH * ((a.OW + kF32Seg - 1) / kF32Seg);
+  if (blocks <= 0) return hipSuccess;
+  if (blocks > 0x7fffffff) return hipErrorInvalidValue;
+  const dim3 grid((unsigned)blocks, (unsigned)((a.cout + kF32Co - 1) / kF32Co));
+  if (a.KH == 3 && a.pad_mode != 0)
+    hipLaunchKernelGGL((conv_nchw_f32_kernel<3, 3, true>), grid, dim3(256), 0, st, x, w, bias, y, a);
+  else if (a.KH == 3)
+    hipLaunchKernelGGL((conv_nchw_f32_kernel<3, 3, false>), grid, dim3(256), 0, st, x, w, bias, y, a);
+  else
+    hipLaunchKernelGGL((conv_nchw_f32_kernel<1, 1, false>), grid, dim3(256), 0, st, x, w, bias, y, a);
+  return hipGetLastError();
+}
+
 hipError_t run_conv_direct(int dtype, const void* x, const void* w, const void* bias, void* y,
                            const DirectConvArgs& a, hipStream_t st) {
   const int64_t total = (int64_t)a.N * a.cout * a.OH * a.OW;

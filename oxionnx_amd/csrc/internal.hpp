@@ -261,6 +261,11 @@ bool fewco_supported(int dtype, const DirectConvArgs& a, int pitch);
 int fewco_slice(const DirectConvArgs& a);
 hipError_t run_conv_fewco(int dtype, const void* x, int pitch, const void* w, const void* bias, void* y, float* ws,
                           const DirectConvArgs& a, hipStream_t st);
+// f32, stride and dilation 1, zero padding, 3x3 or 1x1, NCHW input and output
+// (the patch-staged MFMA kernel)
+bool conv_nchw_f32_supported(const DirectConvArgs& a);
+hipError_t run_conv_nchw_f32(const float* x, const float* w, const float* bias, float* y, const DirectConvArgs& a,
+                             hipStream_t st);
 hipError_t run_conv_fewout(int dtype, const void* x, const void* w, const void* bias, void* y, float* ws,
                            const DirectConvArgs& a, int cslice, hipStream_t st);
 

@@ -608,8 +608,8 @@ def test_conv_instnorm_fusion_matches_unfused(ctx, case):
 def test_nhwc_resize_between_convs(ctx, coord, scales, dt):
     """Conv -> nearest Resize -> Conv with the layout plan keeping both
     intermediates NHWC (the Resize runs NHWC -> NHWC) equals the NCHW forward
-    bit for bit (16 output channels: both forwards run the second conv on
-    the engine), and the oracle within the dtype's bar."""
+    (bit for bit in f16, where both forwards run the same kernels), and the
+    oracle within the dtype's bar."""
     rng = np.random.default_rng(int(scales[2] * 10 + scales[3] * 100))
     inits = {"wa": rng.normal(0, 0.1, (16, 8, 3, 3)).astype(dt), "ba": rng.normal(0, 0.1, 16).astype(dt),
              "wb": rng.normal(0, 0.1, (16, 16, 3, 3)).astype(dt), "bb": rng.normal(0, 0.1, 16).astype(dt),
@@ -624,7 +624,11 @@ def test_nhwc_resize_between_convs(ctx, coord, scales, dt):
     s = Session(g, ctx)
     assert [n.attrs.ints.get("out_nhwc", 0) for n in s.graph.nodes] == [1, 1, 0]
     got = s.run(feeds)["y"]
-    np.testing.assert_array_equal(got, Session(g, ctx, nhwc=False).run(feeds)["y"])
+    want = Session(g, ctx, nhwc=False).run(feeds)["y"]
+    if dt == np.float16:
+        np.testing.assert_array_equal(got, want)
+    else:   # the NCHW forward's first conv runs the patch-staged f32 kernel, the NHWC one the engine
+        close(got, want, 1e-5)
     ref = G.run_graph(g, feeds, half=(dt == np.float16))["y"]
     close(got, ref, 1e-2 if dt == np.float16 else 1e-4)
 
@@ -634,9 +638,11 @@ def test_face_swap_nhwc_trunk_matches_nchw(ctx, dt):
     """Everything from the stem's output to the last upsampling conv kept
     NHWC (convs reading it in place, halo-patch convs applying the reflect
     pad, norms and Resize writing NHWC) gives the same bits as the NCHW
-    forward with its staging transposes.  The RGB head after it is compared
-    within tolerance: on an NHWC f16 input it runs the few-output MFMA
-    kernel, on an NCHW one the engine, which sum in different orders."""
+    forward with its staging transposes in f16 (in f32 the NCHW forward runs
+    its 128x128 upsampling conv on the patch-staged f32 kernel, and is held
+    to 1e-5).  The RGB head after it is compared within tolerance: on an
+    NHWC f16 input it runs the few-output MFMA kernel, on an NCHW one the
+    engine, which sum in different orders."""
     g, feeds = workloads.face_swap_generator(dtype=dt, n_blocks=2)
     head_pad = max(i for i, n in enumerate(g.nodes) if n.op == "Pad")
     trunk_out = g.nodes[head_pad].inputs[0]
@@ -644,11 +650,12 @@ def test_face_swap_nhwc_trunk_matches_nchw(ctx, dt):
     nhwc = Session(trunk, ctx)
     assert sum(1 for n in nhwc.graph.nodes if n.attrs.ints.get("out_nhwc")) >= 3
     assert any(n.op == "Resize" and n.attrs.ints.get("out_nhwc") for n in nhwc.graph.nodes)
-    np.testing.assert_array_equal(nhwc.run(feeds)[trunk_out], Session(trunk, ctx, nhwc=False).run(feeds)[trunk_out])
+    t_got, t_want = nhwc.run(feeds)[trunk_out], Session(trunk, ctx, nhwc=False).run(feeds)[trunk_out]
+    if dt == "f16":
+        np.testing.assert_array_equal(t_got, t_want)
+    else:   # the NCHW forward runs the 128x128 upsampling conv on the patch-staged f32 kernel
+        close(t_got, t_want, 1e-5)
     got = Session(g, ctx).run(feeds)
     want = Session(g, ctx, nhwc=False).run(feeds)
     for k in ("logits", "y"):
-        if dt == "f32":
-            np.testing.assert_array_equal(got[k], want[k], err_msg=k)
-        else:
-            close(got[k], want[k], 2e-3)
+        close(got[k], want[k], 2e-3 if dt == "f16" else 1e-5)

@@ -416,7 +416,11 @@ def test_conv_nhwc_output_matches_nchw(torch, ctx):
     wt = ctx.weight_conv(w)
     y1 = ctx.conv2d(_dev(torch, x), wt, _dev(torch, b), pads=(1, 1, 1, 1))
     y2 = ctx.conv2d(_dev(torch, x), wt, _dev(torch, b), pads=(1, 1, 1, 1), out_layout=L.NHWC)
-    np.testing.assert_array_equal(y1.cpu().numpy(), y2[..., :20].permute(0, 3, 1, 2).cpu().numpy())
+    # NCHW out runs the patch-staged f32 kernel, NHWC out the engine: equal to
+    # f32 rounding, not bit for bit
+    got = y2[..., :20].permute(0, 3, 1, 2).cpu().numpy()
+    assert _rel_err(got, y1.cpu().numpy()) <= 1e-5
+    assert _rel_err(got, O.conv(x, w, b, pads=(1, 1, 1, 1))) <= F32_TOL
 
 
 # Halo-patch path (3x3, stride 1, 256-pixel tiles of whole output rows):

@@ -63,10 +63,11 @@ def test_noalloc_matches_conv2d_twice(torch, ctx, pair):
 
 def test_noalloc_rejects_more_scratch_than_the_static_array(torch, ctx):
     from oxionnx_amd import _lib as L
-    # an NCHW f32 input of 40 MiB needs a staging copy larger than 32 MiB
-    x = torch.zeros((1, 160, 256, 256), dtype=torch.float32, device="cuda")
-    wt = ctx.weight_conv(np.zeros((16, 160, 1, 1), np.float32))
-    out = torch.zeros((1, 16, 256, 256), dtype=torch.float32, device="cuda")
+    # an NCHW f16 input of 40 MiB needs an NHWC staging copy larger than
+    # 32 MiB (f32 NCHW 1x1 / 3x3 convs read their input in place)
+    x = torch.zeros((1, 320, 256, 256), dtype=torch.float16, device="cuda")
+    wt = ctx.weight_conv(np.zeros((16, 320, 1, 1), np.float32), dtype=L.F16)
+    out = torch.zeros((1, 16, 256, 256), dtype=torch.float16, device="cuda")
     with pytest.raises(L.OhipError) as e:
         ctx.conv2d(x, wt, None, out=out, noalloc=True)
     assert e.value.code == L.E_NOMEM and "static" in str(e.value)
