@@ -211,30 +211,38 @@ struct QuantEpi {
     c.cb = (double)comb[n_comb > 1 ? ch : 0];
     return c;
   }
-  struct PreI { Chan c[4]; int32_t ca[4]; };   // c when w_on_i, else ca
+  // Per group of four rows, 64 bytes (the epilogue reads them from LDS for
+  // every group, so they are kept to four 16-byte reads): with the weight
+  // channels on i, k = ca * cs (or cs itself when ca is per activation row),
+  // the int32 bias, the combined scale as stored (f32, widened at use) and
+  // the flip mask in x; with them on j, x holds the rows' correction factor.
+  struct PreI { int32_t k[4]; int32_t bi[4]; float cb[4]; int32_t x[4]; };
   struct PreJ { Chan c; int32_t ca; };         // ca when w_on_i, else c
   __device__ __forceinline__ void load_i(PreI& p, int i) const {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) { p.k[r] = 0; p.bi[r] = 0; p.cb[r] = 0.0f; p.x[r] = 0; }
     if (w_on_i) {
-      int32_t cs[4], bi[4] = {0, 0, 0, 0};
+      int32_t cs[4];
       int8_t fl[4] = {0, 0, 0, 0};
-      float cb[4];
       load4(colsum, i, out.P, vec_ok, cs);
-      if (bias) load4(bias, i, out.P, vec_ok, bi);
+      if (bias) load4(bias, i, out.P, vec_ok, p.bi);
       if (flip) load4(flip, i, out.P, vec_ok, fl);
       if (n_comb > 1) {
-        load4(comb, i, out.P, vec_ok, cb);
+        load4(comb, i, out.P, vec_ok, p.cb);
       } else {
         const float c0 = comb[0];
-        cb[0] = cb[1] = cb[2] = cb[3] = c0;
+        p.cb[0] = p.cb[1] = p.cb[2] = p.cb[3] = c0;
       }
 #pragma unroll
-      for (int r = 0; r < 4; ++r)
-        p.c[r] = Chan{cs[r], (int32_t)((uint32_t)ca * (uint32_t)cs[r]), bi[r], fl[r] ? -1 : 0, (double)cb[r]};
+      for (int r = 0; r < 4; ++r) {
+        p.k[r] = ca_rows ? cs[r] : (int32_t)((uint32_t)ca * (uint32_t)cs[r]);
+        p.x[r] = fl[r] ? -1 : 0;
+      }
     } else if (ca_rows) {
-      load4(ca_rows, i, out.P, vec_ok, p.ca);
+      load4(ca_rows, i, out.P, vec_ok, p.x);
     } else {
 #pragma unroll
-      for (int r = 0; r < 4; ++r) p.ca[r] = ca;
+      for (int r = 0; r < 4; ++r) p.x[r] = ca;
     }
   }
   __device__ __forceinline__ void load_j(PreJ& p, int j) const {
@@ -243,11 +251,11 @@ struct QuantEpi {
     else p.c = chan(jj);
   }
   // the exact int32 accumulator (modulo 2^32): acc + ca * cs, negated for a
-  // flipped channel, + bias; `k` is ca * cs when ca is per tensor
-  static __device__ __forceinline__ int32_t exact(int32_t acc, const Chan& c, int32_t k) {
+  // flipped channel (fl = -1), + bias; `k` is ca * cs
+  static __device__ __forceinline__ int32_t exact(int32_t acc, int32_t fl, int32_t bi, int32_t k) {
     uint32_t v = (uint32_t)acc + (uint32_t)k;
-    v = (v ^ (uint32_t)c.fl) - (uint32_t)c.fl;   // fl = -1: two's complement negation
-    v += (uint32_t)c.bi;
+    v = (v ^ (uint32_t)fl) - (uint32_t)fl;   // fl = -1: two's complement negation
+    v += (uint32_t)bi;
     return (int32_t)v;
   }
   // SatRange::requantize: f64 product with the combined scale, + zp, round
@@ -264,31 +272,26 @@ struct QuantEpi {
   template <class A>
   __device__ __forceinline__ void finish(const PreI& pi, const PreJ& pj, int, int, A acc,
                                          uint32_t (&bits)[4]) const {
-    int32_t v[4], k[4];
+    int32_t v[4];
     double cb[4];
     // a per-row correction factor multiplies per output; a per-tensor one
     // was folded into k (a uniform branch: the common path has no multiply)
-    if (__builtin_expect(ca_rows != nullptr, 0)) {
-#pragma unroll
-      for (int r = 0; r < 4; ++r)
-        k[r] = w_on_i ? (int32_t)((uint32_t)pj.ca * (uint32_t)pi.c[r].cs)
-                      : (int32_t)((uint32_t)pi.ca[r] * (uint32_t)pj.c.cs);
-    } else {
-#pragma unroll
-      for (int r = 0; r < 4; ++r) k[r] = w_on_i ? pi.c[r].k : pj.c.k;
-    }
     if (w_on_i) {
+      const bool rowca = __builtin_expect(ca_rows != nullptr, 0);
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int32_t a = acc[r];   // by value
-        v[r] = exact(a, pi.c[r], k[r]);
-        cb[r] = pi.c[r].cb;
+        const int32_t k = rowca ? (int32_t)((uint32_t)pj.ca * (uint32_t)pi.k[r]) : pi.k[r];
+        v[r] = exact(a, pi.x[r], pi.bi[r], k);
+        cb[r] = (double)pi.cb[r];
       }
     } else {
+      const bool rowca = __builtin_expect(ca_rows != nullptr, 0);
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int32_t a = acc[r];
-        v[r] = exact(a, pj.c, k[r]);
+        const int32_t k = rowca ? (int32_t)((uint32_t)pi.x[r] * (uint32_t)pj.c.cs) : pj.c.k;
+        v[r] = exact(a, pj.c.fl, pj.c.bi, k);
         cb[r] = pj.c.cb;
       }
     }
