@@ -589,6 +589,39 @@ __global__ void __launch_bounds__(kThreads) dequantize_kernel(const uint8_t* __r
 // The dequantised residual sum in one pass: DequantizeLinear of both byte
 // operands, their f32 Add and QuantizeLinear of the sum, each step the
 // arithmetic of its own kernel above (no contraction across the steps).
+__device__ __forceinline__ uint32_t qadd_one(uint32_t ra, uint32_t rb, const QAddArgs& q) {
+#pragma clang fp contract(off)
+  const float va = q.a_signed ? (float)(int8_t)ra : (float)(ra & 0xff);
+  const float vb = q.b_signed ? (float)(int8_t)rb : (float)(rb & 0xff);
+  const float da = (va - q.za) * q.sa;
+  const float db = (vb - q.zb) * q.sb;
+  const float sum = da + db;
+  const float v = sum / q.sc;
+  float r = __builtin_rintf(v);
+  if (!__builtin_isfinite(v)) r = v;
+  float o = r + q.zc;
+  o = o < q.lo ? q.lo : (o > q.hi ? q.hi : o);
+  return (uint32_t)((int32_t)o & 0xff);
+}
+
+// Two NHWC operands of one shape with their own pixel pitches (a resident
+// channel slice is one), four channels a thread: 32-bit loads of both, the
+// bytes through qadd_one, one 32-bit store into the compact output.
+__global__ void __launch_bounds__(kThreads) qadd_pitched_b4_kernel(const uint32_t* __restrict__ a,
+                                                                   const uint32_t* __restrict__ b,
+                                                                   uint32_t* __restrict__ y, int64_t groups, int cg,
+                                                                   int64_t pa, int64_t pb, QAddArgs q) {
+  for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < groups; i += (int64_t)gridDim.x * kThreads) {
+    const int64_t px = i / cg;
+    const int c = (int)(i - px * cg);
+    const uint32_t wa = a[px * pa + c], wb = b[px * pb + c];
+    uint32_t o = 0;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) o |= qadd_one(wa >> (8 * k), wb >> (8 * k), q) << (8 * k);
+    y[i] = o;
+  }
+}
+
 template <bool SAME>
 __global__ void __launch_bounds__(kThreads) qadd_kernel(const uint8_t* __restrict__ a, const uint8_t* __restrict__ b,
                                                         uint8_t* __restrict__ y, int64_t n, BcastPlan p, QAddArgs q) {
@@ -608,17 +641,7 @@ __global__ void __launch_bounds__(kThreads) qadd_kernel(const uint8_t* __restric
         ib += c * p.sb[d];
       }
     }
-    const float va = q.a_signed ? (float)(int8_t)a[ia] : (float)a[ia];
-    const float vb = q.b_signed ? (float)(int8_t)b[ib] : (float)b[ib];
-    const float da = (va - q.za) * q.sa;
-    const float db = (vb - q.zb) * q.sb;
-    const float sum = da + db;
-    const float v = sum / q.sc;
-    float r = __builtin_rintf(v);
-    if (!__builtin_isfinite(v)) r = v;
-    float o = r + q.zc;
-    o = o < q.lo ? q.lo : (o > q.hi ? q.hi : o);
-    y[i] = (uint8_t)((int32_t)o & 0xff);
+    y[i] = (uint8_t)qadd_one(a[ia], b[ib], q);
   }
 }
 
@@ -870,6 +893,20 @@ hipError_t run_quantize(const float* x, uint8_t* y, int64_t n, float scale, floa
 hipError_t run_qadd(const uint8_t* a, const uint8_t* b, uint8_t* y, int64_t n, const BcastPlan& p, bool same,
                     const QAddArgs& q, hipStream_t st) {
   if (n <= 0) return hipSuccess;
+  // pixels x channels with each operand's pitch (or one contiguous run),
+  // whole 4-byte channel groups: the vector kernel
+  const int R = kMaxRank;
+  const bool two_d = p.rank == 2 && p.sa[R - 1] == 1 && p.sb[R - 1] == 1;
+  const int64_t C = two_d ? p.shape[R - 1] : n;
+  const int64_t pa = two_d ? p.sa[R - 2] : n, pb = two_d ? p.sb[R - 2] : n;
+  if ((two_d || same) && C % 4 == 0 && pa % 4 == 0 && pb % 4 == 0 && (uintptr_t)a % 4 == 0 &&
+      (uintptr_t)b % 4 == 0 && (uintptr_t)y % 4 == 0 && C / 4 <= 0x7fffffff) {
+    const int64_t groups = n / 4;
+    hipLaunchKernelGGL(qadd_pitched_b4_kernel, dim3(grid_for(groups)), dim3(kThreads), 0, st,
+                       reinterpret_cast<const uint32_t*>(a), reinterpret_cast<const uint32_t*>(b),
+                       reinterpret_cast<uint32_t*>(y), groups, (int)(C / 4), pa / 4, pb / 4, q);
+    return hipGetLastError();
+  }
   if (same)
     hipLaunchKernelGGL(qadd_kernel<true>, dim3(grid_for(n)), dim3(kThreads), 0, st, a, b, y, n, p, q);
   else
