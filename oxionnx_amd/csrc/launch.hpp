@@ -84,6 +84,14 @@ template <class OutT> struct FloatEpi {
 
   static constexpr int kStageBytes = sizeof(OutT) <= 2 ? (int)sizeof(OutT) : 0;
   static constexpr bool kStageWide = sizeof(OutT) == 4;   // f32 outputs stage as 4-byte elements
+  // finish() reduces to acc + the row term: alpha is 1 (an exact multiply),
+  // no column or full-matrix term (the column term would add -0.0, the exact
+  // identity) and no activation
+  static constexpr bool kHasSimple = kStageBytes > 0;
+  __device__ __forceinline__ bool simple() const {
+    return alpha == 1.0f && (bias_mode == BIAS_I || bias_mode == BIAS_SCALAR || bias_mode == BIAS_NONE) &&
+           act == ACT_NONE;
+  }
   __device__ __forceinline__ int out_bytes() const { return (int)sizeof(OutT); }
   __device__ __forceinline__ OutAddr addr() const { return out; }
   __device__ __forceinline__ bool staged_ok(int bp) const {
@@ -94,6 +102,12 @@ template <class OutT> struct FloatEpi {
 
   struct PreI { float b[4]; };    // beta * bias per row (BIAS_I, BIAS_SCALAR), else -0
   struct PreJ { float b; };       // beta * bias per column (BIAS_J), else -0
+  template <class A>
+  __device__ __forceinline__ void finish_simple(const PreI& pi, A acc, uint32_t (&bits)[4]) const {
+#pragma clang fp contract(off)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) bits[r] = out_bits(from_f32<OutT>(acc[r] + pi.b[r]));
+  }
   __device__ __forceinline__ void load_i(PreI& p, int i) const {
 #pragma clang fp contract(off)
     if (bias_mode == BIAS_I) {
@@ -182,6 +196,9 @@ struct QuantEpi {
   const uint8_t* table;     // byte -> byte map applied after requantisation (may be null)
   int vec_ok;               // every per-channel / per-row array is 16-byte aligned
 
+  static constexpr bool kHasSimple = false;   // (simple() / finish_simple() are never called)
+  __device__ __forceinline__ bool simple() const { return false; }
+  template <class P, class A> __device__ __forceinline__ void finish_simple(const P&, A, uint32_t (&)[4]) const {}
   static constexpr int kStageBytes = 1;
   static constexpr bool kStageWide = true;   // int32 / f32 outputs stage as 4-byte elements
   __device__ __forceinline__ int out_bytes() const { return (out_kind == QOUT_U8 || out_kind == QOUT_I8) ? 1 : 4; }

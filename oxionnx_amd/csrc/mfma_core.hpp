@@ -517,12 +517,16 @@ __device__ __forceinline__ void tile_epilogue(const Epi& epi, A (&acc)[Tl::TP][T
   // epilogue does not set the kernel's register count (and occupancy).
   // (Compile-time loops: every accumulator index is a constant, so the
   // accumulators stay in registers however large the unrolled body is.)
+  // SIMPLE: the staged mode-1 path of an epilogue whose finish reduces to
+  // acc + row term (Epi::simple(), checked once; branch-free groups)
+  auto groups = [&](auto simple_c) __attribute__((always_inline)) {
+  constexpr bool SIMPLE = decltype(simple_c)::value;
   static_for<Tl::TP * 4>([&](auto ag) __attribute__((always_inline)) {
     constexpr int a = decltype(ag)::value / 4, g = decltype(ag)::value % 4;
     const int ig = ibase + a * 32 + 8 * g;
     const typename Epi::PreI pi = s_rows[(ig - p0) >> 2];
     int64_t row = 0;
-    if (!staged) row = out.row(ig);
+    if constexpr (!SIMPLE) if (!staged) row = out.row(ig);
     static_for<Tl::TQ>([&](auto bc) __attribute__((always_inline)) {
       constexpr int b = decltype(bc)::value;
       const int j = jbase + b * 32;
@@ -530,6 +534,11 @@ __device__ __forceinline__ void tile_epilogue(const Epi& epi, A (&acc)[Tl::TP][T
 #pragma unroll
       for (int e = 0; e < 4; ++e) v[e] = acc[a][b][4 * g + e];
       uint32_t bits[4];
+      if constexpr (SIMPLE) {
+        epi.finish_simple(pi, v, bits);
+        stage_write(std::integral_constant<int, EBN>{}, j - q0, ig, bits);
+        return;
+      }
       epi.finish(pi, pj[b], ig, j, v, bits);
       if constexpr (Epi::kStageBytes > 0) {
         if (smode == 1) {
@@ -546,6 +555,13 @@ __device__ __forceinline__ void tile_epilogue(const Epi& epi, A (&acc)[Tl::TP][T
       store_group(out, epi.out_bytes(), row, ig, j, bits);
     });
   });
+  };
+  if constexpr (Epi::kHasSimple) {
+    if (smode == 1 && epi.simple()) groups(std::true_type{});
+    else groups(std::false_type{});
+  } else {
+    groups(std::false_type{});
+  }
 
   OHIP_STAMP(5);
   auto flush = [&](auto ebc) __attribute__((always_inline)) {
@@ -753,11 +769,14 @@ mfma_gemm_kernel(const LX lx, const LY ly, const Epi epi, int nP, int nQ, int kc
 template <class T> struct PartialEpi {
   T* ws;
   int P, Pp, Q;
+  static constexpr bool kHasSimple = false;   // (simple() / finish_simple() are never called)
+  __device__ __forceinline__ bool simple() const { return false; }
+  struct PreI {};
+  template <class A> __device__ __forceinline__ void finish_simple(const PreI&, A, uint32_t (&)[4]) const {}
   static constexpr int kStageBytes = 0;
   static constexpr bool kStageWide = false;
   __device__ __forceinline__ bool staged_ok(int) const { return false; }
   __device__ __forceinline__ bool staged_wide_ok(int) const { return false; }
-  struct PreI {};
   struct PreJ {};
   __device__ __forceinline__ void load_i(PreI&, int) const {}
   __device__ __forceinline__ void load_j(PreJ&, int) const {}
