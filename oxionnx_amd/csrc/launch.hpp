@@ -196,9 +196,14 @@ struct QuantEpi {
   const uint8_t* table;     // byte -> byte map applied after requantisation (may be null)
   int vec_ok;               // every per-channel / per-row array is 16-byte aligned
 
-  static constexpr bool kHasSimple = false;   // (simple() / finish_simple() are never called)
-  __device__ __forceinline__ bool simple() const { return false; }
-  template <class P, class A> __device__ __forceinline__ void finish_simple(const P&, A, uint32_t (&)[4]) const {}
+  // simple(): the common QLinearMatMul / QLinearConv form (weight channels
+  // on i, a per-tensor correction factor, a u8 / i8 output, no table), whose
+  // finish needs only the row terms; the staged epilogue then runs
+  // finish_simple, the same arithmetic with no uniform branches
+  static constexpr bool kHasSimple = true;
+  __device__ __forceinline__ bool simple() const {
+    return w_on_i && ca_rows == nullptr && table == nullptr && (out_kind == QOUT_U8 || out_kind == QOUT_I8);
+  }
   static constexpr int kStageBytes = 1;
   static constexpr bool kStageWide = true;   // int32 / f32 outputs stage as 4-byte elements
   __device__ __forceinline__ int out_bytes() const { return (out_kind == QOUT_U8 || out_kind == QOUT_I8) ? 1 : 4; }
@@ -285,6 +290,12 @@ struct QuantEpi {
     d = __builtin_fmax(d, (double)lo);
     d = __builtin_fmin(d, (double)hi);
     return (int32_t)d;
+  }
+  template <class A>
+  __device__ __forceinline__ void finish_simple(const PreI& pi, A acc, uint32_t (&bits)[4]) const {
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      bits[r] = (uint32_t)requant(exact(acc[r], pi.x[r], pi.bi[r], pi.k[r]), (double)pi.cb[r]) & 0xff;
   }
   template <class A>
   __device__ __forceinline__ void finish(const PreI& pi, const PreJ& pj, int, int, A acc,
