@@ -87,8 +87,9 @@ template <class OutT> struct FloatEpi {
   // finish() reduces to acc + the row term: alpha is 1 (an exact multiply),
   // no column or full-matrix term (the column term would add -0.0, the exact
   // identity) and no activation
-  static constexpr bool kHasSimple = kStageBytes > 0;
-  __device__ __forceinline__ bool simple() const {
+  // (either staging mode: f16 / bf16 outputs stage in mode 1, f32 in mode 2)
+  static constexpr bool kHasSimple = true;
+  __device__ __forceinline__ bool simple(int) const {
     return alpha == 1.0f && (bias_mode == BIAS_I || bias_mode == BIAS_SCALAR || bias_mode == BIAS_NONE) &&
            act == ACT_NONE;
   }
@@ -102,7 +103,7 @@ template <class OutT> struct FloatEpi {
 
   struct PreI { float b[4]; };    // beta * bias per row (BIAS_I, BIAS_SCALAR), else -0
   struct PreJ { float b; };       // beta * bias per column (BIAS_J), else -0
-  template <class A>
+  template <int EB, class A>
   __device__ __forceinline__ void finish_simple(const PreI& pi, A acc, uint32_t (&bits)[4]) const {
 #pragma clang fp contract(off)
 #pragma unroll
@@ -196,13 +197,16 @@ struct QuantEpi {
   const uint8_t* table;     // byte -> byte map applied after requantisation (may be null)
   int vec_ok;               // every per-channel / per-row array is 16-byte aligned
 
-  // simple(): the common QLinearMatMul / QLinearConv form (weight channels
+  // simple(1): the common QLinearMatMul / QLinearConv form (weight channels
   // on i, a per-tensor correction factor, a u8 / i8 output, no table), whose
   // finish needs only the row terms; the staged epilogue then runs
   // finish_simple, the same arithmetic with no uniform branches
   static constexpr bool kHasSimple = true;
-  __device__ __forceinline__ bool simple() const {
-    return w_on_i && ca_rows == nullptr && table == nullptr && (out_kind == QOUT_U8 || out_kind == QOUT_I8);
+  // Mode 2 (4-byte outputs): the raw int32 form (MatMulInteger) likewise.
+  __device__ __forceinline__ bool simple(int mode) const {
+    if (!w_on_i || ca_rows != nullptr) return false;
+    if (mode == 2) return out_kind == QOUT_I32;
+    return table == nullptr && (out_kind == QOUT_U8 || out_kind == QOUT_I8);
   }
   static constexpr int kStageBytes = 1;
   static constexpr bool kStageWide = true;   // int32 / f32 outputs stage as 4-byte elements
@@ -291,11 +295,14 @@ struct QuantEpi {
     d = __builtin_fmin(d, (double)hi);
     return (int32_t)d;
   }
-  template <class A>
+  template <int EB, class A>
   __device__ __forceinline__ void finish_simple(const PreI& pi, A acc, uint32_t (&bits)[4]) const {
 #pragma unroll
-    for (int r = 0; r < 4; ++r)
-      bits[r] = (uint32_t)requant(exact(acc[r], pi.x[r], pi.bi[r], pi.k[r]), (double)pi.cb[r]) & 0xff;
+    for (int r = 0; r < 4; ++r) {
+      const int32_t v = exact(acc[r], pi.x[r], pi.bi[r], pi.k[r]);
+      if constexpr (EB == 4) bits[r] = (uint32_t)v;
+      else bits[r] = (uint32_t)requant(v, (double)pi.cb[r]) & 0xff;
+    }
   }
   template <class A>
   __device__ __forceinline__ void finish(const PreI& pi, const PreJ& pj, int, int, A acc,

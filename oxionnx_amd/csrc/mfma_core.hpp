@@ -517,10 +517,13 @@ __device__ __forceinline__ void tile_epilogue(const Epi& epi, A (&acc)[Tl::TP][T
   // epilogue does not set the kernel's register count (and occupancy).
   // (Compile-time loops: every accumulator index is a constant, so the
   // accumulators stay in registers however large the unrolled body is.)
-  // SIMPLE: the staged mode-1 path of an epilogue whose finish reduces to
-  // acc + row term (Epi::simple(), checked once; branch-free groups)
+  // SEB > 0: the staged path (SEB-byte staged elements: mode 1's narrow or
+  // mode 2's 4-byte ones) of an epilogue whose finish reduces to a function
+  // of the accumulators and the row terms alone (Epi::simple(mode), checked
+  // once; branch-free groups)
   auto groups = [&](auto simple_c) __attribute__((always_inline)) {
-  constexpr bool SIMPLE = decltype(simple_c)::value;
+  constexpr int SEB = decltype(simple_c)::value;
+  constexpr bool SIMPLE = SEB > 0;
   static_for<Tl::TP * 4>([&](auto ag) __attribute__((always_inline)) {
     constexpr int a = decltype(ag)::value / 4, g = decltype(ag)::value % 4;
     const int ig = ibase + a * 32 + 8 * g;
@@ -535,8 +538,8 @@ __device__ __forceinline__ void tile_epilogue(const Epi& epi, A (&acc)[Tl::TP][T
       for (int e = 0; e < 4; ++e) v[e] = acc[a][b][4 * g + e];
       uint32_t bits[4];
       if constexpr (SIMPLE) {
-        epi.finish_simple(pi, v, bits);
-        stage_write(std::integral_constant<int, EBN>{}, j - q0, ig, bits);
+        epi.template finish_simple<SEB>(pi, v, bits);
+        stage_write(std::integral_constant<int, SEB>{}, j - q0, ig, bits);
         return;
       }
       epi.finish(pi, pj[b], ig, j, v, bits);
@@ -556,12 +559,14 @@ __device__ __forceinline__ void tile_epilogue(const Epi& epi, A (&acc)[Tl::TP][T
     });
   });
   };
-  if constexpr (Epi::kHasSimple) {
-    if (smode == 1 && epi.simple()) groups(std::true_type{});
-    else groups(std::false_type{});
-  } else {
-    groups(std::false_type{});
+  bool done = false;
+  if constexpr (Epi::kHasSimple && Epi::kStageBytes > 0) {
+    if (smode == 1 && epi.simple(1)) { groups(std::integral_constant<int, EBN>{}); done = true; }
   }
+  if constexpr (Epi::kHasSimple && kWide) {
+    if (smode == 2 && epi.simple(2)) { groups(std::integral_constant<int, 4>{}); done = true; }
+  }
+  if (!done) groups(std::integral_constant<int, 0>{});
 
   OHIP_STAMP(5);
   auto flush = [&](auto ebc) __attribute__((always_inline)) {
@@ -770,9 +775,9 @@ template <class T> struct PartialEpi {
   T* ws;
   int P, Pp, Q;
   static constexpr bool kHasSimple = false;   // (simple() / finish_simple() are never called)
-  __device__ __forceinline__ bool simple() const { return false; }
+  __device__ __forceinline__ bool simple(int) const { return false; }
   struct PreI {};
-  template <class A> __device__ __forceinline__ void finish_simple(const PreI&, A, uint32_t (&)[4]) const {}
+  template <int EB, class A> __device__ __forceinline__ void finish_simple(const PreI&, A, uint32_t (&)[4]) const {}
   static constexpr int kStageBytes = 0;
   static constexpr bool kStageWide = false;
   __device__ __forceinline__ bool staged_ok(int) const { return false; }
