@@ -734,8 +734,18 @@ __global__ void __launch_bounds__(256) fewout_reduce_kernel(const float* __restr
                                                             T* __restrict__ y, DirectConvArgs a, int slices) {
   const int64_t plane = (int64_t)a.OH * a.OW, total = (int64_t)a.N * a.cout * plane;
   for (int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x; idx < total; idx += (int64_t)gridDim.x * 256) {
-    float v = ws[idx];
-    for (int s = 1; s < slices; ++s) v += ws[(int64_t)s * total + idx];
+    // each group of eight slices loaded before its adds (one round trip per
+    // group); the adds stay in slice order, slice 0 starts the sum
+    float v;
+    for (int s0 = 0; s0 < slices; s0 += 8) {
+      float t[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+        if (s0 + u < slices) t[u] = ws[(int64_t)(s0 + u) * total + idx];
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+        if (s0 + u < slices) v = s0 + u == 0 ? t[u] : v + t[u];
+    }
     const int64_t p = idx % plane, nc = idx / plane;
     const int co = (int)(nc % a.cout), n = (int)(nc / a.cout);
     if (bias) v = v + to_f32(bias[co]);

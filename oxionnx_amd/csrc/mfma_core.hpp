@@ -819,17 +819,18 @@ __global__ void __launch_bounds__(256) split_reduce_kernel(const T* __restrict__
     epi.load_j(pj, j);
     const T* src = ws + (int64_t)j * Pp + i0;
     auto ld = [&](const T* p) __attribute__((always_inline)) { return *reinterpret_cast<const A*>(p); };
-    A acc = ld(src);
-    int s = 1;
-    // four slices' loads in flight before their adds; the adds stay in slice order
-    for (; s + 4 <= splits; s += 4) {
-      const A v0 = ld(src + s * slice);
-      const A v1 = ld(src + (s + 1) * slice);
-      const A v2 = ld(src + (s + 2) * slice);
-      const A v3 = ld(src + (s + 3) * slice);
-      acc += v0; acc += v1; acc += v2; acc += v3;
+    // each group of four slices loaded before its adds (one round trip per
+    // group, not per slice); the adds stay in slice order, slice 0 starts
+    A acc;
+    for (int s0 = 0; s0 < splits; s0 += 4) {
+      A v[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+        if (s0 + u < splits) v[u] = ld(src + (s0 + u) * slice);
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+        if (s0 + u < splits) acc = s0 + u == 0 ? v[u] : acc + v[u];
     }
-    for (; s < splits; ++s) acc += ld(src + s * slice);
     uint32_t bits[4];
     epi.finish(pi, pj, i0, j, acc, bits);
     store_group(out, epi.out_bytes(), out.row(i0), i0, j, bits);

@@ -158,12 +158,26 @@ __global__ void __launch_bounds__(kThreads) instnorm_kernel(const T* __restrict_
 // own reduction slots, so every plane's statistics are the 256-thread
 // block's above; with PPB > 1 (an NHWC output) each pixel's PPB channels
 // are written (and a residual read) as one run.
+#ifdef OHIP_KTIMING
+// Diagnostic build only (never in the shipped library): per-block stamps of
+// the 100 MHz real-time counter at the norm kernel's phase boundaries.
+__device__ uint64_t ohip_ktime_nodes[8 * 65536];
+extern "C" int ohip_ktime_read_nodes(void* host) {
+  return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(ohip_ktime_nodes), sizeof(ohip_ktime_nodes));
+}
+#define NSTAMP(i) do { if (threadIdx.x == 0 && blockIdx.x < 65536) \
+    ohip_ktime_nodes[(i) * 65536 + blockIdx.x] = __builtin_amdgcn_s_memrealtime(); } while (0)
+#else
+#define NSTAMP(i) do {} while (0)
+#endif
+
 template <int PPB>
 __device__ __forceinline__ float group_sum(float v, float* red, int g) {
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
   const int lane = threadIdx.x & 63, wave = (threadIdx.x >> 6) & 3;
-  __syncthreads();
+  // (red is written once per call site: each sum has its own slots, so no
+  // barrier is needed before the write)
   if (lane == 0) red[4 * g + wave] = v;
   __syncthreads();
   float s = 0.0f;
@@ -181,7 +195,8 @@ __global__ void __launch_bounds__(kThreads * PPB) instnorm_partials_kernel(const
 #pragma clang fp contract(off)
   static_assert(kThreads == 256, "256 threads a plane");
   extern __shared__ float xs_all[];        // PPB planes of `spatial` values
-  __shared__ float red[4 * PPB];
+  __shared__ float red[2][4 * PPB];   // the mean's and the variance's wave sums
+  NSTAMP(0);
   const int g = threadIdx.x >> 8, lt = threadIdx.x & 255;
   const int groups = C / PPB;
   const int64_t n = blockIdx.x / groups;
@@ -218,16 +233,18 @@ __global__ void __launch_bounds__(kThreads * PPB) instnorm_partials_kernel(const
     // adds stay in slice order
     typedef float f4 __attribute__((ext_vector_type(4)));
     for (int i = 4 * lt; i < spatial; i += 4 * kThreads) {
-      f4 acc = *reinterpret_cast<const f4*>(src + i);
-      int s = 1;
-      for (; s + 4 <= splits; s += 4) {
-        const f4 v0 = *reinterpret_cast<const f4*>(src + s * slice + i);
-        const f4 v1 = *reinterpret_cast<const f4*>(src + (s + 1) * slice + i);
-        const f4 v2 = *reinterpret_cast<const f4*>(src + (s + 2) * slice + i);
-        const f4 v3 = *reinterpret_cast<const f4*>(src + (s + 3) * slice + i);
-        acc += v0; acc += v1; acc += v2; acc += v3;
+      // every slice of a group of four loaded before the first add (one
+      // round trip per group, not per slice); slice 0 starts the sum
+      f4 acc;
+      for (int s0 = 0; s0 < splits; s0 += 4) {
+        f4 v[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+          if (s0 + u < splits) v[u] = *reinterpret_cast<const f4*>(src + (s0 + u) * slice + i);
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+          if (s0 + u < splits) acc = s0 + u == 0 ? v[u] : acc + v[u];
       }
-      for (; s < splits; ++s) acc += *reinterpret_cast<const f4*>(src + s * slice + i);
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const float a = acc[e];
@@ -242,16 +259,19 @@ __global__ void __launch_bounds__(kThreads * PPB) instnorm_partials_kernel(const
     }
   }
   __syncthreads();
+  NSTAMP(1);
   float s = 0.0f;
   for (int i = lt; i < spatial; i += kThreads) s += xs[i];
-  const float mean = group_sum<PPB>(s, red, g) / (float)spatial;
+  const float mean = group_sum<PPB>(s, red[0], g) / (float)spatial;
+  NSTAMP(2);
   float q = 0.0f;
   for (int i = lt; i < spatial; i += kThreads) {
     const float d = xs[i] - mean;
     q += d * d;
   }
-  const float var = group_sum<PPB>(q, red, g) / (float)spatial;
+  const float var = group_sum<PPB>(q, red[1], g) / (float)spatial;
   const float inv = 1.0f / sqrtf(var + eps);
+  NSTAMP(3);
   const bool affine = aff.scale || aff.bias;
   T* yp = y + plane * spatial;
   for (int i = lt; i < spatial; i += kThreads) {
@@ -271,6 +291,7 @@ __global__ void __launch_bounds__(kThreads * PPB) instnorm_partials_kernel(const
       xs[i] = (float)(T)v;   // the stored value; the residual is added below, per run
     }
   }
+  NSTAMP(4);
   if constexpr (PPB > 1) {
     __syncthreads();
     // each pixel's PPB channels as one run (NHWC output, C per pixel)
@@ -310,6 +331,7 @@ __global__ void __launch_bounds__(kThreads * PPB) instnorm_partials_kernel(const
       }
     }
   }
+  NSTAMP(5);
 }
 
 // ---------------------------------------------------------------- nearest resize (rank 4, H and W)
@@ -743,12 +765,18 @@ hipError_t run_instnorm_partials(int dt, const float* ws, int splits, int64_t Pp
   if (planes <= 0 || spatial <= 0) return hipSuccess;
   if (planes > 0x7fffffff || spatial > kNormPartialsMaxSpatial || splits < 1) return hipErrorInvalidValue;
   const int64_t slice = (int64_t)C * Pp;
-  // an NHWC output takes four channels a block (8- / 16-byte runs per pixel)
-  constexpr int PPB = 4;
-  const bool wide = out_nhwc && C % PPB == 0 && (size_t)PPB * spatial * sizeof(float) <= 64 * 1024 &&
-                    (uintptr_t)y % (PPB * (dt == DT_F32 ? 4 : 2)) == 0 &&
-                    (!aff.residual || !aff.res_nhwc || (uintptr_t)aff.residual % (PPB * (dt == DT_F32 ? 4 : 2)) == 0);
-  if (wide) {
+  // an NHWC output takes PPB channels a block (runs of PPB elements per
+  // pixel); OHIP_NORM_PPB (2 or 4) overrides the default of 4 (a
+  // measurement switch)
+  static const int ppb_env = [] { const char* e = std::getenv("OHIP_NORM_PPB"); return e ? std::atoi(e) : 4; }();
+  const int eb = dt == DT_F32 ? 4 : 2;
+  auto wide_ok = [&](int ppb) {
+    return out_nhwc && C % ppb == 0 && (size_t)ppb * spatial * sizeof(float) <= 64 * 1024 &&
+           (uintptr_t)y % (ppb * eb) == 0 &&
+           (!aff.residual || !aff.res_nhwc || (uintptr_t)aff.residual % (ppb * eb) == 0);
+  };
+  auto launch_wide = [&](auto ppb_c) {
+    constexpr int PPB = decltype(ppb_c)::value;
     const size_t shm = (size_t)PPB * spatial * sizeof(float);
     const unsigned blocks = (unsigned)(planes / PPB);
     if (dt == DT_F32)
@@ -760,7 +788,9 @@ hipError_t run_instnorm_partials(int dt, const float* ws, int splits, int64_t Pp
     else
       return hipErrorInvalidValue;
     return hipGetLastError();
-  }
+  };
+  if (ppb_env == 2 && wide_ok(2)) return launch_wide(std::integral_constant<int, 2>{});
+  if (ppb_env != 1 && wide_ok(4)) return launch_wide(std::integral_constant<int, 4>{});
   const size_t shm = (size_t)spatial * sizeof(float);
   if (dt == DT_F32)
     hipLaunchKernelGGL((instnorm_partials_kernel<float, 1>), dim3((unsigned)planes), dim3(kThreads), shm, st, ws,
