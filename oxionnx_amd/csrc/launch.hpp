@@ -89,7 +89,8 @@ template <class OutT> struct FloatEpi {
   // identity) and no activation
   // (either staging mode: f16 / bf16 outputs stage in mode 1, f32 in mode 2)
   static constexpr bool kHasSimple = true;
-  __device__ __forceinline__ bool simple(int) const {
+  static constexpr bool kSimpleTable = false;
+  __device__ __forceinline__ int simple(int) const {
     return alpha == 1.0f && (bias_mode == BIAS_I || bias_mode == BIAS_SCALAR || bias_mode == BIAS_NONE) &&
            act == ACT_NONE;
   }
@@ -198,15 +199,19 @@ struct QuantEpi {
   int vec_ok;               // every per-channel / per-row array is 16-byte aligned
 
   // simple(1): the common QLinearMatMul / QLinearConv form (weight channels
-  // on i, a per-tensor correction factor, a u8 / i8 output, no table), whose
+  // on i, a per-tensor correction factor, a u8 / i8 output, with or without the byte table), whose
   // finish needs only the row terms; the staged epilogue then runs
   // finish_simple, the same arithmetic with no uniform branches
   static constexpr bool kHasSimple = true;
   // Mode 2 (4-byte outputs): the raw int32 form (MatMulInteger) likewise.
-  __device__ __forceinline__ bool simple(int mode) const {
-    if (!w_on_i || ca_rows != nullptr) return false;
-    if (mode == 2) return out_kind == QOUT_I32;
-    return table == nullptr && (out_kind == QOUT_U8 || out_kind == QOUT_I8);
+  // Returns 1 for the plain form, 2 for a u8 / i8 form with the byte table
+  // (a fused activation), 0 otherwise.
+  static constexpr bool kSimpleTable = true;
+  __device__ __forceinline__ int simple(int mode) const {
+    if (!w_on_i || ca_rows != nullptr) return 0;
+    if (mode == 2) return out_kind == QOUT_I32 ? 1 : 0;
+    if (out_kind != QOUT_U8 && out_kind != QOUT_I8) return 0;
+    return table == nullptr ? 1 : 2;
   }
   static constexpr int kStageBytes = 1;
   static constexpr bool kStageWide = true;   // int32 / f32 outputs stage as 4-byte elements
@@ -301,6 +306,7 @@ struct QuantEpi {
     for (int r = 0; r < 4; ++r) {
       const int32_t v = exact(acc[r], pi.x[r], pi.bi[r], pi.k[r]);
       if constexpr (EB == 4) bits[r] = (uint32_t)v;
+      else if constexpr ((EB & 16) != 0) bits[r] = table[requant(v, (double)pi.cb[r]) & 0xff];
       else bits[r] = (uint32_t)requant(v, (double)pi.cb[r]) & 0xff;
     }
   }

@@ -522,8 +522,9 @@ __device__ __forceinline__ void tile_epilogue(const Epi& epi, A (&acc)[Tl::TP][T
   // of the accumulators and the row terms alone (Epi::simple(mode), checked
   // once; branch-free groups)
   auto groups = [&](auto simple_c) __attribute__((always_inline)) {
-  constexpr int SEB = decltype(simple_c)::value;
-  constexpr bool SIMPLE = SEB > 0;
+  constexpr int SEB = decltype(simple_c)::value;   // staged bytes | 16 for the byte-table form
+  constexpr int SB = SEB & 15;
+  constexpr bool SIMPLE = SB > 0;
   static_for<Tl::TP * 4>([&](auto ag) __attribute__((always_inline)) {
     constexpr int a = decltype(ag)::value / 4, g = decltype(ag)::value % 4;
     const int ig = ibase + a * 32 + 8 * g;
@@ -539,7 +540,7 @@ __device__ __forceinline__ void tile_epilogue(const Epi& epi, A (&acc)[Tl::TP][T
       uint32_t bits[4];
       if constexpr (SIMPLE) {
         epi.template finish_simple<SEB>(pi, v, bits);
-        stage_write(std::integral_constant<int, SEB>{}, j - q0, ig, bits);
+        stage_write(std::integral_constant<int, SB>{}, j - q0, ig, bits);
         return;
       }
       epi.finish(pi, pj[b], ig, j, v, bits);
@@ -561,7 +562,13 @@ __device__ __forceinline__ void tile_epilogue(const Epi& epi, A (&acc)[Tl::TP][T
   };
   bool done = false;
   if constexpr (Epi::kHasSimple && Epi::kStageBytes > 0) {
-    if (smode == 1 && epi.simple(1)) { groups(std::integral_constant<int, EBN>{}); done = true; }
+    if (smode == 1) {
+      const int sm = epi.simple(1);   // 1: the plain form, 2: with the byte table
+      if (sm == 1) { groups(std::integral_constant<int, EBN>{}); done = true; }
+      if constexpr (Epi::kSimpleTable) {
+        if (sm == 2) { groups(std::integral_constant<int, EBN | 16>{}); done = true; }
+      }
+    }
   }
   if constexpr (Epi::kHasSimple && kWide) {
     if (smode == 2 && epi.simple(2)) { groups(std::integral_constant<int, 4>{}); done = true; }
@@ -775,7 +782,8 @@ template <class T> struct PartialEpi {
   T* ws;
   int P, Pp, Q;
   static constexpr bool kHasSimple = false;   // (simple() / finish_simple() are never called)
-  __device__ __forceinline__ bool simple(int) const { return false; }
+  static constexpr bool kSimpleTable = false;
+  __device__ __forceinline__ int simple(int) const { return 0; }
   struct PreI {};
   template <int EB, class A> __device__ __forceinline__ void finish_simple(const PreI&, A, uint32_t (&)[4]) const {}
   static constexpr int kStageBytes = 0;
