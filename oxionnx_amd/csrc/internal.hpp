@@ -219,7 +219,8 @@ struct HaloGeo {
 hipError_t run_halo_float(int dtype, const HaloGeo& g, bool pix_on_x, const FloatOut& o, hipStream_t st);
 // pixel-tile extent and largest staged patch of the halo path
 constexpr int kHaloBPix = 256;
-constexpr int kHaloPixMax = 400;
+constexpr int kHaloPixMax = 400;       // patch pixels of a 16-, 32- or 64-wide output row tile
+constexpr int kHaloPixMaxWide = 520;   // of a 128-wide one: (2 + 2) x 130
 
 hipError_t run_dense_float(int dtype, const DenseOperand& x, const DenseOperand& y, const FloatOut& o, int tile,
                            hipStream_t st);

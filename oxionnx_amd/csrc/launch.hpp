@@ -435,10 +435,11 @@ inline hipError_t launch_split_on(const LX& lx, const LY& ly, const Epi& epi, in
 // pixels per block, eight waves, four stages of two-chunk slabs.  Each XCD
 // owns whole output-channel tiles (the filter is the operand that would be
 // re-read), with every pixel tile of them.
-template <Op O, bool PIXX, class Epi>
-inline hipError_t launch_halo(const HaloGeo& g, const Epi& epi, int P, int Q, int splits, void* ws, hipStream_t st) {
+template <Op O, bool PIXX, class Epi, int PIXMAX>
+inline hipError_t launch_halo_px(const HaloGeo& g, const Epi& epi, int P, int Q, int splits, void* ws,
+                                 hipStream_t st) {
   using Ht = HaloTile<PIXX ? kHaloBPix : 64, PIXX ? 64 : kHaloBPix, PIXX ? 4 : 2, PIXX ? 2 : 4, 2, 4, 3, 3,
-                      kHaloPixMax, PIXX>;
+                      PIXMAX, PIXX>;
   using T = typename std::conditional<O == Op::I8, int32_t, float>::type;
   const int nP = (P + Ht::BP - 1) / Ht::BP, nQ = (Q + Ht::BQ - 1) / Ht::BQ;
   const int64_t nb = (int64_t)nP * nQ;
@@ -458,6 +459,12 @@ inline hipError_t launch_halo(const HaloGeo& g, const Epi& epi, int P, int Q, in
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || epi.out.defer) return e;
   return launch_reduce<O>(ws, splits, P, Q, epi, st);
+}
+// 128-wide output rows (two rows a tile) stage a larger patch
+template <Op O, bool PIXX, class Epi>
+inline hipError_t launch_halo(const HaloGeo& g, const Epi& epi, int P, int Q, int splits, void* ws, hipStream_t st) {
+  if (g.OW == 128) return launch_halo_px<O, PIXX, Epi, kHaloPixMaxWide>(g, epi, P, Q, splits, ws, st);
+  return launch_halo_px<O, PIXX, Epi, kHaloPixMax>(g, epi, P, Q, splits, ws, st);
 }
 
 // Automatic choice (split-K is decided beforehand, plan_splits).  The

@@ -1290,9 +1290,10 @@ static int halo_plan(ohip_ctx* ctx, const ohip_conv_desc* d, int64_t G, int64_t 
   const bool forced = ctx->tile_override == 15;
   if (!halo_allowed() || (ctx->tile_override != 0 && !forced) || G != 1) return 0;
   if (d->kh != 3 || d->kw != 3 || d->stride_h != 1 || d->stride_w != 1 || d->dil_h != 1 || d->dil_w != 1) return 0;
-  if (g.ow != 16 && g.ow != 32 && g.ow != 64) return 0;
+  if (g.ow != 16 && g.ow != 32 && g.ow != 64 && g.ow != 128) return 0;
   const int64_t th = kHaloBPix / g.ow;
-  if (g.oh % th != 0 || (th + 2) * (g.ow + 2) > kHaloPixMax || w_in > 65535) return 0;
+  const int pixmax = g.ow == 128 ? kHaloPixMaxWide : kHaloPixMax;
+  if (g.oh % th != 0 || (th + 2) * (g.ow + 2) > pixmax || w_in > 65535) return 0;
   if (img_bytes >= ((int64_t)1 << 31) - 65536) return 0;
   const int64_t rows = d->n * g.oh * g.ow;
   const double flops = 2.0 * (double)rows * (double)d->cout * (double)d->c * 9.0;

@@ -426,12 +426,14 @@ def test_conv_nhwc_output_matches_nchw(torch, ctx):
 # Halo-patch path (3x3, stride 1, 256-pixel tiles of whole output rows):
 # (x shape, cout, pads).  A channel tail inside the last slab, partial
 # output-channel tiles, two images, an uneven top pad, a valid (unpadded)
-# conv, 64-wide rows, and the 512-channel residual conv (split-K).
+# conv, 64-wide rows, 128-wide rows (two rows a tile, the larger patch), and
+# the 512-channel residual conv (split-K).
 HALO_CASES = [
     ((2, 24, 16, 16), 40, (1, 1, 1, 1)),
     ((1, 8, 15, 16), 24, (2, 1, 1, 1)),
     ((1, 16, 34, 34), 64, (0, 0, 0, 0)),
     ((1, 128, 16, 64), 96, (1, 1, 1, 1)),
+    ((2, 40, 6, 128), 72, (1, 1, 1, 1)),
     ((1, 512, 32, 32), 512, (1, 1, 1, 1)),
 ]
 
