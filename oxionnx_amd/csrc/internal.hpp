@@ -157,7 +157,11 @@ struct SplitChoice {
   int splits, tile;
 };
 inline SplitChoice plan_split_tile(int P, int Q, int kc, int override_tile, bool mfma_f32) {
-  const int s64 = plan_splits(P, Q, kc, override_tile);
+  int s64 = plan_splits(P, Q, kc, override_tile);
+  // f32 on the 64x64 tile: slices of at least 12 k-stages (config 2b's
+  // 128x768x3072, 24 stages: 2 slices 16.0 us against 3 slices 18.3)
+  if (mfma_f32 && override_tile == 0 && !forced_splits() && s64 > 2)
+    s64 = std::max(2, std::min(s64, (kc + 7) / 8 / 12));
   if (override_tile == 0 && mfma_f32 && s64 > 1) {   // only where the 64x64 plan splits too
     const int s = plan_splits(P, Q, kc, 0, 128);
     const int64_t nb = (int64_t)((P + 127) / 128) * ((Q + 127) / 128);
