@@ -437,9 +437,15 @@ int do_conv(ohip_ctx* ctx, const ohip_node* nd, int placement, ohip_output* out,
   const size_t obytes = (size_t)(g.n * g.cout * g.oh * g.ow) * ebytes(dt);
   void* yd = st.alloc(obytes);
   if (!xd || !yd || (b && !bd)) { if (!cache) ohip_weight_release(wt); return OHIP_E_NOMEM; }
+  // a fused residual (input 5) of another shape is broadcast by the binary
+  // kernel after the fused pair, which indexes the pair's output as NCHW
+  const ohip_tensor* res_in = with_norm && nd->n_inputs > 5 ? input(nd, 5) : nullptr;
+  const bool res_bcast = res_in && !(res_in->rank == (int)oshape.size() &&
+                                     std::equal(oshape.begin(), oshape.end(), res_in->shape));
   // a session layout hint: every consumer of this output reads NHWC in place
   const bool y_nhwc = placement == OHIP_PLACE_DEVICE && attr_i(nd, "out_nhwc", 0) == 1 && g.group == 1 &&
-                      !g.rank1 && g.cout % (16 / ebytes(dt)) == 0 && (!with_norm || g.cout % 8 == 0);
+                      !g.rank1 && g.cout % (16 / ebytes(dt)) == 0 && (!with_norm || g.cout % 8 == 0) &&
+                      !res_bcast;
   ohip_conv_desc d{g.n, g.c, g.h, g.w, g.cout, g.kh, g.kw, g.group, g.sh, g.sw, g.dh, g.dw, g.pt, g.pl, g.pb, g.pr,
                    dt, x_nhwc ? OHIP_NHWC : OHIP_NCHW, y_nhwc ? OHIP_NHWC : OHIP_NCHW, 0, 0.0f, 0.0f,
                    OHIP_PAD_ZEROS};

@@ -216,6 +216,10 @@ def _plan_nhwc(nodes, keep_out, inits):
                 continue
         elif n.op not in ("Conv", "OhipConvInstanceNorm") or n.attrs.ints.get("group", 1) != 1:
             continue
+        elif n.op == "OhipConvInstanceNorm" and len(n.inputs) > 5 and n.inputs[5] in inits:
+            # an initializer residual broadcasts (a [1, C, 1, 1] shift); the
+            # binary kernel that adds it after the fused pair reads NCHW
+            continue
         t = n.outputs[0]
         users = cons.get(t, [])
         if t in keep_out or not users:

@@ -602,6 +602,49 @@ def test_conv_instnorm_fusion_matches_unfused(ctx, case):
     close(got, ref, 1e-2 if dt == "f16" else 1e-4)
 
 
+def _bcast_residual_then_conv(dt):
+    """Conv -> OxiInstanceNorm -> Add([1, C, 1, 1] initializer) -> zero-padded
+    Conv: the fused node's residual broadcasts, and its consumer is a conv
+    that would read an NHWC input in place."""
+    g, feeds = _conv_adain_graph(1, 64, 16, dt, adain=False, relu=False, residual="bcast")
+    rng = np.random.default_rng(11)
+    wt = np.float16 if dt == "f16" else np.float32
+    g.initializers["W2"] = rng.normal(0, 0.05, (32, 64, 3, 3)).astype(wt)
+    g.initializers["B2"] = rng.normal(0, 0.05, 32).astype(wt)
+    g.nodes[-1].outputs = ["mid"]
+    g.nodes.append(ep.Node("Conv", ["mid", "W2", "B2"], ["y"],
+                           A(int_lists={"kernel_shape": [3, 3], "pads": [1, 1, 1, 1]}), name="conv2"))
+    return g, feeds
+
+
+@pytest.mark.parametrize("dt", ["f16", "f32"])
+def test_broadcast_residual_output_stays_nchw(ctx, dt):
+    """A fused conv -> norm node whose residual broadcasts writes NCHW even
+    when its output carries the NHWC hint (the broadcast add after the pair
+    indexes NCHW): the planner does not hint it, and a hint forced onto the
+    node is ignored by the dispatcher.  Both forwards equal the NCHW forward
+    bit for bit, and the oracle within the dtype's bar."""
+    g, feeds = _bcast_residual_then_conv(dt)
+    want = Session(g, ctx, nhwc=False).run(feeds)["y"]
+    planned = fuse(g)
+    fused = [n for n in planned.nodes if n.op == "OhipConvInstanceNorm"]
+    assert len(fused) == 1 and len(fused[0].inputs) == 6
+    assert not fused[0].attrs.ints.get("out_nhwc")
+    np.testing.assert_array_equal(Session(g, ctx).run(feeds)["y"], want)
+    forced = []
+    for n in planned.nodes:
+        if n.op == "OhipConvInstanceNorm":
+            a = A(ints=dict(n.attrs.ints), floats=dict(n.attrs.floats), strings=dict(n.attrs.strings),
+                  int_lists=dict(n.attrs.int_lists))
+            a.ints["out_nhwc"] = 1
+            n = ep.Node(n.op, list(n.inputs), list(n.outputs), a, name=n.name)
+        forced.append(n)
+    got = Session(Graph(forced, planned.initializers, g.inputs, g.outputs), ctx, optimize=False).run(feeds)["y"]
+    np.testing.assert_array_equal(got, want)
+    ref = G.run_graph(g, feeds, half=(dt == "f16"))["y"]
+    close(got, ref, 1e-2 if dt == "f16" else 1e-4)
+
+
 @pytest.mark.parametrize("coord", ["half_pixel", "asymmetric", "align_corners"])
 @pytest.mark.parametrize("scales", [(1, 1, 2, 2), (1, 1, 1.5, 0.75), (1, 1, 3, 2.5)], ids=str)
 @pytest.mark.parametrize("dt", [np.float16, np.float32], ids=["f16", "f32"])

@@ -102,3 +102,31 @@ def test_nhwc_plan_hints_conv_and_resize_chains(dt):
     assert len(head) == 1
     assert (head[0].inputs[0] in hinted) == (dt == "f16")
     assert any(by_out[t].op in ("Conv", "OhipConvInstanceNorm") for t in hinted)
+
+
+def test_nhwc_plan_skips_a_broadcast_residual():
+    """A fused conv -> norm node whose residual is a [1, C, 1, 1]
+    initializer (added by the NCHW broadcast kernel after the pair) gets no
+    NHWC hint, although its consumer, a zero-padded conv, reads NHWC; the
+    same chain with a full-shape residual is hinted."""
+    rng = np.random.default_rng(5)
+    conv = {"kernel_shape": [3, 3], "pads": [1, 1, 1, 1]}
+
+    def graph(residual_init):
+        inits = {"W": rng.normal(0, 0.05, (16, 16, 3, 3)).astype(np.float32), "B": _f32(np.zeros(16)),
+                 "W2": rng.normal(0, 0.05, (8, 16, 3, 3)).astype(np.float32)}
+        other = "x"
+        if residual_init:
+            inits["rb"] = rng.normal(0, 1, (1, 16, 1, 1)).astype(np.float32)
+            other = "rb"
+        nodes = [ep.Node("Conv", ["x", "W", "B"], ["h"], A(int_lists=dict(conv)), name="c1"),
+                 ep.Node("OxiInstanceNorm", ["h"], ["n"], A(floats={"epsilon": 1e-5}), name="nm"),
+                 ep.Node("Add", ["n", other], ["r"], name="add"),
+                 ep.Node("Conv", ["r", "W2"], ["y"], A(int_lists=dict(conv)), name="c2")]
+        return Graph(nodes, inits, ["x"], ["y"])
+
+    for residual_init, hinted in ((True, False), (False, True)):
+        nodes = fuse(graph(residual_init)).nodes
+        fused = [n for n in nodes if n.op == "OhipConvInstanceNorm"]
+        assert len(fused) == 1 and len(fused[0].inputs) == 6
+        assert bool(fused[0].attrs.ints.get("out_nhwc")) == hinted

@@ -37,25 +37,31 @@ def _case(torch, ctx, dt, xs, ws, pads, seed):
     return x, wt, b
 
 
-# (dtype, x shape, w shape, pads): the first takes split-K (a 512 -> 512 3x3
-# conv at 32x32), the second is smaller and unsplit
-CALLS = [("f16", (1, 512, 32, 32), (512, 512, 3, 3), (1, 1, 1, 1)),
-         ("f16", (1, 64, 20, 24), (96, 64, 3, 3), (1, 1, 1, 1)),
-         ("f32", (1, 128, 64, 64), (256, 128, 3, 3), (1, 1, 1, 1)),
-         ("f32", (2, 16, 9, 11), (24, 16, 3, 3), (0, 1, 2, 1))]
+# (dtype, x shape, w shape, pads, strides).  Every call uses the scratch:
+# the f16 calls stage their NCHW input as NHWC (the first also splits K on
+# the halo-patch path, a 512 -> 512 3x3 conv at 32x32, 4.8 GFLOP); the f32
+# 512 -> 512 conv takes the halo-patch path too (staging + split-K partial
+# sums: the f32 NCHW kernel that reads its input in place is used only
+# below the halo path's 3 GFLOP), and the second f32 call has stride 2,
+# which that in-place kernel does not take, so it stages its input for the
+# engine
+CALLS = [("f16", (1, 512, 32, 32), (512, 512, 3, 3), (1, 1, 1, 1), (1, 1)),
+         ("f16", (1, 64, 20, 24), (96, 64, 3, 3), (1, 1, 1, 1), (1, 1)),
+         ("f32", (1, 512, 32, 32), (512, 512, 3, 3), (1, 1, 1, 1), (1, 1)),
+         ("f32", (2, 16, 9, 11), (24, 16, 3, 3), (0, 1, 2, 1), (2, 2))]
 
 
 @pytest.mark.parametrize("pair", [(0, 1), (2, 3)], ids=["f16", "f32"])
 def test_noalloc_matches_conv2d_twice(torch, ctx, pair):
     from oxionnx_amd import _lib as L
     for i in pair:
-        dt, xs, ws, pads = CALLS[i]
+        dt, xs, ws, pads, strides = CALLS[i]
         x, wt, b = _case(torch, ctx, dt, xs, ws, pads, seed=i)
-        want = ctx.conv2d(x, wt, b, pads=pads, act=L.ACT_RELU)
+        want = ctx.conv2d(x, wt, b, strides=strides, pads=pads, act=L.ACT_RELU)
         got = torch.full_like(want, float("nan"))
         torch.cuda.synchronize()
         ctx.reset_counters()
-        ctx.conv2d(x, wt, b, pads=pads, act=L.ACT_RELU, out=got, noalloc=True)
+        ctx.conv2d(x, wt, b, strides=strides, pads=pads, act=L.ACT_RELU, out=got, noalloc=True)
         torch.cuda.synchronize()
         assert ctx.counters()["device_allocs"] == 0
         assert torch.equal(got, want), (i, float((got.float() - want.float()).abs().max()))
