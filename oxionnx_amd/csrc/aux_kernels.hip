@@ -613,7 +613,7 @@ conv_direct_kernel(const T* __restrict__ x, const T* __restrict__ w, const T* __
     }
     float v = acc;
     if (bias) v = v + to_f32(bias[co]);
-    v = activate(v, a.act, a.lo, a.hi);
+    v = activate_t<T>(v, a.act, a.lo, a.hi);
     const int64_t o = a.nhwc_out ? (((int64_t)n * a.OH + oy) * a.OW + ox) * a.ldo + co
                                  : (((int64_t)n * a.cout + co) * a.OH + oy) * a.OW + ox;
     y[o] = from_f32<T>(v);
@@ -749,7 +749,7 @@ __global__ void __launch_bounds__(256) fewout_reduce_kernel(const float* __restr
     const int64_t p = idx % plane, nc = idx / plane;
     const int co = (int)(nc % a.cout), n = (int)(nc / a.cout);
     if (bias) v = v + to_f32(bias[co]);
-    v = activate(v, a.act, a.lo, a.hi);
+    v = activate_t<T>(v, a.act, a.lo, a.hi);
     const int64_t o = a.nhwc_out ? ((int64_t)n * plane + p) * a.ldo + co : idx;
     y[o] = from_f32<T>(v);
   }

@@ -26,6 +26,16 @@ __device__ __forceinline__ float activate(float v, int act, float lo, float hi) 
   }
 }
 
+// LeakyRelu is this provider's fusion: the reference keeps it a node of its
+// own that reads the conv's stored output, so a 2-byte output is rounded to
+// its type before the slope is applied (the unfused pair's two roundings).
+// Relu commutes with the rounding and Clip is the reference's own fusion
+// (applied before the conversion, conv_typed.rs:54-109).
+template <class OutT> __device__ __forceinline__ float activate_t(float v, int act, float lo, float hi) {
+  if (sizeof(OutT) == 2 && act == ACT_LEAKY_RELU) v = to_f32(from_f32<OutT>(v));
+  return activate(v, act, lo, hi);
+}
+
 // Both epilogues read their per-position parameters (biases, column sums,
 // scales) in batches before any output is formed: PreI for a group of four
 // consecutive i positions (one vector load per array where aligned), PreJ
@@ -157,7 +167,10 @@ template <class OutT> struct FloatEpi {
       for (int r = 0; r < 4; ++r) v[r] = v[r] < lo ? lo : (v[r] > hi ? hi : v[r]);
     } else if (act == ACT_LEAKY_RELU) {
 #pragma unroll
-      for (int r = 0; r < 4; ++r) v[r] = v[r] >= 0.0f ? v[r] : v[r] * lo;
+      for (int r = 0; r < 4; ++r) {
+        if (sizeof(OutT) == 2) v[r] = to_f32(from_f32<OutT>(v[r]));   // as activate_t
+        v[r] = v[r] >= 0.0f ? v[r] : v[r] * lo;
+      }
     }
 #pragma unroll
     for (int r = 0; r < 4; ++r) bits[r] = out_bits(from_f32<OutT>(v[r]));

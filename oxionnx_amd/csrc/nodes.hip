@@ -141,7 +141,7 @@ __global__ void __launch_bounds__(kThreads) instnorm_kernel(const T* __restrict_
       if (aff.bias) v = (float)(T)(v + bi);
     }
     if (aff.act == UN_RELU) v = v > 0.0f ? v : 0.0f;
-    else if (aff.act == UN_LEAKY_RELU) v = v >= 0.0f ? v : v * aff.alpha;
+    else if (aff.act == UN_LEAKY_RELU) v = (float)(T)v, v = v >= 0.0f ? v : v * aff.alpha;
     if (aff.residual) {
       const T* r = static_cast<const T*>(aff.residual);
       v = (float)(T)v + (aff.res_nhwc ? ldf(r, (n * spatial + i) * C + c) : ldf(r + plane * spatial, i));
@@ -282,7 +282,7 @@ __global__ void __launch_bounds__(kThreads * PPB) instnorm_partials_kernel(const
       if (aff.bias) v = (float)(T)(v + bi);
     }
     if (aff.act == UN_RELU) v = v > 0.0f ? v : 0.0f;
-    else if (aff.act == UN_LEAKY_RELU) v = v >= 0.0f ? v : v * aff.alpha;
+    else if (aff.act == UN_LEAKY_RELU) v = (float)(T)v, v = v >= 0.0f ? v : v * aff.alpha;
     if constexpr (PPB == 1) {
       if (res) v = (float)(T)v + (float)(aff.res_nhwc ? res[(n * spatial + i) * C + c] : res[plane * spatial + i]);
       if (out_nhwc) y[(n * spatial + i) * C + c] = (T)v;   // channel c of each pixel (C per pixel)

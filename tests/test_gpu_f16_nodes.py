@@ -133,11 +133,13 @@ def _node_by_node(ctx, g, feeds):
 
 def test_face_swap_f16_node_by_node(ctx):
     """Every node of the device's f16 forward, given the device's inputs for
-    it, is within 1e-2 of its output magnitude of the oracle; the elements
-    that differ at all are few, and differ by a few f16 ulps at most (the
-    f32 sums of the conv and the norm's statistics run in another order, so
-    a sum that lands near an f16 rounding boundary can round the other
-    way)."""
+    it, is within 1e-2 of its output magnitude of the oracle, at least 99.5 %
+    of its elements are bit-identical to the oracle's and 99.9 % within one
+    f16 ulp.  What differs is a sum that lands near an f16 rounding boundary
+    and rounds the other way (the f32 sums of the conv and the norm's
+    statistics run in another order); a rounding point placed differently
+    (a fused activation applied before the conversion where the reference
+    converts first) would show as a large share of one-ulp differences."""
     g, feeds = workloads.face_swap_generator(dtype="f16")
     _, _, stats = _node_by_node(ctx, g, feeds)
     for s in stats:
@@ -145,18 +147,46 @@ def test_face_swap_f16_node_by_node(ctx):
               f"exact {s['exact']:.5f} <=1ulp {s['within1']:.5f}")
     for s in stats:
         assert s["rel"] <= 1e-2, s
+        assert s["exact"] >= 0.995, s
         assert s["within1"] >= 0.999, s
 
 
-def test_face_swap_f16_graph_output_error(ctx):
-    """The graph output y (Tanh of the logits) against the oracle's f16
-    forward, as a fraction of max |y|, and the logits as a fraction of
-    max |logits|."""
+def _torch_order_conv_half(x_bits, w_bits, b_bits=None, bf16=False, activation=None, act_min=float("-inf"),
+                           act_max=float("inf"), strides=None, pads=None, dilations=None, group=1, nthreads=None):
+    """conv_half with the f32 convolution summed by torch (CPU float32) in
+    place of the oracle's sgemm: the same arithmetic (f16 operands, f32
+    accumulation, one rounding to f16), another summation order."""
+    import torch
+    from oracle import oracle as O
+    assert activation is None
+    t = lambda v: torch.from_numpy(O.half_bits_to_f32(v, bf16))
+    pt, pl, pb, pr = pads or (0, 0, 0, 0)
+    x = torch.nn.functional.pad(t(x_bits), (pl, pr, pt, pb))
+    y = torch.nn.functional.conv2d(x, t(w_bits), None if b_bits is None else t(b_bits),
+                                   stride=tuple(strides or (1, 1)), dilation=tuple(dilations or (1, 1)), groups=group)
+    return O.f32_to_half_bits(y.numpy(), bf16)
+
+
+def test_face_swap_f16_graph_output_error(ctx, monkeypatch):
+    """The logits against the oracle's f16 forward are within 1e-2 of
+    max |logits|.  The graph output y = Tanh(logits) is held to what a
+    second correct CPU forward reaches: the oracle with its convolutions'
+    f32 sums taken in torch's order instead of its sgemm's.  Summation order
+    alone moves y by about 2e-2 of max |y| (the six residual blocks'
+    instance norms amplify one-ulp flips), so no implementation that does
+    not reproduce the reference's sgemm order bit for bit -- the oracle
+    included -- is within 1e-2 of max |y| of the reference; the device is
+    required to be no further from the oracle than that second forward."""
+    from oracle import oracle as O
     g, feeds = workloads.face_swap_generator(dtype="f16")
     out = Session(g, ctx).run(feeds)
     ref = G.run_graph(g, feeds, half=True)
-    errs = {k: float(np.abs(out[k].astype(np.float32) - ref[k]).max()) / float(np.abs(ref[k]).max())
-            for k in ("logits", "y")}
-    print("f16 graph output error (fraction of max |ref|):", errs)
-    assert errs["logits"] <= 1e-2, errs
-    assert errs["y"] <= 1e-2, errs
+    monkeypatch.setattr(O, "conv_half", _torch_order_conv_half)
+    alt = G.run_graph(g, feeds, half=True)
+    rel = lambda a, b: float(np.abs(np.asarray(a, np.float32) - b).max()) / float(np.abs(b).max())
+    dev = {k: rel(out[k], ref[k]) for k in ("logits", "y")}
+    order = {k: rel(alt[k], ref[k]) for k in ("logits", "y")}
+    print("f16 graph outputs, error as a fraction of max |oracle|: device", dev, "summation order only", order)
+    assert dev["logits"] <= 1e-2, dev
+    assert order["y"] > 1e-2, order    # the premise: the bar on y is out of reach of any other order
+    assert dev["y"] <= order["y"], (dev, order)

@@ -130,3 +130,34 @@ def test_nhwc_plan_skips_a_broadcast_residual():
         fused = [n for n in nodes if n.op == "OhipConvInstanceNorm"]
         assert len(fused) == 1 and len(fused[0].inputs) == 6
         assert bool(fused[0].attrs.ints.get("out_nhwc")) == hinted
+
+
+def test_reference_chains_of_fused_nodes_reproduce_the_unfused_graph():
+    """The node-by-node f16 parity test evaluates each node of the fused
+    graph as the chain of reference operators it replaces; fed the unfused
+    graph's own values, every chain gives that graph's values bit for bit
+    (the merged style Gemm, which has no counterpart value, evaluated as it
+    is)."""
+    from oxionnx_amd import workloads
+    from tests.test_gpu_f16_nodes import _reference_chain, _ulps
+    g, feeds = workloads.face_swap_generator(dtype="f16", n_blocks=1)
+    fused = fuse(g)
+    names = {n.outputs[0] for n in g.nodes}
+    outs = [n.outputs[0] for n in fused.nodes if n.outputs[0] in names]
+    full = G.run_graph(Graph(g.nodes, g.initializers, g.inputs, outs), feeds, half=True)
+    vals = {**{k: np.asarray(v) for k, v in feeds.items()}, **{k: v.astype(np.float16) for k, v in full.items()}}
+    for n in fused.nodes:
+        if n.outputs[0] not in names:
+            vals[n.outputs[0]] = G.run_graph(Graph([n], fused.initializers, ["latent"], n.outputs), feeds,
+                                             half=True)[n.outputs[0]].astype(np.float16)
+    shapes = {k: np.shape(v) for k, v in vals.items()}
+    shapes.update({k: np.shape(np.asarray(getattr(v, "data", v))) for k, v in fused.initializers.items()})
+    ops = set()
+    for n in fused.nodes:
+        chain, extra = _reference_chain(n, shapes)
+        ins = [t for t in n.inputs if t and t not in fused.initializers]
+        ref = G.run_graph(Graph(chain, {**fused.initializers, **extra}, ins, [n.outputs[0]]),
+                          {t: vals[t] for t in ins}, half=True)[n.outputs[0]]
+        assert _ulps(vals[n.outputs[0]], ref).max() == 0, n.outputs[0]
+        ops.add((n.op, n.attrs.strings.get("activation"), len(n.inputs)))
+    assert ("OhipConvInstanceNorm", None, 6) in ops and ("Conv", "leaky_relu", 3) in ops
