@@ -460,6 +460,9 @@ int ohip_reset_counters(ohip_ctx* ctx);
  *     geometry allows (automatically only from 3 GFLOP up).
  * 16: 256x256 (8) with a third LDS buffer for the X operand, whose loads run
  *     two stages ahead (the automatic f16 / bf16 choice where 6 would be).
+ * 17: 3x3 stride-1 f16 / bf16 convolutions with 16-, 32- or 64-wide output
+ *     rows take the whole-K halo kernel (no split-K) wherever its geometry
+ *     allows (automatically from 256 blocks and 1.5 GFLOP up).
  * The automatic choice splits K (on 64x64 tiles) when the 64x64 tiling gives
  * fewer than 256 blocks and K is at least 16 stages of 128 bytes. */
 int ohip_set_tile_override(ohip_ctx* ctx, int tile_id);

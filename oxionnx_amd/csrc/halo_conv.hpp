@@ -223,3 +223,197 @@ halo_conv_kernel(const HaloGeo g, const Epi epi, int nP, int nQ, int splits, int
 }
 
 }  // namespace ohip
+
+namespace ohip {
+
+// Whole-K halo convolution (wk_conv_kernel): 3x3, stride 1, one group, NHWC
+// input, for mid-size convolutions whose output (pixels x channels) is too
+// small to give every CU a block of the halo kernel's 256 x 64 tiles
+// without splitting K.  A block takes NPT * 32 pixels (TH whole output rows
+// of one image) x 32 output channels over the whole reduction, so nothing
+// leaves the block but its outputs (no split-K partial sums, no reduction
+// launch): with 32 x 32 images and 512 channels that is 16 x 16 = 256
+// blocks.  Per stage (a slab of CC 16-byte channel chunks) the block DMA-
+// loads the 32 filter rows' slab (9 taps x CC chunks a row) and the input
+// patch of its rows ((TH + 2) x (OW + 2) pixels x CC chunks) into LDS with
+// the halo kernel's layout and swizzle (whole 128-byte lines at CC = 8).
+// The block's waves split the MFMA work instead of the output: wave
+// (pt, ks) takes pixel tile pt (32 pixels) and k-step ks of every slab, for
+// all nine taps, so each wave holds one 32 x 32 accumulator; after the K
+// loop the partial tiles meet in LDS and are added in k-step order (a fixed
+// order: the result does not depend on timing), and waves 0 .. NPT - 1 run
+// the float epilogue on their pixel tile.
+template <int OW_, int NPT_, int CC_, int STAGES_, bool PIX_ON_X_>
+struct WkTile {
+  static constexpr int OW = OW_, NPT = NPT_, CC = CC_, STAGES = STAGES_;
+  static constexpr bool PIX_ON_X = PIX_ON_X_;
+  static constexpr int TH = NPT * 32 / OW, PW = OW + 2, NPIX = (TH + 2) * PW;
+  static constexpr int KSN = CC / 2, kWaves = NPT * KSN, kThreads = kWaves * 64;
+  static constexpr int RW = 9 * CC;                  // chunks per staged filter row
+  static constexpr int WI = 32 * RW / 64;            // filter DMA loads per stage
+  static constexpr int PI = (NPIX * CC + 63) / 64;   // patch DMA loads per stage
+  static constexpr int TI = WI + PI, kStage = TI * 64;
+  static constexpr int NLO = TI / kWaves, NHI = (TI + kWaves - 1) / kWaves;
+  static_assert(CC == 4 || CC == 8, "slabs of 4 or 8 chunks");
+  static_assert(TH * OW == NPT * 32 && (OW & (OW - 1)) == 0, "whole output rows of a power-of-two width");
+  static_assert(kThreads <= 1024, "block size");
+  static_assert(STAGES >= 2 && STAGES * kStage * 16 <= 160 * 1024, "LDS budget");
+  static_assert(kWaves * 64 * 4 <= STAGES * kStage, "the partial tiles fit the stage buffers");
+  static_assert(2 * NHI < 64, "vmcnt range");
+};
+
+template <int CC> __device__ __forceinline__ int wk_swz(int r) {
+  if constexpr (CC == 4) return (r >> 2) & 3;
+  else return (r >> 1) & 7;
+}
+
+template <Op O, class Wt, class Epi>
+__global__ void __launch_bounds__(Wt::kThreads) wk_conv_kernel(const HaloGeo g, const Epi epi, int nP, int nQ) {
+  using A = typename OpT<O>::Acc;
+  constexpr int CC = Wt::CC;
+  __shared__ u32x4 smem[Wt::STAGES * Wt::kStage];
+  const int t = threadIdx.x;
+  const int lane = t & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+  const int pt = wave % Wt::NPT, ks = wave / Wt::NPT;
+  int tp, tq;
+  // each XCD owns whole output-channel tiles (the filter is the operand
+  // that would otherwise be re-read from every XCD)
+  map_tile(blockIdx.x, gridDim.x, nP, nQ, nP, tp, tq);
+  const int pix0 = tp * (Wt::NPT * 32), co0 = tq * 32;
+  const int ohw = g.OH * g.OW;
+  const int n = pix0 / ohw;
+  const int oy0 = (pix0 - n * ohw) >> g.ow_shift;
+
+  const __amdgpu_buffer_rsrc_t rw =
+      __builtin_amdgcn_make_buffer_rsrc((void*)(g.w + (int64_t)co0 * g.ldw), (short)0, 0x7fffffff, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rx =
+      __builtin_amdgcn_make_buffer_rsrc((void*)(g.x + (int64_t)n * g.img_bytes), (short)0, 0x7fffffff, 0x00020000);
+
+  // this thread's share of a stage's DMA loads (load m of a stage belongs
+  // to wave m % waves): global offset at slab 0 and the channel chunk
+  int voff[Wt::NHI], sub[Wt::NHI];
+#pragma unroll
+  for (int i = 0; i < Wt::NHI; ++i) {
+    const int m = i * Wt::kWaves + wave;
+    voff[i] = kOobOffset;
+    sub[i] = 0;
+    if (m < Wt::WI) {
+      const int slot = m * 64 + lane;
+      const int row = slot / Wt::RW, phys = slot - row * Wt::RW;
+      const int tap = phys / CC, c = (phys - tap * CC) ^ wk_swz<CC>(row);
+      sub[i] = c;
+      if (co0 + row < g.cout) voff[i] = (int)(row * g.ldw) + (tap * g.cpc + c) * 16;
+    } else if (m < Wt::TI) {
+      const int slot = (m - Wt::WI) * 64 + lane;
+      const int pix = slot / CC, c = (slot - pix * CC) ^ wk_swz<CC>(pix);
+      const int py = pix / Wt::PW, px = pix - py * Wt::PW;
+      int iy = oy0 + py - g.pt, ix = px - g.pl;
+      if (g.pad_mode == 1) {          // reflect (pads below the extent; the host checks)
+        iy = iy < 0 ? -iy : (iy >= g.H ? 2 * g.H - 2 - iy : iy);
+        ix = ix < 0 ? -ix : (ix >= g.W ? 2 * g.W - 2 - ix : ix);
+      } else if (g.pad_mode == 2) {   // edge
+        iy = iy < 0 ? 0 : (iy >= g.H ? g.H - 1 : iy);
+        ix = ix < 0 ? 0 : (ix >= g.W ? g.W - 1 : ix);
+      }
+      sub[i] = c;
+      if (pix < Wt::NPIX && (unsigned)iy < (unsigned)g.H && (unsigned)ix < (unsigned)g.W)
+        voff[i] = ((iy * g.W + ix) * g.pstride + c) * 16;
+    }
+  }
+  const int nslab = (g.cpc + CC - 1) / CC;
+  // every stage issues the same loads (past the last slab, and in the
+  // channel tail, they read zero through the range check), so the waits
+  // are fixed counts
+  auto issue = [&](int s) __attribute__((always_inline)) {
+    u32x4* base = smem + (s % Wt::STAGES) * Wt::kStage;
+    const bool live = s < nslab;
+    const int soff = s * CC * 16;
+#pragma unroll
+    for (int i = 0; i < Wt::NHI; ++i) {
+      const int m = i * Wt::kWaves + wave;
+      if (m < Wt::TI) {
+        const int off = live && s * CC + sub[i] < g.cpc ? voff[i] : kOobOffset;
+        buf16(m < Wt::WI ? rw : rx, off, soff, base + m * 64);
+      }
+    }
+  };
+  auto wait_stages = [&](auto kc) __attribute__((always_inline)) {
+    constexpr int K = decltype(kc)::value;
+    if (wave < Wt::TI % Wt::kWaves) wait_vmcnt<K * Wt::NHI>();
+    else wait_vmcnt<K * Wt::NLO>();
+  };
+
+  // fragment slots: filter row lane % 32, chunk 2 ks + lane / 32 of each
+  // tap; patch pixel of this lane's output pixel, shifted per tap
+  const int hi = lane >> 5;
+  const int cc = 2 * ks + hi;
+  const int wrow = lane & 31;
+  const int wbase = wrow * Wt::RW + (cc ^ wk_swz<CC>(wrow));
+  const int ql = pt * 32 + (lane & 31);
+  const int pbase = (ql >> g.ow_shift) * Wt::PW + (ql & (Wt::OW - 1));
+
+  A acc;
+#pragma unroll
+  for (int e = 0; e < 16; ++e) acc[e] = 0;
+#pragma unroll
+  for (int s = 0; s < Wt::STAGES - 1; ++s) issue(s);
+  wait_stages(std::integral_constant<int, Wt::STAGES - 2>{});
+  barrier_only();
+  for (int s = 0; s < nslab; ++s) {
+    issue(s + Wt::STAGES - 1);
+    const u32x4* S = smem + (s % Wt::STAGES) * Wt::kStage;
+    const u32x4* SP = S + Wt::WI * 64;
+    u32x4 wf[9], pf[9];
+#pragma unroll
+    for (int tap = 0; tap < 9; ++tap) {
+      const int ky = tap / 3, kx = tap - ky * 3;
+      wf[tap] = S[wbase + tap * CC];
+      const int pix = pbase + ky * Wt::PW + kx;
+      pf[tap] = SP[pix * CC + (cc ^ wk_swz<CC>(pix))];
+    }
+#pragma unroll
+    for (int tap = 0; tap < 9; ++tap) {
+      if constexpr (Wt::PIX_ON_X) acc = OpT<O>::mma(pf[tap], wf[tap], acc);
+      else acc = OpT<O>::mma(wf[tap], pf[tap], acc);
+    }
+    wait_stages(std::integral_constant<int, Wt::STAGES - 2>{});
+    wait_lgkm0();
+    barrier_only();
+  }
+
+  // the waves' partial tiles meet in LDS (the stage buffers, free once every
+  // load has landed: past the last slab they read zero but still land)
+  wait_vmcnt<0>();
+  barrier_only();
+  f32x4* red = reinterpret_cast<f32x4*>(smem);
+#pragma unroll
+  for (int gq = 0; gq < 4; ++gq)
+    red[(wave * 4 + gq) * 64 + lane] = f32x4{acc[4 * gq], acc[4 * gq + 1], acc[4 * gq + 2], acc[4 * gq + 3]};
+  __syncthreads();
+  if (wave >= Wt::NPT) return;
+  // wave pt adds the partial tiles of k-steps 0 .. KSN - 1 in that order and
+  // finishes its 32 pixels x 32 channels
+  const OutAddr out = epi.addr();
+  const int pixl = pix0 + pt * 32;
+  const int jl = Wt::PIX_ON_X ? co0 + (lane & 31) : pixl + (lane & 31);
+  typename Epi::PreJ pj;
+  epi.load_j(pj, jl);
+#pragma unroll
+  for (int gq = 0; gq < 4; ++gq) {
+    f32x4 v = red[(pt * 4 + gq) * 64 + lane];
+#pragma unroll
+    for (int k2 = 1; k2 < Wt::KSN; ++k2) v += red[((pt + k2 * Wt::NPT) * 4 + gq) * 64 + lane];
+    const int i = (Wt::PIX_ON_X ? pixl : co0) + 8 * gq + 4 * hi;
+    typename Epi::PreI pi;
+    epi.load_i(pi, i);
+    typename OpT<O>::Out4 a4;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) a4[e] = v[e];
+    uint32_t bits[4];
+    epi.finish(pi, pj, i, jl, a4, bits);
+    store_group(out, epi.out_bytes(), out.row(i), i, jl, bits);
+  }
+}
+
+}  // namespace ohip

@@ -221,6 +221,9 @@ struct HaloGeo {
   int cout;           // valid filter rows
 };
 hipError_t run_halo_float(int dtype, const HaloGeo& g, bool pix_on_x, const FloatOut& o, hipStream_t st);
+// the whole-K variant (wk_conv_kernel): every block runs the whole
+// reduction, no split-K partial sums (HaloGeo.th unused)
+hipError_t run_wk_float(int dtype, const HaloGeo& g, bool pix_on_x, const FloatOut& o, hipStream_t st);
 // pixel-tile extent and largest staged patch of the halo path
 constexpr int kHaloBPix = 256;
 constexpr int kHaloPixMax = 400;       // patch pixels of a 16-, 32- or 64-wide output row tile

@@ -480,6 +480,29 @@ inline hipError_t launch_halo(const HaloGeo& g, const Epi& epi, int P, int Q, in
   return launch_halo_px<O, PIXX, Epi, kHaloPixMax>(g, epi, P, Q, splits, ws, st);
 }
 
+// Whole-K halo convolution (wk_conv_kernel): NPT * 32 pixels (whole output
+// rows) x 32 output channels a block, eight-chunk (128-byte) slabs, two
+// stages.  32-wide rows take two pixel tiles (eight waves), 16- and 64-wide
+// rows four (sixteen waves: a 64-wide tile is two rows, a 16-wide one
+// eight).
+template <Op O, bool PIXX, class Epi>
+inline hipError_t launch_wk(const HaloGeo& g, const Epi& epi, int P, int Q, hipStream_t st) {
+  auto go = [&](auto wt) -> hipError_t {
+    using Wt = decltype(wt);
+    const int pix = PIXX ? P : Q, co = PIXX ? Q : P;
+    const int nP = pix / (Wt::NPT * 32), nQ = (co + 31) / 32;
+    if (nP <= 0 || nQ <= 0) return hipSuccess;
+    if (pix % (Wt::NPT * 32) != 0 || (int64_t)nP * nQ > 0x7fffffff) return hipErrorInvalidValue;
+    hipLaunchKernelGGL((wk_conv_kernel<O, Wt, Epi>), dim3((unsigned)(nP * nQ)), dim3(Wt::kThreads), 0, st, g, epi,
+                       nP, nQ);
+    return hipGetLastError();
+  };
+  if (g.OW == 32) return go(WkTile<32, 2, 8, 2, PIXX>{});
+  if (g.OW == 64) return go(WkTile<64, 4, 8, 2, PIXX>{});
+  if (g.OW == 16) return go(WkTile<16, 4, 8, 2, PIXX>{});
+  return hipErrorInvalidValue;
+}
+
 // Automatic choice (split-K is decided beforehand, plan_splits).  The
 // largest tile that still gives at least one block per CU (256 CUs); among
 // the smaller tiles, the two-stage 128x128 tile keeps two blocks resident

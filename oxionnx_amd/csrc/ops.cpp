@@ -348,7 +348,7 @@ extern "C" int ohip_sync(ohip_ctx* ctx) {
 
 extern "C" int ohip_set_tile_override(ohip_ctx* ctx, int tile_id) {
   if (!ctx) return fail(OHIP_E_INVALID, "null context");
-  if (tile_id < 0 || tile_id > 16) return fail(OHIP_E_INVALID, "tile id must be 0..16");
+  if (tile_id < 0 || tile_id > 17) return fail(OHIP_E_INVALID, "tile id must be 0..17");
   ctx->tile_override = tile_id;
   return OHIP_OK;
 }
@@ -1311,6 +1311,39 @@ static int halo_plan(ohip_ctx* ctx, const ohip_conv_desc* d, int64_t G, int64_t 
   return (int)std::max<int64_t>(s, 1);
 }
 
+static bool wk_allowed() {
+  static const bool v = [] {
+    const char* e = std::getenv("OHIP_WK");
+    return !(e && e[0] == '0');
+  }();
+  return v;
+}
+
+// Whether a 3x3 stride-1 convolution runs the whole-K halo kernel
+// (wk_conv_kernel): f16 / bf16, output rows 16, 32 or 64 wide tiling its
+// pixel blocks (64 pixels at 32-wide rows, 128 otherwise) and 32-channel
+// blocks into at least one block per CU (256), and enough work (1.5 GFLOP)
+// for the launch to amortise.  Those are the mid-size convolutions the
+// halo kernel would split four or more ways: the whole-K blocks write their
+// outputs once instead (config 4's 512 -> 512 conv at 32x32: 12 us against
+// 18 us plus the reduction of 8 MB of partial sums).  Tile override 17
+// forces it wherever the geometry allows.
+static bool wk_plan(ohip_ctx* ctx, const ohip_conv_desc* d, int64_t G, int64_t w_in, const ConvGeo& g,
+                    int64_t img_bytes) {
+  const bool forced = ctx->tile_override == 17;
+  if (!wk_allowed() || (ctx->tile_override != 0 && !forced) || G != 1) return false;
+  if (d->dtype != OHIP_F16 && d->dtype != OHIP_BF16) return false;
+  if (d->kh != 3 || d->kw != 3 || d->stride_h != 1 || d->stride_w != 1 || d->dil_h != 1 || d->dil_w != 1) return false;
+  if (g.ow != 16 && g.ow != 32 && g.ow != 64) return false;
+  const int64_t tpx = g.ow == 32 ? 64 : 128;
+  if ((g.oh * g.ow) % tpx != 0 || w_in > 65535 || img_bytes >= ((int64_t)1 << 31) - 65536) return false;
+  if (forced) return true;
+  const int64_t rows = d->n * g.oh * g.ow;
+  const int64_t blocks = rows / tpx * ((d->cout + 31) / 32);
+  const double flops = 2.0 * (double)rows * (double)d->cout * (double)d->c * 9.0;
+  return blocks >= 256 && flops >= 1.5e9;
+}
+
 // A fused instance normalisation for conv2d_impl (ohip_conv2d_instnorm).
 struct ConvNorm {
   float eps;
@@ -1466,10 +1499,11 @@ static int conv2d_impl(ohip_ctx* ctx, const ohip_conv_desc* d, const void* x, co
   // 3x3 stride-1 convolutions whose output rows tile 256-pixel blocks run
   // the halo-patch kernel (the input patch staged once per channel slab for
   // all nine taps) instead of the engine's im2col gather.
-  const int hsplits = halo_plan(ctx, d, G, sw_, g, (int)(cp / ce), (int64_t)(sh_ * sw_ * cpt * eb));
-  if (nhwc_pad && !hsplits)
+  const bool wk = wk_plan(ctx, d, G, sw_, g, (int64_t)(sh_ * sw_ * cpt * eb));
+  const int hsplits = wk ? 0 : halo_plan(ctx, d, G, sw_, g, (int)(cp / ce), (int64_t)(sh_ * sw_ * cpt * eb));
+  if (nhwc_pad && !hsplits && !wk)
     return fail(OHIP_DECLINED, "ohip_conv2d: a reflect / edge Pad on an NHWC input needs the halo-patch path");
-  const SplitChoice sc = hsplits ? SplitChoice{hsplits, 0}
+  const SplitChoice sc = wk ? SplitChoice{1, 0} : hsplits ? SplitChoice{hsplits, 0}
                                  : plan_split_tile(sP, sQ, (int)(d->kh * d->kw * (cp / ce)), ctx->tile_override,
                                                    d->dtype == OHIP_F32);
   const int splits = sc.splits;
@@ -1502,7 +1536,7 @@ static int conv2d_impl(ohip_ctx* ctx, const ohip_conv_desc* d, const void* x, co
     return fail(OHIP_E_INVALID, "ohip_conv2d: NHWC input must be 16-byte aligned");
   }
 
-  if (hsplits) {
+  if (hsplits || wk) {
     HaloGeo hg{};
     hg.x = static_cast<const char*>(xin);
     hg.img_bytes = sh_ * sw_ * cpt * eb;
@@ -1532,8 +1566,9 @@ static int conv2d_impl(ohip_ctx* ctx, const ohip_conv_desc* d, const void* x, co
     o.split_ws = splits > 1 ? plan_at(sbase, plan, iw) : nullptr;
     o.defer_reduce = norm ? 1 : 0;
     ctx->counters.contraction_launches++;
-    hipError_t e = run_halo_float(d->dtype, hg, nchw_out, o, ctx->stream);
-    if (e != hipSuccess) return hip_fail(e, "ohip_conv2d halo launch");
+    hipError_t e = wk ? run_wk_float(d->dtype, hg, nchw_out, o, ctx->stream)
+                      : run_halo_float(d->dtype, hg, nchw_out, o, ctx->stream);
+    if (e != hipSuccess) return hip_fail(e, wk ? "ohip_conv2d whole-K halo launch" : "ohip_conv2d halo launch");
     if (norm) {
       e = run_instnorm_partials(d->dtype, static_cast<const float*>(o.split_ws), splits, (rows + 3) / 4 * 4, bias,
                                 y, d->n, ohw, (int)d->cout, norm->eps, norm->aff, norm_nhwc, ctx->stream);
@@ -1617,6 +1652,7 @@ int ohip_conv_halo_splits_internal(ohip_ctx* ctx, const ohip_conv_desc* d) {
     return 0;
   const int eb = elem_bytes(d->dtype), ce = 16 / eb;
   const int64_t cp = round_up(d->c, ce);
+  if (wk_plan(ctx, d, 1, d->w, g, d->h * d->w * cp * eb)) return 1;
   return halo_plan(ctx, d, 1, d->w, g, (int)(cp / ce), d->h * d->w * cp * eb);
 }
 

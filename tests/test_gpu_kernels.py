@@ -478,6 +478,57 @@ def test_halo_conv_matches_oracle(torch, ctx, case, dt, nhwc_out):
     assert _rel_err(got, want) <= HALF_TOL
 
 
+# Whole-K halo path (3x3, stride 1, 64- or 128-pixel tiles of whole output
+# rows x 32 channels, every block over the whole reduction): (x shape, cout,
+# pads).  The 512-channel residual conv of config 4, channel tails inside the
+# eight-chunk slab (24, 72 and 40 channels), partial 32-channel tiles, two
+# images, 16- and 64-wide rows, a valid (unpadded) conv and uneven pads.
+WK_CASES = [
+    ((1, 512, 32, 32), 512, (1, 1, 1, 1)),
+    ((2, 24, 32, 32), 40, (1, 1, 1, 1)),
+    ((1, 72, 16, 64), 96, (1, 1, 1, 1)),
+    ((1, 40, 16, 16), 33, (1, 1, 1, 1)),
+    ((1, 16, 34, 34), 64, (0, 0, 0, 0)),
+    ((1, 8, 33, 32), 24, (2, 1, 1, 1)),
+]
+
+
+@pytest.mark.parametrize("case", WK_CASES, ids=lambda c: f"{c[0]}x{c[1]}p{c[2]}")
+@pytest.mark.parametrize("dt", ["f16", "bf16"])
+@pytest.mark.parametrize("nhwc_out", [False, True], ids=["nchw", "nhwc"])
+def test_wk_conv_matches_oracle(torch, ctx, case, dt, nhwc_out):
+    from oxionnx_amd import _lib as L
+    xs, cout, p = case
+    rng = np.random.default_rng(17 + sum(xs) + cout)
+    x = rng.uniform(-1, 1, xs).astype(np.float32)
+    w = rng.normal(0, 0.05, (cout, xs[1], 3, 3)).astype(np.float32)
+    b = rng.normal(0, 0.01, cout).astype(np.float32)
+    lay = L.NHWC if nhwc_out else L.NCHW
+    bf16 = dt == "bf16"
+    xh, wh, bh = (O.f32_to_half_bits(v, bf16) for v in (x, w, b))
+    tdt = torch.bfloat16 if bf16 else torch.float16
+    wt = ctx.weight_conv(O.half_bits_to_f32(wh, bf16), dtype=L.BF16 if bf16 else L.F16)
+    xt = torch.from_numpy(xh.view(np.int16)).cuda().view(tdt)
+    bt = torch.from_numpy(bh.view(np.int16)).cuda().view(tdt)
+    ctx.set_tile(17)   # the whole-K halo kernel wherever the geometry allows
+    try:
+        y = ctx.conv2d(xt, wt, bt, pads=p, act=L.ACT_RELU, out_layout=lay)
+    finally:
+        ctx.set_tile(0)
+    if nhwc_out:
+        y = y[..., :cout].permute(0, 3, 1, 2)
+    y = y.contiguous()
+    got = O.half_bits_to_f32(y.view(torch.int16).cpu().numpy().view(np.uint16), bf16)
+    want = O.half_bits_to_f32(O.conv_half(xh, wh, bh, bf16=bf16, activation="relu", pads=p), bf16)
+    assert _rel_err(got, want) <= HALF_TOL
+    # the automatic plan takes it for the 512-channel conv (256 blocks)
+    if xs[1] == 512:
+        y2 = ctx.conv2d(xt, wt, bt, pads=p, act=L.ACT_RELU, out_layout=lay)
+        if nhwc_out:
+            y2 = y2[..., :cout].permute(0, 3, 1, 2)
+        assert torch.equal(y2.contiguous(), y)
+
+
 # ------------------------------------------------------------------ few output channels on the MFMA
 FEWCO_CASES = [
     # (N, C, H, W, cout, k, pad mode)
