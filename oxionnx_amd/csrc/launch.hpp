@@ -485,22 +485,31 @@ inline hipError_t launch_halo(const HaloGeo& g, const Epi& epi, int P, int Q, in
 // stages.  32-wide rows take two pixel tiles (eight waves), 16- and 64-wide
 // rows four (sixteen waves: a 64-wide tile is two rows, a 16-wide one
 // eight).
+// A deferred epilogue (the fused conv -> norm node) leaves the raw f32 sums
+// in `ws` instead, as one split-K slice, for the norm kernel that reads
+// partial sums.
 template <Op O, bool PIXX, class Epi>
-inline hipError_t launch_wk(const HaloGeo& g, const Epi& epi, int P, int Q, hipStream_t st) {
-  auto go = [&](auto wt) -> hipError_t {
+inline hipError_t launch_wk(const HaloGeo& g, const Epi& epi, int P, int Q, void* ws, hipStream_t st) {
+  auto go = [&](auto wt, const auto& e) -> hipError_t {
     using Wt = decltype(wt);
+    using E = std::decay_t<decltype(e)>;
     const int pix = PIXX ? P : Q, co = PIXX ? Q : P;
     const int nP = pix / (Wt::NPT * 32), nQ = (co + 31) / 32;
     if (nP <= 0 || nQ <= 0) return hipSuccess;
     if (pix % (Wt::NPT * 32) != 0 || (int64_t)nP * nQ > 0x7fffffff) return hipErrorInvalidValue;
-    hipLaunchKernelGGL((wk_conv_kernel<O, Wt, Epi>), dim3((unsigned)(nP * nQ)), dim3(Wt::kThreads), 0, st, g, epi,
-                       nP, nQ);
+    hipLaunchKernelGGL((wk_conv_kernel<O, Wt, E>), dim3((unsigned)(nP * nQ)), dim3(Wt::kThreads), 0, st, g, e, nP,
+                       nQ);
     return hipGetLastError();
   };
-  if (g.OW == 32) return go(WkTile<32, 2, 8, 2, PIXX>{});
-  if (g.OW == 64) return go(WkTile<64, 4, 8, 2, PIXX>{});
-  if (g.OW == 16) return go(WkTile<16, 4, 8, 2, PIXX>{});
-  return hipErrorInvalidValue;
+  auto pick = [&](const auto& e) -> hipError_t {
+    if (g.OW == 32) return go(WkTile<32, 2, 8, 2, PIXX>{}, e);
+    if (g.OW == 64) return go(WkTile<64, 4, 8, 2, PIXX>{}, e);
+    if (g.OW == 16) return go(WkTile<16, 4, 8, 2, PIXX>{}, e);
+    return hipErrorInvalidValue;
+  };
+  if (!epi.out.defer) return pick(epi);
+  if (!ws || !PIXX || O == Op::I8) return hipErrorInvalidValue;
+  return pick(PartialEpi<float>{reinterpret_cast<float*>(ws), P, (P + 3) / 4 * 4, Q});
 }
 
 // Automatic choice (split-K is decided beforehand, plan_splits).  The

@@ -1507,11 +1507,15 @@ static int conv2d_impl(ohip_ctx* ctx, const ohip_conv_desc* d, const void* x, co
                                  : plan_split_tile(sP, sQ, (int)(d->kh * d->kw * (cp / ce)), ctx->tile_override,
                                                    d->dtype == OHIP_F32);
   const int splits = sc.splits;
-  if (norm && splits == 1) {   // counted again by the two-step path's plain call
+  if (norm && splits == 1 && !wk) {   // counted again by the two-step path's plain call
     ctx->counters.dispatches--;
     return kNormTwoStep;
   }
-  size_t iw = splits > 1 ? plan.add(split_ws_bytes(sP, sQ, splits)) : SIZE_MAX;
+  // the whole-K kernel under a norm leaves its sums as one slice of f32
+  // partial sums for the norm kernel
+  const bool partials = splits > 1 || (wk && norm);
+  size_t iw = partials ? plan.add(splits > 1 ? split_ws_bytes(sP, sQ, splits) : (size_t)sQ * ((sP + 3) / 4 * 4) * 4)
+                       : SIZE_MAX;
   char* sbase = nullptr;
   rc = call_scratch(ctx, plan.total(), noalloc, &sbase);
   if (rc) return rc;
@@ -1563,7 +1567,7 @@ static int conv2d_impl(ohip_ctx* ctx, const ohip_conv_desc* d, const void* x, co
       o.bias_mode = BIAS_I;
     }
     o.splits = splits;
-    o.split_ws = splits > 1 ? plan_at(sbase, plan, iw) : nullptr;
+    o.split_ws = partials ? plan_at(sbase, plan, iw) : nullptr;
     o.defer_reduce = norm ? 1 : 0;
     ctx->counters.contraction_launches++;
     hipError_t e = wk ? run_wk_float(d->dtype, hg, nchw_out, o, ctx->stream)
