@@ -33,7 +33,7 @@ FLAGS = [
 def _compile(src, incremental=False):
     obj = os.path.join(OUT_DIR, os.path.splitext(src)[0] + ".o")
     if incremental and os.path.exists(obj):
-        kern = ["mfma_core.hpp", "launch.hpp", "internal.hpp"]
+        kern = ["mfma_core.hpp", "launch.hpp", "internal.hpp", "halo_conv.hpp"]
         local = {"ops.cpp": ["internal.hpp"], "dispatch.cpp": ["internal.hpp"],
                  "aux_kernels.hip": kern, "nodes.hip": ["internal.hpp"]}.get(src, kern + ["contract.inc"])
         deps = [os.path.join(CSRC, f) for f in [src] + local]

@@ -240,22 +240,31 @@ class HipContext:
         return out
 
     def conv2d_instnorm(self, x, w, bias=None, pads=(0, 0, 0, 0), strides=(1, 1), dilations=(1, 1), eps=1e-5,
-                        gamma=None, beta=None, scale_offset=0, bias_offset=0, relu=False, out=None):
-        """Conv (NCHW, ungrouped, no activation) followed by instance
+                        gamma=None, beta=None, scale_offset=0, bias_offset=0, relu=False, out=None,
+                        residual=None, nhwc=False):
+        """Conv (ungrouped, no activation) followed by instance
         normalisation in one call (ohip_conv2d_instnorm); gamma / beta are
         optional [N, S] device rows of the tensor's dtype (the AdaIN form:
-        channel c of sample n reads element n * S + offset + c)."""
+        channel c of sample n reads element n * S + offset + c); residual is
+        added last.  nhwc: x, the output and the residual are NHWC (channels
+        a whole number of 16-byte chunks), else NCHW."""
         torch = _torch()
         dt = ohip_dtype(x.dtype)
         cout, cin, kh, kw = w.shape
-        n, c, h, wd = x.shape
+        if nhwc:
+            n, h, wd, c = x.shape
+        else:
+            n, c, h, wd = x.shape
         oh = L.lib().ohip_conv_out_dim(h, pads[0], pads[2], kh, dilations[0], strides[0])
         ow = L.lib().ohip_conv_out_dim(wd, pads[1], pads[3], kw, dilations[1], strides[1])
         if out is None:
-            out = torch.empty((n, cout, oh, ow), dtype=x.dtype, device=x.device)
+            shape = (n, oh, ow, cout) if nhwc else (n, cout, oh, ow)
+            out = torch.empty(shape, dtype=x.dtype, device=x.device)
+        lay = L.NHWC if nhwc else L.NCHW
         d = L.ConvDesc(n, c, h, wd, cout, kh, kw, 1, strides[0], strides[1], dilations[0], dilations[1],
-                       pads[0], pads[1], pads[2], pads[3], dt, L.NCHW, L.NCHW, L.ACT_NONE, 0.0, 0.0, 0)
-        nd = L.NormDesc(eps, None, None, 0, 0, 0, L.ACT_RELU if relu else L.ACT_NONE, 0.0)
+                       pads[0], pads[1], pads[2], pads[3], dt, lay, lay, L.ACT_NONE, 0.0, 0.0, 0)
+        nd = L.NormDesc(eps, None, None, 0, 0, 0, L.ACT_RELU if relu else L.ACT_NONE, 0.0,
+                        None if residual is None else residual.data_ptr(), lay)
         if gamma is not None:
             eb = L.ELEM_BYTES[dt]
             nd.scale = gamma.data_ptr() + scale_offset * eb

@@ -635,6 +635,60 @@ def test_conv2d_instnorm_entry_point(torch, ctx, case):
     assert _rel_err(got, want) <= (HALF_TOL if half else F32_TOL)
 
 
+# (x shape, cout, tile): config 4's residual conv (the automatic plan), a
+# 16-wide image pair with a partial 32-channel tile, and a channel tail
+# inside the eight-chunk slab (tile 17 forces the whole-K kernel)
+WK_NORM_CASES = [
+    ((1, 512, 32, 32), 512, 0),
+    ((2, 64, 16, 16), 96, 17),
+    ((1, 40, 32, 32), 72, 17),
+]
+
+
+@pytest.mark.parametrize("case", WK_NORM_CASES, ids=str)
+@pytest.mark.parametrize("residual", [False, True], ids=["plain", "residual"])
+def test_conv_instnorm_nhwc_matches_nchw(torch, ctx, case, residual):
+    """f16 conv -> AdaIN norm -> Relu [-> residual] on the whole-K kernel with
+    NHWC input, output and residual (the norm reader writes four channels of
+    each pixel as one run) equals the NCHW call bit for bit, twice in a row,
+    and both are within the f16 bar of the oracle."""
+    from oxionnx_amd import _lib as L
+    xs, cout, tile = case
+    n, c, h, w_ = xs
+    rng = np.random.default_rng(c + cout + n)
+    x = rng.uniform(-1, 1, xs).astype(np.float32)
+    w = rng.normal(0, 0.05, (cout, c, 3, 3)).astype(np.float32)
+    b = rng.normal(0, 0.01, cout).astype(np.float32)
+    ab = rng.normal(1, 0.3, (n, 2 * cout)).astype(np.float32)
+    res = rng.uniform(-1, 1, (n, cout, h, w_)).astype(np.float32)
+    xh, wh, bh, abh, rh = (O.f32_to_half_bits(v) for v in (x, w, b, ab, res))
+    dev = lambda v: torch.from_numpy(v.view(np.int16)).cuda().view(torch.float16)   # noqa: E731
+    wt = ctx.weight_conv(O.half_bits_to_f32(wh), dtype=L.F16)
+    xt, bt, abt, rt = dev(xh), dev(bh), dev(abh), dev(rh)
+    kw = dict(pads=(1, 1, 1, 1), eps=1e-5, gamma=abt, beta=abt, scale_offset=0, bias_offset=cout, relu=True)
+    ctx.set_tile(tile)
+    try:
+        nchw = ctx.conv2d_instnorm(xt, wt, bt, residual=rt if residual else None, **kw)
+        xn = xt.permute(0, 2, 3, 1).contiguous()
+        rn = rt.permute(0, 2, 3, 1).contiguous()
+        for _ in range(2):
+            got = ctx.conv2d_instnorm(xn, wt, bt, residual=rn if residual else None, nhwc=True, **kw)
+            assert torch.equal(got.permute(0, 3, 1, 2), nchw)
+    finally:
+        ctx.set_tile(0)
+    conv = O.half_bits_to_f32(O.conv_half(xh, wh, bh, pads=(1, 1, 1, 1))).astype(np.float64)
+    g64 = O.half_bits_to_f32(abh).astype(np.float64)
+    rnd = lambda v: O.half_bits_to_f32(O.f32_to_half_bits(v.astype(np.float32))).astype(np.float64)  # noqa: E731
+    mean = conv.mean(axis=(2, 3), keepdims=True)
+    var = ((conv - mean) ** 2).mean(axis=(2, 3), keepdims=True)
+    want = rnd(rnd(rnd((conv - mean) / np.sqrt(var + 1e-5)) * g64[:, :cout, None, None]) + g64[:, cout:, None, None])
+    want = np.maximum(want, 0.0)
+    if residual:
+        want = want + O.half_bits_to_f32(rh).astype(np.float64)
+    got = O.half_bits_to_f32(nchw.contiguous().view(torch.int16).cpu().numpy().view(np.uint16)).astype(np.float64)
+    assert _rel_err(got, want) <= HALF_TOL
+
+
 # ------------------------------------------------------------------ integer GEMM
 @pytest.mark.parametrize("mkn", [(1, 16, 16), (4, 768, 96), (37, 100, 53), (128, 768, 3072), (300, 256, 200)],
                          ids=str)
