@@ -46,8 +46,42 @@ def parse():
                    help="end-to-end items: skip the reference-fusions-only forwards (a kernel trace then holds "
                         "only the provider's fused graph)")
     p.add_argument("--only", default="", help="run one item (for profiling): 'headline', 'copy', "
-                   "'conv_f32_cfg1', 'int8_ffn', or a sweep item such as 'gemm_f16_2048x4096x4096'")
+                   "'conv_f32_cfg1', 'int8_ffn', 'matmul_integer_i32', or a sweep item such as "
+                   "'gemm_f16_2048x4096x4096'")
+    p.add_argument("--trace-stats", default="", metavar="CSV",
+                   help="summarise a rocprofv3 kernel_trace.csv or counter_collection.csv per (kernel, grid) "
+                        "instead of benchmarking")
+    p.add_argument("--trace-last", type=int, default=0,
+                   help="with --trace-stats: also average each group's last N dispatches (the timed steps)")
     return p.parse_args()
+
+
+def trace_stats(path, last):
+    """Per (full kernel name, grid size): dispatch count and average duration
+    (kernel traces), or the average of each counter (counter collections)."""
+    import csv
+    import re
+    rows = list(csv.DictReader(open(path)))
+    groups = {}
+    for r in rows:
+        name = re.sub(r"\s+", " ", r["Kernel_Name"])
+        grid = r.get("Grid_Size") or r.get("Grid_Size_X") or ""
+        groups.setdefault((name, grid), []).append(r)
+    for (name, grid), rs in groups.items():
+        if "Counter_Name" in rs[0]:
+            ctr = {}
+            for r in rs:
+                ctr.setdefault(r["Counter_Name"], []).append(float(r["Counter_Value"]))
+            print(f"kernel {name}\n  grid {grid}")
+            for c, v in ctr.items():
+                print(f"  {c:36s} dispatches {len(v):4d}  avg {sum(v) / len(v):.6g}")
+            continue
+        rs.sort(key=lambda r: int(r["Start_Timestamp"]))
+        d = [(int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3 for r in rs]
+        line = f"dispatches {len(d):5d}  avg {sum(d) / len(d):9.2f} us  min {min(d):9.2f} us"
+        if last and len(d) >= last:
+            line += f"  last {last}: avg {sum(d[-last:]) / last:9.2f} us"
+        print(f"kernel {name}\n  grid {grid}  {line}")
 
 
 def settle_clock(torch, fn, ms):
@@ -129,11 +163,17 @@ def cpu_baseline_f16(seconds):
     flops = 2.0 * rows * k * n
     return {"value": flops / dt / 1e12, "unit": "TFLOP/s", "cores": 1, "host_cores": HOST_CORES, "kind": "port",
             "sample": f"{rows} of {m} output rows of the f16 Gemm ({rows}x{k}x{n}), {dt:.2f} s; "
-                      f"full forward extrapolates to {dt * m / rows:.0f} s"}
+                      f"full forward extrapolates to {dt * m / rows:.0f} s; the restatement runs the "
+                      f"reference's per-element order (ascending k, f32 accumulate, no FMA) as an i-p-j "
+                      f"loop over contiguous B rows, faster than the reference's i-j-k loop that strides "
+                      f"B by n (math_typed.rs:612-629), so this baseline flatters the CPU"}
 
 
 def main():
     args = parse()
+    if args.trace_stats:
+        trace_stats(args.trace_stats, args.trace_last)
+        return
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only; how the path would shard across GPUs "
                                    "is a design note, not a measured path", "n_gpus": args.gpus}))
@@ -190,7 +230,10 @@ def main():
                         continue
                     _, _, _, ww, aa, cc, yy = gemm_setup(torch, ctx, L, mm, kk, nn, dt, rng)
                     iters = 200 if mm * kk * nn < 1e9 else 30
-                    t = time_launches(torch, stream, lambda: ctx.gemm(aa, ww, cc, out=yy), iters, 3)
+                    fn = lambda: ctx.gemm(aa, ww, cc, out=yy)   # noqa: E731
+                    if mm * kk * nn >= 1e10:
+                        settle_clock(torch, fn, 50.0)   # the large shapes at the settled clock, as the headline
+                    t = time_launches(torch, stream, fn, iters, 3)
                     eb = 4 if dt == L.F32 else 2
                     fl = 2.0 * mm * kk * nn
                     by = eb * (mm * kk + kk * nn + mm * nn + nn)
@@ -221,6 +264,9 @@ def main():
                      "kernel": "mfma_gemm_kernel<Op::F16, Tile<256,256,2,4,2,8,3>, DenseRows, DenseRows, FloatEpi<_Float16>, false, false>"},
         "wall_s_timed_region": round(wall, 3),
         "settle_ms_before_warmup": round(settled, 1),
+        "clock_note": "value is measured at the settled clock: the same launch runs back to back for "
+                      "settle_ms_before_warmup before the warm-up steps (an idle MI355X needs 10-20 ms of load "
+                      "to leave its idle clock); the sweep's large shapes settle 50 ms each the same way",
     }
     if not args.no_cpu and not args.only:
         line["cpu_baseline"] = cpu_baseline_f16(args.cpu_seconds)
@@ -250,7 +296,7 @@ def bench_conv(torch, ctx, L, stream, rng, only):
 
 def bench_int8(torch, ctx, L, stream, rng, only):
     """Config 3: QLinearMatMul BERT-base FFN pair + MatMulInteger."""
-    if only and only not in ("int8_ffn",):
+    if only and only not in ("int8_ffn", "matmul_integer_i32"):
         return {}
     out = {}
     a = rng.integers(0, 256, (4096, 768)).astype(np.uint8)
@@ -269,10 +315,13 @@ def bench_int8(torch, ctx, L, stream, rng, only):
         ctx.qgemm(at, w1, a_zp=128, a_scale=0.02, y_scale=0.05, y_zp=128, out=h)
         ctx.qgemm(h, w2, a_zp=128, a_scale=0.05, y_scale=0.05, y_zp=128, out=y)
 
-    t = time_launches(torch, stream, pair, 100, 5)
     ops = 2 * 2.0 * 4096 * 768 * 3072
-    out["int8_ffn_pair"] = {"ms": round(t, 5), "tops": round(ops / t / 1e9, 2),
-                            "frac_mfma": round(ops / t / 1e9 / PEAK_TFLOPS["int8"], 4)}
+    if only != "matmul_integer_i32":
+        t = time_launches(torch, stream, pair, 100, 5)
+        out["int8_ffn_pair"] = {"ms": round(t, 5), "tops": round(ops / t / 1e9, 2),
+                                "frac_mfma": round(ops / t / 1e9 / PEAK_TFLOPS["int8"], 4)}
+    if only == "int8_ffn":
+        return out
     t = time_launches(torch, stream, lambda: ctx.qgemm(at, w1, a_zp=128, out_kind=L.QOUT_I32, out=yi), 100, 5)
     by = 4096 * 768 + 768 * 3072 + 4 * 4096 * 3072
     out["matmul_integer_i32"] = {"ms": round(t, 5), "tops": round(ops / 2 / t / 1e9, 2),
@@ -506,9 +555,9 @@ def bench_e2e(torch, ctx, stream, only, no_cpu, fused_only=False):
                 "host_cores": HOST_CORES,
                 "sample": "one full forward of the same graph and inputs" + (
                     "; integer convolution single-threaded like the reference's integer_conv" if int8 else
-                    "; float convolution as im2col + a blocked, FMA-vectorised i-k-j sgemm over row "
-                    "splits (oracle/oracle_sgemm.c: a stand-in for matrixmultiply's packed microkernel, "
-                    "not that kernel)")}
+                    "; float convolution as im2col + a packed Goto/BLIS sgemm (AVX2/FMA 6x16 "
+                    "microkernel, rows split over the threads; oracle/oracle_sgemm.c: a stand-in for "
+                    "matrixmultiply's packed 8x8 microkernel, not that kernel)")}
             rec["speedup_vs_cpu"] = round(cpu / rec["ms_per_forward"], 1)
             rec["speedup_vs_cpu_run_loop"] = round(cpu / rec["ms_per_forward_run_loop"], 1)
             if not fused_only:
