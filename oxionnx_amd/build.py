@@ -33,9 +33,9 @@ FLAGS = [
 def _compile(src, incremental=False):
     obj = os.path.join(OUT_DIR, os.path.splitext(src)[0] + ".o")
     if incremental and os.path.exists(obj):
-        kern = ["mfma_core.hpp", "launch.hpp", "internal.hpp", "halo_conv.hpp"]
+        kern = ["mfma_core.hpp", "launch.hpp", "internal.hpp", "halo_conv.hpp", "norm_stats.hpp"]
         local = {"ops.cpp": ["internal.hpp"], "dispatch.cpp": ["internal.hpp"],
-                 "aux_kernels.hip": kern, "nodes.hip": ["internal.hpp"]}.get(src, kern + ["contract.inc"])
+                 "aux_kernels.hip": kern, "nodes.hip": ["internal.hpp", "norm_stats.hpp"]}.get(src, kern + ["contract.inc"])
         deps = [os.path.join(CSRC, f) for f in [src] + local]
         if src.endswith(".cpp"):
             deps.append(os.path.join(ROOT, "include", "ohip.h"))

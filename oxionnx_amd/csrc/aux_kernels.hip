@@ -18,9 +18,9 @@ hipError_t run_conv_i8(const Im2colOperand&, const DenseOperand&, bool, const Qu
 hipError_t run_halo_f32(const HaloGeo&, bool, const FloatOut&, hipStream_t);
 hipError_t run_halo_f16(const HaloGeo&, bool, const FloatOut&, hipStream_t);
 hipError_t run_halo_bf16(const HaloGeo&, bool, const FloatOut&, hipStream_t);
-hipError_t run_wk_f32(const HaloGeo&, bool, const FloatOut&, hipStream_t);
-hipError_t run_wk_f16(const HaloGeo&, bool, const FloatOut&, hipStream_t);
-hipError_t run_wk_bf16(const HaloGeo&, bool, const FloatOut&, hipStream_t);
+hipError_t run_wk_f32(const HaloGeo&, bool, const FloatOut&, float*, hipStream_t);
+hipError_t run_wk_f16(const HaloGeo&, bool, const FloatOut&, float*, hipStream_t);
+hipError_t run_wk_bf16(const HaloGeo&, bool, const FloatOut&, float*, hipStream_t);
 
 hipError_t run_dense_float(int dtype, const DenseOperand& x, const DenseOperand& y, const FloatOut& o, int tile,
                            hipStream_t st) {
@@ -51,11 +51,11 @@ hipError_t run_halo_float(int dtype, const HaloGeo& g, bool pix_on_x, const Floa
   }
 }
 
-hipError_t run_wk_float(int dtype, const HaloGeo& g, bool pix_on_x, const FloatOut& o, hipStream_t st) {
+hipError_t run_wk_float(int dtype, const HaloGeo& g, bool pix_on_x, const FloatOut& o, float* mom, hipStream_t st) {
   switch (dtype) {
-    case DT_F32: return run_wk_f32(g, pix_on_x, o, st);
-    case DT_F16: return run_wk_f16(g, pix_on_x, o, st);
-    case DT_BF16: return run_wk_bf16(g, pix_on_x, o, st);
+    case DT_F32: return run_wk_f32(g, pix_on_x, o, mom, st);
+    case DT_F16: return run_wk_f16(g, pix_on_x, o, mom, st);
+    case DT_BF16: return run_wk_bf16(g, pix_on_x, o, mom, st);
     default: return hipErrorInvalidValue;
   }
 }

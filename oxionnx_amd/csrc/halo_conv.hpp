@@ -32,6 +32,7 @@
 #pragma once
 #include "internal.hpp"
 #include "mfma_core.hpp"
+#include "norm_stats.hpp"
 
 namespace ohip {
 
@@ -267,8 +268,13 @@ template <int CC> __device__ __forceinline__ int wk_swz(int r) {
   else return (r >> 1) & 7;
 }
 
+// mom != null (a conv under an instance norm, no activation): the kernel
+// also writes the moments of each 64-pixel segment of every output plane
+// (norm_stats.hpp) at mom[((n * C + c) * S + segment) * 2] = (mean, M2), S =
+// OH * OW / 64, from the values the epilogue stores, T(sum + bias).
 template <Op O, class Wt, class Epi>
-__global__ void __launch_bounds__(Wt::kThreads) wk_conv_kernel(const HaloGeo g, const Epi epi, int nP, int nQ) {
+__global__ void __launch_bounds__(Wt::kThreads) wk_conv_kernel(const HaloGeo g, const Epi epi, int nP, int nQ,
+                                                               float* __restrict__ mom, const void* mbias, int C) {
   using A = typename OpT<O>::Acc;
   constexpr int CC = Wt::CC;
   __shared__ u32x4 smem[Wt::STAGES * Wt::kStage];
@@ -391,6 +397,58 @@ __global__ void __launch_bounds__(Wt::kThreads) wk_conv_kernel(const HaloGeo g, 
   for (int gq = 0; gq < 4; ++gq)
     red[(wave * 4 + gq) * 64 + lane] = f32x4{acc[4 * gq], acc[4 * gq + 1], acc[4 * gq + 2], acc[4 * gq + 3]};
   __syncthreads();
+  // the finished tile of pixel tile pt: its k-steps' partial tiles added in
+  // k-step order (group gq: the lane's rows 8 gq + 4 (lane / 32) .. + 3)
+  auto tile_sum = [&](int gq) __attribute__((always_inline)) {
+    f32x4 v = red[(pt * 4 + gq) * 64 + lane];
+#pragma unroll
+    for (int k2 = 1; k2 < Wt::KSN; ++k2) v += red[((pt + k2 * Wt::NPT) * 4 + gq) * 64 + lane];
+    return v;
+  };
+  // the moments' runs (this lane's four groups and its partner half-wave's)
+  const int co = co0 + (lane & 31);
+  Moments rm[4], pm[4];
+  if constexpr (Wt::PIX_ON_X && O != Op::I8) {
+    if (mom) {
+      // runs of four pixels (a lane's group gq) -> segments of 64 pixels
+      // (pixel tiles 2s and 2s + 1): lane j of the even tile merges the 16
+      // runs in pixel order, the odd tile's through LDS
+      static_assert(Wt::NPT % 2 == 0, "pixel tiles pair into 64-pixel segments");
+      static_assert(Wt::kWaves * 4 * 64 + Wt::NPT / 2 * 32 * 8 / 2 <= Wt::STAGES * Wt::kStage, "LDS");
+      using OutT = typename std::conditional<O == Op::F32, float,
+                   typename std::conditional<O == Op::F16, _Float16, __bf16>::type>::type;
+      // (mean, M2) of the odd tiles' runs, [segment][channel][8]; every run
+      // holds four values, so the counts stay compile-time constants and the
+      // merges' count ratios fold
+      float2* runs = reinterpret_cast<float2*>(smem + Wt::kWaves * 4 * 64);
+      if (wave < Wt::NPT) {
+        const float b = mbias && co < C ? (float)static_cast<const OutT*>(mbias)[co] : -0.0f;
+#pragma unroll
+        for (int gq = 0; gq < 4; ++gq) {
+          const f32x4 v = tile_sum(gq);
+          float h[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) h[e] = (float)(OutT)(v[e] + b);
+          rm[gq] = run_moments4(h[0], h[1], h[2], h[3]);
+        }
+#pragma unroll
+        for (int gq = 0; gq < 4; ++gq) {
+          pm[gq].n = 4.0f;
+          pm[gq].m = __shfl_xor(rm[gq].m, 32);
+          pm[gq].m2 = __shfl_xor(rm[gq].m2, 32);
+        }
+        if ((pt & 1) && hi == 0) {
+          float2* dst = runs + ((pt >> 1) * 32 + (lane & 31)) * 8;
+#pragma unroll
+          for (int gq = 0; gq < 4; ++gq) {
+            dst[2 * gq] = float2{rm[gq].m, rm[gq].m2};
+            dst[2 * gq + 1] = float2{pm[gq].m, pm[gq].m2};
+          }
+        }
+      }
+      __syncthreads();
+    }
+  }
   if (wave >= Wt::NPT) return;
   // wave pt adds the partial tiles of k-steps 0 .. KSN - 1 in that order and
   // finishes its 32 pixels x 32 channels
@@ -401,9 +459,7 @@ __global__ void __launch_bounds__(Wt::kThreads) wk_conv_kernel(const HaloGeo g, 
   epi.load_j(pj, jl);
 #pragma unroll
   for (int gq = 0; gq < 4; ++gq) {
-    f32x4 v = red[(pt * 4 + gq) * 64 + lane];
-#pragma unroll
-    for (int k2 = 1; k2 < Wt::KSN; ++k2) v += red[((pt + k2 * Wt::NPT) * 4 + gq) * 64 + lane];
+    const f32x4 v = tile_sum(gq);
     const int i = (Wt::PIX_ON_X ? pixl : co0) + 8 * gq + 4 * hi;
     typename Epi::PreI pi;
     epi.load_i(pi, i);
@@ -413,6 +469,28 @@ __global__ void __launch_bounds__(Wt::kThreads) wk_conv_kernel(const HaloGeo g, 
     uint32_t bits[4];
     epi.finish(pi, pj, i, jl, a4, bits);
     store_group(out, epi.out_bytes(), out.row(i), i, jl, bits);
+  }
+  // the even tile's lanes merge its segment's runs in pixel order (after
+  // the stores are issued: the merges overlap their write-back)
+  if constexpr (Wt::PIX_ON_X && O != Op::I8) {
+    if (mom) {
+      const float2* runs = reinterpret_cast<const float2*>(smem + Wt::kWaves * 4 * 64);
+      if (!(pt & 1) && hi == 0 && co < C) {
+        Moments acc = rm[0];
+        chan_merge(acc, pm[0]);
+#pragma unroll
+        for (int gq = 1; gq < 4; ++gq) {
+          chan_merge(acc, rm[gq]);
+          chan_merge(acc, pm[gq]);
+        }
+        const float2* src = runs + ((pt >> 1) * 32 + (lane & 31)) * 8;
+#pragma unroll
+        for (int r = 0; r < 8; ++r) chan_merge(acc, Moments{4.0f, src[r].x, src[r].y});
+        const int seg = (pix0 - n * ohw + pt * 32) / kNormSeg;
+        *reinterpret_cast<float2*>(mom + (((int64_t)n * C + co) * (ohw / kNormSeg) + seg) * 2) =
+            float2{acc.m, acc.m2};
+      }
+    }
   }
 }
 

@@ -222,8 +222,9 @@ struct HaloGeo {
 };
 hipError_t run_halo_float(int dtype, const HaloGeo& g, bool pix_on_x, const FloatOut& o, hipStream_t st);
 // the whole-K variant (wk_conv_kernel): every block runs the whole
-// reduction, no split-K partial sums (HaloGeo.th unused)
-hipError_t run_wk_float(int dtype, const HaloGeo& g, bool pix_on_x, const FloatOut& o, hipStream_t st);
+// reduction, no split-K partial sums (HaloGeo.th unused); mom: also the
+// outputs' 64-pixel segment moments (pix_on_x, no activation)
+hipError_t run_wk_float(int dtype, const HaloGeo& g, bool pix_on_x, const FloatOut& o, float* mom, hipStream_t st);
 // pixel-tile extent and largest staged patch of the halo path
 constexpr int kHaloBPix = 256;
 constexpr int kHaloPixMax = 400;       // patch pixels of a 16-, 32- or 64-wide output row tile
@@ -390,6 +391,11 @@ hipError_t run_instnorm(int dt, const void* x, void* y, int64_t planes, int64_t 
 // the split reduction stores it, then normalised as run_instnorm does.  The
 // output is NCHW, or NHWC with C elements per pixel (out_nhwc).
 constexpr int64_t kNormPartialsMaxSpatial = 16384;
+// f16 instance normalisation from the conv output x (NCHW) and its
+// 64-pixel segment moments (wk_conv_kernel's mom); the residual, if any, in
+// the output's layout
+hipError_t run_instnorm_mom(const void* x, const float* mom, void* y, int64_t N, int C, int64_t spatial, float eps,
+                            const NormAffine& aff, bool out_nhwc, hipStream_t st);
 hipError_t run_instnorm_partials(int dt, const float* ws, int splits, int64_t Pp, const void* conv_bias, void* y,
                                  int64_t N, int64_t spatial, int C, float eps, const NormAffine& aff, bool out_nhwc,
                                  hipStream_t st);

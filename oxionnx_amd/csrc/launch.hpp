@@ -487,9 +487,11 @@ inline hipError_t launch_halo(const HaloGeo& g, const Epi& epi, int P, int Q, in
 // eight).
 // A deferred epilogue (the fused conv -> norm node) leaves the raw f32 sums
 // in `ws` instead, as one split-K slice, for the norm kernel that reads
-// partial sums.
+// partial sums.  mom (with the conv's bias and channel count): the
+// kernel also writes each 64-pixel segment's moments (wk_conv_kernel).
 template <Op O, bool PIXX, class Epi>
-inline hipError_t launch_wk(const HaloGeo& g, const Epi& epi, int P, int Q, void* ws, hipStream_t st) {
+inline hipError_t launch_wk(const HaloGeo& g, const Epi& epi, int P, int Q, void* ws, float* mom, const void* mbias,
+                            hipStream_t st) {
   auto go = [&](auto wt, const auto& e) -> hipError_t {
     using Wt = decltype(wt);
     using E = std::decay_t<decltype(e)>;
@@ -497,8 +499,9 @@ inline hipError_t launch_wk(const HaloGeo& g, const Epi& epi, int P, int Q, void
     const int nP = pix / (Wt::NPT * 32), nQ = (co + 31) / 32;
     if (nP <= 0 || nQ <= 0) return hipSuccess;
     if (pix % (Wt::NPT * 32) != 0 || (int64_t)nP * nQ > 0x7fffffff) return hipErrorInvalidValue;
+    if (mom && (!PIXX || (g.OH * g.OW) % kNormSeg != 0)) return hipErrorInvalidValue;
     hipLaunchKernelGGL((wk_conv_kernel<O, Wt, E>), dim3((unsigned)(nP * nQ)), dim3(Wt::kThreads), 0, st, g, e, nP,
-                       nQ);
+                       nQ, mom, mbias, co);
     return hipGetLastError();
   };
   auto pick = [&](const auto& e) -> hipError_t {
@@ -508,7 +511,7 @@ inline hipError_t launch_wk(const HaloGeo& g, const Epi& epi, int P, int Q, void
     return hipErrorInvalidValue;
   };
   if (!epi.out.defer) return pick(epi);
-  if (!ws || !PIXX || O == Op::I8) return hipErrorInvalidValue;
+  if (!ws || !PIXX || O == Op::I8 || mom) return hipErrorInvalidValue;
   return pick(PartialEpi<float>{reinterpret_cast<float*>(ws), P, (P + 3) / 4 * 4, Q});
 }
 

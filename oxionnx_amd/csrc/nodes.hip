@@ -11,6 +11,7 @@
 #include <stdint.h>
 
 #include "internal.hpp"
+#include "norm_stats.hpp"
 
 namespace ohip {
 
@@ -84,39 +85,47 @@ __global__ void __launch_bounds__(kThreads) binary_same_kernel(const T* __restri
 }
 
 // ---------------------------------------------------------------- instance normalisation
-// One block per (n, c) plane: mean, then variance about the mean (two
-// passes, as the reference's normalize_plane), then the rescale with the
-// optional per-channel (or per-(n, c)) affine term and activation.
-__device__ __forceinline__ float block_sum(float v, float* red) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  __syncthreads();
-  if (lane == 0) red[wave] = v;
-  __syncthreads();
-  float s = 0.0f;
-#pragma unroll
-  for (int w = 0; w < kThreads / 64; ++w) s += red[w];
-  return s;
-}
+// One block per (n, c) plane: the plane is staged in LDS as f32 (planes of
+// up to kNormPlaneLds values; larger ones are read from global memory), its
+// statistics follow norm_stats.hpp (each thread a segment's moments, thread
+// 0 merging them in order, 256 segments at a time), then every thread
+// rescales its share with the optional per-channel (or per-(n, c)) affine
+// term and activation.
+constexpr int64_t kNormPlaneLds = 15360;
 
 template <class T>
 __global__ void __launch_bounds__(kThreads) instnorm_kernel(const T* __restrict__ x, T* __restrict__ y, int64_t spatial,
                                                             int C, float eps, NormAffine aff) {
-  __shared__ float red[kThreads / 64];
+  extern __shared__ float xs[];
+  __shared__ Moments segm[kThreads];
+  __shared__ float st[2];
   const int64_t plane = blockIdx.x;
   const T* xp = x + plane * spatial;
   T* yp = y + plane * spatial;
-  float s = 0.0f;
-  for (int64_t i = threadIdx.x; i < spatial; i += kThreads) s += ldf(xp, i);
-  const float mean = block_sum(s, red) / (float)spatial;
-  float q = 0.0f;
-  for (int64_t i = threadIdx.x; i < spatial; i += kThreads) {
-    const float d = ldf(xp, i) - mean;
-    q += d * d;
+  const bool staged = spatial <= kNormPlaneLds;
+  if (staged) {
+    for (int64_t i = threadIdx.x; i < spatial; i += kThreads) xs[i] = ldf(xp, i);
+    __syncthreads();
   }
-  const float var = block_sum(q, red) / (float)spatial;
-  const float inv = 1.0f / sqrtf(var + eps);
+  auto ld = [&](int64_t i) { return staged ? xs[i] : ldf(xp, i); };
+  const int S = norm_segments(spatial);
+  Moments acc{0.0f, 0.0f, 0.0f};
+  for (int s0 = 0; s0 < S; s0 += kThreads) {
+    if (s0 + (int)threadIdx.x < S) segm[threadIdx.x] = segment_moments(ld, spatial, s0 + threadIdx.x);
+    __syncthreads();
+    if (threadIdx.x == 0)
+      for (int s = s0; s < S && s < s0 + kThreads; ++s) {
+        if (s == 0) acc = segm[0];
+        else chan_merge(acc, segm[s - s0]);
+      }
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) {
+    st[0] = acc.m;
+    st[1] = 1.0f / sqrtf(acc.m2 / (float)spatial + eps);
+  }
+  __syncthreads();
+  const float mean = st[0], inv = st[1];
   const int c = (int)(plane % C);
   const int64_t n = plane / C;
   float sc = 1.0f, bi = 0.0f;
@@ -134,7 +143,7 @@ __global__ void __launch_bounds__(kThreads) instnorm_kernel(const T* __restrict_
   // normalised value, the product and the sum are each rounded to T, as the
   // OxiInstanceNorm -> Mul -> Add nodes store them.
   for (int64_t i = threadIdx.x; i < spatial; i += kThreads) {
-    float v = (ldf(xp, i) - mean) * inv;
+    float v = (ld(i) - mean) * inv;
     if (affine) {
       v = (float)(T)v;
       if (aff.scale) v = (float)(T)(v * sc);
@@ -152,12 +161,11 @@ __global__ void __launch_bounds__(kThreads) instnorm_kernel(const T* __restrict_
 
 // The same normalisation over a plane rebuilt from split-K partial sums in
 // LDS: x_i = T(sum over slices in slice order + bias), the value the split
-// reduction would have stored; the three passes then read LDS instead of
-// global memory, in the same order, so the result is the unfused pair's.
-// PPB planes (channels of one image) per block, 256 threads each with its
-// own reduction slots, so every plane's statistics are the 256-thread
-// block's above; with PPB > 1 (an NHWC output) each pixel's PPB channels
-// are written (and a residual read) as one run.
+// reduction would have stored; the statistics (norm_stats.hpp) and the
+// rescale then read LDS instead of global memory, so the result is the
+// unfused pair's.  PPB planes (channels of one image) per block, 256 threads
+// each; with PPB > 1 (an NHWC output) each pixel's PPB channels are written
+// (and a residual read) as one run.
 #ifdef OHIP_KTIMING
 // Diagnostic build only (never in the shipped library): per-block stamps of
 // the 100 MHz real-time counter at the norm kernel's phase boundaries.
@@ -171,21 +179,6 @@ extern "C" int ohip_ktime_read_nodes(void* host) {
 #define NSTAMP(i) do {} while (0)
 #endif
 
-template <int PPB>
-__device__ __forceinline__ float group_sum(float v, float* red, int g) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
-  const int lane = threadIdx.x & 63, wave = (threadIdx.x >> 6) & 3;
-  // (red is written once per call site: each sum has its own slots, so no
-  // barrier is needed before the write)
-  if (lane == 0) red[4 * g + wave] = v;
-  __syncthreads();
-  float s = 0.0f;
-#pragma unroll
-  for (int w = 0; w < 4; ++w) s += red[4 * g + w];
-  return s;
-}
-
 template <class T, int PPB>
 __global__ void __launch_bounds__(kThreads * PPB) instnorm_partials_kernel(const float* __restrict__ ws, int splits,
                                                                            int64_t slice, int64_t Pp,
@@ -195,7 +188,8 @@ __global__ void __launch_bounds__(kThreads * PPB) instnorm_partials_kernel(const
 #pragma clang fp contract(off)
   static_assert(kThreads == 256, "256 threads a plane");
   extern __shared__ float xs_all[];        // PPB planes of `spatial` values
-  __shared__ float red[2][4 * PPB];   // the mean's and the variance's wave sums
+  __shared__ float red[2][4 * PPB];   // each plane's mean and 1 / sqrt(var + eps) (slot 4 g)
+  __shared__ Moments segm[PPB][kThreads];   // each plane's segment moments
   NSTAMP(0);
   const int g = threadIdx.x >> 8, lt = threadIdx.x & 255;
   const int groups = C / PPB;
@@ -260,17 +254,20 @@ __global__ void __launch_bounds__(kThreads * PPB) instnorm_partials_kernel(const
   }
   __syncthreads();
   NSTAMP(1);
-  float s = 0.0f;
-  for (int i = lt; i < spatial; i += kThreads) s += xs[i];
-  const float mean = group_sum<PPB>(s, red[0], g) / (float)spatial;
-  NSTAMP(2);
-  float q = 0.0f;
-  for (int i = lt; i < spatial; i += kThreads) {
-    const float d = xs[i] - mean;
-    q += d * d;
+  // the plane's statistics (norm_stats.hpp): each thread a segment's
+  // moments, thread 0 of the plane merging them in order
+  const int S = norm_segments(spatial);   // <= 256 (kNormPartialsMaxSpatial)
+  if (lt < S) segm[g][lt] = segment_moments([&](int64_t i) { return xs[i]; }, spatial, lt);
+  __syncthreads();
+  if (lt == 0) {
+    Moments acc = segm[g][0];
+    for (int sg = 1; sg < S; ++sg) chan_merge(acc, segm[g][sg]);
+    red[0][4 * g] = acc.m;
+    red[1][4 * g] = 1.0f / sqrtf(acc.m2 / (float)spatial + eps);
   }
-  const float var = group_sum<PPB>(q, red[1], g) / (float)spatial;
-  const float inv = 1.0f / sqrtf(var + eps);
+  __syncthreads();
+  const float mean = red[0][4 * g], inv = red[1][4 * g];
+  NSTAMP(2);
   NSTAMP(3);
   const bool affine = aff.scale || aff.bias;
   T* yp = y + plane * spatial;
@@ -747,14 +744,132 @@ hipError_t run_instnorm(int dt, const void* x, void* y, int64_t planes, int64_t 
                         const NormAffine& aff, hipStream_t st) {
   if (planes <= 0 || spatial <= 0) return hipSuccess;
   if (planes > 0x7fffffff) return hipErrorInvalidValue;
+  const size_t shm = spatial <= kNormPlaneLds ? (size_t)spatial * sizeof(float) : 0;
   if (dt == DT_F32)
-    hipLaunchKernelGGL(instnorm_kernel<float>, dim3((unsigned)planes), dim3(kThreads), 0, st, (const float*)x,
+    hipLaunchKernelGGL(instnorm_kernel<float>, dim3((unsigned)planes), dim3(kThreads), shm, st, (const float*)x,
                        (float*)y, spatial, C, eps, aff);
   else if (dt == DT_F16)
-    hipLaunchKernelGGL(instnorm_kernel<_Float16>, dim3((unsigned)planes), dim3(kThreads), 0, st, (const _Float16*)x,
-                       (_Float16*)y, spatial, C, eps, aff);
+    hipLaunchKernelGGL(instnorm_kernel<_Float16>, dim3((unsigned)planes), dim3(kThreads), shm, st,
+                       (const _Float16*)x, (_Float16*)y, spatial, C, eps, aff);
   else
     return hipErrorInvalidValue;
+  return hipGetLastError();
+}
+
+// Instance normalisation of f16 conv outputs whose statistics arrive as the
+// moments of their 64-pixel segments (wk_conv_kernel with mom): a block
+// takes 32 channels x 64 pixels of one image, merges each channel's
+// segments in order (the plain kernel's statistics, norm_stats.hpp), and
+// normalises its tile with the affine tail, activation and residual of the
+// unfused chain, reading the conv output as NCHW rows and writing 16-byte
+// runs (eight channels of a pixel for an NHWC output, eight pixels of a
+// channel for NCHW).
+__global__ void __launch_bounds__(256) instnorm_mom_kernel(const _Float16* __restrict__ x,
+                                                           const float* __restrict__ mom, _Float16* __restrict__ y,
+                                                           int C, int spatial, float eps, NormAffine aff,
+                                                           int out_nhwc) {
+#pragma clang fp contract(off)
+  typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+  constexpr int kChunk = 32;   // segments of a channel staged per pass
+  __shared__ float st[2][32];
+  __shared__ h8 tile[32][9];   // [channel][eight-pixel chunk] (one chunk of padding)
+  __shared__ float2 segs[32][kChunk + 1];
+  __shared__ float afs[2][32];   // each channel's scale and bias
+  const int S = spatial / kNormSeg;
+  const int nct = (C + 31) / 32;
+  const int pb = (int)(blockIdx.x % S), rest = (int)(blockIdx.x / S);
+  const int c0 = (rest % nct) * 32, n = rest / nct, p0 = pb * kNormSeg;
+  const int t = threadIdx.x;
+  const int cw = C - c0 < 32 ? C - c0 : 32;
+  // every global load of the block in flight before the first wait: this
+  // thread's eight pixels (or, NHWC, eight channels) of the conv output and
+  // of the residual, and its share of the first chunk of segment moments
+  const _Float16* res = static_cast<const _Float16*>(aff.residual);
+  h8 xv{}, r{};
+  int64_t o;
+  bool live;
+  if (out_nhwc) {
+    const int p = t >> 2, q = t & 3;
+    live = 8 * q < cw;
+    o = ((int64_t)n * spatial + p0 + p) * C + c0 + 8 * q;
+  } else {
+    const int cl = t >> 3, k = t & 7;
+    live = cl < cw;
+    o = ((int64_t)n * C + c0 + cl) * spatial + p0 + 8 * k;
+  }
+  {
+    const int cl = t >> 3, k = t & 7;
+    if (cl < cw) xv = *reinterpret_cast<const h8*>(x + ((int64_t)n * C + c0 + cl) * spatial + p0 + 8 * k);
+  }
+  if (res && live) r = *reinterpret_cast<const h8*>(res + o);
+  if (t < cw) {
+    const int64_t ai = aff.per_sample ? (int64_t)n * aff.stride + c0 + t : c0 + t;
+    auto term = [&](const void* p) {
+      return aff.same_type ? (float)static_cast<const _Float16*>(p)[ai] : static_cast<const float*>(p)[ai];
+    };
+    afs[0][t] = aff.scale ? term(aff.scale) : 1.0f;
+    afs[1][t] = aff.bias ? term(aff.bias) : 0.0f;
+  }
+  const float2* mp = reinterpret_cast<const float2*>(mom) + ((int64_t)n * C + c0) * S;
+  Moments acc{0.0f, 0.0f, 0.0f};
+  for (int s0 = 0; s0 < S; s0 += kChunk) {
+    const int len = S - s0 < kChunk ? S - s0 : kChunk;
+    for (int i = t; i < 32 * len; i += 256) {
+      const int cl = i / len, sg = i - cl * len;
+      if (cl < cw) segs[cl][sg] = mp[(int64_t)cl * S + s0 + sg];
+    }
+    if (s0 == 0) tile[t >> 3][t & 7] = xv;
+    __syncthreads();
+    if (t < cw)
+      for (int sg = 0; sg < len; ++sg) {
+        const Moments m{(float)kNormSeg, segs[t][sg].x, segs[t][sg].y};
+        if (s0 + sg == 0) acc = m;
+        else chan_merge(acc, m);
+      }
+    __syncthreads();
+  }
+  if (t < cw) {
+    st[0][t] = acc.m;
+    st[1][t] = 1.0f / sqrtf(acc.m2 / (float)spatial + eps);
+  }
+  __syncthreads();
+  if (!live) return;
+  const bool affine = aff.scale || aff.bias;
+  auto finish = [&](float v0, int cl, float r1) {
+    const float sc = afs[0][cl], bi = afs[1][cl];
+    float v = (v0 - st[0][cl]) * st[1][cl];
+    if (affine) {
+      v = (float)(_Float16)v;
+      if (aff.scale) v = (float)(_Float16)(v * sc);
+      if (aff.bias) v = (float)(_Float16)(v + bi);
+    }
+    if (aff.act == UN_RELU) v = v > 0.0f ? v : 0.0f;
+    else if (aff.act == UN_LEAKY_RELU) v = (float)(_Float16)v, v = v >= 0.0f ? v : v * aff.alpha;
+    if (res) v = (float)(_Float16)v + r1;
+    return (_Float16)v;
+  };
+  h8 out;
+  if (out_nhwc) {
+    const int p = t >> 2, q = t & 3;
+#pragma unroll
+    for (int c = 0; c < 8; ++c) out[c] = finish((float)tile[8 * q + c][p >> 3][p & 7], 8 * q + c, (float)r[c]);
+  } else {
+    const int cl = t >> 3;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) out[e] = finish((float)xv[e], cl, (float)r[e]);
+  }
+  *reinterpret_cast<h8*>(y + o) = out;
+}
+
+hipError_t run_instnorm_mom(const void* x, const float* mom, void* y, int64_t N, int C, int64_t spatial, float eps,
+                            const NormAffine& aff, bool out_nhwc, hipStream_t st) {
+  if (N <= 0 || spatial <= 0) return hipSuccess;
+  if (spatial % kNormSeg != 0 || (out_nhwc && C % 8 != 0) || (aff.residual && aff.res_nhwc != (int)out_nhwc))
+    return hipErrorInvalidValue;
+  const int64_t blocks = N * ((C + 31) / 32) * (spatial / kNormSeg);
+  if (blocks > 0x7fffffff) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(instnorm_mom_kernel, dim3((unsigned)blocks), dim3(256), 0, st, (const _Float16*)x, mom,
+                     (_Float16*)y, C, (int)spatial, eps, aff, (int)out_nhwc);
   return hipGetLastError();
 }
 

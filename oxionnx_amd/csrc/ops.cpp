@@ -1513,9 +1513,17 @@ static int conv2d_impl(ohip_ctx* ctx, const ohip_conv_desc* d, const void* x, co
   }
   // the whole-K kernel under a norm leaves its sums as one slice of f32
   // partial sums for the norm kernel
-  const bool partials = splits > 1 || (wk && norm);
+  // An f16 norm over planes of whole 64-pixel segments takes its statistics
+  // from the whole-K kernel instead: the kernel stores the f16 conv output
+  // (NCHW) and each 64-pixel segment's moments, and the norm kernel merges
+  // those and rescales the stored output in one elementwise pass.
+  const bool wk_mom = wk && norm && d->dtype == OHIP_F16 && ohw % 64 == 0 && (!norm_nhwc || d->cout % 8 == 0) &&
+                      (!norm->aff.residual || norm->aff.res_nhwc == (int)norm_nhwc);
+  const bool partials = splits > 1 || (wk && norm && !wk_mom);
   size_t iw = partials ? plan.add(splits > 1 ? split_ws_bytes(sP, sQ, splits) : (size_t)sQ * ((sP + 3) / 4 * 4) * 4)
                        : SIZE_MAX;
+  const size_t ity = wk_mom ? plan.add((size_t)(d->n * d->cout * ohw) * eb) : SIZE_MAX;
+  const size_t imom = wk_mom ? plan.add((size_t)(d->n * d->cout * (ohw / 64)) * 2 * 4) : SIZE_MAX;
   char* sbase = nullptr;
   rc = call_scratch(ctx, plan.total(), noalloc, &sbase);
   if (rc) return rc;
@@ -1556,7 +1564,7 @@ static int conv2d_impl(ohip_ctx* ctx, const ohip_conv_desc* d, const void* x, co
     o.alpha = 1.0f; o.beta = 1.0f;
     o.bias = bias;
     o.act = act; o.lo = lo; o.hi = hi;
-    o.y = y;
+    o.y = wk_mom ? plan_at(sbase, plan, ity) : y;
     if (nchw_out) {
       o.si = 1; o.sj = ohw; o.bstride = d->cout * ohw; o.ohw = (int)ohw; o.P = (int)rows; o.Q = (int)coutg;
       o.vec = ohw % 4 == 0 && aligned(o.y, 4 * eb);
@@ -1568,12 +1576,16 @@ static int conv2d_impl(ohip_ctx* ctx, const ohip_conv_desc* d, const void* x, co
     }
     o.splits = splits;
     o.split_ws = partials ? plan_at(sbase, plan, iw) : nullptr;
-    o.defer_reduce = norm ? 1 : 0;
+    o.defer_reduce = norm && !wk_mom ? 1 : 0;
+    float* mom = wk_mom ? static_cast<float*>(plan_at(sbase, plan, imom)) : nullptr;
     ctx->counters.contraction_launches++;
-    hipError_t e = wk ? run_wk_float(d->dtype, hg, nchw_out, o, ctx->stream)
+    hipError_t e = wk ? run_wk_float(d->dtype, hg, nchw_out, o, mom, ctx->stream)
                       : run_halo_float(d->dtype, hg, nchw_out, o, ctx->stream);
     if (e != hipSuccess) return hip_fail(e, wk ? "ohip_conv2d whole-K halo launch" : "ohip_conv2d halo launch");
-    if (norm) {
+    if (wk_mom) {
+      e = run_instnorm_mom(o.y, mom, y, d->n, (int)d->cout, ohw, norm->eps, norm->aff, norm_nhwc, ctx->stream);
+      if (e != hipSuccess) return hip_fail(e, "ohip_conv2d_instnorm launch");
+    } else if (norm) {
       e = run_instnorm_partials(d->dtype, static_cast<const float*>(o.split_ws), splits, (rows + 3) / 4 * 4, bias,
                                 y, d->n, ohw, (int)d->cout, norm->eps, norm->aff, norm_nhwc, ctx->stream);
       if (e != hipSuccess) return hip_fail(e, "ohip_conv2d_instnorm launch");

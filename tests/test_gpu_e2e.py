@@ -602,6 +602,35 @@ def test_conv_instnorm_fusion_matches_unfused(ctx, case):
     close(got, ref, 1e-2 if dt == "f16" else 1e-4)
 
 
+# the whole-K conv forced (tile 17) where the automatic plan splits K: f16
+# planes of 16-, 32- and 64-pixel rows, so the norm reads the conv's stored
+# output and the moments of its 64-pixel segments
+WK_MOM_CASES = [
+    (2, 64, 16, "f16", True, True, "skip"),
+    (1, 128, 32, "f16", False, True, None),
+    (1, 64, 64, "f16", True, False, "skip"),
+]
+
+
+@pytest.mark.parametrize("case", WK_MOM_CASES, ids=str)
+def test_conv_instnorm_moments_path_matches_unfused(ctx, case):
+    """The fused node on the whole-K kernel's segment moments equals the
+    unfused chain (the same whole-K conv, then the norm node's own
+    statistics) bit for bit."""
+    n, c, hw, dt, adain, relu, residual = case
+    g, feeds = _conv_adain_graph(n, c, hw, dt, adain, relu, residual=residual)
+    ctx.set_tile(17)
+    try:
+        fused = Session(g, ctx)
+        assert [nd.op for nd in fused.graph.nodes].count("OhipConvInstanceNorm") == 1
+        got = fused.run(feeds)["y"]
+        want = Session(g, ctx, optimize="reference").run(feeds)["y"]
+    finally:
+        ctx.set_tile(0)
+    np.testing.assert_array_equal(got, want)
+    close(got, G.run_graph(g, feeds, half=True)["y"], 1e-2)
+
+
 def _bcast_residual_then_conv(dt):
     """Conv -> OxiInstanceNorm -> Add([1, C, 1, 1] initializer) -> zero-padded
     Conv: the fused node's residual broadcasts, and its consumer is a conv
