@@ -87,17 +87,17 @@ __global__ void __launch_bounds__(kThreads) binary_same_kernel(const T* __restri
 // ---------------------------------------------------------------- instance normalisation
 // One block per (n, c) plane: the plane is staged in LDS as f32 (planes of
 // up to kNormPlaneLds values; larger ones are read from global memory), its
-// statistics follow norm_stats.hpp (each thread a segment's moments, thread
-// 0 merging them in order, 256 segments at a time), then every thread
-// rescales its share with the optional per-channel (or per-(n, c)) affine
-// term and activation.
+// statistics follow norm_stats.hpp (each thread a segment's moments, the
+// block merging a group of 256 as a tree, thread 0 the groups), then every
+// thread rescales its share with the optional per-channel (or per-(n, c))
+// affine term and activation.
 constexpr int64_t kNormPlaneLds = 15360;
 
 template <class T>
 __global__ void __launch_bounds__(kThreads) instnorm_kernel(const T* __restrict__ x, T* __restrict__ y, int64_t spatial,
                                                             int C, float eps, NormAffine aff) {
   extern __shared__ float xs[];
-  __shared__ Moments segm[kThreads];
+  __shared__ float2 segm[2][kNormGroup];
   __shared__ float st[2];
   const int64_t plane = blockIdx.x;
   const T* xp = x + plane * spatial;
@@ -108,16 +108,24 @@ __global__ void __launch_bounds__(kThreads) instnorm_kernel(const T* __restrict_
     __syncthreads();
   }
   auto ld = [&](int64_t i) { return staged ? xs[i] : ldf(xp, i); };
+  static_assert(kThreads == kNormGroup, "a thread per segment of a group");
   const int S = norm_segments(spatial);
   Moments acc{0.0f, 0.0f, 0.0f};
-  for (int s0 = 0; s0 < S; s0 += kThreads) {
-    if (s0 + (int)threadIdx.x < S) segm[threadIdx.x] = segment_moments(ld, spatial, s0 + threadIdx.x);
+  for (int s0 = 0; s0 < S; s0 += kNormGroup) {
+    const int cnt = S - s0 < kNormGroup ? S - s0 : kNormGroup;
+    if ((int)threadIdx.x < cnt) {
+      const Moments m = segment_moments(ld, spatial, s0 + threadIdx.x);
+      segm[0][threadIdx.x] = float2{m.m, m.m2};
+    }
     __syncthreads();
-    if (threadIdx.x == 0)
-      for (int s = s0; s < S && s < s0 + kThreads; ++s) {
-        if (s == 0) acc = segm[0];
-        else chan_merge(acc, segm[s - s0]);
-      }
+    const int64_t gend = (int64_t)(s0 + cnt) * kNormSeg < spatial ? (int64_t)(s0 + cnt) * kNormSeg : spatial;
+    const int n_last = (int)(gend - (int64_t)(s0 + cnt - 1) * kNormSeg);
+    const float2 r = tree_merge(segm[0], segm[1], 0, 1, cnt, n_last, threadIdx.x, kThreads)[0];
+    if (threadIdx.x == 0) {
+      const Moments gm{(float)(gend - (int64_t)s0 * kNormSeg), r.x, r.y};
+      if (s0 == 0) acc = gm;
+      else chan_merge(acc, gm);
+    }
     __syncthreads();
   }
   if (threadIdx.x == 0) {
@@ -189,7 +197,7 @@ __global__ void __launch_bounds__(kThreads * PPB) instnorm_partials_kernel(const
   static_assert(kThreads == 256, "256 threads a plane");
   extern __shared__ float xs_all[];        // PPB planes of `spatial` values
   __shared__ float red[2][4 * PPB];   // each plane's mean and 1 / sqrt(var + eps) (slot 4 g)
-  __shared__ Moments segm[PPB][kThreads];   // each plane's segment moments
+  __shared__ float2 segm[2][PPB][kNormGroup];   // each plane's segment moments and the tree's scratch
   NSTAMP(0);
   const int g = threadIdx.x >> 8, lt = threadIdx.x & 255;
   const int groups = C / PPB;
@@ -256,14 +264,18 @@ __global__ void __launch_bounds__(kThreads * PPB) instnorm_partials_kernel(const
   NSTAMP(1);
   // the plane's statistics (norm_stats.hpp): each thread a segment's
   // moments, thread 0 of the plane merging them in order
-  const int S = norm_segments(spatial);   // <= 256 (kNormPartialsMaxSpatial)
-  if (lt < S) segm[g][lt] = segment_moments([&](int64_t i) { return xs[i]; }, spatial, lt);
+  static_assert(kThreads == kNormGroup, "a thread per segment");
+  const int S = norm_segments(spatial);   // <= 256 (kNormPartialsMaxSpatial): one group
+  if (lt < S) {
+    const Moments m = segment_moments([&](int64_t i) { return xs[i]; }, spatial, lt);
+    segm[0][g][lt] = float2{m.m, m.m2};
+  }
   __syncthreads();
+  const float2* r = tree_merge(&segm[0][0][0], &segm[1][0][0], kNormGroup, PPB, S, spatial - (S - 1) * kNormSeg,
+                               threadIdx.x, kThreads * PPB);
   if (lt == 0) {
-    Moments acc = segm[g][0];
-    for (int sg = 1; sg < S; ++sg) chan_merge(acc, segm[g][sg]);
-    red[0][4 * g] = acc.m;
-    red[1][4 * g] = 1.0f / sqrtf(acc.m2 / (float)spatial + eps);
+    red[0][4 * g] = r[g * kNormGroup].x;
+    red[1][4 * g] = 1.0f / sqrtf(r[g * kNormGroup].y / (float)spatial + eps);
   }
   __syncthreads();
   const float mean = red[0][4 * g], inv = red[1][4 * g];
@@ -759,7 +771,7 @@ hipError_t run_instnorm(int dt, const void* x, void* y, int64_t planes, int64_t 
 // Instance normalisation of f16 conv outputs whose statistics arrive as the
 // moments of their 64-pixel segments (wk_conv_kernel with mom): a block
 // takes 32 channels x 64 pixels of one image, merges each channel's
-// segments in order (the plain kernel's statistics, norm_stats.hpp), and
+// segments as the plain kernel does (norm_stats.hpp's tree), and
 // normalises its tile with the affine tail, activation and residual of the
 // unfused chain, reading the conv output as NCHW rows and writing 16-byte
 // runs (eight channels of a pixel for an NHWC output, eight pixels of a
@@ -770,10 +782,9 @@ __global__ void __launch_bounds__(256) instnorm_mom_kernel(const _Float16* __res
                                                            int out_nhwc) {
 #pragma clang fp contract(off)
   typedef _Float16 h8 __attribute__((ext_vector_type(8)));
-  constexpr int kChunk = 32;   // segments of a channel staged per pass
   __shared__ float st[2][32];
   __shared__ h8 tile[32][9];   // [channel][eight-pixel chunk] (one chunk of padding)
-  __shared__ float2 segs[32][kChunk + 1];
+  extern __shared__ float2 segs[];   // each channel's segment moments, then the tree's scratch: [2][32][S]
   __shared__ float afs[2][32];   // each channel's scale and bias
   const int S = spatial / kNormSeg;
   const int nct = (C + 31) / 32;
@@ -810,27 +821,15 @@ __global__ void __launch_bounds__(256) instnorm_mom_kernel(const _Float16* __res
     afs[0][t] = aff.scale ? term(aff.scale) : 1.0f;
     afs[1][t] = aff.bias ? term(aff.bias) : 0.0f;
   }
+  // the block's channels' segment moments are one contiguous run
   const float2* mp = reinterpret_cast<const float2*>(mom) + ((int64_t)n * C + c0) * S;
-  Moments acc{0.0f, 0.0f, 0.0f};
-  for (int s0 = 0; s0 < S; s0 += kChunk) {
-    const int len = S - s0 < kChunk ? S - s0 : kChunk;
-    for (int i = t; i < 32 * len; i += 256) {
-      const int cl = i / len, sg = i - cl * len;
-      if (cl < cw) segs[cl][sg] = mp[(int64_t)cl * S + s0 + sg];
-    }
-    if (s0 == 0) tile[t >> 3][t & 7] = xv;
-    __syncthreads();
-    if (t < cw)
-      for (int sg = 0; sg < len; ++sg) {
-        const Moments m{(float)kNormSeg, segs[t][sg].x, segs[t][sg].y};
-        if (s0 + sg == 0) acc = m;
-        else chan_merge(acc, m);
-      }
-    __syncthreads();
-  }
+  for (int i = t; i < cw * S; i += 256) segs[i] = mp[i];
+  tile[t >> 3][t & 7] = xv;
+  __syncthreads();
+  const float2* pm = tree_merge(segs, segs + 32 * S, S, cw, S, kNormSeg, t, 256);
   if (t < cw) {
-    st[0][t] = acc.m;
-    st[1][t] = 1.0f / sqrtf(acc.m2 / (float)spatial + eps);
+    st[0][t] = pm[t * S].x;
+    st[1][t] = 1.0f / sqrtf(pm[t * S].y / (float)spatial + eps);
   }
   __syncthreads();
   if (!live) return;
@@ -864,11 +863,13 @@ __global__ void __launch_bounds__(256) instnorm_mom_kernel(const _Float16* __res
 hipError_t run_instnorm_mom(const void* x, const float* mom, void* y, int64_t N, int C, int64_t spatial, float eps,
                             const NormAffine& aff, bool out_nhwc, hipStream_t st) {
   if (N <= 0 || spatial <= 0) return hipSuccess;
-  if (spatial % kNormSeg != 0 || (out_nhwc && C % 8 != 0) || (aff.residual && aff.res_nhwc != (int)out_nhwc))
+  if (spatial % kNormSeg != 0 || spatial > kNormMomMaxSpatial || (out_nhwc && C % 8 != 0) ||
+      (aff.residual && aff.res_nhwc != (int)out_nhwc))
     return hipErrorInvalidValue;
   const int64_t blocks = N * ((C + 31) / 32) * (spatial / kNormSeg);
   if (blocks > 0x7fffffff) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(instnorm_mom_kernel, dim3((unsigned)blocks), dim3(256), 0, st, (const _Float16*)x, mom,
+  const size_t shm = 2 * 32 * (size_t)(spatial / kNormSeg) * sizeof(float2);
+  hipLaunchKernelGGL(instnorm_mom_kernel, dim3((unsigned)blocks), dim3(256), shm, st, (const _Float16*)x, mom,
                      (_Float16*)y, C, (int)spatial, eps, aff, (int)out_nhwc);
   return hipGetLastError();
 }

@@ -1517,7 +1517,8 @@ static int conv2d_impl(ohip_ctx* ctx, const ohip_conv_desc* d, const void* x, co
   // from the whole-K kernel instead: the kernel stores the f16 conv output
   // (NCHW) and each 64-pixel segment's moments, and the norm kernel merges
   // those and rescales the stored output in one elementwise pass.
-  const bool wk_mom = wk && norm && d->dtype == OHIP_F16 && ohw % 64 == 0 && (!norm_nhwc || d->cout % 8 == 0) &&
+  const bool wk_mom = wk && norm && d->dtype == OHIP_F16 && ohw % 64 == 0 && ohw <= kNormMomMaxSpatial &&
+                      (!norm_nhwc || d->cout % 8 == 0) &&
                       (!norm->aff.residual || norm->aff.res_nhwc == (int)norm_nhwc);
   const bool partials = splits > 1 || (wk && norm && !wk_mom);
   size_t iw = partials ? plan.add(splits > 1 ? split_ws_bytes(sP, sQ, splits) : (size_t)sQ * ((sP + 3) / 4 * 4) * 4)

@@ -95,7 +95,10 @@ def test_binary_two_resident_operands(ctx):
     close(out["y"], ref["y"], 1e-6)
 
 
-@pytest.mark.parametrize("shape", [(1, 512, 32, 32), (2, 3, 5, 7), (1, 4, 1, 1), (1, 2, 300), (1, 3, 40, 50), (1, 2, 64, 64)])
+# planes of one segment, of a short last segment (300 values), of 64
+# segments, and of two segment groups read from global memory (150 x 150)
+@pytest.mark.parametrize("shape", [(1, 512, 32, 32), (2, 3, 5, 7), (1, 4, 1, 1), (1, 2, 300), (1, 3, 40, 50),
+                                   (1, 2, 64, 64), (1, 2, 150, 150)])
 def test_oxi_instance_norm(ctx, shape):
     x = (RNG.normal(3, 2, shape)).astype(np.float32)
     node = ep.Node("OxiInstanceNorm", ["x"], ["y"], A(floats={"epsilon": 1e-5}))
@@ -401,14 +404,24 @@ def test_face_swap_generator_f16_end_to_end(ctx):
     bound = 1e-2 * float(np.abs(ref["logits"]).max())
     assert float(np.abs(out["y"].astype(np.float32) - ref["y"]).max()) <= bound
     # accuracy: against the f32 forward of the same weights (f16-rounded), the
-    # device f16 forward is as close as the reference's f16 forward is
+    # device f16 forward is as close as the reference's f16 forward is.  The
+    # mean and RMS errors are the stable measures (the oracle with its
+    # convolutions summed in torch's order lands within 1 % of the
+    # reference's on both); the largest single error is one amplified
+    # rounding flip, and that second correct order alone moves it by 17 %
+    # (logits 0.0317 against 0.0270), so it gets a looser bar.
     g32, _ = workloads.face_swap_generator(dtype="f32")
     g32.initializers.update({k: np.asarray(v, np.float32) for k, v in g.initializers.items()})
     exact = G.run_graph(g32, {k: v.astype(np.float32) for k, v in feeds.items()})
     for k in ("logits", "y"):
-        e_dev = float(np.abs(out[k].astype(np.float32) - exact[k]).max())
-        e_ref = float(np.abs(ref[k] - exact[k]).max())
-        assert e_dev <= 1.25 * e_ref, (k, e_dev, e_ref)
+        e_dev = np.abs(out[k].astype(np.float32) - exact[k])
+        e_ref = np.abs(ref[k] - exact[k])
+        stats = {m: (float(f(e_dev)), float(f(e_ref))) for m, f in
+                 (("mean", np.mean), ("rms", lambda e: np.sqrt(np.mean(e * e))), ("max", np.max))}
+        print(k, "error against the f32 forward (device, reference f16):", stats)
+        assert stats["mean"][0] <= 1.05 * stats["mean"][1], (k, stats)
+        assert stats["rms"][0] <= 1.05 * stats["rms"][1], (k, stats)
+        assert stats["max"][0] <= 1.5 * stats["max"][1], (k, stats)
 
 
 @pytest.mark.parametrize("which", ["yolo", "face_f16"])
