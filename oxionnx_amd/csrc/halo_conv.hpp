@@ -405,46 +405,39 @@ __global__ void __launch_bounds__(Wt::kThreads) wk_conv_kernel(const HaloGeo g, 
     for (int k2 = 1; k2 < Wt::KSN; ++k2) v += red[((pt + k2 * Wt::NPT) * 4 + gq) * 64 + lane];
     return v;
   };
-  // the moments' runs (this lane's four groups and its partner half-wave's)
+  // the moments of this lane's channel over its pixel tile (lanes 0 .. 31)
   const int co = co0 + (lane & 31);
-  Moments rm[4], pm[4];
+  Moments tm{0.0f, 0.0f, 0.0f};
   if constexpr (Wt::PIX_ON_X && O != Op::I8) {
     if (mom) {
-      // runs of four pixels (a lane's group gq) -> segments of 64 pixels
-      // (pixel tiles 2s and 2s + 1): lane j of the even tile merges the 16
-      // runs in pixel order, the odd tile's through LDS
+      // runs of four pixels (group gq of half-wave hi is run 2 gq + hi of
+      // the tile) merge as a tree into the tile's moments; the odd tile of
+      // each pair hands its moments to the even one through LDS
       static_assert(Wt::NPT % 2 == 0, "pixel tiles pair into 64-pixel segments");
-      static_assert(Wt::kWaves * 4 * 64 + Wt::NPT / 2 * 32 * 8 / 2 <= Wt::STAGES * Wt::kStage, "LDS");
+      static_assert(Wt::kWaves * 4 * 64 + Wt::NPT / 2 * 32 / 2 <= Wt::STAGES * Wt::kStage, "LDS");
       using OutT = typename std::conditional<O == Op::F32, float,
                    typename std::conditional<O == Op::F16, _Float16, __bf16>::type>::type;
-      // (mean, M2) of the odd tiles' runs, [segment][channel][8]; every run
-      // holds four values, so the counts stay compile-time constants and the
-      // merges' count ratios fold
-      float2* runs = reinterpret_cast<float2*>(smem + Wt::kWaves * 4 * 64);
+      float2* odd = reinterpret_cast<float2*>(smem + Wt::kWaves * 4 * 64);   // [pair][channel]
       if (wave < Wt::NPT) {
         const float b = mbias && co < C ? (float)static_cast<const OutT*>(mbias)[co] : -0.0f;
+        Moments r[4];
 #pragma unroll
         for (int gq = 0; gq < 4; ++gq) {
           const f32x4 v = tile_sum(gq);
           float h[4];
 #pragma unroll
           for (int e = 0; e < 4; ++e) h[e] = (float)(OutT)(v[e] + b);
-          rm[gq] = run_moments4(h[0], h[1], h[2], h[3]);
+          const Moments own = run_moments4(h[0], h[1], h[2], h[3]);
+          // every run holds four values: the counts are constants and the
+          // merges' count ratios fold
+          r[gq] = own;
+          chan_merge(r[gq], Moments{4.0f, __shfl_xor(own.m, 32), __shfl_xor(own.m2, 32)});
         }
-#pragma unroll
-        for (int gq = 0; gq < 4; ++gq) {
-          pm[gq].n = 4.0f;
-          pm[gq].m = __shfl_xor(rm[gq].m, 32);
-          pm[gq].m2 = __shfl_xor(rm[gq].m2, 32);
-        }
-        if ((pt & 1) && hi == 0) {
-          float2* dst = runs + ((pt >> 1) * 32 + (lane & 31)) * 8;
-#pragma unroll
-          for (int gq = 0; gq < 4; ++gq) {
-            dst[2 * gq] = float2{rm[gq].m, rm[gq].m2};
-            dst[2 * gq + 1] = float2{pm[gq].m, pm[gq].m2};
-          }
-        }
+        chan_merge(r[0], r[1]);
+        chan_merge(r[2], r[3]);
+        chan_merge(r[0], r[2]);
+        tm = r[0];
+        if ((pt & 1) && hi == 0) odd[(pt >> 1) * 32 + (lane & 31)] = float2{tm.m, tm.m2};
       }
       __syncthreads();
     }
@@ -470,25 +463,17 @@ __global__ void __launch_bounds__(Wt::kThreads) wk_conv_kernel(const HaloGeo g, 
     epi.finish(pi, pj, i, jl, a4, bits);
     store_group(out, epi.out_bytes(), out.row(i), i, jl, bits);
   }
-  // the even tile's lanes merge its segment's runs in pixel order (after
-  // the stores are issued: the merges overlap their write-back)
+  // the even tile's lanes complete their segment (after the stores are
+  // issued: the merge overlaps their write-back)
   if constexpr (Wt::PIX_ON_X && O != Op::I8) {
     if (mom) {
-      const float2* runs = reinterpret_cast<const float2*>(smem + Wt::kWaves * 4 * 64);
+      const float2* odd = reinterpret_cast<const float2*>(smem + Wt::kWaves * 4 * 64);
       if (!(pt & 1) && hi == 0 && co < C) {
-        Moments acc = rm[0];
-        chan_merge(acc, pm[0]);
-#pragma unroll
-        for (int gq = 1; gq < 4; ++gq) {
-          chan_merge(acc, rm[gq]);
-          chan_merge(acc, pm[gq]);
-        }
-        const float2* src = runs + ((pt >> 1) * 32 + (lane & 31)) * 8;
-#pragma unroll
-        for (int r = 0; r < 8; ++r) chan_merge(acc, Moments{4.0f, src[r].x, src[r].y});
+        const float2 o = odd[(pt >> 1) * 32 + (lane & 31)];
+        chan_merge(tm, Moments{32.0f, o.x, o.y});
         const int seg = (pix0 - n * ohw + pt * 32) / kNormSeg;
         *reinterpret_cast<float2*>(mom + (((int64_t)n * C + co) * (ohw / kNormSeg) + seg) * 2) =
-            float2{acc.m, acc.m2};
+            float2{tm.m, tm.m2};
       }
     }
   }

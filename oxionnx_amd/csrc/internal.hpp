@@ -391,7 +391,7 @@ hipError_t run_instnorm(int dt, const void* x, void* y, int64_t planes, int64_t 
 // the split reduction stores it, then normalised as run_instnorm does.  The
 // output is NCHW, or NHWC with C elements per pixel (out_nhwc).
 constexpr int64_t kNormPartialsMaxSpatial = 16384;
-// the moments-fed norm's largest plane (64 segments a channel in LDS)
+// the moments-fed norm's largest plane (64 segments a channel, merged in registers)
 constexpr int64_t kNormMomMaxSpatial = 4096;
 // f16 instance normalisation from the conv output x (NCHW) and its
 // 64-pixel segment moments (wk_conv_kernel's mom); the residual, if any, in

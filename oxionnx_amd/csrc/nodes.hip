@@ -87,17 +87,17 @@ __global__ void __launch_bounds__(kThreads) binary_same_kernel(const T* __restri
 // ---------------------------------------------------------------- instance normalisation
 // One block per (n, c) plane: the plane is staged in LDS as f32 (planes of
 // up to kNormPlaneLds values; larger ones are read from global memory), its
-// statistics follow norm_stats.hpp (each thread a segment's moments, the
-// block merging a group of 256 as a tree, thread 0 the groups), then every
-// thread rescales its share with the optional per-channel (or per-(n, c))
-// affine term and activation.
+// statistics follow norm_stats.hpp (each thread a run's moments, sixteen
+// lanes a segment's, one wave a group's tree, thread 0 the groups), then
+// every thread rescales its share with the optional per-channel (or
+// per-(n, c)) affine term and activation.
 constexpr int64_t kNormPlaneLds = 15360;
 
 template <class T>
 __global__ void __launch_bounds__(kThreads) instnorm_kernel(const T* __restrict__ x, T* __restrict__ y, int64_t spatial,
                                                             int C, float eps, NormAffine aff) {
   extern __shared__ float xs[];
-  __shared__ float2 segm[2][kNormGroup];
+  __shared__ float2 segm[kNormGroup];
   __shared__ float st[2];
   const int64_t plane = blockIdx.x;
   const T* xp = x + plane * spatial;
@@ -108,23 +108,24 @@ __global__ void __launch_bounds__(kThreads) instnorm_kernel(const T* __restrict_
     __syncthreads();
   }
   auto ld = [&](int64_t i) { return staged ? xs[i] : ldf(xp, i); };
-  static_assert(kThreads == kNormGroup, "a thread per segment of a group");
+  static_assert(kThreads == kNormGroup, "a group's threads");
   const int S = norm_segments(spatial);
   Moments acc{0.0f, 0.0f, 0.0f};
   for (int s0 = 0; s0 < S; s0 += kNormGroup) {
     const int cnt = S - s0 < kNormGroup ? S - s0 : kNormGroup;
-    if ((int)threadIdx.x < cnt) {
-      const Moments m = segment_moments(ld, spatial, s0 + threadIdx.x);
-      segm[0][threadIdx.x] = float2{m.m, m.m2};
-    }
+    group_segments(ld, spatial, s0, cnt, segm, threadIdx.x);
     __syncthreads();
     const int64_t gend = (int64_t)(s0 + cnt) * kNormSeg < spatial ? (int64_t)(s0 + cnt) * kNormSeg : spatial;
     const int n_last = (int)(gend - (int64_t)(s0 + cnt - 1) * kNormSeg);
-    const float2 r = tree_merge(segm[0], segm[1], 0, 1, cnt, n_last, threadIdx.x, kThreads)[0];
-    if (threadIdx.x == 0) {
-      const Moments gm{(float)(gend - (int64_t)s0 * kNormSeg), r.x, r.y};
-      if (s0 == 0) acc = gm;
-      else chan_merge(acc, gm);
+    if (threadIdx.x < 64) {
+      float2 v[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) v[j] = 4 * (int)threadIdx.x + j < cnt ? segm[4 * threadIdx.x + j] : float2{0.0f, 0.0f};
+      const Moments gm = wave_tree(v, cnt, n_last, threadIdx.x);
+      if (threadIdx.x == 0) {
+        if (s0 == 0) acc = gm;
+        else chan_merge(acc, gm);
+      }
     }
     __syncthreads();
   }
@@ -197,7 +198,7 @@ __global__ void __launch_bounds__(kThreads * PPB) instnorm_partials_kernel(const
   static_assert(kThreads == 256, "256 threads a plane");
   extern __shared__ float xs_all[];        // PPB planes of `spatial` values
   __shared__ float red[2][4 * PPB];   // each plane's mean and 1 / sqrt(var + eps) (slot 4 g)
-  __shared__ float2 segm[2][PPB][kNormGroup];   // each plane's segment moments and the tree's scratch
+  __shared__ float2 segm[PPB][kNormGroup];   // each plane's segment moments
   NSTAMP(0);
   const int g = threadIdx.x >> 8, lt = threadIdx.x & 255;
   const int groups = C / PPB;
@@ -262,20 +263,21 @@ __global__ void __launch_bounds__(kThreads * PPB) instnorm_partials_kernel(const
   }
   __syncthreads();
   NSTAMP(1);
-  // the plane's statistics (norm_stats.hpp): each thread a segment's
-  // moments, thread 0 of the plane merging them in order
-  static_assert(kThreads == kNormGroup, "a thread per segment");
+  // the plane's statistics (norm_stats.hpp): each thread a run's moments,
+  // sixteen lanes a segment's, the plane's first wave the segments' tree
+  static_assert(kThreads == kNormGroup, "a group's threads");
   const int S = norm_segments(spatial);   // <= 256 (kNormPartialsMaxSpatial): one group
-  if (lt < S) {
-    const Moments m = segment_moments([&](int64_t i) { return xs[i]; }, spatial, lt);
-    segm[0][g][lt] = float2{m.m, m.m2};
-  }
+  group_segments([&](int64_t i) { return xs[i]; }, spatial, 0, S, segm[g], lt);
   __syncthreads();
-  const float2* r = tree_merge(&segm[0][0][0], &segm[1][0][0], kNormGroup, PPB, S, spatial - (S - 1) * kNormSeg,
-                               threadIdx.x, kThreads * PPB);
-  if (lt == 0) {
-    red[0][4 * g] = r[g * kNormGroup].x;
-    red[1][4 * g] = 1.0f / sqrtf(r[g * kNormGroup].y / (float)spatial + eps);
+  if (lt < 64) {   // the plane's first wave merges its segments
+    float2 v[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) v[j] = 4 * lt + j < S ? segm[g][4 * lt + j] : float2{0.0f, 0.0f};
+    const Moments pm = wave_tree(v, S, spatial - (S - 1) * kNormSeg, lt);
+    if (lt == 0) {
+      red[0][4 * g] = pm.m;
+      red[1][4 * g] = 1.0f / sqrtf(pm.m2 / (float)spatial + eps);
+    }
   }
   __syncthreads();
   const float mean = red[0][4 * g], inv = red[1][4 * g];
@@ -784,7 +786,6 @@ __global__ void __launch_bounds__(256) instnorm_mom_kernel(const _Float16* __res
   typedef _Float16 h8 __attribute__((ext_vector_type(8)));
   __shared__ float st[2][32];
   __shared__ h8 tile[32][9];   // [channel][eight-pixel chunk] (one chunk of padding)
-  extern __shared__ float2 segs[];   // each channel's segment moments, then the tree's scratch: [2][32][S]
   __shared__ float afs[2][32];   // each channel's scale and bias
   const int S = spatial / kNormSeg;
   const int nct = (C + 31) / 32;
@@ -821,16 +822,26 @@ __global__ void __launch_bounds__(256) instnorm_mom_kernel(const _Float16* __res
     afs[0][t] = aff.scale ? term(aff.scale) : 1.0f;
     afs[1][t] = aff.bias ? term(aff.bias) : 0.0f;
   }
-  // the block's channels' segment moments are one contiguous run
-  const float2* mp = reinterpret_cast<const float2*>(mom) + ((int64_t)n * C + c0) * S;
-  for (int i = t; i < cw * S; i += 256) segs[i] = mp[i];
-  tile[t >> 3][t & 7] = xv;
-  __syncthreads();
-  const float2* pm = tree_merge(segs, segs + 32 * S, S, cw, S, kNormSeg, t, 256);
+  // each of the first cw threads merges its channel's segments in
+  // registers (a whole plane of whole segments: S <= 64)
   if (t < cw) {
-    st[0][t] = pm[t * S].x;
-    st[1][t] = 1.0f / sqrtf(pm[t * S].y / (float)spatial + eps);
+    const float2* mp = reinterpret_cast<const float2*>(mom) + ((int64_t)n * C + c0 + t) * S;
+    auto plane = [&](auto nc) __attribute__((always_inline)) {
+      constexpr int N = decltype(nc)::value;
+      Moments r[N];
+#pragma unroll
+      for (int k = 0; k < N; ++k) {
+        const float2 v = k < S ? mp[k] : float2{0.0f, 0.0f};
+        r[k] = Moments{(float)kNormSeg, v.x, v.y};
+      }
+      tree_regs<N>(r, S);
+      st[0][t] = r[0].m;
+      st[1][t] = 1.0f / sqrtf(r[0].m2 / (float)spatial + eps);
+    };
+    if (S <= 16) plane(std::integral_constant<int, 16>{});
+    else plane(std::integral_constant<int, 64>{});
   }
+  tile[t >> 3][t & 7] = xv;
   __syncthreads();
   if (!live) return;
   const bool affine = aff.scale || aff.bias;
@@ -868,8 +879,7 @@ hipError_t run_instnorm_mom(const void* x, const float* mom, void* y, int64_t N,
     return hipErrorInvalidValue;
   const int64_t blocks = N * ((C + 31) / 32) * (spatial / kNormSeg);
   if (blocks > 0x7fffffff) return hipErrorInvalidValue;
-  const size_t shm = 2 * 32 * (size_t)(spatial / kNormSeg) * sizeof(float2);
-  hipLaunchKernelGGL(instnorm_mom_kernel, dim3((unsigned)blocks), dim3(256), shm, st, (const _Float16*)x, mom,
+  hipLaunchKernelGGL(instnorm_mom_kernel, dim3((unsigned)blocks), dim3(256), 0, st, (const _Float16*)x, mom,
                      (_Float16*)y, C, (int)spatial, eps, aff, (int)out_nhwc);
   return hipGetLastError();
 }
