@@ -53,6 +53,10 @@ def parse():
                         "instead of benchmarking")
     p.add_argument("--trace-last", type=int, default=0,
                    help="with --trace-stats: also average each group's last N dispatches (the timed steps)")
+    p.add_argument("--trace-forward", default="", metavar="MARK",
+                   help="with --trace-stats on a kernel trace: a markdown table of kernel time per forward over "
+                        "the last --trace-last forwards, a forward being the dispatches between two launches of "
+                        "the kernel whose name contains MARK (one launch per forward)")
     return p.parse_args()
 
 
@@ -82,6 +86,32 @@ def trace_stats(path, last):
         if last and len(d) >= last:
             line += f"  last {last}: avg {sum(d[-last:]) / last:9.2f} us"
         print(f"kernel {name}\n  grid {grid}  {line}")
+
+
+def trace_forward(path, mark, last):
+    """Kernel time per forward over the last `last` forwards of a kernel
+    trace: the dispatches after the (F - last)-th launch of the marker
+    kernel up to and including the last one, F = the marker's launches."""
+    import csv
+    import re
+    rows = sorted(csv.DictReader(open(path)), key=lambda r: int(r["Start_Timestamp"]))
+    names = [re.sub(r"\s+", " ", r["Kernel_Name"]) for r in rows]
+    idx = [i for i, n in enumerate(names) if mark in n]
+    last = min(last or len(idx) - 1, len(idx) - 1)
+    if last < 1:
+        raise SystemExit(f"--trace-forward: fewer than two launches of a kernel matching {mark!r}")
+    per = {}
+    for i in range(idx[-last - 1] + 1, idx[-1] + 1):
+        d = (int(rows[i]["End_Timestamp"]) - int(rows[i]["Start_Timestamp"])) / 1e3
+        key = (names[i], rows[i].get("Grid_Size") or rows[i].get("Grid_Size_X") or "")
+        per.setdefault(key, []).append(d)
+    total = sum(sum(v) for v in per.values()) / last
+    print(f"forwards in the trace: {len(idx)}; the last {last}: {total:.1f} us of kernel time per forward\n")
+    print("| kernel | grid | calls per forward | us per call | us per forward | % |")
+    print("|---|---|---|---|---|---|")
+    for (name, grid), v in sorted(per.items(), key=lambda kv: -sum(kv[1])):
+        pf = sum(v) / last
+        print(f"| `{name}` | {grid} | {len(v) / last:.1f} | {sum(v) / len(v):.2f} | {pf:.1f} | {100 * pf / total:.1f} |")
 
 
 def settle_clock(torch, fn, ms):
@@ -172,7 +202,10 @@ def cpu_baseline_f16(seconds):
 def main():
     args = parse()
     if args.trace_stats:
-        trace_stats(args.trace_stats, args.trace_last)
+        if args.trace_forward:
+            trace_forward(args.trace_stats, args.trace_forward, args.trace_last)
+        else:
+            trace_stats(args.trace_stats, args.trace_last)
         return
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only; how the path would shard across GPUs "
