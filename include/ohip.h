@@ -463,6 +463,7 @@ int ohip_reset_counters(ohip_ctx* ctx);
  * 17: 3x3 stride-1 f16 / bf16 convolutions with 16-, 32- or 64-wide output
  *     rows take the whole-K halo kernel (no split-K) wherever its geometry
  *     allows (automatically from 256 blocks and 1.5 GFLOP up).
+ * 18: 192x256 (8, two LDS stages, one block per CU).
  * The automatic choice splits K (on 64x64 tiles) when the 64x64 tiling gives
  * fewer than 256 blocks and K is at least 16 stages of 128 bytes. */
 int ohip_set_tile_override(ohip_ctx* ctx, int tile_id);

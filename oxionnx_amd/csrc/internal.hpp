@@ -123,7 +123,7 @@ struct OutMap {
 // generator's resident NHWC convolutions, so the automatic plan keeps 64x64.)
 // Tile ids that name one unsplit block tile (launch.hpp); 10 and 11 force
 // split-K.
-inline bool plain_tile_id(int t) { return (t >= 1 && t <= 9) || (t >= 12 && t <= 14) || t == 16; }
+inline bool plain_tile_id(int t) { return (t >= 1 && t <= 9) || (t >= 12 && t <= 14) || t == 16 || t == 18; }
 inline int split_tile_size(int, int, int forced_tile) { return forced_tile == 11 ? 128 : 64; }
 // OHIP_SPLITS=n (2..16) forces that many split-K slices wherever a split
 // plan is made (a measurement switch)

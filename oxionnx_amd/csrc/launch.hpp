@@ -389,6 +389,7 @@ using T128d4 = Tile<128, 128, 2, 4, 4>;     // 12: 8 waves, 64x32 per wave, four
 using T64d8 = Tile<64, 64, 2, 2, 8>;        // 13: 4 waves, 32x32 per wave, eight stages
 using T128x4w4 = Tile<128, 128, 2, 2, 4>;   // 14: 4 waves, 64x64 per wave, four stages
 using T256x3 = Tile<256, 256, 2, 4, 2, 8, 3>;  // 16: as 6 with a third X buffer, X loads two stages ahead
+using T192x256 = Tile<192, 256, 2, 4, 2>;   // 18: 8 waves, 96x64 per wave (one block per CU)
 
 
 // Tiles per XCD group along P in the engine's tile order (map_tile);
@@ -541,6 +542,19 @@ inline int pick_tile(int P, int Q, int kc, int forced, bool half = false) {
   return 9;
 }
 
+// Byte outputs (u8 / i8 requantised) of a short-K grid of more than two
+// rounds of 128x128 tiles (two blocks a CU) that the 192x256 tile covers in
+// one round of one block a CU: config 3's first FFN GEMM (4096x768 ->
+// 3072: 768 tiles of 128x128, 256 of 192x256) 22.6 -> 19.4 us.  Its
+// staged byte outputs fit the stage buffers; 4-byte outputs would leave
+// unstaged (MatMulInteger: 29.7 against 24.6 us) and keep the 128x128 tile.
+template <class Epi> inline bool byte_outputs(const Epi&) { return false; }
+inline bool byte_outputs(const QuantEpi& e) { return e.out_kind == QOUT_U8 || e.out_kind == QOUT_I8; }
+inline bool prefer_192x256(int P, int Q, int kc) {
+  auto blocks = [&](int bp, int bq) { return (int64_t)((P + bp - 1) / bp) * ((Q + bq - 1) / bq); };
+  return (kc + 7) / 8 <= 16 && blocks(128, 128) > 512 && blocks(192, 256) <= 256;
+}
+
 // XX / XY: the X / Y operand holds u8 activations that the MFMA reads as
 // int8 after XOR 0x80.
 template <Op O, bool XX, bool XY, class LX, class LY, class Epi>
@@ -557,7 +571,9 @@ inline hipError_t launch_any(const LX& lx, const LY& ly, const Epi& epi, int P, 
       return launch_split_on<O, XX, XY, T128w8>(lx, ly, epi, P, Q, kc, splits, split_ws, st);
     return launch_split_on<O, XX, XY, T64s4>(lx, ly, epi, P, Q, kc, splits, split_ws, st);
   }
-  switch (pick_tile(P, Q, kc, tile, O == Op::F16 || O == Op::BF16)) {
+  int choice = pick_tile(P, Q, kc, tile, O == Op::F16 || O == Op::BF16);
+  if (tile == 0 && byte_outputs(epi) && prefer_192x256(P, Q, kc)) choice = 18;
+  switch (choice) {
     case 2: return launch_tile<O, XX, XY, T128>(lx, ly, epi, P, Q, kc, st);
     case 3: return launch_tile<O, XX, XY, T256x128>(lx, ly, epi, P, Q, kc, st);
     case 4: return launch_tile<O, XX, XY, T128x256>(lx, ly, epi, P, Q, kc, st);
@@ -570,6 +586,7 @@ inline hipError_t launch_any(const LX& lx, const LY& ly, const Epi& epi, int P, 
     case 13: return launch_tile<O, XX, XY, T64d8>(lx, ly, epi, P, Q, kc, st);
     case 14: return launch_tile<O, XX, XY, T128x4w4>(lx, ly, epi, P, Q, kc, st);
     case 16: return launch_tile<O, XX, XY, T256x3>(lx, ly, epi, P, Q, kc, st);
+    case 18: return launch_tile<O, XX, XY, T192x256>(lx, ly, epi, P, Q, kc, st);
     default: return launch_tile<O, XX, XY, T64>(lx, ly, epi, P, Q, kc, st);
   }
 }

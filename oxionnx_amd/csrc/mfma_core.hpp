@@ -499,7 +499,8 @@ __device__ __forceinline__ void tile_epilogue(const Epi& epi, A (&acc)[Tl::TP][T
     constexpr int EB = decltype(ebc)::value;
     constexpr int CPR = Tl::BP * EB / 16;
     const int byte = (ig - p0) * EB;
-    char* dst = stg + lj * (Tl::BP * EB) + (((byte >> 4) ^ (lj & (CPR - 1))) << 4) + (byte & 15);
+    constexpr int SWZ = (CPR & -CPR) - 1;   // XOR inside aligned power-of-two chunk groups of the row
+    char* dst = stg + lj * (Tl::BP * EB) + (((byte >> 4) ^ (lj & SWZ)) << 4) + (byte & 15);
     if constexpr (EB == 4) {
       *reinterpret_cast<u32x4*>(dst) = u32x4{bits[0], bits[1], bits[2], bits[3]};
     } else if constexpr (EB == 2) {
@@ -586,7 +587,8 @@ __device__ __forceinline__ void tile_epilogue(const Epi& epi, A (&acc)[Tl::TP][T
       const int row = c / CPR, cc = c - row * CPR;
       const int j = q0 + row, i = p0 + cc * EPC;
       if (j >= out.Q || i >= out.P) continue;
-      const u32x4 v = *reinterpret_cast<const u32x4*>(stg + row * (Tl::BP * EB) + ((cc ^ (row & (CPR - 1))) << 4));
+      constexpr int SWZ = (CPR & -CPR) - 1;
+      const u32x4 v = *reinterpret_cast<const u32x4*>(stg + row * (Tl::BP * EB) + ((cc ^ (row & SWZ)) << 4));
       char* dst = out.y + (out.row(i) + (int64_t)j * out.sj) * EB;
       if (i + EPC <= out.P) {
         *reinterpret_cast<u32x4*>(dst) = v;

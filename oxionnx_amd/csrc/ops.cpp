@@ -348,7 +348,7 @@ extern "C" int ohip_sync(ohip_ctx* ctx) {
 
 extern "C" int ohip_set_tile_override(ohip_ctx* ctx, int tile_id) {
   if (!ctx) return fail(OHIP_E_INVALID, "null context");
-  if (tile_id < 0 || tile_id > 17) return fail(OHIP_E_INVALID, "tile id must be 0..17");
+  if (tile_id < 0 || tile_id > 18) return fail(OHIP_E_INVALID, "tile id must be 0..18");
   ctx->tile_override = tile_id;
   return OHIP_OK;
 }

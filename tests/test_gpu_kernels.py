@@ -50,7 +50,7 @@ GEMM_SHAPES = [(1, 64, 32), (3, 100, 17), (8, 256, 64), (2, 5000, 40), (9, 64, 4
 
 
 @pytest.mark.parametrize("mkn", GEMM_SHAPES, ids=str)
-@pytest.mark.parametrize("tile", list(range(12)) + [16])
+@pytest.mark.parametrize("tile", list(range(12)) + [16, 18])
 def test_gemm_f32_matches_oracle(torch, ctx, mkn, tile):
     from oxionnx_amd import _lib as L
     m, k, n = mkn
@@ -120,7 +120,7 @@ def test_gemm_golden_vectors(torch, ctx, c):
 @pytest.mark.parametrize("bf16", [False, True], ids=["f16", "bf16"])
 @pytest.mark.parametrize("mkn", [(1, 128, 64), (5, 96, 40), (64, 64, 64), (130, 264, 200), (512, 768, 384)],
                          ids=str)
-@pytest.mark.parametrize("tile", [0, 6, 16])
+@pytest.mark.parametrize("tile", [0, 6, 16, 18])
 def test_gemm_half_matches_oracle(torch, ctx, bf16, mkn, tile):
     from oxionnx_amd import _lib as L
     m, k, n = mkn
@@ -712,6 +712,35 @@ def test_qlinear_matmul_bit_exact(torch, ctx, mkn, a_u8):
                   y_scale=float(y_s), y_zp=y_zp, lo=lo, hi=hi).cpu().numpy()
     want = O.qlinear_matmul(a, a_s, azp, b, b_s, 0, y_s, y_zp, sat_range=(lo, hi))
     np.testing.assert_array_equal(y.astype(np.float32), want)
+
+
+@pytest.mark.parametrize("mkn", [(37, 100, 53), (300, 768, 600), (513, 1024, 200)], ids=str)
+@pytest.mark.parametrize("out", ["u8", "i32"])
+def test_qgemm_192x256_tile_bit_exact(torch, ctx, mkn, out):
+    """The 192x256 tile (18; one block per CU for short-K grids of more
+    than two rounds of 128x128 tiles), u8 outputs staged through LDS (12
+    16-byte chunks a staged row) and raw int32, ragged edges on both axes."""
+    from oxionnx_amd import _lib as L
+    m, k, n = mkn
+    rng = np.random.default_rng(m + 2 * n)
+    a = rng.integers(0, 256, (m, k)).astype(np.uint8)
+    b = rng.integers(-127, 128, (k, n)).astype(np.int8)
+    bs = rng.uniform(0.001, 0.01, n).astype(np.float32)
+    ctx.set_tile(18)
+    try:
+        if out == "u8":
+            w = ctx.weight_qgemm(b, zp=0, scale=np.float32(0.0041))
+            y = ctx.qgemm(_dev(torch, a), w, a_zp=128, out_kind=L.QOUT_U8, a_scale=0.02, y_scale=0.05,
+                          y_zp=128, lo=0, hi=255).cpu().numpy()
+            want = O.qlinear_matmul(a, np.float32(0.02), 128, b, np.float32(0.0041), 0, np.float32(0.05), 128,
+                                    sat_range=(0, 255))
+            np.testing.assert_array_equal(y.astype(np.float32), want)
+        else:
+            w = ctx.weight_qgemm(b, zp=0)
+            y = ctx.qgemm(_dev(torch, a), w, a_zp=128, out_kind=L.QOUT_I32).cpu().numpy()
+            np.testing.assert_array_equal(y, O.matmul_integer(a, b, 128, 0))
+    finally:
+        ctx.set_tile(0)
 
 
 def test_matmul_integer_per_row_zero_point(torch, ctx):
