@@ -140,6 +140,33 @@ def time_launches(torch, stream, fn, iters, warmup):
     return start.elapsed_time(end) / iters  # ms per launch
 
 
+def time_graph(torch, ctx, L, fn, launches=20, reps=10):
+    """ms per launch of fn replayed from a HIP graph of `launches` launches
+    (launch overhead out of the figure).  fn runs once eagerly first, so its
+    workspace comes from the context's pool during the capture."""
+    import ctypes
+    lib = L.lib()
+    fn()
+    torch.cuda.synchronize()
+    L.check(lib.ohip_graph_begin(ctx.h))
+    for _ in range(launches):
+        fn()
+    g = ctypes.c_void_p()
+    L.check(lib.ohip_graph_end(ctx.h, ctypes.byref(g)))
+    try:
+        for _ in range(3):
+            L.check(lib.ohip_graph_launch(g))
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            L.check(lib.ohip_graph_launch(g))
+        L.check(lib.ohip_sync(ctx.h))
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) * 1e3 / (reps * launches)
+    finally:
+        lib.ohip_graph_destroy(g)
+
+
 def gemm_setup(torch, ctx, L, m, k, n, dtype, rng):
     a = rng.uniform(-1, 1, (m, k)).astype(np.float32)
     b = rng.normal(0, 1 / np.sqrt(k), (k, n)).astype(np.float32)
@@ -270,11 +297,17 @@ def main():
                     eb = 4 if dt == L.F32 else 2
                     fl = 2.0 * mm * kk * nn
                     by = eb * (mm * kk + kk * nn + mm * nn + nn)
-                    sweep.append({"shape": [mm, kk, nn], "dtype": name, "ms": round(t, 5),
-                                  "tflops": round(fl / t / 1e9, 2),
-                                  "frac_mfma": round(fl / t / 1e9 / PEAK_TFLOPS[name], 4),
-                                  "gbps": round(by / t / 1e6, 1),
-                                  "frac_hbm": round(by / t / 1e6 / HBM_GBPS, 4)})
+                    entry = {"shape": [mm, kk, nn], "dtype": name, "ms": round(t, 5),
+                             "tflops": round(fl / t / 1e9, 2),
+                             "frac_mfma": round(fl / t / 1e9 / PEAK_TFLOPS[name], 4),
+                             "gbps": round(by / t / 1e6, 1),
+                             "frac_hbm": round(by / t / 1e6 / HBM_GBPS, 4)}
+                    if mm * kk * nn < 1e9:
+                        # the launch-bound shapes also replayed from a HIP graph
+                        tg = time_graph(torch, ctx, L, fn)
+                        entry.update({"ms_graph": round(tg, 5), "gbps_graph": round(by / tg / 1e6, 1),
+                                      "frac_hbm_graph": round(by / tg / 1e6 / HBM_GBPS, 4)})
+                    sweep.append(entry)
                     del ww, aa, cc, yy
             extras["gemm_sweep"] = sweep
             extras.update(bench_conv(torch, ctx, L, stream, rng, args.only))
