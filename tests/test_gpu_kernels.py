@@ -636,12 +636,15 @@ def test_conv2d_instnorm_entry_point(torch, ctx, case):
 
 
 # (x shape, cout, tile): config 4's residual conv (the automatic plan), a
-# 16-wide image pair with a partial 32-channel tile, and a channel tail
-# inside the eight-chunk slab (tile 17 forces the whole-K kernel)
+# 16-wide image pair with a partial 32-channel tile, a channel tail inside
+# the eight-chunk slab (tile 17 forces the whole-K kernel; these planes take
+# the segment-moments norm), and a 128 x 64 plane (8192 values, past the
+# moments norm's 4096: the whole-K sums go to the norm as one slice)
 WK_NORM_CASES = [
     ((1, 512, 32, 32), 512, 0),
     ((2, 64, 16, 16), 96, 17),
     ((1, 40, 32, 32), 72, 17),
+    ((1, 32, 128, 64), 64, 17),
 ]
 
 
