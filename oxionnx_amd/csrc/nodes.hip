@@ -784,6 +784,7 @@ __global__ void __launch_bounds__(256) instnorm_mom_kernel(const _Float16* __res
                                                            int out_nhwc) {
 #pragma clang fp contract(off)
   typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+  NSTAMP(0);
   __shared__ float st[2][32];
   __shared__ h8 tile[32][9];   // [channel][eight-pixel chunk] (one chunk of padding)
   __shared__ float afs[2][32];   // each channel's scale and bias
@@ -843,6 +844,7 @@ __global__ void __launch_bounds__(256) instnorm_mom_kernel(const _Float16* __res
   }
   tile[t >> 3][t & 7] = xv;
   __syncthreads();
+  NSTAMP(1);
   if (!live) return;
   const bool affine = aff.scale || aff.bias;
   auto finish = [&](float v0, int cl, float r1) {
@@ -869,6 +871,7 @@ __global__ void __launch_bounds__(256) instnorm_mom_kernel(const _Float16* __res
     for (int e = 0; e < 8; ++e) out[e] = finish((float)xv[e], cl, (float)r[e]);
   }
   *reinterpret_cast<h8*>(y + o) = out;
+  NSTAMP(2);
 }
 
 hipError_t run_instnorm_mom(const void* x, const float* mom, void* y, int64_t N, int C, int64_t spatial, float eps,
