@@ -154,17 +154,17 @@ __global__ void __launch_bounds__(kThreads) instnorm_kernel(const T* __restrict_
   for (int64_t i = threadIdx.x; i < spatial; i += kThreads) {
     float v = (ld(i) - mean) * inv;
     if (affine) {
-      v = (float)(T)v;
-      if (aff.scale) v = (float)(T)(v * sc);
-      if (aff.bias) v = (float)(T)(v + bi);
+      v = round_to<T>(v);
+      if (aff.scale) v = round_to<T>(v * sc);
+      if (aff.bias) v = round_to<T>(v + bi);
     }
     if (aff.act == UN_RELU) v = v > 0.0f ? v : 0.0f;
-    else if (aff.act == UN_LEAKY_RELU) v = (float)(T)v, v = v >= 0.0f ? v : v * aff.alpha;
+    else if (aff.act == UN_LEAKY_RELU) v = round_to<T>(v), v = v >= 0.0f ? v : v * aff.alpha;
     if (aff.residual) {
       const T* r = static_cast<const T*>(aff.residual);
-      v = (float)(T)v + (aff.res_nhwc ? ldf(r, (n * spatial + i) * C + c) : ldf(r + plane * spatial, i));
+      v = round_to<T>(v) + (aff.res_nhwc ? ldf(r, (n * spatial + i) * C + c) : ldf(r + plane * spatial, i));
     }
-    stf(yp, i, v);
+    stf(yp, i, opaque(v));
   }
 }
 
@@ -288,18 +288,19 @@ __global__ void __launch_bounds__(kThreads * PPB) instnorm_partials_kernel(const
   for (int i = lt; i < spatial; i += kThreads) {
     float v = (xs[i] - mean) * inv;
     if (affine) {
-      v = (float)(T)v;
-      if (aff.scale) v = (float)(T)(v * sc);
-      if (aff.bias) v = (float)(T)(v + bi);
+      v = round_to<T>(v);
+      if (aff.scale) v = round_to<T>(v * sc);
+      if (aff.bias) v = round_to<T>(v + bi);
     }
     if (aff.act == UN_RELU) v = v > 0.0f ? v : 0.0f;
-    else if (aff.act == UN_LEAKY_RELU) v = (float)(T)v, v = v >= 0.0f ? v : v * aff.alpha;
+    else if (aff.act == UN_LEAKY_RELU) v = round_to<T>(v), v = v >= 0.0f ? v : v * aff.alpha;
     if constexpr (PPB == 1) {
-      if (res) v = (float)(T)v + (float)(aff.res_nhwc ? res[(n * spatial + i) * C + c] : res[plane * spatial + i]);
+      if (res) v = round_to<T>(v) + (float)(aff.res_nhwc ? res[(n * spatial + i) * C + c] : res[plane * spatial + i]);
+      v = opaque(v);
       if (out_nhwc) y[(n * spatial + i) * C + c] = (T)v;   // channel c of each pixel (C per pixel)
       else yp[i] = (T)v;
     } else {
-      xs[i] = (float)(T)v;   // the stored value; the residual is added below, per run
+      xs[i] = round_to<T>(v);   // the stored value; the residual is added below, per run
     }
   }
   NSTAMP(4);
@@ -331,7 +332,7 @@ __global__ void __launch_bounds__(kThreads * PPB) instnorm_partials_kernel(const
       for (int k = 0; k < PPB; ++k) {
         float v = xs_all[k * spatial + i];
         if (res) v = v + (float)r[k];
-        o[k] = (T)v;
+        o[k] = (T)opaque(v);
       }
       Run* dp = reinterpret_cast<Run*>(y + pix * C + c0);
 #pragma unroll
@@ -851,14 +852,14 @@ __global__ void __launch_bounds__(256) instnorm_mom_kernel(const _Float16* __res
     const float sc = afs[0][cl], bi = afs[1][cl];
     float v = (v0 - st[0][cl]) * st[1][cl];
     if (affine) {
-      v = (float)(_Float16)v;
-      if (aff.scale) v = (float)(_Float16)(v * sc);
-      if (aff.bias) v = (float)(_Float16)(v + bi);
+      v = round_to<_Float16>(v);
+      if (aff.scale) v = round_to<_Float16>(v * sc);
+      if (aff.bias) v = round_to<_Float16>(v + bi);
     }
     if (aff.act == UN_RELU) v = v > 0.0f ? v : 0.0f;
-    else if (aff.act == UN_LEAKY_RELU) v = (float)(_Float16)v, v = v >= 0.0f ? v : v * aff.alpha;
-    if (res) v = (float)(_Float16)v + r1;
-    return (_Float16)v;
+    else if (aff.act == UN_LEAKY_RELU) v = round_to<_Float16>(v), v = v >= 0.0f ? v : v * aff.alpha;
+    if (res) v = round_to<_Float16>(v) + r1;
+    return (_Float16)opaque(v);
   };
   h8 out;
   if (out_nhwc) {

@@ -23,6 +23,20 @@
 
 namespace ohip {
 
+// The affine tail's storage roundings: v is first materialised as an f32
+// value (the operation's own rounding), then rounded to T, so that the
+// compiler cannot fold the f32 operation and the narrowing into one
+// mixed-precision FMA with a single rounding -- every norm kernel then
+// rounds twice, the same way, whatever its surrounding code.
+__device__ __forceinline__ float opaque(float v) {
+  __asm__("" : "+v"(v));
+  return v;
+}
+template <class T>
+__device__ __forceinline__ float round_to(float v) {
+  return (float)(T)opaque(v);
+}
+
 constexpr int kNormRun = 4;
 constexpr int kNormSeg = 64;      // 16 runs
 constexpr int kNormGroup = 256;   // segments merged as one tree
