@@ -393,11 +393,11 @@ hipError_t run_instnorm(int dt, const void* x, void* y, int64_t planes, int64_t 
 constexpr int64_t kNormPartialsMaxSpatial = 16384;
 // the moments-fed norm's largest plane (64 segments a channel, merged in registers)
 constexpr int64_t kNormMomMaxSpatial = 4096;
-// f16 instance normalisation from the conv output x (NCHW) and its
-// 64-pixel segment moments (wk_conv_kernel's mom); the residual, if any, in
-// the output's layout
-hipError_t run_instnorm_mom(const void* x, const float* mom, void* y, int64_t N, int C, int64_t spatial, float eps,
-                            const NormAffine& aff, bool out_nhwc, hipStream_t st);
+// f16 / f32 (dt) instance normalisation from the conv output x (NCHW) and
+// its 64-pixel segment moments (wk_conv_kernel's mom); the residual, if any,
+// in the output's layout; x, y and the residual aligned to eight elements
+hipError_t run_instnorm_mom(int dt, const void* x, const float* mom, void* y, int64_t N, int C, int64_t spatial,
+                            float eps, const NormAffine& aff, bool out_nhwc, hipStream_t st);
 hipError_t run_instnorm_partials(int dt, const float* ws, int splits, int64_t Pp, const void* conv_bias, void* y,
                                  int64_t N, int64_t spatial, int C, float eps, const NormAffine& aff, bool out_nhwc,
                                  hipStream_t st);

@@ -771,20 +771,20 @@ hipError_t run_instnorm(int dt, const void* x, void* y, int64_t planes, int64_t 
   return hipGetLastError();
 }
 
-// Instance normalisation of f16 conv outputs whose statistics arrive as the
-// moments of their 64-pixel segments (wk_conv_kernel with mom): a block
-// takes 32 channels x 64 pixels of one image, merges each channel's
+// Instance normalisation of f16 / f32 conv outputs whose statistics arrive
+// as the moments of their 64-pixel segments (wk_conv_kernel with mom): a
+// block takes 32 channels x 64 pixels of one image, merges each channel's
 // segments as the plain kernel does (norm_stats.hpp's tree), and
 // normalises its tile with the affine tail, activation and residual of the
-// unfused chain, reading the conv output as NCHW rows and writing 16-byte
-// runs (eight channels of a pixel for an NHWC output, eight pixels of a
-// channel for NCHW).
-__global__ void __launch_bounds__(256) instnorm_mom_kernel(const _Float16* __restrict__ x,
-                                                           const float* __restrict__ mom, _Float16* __restrict__ y,
-                                                           int C, int spatial, float eps, NormAffine aff,
-                                                           int out_nhwc) {
+// unfused chain, reading the conv output as NCHW rows and writing runs of
+// eight elements (eight channels of a pixel for an NHWC output, eight
+// pixels of a channel for NCHW).
+template <class T>
+__global__ void __launch_bounds__(256) instnorm_mom_kernel(const T* __restrict__ x, const float* __restrict__ mom,
+                                                           T* __restrict__ y, int C, int spatial, float eps,
+                                                           NormAffine aff, int out_nhwc) {
 #pragma clang fp contract(off)
-  typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+  typedef T h8 __attribute__((ext_vector_type(8)));   // eight elements: 16 bytes of f16, 32 of f32
   NSTAMP(0);
   __shared__ float st[2][32];
   __shared__ h8 tile[32][9];   // [channel][eight-pixel chunk] (one chunk of padding)
@@ -798,7 +798,7 @@ __global__ void __launch_bounds__(256) instnorm_mom_kernel(const _Float16* __res
   // every global load of the block in flight before the first wait: this
   // thread's eight pixels (or, NHWC, eight channels) of the conv output and
   // of the residual, and its share of the first chunk of segment moments
-  const _Float16* res = static_cast<const _Float16*>(aff.residual);
+  const T* res = static_cast<const T*>(aff.residual);
   h8 xv{}, r{};
   int64_t o;
   bool live;
@@ -819,7 +819,7 @@ __global__ void __launch_bounds__(256) instnorm_mom_kernel(const _Float16* __res
   if (t < cw) {
     const int64_t ai = aff.per_sample ? (int64_t)n * aff.stride + c0 + t : c0 + t;
     auto term = [&](const void* p) {
-      return aff.same_type ? (float)static_cast<const _Float16*>(p)[ai] : static_cast<const float*>(p)[ai];
+      return aff.same_type ? (float)static_cast<const T*>(p)[ai] : static_cast<const float*>(p)[ai];
     };
     afs[0][t] = aff.scale ? term(aff.scale) : 1.0f;
     afs[1][t] = aff.bias ? term(aff.bias) : 0.0f;
@@ -852,14 +852,14 @@ __global__ void __launch_bounds__(256) instnorm_mom_kernel(const _Float16* __res
     const float sc = afs[0][cl], bi = afs[1][cl];
     float v = (v0 - st[0][cl]) * st[1][cl];
     if (affine) {
-      v = round_to<_Float16>(v);
-      if (aff.scale) v = round_to<_Float16>(v * sc);
-      if (aff.bias) v = round_to<_Float16>(v + bi);
+      v = round_to<T>(v);
+      if (aff.scale) v = round_to<T>(v * sc);
+      if (aff.bias) v = round_to<T>(v + bi);
     }
     if (aff.act == UN_RELU) v = v > 0.0f ? v : 0.0f;
-    else if (aff.act == UN_LEAKY_RELU) v = round_to<_Float16>(v), v = v >= 0.0f ? v : v * aff.alpha;
-    if (res) v = round_to<_Float16>(v) + r1;
-    return (_Float16)opaque(v);
+    else if (aff.act == UN_LEAKY_RELU) v = round_to<T>(v), v = v >= 0.0f ? v : v * aff.alpha;
+    if (res) v = round_to<T>(v) + r1;
+    return (T)opaque(v);
   };
   h8 out;
   if (out_nhwc) {
@@ -875,16 +875,24 @@ __global__ void __launch_bounds__(256) instnorm_mom_kernel(const _Float16* __res
   NSTAMP(2);
 }
 
-hipError_t run_instnorm_mom(const void* x, const float* mom, void* y, int64_t N, int C, int64_t spatial, float eps,
-                            const NormAffine& aff, bool out_nhwc, hipStream_t st) {
+hipError_t run_instnorm_mom(int dt, const void* x, const float* mom, void* y, int64_t N, int C, int64_t spatial,
+                            float eps, const NormAffine& aff, bool out_nhwc, hipStream_t st) {
   if (N <= 0 || spatial <= 0) return hipSuccess;
+  const uintptr_t run = dt == DT_F32 ? 32 : 16;   // eight elements
   if (spatial % kNormSeg != 0 || spatial > kNormMomMaxSpatial || (out_nhwc && C % 8 != 0) ||
-      (aff.residual && aff.res_nhwc != (int)out_nhwc))
+      (aff.residual && aff.res_nhwc != (int)out_nhwc) || (uintptr_t)x % run || (uintptr_t)y % run ||
+      (uintptr_t)aff.residual % run)
     return hipErrorInvalidValue;
   const int64_t blocks = N * ((C + 31) / 32) * (spatial / kNormSeg);
   if (blocks > 0x7fffffff) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(instnorm_mom_kernel, dim3((unsigned)blocks), dim3(256), 0, st, (const _Float16*)x, mom,
-                     (_Float16*)y, C, (int)spatial, eps, aff, (int)out_nhwc);
+  if (dt == DT_F16)
+    hipLaunchKernelGGL(instnorm_mom_kernel<_Float16>, dim3((unsigned)blocks), dim3(256), 0, st, (const _Float16*)x,
+                       mom, (_Float16*)y, C, (int)spatial, eps, aff, (int)out_nhwc);
+  else if (dt == DT_F32)
+    hipLaunchKernelGGL(instnorm_mom_kernel<float>, dim3((unsigned)blocks), dim3(256), 0, st, (const float*)x, mom,
+                       (float*)y, C, (int)spatial, eps, aff, (int)out_nhwc);
+  else
+    return hipErrorInvalidValue;
   return hipGetLastError();
 }
 

@@ -1332,7 +1332,7 @@ static bool wk_plan(ohip_ctx* ctx, const ohip_conv_desc* d, int64_t G, int64_t w
                     int64_t img_bytes) {
   const bool forced = ctx->tile_override == 17;
   if (!wk_allowed() || (ctx->tile_override != 0 && !forced) || G != 1) return false;
-  if (d->dtype != OHIP_F16 && d->dtype != OHIP_BF16) return false;
+  if (d->dtype != OHIP_F16 && d->dtype != OHIP_BF16 && d->dtype != OHIP_F32) return false;
   if (d->kh != 3 || d->kw != 3 || d->stride_h != 1 || d->stride_w != 1 || d->dil_h != 1 || d->dil_w != 1) return false;
   if (g.ow != 16 && g.ow != 32 && g.ow != 64) return false;
   const int64_t tpx = g.ow == 32 ? 64 : 128;
@@ -1456,11 +1456,14 @@ static int conv2d_impl(ohip_ctx* ctx, const ohip_conv_desc* d, const void* x, co
   // patch-staged kernel reads the input as it is, a fused reflect / edge pad
   // included (no staging transpose;
   // config 1: 27.7 -> 20.9 us).  Long reductions over few pixels keep the
-  // halo-patch path, whose split-K fills the chip.
+  // halo-patch path, whose split-K fills the chip, and so do the ones the
+  // whole-K kernel takes (the sums a fused norm's conv makes, bit for bit).
+  const int64_t staged_w = fused_pad ? d->w + d->pad_l + d->pad_r : d->w;
+  const int64_t staged_bytes =
+      (fused_pad ? (d->h + d->pad_t + d->pad_b) * (d->w + d->pad_l + d->pad_r) : d->h * d->w) * cpt * eb;
   if (!norm && !direct && !fewout && d->dtype == OHIP_F32 && G == 1 && d->in_layout == OHIP_NCHW &&
-      nchw_f32_allowed() && conv_nchw_f32_supported(a) &&
-      halo_plan(ctx, d, G, fused_pad ? d->w + d->pad_l + d->pad_r : d->w, g, (int)(cp / ce),
-                (fused_pad ? (d->h + d->pad_t + d->pad_b) * (d->w + d->pad_l + d->pad_r) : d->h * d->w) * cpt * eb) == 0) {
+      nchw_f32_allowed() && conv_nchw_f32_supported(a) && !wk_plan(ctx, d, G, staged_w, g, staged_bytes) &&
+      halo_plan(ctx, d, G, staged_w, g, (int)(cp / ce), staged_bytes) == 0) {
     ctx->counters.contraction_launches++;
     hipError_t e = run_conv_nchw_f32(static_cast<const float*>(x), static_cast<const float*>(w->data),
                                      static_cast<const float*>(bias), static_cast<float*>(y), a, ctx->stream);
@@ -1513,13 +1516,14 @@ static int conv2d_impl(ohip_ctx* ctx, const ohip_conv_desc* d, const void* x, co
   }
   // the whole-K kernel under a norm leaves its sums as one slice of f32
   // partial sums for the norm kernel
-  // An f16 norm over planes of whole 64-pixel segments takes its statistics
-  // from the whole-K kernel instead: the kernel stores the f16 conv output
-  // (NCHW) and each 64-pixel segment's moments, and the norm kernel merges
-  // those and rescales the stored output in one elementwise pass.
-  const bool wk_mom = wk && norm && d->dtype == OHIP_F16 && ohw % 64 == 0 && ohw <= kNormMomMaxSpatial &&
-                      (!norm_nhwc || d->cout % 8 == 0) &&
-                      (!norm->aff.residual || norm->aff.res_nhwc == (int)norm_nhwc);
+  // An f16 / f32 norm over planes of whole 64-pixel segments takes its
+  // statistics from the whole-K kernel instead: the kernel stores the conv
+  // output (NCHW) and each 64-pixel segment's moments, and the norm kernel
+  // merges those and rescales the stored output in one elementwise pass.
+  const bool wk_mom = wk && norm && (d->dtype == OHIP_F16 || d->dtype == OHIP_F32) && ohw % 64 == 0 &&
+                      ohw <= kNormMomMaxSpatial && (!norm_nhwc || d->cout % 8 == 0) &&
+                      (!norm->aff.residual || norm->aff.res_nhwc == (int)norm_nhwc) && aligned(y, 8 * eb) &&
+                      aligned(norm->aff.residual, 8 * eb);
   const bool partials = splits > 1 || (wk && norm && !wk_mom);
   size_t iw = partials ? plan.add(splits > 1 ? split_ws_bytes(sP, sQ, splits) : (size_t)sQ * ((sP + 3) / 4 * 4) * 4)
                        : SIZE_MAX;
@@ -1584,7 +1588,8 @@ static int conv2d_impl(ohip_ctx* ctx, const ohip_conv_desc* d, const void* x, co
                       : run_halo_float(d->dtype, hg, nchw_out, o, ctx->stream);
     if (e != hipSuccess) return hip_fail(e, wk ? "ohip_conv2d whole-K halo launch" : "ohip_conv2d halo launch");
     if (wk_mom) {
-      e = run_instnorm_mom(o.y, mom, y, d->n, (int)d->cout, ohw, norm->eps, norm->aff, norm_nhwc, ctx->stream);
+      e = run_instnorm_mom(d->dtype, o.y, mom, y, d->n, (int)d->cout, ohw, norm->eps, norm->aff, norm_nhwc,
+                           ctx->stream);
       if (e != hipSuccess) return hip_fail(e, "ohip_conv2d_instnorm launch");
     } else if (norm) {
       e = run_instnorm_partials(d->dtype, static_cast<const float*>(o.split_ws), splits, (rows + 3) / 4 * 4, bias,

@@ -616,12 +616,15 @@ def test_conv_instnorm_fusion_matches_unfused(ctx, case):
 
 
 # the whole-K conv forced (tile 17) where the automatic plan splits K: f16
-# planes of 16-, 32- and 64-pixel rows, so the norm reads the conv's stored
-# output and the moments of its 64-pixel segments
+# and f32 planes of 16-, 32- and 64-pixel rows, so the norm reads the conv's
+# stored output and the moments of its 64-pixel segments
 WK_MOM_CASES = [
     (2, 64, 16, "f16", True, True, "skip"),
     (1, 128, 32, "f16", False, True, None),
     (1, 64, 64, "f16", True, False, "skip"),
+    (2, 64, 16, "f32", True, True, "skip"),
+    (1, 128, 32, "f32", False, True, None),
+    (1, 64, 64, "f32", True, False, None),
 ]
 
 
@@ -641,7 +644,7 @@ def test_conv_instnorm_moments_path_matches_unfused(ctx, case):
     finally:
         ctx.set_tile(0)
     np.testing.assert_array_equal(got, want)
-    close(got, G.run_graph(g, feeds, half=True)["y"], 1e-2)
+    close(got, G.run_graph(g, feeds, half=(dt == "f16"))["y"], 1e-2 if dt == "f16" else 1e-4)
 
 
 def _bcast_residual_then_conv(dt):
