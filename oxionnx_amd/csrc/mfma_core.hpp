@@ -652,9 +652,13 @@ mfma_gemm_kernel(const LX lx, const LY ly, const Epi epi, int nP, int nQ, int kc
   constexpr int NL = Tl::NX + Tl::NY;     // DMA loads per thread per stage
   // Every stage issues all its loads (past the last stage they read zero or
   // the pad source), so the waits below are fixed counts of outstanding loads.
-  auto xbuf = [&](int kt) __attribute__((always_inline)) { return smem + (kt % Tl::XST) * (Tl::BP * Tl::kRowStride); };
+  // ring slots count stages from kbeg (so an unrolled loop knows them at
+  // compile time)
+  auto xbuf = [&](int kt) __attribute__((always_inline)) {
+    return smem + ((kt - kbeg) % Tl::XST) * (Tl::BP * Tl::kRowStride);
+  };
   auto ybuf = [&](int kt) __attribute__((always_inline)) {
-    return smem + Tl::kYBase + (kt % Tl::STAGES) * (Tl::BQ * Tl::kRowStride);
+    return smem + Tl::kYBase + ((kt - kbeg) % Tl::STAGES) * (Tl::BQ * Tl::kRowStride);
   };
   auto issue_x = [&](int kt) { lx.template issue<Tl::NX, Tl::kWaves, Tl::CH>(sx, kt, wave, xbuf(kt)); };
   auto issue_y = [&](int kt) { ly.template issue<Tl::NY, Tl::kWaves, Tl::CH>(sy, kt, wave, ybuf(kt)); };
@@ -717,13 +721,26 @@ mfma_gemm_kernel(const LX lx, const LY ly, const Epi epi, int nP, int nQ, int kc
   constexpr int NM = Tl::TP * Tl::TQ;      // MFMAs per k-step
   constexpr int NRD = Tl::TP + Tl::TQ;     // fragment reads per k-step
   constexpr int PRE = NM >= 4 ? 2 : 0;     // MFMAs of the last k-step ahead of the barrier
-  for (int kt = kbeg; kt < kend; ++kt) {
-    const u32x4* sX = xbuf(kt);
-    const u32x4* sY = ybuf(kt);
-    const u32x4* snX = xbuf(kt + 1);
-    const u32x4* snY = ybuf(kt + 1);
-    u32x4* sdX = xbuf(kt + Tl::XST - 1);
-    u32x4* sdY = ybuf(kt + Tl::STAGES - 1);
+  // one stage; phc: (kt - kbeg) modulo kUnroll as a compile-time constant,
+  // or -1 (ring slots computed at run time)
+  auto stage = [&](int kt, auto phc) __attribute__((always_inline)) {
+    constexpr int ph = decltype(phc)::value;
+    auto ring = [&](int d, auto isx) __attribute__((always_inline)) -> u32x4* {
+      constexpr bool X = decltype(isx)::value;
+      if constexpr (ph >= 0) {
+        if constexpr (X) return smem + ((ph + d) % Tl::XST) * (Tl::BP * Tl::kRowStride);
+        else return smem + Tl::kYBase + ((ph + d) % Tl::STAGES) * (Tl::BQ * Tl::kRowStride);
+      } else {
+        if constexpr (X) return xbuf(kt + d);
+        else return ybuf(kt + d);
+      }
+    };
+    const u32x4* sX = ring(0, std::true_type{});
+    const u32x4* sY = ring(0, std::false_type{});
+    const u32x4* snX = ring(1, std::true_type{});
+    const u32x4* snY = ring(1, std::false_type{});
+    u32x4* sdX = ring(Tl::XST - 1, std::true_type{});
+    u32x4* sdY = ring(Tl::STAGES - 1, std::false_type{});
     const typename LX::Step stx = lx.template step<Tl::NX, Tl::kWaves, Tl::CH>(sx, kt + Tl::XST - 1);
     const typename LY::Step sty = ly.template step<Tl::NY, Tl::kWaves, Tl::CH>(sy, kt + Tl::STAGES - 1);
     // Y's loads first, then X's (the order the waits count on)
@@ -770,6 +787,20 @@ mfma_gemm_kernel(const LX lx, const LY ly, const Epi epi, int nP, int nQ, int kc
       }
       __builtin_amdgcn_sched_barrier(0);
     });
+  };
+  // A deeper X ring than Y's (tile 16: 3 and 2) would take a division per
+  // ring slot per stage: its loop runs lcm(XST, STAGES) stages a trip with
+  // every slot a constant, the last part trip stage by stage.
+  constexpr int kUnroll = Tl::XST != Tl::STAGES && Tl::XST * Tl::STAGES <= 6 ? Tl::XST * Tl::STAGES : 1;
+  if constexpr (kUnroll > 1) {
+    int kt = kbeg;
+    for (; kt + kUnroll <= kend; kt += kUnroll)
+      static_for<kUnroll>([&](auto u) __attribute__((always_inline)) { stage(kt + decltype(u)::value, u); });
+    static_for<kUnroll - 1>([&](auto u) __attribute__((always_inline)) {
+      if (kt + decltype(u)::value < kend) stage(kt + decltype(u)::value, u);
+    });
+  } else {
+    for (int kt = kbeg; kt < kend; ++kt) stage(kt, std::integral_constant<int, -1>{});
   }
 
   OHIP_STAMP(2);
