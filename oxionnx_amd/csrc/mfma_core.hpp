@@ -217,6 +217,29 @@ struct DenseRows {
   }
 };
 
+// DenseRows whose rows hold whole stages (kc a multiple of the stage's CH
+// chunks, no kwrap): no stage has a K tail, so no per-load select; a stage
+// past the end re-reads the last one (its data is never used) and rows past
+// the edge still read zero through the range check.
+struct DenseRowsWhole : DenseRows {
+  explicit DenseRowsWhole(const DenseRows& d) : DenseRows(d) {}
+  template <int NR, int NW, int CH>
+  __device__ __forceinline__ Step step(const State<NR>&, int kt) const {
+    const int g0 = kt * CH < kc ? kt * CH : kc - CH;
+    return Step{g0 * 16, true};
+  }
+  template <int NR, int NW, int CH>
+  __device__ __forceinline__ void load(const State<NR>& s, const Step& st, int i, int wave, u32x4* lds_rows) const {
+    buf16(s.rs, s.voff[i], st.soff, lds_rows + (i * NW + wave) * 64);
+  }
+  template <int NR, int NW, int CH>
+  __device__ __forceinline__ void issue(const State<NR>& s, int kt, int wave, u32x4* lds_rows) const {
+    const Step st = step<NR, NW, CH>(s, kt);
+#pragma unroll
+    for (int i = 0; i < NR; ++i) load<NR, NW, CH>(s, st, i, wave, lds_rows);
+  }
+};
+
 // Implicit im2col over an NHWC activation whose channel count is padded to a
 // whole number of 16-byte chunks (cpc chunks per pixel).  Row r is output
 // pixel (n, oy, ox); K runs over (ky, kx, channel chunk).
