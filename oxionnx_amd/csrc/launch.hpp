@@ -408,7 +408,7 @@ inline hipError_t launch_tile(const LX& lx, const LY& ly, const Epi& epi, int P,
   if (nb > 0x7fffffff || batch > 65535) return hipErrorInvalidValue;
   // the deep-X 256x256 tile over two dense operands of whole stages: the
   // loader without the K-tail select (f16 headline: one select less per load)
-  if constexpr ((Tl::XST != Tl::STAGES || (O == Op::I8 && Tl::BP * Tl::BQ >= 192 * 256)) &&
+  if constexpr ((Tl::XST != Tl::STAGES || Tl::BP * Tl::BQ >= 128 * 256) &&
                 std::is_same<LX, DenseRows>::value && std::is_same<LY, DenseRows>::value) {
     if (lx.kc == kc && ly.kc == kc && kc >= Tl::CH && kc % Tl::CH == 0 && lx.kwrap == 0 && ly.kwrap == 0) {
       hipLaunchKernelGGL((mfma_gemm_kernel<O, Tl, DenseRowsWhole, DenseRowsWhole, Epi, XX, XY>),
