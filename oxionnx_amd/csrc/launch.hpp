@@ -406,9 +406,13 @@ inline hipError_t launch_tile(const LX& lx, const LY& ly, const Epi& epi, int P,
   const int batch = epi.out.batch > 1 ? epi.out.batch : 1;   // slices on blockIdx.z
   if (nb <= 0) return hipSuccess;
   if (nb > 0x7fffffff || batch > 65535) return hipErrorInvalidValue;
-  // the deep-X 256x256 tile over two dense operands of whole stages: the
-  // loader without the K-tail select (f16 headline: one select less per load)
-  if constexpr ((Tl::XST != Tl::STAGES || Tl::BP * Tl::BQ >= 128 * 256) &&
+  // two dense operands of whole stages on the large tiles (and the int8
+  // 128x128 ones): the loader without the K-tail select, one VALU select
+  // less per load (f16 headline +1-2 %, config 2c +3 %, int8 FFN pair about
+  // +5 %; the small f16 / f32 tiles gain nothing measurable and keep one
+  // loader, which halves their instantiations)
+  if constexpr ((Tl::XST != Tl::STAGES || Tl::BP * Tl::BQ >= 128 * 256 ||
+                 (O == Op::I8 && Tl::BP * Tl::BQ >= 128 * 128)) &&
                 std::is_same<LX, DenseRows>::value && std::is_same<LY, DenseRows>::value) {
     if (lx.kc == kc && ly.kc == kc && kc >= Tl::CH && kc % Tl::CH == 0 && lx.kwrap == 0 && ly.kwrap == 0) {
       hipLaunchKernelGGL((mfma_gemm_kernel<O, Tl, DenseRowsWhole, DenseRowsWhole, Epi, XX, XY>),
