@@ -679,6 +679,8 @@ inline Im2colNHWC make_im2col(const Im2colOperand& c) {
   r.zstride = c.zstride;
   r.zpads = c.zpads;
   for (int i = 0; i < 4; ++i) { r.zpt[i] = c.zpt[i]; r.zpl[i] = c.zpl[i]; }
+  magic_div(r.cpc, &r.cpc_mul, &r.cpc_shift);
+  magic_div(r.KW, &r.kw_mul, &r.kw_shift);
   return r;
 }
 

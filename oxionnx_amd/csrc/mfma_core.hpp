@@ -257,6 +257,8 @@ struct Im2colNHWC {
   int64_t zstride;     // batched launch: slice blockIdx.z reads base + z * zstride
   int zpads;           // > 0: slice z (< zpads <= 4) uses pads zpt[z], zpl[z] instead of pt, pl
   int zpt[4], zpl[4];
+  uint32_t cpc_mul, kw_mul;   // g / cpc and tap / KW as (x * mul) >> shift (magic_div)
+  int cpc_shift, kw_shift;
 
   template <int NR>
   struct State { const char* img[NR]; int iy0[NR], ix0[NR]; uint32_t okmask; int c; };
@@ -288,9 +290,9 @@ struct Im2colNHWC {
     if (kwrap > 0 && gk >= kwrap) gk -= kwrap;
     const bool kin = gk < kc;
     const int g = kin ? gk : 0;
-    const int tap = g / cpc;
+    const int tap = (int)(((uint64_t)(uint32_t)g * cpc_mul) >> cpc_shift);
     const int cc = g - tap * cpc;
-    const int ky = tap / KW;
+    const int ky = (int)(((uint64_t)(uint32_t)tap * kw_mul) >> kw_shift);
     const int kx = tap - ky * KW;
     return Step{ky * dh, kx * dw, cc, kin};
   }
