@@ -537,7 +537,7 @@ inline hipError_t launch_wk(const HaloGeo& g, const Epi& epi, int P, int Q, void
 // per CU and the four-stage 64x64 tile hides the load latency of the
 // narrowest problems.  A short K loop (few 128-byte stages) is dominated by
 // the prologue and the epilogue, which the resident 128x128 blocks overlap.
-inline int pick_tile(int P, int Q, int kc, int forced, bool deep_x = false) {
+inline int pick_tile(int P, int Q, int kc, int forced) {
   if (plain_tile_id(forced)) return forced;
   auto blocks = [&](int bp, int bq) { return (int64_t)((P + bp - 1) / bp) * ((Q + bq - 1) / bq); };
   const int nk = (kc + 7) / 8;
@@ -548,11 +548,12 @@ inline int pick_tile(int P, int Q, int kc, int forced, bool deep_x = false) {
   // two-stage tile; f16 1024x4096x4096 43.8 against 55.5, 768x4096x4096
   // 38.5 against 52.0; f32 within 3 %)
   if (blocks(128, 128) >= 192 && blocks(128, 128) < 320 && blocks(256, 256) < 256) return 12;
-  // f16 / bf16 / int8 take the 256x256 tile with the X operand's loads two
-  // stages ahead (bit-identical; headline 312.0 -> 308.7 us, f16 8192^3
-  // 889.7 -> 868.6, bf16 863.6 -> 844.9; int8 8192^3 2423-2429 -> 2496-2508
-  // TOPS since its loop runs unrolled without K-tail selects; f32 keeps 6)
-  if (blocks(256, 256) >= 256) return deep_x ? 16 : 6;
+  // the 256x256 tile with the X operand's loads two stages ahead
+  // (bit-identical; headline 312.0 -> 308.7 us, f16 8192^3 889.7 -> 868.6,
+  // bf16 863.6 -> 844.9; int8 8192^3 2423-2429 -> 2496-2508 TOPS and f32
+  // 4096x4096x11008 134.0 -> 136.1 TFLOP/s once its loop ran unrolled
+  // without K-tail selects)
+  if (blocks(256, 256) >= 256) return 16;
   if (blocks(256, 128) >= 256) return P >= Q ? 3 : 4;
   if (blocks(128, 128) >= 192) return 8;
   return 9;
@@ -587,7 +588,7 @@ inline hipError_t launch_any(const LX& lx, const LY& ly, const Epi& epi, int P, 
       return launch_split_on<O, XX, XY, T128w8>(lx, ly, epi, P, Q, kc, splits, split_ws, st);
     return launch_split_on<O, XX, XY, T64s4>(lx, ly, epi, P, Q, kc, splits, split_ws, st);
   }
-  int choice = pick_tile(P, Q, kc, tile, O != Op::F32);
+  int choice = pick_tile(P, Q, kc, tile);
   if (tile == 0 && byte_outputs(epi) && prefer_192x256(P, Q, kc)) choice = 18;
   switch (choice) {
     case 2: return launch_tile<O, XX, XY, T128>(lx, ly, epi, P, Q, kc, st);
