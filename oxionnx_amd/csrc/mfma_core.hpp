@@ -813,10 +813,13 @@ mfma_gemm_kernel(const LX lx, const LY ly, const Epi epi, int nP, int nQ, int kc
       __builtin_amdgcn_sched_barrier(0);
     });
   };
-  // A deeper X ring than Y's (tile 16: 3 and 2) would take a division per
-  // ring slot per stage: its loop runs lcm(XST, STAGES) stages a trip with
-  // every slot a constant, the last part trip stage by stage.
-  constexpr int kUnroll = Tl::XST != Tl::STAGES && Tl::XST * Tl::STAGES <= 6 ? Tl::XST * Tl::STAGES : 1;
+  // A ring of three (tile 16's X ring, the three-stage tiles' rings) would
+  // take a division per ring slot per stage: such a loop runs lcm(XST,
+  // STAGES) stages a trip with every slot a constant, the last part trip
+  // stage by stage.  Power-of-two rings keep the plain loop (a mask).
+  constexpr bool kPow2 = (Tl::XST & (Tl::XST - 1)) == 0 && (Tl::STAGES & (Tl::STAGES - 1)) == 0;
+  constexpr int kLcm = Tl::XST == Tl::STAGES ? Tl::XST : Tl::XST * Tl::STAGES;
+  constexpr int kUnroll = !kPow2 && kLcm <= 6 ? kLcm : 1;
   if constexpr (kUnroll > 1) {
     int kt = kbeg;
     for (; kt + kUnroll <= kend; kt += kUnroll)
