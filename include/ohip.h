@@ -459,8 +459,8 @@ int ohip_reset_counters(ohip_ctx* ctx);
  * 15: 3x3 stride-1 convolutions take the halo-patch kernel wherever its
  *     geometry allows (automatically only from 3 GFLOP up).
  * 16: 256x256 (8) with a third LDS buffer for the X operand, whose loads run
- *     two stages ahead (the automatic f16 / bf16 choice where 6 would be).
- * 17: 3x3 stride-1 f16 / bf16 convolutions with 16-, 32- or 64-wide output
+ *     two stages ahead (the automatic choice where 6 would be).
+ * 17: 3x3 stride-1 f16 / bf16 / f32 convolutions with 16-, 32- or 64-wide output
  *     rows take the whole-K halo kernel (no split-K) wherever its geometry
  *     allows (automatically from 256 blocks and 1.5 GFLOP up).
  * 18: 192x256 (8, two LDS stages, one block per CU).
