@@ -118,8 +118,10 @@ def test_gemm_golden_vectors(torch, ctx, c):
 
 
 @pytest.mark.parametrize("bf16", [False, True], ids=["f16", "bf16"])
-@pytest.mark.parametrize("mkn", [(1, 128, 64), (5, 96, 40), (64, 64, 64), (130, 264, 200), (512, 768, 384)],
-                         ids=str)
+# (257, 832, 300): 13 whole K stages (two six-stage trips of tile 16's
+# unrolled loop and a one-stage tail) with ragged rows and columns
+@pytest.mark.parametrize("mkn", [(1, 128, 64), (5, 96, 40), (64, 64, 64), (130, 264, 200), (512, 768, 384),
+                                 (257, 832, 300)], ids=str)
 @pytest.mark.parametrize("tile", [0, 6, 16, 18])
 def test_gemm_half_matches_oracle(torch, ctx, bf16, mkn, tile):
     from oxionnx_amd import _lib as L
