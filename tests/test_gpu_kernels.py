@@ -748,6 +748,30 @@ def test_qgemm_192x256_tile_bit_exact(torch, ctx, mkn, out):
         ctx.set_tile(0)
 
 
+@pytest.mark.parametrize("tile", [6, 16, 8, 12])
+@pytest.mark.parametrize("mkn", [(300, 1664, 520), (257, 1000, 300)], ids=str)
+def test_qgemm_large_tiles_bit_exact(torch, ctx, mkn, tile):
+    """The 256x256 tiles (16: unrolled three-deep X ring) and the int8
+    128x128 ones: K of 13 whole stages (the whole-stage loader; two six-stage
+    trips and a one-stage tail on tile 16) and K with a tail (the loader with
+    the per-load select), ragged edges, u8 outputs."""
+    from oxionnx_amd import _lib as L
+    m, k, n = mkn
+    rng = np.random.default_rng(m + k + n)
+    a = rng.integers(0, 256, (m, k)).astype(np.uint8)
+    b = rng.integers(-127, 128, (k, n)).astype(np.int8)
+    ctx.set_tile(tile)
+    try:
+        w = ctx.weight_qgemm(b, zp=0, scale=np.float32(0.0041))
+        y = ctx.qgemm(_dev(torch, a), w, a_zp=128, out_kind=L.QOUT_U8, a_scale=0.02, y_scale=0.05,
+                      y_zp=128, lo=0, hi=255).cpu().numpy()
+    finally:
+        ctx.set_tile(0)
+    want = O.qlinear_matmul(a, np.float32(0.02), 128, b, np.float32(0.0041), 0, np.float32(0.05), 128,
+                            sat_range=(0, 255))
+    np.testing.assert_array_equal(y.astype(np.float32), want)
+
+
 def test_matmul_integer_per_row_zero_point(torch, ctx):
     from oxionnx_amd import _lib as L
     rng = np.random.default_rng(9)
