@@ -436,14 +436,17 @@ def bench_large(torch, ctx, L, stream, rng, only):
 def bench_widened(torch, ctx, L, stream, rng, only):
     """The convolution forms beyond plain Conv, at decoder / mobile-net shapes,
     f16 NCHW, operands resident:
-    * depthwise 3x3 [1,256,56,56] (the direct kernel; memory-bound: GB/s of
-      input + output + filter against HBM);
+    * depthwise 3x3 [1,256,56,56] (the depthwise band kernel; memory-bound:
+      GB/s of input + output + filter against HBM);
     * grouped 3x3 [1,256,56,56], 8 groups of 32 channels (one MFMA launch,
       the group on the grid z);
     * ConvTranspose 4x4 stride 2 [1,512,32,32] -> [1,256,64,64] (four
       sub-pixel phases on the MFMA engine);
     * config 4's residual conv, 3x3 512 -> 512 at 32x32 (input staging,
-      split-K slices and their reduction included)."""
+      split-K slices and their reduction included).
+    Each is timed after 50 ms of its own launches (the settled clock).  ms:
+    eager launches back to back (host dispatch included); ms_graph: the same
+    launches replayed from a HIP graph."""
     keys = ("depthwise_conv_f16", "grouped_conv_f16", "conv_transpose_f16", "conv_res_f16")
     if only and only not in keys:
         return {}
@@ -452,27 +455,34 @@ def bench_widened(torch, ctx, L, stream, rng, only):
     if not only or only == keys[0]:
         wt = ctx.weight_conv(rng.normal(0, 0.2, (256, 1, 3, 3)).astype(np.float32), dtype=L.F16)
         y = torch.empty((1, 256, 56, 56), dtype=torch.float16, device="cuda")
-        t = time_launches(torch, stream, lambda: ctx.conv2d(x, wt, None, pads=(1, 1, 1, 1), group=256, out=y),
-                          100, 5)
+        f = lambda: ctx.conv2d(x, wt, None, pads=(1, 1, 1, 1), group=256, out=y)
+        settle_clock(torch, f, 50.0)
+        t = time_launches(torch, stream, f, 100, 5)
+        tg = time_graph(torch, ctx, L, f)
         by = 2 * (2 * 256 * 56 * 56 + 256 * 9)
         fl = 2.0 * 256 * 56 * 56 * 9
         out[keys[0]] = {"ms": round(t, 5), "gbps": round(by / t / 1e6, 1),
-                        "frac_hbm": round(by / t / 1e6 / HBM_GBPS, 4), "tflops": round(fl / t / 1e9, 2)}
+                        "frac_hbm": round(by / t / 1e6 / HBM_GBPS, 4), "tflops": round(fl / t / 1e9, 2),
+                        "ms_graph": round(tg, 5), "gbps_graph": round(by / tg / 1e6, 1)}
     if not only or only == keys[1]:
         wt = ctx.weight_conv(rng.normal(0, 0.05, (256, 32, 3, 3)).astype(np.float32), dtype=L.F16)
         y = torch.empty((1, 256, 56, 56), dtype=torch.float16, device="cuda")
-        t = time_launches(torch, stream, lambda: ctx.conv2d(x, wt, None, pads=(1, 1, 1, 1), group=8, out=y),
-                          100, 5)
+        f = lambda: ctx.conv2d(x, wt, None, pads=(1, 1, 1, 1), group=8, out=y)
+        settle_clock(torch, f, 50.0)
+        t = time_launches(torch, stream, f, 100, 5)
+        tg = time_graph(torch, ctx, L, f)
         fl = 2.0 * 256 * 56 * 56 * 32 * 9
         out[keys[1]] = {"ms": round(t, 5), "tflops": round(fl / t / 1e9, 2),
-                        "frac_mfma": round(fl / t / 1e9 / PEAK_TFLOPS["f16"], 4)}
+                        "frac_mfma": round(fl / t / 1e9 / PEAK_TFLOPS["f16"], 4), "ms_graph": round(tg, 5),
+                        "tflops_graph": round(fl / tg / 1e9, 2)}
     if not only or only == keys[2]:
         xt = torch.from_numpy(rng.uniform(-1, 1, (1, 512, 32, 32)).astype(np.float32)).cuda().half()
         wt = ctx.weight_conv_transpose(rng.normal(0, 0.02, (512, 256, 4, 4)).astype(np.float32), dtype=L.F16,
                                        strides=(2, 2), pads=(1, 1, 1, 1))
         y = torch.empty((1, 256, 64, 64), dtype=torch.float16, device="cuda")
-        t = time_launches(torch, stream, lambda: ctx.conv_transpose2d(xt, wt, None, strides=(2, 2),
-                                                                    pads=(1, 1, 1, 1), out=y), 20, 2)
+        f = lambda: ctx.conv_transpose2d(xt, wt, None, strides=(2, 2), pads=(1, 1, 1, 1), out=y)
+        settle_clock(torch, f, 50.0)
+        t = time_launches(torch, stream, f, 20, 2)
         fl = 2.0 * 512 * 32 * 32 * 256 * 16   # every input scatters a 4x4 tap into the output
         out[keys[2]] = {"ms": round(t, 5), "tflops": round(fl / t / 1e9, 2),
                         "frac_mfma": round(fl / t / 1e9 / PEAK_TFLOPS["f16"], 4)}
@@ -481,7 +491,7 @@ def bench_widened(torch, ctx, L, stream, rng, only):
         wt = ctx.weight_conv(rng.normal(0, 0.02, (512, 512, 3, 3)).astype(np.float32), dtype=L.F16)
         y = torch.empty((1, 512, 32, 32), dtype=torch.float16, device="cuda")
         f = lambda: ctx.conv2d(xr, wt, None, pads=(1, 1, 1, 1), out=y)
-        time_launches(torch, stream, f, 20, 5)
+        settle_clock(torch, f, 50.0)
         t = time_launches(torch, stream, f, 100, 0)
         fl = 2.0 * 1024 * 512 * 4608
         out[keys[3]] = {"ms": round(t, 5), "tflops": round(fl / t / 1e9, 2),

@@ -3,6 +3,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <algorithm>
+
 #include "launch.hpp"
 
 namespace ohip {
@@ -1116,10 +1118,123 @@ hipError_t run_conv_nchw_f32(const float* x, const float* w, const float* bias, 
   return hipGetLastError();
 }
 
+// Depthwise 3x3 (one input channel per output channel, zero padding,
+// stride 1 or 2, no dilation): a block takes a band of `rows` output rows of
+// one plane, stages the band's input window in LDS as f32 (one coalesced
+// read of each input row instead of nine cached reads per output), keeps
+// the nine weights in registers, and finishes each output exactly as
+// conv_direct_kernel does: taps in (ky, kx) order with the ones outside the
+// image skipped, + bias, activation.
+constexpr int kDwLds = 8192;   // floats of staged window per block (32 KiB)
+
+template <class T, int S>
+__global__ void __launch_bounds__(256)
+conv_dw3_kernel(const T* __restrict__ x, const T* __restrict__ w, const T* __restrict__ bias, T* __restrict__ y,
+                DirectConvArgs a, int rows) {
+  extern __shared__ float win[];   // the band's window, RW x CW floats
+  const int bands = (a.OH + rows - 1) / rows;
+  const int band = (int)(blockIdx.x % bands);
+  const int plane = (int)(blockIdx.x / bands);   // n * C + c
+  const int co = plane % a.cout, n = plane / a.cout;
+  const int oy0 = band * rows, nr = min(rows, a.OH - oy0);
+  const int iy0 = oy0 * S - a.pt, ix0 = -a.pl;
+  const int RW = (nr - 1) * S + 3, CW = (a.OW - 1) * S + 3;
+  const T* xc = x + (int64_t)plane * a.H * a.W;
+  // the window's loads issued in batches of B before their LDS stores, so
+  // a thread's loads overlap instead of each waiting a round trip
+  constexpr int B = 16;
+  const int nw = RW * CW;
+  for (int base = threadIdx.x; base < nw; base += 256 * B) {
+    float v[B];
+#pragma unroll
+    for (int u = 0; u < B; ++u) {
+      const int i = base + u * 256;
+      const int r = i / CW, c = i - r * CW;
+      const int iy = iy0 + r, ix = ix0 + c;
+      v[u] = i < nw && (unsigned)iy < (unsigned)a.H && (unsigned)ix < (unsigned)a.W
+                 ? to_f32(xc[(int64_t)iy * a.W + ix]) : 0.0f;
+    }
+#pragma unroll
+    for (int u = 0; u < B; ++u)
+      if (base + u * 256 < nw) win[base + u * 256] = v[u];
+  }
+  float wk[9];
+  const T* wr = w + (int64_t)co * a.ldw;
+#pragma unroll
+  for (int k = 0; k < 9; ++k) wk[k] = to_f32(wr[k * a.cpg]);
+  const float bv = bias ? to_f32(bias[co]) : 0.0f;
+  __syncthreads();
+  for (int i = threadIdx.x; i < nr * a.OW; i += 256) {
+    const int r = i / a.OW, ox = i - r * a.OW, oy = oy0 + r;
+    float acc = 0.0f;
+#pragma unroll
+    for (int ky = 0; ky < 3; ++ky) {
+      const int iy = oy * S + ky - a.pt;
+      if ((unsigned)iy >= (unsigned)a.H) continue;
+      const float* wrow = win + (r * S + ky) * CW + ox * S;
+#pragma unroll
+      for (int kx = 0; kx < 3; ++kx) {
+        const int ix = ox * S + kx - a.pl;
+        if ((unsigned)ix >= (unsigned)a.W) continue;
+        acc += wrow[kx] * wk[ky * 3 + kx];
+      }
+    }
+    float v = acc;
+    if (bias) v = v + bv;
+    v = activate_t<T>(v, a.act, a.lo, a.hi);
+    const int64_t o = a.nhwc_out ? (((int64_t)n * a.OH + oy) * a.OW + ox) * a.ldo + co
+                                 : (((int64_t)n * a.cout + co) * a.OH + oy) * a.OW + ox;
+    y[o] = from_f32<T>(v);
+  }
+}
+
+// Output rows per band of the depthwise kernel (large outputs only): bands small enough for
+// about five blocks per CU (a block is a short serial chain of window load,
+// sums and stores; 128 blocks of 36 rows ran 9.6 us on 64 planes of 56x56),
+// at most about eight outputs a thread, within the window's LDS budget;
+// 0 when the geometry is not its.
+inline int dw3_rows(const DirectConvArgs& a) {
+  // OHIP_DW3=0 keeps these convolutions on conv_direct_kernel (a measurement switch)
+  static const bool on = [] { const char* e = std::getenv("OHIP_DW3"); return !(e && e[0] == '0'); }();
+  if (!on) return 0;
+  if (!(a.cg == 1 && a.coutg == 1 && a.KH == 3 && a.KW == 3 && a.dh == 1 && a.dw == 1 && a.sh == a.sw &&
+        (a.sh == 1 || a.sh == 2) && a.pad_mode == 0 && a.OW > 0 && a.OH > 0))
+    return 0;
+  // below about 2^19 outputs the one-thread-per-output kernel is faster
+  // (64 planes of 56x56: 5.8 against 8.6 us; 256 planes: 10.7 against 10.2,
+  // 1024: 30.3 against 19.9, 256 of 224x224: 145 against 51)
+  if ((int64_t)a.N * a.cout * a.OH * a.OW < (1 << 19)) return 0;
+  const int CW = (a.OW - 1) * a.sh + 3;
+  const int max_rows = (kDwLds / CW - 3) / a.sh + 1;
+  if (max_rows < 1) return 0;
+  const int64_t planes = (int64_t)a.N * a.cout;
+  const int64_t fill = std::max<int64_t>(1, (int64_t)a.OH * planes / 1280);
+  return (int)std::max<int64_t>(1, std::min<int64_t>({(int64_t)a.OH, (int64_t)max_rows, 2048 / a.OW, fill}));
+}
+
 hipError_t run_conv_direct(int dtype, const void* x, const void* w, const void* bias, void* y,
                            const DirectConvArgs& a, hipStream_t st) {
   const int64_t total = (int64_t)a.N * a.cout * a.OH * a.OW;
   if (total <= 0) return hipSuccess;
+  if (const int rows = dw3_rows(a)) {
+    const int64_t blocks = (int64_t)a.N * a.cout * ((a.OH + rows - 1) / rows);
+    if (blocks > 0x7fffffff) return hipErrorInvalidValue;
+    const size_t lds = (size_t)((rows - 1) * a.sh + 3) * ((a.OW - 1) * a.sh + 3) * sizeof(float);
+#define OHIP_DW(T, S)                                                                                            \
+  hipLaunchKernelGGL((conv_dw3_kernel<T, S>), dim3((unsigned)blocks), dim3(256), lds, st,                        \
+                     reinterpret_cast<const T*>(x), reinterpret_cast<const T*>(w), reinterpret_cast<const T*>(bias), \
+                     reinterpret_cast<T*>(y), a, rows)
+#define OHIP_DW_S(T) if (a.sh == 1) OHIP_DW(T, 1); else OHIP_DW(T, 2)
+    switch (dtype) {
+      case DT_F32: OHIP_DW_S(float); break;
+      case DT_F16: OHIP_DW_S(_Float16); break;
+      case DT_BF16: OHIP_DW_S(__bf16); break;
+      default: return hipErrorInvalidValue;
+    }
+#undef OHIP_DW_S
+#undef OHIP_DW
+    return hipGetLastError();
+  }
   const unsigned grid = (unsigned)std::min<int64_t>((total + 255) / 256, 65535 * 16);
 #define OHIP_DIRECT(T)                                                                                      \
   hipLaunchKernelGGL(conv_direct_kernel<T>, dim3(grid), dim3(256), 0, st, reinterpret_cast<const T*>(x), \
