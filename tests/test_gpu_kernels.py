@@ -255,6 +255,31 @@ def test_grouped_conv_matches_oracle(torch, ctx, case, dt):
         assert _rel_err(got, want) <= HALF_TOL
 
 
+# bf16 depthwise 3x3 on both sides of the band kernel's 2^19-output gate,
+# against torch's f32 conv of the same bf16-rounded operands (the oracle has
+# no bf16 conv): (x shape, stride, pads [t, l, b, r]).
+DW_BF16_CASES = [((1, 96, 76, 76), 1, (1, 1, 1, 1)), ((1, 288, 115, 63), 2, (1, 1, 1, 1)),
+                 ((2, 8, 12, 10), 1, (0, 1, 1, 0))]
+
+
+@pytest.mark.parametrize("case", DW_BF16_CASES, ids=lambda c: f"{c[0]}s{c[1]}")
+def test_depthwise_bf16_matches_torch_f32(torch, ctx, case):
+    from oxionnx_amd import _lib as L
+    xs, s, p = case
+    c = xs[1]
+    g = torch.Generator(device="cuda").manual_seed(c + xs[2])
+    x = (torch.rand(xs, generator=g, device="cuda") * 2 - 1).to(torch.bfloat16)
+    w = (torch.randn((c, 1, 3, 3), generator=g, device="cuda") * 0.3).to(torch.bfloat16)
+    b = (torch.randn((c,), generator=g, device="cuda") * 0.1).to(torch.bfloat16)
+    wt = ctx.weight_conv(w.float().cpu().numpy(), dtype=L.BF16)
+    y = ctx.conv2d(x, wt, b, strides=(s, s), pads=p, group=c, act=L.ACT_RELU).float()
+    xp = torch.nn.functional.pad(x.float(), (p[1], p[3], p[0], p[2]))
+    want = torch.relu(torch.nn.functional.conv2d(xp, w.float(), b.float(), stride=s, groups=c))
+    assert y.shape == want.shape
+    err = float((y - want).abs().max() / want.abs().max())
+    assert err <= HALF_TOL, err
+
+
 # Batched MatMul with both operands on the device: (A shape, B shape).  The
 # slice rule is the reference's (s % a_batches, s % b_batches), which is not
 # numpy's broadcast for every shape (the [4,1,..] x [3,..] case below).
