@@ -1127,10 +1127,17 @@ hipError_t run_conv_nchw_f32(const float* x, const float* w, const float* bias, 
 // image skipped, + bias, activation.
 constexpr int kDwLds = 8192;   // floats of staged window per block (32 KiB)
 
+// Divisions of the depthwise kernel by the window width and by the runs of
+// four outputs a row (magic_div multipliers: a multiply-high and a shift).
+struct DwDiv {
+  uint32_t cw_mul, rpr_mul;
+  int cw_shift, rpr_shift;
+};
+
 template <class T, int S>
 __global__ void __launch_bounds__(256)
 conv_dw3_kernel(const T* __restrict__ x, const T* __restrict__ w, const T* __restrict__ bias, T* __restrict__ y,
-                DirectConvArgs a, int rows) {
+                DirectConvArgs a, int rows, DwDiv dd, int vec4) {
   extern __shared__ float win[];   // the band's window, RW x CW floats
   const int bands = (a.OH + rows - 1) / rows;
   const int band = (int)(blockIdx.x % bands);
@@ -1140,6 +1147,7 @@ conv_dw3_kernel(const T* __restrict__ x, const T* __restrict__ w, const T* __res
   const int iy0 = oy0 * S - a.pt, ix0 = -a.pl;
   const int RW = (nr - 1) * S + 3, CW = (a.OW - 1) * S + 3;
   const T* xc = x + (int64_t)plane * a.H * a.W;
+  auto udiv = [](int i, uint32_t mul, int shift) { return (int)(((uint64_t)(uint32_t)i * mul) >> shift); };
   // the window's loads issued in batches of B before their LDS stores, so
   // a thread's loads overlap instead of each waiting a round trip
   constexpr int B = 16;
@@ -1149,7 +1157,7 @@ conv_dw3_kernel(const T* __restrict__ x, const T* __restrict__ w, const T* __res
 #pragma unroll
     for (int u = 0; u < B; ++u) {
       const int i = base + u * 256;
-      const int r = i / CW, c = i - r * CW;
+      const int r = udiv(i, dd.cw_mul, dd.cw_shift), c = i - r * CW;
       const int iy = iy0 + r, ix = ix0 + c;
       v[u] = i < nw && (unsigned)iy < (unsigned)a.H && (unsigned)ix < (unsigned)a.W
                  ? to_f32(xc[(int64_t)iy * a.W + ix]) : 0.0f;
@@ -1164,27 +1172,60 @@ conv_dw3_kernel(const T* __restrict__ x, const T* __restrict__ w, const T* __res
   for (int k = 0; k < 9; ++k) wk[k] = to_f32(wr[k * a.cpg]);
   const float bv = bias ? to_f32(bias[co]) : 0.0f;
   __syncthreads();
-  for (int i = threadIdx.x; i < nr * a.OW; i += 256) {
-    const int r = i / a.OW, ox = i - r * a.OW, oy = oy0 + r;
-    float acc = 0.0f;
+  // runs of four outputs of a row: one 3 x (3 S + 3) patch of the window,
+  // each output's taps still summed in (ky, kx) order
+  constexpr int PW = 3 * S + 3;
+  const int rpr = (a.OW + 3) / 4;
+  for (int i = threadIdx.x; i < nr * rpr; i += 256) {
+    const int r = udiv(i, dd.rpr_mul, dd.rpr_shift), ox0 = (i - r * rpr) * 4, oy = oy0 + r;
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    const bool interior = ox0 * S - a.pl >= 0 && (ox0 + 3) * S + 2 - a.pl < a.W;
 #pragma unroll
     for (int ky = 0; ky < 3; ++ky) {
       const int iy = oy * S + ky - a.pt;
       if ((unsigned)iy >= (unsigned)a.H) continue;
-      const float* wrow = win + (r * S + ky) * CW + ox * S;
+      const float* wrow = win + (r * S + ky) * CW + ox0 * S;
+      float pv[PW];
 #pragma unroll
-      for (int kx = 0; kx < 3; ++kx) {
-        const int ix = ox * S + kx - a.pl;
-        if ((unsigned)ix >= (unsigned)a.W) continue;
-        acc += wrow[kx] * wk[ky * 3 + kx];
+      for (int j = 0; j < PW; ++j) pv[j] = ox0 * S + j < CW ? wrow[j] : 0.0f;
+      if (interior) {   // every tap of the run inside the image: no per-tap checks
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+#pragma unroll
+          for (int kx = 0; kx < 3; ++kx) acc[e] += pv[e * S + kx] * wk[ky * 3 + kx];
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+#pragma unroll
+          for (int kx = 0; kx < 3; ++kx) {
+            const int ix = (ox0 + e) * S + kx - a.pl;
+            if ((unsigned)ix < (unsigned)a.W) acc[e] += pv[e * S + kx] * wk[ky * 3 + kx];
+          }
       }
     }
-    float v = acc;
-    if (bias) v = v + bv;
-    v = activate_t<T>(v, a.act, a.lo, a.hi);
-    const int64_t o = a.nhwc_out ? (((int64_t)n * a.OH + oy) * a.OW + ox) * a.ldo + co
-                                 : (((int64_t)n * a.cout + co) * a.OH + oy) * a.OW + ox;
-    y[o] = from_f32<T>(v);
+    if (vec4 && ox0 + 3 < a.OW) {   // NCHW, four aligned outputs: one store
+      typedef T t4 __attribute__((ext_vector_type(4)));
+      t4 o4;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        float v = acc[e];
+        if (bias) v = v + bv;
+        o4[e] = from_f32<T>(activate_t<T>(v, a.act, a.lo, a.hi));
+      }
+      *reinterpret_cast<t4*>(y + (((int64_t)n * a.cout + co) * a.OH + oy) * a.OW + ox0) = o4;
+      continue;
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int ox = ox0 + e;
+      if (ox >= a.OW) break;
+      float v = acc[e];
+      if (bias) v = v + bv;
+      v = activate_t<T>(v, a.act, a.lo, a.hi);
+      const int64_t o = a.nhwc_out ? (((int64_t)n * a.OH + oy) * a.OW + ox) * a.ldo + co
+                                   : (((int64_t)n * a.cout + co) * a.OH + oy) * a.OW + ox;
+      y[o] = from_f32<T>(v);
+    }
   }
 }
 
@@ -1201,8 +1242,9 @@ inline int dw3_rows(const DirectConvArgs& a) {
         (a.sh == 1 || a.sh == 2) && a.pad_mode == 0 && a.OW > 0 && a.OH > 0))
     return 0;
   // below about 2^19 outputs the one-thread-per-output kernel is faster
-  // (64 planes of 56x56: 5.8 against 8.6 us; 256 planes: 10.7 against 10.2,
-  // 1024: 30.3 against 19.9, 256 of 224x224: 145 against 51)
+  // (64 planes of 56x56: 5.8 against 8.6 us before the runs of four; 256
+  // planes: 10.2 against 7.8, 1024: 30.3 against 14.8, 256 of 224x224: 145
+  // against 41)
   if ((int64_t)a.N * a.cout * a.OH * a.OW < (1 << 19)) return 0;
   const int CW = (a.OW - 1) * a.sh + 3;
   const int max_rows = (kDwLds / CW - 3) / a.sh + 1;
@@ -1220,10 +1262,15 @@ hipError_t run_conv_direct(int dtype, const void* x, const void* w, const void* 
     const int64_t blocks = (int64_t)a.N * a.cout * ((a.OH + rows - 1) / rows);
     if (blocks > 0x7fffffff) return hipErrorInvalidValue;
     const size_t lds = (size_t)((rows - 1) * a.sh + 3) * ((a.OW - 1) * a.sh + 3) * sizeof(float);
+    DwDiv dd{};
+    magic_div((a.OW - 1) * a.sh + 3, &dd.cw_mul, &dd.cw_shift);
+    magic_div((a.OW + 3) / 4, &dd.rpr_mul, &dd.rpr_shift);
+    // NCHW rows of whole runs of four, 4-element aligned: vector stores
+    const int vec4 = !a.nhwc_out && a.OW % 4 == 0 && (uintptr_t)y % (4 * (dtype == DT_F32 ? 4 : 2)) == 0;
 #define OHIP_DW(T, S)                                                                                            \
   hipLaunchKernelGGL((conv_dw3_kernel<T, S>), dim3((unsigned)blocks), dim3(256), lds, st,                        \
                      reinterpret_cast<const T*>(x), reinterpret_cast<const T*>(w), reinterpret_cast<const T*>(bias), \
-                     reinterpret_cast<T*>(y), a, rows)
+                     reinterpret_cast<T*>(y), a, rows, dd, vec4)
 #define OHIP_DW_S(T) if (a.sh == 1) OHIP_DW(T, 1); else OHIP_DW(T, 2)
     switch (dtype) {
       case DT_F32: OHIP_DW_S(float); break;
