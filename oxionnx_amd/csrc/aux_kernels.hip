@@ -1130,8 +1130,9 @@ constexpr int kDwLds = 8192;   // floats of staged window per block (32 KiB)
 // Divisions of the depthwise kernel by the window width and by the runs of
 // four outputs a row (magic_div multipliers: a multiply-high and a shift).
 struct DwDiv {
-  uint32_t cw_mul, rpr_mul;
-  int cw_shift, rpr_shift;
+  uint32_t cw_mul, rpr_mul, cpr_mul;
+  int cw_shift, rpr_shift, cpr_shift;
+  int vec_in;   // image rows of whole 16-byte chunks, 16-byte aligned: chunk loads
 };
 
 template <class T, int S>
@@ -1152,6 +1153,42 @@ conv_dw3_kernel(const T* __restrict__ x, const T* __restrict__ w, const T* __res
   // a thread's loads overlap instead of each waiting a round trip
   constexpr int B = 16;
   const int nw = RW * CW;
+  if (dd.vec_in) {
+    // the image part of each window row by 16-byte chunks (EPV elements),
+    // the pad columns (and rows outside the image) as zeros
+    constexpr int EPV = 16 / sizeof(T);
+    typedef T tv __attribute__((ext_vector_type(EPV)));
+    const int cpr = a.W / EPV, nc = RW * cpr;
+    constexpr int BV = 4;
+    for (int base = threadIdx.x; base < nc; base += 256 * BV) {
+      tv v[BV];
+#pragma unroll
+      for (int u = 0; u < BV; ++u) {
+        const int i = base + u * 256;
+        const int r = udiv(i, dd.cpr_mul, dd.cpr_shift), k = i - r * cpr;
+        const int iy = iy0 + r;
+        v[u] = tv{};
+        if (i < nc && (unsigned)iy < (unsigned)a.H)
+          v[u] = *reinterpret_cast<const tv*>(xc + (int64_t)iy * a.W + k * EPV);
+      }
+#pragma unroll
+      for (int u = 0; u < BV; ++u) {
+        const int i = base + u * 256;
+        if (i >= nc) break;
+        const int r = udiv(i, dd.cpr_mul, dd.cpr_shift), k = i - r * cpr;
+#pragma unroll
+        for (int e = 0; e < EPV; ++e) {
+          const int c = a.pl + k * EPV + e;
+          if (c < CW) win[r * CW + c] = to_f32(v[u][e]);
+        }
+      }
+    }
+    const int right = CW - a.pl - a.W > 0 ? CW - a.pl - a.W : 0, np = a.pl + right;
+    for (int i = threadIdx.x; i < RW * np; i += 256) {
+      const int r = i / np, j = i - r * np;
+      win[r * CW + (j < a.pl ? j : a.W + j)] = 0.0f;
+    }
+  } else
   for (int base = threadIdx.x; base < nw; base += 256 * B) {
     float v[B];
 #pragma unroll
@@ -1242,9 +1279,9 @@ inline int dw3_rows(const DirectConvArgs& a) {
         (a.sh == 1 || a.sh == 2) && a.pad_mode == 0 && a.OW > 0 && a.OH > 0))
     return 0;
   // below about 2^19 outputs the one-thread-per-output kernel is faster
-  // (64 planes of 56x56: 5.8 against 8.6 us before the runs of four; 256
-  // planes: 10.2 against 7.8, 1024: 30.3 against 14.8, 256 of 224x224: 145
-  // against 41)
+  // (64 planes of 56x56: 5.8 against 8.6 us before the runs of four and
+  // the chunked window; 256 planes: 10.2 against 6.3, 1024: 30.3 against
+  // 12.3, 256 of 224x224: 145 against 29)
   if ((int64_t)a.N * a.cout * a.OH * a.OW < (1 << 19)) return 0;
   const int CW = (a.OW - 1) * a.sh + 3;
   const int max_rows = (kDwLds / CW - 3) / a.sh + 1;
@@ -1265,6 +1302,9 @@ hipError_t run_conv_direct(int dtype, const void* x, const void* w, const void* 
     DwDiv dd{};
     magic_div((a.OW - 1) * a.sh + 3, &dd.cw_mul, &dd.cw_shift);
     magic_div((a.OW + 3) / 4, &dd.rpr_mul, &dd.rpr_shift);
+    const int epv = dtype == DT_F32 ? 4 : 8;
+    dd.vec_in = a.W % epv == 0 && (uintptr_t)x % 16 == 0 && a.pl >= 0 && a.pl <= 2;
+    magic_div(std::max(1, a.W / epv), &dd.cpr_mul, &dd.cpr_shift);
     // NCHW rows of whole runs of four, 4-element aligned: vector stores
     const int vec4 = !a.nhwc_out && a.OW % 4 == 0 && (uintptr_t)y % (4 * (dtype == DT_F32 ? 4 : 2)) == 0;
 #define OHIP_DW(T, S)                                                                                            \

@@ -214,13 +214,16 @@ GROUP_CASES = [
     # depthwise 3x3 on the band kernel (from 2^19 outputs): bands of 56x56
     # planes, stride 2 with odd extents, uneven pads, a valid conv, 2000-wide
     # rows (four-row windows); the same geometries below 2^19 outputs take
-    # the one-thread-per-output kernel
+    # the one-thread-per-output kernel; rows of whole 16-byte chunks are
+    # staged by chunk loads
     ((2, 96, 56, 56), (96, 1, 3, 3), 96, (1, 1), (1, 1, 1, 1), (1, 1)),
     ((1, 288, 115, 63), (288, 1, 3, 3), 288, (2, 2), (1, 1, 1, 1), (1, 1)),
     ((1, 256, 66, 129), (256, 1, 3, 3), 256, (2, 2), (0, 1, 1, 0), (1, 1)),
     ((1, 96, 76, 76), (96, 1, 3, 3), 96, (1, 1), (0, 0, 0, 0), (1, 1)),
     ((1, 16, 17, 2000), (16, 1, 3, 3), 16, (1, 1), (1, 1, 1, 1), (1, 1)),
     ((1, 16, 57, 31), (16, 1, 3, 3), 16, (2, 2), (1, 1, 1, 1), (1, 1)),
+    ((1, 256, 96, 112), (256, 1, 3, 3), 256, (2, 2), (1, 1, 1, 1), (1, 1)),   # 16-byte row chunks, stride 2
+    ((1, 416, 64, 80), (416, 1, 3, 3), 416, (2, 2), (0, 2, 1, 0), (1, 1)),    # chunks, window narrower than the row
     ((1, 6, 10, 10), (4, 3, 3, 3), 2, (1, 1), (1, 1, 1, 1), (2, 2)),        # narrow groups, dilated
     ((2, 64, 12, 12), (64, 16, 3, 3), 4, (1, 1), (1, 1, 1, 1), (1, 1)),     # MFMA per group, aligned
     ((1, 40, 9, 9), (48, 20, 3, 3), 2, (2, 2), (0, 1, 1, 0), (1, 1)),       # MFMA per group, padded slots
