@@ -1266,7 +1266,7 @@ conv_dw3_kernel(const T* __restrict__ x, const T* __restrict__ w, const T* __res
   }
 }
 
-// Output rows per band of the depthwise kernel (large outputs only): bands small enough for
+// Output rows per band of the depthwise kernel (from 2^18 outputs): bands small enough for
 // about five blocks per CU (a block is a short serial chain of window load,
 // sums and stores; 128 blocks of 36 rows ran 9.6 us on 64 planes of 56x56),
 // at most about eight outputs a thread, within the window's LDS budget;
@@ -1278,11 +1278,11 @@ inline int dw3_rows(const DirectConvArgs& a) {
   if (!(a.cg == 1 && a.coutg == 1 && a.KH == 3 && a.KW == 3 && a.dh == 1 && a.dw == 1 && a.sh == a.sw &&
         (a.sh == 1 || a.sh == 2) && a.pad_mode == 0 && a.OW > 0 && a.OH > 0))
     return 0;
-  // below about 2^19 outputs the one-thread-per-output kernel is faster
-  // (64 planes of 56x56: 5.8 against 8.6 us before the runs of four and
-  // the chunked window; 256 planes: 10.2 against 6.3, 1024: 30.3 against
-  // 12.3, 256 of 224x224: 145 against 29)
-  if ((int64_t)a.N * a.cout * a.OH * a.OW < (1 << 19)) return 0;
+  // below about 2^18 outputs the one-thread-per-output kernel is faster
+  // (64 planes of 56x56: 5.3 against 5.7 us, 256 of 28x28: 5.2 against 6.9;
+  // 128 planes of 56x56: 6.9 against 5.9, 256: 10.2 against 6.3, 1024: 30.3
+  // against 12.3, 256 of 224x224: 145 against 29)
+  if ((int64_t)a.N * a.cout * a.OH * a.OW < (1 << 18)) return 0;
   const int CW = (a.OW - 1) * a.sh + 3;
   const int max_rows = (kDwLds / CW - 3) / a.sh + 1;
   if (max_rows < 1) return 0;

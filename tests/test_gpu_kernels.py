@@ -211,9 +211,9 @@ GROUP_CASES = [
     ((2, 48, 6, 6), (48, 16, 1, 1), 3, (1, 1), (0, 0, 0, 0), (1, 1)),       # 1x1, aligned groups
     ((2, 8, 11, 13), (8, 1, 3, 3), 8, (1, 1), (1, 1, 1, 1), (1, 1)),        # depthwise
     ((1, 6, 9, 9), (12, 1, 5, 5), 6, (2, 2), (2, 1, 2, 1), (1, 1)),         # depthwise, multiplier 2
-    # depthwise 3x3 on the band kernel (from 2^19 outputs): bands of 56x56
+    # depthwise 3x3 on the band kernel (from 2^18 outputs): bands of 56x56
     # planes, stride 2 with odd extents, uneven pads, a valid conv, 2000-wide
-    # rows (four-row windows); the same geometries below 2^19 outputs take
+    # rows (four-row windows); the same geometries below 2^18 outputs take
     # the one-thread-per-output kernel; rows of whole 16-byte chunks are
     # staged by chunk loads
     ((2, 96, 56, 56), (96, 1, 3, 3), 96, (1, 1), (1, 1, 1, 1), (1, 1)),
@@ -222,6 +222,7 @@ GROUP_CASES = [
     ((1, 96, 76, 76), (96, 1, 3, 3), 96, (1, 1), (0, 0, 0, 0), (1, 1)),
     ((1, 16, 17, 2000), (16, 1, 3, 3), 16, (1, 1), (1, 1, 1, 1), (1, 1)),
     ((1, 16, 57, 31), (16, 1, 3, 3), 16, (2, 2), (1, 1, 1, 1), (1, 1)),
+    ((1, 128, 56, 56), (128, 1, 3, 3), 128, (1, 1), (1, 1, 1, 1), (1, 1)),     # just above the gate
     ((1, 256, 96, 112), (256, 1, 3, 3), 256, (2, 2), (1, 1, 1, 1), (1, 1)),   # 16-byte row chunks, stride 2
     ((1, 416, 64, 80), (416, 1, 3, 3), 416, (2, 2), (0, 2, 1, 0), (1, 1)),    # chunks, window narrower than the row
     ((1, 6, 10, 10), (4, 3, 3, 3), 2, (1, 1), (1, 1, 1, 1), (2, 2)),        # narrow groups, dilated
@@ -258,7 +259,7 @@ def test_grouped_conv_matches_oracle(torch, ctx, case, dt):
         assert _rel_err(got, want) <= HALF_TOL
 
 
-# bf16 depthwise 3x3 on both sides of the band kernel's 2^19-output gate,
+# bf16 depthwise 3x3 on both sides of the band kernel's 2^18-output gate,
 # against torch's f32 conv of the same bf16-rounded operands (the oracle has
 # no bf16 conv): (x shape, stride, pads [t, l, b, r]).
 DW_BF16_CASES = [((1, 96, 76, 76), 1, (1, 1, 1, 1)), ((1, 288, 115, 63), 2, (1, 1, 1, 1)),
